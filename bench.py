@@ -1,0 +1,168 @@
+#!/usr/bin/env python3
+"""Benchmark: qwen3-tts per-frame token loop on one MI355X.
+
+Workload: the full frame loop at the reference 0.6B shapes with Q8_0 weights
+(talker step + 2-token code-predictor prefill + 14 code-predictor steps per
+frame, on-device sampling, one hipGraph launch per frame), batch 1, greedy,
+after a 64-token synthetic prompt.  A "step" is one frame.  Weights are
+seeded N(0, 0.02) (norm gains 1 + N(0, 0.02)), quantised with the converter's
+Q8_0 formula.  EOS is biased off (eos_bias = -1e4, an argument of the
+reference's generate()) so every timed frame does the full work.
+
+Prints one JSON line: frames/s, ms per frame, the HBM roofline of the
+dominant kernel and of the whole frame, and the CPU oracle's frames/s on the
+same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen3-tts.cpp_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def frame_bytes(cfg, w, n_kv):
+    """Algorithmic HBM bytes of one frame: every weight byte once per pass
+    that reads it (talker once; code predictor 15 passes; heads once per
+    pass), plus KV reads/writes.  Activations are excluded (<0.1%)."""
+    def nbytes(name):
+        return w[name][2].nbytes
+    talker = sum(nbytes(n) for n in w if n.startswith("talker.blk."))
+    talker += nbytes("talker.codec_head.weight") + nbytes("talker.output_norm.weight")
+    cp_layers = sum(nbytes(n) for n in w if n.startswith("code_pred.blk."))
+    cp = 15 * (cp_layers + nbytes("code_pred.output_norm.weight")) + sum(
+        nbytes(f"code_pred.lm_head.{g}.weight") for g in range(15))
+    kv_row = cfg.n_kv_head * cfg.head_dim * 2 * 2          # K and V, fp16
+    talker_kv = cfg.n_layers * kv_row * (n_kv + 1)           # read n_kv rows + write 1
+    cp_kv = cfg.cp_layers * kv_row * sum(g + 2 for g in range(15))
+    embd = 17 * cfg.hidden_size * 2
+    return talker + cp + talker_kv + cp_kv + embd
+
+
+def cpu_baseline(cfg, w, text, spk, threads, budget_s):
+    """Oracle (C++ CPU restatement) frames/s on the same workload: time two
+    generate() calls of different length and difference them, so prefill
+    and prompt projection cancel."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import q3t_oracle as orc
+    o = orc.Oracle(cfg, w, threads=threads)
+    t0 = time.perf_counter()
+    o.generate(text, spk, max_len=1, temperature=0.0, eos_bias=-1e4)
+    t1 = time.perf_counter()
+    base = t1 - t0
+    n2 = 3
+    t0 = time.perf_counter()
+    o.generate(text, spk, max_len=n2, temperature=0.0, eos_bias=-1e4)
+    per = max((time.perf_counter() - t0 - base) / (n2 - 1), 1e-6)
+    n3 = int(max(4, min(64, budget_s / per)))
+    t0 = time.perf_counter()
+    o.generate(text, spk, max_len=n3, temperature=0.0, eos_bias=-1e4)
+    dt = time.perf_counter() - t0 - base
+    o.close()
+    return (n3 - 1) / dt, n3
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--weights", default="q8_0", choices=["q8_0", "f16"])
+    ap.add_argument("--prompt", type=int, default=64)
+    ap.add_argument("--cpu-threads", type=int, default=4)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-iters", type=int, default=200)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode is a single "
+              "dependent chain; see DESIGN.md for how independent streams would shard).", file=sys.stderr)
+        sys.exit(2)
+
+    from qwen3_tts_amd import config, driver
+    from qwen3_tts_amd.device import Device
+    from qwen3_tts_amd.synth import Weights
+
+    cfg = config.full_06b()
+    w = Weights(cfg, args.weights, seed=2024)
+    rng = np.random.default_rng(12)
+    text = rng.integers(0, cfg.text_vocab, args.prompt).astype(np.int32)
+    spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+
+    dev = Device(cfg, 0)
+    dev.upload_weights(w)
+    pre, trail, pad = driver.build_prefill(dev, cfg, text, spk)
+    total = args.warmup + args.steps
+    plen = pre.shape[0]
+    dev.kv_reserve(plen + total + 8)
+    dev.prefill(pre, 0, want_hidden=False)
+    dev.frames_begin(trail, pad, plen, total, repetition_penalty=1.05, temperature=0.0, top_k=0, eos_bias=-1e4)
+    if args.warmup:
+        _, eos = dev.frames_run(args.warmup)
+        assert not eos
+    dev.sync()
+    t0 = time.perf_counter()
+    codes, eos = dev.frames_run(args.steps)
+    elapsed = time.perf_counter() - t0
+    assert not eos and codes.shape[0] == args.steps, "EOS inside the timed region"
+    ms_per_step = elapsed * 1000.0 / args.steps
+    fps = args.steps / elapsed
+    n_kv_mid = plen + args.warmup + args.steps // 2
+    fbytes = frame_bytes(cfg, w.tensors, n_kv_mid)
+
+    # per-kernel HIP-event timing on the context's stream (talker layer 0)
+    kernels = {}
+    names = {0: "gemv_gate_up_swiglu", 1: "gemv_qkv_rmsnorm", 2: "gemv_down_resid", 3: "gemv_wo_resid",
+             4: "attention_decode"}
+    for k, nm in names.items():
+        us, b = dev.time_kernel(k, args.kernel_iters)
+        kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
+    dom = kernels["gemv_gate_up_swiglu"]
+    dev.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        nthreads = args.cpu_threads
+        cpu_fps, n_frames = cpu_baseline(cfg, w, text, spk, nthreads, args.cpu_budget)
+        cpu = {"value": round(cpu_fps, 3), "unit": "frames/s", "cores": nthreads, "kind": "port",
+               "sample": f"oracle generate() of {n_frames} frames minus a 1-frame run, same weights/prompt, "
+                         f"{nthreads} threads, {os.cpu_count()} host cpus"}
+
+    out = {
+        "metric": "codec frames/sec at batch 1 Q8_0 (RTF vs 12 Hz); achieved HBM GB/s per step",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if args.weights == "q8_0" else "f16",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        "config": {"workload": f"full frame loop, {args.weights.upper()} 0.6B shapes, {args.prompt}-token prompt, "
+                               f"greedy, hipGraph per frame", "global_batch": 1, "frames": args.steps,
+                   "weights": args.weights, "prompt_tokens": args.prompt, "prefill_rows": plen},
+        "rtf_12hz": round(fps / 12.0, 2),
+        "rtf_12_5hz": round(fps / 12.5, 2),
+        "frame_algorithmic_bytes": fbytes,
+        "frame_hbm_gbs": round(fbytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "frame_roofline_frac": round(fbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4) if dom["gbs"] else None, "traffic": None,
+                     "kernel": "gemv_gate_up_swiglu (talker layer 0, Q8_0 1024->2x3072)"},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

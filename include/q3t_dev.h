@@ -1,0 +1,177 @@
+/*
+ * q3t_dev.h -- C ABI of the MI355X (gfx950) device layer for the
+ * qwen3-tts.cpp per-frame token loop.
+ *
+ * This is the boundary a maintainer binds when the reference's
+ * TTSTransformer (src/tts_transformer.h:198-338) stops building ggml graphs
+ * for the talker step and the code predictor and calls the GPU instead.
+ * Nothing here uses C++ types, torch types or CUDA names: plain pointers,
+ * sizes and int status codes (0 = ok, negative = error; the message is
+ * returned by q3t_dev_last_error).
+ *
+ * Threading: one q3t_dev per host thread, like the reference's
+ * TTSTransformer (not thread safe; src/tts_transformer.h:400-404 keeps
+ * mutable state and an RNG per instance).  Host pointers are borrowed for
+ * the duration of a call; outputs are written into caller-owned buffers.
+ *
+ * Numerics (shared with the CPU restatement in oracle/): Q8_0 weights take a
+ * per-32-block Q8_0-quantised activation (int8 x int8 block dots); F16
+ * weights take an fp16-rounded activation; F16 ffn_down takes the fp32
+ * activation; every dot product accumulates exact terms in fp64 and rounds
+ * once to fp32.  KV cache is fp16.
+ */
+#ifndef Q3T_DEV_H
+#define Q3T_DEV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3T_TYPE_F32  0   /* ggml GGML_TYPE_F32  */
+#define Q3T_TYPE_F16  1   /* ggml GGML_TYPE_F16  */
+#define Q3T_TYPE_Q8_0 8   /* ggml GGML_TYPE_Q8_0 */
+
+/* Hyperparameters.  Mirrors tts_transformer_config
+ * (src/tts_transformer.h:59-103) field for field; values come from the
+ * GGUF keys parsed at src/tts_transformer.cpp:228-377. */
+typedef struct q3t_config {
+    int32_t hidden_size;      /* talker width, 1024 */
+    int32_t n_layers;         /* talker blocks, 28 */
+    int32_t n_head;           /* query heads, 16 */
+    int32_t n_kv_head;        /* KV heads, 8 */
+    int32_t head_dim;         /* 128 (the only value the kernels accept) */
+    int32_t ffn_size;         /* 3072 */
+    int32_t codec_vocab;      /* 3072 */
+    int32_t n_codebooks;      /* 16 */
+    int32_t cp_layers;        /* code-predictor blocks, 5 */
+    int32_t cp_vocab;         /* 2048 */
+    int32_t cp_hidden;        /* must equal hidden_size (no mtp_proj) */
+    int32_t cp_ffn;           /* 3072 */
+    int32_t text_vocab;       /* 151936 */
+    int32_t text_embd_dim;    /* 2048 */
+    float   rms_eps;          /* 1e-6 */
+    float   rope_theta;       /* 1e6 */
+    float   cp_rope_theta;    /* defaults to rope_theta (:316-324) */
+    int32_t codec_pad_id, codec_bos_id, codec_eos_id;
+    int32_t tts_bos_id, tts_eos_id, tts_pad_id;
+    int32_t codec_think_id, codec_nothink_id, codec_think_bos_id, codec_think_eos_id;
+    int32_t english_language_id;
+} q3t_config;
+
+/* Per-call sampling controls.  temperature <= 0 selects greedy argmax
+ * (first maximum), as in sample_or_argmax (src/tts_transformer.cpp:2750-2788).
+ * The reference draws from std::mt19937 (src/tts_transformer.h:403); this
+ * layer draws from Philox4x32-10 keyed by `seed` and counted by
+ * (frame, codebook), so a run is reproducible. */
+typedef struct q3t_sampling {
+    float    temperature;
+    int32_t  top_k;
+    uint64_t seed;
+} q3t_sampling;
+
+/* Arguments of the device-resident frame loop: the state generate() keeps
+ * across frames (src/tts_transformer.cpp:3092-3106) and its per-call
+ * controls (repetition penalty, EOS bias ramp, sampling). */
+typedef struct q3t_frame_args {
+    const float * trailing;      /* [n_trailing][hidden]: trailing_text_hidden rows */
+    int32_t       n_trailing;
+    const float * tts_pad;       /* [hidden]: row used once trailing rows run out */
+    int32_t       n_past;        /* positions already in the talker KV (prefill length) */
+    int32_t       max_len;       /* frames the caller will request at most */
+    float         repetition_penalty;
+    float         eos_bias;
+    int32_t       target_frames;
+    q3t_sampling  sampling;
+} q3t_frame_args;
+
+typedef struct q3t_dev q3t_dev;
+
+/* Context on HIP device `device` (ordinal).  Replaces the ggml backend and
+ * scheduler set up in TTSTransformer::load_model
+ * (src/tts_transformer.cpp:68-169, backend choice src/gguf_loader.cpp:154-198). */
+int  q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out);
+/* Frees every device allocation.  Replaces TTSTransformer::unload_model
+ * (src/tts_transformer.cpp:25-51). */
+void q3t_dev_destroy(q3t_dev * dev);
+/* Last error message of this context ("" if none).  Maps onto
+ * TTSTransformer::get_error (src/tts_transformer.h:329). */
+const char * q3t_dev_last_error(const q3t_dev * dev);
+
+/* One GGUF tensor, ggml layout (ne[0] contiguous), ggml type id.  Names and
+ * shapes as create_tensors binds them (src/tts_transformer.cpp:379-668);
+ * replaces load_tensor_data's ggml_backend_tensor_set
+ * (src/tts_transformer.cpp:670-729).  Q8_0 blocks are repacked in HBM
+ * (int8 quants and fp16 scales split) without changing any value. */
+int  q3t_dev_upload_tensor(q3t_dev * dev, const char * name, int32_t ggml_type,
+                           const int64_t ne[4], const void * data, size_t nbytes);
+/* Copies a tensor back in ggml layout (used to check the upload). */
+int  q3t_dev_download_tensor(q3t_dev * dev, const char * name, void * data, size_t nbytes);
+/* Dequantises a Q8_0 tensor on the device to fp32 [ne1][ne0] (fp32(d)*q). */
+int  q3t_dev_dequantize(q3t_dev * dev, const char * name, float * out, size_t n_floats);
+
+/* Talker KV cache of n_ctx positions (fp16, per layer [n_kv_head][n_ctx][head_dim]).
+ * Replaces init_kv_cache / clear_kv_cache (src/tts_transformer.cpp:731-783). */
+int  q3t_dev_kv_reserve(q3t_dev * dev, int32_t n_ctx);
+int  q3t_dev_kv_clear(q3t_dev * dev);
+int32_t q3t_dev_kv_capacity(const q3t_dev * dev);
+/* Writes fp16 K/V rows [n_pos][n_kv_head][head_dim] for positions
+ * [0, n_pos) of talker layer `layer` (used to pre-fill a cache). */
+int  q3t_dev_kv_write(q3t_dev * dev, int32_t layer, int32_t n_pos,
+                      const uint16_t * k, const uint16_t * v);
+
+/* n-token talker forward at positions [n_past, n_past+n).
+ * embd: [n][hidden].  hidden_out: [n][hidden] normed hidden (NULL ok).
+ * logits_out: last row's codec logits [codec_vocab] (NULL ok).
+ * Replaces forward_prefill (src/tts_transformer.cpp:2217-2347). */
+int  q3t_dev_prefill(q3t_dev * dev, const float * embd, int32_t n, int32_t n_past,
+                     float * hidden_out, float * logits_out);
+/* One-token talker step at position n_past.  Replaces forward_step
+ * (src/tts_transformer.cpp:2379-2509). */
+int  q3t_dev_talker_step(q3t_dev * dev, const float * embd, int32_t n_past,
+                         float * logits_out, float * hidden_out);
+/* Code predictor: 2-token prefill [hidden, codec_embd[cb0]] then 14 steps;
+ * codes_out[15] = codebooks 1..15.  logits_out (NULL ok): [15][cp_vocab],
+ * each head's logits before sampling.  `frame` keys the sampler's RNG.
+ * Replaces predict_codes_autoregressive (src/tts_transformer.cpp:2711-2976). */
+int  q3t_dev_code_pred(q3t_dev * dev, const float * hidden, int32_t cb0,
+                       const q3t_sampling * sampling, uint32_t frame,
+                       int32_t * codes_out, float * logits_out);
+
+/* text_proj: fc2(silu(fc1(text_embd[tok]) + b1)) + b2 -> out [n][hidden].
+ * Replaces project_text_tokens (src/tts_transformer.cpp:963-1028). */
+int  q3t_dev_text_proj(q3t_dev * dev, const int32_t * tokens, int32_t n, float * out);
+/* Embedding rows as fp32: table 0 = talker.codec_embd, 1 = code_pred.codec_embd[index],
+ * 2 = talker.text_embd.  Replaces lookup_embedding_rows /
+ * lookup_single_embedding_row (src/tts_transformer.cpp:839-961). */
+int  q3t_dev_embed_rows(q3t_dev * dev, int32_t table, int32_t index,
+                        const int32_t * tokens, int32_t n, float * out);
+
+/* Device-resident frame loop (the body of generate(),
+ * src/tts_transformer.cpp:3108-3309).  frames_begin takes the logits and
+ * normed hidden left on the device by the last q3t_dev_prefill /
+ * q3t_dev_talker_step call; frames_run advances up to n_frames frames with
+ * one hipGraph launch per frame and one host sync per call, appending
+ * [frames][n_codebooks] codes to codes_out.  *eos_out is set once codebook 0
+ * samples EOS (the frame that sampled it is not emitted). */
+int  q3t_dev_frames_begin(q3t_dev * dev, const q3t_frame_args * args);
+int  q3t_dev_frames_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
+                        int32_t * n_emitted_out, int32_t * eos_out);
+
+/* Blocks until all work queued by this context has finished. */
+int  q3t_dev_sync(q3t_dev * dev);
+/* Times `iters` launches of one kernel class of the frame loop with HIP
+ * events on the context's stream; writes the average microseconds per
+ * launch and the algorithmic bytes one launch moves.  which: 0 = talker
+ * gate/up GEMV, 1 = talker QKV GEMV, 2 = talker down GEMV, 3 = talker Wo
+ * GEMV, 4 = talker attention (at position min(n_ctx-1, 512)).  Resets the
+ * frame-loop state.  Used by the benchmark to report roofline fractions. */
+int  q3t_dev_time_kernel(q3t_dev * dev, int32_t which, int32_t iters,
+                         double * avg_us_out, double * bytes_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,177 @@
+/*
+ * q3t_oracle.h -- CPU restatement of the qwen3-tts.cpp per-frame token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path and the timed CPU baseline.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it.  Nothing in the shipped library
+ * (qwen3-tts.cpp_amd/) links, loads or calls it.
+ *
+ * What it restates (reference paths relative to the reference checkout):
+ *   talker decode step          src/tts_transformer.cpp:1619-1769 (build_step_graph)
+ *   n-token prefill             src/tts_transformer.cpp:1474-1617 (build_prefill_forward_graph)
+ *   code-predictor prefill      src/tts_transformer.cpp:1901-2053
+ *   code-predictor step         src/tts_transformer.cpp:2055-2215
+ *   code-predictor loop/sampler src/tts_transformer.cpp:2711-2976 (sample_or_argmax :2750-2788)
+ *   argmax                      src/tts_transformer.cpp:2583-2593
+ *   generate() frame loop       src/tts_transformer.cpp:3007-3309
+ *   text projection             src/tts_transformer.cpp:963-1028
+ *   prefill layout              src/tts_transformer.cpp:1030-1186
+ *
+ * Numerics contract (the ggml kernels the reference calls are not in the
+ * reference checkout; their semantics are restated from upstream ggml):
+ *   - activations are fp32;
+ *   - Q8_0 weight x fp32 activation: the activation row is quantised per
+ *     32-block as ggml-cpu's x86 quantize_row_q8_0 does (d = amax/127 stored
+ *     as fp16, q = round-to-nearest-even(x * (127/amax))), block dot products
+ *     are exact int32, combined as fp16(d_w)*fp16(d_x)*isum;
+ *   - F16 weight x fp32 activation: the activation is rounded to fp16 (RNE);
+ *   - F16 ffn_down is widened to fp32 (ggml_cast) so its activation is NOT
+ *     rounded (src/tts_transformer.cpp:1746-1748);
+ *   - every dot product / sum of squares / softmax denominator accumulates its
+ *     (exact) terms in fp64 and rounds to fp32 once.  ggml accumulates in
+ *     fp32 SIMD lanes in an order that cannot be reproduced here; fp64
+ *     accumulation is at least as accurate and makes the rounded result
+ *     independent of summation order, which is what lets a GPU reduction
+ *     match this restatement bit for bit;
+ *   - exp() is q3t_orc_expf: Cody-Waite range reduction plus a degree-7
+ *     Taylor polynomial (Horner with fused multiply-add), flushed to zero
+ *     below -87; ggml uses its own SIMD exp approximation;
+ *   - RoPE cos/sin come from a table built with the C library's cosf/sinf on
+ *     theta_i = pos * base^(-2i/128) formed by cumulative fp32 product
+ *     (ggml_rope_cache_init);
+ *   - sampling (temperature > 0) uses Philox4x32-10 (Salmon et al., SC'11)
+ *     keyed by a caller seed instead of std::mt19937/discrete_distribution,
+ *     which cannot be reproduced on a GPU: distributional parity only with
+ *     the reference, exact parity with the HIP path.
+ */
+#ifndef Q3T_ORACLE_H
+#define Q3T_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (ggml.h enum ggml_type) */
+#define ORC_TYPE_F32  0
+#define ORC_TYPE_F16  1
+#define ORC_TYPE_Q8_0 8
+
+typedef struct orc_config {
+    int32_t hidden_size;
+    int32_t n_layers;
+    int32_t n_head;
+    int32_t n_kv_head;
+    int32_t head_dim;
+    int32_t ffn_size;
+    int32_t codec_vocab;
+    int32_t n_codebooks;
+    int32_t cp_layers;
+    int32_t cp_vocab;
+    int32_t cp_hidden;
+    int32_t cp_ffn;
+    int32_t text_vocab;
+    int32_t text_embd_dim;
+    float   rms_eps;
+    float   rope_theta;
+    float   cp_rope_theta;
+    int32_t codec_pad_id, codec_bos_id, codec_eos_id;
+    int32_t tts_bos_id, tts_eos_id, tts_pad_id;
+    int32_t codec_think_id, codec_nothink_id, codec_think_bos_id, codec_think_eos_id;
+    int32_t english_language_id;
+} orc_config;
+
+typedef struct orc_gen_params {
+    int32_t max_len;
+    int32_t language_id;
+    float   repetition_penalty;
+    float   temperature;
+    int32_t top_k;
+    float   eos_bias;
+    int32_t target_frames;
+    int32_t rep_loop_detect;
+    uint64_t seed;
+} orc_gen_params;
+
+typedef struct orc_model orc_model;
+
+/* ---- elementwise / kernel-level restatements (unit-test surface) ---- */
+float    orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+float    orc_expf(float x);
+/* converter weight quantisation (scripts/convert_tts_to_gguf.py:304-307 via
+ * gguf-py quants): d = amax/127, q = round-half-away(x/d).  out: n/32 blocks
+ * of 34 bytes (fp16 d, 32 x int8). */
+void orc_quantize_q8_0_weights(const float * x, int64_t n, uint8_t * out);
+/* ggml-cpu x86 activation quantisation; out as above. */
+void orc_quantize_q8_0_act(const float * x, int64_t n, uint8_t * out);
+void orc_dequantize_q8_0(const uint8_t * blocks, int64_t n, float * out);
+/* y[t][r] = W[r,:] . x[t][:]; type selects the reference numerics.
+ * widen_f16 = 1 selects the F16-as-F32 (ffn_down cast) path. */
+void orc_gemv(int type, const void * w, int64_t rows, int64_t k,
+              const float * x, int64_t ntok, float * y, int widen_f16);
+void orc_rmsnorm(const float * x, const float * w, int64_t n, float eps, float * y);
+void orc_rope_neox(float * x, int64_t head_dim, const float * cos_row, const float * sin_row);
+void orc_rope_table(float theta_base, int64_t head_dim, int64_t n_pos, float * cos_tab, float * sin_tab);
+/* single-query GQA decode attention.  q: [n_head][hd] fp32; k,v: fp16
+ * caches laid out [n_kv_head][n_ctx][hd]; first n_kv positions used.
+ * out: [n_head][hd].  probs_out (optional): [n_head][n_kv] post-softmax. */
+void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
+                   int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
+                   int64_t n_kv, float * out, float * probs_out);
+int32_t orc_argmax(const float * x, int32_t n);
+/* talker cb0 sampler (src/tts_transformer.cpp:3109-3184); modifies logits. */
+int32_t orc_sample_cb0(float * logits, int32_t vocab, int32_t eos_id,
+                       const uint8_t * seen, float rep_penalty, float temperature,
+                       int32_t top_k, float eos_bias, int32_t target_frames,
+                       int32_t frame, uint64_t seed);
+/* code-predictor sampler (sample_or_argmax, :2750-2788); modifies logits. */
+int32_t orc_sample_cp(float * logits, int32_t vocab, float temperature, int32_t top_k,
+                      uint64_t seed, uint32_t frame, uint32_t group);
+void orc_philox4x32(uint64_t key, uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t out[4]);
+double orc_uniform(uint64_t seed, uint32_t frame, uint32_t group);
+
+/* ---- model-level ---- */
+orc_model * orc_create(const orc_config * cfg);
+void        orc_destroy(orc_model * m);
+void        orc_set_threads(orc_model * m, int32_t n_threads);
+/* Borrows `data` (caller keeps it alive).  ggml layout, ne0 contiguous. */
+int         orc_set_tensor(orc_model * m, const char * name, int32_t type,
+                           const void * data, size_t nbytes);
+int         orc_check_complete(orc_model * m);
+const char * orc_last_error(const orc_model * m);
+int         orc_kv_reset(orc_model * m, int32_t n_ctx);
+/* n-token prefill at positions [n_past, n_past+n).  hidden_out: [n][d]
+ * (normed), logits_out: last row [codec_vocab] (may be NULL). */
+int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
+                float * hidden_out, float * logits_out);
+int orc_step(orc_model * m, const float * embd, int32_t n_past,
+             float * logits_out, float * hidden_out);
+/* 15 codes for codebooks 1..15.  logits_out (optional): [15][cp_vocab]
+ * logits as produced by each head before sampling. */
+int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,
+                  float temperature, int32_t top_k, uint64_t seed, uint32_t frame,
+                  int32_t * codes_out, float * logits_out);
+int orc_text_proj(orc_model * m, const int32_t * tokens, int32_t n, float * out);
+int orc_embed_row(orc_model * m, const char * table, int32_t index, int32_t token, float * out);
+/* build_prefill_graph: prefill_out [(n_instruct+10 or 9)][d],
+ * trailing_out [max(0,n-9)+1][d], pad_out [d].  Returns prefill_len,
+ * writes trailing_len. */
+int orc_build_prefill(orc_model * m, const int32_t * text, int32_t n_text,
+                      const float * speaker, int32_t language_id,
+                      const int32_t * instruct, int32_t n_instruct,
+                      float * prefill_out, float * trailing_out, float * pad_out,
+                      int32_t * trailing_len_out);
+/* generate(): returns number of frames written to codes_out ([max_len][16]);
+ * negative on error.  first_logits_out (optional): prefill logits row. */
+int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
+                 const float * speaker, const orc_gen_params * p,
+                 const int32_t * instruct, int32_t n_instruct,
+                 int32_t * codes_out, float * first_logits_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

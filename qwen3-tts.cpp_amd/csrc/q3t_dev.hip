@@ -1,0 +1,1017 @@
+// q3t_dev.hip -- device context and C ABI (include/q3t_dev.h) of the MI355X
+// frame loop.  Host code here only moves data, sizes launches and records
+// the per-frame hipGraph; every arithmetic step of the loop runs in the
+// kernels of q3t_kernels.h.  There is no CPU fallback: without a HIP device
+// every entry point fails with an error.
+
+#include "../../include/q3t_dev.h"
+#include "q3t_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace q3t;
+
+namespace {
+
+struct Slot {                 // one uploaded tensor (a view into device memory)
+    int32_t type = -1;
+    int64_t ne0 = 0, ne1 = 0;
+    void * data = nullptr;         // Q8_0: int8 [ne1][ne0]; F16: [ne1][ne0]; F32
+    uint16_t * scales = nullptr;   // Q8_0: fp16 [ne1][ne0/32]
+};
+
+struct Weight {               // what a GEMV launch needs
+    int32_t kind = -1;        // W_Q8 / W_F16
+    const void * w = nullptr;
+    const uint16_t * d = nullptr;
+};
+
+struct LayerDev {
+    Slot qkv;                 // attn_q | attn_k | attn_v rows, concatenated
+    int32_t qkv_parts = 0;
+    Slot wo, wg, wu, wd;
+    const float * attn_norm = nullptr, * ffn_norm = nullptr, * q_norm = nullptr, * k_norm = nullptr;
+};
+
+
+}  // namespace
+
+struct q3t_dev {
+    q3t_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    std::vector<void *> allocs;
+    std::map<std::string, Slot> slots;
+    std::vector<LayerDev> talker, cp;
+    std::vector<Slot> cp_embd, cp_head;
+    Slot codec_embd, codec_head, text_embd, fc1, fc1_b, fc2, fc2_b, out_norm, cp_out_norm;
+
+    // workspace
+    float * xa = nullptr, * xb = nullptr, * qkv = nullptr, * attn = nullptr, * ffn = nullptr;
+    float * hidden = nullptr, * logits = nullptr, * cp_logits = nullptr, * tp_a = nullptr, * tp_b = nullptr;
+    float * stage = nullptr; int32_t stage_rows = 0;
+    float * hidden_all = nullptr; int32_t hidden_all_rows = 0;
+    int32_t * ids = nullptr; int32_t ids_cap = 0;
+    FrameState * st = nullptr;
+    SampleParams * params = nullptr;
+    uint8_t * seen = nullptr;
+    int32_t * codes_out = nullptr; int32_t codes_cap = 0;
+    float * trailing = nullptr; int32_t trailing_cap = 0; int32_t n_trailing = 0;
+    float * pad = nullptr;
+    float * probs = nullptr;
+
+    // caches
+    uint16_t * kc = nullptr, * vc = nullptr; int32_t n_ctx = 0;
+    uint16_t * cpk = nullptr, * cpv = nullptr;
+    float * rope_cos = nullptr, * rope_sin = nullptr, * cp_rope_cos = nullptr, * cp_rope_sin = nullptr;
+    int32_t rope_rows = 0;
+
+    hipGraphExec_t frame_exec = nullptr;
+    hipGraph_t frame_graph = nullptr;
+    int32_t host_emitted = 0;
+    int32_t frames_launched = 0;
+    int32_t frames_max = 0;
+    bool frames_ready = false;
+    bool resolved = false;
+    int n_cu = 256;
+};
+
+namespace {
+
+int fail(q3t_dev * c, const std::string & msg) { c->err = msg; return -1; }
+
+#define HIP_OK(call)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess) return fail(c, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+int dev_alloc(q3t_dev * c, void ** p, size_t bytes) {
+    HIP_OK(hipMalloc(p, std::max<size_t>(bytes, 256)));
+    c->allocs.push_back(*p);
+    return 0;
+}
+
+template <typename T>
+int dev_alloc_t(q3t_dev * c, T ** p, size_t count) {
+    void * v = nullptr;
+    if (dev_alloc(c, &v, count * sizeof(T))) return -1;
+    *p = (T *) v;
+    return 0;
+}
+
+void dev_free(q3t_dev * c, void * p) {
+    if (!p) return;
+    auto it = std::find(c->allocs.begin(), c->allocs.end(), p);
+    if (it != c->allocs.end()) c->allocs.erase(it);
+    (void) hipFree(p);
+}
+
+void drop_graph(q3t_dev * c) {
+    if (c->frame_exec) { (void) hipGraphExecDestroy(c->frame_exec); c->frame_exec = nullptr; }
+    if (c->frame_graph) { (void) hipGraphDestroy(c->frame_graph); c->frame_graph = nullptr; }
+    c->frames_ready = false;
+}
+
+// Expected (ne0, ne1) of a named tensor; false if the name is not used by
+// the frame loop (the reference skips such names, src/tts_transformer.cpp:407-409).
+bool expected_shape(const q3t_config & g, const std::string & n, int64_t & ne0, int64_t & ne1,
+                    int & layer, int & cb, std::string & field, bool & is_cp) {
+    layer = -1; cb = -1; is_cp = false; field.clear(); ne1 = 1;
+    const int64_t d = g.hidden_size, qd = (int64_t) g.n_head * g.head_dim, kd = (int64_t) g.n_kv_head * g.head_dim;
+    if (n == "talker.text_embd.weight") { ne0 = g.text_embd_dim; ne1 = g.text_vocab; return true; }
+    if (n == "talker.text_proj.fc1.weight") { ne0 = g.text_embd_dim; ne1 = g.text_embd_dim; return true; }
+    if (n == "talker.text_proj.fc1.bias") { ne0 = g.text_embd_dim; return true; }
+    if (n == "talker.text_proj.fc2.weight") { ne0 = g.text_embd_dim; ne1 = d; return true; }
+    if (n == "talker.text_proj.fc2.bias") { ne0 = d; return true; }
+    if (n == "talker.codec_embd.weight" || n == "talker.codec_head.weight") { ne0 = d; ne1 = g.codec_vocab; return true; }
+    if (n == "talker.output_norm.weight" || n == "code_pred.output_norm.weight") { ne0 = d; return true; }
+    int idx = -1; char buf[64] = {0};
+    const char * s = n.c_str();
+    if (std::sscanf(s, "code_pred.codec_embd.%d.weight", &idx) == 1) {
+        if (idx < 0 || idx >= g.n_codebooks - 1) return false;
+        cb = idx; field = "cp_embd"; ne0 = d; ne1 = g.cp_vocab; return true;
+    }
+    if (std::sscanf(s, "code_pred.lm_head.%d.weight", &idx) == 1) {
+        if (idx < 0 || idx >= g.n_codebooks - 1) return false;
+        cb = idx; field = "cp_head"; ne0 = d; ne1 = g.cp_vocab; return true;
+    }
+    int nl = 0, ffn = 0;
+    if (std::sscanf(s, "talker.blk.%d.%63s", &idx, buf) == 2) { nl = g.n_layers; ffn = g.ffn_size; }
+    else if (std::sscanf(s, "code_pred.blk.%d.%63s", &idx, buf) == 2) { nl = g.cp_layers; ffn = g.cp_ffn; is_cp = true; }
+    else return false;
+    if (idx < 0 || idx >= nl) return false;
+    layer = idx;
+    field = buf;
+    if (field == "attn_norm.weight" || field == "ffn_norm.weight") { ne0 = d; return true; }
+    if (field == "attn_q_norm.weight" || field == "attn_k_norm.weight") { ne0 = g.head_dim; return true; }
+    if (field == "attn_q.weight") { ne0 = d; ne1 = qd; return true; }
+    if (field == "attn_k.weight" || field == "attn_v.weight") { ne0 = d; ne1 = kd; return true; }
+    if (field == "attn_output.weight") { ne0 = qd; ne1 = d; return true; }
+    if (field == "ffn_gate.weight" || field == "ffn_up.weight") { ne0 = d; ne1 = ffn; return true; }
+    if (field == "ffn_down.weight") { ne0 = ffn; ne1 = d; return true; }
+    return false;
+}
+
+size_t type_bytes(int type, int64_t ne0, int64_t ne1) {
+    const int64_t n = ne0 * ne1;
+    if (type == Q3T_TYPE_Q8_0) return (size_t) (n / 32) * 34;
+    if (type == Q3T_TYPE_F16) return (size_t) n * 2;
+    return (size_t) n * 4;
+}
+
+// Repack ggml Q8_0 blocks (fp16 d + 32 int8) into split arrays and copy.
+int upload_rows(q3t_dev * c, Slot & s, int64_t row0, int type, int64_t ne0, int64_t ne1, const void * data) {
+    if (type == Q3T_TYPE_Q8_0) {
+        const int64_t nb = ne0 / 32;
+        std::vector<int8_t> q((size_t) (ne0 * ne1));
+        std::vector<uint16_t> d((size_t) (nb * ne1));
+        const uint8_t * src = (const uint8_t *) data;
+        for (int64_t b = 0; b < nb * ne1; ++b) {
+            std::memcpy(&d[b], src + b * 34, 2);
+            std::memcpy(&q[b * 32], src + b * 34 + 2, 32);
+        }
+        HIP_OK(hipMemcpy((int8_t *) s.data + row0 * ne0, q.data(), q.size(), hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(s.scales + row0 * nb, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+    } else {
+        const size_t eb = type == Q3T_TYPE_F16 ? 2 : 4;
+        HIP_OK(hipMemcpy((char *) s.data + row0 * ne0 * eb, data, (size_t) (ne0 * ne1) * eb, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+int alloc_slot(q3t_dev * c, Slot & s, int type, int64_t ne0, int64_t ne1) {
+    s.type = type; s.ne0 = ne0; s.ne1 = ne1;
+    if (type == Q3T_TYPE_Q8_0) {
+        if (dev_alloc(c, &s.data, (size_t) (ne0 * ne1))) return -1;
+        void * sc = nullptr;
+        if (dev_alloc(c, &sc, (size_t) (ne0 / 32 * ne1) * 2)) return -1;
+        s.scales = (uint16_t *) sc;
+    } else {
+        if (dev_alloc(c, &s.data, type_bytes(type, ne0, ne1))) return -1;
+    }
+    return 0;
+}
+
+Weight weight_of(const Slot & s, bool widen_f16 = false) {
+    Weight w;
+    w.kind = s.type == Q3T_TYPE_Q8_0 ? W_Q8 : (widen_f16 ? W_F16W : W_F16);
+    w.w = s.data; w.d = s.scales;
+    return w;
+}
+
+int resolve(q3t_dev * c) {
+    if (c->resolved) return 0;
+    const q3t_config & g = c->cfg;
+    auto need = [&](const Slot & s, const char * what) -> int {
+        if (!s.data) return fail(c, std::string("missing tensor: ") + what);
+        return 0;
+    };
+    for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
+        LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
+        char nm[64];
+        std::snprintf(nm, sizeof nm, "%s.blk.%d", i < g.n_layers ? "talker" : "code_pred", i < g.n_layers ? i : i - g.n_layers);
+        if (L.qkv_parts != 7) return fail(c, std::string("missing attn_q/k/v in ") + nm);
+        if (need(L.wo, nm) || need(L.wg, nm) || need(L.wu, nm) || need(L.wd, nm)) return -1;
+        if (!L.attn_norm || !L.ffn_norm || !L.q_norm || !L.k_norm) return fail(c, std::string("missing norm in ") + nm);
+        if (L.wg.type != L.wu.type) return fail(c, std::string("ffn_gate/ffn_up types differ in ") + nm);
+    }
+    for (int i = 0; i < g.n_codebooks - 1; ++i) {
+        if (!c->cp_embd[i].data || !c->cp_head[i].data) return fail(c, "missing code_pred.codec_embd/lm_head " + std::to_string(i));
+        if (c->cp_embd[i].type != Q3T_TYPE_F16 || c->cp_head[i].type != Q3T_TYPE_F16)
+            return fail(c, "code_pred embeddings and heads must be F16");
+    }
+    if (need(c->codec_embd, "talker.codec_embd.weight") || need(c->codec_head, "talker.codec_head.weight") ||
+        need(c->out_norm, "talker.output_norm.weight") || need(c->cp_out_norm, "code_pred.output_norm.weight"))
+        return -1;
+    if (c->codec_embd.type != Q3T_TYPE_F16 || c->codec_head.type != Q3T_TYPE_F16)
+        return fail(c, "talker.codec_embd / codec_head must be F16");
+    c->resolved = true;
+    return 0;
+}
+
+// ------------------------------------------------------------ launches
+struct GemvSpec {
+    Weight w, w2;
+    int rows, K;
+    const float * x; int x_stride;
+    const float * norm_w = nullptr;
+    float * hidden_out = nullptr; int hidden_stride = 0;
+    float * y; int y_stride;
+    const float * resid = nullptr; int resid_stride = 0;
+    const float * bias = nullptr;
+    int epi = EPI_STORE;
+};
+
+template <int WT, int NT, bool DUAL>
+void launch_gemv_t(q3t_dev * c, const GemvArgs & a) {
+    const int BPR = a.K / kQK, LPR = BPR < 32 ? BPR : 32, RPW = 64 / LPR;
+    const int groups = a.rows / RPW;
+    int grid = (groups + 3) / 4;
+    grid = std::max(1, std::min(grid, 2048));
+    const size_t lds = 64 + act_bytes<WT>(NT, a.K);
+    hipLaunchKernelGGL((k_gemv<WT, NT, DUAL>), dim3(grid), dim3(kBlock), lds, c->stream, a);
+}
+
+template <int WT, bool DUAL>
+void launch_gemv_nt(q3t_dev * c, const GemvArgs & a, int nt) {
+    switch (nt) {
+        case 1: launch_gemv_t<WT, 1, DUAL>(c, a); break;
+        case 2: launch_gemv_t<WT, 2, DUAL>(c, a); break;
+        default: launch_gemv_t<WT, 4, DUAL>(c, a); break;
+    }
+}
+
+void gemv(q3t_dev * c, const GemvSpec & s, int nt) {
+    GemvArgs a{};
+    a.w = s.w.w; a.wd = s.w.d; a.w2 = s.w2.w; a.w2d = s.w2.d;
+    a.rows = s.rows; a.K = s.K;
+    a.x = s.x; a.x_stride = s.x_stride;
+    a.norm_w = s.norm_w; a.eps = c->cfg.rms_eps;
+    a.hidden_out = s.hidden_out; a.hidden_stride = s.hidden_stride;
+    a.y = s.y; a.y_stride = s.y_stride;
+    a.resid = s.resid; a.resid_stride = s.resid_stride;
+    a.bias = s.bias;
+    a.done = &c->st->done;
+    a.pro = s.norm_w ? PRO_NORM : PRO_NONE;
+    a.epi = s.epi;
+    const bool dual = s.epi == EPI_SWIGLU;
+    switch (s.w.kind) {
+        case W_Q8: dual ? launch_gemv_nt<W_Q8, true>(c, a, nt) : launch_gemv_nt<W_Q8, false>(c, a, nt); break;
+        case W_F16: dual ? launch_gemv_nt<W_F16, true>(c, a, nt) : launch_gemv_nt<W_F16, false>(c, a, nt); break;
+        default: launch_gemv_nt<W_F16W, false>(c, a, nt); break;
+    }
+}
+
+struct AttnSpec {
+    const float * qkv; const LayerDev * L;
+    uint16_t * kc; uint16_t * vc; int n_ctx;
+    const float * rc; const float * rs;
+    const int32_t * pos_ptr; int pos_const;
+    float * probs = nullptr;
+};
+
+void attention(q3t_dev * c, const AttnSpec & s, int nt) {
+    const q3t_config & g = c->cfg;
+    AttnArgs a{};
+    a.qkv = s.qkv; a.qkv_stride = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
+    a.q_norm = s.L->q_norm; a.k_norm = s.L->k_norm; a.eps = g.rms_eps;
+    a.rope_cos = s.rc; a.rope_sin = s.rs;
+    a.kc = s.kc; a.vc = s.vc; a.n_ctx = s.n_ctx;
+    a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
+    a.pos_ptr = s.pos_ptr; a.pos_const = s.pos_const;
+    a.out = c->attn; a.out_stride = g.n_head * g.head_dim;
+    a.done = &c->st->done;
+    a.scale = 1.0f / std::sqrt((float) g.head_dim);
+    a.nt = nt;
+    a.probs_out = s.probs;
+    hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt), dim3(kBlock), attn_lds_bytes(s.n_ctx), c->stream, a);
+}
+
+// One transformer block over nt tokens; input rows `xin` (stride d),
+// output rows left in c->xa.
+void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int ffn, uint16_t * kc, uint16_t * vc,
+           int n_ctx, const float * rc, const float * rs, const int32_t * pos_ptr, int pos_const) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    GemvSpec s{};
+    s.w = weight_of(L.qkv); s.rows = qkvd; s.K = d; s.x = xin; s.x_stride = d; s.norm_w = L.attn_norm;
+    s.y = c->qkv; s.y_stride = qkvd;
+    gemv(c, s, nt);
+    AttnSpec as{c->qkv, &L, kc, vc, n_ctx, rc, rs, pos_ptr, pos_const};
+    attention(c, as, nt);
+    GemvSpec o{};
+    o.w = weight_of(L.wo); o.rows = d; o.K = qd; o.x = c->attn; o.x_stride = qd;
+    o.y = c->xb; o.y_stride = d; o.resid = xin; o.resid_stride = d; o.epi = EPI_RESID;
+    gemv(c, o, nt);
+    GemvSpec f{};
+    f.w = weight_of(L.wg); f.w2 = weight_of(L.wu); f.rows = ffn; f.K = d; f.x = c->xb; f.x_stride = d;
+    f.norm_w = L.ffn_norm; f.y = c->ffn; f.y_stride = ffn; f.epi = EPI_SWIGLU;
+    gemv(c, f, nt);
+    GemvSpec dn{};
+    dn.w = weight_of(L.wd, true); dn.rows = d; dn.K = ffn; dn.x = c->ffn; dn.x_stride = ffn;
+    dn.y = c->xa; dn.y_stride = d; dn.resid = c->xb; dn.resid_stride = d; dn.epi = EPI_RESID;
+    gemv(c, dn, nt);
+}
+
+// Talker forward of nt (<= 4) tokens whose input rows are `xin`.  The
+// codec head runs on the last row when `head` is set (normed hidden of that
+// row -> c->hidden, logits -> c->logits).
+void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_ptr, int pos_const, bool head) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size;
+    const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
+    for (int il = 0; il < g.n_layers; ++il)
+        layer(c, c->talker[il], il == 0 ? xin : c->xa, nt, g.ffn_size, c->kc + il * lstride, c->vc + il * lstride,
+              c->n_ctx, c->rope_cos, c->rope_sin, pos_ptr, pos_const);
+    if (head) {
+        GemvSpec h{};
+        h.w = weight_of(c->codec_head); h.rows = g.codec_vocab; h.K = d;
+        h.x = c->xa + (size_t) (nt - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
+        h.hidden_out = c->hidden; h.hidden_stride = d; h.y = c->logits; h.y_stride = g.codec_vocab;
+        gemv(c, h, 1);
+    }
+}
+
+// Code predictor for the frame in c->st (codes[0] set), reading the talker's
+// normed hidden from c->hidden; fills st->codes[1..15] and c->cp_logits.
+void code_pred_seq(q3t_dev * c) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size;
+    const size_t lstride = (size_t) g.n_kv_head * 16 * g.head_dim;
+    EmbedArgs e{};
+    e.st = c->st; e.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; i < g.n_codebooks - 1; ++i) e.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    e.hidden = c->hidden; e.trailing = c->trailing; e.n_trailing = c->n_trailing; e.pad = c->pad;
+    e.x = c->stage; e.d = d;
+    const dim3 eg((d + kBlock - 1) / kBlock);
+    SampleArgs sa{};
+    sa.vocab = g.cp_vocab; sa.mode = 1; sa.params = c->params; sa.st = c->st; sa.seen = c->seen; sa.eos_id = g.codec_eos_id;
+    for (int step = 0; step < g.n_codebooks - 1; ++step) {
+        const int nt = step == 0 ? 2 : 1;
+        e.mode = step == 0 ? 0 : 1;
+        e.group = step + 1;
+        hipLaunchKernelGGL(k_embed, eg, dim3(kBlock), 0, c->stream, e);
+        const int pos = step == 0 ? 0 : step + 1;
+        for (int il = 0; il < g.cp_layers; ++il)
+            layer(c, c->cp[il], il == 0 ? c->stage : c->xa, nt, g.cp_ffn, c->cpk + il * lstride, c->cpv + il * lstride,
+                  16, c->cp_rope_cos, c->cp_rope_sin, nullptr, pos);
+        GemvSpec h{};
+        h.w = weight_of(c->cp_head[step]); h.rows = g.cp_vocab; h.K = d;
+        h.x = c->xa + (size_t) (nt - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->cp_out_norm.data;
+        h.y = c->cp_logits + (size_t) step * g.cp_vocab; h.y_stride = g.cp_vocab;
+        gemv(c, h, 1);
+        sa.logits = c->cp_logits + (size_t) step * g.cp_vocab;
+        sa.group = step + 1;
+        hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
+    }
+}
+
+// One whole frame: cb0 sample, code predictor, step embedding, talker step,
+// emit.  Everything reads its dynamic inputs from c->st.
+void frame_seq(q3t_dev * c) {
+    const q3t_config & g = c->cfg;
+    SampleArgs sa{};
+    sa.logits = c->logits; sa.vocab = g.codec_vocab; sa.mode = 0; sa.group = 0;
+    sa.params = c->params; sa.st = c->st; sa.seen = c->seen; sa.eos_id = g.codec_eos_id;
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
+    code_pred_seq(c);
+    EmbedArgs e{};
+    e.mode = 2; e.st = c->st; e.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; i < g.n_codebooks - 1; ++i) e.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    e.hidden = c->hidden; e.trailing = c->trailing; e.n_trailing = c->n_trailing; e.pad = c->pad;
+    e.x = c->stage; e.d = g.hidden_size;
+    hipLaunchKernelGGL(k_embed, dim3((g.hidden_size + kBlock - 1) / kBlock), dim3(kBlock), 0, c->stream, e);
+    talker_chunk(c, c->stage, 1, &c->st->n_past, 0, true);
+    hipLaunchKernelGGL(k_frame_end, dim3(1), dim3(64), 0, c->stream, c->st, c->codes_out, g.n_codebooks);
+}
+
+int set_state(q3t_dev * c, const FrameState & s) {
+    HIP_OK(hipMemcpyAsync(c->st, &s, sizeof s, hipMemcpyHostToDevice, c->stream));
+    return 0;
+}
+
+int ensure_stage(q3t_dev * c, int rows) {
+    if (rows <= c->stage_rows) return 0;
+    dev_free(c, c->stage);
+    c->stage = nullptr;
+    const int r = std::max(rows, 16);
+    if (dev_alloc_t(c, &c->stage, (size_t) r * std::max(c->cfg.hidden_size, c->cfg.text_embd_dim))) return -1;
+    c->stage_rows = r;
+    drop_graph(c);
+    return 0;
+}
+
+int check_ready(q3t_dev * c) {
+    if (resolve(c)) return -1;
+    if (!c->kc) return fail(c, "KV cache not reserved");
+    return 0;
+}
+
+int sync(q3t_dev * c) {
+    HIP_OK(hipStreamSynchronize(c->stream));
+    HIP_OK(hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+
+// =================================================================== C ABI
+extern "C" {
+
+int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
+    if (!cfg || !out) return -1;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return -2;
+    if (device < 0 || device >= n) return -3;
+    q3t_dev * c = new q3t_dev();
+    c->cfg = *cfg;
+    c->device = device;
+    const q3t_config & g = c->cfg;
+    auto bad = [&](const char * m) { c->err = m; *out = c; return -1; };
+    if (g.head_dim != 128) return bad("head_dim must be 128");
+    if (g.cp_hidden != g.hidden_size) return bad("code predictor width must equal talker width (mtp_proj unsupported)");
+    if (g.hidden_size % 256 || g.ffn_size % 256 || g.cp_ffn % 256 || g.text_embd_dim % 256)
+        return bad("hidden/ffn/text widths must be multiples of 256");
+    auto ok_k = [](int k) { int b = k / 32; return b % 32 == 0 || (b <= 32 && (b & (b - 1)) == 0); };
+    if (!ok_k(g.hidden_size) || !ok_k(g.ffn_size) || !ok_k(g.cp_ffn) || !ok_k(g.text_embd_dim) ||
+        !ok_k(g.n_head * g.head_dim))
+        return bad("unsupported reduction width");
+    if (g.n_head % g.n_kv_head) return bad("n_head must be a multiple of n_kv_head");
+    if (g.codec_vocab > kMaxVocab || g.cp_vocab > kMaxVocab) return bad("vocabulary too large for the on-device sampler");
+    if (g.codec_vocab < 1024 || g.n_codebooks != 16) return bad("codec vocabulary must be >= 1024 with 16 codebooks");
+    if (hipSetDevice(device) != hipSuccess) return bad("hipSetDevice failed");
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bad("hipStreamCreate failed");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->n_cu = prop.multiProcessorCount;
+    c->talker.resize(g.n_layers);
+    c->cp.resize(g.cp_layers);
+    c->cp_embd.resize(g.n_codebooks - 1);
+    c->cp_head.resize(g.n_codebooks - 1);
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim;
+    const int wide = std::max({d, g.text_embd_dim, g.ffn_size, g.cp_ffn});
+    int rc = 0;
+    rc |= dev_alloc_t(c, &c->xa, (size_t) 4 * wide);
+    rc |= dev_alloc_t(c, &c->xb, (size_t) 4 * wide);
+    rc |= dev_alloc_t(c, &c->qkv, (size_t) 4 * (qd + 2 * kd));
+    rc |= dev_alloc_t(c, &c->attn, (size_t) 4 * qd);
+    rc |= dev_alloc_t(c, &c->ffn, (size_t) 4 * wide);
+    rc |= dev_alloc_t(c, &c->tp_a, (size_t) 4 * wide);
+    rc |= dev_alloc_t(c, &c->tp_b, (size_t) 4 * wide);
+    rc |= dev_alloc_t(c, &c->hidden, (size_t) 4 * d);
+    rc |= dev_alloc_t(c, &c->logits, (size_t) g.codec_vocab);
+    rc |= dev_alloc_t(c, &c->cp_logits, (size_t) (g.n_codebooks - 1) * g.cp_vocab);
+    rc |= dev_alloc_t(c, &c->st, 1);
+    rc |= dev_alloc_t(c, &c->params, 1);
+    rc |= dev_alloc_t(c, &c->seen, (size_t) g.codec_vocab);
+    rc |= dev_alloc_t(c, &c->pad, (size_t) d);
+    rc |= dev_alloc_t(c, &c->trailing, (size_t) d);
+    rc |= dev_alloc_t(c, &c->codes_out, (size_t) 16);
+    rc |= dev_alloc_t(c, &c->probs, (size_t) g.n_head * 16384);
+    c->trailing_cap = 1; c->codes_cap = 1;
+    rc |= ensure_stage(c, 16);
+    if (rc) { *out = c; return -1; }
+    FrameState s{};
+    s.max_frames = 0;
+    if (set_state(c, s) || sync(c)) { *out = c; return -1; }
+    *out = c;
+    return 0;
+}
+
+void q3t_dev_destroy(q3t_dev * c) {
+    if (!c) return;
+    (void) hipSetDevice(c->device);
+    if (c->stream) (void) hipStreamSynchronize(c->stream);
+    drop_graph(c);
+    for (void * p : c->allocs) (void) hipFree(p);
+    if (c->stream) (void) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char * q3t_dev_last_error(const q3t_dev * c) { return c ? c->err.c_str() : "null context"; }
+
+int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const int64_t ne[4], const void * data,
+                          size_t nbytes) {
+    if (!c || !name || !ne || !data) return -1;
+    int64_t e0, e1; int layer, cb; std::string field; bool is_cp;
+    if (!expected_shape(c->cfg, name, e0, e1, layer, cb, field, is_cp)) return 0;   // not on this path
+    if (type != Q3T_TYPE_F32 && type != Q3T_TYPE_F16 && type != Q3T_TYPE_Q8_0)
+        return fail(c, std::string("unsupported tensor type for ") + name);
+    if (ne[0] != e0 || ne[1] != e1 || ne[2] != 1 || ne[3] != 1)
+        return fail(c, std::string("shape mismatch for ") + name);
+    if (type == Q3T_TYPE_Q8_0 && e0 % 32) return fail(c, std::string("Q8_0 row not a multiple of 32: ") + name);
+    if (nbytes != type_bytes(type, e0, e1)) return fail(c, std::string("byte size mismatch for ") + name);
+    const bool is_matrix = e1 > 1;
+    if (!is_matrix && type != Q3T_TYPE_F32) return fail(c, std::string("1-D tensors must be F32: ") + name);
+    HIP_OK(hipSetDevice(c->device));
+    drop_graph(c);
+    c->resolved = false;
+    const q3t_config & g = c->cfg;
+    if (layer >= 0) {
+        LayerDev & L = is_cp ? c->cp[layer] : c->talker[layer];
+        if (field == "attn_q.weight" || field == "attn_k.weight" || field == "attn_v.weight") {
+            const int64_t qd = (int64_t) g.n_head * g.head_dim, kd = (int64_t) g.n_kv_head * g.head_dim;
+            if (!L.qkv.data) { if (alloc_slot(c, L.qkv, type, e0, qd + 2 * kd)) return -1; }
+            else if (L.qkv.type != type) return fail(c, std::string("attn_q/k/v must share one type: ") + name);
+            const int part = field == "attn_q.weight" ? 1 : field == "attn_k.weight" ? 2 : 4;
+            const int64_t row0 = part == 1 ? 0 : part == 2 ? qd : qd + kd;
+            if (upload_rows(c, L.qkv, row0, type, e0, e1, data)) return -1;
+            L.qkv_parts |= part;
+            Slot v = L.qkv; v.ne1 = e1;
+            v.data = type == Q3T_TYPE_Q8_0 ? (void *) ((int8_t *) L.qkv.data + row0 * e0)
+                                           : (void *) ((char *) L.qkv.data + row0 * e0 * (type == Q3T_TYPE_F16 ? 2 : 4));
+            if (v.scales) v.scales = L.qkv.scales + row0 * (e0 / 32);
+            c->slots[name] = v;
+            return 0;
+        }
+        Slot s;
+        if (alloc_slot(c, s, type, e0, e1) || upload_rows(c, s, 0, type, e0, e1, data)) return -1;
+        c->slots[name] = s;
+        if (field == "attn_output.weight") L.wo = s;
+        else if (field == "ffn_gate.weight") L.wg = s;
+        else if (field == "ffn_up.weight") L.wu = s;
+        else if (field == "ffn_down.weight") L.wd = s;
+        else if (field == "attn_norm.weight") L.attn_norm = (const float *) s.data;
+        else if (field == "ffn_norm.weight") L.ffn_norm = (const float *) s.data;
+        else if (field == "attn_q_norm.weight") L.q_norm = (const float *) s.data;
+        else if (field == "attn_k_norm.weight") L.k_norm = (const float *) s.data;
+        return 0;
+    }
+    Slot s;
+    if (alloc_slot(c, s, type, e0, e1) || upload_rows(c, s, 0, type, e0, e1, data)) return -1;
+    c->slots[name] = s;
+    const std::string n = name;
+    if (field == "cp_embd") c->cp_embd[cb] = s;
+    else if (field == "cp_head") c->cp_head[cb] = s;
+    else if (n == "talker.text_embd.weight") c->text_embd = s;
+    else if (n == "talker.text_proj.fc1.weight") c->fc1 = s;
+    else if (n == "talker.text_proj.fc1.bias") c->fc1_b = s;
+    else if (n == "talker.text_proj.fc2.weight") c->fc2 = s;
+    else if (n == "talker.text_proj.fc2.bias") c->fc2_b = s;
+    else if (n == "talker.codec_embd.weight") c->codec_embd = s;
+    else if (n == "talker.codec_head.weight") c->codec_head = s;
+    else if (n == "talker.output_norm.weight") c->out_norm = s;
+    else if (n == "code_pred.output_norm.weight") c->cp_out_norm = s;
+    return 0;
+}
+
+int q3t_dev_download_tensor(q3t_dev * c, const char * name, void * data, size_t nbytes) {
+    if (!c || !name || !data) return -1;
+    auto it = c->slots.find(name);
+    if (it == c->slots.end()) return fail(c, std::string("no such tensor: ") + name);
+    const Slot & s = it->second;
+    if (nbytes != type_bytes(s.type, s.ne0, s.ne1)) return fail(c, "byte size mismatch");
+    HIP_OK(hipSetDevice(c->device));
+    if (s.type == Q3T_TYPE_Q8_0) {
+        const int64_t nb = s.ne0 / 32;
+        std::vector<int8_t> q((size_t) (s.ne0 * s.ne1));
+        std::vector<uint16_t> d((size_t) (nb * s.ne1));
+        HIP_OK(hipMemcpy(q.data(), s.data, q.size(), hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(d.data(), s.scales, d.size() * 2, hipMemcpyDeviceToHost));
+        uint8_t * dst = (uint8_t *) data;
+        for (int64_t b = 0; b < nb * s.ne1; ++b) {
+            std::memcpy(dst + b * 34, &d[b], 2);
+            std::memcpy(dst + b * 34 + 2, &q[b * 32], 32);
+        }
+    } else {
+        HIP_OK(hipMemcpy(data, s.data, nbytes, hipMemcpyDeviceToHost));
+    }
+    return 0;
+}
+
+int q3t_dev_dequantize(q3t_dev * c, const char * name, float * out, size_t n_floats) {
+    if (!c || !name || !out) return -1;
+    auto it = c->slots.find(name);
+    if (it == c->slots.end()) return fail(c, std::string("no such tensor: ") + name);
+    const Slot & s = it->second;
+    if (s.type != Q3T_TYPE_Q8_0) return fail(c, "not a Q8_0 tensor");
+    const int64_t n = s.ne0 * s.ne1;
+    if ((int64_t) n_floats != n) return fail(c, "size mismatch");
+    HIP_OK(hipSetDevice(c->device));
+    float * tmp = nullptr;
+    HIP_OK(hipMalloc(&tmp, (size_t) n * 4));
+    hipLaunchKernelGGL(k_dequant_q8, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, c->stream,
+                       (const int8_t *) s.data, s.scales, n, tmp);
+    hipError_t e = hipMemcpyAsync(out, tmp, (size_t) n * 4, hipMemcpyDeviceToHost, c->stream);
+    hipError_t e2 = hipStreamSynchronize(c->stream);
+    (void) hipFree(tmp);
+    if (e != hipSuccess || e2 != hipSuccess) return fail(c, "dequantize failed");
+    return 0;
+}
+
+int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
+    if (!c) return -1;
+    const q3t_config & g = c->cfg;
+    if (n_ctx <= 0) return fail(c, "n_ctx must be > 0");
+    if (n_ctx > 12288) return fail(c, "n_ctx above 12288 is not supported by the decode attention kernel");
+    HIP_OK(hipSetDevice(c->device));
+    HIP_OK(hipStreamSynchronize(c->stream));
+    drop_graph(c);
+    dev_free(c, c->kc); dev_free(c, c->vc); dev_free(c, c->cpk); dev_free(c, c->cpv);
+    dev_free(c, c->rope_cos); dev_free(c, c->rope_sin); dev_free(c, c->cp_rope_cos); dev_free(c, c->cp_rope_sin);
+    c->kc = c->vc = c->cpk = c->cpv = nullptr;
+    const size_t kv = (size_t) g.n_layers * g.n_kv_head * n_ctx * g.head_dim;
+    const size_t ckv = (size_t) g.cp_layers * g.n_kv_head * 16 * g.head_dim;
+    if (dev_alloc_t(c, &c->kc, kv) || dev_alloc_t(c, &c->vc, kv) || dev_alloc_t(c, &c->cpk, ckv) ||
+        dev_alloc_t(c, &c->cpv, ckv))
+        return -1;
+    HIP_OK(hipMemsetAsync(c->kc, 0, kv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->vc, 0, kv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->cpk, 0, ckv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->cpv, 0, ckv * 2, c->stream));
+    // RoPE tables: theta_i = pos * base^(-2i/hd) by cumulative fp32 product
+    // (ggml_rope_cache_init), cos/sin from the C library, once per context.
+    const int rows = std::max(n_ctx, 16), half = g.head_dim / 2;
+    std::vector<float> tc((size_t) rows * half), ts((size_t) rows * half), cc((size_t) rows * half), cs((size_t) rows * half);
+    auto fill = [&](float base, std::vector<float> & co, std::vector<float> & si) {
+        const float theta_scale = std::pow(base, -2.0f / (float) g.head_dim);
+        for (int p = 0; p < rows; ++p) {
+            float theta = (float) p;
+            for (int i = 0; i < half; ++i) {
+                co[(size_t) p * half + i] = std::cos(theta);
+                si[(size_t) p * half + i] = std::sin(theta);
+                theta *= theta_scale;
+            }
+        }
+    };
+    fill(g.rope_theta, tc, ts);
+    fill(g.cp_rope_theta, cc, cs);
+    if (dev_alloc_t(c, &c->rope_cos, tc.size()) || dev_alloc_t(c, &c->rope_sin, ts.size()) ||
+        dev_alloc_t(c, &c->cp_rope_cos, cc.size()) || dev_alloc_t(c, &c->cp_rope_sin, cs.size()))
+        return -1;
+    HIP_OK(hipMemcpy(c->rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(c->rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(c->cp_rope_cos, cc.data(), cc.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(c->cp_rope_sin, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    c->n_ctx = n_ctx;
+    c->rope_rows = rows;
+    return sync(c);
+}
+
+int q3t_dev_kv_clear(q3t_dev * c) { return c ? 0 : -1; }
+
+int32_t q3t_dev_kv_capacity(const q3t_dev * c) { return c ? c->n_ctx : 0; }
+
+int q3t_dev_kv_write(q3t_dev * c, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v) {
+    if (!c || !k || !v) return -1;
+    const q3t_config & g = c->cfg;
+    if (!c->kc) return fail(c, "KV cache not reserved");
+    if (layer < 0 || layer >= g.n_layers || n_pos < 0 || n_pos > c->n_ctx) return fail(c, "kv_write out of range");
+    HIP_OK(hipSetDevice(c->device));
+    const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
+    std::vector<uint16_t> tk((size_t) n_pos * g.head_dim);
+    for (int h = 0; h < g.n_kv_head; ++h) {
+        for (int which = 0; which < 2; ++which) {
+            const uint16_t * src = which ? v : k;
+            for (int p = 0; p < n_pos; ++p)
+                std::memcpy(&tk[(size_t) p * g.head_dim], src + ((size_t) p * g.n_kv_head + h) * g.head_dim,
+                            g.head_dim * 2);
+            uint16_t * dst = (which ? c->vc : c->kc) + layer * lstride + (size_t) h * c->n_ctx * g.head_dim;
+            HIP_OK(hipMemcpy(dst, tk.data(), tk.size() * 2, hipMemcpyHostToDevice));
+        }
+    }
+    return 0;
+}
+
+int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, float * hidden_out, float * logits_out) {
+    if (!c || !embd) return -1;
+    if (n <= 0) return fail(c, "n_tokens must be > 0");
+    HIP_OK(hipSetDevice(c->device));
+    if (check_ready(c)) return -1;
+    if (n_past < 0 || n_past + n > c->n_ctx) return fail(c, "Context length exceeded");
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size;
+    if (ensure_stage(c, n)) return -1;
+    if (hidden_out && n > c->hidden_all_rows) {
+        dev_free(c, c->hidden_all);
+        c->hidden_all = nullptr;
+        if (dev_alloc_t(c, &c->hidden_all, (size_t) n * d)) return -1;
+        c->hidden_all_rows = n;
+    }
+    FrameState s{};
+    if (set_state(c, s)) return -1;
+    HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) n * d * 4, hipMemcpyHostToDevice, c->stream));
+    for (int t0 = 0; t0 < n;) {
+        const int left = n - t0;
+        const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        const bool last = t0 + nt == n;
+        talker_chunk(c, c->stage + (size_t) t0 * d, nt, nullptr, n_past + t0, last);
+        if (hidden_out)
+            hipLaunchKernelGGL(k_rmsnorm_rows, dim3(nt), dim3(kBlock), 0, c->stream, c->xa,
+                               (const float *) c->out_norm.data, g.rms_eps, d, c->hidden_all + (size_t) t0 * d);
+        t0 += nt;
+    }
+    if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden_all, (size_t) n * d * 4, hipMemcpyDeviceToHost, c->stream));
+    if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float * logits_out, float * hidden_out) {
+    if (!c || !embd) return fail(c, "step_embd is null");
+    HIP_OK(hipSetDevice(c->device));
+    if (check_ready(c)) return -1;
+    if (n_past < 0 || n_past + 1 > c->n_ctx) return fail(c, "Context length exceeded");
+    const q3t_config & g = c->cfg;
+    FrameState s{};
+    s.n_past = n_past;
+    if (set_state(c, s)) return -1;
+    HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
+    talker_chunk(c, c->stage, 1, &c->st->n_past, 0, true);
+    if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden, (size_t) g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_sampling * sampling, uint32_t frame,
+                      int32_t * codes_out, float * logits_out) {
+    if (!c || !hidden || !codes_out) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (resolve(c)) return -1;
+    if (!c->cpk) return fail(c, "KV cache not reserved");
+    const q3t_config & g = c->cfg;
+    if (cb0 < 0 || cb0 >= g.codec_vocab) return fail(c, "Embedding token ID out of range");
+    SampleParams p{};
+    p.temperature = sampling ? sampling->temperature : 0.0f;
+    p.top_k = sampling ? sampling->top_k : 0;
+    p.rep_penalty = 1.0f;
+    p.seed = sampling ? sampling->seed : 0;
+    HIP_OK(hipMemcpyAsync(c->params, &p, sizeof p, hipMemcpyHostToDevice, c->stream));
+    FrameState s{};
+    s.codes[0] = cb0;
+    s.frame = (int32_t) frame;
+    if (set_state(c, s)) return -1;
+    HIP_OK(hipMemcpyAsync(c->hidden, hidden, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
+    code_pred_seq(c);
+    FrameState r{};
+    HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
+    if (logits_out)
+        HIP_OK(hipMemcpyAsync(logits_out, c->cp_logits, (size_t) (g.n_codebooks - 1) * g.cp_vocab * 4,
+                              hipMemcpyDeviceToHost, c->stream));
+    if (sync(c)) return -1;
+    for (int i = 0; i < g.n_codebooks - 1; ++i) codes_out[i] = r.codes[i + 1];
+    return 0;
+}
+
+int q3t_dev_text_proj(q3t_dev * c, const int32_t * tokens, int32_t n, float * out) {
+    if (!c || !tokens || !out) return -1;
+    if (n <= 0) return 0;
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    if (!c->text_embd.data || !c->fc1.data || !c->fc1_b.data || !c->fc2.data || !c->fc2_b.data)
+        return fail(c, "text projection tensors missing");
+    if (c->text_embd.type != Q3T_TYPE_F16) return fail(c, "talker.text_embd must be F16");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= g.text_vocab) return fail(c, "Embedding token ID out of range");
+    if (n > c->ids_cap) {
+        dev_free(c, c->ids);
+        c->ids = nullptr;
+        if (dev_alloc_t(c, &c->ids, (size_t) n)) return -1;
+        c->ids_cap = n;
+    }
+    if (ensure_stage(c, n)) return -1;
+    FrameState s{};
+    if (set_state(c, s)) return -1;
+    HIP_OK(hipMemcpyAsync(c->ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
+    const int te = g.text_embd_dim, d = g.hidden_size;
+    hipLaunchKernelGGL(k_gather_rows, dim3((te + 255) / 256, n), dim3(256), 0, c->stream,
+                       (const uint16_t *) c->text_embd.data, (int64_t) te, c->ids, n, c->stage);
+    std::vector<float> tmp;
+    for (int t0 = 0; t0 < n;) {
+        const int left = n - t0;
+        const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        GemvSpec a{};
+        a.w = weight_of(c->fc1); a.rows = te; a.K = te; a.x = c->stage + (size_t) t0 * te; a.x_stride = te;
+        a.y = c->tp_a; a.y_stride = te; a.bias = (const float *) c->fc1_b.data; a.epi = EPI_BIAS_SILU;
+        gemv(c, a, nt);
+        GemvSpec b{};
+        b.w = weight_of(c->fc2); b.rows = d; b.K = te; b.x = c->tp_a; b.x_stride = te;
+        b.y = c->tp_b; b.y_stride = d; b.bias = (const float *) c->fc2_b.data; b.epi = EPI_BIAS;
+        gemv(c, b, nt);
+        HIP_OK(hipMemcpyAsync(out + (size_t) t0 * d, c->tp_b, (size_t) nt * d * 4, hipMemcpyDeviceToHost, c->stream));
+        t0 += nt;
+    }
+    return sync(c);
+}
+
+int q3t_dev_embed_rows(q3t_dev * c, int32_t table, int32_t index, const int32_t * tokens, int32_t n, float * out) {
+    if (!c || !tokens || !out) return -1;
+    if (n <= 0) return 0;
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    const Slot * s = nullptr;
+    int64_t vocab = 0;
+    if (table == 0) { s = &c->codec_embd; vocab = g.codec_vocab; }
+    else if (table == 1) {
+        if (index < 0 || index >= g.n_codebooks - 1) return fail(c, "codebook index out of range");
+        s = &c->cp_embd[index]; vocab = g.cp_vocab;
+    } else { s = &c->text_embd; vocab = g.text_vocab; }
+    if (!s->data) return fail(c, "Embedding tensor not found");
+    if (s->type != Q3T_TYPE_F16) return fail(c, "embedding tables must be F16");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= vocab) return fail(c, "Embedding token ID out of range");
+    if (n > c->ids_cap) {
+        dev_free(c, c->ids);
+        c->ids = nullptr;
+        if (dev_alloc_t(c, &c->ids, (size_t) n)) return -1;
+        c->ids_cap = n;
+    }
+    const int64_t dim = s->ne0;
+    float * tmp = nullptr;
+    HIP_OK(hipMalloc(&tmp, (size_t) n * dim * 4));
+    HIP_OK(hipMemcpyAsync(c->ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned) ((dim + 255) / 256), n), dim3(256), 0, c->stream,
+                       (const uint16_t *) s->data, dim, c->ids, n, tmp);
+    hipError_t e = hipMemcpyAsync(out, tmp, (size_t) n * dim * 4, hipMemcpyDeviceToHost, c->stream);
+    hipError_t e2 = hipStreamSynchronize(c->stream);
+    (void) hipFree(tmp);
+    if (e != hipSuccess || e2 != hipSuccess) return fail(c, "embedding lookup failed");
+    return 0;
+}
+
+int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
+    if (!c || !a) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (check_ready(c)) return -1;
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size;
+    if (!a->tts_pad) return fail(c, "tts_pad row is null");
+    if (a->n_trailing < 0 || (a->n_trailing > 0 && !a->trailing)) return fail(c, "bad trailing rows");
+    if (a->max_len < 0) return fail(c, "max_len must be >= 0");
+    if (a->n_past < 1 || a->n_past + a->max_len > c->n_ctx) return fail(c, "Context length exceeded");
+    if (a->max_len > c->codes_cap) {
+        dev_free(c, c->codes_out);
+        c->codes_out = nullptr;
+        if (dev_alloc_t(c, &c->codes_out, (size_t) a->max_len * g.n_codebooks)) return -1;
+        c->codes_cap = a->max_len;
+        drop_graph(c);
+    }
+    if (a->n_trailing > c->trailing_cap) {
+        dev_free(c, c->trailing);
+        c->trailing = nullptr;
+        if (dev_alloc_t(c, &c->trailing, (size_t) a->n_trailing * d)) return -1;
+        c->trailing_cap = a->n_trailing;
+        drop_graph(c);
+    }
+    if (c->n_trailing != a->n_trailing) drop_graph(c);
+    c->n_trailing = a->n_trailing;
+    if (a->n_trailing)
+        HIP_OK(hipMemcpyAsync(c->trailing, a->trailing, (size_t) a->n_trailing * d * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->pad, a->tts_pad, (size_t) d * 4, hipMemcpyHostToDevice, c->stream));
+    SampleParams p{};
+    p.temperature = a->sampling.temperature;
+    p.top_k = a->sampling.top_k;
+    p.rep_penalty = a->repetition_penalty;
+    p.eos_bias = a->eos_bias;
+    p.target_frames = a->target_frames;
+    p.seed = a->sampling.seed;
+    HIP_OK(hipMemcpyAsync(c->params, &p, sizeof p, hipMemcpyHostToDevice, c->stream));
+    FrameState s{};
+    s.n_past = a->n_past;
+    s.max_frames = a->max_len;
+    if (set_state(c, s)) return -1;
+    HIP_OK(hipMemsetAsync(c->seen, 0, (size_t) g.codec_vocab, c->stream));
+    if (sync(c)) return -1;
+    if (!c->frame_exec) {
+        HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        frame_seq(c);
+        hipGraph_t graph = nullptr;
+        HIP_OK(hipStreamEndCapture(c->stream, &graph));
+        c->frame_graph = graph;
+        HIP_OK(hipGraphInstantiate(&c->frame_exec, graph, nullptr, nullptr, 0));
+    }
+    c->host_emitted = 0;
+    c->frames_launched = 0;
+    c->frames_max = a->max_len;
+    c->frames_ready = true;
+    return 0;
+}
+
+int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32_t * n_emitted_out, int32_t * eos_out) {
+    if (!c) return -1;
+    if (!c->frames_ready) return fail(c, "frames_begin not called");
+    HIP_OK(hipSetDevice(c->device));
+    n_frames = std::max(0, std::min(n_frames, c->frames_max - c->frames_launched));
+    for (int i = 0; i < n_frames; ++i) HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
+    c->frames_launched += n_frames;
+    FrameState r{};
+    HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
+    if (sync(c)) return -1;
+    const int ncb = c->cfg.n_codebooks;
+    const int fresh = r.n_emitted - c->host_emitted;
+    if (fresh > 0 && codes_out)
+        HIP_OK(hipMemcpy(codes_out, c->codes_out + (size_t) c->host_emitted * ncb, (size_t) fresh * ncb * 4,
+                         hipMemcpyDeviceToHost));
+    c->host_emitted = r.n_emitted;
+    if (n_emitted_out) *n_emitted_out = fresh;
+    if (eos_out) *eos_out = r.eos;
+    return 0;
+}
+
+int q3t_dev_sync(q3t_dev * c) {
+    if (!c) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    return sync(c);
+}
+
+int q3t_dev_time_kernel(q3t_dev * c, int32_t which, int32_t iters, double * avg_us_out, double * bytes_out) {
+    if (!c || iters <= 0) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (check_ready(c)) return -1;
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim;
+    const LayerDev & L = c->talker[0];
+    auto wbytes = [](const Slot & s) { return (double) type_bytes(s.type, s.ne0, s.ne1); };
+    double bytes = 0.0;
+    GemvSpec s{};
+    const int pos = std::min(c->n_ctx - 1, 512);
+    if (which < 0 || which > 4) return fail(c, "unknown kernel class");
+    {
+        FrameState st{};
+        st.n_past = pos;
+        if (set_state(c, st)) return -1;
+    }
+    auto enqueue = [&]() {
+        switch (which) {
+            case 0:
+                s = GemvSpec{}; s.w = weight_of(L.wg); s.w2 = weight_of(L.wu); s.rows = g.ffn_size; s.K = d;
+                s.x = c->xb; s.x_stride = d; s.norm_w = L.ffn_norm; s.y = c->ffn; s.y_stride = g.ffn_size; s.epi = EPI_SWIGLU;
+                gemv(c, s, 1);
+                bytes = wbytes(L.wg) + wbytes(L.wu);
+                break;
+            case 1:
+                s = GemvSpec{}; s.w = weight_of(L.qkv); s.rows = qd + 2 * kd; s.K = d; s.x = c->xa; s.x_stride = d;
+                s.norm_w = L.attn_norm; s.y = c->qkv; s.y_stride = qd + 2 * kd;
+                gemv(c, s, 1);
+                bytes = wbytes(L.qkv);
+                break;
+            case 2:
+                s = GemvSpec{}; s.w = weight_of(L.wd, true); s.rows = d; s.K = g.ffn_size; s.x = c->ffn; s.x_stride = g.ffn_size;
+                s.y = c->xa; s.y_stride = d; s.resid = c->xb; s.resid_stride = d; s.epi = EPI_RESID;
+                gemv(c, s, 1);
+                bytes = wbytes(L.wd);
+                break;
+            case 3:
+                s = GemvSpec{}; s.w = weight_of(L.wo); s.rows = d; s.K = qd; s.x = c->attn; s.x_stride = qd;
+                s.y = c->xb; s.y_stride = d; s.resid = c->xa; s.resid_stride = d; s.epi = EPI_RESID;
+                gemv(c, s, 1);
+                bytes = wbytes(L.wo);
+                break;
+            case 4: {
+                AttnSpec as{c->qkv, &L, c->kc, c->vc, c->n_ctx, c->rope_cos, c->rope_sin, &c->st->n_past, 0};
+                attention(c, as, 1);
+                bytes = 2.0 * (double) (pos + 1) * kd * 2;   // K and V rows read
+                break;
+            }
+            default:
+                break;
+        }
+    };
+    enqueue();   // warm-up
+    if (sync(c)) return -1;
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    HIP_OK(hipEventRecord(e0, c->stream));
+    for (int i = 0; i < iters; ++i) enqueue();
+    HIP_OK(hipEventRecord(e1, c->stream));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    (void) hipEventDestroy(e0);
+    (void) hipEventDestroy(e1);
+    if (avg_us_out) *avg_us_out = (double) ms * 1000.0 / iters;
+    if (bytes_out) *bytes_out = bytes;
+    return sync(c);
+}
+
+}  // extern "C"

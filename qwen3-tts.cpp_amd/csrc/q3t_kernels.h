@@ -1,0 +1,653 @@
+// q3t_kernels.h -- gfx950 kernels of the talker / code-predictor decode loop.
+//
+//   k_gemv        Q8_0 / F16 / F16-widened GEMV for 1, 2 or 4 tokens, with a
+//                 fused prologue (RMSNorm, activation quantisation into LDS)
+//                 and epilogue (store, residual add, bias, bias+SiLU, SwiGLU
+//                 of a gate/up pair).  Replaces ggml_rms_norm + ggml_mul +
+//                 ggml_mul_mat (+ ggml_add / ggml_silu / ggml_mul) at
+//                 src/tts_transformer.cpp:1656-1661, 1732-1750, 1755-1762.
+//   k_attention   QK-norm + NEOX RoPE + fp16 KV append + GQA decode attention
+//                 for one (query head, token); replaces :1667-1730.
+//   k_sample      codec-head / code-predictor sampler on device; replaces the
+//                 host sampler at :3109-3184 and sample_or_argmax :2750-2788.
+//   k_embed       embedding gathers and the step-embedding sum (:3264-3295,
+//                 :2790-2793, :2091).
+//   k_frame_end   emits the frame's 16 codes and advances n_past / frame.
+#pragma once
+
+#include "q3t_numerics.h"
+
+namespace q3t {
+
+enum WeightKind { W_Q8 = 0, W_F16 = 1, W_F16W = 2 };
+enum Prologue { PRO_NONE = 0, PRO_NORM = 1 };
+enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_BIAS = 2, EPI_BIAS_SILU = 3, EPI_SWIGLU = 4 };
+
+// Device-resident state of the frame loop (one per context).
+struct FrameState {
+    int32_t n_past;      // talker positions in the KV cache
+    int32_t frame;       // index of the frame being generated
+    int32_t done;        // 1 once EOS was sampled or max_frames were emitted: every kernel exits early
+    int32_t n_emitted;   // frames written to codes_out
+    int32_t codes[16];   // codes of the current frame
+    int32_t max_frames;  // capacity of codes_out (and of the KV positions reserved for the loop)
+    int32_t eos;         // 1 once codebook 0 sampled EOS
+    int32_t pad[2];
+};
+
+struct SampleParams {
+    float    temperature;
+    int32_t  top_k;
+    float    rep_penalty;
+    float    eos_bias;
+    int32_t  target_frames;
+    int32_t  pad;
+    uint64_t seed;
+};
+
+struct GemvArgs {
+    const void * w;  const uint16_t * wd;    // weight (int8 quants or fp16) + Q8_0 scales
+    const void * w2; const uint16_t * w2d;   // second (up) weight for EPI_SWIGLU
+    int32_t rows, K;
+    const float * x; int32_t x_stride;       // input rows [NT][x_stride]
+    const float * norm_w; float eps;         // PRO_NORM
+    float * hidden_out; int32_t hidden_stride;  // PRO_NORM: normed rows (block 0 writes)
+    float * y; int32_t y_stride;             // output rows [NT][y_stride]
+    const float * resid; int32_t resid_stride;
+    const float * bias;
+    const int32_t * done;
+    int32_t pro, epi;
+};
+
+// ------------------------------------------------------------------ GEMV
+// LDS: 4 doubles of reduction scratch, then the activation of NT tokens:
+//   W_Q8  : int8 [NT][K] then float scale [NT][K/32] (fp16-rounded d)
+//   W_F16 : fp16 [NT][K] (activation rounded to fp16)
+//   W_F16W: fp32 [NT][K]
+template <int WT>
+__host__ __device__ constexpr size_t act_bytes(int nt, int k) {
+    return WT == W_Q8 ? (size_t) nt * k + (size_t) nt * (k / kQK) * 4
+         : WT == W_F16 ? (size_t) nt * k * 2 : (size_t) nt * k * 4;
+}
+
+template <int WT, int NT>
+__device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char * act) {
+    const int K = a.K, t = threadIdx.x;
+    for (int tok = 0; tok < NT; ++tok) {
+        const float * x = a.x + (size_t) tok * a.x_stride;
+        float scale = 1.0f;
+        if (a.pro == PRO_NORM) {
+            double ss = 0.0;
+            for (int e = t; e < K; e += kBlock) { const float v = x[e]; ss += (double) (v * v); }
+            const double tot = block_sum_d(ss, red);
+            const float mean = (float) (tot / (double) K);
+            scale = 1.0f / sqrtf(mean + a.eps);
+        }
+        for (int e = t; e < K; e += kBlock) {
+            float v = x[e];
+            if (a.pro == PRO_NORM) {
+                v = v * scale;
+                v = v * a.norm_w[e];
+                if (a.hidden_out && blockIdx.x == 0) a.hidden_out[(size_t) tok * a.hidden_stride + e] = v;
+            }
+            if (WT == W_Q8) {
+                // the 32 consecutive lanes t..t+31 hold one Q8_0 block
+                float am = fabsf(v);
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+                const float d = am / 127.0f;
+                const float id = am != 0.0f ? 127.0f / am : 0.0f;
+                int8_t * q = (int8_t *) act;
+                q[(size_t) tok * K + e] = (int8_t) (int) rintf(v * id);
+                if ((t & 31) == 0) {
+                    float * sd = (float *) (act + (size_t) NT * K);
+                    sd[tok * (K / kQK) + e / kQK] = round_f16(d);
+                }
+            } else if (WT == W_F16) {
+                ((uint16_t *) act)[(size_t) tok * K + e] = f2h(v);
+            } else {
+                ((float *) act)[(size_t) tok * K + e] = v;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int NT>
+__device__ __forceinline__ void gemv_store(const GemvArgs & a, int r, const double * acc, const double * acc2) {
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok) {
+        const float v = (float) acc[tok];
+        float o;
+        switch (a.epi) {
+            case EPI_RESID: o = v + a.resid[(size_t) tok * a.resid_stride + r]; break;
+            case EPI_BIAS: o = v + a.bias[r]; break;
+            case EPI_BIAS_SILU: o = silu_q3t(v + a.bias[r]); break;
+            case EPI_SWIGLU: o = silu_q3t(v) * (float) acc2[tok]; break;
+            default: o = v; break;
+        }
+        a.y[(size_t) tok * a.y_stride + r] = o;
+    }
+}
+
+// Lane layout: a row's K/32 blocks are spread over LPR = min(32, K/32)
+// consecutive lanes (each lane owns whole 32-element blocks, SLOTS of them
+// per row), so one wave covers 64/LPR rows per iteration and every weight
+// load instruction reads a contiguous 2 KB (Q8) / 4 KB (F16) span.  The
+// per-lane fp64 partials are summed over the LPR lanes with xor shuffles.
+template <int WT, int NT, bool DUAL>
+__device__ __forceinline__ void gemv_rows(const GemvArgs & a, const char * act) {
+    const int K = a.K, BPR = K / kQK;
+    const int LPR = BPR < 32 ? BPR : 32;
+    const int SLOTS = BPR / LPR;
+    const int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lir = lane & (LPR - 1), rsub = lane / LPR;
+    const int ngroups = a.rows / RPW;
+    for (int g = blockIdx.x * (kBlock / 64) + wave; g < ngroups; g += gridDim.x * (kBlock / 64)) {
+        const int r = g * RPW + rsub;
+        double acc[NT], acc2[NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) { acc[i] = 0.0; acc2[i] = 0.0; }
+        for (int s = 0; s < SLOTS; ++s) {
+            const int b = lir + s * LPR;
+            if (WT == W_Q8) {
+                const int4 * wp = (const int4 *) ((const int8_t *) a.w + (size_t) r * K + b * kQK);
+                const int4 w0 = wp[0], w1 = wp[1];
+                const float dw = h2f(a.wd[(size_t) r * BPR + b]);
+                int4 u0, u1; float du = 0.0f;
+                if (DUAL) {
+                    const int4 * up = (const int4 *) ((const int8_t *) a.w2 + (size_t) r * K + b * kQK);
+                    u0 = up[0]; u1 = up[1];
+                    du = h2f(a.w2d[(size_t) r * BPR + b]);
+                }
+                const int8_t * xq = (const int8_t *) act;
+                const float * xd = (const float *) (act + (size_t) NT * K);
+#pragma unroll
+                for (int tok = 0; tok < NT; ++tok) {
+                    const int4 * xp = (const int4 *) (xq + (size_t) tok * K + b * kQK);
+                    const int4 x0 = xp[0], x1 = xp[1];
+                    const float dx = xd[tok * BPR + b];
+                    acc[tok] += (double) (dw * dx) * (double) dot32_i8(w0, w1, x0, x1);
+                    if (DUAL) acc2[tok] += (double) (du * dx) * (double) dot32_i8(u0, u1, x0, x1);
+                }
+            } else {
+                const uint16_t * wrow = (const uint16_t *) a.w + (size_t) r * K + b * kQK;
+                const uint16_t * urow = DUAL ? (const uint16_t *) a.w2 + (size_t) r * K + b * kQK : nullptr;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {       // 4 chunks of 8 halves (16 bytes)
+                    const int4 wv = ((const int4 *) wrow)[c];
+                    const uint16_t * wh = (const uint16_t *) &wv;
+                    int4 uv;
+                    if (DUAL) uv = ((const int4 *) urow)[c];
+                    const uint16_t * uh = (const uint16_t *) &uv;
+#pragma unroll
+                    for (int tok = 0; tok < NT; ++tok) {
+                        if (WT == W_F16) {
+                            const int4 xv = *(const int4 *) ((const uint16_t *) act + (size_t) tok * K + b * kQK + c * 8);
+                            const uint16_t * xh = (const uint16_t *) &xv;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const float xf = h2f(xh[j]);
+                                acc[tok] += (double) (h2f(wh[j]) * xf);   // exact fp16*fp16 product
+                                if (DUAL) acc2[tok] += (double) (h2f(uh[j]) * xf);
+                            }
+                        } else {
+                            const float * xf = (const float *) act + (size_t) tok * K + b * kQK + c * 8;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                acc[tok] = fma((double) h2f(wh[j]), (double) xf[j], acc[tok]);
+                                if (DUAL) acc2[tok] = fma((double) h2f(uh[j]), (double) xf[j], acc2[tok]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) {
+            for (int o = LPR / 2; o > 0; o >>= 1) {
+                acc[tok] += __shfl_xor(acc[tok], o);
+                if (DUAL) acc2[tok] += __shfl_xor(acc2[tok], o);
+            }
+        }
+        if (lir == 0) gemv_store<NT>(a, r, acc, acc2);
+    }
+}
+
+template <int WT, int NT, bool DUAL>
+__global__ __launch_bounds__(kBlock) void k_gemv(GemvArgs a) {
+    if (a.done && *a.done) return;
+    extern __shared__ __align__(16) char smem[];
+    double * red = (double *) smem;
+    char * act = smem + 64;
+    build_act<WT, NT>(a, red, act);
+    gemv_rows<WT, NT, DUAL>(a, act);
+}
+
+// ------------------------------------------------------------- attention
+struct AttnArgs {
+    const float * qkv; int32_t qkv_stride;        // [NT][n_head*hd + 2*n_kv*hd]
+    const float * q_norm; const float * k_norm; float eps;
+    const float * rope_cos; const float * rope_sin;  // [pos][hd/2]
+    uint16_t * kc; uint16_t * vc;                  // layer base, [n_kv_head][n_ctx][hd]
+    int32_t n_ctx, n_head, n_kv_head;
+    const int32_t * pos_ptr; int32_t pos_const;    // position of token 0
+    float * out; int32_t out_stride;               // [NT][n_head*hd]
+    const int32_t * done;
+    float scale;
+    int32_t nt;
+    float * probs_out;                             // optional [n_head][n_kv] (token 0)
+};
+
+constexpr int kHD = 128;
+
+// RMSNorm over one head (hd = 128) held by threads 0..127, then NEOX RoPE;
+// returns the rotated value for element threadIdx.x (threads < 128).
+__device__ __forceinline__ float head_norm_rope(float v, const float * w, float eps, const float * c,
+                                                const float * s, float * tmp, double * red) {
+    const int t = threadIdx.x;
+    const double ss = t < kHD ? (double) (v * v) : 0.0;
+    const double tot = block_sum_d(ss, red);
+    const float mean = (float) (tot / (double) kHD);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    if (t < kHD) { v = v * scale; v = v * w[t]; tmp[t] = v; }
+    __syncthreads();
+    float o = 0.0f;
+    if (t < kHD) {
+        const int i = t & 63;
+        const float x0 = tmp[i], x1 = tmp[i + 64];
+        if (t < 64) { const float p = x0 * c[i], q = x1 * s[i]; o = p - q; }
+        else        { const float p = x0 * s[i], q = x1 * c[i]; o = p + q; }
+    }
+    __syncthreads();
+    return o;
+}
+
+__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
+    if (a.done && *a.done) return;
+    extern __shared__ __align__(16) char smem[];
+    double * red = (double *) smem;                   // 4 doubles
+    float * fred = (float *) (smem + 32);             // 4 floats
+    float * tmp = (float *) (smem + 64);              // 128
+    float * qf = tmp + kHD;                           // 128: fp16-rounded rotated q
+    float * knew = qf + kHD;                          // [4][128]
+    float * vnew = knew + 4 * kHD;                    // [4][128]
+    double * pv = (double *) (vnew + 4 * kHD);        // [4 waves][128]
+    float * sc = (float *) (pv + 4 * kHD);            // [n_kv] scores, then fp16 probs
+
+    const int h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x;
+    const int group = a.n_head / a.n_kv_head, g = h / group;
+    const int qd = a.n_head * kHD, kd = a.n_kv_head * kHD;
+    const int pos0 = a.pos_ptr ? *a.pos_ptr : a.pos_const;
+    const int pos = pos0 + tok, n_kv = pos + 1;
+
+    // q of this head/token
+    {
+        const float * row = a.qkv + (size_t) tok * a.qkv_stride;
+        const float v = t < kHD ? row[h * kHD + t] : 0.0f;
+        const float o = head_norm_rope(v, a.q_norm, a.eps, a.rope_cos + (size_t) pos * 64,
+                                       a.rope_sin + (size_t) pos * 64, tmp, red);
+        if (t < kHD) qf[t] = round_f16(o);
+    }
+    // k, v of this KV head for the chunk tokens 0..tok (positions >= pos0 are
+    // never read from the cache inside this launch)
+    for (int j = 0; j <= tok; ++j) {
+        const float * row = a.qkv + (size_t) j * a.qkv_stride;
+        const float kvv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
+        const float o = head_norm_rope(kvv, a.k_norm, a.eps, a.rope_cos + (size_t) (pos0 + j) * 64,
+                                       a.rope_sin + (size_t) (pos0 + j) * 64, tmp, red);
+        if (t < kHD) {
+            const uint16_t kh = f2h(o);
+            const uint16_t vh = f2h(row[qd + kd + g * kHD + t]);
+            knew[j * kHD + t] = h2f(kh);
+            vnew[j * kHD + t] = h2f(vh);
+            if (j == tok && (h % group) == 0) {
+                a.kc[((size_t) g * a.n_ctx + pos) * kHD + t] = kh;
+                a.vc[((size_t) g * a.n_ctx + pos) * kHD + t] = vh;
+            }
+        }
+    }
+    __syncthreads();
+
+    // scores: 8 lanes per position, 16 dims per lane
+    const int lane = t & 63, wave = t >> 6;
+    const int sub = lane & 7, pw = lane >> 3;
+    const uint16_t * kbase = a.kc + (size_t) g * a.n_ctx * kHD;
+    float lmax = -INFINITY;
+    for (int j0 = 0; j0 < n_kv; j0 += 32) {
+        const int j = j0 + wave * 8 + pw;
+        double acc = 0.0;
+        if (j < n_kv) {
+            if (j < pos0) {
+                const int4 * kp = (const int4 *) (kbase + (size_t) j * kHD + sub * 16);
+                const int4 k0 = kp[0], k1 = kp[1];
+                const uint16_t * kh0 = (const uint16_t *) &k0;
+                const uint16_t * kh1 = (const uint16_t *) &k1;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + e] * h2f(kh0[e]));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + 8 + e] * h2f(kh1[e]));
+            } else {
+                const float * kr = knew + (j - pos0) * kHD + sub * 16;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc += (double) (qf[sub * 16 + e] * kr[e]);
+            }
+        }
+        acc += __shfl_xor(acc, 4);
+        acc += __shfl_xor(acc, 2);
+        acc += __shfl_xor(acc, 1);
+        if (j < n_kv) {
+            const float s = (float) acc * a.scale;
+            if (sub == 0) sc[j] = s;
+            lmax = fmaxf(lmax, s);
+        }
+    }
+    const float mx = block_max_f(lmax, fred);
+    double lsum = 0.0;
+    for (int j = t; j < n_kv; j += kBlock) {
+        const float e = expf_q3t(sc[j] - mx);
+        sc[j] = e;
+        lsum += (double) e;
+    }
+    const double sum = block_sum_d(lsum, red);
+    const float inv = (float) (1.0 / sum);
+    for (int j = t; j < n_kv; j += kBlock) {
+        const float p = sc[j] * inv;
+        if (a.probs_out && tok == 0) a.probs_out[(size_t) h * n_kv + j] = p;
+        sc[j] = round_f16(p);
+    }
+    __syncthreads();
+
+    // P.V: 16 lanes per position, 8 dims per lane, 4 positions per wave step
+    const int dsub = lane & 15, pq = lane >> 4;
+    const uint16_t * vbase = a.vc + (size_t) g * a.n_ctx * kHD;
+    double o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0;
+    for (int j0 = 0; j0 < n_kv; j0 += 16) {
+        const int j = j0 + wave * 4 + pq;
+        if (j < n_kv) {
+            const float p = sc[j];
+            if (j < pos0) {
+                const int4 vv = *(const int4 *) (vbase + (size_t) j * kHD + dsub * 8);
+                const uint16_t * vh = (const uint16_t *) &vv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] += (double) (p * h2f(vh[e]));
+            } else {
+                const float * vr = vnew + (j - pos0) * kHD + dsub * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] += (double) (p * vr[e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        o[e] += __shfl_xor(o[e], 16);
+        o[e] += __shfl_xor(o[e], 32);
+    }
+    if (pq == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[wave * kHD + dsub * 8 + e] = o[e];
+    }
+    __syncthreads();
+    if (t < kHD) {
+        const double r = (pv[t] + pv[kHD + t]) + (pv[2 * kHD + t] + pv[3 * kHD + t]);
+        a.out[(size_t) tok * a.out_stride + h * kHD + t] = (float) r;
+    }
+}
+
+__host__ __device__ constexpr size_t attn_lds_bytes(int n_ctx) {
+    return 64 + (size_t) (2 * kHD + 8 * kHD) * 4 + (size_t) 4 * kHD * 8 + (size_t) n_ctx * 4;
+}
+
+// ---------------------------------------------------------------- sampler
+struct SampleArgs {
+    const float * logits; int32_t vocab;
+    int32_t mode;                 // 0: talker codebook 0, 1: code predictor
+    int32_t group;                // code-predictor codebook (1..15)
+    const SampleParams * params;
+    FrameState * st;
+    uint8_t * seen;               // talker: codebook-0 tokens already generated
+    int32_t eos_id;
+};
+
+constexpr int kSampleThreads = 1024;
+constexpr int kMaxVocab = 4096;
+
+__device__ __forceinline__ uint32_t f2key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
+    FrameState * st = a.st;
+    if (st->done) return;
+    __shared__ float l[kMaxVocab];
+    __shared__ uint32_t hist[256];
+    __shared__ double dsc[kSampleThreads];
+    __shared__ float fv[kSampleThreads / 64];
+    __shared__ int32_t iv[kSampleThreads / 64];
+    __shared__ uint32_t sel[2];
+    __shared__ int32_t pick[2];
+    const int t = threadIdx.x, V = a.vocab;
+    const SampleParams & P = *a.params;
+    const int frame = st->frame;
+
+    for (int i = t; i < V; i += kSampleThreads) {
+        float v = a.logits[i];
+        if (a.mode == 0) {
+            if (i >= V - 1024 && i != a.eos_id) v = -INFINITY;
+            if (P.rep_penalty != 1.0f && a.seen[i]) v = v > 0.0f ? v / P.rep_penalty : v * P.rep_penalty;
+        }
+        l[i] = v;
+    }
+    float eff = 0.0f;
+    if (a.mode == 0) {
+        eff = P.eos_bias;
+        if (P.target_frames > 0 && frame > P.target_frames) {
+            eff += 0.1f * (float) (frame - P.target_frames);
+            if (eff > 6.0f) eff = 6.0f;
+        }
+    }
+    __syncthreads();
+    int32_t tok;
+    if (P.temperature <= 0.0f) {
+        if (a.mode == 0 && eff != 0.0f && t == 0) l[a.eos_id] += eff;
+        __syncthreads();
+        // empty = (-inf, INT_MAX); ascending scan with strict '>' keeps the first maximum
+        float bv = -INFINITY; int32_t bi = 0x7fffffff;
+        for (int i = t; i < V; i += kSampleThreads)
+            if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
+        // first maximum: larger value wins, equal values keep the smaller index
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int32_t oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((t & 63) == 0) { fv[t >> 6] = bv; iv[t >> 6] = bi; }
+        __syncthreads();
+        if (t == 0) {
+            float b = fv[0]; int32_t i0 = iv[0];
+            for (int w = 1; w < kSampleThreads / 64; ++w)
+                if (fv[w] > b || (fv[w] == b && iv[w] < i0)) { b = fv[w]; i0 = iv[w]; }
+            pick[0] = i0;
+        }
+        __syncthreads();
+        tok = pick[0];
+    } else {
+        for (int i = t; i < V; i += kSampleThreads) l[i] = l[i] / P.temperature;
+        __syncthreads();
+        if (a.mode == 0 && eff != 0.0f && t == 0) l[a.eos_id] += eff;
+        __syncthreads();
+        const int K = P.top_k;
+        if (K > 0 && K < V) {
+            // radix select of the K-th largest key, 8 bits per pass from the top
+            uint32_t prefix = 0, mask = 0;
+            int remaining = K;
+            for (int shift = 24; shift >= 0; shift -= 8) {
+                for (int i = t; i < 256; i += kSampleThreads) hist[i] = 0;
+                __syncthreads();
+                for (int i = t; i < V; i += kSampleThreads) {
+                    const uint32_t k = f2key(l[i]);
+                    if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+                }
+                __syncthreads();
+                if (t == 0) {
+                    int cum = 0, b = 255;
+                    for (; b > 0; --b) {
+                        if (cum + (int) hist[b] >= remaining) break;
+                        cum += (int) hist[b];
+                    }
+                    sel[0] = (uint32_t) b;
+                    sel[1] = (uint32_t) (remaining - cum);
+                }
+                __syncthreads();
+                prefix |= sel[0] << shift;
+                mask |= 255u << shift;
+                remaining = (int) sel[1];
+                __syncthreads();
+            }
+            const float thr = key2f(prefix);
+            for (int i = t; i < V; i += kSampleThreads)
+                if (l[i] < thr) l[i] = -INFINITY;
+            __syncthreads();
+        }
+        float lm = -INFINITY;
+        for (int i = t; i < V; i += kSampleThreads) lm = fmaxf(lm, l[i]);
+        lm = wave_max_f(lm);
+        if ((t & 63) == 0) fv[t >> 6] = lm;
+        __syncthreads();
+        float mx = fv[0];
+        for (int w = 1; w < kSampleThreads / 64; ++w) mx = fmaxf(mx, fv[w]);
+        __syncthreads();
+        // e = exp(l - max); denominator in fp64
+        const int C = (V + kSampleThreads - 1) / kSampleThreads;   // contiguous chunk per thread
+        double ls = 0.0;
+        for (int c = 0; c < C; ++c) {
+            const int i = t * C + c;
+            if (i < V) { const float e = expf_q3t(l[i] - mx); l[i] = e; ls += (double) e; }
+        }
+        dsc[t] = ls;
+        __syncthreads();
+        for (int off = kSampleThreads / 2; off > 0; off >>= 1) {
+            if (t < off) dsc[t] += dsc[t + off];
+            __syncthreads();
+        }
+        const double sum = dsc[0];
+        __syncthreads();
+        double lp = 0.0;
+        for (int c = 0; c < C; ++c) {
+            const int i = t * C + c;
+            if (i < V) { const float p = (float) ((double) l[i] / sum); l[i] = p; lp += (double) p; }
+        }
+        // inclusive scan of per-thread sums (Hillis-Steele) for the CDF
+        dsc[t] = lp;
+        __syncthreads();
+        for (int off = 1; off < kSampleThreads; off <<= 1) {
+            const double v = t >= off ? dsc[t - off] : 0.0;
+            __syncthreads();
+            dsc[t] += v;
+            __syncthreads();
+        }
+        const double total = dsc[kSampleThreads - 1];
+        const double u = philox_uniform(P.seed, (uint32_t) frame, a.mode == 0 ? 0u : (uint32_t) a.group);
+        const double target = u * total;
+        if (t == 0) { pick[0] = 0x7fffffff; pick[1] = -1; }
+        __syncthreads();
+        double cum = t > 0 ? dsc[t - 1] : 0.0;
+        for (int c = 0; c < C; ++c) {
+            const int i = t * C + c;
+            if (i < V && l[i] > 0.0f) {
+                cum += (double) l[i];
+                atomicMax(&pick[1], i);
+                if (cum > target) { atomicMin(&pick[0], i); break; }
+            }
+        }
+        __syncthreads();
+        tok = pick[0] != 0x7fffffff ? pick[0] : (pick[1] >= 0 ? pick[1] : 0);
+    }
+    if (t == 0) {
+        if (a.mode == 0) {
+            st->codes[0] = tok;
+            if (tok == a.eos_id) { st->done = 1; st->eos = 1; }
+            else a.seen[tok] = 1;
+        } else {
+            st->codes[a.group] = tok;
+        }
+    }
+}
+
+// ------------------------------------------------------------- embeddings
+struct EmbedArgs {
+    int32_t mode;     // 0: code-predictor prefill rows, 1: code-predictor step row, 2: talker step sum
+    int32_t group;    // mode 1: codebook g being predicted (2..15)
+    const FrameState * st;
+    const uint16_t * codec_embd;
+    const uint16_t * cp_embd[15];
+    const float * hidden;
+    const float * trailing; int32_t n_trailing;
+    const float * pad;
+    float * x;
+    int32_t d;
+};
+
+__global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
+    const FrameState * st = a.st;
+    if (st->done) return;
+    const int e = blockIdx.x * kBlock + threadIdx.x;
+    if (e >= a.d) return;
+    const size_t d = (size_t) a.d;
+    if (a.mode == 0) {
+        a.x[e] = a.hidden[e];
+        a.x[d + e] = h2f(a.codec_embd[(size_t) st->codes[0] * d + e]);
+    } else if (a.mode == 1) {
+        a.x[e] = h2f(a.cp_embd[a.group - 2][(size_t) st->codes[a.group - 1] * d + e]);
+    } else {
+        float s = h2f(a.codec_embd[(size_t) st->codes[0] * d + e]);
+        for (int g = 1; g < 16; ++g) s = s + h2f(a.cp_embd[g - 1][(size_t) st->codes[g] * d + e]);
+        const int f = st->frame;
+        const float tr = f < a.n_trailing ? a.trailing[(size_t) f * d + e] : a.pad[e];
+        a.x[e] = s + tr;
+    }
+}
+
+__global__ void k_frame_end(FrameState * st, int32_t * codes_out, int32_t n_cb) {
+    if (threadIdx.x != 0 || st->done) return;
+    for (int g = 0; g < n_cb; ++g) codes_out[(size_t) st->n_emitted * n_cb + g] = st->codes[g];
+    st->n_emitted += 1;
+    st->n_past += 1;
+    st->frame += 1;
+    if (st->n_emitted >= st->max_frames) st->done = 1;   // no KV position is used past the reserved range
+}
+
+// normed rows for the prefill's all-token hidden output
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float * x, const float * w, float eps, int32_t d,
+                                                        float * y) {
+    __shared__ double red[4];
+    const float * xr = x + (size_t) blockIdx.x * d;
+    double ss = 0.0;
+    for (int e = threadIdx.x; e < d; e += kBlock) { const float v = xr[e]; ss += (double) (v * v); }
+    const double tot = block_sum_d(ss, red);
+    const float mean = (float) (tot / (double) d);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int e = threadIdx.x; e < d; e += kBlock) { float v = xr[e] * scale; y[(size_t) blockIdx.x * d + e] = v * w[e]; }
+}
+
+// dequantise a repacked Q8_0 tensor: out = fp32(d) * q
+__global__ void k_dequant_q8(const int8_t * q, const uint16_t * d, int64_t n, float * out) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = h2f(d[i / kQK]) * (float) q[i];
+}
+
+// gather rows of an fp16 table into fp32 rows (token ids from host copy)
+__global__ void k_gather_rows(const uint16_t * table, int64_t dim, const int32_t * ids, int32_t n, float * out) {
+    const int r = blockIdx.y;
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < dim; e += (int64_t) gridDim.x * blockDim.x)
+        out[(size_t) r * dim + e] = h2f(table[(size_t) ids[r] * dim + e]);
+}
+
+}  // namespace q3t

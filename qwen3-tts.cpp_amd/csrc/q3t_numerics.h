@@ -1,0 +1,109 @@
+// q3t_numerics.h -- device-side arithmetic shared by every kernel of the
+// frame loop.  Each helper rounds exactly where the reference's ggml CPU
+// path rounds (fp16 activations, fp16 KV, Q8_0 activation quantisation);
+// reductions take exact terms and accumulate in fp64 so that the rounded
+// fp32 result does not depend on how the GPU splits the sum.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace q3t {
+
+constexpr int kBlock = 256;   // threads per workgroup for GEMV / attention
+constexpr int kQK = 32;       // Q8_0 block length
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+__device__ __forceinline__ float round_f16(float f) { return h2f(f2h(f)); }
+
+// exp(x): Cody-Waite reduction x = k*ln2 + r (ln2 split hi/lo, fused
+// multiply-add), exp(r) by its degree-7 Taylor polynomial in Horner form,
+// scaled by 2^k built from the exponent field.  Results below 2^-126 are
+// flushed to zero (x < -87); x > 88.7228 overflows to +inf.  Max error
+// about 1 ulp; the same steps are restated on the CPU for parity.
+__device__ __forceinline__ float expf_q3t(float x) {
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.72283935546875f) return __int_as_float(0x7f800000);
+    const float k = rintf(x * 1.44269504088896341f);
+    float r = fmaf(-k, 0.693145751953125f, x);
+    r = fmaf(-k, 1.428606765330187e-06f, r);
+    float p = 1.98412698412698413e-4f;
+    p = fmaf(p, r, 1.38888888888888889e-3f);
+    p = fmaf(p, r, 8.33333333333333333e-3f);
+    p = fmaf(p, r, 4.16666666666666667e-2f);
+    p = fmaf(p, r, 1.66666666666666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ki = (int) k;
+    if (ki > 127) { p = p * 2.0f; ki -= 1; }
+    return p * __int_as_float((ki + 127) << 23);
+}
+
+// ggml_silu_f32: x / (1 + e^-x), correctly rounded division.
+__device__ __forceinline__ float silu_q3t(float x) { return x / (1.0f + expf_q3t(-x)); }
+
+// Wave64 reductions.  All 64 lanes must be active.
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Workgroup-wide fp64 sum for 256 threads; every thread gets the same value.
+// red: 4 doubles of LDS.
+__device__ __forceinline__ double block_sum_d(double v, double * red) {
+    v = wave_sum_d(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max_f(float v, float * red) {
+    v = wave_max_f(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Eight int8x4 dot products: sum of 32 int8 products, exact in int32.
+__device__ __forceinline__ int dot32_i8(const int4 a0, const int4 a1, const int4 b0, const int4 b1) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(a0.x, b0.x, s, false);
+    s = __builtin_amdgcn_sdot4(a0.y, b0.y, s, false);
+    s = __builtin_amdgcn_sdot4(a0.z, b0.z, s, false);
+    s = __builtin_amdgcn_sdot4(a0.w, b0.w, s, false);
+    s = __builtin_amdgcn_sdot4(a1.x, b1.x, s, false);
+    s = __builtin_amdgcn_sdot4(a1.y, b1.y, s, false);
+    s = __builtin_amdgcn_sdot4(a1.z, b1.z, s, false);
+    s = __builtin_amdgcn_sdot4(a1.w, b1.w, s, false);
+    return s;
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11).  Returns a uniform double in [0,1) from 53 bits.
+__device__ __forceinline__ double philox_uniform(uint64_t key, uint32_t c0, uint32_t c1) {
+    uint32_t k0 = (uint32_t) key, k1 = (uint32_t) (key >> 32);
+    uint32_t c[4] = {c0, c1, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        const uint64_t p0 = (uint64_t) 0xD2511F53u * c[0];
+        const uint64_t p1 = (uint64_t) 0xCD9E8D57u * c[2];
+        const uint32_t n0 = (uint32_t) (p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n2 = (uint32_t) (p0 >> 32) ^ c[3] ^ k1;
+        c[0] = n0; c[1] = (uint32_t) p1; c[2] = n2; c[3] = (uint32_t) p0;
+    }
+    return ((double) (c[0] >> 5) * 67108864.0 + (double) (c[1] >> 6)) * (1.0 / 9007199254740992.0);
+}
+
+}  // namespace q3t

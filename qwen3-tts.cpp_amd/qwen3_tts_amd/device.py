@@ -1,0 +1,205 @@
+"""ctypes binding of the device C ABI (include/q3t_dev.h).
+
+This is the Python-side equivalent of the binding a host application adds
+(see INTEGRATION.md); tests and the benchmark drive the GPU path only through
+it.  The shared library is built in-tree (``lib/libq3t_hip.so``); loading it
+fails loudly when it is missing: there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from .config import CConfig
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libq3t_hip.so")
+
+EXPORTS = [
+    "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
+    "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
+    "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
+    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_frames_begin",
+    "q3t_dev_frames_run", "q3t_dev_sync", "q3t_dev_time_kernel",
+]
+
+
+class CSampling(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("seed", ctypes.c_uint64)]
+
+
+class CFrameArgs(ctypes.Structure):
+    _fields_ = [
+        ("trailing", ctypes.c_void_p), ("n_trailing", ctypes.c_int32), ("tts_pad", ctypes.c_void_p),
+        ("n_past", ctypes.c_int32), ("max_len", ctypes.c_int32), ("repetition_penalty", ctypes.c_float),
+        ("eos_bias", ctypes.c_float), ("target_frames", ctypes.c_int32), ("sampling", CSampling),
+    ]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"HIP device library not built: {path} (run __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        vp, i32, u32, f32p = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_void_p
+        lib.q3t_dev_create.argtypes = [ctypes.POINTER(CConfig), i32, ctypes.POINTER(vp)]
+        lib.q3t_dev_destroy.argtypes = [vp]
+        lib.q3t_dev_destroy.restype = None
+        lib.q3t_dev_last_error.argtypes = [vp]
+        lib.q3t_dev_last_error.restype = ctypes.c_char_p
+        lib.q3t_dev_upload_tensor.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(ctypes.c_int64), vp, ctypes.c_size_t]
+        lib.q3t_dev_download_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
+        lib.q3t_dev_dequantize.argtypes = [vp, ctypes.c_char_p, f32p, ctypes.c_size_t]
+        lib.q3t_dev_kv_reserve.argtypes = [vp, i32]
+        lib.q3t_dev_kv_clear.argtypes = [vp]
+        lib.q3t_dev_kv_capacity.argtypes = [vp]
+        lib.q3t_dev_kv_write.argtypes = [vp, i32, i32, vp, vp]
+        lib.q3t_dev_prefill.argtypes = [vp, f32p, i32, i32, f32p, f32p]
+        lib.q3t_dev_talker_step.argtypes = [vp, f32p, i32, f32p, f32p]
+        lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
+        lib.q3t_dev_text_proj.argtypes = [vp, vp, i32, f32p]
+        lib.q3t_dev_embed_rows.argtypes = [vp, i32, i32, vp, i32, f32p]
+        lib.q3t_dev_frames_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
+        lib.q3t_dev_frames_run.argtypes = [vp, i32, vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+        lib.q3t_dev_sync.argtypes = [vp]
+        lib.q3t_dev_time_kernel.argtypes = [vp, i32, i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+        _lib = lib
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class DeviceError(RuntimeError):
+    pass
+
+
+class Device:
+    """One device context (q3t_dev) on HIP device `device`."""
+
+    def __init__(self, cfg, device=0):
+        self.lib = load_library()
+        self.cfg = cfg
+        self._c_cfg = cfg.to_c()
+        h = ctypes.c_void_p()
+        rc = self.lib.q3t_dev_create(ctypes.byref(self._c_cfg), device, ctypes.byref(h))
+        self.h = h
+        if rc != 0:
+            msg = self.error() if h else f"q3t_dev_create returned {rc} (no HIP device?)"
+            self.close()
+            raise DeviceError(msg)
+        self._keep = []
+
+    def error(self):
+        return self.lib.q3t_dev_last_error(self.h).decode() if self.h else ""
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise DeviceError(f"{what}: {self.error()}")
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.q3t_dev_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    # -- weights
+    def upload(self, name, ttype, ne, arr):
+        arr = np.ascontiguousarray(arr)
+        ne4 = (ctypes.c_int64 * 4)(ne[0], ne[1], 1, 1)
+        self._check(self.lib.q3t_dev_upload_tensor(self.h, name.encode(), ttype, ne4, _p(arr), arr.nbytes), f"upload {name}")
+
+    def upload_weights(self, weights):
+        for name, (ttype, ne, arr) in weights.items():
+            self.upload(name, ttype, ne, arr)
+
+    def download(self, name, nbytes):
+        out = np.empty(nbytes, dtype=np.uint8)
+        self._check(self.lib.q3t_dev_download_tensor(self.h, name.encode(), _p(out), nbytes), f"download {name}")
+        return out
+
+    def dequantize(self, name, n):
+        out = np.empty(n, dtype=np.float32)
+        self._check(self.lib.q3t_dev_dequantize(self.h, name.encode(), _p(out), n), f"dequantize {name}")
+        return out
+
+    # -- caches
+    def kv_reserve(self, n_ctx):
+        self._check(self.lib.q3t_dev_kv_reserve(self.h, n_ctx), "kv_reserve")
+
+    def kv_write(self, layer, k, v):
+        k = np.ascontiguousarray(k, dtype=np.float16)
+        v = np.ascontiguousarray(v, dtype=np.float16)
+        self._check(self.lib.q3t_dev_kv_write(self.h, layer, k.shape[0], _p(k), _p(v)), "kv_write")
+
+    # -- forward passes
+    def prefill(self, embd, n_past=0, want_hidden=True):
+        embd = np.ascontiguousarray(embd, dtype=np.float32)
+        n = embd.shape[0]
+        hid = np.empty((n, self.cfg.hidden_size), np.float32) if want_hidden else None
+        logits = np.empty(self.cfg.codec_vocab, np.float32)
+        self._check(self.lib.q3t_dev_prefill(self.h, _p(embd), n, n_past, _p(hid), _p(logits)), "prefill")
+        return hid, logits
+
+    def talker_step(self, embd, n_past):
+        embd = np.ascontiguousarray(embd, dtype=np.float32)
+        logits = np.empty(self.cfg.codec_vocab, np.float32)
+        hid = np.empty(self.cfg.hidden_size, np.float32)
+        self._check(self.lib.q3t_dev_talker_step(self.h, _p(embd), n_past, _p(logits), _p(hid)), "talker_step")
+        return logits, hid
+
+    def code_pred(self, hidden, cb0, temperature=0.0, top_k=0, seed=0, frame=0):
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+        codes = np.empty(self.cfg.n_codebooks - 1, np.int32)
+        logits = np.empty((self.cfg.n_codebooks - 1, self.cfg.cp_vocab), np.float32)
+        s = CSampling(temperature, top_k, seed)
+        self._check(self.lib.q3t_dev_code_pred(self.h, _p(hidden), int(cb0), ctypes.byref(s), frame, _p(codes), _p(logits)),
+                    "code_pred")
+        return codes, logits
+
+    def text_proj(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(tokens), self.cfg.hidden_size), np.float32)
+        self._check(self.lib.q3t_dev_text_proj(self.h, _p(tokens), len(tokens), _p(out)), "text_proj")
+        return out
+
+    def embed_rows(self, table, index, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        dim = self.cfg.text_embd_dim if table == 2 else self.cfg.hidden_size
+        out = np.empty((len(tokens), dim), np.float32)
+        self._check(self.lib.q3t_dev_embed_rows(self.h, table, index, _p(tokens), len(tokens), _p(out)), "embed_rows")
+        return out
+
+    # -- frame loop
+    def frames_begin(self, trailing, tts_pad, n_past, max_len, repetition_penalty=1.05, temperature=0.0, top_k=0,
+                     eos_bias=0.0, target_frames=0, seed=0):
+        trailing = np.ascontiguousarray(trailing, dtype=np.float32)
+        tts_pad = np.ascontiguousarray(tts_pad, dtype=np.float32)
+        self._keep = [trailing, tts_pad]
+        a = CFrameArgs(_p(trailing), trailing.shape[0], _p(tts_pad), n_past, max_len, repetition_penalty, eos_bias,
+                       target_frames, CSampling(temperature, top_k, seed))
+        self._check(self.lib.q3t_dev_frames_begin(self.h, ctypes.byref(a)), "frames_begin")
+
+    def frames_run(self, n_frames):
+        out = np.empty((max(n_frames, 1), self.cfg.n_codebooks), np.int32)
+        n = ctypes.c_int32()
+        eos = ctypes.c_int32()
+        self._check(self.lib.q3t_dev_frames_run(self.h, n_frames, _p(out), ctypes.byref(n), ctypes.byref(eos)),
+                    "frames_run")
+        return out[: n.value].copy(), bool(eos.value)
+
+    def sync(self):
+        self._check(self.lib.q3t_dev_sync(self.h), "sync")
+
+    def time_kernel(self, which, iters):
+        us = ctypes.c_double()
+        b = ctypes.c_double()
+        self._check(self.lib.q3t_dev_time_kernel(self.h, which, iters, ctypes.byref(us), ctypes.byref(b)), "time_kernel")
+        return us.value, b.value

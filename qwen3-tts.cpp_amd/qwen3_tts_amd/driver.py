@@ -1,0 +1,119 @@
+"""Host driver of the device frame loop: the control flow of
+TTSTransformer::generate (src/tts_transformer.cpp:3007-3371) over the C ABI.
+
+The arithmetic of the loop (talker step, code predictor, samplers, step
+embedding) runs on the GPU; this module only assembles the prefill rows
+(host glue in the reference too, src/tts_transformer.cpp:1030-1186), sizes
+the KV cache, and replays frames in chunks, applying the per-frame callback
+and the opt-in repetition-loop truncation after each chunk in frame order.
+Frames computed past an EOS / abort / truncation point are discarded, so the
+output equals the reference's frame-by-frame loop.
+"""
+import numpy as np
+
+
+class GenerateError(RuntimeError):
+    pass
+
+
+def build_prefill(dev, cfg, text, speaker=None, language_id=2050, instruct=None):
+    """build_prefill_graph (src/tts_transformer.cpp:1030-1186) on the device
+    text projection and embedding gathers.  Returns (prefill [n][d],
+    trailing [m][d], tts_pad [d])."""
+    text = np.asarray(text, np.int32)
+    if len(text) < 4:
+        raise GenerateError("Need at least 4 text tokens for prefill")
+    sp = dev.text_proj([cfg.tts_bos_id, cfg.tts_eos_id, cfg.tts_pad_id])
+    bos_e, eos_e, pad_e = sp[0], sp[1], sp[2]
+    role = dev.text_proj(text[:3])
+    if language_id < 0:
+        codec_tok = [cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id]
+    else:
+        codec_tok = [cfg.codec_think_id, cfg.codec_think_bos_id, language_id, cfg.codec_think_eos_id]
+    rows = [dev.embed_rows(0, 0, codec_tok)]
+    if speaker is not None:
+        rows.append(np.asarray(speaker, np.float32).reshape(1, -1))
+    rows.append(dev.embed_rows(0, 0, [cfg.codec_pad_id, cfg.codec_bos_id]))
+    cin = np.concatenate(rows, axis=0)
+    ov_len = cin.shape[0] - 1
+    overlay = np.stack([bos_e if t == ov_len - 1 else pad_e for t in range(ov_len)])
+    codec_plus = (overlay + cin[:ov_len]).astype(np.float32)
+    first = dev.text_proj(text[3:4])[0]
+    last = (first + cin[-1]).astype(np.float32)
+    parts = []
+    if instruct is not None and len(instruct) > 0:
+        parts.append(dev.text_proj(instruct))
+    parts += [role, codec_plus, last[None]]
+    prefill = np.concatenate(parts, axis=0).astype(np.float32)
+    n_trail = max(0, len(text) - 9)
+    trail = [dev.text_proj(text[4:4 + n_trail])] if n_trail > 0 else []
+    trailing = np.concatenate(trail + [eos_e[None]], axis=0).astype(np.float32)
+    return prefill, trailing, pad_e.astype(np.float32)
+
+
+def _rep_loop(frames, state, n_cb):
+    """Opt-in repetition-loop detector (src/tts_transformer.cpp:3225-3254).
+    Returns the truncation length or None."""
+    nf = len(frames)
+    is_rep = False
+    for back in range(1, 7):
+        if is_rep or back >= nf:
+            break
+        a, b = frames[nf - 1], frames[nf - 1 - back]
+        if int(np.sum(a == b)) >= 10:
+            is_rep = True
+    if is_rep:
+        if state["run"] == 0:
+            state["start"] = nf - 1
+        state["run"] += 1
+    else:
+        state["run"] = 0
+    if state["run"] >= 5:
+        return state["start"]
+    return None
+
+
+def generate(dev, cfg, text, speaker=None, max_len=64, language_id=2050, repetition_penalty=1.05, temperature=0.9,
+             top_k=50, instruct=None, eos_bias=0.0, target_frames=0, rep_loop_detect=False, on_frame=None, seed=0,
+             chunk=32, prefill_rows=None):
+    """Returns int32 codes [n_frames][n_codebooks].  `prefill_rows`, when
+    given, is (prefill, trailing, tts_pad) and skips build_prefill."""
+    if max_len <= 0:
+        return np.zeros((0, cfg.n_codebooks), np.int32)
+    if prefill_rows is None:
+        prefill_rows = build_prefill(dev, cfg, text, speaker, language_id, instruct)
+    prefill, trailing, pad = prefill_rows
+    plen = prefill.shape[0]
+    required = plen + max_len + 8
+    cap = dev.lib.q3t_dev_kv_capacity(dev.h)
+    if cap < required or cap > max(required * 2, 512):
+        dev.kv_reserve(required)
+    dev.prefill(prefill, 0, want_hidden=False)
+    dev.frames_begin(trailing, pad, plen, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
+                     seed)
+    out = []
+    rep_frames, rep_state = [], {"run": 0, "start": 0}
+    produced = 0
+    while produced < max_len:
+        n = min(chunk, max_len - produced)
+        codes, eos = dev.frames_run(n)
+        stop = False
+        for f in range(codes.shape[0]):
+            frame = produced + f
+            out.append(codes[f])
+            if on_frame is not None and not on_frame(codes[f], cfg.n_codebooks, frame):
+                stop = True
+                break
+            if rep_loop_detect:
+                rep_frames.append(codes[f])
+            cut = _rep_loop(rep_frames, rep_state, cfg.n_codebooks)
+            if cut is not None:
+                out = out[:cut]
+                stop = True
+                break
+        produced += codes.shape[0]
+        if stop or eos or codes.shape[0] < n:
+            break
+    if not out:
+        return np.zeros((0, cfg.n_codebooks), np.int32)
+    return np.stack(out).astype(np.int32)

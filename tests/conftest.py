@@ -1,0 +1,20 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "qwen3-tts.cpp_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X); runs the device C ABI")
+    config.addinivalue_line("markers", "slow: full 0.6B-shape case")
+
+
+@pytest.fixture(scope="session")
+def oracle_lib():
+    import q3t_oracle
+    return q3t_oracle

@@ -1,0 +1,180 @@
+"""HIP path vs the CPU oracle, through the device C ABI (include/q3t_dev.h).
+
+The numerics contract makes the two bit-identical (fp64 accumulation of exact
+terms, identical rounding points, the same exp and RoPE table), so most
+checks are exact; the contractual bounds from the task (logits within 1e-2
+max-abs, identical greedy codebook tokens) are asserted as well.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import q3t_oracle as orc
+from qwen3_tts_amd import config as qcfg
+from qwen3_tts_amd import driver
+from qwen3_tts_amd.device import Device
+from qwen3_tts_amd.synth import Weights, dequantize_q8_0
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-2   # max-abs logits tolerance (F16 path) from the parity contract
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make(cfg, wtype, seed=7, n_ctx=256, norm_mode="one"):
+    w = Weights(cfg, wtype, seed=seed, norm_mode=norm_mode)
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    dev.kv_reserve(n_ctx)
+    o = orc.Oracle(cfg, w, threads=8)
+    o.kv_reset(n_ctx)
+    return w, dev, o
+
+
+@pytest.fixture(scope="module", params=["q8_0", "f16"])
+def tiny_model(request):
+    cfg = qcfg.tiny()
+    say(f"[gpu] tiny model {request.param}")
+    w, dev, o = make(cfg, request.param)
+    yield cfg, w, dev, o
+    dev.close()
+
+
+def test_upload_roundtrip_and_dequant(tiny_model):
+    cfg, w, dev, o = tiny_model
+    for name in ["talker.blk.0.attn_q.weight", "talker.blk.1.ffn_down.weight", "talker.codec_head.weight",
+                 "code_pred.blk.0.attn_v.weight", "talker.output_norm.weight"]:
+        ttype, ne, arr = w[name]
+        back = dev.download(name, arr.nbytes)
+        assert np.array_equal(back, arr.view(np.uint8).ravel()), name
+        if ttype == 8:
+            deq = dev.dequantize(name, ne[0] * ne[1])
+            assert np.array_equal(deq.view(np.uint32), dequantize_q8_0(arr).view(np.uint32)), name
+            assert np.array_equal(deq.view(np.uint32), orc.dequantize(arr, ne[0] * ne[1]).view(np.uint32))
+
+
+def test_prefill_and_steps_match_oracle(tiny_model):
+    cfg, w, dev, o = tiny_model
+    rng = np.random.default_rng(1)
+    d = cfg.hidden_size
+    embd = (rng.standard_normal((10, d)) * 0.05).astype(np.float32)
+    say("[gpu] prefill 10 rows")
+    hid_g, log_g = dev.prefill(embd, 0)
+    hid_o, log_o = o.prefill(embd, 0)
+    assert np.abs(log_g - log_o).max() <= LOGIT_TOL
+    assert np.array_equal(hid_g, hid_o)
+    assert np.array_equal(log_g, log_o)
+    for s in range(6):
+        e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+        lg, hg = dev.talker_step(e, 10 + s)
+        lo, ho = o.step(e, 10 + s)
+        assert np.abs(lg - lo).max() <= LOGIT_TOL
+        assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
+        assert np.array_equal(hg, ho)
+
+
+def test_code_pred_greedy_matches_oracle(tiny_model):
+    cfg, w, dev, o = tiny_model
+    rng = np.random.default_rng(2)
+    hid = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+    for cb0 in (0, 17, 2047):
+        cg, lg = dev.code_pred(hid, cb0)
+        co, lo = o.code_pred(hid, cb0)
+        assert np.abs(lg - lo).max() <= LOGIT_TOL
+        assert np.array_equal(lg, lo)
+        assert np.array_equal(cg, co)
+        assert np.array_equal(cg, lg.argmax(axis=1))
+
+
+def test_code_pred_sampled_matches_oracle(tiny_model):
+    cfg, w, dev, o = tiny_model
+    hid = np.random.default_rng(3).standard_normal(cfg.hidden_size).astype(np.float32)
+    for seed in (1, 99):
+        cg, _ = dev.code_pred(hid, 5, temperature=0.9, top_k=50, seed=seed, frame=3)
+        co, _ = o.code_pred(hid, 5, temperature=0.9, top_k=50, seed=seed, frame=3)
+        assert np.array_equal(cg, co)
+
+
+def test_text_proj_and_embeddings(tiny_model):
+    cfg, w, dev, o = tiny_model
+    toks = np.array([0, 5, cfg.text_vocab - 1, 1234, 77, 3], np.int32)
+    assert np.array_equal(dev.text_proj(toks), o.text_proj(toks))
+    rows = dev.embed_rows(0, 0, [cfg.codec_bos_id, 3])
+    assert np.array_equal(rows[0], o.embed_row("codec", 0, cfg.codec_bos_id))
+    rows = dev.embed_rows(1, 14, [2047])
+    assert np.array_equal(rows[0], o.embed_row("cp", 14, 2047))
+
+
+def test_generate_greedy_64_frames(tiny_model):
+    cfg, w, dev, o = tiny_model
+    text = np.random.default_rng(4).integers(0, cfg.text_vocab - 8, 32).astype(np.int32)
+    spk = np.random.default_rng(5).standard_normal(cfg.hidden_size).astype(np.float32)
+    say("[gpu] generate greedy 64")
+    co, _ = o.generate(text, spk, max_len=64, temperature=0.0, top_k=0)
+    cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, chunk=16)
+    assert co.shape == cg.shape, (co.shape, cg.shape)
+    assert np.array_equal(cg, co)
+
+
+def test_generate_sampled_matches_oracle(tiny_model):
+    cfg, w, dev, o = tiny_model
+    text = np.random.default_rng(6).integers(0, cfg.text_vocab - 8, 20).astype(np.int32)
+    say("[gpu] generate sampled 24")
+    co, _ = o.generate(text, None, max_len=24, temperature=0.9, top_k=50, seed=11)
+    cg = driver.generate(dev, cfg, text, None, max_len=24, temperature=0.9, top_k=50, seed=11, chunk=5)
+    assert np.array_equal(cg, co)
+
+
+def test_generate_eos_bias_stops(tiny_model):
+    cfg, w, dev, o = tiny_model
+    text = np.arange(12, dtype=np.int32)
+    cg = driver.generate(dev, cfg, text, None, max_len=8, temperature=0.0, eos_bias=1e4)
+    co, _ = o.generate(text, None, max_len=8, temperature=0.0, eos_bias=1e4)
+    assert cg.shape[0] == 0 and co.shape[0] == 0
+
+
+def test_generate_target_frames_ramp(tiny_model):
+    cfg, w, dev, o = tiny_model
+    text = np.arange(3, 20, dtype=np.int32)
+    co, _ = o.generate(text, None, max_len=40, temperature=0.0, eos_bias=0.0, target_frames=2)
+    cg = driver.generate(dev, cfg, text, None, max_len=40, temperature=0.0, eos_bias=0.0, target_frames=2, chunk=7)
+    assert np.array_equal(cg, co)
+
+
+def test_callback_abort(tiny_model):
+    cfg, w, dev, o = tiny_model
+    text = np.arange(10, 30, dtype=np.int32)
+    seen = []
+
+    def cb(codes, n, frame):
+        seen.append(frame)
+        return frame < 4
+
+    cg = driver.generate(dev, cfg, text, None, max_len=30, temperature=0.0, on_frame=cb, chunk=8)
+    assert seen == [0, 1, 2, 3, 4]
+    assert cg.shape[0] == 5
+
+
+@pytest.mark.slow
+def test_full_q8_frame_loop_64_greedy():
+    cfg = qcfg.full_06b()
+    say("[gpu] full 0.6B Q8_0: synth + upload")
+    w, dev, o = make(cfg, "q8_0", seed=3, n_ctx=256)
+    text = np.random.default_rng(8).integers(0, 151936, 32).astype(np.int32)
+    spk = np.random.default_rng(9).standard_normal(1024).astype(np.float32)
+    say("[gpu] full: oracle generate 64")
+    co, first_o = o.generate(text, spk, max_len=64, temperature=0.0, top_k=0)
+    say("[gpu] full: device generate 64")
+    pre = driver.build_prefill(dev, cfg, text, spk)
+    opre, otr, opad = o.build_prefill(text, spk)
+    assert np.array_equal(pre[0], opre) and np.array_equal(pre[1], otr) and np.array_equal(pre[2], opad)
+    _, first_g = dev.prefill(pre[0], 0, want_hidden=False)
+    assert np.abs(first_g - first_o).max() <= LOGIT_TOL
+    cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, prefill_rows=pre)
+    say(f"[gpu] full: frames oracle={co.shape[0]} device={cg.shape[0]}")
+    assert np.array_equal(cg, co)
+    dev.close()
