@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -262,13 +263,36 @@ void launch_gemv_t(q3t_dev * c, const GemvArgs & a) {
     hipLaunchKernelGGL((k_gemv<WT, NT, DUAL>), dim3(grid), dim3(kBlock), lds, c->stream, a);
 }
 
+// register path: G row groups per wave, SLOTS = blocks per lane
+template <int WT, int NT, bool DUAL, int SLOTS, int G>
+void launch_gemv_r(q3t_dev * c, const GemvArgs & a) {
+    const int BPR = a.K / kQK, LPR = BPR / SLOTS, RPW = 64 / LPR;
+    const int groups = a.rows / RPW;
+    const int grid = std::max(1, (groups + 4 * G - 1) / (4 * G));
+    hipLaunchKernelGGL((k_gemv_r<WT, NT, DUAL, SLOTS, G>), dim3(grid), dim3(kBlock), 0, c->stream, a);
+}
+
+template <int WT, int NT, bool DUAL>
+void launch_gemv_rs(q3t_dev * c, const GemvArgs & a) {
+    const int BPR = a.K / kQK;
+    if (BPR <= 32) launch_gemv_r<WT, NT, DUAL, 1, 2>(c, a);
+    else if (BPR == 64) launch_gemv_r<WT, NT, DUAL, 2, 1>(c, a);
+    else launch_gemv_r<WT, NT, DUAL, 3, 1>(c, a);
+}
+
 template <int WT, bool DUAL>
-void launch_gemv_nt(q3t_dev * c, const GemvArgs & a, int nt) {
-    switch (nt) {
-        case 1: launch_gemv_t<WT, 1, DUAL>(c, a); break;
-        case 2: launch_gemv_t<WT, 2, DUAL>(c, a); break;
-        default: launch_gemv_t<WT, 4, DUAL>(c, a); break;
-    }
+void launch_gemv_nt(q3t_dev * c, const GemvArgs & a, int nt, bool reg) {
+    if (reg && nt == 1) launch_gemv_rs<WT, 1, DUAL>(c, a);
+    else if (reg && nt == 2) launch_gemv_rs<WT, 2, DUAL>(c, a);
+    else if (nt == 1) launch_gemv_t<WT, 1, DUAL>(c, a);
+    else if (nt == 2) launch_gemv_t<WT, 2, DUAL>(c, a);
+    else launch_gemv_t<WT, 4, DUAL>(c, a);
+}
+
+// K values the register path covers: K/32 a power of two up to 32, or 64, or 96.
+bool reg_path_ok(int K) {
+    const int b = K / kQK;
+    return (b <= 32 && (b & (b - 1)) == 0) || b == 64 || b == 96;
 }
 
 void gemv(q3t_dev * c, const GemvSpec & s, int nt) {
@@ -284,11 +308,14 @@ void gemv(q3t_dev * c, const GemvSpec & s, int nt) {
     a.done = &c->st->done;
     a.pro = s.norm_w ? PRO_NORM : PRO_NONE;
     a.epi = s.epi;
+    // 1-2 tokens take the register path; more tokens (prefill chunks of 4)
+    // take the LDS path, which reads plain fp32 rows only
+    const bool reg = nt <= 2 && reg_path_ok(s.K);
     const bool dual = s.epi == EPI_SWIGLU;
     switch (s.w.kind) {
-        case W_Q8: dual ? launch_gemv_nt<W_Q8, true>(c, a, nt) : launch_gemv_nt<W_Q8, false>(c, a, nt); break;
-        case W_F16: dual ? launch_gemv_nt<W_F16, true>(c, a, nt) : launch_gemv_nt<W_F16, false>(c, a, nt); break;
-        default: launch_gemv_nt<W_F16W, false>(c, a, nt); break;
+        case W_Q8: dual ? launch_gemv_nt<W_Q8, true>(c, a, nt, reg) : launch_gemv_nt<W_Q8, false>(c, a, nt, reg); break;
+        case W_F16: dual ? launch_gemv_nt<W_F16, true>(c, a, nt, reg) : launch_gemv_nt<W_F16, false>(c, a, nt, reg); break;
+        default: launch_gemv_nt<W_F16W, false>(c, a, nt, reg); break;
     }
 }
 
@@ -343,9 +370,9 @@ void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int ffn, 
     gemv(c, dn, nt);
 }
 
-// Talker forward of nt (<= 4) tokens whose input rows are `xin`.  The
-// codec head runs on the last row when `head` is set (normed hidden of that
-// row -> c->hidden, logits -> c->logits).
+// Talker forward of nt (<= 4) tokens whose input rows are `xin`.  The codec
+// head runs on the last row when `head` is set (normed hidden of that row ->
+// c->hidden, logits -> c->logits).
 void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_ptr, int pos_const, bool head) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size;
@@ -362,25 +389,31 @@ void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_pt
     }
 }
 
-// Code predictor for the frame in c->st (codes[0] set), reading the talker's
-// normed hidden from c->hidden; fills st->codes[1..15] and c->cp_logits.
-void code_pred_seq(q3t_dev * c) {
+SampleArgs sample_args(q3t_dev * c, int mode, int group) {
+    const q3t_config & g = c->cfg;
+    SampleArgs sa{};
+    sa.mode = mode; sa.group = group;
+    sa.vocab = mode == 0 ? g.codec_vocab : g.cp_vocab;
+    sa.logits = mode == 0 ? c->logits : c->cp_logits + (size_t) (group - 1) * g.cp_vocab;
+    sa.params = c->params; sa.st = c->st; sa.seen = c->seen; sa.eos_id = g.codec_eos_id;
+    sa.stage = c->stage; sa.hidden = c->hidden; sa.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; i < g.n_codebooks - 1; ++i) sa.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    sa.trailing = c->trailing; sa.n_trailing = c->n_trailing; sa.pad = c->pad;
+    sa.d = g.hidden_size;
+    return sa;
+}
+
+// Code predictor for the frame in c->st.  Its prefill rows [hidden;
+// codec_embd[codebook-0 token]] are already in c->stage; each sampler gathers
+// the next step's input row into c->stage.  Fills st->codes[1..15] and
+// c->cp_logits; in the frame loop the codebook-15 sampler emits the frame and
+// gathers the talker step embedding.
+void code_pred_seq(q3t_dev * c, bool frame_loop) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size;
     const size_t lstride = (size_t) g.n_kv_head * 16 * g.head_dim;
-    EmbedArgs e{};
-    e.st = c->st; e.codec_embd = (const uint16_t *) c->codec_embd.data;
-    for (int i = 0; i < g.n_codebooks - 1; ++i) e.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
-    e.hidden = c->hidden; e.trailing = c->trailing; e.n_trailing = c->n_trailing; e.pad = c->pad;
-    e.x = c->stage; e.d = d;
-    const dim3 eg((d + kBlock - 1) / kBlock);
-    SampleArgs sa{};
-    sa.vocab = g.cp_vocab; sa.mode = 1; sa.params = c->params; sa.st = c->st; sa.seen = c->seen; sa.eos_id = g.codec_eos_id;
     for (int step = 0; step < g.n_codebooks - 1; ++step) {
         const int nt = step == 0 ? 2 : 1;
-        e.mode = step == 0 ? 0 : 1;
-        e.group = step + 1;
-        hipLaunchKernelGGL(k_embed, eg, dim3(kBlock), 0, c->stream, e);
         const int pos = step == 0 ? 0 : step + 1;
         for (int il = 0; il < g.cp_layers; ++il)
             layer(c, c->cp[il], il == 0 ? c->stage : c->xa, nt, g.cp_ffn, c->cpk + il * lstride, c->cpv + il * lstride,
@@ -390,29 +423,22 @@ void code_pred_seq(q3t_dev * c) {
         h.x = c->xa + (size_t) (nt - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->cp_out_norm.data;
         h.y = c->cp_logits + (size_t) step * g.cp_vocab; h.y_stride = g.cp_vocab;
         gemv(c, h, 1);
-        sa.logits = c->cp_logits + (size_t) step * g.cp_vocab;
-        sa.group = step + 1;
+        SampleArgs sa = sample_args(c, 1, step + 1);
+        if (frame_loop) sa.codes_out = c->codes_out;
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
     }
 }
 
-// One whole frame: cb0 sample, code predictor, step embedding, talker step,
-// emit.  Everything reads its dynamic inputs from c->st.
+// One whole frame: open the frame and sample codebook 0 (gathering the
+// code-predictor prefill rows), the code predictor (emits the frame and
+// gathers the step embedding), the talker step.  Every kernel reads its
+// dynamic inputs from c->st.
 void frame_seq(q3t_dev * c) {
-    const q3t_config & g = c->cfg;
-    SampleArgs sa{};
-    sa.logits = c->logits; sa.vocab = g.codec_vocab; sa.mode = 0; sa.group = 0;
-    sa.params = c->params; sa.st = c->st; sa.seen = c->seen; sa.eos_id = g.codec_eos_id;
+    SampleArgs sa = sample_args(c, 0, 0);
+    sa.open_frame = 1;
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
-    code_pred_seq(c);
-    EmbedArgs e{};
-    e.mode = 2; e.st = c->st; e.codec_embd = (const uint16_t *) c->codec_embd.data;
-    for (int i = 0; i < g.n_codebooks - 1; ++i) e.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
-    e.hidden = c->hidden; e.trailing = c->trailing; e.n_trailing = c->n_trailing; e.pad = c->pad;
-    e.x = c->stage; e.d = g.hidden_size;
-    hipLaunchKernelGGL(k_embed, dim3((g.hidden_size + kBlock - 1) / kBlock), dim3(kBlock), 0, c->stream, e);
-    talker_chunk(c, c->stage, 1, &c->st->n_past, 0, true);
-    hipLaunchKernelGGL(k_frame_end, dim3(1), dim3(64), 0, c->stream, c->st, c->codes_out, g.n_codebooks);
+    code_pred_seq(c, true);
+    talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
 }
 
 int set_state(q3t_dev * c, const FrameState & s) {
@@ -743,10 +769,10 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     if (n_past < 0 || n_past + 1 > c->n_ctx) return fail(c, "Context length exceeded");
     const q3t_config & g = c->cfg;
     FrameState s{};
-    s.n_past = n_past;
+    s.talker_pos = n_past;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
-    talker_chunk(c, c->stage, 1, &c->st->n_past, 0, true);
+    talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
     if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden, (size_t) g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
     return sync(c);
@@ -771,7 +797,9 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     s.frame = (int32_t) frame;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->hidden, hidden, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
-    code_pred_seq(c);
+    hipLaunchKernelGGL(k_cp_input, dim3((g.hidden_size + 255) / 256), dim3(256), 0, c->stream, c->st, c->hidden,
+                       (const uint16_t *) c->codec_embd.data, g.hidden_size, c->stage);
+    code_pred_seq(c, false);
     FrameState r{};
     HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
     if (logits_out)
@@ -896,7 +924,8 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     p.seed = a->sampling.seed;
     HIP_OK(hipMemcpyAsync(c->params, &p, sizeof p, hipMemcpyHostToDevice, c->stream));
     FrameState s{};
-    s.n_past = a->n_past;
+    s.base_pos = a->n_past;
+    s.talker_pos = a->n_past;
     s.max_frames = a->max_len;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemsetAsync(c->seen, 0, (size_t) g.codec_vocab, c->stream));
@@ -921,7 +950,13 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     if (!c->frames_ready) return fail(c, "frames_begin not called");
     HIP_OK(hipSetDevice(c->device));
     n_frames = std::max(0, std::min(n_frames, c->frames_max - c->frames_launched));
-    for (int i = 0; i < n_frames; ++i) HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
+    // Q3T_NO_GRAPH=1 enqueues the frame's kernels directly (for tracers that
+    // do not follow graph launches); the kernels and results are the same.
+    static const bool no_graph = [] { const char * e = std::getenv("Q3T_NO_GRAPH"); return e && e[0] == '1'; }();
+    for (int i = 0; i < n_frames; ++i) {
+        if (no_graph) frame_seq(c);
+        else HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
+    }
     c->frames_launched += n_frames;
     FrameState r{};
     HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
@@ -957,7 +992,7 @@ int q3t_dev_time_kernel(q3t_dev * c, int32_t which, int32_t iters, double * avg_
     if (which < 0 || which > 4) return fail(c, "unknown kernel class");
     {
         FrameState st{};
-        st.n_past = pos;
+        st.talker_pos = pos;
         if (set_state(c, st)) return -1;
     }
     auto enqueue = [&]() {
@@ -987,7 +1022,7 @@ int q3t_dev_time_kernel(q3t_dev * c, int32_t which, int32_t iters, double * avg_
                 bytes = wbytes(L.wo);
                 break;
             case 4: {
-                AttnSpec as{c->qkv, &L, c->kc, c->vc, c->n_ctx, c->rope_cos, c->rope_sin, &c->st->n_past, 0};
+                AttnSpec as{c->qkv, &L, c->kc, c->vc, c->n_ctx, c->rope_cos, c->rope_sin, &c->st->talker_pos, 0};
                 attention(c, as, 1);
                 bytes = 2.0 * (double) (pos + 1) * kd * 2;   // K and V rows read
                 break;

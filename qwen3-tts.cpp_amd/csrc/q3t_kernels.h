@@ -10,9 +10,12 @@
 //                 for one (query head, token); replaces :1667-1730.
 //   k_sample      codec-head / code-predictor sampler on device; replaces the
 //                 host sampler at :3109-3184 and sample_or_argmax :2750-2788.
-//   k_embed       embedding gathers and the step-embedding sum (:3264-3295,
-//                 :2790-2793, :2091).
-//   k_frame_end   emits the frame's 16 codes and advances n_past / frame.
+//                 It also gathers the next pass's input rows: the
+//                 code-predictor inputs (:2790-2793, :2091) and the talker
+//                 step embedding (:3264-3295).
+//   k_gemv_r      (q3t_gemv_reg.h) the decode-loop GEMV for 1-2 tokens:
+//                 weights prefetched into registers at entry, activation
+//                 normalised/quantised per lane in registers.
 #pragma once
 
 #include "q3t_numerics.h"
@@ -23,16 +26,19 @@ enum WeightKind { W_Q8 = 0, W_F16 = 1, W_F16W = 2 };
 enum Prologue { PRO_NONE = 0, PRO_NORM = 1 };
 enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_BIAS = 2, EPI_BIAS_SILU = 3, EPI_SWIGLU = 4 };
 
-// Device-resident state of the frame loop (one per context).
+// Device-resident state of the frame loop (one per context).  The
+// codebook-0 sampler opens a frame (frame = next_frame++, talker_pos =
+// base_pos + frame); the codebook-15 sampler emits the frame's codes.
 struct FrameState {
-    int32_t n_past;      // talker positions in the KV cache
+    int32_t talker_pos;  // position the talker step of this frame writes
     int32_t frame;       // index of the frame being generated
-    int32_t done;        // 1 once EOS was sampled or max_frames were emitted: every kernel exits early
+    int32_t done;        // 1 once EOS was sampled or max_frames were opened: every kernel exits early
     int32_t n_emitted;   // frames written to codes_out
     int32_t codes[16];   // codes of the current frame
     int32_t max_frames;  // capacity of codes_out (and of the KV positions reserved for the loop)
     int32_t eos;         // 1 once codebook 0 sampled EOS
-    int32_t pad[2];
+    int32_t base_pos;    // talker position of frame 0's step (the prefill length)
+    int32_t next_frame;  // frame index the next codebook-0 sampler opens
 };
 
 struct SampleParams {
@@ -410,6 +416,18 @@ struct SampleArgs {
     FrameState * st;
     uint8_t * seen;               // talker: codebook-0 tokens already generated
     int32_t eos_id;
+    int32_t open_frame;           // mode 0: open a frame (frame loop); 0 for standalone calls
+    int32_t * codes_out;          // mode 1, group 15: frame loop emits [frame][16] here (NULL: no emit)
+    // input rows of the next pass, gathered once the token is known:
+    //   mode 0        stage = [hidden; codec_embd[tok]]          (code-predictor prefill)
+    //   mode 1, g<15  stage = code_pred_embd[g-1][tok]            (code-predictor step g)
+    //   mode 1, g=15  stage = step embedding of the frame when codes_out is set (talker step)
+    float * stage;
+    const float * hidden;
+    const uint16_t * codec_embd;
+    const uint16_t * cp_embd[15];
+    const float * trailing; int32_t n_trailing; const float * pad;
+    int32_t d;
 };
 
 constexpr int kSampleThreads = 1024;
@@ -425,7 +443,18 @@ __device__ __forceinline__ float key2f(uint32_t k) {
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     FrameState * st = a.st;
-    if (st->done) return;
+    __shared__ int32_t s_frame;
+    if (threadIdx.x == 0) {
+        int32_t f = st->frame;
+        if (a.mode == 0 && a.open_frame && !st->done) {
+            f = st->next_frame;
+            if (f >= st->max_frames) st->done = 1;
+            else { st->frame = f; st->next_frame = f + 1; st->talker_pos = st->base_pos + f; }
+        }
+        s_frame = st->done ? -1 : f;
+    }
+    __syncthreads();
+    if (s_frame < 0) return;
     __shared__ float l[kMaxVocab];
     __shared__ uint32_t hist[256];
     __shared__ double dsc[kSampleThreads];
@@ -435,7 +464,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     __shared__ int32_t pick[2];
     const int t = threadIdx.x, V = a.vocab;
     const SampleParams & P = *a.params;
-    const int frame = st->frame;
+    const int frame = s_frame;
 
     for (int i = t; i < V; i += kSampleThreads) {
         float v = a.logits[i];
@@ -577,51 +606,45 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             else a.seen[tok] = 1;
         } else {
             st->codes[a.group] = tok;
+            if (a.codes_out && a.group == 15) {
+                for (int g = 0; g < 15; ++g) a.codes_out[(size_t) frame * 16 + g] = st->codes[g];
+                a.codes_out[(size_t) frame * 16 + 15] = tok;
+                st->n_emitted = frame + 1;
+            }
+        }
+    }
+    if (!a.stage) return;
+    const size_t d = (size_t) a.d;
+    if (a.mode == 0) {
+        if (tok == a.eos_id) return;
+        for (int e = t; e < a.d; e += kSampleThreads) {
+            a.stage[e] = a.hidden[e];
+            a.stage[d + e] = h2f(a.codec_embd[(size_t) tok * d + e]);
+        }
+    } else if (a.group < 15) {
+        for (int e = t; e < a.d; e += kSampleThreads) a.stage[e] = h2f(a.cp_embd[a.group - 1][(size_t) tok * d + e]);
+    } else if (a.codes_out) {
+        // step embedding (src/tts_transformer.cpp:3264-3295), summed in the reference order
+        __shared__ int32_t sc[16];
+        if (t < 15) sc[t] = st->codes[t];
+        __syncthreads();
+        for (int e = t; e < a.d; e += kSampleThreads) {
+            float s = h2f(a.codec_embd[(size_t) sc[0] * d + e]);
+            for (int g = 1; g < 15; ++g) s = s + h2f(a.cp_embd[g - 1][(size_t) sc[g] * d + e]);
+            s = s + h2f(a.cp_embd[14][(size_t) tok * d + e]);
+            const float tr = frame < a.n_trailing ? a.trailing[(size_t) frame * d + e] : a.pad[e];
+            a.stage[e] = s + tr;
         }
     }
 }
 
-// ------------------------------------------------------------- embeddings
-struct EmbedArgs {
-    int32_t mode;     // 0: code-predictor prefill rows, 1: code-predictor step row, 2: talker step sum
-    int32_t group;    // mode 1: codebook g being predicted (2..15)
-    const FrameState * st;
-    const uint16_t * codec_embd;
-    const uint16_t * cp_embd[15];
-    const float * hidden;
-    const float * trailing; int32_t n_trailing;
-    const float * pad;
-    float * x;
-    int32_t d;
-};
-
-__global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
-    const FrameState * st = a.st;
-    if (st->done) return;
-    const int e = blockIdx.x * kBlock + threadIdx.x;
-    if (e >= a.d) return;
-    const size_t d = (size_t) a.d;
-    if (a.mode == 0) {
-        a.x[e] = a.hidden[e];
-        a.x[d + e] = h2f(a.codec_embd[(size_t) st->codes[0] * d + e]);
-    } else if (a.mode == 1) {
-        a.x[e] = h2f(a.cp_embd[a.group - 2][(size_t) st->codes[a.group - 1] * d + e]);
-    } else {
-        float s = h2f(a.codec_embd[(size_t) st->codes[0] * d + e]);
-        for (int g = 1; g < 16; ++g) s = s + h2f(a.cp_embd[g - 1][(size_t) st->codes[g] * d + e]);
-        const int f = st->frame;
-        const float tr = f < a.n_trailing ? a.trailing[(size_t) f * d + e] : a.pad[e];
-        a.x[e] = s + tr;
-    }
-}
-
-__global__ void k_frame_end(FrameState * st, int32_t * codes_out, int32_t n_cb) {
-    if (threadIdx.x != 0 || st->done) return;
-    for (int g = 0; g < n_cb; ++g) codes_out[(size_t) st->n_emitted * n_cb + g] = st->codes[g];
-    st->n_emitted += 1;
-    st->n_past += 1;
-    st->frame += 1;
-    if (st->n_emitted >= st->max_frames) st->done = 1;   // no KV position is used past the reserved range
+// code-predictor prefill input rows for a standalone call: [hidden; codec_embd[codes[0]]]
+__global__ void k_cp_input(const FrameState * st, const float * hidden, const uint16_t * codec_embd, int32_t d,
+                           float * stage) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= d) return;
+    stage[e] = hidden[e];
+    stage[d + e] = h2f(codec_embd[(size_t) st->codes[0] * d + e]);
 }
 
 // normed rows for the prefill's all-token hidden output
@@ -651,3 +674,5 @@ __global__ void k_gather_rows(const uint16_t * table, int64_t dim, const int32_t
 }
 
 }  // namespace q3t
+
+#include "q3t_gemv_reg.h"

@@ -58,6 +58,33 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return v;
 }
 
+// Cross-lane moves through DPP (VALU, a few cycles) instead of ds_bpermute.
+// ctrl: 0xB1 = quad_perm[1,0,3,2] (xor 1), 0x4E = quad_perm[2,3,0,1] (xor 2),
+// 0x141 = row_half_mirror (lane i <-> 7-i), 0x140 = row_mirror (i <-> 15-i).
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+// lane i <-> i ^ 16 within each 32-lane half (ds_swizzle bit mode, xor_mask 0x10)
+__device__ __forceinline__ double swz16_d(double v) {
+    const int lo = __builtin_amdgcn_ds_swizzle(__double2loint(v), 0x401F);
+    const int hi = __builtin_amdgcn_ds_swizzle(__double2hiint(v), 0x401F);
+    return __hiloint2double(hi, lo);
+}
+// Sum over each aligned group of n lanes (n = 8, 16 or 32, a power of two
+// <= 32).  Every lane of a group ends with the bitwise-same value (each step
+// adds a lane's value and its partner's, and fp addition commutes).
+__device__ __forceinline__ double group_sum_d(double v, int n) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    if (n > 4) v += dpp_d<0x141>(v);
+    if (n > 8) v += dpp_d<0x140>(v);
+    if (n > 16) v += swz16_d(v);
+    return v;
+}
+
 // Workgroup-wide fp64 sum for 256 threads; every thread gets the same value.
 // red: 4 doubles of LDS.
 __device__ __forceinline__ double block_sum_d(double v, double * red) {
