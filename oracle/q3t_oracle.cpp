@@ -778,6 +778,9 @@ int orc_build_prefill(orc_model * m, const int32_t * text, int32_t n_text,
     return plen;
 }
 
+int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const float * trail, int32_t trail_len,
+                      const float * pad, const orc_gen_params * p, int32_t * codes_out, float * first_logits_out);
+
 int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
                  const float * speaker, const orc_gen_params * p,
                  const int32_t * instruct, int32_t n_instruct,
@@ -786,16 +789,27 @@ int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
     if (n_text < 4) { m->err = "Need at least 4 text tokens for generation"; return -1; }
     if (p->max_len <= 0) return 0;
     const int64_t d = c.hidden_size;
-    const int32_t ncb = c.n_codebooks;
     std::vector<float> pre((size_t) (std::max(0, n_instruct) + 10) * d);
     std::vector<float> trail((size_t) (std::max(0, n_text - 9) + 1) * d), pad(d);
     int32_t trail_len = 0;
     const int32_t plen = orc_build_prefill(m, text, n_text, speaker, p->language_id, instruct, n_instruct,
                                            pre.data(), trail.data(), pad.data(), &trail_len);
     if (plen < 0) return -1;
+    return orc_generate_rows(m, pre.data(), plen, trail.data(), trail_len, pad.data(), p, codes_out, first_logits_out);
+}
+
+// generate() from prebuilt prefill rows (src/tts_transformer.cpp:3061-3309;
+// generate_icl shares the loop, :3425-3640).
+int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const float * trail, int32_t trail_len,
+                      const float * pad_row, const orc_gen_params * p, int32_t * codes_out, float * first_logits_out) {
+    const orc_config & c = m->cfg;
+    if (p->max_len <= 0) return 0;
+    const int64_t d = c.hidden_size;
+    const int32_t ncb = c.n_codebooks;
+    std::vector<float> pad(pad_row, pad_row + d);
     orc_kv_reset(m, plen + p->max_len + 8);
     std::vector<float> logits(c.codec_vocab);
-    if (orc_prefill(m, pre.data(), plen, 0, nullptr, logits.data())) return -1;
+    if (orc_prefill(m, pre, plen, 0, nullptr, logits.data())) return -1;
     if (first_logits_out) std::memcpy(first_logits_out, logits.data(), logits.size() * sizeof(float));
     std::vector<uint8_t> seen(c.codec_vocab, 0);
     std::vector<int32_t> frame_codes(ncb), cps(ncb - 1);
@@ -835,7 +849,7 @@ int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
             embd_row(m->cp_embd[g - 1], d, frame_codes[g], row.data());
             for (int64_t h = 0; h < d; ++h) step[h] += row[h];
         }
-        const float * tr = frame < trail_len ? trail.data() + (size_t) frame * d : pad.data();
+        const float * tr = frame < trail_len ? trail + (size_t) frame * d : pad.data();
         for (int64_t h = 0; h < d; ++h) step[h] += tr[h];
         if (orc_step(m, step.data(), n_past, logits.data(), nullptr)) return -1;
         ++n_past;

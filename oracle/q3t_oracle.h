@@ -171,6 +171,12 @@ int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
                  const int32_t * instruct, int32_t n_instruct,
                  int32_t * codes_out, float * first_logits_out);
 
+/* the generate() frame loop from prebuilt rows (prefill [plen][d],
+ * trailing [trail_len][d], tts_pad [d]); used for the ICL layout. */
+int orc_generate_rows(orc_model * m, const float * prefill, int32_t plen, const float * trailing,
+                      int32_t trail_len, const float * pad, const orc_gen_params * p,
+                      int32_t * codes_out, float * first_logits_out);
+
 #ifdef __cplusplus
 }
 #endif

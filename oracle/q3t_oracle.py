@@ -81,6 +81,7 @@ def lib():
         L.orc_embed_row.argtypes = [vp, ctypes.c_char_p, i32, i32, vp]
         L.orc_build_prefill.argtypes = [vp, vp, i32, vp, i32, vp, i32, vp, vp, vp, ctypes.POINTER(i32)]
         L.orc_generate.argtypes = [vp, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, i32, vp, vp]
+        L.orc_generate_rows.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, vp]
         _lib = L
     return _lib
 
@@ -292,3 +293,17 @@ class Oracle:
         if n < 0:
             raise RuntimeError(self.error())
         return codes[:n].copy(), first
+
+    def generate_rows(self, prefill, trailing, pad, max_len=64, repetition_penalty=1.05, temperature=0.0, top_k=0,
+                      eos_bias=0.0, target_frames=0, rep_loop_detect=False, seed=0):
+        prefill = np.ascontiguousarray(prefill, np.float32)
+        trailing = np.ascontiguousarray(trailing, np.float32).reshape(-1, self.cfg.hidden_size)
+        pad = np.ascontiguousarray(pad, np.float32)
+        p = OrcGenParams(max_len, 0, repetition_penalty, temperature, top_k, eos_bias, target_frames,
+                         1 if rep_loop_detect else 0, seed)
+        codes = np.empty((max(max_len, 1), self.cfg.n_codebooks), np.int32)
+        n = self.L.orc_generate_rows(self.h, _p(prefill), prefill.shape[0], _p(trailing), trailing.shape[0], _p(pad),
+                                     ctypes.byref(p), _p(codes), None)
+        if n < 0:
+            raise RuntimeError(self.error())
+        return codes[:n].copy()

@@ -1,0 +1,501 @@
+// tts_transformer.cpp -- TTSTransformer over the MI355X device layer.
+//
+// Host control flow restated from the reference (src/tts_transformer.cpp):
+// GGUF key parsing (:228-377), prefill layouts (:1030-1472), forward
+// wrappers (:2217-2509), the generate()/generate_icl() frame loops
+// (:3007-3656).  Every tensor operation goes through include/q3t_dev.h.
+#include "tts_transformer.h"
+
+#include "../../include/q3t_dev.h"
+#include "gguf_reader.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <initializer_list>
+
+namespace qwen3_tts {
+
+namespace {
+
+q3t_config to_dev_config(const tts_transformer_config & c) {
+    q3t_config d{};
+    d.hidden_size = c.hidden_size; d.n_layers = c.n_layers; d.n_head = c.n_attention_heads;
+    d.n_kv_head = c.n_key_value_heads; d.head_dim = c.head_dim; d.ffn_size = c.intermediate_size;
+    d.codec_vocab = c.codec_vocab_size; d.n_codebooks = c.n_codebooks; d.cp_layers = c.code_pred_layers;
+    d.cp_vocab = c.code_pred_vocab_size; d.cp_hidden = c.code_pred_hidden_size;
+    d.cp_ffn = c.code_pred_intermediate_size; d.text_vocab = c.text_vocab_size; d.text_embd_dim = c.text_embd_dim;
+    d.rms_eps = c.rms_norm_eps; d.rope_theta = c.rope_theta; d.cp_rope_theta = c.code_pred_rope_theta;
+    d.codec_pad_id = c.codec_pad_id; d.codec_bos_id = c.codec_bos_id; d.codec_eos_id = c.codec_eos_id;
+    d.tts_bos_id = c.tts_bos_token_id; d.tts_eos_id = c.tts_eos_token_id; d.tts_pad_id = c.tts_pad_token_id;
+    d.codec_think_id = c.codec_think_id; d.codec_nothink_id = c.codec_nothink_id;
+    d.codec_think_bos_id = c.codec_think_bos_id; d.codec_think_eos_id = c.codec_think_eos_id;
+    d.english_language_id = c.english_language_id;
+    return d;
+}
+
+// GGUF keys and fallbacks of parse_config (src/tts_transformer.cpp:250-374).
+void parse_config(const GGUFReader & g, tts_transformer_config & cfg) {
+    auto u32 = [&](std::initializer_list<const char *> keys, int32_t def) -> int32_t {
+        for (const char * k : keys) { uint32_t v; if (g.get_u32(k, v)) return (int32_t) v; }
+        return def;
+    };
+    auto f32 = [&](std::initializer_list<const char *> keys, float def) -> float {
+        for (const char * k : keys) { float v; if (g.get_f32(k, v)) return v; }
+        return def;
+    };
+    cfg.text_vocab_size = u32({"qwen3-tts.text.vocab_size", "qwen3-tts.text_vocab_size"}, 151936);
+    cfg.text_embd_dim = u32({"qwen3-tts.text.embedding_dim", "qwen3-tts.text_hidden_size"}, 2048);
+    cfg.hidden_size = u32({"qwen3-tts.talker.embedding_length", "qwen3-tts.embedding_length"}, 1024);
+    cfg.n_layers = u32({"qwen3-tts.talker.block_count", "qwen3-tts.block_count"}, 28);
+    cfg.n_attention_heads = u32({"qwen3-tts.talker.attention.head_count", "qwen3-tts.attention.head_count"}, 16);
+    cfg.n_key_value_heads = u32({"qwen3-tts.talker.attention.head_count_kv", "qwen3-tts.attention.head_count_kv"}, 8);
+    cfg.intermediate_size = u32({"qwen3-tts.talker.feed_forward_length", "qwen3-tts.feed_forward_length"}, 3072);
+    cfg.head_dim = u32({"qwen3-tts.talker.attention.key_length", "qwen3-tts.attention.key_length"}, 128);
+    cfg.rms_norm_eps = f32({"qwen3-tts.talker.attention.layer_norm_rms_epsilon",
+                            "qwen3-tts.attention.layer_norm_rms_epsilon"}, 1e-6f);
+    cfg.rope_theta = f32({"qwen3-tts.talker.rope.freq_base", "qwen3-tts.rope.freq_base"}, 1000000.0f);
+    cfg.codec_vocab_size = u32({"qwen3-tts.talker.codec_vocab_size", "qwen3-tts.vocab_size"}, 3072);
+    cfg.n_codebooks = u32({"qwen3-tts.talker.num_codebooks", "qwen3-tts.num_code_groups"}, 16);
+    cfg.code_pred_layers = u32({"qwen3-tts.code_pred.layer_count", "qwen3-tts.code_predictor.layer_count"}, 5);
+    cfg.code_pred_vocab_size = u32({"qwen3-tts.code_pred.vocab_size", "qwen3-tts.code_predictor.vocab_size"}, 2048);
+    cfg.code_pred_hidden_size = u32({"qwen3-tts.code_pred.embedding_length",
+                                     "qwen3-tts.code_predictor.embedding_length"}, 1024);
+    cfg.code_pred_intermediate_size = u32({"qwen3-tts.code_pred.feed_forward_length",
+                                           "qwen3-tts.code_predictor.feed_forward_length"}, 3072);
+    // code-predictor theta falls back to the talker's (both HF configs use 1e6)
+    cfg.code_pred_rope_theta = f32({"qwen3-tts.code_pred.rope.freq_base", "qwen3-tts.code_predictor.rope.freq_base"},
+                                   cfg.rope_theta);
+    cfg.codec_pad_id = u32({"qwen3-tts.codec.pad_id"}, 2148);
+    cfg.codec_bos_id = u32({"qwen3-tts.codec.bos_id"}, 2149);
+    cfg.codec_eos_id = u32({"qwen3-tts.codec.eos_id", "qwen3-tts.codec.eos_token_id"}, 2150);
+    cfg.tts_bos_token_id = u32({"qwen3-tts.tts_bos_token_id", "qwen3-tts.tts.bos_token_id", "qwen3-tts.tts.bos_id"}, 151672);
+    cfg.tts_eos_token_id = u32({"qwen3-tts.tts_eos_token_id", "qwen3-tts.tts.eos_token_id", "qwen3-tts.tts.eos_id"}, 151673);
+    cfg.tts_pad_token_id = u32({"qwen3-tts.tts_pad_token_id", "qwen3-tts.tts.pad_token_id", "qwen3-tts.tts.pad_id"}, 151671);
+    cfg.codec_think_id = u32({"qwen3-tts.codec.think_id", "qwen3-tts.codec_think_id"}, 2154);
+    cfg.codec_nothink_id = u32({"qwen3-tts.codec.nothink_id", "qwen3-tts.codec_nothink_id"}, 2155);
+    cfg.codec_think_bos_id = u32({"qwen3-tts.codec.think_bos_id", "qwen3-tts.codec_think_bos_id"}, 2156);
+    cfg.codec_think_eos_id = u32({"qwen3-tts.codec.think_eos_id", "qwen3-tts.codec_think_eos_id"}, 2157);
+    cfg.english_language_id = u32({"qwen3-tts.language.english_id", "qwen3-tts.codec.language.english_id",
+                                   "qwen3-tts.language_id"}, 2050);
+}
+
+uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+}  // namespace
+
+TTSTransformer::TTSTransformer() = default;
+
+TTSTransformer::~TTSTransformer() { unload_model(); }
+
+bool TTSTransformer::dev_ok(int rc) {
+    if (rc == 0) return true;
+    error_msg_ = dev_ ? q3t_dev_last_error(dev_) : "device not initialised";
+    if (error_msg_.empty()) error_msg_ = "device call failed";
+    return false;
+}
+
+void TTSTransformer::unload_model() {
+    if (dev_) { q3t_dev_destroy(dev_); dev_ = nullptr; }
+    last_hidden_.clear();
+    kv_n_ctx_ = 0;
+    kv_n_used_ = 0;
+}
+
+void TTSTransformer::set_n_threads(int32_t) {}
+
+bool TTSTransformer::load_model(const std::string & model_path) {
+    unload_model();
+    GGUFReader g;
+    if (!g.open(model_path)) { error_msg_ = g.error(); return false; }
+    parse_config(g, config_);
+    const q3t_config dc = to_dev_config(config_);
+    int device = 0;
+    if (const char * e = std::getenv("QWEN3_TTS_DEVICE")) device = std::atoi(e);
+    const int rc = q3t_dev_create(&dc, device, &dev_);
+    if (rc != 0) {
+        error_msg_ = dev_ ? q3t_dev_last_error(dev_) : "no HIP device available for TTSTransformer";
+        if (dev_) { q3t_dev_destroy(dev_); dev_ = nullptr; }
+        return false;
+    }
+    std::vector<uint8_t> buf;
+    for (const GGUFTensorInfo & t : g.tensors()) {
+        if (t.name.find("spk_enc.") != std::string::npos || t.name.find("tok_") != std::string::npos) continue;
+        if (t.nbytes == 0) continue;
+        if (!g.read_tensor(t, buf)) { error_msg_ = g.error(); unload_model(); return false; }
+        if (!dev_ok(q3t_dev_upload_tensor(dev_, t.name.c_str(), t.type, t.ne, buf.data(), buf.size()))) {
+            unload_model();
+            return false;
+        }
+    }
+    fprintf(stderr, "  TTSTransformer backend: HIP (MI355X frame loop)\n");
+    return true;
+}
+
+bool TTSTransformer::init_kv_cache(int32_t n_ctx) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!dev_ok(q3t_dev_kv_reserve(dev_, n_ctx))) return false;
+    kv_n_ctx_ = n_ctx;
+    kv_n_used_ = 0;
+    return true;
+}
+
+void TTSTransformer::clear_kv_cache() { kv_n_used_ = 0; }
+
+// The device keeps a fixed 16-position code-predictor cache per context
+// (the most a frame uses: 2-token prefill + 14 steps).
+bool TTSTransformer::init_code_pred_kv_cache(int32_t n_ctx) {
+    if (n_ctx > 16) { error_msg_ = "code predictor cache holds 16 positions"; return false; }
+    return true;
+}
+
+void TTSTransformer::clear_code_pred_kv_cache() {}
+
+bool TTSTransformer::lookup_rows(int32_t table, int32_t index, const int32_t * ids, int32_t n,
+                                 std::vector<float> & out) {
+    const int32_t dim = table == 2 ? config_.text_embd_dim : config_.hidden_size;
+    out.resize((size_t) n * dim);
+    return dev_ok(q3t_dev_embed_rows(dev_, table, index, ids, n, out.data()));
+}
+
+bool TTSTransformer::project_text_tokens(const int32_t * text_tokens, int32_t n_tokens, std::vector<float> & output) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (n_tokens <= 0) { output.clear(); return true; }
+    output.resize((size_t) n_tokens * config_.hidden_size);
+    return dev_ok(q3t_dev_text_proj(dev_, text_tokens, n_tokens, output.data()));
+}
+
+bool TTSTransformer::forward_prefill(const float * prefill_embd, int32_t n_tokens, int32_t n_past,
+                                     std::vector<float> & output, std::vector<float> * logits_out) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!prefill_embd) { error_msg_ = "prefill_embd is null"; return false; }
+    if (n_tokens <= 0) { error_msg_ = "n_tokens must be > 0"; return false; }
+    if (kv_n_ctx_ == 0 && !init_kv_cache(std::max<int32_t>(256, n_past + n_tokens + 16))) return false;
+    if (n_past + n_tokens > kv_n_ctx_) { error_msg_ = "Context length exceeded"; return false; }
+    const int32_t d = config_.hidden_size;
+    output.resize((size_t) n_tokens * d);
+    std::vector<float> logits(config_.codec_vocab_size);
+    if (!dev_ok(q3t_dev_prefill(dev_, prefill_embd, n_tokens, n_past, output.data(), logits.data()))) return false;
+    last_hidden_.assign(output.end() - d, output.end());
+    if (logits_out) *logits_out = logits;
+    kv_n_used_ = n_past + n_tokens;
+    return true;
+}
+
+bool TTSTransformer::forward_text(const int32_t * text_tokens, int32_t n_tokens, const float * speaker_embd,
+                                  int32_t n_past, std::vector<float> & output) {
+    if (!text_tokens) { error_msg_ = "text_tokens is null"; return false; }
+    if (n_tokens <= 0) { error_msg_ = "n_tokens must be > 0"; return false; }
+    std::vector<float> projected;
+    if (!project_text_tokens(text_tokens, n_tokens, projected)) return false;
+    if (speaker_embd) {
+        const int32_t d = config_.hidden_size;
+        for (int32_t t = 0; t < n_tokens; ++t)
+            for (int32_t h = 0; h < d; ++h) projected[(size_t) t * d + h] += speaker_embd[h];
+    }
+    return forward_prefill(projected.data(), n_tokens, n_past, output, nullptr);
+}
+
+bool TTSTransformer::forward_step(const float * step_embd, int32_t n_past, std::vector<float> & output,
+                                  std::vector<float> * hidden_out) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!step_embd) { error_msg_ = "step_embd is null"; return false; }
+    if (kv_n_ctx_ == 0 && !init_kv_cache(std::max<int32_t>(256, n_past + 1 + 16))) return false;
+    if (n_past + 1 > kv_n_ctx_) { error_msg_ = "Context length exceeded"; return false; }
+    output.resize(config_.codec_vocab_size);
+    last_hidden_.resize(config_.hidden_size);
+    if (!dev_ok(q3t_dev_talker_step(dev_, step_embd, n_past, output.data(), last_hidden_.data()))) return false;
+    if (hidden_out) *hidden_out = last_hidden_;
+    kv_n_used_ = n_past + 1;
+    return true;
+}
+
+bool TTSTransformer::forward_codec(int32_t codec_token, int32_t n_past, std::vector<float> & output) {
+    std::vector<float> row;
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!lookup_rows(0, 0, &codec_token, 1, row)) return false;
+    return forward_step(row.data(), n_past, output, nullptr);
+}
+
+bool TTSTransformer::get_hidden_states(std::vector<float> & hidden) const {
+    if (last_hidden_.empty()) return false;
+    hidden = last_hidden_;
+    return true;
+}
+
+// The reference's legacy single-pass predictor (build_code_pred_graph,
+// src/tts_transformer.cpp:1771-1899) is not used by generate(); the device
+// path does not implement it.
+bool TTSTransformer::predict_codes(const float *, const int32_t *, std::vector<float> &) {
+    error_msg_ = "predict_codes (legacy single-pass code predictor) is not available on the device path; "
+                 "use predict_codes_autoregressive";
+    return false;
+}
+
+bool TTSTransformer::predict_codes_autoregressive(const float * hidden, int32_t codebook_0_token,
+                                                  std::vector<int32_t> & output, float temperature, int32_t top_k) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (kv_n_ctx_ == 0 && !init_kv_cache(256)) return false;
+    output.resize(config_.n_codebooks - 1);
+    q3t_sampling s{temperature, top_k, seed_};
+    return dev_ok(q3t_dev_code_pred(dev_, hidden, codebook_0_token, &s, sample_calls_++, output.data(), nullptr));
+}
+
+bool TTSTransformer::build_prefill_graph(const int32_t * text_tokens, int32_t n_tokens, const float * speaker_embd,
+                                         int32_t language_id, std::vector<float> & prefill_embd,
+                                         std::vector<float> & trailing_text_hidden, std::vector<float> & tts_pad_embed,
+                                         const int32_t * instruct_tokens, int32_t n_instruct) {
+    if (!text_tokens) { error_msg_ = "text_tokens is null"; return false; }
+    if (n_tokens < 4) { error_msg_ = "Need at least 4 text tokens for prefill"; return false; }
+    const tts_transformer_config & cfg = config_;
+    const int32_t d = cfg.hidden_size;
+    int32_t special[3] = {cfg.tts_bos_token_id, cfg.tts_eos_token_id, cfg.tts_pad_token_id};
+    std::vector<float> sp, role, first, codec_rows, tail_rows;
+    if (!project_text_tokens(special, 3, sp) || !project_text_tokens(text_tokens, 3, role)) return false;
+    const float * bos_e = sp.data();
+    const float * eos_e = sp.data() + d;
+    tts_pad_embed.assign(sp.begin() + 2 * d, sp.begin() + 3 * d);
+    std::vector<int32_t> codec_tok;
+    if (language_id < 0) codec_tok = {cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id};
+    else codec_tok = {cfg.codec_think_id, cfg.codec_think_bos_id, language_id, cfg.codec_think_eos_id};
+    int32_t tail_tok[2] = {cfg.codec_pad_id, cfg.codec_bos_id};
+    if (!lookup_rows(0, 0, codec_tok.data(), (int32_t) codec_tok.size(), codec_rows) ||
+        !lookup_rows(0, 0, tail_tok, 2, tail_rows))
+        return false;
+    std::vector<float> cin = codec_rows;
+    if (speaker_embd) cin.insert(cin.end(), speaker_embd, speaker_embd + d);
+    cin.insert(cin.end(), tail_rows.begin(), tail_rows.end());
+    const int32_t in_len = (int32_t) (cin.size() / d);
+    const int32_t ov_len = in_len - 1;
+    if (!project_text_tokens(text_tokens + 3, 1, first)) return false;
+    std::vector<float> instr;
+    if (instruct_tokens && n_instruct > 0) {
+        if (!project_text_tokens(instruct_tokens, n_instruct, instr)) return false;
+    } else {
+        n_instruct = 0;
+    }
+    const int32_t plen = n_instruct + 3 + ov_len + 1;
+    prefill_embd.assign((size_t) plen * d, 0.0f);
+    std::copy(instr.begin(), instr.end(), prefill_embd.begin());
+    std::copy(role.begin(), role.end(), prefill_embd.begin() + (size_t) n_instruct * d);
+    for (int32_t t = 0; t < ov_len; ++t) {
+        const float * ov = (t == ov_len - 1) ? bos_e : tts_pad_embed.data();
+        float * dst = prefill_embd.data() + (size_t) (n_instruct + 3 + t) * d;
+        for (int32_t h = 0; h < d; ++h) dst[h] = ov[h] + cin[(size_t) t * d + h];
+    }
+    float * last = prefill_embd.data() + (size_t) (plen - 1) * d;
+    for (int32_t h = 0; h < d; ++h) last[h] = first[h] + cin[(size_t) (in_len - 1) * d + h];
+    const int32_t n_trail = std::max(0, n_tokens - 9);
+    std::vector<float> tr;
+    if (n_trail > 0 && !project_text_tokens(text_tokens + 4, n_trail, tr)) return false;
+    trailing_text_hidden = tr;
+    trailing_text_hidden.insert(trailing_text_hidden.end(), eos_e, eos_e + d);
+    return true;
+}
+
+bool TTSTransformer::build_prefill_graph_icl(const int32_t * text_tokens, int32_t n_tokens,
+                                             const int32_t * ref_text_tokens, int32_t n_ref_text,
+                                             const int32_t * ref_codec_tokens, int32_t n_ref_frames,
+                                             const float * speaker_embd, std::vector<float> & prefill_embd,
+                                             std::vector<float> & trailing_text_hidden,
+                                             std::vector<float> & tts_pad_embed) {
+    if (!text_tokens || n_tokens < 4) { error_msg_ = "ICL: need at least 4 target text tokens"; return false; }
+    if (!ref_codec_tokens || n_ref_frames < 1) { error_msg_ = "ICL: need at least 1 reference codec frame"; return false; }
+    const tts_transformer_config & cfg = config_;
+    const int32_t d = cfg.hidden_size;
+    int32_t special[3] = {cfg.tts_bos_token_id, cfg.tts_eos_token_id, cfg.tts_pad_token_id};
+    std::vector<float> sp, role, codec_rows, tail_rows;
+    if (!project_text_tokens(special, 3, sp) || !project_text_tokens(text_tokens, 3, role)) return false;
+    const float * bos_e = sp.data();
+    tts_pad_embed.assign(sp.begin() + 2 * d, sp.begin() + 3 * d);
+    // ICL prefix has no language token
+    int32_t codec_tok[3] = {cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id};
+    int32_t tail_tok[2] = {cfg.codec_pad_id, cfg.codec_bos_id};
+    if (!lookup_rows(0, 0, codec_tok, 3, codec_rows) || !lookup_rows(0, 0, tail_tok, 2, tail_rows)) return false;
+    std::vector<float> cin = codec_rows;
+    if (speaker_embd) cin.insert(cin.end(), speaker_embd, speaker_embd + d);
+    cin.insert(cin.end(), tail_rows.begin(), tail_rows.end());
+    const int32_t ov_len = (int32_t) (cin.size() / d) - 1;
+    prefill_embd.assign((size_t) (3 + ov_len) * d, 0.0f);
+    std::copy(role.begin(), role.end(), prefill_embd.begin());
+    for (int32_t t = 0; t < ov_len; ++t) {
+        const float * ov = (t == ov_len - 1) ? bos_e : tts_pad_embed.data();
+        float * dst = prefill_embd.data() + (size_t) (3 + t) * d;
+        for (int32_t h = 0; h < d; ++h) dst[h] = ov[h] + cin[(size_t) t * d + h];
+    }
+    // text stream: ref_text[3:-5] ++ target[3:-5] ++ tts_eos
+    std::vector<int32_t> text;
+    const int32_t r_end = std::max(3, n_ref_text - 5);
+    for (int32_t i = 3; i < r_end && i < n_ref_text; ++i) text.push_back(ref_text_tokens[i]);
+    const int32_t t_end = std::max(3, n_tokens - 5);
+    for (int32_t i = 3; i < t_end && i < n_tokens; ++i) text.push_back(text_tokens[i]);
+    text.push_back(cfg.tts_eos_token_id);
+    // codec stream: codec_bos, then each reference frame's summed embeddings
+    const int32_t n_codec = n_ref_frames + 1;
+    std::vector<float> codec((size_t) n_codec * d, 0.0f), row;
+    int32_t bos = cfg.codec_bos_id;
+    if (!lookup_rows(0, 0, &bos, 1, row)) return false;
+    std::copy(row.begin(), row.end(), codec.begin());
+    for (int32_t f = 0; f < n_ref_frames; ++f) {
+        float * dst = codec.data() + (size_t) (f + 1) * d;
+        int32_t c0 = ref_codec_tokens[(size_t) f * 16];
+        if (!lookup_rows(0, 0, &c0, 1, row)) return false;
+        std::copy(row.begin(), row.end(), dst);
+        for (int32_t cb = 1; cb < 16 && cb < cfg.n_codebooks; ++cb) {
+            int32_t tok = ref_codec_tokens[(size_t) f * 16 + cb];
+            if (!lookup_rows(1, cb - 1, &tok, 1, row)) return false;
+            for (int32_t h = 0; h < d; ++h) dst[h] += row[h];
+        }
+    }
+    const int32_t n_text = (int32_t) text.size();
+    std::vector<float> tp;
+    if (!project_text_tokens(text.data(), n_text, tp)) return false;
+    std::vector<float> icl((size_t) n_codec * d, 0.0f);
+    for (int32_t i = 0; i < n_codec; ++i) {
+        float * dst = icl.data() + (size_t) i * d;
+        const float * trow = i < n_text ? tp.data() + (size_t) i * d : tts_pad_embed.data();
+        for (int32_t h = 0; h < d; ++h) dst[h] += trow[h];
+        const float * crow = codec.data() + (size_t) i * d;
+        for (int32_t h = 0; h < d; ++h) dst[h] += crow[h];
+    }
+    prefill_embd.insert(prefill_embd.end(), icl.begin(), icl.end());
+    trailing_text_hidden.clear();
+    if (n_text > n_codec) trailing_text_hidden.assign(tp.begin() + (size_t) n_codec * d, tp.end());
+    return true;
+}
+
+bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::vector<float> & trailing,
+                                const std::vector<float> & pad, int32_t max_len, float repetition_penalty,
+                                float temperature, int32_t top_k, float eos_bias, int32_t target_frames,
+                                bool rep_loop_detect, const FrameCallback & on_frame, std::vector<int32_t> & output) {
+    const tts_transformer_config & cfg = config_;
+    const int32_t d = cfg.hidden_size, ncb = cfg.n_codebooks;
+    const int32_t plen = (int32_t) (prefill.size() / d);
+    const int32_t required = plen + max_len + 8;
+    if (kv_n_ctx_ < required || kv_n_ctx_ > std::max<int32_t>(required * 2, 512)) {
+        if (!init_kv_cache(required)) return false;
+    }
+    clear_kv_cache();
+    std::vector<float> hidden;
+    if (!forward_prefill(prefill.data(), plen, 0, hidden, nullptr)) return false;
+    q3t_frame_args a{};
+    a.trailing = trailing.empty() ? nullptr : trailing.data();
+    a.n_trailing = (int32_t) (trailing.size() / d);
+    a.tts_pad = pad.data();
+    a.n_past = plen;
+    a.max_len = max_len;
+    a.repetition_penalty = repetition_penalty;
+    a.eos_bias = eos_bias;
+    a.target_frames = target_frames;
+    a.sampling = q3t_sampling{temperature, top_k, seed_};
+    if (temperature > 0.0f) seed_ = splitmix64(seed_);   // next call draws a fresh stream
+    if (!dev_ok(q3t_dev_frames_begin(dev_, &a))) return false;
+    int chunk = 8;
+    if (const char * e = std::getenv("QWEN3_TTS_FRAME_CHUNK")) chunk = std::max(1, std::atoi(e));
+    output.clear();
+    output.reserve((size_t) max_len * ncb);
+    std::vector<int32_t> buf((size_t) chunk * ncb);
+    std::vector<std::vector<int32_t>> rep_frames;
+    int32_t rep_run_len = 0, rep_run_start = 0;
+    int32_t produced = 0;
+    while (produced < max_len) {
+        const int32_t n = std::min(chunk, max_len - produced);
+        int32_t got = 0, eos = 0;
+        if (!dev_ok(q3t_dev_frames_run(dev_, n, buf.data(), &got, &eos))) return false;
+        bool stop = false;
+        for (int32_t f = 0; f < got && !stop; ++f) {
+            const int32_t * codes = buf.data() + (size_t) f * ncb;
+            const int32_t frame = produced + f;
+            output.insert(output.end(), codes, codes + ncb);
+            if (on_frame && !on_frame(codes, ncb, frame)) { stop = true; break; }
+            if (rep_loop_detect) rep_frames.emplace_back(codes, codes + ncb);
+            const size_t nf = rep_frames.size();
+            bool is_rep = false;
+            for (int back = 1; back <= 6 && !is_rep && (size_t) back < nf; ++back) {
+                int matches = 0;
+                for (int cb = 0; cb < ncb; ++cb) matches += rep_frames[nf - 1][cb] == rep_frames[nf - 1 - back][cb];
+                if (matches >= 10) is_rep = true;
+            }
+            if (is_rep) { if (rep_run_len == 0) rep_run_start = (int32_t) (nf - 1); ++rep_run_len; }
+            else rep_run_len = 0;
+            if (rep_run_len >= 5) {
+                fprintf(stderr, "  Repetition loop detected at frame %d, truncating %d frames\n", (int) (nf - 1),
+                        (int) rep_run_len);
+                output.resize((size_t) rep_run_start * ncb);
+                stop = true;
+            }
+        }
+        produced += got;
+        if (stop || eos || got < n) break;
+    }
+    kv_n_used_ = plen + produced;
+    return true;
+}
+
+bool TTSTransformer::generate(const int32_t * text_tokens, int32_t n_tokens, const float * speaker_embd,
+                              int32_t max_len, std::vector<int32_t> & output, int32_t language_id,
+                              float repetition_penalty, float temperature, int32_t top_k,
+                              const int32_t * instruct_tokens, int32_t n_instruct, float eos_bias,
+                              int32_t target_frames, bool rep_loop_detect, const FrameCallback & on_frame) {
+    attn_rows_.clear();
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!text_tokens) { error_msg_ = "text_tokens is null"; return false; }
+    if (n_tokens < 4) { error_msg_ = "Need at least 4 text tokens for generation"; return false; }
+    if (max_len <= 0) { output.clear(); return true; }
+    std::vector<float> prefill, trailing, pad;
+    if (!build_prefill_graph(text_tokens, n_tokens, speaker_embd, language_id, prefill, trailing, pad,
+                             instruct_tokens, n_instruct))
+        return false;
+    if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
+                    rep_loop_detect, on_frame, output))
+        return false;
+    write_attn_dump();
+    return true;
+}
+
+bool TTSTransformer::generate_icl(const int32_t * text_tokens, int32_t n_tokens, const int32_t * ref_text_tokens,
+                                  int32_t n_ref_text, const int32_t * ref_codec_tokens, int32_t n_ref_frames,
+                                  const float * speaker_embd, int32_t max_len, std::vector<int32_t> & output,
+                                  int32_t /*language_id*/, float repetition_penalty, float temperature, int32_t top_k,
+                                  float eos_bias, int32_t target_frames, bool rep_loop_detect,
+                                  const FrameCallback & on_frame) {
+    attn_rows_.clear();
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!text_tokens || n_tokens < 4) { error_msg_ = "ICL: need at least 4 target text tokens"; return false; }
+    if (!ref_codec_tokens || n_ref_frames < 1) { error_msg_ = "ICL: need at least 1 reference codec frame"; return false; }
+    if (max_len <= 0) { output.clear(); return true; }
+    std::vector<float> prefill, trailing, pad;
+    if (!build_prefill_graph_icl(text_tokens, n_tokens, ref_text_tokens, n_ref_text, ref_codec_tokens, n_ref_frames,
+                                 speaker_embd, prefill, trailing, pad))
+        return false;
+    if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
+                    rep_loop_detect, on_frame, output))
+        return false;
+    write_attn_dump();
+    return true;
+}
+
+bool TTSTransformer::forward(const int32_t * tokens, int32_t n_tokens, int32_t n_past, std::vector<float> & output) {
+    return forward_text(tokens, n_tokens, nullptr, n_past, output);
+}
+
+bool TTSTransformer::forward_with_audio(const int32_t * tokens, int32_t n_tokens, const float *, int32_t, int32_t,
+                                        int32_t n_past, std::vector<float> & output) {
+    return forward_text(tokens, n_tokens, nullptr, n_past, output);
+}
+
+// Attention-row capture is not wired into the device frame loop; an
+// enabled dump writes no file and says so.
+bool TTSTransformer::write_attn_dump() {
+    if (!attn_dump_ || attn_dump_path_.empty()) return true;
+    fprintf(stderr, "attn-dump: not captured by the device frame loop; %s not written\n", attn_dump_path_.c_str());
+    return true;
+}
+
+}  // namespace qwen3_tts

@@ -1,0 +1,82 @@
+"""The drop-in C++ TTSTransformer (qwen3-tts.cpp_amd/csrc/tts_transformer.h)
+loads a GGUF and runs generate / generate_icl / predict_codes_autoregressive
+on the GPU; its codes must equal the CPU oracle's.  Mirrors the reference's
+tests/test_transformer.cpp (load, KV init, generate, frame comparison)."""
+import os
+import struct
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import q3t_oracle as orc
+from qwen3_tts_amd import config as qcfg
+from qwen3_tts_amd import gguf
+from qwen3_tts_amd.device import PKG_DIR
+from qwen3_tts_amd.synth import Weights
+
+pytestmark = pytest.mark.gpu
+BIN = os.path.join(PKG_DIR, "lib", "test_transformer_dev")
+
+
+def icl_rows(o, cfg, text, ref_text, ref_codes, spk):
+    """build_prefill_graph_icl (src/tts_transformer.cpp:1188-1472) from oracle primitives."""
+    d = cfg.hidden_size
+    bos, eos, pad = o.text_proj(np.array([cfg.tts_bos_id, cfg.tts_eos_id, cfg.tts_pad_id], np.int32))
+    role = o.text_proj(text[:3])
+    rows = [o.embed_row("codec", 0, t) for t in (cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id)]
+    rows += [spk] + [o.embed_row("codec", 0, cfg.codec_pad_id), o.embed_row("codec", 0, cfg.codec_bos_id)]
+    cin = np.stack(rows).astype(np.float32)
+    ov = len(rows) - 1
+    over = np.stack([bos if t == ov - 1 else pad for t in range(ov)]) + cin[:ov]
+    stream = list(ref_text[3:max(3, len(ref_text) - 5)]) + list(text[3:max(3, len(text) - 5)]) + [cfg.tts_eos_id]
+    tp = o.text_proj(np.array(stream, np.int32))
+    codec = [o.embed_row("codec", 0, cfg.codec_bos_id)]
+    for f in range(ref_codes.shape[0]):
+        r = o.embed_row("codec", 0, int(ref_codes[f, 0])).copy()
+        for cb in range(1, 16):
+            r = (r + o.embed_row("cp", cb - 1, int(ref_codes[f, cb]))).astype(np.float32)
+        codec.append(r)
+    n_codec = len(codec)
+    icl = []
+    for i in range(n_codec):
+        t = tp[i] if i < len(stream) else pad
+        icl.append(((np.zeros(d, np.float32) + t) + codec[i]).astype(np.float32))
+    prefill = np.concatenate([role, over.astype(np.float32), np.stack(icl)]).astype(np.float32)
+    trailing = tp[n_codec:] if len(stream) > n_codec else np.zeros((0, d), np.float32)
+    return prefill, trailing, pad
+
+
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_facade_matches_oracle(tmp_path, wtype):
+    assert os.path.exists(BIN), "build() first"
+    cfg = qcfg.tiny()
+    w = Weights(cfg, wtype, seed=31)
+    model = tmp_path / "tiny.gguf"
+    gguf.write(str(model), cfg, w)
+    rng = np.random.default_rng(32)
+    text = rng.integers(0, cfg.text_vocab - 8, 26).astype(np.int32)
+    spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+    ref_codes = np.concatenate([rng.integers(0, 2048, (6, 1)), rng.integers(0, 2048, (6, 15))], axis=1).astype(np.int32)
+    max_len = 20
+    with open(tmp_path / "in.bin", "wb") as f:
+        f.write(struct.pack("<i", len(text)) + text.tobytes() + spk.tobytes())
+        f.write(struct.pack("<ii", max_len, ref_codes.shape[0]) + ref_codes.tobytes())
+    print(f"[gpu] facade {wtype}", file=sys.stderr, flush=True)
+    r = subprocess.run([BIN, str(model), str(tmp_path / "in.bin"), str(tmp_path)], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout, r.stderr, file=sys.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    codes = np.fromfile(tmp_path / "codes.bin", np.int32).reshape(-1, 16)
+    o = orc.Oracle(cfg, w, threads=8)
+    co, _ = o.generate(text, spk, max_len=max_len, temperature=0.0)
+    assert np.array_equal(codes, co)
+    hid = np.fromfile(tmp_path / "hidden.bin", np.float32)
+    cp = np.fromfile(tmp_path / "cp.bin", np.int32)
+    cpo, _ = o.code_pred(hid, 5)
+    assert np.array_equal(cp, cpo)
+    icl = np.fromfile(tmp_path / "icl.bin", np.int32).reshape(-1, 16)
+    pre, trail, pad = icl_rows(o, cfg, text, text, ref_codes, spk)
+    io = o.generate_rows(pre, trail, pad, max_len=max_len, temperature=0.0)
+    assert np.array_equal(icl, io)
