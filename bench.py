@@ -79,7 +79,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
+                    help="persistent: one cooperative kernel per frame; graph: the captured multi-kernel frame")
     args = ap.parse_args()
+    os.environ["Q3T_FRAME_KERNEL"] = "1" if args.path == "persistent" else "0"
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode is a single "
               "dependent chain; see DESIGN.md for how independent streams would shard).", file=sys.stderr)
@@ -107,9 +110,12 @@ def main():
         _, eos = dev.frames_run(args.warmup)
         assert not eos
     dev.sync()
+    us0, n0, _ = dev.frames_stats()
     t0 = time.perf_counter()
     codes, eos = dev.frames_run(args.steps)
     elapsed = time.perf_counter() - t0
+    us1, n1, path = dev.frames_stats()
+    frame_kernel_us = (us1 - us0) / max(n1 - n0, 1)   # HIP events around the frame launches
     assert not eos and codes.shape[0] == args.steps, "EOS inside the timed region"
     ms_per_step = elapsed * 1000.0 / args.steps
     fps = args.steps / elapsed
@@ -123,8 +129,15 @@ def main():
     for k, nm in names.items():
         us, b = dev.time_kernel(k, args.kernel_iters)
         kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
-    dom = kernels["gemv_gate_up_swiglu"]
     dev.close()
+    if path == 1:
+        # the whole frame is one kernel: its roofline is the frame's algorithmic bytes over its duration
+        dom_name = "k_frame (persistent cooperative frame kernel, 256 workgroups x 256 threads)"
+        dom = {"avg_us": round(frame_kernel_us, 3), "bytes": fbytes, "gbs": round(fbytes / frame_kernel_us / 1e3, 1)}
+        kernels["k_frame"] = dom
+    else:
+        dom_name = "gemv_gate_up_swiglu (talker layer 0, Q8_0 1024->2x3072)"
+        dom = kernels["gemv_gate_up_swiglu"]
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -148,7 +161,8 @@ def main():
         "dtype": "int8" if args.weights == "q8_0" else "f16",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
         "config": {"workload": f"full frame loop, {args.weights.upper()} 0.6B shapes, {args.prompt}-token prompt, "
-                               f"greedy, hipGraph per frame", "global_batch": 1, "frames": args.steps,
+                               f"greedy, " + ("one persistent kernel per frame" if path == 1 else "hipGraph per frame"),
+                   "global_batch": 1, "frames": args.steps,
                    "weights": args.weights, "prompt_tokens": args.prompt, "prefill_rows": plen},
         "rtf_12hz": round(fps / 12.0, 2),
         "rtf_12_5hz": round(fps / 12.5, 2),
@@ -157,7 +171,7 @@ def main():
         "frame_roofline_frac": round(fbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4) if dom["gbs"] else None, "traffic": None,
-                     "kernel": "gemv_gate_up_swiglu (talker layer 0, Q8_0 1024->2x3072)"},
+                     "kernel": dom_name},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

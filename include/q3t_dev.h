@@ -160,6 +160,15 @@ int  q3t_dev_frames_begin(q3t_dev * dev, const q3t_frame_args * args);
 int  q3t_dev_frames_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
                         int32_t * n_emitted_out, int32_t * eos_out);
 
+/* Frame-loop statistics since the last q3t_dev_frames_begin: GPU time of
+ * the frame launches (HIP events around each frames_run's launches, in
+ * microseconds), the number of frames launched, and which implementation ran
+ * them (1 = one persistent cooperative kernel per frame, 0 = the captured
+ * multi-kernel graph).  Instrumentation with no counterpart in the
+ * reference; the benchmark and the tests use it. */
+int  q3t_dev_frames_stats(q3t_dev * dev, double * gpu_us_out, int64_t * frames_out,
+                          int32_t * path_out);
+
 /* Blocks until all work queued by this context has finished. */
 int  q3t_dev_sync(q3t_dev * dev);
 /* Times `iters` launches of one kernel class of the frame loop with HIP

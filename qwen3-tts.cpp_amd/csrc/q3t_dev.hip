@@ -6,6 +6,7 @@
 
 #include "../../include/q3t_dev.h"
 #include "q3t_kernels.h"
+#include "q3t_frame_kernel.h"
 
 #include <hip/hip_runtime.h>
 
@@ -78,6 +79,17 @@ struct q3t_dev {
 
     hipGraphExec_t frame_exec = nullptr;
     hipGraph_t frame_graph = nullptr;
+    // persistent frame kernel (q3t_frame_kernel.h)
+    bool fk_ok = false;            // model / context qualify this context for it
+    int fk_variant = 0;            // 1: slots (1,2,3), 2: slots (1,1,1)
+    int fk_grid = 0;
+    fk::LayerQ8 * fk_layers = nullptr;
+    uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
+    int32_t * fk_err = nullptr;
+    fk::Args * fk_args_dev = nullptr;
+    hipEvent_t run_ev[2] = {nullptr, nullptr};
+    double run_us = 0.0;
+    int64_t run_frames = 0;
     int32_t host_emitted = 0;
     int32_t frames_launched = 0;
     int32_t frames_max = 0;
@@ -471,6 +483,111 @@ int sync(q3t_dev * c) {
 
 }  // namespace
 
+// Decides whether the persistent frame kernel can run this context and
+// prepares its tables.  Falls back to the multi-kernel graph otherwise.
+int slots_for(int K) {
+    const int b = K / kQK;
+    if (b <= 32 && (b & (b - 1)) == 0) return 1;
+    if (b == 64) return 2;
+    if (b == 96) return 3;
+    return 0;
+}
+
+int fk_prepare(q3t_dev * c) {
+    c->fk_ok = false;
+    if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
+    const q3t_config & g = c->cfg;
+    const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int sq = slots_for(g.hidden_size), so = slots_for(qd), sd = slots_for(g.ffn_size);
+    int variant = 0;
+    if (sq == 1 && so == 2 && sd == 3) variant = 1;
+    if (sq == 1 && so == 1 && sd == 1) variant = 2;
+    if (!variant || g.ffn_size != g.cp_ffn || g.n_head != 2 * g.n_kv_head || g.head_dim != 128 ||
+        c->n_ctx > fk::kMaxCtx || g.cp_layers > fk::kCpLayers || g.hidden_size > 1024 || g.hidden_size % kQK ||
+        g.codec_vocab > 2 * 3072 || g.cp_vocab > 2 * 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 ||
+        qkvd > fk::kSlot / 2 || g.ffn_size > 3072 || qd > 3072)
+        return 0;
+    for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
+        const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
+        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
+            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
+            return 0;
+    }
+    // one workgroup per CU (the LDS footprint allows no more), all co-resident
+    const void * fn = variant == 1 ? (const void *) fk::k_frame<1, 2, 3> : (const void *) fk::k_frame<1, 1, 1>;
+    int per_cu = 0;
+    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, fk::kT, 0));
+    const int grid = std::min(256, per_cu * c->n_cu);
+    if (grid < 1) return 0;
+    const int nw = grid * fk::kW;
+    auto fits = [&](int rows, int K, int slots) {
+        const int rpw = 64 / ((K / kQK) / slots);
+        return rows % rpw == 0 && rows / rpw <= 2 * nw;
+    };
+    if (!fits(qkvd, g.hidden_size, sq) || !fits(g.ffn_size, g.hidden_size, sq) || !fits(g.hidden_size, qd, so) ||
+        !fits(g.hidden_size, g.ffn_size, sd) || !fits(g.codec_vocab, g.hidden_size, 1) ||
+        !fits(g.cp_vocab, g.hidden_size, 1) || g.n_kv_head > grid)
+        return 0;
+    const int phases = 15 * (2 + 5 * g.cp_layers) + 1 + 5 * g.n_layers;
+    if (phases >= 4096) return 0;
+    if (!c->fk_layers) {
+        std::vector<fk::LayerQ8> t(g.n_layers + g.cp_layers);
+        for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
+            const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
+            t[i] = fk::LayerQ8{(const int8_t *) L.qkv.data, L.qkv.scales, (const int8_t *) L.wo.data, L.wo.scales,
+                               (const int8_t *) L.wg.data, L.wg.scales, (const int8_t *) L.wu.data, L.wu.scales,
+                               (const int8_t *) L.wd.data, L.wd.scales, L.attn_norm, L.ffn_norm, L.q_norm, L.k_norm};
+        }
+        if (dev_alloc_t(c, &c->fk_layers, t.size())) return -1;
+        HIP_OK(hipMemcpy(c->fk_layers, t.data(), t.size() * sizeof(fk::LayerQ8), hipMemcpyHostToDevice));
+    }
+    const size_t bytes = (size_t) phases * fk::kSlot * sizeof(uint64_t);
+    if (bytes > c->fk_arena_bytes) {
+        dev_free(c, c->fk_arena);
+        c->fk_arena = nullptr;
+        if (dev_alloc(c, (void **) &c->fk_arena, bytes)) return -1;
+        c->fk_arena_bytes = bytes;
+    }
+    if (!c->fk_err && dev_alloc_t(c, &c->fk_err, 1)) return -1;
+    if (!c->fk_args_dev && dev_alloc_t(c, &c->fk_args_dev, 1)) return -1;
+    c->fk_grid = grid;
+    c->fk_variant = variant;
+    c->fk_ok = true;
+    return 0;
+}
+
+fk::Args fk_args(q3t_dev * c) {
+    const q3t_config & g = c->cfg;
+    fk::Args A{};
+    A.talker = c->fk_layers; A.cp = c->fk_layers + g.n_layers;
+    A.n_layers = g.n_layers; A.cp_layers = g.cp_layers; A.d = g.hidden_size; A.n_head = g.n_head;
+    A.n_kv_head = g.n_kv_head; A.ffn = g.ffn_size; A.cp_ffn = g.cp_ffn; A.codec_vocab = g.codec_vocab;
+    A.cp_vocab = g.cp_vocab; A.eos_id = g.codec_eos_id; A.n_ctx = c->n_ctx;
+    A.eps = g.rms_eps; A.attn_scale = 1.0f / std::sqrt((float) g.head_dim);
+    A.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; i < 15; ++i) {
+        A.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+        A.cp_head[i] = (const uint16_t *) c->cp_head[i].data;
+    }
+    A.codec_head = (const uint16_t *) c->codec_head.data;
+    A.out_norm = (const float *) c->out_norm.data; A.cp_out_norm = (const float *) c->cp_out_norm.data;
+    A.rope_cos = c->rope_cos; A.rope_sin = c->rope_sin; A.cp_rope_cos = c->cp_rope_cos; A.cp_rope_sin = c->cp_rope_sin;
+    A.kc = c->kc; A.vc = c->vc;
+    A.arena = c->fk_arena;
+    A.logits = c->logits; A.hidden = c->hidden;
+    A.st = c->st; A.params = c->params; A.seen = c->seen; A.codes_out = c->codes_out;
+    A.trailing = c->trailing; A.n_trailing = c->n_trailing; A.pad = c->pad;
+    A.err = c->fk_err;
+    return A;
+}
+
+int fk_launch(q3t_dev * c, int32_t frame) {
+    void * args[] = {&c->fk_args_dev, &frame};
+    const void * fn = c->fk_variant == 1 ? (const void *) fk::k_frame<1, 2, 3> : (const void *) fk::k_frame<1, 1, 1>;
+    HIP_OK(hipLaunchCooperativeKernel(fn, dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream));
+    return 0;
+}
+
 // =================================================================== C ABI
 extern "C" {
 
@@ -539,6 +656,7 @@ void q3t_dev_destroy(q3t_dev * c) {
     (void) hipSetDevice(c->device);
     if (c->stream) (void) hipStreamSynchronize(c->stream);
     drop_graph(c);
+    for (hipEvent_t e : c->run_ev) if (e) (void) hipEventDestroy(e);
     for (void * p : c->allocs) (void) hipFree(p);
     if (c->stream) (void) hipStreamDestroy(c->stream);
     delete c;
@@ -929,8 +1047,17 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     s.max_frames = a->max_len;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemsetAsync(c->seen, 0, (size_t) g.codec_vocab, c->stream));
+    if (a->max_len >= (1 << 19)) return fail(c, "max_len too large");
+    if (fk_prepare(c)) return -1;
+    if (c->fk_ok) {
+        HIP_OK(hipMemsetAsync(c->fk_arena, 0, c->fk_arena_bytes, c->stream));
+        HIP_OK(hipMemsetAsync(c->fk_err, 0, sizeof(int32_t), c->stream));
+        static thread_local fk::Args host_args;
+        host_args = fk_args(c);
+        HIP_OK(hipMemcpyAsync(c->fk_args_dev, &host_args, sizeof host_args, hipMemcpyHostToDevice, c->stream));
+    }
     if (sync(c)) return -1;
-    if (!c->frame_exec) {
+    if (!c->fk_ok && !c->frame_exec) {
         HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         frame_seq(c);
         hipGraph_t graph = nullptr;
@@ -940,6 +1067,8 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     }
     c->host_emitted = 0;
     c->frames_launched = 0;
+    c->run_us = 0.0;
+    c->run_frames = 0;
     c->frames_max = a->max_len;
     c->frames_ready = true;
     return 0;
@@ -953,14 +1082,30 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     // Q3T_NO_GRAPH=1 enqueues the frame's kernels directly (for tracers that
     // do not follow graph launches); the kernels and results are the same.
     static const bool no_graph = [] { const char * e = std::getenv("Q3T_NO_GRAPH"); return e && e[0] == '1'; }();
+    if (!c->run_ev[0]) {
+        HIP_OK(hipEventCreate(&c->run_ev[0]));
+        HIP_OK(hipEventCreate(&c->run_ev[1]));
+    }
+    if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[0], c->stream));
     for (int i = 0; i < n_frames; ++i) {
-        if (no_graph) frame_seq(c);
+        if (c->fk_ok) { if (fk_launch(c, c->frames_launched + i)) return -1; }
+        else if (no_graph) frame_seq(c);
         else HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
     }
+    if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[1], c->stream));
     c->frames_launched += n_frames;
     FrameState r{};
     HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
+    int32_t fk_err = 0;
+    if (c->fk_ok) HIP_OK(hipMemcpyAsync(&fk_err, c->fk_err, sizeof fk_err, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
+    if (fk_err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+    if (n_frames > 0) {
+        float ms = 0.0f;
+        HIP_OK(hipEventElapsedTime(&ms, c->run_ev[0], c->run_ev[1]));
+        c->run_us += 1e3 * ms;
+        c->run_frames += n_frames;
+    }
     const int ncb = c->cfg.n_codebooks;
     const int fresh = r.n_emitted - c->host_emitted;
     if (fresh > 0 && codes_out)
@@ -969,6 +1114,14 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     c->host_emitted = r.n_emitted;
     if (n_emitted_out) *n_emitted_out = fresh;
     if (eos_out) *eos_out = r.eos;
+    return 0;
+}
+
+int q3t_dev_frames_stats(q3t_dev * c, double * gpu_us_out, int64_t * frames_out, int32_t * path_out) {
+    if (!c) return -1;
+    if (gpu_us_out) *gpu_us_out = c->run_us;
+    if (frames_out) *frames_out = c->run_frames;
+    if (path_out) *path_out = c->fk_ok ? 1 : 0;
     return 0;
 }
 

@@ -441,6 +441,140 @@ __device__ __forceinline__ float key2f(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// LDS scratch of the sampling core for NTH threads.
+template <int NTH>
+struct SampleScratch {
+    uint32_t hist[256];
+    double dsc[NTH];
+    float fv[NTH / 64];
+    int32_t iv[NTH / 64];
+    uint32_t sel[2];
+    int32_t pick[2];
+};
+
+// Token from prepared logits l[0..V) in LDS (suppression / penalty already
+// applied; `eff` is the EOS bias for the talker, 0 otherwise), following
+// sample_or_argmax (src/tts_transformer.cpp:2750-2788) and the talker sampler
+// (:3146-3183): greedy first-index argmax, or temperature, EOS bias, top-k
+// threshold (ties kept), softmax with fp64 denominator, draw against the
+// Philox uniform of (seed, frame, group).  Every thread returns the token.
+// l is overwritten.
+template <int NTH>
+__device__ int32_t sample_core(float * l, int V, float temperature, int top_k, int eos_id, float eff,
+                               uint64_t seed, uint32_t frame, uint32_t group, SampleScratch<NTH> & S) {
+    const int t = threadIdx.x;
+    if (temperature <= 0.0f) {
+        if (eff != 0.0f && t == 0) l[eos_id] += eff;
+        __syncthreads();
+        // empty = (-inf, INT_MAX); ascending scan with strict '>' keeps the first maximum
+        float bv = -INFINITY; int32_t bi = 0x7fffffff;
+        for (int i = t; i < V; i += NTH)
+            if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int32_t oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((t & 63) == 0) { S.fv[t >> 6] = bv; S.iv[t >> 6] = bi; }
+        __syncthreads();
+        float b = S.fv[0]; int32_t i0 = S.iv[0];
+        for (int w = 1; w < NTH / 64; ++w)
+            if (S.fv[w] > b || (S.fv[w] == b && S.iv[w] < i0)) { b = S.fv[w]; i0 = S.iv[w]; }
+        __syncthreads();
+        return i0;
+    }
+    for (int i = t; i < V; i += NTH) l[i] = l[i] / temperature;
+    __syncthreads();
+    if (eff != 0.0f && t == 0) l[eos_id] += eff;
+    __syncthreads();
+    if (top_k > 0 && top_k < V) {
+        // radix select of the top_k-th largest key, 8 bits per pass from the top
+        uint32_t prefix = 0, mask = 0;
+        int remaining = top_k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int i = t; i < 256; i += NTH) S.hist[i] = 0;
+            __syncthreads();
+            for (int i = t; i < V; i += NTH) {
+                const uint32_t k = f2key(l[i]);
+                if ((k & mask) == prefix) atomicAdd(&S.hist[(k >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (t == 0) {
+                int cum = 0, b = 255;
+                for (; b > 0; --b) {
+                    if (cum + (int) S.hist[b] >= remaining) break;
+                    cum += (int) S.hist[b];
+                }
+                S.sel[0] = (uint32_t) b;
+                S.sel[1] = (uint32_t) (remaining - cum);
+            }
+            __syncthreads();
+            prefix |= S.sel[0] << shift;
+            mask |= 255u << shift;
+            remaining = (int) S.sel[1];
+            __syncthreads();
+        }
+        const float thr = key2f(prefix);
+        for (int i = t; i < V; i += NTH)
+            if (l[i] < thr) l[i] = -INFINITY;
+        __syncthreads();
+    }
+    float lm = -INFINITY;
+    for (int i = t; i < V; i += NTH) lm = fmaxf(lm, l[i]);
+    lm = wave_max_f(lm);
+    if ((t & 63) == 0) S.fv[t >> 6] = lm;
+    __syncthreads();
+    float mx = S.fv[0];
+    for (int w = 1; w < NTH / 64; ++w) mx = fmaxf(mx, S.fv[w]);
+    __syncthreads();
+    const int C = (V + NTH - 1) / NTH;          // contiguous chunk per thread
+    double ls = 0.0;
+    for (int c = 0; c < C; ++c) {
+        const int i = t * C + c;
+        if (i < V) { const float e = expf_q3t(l[i] - mx); l[i] = e; ls += (double) e; }
+    }
+    S.dsc[t] = ls;
+    __syncthreads();
+    for (int off = NTH / 2; off > 0; off >>= 1) {
+        if (t < off) S.dsc[t] += S.dsc[t + off];
+        __syncthreads();
+    }
+    const double sum = S.dsc[0];
+    __syncthreads();
+    double lp = 0.0;
+    for (int c = 0; c < C; ++c) {
+        const int i = t * C + c;
+        if (i < V) { const float p = (float) ((double) l[i] / sum); l[i] = p; lp += (double) p; }
+    }
+    // inclusive scan of per-thread sums (Hillis-Steele) for the CDF
+    S.dsc[t] = lp;
+    __syncthreads();
+    for (int off = 1; off < NTH; off <<= 1) {
+        const double v = t >= off ? S.dsc[t - off] : 0.0;
+        __syncthreads();
+        S.dsc[t] += v;
+        __syncthreads();
+    }
+    const double total = S.dsc[NTH - 1];
+    const double u = philox_uniform(seed, frame, group);
+    const double target = u * total;
+    if (t == 0) { S.pick[0] = 0x7fffffff; S.pick[1] = -1; }
+    __syncthreads();
+    double cum = t > 0 ? S.dsc[t - 1] : 0.0;
+    for (int c = 0; c < C; ++c) {
+        const int i = t * C + c;
+        if (i < V && l[i] > 0.0f) {
+            cum += (double) l[i];
+            atomicMax(&S.pick[1], i);
+            if (cum > target) { atomicMin(&S.pick[0], i); break; }
+        }
+    }
+    __syncthreads();
+    const int32_t tok = S.pick[0] != 0x7fffffff ? S.pick[0] : (S.pick[1] >= 0 ? S.pick[1] : 0);
+    __syncthreads();
+    return tok;
+}
+
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     FrameState * st = a.st;
     __shared__ int32_t s_frame;
@@ -456,16 +590,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     __syncthreads();
     if (s_frame < 0) return;
     __shared__ float l[kMaxVocab];
-    __shared__ uint32_t hist[256];
-    __shared__ double dsc[kSampleThreads];
-    __shared__ float fv[kSampleThreads / 64];
-    __shared__ int32_t iv[kSampleThreads / 64];
-    __shared__ uint32_t sel[2];
-    __shared__ int32_t pick[2];
+    __shared__ SampleScratch<kSampleThreads> S;
     const int t = threadIdx.x, V = a.vocab;
     const SampleParams & P = *a.params;
     const int frame = s_frame;
-
     for (int i = t; i < V; i += kSampleThreads) {
         float v = a.logits[i];
         if (a.mode == 0) {
@@ -483,122 +611,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         }
     }
     __syncthreads();
-    int32_t tok;
-    if (P.temperature <= 0.0f) {
-        if (a.mode == 0 && eff != 0.0f && t == 0) l[a.eos_id] += eff;
-        __syncthreads();
-        // empty = (-inf, INT_MAX); ascending scan with strict '>' keeps the first maximum
-        float bv = -INFINITY; int32_t bi = 0x7fffffff;
-        for (int i = t; i < V; i += kSampleThreads)
-            if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
-        // first maximum: larger value wins, equal values keep the smaller index
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int32_t oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((t & 63) == 0) { fv[t >> 6] = bv; iv[t >> 6] = bi; }
-        __syncthreads();
-        if (t == 0) {
-            float b = fv[0]; int32_t i0 = iv[0];
-            for (int w = 1; w < kSampleThreads / 64; ++w)
-                if (fv[w] > b || (fv[w] == b && iv[w] < i0)) { b = fv[w]; i0 = iv[w]; }
-            pick[0] = i0;
-        }
-        __syncthreads();
-        tok = pick[0];
-    } else {
-        for (int i = t; i < V; i += kSampleThreads) l[i] = l[i] / P.temperature;
-        __syncthreads();
-        if (a.mode == 0 && eff != 0.0f && t == 0) l[a.eos_id] += eff;
-        __syncthreads();
-        const int K = P.top_k;
-        if (K > 0 && K < V) {
-            // radix select of the K-th largest key, 8 bits per pass from the top
-            uint32_t prefix = 0, mask = 0;
-            int remaining = K;
-            for (int shift = 24; shift >= 0; shift -= 8) {
-                for (int i = t; i < 256; i += kSampleThreads) hist[i] = 0;
-                __syncthreads();
-                for (int i = t; i < V; i += kSampleThreads) {
-                    const uint32_t k = f2key(l[i]);
-                    if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-                }
-                __syncthreads();
-                if (t == 0) {
-                    int cum = 0, b = 255;
-                    for (; b > 0; --b) {
-                        if (cum + (int) hist[b] >= remaining) break;
-                        cum += (int) hist[b];
-                    }
-                    sel[0] = (uint32_t) b;
-                    sel[1] = (uint32_t) (remaining - cum);
-                }
-                __syncthreads();
-                prefix |= sel[0] << shift;
-                mask |= 255u << shift;
-                remaining = (int) sel[1];
-                __syncthreads();
-            }
-            const float thr = key2f(prefix);
-            for (int i = t; i < V; i += kSampleThreads)
-                if (l[i] < thr) l[i] = -INFINITY;
-            __syncthreads();
-        }
-        float lm = -INFINITY;
-        for (int i = t; i < V; i += kSampleThreads) lm = fmaxf(lm, l[i]);
-        lm = wave_max_f(lm);
-        if ((t & 63) == 0) fv[t >> 6] = lm;
-        __syncthreads();
-        float mx = fv[0];
-        for (int w = 1; w < kSampleThreads / 64; ++w) mx = fmaxf(mx, fv[w]);
-        __syncthreads();
-        // e = exp(l - max); denominator in fp64
-        const int C = (V + kSampleThreads - 1) / kSampleThreads;   // contiguous chunk per thread
-        double ls = 0.0;
-        for (int c = 0; c < C; ++c) {
-            const int i = t * C + c;
-            if (i < V) { const float e = expf_q3t(l[i] - mx); l[i] = e; ls += (double) e; }
-        }
-        dsc[t] = ls;
-        __syncthreads();
-        for (int off = kSampleThreads / 2; off > 0; off >>= 1) {
-            if (t < off) dsc[t] += dsc[t + off];
-            __syncthreads();
-        }
-        const double sum = dsc[0];
-        __syncthreads();
-        double lp = 0.0;
-        for (int c = 0; c < C; ++c) {
-            const int i = t * C + c;
-            if (i < V) { const float p = (float) ((double) l[i] / sum); l[i] = p; lp += (double) p; }
-        }
-        // inclusive scan of per-thread sums (Hillis-Steele) for the CDF
-        dsc[t] = lp;
-        __syncthreads();
-        for (int off = 1; off < kSampleThreads; off <<= 1) {
-            const double v = t >= off ? dsc[t - off] : 0.0;
-            __syncthreads();
-            dsc[t] += v;
-            __syncthreads();
-        }
-        const double total = dsc[kSampleThreads - 1];
-        const double u = philox_uniform(P.seed, (uint32_t) frame, a.mode == 0 ? 0u : (uint32_t) a.group);
-        const double target = u * total;
-        if (t == 0) { pick[0] = 0x7fffffff; pick[1] = -1; }
-        __syncthreads();
-        double cum = t > 0 ? dsc[t - 1] : 0.0;
-        for (int c = 0; c < C; ++c) {
-            const int i = t * C + c;
-            if (i < V && l[i] > 0.0f) {
-                cum += (double) l[i];
-                atomicMax(&pick[1], i);
-                if (cum > target) { atomicMin(&pick[0], i); break; }
-            }
-        }
-        __syncthreads();
-        tok = pick[0] != 0x7fffffff ? pick[0] : (pick[1] >= 0 ? pick[1] : 0);
-    }
+    const int32_t tok = sample_core<kSampleThreads>(l, V, P.temperature, P.top_k, a.eos_id, eff, P.seed,
+                                                    (uint32_t) frame, a.mode == 0 ? 0u : (uint32_t) a.group, S);
     if (t == 0) {
         if (a.mode == 0) {
             st->codes[0] = tok;

@@ -15,7 +15,14 @@ constexpr int kBlock = 256;   // threads per workgroup for GEMV / attention
 constexpr int kQK = 32;       // Q8_0 block length
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+// The empty asm makes the fp32 value opaque: without it the compiler folds
+// f2h(a * b) into v_fma_mixlo_f16 (one rounding of the exact product to
+// fp16), which differs from rounding to fp32 and then to fp16 whenever the
+// fp32 product lands exactly on an fp16 tie.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    __asm__("" : "+v"(f));
+    return __half_as_ushort(__float2half_rn(f));
+}
 __device__ __forceinline__ float round_f16(float f) { return h2f(f2h(f)); }
 
 // exp(x): Cody-Waite reduction x = k*ln2 + r (ln2 split hi/lo, fused

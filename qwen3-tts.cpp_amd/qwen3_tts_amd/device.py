@@ -20,7 +20,7 @@ EXPORTS = [
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
     "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_frames_begin",
-    "q3t_dev_frames_run", "q3t_dev_sync", "q3t_dev_time_kernel",
+    "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_sync", "q3t_dev_time_kernel",
 ]
 
 
@@ -66,6 +66,8 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_frames_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
         lib.q3t_dev_frames_run.argtypes = [vp, i32, vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
         lib.q3t_dev_sync.argtypes = [vp]
+        lib.q3t_dev_frames_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
+                                             ctypes.POINTER(i32)]
         lib.q3t_dev_time_kernel.argtypes = [vp, i32, i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         _lib = lib
     return _lib
@@ -194,6 +196,16 @@ class Device:
         self._check(self.lib.q3t_dev_frames_run(self.h, n_frames, _p(out), ctypes.byref(n), ctypes.byref(eos)),
                     "frames_run")
         return out[: n.value].copy(), bool(eos.value)
+
+    def frames_stats(self):
+        """(GPU microseconds of frame launches, frames launched, path) since
+        frames_begin; path 1 = persistent frame kernel, 0 = kernel graph."""
+        us = ctypes.c_double()
+        n = ctypes.c_int64()
+        path = ctypes.c_int32()
+        self._check(self.lib.q3t_dev_frames_stats(self.h, ctypes.byref(us), ctypes.byref(n), ctypes.byref(path)),
+                    "frames_stats")
+        return us.value, n.value, path.value
 
     def sync(self):
         self._check(self.lib.q3t_dev_sync(self.h), "sync")

@@ -35,6 +35,21 @@ def make(cfg, wtype, seed=7, n_ctx=256, norm_mode="one"):
     return w, dev, o
 
 
+@pytest.fixture(params=["persistent", "graph"])
+def frame_path(request, monkeypatch):
+    """Runs a frame-loop test on both implementations: the persistent
+    cooperative frame kernel (chosen for Q8_0 models) and the captured
+    multi-kernel graph (Q3T_FRAME_KERNEL=0, and every F16 model)."""
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
+    return request.param
+
+
+def check_path(dev, wtype, frame_path):
+    us, n, path = dev.frames_stats()
+    want = 1 if (frame_path == "persistent" and wtype == "q8_0") else 0
+    assert path == want, (frame_path, wtype, path)
+
+
 @pytest.fixture(scope="module", params=["q8_0", "f16"])
 def tiny_model(request):
     cfg = qcfg.tiny()
@@ -109,27 +124,29 @@ def test_text_proj_and_embeddings(tiny_model):
     assert np.array_equal(rows[0], o.embed_row("cp", 14, 2047))
 
 
-def test_generate_greedy_64_frames(tiny_model):
+def test_generate_greedy_64_frames(tiny_model, frame_path):
     cfg, w, dev, o = tiny_model
     text = np.random.default_rng(4).integers(0, cfg.text_vocab - 8, 32).astype(np.int32)
     spk = np.random.default_rng(5).standard_normal(cfg.hidden_size).astype(np.float32)
     say("[gpu] generate greedy 64")
     co, _ = o.generate(text, spk, max_len=64, temperature=0.0, top_k=0)
     cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, chunk=16)
+    check_path(dev, w.wtype, frame_path)
     assert co.shape == cg.shape, (co.shape, cg.shape)
     assert np.array_equal(cg, co)
 
 
-def test_generate_sampled_matches_oracle(tiny_model):
+def test_generate_sampled_matches_oracle(tiny_model, frame_path):
     cfg, w, dev, o = tiny_model
     text = np.random.default_rng(6).integers(0, cfg.text_vocab - 8, 20).astype(np.int32)
     say("[gpu] generate sampled 24")
     co, _ = o.generate(text, None, max_len=24, temperature=0.9, top_k=50, seed=11)
     cg = driver.generate(dev, cfg, text, None, max_len=24, temperature=0.9, top_k=50, seed=11, chunk=5)
+    check_path(dev, w.wtype, frame_path)
     assert np.array_equal(cg, co)
 
 
-def test_generate_eos_bias_stops(tiny_model):
+def test_generate_eos_bias_stops(tiny_model, frame_path):
     cfg, w, dev, o = tiny_model
     text = np.arange(12, dtype=np.int32)
     cg = driver.generate(dev, cfg, text, None, max_len=8, temperature=0.0, eos_bias=1e4)
@@ -137,15 +154,16 @@ def test_generate_eos_bias_stops(tiny_model):
     assert cg.shape[0] == 0 and co.shape[0] == 0
 
 
-def test_generate_target_frames_ramp(tiny_model):
+def test_generate_target_frames_ramp(tiny_model, frame_path):
     cfg, w, dev, o = tiny_model
     text = np.arange(3, 20, dtype=np.int32)
     co, _ = o.generate(text, None, max_len=40, temperature=0.0, eos_bias=0.0, target_frames=2)
     cg = driver.generate(dev, cfg, text, None, max_len=40, temperature=0.0, eos_bias=0.0, target_frames=2, chunk=7)
+    check_path(dev, w.wtype, frame_path)
     assert np.array_equal(cg, co)
 
 
-def test_callback_abort(tiny_model):
+def test_callback_abort(tiny_model, frame_path):
     cfg, w, dev, o = tiny_model
     text = np.arange(10, 30, dtype=np.int32)
     seen = []
@@ -160,7 +178,7 @@ def test_callback_abort(tiny_model):
 
 
 @pytest.mark.slow
-def test_full_q8_frame_loop_64_greedy():
+def test_full_q8_frame_loop_64_greedy(frame_path):
     cfg = qcfg.full_06b()
     say("[gpu] full 0.6B Q8_0: synth + upload")
     w, dev, o = make(cfg, "q8_0", seed=3, n_ctx=256)
@@ -174,7 +192,26 @@ def test_full_q8_frame_loop_64_greedy():
     assert np.array_equal(pre[0], opre) and np.array_equal(pre[1], otr) and np.array_equal(pre[2], opad)
     _, first_g = dev.prefill(pre[0], 0, want_hidden=False)
     assert np.abs(first_g - first_o).max() <= LOGIT_TOL
+    say(f"[gpu] full: device generate 64 ({frame_path})")
     cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, prefill_rows=pre)
+    check_path(dev, "q8_0", frame_path)
     say(f"[gpu] full: frames oracle={co.shape[0]} device={cg.shape[0]}")
     assert np.array_equal(cg, co)
     dev.close()
+
+
+def test_fp16_tie_rounding_regression(frame_path):
+    """Weights and prompt on which one attention probability of the talker
+    (frame 13, layer 1) lands exactly on an fp16 tie after fp32 rounding; a
+    fused multiply-and-convert (one rounding) picks the other neighbour and
+    codebook 3 of frame 14 flips."""
+    cfg = qcfg.tiny()
+    w, dev, o = make(cfg, "q8_0", seed=31)
+    rng = np.random.default_rng(32)
+    text = rng.integers(0, cfg.text_vocab - 8, 26).astype(np.int32)
+    spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+    co, _ = o.generate(text, spk, max_len=20, temperature=0.0)
+    cg = driver.generate(dev, cfg, text, spk, max_len=20, temperature=0.0, top_k=0, chunk=8)
+    check_path(dev, "q8_0", frame_path)
+    dev.close()
+    assert np.array_equal(cg, co)
