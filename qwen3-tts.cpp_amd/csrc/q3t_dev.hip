@@ -81,7 +81,7 @@ struct q3t_dev {
     hipGraph_t frame_graph = nullptr;
     // persistent frame kernel (q3t_frame_kernel.h)
     bool fk_ok = false;            // model / context qualify this context for it
-    int fk_variant = 0;            // 1: slots (1,2,3), 2: slots (1,1,1)
+    int fk_variant = 0;            // see fk_kernel()
     int fk_grid = 0;
     fk::LayerQ8 * fk_layers = nullptr;
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
@@ -485,6 +485,13 @@ int sync(q3t_dev * c) {
 
 // Decides whether the persistent frame kernel can run this context and
 // prepares its tables.  Falls back to the multi-kernel graph otherwise.
+// The kernel is instantiated for fixed (hidden, query width, FFN width):
+// variant 1 = (1024, 2048, 3072), the 0.6B talker and code predictor;
+// variant 2 = (256, 512, 512), the small test shapes.
+const void * fk_kernel(int variant) {
+    return variant == 1 ? (const void *) fk::k_frame<1024, 2048, 3072> : (const void *) fk::k_frame<256, 512, 512>;
+}
+
 int slots_for(int K) {
     const int b = K / kQK;
     if (b <= 32 && (b & (b - 1)) == 0) return 1;
@@ -500,12 +507,11 @@ int fk_prepare(q3t_dev * c) {
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int sq = slots_for(g.hidden_size), so = slots_for(qd), sd = slots_for(g.ffn_size);
     int variant = 0;
-    if (sq == 1 && so == 2 && sd == 3) variant = 1;
-    if (sq == 1 && so == 1 && sd == 1) variant = 2;
-    if (!variant || g.ffn_size != g.cp_ffn || g.n_head != 2 * g.n_kv_head || g.head_dim != 128 ||
-        c->n_ctx > fk::kMaxCtx || g.cp_layers > fk::kCpLayers || g.hidden_size > 1024 || g.hidden_size % kQK ||
-        g.codec_vocab > 2 * 3072 || g.cp_vocab > 2 * 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 ||
-        qkvd > fk::kSlot / 2 || g.ffn_size > 3072 || qd > 3072)
+    if (g.hidden_size == 1024 && qd == 2048 && g.ffn_size == 3072) variant = 1;
+    if (g.hidden_size == 256 && qd == 512 && g.ffn_size == 512) variant = 2;
+    if (!variant || g.ffn_size != g.cp_ffn || g.cp_hidden != g.hidden_size || g.n_head != 2 * g.n_kv_head ||
+        g.head_dim != 128 || c->n_ctx > fk::kMaxCtx || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
+        g.cp_vocab > 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 || qkvd > fk::kHS)
         return 0;
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
@@ -514,9 +520,8 @@ int fk_prepare(q3t_dev * c) {
             return 0;
     }
     // one workgroup per CU (the LDS footprint allows no more), all co-resident
-    const void * fn = variant == 1 ? (const void *) fk::k_frame<1, 2, 3> : (const void *) fk::k_frame<1, 1, 1>;
     int per_cu = 0;
-    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, fk::kT, 0));
+    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fk_kernel(variant), fk::kT, 0));
     const int grid = std::min(256, per_cu * c->n_cu);
     if (grid < 1) return 0;
     const int nw = grid * fk::kW;
@@ -583,8 +588,7 @@ fk::Args fk_args(q3t_dev * c) {
 
 int fk_launch(q3t_dev * c, int32_t frame) {
     void * args[] = {&c->fk_args_dev, &frame};
-    const void * fn = c->fk_variant == 1 ? (const void *) fk::k_frame<1, 2, 3> : (const void *) fk::k_frame<1, 1, 1>;
-    HIP_OK(hipLaunchCooperativeKernel(fn, dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream));
+    HIP_OK(hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream));
     return 0;
 }
 

@@ -13,6 +13,9 @@
 //     p of frame f carries tag ((f + 1) << 12) | p and owns arena slot p;
 //   - a workgroup prefetches its phase weights into registers before it
 //     polls the phase input, so weight latency hides behind the wait;
+//   - the phase input is prepared once per workgroup: all 256 threads load
+//     it, apply the RMSNorm and quantise it to Q8_0 (or round it to fp16 for
+//     the F16 heads) into LDS; the GEMV lanes then only run dot products;
 //   - workgroup g (< n_kv_head) owns KV head g for attention; the code
 //     predictor's 16-position KV cache lives in that workgroup's LDS for the
 //     whole frame;
@@ -22,8 +25,11 @@
 //   - every wait is bounded: a timeout marks the thread dead (it never waits
 //     again), sets an error flag the host reads after the frame, so a bug
 //     cannot hang the GPU.
-// Numerics are those of the multi-kernel path (q3t_gemv_reg.h, k_attention,
-// sample_core): fp64 accumulation of exact terms, identical rounding points.
+// The model dimensions are template parameters (hidden D, query width QD =
+// 2 x KV width, FFN width FF), so every loop over an activation is unrolled
+// into registers.  Numerics are those of the multi-kernel path
+// (q3t_gemv_reg.h, k_attention, sample_core): fp64 accumulation of exact
+// terms, identical rounding points.
 #pragma once
 
 #include "q3t_kernels.h"
@@ -34,9 +40,11 @@ namespace fk {
 constexpr int kT = 256;                 // threads per workgroup
 constexpr int kW = kT / 64;             // waves per workgroup
 constexpr int kSlot = 8192;             // tagged elements per phase slot
+constexpr int kHS = kSlot / 2;          // per-token stride inside a slot
 constexpr int kMaxCtx = 4096;           // talker positions the attention phase can hold in LDS
 constexpr unsigned kSpin = 1u << 20;    // polls before a wait gives up
 constexpr int kCpLayers = 5;            // code-predictor layers whose KV fits in LDS
+constexpr int kMaxBlk = 96;             // Q8_0 blocks of the widest GEMV input (3072)
 
 struct LayerQ8 {
     const int8_t * qkv; const uint16_t * qkv_d;
@@ -65,15 +73,32 @@ struct Args {
     int32_t * err;
 };
 
+// Geometry of a Q8_0 GEMV with input width K: each row is split over LPR
+// lanes holding SLOTS blocks each; a wave covers RPW rows ("row group").
+template <int K>
+struct Geo {
+    static constexpr int BPR = K / kQK;
+    static constexpr int SLOTS = BPR > 32 ? BPR / 32 : 1;
+    static constexpr int LPR = BPR / SLOTS;
+    static constexpr int RPW = 64 / LPR;
+    static constexpr int CH = K / kT;          // input elements per thread per token
+    static_assert(K % kT == 0 && BPR % SLOTS == 0 && (LPR & (LPR - 1)) == 0 && LPR >= 4 && LPR <= 32,
+                  "unsupported GEMV width");
+};
+
 struct Lds {
-    float x[2 * 3072];                      // phase input rows / logits
-    float a[2 * 4 * 128];                   // attention: q (2 heads x 2 tok), new k, new v rows
-    float sc[2 * kMaxCtx];                  // attention scores / probabilities, 2 heads
-    double pv[kW * 128];
-    uint16_t cpk[kCpLayers][16 * 128];      // code-predictor KV of this workgroup's KV head, per layer
-    uint16_t cpv[kCpLayers][16 * 128];
-    double red[kW];
-    float fred[kW];
+    alignas(16) float x[3072];                  // gathered layer-0 rows [nt][D] / sampler logits
+    alignas(16) int8_t qlo[2 * kMaxBlk * 16];   // Q8 input: bytes 0..15 of block b of token t at (t*BPR+b)*16
+    alignas(16) int8_t qhi[2 * kMaxBlk * 16];   // bytes 16..31
+    float qdx[2 * kMaxBlk];                     // fp16-rounded block scales
+    alignas(16) uint16_t hq[4][32 * 8];         // F16 head input: halves 8c..8c+7 of block b at hq[c][b*8]
+    float a[2 * 4 * 128];                       // attention: q (2 tok x 2 heads), new k, new v rows
+    float sc[2 * kMaxCtx];                      // attention scores / probabilities, 2 heads
+    double pv[kW * 2 * 128];                    // attention P.V partials [wave][head][dim]
+    alignas(16) uint16_t cpk[kCpLayers][16 * 128];   // code-predictor KV of this workgroup's KV head
+    alignas(16) uint16_t cpv[kCpLayers][16 * 128];
+    double red[2 * kW];
+    float fred[2 * kW];
     int32_t codes[16];
     SampleScratch<kT> S;
 };
@@ -95,6 +120,7 @@ __device__ __forceinline__ float twait(const uint64_t * p, uint32_t tag, bool & 
     }
     return __uint_as_float((uint32_t) v);
 }
+
 // Waits for up to kB tagged elements at once: all loads are issued before
 // any tag is checked, and a re-poll reloads only the elements still missing,
 // so a thread pays about one round trip per batch instead of one per element.
@@ -102,9 +128,9 @@ constexpr int kB = 8;
 __device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[kB], int cnt, uint32_t tag, float (&out)[kB],
                                             bool & dead, int32_t * err) {
     uint64_t v[kB];
+    unsigned n = 0;
 #pragma unroll
     for (int k = 0; k < kB; ++k) v[k] = k < cnt ? tload(ptr[k]) : ((uint64_t) tag << 32);
-    unsigned n = 0;
     while (!dead) {
         bool all = true;
 #pragma unroll
@@ -120,69 +146,145 @@ __device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[kB], i
     for (int k = 0; k < kB; ++k) out[k] = __uint_as_float((uint32_t) v[k]);
 }
 
-// all threads: rows [nt][n] of a tagged slot (row stride `stride`) into LDS dst [nt][n]
-__device__ __forceinline__ void stage(const uint64_t * slot, int nt, int n, int stride, uint32_t tag, float * dst,
-                                      bool & dead, int32_t * err) {
-    const int total = nt * n;
-    for (int e0 = 0; e0 < total; e0 += kB * kT) {
+// Thread t's elements of rows [NT][K] of a tagged slot: v[tok][c] = row
+// element c * kT + t.
+template <int NT, int K>
+__device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag, float (&v)[NT][K / kT], bool & dead,
+                                            int32_t * err) {
+    constexpr int CH = K / kT, F = NT * CH;
+#pragma unroll
+    for (int f0 = 0; f0 < F; f0 += kB) {
+        const uint64_t * ptr[kB];
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+            const int f = f0 + k < F ? f0 + k : 0;
+            ptr[k] = slot + (size_t) (f / CH) * kHS + (f % CH) * kT + threadIdx.x;
+        }
+        float val[kB];
+        twait_batch(ptr, F - f0 < kB ? F - f0 : kB, tag, val, dead, err);
+#pragma unroll
+        for (int k = 0; k < kB; ++k)
+            if (f0 + k < F) v[(f0 + k) / CH][(f0 + k) % CH] = val[k];
+    }
+}
+
+// Plain row [n] of a tagged slot into LDS dst[i] (sampler logits).
+__device__ __forceinline__ void stage_plain(const uint64_t * slot, int n, uint32_t tag, float * dst, bool & dead,
+                                            int32_t * err) {
+    for (int i0 = 0; i0 < n; i0 += kB * kT) {
         const uint64_t * ptr[kB];
         int cnt = 0;
 #pragma unroll
         for (int k = 0; k < kB; ++k) {
-            const int e = e0 + k * kT + (int) threadIdx.x;
-            const int tt = e < total ? e / n : 0, i = e < total ? e - tt * n : 0;
-            ptr[k] = slot + (size_t) tt * stride + i;
-            if (e < total) cnt = k + 1;
+            const int i = i0 + k * kT + (int) threadIdx.x;
+            ptr[k] = slot + (i < n ? i : 0);
+            if (i < n) cnt = k + 1;
         }
         float val[kB];
         twait_batch(ptr, cnt, tag, val, dead, err);
 #pragma unroll
         for (int k = 0; k < kB; ++k) {
-            const int e = e0 + k * kT + (int) threadIdx.x;
-            if (e < total) dst[e] = val[k];
+            const int i = i0 + k * kT + (int) threadIdx.x;
+            if (i < n) dst[i] = val[k];
         }
     }
     __syncthreads();
 }
 
-__device__ __forceinline__ double wg_sum(double v, double * red) {
-    v = wave_sum_d(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double s = red[0];
-    for (int w = 1; w < kW; ++w) s += red[w];
-    __syncthreads();
-    return s;
+// ------------------------------------------------------ cross-lane helpers
+// max over each aligned 32-lane half of the wave (same DPP pattern as group_sum_d)
+__device__ __forceinline__ float max32_f(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+    return v;
 }
-__device__ __forceinline__ float wg_max(float v, float * red) {
-    v = wave_max_f(v);
+
+// ------------------------------------------------------- input preparation
+// RMSNorm of thread-distributed rows v[NT][K/kT]: y = (x * scale) * w with
+// scale = 1/sqrt(mean(fl(x*x)) + eps), the sum of squares accumulated in
+// fp64.  Every thread ends with its normed elements.
+// The norm weights this thread needs (w[c * kT + t]), loaded before the
+// phase input is awaited.
+template <int K>
+__device__ __forceinline__ void norm_prefetch(const float * w, float (&nw)[K / kT]) {
+#pragma unroll
+    for (int c = 0; c < K / kT; ++c) nw[c] = w[c * kT + threadIdx.x];
+}
+
+template <int NT, int K>
+__device__ __forceinline__ void rms_rows(float (&v)[NT][K / kT], const float (&nw)[K / kT], float eps, Lds & L) {
+    constexpr int CH = K / kT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) ss += (double) (v[t][c] * v[t][c]);
+        ss = wave_sum_d(ss);
+        if (lane == 0) L.red[t * kW + wave] = ss;
+    }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        double tot = L.red[t * kW];
+#pragma unroll
+        for (int w2 = 1; w2 < kW; ++w2) tot += L.red[t * kW + w2];
+        const float mean = (float) (tot / (double) K);
+        const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float y = v[t][c] * scale;
+            v[t][c] = y * nw[c];
+        }
+    }
+}
+
+// Q8_0 activation quantisation (ggml-cpu x86 quantize_row_q8_0: d =
+// amax/127 stored as fp16, q = round-to-nearest-even(x * 127/amax)) of
+// thread-distributed rows into LDS.  A 32-element block is 32 consecutive
+// threads, so its amax is a 32-lane reduction.
+template <int NT, int K>
+__device__ __forceinline__ void quant_rows(const float (&v)[NT][K / kT], Lds & L) {
+    constexpr int CH = K / kT, BPR = K / kQK;
+    const int t = threadIdx.x, e = t & 31;
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok)
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float x = v[tok][c];
+            const float am = max32_f(fabsf(x));
+            const float d = am / 127.0f;
+            const float id = am != 0.0f ? 127.0f / am : 0.0f;
+            const int q = (int) rintf(x * id);
+            const int b = (c * kT + t) >> 5;
+            int8_t * dst = e < 16 ? L.qlo : L.qhi;
+            dst[(tok * BPR + b) * 16 + (e & 15)] = (int8_t) q;
+            if (e == 0) L.qdx[tok * BPR + b] = round_f16(d);
+        }
     __syncthreads();
-    float s = red[0];
-    for (int w = 1; w < kW; ++w) s = fmaxf(s, red[w]);
-    __syncthreads();
-    return s;
 }
 
 // ------------------------------------------------------------------- GEMV
 // Row groups of a GEMV are dealt to the grid's waves: wave gw takes groups
 // gw and gw + nwaves (at most two per wave; the host checks).
-template <int SLOTS, bool DUAL>
+template <int K, bool DUAL>
 struct Q8Regs {
-    int4 w[2][SLOTS][2], u[2][SLOTS][2];
-    float dw[2][SLOTS], du[2][SLOTS];
+    static constexpr int S = Geo<K>::SLOTS;
+    int4 w[2][S][2], u[2][S][2];
+    float dw[2][S], du[2][S];
     uint64_t res[2][2];   // residual elements (tagged) read early by the storing lanes
-    int ng;          // groups this wave owns (0..2)
+    int ng;               // groups this wave owns (0..2)
 };
 
-template <int SLOTS, bool DUAL>
-__device__ __forceinline__ void q8_prefetch(Q8Regs<SLOTS, DUAL> & R, const int8_t * W, const uint16_t * Wd,
-                                            const int8_t * U, const uint16_t * Ud, int rows, int K) {
-    const int BPR = K / kQK, LPR = BPR / SLOTS, RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR;
-    const int groups = rows / RPW;
+template <int K, bool DUAL>
+__device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * W, const uint16_t * Wd,
+                                            const int8_t * U, const uint16_t * Ud, int rows) {
+    using G = Geo<K>;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
+    const int groups = rows / G::RPW;
     const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
     R.ng = 0;
 #pragma unroll
@@ -190,17 +292,17 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<SLOTS, DUAL> & R, const int8_
         const int g = gw + gi * nw;
         if (g >= groups) break;
         R.ng = gi + 1;
-        const int r = g * RPW + rsub;
+        const int r = g * G::RPW + rsub;
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int b = lir + s * LPR;
+        for (int s = 0; s < G::SLOTS; ++s) {
+            const int b = lir + s * G::LPR;
             const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
             R.w[gi][s][0] = wp[0]; R.w[gi][s][1] = wp[1];
-            R.dw[gi][s] = h2f(Wd[(size_t) r * BPR + b]);
+            R.dw[gi][s] = h2f(Wd[(size_t) r * G::BPR + b]);
             if (DUAL) {
                 const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
                 R.u[gi][s][0] = up[0]; R.u[gi][s][1] = up[1];
-                R.du[gi][s] = h2f(Ud[(size_t) r * BPR + b]);
+                R.du[gi][s] = h2f(Ud[(size_t) r * G::BPR + b]);
             }
         }
     }
@@ -208,137 +310,112 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<SLOTS, DUAL> & R, const int8_
 
 // Issues the residual loads of the rows this lane will store (EPI_RESID),
 // before the phase input is awaited; q8_compute re-polls any not yet tagged.
-template <int NT, int SLOTS, bool DUAL>
-__device__ __forceinline__ void res_prefetch(Q8Regs<SLOTS, DUAL> & R, int K, const uint64_t * res, int res_stride) {
-    const int BPR = K / kQK, LPR = BPR / SLOTS, RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR;
+template <int NT, int K, bool DUAL>
+__device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL> & R, const uint64_t * res) {
+    using G = Geo<K>;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
     if (lir != 0) return;
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
         if (gi >= R.ng) break;
-        const int r = (gw + gi * nw) * RPW + rsub;
+        const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) R.res[gi][t] = tload(res + (size_t) t * res_stride + r);
+        for (int t = 0; t < NT; ++t) R.res[gi][t] = tload(res + (size_t) t * kHS + r);
     }
 }
 
-__device__ __forceinline__ bool wg_has_rows(int rows, int K, int slots) {
-    const int LPR = (K / kQK) / slots, RPW = 64 / LPR;
-    return blockIdx.x * kW < rows / RPW;
+template <int K>
+__device__ __forceinline__ bool wg_has_rows(int rows) {
+    return (int) blockIdx.x * kW < rows / Geo<K>::RPW;
 }
 
-// One lane's 32-element block of token `tok` from LDS x [nt][K].
-__device__ __forceinline__ void blk_lds(const float * x, int K, int tok, int blk, float (&v)[32]) {
-    const float4 * p = (const float4 *) (x + (size_t) tok * K + blk * kQK);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) { const float4 q = p[c]; v[4 * c] = q.x; v[4 * c + 1] = q.y; v[4 * c + 2] = q.z; v[4 * c + 3] = q.w; }
-}
-
-// Q8_0 GEMV over LDS input x [NT][K] (optionally RMSNorm'd with norm_w),
-// epilogue, tagged stores into out [NT][out_stride].  res: residual slot
-// (tagged, read by the storing lane) for EPI_RESID.
-template <int NT, int SLOTS, bool DUAL>
-__device__ __forceinline__ void q8_compute(const Q8Regs<SLOTS, DUAL> & R, int rows, int K, const float * x,
-                                           const float * norm_w, float eps, int epi, const uint64_t * res,
-                                           uint32_t res_tag, int res_stride, uint64_t * out, uint32_t out_tag,
-                                           int out_stride, bool & dead, int32_t * err) {
+// Q8_0 GEMV over the quantised LDS input, epilogue, tagged stores into
+// out [NT][kHS].  res: residual slot (tagged) for EPI_RESID.
+template <int NT, int K, bool DUAL>
+__device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
+                                           uint32_t res_tag, uint64_t * out, uint32_t out_tag, bool & dead,
+                                           int32_t * err) {
+    using G = Geo<K>;
     if (R.ng == 0) return;
-    const int BPR = K / kQK, LPR = BPR / SLOTS, RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
-    float scale[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        scale[t] = 1.0f;
-        if (norm_w) {
-            double ss = 0.0;
-#pragma unroll
-            for (int s = 0; s < SLOTS; ++s) {
-                float v[32];
-                blk_lds(x, K, t, lir + s * LPR, v);
-#pragma unroll
-                for (int j = 0; j < 32; ++j) ss += (double) (v[j] * v[j]);
-            }
-            ss = group_sum_d(ss, LPR);
-            const float mean = (float) (ss / (double) K);
-            scale[t] = 1.0f / sqrtf(mean + eps);
-        }
-    }
     double acc[2][NT], acc2[2][NT];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
         for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int b = lir + s * LPR;
-        float nw_[32];
-        if (norm_w) {
-            const float4 * p = (const float4 *) (norm_w + b * kQK);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) { const float4 q = p[c]; nw_[4 * c] = q.x; nw_[4 * c + 1] = q.y; nw_[4 * c + 2] = q.z; nw_[4 * c + 3] = q.w; }
-        }
+    for (int s = 0; s < G::SLOTS; ++s) {
+        const int b = lir + s * G::LPR;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            float v[32];
-            blk_lds(x, K, t, b, v);
-            if (norm_w) {
-#pragma unroll
-                for (int j = 0; j < 32; ++j) { const float y = v[j] * scale[t]; v[j] = y * nw_[j]; }
-            }
-            float am = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(v[j]));
-            const float d = am / 127.0f;
-            const float id = am != 0.0f ? 127.0f / am : 0.0f;
-            int q[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const int a0 = (int) rintf(v[4 * c] * id), a1 = (int) rintf(v[4 * c + 1] * id);
-                const int a2 = (int) rintf(v[4 * c + 2] * id), a3 = (int) rintf(v[4 * c + 3] * id);
-                q[c] = (a0 & 0xff) | ((a1 & 0xff) << 8) | ((a2 & 0xff) << 16) | ((int) ((unsigned) a3 << 24));
-            }
-            const int4 x0 = make_int4(q[0], q[1], q[2], q[3]), x1 = make_int4(q[4], q[5], q[6], q[7]);
-            const float dx = round_f16(d);
+            const int4 x0 = *(const int4 *) &L.qlo[(t * G::BPR + b) * 16];
+            const int4 x1 = *(const int4 *) &L.qhi[(t * G::BPR + b) * 16];
+            const float dx = L.qdx[t * G::BPR + b];
 #pragma unroll
             for (int gi = 0; gi < 2; ++gi) {
                 if (gi >= R.ng) break;
-                acc[gi][t] += (double) (R.dw[gi][s] * dx) * (double) dot32_i8(R.w[gi][s][0], R.w[gi][s][1], x0, x1);
-                if (DUAL) acc2[gi][t] += (double) (R.du[gi][s] * dx) * (double) dot32_i8(R.u[gi][s][0], R.u[gi][s][1], x0, x1);
+                // d_w * d_x (two fp16 values) is exact in fp32 and its product with
+                // the int32 block sum exact in fp64: fma rounds like mul + add
+                acc[gi][t] = fma((double) (R.dw[gi][s] * dx), (double) dot32_i8(R.w[gi][s][0], R.w[gi][s][1], x0, x1),
+                                 acc[gi][t]);
+                if (DUAL)
+                    acc2[gi][t] = fma((double) (R.du[gi][s] * dx),
+                                      (double) dot32_i8(R.u[gi][s][0], R.u[gi][s][1], x0, x1), acc2[gi][t]);
             }
         }
     }
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
         if (gi >= R.ng) break;
-        const int r = (gw + gi * nw) * RPW + rsub;
+        const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const double a1 = group_sum_d(acc[gi][t], LPR);
-            const double a2 = DUAL ? group_sum_d(acc2[gi][t], LPR) : 0.0;
+            const double a1 = group_sum_d(acc[gi][t], G::LPR);
+            const double a2 = DUAL ? group_sum_d(acc2[gi][t], G::LPR) : 0.0;
             if (lir != 0) continue;
             const float v = (float) a1;
             float o;
             if (epi == EPI_RESID) {
                 const uint64_t rv = R.res[gi][t];
                 o = v + ((uint32_t) (rv >> 32) == res_tag ? __uint_as_float((uint32_t) rv)
-                                                          : twait(res + (size_t) t * res_stride + r, res_tag, dead, err));
+                                                          : twait(res + (size_t) t * kHS + r, res_tag, dead, err));
+            } else if (epi == EPI_SWIGLU) {
+                o = silu_q3t(v) * (float) a2;
+            } else {
+                o = v;
             }
-            else if (epi == EPI_SWIGLU) o = silu_q3t(v) * (float) a2;
-            else o = v;
-            tstore(out + (size_t) t * out_stride + r, out_tag, o);
+            tstore(out + (size_t) t * kHS + r, out_tag, o);
         }
     }
 }
 
-// F16 head GEMV (K = d, one slot per lane), RMSNorm'd input row in LDS.
-// Outputs tagged (code predictor) or plain (talker: logits, plus the normed
-// hidden written by workgroup 0).
-__device__ __forceinline__ void f16_head(const uint16_t * W, int rows, int K, const float * x, const float * norm_w,
-                                         float eps, uint64_t * out_tagged, uint32_t tag, float * out_plain,
-                                         float * hidden_out) {
-    const int BPR = K / kQK, LPR = BPR, RPW = 64 / LPR;   // K <= 1024
+// ------------------------------------------------------------------ F16 head
+// RMSNorm'd input row, rounded to fp16 into LDS (the F16 weight x fp32
+// activation contract); workgroup 0 also writes the normed fp32 row to
+// hidden_out when given.
+template <int K>
+__device__ __forceinline__ void head_input(float (&v)[1][K / kT], const float (&nw)[K / kT], float eps, Lds & L,
+                                           float * hidden_out) {
+    constexpr int CH = K / kT;
+    rms_rows<1, K>(v, nw, eps, L);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * kT + threadIdx.x, b = i >> 5, e = i & 31;
+        if (hidden_out && blockIdx.x == 0) hidden_out[i] = v[0][c];
+        L.hq[e >> 3][b * 8 + (e & 7)] = f2h(v[0][c]);
+    }
+    __syncthreads();
+}
+
+// F16 GEMV (one 32-element block per lane), outputs tagged (code predictor)
+// or plain (talker logits).
+template <int K>
+__device__ __forceinline__ void f16_head(const uint16_t * W, int rows, const Lds & L, uint64_t * out_tagged,
+                                         uint32_t tag, float * out_plain) {
+    static_assert(K / kQK <= 32 && ((K / kQK) & (K / kQK - 1)) == 0, "head width");
+    constexpr int LPR = K / kQK, RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR;
     const int groups = rows / RPW;
     const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
@@ -353,38 +430,19 @@ __device__ __forceinline__ void f16_head(const uint16_t * W, int rows, int K, co
 #pragma unroll
         for (int c = 0; c < 4; ++c) w[gi][c] = wp[c];
     }
-    float v[32];
-    blk_lds(x, K, 0, lir, v);
-    double ss = 0.0;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) ss += (double) (v[j] * v[j]);
-    ss = group_sum_d(ss, LPR);
-    const float scale = 1.0f / sqrtf((float) (ss / (double) K) + eps);
-    const float4 * np = (const float4 *) (norm_w + lir * kQK);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const float4 q = np[c];
-        float y;
-        y = v[4 * c] * scale; v[4 * c] = y * q.x;
-        y = v[4 * c + 1] * scale; v[4 * c + 1] = y * q.y;
-        y = v[4 * c + 2] * scale; v[4 * c + 2] = y * q.z;
-        y = v[4 * c + 3] * scale; v[4 * c + 3] = y * q.w;
-    }
-    if (hidden_out && blockIdx.x == 0 && threadIdx.x < LPR) {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) hidden_out[lir * kQK + j] = v[j];
-    }
     if (ng == 0) return;
     double acc[2] = {0.0, 0.0};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+        const int4 x4 = *(const int4 *) &L.hq[c][lir * 8];
+        const uint16_t * xh = (const uint16_t *) &x4;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float xf = round_f16(v[8 * c + j]);
+            const double xd = (double) h2f(xh[j]);
 #pragma unroll
             for (int gi = 0; gi < 2; ++gi) {
                 const uint16_t * wh = (const uint16_t *) &w[gi][c];
-                acc[gi] += (double) (h2f(wh[j]) * xf);
+                acc[gi] = fma((double) h2f(wh[j]), xd, acc[gi]);   // fp16 x fp16: exact product
             }
         }
     }
@@ -400,174 +458,195 @@ __device__ __forceinline__ void f16_head(const uint16_t * W, int rows, int K, co
 }
 
 // -------------------------------------------------------------- attention
-// QK-norm + NEOX RoPE of one 128-row held by threads 0..127 (value v);
-// returns the rotated element for threads < 128.
-__device__ __forceinline__ float norm_rope(float v, const float * w, float eps, const float * c, const float * s,
-                                           float * tmp, double * red) {
-    const int t = threadIdx.x;
-    const double ss = wg_sum(t < 128 ? (double) (v * v) : 0.0, red);
-    const float mean = (float) (ss / 128.0);
-    const float scale = 1.0f / sqrtf(mean + eps);
-    if (t < 128) { float y = v * scale; tmp[t] = y * w[t]; }
-    __syncthreads();
-    float o = 0.0f;
-    if (t < 128) {
-        const int i = t & 63;
-        const float x0 = tmp[i], x1 = tmp[i + 64];
-        if (t < 64) { const float p = x0 * c[i], q = x1 * s[i]; o = p - q; }
-        else        { const float p = x0 * s[i], q = x1 * c[i]; o = p + q; }
-    }
-    __syncthreads();
-    return o;
-}
-
-// Attention of KV head g = blockIdx.x for its `group` query heads and nt
-// tokens at positions pos0.. (causal).  Talker (cp == false): positions
-// < pos0 from the HBM cache, new rows appended there; code predictor: all
-// rows in this workgroup's LDS.
+// Attention of KV head g = blockIdx.x for its two query heads and nt tokens
+// at positions pos0.. (causal).  Talker (cp == false): positions < pos0 come
+// from the HBM cache and the new rows are appended there; code predictor:
+// all rows live in this workgroup's LDS.
+//
+// Wave w owns row w of (q0, q1, k, v): lane l holds elements l and l + 64,
+// which are exactly the NEOX rotation pairs, so QK-norm and RoPE need only
+// wave reductions.  Scores and P.V use 16 lanes per position (8 dims per
+// lane) for both query heads at once; softmax max / sum and the P.V combine
+// are the only workgroup barriers.
 __device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int nt, int pos0,
-                                const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
+                                int qd, const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
                                 bool & dead) {
-    const int g = blockIdx.x, t = threadIdx.x;
-    const int group = A.n_head / A.n_kv_head, qd = A.n_head * 128, kd = A.n_kv_head * 128, qkvd = qd + 2 * kd;
+    const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int kd = qd / 2;
     const float * rc = cp ? A.cp_rope_cos : A.rope_cos;
     const float * rs = cp ? A.cp_rope_sin : A.rope_sin;
-    float * qf = L.a;                      // [group][nt][128] rotated, fp16-rounded q
-    float * knew = L.a + 4 * 128;          // [nt][128]
-    float * vnew = knew + 2 * 128;         // [nt][128]
-    float * tmp = L.x;                     // 128 scratch
+    float * qf = L.a;                      // [tok][head][128] rotated, fp16-rounded q
+    float * knew = L.a + 4 * 128;          // [tok][128]
+    float * vnew = knew + 2 * 128;         // [tok][128]
     uint16_t * kc = A.kc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
     uint16_t * vc = A.vc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
-    // stage this head group's q, k, v rows
-    float qraw[2][2], kraw[2], vraw[2];
+
+    // ---- stage + QK-norm + RoPE, one row per wave
     {
-        // (q0, q1, k, v) of each token, one batch; threads >= 128 load nothing
+        const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
-        const int tc = t < 128 ? t : 0;
 #pragma unroll
         for (int tok = 0; tok < 2; ++tok) {
-            const uint64_t * row = qkv + (size_t) (tok < nt ? tok : 0) * kSlot / 2;
-            ptr[4 * tok + 0] = row + (g * group + 0) * 128 + tc;
-            ptr[4 * tok + 1] = row + (g * group + 1) * 128 + tc;
-            ptr[4 * tok + 2] = row + qd + g * 128 + tc;
-            ptr[4 * tok + 3] = row + qd + kd + g * 128 + tc;
+            const uint64_t * row = qkv + (size_t) (tok < nt ? tok : 0) * kHS + col;
+            ptr[2 * tok] = row + lane;
+            ptr[2 * tok + 1] = row + lane + 64;
+        }
+#pragma unroll
+        for (int k = 4; k < kB; ++k) ptr[k] = ptr[0];
+        // norm weights and RoPE rows do not depend on the new rows: load them first
+        const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
+        const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
+        float rcv[2], rsv[2];
+#pragma unroll
+        for (int tok = 0; tok < 2; ++tok) {
+            const int pos = pos0 + (tok < nt ? tok : 0);
+            rcv[tok] = rc[(size_t) pos * 64 + lane];
+            rsv[tok] = rs[(size_t) pos * 64 + lane];
         }
         float val[kB];
-        twait_batch(ptr, t < 128 ? 4 * nt : 0, qkv_tag, val, dead, A.err);
-#pragma unroll
-        for (int tok = 0; tok < 2; ++tok) {
-            qraw[0][tok] = val[4 * tok]; qraw[1][tok] = val[4 * tok + 1];
-            kraw[tok] = val[4 * tok + 2]; vraw[tok] = val[4 * tok + 3];
-        }
-    }
-    (void) qkvd;
-    for (int tok = 0; tok < nt; ++tok) {
-        const int pos = pos0 + tok;
-        for (int hq = 0; hq < group; ++hq) {
-            const float o = norm_rope(qraw[hq][tok], W.q_norm, A.eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, L.red);
-            if (t < 128) qf[(hq * 2 + tok) * 128 + t] = round_f16(o);
-        }
-        const float o = norm_rope(kraw[tok], W.k_norm, A.eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, L.red);
-        if (t < 128) {
-            const uint16_t kh = f2h(o), vh = f2h(vraw[tok]);
-            knew[tok * 128 + t] = h2f(kh);
-            vnew[tok * 128 + t] = h2f(vh);
-            if (cp) { L.cpk[layer][pos * 128 + t] = kh; L.cpv[layer][pos * 128 + t] = vh; }
-            else { kc[(size_t) pos * 128 + t] = kh; vc[(size_t) pos * 128 + t] = vh; }
+        twait_batch(ptr, 2 * nt, qkv_tag, val, dead, A.err);
+        for (int tok = 0; tok < nt; ++tok) {
+            const int pos = pos0 + tok;
+            const float x0 = val[2 * tok], x1 = val[2 * tok + 1];
+            if (wave < 3) {
+                const double ss = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
+                const float mean = (float) (ss / 128.0);
+                const float scale = 1.0f / sqrtf(mean + A.eps);
+                float y0 = x0 * scale, y1 = x1 * scale;
+                y0 = y0 * nw0;
+                y1 = y1 * nw1;
+                const float c = rcv[tok], sn = rsv[tok];
+                const float a0 = y0 * c, b0 = y1 * sn, a1 = y0 * sn, b1 = y1 * c;
+                const float o0 = a0 - b0, o1 = a1 + b1;
+                if (wave < 2) {
+                    qf[(tok * 2 + wave) * 128 + lane] = round_f16(o0);
+                    qf[(tok * 2 + wave) * 128 + lane + 64] = round_f16(o1);
+                } else {
+                    const uint16_t h0 = f2h(o0), h1 = f2h(o1);
+                    knew[tok * 128 + lane] = h2f(h0);
+                    knew[tok * 128 + lane + 64] = h2f(h1);
+                    if (cp) { L.cpk[layer][pos * 128 + lane] = h0; L.cpk[layer][pos * 128 + lane + 64] = h1; }
+                    else { kc[(size_t) pos * 128 + lane] = h0; kc[(size_t) pos * 128 + lane + 64] = h1; }
+                }
+            } else {
+                const uint16_t h0 = f2h(x0), h1 = f2h(x1);
+                vnew[tok * 128 + lane] = h2f(h0);
+                vnew[tok * 128 + lane + 64] = h2f(h1);
+                if (cp) { L.cpv[layer][pos * 128 + lane] = h0; L.cpv[layer][pos * 128 + lane + 64] = h1; }
+                else { vc[(size_t) pos * 128 + lane] = h0; vc[(size_t) pos * 128 + lane + 64] = h1; }
+            }
         }
     }
     __syncthreads();
-    const int lane = t & 63, wave = t >> 6;
+
+    const int sub = lane & 15, pw = lane >> 4;   // dims [sub*8, sub*8+8) of position j0 + wave*4 + pw
     for (int tok = 0; tok < nt; ++tok) {
         const int n_kv = pos0 + tok + 1;
-        // scores for every query head of the group: 8 lanes per position, 16 dims per lane
-        const int sub = lane & 7, pw = lane >> 3;
-        float lmax[2] = {-INFINITY, -INFINITY};
-        for (int j0 = 0; j0 < n_kv; j0 += 8 * kW) {
-            const int j = j0 + wave * 8 + pw;
-            float kv16[16];
+        double q0[8], q1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            q0[e] = (double) qf[(tok * 2 + 0) * 128 + sub * 8 + e];
+            q1[e] = (double) qf[(tok * 2 + 1) * 128 + sub * 8 + e];
+        }
+        // ---- scores
+        float lm0 = -INFINITY, lm1 = -INFINITY;
+#pragma unroll 2
+        for (int j0 = 0; j0 < n_kv; j0 += 4 * kW) {
+            const int j = j0 + wave * 4 + pw;
+            float kv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kv[e] = 0.0f;
             if (j < n_kv) {
-                if (cp) {
+                if (j >= pos0) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) kv16[e] = h2f(L.cpk[layer][j * 128 + sub * 16 + e]);
-                } else if (j < pos0) {
-                    const int4 * kp = (const int4 *) (kc + (size_t) j * 128 + sub * 16);
-                    const int4 k0 = kp[0], k1 = kp[1];
-                    const uint16_t * a0 = (const uint16_t *) &k0;
-                    const uint16_t * a1 = (const uint16_t *) &k1;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) { kv16[e] = h2f(a0[e]); kv16[8 + e] = h2f(a1[e]); }
+                    for (int e = 0; e < 8; ++e) kv[e] = knew[(j - pos0) * 128 + sub * 8 + e];
                 } else {
+                    const int4 k4 = cp ? *(const int4 *) &L.cpk[layer][j * 128 + sub * 8]
+                                       : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
+                    const uint16_t * kh = (const uint16_t *) &k4;
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) kv16[e] = knew[(j - pos0) * 128 + sub * 16 + e];
+                    for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
                 }
             }
-            for (int hq = 0; hq < group; ++hq) {
-                double acc = 0.0;
-                if (j < n_kv) {
-                    const float * q = qf + (hq * 2 + tok) * 128 + sub * 16;
+            // fp16 x fp16 products are exact in fp64, so fma(q, k, acc) rounds
+            // exactly like acc + (double)(q * k)
+            double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) acc += (double) (q[e] * kv16[e]);
-                }
-                acc += __shfl_xor(acc, 4);
-                acc += __shfl_xor(acc, 2);
-                acc += __shfl_xor(acc, 1);
-                if (j < n_kv) {
-                    const float s = (float) acc * A.attn_scale;
-                    if (sub == 0) L.sc[hq * kMaxCtx + j] = s;
-                    lmax[hq] = fmaxf(lmax[hq], s);
-                }
+            for (int e = 0; e < 8; ++e) {
+                const double kd = (double) kv[e];
+                a0 = fma(q0[e], kd, a0);
+                a1 = fma(q1[e], kd, a1);
+            }
+            a0 = group_sum_d(a0, 16);
+            a1 = group_sum_d(a1, 16);
+            if (j < n_kv) {
+                const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
+                if (sub == 0) { L.sc[j] = s0; L.sc[kMaxCtx + j] = s1; }
+                lm0 = fmaxf(lm0, s0);
+                lm1 = fmaxf(lm1, s1);
             }
         }
-        for (int hq = 0; hq < group; ++hq) {
-            float * sc = L.sc + hq * kMaxCtx;
-            const float mx = wg_max(lmax[hq], L.fred);
-            double ls = 0.0;
-            for (int j = t; j < n_kv; j += kT) { const float e = expf_q3t(sc[j] - mx); sc[j] = e; ls += (double) e; }
-            const double sum = wg_sum(ls, L.red);
-            const float inv = (float) (1.0 / sum);
-            for (int j = t; j < n_kv; j += kT) sc[j] = round_f16(sc[j] * inv);
-            __syncthreads();
-            // P.V: 16 lanes per position, 8 dims per lane
-            const int dsub = lane & 15, pq = lane >> 4;
-            double o[8];
+        lm0 = wave_max_f(lm0);
+        lm1 = wave_max_f(lm1);
+        if (lane == 0) { L.fred[wave] = lm0; L.fred[kW + wave] = lm1; }
+        __syncthreads();
+        float mx0 = L.fred[0], mx1 = L.fred[kW];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = 0.0;
-            for (int j0 = 0; j0 < n_kv; j0 += 4 * kW) {
-                const int j = j0 + wave * 4 + pq;
-                if (j < n_kv) {
-                    const float p = sc[j];
-                    float vv[8];
-                    if (cp) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = h2f(L.cpv[layer][j * 128 + dsub * 8 + e]);
-                    } else if (j < pos0) {
-                        const int4 q4 = *(const int4 *) (vc + (size_t) j * 128 + dsub * 8);
-                        const uint16_t * vh = (const uint16_t *) &q4;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = h2f(vh[e]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = vnew[(j - pos0) * 128 + dsub * 8 + e];
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] += (double) (p * vv[e]);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) { o[e] += __shfl_xor(o[e], 16); o[e] += __shfl_xor(o[e], 32); }
-            if (pq == 0) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) L.pv[wave * 128 + dsub * 8 + e] = o[e];
-            }
-            __syncthreads();
-            if (t < 128) {
-                double r = L.pv[t];
-                for (int w = 1; w < kW; ++w) r += L.pv[w * 128 + t];
-                tstore(out + (size_t) tok * (kSlot / 2) + (g * group + hq) * 128 + t, out_tag, (float) r);
-            }
-            __syncthreads();
+        for (int w = 1; w < kW; ++w) { mx0 = fmaxf(mx0, L.fred[w]); mx1 = fmaxf(mx1, L.fred[kW + w]); }
+        // ---- exp and denominators (each thread its own positions)
+        double ls0 = 0.0, ls1 = 0.0;
+        for (int j = t; j < n_kv; j += kT) {
+            const float e0 = expf_q3t(L.sc[j] - mx0), e1 = expf_q3t(L.sc[kMaxCtx + j] - mx1);
+            L.sc[j] = e0; L.sc[kMaxCtx + j] = e1;
+            ls0 += (double) e0; ls1 += (double) e1;
         }
+        ls0 = wave_sum_d(ls0);
+        ls1 = wave_sum_d(ls1);
+        if (lane == 0) { L.red[wave] = ls0; L.red[kW + wave] = ls1; }
+        __syncthreads();
+        double sum0 = L.red[0], sum1 = L.red[kW];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) { sum0 += L.red[w]; sum1 += L.red[kW + w]; }
+        const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
+        // fp16-rounded probabilities, each thread its own positions
+        for (int j = t; j < n_kv; j += kT) {
+            L.sc[j] = round_f16(L.sc[j] * inv0);
+            L.sc[kMaxCtx + j] = round_f16(L.sc[kMaxCtx + j] * inv1);
+        }
+        __syncthreads();
+        // ---- P.V: lane l owns dims 2l, 2l+1 of both heads; wave w takes
+        // positions j = w, w + 4, ...; no cross-lane reduction
+        double o00 = 0.0, o01 = 0.0, o10 = 0.0, o11 = 0.0;
+#pragma unroll 4
+        for (int j = wave; j < n_kv; j += kW) {
+            const double p0 = (double) L.sc[j], p1 = (double) L.sc[kMaxCtx + j];
+            float v0, v1;
+            if (j >= pos0) {
+                v0 = vnew[(j - pos0) * 128 + 2 * lane];
+                v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
+            } else {
+                const uint32_t w2 = cp ? *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane]
+                                       : *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane);
+                v0 = h2f((uint16_t) (w2 & 0xffffu));
+                v1 = h2f((uint16_t) (w2 >> 16));
+            }
+            const double d0 = (double) v0, d1 = (double) v1;
+            o00 = fma(p0, d0, o00); o01 = fma(p0, d1, o01);
+            o10 = fma(p1, d0, o10); o11 = fma(p1, d1, o11);
+        }
+        L.pv[(wave * 2 + 0) * 128 + 2 * lane] = o00;
+        L.pv[(wave * 2 + 0) * 128 + 2 * lane + 1] = o01;
+        L.pv[(wave * 2 + 1) * 128 + 2 * lane] = o10;
+        L.pv[(wave * 2 + 1) * 128 + 2 * lane + 1] = o11;
+        __syncthreads();
+        {
+            const int h = t >> 7, e = t & 127;
+            double r = L.pv[h * 128 + e];
+#pragma unroll
+            for (int w = 1; w < kW; ++w) r += L.pv[(w * 2 + h) * 128 + e];
+            tstore(out + (size_t) tok * kHS + (g * 2 + h) * 128 + e, out_tag, (float) r);
+        }
+        __syncthreads();
     }
 }
 
@@ -596,65 +675,86 @@ __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
 __device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, uint32_t tag, int frame, int group,
                              bool & dead) {
     const SampleParams & P = *A.params;
-    stage(logits, 1, A.cp_vocab, 0, tag, L.x, dead, A.err);
+    stage_plain(logits, A.cp_vocab, tag, L.x, dead, A.err);
     return sample_core<kT>(L.x, A.cp_vocab, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame,
                            (uint32_t) group, L.S);
 }
 
 // ------------------------------------------------------------------ layers
-template <int NT, int SQ, int SO, int SD>
+// One decoder layer (QKV -> attention -> Wo + residual -> gate/up SwiGLU ->
+// down + residual) for NT tokens.  The input rows come from tagged slot p_in,
+// or (x_lds != nullptr, layer 0) from the rows gathered into LDS.  The
+// output is tagged slot p_out.
+template <int NT, int D, int QD, int FF>
 __device__ void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int pos0, uint32_t tb, int & p,
-                        int p_in, bool in_in_lds, int & p_out, bool & dead) {
-    const int d = A.d, qd = A.n_head * 128, kd = A.n_kv_head * 128, qkvd = qd + 2 * kd;
-    const int ffn = cp ? A.cp_ffn : A.ffn;
+                        int p_in, const float * x_lds, int & p_out, bool & dead) {
+    constexpr int QKVD = 2 * QD;
     uint64_t * ar = A.arena;
-    constexpr int HS = kSlot / 2;          // per-token stride inside a slot
     // QKV (RMSNorm'd input)
     const int p_qkv = p++;
-    if (wg_has_rows(qkvd, d, SQ)) {
-        Q8Regs<SQ, false> R;
-        q8_prefetch<SQ, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, qkvd, d);
-        if (!in_in_lds) stage(ar + (size_t) p_in * kSlot, NT, d, HS, tb | p_in, L.x, dead, A.err);
-        q8_compute<NT, SQ, false>(R, qkvd, d, L.x, W.attn_norm, A.eps, EPI_STORE, nullptr, 0, 0,
-                                  ar + (size_t) p_qkv * kSlot, tb | p_qkv, HS, dead, A.err);
+    if (wg_has_rows<D>(QKVD)) {
+        Q8Regs<D, false> R;
+        q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD);
+        float nw[D / kT];
+        norm_prefetch<D>(W.attn_norm, nw);
+        float v[NT][D / kT];
+        if (x_lds) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int c = 0; c < D / kT; ++c) v[t][c] = x_lds[t * D + c * kT + threadIdx.x];
+        } else {
+            load_tagged<NT, D>(ar + (size_t) p_in * kSlot, tb | p_in, v, dead, A.err);
+        }
+        rms_rows<NT, D>(v, nw, A.eps, L);
+        quant_rows<NT, D>(v, L);
+        q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, dead, A.err);
     }
     __syncthreads();
     // attention (workgroup g < n_kv_head owns KV head g)
     const int p_att = p++;
     if ((int) blockIdx.x < A.n_kv_head)
-        attention_phase(A, L, W, layer, cp, NT, pos0, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+        attention_phase(A, L, W, layer, cp, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
                         ar + (size_t) p_att * kSlot, tb | p_att, dead);
     __syncthreads();
     // Wo + residual (the block input)
     const int p_wo = p++;
-    if (wg_has_rows(d, qd, SO)) {
-        Q8Regs<SO, false> R;
-        q8_prefetch<SO, false>(R, W.wo, W.wo_d, nullptr, nullptr, d, qd);
-        res_prefetch<NT, SO, false>(R, qd, ar + (size_t) p_in * kSlot, HS);
-        stage(ar + (size_t) p_att * kSlot, NT, qd, HS, tb | p_att, L.x, dead, A.err);
-        q8_compute<NT, SO, false>(R, d, qd, L.x, nullptr, A.eps, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in, HS,
-                                  ar + (size_t) p_wo * kSlot, tb | p_wo, HS, dead, A.err);
+    if (wg_has_rows<QD>(D)) {
+        Q8Regs<QD, false> R;
+        q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D);
+        res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot);
+        float v[NT][QD / kT];
+        load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
+        quant_rows<NT, QD>(v, L);
+        q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in, ar + (size_t) p_wo * kSlot,
+                                  tb | p_wo, dead, A.err);
     }
     __syncthreads();
     // gate/up + SwiGLU (RMSNorm'd)
     const int p_gu = p++;
-    if (wg_has_rows(ffn, d, SQ)) {
-        Q8Regs<SQ, true> R;
-        q8_prefetch<SQ, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, ffn, d);
-        stage(ar + (size_t) p_wo * kSlot, NT, d, HS, tb | p_wo, L.x, dead, A.err);
-        q8_compute<NT, SQ, true>(R, ffn, d, L.x, W.ffn_norm, A.eps, EPI_SWIGLU, nullptr, 0, 0,
-                                 ar + (size_t) p_gu * kSlot, tb | p_gu, HS, dead, A.err);
+    if (wg_has_rows<D>(FF)) {
+        Q8Regs<D, true> R;
+        q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF);
+        float nw[D / kT];
+        norm_prefetch<D>(W.ffn_norm, nw);
+        float v[NT][D / kT];
+        load_tagged<NT, D>(ar + (size_t) p_wo * kSlot, tb | p_wo, v, dead, A.err);
+        rms_rows<NT, D>(v, nw, A.eps, L);
+        quant_rows<NT, D>(v, L);
+        q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, dead, A.err);
     }
     __syncthreads();
     // down + residual
     const int p_dn = p++;
-    if (wg_has_rows(d, ffn, SD)) {
-        Q8Regs<SD, false> R;
-        q8_prefetch<SD, false>(R, W.wd, W.wd_d, nullptr, nullptr, d, ffn);
-        res_prefetch<NT, SD, false>(R, ffn, ar + (size_t) p_wo * kSlot, HS);
-        stage(ar + (size_t) p_gu * kSlot, NT, ffn, HS, tb | p_gu, L.x, dead, A.err);
-        q8_compute<NT, SD, false>(R, d, ffn, L.x, nullptr, A.eps, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo, HS,
-                                  ar + (size_t) p_dn * kSlot, tb | p_dn, HS, dead, A.err);
+    if (wg_has_rows<FF>(D)) {
+        Q8Regs<FF, false> R;
+        q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D);
+        res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot);
+        float v[NT][FF / kT];
+        load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
+        quant_rows<NT, FF>(v, L);
+        q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo, ar + (size_t) p_dn * kSlot,
+                                  tb | p_dn, dead, A.err);
     }
     __syncthreads();
     p_out = p_dn;
@@ -665,12 +765,13 @@ __device__ void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, b
 __device__ __forceinline__ void publish(const Args & A, const float * x, int nt, int d, int p, uint32_t tb) {
     if (blockIdx.x != 0) return;
     for (int t = 0; t < nt; ++t)
-        for (int i = threadIdx.x; i < d; i += kT) tstore(A.arena + (size_t) p * kSlot + (size_t) t * (kSlot / 2) + i, tb | p, x[t * d + i]);
+        for (int i = threadIdx.x; i < d; i += kT)
+            tstore(A.arena + (size_t) p * kSlot + (size_t) t * kHS + i, tb | p, x[t * d + i]);
 }
 
-template <int SQ, int SO, int SD>
 // The argument block lives in device memory: dynamic indexing into a by-value
 // kernel argument (cp_embd[s], cp_head[s]) would copy it to private scratch.
+template <int D, int QD, int FF>
 __global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int32_t frame) {
     const Args & A = *Ap;
     __shared__ Lds L;
@@ -678,7 +779,6 @@ __global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int3
     FrameState * st = A.st;
     if (st->done) return;
     const uint32_t tb = (uint32_t) (frame + 1) << 12;
-    const int d = A.d;
     const int t = threadIdx.x;
     int p = 0;
 
@@ -698,29 +798,34 @@ __global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int3
     for (int s = 0; s < 15; ++s) {
         const int p_x = p++;
         if (s == 0) {
-            for (int i = t; i < d; i += kT) {
+            for (int i = t; i < D; i += kT) {
                 L.x[i] = A.hidden[i];
-                L.x[d + i] = h2f(A.codec_embd[(size_t) tok0 * d + i]);
+                L.x[D + i] = h2f(A.codec_embd[(size_t) tok0 * D + i]);
             }
         } else {
-            for (int i = t; i < d; i += kT) L.x[i] = h2f(A.cp_embd[s - 1][(size_t) code * d + i]);
+            for (int i = t; i < D; i += kT) L.x[i] = h2f(A.cp_embd[s - 1][(size_t) code * D + i]);
         }
         __syncthreads();
         const int nt = s == 0 ? 2 : 1;
         const int pos0 = s == 0 ? 0 : s + 1;
-        publish(A, L.x, nt, d, p_x, tb);
+        publish(A, L.x, nt, D, p_x, tb);
         int p_in = p_x, p_out = p_x;
         for (int l = 0; l < A.cp_layers; ++l) {
-            if (nt == 2) layer_t<2, SQ, SO, SD>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, l == 0, p_out, dead);
-            else layer_t<1, SQ, SO, SD>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, l == 0, p_out, dead);
+            const float * x_lds = l == 0 ? L.x : nullptr;
+            if (nt == 2) layer_t<2, D, QD, FF>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else layer_t<1, D, QD, FF>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
             p_in = p_out;
         }
         // head on the last token's normed row
         const int p_head = p++;
-        stage(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * (kSlot / 2), 1, d, kSlot / 2, tb | p_out, L.x,
-              dead, A.err);
-        f16_head(A.cp_head[s], A.cp_vocab, d, L.x, A.cp_out_norm, A.eps, A.arena + (size_t) p_head * kSlot,
-                 tb | p_head, nullptr, nullptr);
+        {
+            float nw[D / kT];
+            norm_prefetch<D>(A.cp_out_norm, nw);
+            float v[1][D / kT];
+            load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
+            head_input<D>(v, nw, A.eps, L, nullptr);
+        }
+        f16_head<D>(A.cp_head[s], A.cp_vocab, L, A.arena + (size_t) p_head * kSlot, tb | p_head, nullptr);
         __syncthreads();
         code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
         if (t == 0) L.codes[s + 1] = code;
@@ -731,22 +836,28 @@ __global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int3
 
     // ---- talker step on the step embedding
     const int p_x = p++;
-    for (int i = t; i < d; i += kT) {
-        float s = h2f(A.codec_embd[(size_t) L.codes[0] * d + i]);
-        for (int g = 1; g < 16; ++g) s = s + h2f(A.cp_embd[g - 1][(size_t) L.codes[g] * d + i]);
-        const float tr = frame < A.n_trailing ? A.trailing[(size_t) frame * d + i] : A.pad[i];
+    for (int i = t; i < D; i += kT) {
+        float s = h2f(A.codec_embd[(size_t) L.codes[0] * D + i]);
+        for (int g = 1; g < 16; ++g) s = s + h2f(A.cp_embd[g - 1][(size_t) L.codes[g] * D + i]);
+        const float tr = frame < A.n_trailing ? A.trailing[(size_t) frame * D + i] : A.pad[i];
         L.x[i] = s + tr;
     }
     __syncthreads();
-    publish(A, L.x, 1, d, p_x, tb);
+    publish(A, L.x, 1, D, p_x, tb);
     const int pos = st->base_pos + frame;
     int p_in = p_x, p_out = p_x;
     for (int l = 0; l < A.n_layers; ++l) {
-        layer_t<1, SQ, SO, SD>(A, L, A.talker[l], l, false, pos, tb, p, p_in, l == 0, p_out, dead);
+        layer_t<1, D, QD, FF>(A, L, A.talker[l], l, false, pos, tb, p, p_in, l == 0 ? L.x : nullptr, p_out, dead);
         p_in = p_out;
     }
-    stage(A.arena + (size_t) p_out * kSlot, 1, d, kSlot / 2, tb | p_out, L.x, dead, A.err);
-    f16_head(A.codec_head, A.codec_vocab, d, L.x, A.out_norm, A.eps, nullptr, 0, A.logits, A.hidden);
+    {
+        float nw[D / kT];
+        norm_prefetch<D>(A.out_norm, nw);
+        float v[1][D / kT];
+        load_tagged<1, D>(A.arena + (size_t) p_out * kSlot, tb | p_out, v, dead, A.err);
+        head_input<D>(v, nw, A.eps, L, A.hidden);
+    }
+    f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits);
     if (blockIdx.x == 0 && t == 0) {
         st->frame = frame;
         st->next_frame = frame + 1;

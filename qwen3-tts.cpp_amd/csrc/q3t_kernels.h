@@ -470,11 +470,7 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
         float bv = -INFINITY; int32_t bi = 0x7fffffff;
         for (int i = t; i < V; i += NTH)
             if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int32_t oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        wave_argmax(bv, bi);
         if ((t & 63) == 0) { S.fv[t >> 6] = bv; S.iv[t >> 6] = bi; }
         __syncthreads();
         float b = S.fv[0]; int32_t i0 = S.iv[0];

@@ -53,18 +53,6 @@ __device__ __forceinline__ float expf_q3t(float x) {
 // ggml_silu_f32: x / (1 + e^-x), correctly rounded division.
 __device__ __forceinline__ float silu_q3t(float x) { return x / (1.0f + expf_q3t(-x)); }
 
-// Wave64 reductions.  All 64 lanes must be active.
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
 // Cross-lane moves through DPP (VALU, a few cycles) instead of ds_bpermute.
 // ctrl: 0xB1 = quad_perm[1,0,3,2] (xor 1), 0x4E = quad_perm[2,3,0,1] (xor 2),
 // 0x141 = row_half_mirror (lane i <-> 7-i), 0x140 = row_mirror (i <-> 15-i).
@@ -90,6 +78,48 @@ __device__ __forceinline__ double group_sum_d(double v, int n) {
     if (n > 8) v += dpp_d<0x140>(v);
     if (n > 16) v += swz16_d(v);
     return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                            __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+
+// Wave64 reductions (all 64 lanes active): DPP / swizzle within each 32-lane
+// half, then the two halves through readlane.  Every lane gets the same value.
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v = group_sum_d(v, 32);
+    return readlane_d(v, 0) + readlane_d(v, 32);
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+}
+// First-index argmax over the wave: (value, index) with the larger value, or
+// the smaller index on equal values.  Every lane gets the winner.
+__device__ __forceinline__ void argmax_step(float & bv, int & bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+__device__ __forceinline__ void wave_argmax(float & bv, int & bi) {
+    argmax_step(bv, bi, dpp_f<0xB1>(bv), __builtin_amdgcn_update_dpp(0, bi, 0xB1, 0xF, 0xF, false));
+    argmax_step(bv, bi, dpp_f<0x4E>(bv), __builtin_amdgcn_update_dpp(0, bi, 0x4E, 0xF, 0xF, false));
+    argmax_step(bv, bi, dpp_f<0x141>(bv), __builtin_amdgcn_update_dpp(0, bi, 0x141, 0xF, 0xF, false));
+    argmax_step(bv, bi, dpp_f<0x140>(bv), __builtin_amdgcn_update_dpp(0, bi, 0x140, 0xF, 0xF, false));
+    argmax_step(bv, bi, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bv), 0x401F)),
+                __builtin_amdgcn_ds_swizzle(bi, 0x401F));
+    float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+    int i0 = __builtin_amdgcn_readlane(bi, 0);
+    argmax_step(v0, i0, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 32)), __builtin_amdgcn_readlane(bi, 32));
+    bv = v0; bi = i0;
 }
 
 // Workgroup-wide fp64 sum for 256 threads; every thread gets the same value.
