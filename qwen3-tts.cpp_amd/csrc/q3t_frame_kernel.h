@@ -468,7 +468,7 @@ __device__ __forceinline__ void f16_head(const uint16_t * W, int rows, const Lds
 // wave reductions.  Scores and P.V use 16 lanes per position (8 dims per
 // lane) for both query heads at once; softmax max / sum and the P.V combine
 // are the only workgroup barriers.
-__device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int nt, int pos0,
+__device__ __attribute__((always_inline)) void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int nt, int pos0,
                                 int qd, const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
                                 bool & dead) {
     const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -482,6 +482,11 @@ __device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int 
     uint16_t * vc = A.vc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
 
     // ---- stage + QK-norm + RoPE, one row per wave
+    constexpr int kVPre = 8;                 // V positions per wave fetched before the wait
+    int4 kpre0 = make_int4(0, 0, 0, 0), kpre1 = make_int4(0, 0, 0, 0);
+    uint32_t vpre[kVPre];
+#pragma unroll
+    for (int i = 0; i < kVPre; ++i) vpre[i] = 0u;
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
@@ -502,6 +507,19 @@ __device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int 
             const int pos = pos0 + (tok < nt ? tok : 0);
             rcv[tok] = rc[(size_t) pos * 64 + lane];
             rsv[tok] = rs[(size_t) pos * 64 + lane];
+        }
+        // talker: the cached K/V rows of the first positions do not depend on
+        // the new token either (they were written by earlier steps)
+        if (!cp) {
+            const int sb = lane & 15, pb = lane >> 4;
+            const int ja = wave * 4 + pb, jb = 16 + wave * 4 + pb;
+            if (ja < pos0) kpre0 = *(const int4 *) (kc + (size_t) ja * 128 + sb * 8);
+            if (jb < pos0) kpre1 = *(const int4 *) (kc + (size_t) jb * 128 + sb * 8);
+#pragma unroll
+            for (int i = 0; i < kVPre; ++i) {
+                const int j = wave + kW * i;
+                vpre[i] = j < pos0 ? *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane) : 0u;
+            }
         }
         float val[kB];
         twait_batch(ptr, 2 * nt, qkv_tag, val, dead, A.err);
@@ -562,7 +580,8 @@ __device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int 
                     for (int e = 0; e < 8; ++e) kv[e] = knew[(j - pos0) * 128 + sub * 8 + e];
                 } else {
                     const int4 k4 = cp ? *(const int4 *) &L.cpk[layer][j * 128 + sub * 8]
-                                       : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
+                                  : j0 == 0 ? kpre0 : j0 == 16 ? kpre1
+                                            : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
                     const uint16_t * kh = (const uint16_t *) &k4;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
@@ -617,23 +636,31 @@ __device__ void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int 
         // ---- P.V: lane l owns dims 2l, 2l+1 of both heads; wave w takes
         // positions j = w, w + 4, ...; no cross-lane reduction
         double o00 = 0.0, o01 = 0.0, o10 = 0.0, o11 = 0.0;
-#pragma unroll 4
-        for (int j = wave; j < n_kv; j += kW) {
+        auto pv_pos = [&](int j, uint32_t w2) {
             const double p0 = (double) L.sc[j], p1 = (double) L.sc[kMaxCtx + j];
             float v0, v1;
             if (j >= pos0) {
                 v0 = vnew[(j - pos0) * 128 + 2 * lane];
                 v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
             } else {
-                const uint32_t w2 = cp ? *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane]
-                                       : *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane);
                 v0 = h2f((uint16_t) (w2 & 0xffffu));
                 v1 = h2f((uint16_t) (w2 >> 16));
             }
             const double d0 = (double) v0, d1 = (double) v1;
             o00 = fma(p0, d0, o00); o01 = fma(p0, d1, o01);
             o10 = fma(p1, d0, o10); o11 = fma(p1, d1, o11);
+        };
+        auto v_at = [&](int j) -> uint32_t {
+            return cp ? *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane]
+                      : *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane);
+        };
+#pragma unroll
+        for (int i = 0; i < kVPre; ++i) {
+            const int j = wave + kW * i;
+            if (j < n_kv) pv_pos(j, cp || j >= pos0 ? (j < pos0 ? v_at(j) : 0u) : vpre[i]);
         }
+#pragma unroll 4
+        for (int j = wave + kW * kVPre; j < n_kv; j += kW) pv_pos(j, j < pos0 ? v_at(j) : 0u);
         L.pv[(wave * 2 + 0) * 128 + 2 * lane] = o00;
         L.pv[(wave * 2 + 0) * 128 + 2 * lane + 1] = o01;
         L.pv[(wave * 2 + 1) * 128 + 2 * lane] = o10;
@@ -686,7 +713,7 @@ __device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, u
 // or (x_lds != nullptr, layer 0) from the rows gathered into LDS.  The
 // output is tagged slot p_out.
 template <int NT, int D, int QD, int FF>
-__device__ void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int pos0, uint32_t tb, int & p,
+__device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int pos0, uint32_t tb, int & p,
                         int p_in, const float * x_lds, int & p_out, bool & dead) {
     constexpr int QKVD = 2 * QD;
     uint64_t * ar = A.arena;
@@ -771,8 +798,11 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
 
 // The argument block lives in device memory: dynamic indexing into a by-value
 // kernel argument (cp_embd[s], cp_head[s]) would copy it to private scratch.
+// One workgroup per CU, so one wave per SIMD: the full unified register file
+// (256 VGPRs + 256 AGPRs) is available to every wave.
 template <int D, int QD, int FF>
-__global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int32_t frame) {
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(const Args * __restrict__ Ap,
+                                                                                         int32_t frame) {
     const Args & A = *Ap;
     __shared__ Lds L;
     bool dead = false;
@@ -793,71 +823,64 @@ __global__ __launch_bounds__(kT) void k_frame(const Args * __restrict__ Ap, int3
     }
     if (t == 0) L.codes[0] = tok0;
 
-    // ---- code predictor: 2-token prefill [hidden; codec_embd[tok0]] + 14 steps
+    // ---- 16 passes: s = 0..14 code predictor (s = 0 is the 2-token prefill
+    // [hidden; codec_embd[tok0]], then one step per codebook), s = 15 the
+    // talker step on the summed step embedding.  One call site per layer
+    // shape keeps the inlined program small.
     int code = tok0;
-    for (int s = 0; s < 15; ++s) {
+    const int pos = st->base_pos + frame;
+    for (int s = 0; s <= 15; ++s) {
+        const bool tk = s == 15;
         const int p_x = p++;
         if (s == 0) {
             for (int i = t; i < D; i += kT) {
                 L.x[i] = A.hidden[i];
                 L.x[D + i] = h2f(A.codec_embd[(size_t) tok0 * D + i]);
             }
-        } else {
+        } else if (!tk) {
             for (int i = t; i < D; i += kT) L.x[i] = h2f(A.cp_embd[s - 1][(size_t) code * D + i]);
+        } else {
+            // emit the frame, then the step embedding (reference summation order)
+            if (blockIdx.x == 0 && t < 16) A.codes_out[(size_t) frame * 16 + t] = L.codes[t];
+            for (int i = t; i < D; i += kT) {
+                float e = h2f(A.codec_embd[(size_t) L.codes[0] * D + i]);
+                for (int g = 1; g < 16; ++g) e = e + h2f(A.cp_embd[g - 1][(size_t) L.codes[g] * D + i]);
+                const float tr = frame < A.n_trailing ? A.trailing[(size_t) frame * D + i] : A.pad[i];
+                L.x[i] = e + tr;
+            }
         }
         __syncthreads();
         const int nt = s == 0 ? 2 : 1;
-        const int pos0 = s == 0 ? 0 : s + 1;
+        const int pos0 = tk ? pos : s == 0 ? 0 : s + 1;
         publish(A, L.x, nt, D, p_x, tb);
         int p_in = p_x, p_out = p_x;
-        for (int l = 0; l < A.cp_layers; ++l) {
+        const int nl = tk ? A.n_layers : A.cp_layers;
+        const LayerQ8 * Ls = tk ? A.talker : A.cp;
+        for (int l = 0; l < nl; ++l) {
             const float * x_lds = l == 0 ? L.x : nullptr;
-            if (nt == 2) layer_t<2, D, QD, FF>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else layer_t<1, D, QD, FF>(A, L, A.cp[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            if (nt == 2) layer_t<2, D, QD, FF>(A, L, Ls[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else layer_t<1, D, QD, FF>(A, L, Ls[l], l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
             p_in = p_out;
         }
         // head on the last token's normed row
-        const int p_head = p++;
+        const int p_head = tk ? 0 : p++;
         {
             float nw[D / kT];
-            norm_prefetch<D>(A.cp_out_norm, nw);
+            norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
             float v[1][D / kT];
             load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
-            head_input<D>(v, nw, A.eps, L, nullptr);
+            head_input<D>(v, nw, A.eps, L, tk ? A.hidden : nullptr);
         }
-        f16_head<D>(A.cp_head[s], A.cp_vocab, L, A.arena + (size_t) p_head * kSlot, tb | p_head, nullptr);
-        __syncthreads();
-        code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
-        if (t == 0) L.codes[s + 1] = code;
-        __syncthreads();
+        if (tk) {
+            f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits);
+        } else {
+            f16_head<D>(A.cp_head[s], A.cp_vocab, L, A.arena + (size_t) p_head * kSlot, tb | p_head, nullptr);
+            __syncthreads();
+            code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
+            if (t == 0) L.codes[s + 1] = code;
+            __syncthreads();
+        }
     }
-    // ---- emit the frame
-    if (blockIdx.x == 0 && t < 16) A.codes_out[(size_t) frame * 16 + t] = L.codes[t];
-
-    // ---- talker step on the step embedding
-    const int p_x = p++;
-    for (int i = t; i < D; i += kT) {
-        float s = h2f(A.codec_embd[(size_t) L.codes[0] * D + i]);
-        for (int g = 1; g < 16; ++g) s = s + h2f(A.cp_embd[g - 1][(size_t) L.codes[g] * D + i]);
-        const float tr = frame < A.n_trailing ? A.trailing[(size_t) frame * D + i] : A.pad[i];
-        L.x[i] = s + tr;
-    }
-    __syncthreads();
-    publish(A, L.x, 1, D, p_x, tb);
-    const int pos = st->base_pos + frame;
-    int p_in = p_x, p_out = p_x;
-    for (int l = 0; l < A.n_layers; ++l) {
-        layer_t<1, D, QD, FF>(A, L, A.talker[l], l, false, pos, tb, p, p_in, l == 0 ? L.x : nullptr, p_out, dead);
-        p_in = p_out;
-    }
-    {
-        float nw[D / kT];
-        norm_prefetch<D>(A.out_norm, nw);
-        float v[1][D / kT];
-        load_tagged<1, D>(A.arena + (size_t) p_out * kSlot, tb | p_out, v, dead, A.err);
-        head_input<D>(v, nw, A.eps, L, A.hidden);
-    }
-    f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits);
     if (blockIdx.x == 0 && t == 0) {
         st->frame = frame;
         st->next_frame = frame + 1;
