@@ -78,7 +78,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=4)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--kernel-iters", type=int, default=200,
+                    help="launches per per-kernel timing of the multi-kernel path (0: skip)")
     ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
                     help="persistent: one cooperative kernel per frame; graph: the captured multi-kernel frame")
     args = ap.parse_args()
@@ -126,11 +127,23 @@ def main():
     kernels = {}
     names = {0: "gemv_gate_up_swiglu", 1: "gemv_qkv_rmsnorm", 2: "gemv_down_resid", 3: "gemv_wo_resid",
              4: "attention_decode"}
-    for k, nm in names.items():
-        us, b = dev.time_kernel(k, args.kernel_iters)
-        kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
+    if args.kernel_iters > 0 or path != 1:
+        for k, nm in names.items():
+            us, b = dev.time_kernel(k, max(args.kernel_iters, 20))
+            kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
+    # plain 64 MiB copy kernel: the achievable-bandwidth reference and the
+    # calibration point for the FETCH_SIZE / WRITE_SIZE counters
+    us, b = dev.time_kernel(5, 20)
+    kernels["k_copy16 (64 MiB device copy)"] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1)}
     dev.close()
+    traffic = None
     if path == 1:
+        # HBM-side bytes per k_frame dispatch from the FETCH_SIZE / WRITE_SIZE
+        # counter runs (calibrated on a 64 MiB copy kernel), when committed
+        tp = os.path.join(ROOT, "profiles", "k_frame_q8_0_06b_traffic.json")
+        if args.weights == "q8_0" and os.path.exists(tp):
+            with open(tp) as f:
+                traffic = json.load(f)["traffic_bytes_per_dispatch"]
         # the whole frame is one kernel: its roofline is the frame's algorithmic bytes over its duration
         dom_name = "k_frame (persistent cooperative frame kernel, 256 workgroups x 256 threads)"
         dom = {"avg_us": round(frame_kernel_us, 3), "bytes": fbytes, "gbs": round(fbytes / frame_kernel_us / 1e3, 1)}
@@ -170,7 +183,7 @@ def main():
         "frame_hbm_gbs": round(fbytes / (ms_per_step * 1e-3) / 1e9, 1),
         "frame_roofline_frac": round(fbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4) if dom["gbs"] else None, "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4) if dom["gbs"] else None, "traffic": traffic,
                      "kernel": dom_name},
         "kernels": kernels,
         "cpu_baseline": cpu,

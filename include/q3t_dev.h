@@ -175,8 +175,10 @@ int  q3t_dev_sync(q3t_dev * dev);
  * events on the context's stream; writes the average microseconds per
  * launch and the algorithmic bytes one launch moves.  which: 0 = talker
  * gate/up GEMV, 1 = talker QKV GEMV, 2 = talker down GEMV, 3 = talker Wo
- * GEMV, 4 = talker attention (at position min(n_ctx-1, 512)).  Resets the
- * frame-loop state.  Used by the benchmark to report roofline fractions. */
+ * GEMV, 4 = talker attention (at position min(n_ctx-1, 512)), 5 = a plain
+ * 64 MiB device-to-device copy kernel (k_copy16; the calibration point for
+ * the HBM byte counters).  Resets the frame-loop state.  Used by the
+ * benchmark to report roofline fractions. */
 int  q3t_dev_time_kernel(q3t_dev * dev, int32_t which, int32_t iters,
                          double * avg_us_out, double * bytes_out);
 

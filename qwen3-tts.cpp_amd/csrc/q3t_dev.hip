@@ -88,6 +88,7 @@ struct q3t_dev {
     int32_t * fk_err = nullptr;
     fk::Args * fk_args_dev = nullptr;
     hipEvent_t run_ev[2] = {nullptr, nullptr};
+    uint8_t * copy_buf = nullptr;      // copy-kernel calibration buffers (time_kernel class 5)
     double run_us = 0.0;
     int64_t run_frames = 0;
     int32_t host_emitted = 0;
@@ -482,6 +483,14 @@ int sync(q3t_dev * c) {
 }
 
 }  // namespace
+
+constexpr size_t kCopyBytes = (size_t) 64 << 20;
+
+// Plain 16-byte streaming copy: the reference point for the HBM byte
+// counters (FETCH_SIZE / WRITE_SIZE) of the other kernels.
+__global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, int4 * __restrict__ dst, size_t n) {
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256) dst[i] = src[i];
+}
 
 // Decides whether the persistent frame kernel can run this context and
 // prepares its tables.  Falls back to the multi-kernel graph otherwise.
@@ -1146,7 +1155,12 @@ int q3t_dev_time_kernel(q3t_dev * c, int32_t which, int32_t iters, double * avg_
     double bytes = 0.0;
     GemvSpec s{};
     const int pos = std::min(c->n_ctx - 1, 512);
-    if (which < 0 || which > 4) return fail(c, "unknown kernel class");
+    if (which < 0 || which > 5) return fail(c, "unknown kernel class");
+    if (which == 5 && !c->copy_buf) {
+        // 64 MiB source + 64 MiB destination for the copy-kernel calibration
+        if (dev_alloc(c, (void **) &c->copy_buf, (size_t) 2 * kCopyBytes)) return -1;
+        HIP_OK(hipMemsetAsync(c->copy_buf, 0, (size_t) 2 * kCopyBytes, c->stream));
+    }
     {
         FrameState st{};
         st.talker_pos = pos;
@@ -1182,6 +1196,13 @@ int q3t_dev_time_kernel(q3t_dev * c, int32_t which, int32_t iters, double * avg_
                 AttnSpec as{c->qkv, &L, c->kc, c->vc, c->n_ctx, c->rope_cos, c->rope_sin, &c->st->talker_pos, 0};
                 attention(c, as, 1);
                 bytes = 2.0 * (double) (pos + 1) * kd * 2;   // K and V rows read
+                break;
+            }
+            case 5: {
+                const size_t n16 = kCopyBytes / 16;
+                hipLaunchKernelGGL(k_copy16, dim3(4096), dim3(256), 0, c->stream, (const int4 *) c->copy_buf,
+                                   (int4 *) (c->copy_buf + kCopyBytes), n16);
+                bytes = 2.0 * (double) kCopyBytes;   // read + write
                 break;
             }
             default:
