@@ -43,6 +43,18 @@
  *     keyed by a caller seed instead of std::mt19937/discrete_distribution,
  *     which cannot be reproduced on a GPU: distributional parity only with
  *     the reference, exact parity with the HIP path.
+ *
+ * Pinning status (tests/test_oracle.py): every function here is checked
+ * against closed forms, fp64 brute force, the reference's fixture
+ * reference/det_prefill_token_types.json, known-answer vectors (Philox) or
+ * self-consistency (prefill == sequential steps).  What ggml's own CPU build
+ * would decide differently is NOT pinned, because ggml is absent (empty
+ * submodule) and the reference's det_*.bin fixtures are absent:
+ *   orc_gemv            parity unpinned vs ggml's fp32 SIMD accumulation order
+ *   orc_quantize_q8_0_act  parity unpinned vs ggml's build (formula as published)
+ *   orc_expf / softmax / SiLU  parity unpinned vs ggml's exp approximation
+ *   orc_rope_table      parity unpinned vs ggml_rope_cache_init's recurrence
+ *   orc_sample_cb0 / orc_sample_cp (temperature > 0)  distributional parity only
  */
 #ifndef Q3T_ORACLE_H
 #define Q3T_ORACLE_H
