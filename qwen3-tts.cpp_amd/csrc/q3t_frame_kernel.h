@@ -557,6 +557,67 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
     }
     __syncthreads();
 
+    if (cp) {
+        // Code predictor: at most 16 positions, all in LDS.  Wave hq (0, 1)
+        // handles query head 2g + hq alone, so no workgroup barrier follows:
+        // scores with 4 lanes per position (32 dims each, quad DPP sum),
+        // softmax with wave reductions, P.V with 2 dims per lane and each
+        // probability broadcast by readlane.
+        if (wave < 2) {
+            const int hq = wave, jq = lane >> 2, sq = lane & 3;
+            for (int tok = 0; tok < nt; ++tok) {
+                const int n_kv = pos0 + tok + 1;
+                double acc = 0.0;
+                if (jq < n_kv) {
+                    const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        float kv[8];
+                        if (jq >= pos0) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) kv[e] = knew[(jq - pos0) * 128 + sq * 32 + c * 8 + e];
+                        } else {
+                            const int4 k4 = *(const int4 *) &L.cpk[layer][jq * 128 + sq * 32 + c * 8];
+                            const uint16_t * kh = (const uint16_t *) &k4;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
+                        }
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc = fma((double) q[c * 8 + e], (double) kv[e], acc);
+                    }
+                }
+                acc += dpp_d<0xB1>(acc);
+                acc += dpp_d<0x4E>(acc);
+                const float sv = jq < n_kv ? (float) acc * A.attn_scale : -INFINITY;
+                const float mx = wave_max_f(sv);
+                const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
+                const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
+                const float inv = (float) (1.0 / sum);
+                const float pr = round_f16(ev * inv);
+                double o0 = 0.0, o1 = 0.0;
+                for (int j = 0; j < n_kv; ++j) {
+                    const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
+                    float v0, v1;
+                    if (j >= pos0) {
+                        v0 = vnew[(j - pos0) * 128 + 2 * lane];
+                        v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
+                    } else {
+                        const uint32_t w2 = *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane];
+                        v0 = h2f((uint16_t) (w2 & 0xffffu));
+                        v1 = h2f((uint16_t) (w2 >> 16));
+                    }
+                    o0 = fma(pj, (double) v0, o0);
+                    o1 = fma(pj, (double) v1, o1);
+                }
+                uint64_t * dst = out + (size_t) tok * kHS + (g * 2 + hq) * 128 + 2 * lane;
+                tstore(dst, out_tag, (float) o0);
+                tstore(dst + 1, out_tag, (float) o1);
+            }
+        }
+        __syncthreads();
+        return;
+    }
+
     const int sub = lane & 15, pw = lane >> 4;   // dims [sub*8, sub*8+8) of position j0 + wave*4 + pw
     for (int tok = 0; tok < nt; ++tok) {
         const int n_kv = pos0 + tok + 1;
