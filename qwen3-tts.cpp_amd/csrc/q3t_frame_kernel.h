@@ -279,13 +279,21 @@ struct Q8Regs {
     int ng;               // groups this wave owns (0..2)
 };
 
+// Row-group owner of wave gw when a phase's groups start at wave `rot`
+// (phases that follow a phase with uneven work start where the idle waves are).
+__device__ __forceinline__ int rot_wave(int rot) {
+    const int nw = gridDim.x * kW;
+    const int gw = blockIdx.x * kW + (threadIdx.x >> 6) + nw - rot;
+    return gw >= nw ? gw - nw : gw;
+}
+
 template <int K, bool DUAL>
 __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * W, const uint16_t * Wd,
-                                            const int8_t * U, const uint16_t * Ud, int rows) {
+                                            const int8_t * U, const uint16_t * Ud, int rows, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int groups = rows / G::RPW;
-    const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
     R.ng = 0;
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -311,10 +319,10 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * 
 // Issues the residual loads of the rows this lane will store (EPI_RESID),
 // before the phase input is awaited; q8_compute re-polls any not yet tagged.
 template <int NT, int K, bool DUAL>
-__device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL> & R, const uint64_t * res) {
+__device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL> & R, const uint64_t * res, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
-    const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
     if (lir != 0) return;
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -325,21 +333,27 @@ __device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL> & R, const uint64_t
     }
 }
 
+// Whether any wave of this workgroup owns a row group.  rot is a multiple of
+// kW, so a workgroup's waves stay consecutive in the rotated order and the
+// first one owns a group whenever any does.
 template <int K>
-__device__ __forceinline__ bool wg_has_rows(int rows) {
-    return (int) blockIdx.x * kW < rows / Geo<K>::RPW;
+__device__ __forceinline__ bool wg_has_rows(int rows, int rot) {
+    const int nw = gridDim.x * kW;
+    int first = (int) blockIdx.x * kW + nw - rot;
+    if (first >= nw) first -= nw;
+    return first < rows / Geo<K>::RPW;
 }
 
 // Q8_0 GEMV over the quantised LDS input, epilogue, tagged stores into
 // out [NT][kHS].  res: residual slot (tagged) for EPI_RESID.
 template <int NT, int K, bool DUAL>
 __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
-                                           uint32_t res_tag, uint64_t * out, uint32_t out_tag, bool & dead,
+                                           uint32_t res_tag, uint64_t * out, uint32_t out_tag, int rot, bool & dead,
                                            int32_t * err) {
     using G = Geo<K>;
     if (R.ng == 0) return;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
-    const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
     double acc[2][NT], acc2[2][NT];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi)
@@ -778,11 +792,15 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
                         int p_in, const float * x_lds, int & p_out, bool & dead) {
     constexpr int QKVD = 2 * QD;
     uint64_t * ar = A.arena;
+    // Wo and down have fewer row groups than waves: they start at the second
+    // half of the waves, away from the attention workgroups (0..n_kv_head-1)
+    // and from the waves that carry two gate/up groups (the first ones)
+    const int rot = (int) (gridDim.x / 2) * kW;
     // QKV (RMSNorm'd input)
     const int p_qkv = p++;
-    if (wg_has_rows<D>(QKVD)) {
+    if (wg_has_rows<D>(QKVD, 0)) {
         Q8Regs<D, false> R;
-        q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD);
+        q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
         float nw[D / kT];
         norm_prefetch<D>(W.attn_norm, nw);
         float v[NT][D / kT];
@@ -796,7 +814,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         }
         rms_rows<NT, D>(v, nw, A.eps, L);
         quant_rows<NT, D>(v, L);
-        q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, dead, A.err);
+        q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead, A.err);
     }
     __syncthreads();
     // attention (workgroup g < n_kv_head owns KV head g)
@@ -807,42 +825,42 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     __syncthreads();
     // Wo + residual (the block input)
     const int p_wo = p++;
-    if (wg_has_rows<QD>(D)) {
+    if (wg_has_rows<QD>(D, rot)) {
         Q8Regs<QD, false> R;
-        q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D);
-        res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot);
+        q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
+        res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
         float v[NT][QD / kT];
         load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
         quant_rows<NT, QD>(v, L);
         q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in, ar + (size_t) p_wo * kSlot,
-                                  tb | p_wo, dead, A.err);
+                                  tb | p_wo, rot, dead, A.err);
     }
     __syncthreads();
     // gate/up + SwiGLU (RMSNorm'd)
     const int p_gu = p++;
-    if (wg_has_rows<D>(FF)) {
+    if (wg_has_rows<D>(FF, 0)) {
         Q8Regs<D, true> R;
-        q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF);
+        q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
         float nw[D / kT];
         norm_prefetch<D>(W.ffn_norm, nw);
         float v[NT][D / kT];
         load_tagged<NT, D>(ar + (size_t) p_wo * kSlot, tb | p_wo, v, dead, A.err);
         rms_rows<NT, D>(v, nw, A.eps, L);
         quant_rows<NT, D>(v, L);
-        q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, dead, A.err);
+        q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0, dead, A.err);
     }
     __syncthreads();
     // down + residual
     const int p_dn = p++;
-    if (wg_has_rows<FF>(D)) {
+    if (wg_has_rows<FF>(D, rot)) {
         Q8Regs<FF, false> R;
-        q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D);
-        res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot);
+        q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
+        res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
         float v[NT][FF / kT];
         load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
         quant_rows<NT, FF>(v, L);
         q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo, ar + (size_t) p_dn * kSlot,
-                                  tb | p_dn, dead, A.err);
+                                  tb | p_dn, rot, dead, A.err);
     }
     __syncthreads();
     p_out = p_dn;
