@@ -87,6 +87,7 @@ struct q3t_dev {
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
     int32_t * fk_err = nullptr;
     fk::Args * fk_args_dev = nullptr;
+    float * fk_cand = nullptr;         // talker-head greedy candidates: 256 values then 256 indices
     hipEvent_t run_ev[2] = {nullptr, nullptr};
     uint8_t * copy_buf = nullptr;      // copy-kernel calibration buffers (time_kernel class 5)
     double run_us = 0.0;
@@ -564,6 +565,7 @@ int fk_prepare(q3t_dev * c) {
     }
     if (!c->fk_err && dev_alloc_t(c, &c->fk_err, 1)) return -1;
     if (!c->fk_args_dev && dev_alloc_t(c, &c->fk_args_dev, 1)) return -1;
+    if (!c->fk_cand && dev_alloc_t(c, &c->fk_cand, 2 * 256)) return -1;
     c->fk_grid = grid;
     c->fk_variant = variant;
     c->fk_ok = true;
@@ -592,6 +594,8 @@ fk::Args fk_args(q3t_dev * c) {
     A.st = c->st; A.params = c->params; A.seen = c->seen; A.codes_out = c->codes_out;
     A.trailing = c->trailing; A.n_trailing = c->n_trailing; A.pad = c->pad;
     A.err = c->fk_err;
+    A.cand_val = c->fk_cand;
+    A.cand_idx = (int32_t *) (c->fk_cand + 256);
     return A;
 }
 

@@ -71,6 +71,7 @@ struct Args {
     FrameState * st; const SampleParams * params; uint8_t * seen; int32_t * codes_out;
     const float * trailing; int32_t n_trailing; const float * pad;
     int32_t * err;
+    float * cand_val; int32_t * cand_idx;    // talker-head greedy candidates, one per workgroup
 };
 
 // Geometry of a Q8_0 GEMV with input width K: each row is split over LPR
@@ -99,6 +100,7 @@ struct Lds {
     alignas(16) uint16_t cpv[kCpLayers][16 * 128];
     double red[2 * kW];
     float fred[2 * kW];
+    int32_t ired[kW];
     int32_t codes[16];
     SampleScratch<kT> S;
 };
@@ -423,16 +425,29 @@ __device__ __forceinline__ void head_input(float (&v)[1][K / kT], const float (&
     __syncthreads();
 }
 
+// Codebook-0 logit transforms of the talker sampler (suppression window,
+// repetition penalty over the tokens seen so far plus this frame's, EOS
+// bias), applied by the head for the next frame's greedy candidate.
+struct Cb0Xf {
+    int V, eos, tok0;
+    float rep, eff;
+    const uint8_t * seen;
+};
+
 // F16 GEMV (one 32-element block per lane), outputs tagged (code predictor)
-// or plain (talker logits).
+// or plain (talker logits).  Every workgroup also publishes its greedy
+// candidate: the first maximum over its rows (after the codebook-0
+// transforms when xf != nullptr), tagged at cand_tagged[2b], [2b+1] or plain
+// in cand_val[b] / cand_idx[b].  All threads of the workgroup must call it.
 template <int K>
-__device__ __forceinline__ void f16_head(const uint16_t * W, int rows, const Lds & L, uint64_t * out_tagged,
-                                         uint32_t tag, float * out_plain) {
+__device__ __forceinline__ void f16_head(const uint16_t * W, int rows, Lds & L, uint64_t * out_tagged,
+                                         uint32_t tag, float * out_plain, const Cb0Xf * xf, uint64_t * cand_tagged,
+                                         float * cand_val, int32_t * cand_idx) {
     static_assert(K / kQK <= 32 && ((K / kQK) & (K / kQK - 1)) == 0, "head width");
     constexpr int LPR = K / kQK, RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR;
+    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
     const int groups = rows / RPW;
-    const int gw = blockIdx.x * kW + (threadIdx.x >> 6), nw = gridDim.x * kW;
+    const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;
     int4 w[2][4];
     int ng = 0;
 #pragma unroll
@@ -444,31 +459,72 @@ __device__ __forceinline__ void f16_head(const uint16_t * W, int rows, const Lds
 #pragma unroll
         for (int c = 0; c < 4; ++c) w[gi][c] = wp[c];
     }
-    if (ng == 0) return;
-    double acc[2] = {0.0, 0.0};
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (ng > 0) {
+        double acc[2] = {0.0, 0.0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int4 x4 = *(const int4 *) &L.hq[c][lir * 8];
-        const uint16_t * xh = (const uint16_t *) &x4;
+        for (int c = 0; c < 4; ++c) {
+            const int4 x4 = *(const int4 *) &L.hq[c][lir * 8];
+            const uint16_t * xh = (const uint16_t *) &x4;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const double xd = (double) h2f(xh[j]);
+            for (int j = 0; j < 8; ++j) {
+                const double xd = (double) h2f(xh[j]);
 #pragma unroll
-            for (int gi = 0; gi < 2; ++gi) {
-                const uint16_t * wh = (const uint16_t *) &w[gi][c];
-                acc[gi] = fma((double) h2f(wh[j]), xd, acc[gi]);   // fp16 x fp16: exact product
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint16_t * wh = (const uint16_t *) &w[gi][c];
+                    acc[gi] = fma((double) h2f(wh[j]), xd, acc[gi]);   // fp16 x fp16: exact product
+                }
             }
         }
-    }
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-        if (gi >= ng) break;
-        const double a = group_sum_d(acc[gi], LPR);
-        if (lir != 0) continue;
-        const int r = (gw + gi * nw) * RPW + rsub;
-        if (out_tagged) tstore(out_tagged + r, tag, (float) a);
-        else out_plain[r] = (float) a;
+        for (int gi = 0; gi < 2; ++gi) {
+            if (gi >= ng) break;
+            const double a = group_sum_d(acc[gi], LPR);
+            if (lir != 0) continue;
+            const int r = (gw + gi * nw) * RPW + rsub;
+            if (out_tagged) tstore(out_tagged + r, tag, (float) a);
+            else out_plain[r] = (float) a;
+            float v = (float) a;
+            if (xf) {
+                if (r >= xf->V - 1024 && r != xf->eos) v = -INFINITY;
+                if (xf->rep != 1.0f && (xf->seen[r] || r == xf->tok0)) v = v > 0.0f ? v / xf->rep : v * xf->rep;
+                if (r == xf->eos && xf->eff != 0.0f) v = v + xf->eff;
+            }
+            if (v > bv || (v == bv && r < bi)) { bv = v; bi = r; }
+        }
     }
+    wave_argmax(bv, bi);
+    if (lane == 0) { L.fred[wave] = bv; L.ired[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = L.fred[0];
+        int i = L.ired[0];
+#pragma unroll
+        for (int w2 = 1; w2 < kW; ++w2) argmax_step(v, i, L.fred[w2], L.ired[w2]);
+        if (cand_tagged) {
+            tstore(cand_tagged + 2 * blockIdx.x, tag, v);
+            tstore(cand_tagged + 2 * blockIdx.x + 1, tag, __int_as_float(i));
+        } else {
+            cand_val[blockIdx.x] = v;
+            cand_idx[blockIdx.x] = i;
+        }
+    }
+}
+
+// First-index argmax over the workgroups' candidates (values v, indices i
+// held by threads t < gridDim.x).
+__device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
+    wave_argmax(v, i);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { L.fred[wave] = v; L.ired[wave] = i; }
+    __syncthreads();
+    float bv = L.fred[0];
+    int bi = L.ired[0];
+#pragma unroll
+    for (int w2 = 1; w2 < kW; ++w2) argmax_step(bv, bi, L.fred[w2], L.ired[w2]);
+    __syncthreads();
+    return bi;
 }
 
 // -------------------------------------------------------------- attention
@@ -758,6 +814,13 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
 __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
     const SampleParams & P = *A.params;
     const int V = A.codec_vocab;
+    if (P.temperature <= 0.0f && frame > 0) {
+        // greedy: the previous frame's talker head left one transformed
+        // candidate per workgroup
+        const int t = threadIdx.x;
+        const bool in = t < (int) gridDim.x;
+        return reduce_candidates(in ? A.cand_val[t] : -INFINITY, in ? A.cand_idx[t] : 0x7fffffff, L);
+    }
     for (int i = threadIdx.x; i < V; i += kT) {
         float v = A.logits[i];
         if (i >= V - 1024 && i != A.eos_id) v = -INFINITY;
@@ -777,6 +840,23 @@ __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
 __device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, uint32_t tag, int frame, int group,
                              bool & dead) {
     const SampleParams & P = *A.params;
+    if (P.temperature <= 0.0f) {
+        // greedy: one (value, index) candidate per head workgroup, tagged
+        // after the logits in the head slot
+        const int t = threadIdx.x;
+        float v = -INFINITY;
+        int i = 0x7fffffff;
+        if (t < (int) gridDim.x) {
+            const uint64_t * ptr[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) ptr[k] = logits + kHS + 2 * t + (k & 1);
+            float val[kB];
+            twait_batch(ptr, 2, tag, val, dead, A.err);
+            v = val[0];
+            i = __float_as_int(val[1]);
+        }
+        return reduce_candidates(v, i, L);
+    }
     stage_plain(logits, A.cp_vocab, tag, L.x, dead, A.err);
     return sample_core<kT>(L.x, A.cp_vocab, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame,
                            (uint32_t) group, L.S);
@@ -951,9 +1031,16 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             head_input<D>(v, nw, A.eps, L, tk ? A.hidden : nullptr);
         }
         if (tk) {
-            f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits);
+            const SampleParams & P = *A.params;
+            Cb0Xf xf{A.codec_vocab, A.eos_id, L.codes[0], P.rep_penalty, P.eos_bias, A.seen};
+            if (P.target_frames > 0 && frame + 1 > P.target_frames) {   // the next frame's EOS-bias ramp
+                xf.eff += 0.1f * (float) (frame + 1 - P.target_frames);
+                if (xf.eff > 6.0f) xf.eff = 6.0f;
+            }
+            f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits, &xf, nullptr, A.cand_val, A.cand_idx);
         } else {
-            f16_head<D>(A.cp_head[s], A.cp_vocab, L, A.arena + (size_t) p_head * kSlot, tb | p_head, nullptr);
+            uint64_t * hs = A.arena + (size_t) p_head * kSlot;
+            f16_head<D>(A.cp_head[s], A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
             __syncthreads();
             code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
             if (t == 0) L.codes[s + 1] = code;
