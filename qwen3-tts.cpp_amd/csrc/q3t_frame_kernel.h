@@ -82,10 +82,19 @@ struct Geo {
     static constexpr int SLOTS = BPR > 32 ? BPR / 32 : 1;
     static constexpr int LPR = BPR / SLOTS;
     static constexpr int RPW = 64 / LPR;
-    static constexpr int CH = K / kT;          // input elements per thread per token
-    static_assert(K % kT == 0 && BPR % SLOTS == 0 && (LPR & (LPR - 1)) == 0 && LPR >= 4 && LPR <= 32,
+    static constexpr int G4 = K / 4;                   // groups of 4 consecutive input elements
+    static constexpr int CHG = (G4 + kT - 1) / kT;     // groups per thread per token
+    static_assert(BPR % SLOTS == 0 && (LPR & (LPR - 1)) == 0 && LPR >= 4 && LPR <= 32 && G4 % 64 == 0,
                   "unsupported GEMV width");
 };
+
+// Thread t's share of NT input rows of width K: groups g = t + c * kT of 4
+// consecutive elements (4g .. 4g+3); 8 consecutive threads cover one Q8_0
+// block.  Groups with g >= K/4 belong to whole idle waves (K/4 % 64 == 0).
+template <int NT, int K>
+using RowsT = float[NT][Geo<K>::CHG][4];
+template <int K>
+using NormT = float[Geo<K>::CHG][4];
 
 struct Lds {
     alignas(16) float x[3072];                  // gathered layer-0 rows [nt][D] / sampler logits
@@ -127,46 +136,72 @@ __device__ __forceinline__ float twait(const uint64_t * p, uint32_t tag, bool & 
 // any tag is checked, and a re-poll reloads only the elements still missing,
 // so a thread pays about one round trip per batch instead of one per element.
 constexpr int kB = 8;
-__device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[kB], int cnt, uint32_t tag, float (&out)[kB],
+template <int N>
+__device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[N], int cnt, uint32_t tag, float (&out)[N],
                                             bool & dead, int32_t * err) {
-    uint64_t v[kB];
+    uint64_t v[N];
     unsigned n = 0;
 #pragma unroll
-    for (int k = 0; k < kB; ++k) v[k] = k < cnt ? tload(ptr[k]) : ((uint64_t) tag << 32);
+    for (int k = 0; k < N; ++k) v[k] = k < cnt ? tload(ptr[k]) : ((uint64_t) tag << 32);
     while (!dead) {
         bool all = true;
 #pragma unroll
-        for (int k = 0; k < kB; ++k) all = all && (uint32_t) (v[k] >> 32) == tag;
+        for (int k = 0; k < N; ++k) all = all && (uint32_t) (v[k] >> 32) == tag;
         if (all) break;
         if (++n > kSpin) { dead = true; atomicExch(err, 1); break; }
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int k = 0; k < kB; ++k)
+        for (int k = 0; k < N; ++k)
             if ((uint32_t) (v[k] >> 32) != tag) v[k] = tload(ptr[k]);
     }
 #pragma unroll
-    for (int k = 0; k < kB; ++k) out[k] = __uint_as_float((uint32_t) v[k]);
+    for (int k = 0; k < N; ++k) out[k] = __uint_as_float((uint32_t) v[k]);
 }
 
-// Thread t's elements of rows [NT][K] of a tagged slot: v[tok][c] = row
-// element c * kT + t.
+// Thread t's groups of rows [NT][K] of a tagged slot (row stride kHS), in
+// batches of up to 12 loads ordered group-major, so the valid loads of a
+// thread always form a prefix of each batch.
 template <int NT, int K>
-__device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag, float (&v)[NT][K / kT], bool & dead,
+__device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag, RowsT<NT, K> & v, bool & dead,
                                             int32_t * err) {
-    constexpr int CH = K / kT, F = NT * CH;
+    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4, F = CHG * NT * 4;
+    constexpr int NB = F <= 12 ? F : (F % 12 == 0 ? 12 : 8);
+    static_assert(F % NB == 0, "batch split");
 #pragma unroll
-    for (int f0 = 0; f0 < F; f0 += kB) {
-        const uint64_t * ptr[kB];
+    for (int f0 = 0; f0 < F; f0 += NB) {
+        const uint64_t * ptr[NB];
+        int cnt = 0;
 #pragma unroll
-        for (int k = 0; k < kB; ++k) {
-            const int f = f0 + k < F ? f0 + k : 0;
-            ptr[k] = slot + (size_t) (f / CH) * kHS + (f % CH) * kT + threadIdx.x;
+        for (int k = 0; k < NB; ++k) {
+            const int f = f0 + k, c = f / (NT * 4), tok = (f / 4) % NT, e = f % 4;
+            const int g = (int) threadIdx.x + kT * c;
+            const bool ok = g < G4;
+            ptr[k] = slot + (size_t) tok * kHS + (ok ? 4 * g + e : 0);
+            if (ok) cnt = k + 1;
         }
-        float val[kB];
-        twait_batch(ptr, F - f0 < kB ? F - f0 : kB, tag, val, dead, err);
+        float val[NB];
+        twait_batch<NB>(ptr, cnt, tag, val, dead, err);
 #pragma unroll
-        for (int k = 0; k < kB; ++k)
-            if (f0 + k < F) v[(f0 + k) / CH][(f0 + k) % CH] = val[k];
+        for (int k = 0; k < NB; ++k) {
+            const int f = f0 + k, c = f / (NT * 4), tok = (f / 4) % NT, e = f % 4;
+            v[tok][c][e] = val[k];
+        }
+    }
+}
+
+// The same groups from plain LDS rows x [NT][K].
+template <int NT, int K>
+__device__ __forceinline__ void load_lds(const float * x, RowsT<NT, K> & v) {
+    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4;
+#pragma unroll
+    for (int c = 0; c < CHG; ++c) {
+        const int g = (int) threadIdx.x + kT * c;
+        if (g >= G4) break;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 q = *(const float4 *) (x + t * K + 4 * g);
+            v[t][c][0] = q.x; v[t][c][1] = q.y; v[t][c][2] = q.z; v[t][c][3] = q.w;
+        }
     }
 }
 
@@ -183,7 +218,7 @@ __device__ __forceinline__ void stage_plain(const uint64_t * slot, int n, uint32
             if (i < n) cnt = k + 1;
         }
         float val[kB];
-        twait_batch(ptr, cnt, tag, val, dead, err);
+        twait_batch<kB>(ptr, cnt, tag, val, dead, err);
 #pragma unroll
         for (int k = 0; k < kB; ++k) {
             const int i = i0 + k * kT + (int) threadIdx.x;
@@ -194,37 +229,39 @@ __device__ __forceinline__ void stage_plain(const uint64_t * slot, int n, uint32
 }
 
 // ------------------------------------------------------ cross-lane helpers
-// max over each aligned 32-lane half of the wave (same DPP pattern as group_sum_d)
-__device__ __forceinline__ float max32_f(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    v = fmaxf(v, dpp_f<0x140>(v));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
-    return v;
-}
 
 // ------------------------------------------------------- input preparation
 // RMSNorm of thread-distributed rows v[NT][K/kT]: y = (x * scale) * w with
 // scale = 1/sqrt(mean(fl(x*x)) + eps), the sum of squares accumulated in
 // fp64.  Every thread ends with its normed elements.
-// The norm weights this thread needs (w[c * kT + t]), loaded before the
-// phase input is awaited.
+// The norm weights of this thread's groups, loaded before the phase input
+// is awaited.
 template <int K>
-__device__ __forceinline__ void norm_prefetch(const float * w, float (&nw)[K / kT]) {
+__device__ __forceinline__ void norm_prefetch(const float * w, NormT<K> & nw) {
 #pragma unroll
-    for (int c = 0; c < K / kT; ++c) nw[c] = w[c * kT + threadIdx.x];
+    for (int c = 0; c < Geo<K>::CHG; ++c) {
+        const int g = (int) threadIdx.x + kT * c;
+        if (g >= Geo<K>::G4) break;
+        const float4 q = *(const float4 *) (w + 4 * g);
+        nw[c][0] = q.x; nw[c][1] = q.y; nw[c][2] = q.z; nw[c][3] = q.w;
+    }
 }
 
+// RMSNorm of thread-distributed rows: y = (x * scale) * w with scale =
+// 1/sqrt(mean(fl(x*x)) + eps), the sum of squares accumulated in fp64.
+// Every thread ends with its normed elements.
 template <int NT, int K>
-__device__ __forceinline__ void rms_rows(float (&v)[NT][K / kT], const float (&nw)[K / kT], float eps, Lds & L) {
-    constexpr int CH = K / kT;
+__device__ __forceinline__ void rms_rows(RowsT<NT, K> & v, const NormT<K> & nw, float eps, Lds & L) {
+    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         double ss = 0.0;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) ss += (double) (v[t][c] * v[t][c]);
+        for (int c = 0; c < CHG; ++c)
+            if ((int) threadIdx.x + kT * c < G4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss += (double) (v[t][c][e] * v[t][c][e]);
         ss = wave_sum_d(ss);
         if (lane == 0) L.red[t * kW + wave] = ss;
     }
@@ -237,35 +274,44 @@ __device__ __forceinline__ void rms_rows(float (&v)[NT][K / kT], const float (&n
         const float mean = (float) (tot / (double) K);
         const float scale = 1.0f / sqrtf(mean + eps);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const float y = v[t][c] * scale;
-            v[t][c] = y * nw[c];
-        }
+        for (int c = 0; c < CHG; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float y = v[t][c][e] * scale;
+                v[t][c][e] = y * nw[c][e];
+            }
     }
 }
 
 // Q8_0 activation quantisation (ggml-cpu x86 quantize_row_q8_0: d =
 // amax/127 stored as fp16, q = round-to-nearest-even(x * 127/amax)) of
-// thread-distributed rows into LDS.  A 32-element block is 32 consecutive
-// threads, so its amax is a 32-lane reduction.
+// thread-distributed rows into LDS.  A block is 8 consecutive threads of 4
+// elements, so its amax is a 3-step DPP reduction and the two divisions are
+// shared by 4 elements.
 template <int NT, int K>
-__device__ __forceinline__ void quant_rows(const float (&v)[NT][K / kT], Lds & L) {
-    constexpr int CH = K / kT, BPR = K / kQK;
-    const int t = threadIdx.x, e = t & 31;
+__device__ __forceinline__ void quant_rows(const RowsT<NT, K> & v, Lds & L) {
+    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4, BPR = K / kQK;
 #pragma unroll
-    for (int tok = 0; tok < NT; ++tok)
+    for (int c = 0; c < CHG; ++c) {
+        const int g = (int) threadIdx.x + kT * c;
+        if (g >= G4) break;                 // whole waves (G4 % 64 == 0)
+        const int b = g >> 3, eo = (g & 7) * 4;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const float x = v[tok][c];
-            const float am = max32_f(fabsf(x));
+        for (int tok = 0; tok < NT; ++tok) {
+            float am = fmaxf(fmaxf(fabsf(v[tok][c][0]), fabsf(v[tok][c][1])), fmaxf(fabsf(v[tok][c][2]), fabsf(v[tok][c][3])));
+            am = fmaxf(am, dpp_f<0xB1>(am));
+            am = fmaxf(am, dpp_f<0x4E>(am));
+            am = fmaxf(am, dpp_f<0x141>(am));
             const float d = am / 127.0f;
             const float id = am != 0.0f ? 127.0f / am : 0.0f;
-            const int q = (int) rintf(x * id);
-            const int b = (c * kT + t) >> 5;
-            int8_t * dst = e < 16 ? L.qlo : L.qhi;
-            dst[(tok * BPR + b) * 16 + (e & 15)] = (int8_t) q;
-            if (e == 0) L.qdx[tok * BPR + b] = round_f16(d);
+            int packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) packed |= ((int) rintf(v[tok][c][e] * id) & 0xff) << (8 * e);
+            int8_t * dst = eo < 16 ? L.qlo : L.qhi;
+            *(int *) &dst[(tok * BPR + b) * 16 + (eo & 15)] = packed;
+            if ((g & 7) == 0) L.qdx[tok * BPR + b] = round_f16(d);
         }
+    }
     __syncthreads();
 }
 
@@ -412,15 +458,18 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
 // activation contract); workgroup 0 also writes the normed fp32 row to
 // hidden_out when given.
 template <int K>
-__device__ __forceinline__ void head_input(float (&v)[1][K / kT], const float (&nw)[K / kT], float eps, Lds & L,
+__device__ __forceinline__ void head_input(RowsT<1, K> & v, const NormT<K> & nw, float eps, Lds & L,
                                            float * hidden_out) {
-    constexpr int CH = K / kT;
     rms_rows<1, K>(v, nw, eps, L);
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int i = c * kT + threadIdx.x, b = i >> 5, e = i & 31;
-        if (hidden_out && blockIdx.x == 0) hidden_out[i] = v[0][c];
-        L.hq[e >> 3][b * 8 + (e & 7)] = f2h(v[0][c]);
+    for (int c = 0; c < Geo<K>::CHG; ++c) {
+        const int g = (int) threadIdx.x + kT * c;
+        if (g >= Geo<K>::G4) break;
+        const int b = g >> 3, e32 = (g & 7) * 4;
+        if (hidden_out && blockIdx.x == 0)
+            *(float4 *) (hidden_out + 4 * g) = make_float4(v[0][c][0], v[0][c][1], v[0][c][2], v[0][c][3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) L.hq[(e32 + e) >> 3][b * 8 + ((e32 + e) & 7)] = f2h(v[0][c][e]);
     }
     __syncthreads();
 }
@@ -592,7 +641,7 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
             }
         }
         float val[kB];
-        twait_batch(ptr, 2 * nt, qkv_tag, val, dead, A.err);
+        twait_batch<kB>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
         for (int tok = 0; tok < nt; ++tok) {
             const int pos = pos0 + tok;
             const float x0 = val[2 * tok], x1 = val[2 * tok + 1];
@@ -851,7 +900,7 @@ __device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, u
 #pragma unroll
             for (int k = 0; k < kB; ++k) ptr[k] = logits + kHS + 2 * t + (k & 1);
             float val[kB];
-            twait_batch(ptr, 2, tag, val, dead, A.err);
+            twait_batch<kB>(ptr, 2, tag, val, dead, A.err);
             v = val[0];
             i = __float_as_int(val[1]);
         }
@@ -881,14 +930,11 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (wg_has_rows<D>(QKVD, 0)) {
         Q8Regs<D, false> R;
         q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
-        float nw[D / kT];
+        NormT<D> nw;
         norm_prefetch<D>(W.attn_norm, nw);
-        float v[NT][D / kT];
+        RowsT<NT, D> v;
         if (x_lds) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int c = 0; c < D / kT; ++c) v[t][c] = x_lds[t * D + c * kT + threadIdx.x];
+            load_lds<NT, D>(x_lds, v);
         } else {
             load_tagged<NT, D>(ar + (size_t) p_in * kSlot, tb | p_in, v, dead, A.err);
         }
@@ -909,7 +955,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         Q8Regs<QD, false> R;
         q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
         res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
-        float v[NT][QD / kT];
+        RowsT<NT, QD> v;
         load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
         quant_rows<NT, QD>(v, L);
         q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in, ar + (size_t) p_wo * kSlot,
@@ -921,9 +967,9 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (wg_has_rows<D>(FF, 0)) {
         Q8Regs<D, true> R;
         q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
-        float nw[D / kT];
+        NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
-        float v[NT][D / kT];
+        RowsT<NT, D> v;
         load_tagged<NT, D>(ar + (size_t) p_wo * kSlot, tb | p_wo, v, dead, A.err);
         rms_rows<NT, D>(v, nw, A.eps, L);
         quant_rows<NT, D>(v, L);
@@ -936,7 +982,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         Q8Regs<FF, false> R;
         q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
         res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
-        float v[NT][FF / kT];
+        RowsT<NT, FF> v;
         load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
         quant_rows<NT, FF>(v, L);
         q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo, ar + (size_t) p_dn * kSlot,
@@ -1024,9 +1070,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         // head on the last token's normed row
         const int p_head = tk ? 0 : p++;
         {
-            float nw[D / kT];
+            NormT<D> nw;
             norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
-            float v[1][D / kT];
+            RowsT<1, D> v;
             load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
             head_input<D>(v, nw, A.eps, L, tk ? A.hidden : nullptr);
         }
