@@ -103,8 +103,7 @@ struct Lds {
     float qdx[2 * kMaxBlk];                     // fp16-rounded block scales
     alignas(16) uint16_t hq[4][32 * 8];         // F16 head input: halves 8c..8c+7 of block b at hq[c][b*8]
     float a[2 * 4 * 128];                       // attention: q (2 tok x 2 heads), new k, new v rows
-    float sc[2 * kMaxCtx];                      // attention scores / probabilities, 2 heads
-    double pv[kW * 2 * 128];                    // attention P.V partials [wave][head][dim]
+    alignas(16) float sc[2 * kMaxCtx];          // attention scores / probabilities, 2 heads; P.V partials
     alignas(16) uint16_t cpk[kCpLayers][16 * 128];   // code-predictor KV of this workgroup's KV head
     alignas(16) uint16_t cpv[kCpLayers][16 * 128];
     double red[2 * kW];
@@ -601,11 +600,10 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
     uint16_t * vc = A.vc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
 
     // ---- stage + QK-norm + RoPE, one row per wave
-    constexpr int kVPre = 8;                 // V positions per wave fetched before the wait
+    // talker K/V rows of the first two position blocks (16 lanes x 16 bytes
+    // per position), fetched before the QKV wait
     int4 kpre0 = make_int4(0, 0, 0, 0), kpre1 = make_int4(0, 0, 0, 0);
-    uint32_t vpre[kVPre];
-#pragma unroll
-    for (int i = 0; i < kVPre; ++i) vpre[i] = 0u;
+    int4 vpre0 = make_int4(0, 0, 0, 0), vpre1 = make_int4(0, 0, 0, 0);
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
@@ -632,12 +630,13 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
         if (!cp) {
             const int sb = lane & 15, pb = lane >> 4;
             const int ja = wave * 4 + pb, jb = 16 + wave * 4 + pb;
-            if (ja < pos0) kpre0 = *(const int4 *) (kc + (size_t) ja * 128 + sb * 8);
-            if (jb < pos0) kpre1 = *(const int4 *) (kc + (size_t) jb * 128 + sb * 8);
-#pragma unroll
-            for (int i = 0; i < kVPre; ++i) {
-                const int j = wave + kW * i;
-                vpre[i] = j < pos0 ? *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane) : 0u;
+            if (ja < pos0) {
+                kpre0 = *(const int4 *) (kc + (size_t) ja * 128 + sb * 8);
+                vpre0 = *(const int4 *) (vc + (size_t) ja * 128 + sb * 8);
+            }
+            if (jb < pos0) {
+                kpre1 = *(const int4 *) (kc + (size_t) jb * 128 + sb * 8);
+                vpre1 = *(const int4 *) (vc + (size_t) jb * 128 + sb * 8);
             }
         }
         float val[kB];
@@ -737,9 +736,14 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
         return;
     }
 
-    const int sub = lane & 15, pw = lane >> 4;   // dims [sub*8, sub*8+8) of position j0 + wave*4 + pw
+    // Talker: 16 lanes per position (8 dims = 16 bytes each), 4 positions per
+    // wave and 16 per workgroup per block; K and V rows are loaded in chunks
+    // of 8 blocks issued before any is used.
+    const int sub = lane & 15, pw = lane >> 4;
+    constexpr int kCh = 8;
     for (int tok = 0; tok < nt; ++tok) {
         const int n_kv = pos0 + tok + 1;
+        const int nblk = (n_kv + 4 * kW - 1) / (4 * kW);
         double q0[8], q1[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -748,41 +752,44 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
         }
         // ---- scores
         float lm0 = -INFINITY, lm1 = -INFINITY;
-#pragma unroll 2
-        for (int j0 = 0; j0 < n_kv; j0 += 4 * kW) {
-            const int j = j0 + wave * 4 + pw;
-            float kv[8];
+        for (int i0 = 0; i0 < nblk; i0 += kCh) {
+            int4 kk[kCh];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kv[e] = 0.0f;
-            if (j < n_kv) {
-                if (j >= pos0) {
+            for (int u = 0; u < kCh; ++u) {
+                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
+                kk[u] = make_int4(0, 0, 0, 0);
+                if (i < nblk && j < pos0)
+                    kk[u] = i == 0 ? kpre0 : i == 1 ? kpre1 : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < kCh; ++u) {
+                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
+                if (i >= nblk) break;                 // uniform
+                float kv[8];
+                if (j >= pos0 && j < n_kv) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kv[e] = knew[(j - pos0) * 128 + sub * 8 + e];
                 } else {
-                    const int4 k4 = cp ? *(const int4 *) &L.cpk[layer][j * 128 + sub * 8]
-                                  : j0 == 0 ? kpre0 : j0 == 16 ? kpre1
-                                            : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
-                    const uint16_t * kh = (const uint16_t *) &k4;
+                    const uint16_t * kh = (const uint16_t *) &kk[u];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
                 }
-            }
-            // fp16 x fp16 products are exact in fp64, so fma(q, k, acc) rounds
-            // exactly like acc + (double)(q * k)
-            double a0 = 0.0, a1 = 0.0;
+                // fp16 x fp16 products are exact in fp64: fma rounds like mul + add
+                double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const double kd = (double) kv[e];
-                a0 = fma(q0[e], kd, a0);
-                a1 = fma(q1[e], kd, a1);
-            }
-            a0 = group_sum_d(a0, 16);
-            a1 = group_sum_d(a1, 16);
-            if (j < n_kv) {
-                const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
-                if (sub == 0) { L.sc[j] = s0; L.sc[kMaxCtx + j] = s1; }
-                lm0 = fmaxf(lm0, s0);
-                lm1 = fmaxf(lm1, s1);
+                for (int e = 0; e < 8; ++e) {
+                    const double kd = (double) kv[e];
+                    a0 = fma(q0[e], kd, a0);
+                    a1 = fma(q1[e], kd, a1);
+                }
+                a0 = group_sum_d(a0, 16);
+                a1 = group_sum_d(a1, 16);
+                if (j < n_kv) {
+                    const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
+                    if (sub == 0) { L.sc[j] = s0; L.sc[kMaxCtx + j] = s1; }
+                    lm0 = fmaxf(lm0, s0);
+                    lm1 = fmaxf(lm1, s1);
+                }
             }
         }
         lm0 = wave_max_f(lm0);
@@ -813,44 +820,60 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
             L.sc[kMaxCtx + j] = round_f16(L.sc[kMaxCtx + j] * inv1);
         }
         __syncthreads();
-        // ---- P.V: lane l owns dims 2l, 2l+1 of both heads; wave w takes
-        // positions j = w, w + 4, ...; no cross-lane reduction
-        double o00 = 0.0, o01 = 0.0, o10 = 0.0, o11 = 0.0;
-        auto pv_pos = [&](int j, uint32_t w2) {
-            const double p0 = (double) L.sc[j], p1 = (double) L.sc[kMaxCtx + j];
-            float v0, v1;
-            if (j >= pos0) {
-                v0 = vnew[(j - pos0) * 128 + 2 * lane];
-                v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
-            } else {
-                v0 = h2f((uint16_t) (w2 & 0xffffu));
-                v1 = h2f((uint16_t) (w2 >> 16));
-            }
-            const double d0 = (double) v0, d1 = (double) v1;
-            o00 = fma(p0, d0, o00); o01 = fma(p0, d1, o01);
-            o10 = fma(p1, d0, o10); o11 = fma(p1, d1, o11);
-        };
-        auto v_at = [&](int j) -> uint32_t {
-            return cp ? *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane]
-                      : *(const uint32_t *) (vc + (size_t) j * 128 + 2 * lane);
-        };
+        // ---- P.V, same position blocks; partial sums over this lane's positions
+        double o0[8], o1[8];
 #pragma unroll
-        for (int i = 0; i < kVPre; ++i) {
-            const int j = wave + kW * i;
-            if (j < n_kv) pv_pos(j, cp || j >= pos0 ? (j < pos0 ? v_at(j) : 0u) : vpre[i]);
+        for (int e = 0; e < 8; ++e) { o0[e] = 0.0; o1[e] = 0.0; }
+        for (int i0 = 0; i0 < nblk; i0 += kCh) {
+            int4 vv4[kCh];
+#pragma unroll
+            for (int u = 0; u < kCh; ++u) {
+                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
+                vv4[u] = make_int4(0, 0, 0, 0);
+                if (i < nblk && j < pos0)
+                    vv4[u] = i == 0 ? vpre0 : i == 1 ? vpre1 : *(const int4 *) (vc + (size_t) j * 128 + sub * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < kCh; ++u) {
+                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
+                if (i >= nblk) break;                 // uniform
+                if (j < n_kv) {
+                    const double p0 = (double) L.sc[j], p1 = (double) L.sc[kMaxCtx + j];
+                    float vv[8];
+                    if (j >= pos0) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) vv[e] = vnew[(j - pos0) * 128 + sub * 8 + e];
+                    } else {
+                        const uint16_t * vh = (const uint16_t *) &vv4[u];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) vv[e] = h2f(vh[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const double vd = (double) vv[e];
+                        o0[e] = fma(p0, vd, o0[e]);
+                        o1[e] = fma(p1, vd, o1[e]);
+                    }
+                }
+            }
         }
-#pragma unroll 4
-        for (int j = wave + kW * kVPre; j < n_kv; j += kW) pv_pos(j, j < pos0 ? v_at(j) : 0u);
-        L.pv[(wave * 2 + 0) * 128 + 2 * lane] = o00;
-        L.pv[(wave * 2 + 0) * 128 + 2 * lane + 1] = o01;
-        L.pv[(wave * 2 + 1) * 128 + 2 * lane] = o10;
-        L.pv[(wave * 2 + 1) * 128 + 2 * lane + 1] = o11;
+        // combine the 16 partials of each output through LDS (the score buffer
+        // is free once every wave is past its last probability read)
+        __syncthreads();
+        double * part = (double *) L.sc;        // [wave][lane][16]
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            part[(wave * 64 + lane) * 16 + e] = o0[e];
+            part[(wave * 64 + lane) * 16 + 8 + e] = o1[e];
+        }
         __syncthreads();
         {
-            const int h = t >> 7, e = t & 127;
-            double r = L.pv[h * 128 + e];
+            const int h = t >> 7, e = t & 127, sb = e >> 3, ee = e & 7;
+            double r = 0.0;
 #pragma unroll
-            for (int w = 1; w < kW; ++w) r += L.pv[(w * 2 + h) * 128 + e];
+            for (int w = 0; w < kW; ++w)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) r += part[(w * 64 + q * 16 + sb) * 16 + h * 8 + ee];
             tstore(out + (size_t) tok * kHS + (g * 2 + h) * 128 + e, out_tag, (float) r);
         }
         __syncthreads();
