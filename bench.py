@@ -68,6 +68,37 @@ def cpu_baseline(cfg, w, text, spk, threads, budget_s):
     return (n3 - 1) / dt, n3
 
 
+def prefill_bench(args, cfg, w):
+    """One talker prefill of args.prefill rows (seeded N(0, 0.05) rows), the
+    long-prompt half of the long-context configuration.  Q8_0 models take the
+    int8 MFMA GEMM path; reports rows/s and the MFMA (int8) utilisation of the
+    five GEMMs per layer against the 5.0 POP/s dense peak."""
+    from qwen3_tts_amd.device import Device
+    n = args.prefill
+    dev = Device(cfg, 0)
+    dev.upload_weights(w)
+    dev.kv_reserve(n + 8)
+    rows = (np.random.default_rng(21).standard_normal((n, cfg.hidden_size)) * 0.05).astype(np.float32)
+    for _ in range(max(args.warmup, 1)):
+        dev.prefill(rows, 0, want_hidden=False)
+    steps = max(args.steps, 1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dev.prefill(rows, 0, want_hidden=False)
+    dt = (time.perf_counter() - t0) / steps
+    dev.close()
+    d, qd = cfg.hidden_size, cfg.n_head * cfg.head_dim
+    qkvd = qd + 2 * cfg.n_kv_head * cfg.head_dim
+    gemm_ops = 2.0 * n * cfg.n_layers * (qkvd * d + d * qd + 2 * cfg.ffn_size * d + d * cfg.ffn_size)
+    print(json.dumps({
+        "metric": "talker prefill rows/s (long prompt)", "value": round(n / dt, 1), "unit": "rows/s", "n_gpus": 1,
+        "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True,
+        "dtype": "int8" if args.weights == "q8_0" else "f16", "data": "synthetic",
+        "config": {"workload": f"talker prefill, {n} rows, {args.weights.upper()} 0.6B shapes", "rows": n},
+        "gemm_tops": round(gemm_ops / dt / 1e12, 2),
+        "mfma_util": round(gemm_ops / dt / 5.0e15, 4) if args.weights == "q8_0" else None}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,6 +111,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=200,
                     help="launches per per-kernel timing of the multi-kernel path (0: skip)")
+    ap.add_argument("--prefill", type=int, default=0,
+                    help="instead of the frame loop, time one talker prefill of this many rows (Q8_0: int8 MFMA path)")
     ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
                     help="persistent: one cooperative kernel per frame; graph: the captured multi-kernel frame")
     args = ap.parse_args()
@@ -95,6 +128,8 @@ def main():
 
     cfg = config.full_06b()
     w = Weights(cfg, args.weights, seed=2024)
+    if args.prefill > 0:
+        return prefill_bench(args, cfg, w)
     rng = np.random.default_rng(12)
     text = rng.integers(0, cfg.text_vocab, args.prompt).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)

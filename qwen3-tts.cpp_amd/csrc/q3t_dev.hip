@@ -7,6 +7,7 @@
 #include "../../include/q3t_dev.h"
 #include "q3t_kernels.h"
 #include "q3t_frame_kernel.h"
+#include "q3t_prefill.h"
 
 #include <hip/hip_runtime.h>
 
@@ -62,6 +63,11 @@ struct q3t_dev {
     float * hidden = nullptr, * logits = nullptr, * cp_logits = nullptr, * tp_a = nullptr, * tp_b = nullptr;
     float * stage = nullptr; int32_t stage_rows = 0;
     float * hidden_all = nullptr; int32_t hidden_all_rows = 0;
+    // MFMA prefill work buffers (sized for pf_rows tokens)
+    int32_t pf_rows = 0;
+    int8_t * pf_q = nullptr; float * pf_dx = nullptr;
+    float * pf_xa = nullptr, * pf_xb = nullptr, * pf_qkv = nullptr, * pf_att = nullptr;
+    float * pf_g = nullptr, * pf_u = nullptr, * pf_f = nullptr;
     int32_t * ids = nullptr; int32_t ids_cap = 0;
     FrameState * st = nullptr;
     SampleParams * params = nullptr;
@@ -864,6 +870,99 @@ int q3t_dev_kv_write(q3t_dev * c, int32_t layer, int32_t n_pos, const uint16_t *
     return 0;
 }
 
+// Whether the talker prefill of n tokens runs on the int8 MFMA path: Q8_0
+// layers with GEMM-friendly widths, n >= 16 (Q3T_PREFILL_MFMA=0 disables it,
+// =1 uses it for any n).
+bool use_mfma_prefill(q3t_dev * c, int n) {
+    const char * e = std::getenv("Q3T_PREFILL_MFMA");
+    if (e && e[0] == '0') return false;
+    if (!(e && e[0] == '1') && n < 16) return false;
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    if (g.head_dim != 128 || d % 128 || qd % 128 || g.ffn_size % 128 || qkvd % pf::kTile || d % pf::kTile ||
+        g.ffn_size % pf::kTile)
+        return false;
+    for (int i = 0; i < g.n_layers; ++i) {
+        const LayerDev & L = c->talker[i];
+        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
+            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
+            return false;
+    }
+    return true;
+}
+
+int ensure_pf(q3t_dev * c, int n) {
+    if (n <= c->pf_rows) return 0;
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    const int kmax = std::max(std::max(d, qd), g.ffn_size);
+    for (void * p : {(void *) c->pf_q, (void *) c->pf_dx, (void *) c->pf_xa, (void *) c->pf_xb, (void *) c->pf_qkv,
+                     (void *) c->pf_att, (void *) c->pf_g, (void *) c->pf_u, (void *) c->pf_f})
+        if (p) dev_free(c, p);
+    c->pf_rows = 0;
+    const size_t r = (size_t) n;
+    if (dev_alloc_t(c, &c->pf_q, r * kmax) || dev_alloc_t(c, &c->pf_dx, r * (kmax / kQK)) ||
+        dev_alloc_t(c, &c->pf_xa, r * d) || dev_alloc_t(c, &c->pf_xb, r * d) || dev_alloc_t(c, &c->pf_qkv, r * qkvd) ||
+        dev_alloc_t(c, &c->pf_att, r * qd) || dev_alloc_t(c, &c->pf_g, r * g.ffn_size) ||
+        dev_alloc_t(c, &c->pf_u, r * g.ffn_size) || dev_alloc_t(c, &c->pf_f, r * g.ffn_size))
+        return -1;
+    c->pf_rows = n;
+    return 0;
+}
+
+void pf_gemm(q3t_dev * c, const Slot & w, int N, int K, int n, float * y, const float * res) {
+    const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
+    hipLaunchKernelGGL(pf::k_gemm_q8, grid, dim3(kBlock), pf::gemm_lds_bytes(K), c->stream, (const int8_t *) w.data,
+                       (const uint16_t *) w.scales, N, K, (const int8_t *) c->pf_q, (const float *) c->pf_dx, n, y, N,
+                       res, N, res ? (int) EPI_RESID : (int) EPI_STORE);
+}
+
+void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w) {
+    hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, K, K, w, c->cfg.rms_eps, c->pf_q,
+                       c->pf_dx);
+}
+
+// Talker prefill of n tokens (rows in c->stage) on the MFMA path; the output
+// rows end in c->pf_xa, the last row's head output in c->hidden / c->logits.
+void prefill_mfma(q3t_dev * c, int n, int n_past) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int ffn = g.ffn_size;
+    const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
+    const float scale = 1.0f / std::sqrt((float) g.head_dim);
+    const float * x = c->stage;
+    for (int il = 0; il < g.n_layers; ++il) {
+        const LayerDev & L = c->talker[il];
+        uint16_t * kc = c->kc + il * lstride;
+        uint16_t * vc = c->vc + il * lstride;
+        pf_quant(c, x, n, d, L.attn_norm);
+        pf_gemm(c, L.qkv, qkvd, d, n, c->pf_qkv, nullptr);
+        hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+                           qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
+                           kc, vc, c->n_ctx, n_past);
+        hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
+                           c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
+                           (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
+                           g.n_kv_head, n_past, scale, c->pf_att, qd);
+        pf_quant(c, c->pf_att, n, qd, nullptr);
+        pf_gemm(c, L.wo, d, qd, n, c->pf_xb, x);
+        pf_quant(c, c->pf_xb, n, d, L.ffn_norm);
+        pf_gemm(c, L.wg, ffn, d, n, c->pf_g, nullptr);
+        pf_gemm(c, L.wu, ffn, d, n, c->pf_u, nullptr);
+        const size_t cnt = (size_t) n * ffn;
+        hipLaunchKernelGGL(pf::k_swiglu_rows, dim3((unsigned) std::min<size_t>((cnt + kBlock - 1) / kBlock, 4096)),
+                           dim3(kBlock), 0, c->stream, (const float *) c->pf_g, (const float *) c->pf_u, c->pf_f, cnt);
+        pf_quant(c, c->pf_f, n, ffn, nullptr);
+        pf_gemm(c, L.wd, d, ffn, n, c->pf_xa, c->pf_xb);
+        x = c->pf_xa;
+    }
+    GemvSpec h{};
+    h.w = weight_of(c->codec_head); h.rows = g.codec_vocab; h.K = d;
+    h.x = c->pf_xa + (size_t) (n - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
+    h.hidden_out = c->hidden; h.hidden_stride = d; h.y = c->logits; h.y_stride = g.codec_vocab;
+    gemv(c, h, 1);
+}
+
 int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, float * hidden_out, float * logits_out) {
     if (!c || !embd) return -1;
     if (n <= 0) return fail(c, "n_tokens must be > 0");
@@ -882,6 +981,16 @@ int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, 
     FrameState s{};
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) n * d * 4, hipMemcpyHostToDevice, c->stream));
+    if (use_mfma_prefill(c, n)) {
+        if (ensure_pf(c, n)) return -1;
+        prefill_mfma(c, n, n_past);
+        if (hidden_out)
+            hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xa,
+                               (const float *) c->out_norm.data, g.rms_eps, d, c->hidden_all);
+        if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden_all, (size_t) n * d * 4, hipMemcpyDeviceToHost, c->stream));
+        if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+        return sync(c);
+    }
     for (int t0 = 0; t0 < n;) {
         const int left = n - t0;
         const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;

@@ -1,0 +1,265 @@
+// q3t_prefill.h -- long-prompt talker prefill for Q8_0 models on int8 MFMA.
+//
+// The n-token prefill (forward_prefill, src/tts_transformer.cpp:2217-2347 /
+// build_prefill_forward_graph :1474-1617) is a real contraction once n is in
+// the tens or thousands, so each layer runs as
+//   quantise rows (RMSNorm where the layer has one, Q8_0 per 32-block)
+//   -> GEMM on v_mfma_i32_16x16x32_i8 (one MFMA = one 32-element Q8_0 block,
+//      exact in int32) with the block scales applied in fp64
+//   -> K/V rows into the cache -> causal attention over the cache
+//   -> quantise -> Wo GEMM (+ residual) -> quantise (+ RMSNorm) -> gate and up
+//      GEMMs -> SwiGLU -> quantise -> down GEMM (+ residual).
+// Every sum is of exact terms in fp64 rounded once, the contract of the GEMV
+// path, so the result equals the chunked GEMV prefill bit for bit.
+#pragma once
+
+#include "q3t_kernels.h"
+
+namespace q3t {
+namespace pf {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One row per block: optional RMSNorm (y = (x * scale) * w, scale from the
+// fp64 sum of fp32 squares), then Q8_0 quantisation per 32-element block
+// (d = amax/127 as fp16, q = rint(x * 127/amax)).  q: int8 [n][K]; dx: the
+// fp16-rounded scales as float [n][K/32].
+__global__ __launch_bounds__(kBlock) void k_quant_rows(const float * __restrict__ x, int32_t xs, int32_t K,
+                                                       const float * __restrict__ w, float eps, int8_t * __restrict__ q,
+                                                       float * __restrict__ dx) {
+    __shared__ double red[4];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float * xr = x + (size_t) row * xs;
+    float scale = 1.0f;
+    if (w) {
+        double ss = 0.0;
+        for (int i = t; i < K; i += kBlock) ss += (double) (xr[i] * xr[i]);
+        const double tot = block_sum_d(ss, red);
+        const float mean = (float) (tot / (double) K);
+        scale = 1.0f / sqrtf(mean + eps);
+    }
+    const int nb = K / kQK;
+    for (int b = t; b < nb; b += kBlock) {
+        float v[kQK];
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kQK; ++e) {
+            float y = xr[b * kQK + e];
+            if (w) { const float s = y * scale; y = s * w[b * kQK + e]; }
+            v[e] = y;
+            am = fmaxf(am, fabsf(y));
+        }
+        const float d = am / 127.0f;
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        int8_t * qr = q + (size_t) row * K + b * kQK;
+#pragma unroll
+        for (int c = 0; c < kQK / 4; ++c) {
+            int p = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p |= ((int) rintf(v[4 * c + e] * id) & 0xff) << (8 * e);
+            *(int *) (qr + 4 * c) = p;
+        }
+        dx[(size_t) row * nb + b] = round_f16(d);
+    }
+}
+
+constexpr int kTile = 64;       // output rows and tokens per workgroup
+constexpr int kU = 4;           // Q8_0 blocks loaded ahead per step
+
+// Y[t][r] = epi(sum_b fp16(dw[r][b]) * dx[t][b] * sum_k W[r][32b+k] Q[t][32b+k])
+// for a 64-row x 64-token tile.  Wave (wr, wt) = (wave & 1, wave >> 1) owns
+// rows wr*32.. and tokens wt*32.. as 2 x 2 MFMA tiles of 16 x 16.  MFMA lane
+// layout (16x16x32 i8): A[m = l%16][k = 8(l/16)..+7], B[k = 8(l/16)..+7][n =
+// l%16], D[m = 4(l/16)+i][n = l%16].  epi: EPI_STORE or EPI_RESID (res [n][rs]).
+// Requires N % 64 == 0 and K % 128 == 0 (the host checks).
+__global__ __launch_bounds__(kBlock) void k_gemm_q8(const int8_t * __restrict__ W, const uint16_t * __restrict__ Wd,
+                                                    int32_t N, int32_t K, const int8_t * __restrict__ Q,
+                                                    const float * __restrict__ dx, int32_t n, float * __restrict__ Y,
+                                                    int32_t ys, const float * __restrict__ res, int32_t rs, int32_t epi) {
+    extern __shared__ __align__(16) char smem[];
+    const int BPR = K / kQK;
+    float * sdw = (float *) smem;                  // [64 rows][BPR] weight scales
+    float * sdx = sdw + kTile * BPR;               // [64 tokens][BPR] activation scales
+    const int r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wr = wave & 1, wt = wave >> 1;
+    for (int i = t; i < kTile * BPR; i += kBlock) {
+        const int rr = i / BPR, b = i - rr * BPR;
+        sdw[i] = h2f(Wd[(size_t) (r0 + rr) * BPR + b]);
+        const int tok = t0 + rr;
+        sdx[i] = tok < n ? dx[(size_t) tok * BPR + b] : 0.0f;
+    }
+    __syncthreads();
+    const int lm = lane & 15, lk = lane >> 4;
+    const int8_t * wrow[2];
+    const int8_t * qrow[2];
+    bool qok[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        wrow[i] = W + (size_t) (r0 + wr * 32 + i * 16 + lm) * K + 8 * lk;
+        const int tok = t0 + wt * 32 + i * 16 + lm;
+        qok[i] = tok < n;
+        qrow[i] = Q + (size_t) (qok[i] ? tok : 0) * K + 8 * lk;
+    }
+    double acc[2][2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0;
+    const v4i zero = {0, 0, 0, 0};
+    for (int b0 = 0; b0 < BPR; b0 += kU) {
+        long a[kU][2], bq[kU][2];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[u][i] = *(const long *) (wrow[i] + (b0 + u) * kQK);
+                bq[u][i] = qok[i] ? *(const long *) (qrow[i] + (b0 + u) * kQK) : 0L;
+            }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int b = b0 + u;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float dwv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dwv[e] = sdw[(wr * 32 + i * 16 + 4 * lk + e) * BPR + b];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u][i], bq[u][j], zero, 0, 0, 0);
+                    const float dxv = sdx[(wt * 32 + j * 16 + lm) * BPR + b];
+                    // fp16 x fp16 scale product exact in fp32; times the int32 block sum exact in fp64
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fma((double) (dwv[e] * dxv), (double) d[e], acc[i][j][e]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int tok = t0 + wt * 32 + j * 16 + lm;
+            if (tok >= n) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + wr * 32 + i * 16 + 4 * lk + e;
+                float v = (float) acc[i][j][e];
+                if (epi == EPI_RESID) v = v + res[(size_t) tok * rs + r];
+                Y[(size_t) tok * ys + r] = v;
+            }
+        }
+}
+
+__host__ __device__ constexpr size_t gemm_lds_bytes(int K) { return (size_t) 2 * kTile * (K / kQK) * sizeof(float); }
+
+// SwiGLU over rows: f = silu(g) * u.
+__global__ __launch_bounds__(kBlock) void k_swiglu_rows(const float * __restrict__ g, const float * __restrict__ u,
+                                                        float * __restrict__ f, size_t count) {
+    for (size_t i = (size_t) blockIdx.x * kBlock + threadIdx.x; i < count; i += (size_t) gridDim.x * kBlock)
+        f[i] = silu_q3t(g[i]) * u[i];
+}
+
+// K (QK-norm + NEOX RoPE, fp16) and V (fp16) rows of n tokens into the KV
+// cache at positions pos0 + tok.  Block (g, tok), 256 threads (threads < 128
+// own one element each).
+__global__ __launch_bounds__(kBlock) void k_kv_rows(const float * __restrict__ qkv, int32_t qkv_stride, int32_t qd,
+                                                    int32_t kd, const float * __restrict__ k_norm, float eps,
+                                                    const float * __restrict__ rc, const float * __restrict__ rs,
+                                                    uint16_t * __restrict__ kc, uint16_t * __restrict__ vc, int32_t n_ctx,
+                                                    int32_t pos0) {
+    __shared__ double red[4];
+    __shared__ float tmp[kHD];
+    const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, pos = pos0 + tok;
+    const float * row = qkv + (size_t) tok * qkv_stride;
+    const float kv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
+    const float o = head_norm_rope(kv, k_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
+    if (t < kHD) {
+        kc[((size_t) g * n_ctx + pos) * kHD + t] = f2h(o);
+        vc[((size_t) g * n_ctx + pos) * kHD + t] = f2h(row[qd + kd + g * kHD + t]);
+    }
+}
+
+// Causal attention of n tokens over the cache (all rows already written).
+// Block (h, tok): q-norm + RoPE, scores over positions [0, pos0+tok], fp64
+// softmax denominator, fp16 probabilities, fp64 P.V.  out [n][qd].
+__global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__ qkv, int32_t qkv_stride,
+                                                      const float * __restrict__ q_norm, float eps,
+                                                      const float * __restrict__ rc, const float * __restrict__ rs,
+                                                      const uint16_t * __restrict__ kc, const uint16_t * __restrict__ vc,
+                                                      int32_t n_ctx, int32_t n_head, int32_t n_kv_head, int32_t pos0,
+                                                      float scale, float * __restrict__ out, int32_t out_stride) {
+    extern __shared__ __align__(16) char smem[];
+    double * red = (double *) smem;                   // 4 doubles
+    float * fred = (float *) (smem + 32);             // 4 floats
+    float * tmp = (float *) (smem + 64);              // 128
+    float * qf = tmp + kHD;                           // 128
+    double * pv = (double *) (qf + kHD);              // [4 waves][128]
+    float * sc = (float *) (pv + 4 * kHD);            // [n_kv]
+    const int h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x;
+    const int g = h / (n_head / n_kv_head);
+    const int pos = pos0 + tok, n_kv = pos + 1;
+    {
+        const float v = t < kHD ? qkv[(size_t) tok * qkv_stride + h * kHD + t] : 0.0f;
+        const float o = head_norm_rope(v, q_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
+        if (t < kHD) qf[t] = round_f16(o);
+    }
+    __syncthreads();
+    const int lane = t & 63, wave = t >> 6, sub = lane & 15, pw = lane >> 4;
+    const uint16_t * kb = kc + (size_t) g * n_ctx * kHD;
+    const uint16_t * vb = vc + (size_t) g * n_ctx * kHD;
+    double qd8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qd8[e] = (double) qf[sub * 8 + e];
+    float lmax = -INFINITY;
+    for (int j0 = 0; j0 < n_kv; j0 += 16) {
+        const int j = j0 + wave * 4 + pw;
+        double acc = 0.0;
+        if (j < n_kv) {
+            const int4 k4 = *(const int4 *) (kb + (size_t) j * kHD + sub * 8);
+            const uint16_t * kh = (const uint16_t *) &k4;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc = fma(qd8[e], (double) h2f(kh[e]), acc);   // exact products
+        }
+        acc = group_sum_d(acc, 16);
+        if (j < n_kv) {
+            const float s = (float) acc * scale;
+            if (sub == 0) sc[j] = s;
+            lmax = fmaxf(lmax, s);
+        }
+    }
+    const float mx = block_max_f(lmax, fred);
+    double lsum = 0.0;
+    for (int j = t; j < n_kv; j += kBlock) {
+        const float e = expf_q3t(sc[j] - mx);
+        sc[j] = e;
+        lsum += (double) e;
+    }
+    const double sum = block_sum_d(lsum, red);
+    const float inv = (float) (1.0 / sum);
+    for (int j = t; j < n_kv; j += kBlock) sc[j] = round_f16(sc[j] * inv);
+    __syncthreads();
+    // P.V: lane owns dims 2*lane, 2*lane+1; wave w takes positions w, w+4, ...
+    double o0 = 0.0, o1 = 0.0;
+    for (int j = wave; j < n_kv; j += 4) {
+        const double p = (double) sc[j];
+        const uint32_t w2 = *(const uint32_t *) (vb + (size_t) j * kHD + 2 * lane);
+        o0 = fma(p, (double) h2f((uint16_t) (w2 & 0xffffu)), o0);
+        o1 = fma(p, (double) h2f((uint16_t) (w2 >> 16)), o1);
+    }
+    pv[wave * kHD + 2 * lane] = o0;
+    pv[wave * kHD + 2 * lane + 1] = o1;
+    __syncthreads();
+    if (t < kHD) {
+        const double r = (pv[t] + pv[kHD + t]) + (pv[2 * kHD + t] + pv[3 * kHD + t]);
+        out[(size_t) tok * out_stride + h * kHD + t] = (float) r;
+    }
+}
+
+__host__ __device__ constexpr size_t attn_rows_lds_bytes(int n_ctx) {
+    return 64 + 2 * kHD * sizeof(float) + 4 * kHD * sizeof(double) + (size_t) n_ctx * sizeof(float);
+}
+
+}  // namespace pf
+}  // namespace q3t

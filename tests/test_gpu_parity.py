@@ -72,12 +72,20 @@ def test_upload_roundtrip_and_dequant(tiny_model):
             assert np.array_equal(deq.view(np.uint32), orc.dequantize(arr, ne[0] * ne[1]).view(np.uint32))
 
 
-def test_prefill_and_steps_match_oracle(tiny_model):
+@pytest.fixture(params=["gemv", "mfma"])
+def prefill_path(request, monkeypatch):
+    """Runs a prefill test on the chunked GEMV prefill and on the int8 MFMA
+    prefill (Q8_0 models; F16 models always take the GEMV path)."""
+    monkeypatch.setenv("Q3T_PREFILL_MFMA", "1" if request.param == "mfma" else "0")
+    return request.param
+
+
+def test_prefill_and_steps_match_oracle(tiny_model, prefill_path):
     cfg, w, dev, o = tiny_model
     rng = np.random.default_rng(1)
     d = cfg.hidden_size
     embd = (rng.standard_normal((10, d)) * 0.05).astype(np.float32)
-    say("[gpu] prefill 10 rows")
+    say(f"[gpu] prefill 10 rows ({prefill_path})")
     hid_g, log_g = dev.prefill(embd, 0)
     hid_o, log_o = o.prefill(embd, 0)
     assert np.abs(log_g - log_o).max() <= LOGIT_TOL
@@ -215,3 +223,31 @@ def test_fp16_tie_rounding_regression(frame_path):
     check_path(dev, "q8_0", frame_path)
     dev.close()
     assert np.array_equal(cg, co)
+
+
+@pytest.mark.slow
+def test_full_q8_mfma_prefill_200_rows():
+    """int8 MFMA prefill of 200 rows at the 0.6B shapes: every normed hidden
+    row and the last-row logits equal the oracle; a following talker step
+    (which reads the 200 cached K/V rows) matches too."""
+    cfg = qcfg.full_06b()
+    say("[gpu] full 0.6B Q8_0 MFMA prefill: synth + upload")
+    w, dev, o = make(cfg, "q8_0", seed=5, n_ctx=256)
+    rng = np.random.default_rng(13)
+    embd = (rng.standard_normal((200, cfg.hidden_size)) * 0.05).astype(np.float32)
+    import os
+    os.environ["Q3T_PREFILL_MFMA"] = "1"
+    try:
+        say("[gpu] full: device prefill 200")
+        hid_g, log_g = dev.prefill(embd, 0)
+        e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+        lg, hg = dev.talker_step(e, 200)
+    finally:
+        del os.environ["Q3T_PREFILL_MFMA"]
+    say("[gpu] full: oracle prefill 200")
+    hid_o, log_o = o.prefill(embd, 0)
+    lo, ho = o.step(e, 200)
+    dev.close()
+    assert np.array_equal(hid_g, hid_o)
+    assert np.array_equal(log_g, log_o)
+    assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
