@@ -30,7 +30,10 @@ HBM_PEAK_GBS = 8000.0
 def frame_bytes(cfg, w, n_kv):
     """Algorithmic HBM bytes of one frame: every weight byte once per pass
     that reads it (talker once; code predictor 15 passes; heads once per
-    pass), plus KV reads/writes.  Activations are excluded (<0.1%)."""
+    pass), plus KV reads/writes.  Activations are excluded (<0.1%).  n_kv is
+    the talker KV length, or a list of lengths (one per stream) for the
+    multi-stream loop, which reads every weight once per frame for all
+    streams together."""
     def nbytes(name):
         return w[name][2].nbytes
     talker = sum(nbytes(n) for n in w if n.startswith("talker.blk."))
@@ -39,10 +42,13 @@ def frame_bytes(cfg, w, n_kv):
     cp = 15 * (cp_layers + nbytes("code_pred.output_norm.weight")) + sum(
         nbytes(f"code_pred.lm_head.{g}.weight") for g in range(15))
     kv_row = cfg.n_kv_head * cfg.head_dim * 2 * 2          # K and V, fp16
-    talker_kv = cfg.n_layers * kv_row * (n_kv + 1)           # read n_kv rows + write 1
-    cp_kv = cfg.cp_layers * kv_row * sum(g + 2 for g in range(15))
-    embd = 17 * cfg.hidden_size * 2
-    return talker + cp + talker_kv + cp_kv + embd
+    per_stream = 0
+    for n in (n_kv if isinstance(n_kv, (list, tuple)) else [n_kv]):
+        talker_kv = cfg.n_layers * kv_row * (n + 1)          # read n rows + write 1
+        cp_kv = cfg.cp_layers * kv_row * sum(g + 2 for g in range(15))
+        embd = 17 * cfg.hidden_size * 2
+        per_stream += talker_kv + cp_kv + embd
+    return talker + cp + per_stream
 
 
 def cpu_baseline(cfg, w, text, spk, threads, budget_s):
@@ -99,6 +105,77 @@ def prefill_bench(args, cfg, w):
         "mfma_util": round(gemm_ops / dt / 5.0e15, 4) if args.weights == "q8_0" else None}))
 
 
+def streams_bench(args, cfg, w):
+    """Multi-stream batched decode: args.streams independent utterances, each
+    a 128-token prompt (build_prefill rows) behind a seeded synthetic history
+    so that its talker KV starts at a length drawn uniformly from
+    [128, 2048]; greedy, EOS biased off, every stream advancing one frame per
+    graph launch.  Reports aggregate frames/s over all streams, the int8 MFMA
+    utilisation of the batched layer GEMMs against the 5.0 POP/s dense peak,
+    and the HBM rate of the frame's algorithmic bytes (weights once per
+    frame, every stream's KV)."""
+    from qwen3_tts_amd import driver
+    from qwen3_tts_amd.device import Device
+    B = args.streams
+    rng = np.random.default_rng(77)
+    kv_len = rng.integers(128, 2049, B)
+    dev = Device(cfg, 0)
+    dev.upload_weights(w)
+    total = args.warmup + args.steps
+    n_ctx = int(kv_len.max()) + total + 8
+    rows, plens = [], []
+    for b in range(B):
+        text = rng.integers(0, cfg.text_vocab, 128).astype(np.int32)
+        spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+        pre, trail, pad = driver.build_prefill(dev, cfg, text, spk)
+        hist = (rng.standard_normal((int(kv_len[b]) - pre.shape[0], cfg.hidden_size)) * 0.05).astype(np.float32)
+        rows.append((np.concatenate([hist, pre]).astype(np.float32), trail, pad))
+    dev.streams_reserve(B, n_ctx)
+    args_list = []
+    for b, (ctx, trail, pad) in enumerate(rows):
+        dev.stream_prefill(b, ctx)
+        plens.append(ctx.shape[0])
+        args_list.append(dict(trailing=trail, tts_pad=pad, n_past=ctx.shape[0], max_len=total, repetition_penalty=1.05,
+                              temperature=0.0, top_k=0, eos_bias=-1e4))
+    dev.streams_begin(args_list)
+    if args.warmup:
+        codes, eos = dev.streams_run(args.warmup)
+        assert not any(eos)
+    dev.sync()
+    us0, n0, _ = dev.frames_stats()
+    t0 = time.perf_counter()
+    codes, eos = dev.streams_run(args.steps)
+    elapsed = time.perf_counter() - t0
+    us1, n1, path = dev.frames_stats()
+    dev.close()
+    assert path == 2 and not any(eos) and all(c.shape[0] == args.steps for c in codes), "stream stopped early"
+    gpu_frame_s = (us1 - us0) * 1e-6 / max(n1 - n0, 1)
+    fps = B * args.steps / elapsed
+    d, qd = cfg.hidden_size, cfg.n_head * cfg.head_dim
+    qkvd = qd + 2 * cfg.n_kv_head * cfg.head_dim
+    layer_macs = qkvd * d + d * qd + 2 * cfg.ffn_size * d + d * cfg.ffn_size
+    # talker: 1 row per stream per frame; code predictor: 2 + 14 rows per stream per frame
+    frame_ops = 2.0 * B * layer_macs * (cfg.n_layers + 16 * cfg.cp_layers)
+    fbytes = frame_bytes(cfg, w.tensors, [p + args.warmup + args.steps // 2 for p in plens])
+    out = {
+        "metric": "aggregate codec frames/sec, multi-stream batched decode Q8_0", "value": round(fps, 1),
+        "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded weights, uniform prompt ids, N(0,0.05) history)",
+        "config": {"workload": f"{B} streams, 128-token prompts, talker KV lengths uniform in [128, 2048], greedy, "
+                               f"Q8_0 0.6B shapes, one hipGraph per frame of all streams",
+                   "global_batch": B, "frames_per_stream": args.steps, "kv_lengths": [int(x) for x in plens]},
+        "gpu_ms_per_frame": round(gpu_frame_s * 1e3, 4),
+        "per_stream_fps": round(args.steps / elapsed, 2),
+        "layer_gemm_tops": round(frame_ops / gpu_frame_s / 1e12, 2),
+        "mfma_util": round(frame_ops / gpu_frame_s / 5.0e15, 5),
+        "frame_algorithmic_bytes": int(fbytes),
+        "frame_hbm_gbs": round(fbytes / gpu_frame_s / 1e9, 1),
+        "frame_roofline_frac": round(fbytes / gpu_frame_s / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,6 +190,8 @@ def main():
                     help="launches per per-kernel timing of the multi-kernel path (0: skip)")
     ap.add_argument("--prefill", type=int, default=0,
                     help="instead of the frame loop, time one talker prefill of this many rows (Q8_0: int8 MFMA path)")
+    ap.add_argument("--streams", type=int, default=0,
+                    help="instead of batch 1, time multi-stream batched decode of this many streams (Q8_0)")
     ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
                     help="persistent: one cooperative kernel per frame; graph: the captured multi-kernel frame")
     args = ap.parse_args()
@@ -130,6 +209,8 @@ def main():
     w = Weights(cfg, args.weights, seed=2024)
     if args.prefill > 0:
         return prefill_bench(args, cfg, w)
+    if args.streams > 0:
+        return streams_bench(args, cfg, w)
     rng = np.random.default_rng(12)
     text = rng.integers(0, cfg.text_vocab, args.prompt).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)

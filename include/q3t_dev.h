@@ -160,14 +160,39 @@ int  q3t_dev_frames_begin(q3t_dev * dev, const q3t_frame_args * args);
 int  q3t_dev_frames_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
                         int32_t * n_emitted_out, int32_t * eos_out);
 
-/* Frame-loop statistics since the last q3t_dev_frames_begin: GPU time of
- * the frame launches (HIP events around each frames_run's launches, in
- * microseconds), the number of frames launched, and which implementation ran
- * them (1 = one persistent cooperative kernel per frame, 0 = the captured
- * multi-kernel graph).  Instrumentation with no counterpart in the
+/* Frame-loop statistics since the last q3t_dev_frames_begin or
+ * q3t_dev_streams_begin: GPU time of the frame launches (HIP events around
+ * each frames_run / streams_run's launches, in microseconds), the number of
+ * frame launches, and which implementation ran them (1 = one persistent
+ * cooperative kernel per frame, 0 = the captured multi-kernel graph, 2 = the
+ * multi-stream graph, one launch advancing every stream by a frame).  Instrumentation with no counterpart in the
  * reference; the benchmark and the tests use it. */
 int  q3t_dev_frames_stats(q3t_dev * dev, double * gpu_us_out, int64_t * frames_out,
                           int32_t * path_out);
+
+/* Multi-stream decode: n_streams independent generate() frame loops
+ * (src/tts_transformer.cpp:3108-3309, one per utterance) advanced together.
+ * The reference runs one utterance per TTSTransformer at batch 1; this is
+ * the batched form of the same loop, each stream bit-identical to its own
+ * q3t_dev_frames_* run (same weights, prompt rows, arguments and seed).
+ * Every talker / code-predictor layer runs as one int8 MFMA GEMM over the
+ * streams' rows, attention and the samplers as one block per stream.
+ * Requires Q8_0 layer weights.
+ *
+ * streams_reserve allocates per-stream KV caches of n_ctx positions (and
+ * re-reserves the context's own cache to n_ctx for the shared RoPE tables);
+ * stream_prefill runs forward_prefill (:2217-2347) for one stream at n_past 0
+ * into its cache; streams_begin takes one q3t_frame_args per stream (n_past
+ * = that stream's prompt length); streams_run advances every live stream by
+ * up to n_frames frames.  codes_out is [n_streams][n_frames][n_codebooks]:
+ * stream b's new frames start at codes_out + b*n_frames*16, their count in
+ * n_emitted_out[b], eos_out[b] = 1 once its codebook 0 sampled EOS.  Streams
+ * that stopped (EOS or max_len) idle while the others run. */
+int  q3t_dev_streams_reserve(q3t_dev * dev, int32_t n_streams, int32_t n_ctx);
+int  q3t_dev_stream_prefill(q3t_dev * dev, int32_t stream, const float * embd, int32_t n);
+int  q3t_dev_streams_begin(q3t_dev * dev, const q3t_frame_args * args);
+int  q3t_dev_streams_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
+                         int32_t * n_emitted_out, int32_t * eos_out);
 
 /* Blocks until all work queued by this context has finished. */
 int  q3t_dev_sync(q3t_dev * dev);

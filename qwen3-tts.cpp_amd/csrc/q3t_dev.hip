@@ -68,6 +68,26 @@ struct q3t_dev {
     int8_t * pf_q = nullptr; float * pf_dx = nullptr;
     float * pf_xa = nullptr, * pf_xb = nullptr, * pf_qkv = nullptr, * pf_att = nullptr;
     float * pf_g = nullptr, * pf_u = nullptr, * pf_f = nullptr;
+    // multi-stream decode: nb independent streams sharing the weights
+    int32_t nb = 0, sb_ctx = 0;
+    uint16_t * skc = nullptr, * svc = nullptr;        // [stream][layer][kv_head][sb_ctx][128]
+    uint16_t * scpk = nullptr, * scpv = nullptr;      // [stream][cp_layer][kv_head][16][128]
+    FrameState * sst = nullptr;
+    SampleParams * sparams = nullptr;
+    uint8_t * sseen = nullptr;                        // [stream][codec_vocab]
+    int32_t * scodes = nullptr; int32_t scodes_cap = 0;      // [stream][scodes_cap][16]
+    float * strail = nullptr; int32_t strail_cap = 0;        // [stream][strail_cap][d]
+    int32_t * sntrail = nullptr;                      // [stream]
+    float * spad = nullptr, * shidden = nullptr;      // [stream][d]
+    float * slogits = nullptr, * scplogits = nullptr; // [stream][codec_vocab], [stream][cp_vocab]
+    float * sstage = nullptr;                         // [stream][2][d]
+    float * bxa = nullptr, * bxb = nullptr, * bqkv = nullptr, * batt = nullptr;   // [2 * nb][...]
+    float * bg = nullptr, * bu = nullptr, * bf = nullptr;
+    int8_t * bq = nullptr; float * bdx = nullptr;
+    hipGraphExec_t s_exec = nullptr; hipGraph_t s_graph = nullptr;
+    int32_t s_launched = 0, s_max = 0; bool s_ready = false;
+    bool stats_streams = false;    // frame statistics describe the multi-stream loop
+    std::vector<int32_t> s_emitted;
     int32_t * ids = nullptr; int32_t ids_cap = 0;
     FrameState * st = nullptr;
     SampleParams * params = nullptr;
@@ -135,6 +155,12 @@ void dev_free(q3t_dev * c, void * p) {
     auto it = std::find(c->allocs.begin(), c->allocs.end(), p);
     if (it != c->allocs.end()) c->allocs.erase(it);
     (void) hipFree(p);
+}
+
+void drop_stream_graph(q3t_dev * c) {
+    if (c->s_exec) { (void) hipGraphExecDestroy(c->s_exec); c->s_exec = nullptr; }
+    if (c->s_graph) { (void) hipGraphDestroy(c->s_graph); c->s_graph = nullptr; }
+    c->s_ready = false;
 }
 
 void drop_graph(q3t_dev * c) {
@@ -271,6 +297,7 @@ struct GemvSpec {
     const float * resid = nullptr; int resid_stride = 0;
     const float * bias = nullptr;
     int epi = EPI_STORE;
+    bool no_done = false;      // multi-stream heads: no single frame state to consult
 };
 
 template <int WT, int NT, bool DUAL>
@@ -325,7 +352,7 @@ void gemv(q3t_dev * c, const GemvSpec & s, int nt) {
     a.y = s.y; a.y_stride = s.y_stride;
     a.resid = s.resid; a.resid_stride = s.resid_stride;
     a.bias = s.bias;
-    a.done = &c->st->done;
+    a.done = s.no_done ? nullptr : &c->st->done;
     a.pro = s.norm_w ? PRO_NORM : PRO_NONE;
     a.epi = s.epi;
     // 1-2 tokens take the register path; more tokens (prefill chunks of 4)
@@ -679,6 +706,7 @@ void q3t_dev_destroy(q3t_dev * c) {
     (void) hipSetDevice(c->device);
     if (c->stream) (void) hipStreamSynchronize(c->stream);
     drop_graph(c);
+    drop_stream_graph(c);
     for (hipEvent_t e : c->run_ev) if (e) (void) hipEventDestroy(e);
     for (void * p : c->allocs) (void) hipFree(p);
     if (c->stream) (void) hipStreamDestroy(c->stream);
@@ -804,6 +832,7 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
     HIP_OK(hipSetDevice(c->device));
     HIP_OK(hipStreamSynchronize(c->stream));
     drop_graph(c);
+    drop_stream_graph(c);
     dev_free(c, c->kc); dev_free(c, c->vc); dev_free(c, c->cpk); dev_free(c, c->cpv);
     dev_free(c, c->rope_cos); dev_free(c, c->rope_sin); dev_free(c, c->cp_rope_cos); dev_free(c, c->cp_rope_sin);
     c->kc = c->vc = c->cpk = c->cpv = nullptr;
@@ -910,16 +939,19 @@ int ensure_pf(q3t_dev * c, int n) {
     return 0;
 }
 
-void pf_gemm(q3t_dev * c, const Slot & w, int N, int K, int n, float * y, const float * res) {
+void pf_gemm(q3t_dev * c, const Slot & w, int N, int K, int n, float * y, const float * res, int rs = -1,
+             const int8_t * q = nullptr, const float * dx = nullptr) {
     const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
     hipLaunchKernelGGL(pf::k_gemm_q8, grid, dim3(kBlock), pf::gemm_lds_bytes(K), c->stream, (const int8_t *) w.data,
-                       (const uint16_t *) w.scales, N, K, (const int8_t *) c->pf_q, (const float *) c->pf_dx, n, y, N,
-                       res, N, res ? (int) EPI_RESID : (int) EPI_STORE);
+                       (const uint16_t *) w.scales, N, K, q ? q : (const int8_t *) c->pf_q,
+                       dx ? dx : (const float *) c->pf_dx, n, y, N, res, rs < 0 ? N : rs,
+                       res ? (int) EPI_RESID : (int) EPI_STORE);
 }
 
-void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w) {
-    hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, K, K, w, c->cfg.rms_eps, c->pf_q,
-                       c->pf_dx);
+void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w, int xs = -1, int8_t * q = nullptr,
+              float * dx = nullptr) {
+    hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, xs < 0 ? K : xs, K, w, c->cfg.rms_eps,
+                       q ? q : c->pf_q, dx ? dx : c->pf_dx);
 }
 
 // Talker prefill of n tokens (rows in c->stage) on the MFMA path; the output
@@ -1197,6 +1229,7 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     c->run_frames = 0;
     c->frames_max = a->max_len;
     c->frames_ready = true;
+    c->stats_streams = false;
     return 0;
 }
 
@@ -1243,11 +1276,318 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     return 0;
 }
 
+// ------------------------------------------------------------ multi-stream
+// nb independent utterances share the weights: every GEMV of the frame
+// becomes an (nb x nt)-row GEMM on the int8 MFMA kernel, attention and the
+// samplers run one block per stream (grid z / x), each stream keeps its own
+// KV caches, frame state, sampler state and trailing text.
+
+// F16 / Q8 GEMV over n rows in launches of 4, 2 or 1 rows.
+static void gemv_rows(q3t_dev * c, const GemvSpec & s, int n) {
+    for (int r = 0; r < n;) {
+        const int nt = n - r >= 4 ? 4 : n - r >= 2 ? 2 : 1;
+        GemvSpec t = s;
+        t.x = s.x + (size_t) r * s.x_stride;
+        t.y = s.y + (size_t) r * s.y_stride;
+        if (s.hidden_out) t.hidden_out = s.hidden_out + (size_t) r * s.hidden_stride;
+        gemv(c, t, nt);
+        r += nt;
+    }
+}
+
+struct StreamKV {
+    uint16_t * kc; uint16_t * vc;   // stream 0, this layer
+    int64_t stream;                 // elements per stream
+    int n_ctx;
+    const float * rc; const float * rs;
+    const int32_t * pos_ptr; int pos_const;
+};
+
+// One decoder layer over n = nb * nt rows (stream-major); output rows in c->bxa.
+static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, int nt, const StreamKV & kv) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int ffn = g.ffn_size, n = c->nb * nt;
+    pf_quant(c, x, n, d, L.attn_norm, d, c->bq, c->bdx);
+    pf_gemm(c, L.qkv, qkvd, d, n, c->bqkv, nullptr, -1, c->bq, c->bdx);
+    AttnArgs a{};
+    a.qkv = c->bqkv; a.qkv_stride = qkvd; a.qkv_stream = nt * qkvd;
+    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
+    a.rope_cos = kv.rc; a.rope_sin = kv.rs;
+    a.kc = kv.kc; a.vc = kv.vc; a.n_ctx = kv.n_ctx; a.kv_stream = kv.stream;
+    a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
+    a.pos_ptr = kv.pos_ptr; a.pos_const = kv.pos_const; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.out = c->batt; a.out_stride = qd; a.out_stream = nt * qd;
+    a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.scale = 1.0f / std::sqrt((float) g.head_dim);
+    a.nt = nt;
+    hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
+    pf_quant(c, c->batt, n, qd, nullptr, qd, c->bq, c->bdx);
+    pf_gemm(c, L.wo, d, qd, n, c->bxb, x, d, c->bq, c->bdx);
+    pf_quant(c, c->bxb, n, d, L.ffn_norm, d, c->bq, c->bdx);
+    pf_gemm(c, L.wg, ffn, d, n, c->bg, nullptr, -1, c->bq, c->bdx);
+    pf_gemm(c, L.wu, ffn, d, n, c->bu, nullptr, -1, c->bq, c->bdx);
+    const size_t cnt = (size_t) n * ffn;
+    hipLaunchKernelGGL(pf::k_swiglu_rows, dim3((unsigned) std::min<size_t>((cnt + kBlock - 1) / kBlock, 4096)),
+                       dim3(kBlock), 0, c->stream, (const float *) c->bg, (const float *) c->bu, c->bf, cnt);
+    pf_quant(c, c->bf, n, ffn, nullptr, ffn, c->bq, c->bdx);
+    pf_gemm(c, L.wd, d, ffn, n, c->bxa, c->bxb, d, c->bq, c->bdx);
+}
+
+static SampleArgs stream_sample_args(q3t_dev * c, int mode, int group) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size;
+    SampleArgs sa{};
+    sa.mode = mode; sa.group = group;
+    sa.vocab = mode == 0 ? g.codec_vocab : g.cp_vocab;
+    sa.logits = mode == 0 ? c->slogits : c->scplogits;
+    sa.logits_stream = sa.vocab;
+    sa.params = c->sparams; sa.st = c->sst; sa.seen = c->sseen; sa.seen_stream = g.codec_vocab;
+    sa.eos_id = g.codec_eos_id;
+    sa.stage = c->sstage; sa.stage_stream = mode == 0 ? 2 * d : d;
+    sa.hidden = c->shidden; sa.hidden_stream = d;
+    sa.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; i < g.n_codebooks - 1; ++i) sa.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    sa.trailing = c->strail; sa.trailing_stream = c->strail_cap * d; sa.n_trailing_arr = c->sntrail;
+    sa.pad = c->spad; sa.pad_stream = d;
+    sa.d = d;
+    return sa;
+}
+
+// One frame of every stream: codebook-0 samplers, code predictor (2-token
+// prefill + 14 steps), talker step; each stream's frame state advances
+// unless it is done.
+static void streams_frame_seq(q3t_dev * c) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, B = c->nb;
+    SampleArgs sa = stream_sample_args(c, 0, 0);
+    sa.open_frame = 1;
+    hipLaunchKernelGGL(k_sample, dim3(B), dim3(kSampleThreads), 0, c->stream, sa);
+    const int64_t cp_lstride = (int64_t) g.n_kv_head * 16 * g.head_dim;
+    for (int step = 0; step < g.n_codebooks - 1; ++step) {
+        const int nt = step == 0 ? 2 : 1;
+        const int pos = step == 0 ? 0 : step + 1;
+        const float * x = c->sstage;
+        for (int il = 0; il < g.cp_layers; ++il) {
+            StreamKV kv{c->scpk + il * cp_lstride, c->scpv + il * cp_lstride, cp_lstride * g.cp_layers, 16,
+                        c->cp_rope_cos, c->cp_rope_sin, nullptr, pos};
+            stream_layer(c, c->cp[il], x, nt, kv);
+            x = c->bxa;
+        }
+        GemvSpec h{};
+        h.w = weight_of(c->cp_head[step]); h.rows = g.cp_vocab; h.K = d;
+        h.x = c->bxa + (size_t) (nt - 1) * d; h.x_stride = nt * d; h.norm_w = (const float *) c->cp_out_norm.data;
+        h.y = c->scplogits; h.y_stride = g.cp_vocab; h.no_done = true;
+        gemv_rows(c, h, B);
+        SampleArgs sc = stream_sample_args(c, 1, step + 1);
+        if (step + 1 == 15) { sc.codes_out = c->scodes; sc.codes_stream = c->scodes_cap * 16; }
+        hipLaunchKernelGGL(k_sample, dim3(B), dim3(kSampleThreads), 0, c->stream, sc);
+    }
+    const int64_t lstride = (int64_t) g.n_kv_head * c->sb_ctx * g.head_dim;
+    const float * x = c->sstage;
+    for (int il = 0; il < g.n_layers; ++il) {
+        StreamKV kv{c->skc + il * lstride, c->svc + il * lstride, lstride * g.n_layers, c->sb_ctx, c->rope_cos,
+                    c->rope_sin, &c->sst[0].talker_pos, 0};
+        stream_layer(c, c->talker[il], x, 1, kv);
+        x = c->bxa;
+    }
+    GemvSpec h{};
+    h.w = weight_of(c->codec_head); h.rows = g.codec_vocab; h.K = d;
+    h.x = c->bxa; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
+    h.hidden_out = c->shidden; h.hidden_stride = d; h.y = c->slogits; h.y_stride = g.codec_vocab; h.no_done = true;
+    gemv_rows(c, h, B);
+}
+
+int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
+    if (!c) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (resolve(c)) return -1;
+    const q3t_config & g = c->cfg;
+    if (n_streams < 1 || n_streams > 64) return fail(c, "n_streams must be in [1, 64]");
+    if (n_ctx < 1) return fail(c, "n_ctx must be > 0");
+    for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
+        const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
+        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
+            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
+            return fail(c, "multi-stream decode needs Q8_0 layer weights (int8 MFMA GEMMs)");
+    }
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    if (g.head_dim != 128 || d % 128 || qd % 128 || g.ffn_size % 128 || qkvd % pf::kTile || d % pf::kTile ||
+        g.ffn_size % pf::kTile || g.cp_ffn != g.ffn_size || g.cp_hidden != d)
+        return fail(c, "multi-stream decode: unsupported model widths");
+    // the streams' talker caches share the context's RoPE tables and KV layout stride
+    if (c->n_ctx != n_ctx && q3t_dev_kv_reserve(c, n_ctx)) return -1;
+    HIP_OK(hipStreamSynchronize(c->stream));
+    drop_stream_graph(c);
+    for (void * p : {(void *) c->skc, (void *) c->svc, (void *) c->scpk, (void *) c->scpv, (void *) c->sst,
+                     (void *) c->sparams, (void *) c->sseen, (void *) c->sntrail, (void *) c->spad, (void *) c->shidden,
+                     (void *) c->slogits, (void *) c->scplogits, (void *) c->sstage, (void *) c->bxa, (void *) c->bxb,
+                     (void *) c->bqkv, (void *) c->batt, (void *) c->bg, (void *) c->bu, (void *) c->bf, (void *) c->bq,
+                     (void *) c->bdx, (void *) c->scodes, (void *) c->strail})
+        if (p) dev_free(c, p);
+    c->scodes = nullptr; c->strail = nullptr; c->scodes_cap = 0; c->strail_cap = 0;
+    const size_t B = (size_t) n_streams, rows = 2 * B;
+    const size_t kv = (size_t) g.n_layers * g.n_kv_head * n_ctx * g.head_dim;
+    const size_t ckv = (size_t) g.cp_layers * g.n_kv_head * 16 * g.head_dim;
+    const int kmax = std::max(std::max(d, qd), g.ffn_size);
+    if (dev_alloc_t(c, &c->skc, B * kv) || dev_alloc_t(c, &c->svc, B * kv) || dev_alloc_t(c, &c->scpk, B * ckv) ||
+        dev_alloc_t(c, &c->scpv, B * ckv) || dev_alloc_t(c, &c->sst, B) || dev_alloc_t(c, &c->sparams, B) ||
+        dev_alloc_t(c, &c->sseen, B * g.codec_vocab) || dev_alloc_t(c, &c->sntrail, B) ||
+        dev_alloc_t(c, &c->spad, B * d) || dev_alloc_t(c, &c->shidden, B * d) ||
+        dev_alloc_t(c, &c->slogits, B * g.codec_vocab) || dev_alloc_t(c, &c->scplogits, B * g.cp_vocab) ||
+        dev_alloc_t(c, &c->sstage, B * 2 * d) || dev_alloc_t(c, &c->bxa, rows * d) || dev_alloc_t(c, &c->bxb, rows * d) ||
+        dev_alloc_t(c, &c->bqkv, rows * qkvd) || dev_alloc_t(c, &c->batt, rows * qd) ||
+        dev_alloc_t(c, &c->bg, rows * g.ffn_size) || dev_alloc_t(c, &c->bu, rows * g.ffn_size) ||
+        dev_alloc_t(c, &c->bf, rows * g.ffn_size) || dev_alloc_t(c, &c->bq, rows * kmax) ||
+        dev_alloc_t(c, &c->bdx, rows * (kmax / kQK)))
+        return -1;
+    HIP_OK(hipMemsetAsync(c->skc, 0, B * kv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->svc, 0, B * kv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->scpk, 0, B * ckv * 2, c->stream));
+    HIP_OK(hipMemsetAsync(c->scpv, 0, B * ckv * 2, c->stream));
+    c->nb = n_streams;
+    c->sb_ctx = n_ctx;
+    c->s_emitted.assign(B, 0);
+    return sync(c);
+}
+
+int q3t_dev_stream_prefill(q3t_dev * c, int32_t stream, const float * embd, int32_t n) {
+    if (!c || !embd) return -1;
+    if (stream < 0 || stream >= c->nb) return fail(c, "stream index out of range (q3t_dev_streams_reserve first)");
+    if (n < 1 || n > c->sb_ctx) return fail(c, "Context length exceeded");
+    if (c->n_ctx != c->sb_ctx) return fail(c, "KV cache re-reserved since q3t_dev_streams_reserve; reserve the streams again");
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    const size_t kv = (size_t) g.n_layers * g.n_kv_head * c->sb_ctx * g.head_dim;
+    // run the single-stream prefill against this stream's cache
+    uint16_t * kc0 = c->kc, * vc0 = c->vc;
+    c->kc = c->skc + stream * kv;
+    c->vc = c->svc + stream * kv;
+    const int rc = q3t_dev_prefill(c, embd, n, 0, nullptr, nullptr);
+    c->kc = kc0;
+    c->vc = vc0;
+    if (rc) return rc;
+    HIP_OK(hipMemcpyAsync(c->slogits + (size_t) stream * g.codec_vocab, c->logits, (size_t) g.codec_vocab * 4,
+                          hipMemcpyDeviceToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->shidden + (size_t) stream * g.hidden_size, c->hidden, (size_t) g.hidden_size * 4,
+                          hipMemcpyDeviceToDevice, c->stream));
+    return sync(c);
+}
+
+int q3t_dev_streams_begin(q3t_dev * c, const q3t_frame_args * args) {
+    if (!c || !args) return -1;
+    if (c->nb < 1) return fail(c, "q3t_dev_streams_reserve first");
+    if (c->n_ctx != c->sb_ctx) return fail(c, "KV cache re-reserved since q3t_dev_streams_reserve; reserve the streams again");
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, B = c->nb;
+    int max_len = 0, max_trail = 1;
+    for (int b = 0; b < B; ++b) {
+        const q3t_frame_args & a = args[b];
+        if (!a.tts_pad) return fail(c, "tts_pad row is null");
+        if (a.n_trailing < 0 || (a.n_trailing > 0 && !a.trailing)) return fail(c, "bad trailing rows");
+        if (a.max_len < 0 || a.max_len >= (1 << 19)) return fail(c, "max_len out of range");
+        if (a.n_past < 1 || a.n_past + a.max_len > c->sb_ctx) return fail(c, "Context length exceeded");
+        max_len = std::max(max_len, a.max_len);
+        max_trail = std::max(max_trail, a.n_trailing);
+    }
+    if (max_len > c->scodes_cap || max_trail > c->strail_cap) {
+        if (c->scodes) dev_free(c, c->scodes);
+        if (c->strail) dev_free(c, c->strail);
+        c->scodes = nullptr; c->strail = nullptr;
+        const int cap = std::max(max_len, c->scodes_cap), tcap = std::max(max_trail, c->strail_cap);
+        if (dev_alloc_t(c, &c->scodes, (size_t) B * std::max(cap, 1) * 16) ||
+            dev_alloc_t(c, &c->strail, (size_t) B * tcap * d))
+            return -1;
+        c->scodes_cap = std::max(cap, 1);
+        c->strail_cap = tcap;
+        drop_stream_graph(c);
+    }
+    std::vector<FrameState> st(B);
+    std::vector<SampleParams> sp(B);
+    std::vector<int32_t> ntr(B);
+    for (int b = 0; b < B; ++b) {
+        const q3t_frame_args & a = args[b];
+        st[b] = FrameState{};
+        st[b].base_pos = a.n_past; st[b].talker_pos = a.n_past; st[b].max_frames = a.max_len;
+        sp[b] = SampleParams{};
+        sp[b].temperature = a.sampling.temperature; sp[b].top_k = a.sampling.top_k;
+        sp[b].rep_penalty = a.repetition_penalty; sp[b].eos_bias = a.eos_bias;
+        sp[b].target_frames = a.target_frames; sp[b].seed = a.sampling.seed;
+        ntr[b] = a.n_trailing;
+        if (a.n_trailing)
+            HIP_OK(hipMemcpyAsync(c->strail + (size_t) b * c->strail_cap * d, a.trailing, (size_t) a.n_trailing * d * 4,
+                                  hipMemcpyHostToDevice, c->stream));
+        HIP_OK(hipMemcpyAsync(c->spad + (size_t) b * d, a.tts_pad, (size_t) d * 4, hipMemcpyHostToDevice, c->stream));
+    }
+    HIP_OK(hipMemcpyAsync(c->sst, st.data(), sizeof(FrameState) * B, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->sparams, sp.data(), sizeof(SampleParams) * B, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->sntrail, ntr.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemsetAsync(c->sseen, 0, (size_t) B * g.codec_vocab, c->stream));
+    if (sync(c)) return -1;
+    if (!c->s_exec) {
+        HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        streams_frame_seq(c);
+        hipGraph_t graph = nullptr;
+        HIP_OK(hipStreamEndCapture(c->stream, &graph));
+        c->s_graph = graph;
+        HIP_OK(hipGraphInstantiate(&c->s_exec, graph, nullptr, nullptr, 0));
+    }
+    c->s_emitted.assign(B, 0);
+    c->s_launched = 0;
+    c->s_max = max_len;
+    c->s_ready = true;
+    c->run_us = 0.0;
+    c->run_frames = 0;
+    c->stats_streams = true;
+    return 0;
+}
+
+int q3t_dev_streams_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32_t * n_emitted_out, int32_t * eos_out) {
+    if (!c) return -1;
+    if (!c->s_ready) return fail(c, "q3t_dev_streams_begin not called");
+    HIP_OK(hipSetDevice(c->device));
+    const int B = c->nb;
+    const int n = std::max(0, std::min(n_frames, c->s_max - c->s_launched));
+    static const bool no_graph = [] { const char * e = std::getenv("Q3T_NO_GRAPH"); return e && e[0] == '1'; }();
+    if (!c->run_ev[0]) {
+        HIP_OK(hipEventCreate(&c->run_ev[0]));
+        HIP_OK(hipEventCreate(&c->run_ev[1]));
+    }
+    if (n > 0) HIP_OK(hipEventRecord(c->run_ev[0], c->stream));
+    for (int i = 0; i < n; ++i) {
+        if (no_graph) streams_frame_seq(c);
+        else HIP_OK(hipGraphLaunch(c->s_exec, c->stream));
+    }
+    if (n > 0) HIP_OK(hipEventRecord(c->run_ev[1], c->stream));
+    c->s_launched += n;
+    std::vector<FrameState> st(B);
+    HIP_OK(hipMemcpyAsync(st.data(), c->sst, sizeof(FrameState) * B, hipMemcpyDeviceToHost, c->stream));
+    if (sync(c)) return -1;
+    if (n > 0) {
+        float ms = 0.0f;
+        HIP_OK(hipEventElapsedTime(&ms, c->run_ev[0], c->run_ev[1]));
+        c->run_us += 1e3 * ms;
+        c->run_frames += n;
+    }
+    for (int b = 0; b < B; ++b) {
+        const int fresh = st[b].n_emitted - c->s_emitted[b];
+        if (fresh > 0 && codes_out)
+            HIP_OK(hipMemcpy(codes_out + (size_t) b * std::max(n_frames, 1) * 16,
+                             c->scodes + ((size_t) b * c->scodes_cap + c->s_emitted[b]) * 16, (size_t) fresh * 16 * 4,
+                             hipMemcpyDeviceToHost));
+        if (n_emitted_out) n_emitted_out[b] = std::max(fresh, 0);
+        if (eos_out) eos_out[b] = st[b].eos;
+        c->s_emitted[b] = st[b].n_emitted;
+    }
+    return 0;
+}
+
 int q3t_dev_frames_stats(q3t_dev * c, double * gpu_us_out, int64_t * frames_out, int32_t * path_out) {
     if (!c) return -1;
     if (gpu_us_out) *gpu_us_out = c->run_us;
     if (frames_out) *frames_out = c->run_frames;
-    if (path_out) *path_out = c->fk_ok ? 1 : 0;
+    if (path_out) *path_out = c->stats_streams ? 2 : c->fk_ok ? 1 : 0;
     return 0;
 }
 

@@ -244,6 +244,10 @@ struct AttnArgs {
     float scale;
     int32_t nt;
     float * probs_out;                             // optional [n_head][n_kv] (token 0)
+    // independent streams (blockIdx.z): element offsets per stream; 0 for one stream
+    int64_t kv_stream;                             // in kc / vc
+    int32_t qkv_stream, out_stream;                // in qkv / out (floats)
+    int32_t pos_stream, done_stream;               // in pos_ptr / done (int32)
 };
 
 constexpr int kHD = 128;
@@ -271,7 +275,13 @@ __device__ __forceinline__ float head_norm_rope(float v, const float * w, float 
 }
 
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
-    if (a.done && *a.done) return;
+    {
+        const int z = blockIdx.z;
+        if (a.done && a.done[(size_t) z * a.done_stream]) return;
+        a.kc += z * a.kv_stream; a.vc += z * a.kv_stream;
+        a.qkv += (size_t) z * a.qkv_stream; a.out += (size_t) z * a.out_stream;
+        if (a.pos_ptr) a.pos_ptr += (size_t) z * a.pos_stream;
+    }
     extern __shared__ __align__(16) char smem[];
     double * red = (double *) smem;                   // 4 doubles
     float * fred = (float *) (smem + 32);             // 4 floats
@@ -428,6 +438,10 @@ struct SampleArgs {
     const uint16_t * cp_embd[15];
     const float * trailing; int32_t n_trailing; const float * pad;
     int32_t d;
+    // independent streams (blockIdx.x = stream): st and params are arrays;
+    // element offsets per stream for the rest (0 for one stream)
+    int32_t logits_stream, seen_stream, stage_stream, codes_stream, hidden_stream, trailing_stream, pad_stream;
+    const int32_t * n_trailing_arr;   // per-stream trailing-row counts (NULL: n_trailing)
 };
 
 constexpr int kSampleThreads = 1024;
@@ -572,6 +586,18 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
 }
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
+    {
+        const int b = blockIdx.x;
+        a.st += b; a.params += b;
+        a.logits += (size_t) b * a.logits_stream;
+        a.seen += (size_t) b * a.seen_stream;
+        if (a.stage) a.stage += (size_t) b * a.stage_stream;
+        if (a.codes_out) a.codes_out += (size_t) b * a.codes_stream;
+        if (a.hidden) a.hidden += (size_t) b * a.hidden_stream;
+        if (a.trailing) a.trailing += (size_t) b * a.trailing_stream;
+        if (a.pad) a.pad += (size_t) b * a.pad_stream;
+        if (a.n_trailing_arr) a.n_trailing = a.n_trailing_arr[b];
+    }
     FrameState * st = a.st;
     __shared__ int32_t s_frame;
     if (threadIdx.x == 0) {

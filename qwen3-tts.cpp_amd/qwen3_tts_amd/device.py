@@ -20,7 +20,8 @@ EXPORTS = [
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
     "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_frames_begin",
-    "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_sync", "q3t_dev_time_kernel",
+    "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
+    "q3t_dev_streams_begin", "q3t_dev_streams_run", "q3t_dev_sync", "q3t_dev_time_kernel",
 ]
 
 
@@ -68,6 +69,10 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_sync.argtypes = [vp]
         lib.q3t_dev_frames_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
                                              ctypes.POINTER(i32)]
+        lib.q3t_dev_streams_reserve.argtypes = [vp, i32, i32]
+        lib.q3t_dev_stream_prefill.argtypes = [vp, i32, f32p, i32]
+        lib.q3t_dev_streams_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
+        lib.q3t_dev_streams_run.argtypes = [vp, i32, vp, vp, vp]
         lib.q3t_dev_time_kernel.argtypes = [vp, i32, i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         _lib = lib
     return _lib
@@ -197,9 +202,44 @@ class Device:
                     "frames_run")
         return out[: n.value].copy(), bool(eos.value)
 
+    def streams_reserve(self, n_streams, n_ctx):
+        self._check(self.lib.q3t_dev_streams_reserve(self.h, n_streams, n_ctx), "streams_reserve")
+        self.n_streams = n_streams
+
+    def stream_prefill(self, stream, embd):
+        embd = np.ascontiguousarray(embd, dtype=np.float32)
+        self._check(self.lib.q3t_dev_stream_prefill(self.h, stream, _p(embd), embd.shape[0]), "stream_prefill")
+
+    def streams_begin(self, streams):
+        """streams: one dict per stream with the keyword arguments of
+        frames_begin (trailing, tts_pad, n_past, max_len, ...)."""
+        args = (CFrameArgs * len(streams))()
+        keep = []
+        for b, kw in enumerate(streams):
+            tr = np.ascontiguousarray(kw["trailing"], dtype=np.float32)
+            pad = np.ascontiguousarray(kw["tts_pad"], dtype=np.float32)
+            keep += [tr, pad]
+            args[b] = CFrameArgs(_p(tr), tr.shape[0], _p(pad), kw["n_past"], kw["max_len"],
+                                 kw.get("repetition_penalty", 1.05), kw.get("eos_bias", 0.0),
+                                 kw.get("target_frames", 0),
+                                 CSampling(kw.get("temperature", 0.0), kw.get("top_k", 0), kw.get("seed", 0)))
+        self._keep = keep
+        self._check(self.lib.q3t_dev_streams_begin(self.h, args), "streams_begin")
+
+    def streams_run(self, n_frames):
+        """Advances every live stream by up to n_frames frames; returns a list
+        of per-stream [frames][16] code arrays and a list of EOS flags."""
+        B = self.n_streams
+        out = np.empty((B, max(n_frames, 1), self.cfg.n_codebooks), np.int32)
+        n = np.zeros(B, np.int32)
+        eos = np.zeros(B, np.int32)
+        self._check(self.lib.q3t_dev_streams_run(self.h, n_frames, _p(out), _p(n), _p(eos)), "streams_run")
+        return [out[b, : n[b]].copy() for b in range(B)], [bool(e) for e in eos]
+
     def frames_stats(self):
-        """(GPU microseconds of frame launches, frames launched, path) since
-        frames_begin; path 1 = persistent frame kernel, 0 = kernel graph."""
+        """(GPU microseconds of frame launches, frame launches, path) since
+        frames_begin / streams_begin; path 1 = persistent frame kernel,
+        0 = kernel graph, 2 = multi-stream graph."""
         us = ctypes.c_double()
         n = ctypes.c_int64()
         path = ctypes.c_int32()

@@ -117,3 +117,42 @@ def generate(dev, cfg, text, speaker=None, max_len=64, language_id=2050, repetit
     if not out:
         return np.zeros((0, cfg.n_codebooks), np.int32)
     return np.stack(out).astype(np.int32)
+
+
+def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None):
+    """Batched form of generate() over independent utterances.
+
+    `streams` is a list of dicts, one per utterance, each with `prefill_rows`
+    ((prefill, trailing, tts_pad) as build_prefill returns them) and the
+    generate() controls max_len, repetition_penalty, temperature, top_k,
+    eos_bias, target_frames, seed.  Every stream's codes equal what
+    generate() returns for it alone; all streams advance together, one
+    device graph launch per frame.  Returns a list of [n_frames][16] arrays.
+    """
+    if not streams:
+        return []
+    need = max(s["prefill_rows"][0].shape[0] + s.get("max_len", 64) + 8 for s in streams)
+    dev.streams_reserve(len(streams), max(need, n_ctx or 0))
+    args = []
+    for b, s in enumerate(streams):
+        prefill, trailing, pad = s["prefill_rows"]
+        dev.stream_prefill(b, prefill)
+        args.append(dict(trailing=trailing, tts_pad=pad, n_past=prefill.shape[0], max_len=s.get("max_len", 64),
+                         repetition_penalty=s.get("repetition_penalty", 1.05), eos_bias=s.get("eos_bias", 0.0),
+                         target_frames=s.get("target_frames", 0), temperature=s.get("temperature", 0.9),
+                         top_k=s.get("top_k", 50), seed=s.get("seed", 0)))
+    dev.streams_begin(args)
+    out = [[] for _ in streams]
+    live = [a["max_len"] > 0 for a in args]
+    produced = 0
+    max_len = max(a["max_len"] for a in args)
+    while produced < max_len and any(live):
+        n = min(chunk, max_len - produced)
+        codes, eos = dev.streams_run(n)
+        for b in range(len(streams)):
+            if codes[b].shape[0]:
+                out[b].append(codes[b])
+            if eos[b] or sum(c.shape[0] for c in out[b]) >= args[b]["max_len"]:
+                live[b] = False
+        produced += n
+    return [np.concatenate(o).astype(np.int32) if o else np.zeros((0, cfg.n_codebooks), np.int32) for o in out]
