@@ -8,6 +8,7 @@
 #include "q3t_kernels.h"
 #include "q3t_frame_kernel.h"
 #include "q3t_prefill.h"
+#include "q3t_streams.h"
 
 #include <hip/hip_runtime.h>
 
@@ -82,8 +83,11 @@ struct q3t_dev {
     float * slogits = nullptr, * scplogits = nullptr; // [stream][codec_vocab], [stream][cp_vocab]
     float * sstage = nullptr;                         // [stream][2][d]
     float * bxa = nullptr, * bxb = nullptr, * bqkv = nullptr, * batt = nullptr;   // [2 * nb][...]
-    float * bg = nullptr, * bu = nullptr, * bf = nullptr;
-    int8_t * bq = nullptr; float * bdx = nullptr;
+    int8_t * bq8 = nullptr; float * bdx8 = nullptr;   // Q8_0 rows [2 * nb][max(qd, ffn)] and scales
+    float * srs = nullptr;                            // RMSNorm row scales [2 * nb]
+    // split-K partials and per-tile tickets, one set per GEMM call type
+    // (QKV, Wo, gate/up, down): a set's tickets advance by S per launch
+    uint64_t * spart[4] = {}; uint32_t * scnt[4] = {}; int32_t * serr = nullptr;
     hipGraphExec_t s_exec = nullptr; hipGraph_t s_graph = nullptr;
     int32_t s_launched = 0, s_max = 0; bool s_ready = false;
     bool stats_streams = false;    // frame statistics describe the multi-stream loop
@@ -1276,6 +1280,10 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     return 0;
 }
 
+}  // extern "C"
+
+namespace {
+
 // ------------------------------------------------------------ multi-stream
 // nb independent utterances share the weights: every GEMV of the frame
 // becomes an (nb x nt)-row GEMM on the int8 MFMA kernel, attention and the
@@ -1303,35 +1311,155 @@ struct StreamKV {
     const int32_t * pos_ptr; int pos_const;
 };
 
+// The three shapes of decode GEMM a layer needs (ms::k_gemm_sk):
+//   QKV      RMSNorm'd fp32 rows quantised in registers, fp32 out
+//   PROJ     pre-quantised rows in (attention / SwiGLU output), + residual
+//   GATE_UP  RMSNorm'd rows, gate and up matrices, SwiGLU, Q8_0 out
+enum GemmKind { G_QKV = 0, G_PROJ = 1, G_GATE_UP = 2 };
+constexpr int kGemmKB[3] = {2, 4, 2};       // max Q8_0 blocks per wave
+constexpr int kGemmMT[3] = {1, 1, 2};       // 16-row tiles per workgroup
+constexpr int kGemmS[3] = {4, 8, 4};        // preferred K splits
+
+template <int NT, int KIND>
+const void * gemm_kernel() {
+    if (KIND == G_QKV) return (const void *) ms::k_gemm_sk<NT, 1, false, ms::IN_NORM, ms::OUT_F32, kGemmKB[G_QKV]>;
+    if (KIND == G_PROJ) return (const void *) ms::k_gemm_sk<NT, 1, false, ms::IN_Q8, ms::OUT_RESID, kGemmKB[G_PROJ]>;
+    return (const void *) ms::k_gemm_sk<NT, 2, true, ms::IN_NORM, ms::OUT_SWIGLU_Q8, kGemmKB[G_GATE_UP]>;
+}
+
+template <int KIND>
+const void * gemm_kernel_nt(int nt) {
+    switch (nt) {
+        case 1: return gemm_kernel<1, KIND>();
+        case 2: return gemm_kernel<2, KIND>();
+        case 3: return gemm_kernel<3, KIND>();
+        default: return gemm_kernel<4, KIND>();
+    }
+}
+
+const void * gemm_fn(int kind, int nt) {
+    return kind == G_QKV ? gemm_kernel_nt<G_QKV>(nt) : kind == G_PROJ ? gemm_kernel_nt<G_PROJ>(nt)
+                                                                      : gemm_kernel_nt<G_GATE_UP>(nt);
+}
+
+// K splits for a contraction of nb Q8_0 blocks: the largest S <= the kind's
+// preference with nb % (4 S) == 0 and at most KB blocks per wave; 0 if none.
+int gemm_splits(int kind, int nb) {
+    for (int S = kGemmS[kind]; S >= 1; S >>= 1)
+        if (nb % (ms::kWaves * S) == 0 && nb / (ms::kWaves * S) <= kGemmKB[kind]) return S;
+    return 0;
+}
+
+size_t gemm_lds(int kind, int nt, int K) {
+    const int S = gemm_splits(kind, K / kQK);
+    return ms::gemm_sk_lds_bytes(nt, kGemmMT[kind], kind == G_GATE_UP, S ? K / kQK / S : 0);
+}
+
+// tagged words of the partials one launch may store: tiles x S x 2 per value x values per lane x 64 lanes
+size_t gemm_part_words(int kind, int nt, int N, int K) {
+    const int mt = kGemmMT[kind], nw = kind == G_GATE_UP ? 2 : 1;
+    return (size_t) (N / (ms::kRows * mt)) * gemm_splits(kind, K / kQK) * 2 * nw * mt * nt * 4 * 64;
+}
+
+// call types sharing a ticket/partial set
+enum GemmSite { S_QKV = 0, S_WO = 1, S_GATE_UP = 2, S_DOWN = 3 };
+
+void gemm_rows(q3t_dev * c, int kind, int site, ms::GemmArgs a) {
+    const int nt = (a.n + 15) / 16;
+    const int S = gemm_splits(kind, a.K / kQK);
+    a.part = c->spart[site]; a.cnt = c->scnt[site]; a.err = c->serr;
+    void * args[] = {(void *) &a};
+    (void) hipLaunchKernel(gemm_fn(kind, nt), dim3(a.N / (ms::kRows * kGemmMT[kind]), S), dim3(ms::kThreads), args,
+                           gemm_lds(kind, nt, a.K), c->stream);
+}
+
+// Contraction length of each decode GEMM kind: the normed inputs are model
+// rows (d), the projections read attention or SwiGLU rows.
+int gemm_k(int kind, int d, int kproj) { return kind == G_PROJ ? kproj : d; }
+
+// Allows each decode GEMM its dynamic LDS.
+hipError_t allow_gemm_lds(int d, int kproj) {
+    for (int kind = 0; kind < 3; ++kind)
+        for (int nt = 1; nt <= 4; ++nt) {
+            const hipError_t e = hipFuncSetAttribute(gemm_fn(kind, nt), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int) gemm_lds(kind, nt, gemm_k(kind, d, kproj)));
+            if (e != hipSuccess) return e;
+        }
+    return hipSuccess;
+}
+
+// RMSNorm row scales of n rows of width K into c->srs.
+void row_scales(q3t_dev * c, const float * x, int xs, int K, int n) {
+    hipLaunchKernelGGL(ms::k_row_scale, dim3(n), dim3(kBlock), 0, c->stream, x, xs, K, c->cfg.rms_eps, c->srs);
+}
+
+void attn_gqa(q3t_dev * c, const LayerDev & L, const StreamKV & kv) {
+    const q3t_config & g = c->cfg;
+    const int qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim, G = g.n_head / g.n_kv_head;
+    ms::GqaArgs a{};
+    a.qkv = c->bqkv; a.qkv_stride = qkvd;
+    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
+    a.rope_cos = kv.rc; a.rope_sin = kv.rs;
+    a.kc = kv.kc; a.vc = kv.vc; a.kv_stream = kv.stream;
+    a.n_ctx = kv.n_ctx; a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
+    a.pos = kv.pos_ptr; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.out = c->batt; a.out_stride = qd;
+    a.out_q = c->bq8; a.out_dx = c->bdx8;
+    a.scale = 1.0f / std::sqrt((float) g.head_dim);
+    const dim3 grid(g.n_kv_head, c->nb), block(ms::kAThreads);
+    const size_t lds = ms::attn_gqa_lds_bytes(G, kv.n_ctx);
+    if (G == 1) hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, lds, c->stream, a);
+    else if (G == 2) hipLaunchKernelGGL(ms::k_attn_gqa<2>, grid, block, lds, c->stream, a);
+    else hipLaunchKernelGGL(ms::k_attn_gqa<4>, grid, block, lds, c->stream, a);
+}
+
 // One decoder layer over n = nb * nt rows (stream-major); output rows in c->bxa.
+// Four decode-shaped GEMMs and one attention launch (the talker's GQA kernel
+// for one token per stream; for the code predictor's 16-position cache the
+// per-head kernel over nt tokens).  Activations pass between them as fp32
+// residual rows (RMSNorm + quantisation inside the consuming GEMM) or as
+// Q8_0 rows quantised by the producer (attention output, SwiGLU output).
 static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, int nt, const StreamKV & kv) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int ffn = g.ffn_size, n = c->nb * nt;
-    pf_quant(c, x, n, d, L.attn_norm, d, c->bq, c->bdx);
-    pf_gemm(c, L.qkv, qkvd, d, n, c->bqkv, nullptr, -1, c->bq, c->bdx);
-    AttnArgs a{};
-    a.qkv = c->bqkv; a.qkv_stride = qkvd; a.qkv_stream = nt * qkvd;
-    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
-    a.rope_cos = kv.rc; a.rope_sin = kv.rs;
-    a.kc = kv.kc; a.vc = kv.vc; a.n_ctx = kv.n_ctx; a.kv_stream = kv.stream;
-    a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
-    a.pos_ptr = kv.pos_ptr; a.pos_const = kv.pos_const; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
-    a.out = c->batt; a.out_stride = qd; a.out_stream = nt * qd;
-    a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
-    a.scale = 1.0f / std::sqrt((float) g.head_dim);
-    a.nt = nt;
-    hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
-    pf_quant(c, c->batt, n, qd, nullptr, qd, c->bq, c->bdx);
-    pf_gemm(c, L.wo, d, qd, n, c->bxb, x, d, c->bq, c->bdx);
-    pf_quant(c, c->bxb, n, d, L.ffn_norm, d, c->bq, c->bdx);
-    pf_gemm(c, L.wg, ffn, d, n, c->bg, nullptr, -1, c->bq, c->bdx);
-    pf_gemm(c, L.wu, ffn, d, n, c->bu, nullptr, -1, c->bq, c->bdx);
-    const size_t cnt = (size_t) n * ffn;
-    hipLaunchKernelGGL(pf::k_swiglu_rows, dim3((unsigned) std::min<size_t>((cnt + kBlock - 1) / kBlock, 4096)),
-                       dim3(kBlock), 0, c->stream, (const float *) c->bg, (const float *) c->bu, c->bf, cnt);
-    pf_quant(c, c->bf, n, ffn, nullptr, ffn, c->bq, c->bdx);
-    pf_gemm(c, L.wd, d, ffn, n, c->bxa, c->bxb, d, c->bq, c->bdx);
+    row_scales(c, x, d, d, n);
+    ms::GemmArgs q{};
+    q.W = (const int8_t *) L.qkv.data; q.Wd = L.qkv.scales; q.N = qkvd; q.K = d;
+    q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
+    gemm_rows(c, G_QKV, S_QKV, q);
+    if (kv.pos_ptr && nt == 1) {
+        attn_gqa(c, L, kv);
+    } else {
+        AttnArgs a{};
+        a.qkv = c->bqkv; a.qkv_stride = qkvd; a.qkv_stream = nt * qkvd;
+        a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
+        a.rope_cos = kv.rc; a.rope_sin = kv.rs;
+        a.kc = kv.kc; a.vc = kv.vc; a.n_ctx = kv.n_ctx; a.kv_stream = kv.stream;
+        a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
+        a.pos_ptr = kv.pos_ptr; a.pos_const = kv.pos_const; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
+        a.out = c->batt; a.out_stride = qd; a.out_stream = nt * qd;
+        a.out_q = c->bq8; a.out_dx = c->bdx8;
+        a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
+        a.scale = 1.0f / std::sqrt((float) g.head_dim);
+        a.nt = nt;
+        hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
+    }
+    ms::GemmArgs o{};
+    o.W = (const int8_t *) L.wo.data; o.Wd = L.wo.scales; o.N = d; o.K = qd;
+    o.q = c->bq8; o.qdx = c->bdx8; o.n = n; o.y = c->bxb; o.ys = d; o.res = x; o.rs = d;
+    gemm_rows(c, G_PROJ, S_WO, o);
+    row_scales(c, c->bxb, d, d, n);
+    ms::GemmArgs f{};
+    f.W = (const int8_t *) L.wg.data; f.Wd = L.wg.scales; f.W2 = (const int8_t *) L.wu.data; f.W2d = L.wu.scales;
+    f.N = ffn; f.K = d; f.x = c->bxb; f.xs = d; f.rscale = c->srs; f.norm_w = L.ffn_norm; f.n = n;
+    f.yq = c->bq8; f.ydx = c->bdx8;
+    gemm_rows(c, G_GATE_UP, S_GATE_UP, f);
+    ms::GemmArgs dn{};
+    dn.W = (const int8_t *) L.wd.data; dn.Wd = L.wd.scales; dn.N = d; dn.K = ffn;
+    dn.q = c->bq8; dn.qdx = c->bdx8; dn.n = n; dn.y = c->bxa; dn.ys = d; dn.res = c->bxb; dn.rs = d;
+    gemm_rows(c, G_PROJ, S_DOWN, dn);
 }
 
 static SampleArgs stream_sample_args(q3t_dev * c, int mode, int group) {
@@ -1398,12 +1526,16 @@ static void streams_frame_seq(q3t_dev * c) {
     gemv_rows(c, h, B);
 }
 
+}  // namespace
+
+extern "C" {
+
 int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     if (!c) return -1;
     HIP_OK(hipSetDevice(c->device));
     if (resolve(c)) return -1;
     const q3t_config & g = c->cfg;
-    if (n_streams < 1 || n_streams > 64) return fail(c, "n_streams must be in [1, 64]");
+    if (n_streams < 1 || n_streams > 32) return fail(c, "n_streams must be in [1, 32]");
     if (n_ctx < 1) return fail(c, "n_ctx must be > 0");
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
@@ -1412,9 +1544,27 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
             return fail(c, "multi-stream decode needs Q8_0 layer weights (int8 MFMA GEMMs)");
     }
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
-    if (g.head_dim != 128 || d % 128 || qd % 128 || g.ffn_size % 128 || qkvd % pf::kTile || d % pf::kTile ||
-        g.ffn_size % pf::kTile || g.cp_ffn != g.ffn_size || g.cp_hidden != d)
+    const int G = g.n_kv_head > 0 ? g.n_head / g.n_kv_head : 0;
+    // decode GEMM: K a multiple of 8 waves x 32, at most 12 blocks per wave; N a multiple of 16
+    // decode GEMMs: every contraction splits into 4-wave slices of at most KB
+    // blocks per wave; N a multiple of 16 (32 for gate/up)
+    if (g.head_dim != 128 || d % kQK || qd % kQK || g.ffn_size % kQK || !gemm_splits(G_QKV, d / kQK) ||
+        !gemm_splits(G_GATE_UP, d / kQK) || !gemm_splits(G_PROJ, qd / kQK) || !gemm_splits(G_PROJ, g.ffn_size / kQK) ||
+        qkvd % ms::kRows || d % ms::kRows || g.ffn_size % (2 * ms::kRows) || g.cp_ffn != g.ffn_size ||
+        g.cp_hidden != d || g.n_head % g.n_kv_head || !(G == 1 || G == 2 || G == 4))
         return fail(c, "multi-stream decode: unsupported model widths");
+    int max_lds = 0;
+    HIP_OK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device));
+    const size_t al = ms::attn_gqa_lds_bytes(G, n_ctx);
+    const int kproj = std::max(qd, g.ffn_size);
+    size_t gl = 0;
+    for (int kind = 0; kind < 3; ++kind) gl = std::max(gl, gemm_lds(kind, 4, gemm_k(kind, d, kproj)));
+    if (gl > (size_t) max_lds) return fail(c, "multi-stream decode: GEMM LDS exceeds the device limit");
+    if (al > (size_t) max_lds) return fail(c, "multi-stream decode: n_ctx too large for the attention kernel's LDS");
+    HIP_OK(allow_gemm_lds(d, kproj));
+    HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
+    HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
+    HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
     // the streams' talker caches share the context's RoPE tables and KV layout stride
     if (c->n_ctx != n_ctx && q3t_dev_kv_reserve(c, n_ctx)) return -1;
     HIP_OK(hipStreamSynchronize(c->stream));
@@ -1422,14 +1572,18 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     for (void * p : {(void *) c->skc, (void *) c->svc, (void *) c->scpk, (void *) c->scpv, (void *) c->sst,
                      (void *) c->sparams, (void *) c->sseen, (void *) c->sntrail, (void *) c->spad, (void *) c->shidden,
                      (void *) c->slogits, (void *) c->scplogits, (void *) c->sstage, (void *) c->bxa, (void *) c->bxb,
-                     (void *) c->bqkv, (void *) c->batt, (void *) c->bg, (void *) c->bu, (void *) c->bf, (void *) c->bq,
-                     (void *) c->bdx, (void *) c->scodes, (void *) c->strail})
+                     (void *) c->bqkv, (void *) c->batt, (void *) c->bq8, (void *) c->bdx8, (void *) c->srs,
+                     (void *) c->serr, (void *) c->scodes, (void *) c->strail})
         if (p) dev_free(c, p);
+    for (int i = 0; i < 4; ++i) {
+        if (c->spart[i]) dev_free(c, c->spart[i]);
+        if (c->scnt[i]) dev_free(c, c->scnt[i]);
+        c->spart[i] = nullptr; c->scnt[i] = nullptr;
+    }
     c->scodes = nullptr; c->strail = nullptr; c->scodes_cap = 0; c->strail_cap = 0;
     const size_t B = (size_t) n_streams, rows = 2 * B;
     const size_t kv = (size_t) g.n_layers * g.n_kv_head * n_ctx * g.head_dim;
     const size_t ckv = (size_t) g.cp_layers * g.n_kv_head * 16 * g.head_dim;
-    const int kmax = std::max(std::max(d, qd), g.ffn_size);
     if (dev_alloc_t(c, &c->skc, B * kv) || dev_alloc_t(c, &c->svc, B * kv) || dev_alloc_t(c, &c->scpk, B * ckv) ||
         dev_alloc_t(c, &c->scpv, B * ckv) || dev_alloc_t(c, &c->sst, B) || dev_alloc_t(c, &c->sparams, B) ||
         dev_alloc_t(c, &c->sseen, B * g.codec_vocab) || dev_alloc_t(c, &c->sntrail, B) ||
@@ -1437,10 +1591,25 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
         dev_alloc_t(c, &c->slogits, B * g.codec_vocab) || dev_alloc_t(c, &c->scplogits, B * g.cp_vocab) ||
         dev_alloc_t(c, &c->sstage, B * 2 * d) || dev_alloc_t(c, &c->bxa, rows * d) || dev_alloc_t(c, &c->bxb, rows * d) ||
         dev_alloc_t(c, &c->bqkv, rows * qkvd) || dev_alloc_t(c, &c->batt, rows * qd) ||
-        dev_alloc_t(c, &c->bg, rows * g.ffn_size) || dev_alloc_t(c, &c->bu, rows * g.ffn_size) ||
-        dev_alloc_t(c, &c->bf, rows * g.ffn_size) || dev_alloc_t(c, &c->bq, rows * kmax) ||
-        dev_alloc_t(c, &c->bdx, rows * (kmax / kQK)))
+        dev_alloc_t(c, &c->bq8, rows * std::max(qd, g.ffn_size)) ||
+        dev_alloc_t(c, &c->bdx8, rows * (std::max(qd, g.ffn_size) / kQK)) || dev_alloc_t(c, &c->srs, rows))
         return -1;
+    {
+        // tickets and tags start at 0 (a tag is >= 1), zeroed here, outside any graph
+        const int nt = (int) ((rows + 15) / 16);
+        const size_t words[4] = {gemm_part_words(G_QKV, nt, qkvd, d), gemm_part_words(G_PROJ, nt, d, qd),
+                                 gemm_part_words(G_GATE_UP, nt, g.ffn_size, d),
+                                 gemm_part_words(G_PROJ, nt, d, g.ffn_size)};
+        const size_t tiles = (size_t) std::max(qkvd, std::max(d, g.ffn_size)) / ms::kRows;
+        for (int i = 0; i < 4; ++i) {
+            const size_t nw = std::max(words[i], (size_t) 64);
+            if (dev_alloc_t(c, &c->spart[i], nw) || dev_alloc_t(c, &c->scnt[i], tiles)) return -1;
+            HIP_OK(hipMemsetAsync(c->spart[i], 0, nw * 8, c->stream));
+            HIP_OK(hipMemsetAsync(c->scnt[i], 0, tiles * sizeof(uint32_t), c->stream));
+        }
+        if (dev_alloc_t(c, &c->serr, 1)) return -1;
+        HIP_OK(hipMemsetAsync(c->serr, 0, sizeof(int32_t), c->stream));
+    }
     HIP_OK(hipMemsetAsync(c->skc, 0, B * kv * 2, c->stream));
     HIP_OK(hipMemsetAsync(c->svc, 0, B * kv * 2, c->stream));
     HIP_OK(hipMemsetAsync(c->scpk, 0, B * ckv * 2, c->stream));
@@ -1562,8 +1731,14 @@ int q3t_dev_streams_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int3
     if (n > 0) HIP_OK(hipEventRecord(c->run_ev[1], c->stream));
     c->s_launched += n;
     std::vector<FrameState> st(B);
+    int32_t err = 0;
     HIP_OK(hipMemcpyAsync(st.data(), c->sst, sizeof(FrameState) * B, hipMemcpyDeviceToHost, c->stream));
+    HIP_OK(hipMemcpyAsync(&err, c->serr, sizeof err, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
+    if (err) {
+        c->s_ready = false;
+        return fail(c, "multi-stream decode: a split-K partial never arrived (device wait timed out)");
+    }
     if (n > 0) {
         float ms = 0.0f;
         HIP_OK(hipEventElapsedTime(&ms, c->run_ev[0], c->run_ev[1]));

@@ -248,6 +248,9 @@ struct AttnArgs {
     int64_t kv_stream;                             // in kc / vc
     int32_t qkv_stream, out_stream;                // in qkv / out (floats)
     int32_t pos_stream, done_stream;               // in pos_ptr / done (int32)
+    // optional Q8_0 copy of the output rows for the next projection:
+    // out_q [NT][out_stride] int8, out_dx [NT][out_stride / 32] (same stream offsets)
+    int8_t * out_q; float * out_dx;
 };
 
 constexpr int kHD = 128;
@@ -274,12 +277,26 @@ __device__ __forceinline__ float head_norm_rope(float v, const float * w, float 
     return o;
 }
 
+// Q8_0 quantisation of one value per lane, a block being 32 consecutive lanes
+// (d = amax/127 as fp16, q = rint(x * 127/amax)); the block's first lane
+// stores the scale.
+__device__ __forceinline__ int8_t quant_lane32(float v, float * dx, bool first) {
+    float am = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    const float d = am / 127.0f;
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    if (first) *dx = round_f16(d);
+    return (int8_t) (int) rintf(v * id);
+}
+
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     {
         const int z = blockIdx.z;
         if (a.done && a.done[(size_t) z * a.done_stream]) return;
         a.kc += z * a.kv_stream; a.vc += z * a.kv_stream;
         a.qkv += (size_t) z * a.qkv_stream; a.out += (size_t) z * a.out_stream;
+        if (a.out_q) { a.out_q += (size_t) z * a.out_stream; a.out_dx += (size_t) z * (a.out_stream / kQK); }
         if (a.pos_ptr) a.pos_ptr += (size_t) z * a.pos_stream;
     }
     extern __shared__ __align__(16) char smem[];
@@ -409,7 +426,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     __syncthreads();
     if (t < kHD) {
         const double r = (pv[t] + pv[kHD + t]) + (pv[2 * kHD + t] + pv[3 * kHD + t]);
-        a.out[(size_t) tok * a.out_stride + h * kHD + t] = (float) r;
+        const float o = (float) r;
+        a.out[(size_t) tok * a.out_stride + h * kHD + t] = o;
+        if (a.out_q) {
+            // Q8_0 block = 32 consecutive threads of a fully active wave
+            const size_t e = (size_t) tok * a.out_stride + h * kHD + t;
+            a.out_q[e] = quant_lane32(o, a.out_dx + e / kQK, (t & 31) == 0);
+        }
     }
 }
 
