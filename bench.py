@@ -105,6 +105,59 @@ def prefill_bench(args, cfg, w):
         "mfma_util": round(gemm_ops / dt / 5.0e15, 4) if args.weights == "q8_0" else None}))
 
 
+def long_bench(args, cfg, w):
+    """Long-context sampled decode: prefill rows [N(0,1) speaker row;
+    text_proj(2048 uniform ids)] through one prefill call, then args.steps
+    sampled frames (temperature 0.9, top-k 50, repetition penalty 1.05, fixed
+    seed; EOS biased off so every frame does full work) while the talker
+    context grows from 2049 to 2049 + warmup + steps positions.  Reports the
+    prefill time and the decode frames/s with the HBM rate of the frame's
+    algorithmic bytes at the mid-run context."""
+    from qwen3_tts_amd.device import Device
+    rng = np.random.default_rng(44)
+    dev = Device(cfg, 0)
+    dev.upload_weights(w)
+    ids = rng.integers(0, cfg.text_vocab, args.long_prompt).astype(np.int32)
+    spk = rng.standard_normal((1, cfg.hidden_size)).astype(np.float32)
+    rows = np.concatenate([spk, dev.text_proj(ids)]).astype(np.float32)
+    pad = dev.text_proj([cfg.tts_pad_id])[0]
+    plen = rows.shape[0]
+    total = args.warmup + args.steps
+    dev.kv_reserve(plen + total + 8)
+    dev.prefill(rows[:16], 0, want_hidden=False)   # first-call set-up outside the timing
+    t0 = time.perf_counter()
+    dev.prefill(rows, 0, want_hidden=False)
+    prefill_s = time.perf_counter() - t0
+    dev.frames_begin(pad[None], pad, plen, total, repetition_penalty=1.05, temperature=args.temperature,
+                     top_k=50 if args.temperature > 0 else 0, eos_bias=-1e4, seed=1234)
+    if args.warmup:
+        _, eos = dev.frames_run(args.warmup)
+        assert not eos
+    dev.sync()
+    t0 = time.perf_counter()
+    codes, eos = dev.frames_run(args.steps)
+    elapsed = time.perf_counter() - t0
+    us, n, path = dev.frames_stats()
+    dev.close()
+    assert not eos and codes.shape[0] == args.steps
+    fps = args.steps / elapsed
+    fbytes = frame_bytes(cfg, w.tensors, plen + args.warmup + args.steps // 2)
+    print(json.dumps({
+        "metric": "codec frames/sec, long-context sampled decode", "value": round(fps, 2), "unit": "frames/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if args.weights == "q8_0" else "f16", "data": "synthetic (seeded weights, uniform ids)",
+        "config": {"workload": f"{args.weights.upper()} 0.6B shapes, {plen}-row prefill (speaker row + text_proj of "
+                               f"{args.long_prompt} ids), " + (f"sampled T={args.temperature} top-k 50" if
+                               args.temperature > 0 else "greedy") + f", rep 1.05, context {plen} -> "
+                               f"{plen + total}", "global_batch": 1, "prefill_rows": plen,
+                   "frame_path": {0: "captured multi-kernel graph", 1: "persistent frame kernel"}.get(path, path)},
+        "prefill_ms": round(prefill_s * 1e3, 2),
+        "frame_algorithmic_bytes_mid": fbytes,
+        "frame_hbm_gbs": round(fbytes * fps / 1e9, 1),
+        "frame_roofline_frac": round(fbytes * fps / 1e9 / HBM_PEAK_GBS, 4)}))
+
+
 def streams_bench(args, cfg, w):
     """Multi-stream batched decode: args.streams independent utterances, each
     a 128-token prompt (build_prefill rows) behind a seeded synthetic history
@@ -190,6 +243,10 @@ def main():
                     help="launches per per-kernel timing of the multi-kernel path (0: skip)")
     ap.add_argument("--prefill", type=int, default=0,
                     help="instead of the frame loop, time one talker prefill of this many rows (Q8_0: int8 MFMA path)")
+    ap.add_argument("--long", action="store_true",
+                    help="instead of the short-prompt greedy loop, time long-context sampled decode after a long prefill")
+    ap.add_argument("--long-prompt", type=int, default=2048, help="text ids of the --long prefill")
+    ap.add_argument("--temperature", type=float, default=0.9, help="--long sampling temperature (0: greedy)")
     ap.add_argument("--streams", type=int, default=0,
                     help="instead of batch 1, time multi-stream batched decode of this many streams (Q8_0)")
     ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
@@ -211,6 +268,8 @@ def main():
         return prefill_bench(args, cfg, w)
     if args.streams > 0:
         return streams_bench(args, cfg, w)
+    if args.long:
+        return long_bench(args, cfg, w)
     rng = np.random.default_rng(12)
     text = rng.integers(0, cfg.text_vocab, args.prompt).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)

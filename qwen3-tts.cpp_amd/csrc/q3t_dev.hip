@@ -557,7 +557,7 @@ int fk_prepare(q3t_dev * c) {
     if (g.hidden_size == 1024 && qd == 2048 && g.ffn_size == 3072) variant = 1;
     if (g.hidden_size == 256 && qd == 512 && g.ffn_size == 512) variant = 2;
     if (!variant || g.ffn_size != g.cp_ffn || g.cp_hidden != g.hidden_size || g.n_head != 2 * g.n_kv_head ||
-        g.head_dim != 128 || c->n_ctx > fk::kMaxCtx || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
+        g.head_dim != 128 || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
         g.cp_vocab > 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 || qkvd > fk::kHS)
         return 0;
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
@@ -580,7 +580,14 @@ int fk_prepare(q3t_dev * c) {
         !fits(g.hidden_size, g.ffn_size, sd) || !fits(g.codec_vocab, g.hidden_size, 1) ||
         !fits(g.cp_vocab, g.hidden_size, 1) || g.n_kv_head > grid)
         return 0;
-    const int phases = 15 * (2 + 5 * g.cp_layers) + 1 + 5 * g.n_layers;
+    // talker attention: grid / n_kv_head position chunks per KV head, each
+    // chunk's scores in LDS; phase C's partials fill kPvSlots slots
+    const int chunks = grid / g.n_kv_head;
+    const int chunk_len = 16 * ((c->n_ctx + 16 * chunks - 1) / (16 * chunks));
+    if (chunk_len > fk::kMaxChunk || chunks > 128 || (size_t) grid * 512 > (size_t) fk::kPvSlots * fk::kSlot ||
+        (g.n_head * 128 + grid - 1) / grid * 2 * chunks > 2 * fk::kMaxChunk)
+        return 0;
+    const int phases = 15 * (2 + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
     if (phases >= 4096) return 0;
     if (!c->fk_layers) {
         std::vector<fk::LayerQ8> t(g.n_layers + g.cp_layers);

@@ -576,34 +576,22 @@ __device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
 }
 
 // -------------------------------------------------------------- attention
-// Attention of KV head g = blockIdx.x for its two query heads and nt tokens
-// at positions pos0.. (causal).  Talker (cp == false): positions < pos0 come
-// from the HBM cache and the new rows are appended there; code predictor:
-// all rows live in this workgroup's LDS.
+// Code-predictor attention of KV head g = blockIdx.x for its two query heads
+// and nt tokens at positions pos0.. (causal); the 16-position KV cache of
+// every code-predictor layer lives in this workgroup's LDS.
 //
 // Wave w owns row w of (q0, q1, k, v): lane l holds elements l and l + 64,
 // which are exactly the NEOX rotation pairs, so QK-norm and RoPE need only
-// wave reductions.  Scores and P.V use 16 lanes per position (8 dims per
-// lane) for both query heads at once; softmax max / sum and the P.V combine
-// are the only workgroup barriers.
-__device__ __attribute__((always_inline)) void attention_phase(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int nt, int pos0,
-                                int qd, const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
-                                bool & dead) {
+// wave reductions.  Wave hq (0, 1) then handles query head 2g + hq alone.
+__device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds & L, const LayerQ8 & W, int layer,
+                                                            int nt, int pos0, int qd, const uint64_t * qkv,
+                                                            uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
+                                                            bool & dead) {
     const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kd = qd / 2;
-    const float * rc = cp ? A.cp_rope_cos : A.rope_cos;
-    const float * rs = cp ? A.cp_rope_sin : A.rope_sin;
     float * qf = L.a;                      // [tok][head][128] rotated, fp16-rounded q
     float * knew = L.a + 4 * 128;          // [tok][128]
     float * vnew = knew + 2 * 128;         // [tok][128]
-    uint16_t * kc = A.kc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
-    uint16_t * vc = A.vc + ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
-
-    // ---- stage + QK-norm + RoPE, one row per wave
-    // talker K/V rows of the first two position blocks (16 lanes x 16 bytes
-    // per position), fetched before the QKV wait
-    int4 kpre0 = make_int4(0, 0, 0, 0), kpre1 = make_int4(0, 0, 0, 0);
-    int4 vpre0 = make_int4(0, 0, 0, 0), vpre1 = make_int4(0, 0, 0, 0);
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
@@ -622,22 +610,8 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
 #pragma unroll
         for (int tok = 0; tok < 2; ++tok) {
             const int pos = pos0 + (tok < nt ? tok : 0);
-            rcv[tok] = rc[(size_t) pos * 64 + lane];
-            rsv[tok] = rs[(size_t) pos * 64 + lane];
-        }
-        // talker: the cached K/V rows of the first positions do not depend on
-        // the new token either (they were written by earlier steps)
-        if (!cp) {
-            const int sb = lane & 15, pb = lane >> 4;
-            const int ja = wave * 4 + pb, jb = 16 + wave * 4 + pb;
-            if (ja < pos0) {
-                kpre0 = *(const int4 *) (kc + (size_t) ja * 128 + sb * 8);
-                vpre0 = *(const int4 *) (vc + (size_t) ja * 128 + sb * 8);
-            }
-            if (jb < pos0) {
-                kpre1 = *(const int4 *) (kc + (size_t) jb * 128 + sb * 8);
-                vpre1 = *(const int4 *) (vc + (size_t) jb * 128 + sb * 8);
-            }
+            rcv[tok] = A.cp_rope_cos[(size_t) pos * 64 + lane];
+            rsv[tok] = A.cp_rope_sin[(size_t) pos * 64 + lane];
         }
         float val[kB];
         twait_batch<kB>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
@@ -661,223 +635,393 @@ __device__ __attribute__((always_inline)) void attention_phase(const Args & A, L
                     const uint16_t h0 = f2h(o0), h1 = f2h(o1);
                     knew[tok * 128 + lane] = h2f(h0);
                     knew[tok * 128 + lane + 64] = h2f(h1);
-                    if (cp) { L.cpk[layer][pos * 128 + lane] = h0; L.cpk[layer][pos * 128 + lane + 64] = h1; }
-                    else { kc[(size_t) pos * 128 + lane] = h0; kc[(size_t) pos * 128 + lane + 64] = h1; }
+                    L.cpk[layer][pos * 128 + lane] = h0;
+                    L.cpk[layer][pos * 128 + lane + 64] = h1;
                 }
             } else {
                 const uint16_t h0 = f2h(x0), h1 = f2h(x1);
                 vnew[tok * 128 + lane] = h2f(h0);
                 vnew[tok * 128 + lane + 64] = h2f(h1);
-                if (cp) { L.cpv[layer][pos * 128 + lane] = h0; L.cpv[layer][pos * 128 + lane + 64] = h1; }
-                else { vc[(size_t) pos * 128 + lane] = h0; vc[(size_t) pos * 128 + lane + 64] = h1; }
+                L.cpv[layer][pos * 128 + lane] = h0;
+                L.cpv[layer][pos * 128 + lane + 64] = h1;
             }
         }
     }
     __syncthreads();
 
-    if (cp) {
-        // Code predictor: at most 16 positions, all in LDS.  Wave hq (0, 1)
-        // handles query head 2g + hq alone, so no workgroup barrier follows:
-        // scores with 4 lanes per position (32 dims each, quad DPP sum),
-        // softmax with wave reductions, P.V with 2 dims per lane and each
-        // probability broadcast by readlane.
-        if (wave < 2) {
-            const int hq = wave, jq = lane >> 2, sq = lane & 3;
-            for (int tok = 0; tok < nt; ++tok) {
-                const int n_kv = pos0 + tok + 1;
-                double acc = 0.0;
-                if (jq < n_kv) {
-                    const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
+    // At most 16 positions, all in LDS, so no workgroup barrier follows:
+    // scores with 4 lanes per position (32 dims each, quad DPP sum), softmax
+    // with wave reductions, P.V with 2 dims per lane and each probability
+    // broadcast by readlane.
+    if (wave < 2) {
+        const int hq = wave, jq = lane >> 2, sq = lane & 3;
+        for (int tok = 0; tok < nt; ++tok) {
+            const int n_kv = pos0 + tok + 1;
+            double acc = 0.0;
+            if (jq < n_kv) {
+                const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        float kv[8];
-                        if (jq >= pos0) {
+                for (int c = 0; c < 4; ++c) {
+                    float kv[8];
+                    if (jq >= pos0) {
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) kv[e] = knew[(jq - pos0) * 128 + sq * 32 + c * 8 + e];
-                        } else {
-                            const int4 k4 = *(const int4 *) &L.cpk[layer][jq * 128 + sq * 32 + c * 8];
-                            const uint16_t * kh = (const uint16_t *) &k4;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
-                        }
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc = fma((double) q[c * 8 + e], (double) kv[e], acc);
-                    }
-                }
-                acc += dpp_d<0xB1>(acc);
-                acc += dpp_d<0x4E>(acc);
-                const float sv = jq < n_kv ? (float) acc * A.attn_scale : -INFINITY;
-                const float mx = wave_max_f(sv);
-                const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
-                const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
-                const float inv = (float) (1.0 / sum);
-                const float pr = round_f16(ev * inv);
-                double o0 = 0.0, o1 = 0.0;
-                for (int j = 0; j < n_kv; ++j) {
-                    const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
-                    float v0, v1;
-                    if (j >= pos0) {
-                        v0 = vnew[(j - pos0) * 128 + 2 * lane];
-                        v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
+                        for (int e = 0; e < 8; ++e) kv[e] = knew[(jq - pos0) * 128 + sq * 32 + c * 8 + e];
                     } else {
-                        const uint32_t w2 = *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane];
-                        v0 = h2f((uint16_t) (w2 & 0xffffu));
-                        v1 = h2f((uint16_t) (w2 >> 16));
+                        const int4 k4 = *(const int4 *) &L.cpk[layer][jq * 128 + sq * 32 + c * 8];
+                        const uint16_t * kh = (const uint16_t *) &k4;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
                     }
-                    o0 = fma(pj, (double) v0, o0);
-                    o1 = fma(pj, (double) v1, o1);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = fma((double) q[c * 8 + e], (double) kv[e], acc);
                 }
-                uint64_t * dst = out + (size_t) tok * kHS + (g * 2 + hq) * 128 + 2 * lane;
-                tstore(dst, out_tag, (float) o0);
-                tstore(dst + 1, out_tag, (float) o1);
             }
-        }
-        __syncthreads();
-        return;
-    }
-
-    // Talker: 16 lanes per position (8 dims = 16 bytes each), 4 positions per
-    // wave and 16 per workgroup per block; K and V rows are loaded in chunks
-    // of 8 blocks issued before any is used.
-    const int sub = lane & 15, pw = lane >> 4;
-    constexpr int kCh = 8;
-    for (int tok = 0; tok < nt; ++tok) {
-        const int n_kv = pos0 + tok + 1;
-        const int nblk = (n_kv + 4 * kW - 1) / (4 * kW);
-        double q0[8], q1[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            q0[e] = (double) qf[(tok * 2 + 0) * 128 + sub * 8 + e];
-            q1[e] = (double) qf[(tok * 2 + 1) * 128 + sub * 8 + e];
-        }
-        // ---- scores
-        float lm0 = -INFINITY, lm1 = -INFINITY;
-        for (int i0 = 0; i0 < nblk; i0 += kCh) {
-            int4 kk[kCh];
-#pragma unroll
-            for (int u = 0; u < kCh; ++u) {
-                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
-                kk[u] = make_int4(0, 0, 0, 0);
-                if (i < nblk && j < pos0)
-                    kk[u] = i == 0 ? kpre0 : i == 1 ? kpre1 : *(const int4 *) (kc + (size_t) j * 128 + sub * 8);
-            }
-#pragma unroll
-            for (int u = 0; u < kCh; ++u) {
-                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
-                if (i >= nblk) break;                 // uniform
-                float kv[8];
-                if (j >= pos0 && j < n_kv) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) kv[e] = knew[(j - pos0) * 128 + sub * 8 + e];
+            acc += dpp_d<0xB1>(acc);
+            acc += dpp_d<0x4E>(acc);
+            const float sv = jq < n_kv ? (float) acc * A.attn_scale : -INFINITY;
+            const float mx = wave_max_f(sv);
+            const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
+            const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
+            const float inv = (float) (1.0 / sum);
+            const float pr = round_f16(ev * inv);
+            double o0 = 0.0, o1 = 0.0;
+            for (int j = 0; j < n_kv; ++j) {
+                const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
+                float v0, v1;
+                if (j >= pos0) {
+                    v0 = vnew[(j - pos0) * 128 + 2 * lane];
+                    v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
                 } else {
-                    const uint16_t * kh = (const uint16_t *) &kk[u];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
+                    const uint32_t w2 = *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane];
+                    v0 = h2f((uint16_t) (w2 & 0xffffu));
+                    v1 = h2f((uint16_t) (w2 >> 16));
                 }
-                // fp16 x fp16 products are exact in fp64: fma rounds like mul + add
-                double a0 = 0.0, a1 = 0.0;
+                o0 = fma(pj, (double) v0, o0);
+                o1 = fma(pj, (double) v1, o1);
+            }
+            uint64_t * dst = out + (size_t) tok * kHS + (g * 2 + hq) * 128 + 2 * lane;
+            tstore(dst, out_tag, (float) o0);
+            tstore(dst + 1, out_tag, (float) o1);
+        }
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------- talker attention (split)
+// The talker's attention over its HBM cache runs on every workgroup: b =
+// blockIdx.x takes KV head g = b % H and position chunk c = b / H (C = grid/H
+// chunks of Lc positions, Lc a multiple of 16).  The softmax is exact as in
+// the reference, so its global maximum and sum each need a hand-off:
+//   A  stage q (both heads), k, v; scores of the chunk -> chunk maxima
+//   B  global maxima -> exp of the chunk, fp64 chunk sums
+//   C  global sums (added in chunk order) -> fp16 probabilities -> fp64 P.V
+//      partials of the chunk (256 per workgroup, published as 32-bit halves
+//      over kPvSlots consecutive slots)
+//   D  each workgroup adds the C partials of 8 outputs in chunk order and
+//      publishes the attention rows the Wo GEMV reads
+// The chunk's cached K and V rows are loaded before the QKV wait (they do not
+// depend on the new token), kPre position steps of each.
+constexpr int kPre = 4;                      // position steps of K and V prefetched per thread
+constexpr int kPvSlots = 16;                 // arena slots phase C spans (256 wg x 512 halves)
+constexpr int kMaxChunk = kMaxCtx;           // longest chunk whose scores fit L.sc
+
+struct AttSplit {
+    int g, c, C, Lc, j0, j1;
+};
+__device__ __forceinline__ AttSplit att_split(const Args & A, int n_kv) {
+    AttSplit s;
+    const int H = A.n_kv_head;
+    s.C = (int) gridDim.x / H;
+    s.Lc = 16 * ((n_kv + 16 * s.C - 1) / (16 * s.C));
+    s.g = (int) blockIdx.x % H;
+    s.c = (int) blockIdx.x / H;
+    s.j0 = s.c * s.Lc;
+    s.j1 = min(s.j0 + s.Lc, n_kv);
+    return s;
+}
+
+struct KvPre {
+    int4 k[kPre], v[kPre];
+};
+
+// Position of step i for this lane: 16 lanes per position (8 dims each),
+// 4 positions per wave, 16 per workgroup step.
+__device__ __forceinline__ int att_pos(const AttSplit & s, int i) {
+    return s.j0 + i * 16 + (int) (threadIdx.x >> 6) * 4 + (int) ((threadIdx.x & 63) >> 4);
+}
+
+__device__ __forceinline__ void att_prefetch(const Args & A, int layer, const AttSplit & s, int pos0, KvPre & P) {
+    if (s.c >= s.C) return;
+    const int sub = threadIdx.x & 15;
+    const size_t base = ((size_t) layer * A.n_kv_head + s.g) * A.n_ctx * 128;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const double kd = (double) kv[e];
-                    a0 = fma(q0[e], kd, a0);
-                    a1 = fma(q1[e], kd, a1);
-                }
-                a0 = group_sum_d(a0, 16);
-                a1 = group_sum_d(a1, 16);
-                if (j < n_kv) {
-                    const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
-                    if (sub == 0) { L.sc[j] = s0; L.sc[kMaxCtx + j] = s1; }
-                    lm0 = fmaxf(lm0, s0);
-                    lm1 = fmaxf(lm1, s1);
+    for (int i = 0; i < kPre; ++i) {
+        const int j = att_pos(s, i);
+        if (j < s.j1 && j < pos0) {
+            P.k[i] = *(const int4 *) (A.kc + base + (size_t) j * 128 + sub * 8);
+            P.v[i] = *(const int4 *) (A.vc + base + (size_t) j * 128 + sub * 8);
+        }
+    }
+}
+
+__device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & L, const LayerQ8 & W, int layer,
+                                                          int pos0, int qd, const AttSplit & s, const KvPre & P,
+                                                          const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out,
+                                                          uint32_t out_tag, bool & dead) {
+    if (s.c >= s.C) return;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = s.g;
+    const int kd = qd / 2;
+    float * qf = L.a;                      // [head][128] rotated, fp16-rounded q
+    float * knew = L.a + 2 * 128;          // [128]
+    float * vnew = knew + 128;             // [128]
+    const size_t base = ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
+    {
+        const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
+        const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
+        const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
+        const float rcv = A.rope_cos[(size_t) pos0 * 64 + lane], rsv = A.rope_sin[(size_t) pos0 * 64 + lane];
+        const uint64_t * ptr[2] = {qkv + col + lane, qkv + col + lane + 64};
+        float val[2];
+        twait_batch<2>(ptr, 2, qkv_tag, val, dead, A.err);
+        const float x0 = val[0], x1 = val[1];
+        const bool writer = s.c == 0;      // one workgroup per KV head appends the new rows
+        if (wave < 3) {
+            const double ss = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
+            const float mean = (float) (ss / 128.0);
+            const float scale = 1.0f / sqrtf(mean + A.eps);
+            float y0 = x0 * scale, y1 = x1 * scale;
+            y0 = y0 * nw0;
+            y1 = y1 * nw1;
+            const float a0 = y0 * rcv, b0 = y1 * rsv, a1 = y0 * rsv, b1 = y1 * rcv;
+            const float o0 = a0 - b0, o1 = a1 + b1;
+            if (wave < 2) {
+                qf[wave * 128 + lane] = round_f16(o0);
+                qf[wave * 128 + lane + 64] = round_f16(o1);
+            } else {
+                const uint16_t h0 = f2h(o0), h1 = f2h(o1);
+                knew[lane] = h2f(h0);
+                knew[lane + 64] = h2f(h1);
+                if (writer) {
+                    A.kc[base + (size_t) pos0 * 128 + lane] = h0;
+                    A.kc[base + (size_t) pos0 * 128 + lane + 64] = h1;
                 }
             }
-        }
-        lm0 = wave_max_f(lm0);
-        lm1 = wave_max_f(lm1);
-        if (lane == 0) { L.fred[wave] = lm0; L.fred[kW + wave] = lm1; }
-        __syncthreads();
-        float mx0 = L.fred[0], mx1 = L.fred[kW];
-#pragma unroll
-        for (int w = 1; w < kW; ++w) { mx0 = fmaxf(mx0, L.fred[w]); mx1 = fmaxf(mx1, L.fred[kW + w]); }
-        // ---- exp and denominators (each thread its own positions)
-        double ls0 = 0.0, ls1 = 0.0;
-        for (int j = t; j < n_kv; j += kT) {
-            const float e0 = expf_q3t(L.sc[j] - mx0), e1 = expf_q3t(L.sc[kMaxCtx + j] - mx1);
-            L.sc[j] = e0; L.sc[kMaxCtx + j] = e1;
-            ls0 += (double) e0; ls1 += (double) e1;
-        }
-        ls0 = wave_sum_d(ls0);
-        ls1 = wave_sum_d(ls1);
-        if (lane == 0) { L.red[wave] = ls0; L.red[kW + wave] = ls1; }
-        __syncthreads();
-        double sum0 = L.red[0], sum1 = L.red[kW];
-#pragma unroll
-        for (int w = 1; w < kW; ++w) { sum0 += L.red[w]; sum1 += L.red[kW + w]; }
-        const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
-        // fp16-rounded probabilities, each thread its own positions
-        for (int j = t; j < n_kv; j += kT) {
-            L.sc[j] = round_f16(L.sc[j] * inv0);
-            L.sc[kMaxCtx + j] = round_f16(L.sc[kMaxCtx + j] * inv1);
-        }
-        __syncthreads();
-        // ---- P.V, same position blocks; partial sums over this lane's positions
-        double o0[8], o1[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { o0[e] = 0.0; o1[e] = 0.0; }
-        for (int i0 = 0; i0 < nblk; i0 += kCh) {
-            int4 vv4[kCh];
-#pragma unroll
-            for (int u = 0; u < kCh; ++u) {
-                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
-                vv4[u] = make_int4(0, 0, 0, 0);
-                if (i < nblk && j < pos0)
-                    vv4[u] = i == 0 ? vpre0 : i == 1 ? vpre1 : *(const int4 *) (vc + (size_t) j * 128 + sub * 8);
-            }
-#pragma unroll
-            for (int u = 0; u < kCh; ++u) {
-                const int i = i0 + u, j = i * 4 * kW + wave * 4 + pw;
-                if (i >= nblk) break;                 // uniform
-                if (j < n_kv) {
-                    const double p0 = (double) L.sc[j], p1 = (double) L.sc[kMaxCtx + j];
-                    float vv[8];
-                    if (j >= pos0) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = vnew[(j - pos0) * 128 + sub * 8 + e];
-                    } else {
-                        const uint16_t * vh = (const uint16_t *) &vv4[u];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = h2f(vh[e]);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const double vd = (double) vv[e];
-                        o0[e] = fma(p0, vd, o0[e]);
-                        o1[e] = fma(p1, vd, o1[e]);
-                    }
-                }
+        } else {
+            const uint16_t h0 = f2h(x0), h1 = f2h(x1);
+            vnew[lane] = h2f(h0);
+            vnew[lane + 64] = h2f(h1);
+            if (writer) {
+                A.vc[base + (size_t) pos0 * 128 + lane] = h0;
+                A.vc[base + (size_t) pos0 * 128 + lane + 64] = h1;
             }
         }
-        // combine the 16 partials of each output through LDS (the score buffer
-        // is free once every wave is past its last probability read)
-        __syncthreads();
-        double * part = (double *) L.sc;        // [wave][lane][16]
+    }
+    __syncthreads();
+    const int sub = lane & 15;
+    double q0[8], q1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        q0[e] = (double) qf[sub * 8 + e];
+        q1[e] = (double) qf[128 + sub * 8 + e];
+    }
+    float lm0 = -INFINITY, lm1 = -INFINITY;
+    const int steps = s.Lc / 16;
+    for (int i = 0; i < steps; ++i) {
+        const int j = att_pos(s, i);
+        int4 kk = make_int4(0, 0, 0, 0);
+        if (i < kPre) {
+#pragma unroll
+            for (int u = 0; u < kPre; ++u) if (u == i) kk = P.k[u];
+        } else if (j < s.j1 && j < pos0) {
+            kk = *(const int4 *) (A.kc + base + (size_t) j * 128 + sub * 8);
+        }
+        float kv[8];
+        if (j == pos0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kv[e] = knew[sub * 8 + e];
+        } else {
+            const uint16_t * kh = (const uint16_t *) &kk;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
+        }
+        // fp16 x fp16 products are exact in fp64: fma rounds like mul + add
+        double a0 = 0.0, a1 = 0.0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            part[(wave * 64 + lane) * 16 + e] = o0[e];
-            part[(wave * 64 + lane) * 16 + 8 + e] = o1[e];
+            const double kd8 = (double) kv[e];
+            a0 = fma(q0[e], kd8, a0);
+            a1 = fma(q1[e], kd8, a1);
         }
-        __syncthreads();
-        {
-            const int h = t >> 7, e = t & 127, sb = e >> 3, ee = e & 7;
-            double r = 0.0;
-#pragma unroll
-            for (int w = 0; w < kW; ++w)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) r += part[(w * 64 + q * 16 + sb) * 16 + h * 8 + ee];
-            tstore(out + (size_t) tok * kHS + (g * 2 + h) * 128 + e, out_tag, (float) r);
+        a0 = group_sum_d(a0, 16);
+        a1 = group_sum_d(a1, 16);
+        if (j < s.j1) {
+            const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
+            if (sub == 0) { L.sc[j - s.j0] = s0; L.sc[kMaxChunk + j - s.j0] = s1; }
+            lm0 = fmaxf(lm0, s0);
+            lm1 = fmaxf(lm1, s1);
         }
-        __syncthreads();
     }
+    lm0 = wave_max_f(lm0);
+    lm1 = wave_max_f(lm1);
+    if (lane == 0) { L.fred[wave] = lm0; L.fred[kW + wave] = lm1; }
+    __syncthreads();
+    if (t < 2) {
+        float m = L.fred[t * kW];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) m = fmaxf(m, L.fred[t * kW + w]);
+        tstore(out + blockIdx.x * 2 + t, out_tag, m);
+    }
+}
+
+__device__ __attribute__((always_inline)) void att_sums(const Args & A, Lds & L, const AttSplit & s,
+                                                        const uint64_t * in, uint32_t in_tag, uint64_t * out,
+                                                        uint32_t out_tag, bool & dead) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, H = A.n_kv_head;
+    float * gm = L.a + 4 * 128;            // [C][2] chunk maxima of this KV head
+    if (s.c < s.C) {
+        for (int i = t; i < 2 * s.C; i += kT) gm[i] = twait(in + (s.g + (i >> 1) * H) * 2 + (i & 1), in_tag, dead, A.err);
+    }
+    __syncthreads();
+    if (s.c >= s.C) return;
+    float mx0 = gm[0], mx1 = gm[1];
+    for (int c = 1; c < s.C; ++c) { mx0 = fmaxf(mx0, gm[2 * c]); mx1 = fmaxf(mx1, gm[2 * c + 1]); }
+    double ls0 = 0.0, ls1 = 0.0;
+    const int n = s.j1 - s.j0;
+    for (int j = t; j < n; j += kT) {
+        const float e0 = expf_q3t(L.sc[j] - mx0), e1 = expf_q3t(L.sc[kMaxChunk + j] - mx1);
+        L.sc[j] = e0; L.sc[kMaxChunk + j] = e1;
+        ls0 += (double) e0; ls1 += (double) e1;
+    }
+    ls0 = wave_sum_d(ls0);
+    ls1 = wave_sum_d(ls1);
+    if (lane == 0) { L.red[wave] = ls0; L.red[kW + wave] = ls1; }
+    __syncthreads();
+    if (t < 2) {
+        double sm = L.red[t * kW];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) sm += L.red[t * kW + w];
+        tstore(out + blockIdx.x * 4 + 2 * t, out_tag, __int_as_float(__double2loint(sm)));
+        tstore(out + blockIdx.x * 4 + 2 * t + 1, out_tag, __int_as_float(__double2hiint(sm)));
+    }
+}
+
+__device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, int layer, int pos0,
+                                                      const AttSplit & s, const KvPre & P, const uint64_t * in,
+                                                      uint32_t in_tag, uint64_t * out, uint32_t out_tag,
+                                                      bool & dead) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, H = A.n_kv_head;
+    uint32_t * gs = (uint32_t *) (L.a + 4 * 128);   // [C][2 heads][2 halves] chunk sums
+    if (s.c < s.C) {
+        for (int i = t; i < 4 * s.C; i += kT)
+            gs[i] = __float_as_uint(twait(in + (s.g + (i >> 2) * H) * 4 + (i & 3), in_tag, dead, A.err));
+    }
+    __syncthreads();
+    if (s.c >= s.C) return;
+    double sum0 = 0.0, sum1 = 0.0;
+    for (int c = 0; c < s.C; ++c) {
+        sum0 += __hiloint2double((int) gs[4 * c + 1], (int) gs[4 * c]);
+        sum1 += __hiloint2double((int) gs[4 * c + 3], (int) gs[4 * c + 2]);
+    }
+    const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
+    const int n = s.j1 - s.j0;
+    for (int j = t; j < n; j += kT) {
+        L.sc[j] = round_f16(L.sc[j] * inv0);
+        L.sc[kMaxChunk + j] = round_f16(L.sc[kMaxChunk + j] * inv1);
+    }
+    __syncthreads();
+    const int sub = lane & 15;
+    const float * vnew = L.a + 3 * 128;
+    const size_t base = ((size_t) layer * A.n_kv_head + s.g) * A.n_ctx * 128;
+    double o0[8], o1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { o0[e] = 0.0; o1[e] = 0.0; }
+    const int steps = s.Lc / 16;
+    for (int i = 0; i < steps; ++i) {
+        const int j = att_pos(s, i);
+        int4 vv4 = make_int4(0, 0, 0, 0);
+        if (i < kPre) {
+#pragma unroll
+            for (int u = 0; u < kPre; ++u) if (u == i) vv4 = P.v[u];
+        } else if (j < s.j1 && j < pos0) {
+            vv4 = *(const int4 *) (A.vc + base + (size_t) j * 128 + sub * 8);
+        }
+        if (j < s.j1) {
+            const double p0 = (double) L.sc[j - s.j0], p1 = (double) L.sc[kMaxChunk + j - s.j0];
+            float vv[8];
+            if (j == pos0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vv[e] = vnew[sub * 8 + e];
+            } else {
+                const uint16_t * vh = (const uint16_t *) &vv4;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vv[e] = h2f(vh[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double vd = (double) vv[e];
+                o0[e] = fma(p0, vd, o0[e]);
+                o1[e] = fma(p1, vd, o1[e]);
+            }
+        }
+    }
+    // the 4 positions of a wave step: lanes l, l^16, l^32, l^48 hold the same dims
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        o0[e] += swz16_d(o0[e]);
+        o0[e] += __shfl_xor(o0[e], 32);
+        o1[e] += swz16_d(o1[e]);
+        o1[e] += __shfl_xor(o1[e], 32);
+    }
+    __syncthreads();                        // the probabilities are consumed: reuse L.sc
+    double * part = (double *) L.sc;        // [wave][head][128]
+    if (lane < 16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            part[(wave * 2 + 0) * 128 + sub * 8 + e] = o0[e];
+            part[(wave * 2 + 1) * 128 + sub * 8 + e] = o1[e];
+        }
+    }
+    __syncthreads();
+    {
+        const int h = t >> 7, d = t & 127;
+        double r = part[h * 128 + d];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) r += part[(w * 2 + h) * 128 + d];
+        uint64_t * dst = out + (size_t) blockIdx.x * 512 + h * 256 + d * 2;
+        tstore(dst, out_tag, __int_as_float(__double2loint(r)));
+        tstore(dst + 1, out_tag, __int_as_float(__double2hiint(r)));
+    }
+}
+
+// Phase D: 8 attention outputs per workgroup (n_head * 128 over the grid),
+// each the chunk-ordered fp64 sum of its KV head's C partials.
+__device__ __attribute__((always_inline)) void att_combine(const Args & A, Lds & L, const uint64_t * in,
+                                                           uint32_t in_tag, uint64_t * out, uint32_t out_tag,
+                                                           bool & dead) {
+    const int t = threadIdx.x, H = A.n_kv_head, C = (int) gridDim.x / H;
+    const int n_out = A.n_head * 128;
+    const int opw = (n_out + (int) gridDim.x - 1) / (int) gridDim.x;   // outputs per workgroup
+    uint32_t * w = (uint32_t *) L.sc;        // [opw][C][2]
+    for (int i = t; i < opw * 2 * C; i += kT) {
+        const int k = i / (2 * C), c = (i >> 1) % C, half = i & 1;
+        const int o = (int) blockIdx.x * opw + k;
+        uint32_t v = 0;
+        if (o < n_out) {
+            const int hq = o >> 7, d = o & 127, g = hq >> 1, hh = hq & 1;
+            v = __float_as_uint(twait(in + (size_t) (g + c * H) * 512 + hh * 256 + d * 2 + half, in_tag, dead, A.err));
+        }
+        w[i] = v;
+    }
+    __syncthreads();
+    if (t < opw) {
+        const int o = (int) blockIdx.x * opw + t;
+        if (o < n_out) {
+            double r = 0.0;
+            for (int c = 0; c < C; ++c) r += __hiloint2double((int) w[(t * C + c) * 2 + 1], (int) w[(t * C + c) * 2]);
+            tstore(out + o, out_tag, (float) r);
+        }
+    }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------- samplers
@@ -948,6 +1092,10 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     // half of the waves, away from the attention workgroups (0..n_kv_head-1)
     // and from the waves that carry two gate/up groups (the first ones)
     const int rot = (int) (gridDim.x / 2) * kW;
+    // talker: this workgroup's chunk of cached K/V rows, loaded now (it does
+    // not depend on anything this frame computes)
+    KvPre kv;
+    if (!cp) att_prefetch(A, layer, att_split(A, pos0 + 1), pos0, kv);
     // QKV (RMSNorm'd input)
     const int p_qkv = p++;
     if (wg_has_rows<D>(QKVD, 0)) {
@@ -966,12 +1114,30 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead, A.err);
     }
     __syncthreads();
-    // attention (workgroup g < n_kv_head owns KV head g)
-    const int p_att = p++;
-    if ((int) blockIdx.x < A.n_kv_head)
-        attention_phase(A, L, W, layer, cp, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
-                        ar + (size_t) p_att * kSlot, tb | p_att, dead);
-    __syncthreads();
+    // attention: code predictor on workgroup g < n_kv_head (KV head g, cache
+    // in LDS); talker split over every workgroup in four phases
+    int p_att;
+    if (cp) {
+        p_att = p++;
+        if ((int) blockIdx.x < A.n_kv_head)
+            attention_cp(A, L, W, layer, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+                         ar + (size_t) p_att * kSlot, tb | p_att, dead);
+        __syncthreads();
+    } else {
+        const AttSplit sp = att_split(A, pos0 + 1);
+        const int p_a = p++, p_b = p++, p_c = p;
+        p += kPvSlots;
+        p_att = p++;
+        att_scores(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+                   ar + (size_t) p_a * kSlot, tb | p_a, dead);
+        __syncthreads();
+        att_sums(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
+        __syncthreads();
+        att_pv(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot, tb | p_c,
+               dead);
+        __syncthreads();
+        att_combine(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot, tb | p_att, dead);
+    }
     // Wo + residual (the block input)
     const int p_wo = p++;
     if (wg_has_rows<QD>(D, rot)) {
