@@ -532,11 +532,17 @@ __global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, i
 
 // Decides whether the persistent frame kernel can run this context and
 // prepares its tables.  Falls back to the multi-kernel graph otherwise.
-// The kernel is instantiated for fixed (hidden, query width, FFN width):
-// variant 1 = (1024, 2048, 3072), the 0.6B talker and code predictor;
-// variant 2 = (256, 512, 512), the small test shapes.
+// The kernel is instantiated for fixed (hidden, query width, FFN width) and
+// layer weight type: variant 1 / 3 = (1024, 2048, 3072), the 0.6B talker and
+// code predictor, Q8_0 / F16 layers; variant 2 / 4 = (256, 512, 512), the
+// small test shapes.
 const void * fk_kernel(int variant) {
-    return variant == 1 ? (const void *) fk::k_frame<1024, 2048, 3072> : (const void *) fk::k_frame<256, 512, 512>;
+    switch (variant) {
+        case 1: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8>;
+        case 2: return (const void *) fk::k_frame<256, 512, 512, W_Q8>;
+        case 3: return (const void *) fk::k_frame<1024, 2048, 3072, W_F16>;
+        default: return (const void *) fk::k_frame<256, 512, 512, W_F16>;
+    }
 }
 
 int slots_for(int K) {
@@ -560,12 +566,14 @@ int fk_prepare(q3t_dev * c) {
         g.head_dim != 128 || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
         g.cp_vocab > 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 || qkvd > fk::kHS)
         return 0;
+    // every layer matrix Q8_0, or every one F16
+    const int lt = c->talker[0].qkv.type;
+    if (lt != Q3T_TYPE_Q8_0 && lt != Q3T_TYPE_F16) return 0;
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
-        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
-            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
-            return 0;
+        if (L.qkv.type != lt || L.wo.type != lt || L.wg.type != lt || L.wu.type != lt || L.wd.type != lt) return 0;
     }
+    if (lt == Q3T_TYPE_F16) variant += 2;
     // one workgroup per CU (the LDS footprint allows no more), all co-resident
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fk_kernel(variant), fk::kT, 0));

@@ -103,7 +103,11 @@ struct Lds {
     float qdx[2 * kMaxBlk];                     // fp16-rounded block scales
     alignas(16) uint16_t hq[4][32 * 8];         // F16 head input: halves 8c..8c+7 of block b at hq[c][b*8]
     float a[2 * 4 * 128];                       // attention: q (2 tok x 2 heads), new k, new v rows
-    alignas(16) float sc[2 * kMaxCtx];          // attention scores / probabilities, 2 heads; P.V partials
+    union {                                     // attention and F16 GEMV inputs are never live together
+        alignas(16) float sc[2 * kMaxCtx];      // attention scores / probabilities, 2 heads; P.V partials
+        alignas(16) uint16_t hf[2][4][kMaxBlk * 8];   // F16 GEMV input: halves 8c..8c+7 of block b at hf[t][c][b*8]
+        alignas(16) float xw[2][8][kMaxBlk * 4];      // widened F16 GEMV input: fp32 4c..4c+3 of block b at xw[t][c][b*4]
+    };
     alignas(16) uint16_t cpk[kCpLayers][16 * 128];   // code-predictor KV of this workgroup's KV head
     alignas(16) uint16_t cpv[kCpLayers][16 * 128];
     double red[2 * kW];
@@ -425,6 +429,190 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
                     acc2[gi][t] = fma((double) (R.du[gi][s] * dx),
                                       (double) dot32_i8(R.u[gi][s][0], R.u[gi][s][1], x0, x1), acc2[gi][t]);
             }
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        if (gi >= R.ng) break;
+        const int r = (gw + gi * nw) * G::RPW + rsub;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const double a1 = group_sum_d(acc[gi][t], G::LPR);
+            const double a2 = DUAL ? group_sum_d(acc2[gi][t], G::LPR) : 0.0;
+            if (lir != 0) continue;
+            const float v = (float) a1;
+            float o;
+            if (epi == EPI_RESID) {
+                const uint64_t rv = R.res[gi][t];
+                o = v + ((uint32_t) (rv >> 32) == res_tag ? __uint_as_float((uint32_t) rv)
+                                                          : twait(res + (size_t) t * kHS + r, res_tag, dead, err));
+            } else if (epi == EPI_SWIGLU) {
+                o = silu_q3t(v) * (float) a2;
+            } else {
+                o = v;
+            }
+            tstore(out + (size_t) t * kHS + r, out_tag, o);
+        }
+    }
+}
+
+// ------------------------------------------------------------- F16 GEMV
+// F16 weights (the F16 model's layers): the activation is rounded to fp16
+// (or kept fp32 for ffn_down, which the reference widens to F32) and every
+// product, exact in fp64, is accumulated in fp64.  Same row geometry as the
+// Q8_0 GEMV: a lane holds whole 32-element blocks, 64 bytes each.
+template <int K, bool DUAL>
+struct F16Regs {
+    static constexpr int S = Geo<K>::SLOTS;
+    int4 w[2][S][4], u[DUAL ? 2 : 1][DUAL ? S : 1][4];
+    uint64_t res[2][2];
+    int ng;
+};
+
+template <int K, bool DUAL>
+__device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_t * W, const uint16_t * U, int rows,
+                                             int rot) {
+    using G = Geo<K>;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
+    const int groups = rows / G::RPW;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
+    R.ng = 0;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = gw + gi * nw;
+        if (g >= groups) break;
+        R.ng = gi + 1;
+        const int r = g * G::RPW + rsub;
+#pragma unroll
+        for (int s = 0; s < G::SLOTS; ++s) {
+            const int b = lir + s * G::LPR;
+            const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) R.w[gi][s][c] = wp[c];
+            if (DUAL) {
+                const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) R.u[DUAL ? gi : 0][DUAL ? s : 0][c] = up[c];
+            }
+        }
+    }
+}
+
+template <int NT, int K, bool DUAL>
+__device__ __forceinline__ void res_prefetch16(F16Regs<K, DUAL> & R, const uint64_t * res, int rot) {
+    using G = Geo<K>;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
+    if (lir != 0) return;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        if (gi >= R.ng) break;
+        const int r = (gw + gi * nw) * G::RPW + rsub;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) R.res[gi][t] = tload(res + (size_t) t * kHS + r);
+    }
+}
+
+// Thread-distributed rows into the F16 GEMV input layout: rounded to fp16
+// (WIDE = false) or kept fp32 (WIDE = true).
+template <int NT, int K, bool WIDE>
+__device__ __forceinline__ void f16_rows(const RowsT<NT, K> & v, Lds & L) {
+    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4;
+#pragma unroll
+    for (int c = 0; c < CHG; ++c) {
+        const int g = (int) threadIdx.x + kT * c;
+        if (g >= G4) break;
+        const int b = g >> 3, e32 = (g & 7) * 4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (WIDE) {
+                *(float4 *) &L.xw[t][g & 7][b * 4] = make_float4(v[t][c][0], v[t][c][1], v[t][c][2], v[t][c][3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) L.hf[t][(e32 + e) >> 3][b * 8 + ((e32 + e) & 7)] = f2h(v[t][c][e]);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// fp16 element j (0..7) of 8 packed in an int4, without taking the register's address
+__device__ __forceinline__ float h8(const int4 & v, int j) {
+    const int w = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
+    return h2f((uint16_t) ((j & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu)));
+}
+
+template <int NT, int K, bool DUAL, bool WIDE>
+__device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
+                                            uint32_t res_tag, uint64_t * out, uint32_t out_tag, int rot, bool & dead,
+                                            int32_t * err) {
+    using G = Geo<K>;
+    if (R.ng == 0) return;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
+    const int gw = rot_wave(rot), nw = gridDim.x * kW;
+    double acc[2][NT], acc2[2][NT];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
+#pragma unroll
+    for (int s = 0; s < G::SLOTS; ++s) {
+        const int b = lir + s * G::LPR;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            // activation elements 8c..8c+7 of block b, every token, kept packed
+            // (fp16) or as fp32 until each product is formed
+            int4 xp[NT];
+            float xa[WIDE ? NT : 1][8];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (WIDE) {
+                    const float4 x0 = *(const float4 *) &L.xw[t][2 * c][b * 4];
+                    const float4 x1 = *(const float4 *) &L.xw[t][2 * c + 1][b * 4];
+                    float * xr = xa[WIDE ? t : 0];
+                    xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w;
+                    xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
+                } else {
+                    xp[t] = *(const int4 *) &L.hf[t][c][b * 8];
+                }
+            }
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                if (gi >= R.ng) break;
+                // The packed weights pass through an empty asm here, so their
+                // conversions are not hoisted ahead of the input barrier.
+                int4 wv = R.w[gi][s][c], uv = R.u[DUAL ? gi : 0][DUAL ? s : 0][c];
+                __asm__ volatile("" : "+v"(wv.x), "+v"(wv.y), "+v"(wv.z), "+v"(wv.w));
+                if (DUAL) __asm__ volatile("" : "+v"(uv.x), "+v"(uv.y), "+v"(uv.z), "+v"(uv.w));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float wf = h8(wv, j), uf = DUAL ? h8(uv, j) : 0.0f;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        if (WIDE) {
+                            // fp16 x fp32 is exact in fp64.  It is formed as the fp32 product
+                            // plus its fma residual (TwoProduct: exact unless the product is
+                            // below 2^-102 and the residual underflows), whose fp64 sum is
+                            // exact, then added once.  Fewer live fp64 values than converting
+                            // both operands keeps this phase within the register file.
+                            const float xf = xa[WIDE ? t : 0][j];
+                            const float pr = wf * xf, pe = fmaf(wf, xf, -pr);
+                            acc[gi][t] += (double) pr + (double) pe;
+                            if (DUAL) {
+                                const float qr = uf * xf, qe = fmaf(uf, xf, -qr);
+                                acc2[gi][t] += (double) qr + (double) qe;
+                            }
+                        } else {
+                            // fp16 x fp16: exact in fp32
+                            const float xf = h8(xp[t], j);
+                            acc[gi][t] += (double) (wf * xf);
+                            if (DUAL) acc2[gi][t] += (double) (uf * xf);
+                        }
+                    }
+                }
+            }
+            // keep each chunk's loads and conversions next to their use
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
@@ -1083,7 +1271,7 @@ __device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, u
 // down + residual) for NT tokens.  The input rows come from tagged slot p_in,
 // or (x_lds != nullptr, layer 0) from the rows gathered into LDS.  The
 // output is tagged slot p_out.
-template <int NT, int D, int QD, int FF>
+template <int NT, int D, int QD, int FF, int WT>
 __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int pos0, uint32_t tb, int & p,
                         int p_in, const float * x_lds, int & p_out, bool & dead) {
     constexpr int QKVD = 2 * QD;
@@ -1100,7 +1288,9 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     const int p_qkv = p++;
     if (wg_has_rows<D>(QKVD, 0)) {
         Q8Regs<D, false> R;
-        q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
+        F16Regs<D, false> F;
+        if constexpr (WT == W_Q8) q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
+        else f16_prefetch<D, false>(F, (const uint16_t *) W.qkv, nullptr, QKVD, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.attn_norm, nw);
         RowsT<NT, D> v;
@@ -1110,8 +1300,14 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
             load_tagged<NT, D>(ar + (size_t) p_in * kSlot, tb | p_in, v, dead, A.err);
         }
         rms_rows<NT, D>(v, nw, A.eps, L);
-        quant_rows<NT, D>(v, L);
-        q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead, A.err);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, D>(v, L);
+            q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead, A.err);
+        } else {
+            f16_rows<NT, D, false>(v, L);
+            f16_compute<NT, D, false, false>(F, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0,
+                                             dead, A.err);
+        }
     }
     __syncthreads();
     // attention: code predictor on workgroup g < n_kv_head (KV head g, cache
@@ -1141,41 +1337,69 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     // Wo + residual (the block input)
     const int p_wo = p++;
     if (wg_has_rows<QD>(D, rot)) {
-        Q8Regs<QD, false> R;
-        q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
-        res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
         RowsT<NT, QD> v;
-        load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
-        quant_rows<NT, QD>(v, L);
-        q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in, ar + (size_t) p_wo * kSlot,
-                                  tb | p_wo, rot, dead, A.err);
+        if constexpr (WT == W_Q8) {
+            Q8Regs<QD, false> R;
+            q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
+            res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
+            load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
+            quant_rows<NT, QD>(v, L);
+            q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
+                                      ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
+        } else {
+            F16Regs<QD, false> F;
+            f16_prefetch<QD, false>(F, (const uint16_t *) W.wo, nullptr, D, rot);
+            res_prefetch16<NT, QD, false>(F, ar + (size_t) p_in * kSlot, rot);
+            load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
+            f16_rows<NT, QD, false>(v, L);
+            f16_compute<NT, QD, false, false>(F, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
+                                              ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
+        }
     }
     __syncthreads();
     // gate/up + SwiGLU (RMSNorm'd)
     const int p_gu = p++;
     if (wg_has_rows<D>(FF, 0)) {
         Q8Regs<D, true> R;
-        q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
+        F16Regs<D, true> F;
+        if constexpr (WT == W_Q8) q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
+        else f16_prefetch<D, true>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
         RowsT<NT, D> v;
         load_tagged<NT, D>(ar + (size_t) p_wo * kSlot, tb | p_wo, v, dead, A.err);
         rms_rows<NT, D>(v, nw, A.eps, L);
-        quant_rows<NT, D>(v, L);
-        q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0, dead, A.err);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, D>(v, L);
+            q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0, dead, A.err);
+        } else {
+            f16_rows<NT, D, false>(v, L);
+            f16_compute<NT, D, true, false>(F, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0,
+                                            dead, A.err);
+        }
     }
     __syncthreads();
-    // down + residual
+    // down + residual (F16: the fp32 activation, ffn_down being widened to F32)
     const int p_dn = p++;
     if (wg_has_rows<FF>(D, rot)) {
-        Q8Regs<FF, false> R;
-        q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
-        res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
         RowsT<NT, FF> v;
-        load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
-        quant_rows<NT, FF>(v, L);
-        q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo, ar + (size_t) p_dn * kSlot,
-                                  tb | p_dn, rot, dead, A.err);
+        if constexpr (WT == W_Q8) {
+            Q8Regs<FF, false> R;
+            q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
+            res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
+            load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
+            quant_rows<NT, FF>(v, L);
+            q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
+                                      ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
+        } else {
+            F16Regs<FF, false> F;
+            f16_prefetch<FF, false>(F, (const uint16_t *) W.wd, nullptr, D, rot);
+            res_prefetch16<NT, FF, false>(F, ar + (size_t) p_wo * kSlot, rot);
+            load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
+            f16_rows<NT, FF, true>(v, L);
+            f16_compute<NT, FF, false, true>(F, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
+                                             ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
+        }
     }
     __syncthreads();
     p_out = p_dn;
@@ -1194,7 +1418,7 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
 // kernel argument (cp_embd[s], cp_head[s]) would copy it to private scratch.
 // One workgroup per CU, so one wave per SIMD: the full unified register file
 // (256 VGPRs + 256 AGPRs) is available to every wave.
-template <int D, int QD, int FF>
+template <int D, int QD, int FF, int WT>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(const Args * __restrict__ Ap,
                                                                                          int32_t frame) {
     const Args & A = *Ap;
@@ -1252,8 +1476,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const LayerQ8 * Ls = tk ? A.talker : A.cp;
         for (int l = 0; l < nl; ++l) {
             const float * x_lds = l == 0 ? L.x : nullptr;
-            if (nt == 2) layer_t<2, D, QD, FF>(A, L, Ls[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else layer_t<1, D, QD, FF>(A, L, Ls[l], l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
+            if (nt == 2) layer_t<2, D, QD, FF, WT>(A, L, Ls[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else layer_t<1, D, QD, FF, WT>(A, L, Ls[l], l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
             p_in = p_out;
         }
         // head on the last token's normed row

@@ -38,15 +38,15 @@ def make(cfg, wtype, seed=7, n_ctx=256, norm_mode="one"):
 @pytest.fixture(params=["persistent", "graph"])
 def frame_path(request, monkeypatch):
     """Runs a frame-loop test on both implementations: the persistent
-    cooperative frame kernel (chosen for Q8_0 models) and the captured
-    multi-kernel graph (Q3T_FRAME_KERNEL=0, and every F16 model)."""
+    cooperative frame kernel (the default, Q8_0 or F16 layers) and the
+    captured multi-kernel graph (Q3T_FRAME_KERNEL=0)."""
     monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
     return request.param
 
 
 def check_path(dev, wtype, frame_path):
     us, n, path = dev.frames_stats()
-    want = 1 if (frame_path == "persistent" and wtype == "q8_0") else 0
+    want = 1 if frame_path == "persistent" else 0
     assert path == want, (frame_path, wtype, path)
 
 
@@ -251,3 +251,55 @@ def test_full_q8_mfma_prefill_200_rows():
     assert np.array_equal(hid_g, hid_o)
     assert np.array_equal(log_g, log_o)
     assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+
+
+@pytest.mark.slow
+def test_full_f16_frame_loop_24_greedy(frame_path):
+    """0.6B shapes with F16 weights: F16 GEMVs with fp16-rounded inputs and the
+    widened fp32-input ffn_down, 24 greedy frames equal to the oracle."""
+    cfg = qcfg.full_06b()
+    say("[gpu] full 0.6B F16: synth + upload")
+    w, dev, o = make(cfg, "f16", seed=4, n_ctx=256)
+    text = np.random.default_rng(18).integers(0, 151936, 24).astype(np.int32)
+    spk = np.random.default_rng(19).standard_normal(1024).astype(np.float32)
+    say("[gpu] full F16: oracle generate 24")
+    co, _ = o.generate(text, spk, max_len=24, temperature=0.0, top_k=0)
+    say(f"[gpu] full F16: device generate 24 ({frame_path})")
+    cg = driver.generate(dev, cfg, text, spk, max_len=24, temperature=0.0, top_k=0, chunk=8)
+    check_path(dev, "f16", frame_path)
+    dev.close()
+    assert np.array_equal(cg, co)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_long_context_persistent_matches_graph(wtype, monkeypatch):
+    """The persistent kernel's split talker attention at a 2,100-position
+    context (32 chunks of 80 positions per KV head: prefetched and in-phase
+    cache loads, a partial last chunk) against the multi-kernel frame, whose
+    single-workgroup attention is pinned to the oracle at short contexts.
+    Both paths must give the same codes frame for frame."""
+    cfg = qcfg.full_06b()
+    say(f"[gpu] long context {wtype}: synth + upload")
+    w = Weights(cfg, wtype, seed=6, norm_mode="one")
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    rng = np.random.default_rng(23)
+    rows = (rng.standard_normal((2100, cfg.hidden_size)) * 0.05).astype(np.float32)
+    pad = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+    out = {}
+    try:
+        dev.kv_reserve(2100 + 16)
+        for path in ("1", "0"):
+            monkeypatch.setenv("Q3T_FRAME_KERNEL", path)
+            say(f"[gpu] long context {wtype}: prefill 2100, 6 frames, Q3T_FRAME_KERNEL={path}")
+            dev.prefill(rows, 0, want_hidden=False)
+            dev.frames_begin(pad[None], pad, 2100, 6, repetition_penalty=1.05, temperature=0.0, top_k=0,
+                             eos_bias=-1e4)
+            codes, eos = dev.frames_run(6)
+            us, n, used = dev.frames_stats()
+            assert used == int(path) and codes.shape[0] == 6
+            out[path] = codes
+    finally:
+        dev.close()
+    assert np.array_equal(out["1"], out["0"])
