@@ -532,14 +532,38 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
                 if ((k & mask) == prefix) atomicAdd(&S.hist[(k >> shift) & 255u], 1u);
             }
             __syncthreads();
-            if (t == 0) {
-                int cum = 0, b = 255;
-                for (; b > 0; --b) {
-                    if (cum + (int) S.hist[b] >= remaining) break;
-                    cum += (int) S.hist[b];
+            if (t < 64) {
+                // The bin holding the remaining-th largest key: the highest b >= 1
+                // with count(bins >= b) >= remaining (else bin 0), and how many of
+                // its keys are still to go.  Wave 0 finds it with a suffix scan,
+                // lane l owning bins 4l .. 4l+3.
+                int h[4], own = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { h[e] = (int) S.hist[4 * t + e]; own += h[e]; }
+                int incl = own;                        // keys in bins of lanes >= t
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const int o = __shfl_down(incl, off);
+                    if (t + off < 64) incl += o;
                 }
-                S.sel[0] = (uint32_t) b;
-                S.sel[1] = (uint32_t) (remaining - cum);
+                int above = incl - own, best = -1, best_above = 0;
+#pragma unroll
+                for (int e = 3; e >= 0; --e) {
+                    const int b = 4 * t + e;
+                    if (best < 0 && b >= 1 && above + h[e] >= remaining) { best = b; best_above = above; }
+                    above += h[e];
+                }
+                int bmax = best;
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) bmax = max(bmax, __shfl_xor(bmax, off));
+                if (bmax >= 0 && best == bmax) {
+                    S.sel[0] = (uint32_t) best;
+                    S.sel[1] = (uint32_t) (remaining - best_above);
+                }
+                if (bmax < 0 && t == 0) {
+                    S.sel[0] = 0u;
+                    S.sel[1] = (uint32_t) (remaining - (incl - h[0]));
+                }
             }
             __syncthreads();
             prefix |= S.sel[0] << shift;
