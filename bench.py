@@ -105,6 +105,53 @@ def prefill_bench(args, cfg, w):
         "mfma_util": round(gemm_ops / dt / 5.0e15, 4) if args.weights == "q8_0" else None}))
 
 
+def step_bench(args, cfg, w):
+    """One talker decode step (forward_step: 28 layers + output norm + codec
+    head, batch 1) with the KV cache pre-filled at 512 positions with seeded
+    N(0, 1) fp16 K/V rows, the new token at position 512.  Each call is one
+    q3t_dev_talker_step (the multi-kernel step, logits and hidden copied back
+    to the host); reports the mean wall time per step and the per-kernel HIP
+    event timings of talker layer 0 at that context."""
+    from qwen3_tts_amd.device import Device
+    rng = np.random.default_rng(31)
+    n_kv = 512
+    dev = Device(cfg, 0)
+    dev.upload_weights(w)
+    dev.kv_reserve(n_kv + 8)
+    for layer in range(cfg.n_layers):
+        k = rng.standard_normal((n_kv, cfg.n_kv_head, cfg.head_dim)).astype(np.float16)
+        v = rng.standard_normal((n_kv, cfg.n_kv_head, cfg.head_dim)).astype(np.float16)
+        dev.kv_write(layer, k, v)
+    x = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+    for _ in range(max(args.warmup, 1)):
+        dev.talker_step(x, n_kv)
+    steps = max(args.steps, 1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dev.talker_step(x, n_kv)
+    dt = (time.perf_counter() - t0) / steps
+    kernels = {}
+    names = {0: "gemv_gate_up_swiglu", 1: "gemv_qkv_rmsnorm", 2: "gemv_down_resid", 3: "gemv_wo_resid",
+             4: "attention_decode"}
+    for k_, nm in names.items():
+        us, b = dev.time_kernel(k_, 100)
+        kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
+    dev.close()
+    wbytes = sum(a.nbytes for n_, (_, _, a) in w.tensors.items() if n_.startswith("talker.blk.")) + \
+        w.tensors["talker.codec_head.weight"][2].nbytes
+    kvbytes = cfg.n_layers * cfg.n_kv_head * cfg.head_dim * 2 * 2 * (n_kv + 1)
+    print(json.dumps({
+        "metric": "talker decode step latency (KV 512)", "value": round(dt * 1e3, 4), "unit": "ms",
+        "n_gpus": 1, "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": False, "dtype": "int8" if args.weights == "q8_0" else "f16",
+        "data": "synthetic (seeded weights, N(0,1) fp16 KV)",
+        "config": {"workload": f"one talker decode step, {args.weights.upper()} 0.6B shapes, KV pre-filled to "
+                               f"{n_kv} positions, multi-kernel step with host copy-back", "global_batch": 1},
+        "step_algorithmic_bytes": int(wbytes + kvbytes),
+        "step_hbm_gbs": round((wbytes + kvbytes) / dt / 1e9, 1),
+        "kernels": kernels}))
+
+
 def long_bench(args, cfg, w):
     """Long-context sampled decode: prefill rows [N(0,1) speaker row;
     text_proj(2048 uniform ids)] through one prefill call, then args.steps
@@ -243,6 +290,8 @@ def main():
                     help="launches per per-kernel timing of the multi-kernel path (0: skip)")
     ap.add_argument("--prefill", type=int, default=0,
                     help="instead of the frame loop, time one talker prefill of this many rows (Q8_0: int8 MFMA path)")
+    ap.add_argument("--talker-step", action="store_true",
+                    help="instead of the frame loop, time one talker decode step at a 512-position KV cache")
     ap.add_argument("--long", action="store_true",
                     help="instead of the short-prompt greedy loop, time long-context sampled decode after a long prefill")
     ap.add_argument("--long-prompt", type=int, default=2048, help="text ids of the --long prefill")
@@ -270,6 +319,8 @@ def main():
         return streams_bench(args, cfg, w)
     if args.long:
         return long_bench(args, cfg, w)
+    if args.talker_step:
+        return step_bench(args, cfg, w)
     rng = np.random.default_rng(12)
     text = rng.integers(0, cfg.text_vocab, args.prompt).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)

@@ -918,25 +918,26 @@ int q3t_dev_kv_write(q3t_dev * c, int32_t layer, int32_t n_pos, const uint16_t *
     return 0;
 }
 
-// Whether the talker prefill of n tokens runs on the int8 MFMA path: Q8_0
-// layers with GEMM-friendly widths, n >= 16 (Q3T_PREFILL_MFMA=0 disables it,
-// =1 uses it for any n).
-bool use_mfma_prefill(q3t_dev * c, int n) {
+// Which tiled path the talker prefill of n tokens takes: 1 = int8 MFMA GEMMs
+// (Q8_0 layers), 2 = exact F16 VALU GEMMs (F16 layers), 0 = the chunked GEMV
+// prefill.  Tiled needs GEMM-friendly widths and n >= 16
+// (Q3T_PREFILL_MFMA=0 disables it, =1 uses it for any n).
+int tiled_prefill(q3t_dev * c, int n) {
     const char * e = std::getenv("Q3T_PREFILL_MFMA");
-    if (e && e[0] == '0') return false;
-    if (!(e && e[0] == '1') && n < 16) return false;
+    if (e && e[0] == '0') return 0;
+    if (!(e && e[0] == '1') && n < 16) return 0;
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
     if (g.head_dim != 128 || d % 128 || qd % 128 || g.ffn_size % 128 || qkvd % pf::kTile || d % pf::kTile ||
         g.ffn_size % pf::kTile)
-        return false;
+        return 0;
+    const int lt = c->talker[0].qkv.type;
+    if (lt != Q3T_TYPE_Q8_0 && lt != Q3T_TYPE_F16) return 0;
     for (int i = 0; i < g.n_layers; ++i) {
         const LayerDev & L = c->talker[i];
-        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
-            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
-            return false;
+        if (L.qkv.type != lt || L.wo.type != lt || L.wg.type != lt || L.wu.type != lt || L.wd.type != lt) return 0;
     }
-    return true;
+    return lt == Q3T_TYPE_Q8_0 ? 1 : 2;
 }
 
 int ensure_pf(q3t_dev * c, int n) {
@@ -971,6 +972,60 @@ void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w, int x
               float * dx = nullptr) {
     hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, xs < 0 ? K : xs, K, w, c->cfg.rms_eps,
                        q ? q : c->pf_q, dx ? dx : c->pf_dx);
+}
+
+// F16 weights x fp32 rows on the exact VALU GEMM: y = epi(W . rows of x),
+// x rounded to fp16 unless wide (the widened ffn_down).
+void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, int xs, bool wide, float * y,
+                 const float * res, int rs) {
+    const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
+    if (wide)
+        hipLaunchKernelGGL(pf::k_gemm_f16<true>, grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, x, xs,
+                           n, y, N, res, rs);
+    else
+        hipLaunchKernelGGL(pf::k_gemm_f16<false>, grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, x,
+                           xs, n, y, N, res, rs);
+}
+
+// Talker prefill of n tokens (rows in c->stage) with F16 layers on the exact
+// VALU GEMMs; same layer program and buffers as prefill_mfma (c->pf_f holds
+// the RMSNorm'd rows until SwiGLU overwrites it).
+void prefill_f16(q3t_dev * c, int n, int n_past) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int ffn = g.ffn_size;
+    const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
+    const float scale = 1.0f / std::sqrt((float) g.head_dim);
+    const float * x = c->stage;
+    for (int il = 0; il < g.n_layers; ++il) {
+        const LayerDev & L = c->talker[il];
+        uint16_t * kc = c->kc + il * lstride;
+        uint16_t * vc = c->vc + il * lstride;
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, x, L.attn_norm, g.rms_eps, d, c->pf_f);
+        pf_gemm_f16(c, L.qkv, qkvd, d, n, c->pf_f, d, false, c->pf_qkv, nullptr, 0);
+        hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+                           qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
+                           kc, vc, c->n_ctx, n_past);
+        hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
+                           c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
+                           (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
+                           g.n_kv_head, n_past, scale, c->pf_att, qd);
+        pf_gemm_f16(c, L.wo, d, qd, n, c->pf_att, qd, false, c->pf_xb, x, d);
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xb, L.ffn_norm,
+                           g.rms_eps, d, c->pf_f);
+        pf_gemm_f16(c, L.wg, ffn, d, n, c->pf_f, d, false, c->pf_g, nullptr, 0);
+        pf_gemm_f16(c, L.wu, ffn, d, n, c->pf_f, d, false, c->pf_u, nullptr, 0);
+        const size_t cnt = (size_t) n * ffn;
+        hipLaunchKernelGGL(pf::k_swiglu_rows, dim3((unsigned) std::min<size_t>((cnt + kBlock - 1) / kBlock, 4096)),
+                           dim3(kBlock), 0, c->stream, (const float *) c->pf_g, (const float *) c->pf_u, c->pf_f, cnt);
+        pf_gemm_f16(c, L.wd, d, ffn, n, c->pf_f, ffn, true, c->pf_xa, c->pf_xb, d);
+        x = c->pf_xa;
+    }
+    GemvSpec h{};
+    h.w = weight_of(c->codec_head); h.rows = g.codec_vocab; h.K = d;
+    h.x = c->pf_xa + (size_t) (n - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
+    h.hidden_out = c->hidden; h.hidden_stride = d; h.y = c->logits; h.y_stride = g.codec_vocab;
+    gemv(c, h, 1);
 }
 
 // Talker prefill of n tokens (rows in c->stage) on the MFMA path; the output
@@ -1032,9 +1087,10 @@ int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, 
     FrameState s{};
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) n * d * 4, hipMemcpyHostToDevice, c->stream));
-    if (use_mfma_prefill(c, n)) {
+    if (const int tp = tiled_prefill(c, n)) {
         if (ensure_pf(c, n)) return -1;
-        prefill_mfma(c, n, n_past);
+        if (tp == 1) prefill_mfma(c, n, n_past);
+        else prefill_f16(c, n, n_past);
         if (hidden_out)
             hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xa,
                                (const float *) c->out_norm.data, g.rms_eps, d, c->hidden_all);

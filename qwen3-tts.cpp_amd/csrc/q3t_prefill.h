@@ -154,6 +154,78 @@ __global__ __launch_bounds__(kBlock) void k_gemm_q8(const int8_t * __restrict__ 
 
 __host__ __device__ constexpr size_t gemm_lds_bytes(int K) { return (size_t) 2 * kTile * (K / kQK) * sizeof(float); }
 
+// F16 weights: Y[t][r] = epi(sum_k W[r][k] * x[t][k]) with x rounded to fp16
+// (WIDE = false, the F16-weight contract) or kept fp32 (WIDE = true, the
+// widened ffn_down).  Both products are exact in fp64, so each is one fp64
+// fma and the sum is rounded to fp32 once, as in the GEMV path.  fp16 MFMA
+// would accumulate in fp32, so this runs on the VALU: a 64-row x 64-token
+// tile per workgroup, K in steps of 32 staged as fp32 in LDS, each thread a
+// 4 x 4 block of outputs (rows 4*(t%16).., tokens 4*(t/16)..).
+// Requires N % 64 == 0, K % 32 == 0 (the host checks).
+constexpr int kF16Kc = 32;
+template <bool WIDE>
+__global__ __launch_bounds__(kBlock) void k_gemm_f16(const uint16_t * __restrict__ W, int32_t N, int32_t K,
+                                                     const float * __restrict__ x, int32_t xs, int32_t n,
+                                                     float * __restrict__ Y, int32_t ys, const float * __restrict__ res,
+                                                     int32_t rs) {
+    __shared__ float sw[kF16Kc][kTile + 1];   // [k][row]
+    __shared__ float sx[kF16Kc][kTile + 1];   // [k][token]
+    const int t = threadIdx.x, r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
+    const int tr = (t & 15) * 4, tt = (t >> 4) * 4;
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    // staging: thread t loads 8 consecutive k of row / token (t / 4), part t % 4
+    const int lr = t >> 2, lk = (t & 3) * 8;
+    for (int k0 = 0; k0 < K; k0 += kF16Kc) {
+        {
+            const int4 wv = *(const int4 *) (W + (size_t) (r0 + lr) * K + k0 + lk);
+            const uint16_t * wh = (const uint16_t *) &wv;
+            const int tok = t0 + lr;
+            float xv[8];
+            if (tok < n) {
+                const float4 a = *(const float4 *) (x + (size_t) tok * xs + k0 + lk);
+                const float4 b = *(const float4 *) (x + (size_t) tok * xs + k0 + lk + 4);
+                xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sw[lk + e][lr] = h2f(wh[e]);
+                sx[lk + e][lr] = WIDE ? xv[e] : round_f16(xv[e]);
+            }
+            __syncthreads();
+        }
+#pragma unroll 8
+        for (int k = 0; k < kF16Kc; ++k) {
+            double wd[4], xd[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { wd[i] = (double) sw[k][tr + i]; xd[i] = (double) sx[k][tt + i]; }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fma(wd[i], xd[j], acc[i][j]);   // exact products
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tok = t0 + tt + j;
+        if (tok >= n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = r0 + tr + i;
+            float v = (float) acc[i][j];
+            if (res) v = v + res[(size_t) tok * rs + r];
+            Y[(size_t) tok * ys + r] = v;
+        }
+    }
+}
+
 // SwiGLU over rows: f = silu(g) * u.
 __global__ __launch_bounds__(kBlock) void k_swiglu_rows(const float * __restrict__ g, const float * __restrict__ u,
                                                         float * __restrict__ f, size_t count) {

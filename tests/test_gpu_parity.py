@@ -226,6 +226,35 @@ def test_fp16_tie_rounding_regression(frame_path):
 
 
 @pytest.mark.slow
+def test_full_f16_tiled_prefill_200_rows():
+    """Exact F16 VALU-GEMM prefill of 200 rows at the 0.6B shapes (fp16-rounded
+    inputs, widened ffn_down): every normed hidden row and the last-row logits
+    equal the oracle, and so does a following talker step over the 200 cached
+    rows."""
+    cfg = qcfg.full_06b()
+    say("[gpu] full 0.6B F16 tiled prefill: synth + upload")
+    w, dev, o = make(cfg, "f16", seed=8, n_ctx=256)
+    rng = np.random.default_rng(14)
+    embd = (rng.standard_normal((200, cfg.hidden_size)) * 0.05).astype(np.float32)
+    import os
+    os.environ["Q3T_PREFILL_MFMA"] = "1"
+    try:
+        say("[gpu] full F16: device prefill 200")
+        hid_g, log_g = dev.prefill(embd, 0)
+        e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+        lg, hg = dev.talker_step(e, 200)
+    finally:
+        del os.environ["Q3T_PREFILL_MFMA"]
+    say("[gpu] full F16: oracle prefill 200")
+    hid_o, log_o = o.prefill(embd, 0)
+    lo, ho = o.step(e, 200)
+    dev.close()
+    assert np.array_equal(hid_g, hid_o)
+    assert np.array_equal(log_g, log_o)
+    assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+
+
+@pytest.mark.slow
 def test_full_q8_mfma_prefill_200_rows():
     """int8 MFMA prefill of 200 rows at the 0.6B shapes: every normed hidden
     row and the last-row logits equal the oracle; a following talker step
