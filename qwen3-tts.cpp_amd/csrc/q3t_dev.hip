@@ -112,6 +112,8 @@ struct q3t_dev {
     // persistent frame kernel (q3t_frame_kernel.h)
     bool fk_ok = false;            // model / context qualify this context for it
     int fk_variant = 0;            // see fk_kernel()
+    bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
+    bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
     int fk_grid = 0;
     fk::LayerQ8 * fk_layers = nullptr;
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
@@ -380,6 +382,27 @@ struct AttnSpec {
 
 void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     const q3t_config & g = c->cfg;
+    const int G = g.n_head / g.n_kv_head;
+    if (nt == 1 && s.rc == c->rope_cos && !s.probs && (G == 1 || G == 2 || G == 4) && c->gqa_lds_ok) {
+        // one talker token: a 16-wave workgroup per KV head reads each cached
+        // K/V row once for the group's query heads (ms::k_attn_gqa)
+        ms::GqaArgs q{};
+        q.qkv = s.qkv; q.qkv_stride = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
+        q.q_norm = s.L->q_norm; q.k_norm = s.L->k_norm; q.eps = g.rms_eps;
+        q.rope_cos = s.rc; q.rope_sin = s.rs;
+        q.kc = s.kc; q.vc = s.vc; q.kv_stream = 0; q.n_ctx = s.n_ctx;
+        q.n_head = g.n_head; q.n_kv_head = g.n_kv_head;
+        q.pos = s.pos_ptr; q.pos_stream = 0; q.pos_const = s.pos_const;
+        q.done = &c->st->done; q.done_stream = 0;
+        q.out = c->attn; q.out_stride = g.n_head * g.head_dim;
+        q.scale = 1.0f / std::sqrt((float) g.head_dim);
+        const dim3 grid(g.n_kv_head, 1), block(ms::kAThreads);
+        const size_t lds = ms::attn_gqa_lds_bytes(G, s.n_ctx);
+        if (G == 1) hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, lds, c->stream, q);
+        else if (G == 2) hipLaunchKernelGGL(ms::k_attn_gqa<2>, grid, block, lds, c->stream, q);
+        else hipLaunchKernelGGL(ms::k_attn_gqa<4>, grid, block, lds, c->stream, q);
+        return;
+    }
     AttnArgs a{};
     a.qkv = s.qkv; a.qkv_stride = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
     a.q_norm = s.L->q_norm; a.k_norm = s.L->k_norm; a.eps = g.rms_eps;
@@ -555,6 +578,7 @@ int slots_for(int K) {
 
 int fk_prepare(q3t_dev * c) {
     c->fk_ok = false;
+    if (c->fk_refused) return 0;
     if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
@@ -651,9 +675,21 @@ fk::Args fk_args(q3t_dev * c) {
     return A;
 }
 
-int fk_launch(q3t_dev * c, int32_t frame) {
+hipError_t fk_launch(q3t_dev * c, int32_t frame) {
     void * args[] = {&c->fk_args_dev, &frame};
-    HIP_OK(hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream));
+    return hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream);
+}
+
+// The captured multi-kernel frame, built on first use.
+int ensure_frame_graph(q3t_dev * c) {
+    if (c->frame_exec) return 0;
+    HIP_OK(hipStreamSynchronize(c->stream));
+    HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    frame_seq(c);
+    hipGraph_t graph = nullptr;
+    HIP_OK(hipStreamEndCapture(c->stream, &graph));
+    c->frame_graph = graph;
+    HIP_OK(hipGraphInstantiate(&c->frame_exec, graph, nullptr, nullptr, 0));
     return 0;
 }
 
@@ -890,6 +926,22 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
     HIP_OK(hipMemcpy(c->cp_rope_sin, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
     c->n_ctx = n_ctx;
     c->rope_rows = rows;
+    {
+        // single-token talker attention through the GQA kernel when its LDS fits
+        int max_lds = 0;
+        HIP_OK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device));
+        const int G = g.n_kv_head > 0 ? g.n_head / g.n_kv_head : 0;
+        c->gqa_lds_ok = false;
+        if (G == 1 || G == 2 || G == 4) {
+            const size_t al = ms::attn_gqa_lds_bytes(G, n_ctx);
+            if (al <= (size_t) max_lds) {
+                const void * fn = G == 1 ? (const void *) ms::k_attn_gqa<1>
+                                : G == 2 ? (const void *) ms::k_attn_gqa<2> : (const void *) ms::k_attn_gqa<4>;
+                HIP_OK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
+                c->gqa_lds_ok = true;
+            }
+        }
+    }
     return sync(c);
 }
 
@@ -1290,14 +1342,7 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
         HIP_OK(hipMemcpyAsync(c->fk_args_dev, &host_args, sizeof host_args, hipMemcpyHostToDevice, c->stream));
     }
     if (sync(c)) return -1;
-    if (!c->fk_ok && !c->frame_exec) {
-        HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        frame_seq(c);
-        hipGraph_t graph = nullptr;
-        HIP_OK(hipStreamEndCapture(c->stream, &graph));
-        c->frame_graph = graph;
-        HIP_OK(hipGraphInstantiate(&c->frame_exec, graph, nullptr, nullptr, 0));
-    }
+    if (!c->fk_ok && ensure_frame_graph(c)) return -1;
     c->host_emitted = 0;
     c->frames_launched = 0;
     c->run_us = 0.0;
@@ -1322,8 +1367,21 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     }
     if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[0], c->stream));
     for (int i = 0; i < n_frames; ++i) {
-        if (c->fk_ok) { if (fk_launch(c, c->frames_launched + i)) return -1; }
-        else if (no_graph) frame_seq(c);
+        if (c->fk_ok) {
+            const hipError_t e = fk_launch(c, c->frames_launched + i);
+            if (e == hipSuccess) continue;
+            // The cooperative launch can be refused while another process holds
+            // the device's cooperative-launch resources.  Nothing was enqueued:
+            // continue this context on the captured multi-kernel frame, which
+            // shares the frame state and gives the same codes.
+            (void) hipGetLastError();
+            std::fprintf(stderr, "q3t: cooperative frame-kernel launch refused (%s); using the multi-kernel frame\n",
+                         hipGetErrorString(e));
+            c->fk_ok = false;
+            c->fk_refused = true;
+            if (ensure_frame_graph(c)) return -1;
+        }
+        if (no_graph) frame_seq(c);
         else HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
     }
     if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[1], c->stream));

@@ -379,10 +379,11 @@ struct GqaArgs {
     uint16_t * kc; uint16_t * vc;              // layer base of stream 0, [n_kv_head][n_ctx][128]
     int64_t kv_stream;                         // elements per stream
     int32_t n_ctx, n_head, n_kv_head;
-    const int32_t * pos; int32_t pos_stream;   // position of stream s at pos[s * pos_stream]
-    const int32_t * done; int32_t done_stream; // stream s idles while done[s * done_stream]
+    const int32_t * pos; int32_t pos_stream;   // position of stream s at pos[s * pos_stream] (NULL: pos_const)
+    int32_t pos_const;
+    const int32_t * done; int32_t done_stream; // stream s idles while done[s * done_stream] (NULL: never)
     float * out; int32_t out_stride;           // stream s's [n_head * 128] row
-    int8_t * out_q; float * out_dx;            // its Q8_0 copy: [n_head * 128] int8, [n_head * 4] scales
+    int8_t * out_q; float * out_dx;            // its Q8_0 copy: [n_head * 128] int8, [n_head * 4] scales (NULL: none)
     float scale;
 };
 
@@ -414,7 +415,7 @@ __device__ __forceinline__ void wave_norm_rope(float & x0, float & x1, const flo
 template <int G>
 __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
     const int g = blockIdx.x, z = blockIdx.y;
-    if (a.done[(size_t) z * a.done_stream]) return;
+    if (a.done && a.done[(size_t) z * a.done_stream]) return;
     extern __shared__ __align__(16) char smem[];
     float * qf = (float *) smem;                  // [G][128] fp16-rounded rotated q
     float * knew = qf + G * kHD;                  // [128]
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
     double * pv = (double *) sc;                  // after the scores are consumed: [16][G][128]
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int pos = a.pos[(size_t) z * a.pos_stream], n_kv = pos + 1;
+    const int pos = a.pos ? a.pos[(size_t) z * a.pos_stream] : a.pos_const, n_kv = pos + 1;
     const int qd = a.n_head * kHD, kd = a.n_kv_head * kHD;
     const float * row = a.qkv + (size_t) z * a.qkv_stride;
     uint16_t * kbase = a.kc + z * a.kv_stream + (size_t) g * a.n_ctx * kHD;
@@ -612,7 +613,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
         const float o = (float) r;
         const size_t e = (size_t) z * a.out_stride + (g * G + h) * kHD + d;
         a.out[e] = o;
-        a.out_q[e] = quant_lane32(o, a.out_dx + e / kQK, (t & 31) == 0);
+        if (a.out_q) a.out_q[e] = quant_lane32(o, a.out_dx + e / kQK, (t & 31) == 0);
     }
 }
 
