@@ -910,6 +910,7 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
 // The chunk's cached K and V rows are loaded before the QKV wait (they do not
 // depend on the new token), kPre position steps of each.
 constexpr int kPre = 4;                      // position steps of K and V prefetched per thread
+constexpr int kScoreRow = 1024;              // two-phase form: scores per head row (8 groups x 2 heads in 2 slots)
 constexpr int kPvSlots = 16;                 // arena slots phase C spans (256 wg x 512 halves)
 constexpr int kMaxChunk = kMaxCtx;           // longest chunk whose scores fit L.sc
 
@@ -952,10 +953,12 @@ __device__ __forceinline__ void att_prefetch(const Args & A, int layer, const At
     }
 }
 
+// score_out != nullptr (two-phase form): the chunk's scores themselves are
+// published at score_out[(2g + h) * kScoreRow + j] instead of its maxima.
 __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                           int pos0, int qd, const AttSplit & s, const KvPre & P,
                                                           const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out,
-                                                          uint32_t out_tag, bool & dead) {
+                                                          uint32_t out_tag, bool & dead, uint64_t * score_out = nullptr) {
     if (s.c >= s.C) return;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = s.g;
     const int kd = qd / 2;
@@ -1044,11 +1047,20 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
         a1 = group_sum_d(a1, 16);
         if (j < s.j1) {
             const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
-            if (sub == 0) { L.sc[j - s.j0] = s0; L.sc[kMaxChunk + j - s.j0] = s1; }
+            if (sub == 0) {
+                if (score_out) {
+                    tstore(score_out + (size_t) (2 * g) * kScoreRow + j, out_tag, s0);
+                    tstore(score_out + (size_t) (2 * g + 1) * kScoreRow + j, out_tag, s1);
+                } else {
+                    L.sc[j - s.j0] = s0;
+                    L.sc[kMaxChunk + j - s.j0] = s1;
+                }
+            }
             lm0 = fmaxf(lm0, s0);
             lm1 = fmaxf(lm1, s1);
         }
     }
+    if (score_out) return;
     lm0 = wave_max_f(lm0);
     lm1 = wave_max_f(lm1);
     if (lane == 0) { L.fred[wave] = lm0; L.fred[kW + wave] = lm1; }
@@ -1181,6 +1193,135 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
     }
 }
 
+// Talker contexts up to kScoreRow positions take two phases instead of four:
+//   A  as in the split form, but each chunk workgroup publishes its scores
+//      (2 heads x its positions, into two consecutive arena slots);
+//   B  every workgroup of KV head g gathers the head group's whole score row,
+//      runs the softmax (maximum, exp, fp64 sum, fp16 probabilities; cheap and
+//      identical in every workgroup) and forms DPW = 128 * H / grid output
+//      dims of both heads over all positions, publishing the attention rows.
+// This workgroup's V columns (positions t + 256u) are loaded before the QKV
+// wait.  Longer contexts use the four-phase form.
+struct KvCols {
+    uint16_t v[4][4];                        // V[t + 256u][c*DPW + d]
+};
+
+__device__ __forceinline__ bool att_two_phase(const Args & A, int n_kv) {
+    const int C = (int) gridDim.x / A.n_kv_head;
+    return n_kv <= kScoreRow && C >= 32 && 128 % C == 0 && 2 * A.n_kv_head * kScoreRow <= 2 * kSlot;
+}
+
+__device__ __forceinline__ void att2_prefetch(const Args & A, int layer, int pos0, KvCols & P) {
+    const int H = A.n_kv_head, C = (int) gridDim.x / H, dpw = 128 / C;
+    const int g = (int) blockIdx.x % H, c = (int) blockIdx.x / H;
+    if (c >= C) return;
+    const size_t base = ((size_t) layer * H + g) * A.n_ctx * 128;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int j = (int) threadIdx.x + u * kT;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            if (d < dpw && j < pos0) P.v[u][d] = A.vc[base + (size_t) j * 128 + c * dpw + d];
+    }
+}
+
+__device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, int pos0, const KvCols & P,
+                                                       const uint64_t * scores, uint32_t sc_tag, uint64_t * out,
+                                                       uint32_t out_tag, bool & dead) {
+    const int H = A.n_kv_head, C = (int) gridDim.x / H, dpw = 128 / C;
+    const int g = (int) blockIdx.x % H, c = (int) blockIdx.x / H;
+    if (c >= C) return;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, n_kv = pos0 + 1;
+    const float * vnew = L.a + 3 * 128;
+    // the head group's score rows into L.sc[h * kMaxChunk + j]
+    for (int i0 = 0; i0 < 2 * n_kv; i0 += kB * kT) {
+        const uint64_t * ptr[kB];
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+            const int i = i0 + k * kT + t;
+            const int h = i >= n_kv, j = i - h * n_kv;
+            ptr[k] = scores + (size_t) (2 * g + h) * kScoreRow + (i < 2 * n_kv ? j : 0);
+            if (i < 2 * n_kv) cnt = k + 1;
+        }
+        float val[kB];
+        twait_batch<kB>(ptr, cnt, sc_tag, val, dead, A.err);
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+            const int i = i0 + k * kT + t;
+            if (i < 2 * n_kv) {
+                const int h = i >= n_kv, j = i - h * n_kv;
+                L.sc[h * kMaxChunk + j] = val[k];
+            }
+        }
+    }
+    __syncthreads();
+    float lm0 = -INFINITY, lm1 = -INFINITY;
+    for (int j = t; j < n_kv; j += kT) { lm0 = fmaxf(lm0, L.sc[j]); lm1 = fmaxf(lm1, L.sc[kMaxChunk + j]); }
+    lm0 = wave_max_f(lm0);
+    lm1 = wave_max_f(lm1);
+    if (lane == 0) { L.fred[wave] = lm0; L.fred[kW + wave] = lm1; }
+    __syncthreads();
+    float mx0 = L.fred[0], mx1 = L.fred[kW];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) { mx0 = fmaxf(mx0, L.fred[w]); mx1 = fmaxf(mx1, L.fred[kW + w]); }
+    double ls0 = 0.0, ls1 = 0.0;
+    for (int j = t; j < n_kv; j += kT) {
+        const float e0 = expf_q3t(L.sc[j] - mx0), e1 = expf_q3t(L.sc[kMaxChunk + j] - mx1);
+        L.sc[j] = e0; L.sc[kMaxChunk + j] = e1;
+        ls0 += (double) e0; ls1 += (double) e1;
+    }
+    ls0 = wave_sum_d(ls0);
+    ls1 = wave_sum_d(ls1);
+    if (lane == 0) { L.red[wave] = ls0; L.red[kW + wave] = ls1; }
+    __syncthreads();
+    double sum0 = L.red[0], sum1 = L.red[kW];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) { sum0 += L.red[w]; sum1 += L.red[kW + w]; }
+    const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
+    // P.V for this workgroup's dims: thread t owns positions t + 256u
+    double o[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[h][d] = 0.0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int j = t + u * kT;
+        if (j < n_kv) {
+            const double p0 = (double) round_f16(L.sc[j] * inv0), p1 = (double) round_f16(L.sc[kMaxChunk + j] * inv1);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                if (d >= dpw) break;
+                // fp16 probability x fp16 value: exact in fp64
+                const double vd = (double) (j == pos0 ? vnew[c * dpw + d] : h2f(P.v[u][d]));
+                o[0][d] = fma(p0, vd, o[0][d]);
+                o[1][d] = fma(p1, vd, o[1][d]);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[h][d] = wave_sum_d(o[h][d]);
+    double * part = (double *) L.sc;       // [wave][head][4] (the probabilities are consumed)
+    __syncthreads();
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) part[(wave * 2 + h) * 4 + d] = o[h][d];
+    }
+    __syncthreads();
+    if (t < 2 * dpw) {
+        const int h = t / dpw, d = t % dpw;
+        double r = part[h * 4 + d];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) r += part[(w * 2 + h) * 4 + d];
+        tstore(out + (g * 2 + h) * 128 + c * dpw + d, out_tag, (float) r);
+    }
+}
+
 // Phase D: 8 attention outputs per workgroup (n_head * 128 over the grid),
 // each the chunk-ordered fp64 sum of its KV head's C partials.
 __device__ __attribute__((always_inline)) void att_combine(const Args & A, Lds & L, const uint64_t * in,
@@ -1283,7 +1424,10 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     // talker: this workgroup's chunk of cached K/V rows, loaded now (it does
     // not depend on anything this frame computes)
     KvPre kv;
+    KvCols kc2;
+    const bool two_phase = !cp && att_two_phase(A, pos0 + 1);
     if (!cp) att_prefetch(A, layer, att_split(A, pos0 + 1), pos0, kv);
+    if (two_phase) att2_prefetch(A, layer, pos0, kc2);
     // QKV (RMSNorm'd input)
     const int p_qkv = p++;
     if (wg_has_rows<D>(QKVD, 0)) {
@@ -1318,6 +1462,18 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         if ((int) blockIdx.x < A.n_kv_head)
             attention_cp(A, L, W, layer, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
                          ar + (size_t) p_att * kSlot, tb | p_att, dead);
+        __syncthreads();
+    } else if (two_phase) {
+        // scores in the two slots p_a, p_a + 1; the other split-phase slots stay
+        // unused, so both forms share one phase numbering
+        const AttSplit sp = att_split(A, pos0 + 1);
+        const int p_a = p;
+        p += 2 + kPvSlots;
+        p_att = p++;
+        att_scores(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+                   ar + (size_t) p_a * kSlot, tb | p_a, dead, ar + (size_t) p_a * kSlot);
+        __syncthreads();
+        att2_pv(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot, tb | p_att, dead);
         __syncthreads();
     } else {
         const AttSplit sp = att_split(A, pos0 + 1);
