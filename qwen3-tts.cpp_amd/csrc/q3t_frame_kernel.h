@@ -675,26 +675,40 @@ struct Cb0Xf {
 // candidate: the first maximum over its rows (after the codebook-0
 // transforms when xf != nullptr), tagged at cand_tagged[2b], [2b+1] or plain
 // in cand_val[b] / cand_idx[b].  All threads of the workgroup must call it.
+struct HeadRegs {
+    int4 w[2][4];
+    int ng;
+};
+
+// The head rows' weights of this lane, loaded before the head input is awaited.
 template <int K>
-__device__ __forceinline__ void f16_head(const uint16_t * W, int rows, Lds & L, uint64_t * out_tagged,
+__device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, HeadRegs & H) {
+    constexpr int LPR = K / kQK, RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
+    const int groups = rows / RPW;
+    const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;
+    H.ng = 0;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = gw + gi * nw;
+        if (g >= groups) break;
+        H.ng = gi + 1;
+        const int4 * wp = (const int4 *) (W + (size_t) (g * RPW + rsub) * K + lir * kQK);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) H.w[gi][c] = wp[c];
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, uint64_t * out_tagged,
                                          uint32_t tag, float * out_plain, const Cb0Xf * xf, uint64_t * cand_tagged,
                                          float * cand_val, int32_t * cand_idx) {
     static_assert(K / kQK <= 32 && ((K / kQK) & (K / kQK - 1)) == 0, "head width");
     constexpr int LPR = K / kQK, RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
-    const int groups = rows / RPW;
     const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;
-    int4 w[2][4];
-    int ng = 0;
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-        const int g = gw + gi * nw;
-        if (g >= groups) break;
-        ng = gi + 1;
-        const int4 * wp = (const int4 *) (W + (size_t) (g * RPW + rsub) * K + lir * kQK);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) w[gi][c] = wp[c];
-    }
+    const int ng = H.ng;
+    (void) rows;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     if (ng > 0) {
@@ -707,10 +721,8 @@ __device__ __forceinline__ void f16_head(const uint16_t * W, int rows, Lds & L, 
             for (int j = 0; j < 8; ++j) {
                 const double xd = (double) h2f(xh[j]);
 #pragma unroll
-                for (int gi = 0; gi < 2; ++gi) {
-                    const uint16_t * wh = (const uint16_t *) &w[gi][c];
-                    acc[gi] = fma((double) h2f(wh[j]), xd, acc[gi]);   // fp16 x fp16: exact product
-                }
+                for (int gi = 0; gi < 2; ++gi)
+                    acc[gi] = fma((double) h8(H.w[gi][c], j), xd, acc[gi]);   // fp16 x fp16: exact product
             }
         }
 #pragma unroll
@@ -1638,6 +1650,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         }
         // head on the last token's normed row
         const int p_head = tk ? 0 : p++;
+        HeadRegs hr;
+        if (tk) f16_head_prefetch<D>(A.codec_head, A.codec_vocab, hr);
+        else f16_head_prefetch<D>(A.cp_head[s], A.cp_vocab, hr);
         {
             NormT<D> nw;
             norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
@@ -1652,10 +1667,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 xf.eff += 0.1f * (float) (frame + 1 - P.target_frames);
                 if (xf.eff > 6.0f) xf.eff = 6.0f;
             }
-            f16_head<D>(A.codec_head, A.codec_vocab, L, nullptr, 0, A.logits, &xf, nullptr, A.cand_val, A.cand_idx);
+            f16_head<D>(hr, A.codec_vocab, L, nullptr, 0, A.logits, &xf, nullptr, A.cand_val, A.cand_idx);
         } else {
             uint64_t * hs = A.arena + (size_t) p_head * kSlot;
-            f16_head<D>(A.cp_head[s], A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
+            f16_head<D>(hr, A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
             __syncthreads();
             code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
             if (t == 0) L.codes[s + 1] = code;
