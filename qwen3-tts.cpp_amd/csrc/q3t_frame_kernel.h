@@ -782,7 +782,10 @@ __device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
 //
 // Wave w owns row w of (q0, q1, k, v): lane l holds elements l and l + 64,
 // which are exactly the NEOX rotation pairs, so QK-norm and RoPE need only
-// wave reductions.  Wave hq (0, 1) then handles query head 2g + hq alone.
+// wave reductions; the new K/V rows go straight into the LDS cache.  Then
+// waves w and w + 2 both handle query head 2g + (w & 1): each computes the
+// (at most 16) scores and the softmax, and forms 64 of the head's 128 output
+// dims, so all four waves work and no workgroup barrier is needed.
 __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                             int nt, int pos0, int qd, const uint64_t * qkv,
                                                             uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
@@ -790,8 +793,6 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
     const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kd = qd / 2;
     float * qf = L.a;                      // [tok][head][128] rotated, fp16-rounded q
-    float * knew = L.a + 4 * 128;          // [tok][128]
-    float * vnew = knew + 2 * 128;         // [tok][128]
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
@@ -832,77 +833,57 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
                     qf[(tok * 2 + wave) * 128 + lane] = round_f16(o0);
                     qf[(tok * 2 + wave) * 128 + lane + 64] = round_f16(o1);
                 } else {
-                    const uint16_t h0 = f2h(o0), h1 = f2h(o1);
-                    knew[tok * 128 + lane] = h2f(h0);
-                    knew[tok * 128 + lane + 64] = h2f(h1);
-                    L.cpk[layer][pos * 128 + lane] = h0;
-                    L.cpk[layer][pos * 128 + lane + 64] = h1;
+                    L.cpk[layer][pos * 128 + lane] = f2h(o0);
+                    L.cpk[layer][pos * 128 + lane + 64] = f2h(o1);
                 }
             } else {
-                const uint16_t h0 = f2h(x0), h1 = f2h(x1);
-                vnew[tok * 128 + lane] = h2f(h0);
-                vnew[tok * 128 + lane + 64] = h2f(h1);
-                L.cpv[layer][pos * 128 + lane] = h0;
-                L.cpv[layer][pos * 128 + lane + 64] = h1;
+                L.cpv[layer][pos * 128 + lane] = f2h(x0);
+                L.cpv[layer][pos * 128 + lane + 64] = f2h(x1);
             }
         }
     }
     __syncthreads();
 
-    // At most 16 positions, all in LDS, so no workgroup barrier follows:
-    // scores with 4 lanes per position (32 dims each, quad DPP sum), softmax
-    // with wave reductions, P.V with 2 dims per lane and each probability
-    // broadcast by readlane.
-    if (wave < 2) {
-        const int hq = wave, jq = lane >> 2, sq = lane & 3;
-        for (int tok = 0; tok < nt; ++tok) {
-            const int n_kv = pos0 + tok + 1;
-            double acc = 0.0;
-            if (jq < n_kv) {
-                const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
+    // Scores with 4 lanes per position (32 dims each, quad DPP sum), softmax
+    // with wave reductions, P.V with one dim per lane over the positions
+    // (unrolled to the cache length; each probability broadcast by readlane).
+    const int hq = wave & 1, d = (wave >> 1) * 64 + lane;
+    const int jq = lane >> 2, sq = lane & 3;
+    const uint16_t * kc = L.cpk[layer];
+    const uint16_t * vc = L.cpv[layer];
+    for (int tok = 0; tok < nt; ++tok) {
+        const int n_kv = pos0 + tok + 1;
+        double acc = 0.0;
+        if (jq < n_kv) {
+            const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    float kv[8];
-                    if (jq >= pos0) {
+            for (int c = 0; c < 4; ++c) {
+                const int4 k4 = *(const int4 *) &kc[jq * 128 + sq * 32 + c * 8];
+                const float4 qa = *(const float4 *) &q[c * 8], qb = *(const float4 *) &q[c * 8 + 4];
+                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) kv[e] = knew[(jq - pos0) * 128 + sq * 32 + c * 8 + e];
-                    } else {
-                        const int4 k4 = *(const int4 *) &L.cpk[layer][jq * 128 + sq * 32 + c * 8];
-                        const uint16_t * kh = (const uint16_t *) &k4;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = fma((double) q[c * 8 + e], (double) kv[e], acc);
-                }
+                for (int e = 0; e < 8; ++e) acc = fma((double) qv[e], (double) h8(k4, e), acc);
             }
-            acc += dpp_d<0xB1>(acc);
-            acc += dpp_d<0x4E>(acc);
-            const float sv = jq < n_kv ? (float) acc * A.attn_scale : -INFINITY;
-            const float mx = wave_max_f(sv);
-            const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
-            const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
-            const float inv = (float) (1.0 / sum);
-            const float pr = round_f16(ev * inv);
-            double o0 = 0.0, o1 = 0.0;
-            for (int j = 0; j < n_kv; ++j) {
-                const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
-                float v0, v1;
-                if (j >= pos0) {
-                    v0 = vnew[(j - pos0) * 128 + 2 * lane];
-                    v1 = vnew[(j - pos0) * 128 + 2 * lane + 1];
-                } else {
-                    const uint32_t w2 = *(const uint32_t *) &L.cpv[layer][j * 128 + 2 * lane];
-                    v0 = h2f((uint16_t) (w2 & 0xffffu));
-                    v1 = h2f((uint16_t) (w2 >> 16));
-                }
-                o0 = fma(pj, (double) v0, o0);
-                o1 = fma(pj, (double) v1, o1);
-            }
-            uint64_t * dst = out + (size_t) tok * kHS + (g * 2 + hq) * 128 + 2 * lane;
-            tstore(dst, out_tag, (float) o0);
-            tstore(dst + 1, out_tag, (float) o1);
         }
+        acc += dpp_d<0xB1>(acc);
+        acc += dpp_d<0x4E>(acc);
+        const float sv = jq < n_kv ? (float) acc * A.attn_scale : -INFINITY;
+        const float mx = wave_max_f(sv);
+        const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
+        const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
+        const float inv = (float) (1.0 / sum);
+        const float pr = round_f16(ev * inv);
+        float vv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vv[j] = h2f(vc[j * 128 + d]);
+        double o = 0.0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (j >= n_kv) break;
+            const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
+            o = fma(pj, (double) vv[j], o);
+        }
+        tstore(out + (size_t) tok * kHS + (g * 2 + hq) * 128 + d, out_tag, (float) o);
     }
     __syncthreads();
 }
@@ -1394,7 +1375,7 @@ __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
 }
 
 // code-predictor token of codebook `group` from tagged head logits
-__device__ int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, uint32_t tag, int frame, int group,
+__device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, uint32_t tag, int frame, int group,
                              bool & dead) {
     const SampleParams & P = *A.params;
     if (P.temperature <= 0.0f) {
