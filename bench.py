@@ -109,9 +109,10 @@ def step_bench(args, cfg, w):
     """One talker decode step (forward_step: 28 layers + output norm + codec
     head, batch 1) with the KV cache pre-filled at 512 positions with seeded
     N(0, 1) fp16 K/V rows, the new token at position 512.  Each call is one
-    q3t_dev_talker_step (the multi-kernel step, logits and hidden copied back
-    to the host); reports the mean wall time per step and the per-kernel HIP
-    event timings of talker layer 0 at that context."""
+    q3t_dev_talker_step (the persistent kernel's talker pass, logits and
+    hidden copied back to the host); reports the mean wall time per step and
+    the HIP event timings of the multi-kernel step's kernels for talker layer
+    0 at that context."""
     from qwen3_tts_amd.device import Device
     rng = np.random.default_rng(31)
     n_kv = 512
@@ -146,7 +147,7 @@ def step_bench(args, cfg, w):
         "higher_is_better": False, "dtype": "int8" if args.weights == "q8_0" else "f16",
         "data": "synthetic (seeded weights, N(0,1) fp16 KV)",
         "config": {"workload": f"one talker decode step, {args.weights.upper()} 0.6B shapes, KV pre-filled to "
-                               f"{n_kv} positions, multi-kernel step with host copy-back", "global_batch": 1},
+                               f"{n_kv} positions, persistent-kernel step with host copy-back", "global_batch": 1},
         "step_algorithmic_bytes": int(wbytes + kvbytes),
         "step_hbm_gbs": round((wbytes + kvbytes) / dt / 1e9, 1),
         "kernels": kernels}))

@@ -119,6 +119,9 @@ struct q3t_dev {
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
     int32_t * fk_err = nullptr;
     fk::Args * fk_args_dev = nullptr;
+    bool fk_args_ok = false;           // fk_args_dev holds this context's current arguments
+    bool fk_layers_stale = false;      // a layer tensor was uploaded after fk_layers was built
+    int32_t fk_epoch = 0;              // launches since the arena was cleared (the phase tags)
     float * fk_cand = nullptr;         // talker-head greedy candidates: 256 values then 256 indices
     hipEvent_t run_ev[2] = {nullptr, nullptr};
     uint8_t * copy_buf = nullptr;      // copy-kernel calibration buffers (time_kernel class 5)
@@ -173,6 +176,7 @@ void drop_graph(q3t_dev * c) {
     if (c->frame_exec) { (void) hipGraphExecDestroy(c->frame_exec); c->frame_exec = nullptr; }
     if (c->frame_graph) { (void) hipGraphDestroy(c->frame_graph); c->frame_graph = nullptr; }
     c->frames_ready = false;
+    c->fk_args_ok = false;
 }
 
 // Expected (ne0, ne1) of a named tensor; false if the name is not used by
@@ -621,7 +625,7 @@ int fk_prepare(q3t_dev * c) {
         return 0;
     const int phases = 15 * (2 + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
     if (phases >= 4096) return 0;
-    if (!c->fk_layers) {
+    if (!c->fk_layers || c->fk_layers_stale) {
         std::vector<fk::LayerQ8> t(g.n_layers + g.cp_layers);
         for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
             const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
@@ -629,8 +633,9 @@ int fk_prepare(q3t_dev * c) {
                                (const int8_t *) L.wg.data, L.wg.scales, (const int8_t *) L.wu.data, L.wu.scales,
                                (const int8_t *) L.wd.data, L.wd.scales, L.attn_norm, L.ffn_norm, L.q_norm, L.k_norm};
         }
-        if (dev_alloc_t(c, &c->fk_layers, t.size())) return -1;
+        if (!c->fk_layers && dev_alloc_t(c, &c->fk_layers, t.size())) return -1;
         HIP_OK(hipMemcpy(c->fk_layers, t.data(), t.size() * sizeof(fk::LayerQ8), hipMemcpyHostToDevice));
+        c->fk_layers_stale = false;
     }
     const size_t bytes = (size_t) phases * fk::kSlot * sizeof(uint64_t);
     if (bytes > c->fk_arena_bytes) {
@@ -672,13 +677,95 @@ fk::Args fk_args(q3t_dev * c) {
     A.err = c->fk_err;
     A.cand_val = c->fk_cand;
     A.cand_idx = (int32_t *) (c->fk_cand + 256);
+    A.step_in = c->stage;
     return A;
 }
 
-hipError_t fk_launch(q3t_dev * c, int32_t frame) {
-    void * args[] = {&c->fk_args_dev, &frame};
-    return hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream);
+// Uploads the kernel arguments (the device copy is read by every launch).
+int fk_upload_args(q3t_dev * c) {
+    static thread_local fk::Args host_args;
+    host_args = fk_args(c);
+    HIP_OK(hipMemcpyAsync(c->fk_args_dev, &host_args, sizeof host_args, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipStreamSynchronize(c->stream));
+    c->fk_args_ok = true;
+    return 0;
 }
+
+// One launch of the persistent kernel.  Every launch since the arena was last
+// cleared gets its own epoch, so no phase tag repeats; before the 20-bit epoch
+// would wrap, the arena is cleared again (stream-ordered before the launch).
+hipError_t fk_launch(q3t_dev * c, int32_t frame, int32_t mode) {
+    constexpr int32_t kMaxEpoch = (1 << 20) - 2;
+    if (c->fk_epoch >= kMaxEpoch) {
+        const hipError_t e = hipMemsetAsync(c->fk_arena, 0, c->fk_arena_bytes, c->stream);
+        if (e != hipSuccess) return e;
+        c->fk_epoch = 0;
+    }
+    int32_t epoch = c->fk_epoch;
+    void * args[] = {&c->fk_args_dev, &frame, &epoch, &mode};
+    const hipError_t e =
+        hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream);
+    if (e == hipSuccess) ++c->fk_epoch;
+    return e;
+}
+
+// Whether a single-step call (talker step or code predictor) can run on the
+// persistent kernel: prepares it and uploads the arguments when needed.
+int fk_step_ready(q3t_dev * c, bool & ok) {
+    ok = false;
+    if (!c->fk_ok || !c->fk_args_ok) {
+        if (fk_prepare(c)) return -1;
+        if (!c->fk_ok) return 0;
+        if (!c->fk_args_ok) {
+            HIP_OK(hipMemsetAsync(c->fk_arena, 0, c->fk_arena_bytes, c->stream));
+            c->fk_epoch = 0;
+            if (fk_upload_args(c)) return -1;
+        }
+    }
+    ok = true;
+    return 0;
+}
+
+// The code predictor's head logits of a MODE_CODE_PRED launch, from the tagged
+// head slots (slot first + s * stride for step s) into out [n][vocab].
+__global__ void k_untag_heads(const uint64_t * __restrict__ arena, int first, int stride, int n, int vocab,
+                              float * __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * vocab) return;
+    const int s = i / vocab, r = i - s * vocab;
+    out[i] = __uint_as_float((uint32_t) arena[(size_t) (first + s * stride) * fk::kSlot + r]);
+}
+
+// A single-step launch (talker step or code predictor) on the persistent
+// kernel; false when it cannot run (the caller then takes the multi-kernel
+// path, which gives the same results).
+int fk_step(q3t_dev * c, int32_t frame, int32_t mode, bool & ran) {
+    ran = false;
+    bool ok = false;
+    if (fk_step_ready(c, ok)) return -1;
+    if (!ok) return 0;
+    HIP_OK(hipMemsetAsync(c->fk_err, 0, sizeof(int32_t), c->stream));
+    const hipError_t e = fk_launch(c, frame, mode);
+    if (e != hipSuccess) {
+        (void) hipGetLastError();
+        std::fprintf(stderr, "q3t: cooperative frame-kernel launch refused (%s); using the multi-kernel path\n",
+                     hipGetErrorString(e));
+        c->fk_ok = false;
+        c->fk_refused = true;
+        return 0;
+    }
+    ran = true;
+    return 0;
+}
+
+// The frame kernel's error flag after a launch has completed.
+int fk_check_err(q3t_dev * c) {
+    int32_t err = 0;
+    HIP_OK(hipMemcpy(&err, c->fk_err, sizeof err, hipMemcpyDeviceToHost));
+    if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+    return 0;
+}
+
 
 // The captured multi-kernel frame, built on first use.
 int ensure_frame_graph(q3t_dev * c) {
@@ -786,6 +873,7 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
     HIP_OK(hipSetDevice(c->device));
     drop_graph(c);
     c->resolved = false;
+    c->fk_layers_stale = true;
     const q3t_config & g = c->cfg;
     if (layer >= 0) {
         LayerDev & L = is_cp ? c->cp[layer] : c->talker[layer];
@@ -1175,10 +1263,13 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     s.talker_pos = n_past;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
-    talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
+    bool ran = false;
+    if (fk_step(c, 0, fk::MODE_TALKER_STEP, ran)) return -1;
+    if (!ran) talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
     if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden, (size_t) g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
-    return sync(c);
+    if (sync(c)) return -1;
+    return ran ? fk_check_err(c) : 0;
 }
 
 int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_sampling * sampling, uint32_t frame,
@@ -1200,15 +1291,27 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     s.frame = (int32_t) frame;
     if (set_state(c, s)) return -1;
     HIP_OK(hipMemcpyAsync(c->hidden, hidden, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
-    hipLaunchKernelGGL(k_cp_input, dim3((g.hidden_size + 255) / 256), dim3(256), 0, c->stream, c->st, c->hidden,
-                       (const uint16_t *) c->codec_embd.data, g.hidden_size, c->stage);
-    code_pred_seq(c, false);
+    // the persistent kernel needs the talker KV reservation for its tables
+    bool ran = false;
+    if (c->kc && fk_step(c, (int32_t) frame, fk::MODE_CODE_PRED, ran)) return -1;
+    if (ran) {
+        if (logits_out) {
+            const int stride = 2 + 5 * g.cp_layers, n = g.n_codebooks - 1;
+            hipLaunchKernelGGL(k_untag_heads, dim3((n * g.cp_vocab + 255) / 256), dim3(256), 0, c->stream,
+                               c->fk_arena, stride - 1, stride, n, g.cp_vocab, c->cp_logits);
+        }
+    } else {
+        hipLaunchKernelGGL(k_cp_input, dim3((g.hidden_size + 255) / 256), dim3(256), 0, c->stream, c->st, c->hidden,
+                           (const uint16_t *) c->codec_embd.data, g.hidden_size, c->stage);
+        code_pred_seq(c, false);
+    }
     FrameState r{};
     HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
     if (logits_out)
         HIP_OK(hipMemcpyAsync(logits_out, c->cp_logits, (size_t) (g.n_codebooks - 1) * g.cp_vocab * 4,
                               hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
+    if (ran && fk_check_err(c)) return -1;
     for (int i = 0; i < g.n_codebooks - 1; ++i) codes_out[i] = r.codes[i + 1];
     return 0;
 }
@@ -1337,9 +1440,8 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     if (c->fk_ok) {
         HIP_OK(hipMemsetAsync(c->fk_arena, 0, c->fk_arena_bytes, c->stream));
         HIP_OK(hipMemsetAsync(c->fk_err, 0, sizeof(int32_t), c->stream));
-        static thread_local fk::Args host_args;
-        host_args = fk_args(c);
-        HIP_OK(hipMemcpyAsync(c->fk_args_dev, &host_args, sizeof host_args, hipMemcpyHostToDevice, c->stream));
+        c->fk_epoch = 0;
+        if (fk_upload_args(c)) return -1;
     }
     if (sync(c)) return -1;
     if (!c->fk_ok && ensure_frame_graph(c)) return -1;
@@ -1368,7 +1470,7 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[0], c->stream));
     for (int i = 0; i < n_frames; ++i) {
         if (c->fk_ok) {
-            const hipError_t e = fk_launch(c, c->frames_launched + i);
+            const hipError_t e = fk_launch(c, c->frames_launched + i, fk::MODE_FRAME);
             if (e == hipSuccess) continue;
             // The cooperative launch can be refused while another process holds
             // the device's cooperative-launch resources.  Nothing was enqueued:

@@ -72,6 +72,15 @@ struct Args {
     const float * trailing; int32_t n_trailing; const float * pad;
     int32_t * err;
     float * cand_val; int32_t * cand_idx;    // talker-head greedy candidates, one per workgroup
+    const float * step_in;                   // MODE_TALKER_STEP: the step embedding [D]
+};
+
+// What one launch runs: a whole frame, or one of its two halves alone (the
+// reference's separate forward_step and predict_codes_autoregressive calls).
+enum : int32_t {
+    MODE_FRAME = 0,          // codebook-0 sample, code predictor, talker step; frame state advanced
+    MODE_TALKER_STEP = 1,    // talker step on step_in at st->talker_pos -> logits, hidden
+    MODE_CODE_PRED = 2,      // code predictor on hidden and st->codes[0] -> st->codes[1..15]
 };
 
 // Geometry of a Q8_0 GEMV with input width K: each row is split over LPR
@@ -117,12 +126,46 @@ struct Lds {
     SampleScratch<kT> S;
 };
 
+// ------------------------------------------------------ global accessors
+// Every pointer comes from the argument block, so the compiler cannot prove
+// its address space and would emit flat accesses, which also count against
+// the LDS wait counter: an LDS wait would then stall on weight prefetches in
+// flight.  These accessors address the global space explicitly.
+#define Q3T_GAS __attribute__((address_space(1)))
+typedef int gvi4 __attribute__((ext_vector_type(4)));
+typedef float gvf4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 gld4(const void * p) {
+    const gvi4 v = *(const Q3T_GAS gvi4 *) p;
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gldf4(const float * p) {
+    const gvf4 v = *(const Q3T_GAS gvf4 *) p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <class T>
+__device__ __forceinline__ T gld(const T * p) { return *(const Q3T_GAS T *) p; }
+template <class T>
+__device__ __forceinline__ void gst(T * p, T v) { *(Q3T_GAS T *) p = v; }
+
+// A layer descriptor read through the constant address space, one field at a
+// time (an aggregate copy would lose the address space): the kernel never
+// writes the descriptors, so the pointers arrive by scalar loads and the
+// accesses through them are global ones.
+template <class T>
+__device__ __forceinline__ T cld(const T * p) { return *(const __attribute__((address_space(4))) T *) p; }
+__device__ __forceinline__ LayerQ8 layer_desc(const LayerQ8 * p) {
+    return LayerQ8{cld(&p->qkv), cld(&p->qkv_d), cld(&p->wo), cld(&p->wo_d), cld(&p->wg), cld(&p->wg_d),
+                   cld(&p->wu), cld(&p->wu_d), cld(&p->wd), cld(&p->wd_d), cld(&p->attn_norm), cld(&p->ffn_norm),
+                   cld(&p->q_norm), cld(&p->k_norm)};
+}
+
 // ---------------------------------------------------------------- tagged I/O
 __device__ __forceinline__ uint64_t tload(const uint64_t * p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((const Q3T_GAS uint64_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void tstore(uint64_t * p, uint32_t tag, float v) {
-    __hip_atomic_store(p, ((uint64_t) tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((Q3T_GAS uint64_t *) p, ((uint64_t) tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float twait(const uint64_t * p, uint32_t tag, bool & dead, int32_t * err) {
     uint64_t v = tload(p);
@@ -245,7 +288,7 @@ __device__ __forceinline__ void norm_prefetch(const float * w, NormT<K> & nw) {
     for (int c = 0; c < Geo<K>::CHG; ++c) {
         const int g = (int) threadIdx.x + kT * c;
         if (g >= Geo<K>::G4) break;
-        const float4 q = *(const float4 *) (w + 4 * g);
+        const float4 q = gldf4(w + 4 * g);
         nw[c][0] = q.x; nw[c][1] = q.y; nw[c][2] = q.z; nw[c][3] = q.w;
     }
 }
@@ -325,7 +368,7 @@ template <int K, bool DUAL>
 struct Q8Regs {
     static constexpr int S = Geo<K>::SLOTS;
     int4 w[2][S][2], u[2][S][2];
-    float dw[2][S], du[2][S];
+    uint16_t dw[2][S], du[2][S];   // fp16 block scales, converted at use so the prefetch never waits
     uint64_t res[2][2];   // residual elements (tagged) read early by the storing lanes
     int ng;               // groups this wave owns (0..2)
 };
@@ -356,12 +399,12 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * 
         for (int s = 0; s < G::SLOTS; ++s) {
             const int b = lir + s * G::LPR;
             const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
-            R.w[gi][s][0] = wp[0]; R.w[gi][s][1] = wp[1];
-            R.dw[gi][s] = h2f(Wd[(size_t) r * G::BPR + b]);
+            R.w[gi][s][0] = gld4(wp); R.w[gi][s][1] = gld4(wp + 1);
+            R.dw[gi][s] = gld(Wd + (size_t) r * G::BPR + b);
             if (DUAL) {
                 const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
-                R.u[gi][s][0] = up[0]; R.u[gi][s][1] = up[1];
-                R.du[gi][s] = h2f(Ud[(size_t) r * G::BPR + b]);
+                R.u[gi][s][0] = gld4(up); R.u[gi][s][1] = gld4(up + 1);
+                R.du[gi][s] = gld(Ud + (size_t) r * G::BPR + b);
             }
         }
     }
@@ -410,6 +453,18 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
     for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
         for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
+    // the scales enter here: the empty asm keeps their conversion (and the
+    // wait for their loads) from being hoisted into the prefetch
+    float sw[2][G::SLOTS], su[2][G::SLOTS];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int s = 0; s < G::SLOTS; ++s) {
+            uint32_t a = R.dw[gi][s], c = DUAL ? R.du[gi][s] : 0u;
+            asm volatile("" : "+v"(a), "+v"(c));
+            sw[gi][s] = h2f((uint16_t) a);
+            su[gi][s] = h2f((uint16_t) c);
+        }
 #pragma unroll
     for (int s = 0; s < G::SLOTS; ++s) {
         const int b = lir + s * G::LPR;
@@ -423,10 +478,10 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
                 if (gi >= R.ng) break;
                 // d_w * d_x (two fp16 values) is exact in fp32 and its product with
                 // the int32 block sum exact in fp64: fma rounds like mul + add
-                acc[gi][t] = fma((double) (R.dw[gi][s] * dx), (double) dot32_i8(R.w[gi][s][0], R.w[gi][s][1], x0, x1),
+                acc[gi][t] = fma((double) (sw[gi][s] * dx), (double) dot32_i8(R.w[gi][s][0], R.w[gi][s][1], x0, x1),
                                  acc[gi][t]);
                 if (DUAL)
-                    acc2[gi][t] = fma((double) (R.du[gi][s] * dx),
+                    acc2[gi][t] = fma((double) (su[gi][s] * dx),
                                       (double) dot32_i8(R.u[gi][s][0], R.u[gi][s][1], x0, x1), acc2[gi][t]);
             }
         }
@@ -488,11 +543,11 @@ __device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_
             const int b = lir + s * G::LPR;
             const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) R.w[gi][s][c] = wp[c];
+            for (int c = 0; c < 4; ++c) R.w[gi][s][c] = gld4(wp + c);
             if (DUAL) {
                 const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) R.u[DUAL ? gi : 0][DUAL ? s : 0][c] = up[c];
+                for (int c = 0; c < 4; ++c) R.u[DUAL ? gi : 0][DUAL ? s : 0][c] = gld4(up + c);
             }
         }
     }
@@ -654,7 +709,7 @@ __device__ __forceinline__ void head_input(RowsT<1, K> & v, const NormT<K> & nw,
         if (g >= Geo<K>::G4) break;
         const int b = g >> 3, e32 = (g & 7) * 4;
         if (hidden_out && blockIdx.x == 0)
-            *(float4 *) (hidden_out + 4 * g) = make_float4(v[0][c][0], v[0][c][1], v[0][c][2], v[0][c][3]);
+            for (int e = 0; e < 4; ++e) gst(hidden_out + 4 * g + e, v[0][c][e]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) L.hq[(e32 + e) >> 3][b * 8 + ((e32 + e) & 7)] = f2h(v[0][c][e]);
     }
@@ -674,7 +729,8 @@ struct Cb0Xf {
 // or plain (talker logits).  Every workgroup also publishes its greedy
 // candidate: the first maximum over its rows (after the codebook-0
 // transforms when xf != nullptr), tagged at cand_tagged[2b], [2b+1] or plain
-// in cand_val[b] / cand_idx[b].  All threads of the workgroup must call it.
+// in cand_val[b] / cand_idx[b] (neither when both are null).  All threads of
+// the workgroup must call it.
 struct HeadRegs {
     int4 w[2][4];
     int ng;
@@ -695,7 +751,7 @@ __device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, 
         H.ng = gi + 1;
         const int4 * wp = (const int4 *) (W + (size_t) (g * RPW + rsub) * K + lir * kQK);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) H.w[gi][c] = wp[c];
+        for (int c = 0; c < 4; ++c) H.w[gi][c] = gld4(wp + c);
     }
 }
 
@@ -732,11 +788,11 @@ __device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, 
             if (lir != 0) continue;
             const int r = (gw + gi * nw) * RPW + rsub;
             if (out_tagged) tstore(out_tagged + r, tag, (float) a);
-            else out_plain[r] = (float) a;
+            else gst(out_plain + r, (float) a);
             float v = (float) a;
             if (xf) {
                 if (r >= xf->V - 1024 && r != xf->eos) v = -INFINITY;
-                if (xf->rep != 1.0f && (xf->seen[r] || r == xf->tok0)) v = v > 0.0f ? v / xf->rep : v * xf->rep;
+                if (xf->rep != 1.0f && (gld(xf->seen + r) || r == xf->tok0)) v = v > 0.0f ? v / xf->rep : v * xf->rep;
                 if (r == xf->eos && xf->eff != 0.0f) v = v + xf->eff;
             }
             if (v > bv || (v == bv && r < bi)) { bv = v; bi = r; }
@@ -745,7 +801,7 @@ __device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, 
     wave_argmax(bv, bi);
     if (lane == 0) { L.fred[wave] = bv; L.ired[wave] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && (cand_tagged || cand_val)) {
         float v = L.fred[0];
         int i = L.ired[0];
 #pragma unroll
@@ -754,8 +810,8 @@ __device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, 
             tstore(cand_tagged + 2 * blockIdx.x, tag, v);
             tstore(cand_tagged + 2 * blockIdx.x + 1, tag, __int_as_float(i));
         } else {
-            cand_val[blockIdx.x] = v;
-            cand_idx[blockIdx.x] = i;
+            gst(cand_val + blockIdx.x, v);
+            gst(cand_idx + blockIdx.x, (int32_t) i);
         }
     }
 }
@@ -806,13 +862,13 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
         for (int k = 4; k < kB; ++k) ptr[k] = ptr[0];
         // norm weights and RoPE rows do not depend on the new rows: load them first
         const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
-        const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
+        const float nw0 = gld(nwp + lane), nw1 = gld(nwp + lane + 64);
         float rcv[2], rsv[2];
 #pragma unroll
         for (int tok = 0; tok < 2; ++tok) {
             const int pos = pos0 + (tok < nt ? tok : 0);
-            rcv[tok] = A.cp_rope_cos[(size_t) pos * 64 + lane];
-            rsv[tok] = A.cp_rope_sin[(size_t) pos * 64 + lane];
+            rcv[tok] = gld(A.cp_rope_cos + (size_t) pos * 64 + lane);
+            rsv[tok] = gld(A.cp_rope_sin + (size_t) pos * 64 + lane);
         }
         float val[kB];
         twait_batch<kB>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
@@ -940,8 +996,8 @@ __device__ __forceinline__ void att_prefetch(const Args & A, int layer, const At
     for (int i = 0; i < kPre; ++i) {
         const int j = att_pos(s, i);
         if (j < s.j1 && j < pos0) {
-            P.k[i] = *(const int4 *) (A.kc + base + (size_t) j * 128 + sub * 8);
-            P.v[i] = *(const int4 *) (A.vc + base + (size_t) j * 128 + sub * 8);
+            P.k[i] = gld4(A.kc + base + (size_t) j * 128 + sub * 8);
+            P.v[i] = gld4(A.vc + base + (size_t) j * 128 + sub * 8);
         }
     }
 }
@@ -962,8 +1018,8 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
-        const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
-        const float rcv = A.rope_cos[(size_t) pos0 * 64 + lane], rsv = A.rope_sin[(size_t) pos0 * 64 + lane];
+        const float nw0 = gld(nwp + lane), nw1 = gld(nwp + lane + 64);
+        const float rcv = gld(A.rope_cos + (size_t) pos0 * 64 + lane), rsv = gld(A.rope_sin + (size_t) pos0 * 64 + lane);
         const uint64_t * ptr[2] = {qkv + col + lane, qkv + col + lane + 64};
         float val[2];
         twait_batch<2>(ptr, 2, qkv_tag, val, dead, A.err);
@@ -986,8 +1042,8 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
                 knew[lane] = h2f(h0);
                 knew[lane + 64] = h2f(h1);
                 if (writer) {
-                    A.kc[base + (size_t) pos0 * 128 + lane] = h0;
-                    A.kc[base + (size_t) pos0 * 128 + lane + 64] = h1;
+                    gst(A.kc + base + (size_t) pos0 * 128 + lane, h0);
+                    gst(A.kc + base + (size_t) pos0 * 128 + lane + 64, h1);
                 }
             }
         } else {
@@ -995,8 +1051,8 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
             vnew[lane] = h2f(h0);
             vnew[lane + 64] = h2f(h1);
             if (writer) {
-                A.vc[base + (size_t) pos0 * 128 + lane] = h0;
-                A.vc[base + (size_t) pos0 * 128 + lane + 64] = h1;
+                gst(A.vc + base + (size_t) pos0 * 128 + lane, h0);
+                gst(A.vc + base + (size_t) pos0 * 128 + lane + 64, h1);
             }
         }
     }
@@ -1017,7 +1073,7 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
 #pragma unroll
             for (int u = 0; u < kPre; ++u) if (u == i) kk = P.k[u];
         } else if (j < s.j1 && j < pos0) {
-            kk = *(const int4 *) (A.kc + base + (size_t) j * 128 + sub * 8);
+            kk = gld4(A.kc + base + (size_t) j * 128 + sub * 8);
         }
         float kv[8];
         if (j == pos0) {
@@ -1136,7 +1192,7 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
 #pragma unroll
             for (int u = 0; u < kPre; ++u) if (u == i) vv4 = P.v[u];
         } else if (j < s.j1 && j < pos0) {
-            vv4 = *(const int4 *) (A.vc + base + (size_t) j * 128 + sub * 8);
+            vv4 = gld4(A.vc + base + (size_t) j * 128 + sub * 8);
         }
         if (j < s.j1) {
             const double p0 = (double) L.sc[j - s.j0], p1 = (double) L.sc[kMaxChunk + j - s.j0];
@@ -1214,7 +1270,7 @@ __device__ __forceinline__ void att2_prefetch(const Args & A, int layer, int pos
         const int j = (int) threadIdx.x + u * kT;
 #pragma unroll
         for (int d = 0; d < 4; ++d)
-            if (d < dpw && j < pos0) P.v[u][d] = A.vc[base + (size_t) j * 128 + c * dpw + d];
+            if (d < dpw && j < pos0) P.v[u][d] = gld(A.vc + base + (size_t) j * 128 + c * dpw + d);
     }
 }
 
@@ -1357,12 +1413,12 @@ __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
         // candidate per workgroup
         const int t = threadIdx.x;
         const bool in = t < (int) gridDim.x;
-        return reduce_candidates(in ? A.cand_val[t] : -INFINITY, in ? A.cand_idx[t] : 0x7fffffff, L);
+        return reduce_candidates(in ? gld(A.cand_val + t) : -INFINITY, in ? gld(A.cand_idx + t) : 0x7fffffff, L);
     }
     for (int i = threadIdx.x; i < V; i += kT) {
-        float v = A.logits[i];
+        float v = gld(A.logits + i);
         if (i >= V - 1024 && i != A.eos_id) v = -INFINITY;
-        if (P.rep_penalty != 1.0f && A.seen[i]) v = v > 0.0f ? v / P.rep_penalty : v * P.rep_penalty;
+        if (P.rep_penalty != 1.0f && gld(A.seen + i)) v = v > 0.0f ? v / P.rep_penalty : v * P.rep_penalty;
         L.x[i] = v;
     }
     float eff = P.eos_bias;
@@ -1567,15 +1623,18 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
 // kernel argument (cp_embd[s], cp_head[s]) would copy it to private scratch.
 // One workgroup per CU, so one wave per SIMD: the full unified register file
 // (256 VGPRs + 256 AGPRs) is available to every wave.
+// `frame` indexes the sampler streams and the frame state; `epoch` (distinct
+// for every launch since the arena was last cleared) makes the phase tags.
 template <int D, int QD, int FF, int WT>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(const Args * __restrict__ Ap,
-                                                                                         int32_t frame) {
+                                                                                         int32_t frame, int32_t epoch,
+                                                                                         int32_t mode) {
     const Args & A = *Ap;
     __shared__ Lds L;
     bool dead = false;
     FrameState * st = A.st;
     if (st->done) return;
-    const uint32_t tb = (uint32_t) (frame + 1) << 12;
+    const uint32_t tb = (uint32_t) (epoch + 1) << 12;
     const int t = threadIdx.x;
     int p = 0;
 
@@ -1583,10 +1642,15 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // writes the frame state only at the end of the kernel: by then every
     // workgroup has finished this sampler (it consumed their later outputs),
     // so none can still be reading `seen`.
-    const int32_t tok0 = sample_cb0(A, L, frame);
-    if (tok0 == A.eos_id) {
-        if (blockIdx.x == 0 && t == 0) { st->frame = frame; st->codes[0] = tok0; st->done = 1; st->eos = 1; }
-        return;
+    int32_t tok0 = 0;
+    if (mode == MODE_FRAME) {
+        tok0 = sample_cb0(A, L, frame);
+        if (tok0 == A.eos_id) {
+            if (blockIdx.x == 0 && t == 0) { st->frame = frame; st->codes[0] = tok0; st->done = 1; st->eos = 1; }
+            return;
+        }
+    } else if (mode == MODE_CODE_PRED) {
+        tok0 = st->codes[0];
     }
     if (t == 0) L.codes[0] = tok0;
 
@@ -1595,24 +1659,27 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // talker step on the summed step embedding.  One call site per layer
     // shape keeps the inlined program small.
     int code = tok0;
-    const int pos = st->base_pos + frame;
-    for (int s = 0; s <= 15; ++s) {
+    const int pos = mode == MODE_TALKER_STEP ? st->talker_pos : st->base_pos + frame;
+    const int s_first = mode == MODE_TALKER_STEP ? 15 : 0, s_last = mode == MODE_CODE_PRED ? 14 : 15;
+    for (int s = s_first; s <= s_last; ++s) {
         const bool tk = s == 15;
         const int p_x = p++;
         if (s == 0) {
             for (int i = t; i < D; i += kT) {
-                L.x[i] = A.hidden[i];
-                L.x[D + i] = h2f(A.codec_embd[(size_t) tok0 * D + i]);
+                L.x[i] = gld(A.hidden + i);
+                L.x[D + i] = h2f(gld(A.codec_embd + (size_t) tok0 * D + i));
             }
         } else if (!tk) {
-            for (int i = t; i < D; i += kT) L.x[i] = h2f(A.cp_embd[s - 1][(size_t) code * D + i]);
+            for (int i = t; i < D; i += kT) L.x[i] = h2f(gld(A.cp_embd[s - 1] + (size_t) code * D + i));
+        } else if (mode == MODE_TALKER_STEP) {
+            for (int i = t; i < D; i += kT) L.x[i] = gld(A.step_in + i);
         } else {
             // emit the frame, then the step embedding (reference summation order)
             if (blockIdx.x == 0 && t < 16) A.codes_out[(size_t) frame * 16 + t] = L.codes[t];
             for (int i = t; i < D; i += kT) {
-                float e = h2f(A.codec_embd[(size_t) L.codes[0] * D + i]);
-                for (int g = 1; g < 16; ++g) e = e + h2f(A.cp_embd[g - 1][(size_t) L.codes[g] * D + i]);
-                const float tr = frame < A.n_trailing ? A.trailing[(size_t) frame * D + i] : A.pad[i];
+                float e = h2f(gld(A.codec_embd + (size_t) L.codes[0] * D + i));
+                for (int g = 1; g < 16; ++g) e = e + h2f(gld(A.cp_embd[g - 1] + (size_t) L.codes[g] * D + i));
+                const float tr = frame < A.n_trailing ? gld(A.trailing + (size_t) frame * D + i) : gld(A.pad + i);
                 L.x[i] = e + tr;
             }
         }
@@ -1625,8 +1692,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const LayerQ8 * Ls = tk ? A.talker : A.cp;
         for (int l = 0; l < nl; ++l) {
             const float * x_lds = l == 0 ? L.x : nullptr;
-            if (nt == 2) layer_t<2, D, QD, FF, WT>(A, L, Ls[l], l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else layer_t<1, D, QD, FF, WT>(A, L, Ls[l], l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
+            const LayerQ8 Wl = layer_desc(Ls + l);
+            if (nt == 2) layer_t<2, D, QD, FF, WT>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else layer_t<1, D, QD, FF, WT>(A, L, Wl, l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
             p_in = p_out;
         }
         // head on the last token's normed row
@@ -1648,7 +1716,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 xf.eff += 0.1f * (float) (frame + 1 - P.target_frames);
                 if (xf.eff > 6.0f) xf.eff = 6.0f;
             }
-            f16_head<D>(hr, A.codec_vocab, L, nullptr, 0, A.logits, &xf, nullptr, A.cand_val, A.cand_idx);
+            if (mode == MODE_FRAME)
+                f16_head<D>(hr, A.codec_vocab, L, nullptr, 0, A.logits, &xf, nullptr, A.cand_val, A.cand_idx);
+            else
+                f16_head<D>(hr, A.codec_vocab, L, nullptr, 0, A.logits, nullptr, nullptr, nullptr, nullptr);
         } else {
             uint64_t * hs = A.arena + (size_t) p_head * kSlot;
             f16_head<D>(hr, A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
@@ -1658,7 +1729,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             __syncthreads();
         }
     }
-    if (blockIdx.x == 0 && t == 0) {
+    if (mode == MODE_CODE_PRED && blockIdx.x == 0 && t == 0)
+        for (int g = 1; g < 16; ++g) st->codes[g] = L.codes[g];
+    if (mode == MODE_FRAME && blockIdx.x == 0 && t == 0) {
         st->frame = frame;
         st->next_frame = frame + 1;
         st->talker_pos = pos;
