@@ -459,11 +459,13 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
 
     // scores: 16 lanes per position (8 dims each), 4 positions per wave, kAU in flight
     const int dsub = lane & 15, pq = lane >> 4;
-    float q[G][8];
+    // fp16 x fp16 products are exact in fp64: fma rounds like the fp32
+    // product added in fp64, with one conversion per cached element
+    double q[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q[h][e] = qf[h * kHD + dsub * 8 + e];
+        for (int e = 0; e < 8; ++e) q[h][e] = (double) qf[h * kHD + dsub * 8 + e];
     float lmax[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) lmax[h] = -INFINITY;
@@ -486,20 +488,20 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
 #pragma unroll
         for (int u = 0; u < kAU; ++u) {
             const int j = j0 + u * kStep + wave * 4 + pq;
-            float kf[8];
+            double kf[8];
             if (j < pos) {
                 const uint16_t * kh = (const uint16_t *) &kv[u];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) kf[e] = h2f(kh[e]);
+                for (int e = 0; e < 8; ++e) kf[e] = (double) h2f(kh[e]);
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) kf[e] = j == pos ? knew[dsub * 8 + e] : 0.0f;
+                for (int e = 0; e < 8; ++e) kf[e] = j == pos ? (double) knew[dsub * 8 + e] : 0.0;
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 double s = 0.0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) s += (double) (q[h][e] * kf[e]);
+                for (int e = 0; e < 8; ++e) s = fma(q[h][e], kf[e], s);
                 s = group_sum_d(s, 16);
                 if (j < n_kv) {
                     const float sv = (float) s * a.scale;
@@ -571,20 +573,20 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
         for (int u = 0; u < kAU; ++u) {
             const int j = j0 + u * kStep + wave * 4 + pq;
             if (j >= n_kv) continue;
-            float vf[8];
+            double vf[8];
             if (j < pos) {
                 const uint16_t * vh = (const uint16_t *) &vv[u];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = h2f(vh[e]);
+                for (int e = 0; e < 8; ++e) vf[e] = (double) h2f(vh[e]);
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = vnew[dsub * 8 + e];
+                for (int e = 0; e < 8; ++e) vf[e] = (double) vnew[dsub * 8 + e];
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const float p = sc[h * a.n_ctx + j];
+                const double p = (double) sc[h * a.n_ctx + j];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[h][e] += (double) (p * vf[e]);
+                for (int e = 0; e < 8; ++e) o[h][e] = fma(p, vf[e], o[h][e]);
             }
         }
 #pragma unroll
