@@ -85,6 +85,7 @@ struct q3t_dev {
     float * bxa = nullptr, * bxb = nullptr, * bqkv = nullptr, * batt = nullptr;   // [2 * nb][...]
     int8_t * bq8 = nullptr; float * bdx8 = nullptr;   // Q8_0 rows [2 * nb][max(qd, ffn)] and scales
     float * srs = nullptr;                            // RMSNorm row scales [2 * nb]
+    double * sss[2] = {nullptr, nullptr};             // per-tile sums of squares of Wo / down outputs [d/16][2 nb]
     // split-K partials and per-tile tickets, one set per GEMM call type
     // (QKV, Wo, gate/up, down): a set's tickets advance by S per launch
     uint64_t * spart[4] = {}; uint32_t * scnt[4] = {}; int32_t * serr = nullptr;
@@ -1646,19 +1647,26 @@ void attn_gqa(q3t_dev * c, const LayerDev & L, const StreamKV & kv) {
 }
 
 // One decoder layer over n = nb * nt rows (stream-major); output rows in c->bxa.
+// The residual-producing GEMMs (Wo, down) also leave per-tile sums of squares
+// of their output rows, from which the next normed GEMM forms its RMSNorm
+// scales; only a layer's first input (x_ss false: gathered rows) needs the
+// row-scale kernel.
 // Four decode-shaped GEMMs and one attention launch (the talker's GQA kernel
 // for one token per stream; for the code predictor's 16-position cache the
 // per-head kernel over nt tokens).  Activations pass between them as fp32
 // residual rows (RMSNorm + quantisation inside the consuming GEMM) or as
 // Q8_0 rows quantised by the producer (attention output, SwiGLU output).
-static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, int nt, const StreamKV & kv) {
+static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
-    const int ffn = g.ffn_size, n = c->nb * nt;
-    row_scales(c, x, d, d, n);
+    const int ffn = g.ffn_size, n = c->nb * nt, tiles = d / ms::kRows;
+    const bool fuse = tiles / 4 <= ms::kSsPer;   // row scales from the producer's per-tile sums
+    x_ss = x_ss && fuse;
+    if (!x_ss) row_scales(c, x, d, d, n);
     ms::GemmArgs q{};
     q.W = (const int8_t *) L.qkv.data; q.Wd = L.qkv.scales; q.N = qkvd; q.K = d;
     q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
+    if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
     gemm_rows(c, G_QKV, S_QKV, q);
     if (kv.pos_ptr && nt == 1) {
         attn_gqa(c, L, kv);
@@ -1680,16 +1688,19 @@ static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, int n
     ms::GemmArgs o{};
     o.W = (const int8_t *) L.wo.data; o.Wd = L.wo.scales; o.N = d; o.K = qd;
     o.q = c->bq8; o.qdx = c->bdx8; o.n = n; o.y = c->bxb; o.ys = d; o.res = x; o.rs = d;
+    if (fuse) o.ss_out = c->sss[0];
     gemm_rows(c, G_PROJ, S_WO, o);
-    row_scales(c, c->bxb, d, d, n);
+    if (!fuse) row_scales(c, c->bxb, d, d, n);
     ms::GemmArgs f{};
     f.W = (const int8_t *) L.wg.data; f.Wd = L.wg.scales; f.W2 = (const int8_t *) L.wu.data; f.W2d = L.wu.scales;
     f.N = ffn; f.K = d; f.x = c->bxb; f.xs = d; f.rscale = c->srs; f.norm_w = L.ffn_norm; f.n = n;
+    if (fuse) { f.ss_in = c->sss[0]; f.ss_tiles = tiles; f.eps = g.rms_eps; }
     f.yq = c->bq8; f.ydx = c->bdx8;
     gemm_rows(c, G_GATE_UP, S_GATE_UP, f);
     ms::GemmArgs dn{};
     dn.W = (const int8_t *) L.wd.data; dn.Wd = L.wd.scales; dn.N = d; dn.K = ffn;
     dn.q = c->bq8; dn.qdx = c->bdx8; dn.n = n; dn.y = c->bxa; dn.ys = d; dn.res = c->bxb; dn.rs = d;
+    if (fuse) dn.ss_out = c->sss[1];
     gemm_rows(c, G_PROJ, S_DOWN, dn);
 }
 
@@ -1730,7 +1741,7 @@ static void streams_frame_seq(q3t_dev * c) {
         for (int il = 0; il < g.cp_layers; ++il) {
             StreamKV kv{c->scpk + il * cp_lstride, c->scpv + il * cp_lstride, cp_lstride * g.cp_layers, 16,
                         c->cp_rope_cos, c->cp_rope_sin, nullptr, pos};
-            stream_layer(c, c->cp[il], x, nt, kv);
+            stream_layer(c, c->cp[il], x, il > 0, nt, kv);
             x = c->bxa;
         }
         GemvSpec h{};
@@ -1747,7 +1758,7 @@ static void streams_frame_seq(q3t_dev * c) {
     for (int il = 0; il < g.n_layers; ++il) {
         StreamKV kv{c->skc + il * lstride, c->svc + il * lstride, lstride * g.n_layers, c->sb_ctx, c->rope_cos,
                     c->rope_sin, &c->sst[0].talker_pos, 0};
-        stream_layer(c, c->talker[il], x, 1, kv);
+        stream_layer(c, c->talker[il], x, il > 0, 1, kv);
         x = c->bxa;
     }
     GemvSpec h{};
@@ -1804,7 +1815,7 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
                      (void *) c->sparams, (void *) c->sseen, (void *) c->sntrail, (void *) c->spad, (void *) c->shidden,
                      (void *) c->slogits, (void *) c->scplogits, (void *) c->sstage, (void *) c->bxa, (void *) c->bxb,
                      (void *) c->bqkv, (void *) c->batt, (void *) c->bq8, (void *) c->bdx8, (void *) c->srs,
-                     (void *) c->serr, (void *) c->scodes, (void *) c->strail})
+                     (void *) c->serr, (void *) c->scodes, (void *) c->strail, (void *) c->sss[0], (void *) c->sss[1]})
         if (p) dev_free(c, p);
     for (int i = 0; i < 4; ++i) {
         if (c->spart[i]) dev_free(c, c->spart[i]);
@@ -1823,7 +1834,8 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
         dev_alloc_t(c, &c->sstage, B * 2 * d) || dev_alloc_t(c, &c->bxa, rows * d) || dev_alloc_t(c, &c->bxb, rows * d) ||
         dev_alloc_t(c, &c->bqkv, rows * qkvd) || dev_alloc_t(c, &c->batt, rows * qd) ||
         dev_alloc_t(c, &c->bq8, rows * std::max(qd, g.ffn_size)) ||
-        dev_alloc_t(c, &c->bdx8, rows * (std::max(qd, g.ffn_size) / kQK)) || dev_alloc_t(c, &c->srs, rows))
+        dev_alloc_t(c, &c->bdx8, rows * (std::max(qd, g.ffn_size) / kQK)) || dev_alloc_t(c, &c->srs, rows) ||
+        dev_alloc_t(c, &c->sss[0], rows * (d / ms::kRows)) || dev_alloc_t(c, &c->sss[1], rows * (d / ms::kRows)))
         return -1;
     {
         // tickets and tags start at 0 (a tag is >= 1), zeroed here, outside any graph

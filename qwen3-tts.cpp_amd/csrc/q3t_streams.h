@@ -48,11 +48,14 @@ struct GemmArgs {
     int32_t N, K;
     const int8_t * q; const float * qdx;       // IN_Q8: activation rows [n][K] int8, scales [n][K/32]
     const float * x; int32_t xs;               // IN_NORM: activation rows [n][xs] fp32
-    const float * rscale;                      //          1/sqrt(mean(x^2) + eps) per row
+    const float * rscale;                      //          1/sqrt(mean(x^2) + eps) per row, or:
+    const double * ss_in; int32_t ss_tiles;    //          the producing GEMM's per-tile sums of squares [tiles][n]
+    float eps;
     const float * norm_w;                      //          RMSNorm gain [K]
     int32_t n;                                 // activation rows, <= 16 * NT
     float * y; int32_t ys;                     // OUT_F32 / OUT_RESID rows [n][ys]
     const float * res; int32_t rs;             // OUT_RESID residual rows [n][rs]
+    double * ss_out;                           // OUT_RESID: per-tile sums of squares of the rows [tiles][n] (or NULL)
     int8_t * yq; float * ydx;                  // OUT_SWIGLU_Q8 rows [n][N] int8, scales [n][N/32]
     uint64_t * part;                           // split-K partials [tiles][S][2 NV][64] tagged words
     uint32_t * cnt;                            // per-tile arrival counters (S per launch, never reset)
@@ -60,6 +63,7 @@ struct GemmArgs {
 };
 
 constexpr unsigned kSkSpin = 1u << 20;     // polls before a split-K wait gives up
+constexpr int kSsPer = 16;                 // per-tile sums of squares one lane adds (hidden <= 1024)
 
 // Dynamic LDS: weight scales of the slice [NW][MT*16][K/32/S] f32 and the
 // cross-wave partials [2][NW][MT][NT][4][64] f64.
@@ -165,7 +169,25 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
                 }
         } else {
             const float * xr = a.x + (size_t) (ok ? tok : 0) * a.xs + 8 * lk;
-            rsc[QIN ? 0 : j] = ok ? a.rscale[tok] : 0.0f;
+            if (a.ss_in) {
+                // RMSNorm row scale from the producer's per-tile sums: lane
+                // group lk adds a quarter of the tiles in order, then a fixed
+                // pairwise tree ((q0 + q1) + (q2 + q3))
+                const int per = a.ss_tiles / 4;   // <= kSsPer (the host checks)
+                double sv[kSsPer];
+#pragma unroll
+                for (int i = 0; i < kSsPer; ++i)
+                    sv[i] = ok && i < per ? a.ss_in[(size_t) (lk * per + i) * a.n + tok] : 0.0;
+                double part = 0.0;
+#pragma unroll
+                for (int i = 0; i < kSsPer; ++i) part += sv[i];
+                part += __shfl_xor(part, 16);
+                part += __shfl_xor(part, 32);
+                const float mean = (float) (part / (double) a.K);
+                rsc[QIN ? 0 : j] = ok ? 1.0f / sqrtf(mean + a.eps) : 0.0f;
+            } else {
+                rsc[QIN ? 0 : j] = ok ? a.rscale[tok] : 0.0f;
+            }
 #pragma unroll
             for (int i = 0; i < KB; ++i) {
                 float4 u0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u1 = u0;
@@ -350,7 +372,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
                 if (lk == 0) a.ydx[(size_t) tok * (a.N / kQK) + r0 / kQK] = round_f16(d);
             }
         } else {
-            if (tok >= a.n) continue;
+            const bool ok = tok < a.n;
+            double sq = 0.0;   // this lane's part of the tile's sum of squares of row tok
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 float o[4];
@@ -358,9 +381,15 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     const int r = r0 + 16 * m + 4 * lk + e;
                     const float v = (float) acc[(m * NT + j) * 4 + e];
-                    o[e] = OUT == OUT_RESID ? v + a.res[(size_t) tok * a.rs + r] : v;
+                    o[e] = OUT == OUT_RESID && ok ? v + a.res[(size_t) tok * a.rs + r] : v;
+                    sq += (double) (o[e] * o[e]);
                 }
-                *(float4 *) (a.y + (size_t) tok * a.ys + r0 + 16 * m + 4 * lk) = make_float4(o[0], o[1], o[2], o[3]);
+                if (ok) *(float4 *) (a.y + (size_t) tok * a.ys + r0 + 16 * m + 4 * lk) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+            if (OUT == OUT_RESID && a.ss_out) {
+                sq += __shfl_xor(sq, 16);
+                sq += __shfl_xor(sq, 32);
+                if (ok && lk == 0) a.ss_out[(size_t) tile * a.n + tok] = sq;
             }
         }
     }
