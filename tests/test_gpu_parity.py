@@ -332,3 +332,55 @@ def test_long_context_persistent_matches_graph(wtype, monkeypatch):
     finally:
         dev.close()
     assert np.array_equal(out["1"], out["0"])
+
+
+@pytest.fixture(params=["persistent", "graph"])
+def step_path(request, monkeypatch):
+    """Single talker steps and code-predictor calls on the persistent kernel's
+    step modes (the default) and on the multi-kernel sequences
+    (Q3T_FRAME_KERNEL=0).  The choice is made when a context first runs
+    one, so each test builds its own device."""
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
+    return request.param
+
+
+def _steps_and_code_pred(cfg, wtype, seed, n_prefill, step_path):
+    w, dev, o = make(cfg, wtype, seed=seed, n_ctx=n_prefill + 16)
+    try:
+        rng = np.random.default_rng(seed + 100)
+        d = cfg.hidden_size
+        embd = (rng.standard_normal((n_prefill, d)) * 0.05).astype(np.float32)
+        say(f"[gpu] steps + code_pred {wtype} ({step_path}): prefill {n_prefill}")
+        hid_g, log_g = dev.prefill(embd, 0)
+        hid_o, log_o = o.prefill(embd, 0)
+        assert np.array_equal(log_g, log_o)
+        for s in range(3):
+            e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+            lg, hg = dev.talker_step(e, n_prefill + s)
+            lo, ho = o.step(e, n_prefill + s)
+            assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
+            assert np.array_equal(hg, ho)
+            cb0 = int(np.argmax(lg[:cfg.codec_vocab - 1024]))
+            cg, lcg = dev.code_pred(hg, cb0, frame=s)
+            co, lco = o.code_pred(ho, cb0, frame=s)
+            assert np.array_equal(cg, co) and np.array_equal(lcg, lco)
+            cg, _ = dev.code_pred(hg, cb0, temperature=0.9, top_k=50, seed=11 + s, frame=s)
+            co, _ = o.code_pred(ho, cb0, temperature=0.9, top_k=50, seed=11 + s, frame=s)
+            assert np.array_equal(cg, co)
+    finally:
+        dev.close()
+
+
+def test_steps_and_code_pred_tiny(step_path):
+    """Talker steps then greedy and sampled code-predictor calls, each checked
+    against the oracle, at the small shapes for both weight types."""
+    cfg = qcfg.tiny()
+    for wtype in ("q8_0", "f16"):
+        _steps_and_code_pred(cfg, wtype, 31, 12, step_path)
+
+
+@pytest.mark.slow
+def test_steps_and_code_pred_full_q8(step_path):
+    """The same at the 0.6B shapes with Q8_0 layers, after a 300-row prefill
+    (the talker steps take the split attention of the persistent kernel)."""
+    _steps_and_code_pred(qcfg.full_06b(), "q8_0", 32, 300, step_path)
