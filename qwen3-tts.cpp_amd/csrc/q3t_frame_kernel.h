@@ -144,6 +144,22 @@ __device__ __forceinline__ float4 gldf4(const float * p) {
 }
 template <class T>
 __device__ __forceinline__ T gld(const T * p) { return *(const Q3T_GAS T *) p; }
+// Non-temporal variants (NTL) for the talker weights, read once per frame:
+// they then leave the memory-side cache to the code predictor's weights,
+// which every pass of the next frame re-reads.  NTL must be a constant (a
+// runtime choice between the two forms folds into one plain load).
+template <bool NTL>
+__device__ __forceinline__ int4 gld4n(const void * p) {
+    gvi4 v;
+    if constexpr (NTL) v = __builtin_nontemporal_load((const Q3T_GAS gvi4 *) p);
+    else v = *(const Q3T_GAS gvi4 *) p;
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+template <bool NTL, class T>
+__device__ __forceinline__ T gldn(const T * p) {
+    if constexpr (NTL) return __builtin_nontemporal_load((const Q3T_GAS T *) p);
+    else return *(const Q3T_GAS T *) p;
+}
 template <class T>
 __device__ __forceinline__ void gst(T * p, T v) { *(Q3T_GAS T *) p = v; }
 
@@ -381,7 +397,7 @@ __device__ __forceinline__ int rot_wave(int rot) {
     return gw >= nw ? gw - nw : gw;
 }
 
-template <int K, bool DUAL>
+template <int K, bool DUAL, bool NTL>
 __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * W, const uint16_t * Wd,
                                             const int8_t * U, const uint16_t * Ud, int rows, int rot) {
     using G = Geo<K>;
@@ -399,12 +415,12 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * 
         for (int s = 0; s < G::SLOTS; ++s) {
             const int b = lir + s * G::LPR;
             const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
-            R.w[gi][s][0] = gld4(wp); R.w[gi][s][1] = gld4(wp + 1);
-            R.dw[gi][s] = gld(Wd + (size_t) r * G::BPR + b);
+            R.w[gi][s][0] = gld4n<NTL>(wp); R.w[gi][s][1] = gld4n<NTL>(wp + 1);
+            R.dw[gi][s] = gldn<NTL>(Wd + (size_t) r * G::BPR + b);
             if (DUAL) {
                 const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
-                R.u[gi][s][0] = gld4(up); R.u[gi][s][1] = gld4(up + 1);
-                R.du[gi][s] = gld(Ud + (size_t) r * G::BPR + b);
+                R.u[gi][s][0] = gld4n<NTL>(up); R.u[gi][s][1] = gld4n<NTL>(up + 1);
+                R.du[gi][s] = gldn<NTL>(Ud + (size_t) r * G::BPR + b);
             }
         }
     }
@@ -524,7 +540,7 @@ struct F16Regs {
     int ng;
 };
 
-template <int K, bool DUAL>
+template <int K, bool DUAL, bool NTL>
 __device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_t * W, const uint16_t * U, int rows,
                                              int rot) {
     using G = Geo<K>;
@@ -543,11 +559,11 @@ __device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_
             const int b = lir + s * G::LPR;
             const int4 * wp = (const int4 *) (W + (size_t) r * K + b * kQK);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) R.w[gi][s][c] = gld4(wp + c);
+            for (int c = 0; c < 4; ++c) R.w[gi][s][c] = gld4n<NTL>(wp + c);
             if (DUAL) {
                 const int4 * up = (const int4 *) (U + (size_t) r * K + b * kQK);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) R.u[DUAL ? gi : 0][DUAL ? s : 0][c] = gld4(up + c);
+                for (int c = 0; c < 4; ++c) R.u[DUAL ? gi : 0][DUAL ? s : 0][c] = gld4n<NTL>(up + c);
             }
         }
     }
@@ -737,7 +753,7 @@ struct HeadRegs {
 };
 
 // The head rows' weights of this lane, loaded before the head input is awaited.
-template <int K>
+template <int K, bool NTL>
 __device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, HeadRegs & H) {
     constexpr int LPR = K / kQK, RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
@@ -751,7 +767,7 @@ __device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, 
         H.ng = gi + 1;
         const int4 * wp = (const int4 *) (W + (size_t) (g * RPW + rsub) * K + lir * kQK);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) H.w[gi][c] = gld4(wp + c);
+        for (int c = 0; c < 4; ++c) H.w[gi][c] = gld4n<NTL>(wp + c);
     }
 }
 
@@ -1460,8 +1476,9 @@ __device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds 
 // One decoder layer (QKV -> attention -> Wo + residual -> gate/up SwiGLU ->
 // down + residual) for NT tokens.  The input rows come from tagged slot p_in,
 // or (x_lds != nullptr, layer 0) from the rows gathered into LDS.  The
-// output is tagged slot p_out.
-template <int NT, int D, int QD, int FF, int WT>
+// output is tagged slot p_out.  TK: a talker layer (weights read
+// non-temporally).
+template <int NT, int D, int QD, int FF, int WT, bool TK>
 __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp, int pos0, uint32_t tb, int & p,
                         int p_in, const float * x_lds, int & p_out, bool & dead) {
     constexpr int QKVD = 2 * QD;
@@ -1482,8 +1499,8 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (wg_has_rows<D>(QKVD, 0)) {
         Q8Regs<D, false> R;
         F16Regs<D, false> F;
-        if constexpr (WT == W_Q8) q8_prefetch<D, false>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
-        else f16_prefetch<D, false>(F, (const uint16_t *) W.qkv, nullptr, QKVD, 0);
+        if constexpr (WT == W_Q8) q8_prefetch<D, false, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
+        else f16_prefetch<D, false, TK>(F, (const uint16_t *) W.qkv, nullptr, QKVD, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.attn_norm, nw);
         RowsT<NT, D> v;
@@ -1545,7 +1562,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         RowsT<NT, QD> v;
         if constexpr (WT == W_Q8) {
             Q8Regs<QD, false> R;
-            q8_prefetch<QD, false>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
+            q8_prefetch<QD, false, TK>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
             res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
             load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
             quant_rows<NT, QD>(v, L);
@@ -1553,7 +1570,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
                                       ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
         } else {
             F16Regs<QD, false> F;
-            f16_prefetch<QD, false>(F, (const uint16_t *) W.wo, nullptr, D, rot);
+            f16_prefetch<QD, false, TK>(F, (const uint16_t *) W.wo, nullptr, D, rot);
             res_prefetch16<NT, QD, false>(F, ar + (size_t) p_in * kSlot, rot);
             load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
             f16_rows<NT, QD, false>(v, L);
@@ -1567,8 +1584,8 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (wg_has_rows<D>(FF, 0)) {
         Q8Regs<D, true> R;
         F16Regs<D, true> F;
-        if constexpr (WT == W_Q8) q8_prefetch<D, true>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
-        else f16_prefetch<D, true>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
+        if constexpr (WT == W_Q8) q8_prefetch<D, true, TK>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
+        else f16_prefetch<D, true, TK>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
         RowsT<NT, D> v;
@@ -1590,7 +1607,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         RowsT<NT, FF> v;
         if constexpr (WT == W_Q8) {
             Q8Regs<FF, false> R;
-            q8_prefetch<FF, false>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
+            q8_prefetch<FF, false, TK>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
             res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
             load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
             quant_rows<NT, FF>(v, L);
@@ -1598,7 +1615,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
                                       ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
         } else {
             F16Regs<FF, false> F;
-            f16_prefetch<FF, false>(F, (const uint16_t *) W.wd, nullptr, D, rot);
+            f16_prefetch<FF, false, TK>(F, (const uint16_t *) W.wd, nullptr, D, rot);
             res_prefetch16<NT, FF, false>(F, ar + (size_t) p_wo * kSlot, rot);
             load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
             f16_rows<NT, FF, true>(v, L);
@@ -1693,15 +1710,16 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         for (int l = 0; l < nl; ++l) {
             const float * x_lds = l == 0 ? L.x : nullptr;
             const LayerQ8 Wl = layer_desc(Ls + l);
-            if (nt == 2) layer_t<2, D, QD, FF, WT>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else layer_t<1, D, QD, FF, WT>(A, L, Wl, l, !tk, pos0, tb, p, p_in, x_lds, p_out, dead);
+            if (nt == 2) layer_t<2, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
+            else layer_t<1, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
             p_in = p_out;
         }
         // head on the last token's normed row
         const int p_head = tk ? 0 : p++;
         HeadRegs hr;
-        if (tk) f16_head_prefetch<D>(A.codec_head, A.codec_vocab, hr);
-        else f16_head_prefetch<D>(A.cp_head[s], A.cp_vocab, hr);
+        if (tk) f16_head_prefetch<D, true>(A.codec_head, A.codec_vocab, hr);
+        else f16_head_prefetch<D, false>(A.cp_head[s], A.cp_vocab, hr);
         {
             NormT<D> nw;
             norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
