@@ -129,13 +129,18 @@ int  q3t_dev_kv_write(q3t_dev * dev, int32_t layer, int32_t n_pos,
 int  q3t_dev_prefill(q3t_dev * dev, const float * embd, int32_t n, int32_t n_past,
                      float * hidden_out, float * logits_out);
 /* One-token talker step at position n_past.  Replaces forward_step
- * (src/tts_transformer.cpp:2379-2509). */
+ * (src/tts_transformer.cpp:2379-2509).  Runs as one launch of the
+ * persistent frame kernel's talker pass where that kernel applies (else the
+ * multi-kernel step; same results). */
 int  q3t_dev_talker_step(q3t_dev * dev, const float * embd, int32_t n_past,
                          float * logits_out, float * hidden_out);
 /* Code predictor: 2-token prefill [hidden, codec_embd[cb0]] then 14 steps;
  * codes_out[15] = codebooks 1..15.  logits_out (NULL ok): [15][cp_vocab],
  * each head's logits before sampling.  `frame` keys the sampler's RNG.
- * Replaces predict_codes_autoregressive (src/tts_transformer.cpp:2711-2976). */
+ * Replaces predict_codes_autoregressive (src/tts_transformer.cpp:2711-2976).
+ * Runs on the persistent frame kernel's code-predictor passes when the talker
+ * KV cache is reserved and that kernel applies (else the multi-kernel
+ * sequence; same results). */
 int  q3t_dev_code_pred(q3t_dev * dev, const float * hidden, int32_t cb0,
                        const q3t_sampling * sampling, uint32_t frame,
                        int32_t * codes_out, float * logits_out);
