@@ -48,7 +48,9 @@ typedef struct q3t_config {
     int32_t n_codebooks;      /* 16 */
     int32_t cp_layers;        /* code-predictor blocks, 5 */
     int32_t cp_vocab;         /* 2048 */
-    int32_t cp_hidden;        /* must equal hidden_size (no mtp_proj) */
+    int32_t cp_hidden;        /* code predictor width; below hidden_size the
+                               * model carries code_pred.mtp_proj (1.7B layout,
+                               * src/tts_transformer.cpp:548-553, :1942-1947) */
     int32_t cp_ffn;           /* 3072 */
     int32_t text_vocab;       /* 151936 */
     int32_t text_embd_dim;    /* 2048 */

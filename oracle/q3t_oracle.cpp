@@ -470,6 +470,7 @@ struct orc_model {
     std::vector<Layer> talker, cp;
     std::vector<Tensor> cp_embd, cp_head;
     Tensor text_embd, fc1, fc1_b, fc2, fc2_b, codec_embd, codec_head, out_norm, cp_out_norm;
+    Tensor mtp_w, mtp_b;                          // code_pred.mtp_proj (only when cp_hidden != hidden_size)
     KV kv, cp_kv;
     std::vector<float> rope_cos, rope_sin;        // talker theta
     std::vector<float> cp_rope_cos, cp_rope_sin;  // code-predictor theta
@@ -499,11 +500,11 @@ void gemv_t(orc_model * m, const Tensor & w, int64_t rows, int64_t k, const floa
     gemv_impl(&m->pool, w.type, w.data, rows, k, x, ntok, y, is_down ? 1 : 0);
 }
 
-// One transformer layer over ntok consecutive positions starting at pos0.
-void layer_forward(orc_model * m, const Layer & L, int64_t ffn, float * x, int64_t ntok, int32_t pos0,
+// One transformer layer of width d over ntok consecutive positions starting at pos0.
+void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float * x, int64_t ntok, int32_t pos0,
                    KV & kv, int32_t il, const float * rc, const float * rs) {
     const orc_config & c = m->cfg;
-    const int64_t d = c.hidden_size, hd = c.head_dim, nh = c.n_head, nkv = c.n_kv_head;
+    const int64_t hd = c.head_dim, nh = c.n_head, nkv = c.n_kv_head;
     const int64_t qd = nh * hd, kd = nkv * hd, half = hd / 2;
     std::vector<float> h(ntok * d), q(ntok * qd), k(ntok * kd), v(ntok * kd), o(ntok * qd), t(ntok * d);
     for (int64_t i = 0; i < ntok; ++i) orc_rmsnorm(x + i * d, fp(L.attn_norm), d, c.rms_eps, h.data() + i * d);
@@ -572,6 +573,9 @@ bool resolve(orc_model * m) {
         if (!get("code_pred.codec_embd." + std::to_string(g) + ".weight", m->cp_embd[g])) return false;
         if (!get("code_pred.lm_head." + std::to_string(g) + ".weight", m->cp_head[g])) return false;
     }
+    if (c.cp_hidden != c.hidden_size &&
+        !(get("code_pred.mtp_proj.weight", m->mtp_w) && get("code_pred.mtp_proj.bias", m->mtp_b)))
+        return false;
     return get("talker.codec_embd.weight", m->codec_embd) && get("talker.codec_head.weight", m->codec_head) &&
            get("talker.output_norm.weight", m->out_norm) && get("code_pred.output_norm.weight", m->cp_out_norm) &&
            get("talker.text_embd.weight", m->text_embd) && get("talker.text_proj.fc1.weight", m->fc1) &&
@@ -597,7 +601,8 @@ bool talker_forward(orc_model * m, const float * embd, int32_t n, int32_t n_past
     const int64_t d = c.hidden_size;
     std::vector<float> x(embd, embd + (size_t) n * d);
     for (int il = 0; il < c.n_layers; ++il)
-        layer_forward(m, m->talker[il], c.ffn_size, x.data(), n, n_past, m->kv, il, m->rope_cos.data(), m->rope_sin.data());
+        layer_forward(m, m->talker[il], d, c.ffn_size, x.data(), n, n_past, m->kv, il, m->rope_cos.data(),
+                      m->rope_sin.data());
     std::vector<float> hid((size_t) n * d);
     for (int32_t i = 0; i < n; ++i) orc_rmsnorm(x.data() + i * d, fp(m->out_norm), d, c.rms_eps, hid.data() + i * d);
     if (hidden_out) std::memcpy(hidden_out, hid.data(), hid.size() * sizeof(float));
@@ -664,26 +669,40 @@ int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,
         m->cp_kv.v.assign(m->cp_kv.k.size(), 0);
     }
     ensure_rope(m, 16);
-    const int64_t d = c.hidden_size;
+    // the inputs are talker-width rows (hidden, codec / code-predictor
+    // embeddings); the MTP projection, when present, maps them to the code
+    // predictor's width (src/tts_transformer.cpp:1942-1947, :2096-2101)
+    const int64_t d = c.hidden_size, dc = c.cp_hidden;
+    const bool mtp = dc != d;
     const int32_t V = c.cp_vocab;
     const int ng = c.n_codebooks - 1;
     if (cb0 < 0 || cb0 >= c.codec_vocab) { m->err = "Embedding token ID out of range"; return -1; }
-    std::vector<float> x(2 * d), hid(d), logits(V);
-    std::memcpy(x.data(), hidden, d * sizeof(float));
-    embd_row(m->codec_embd, d, cb0, x.data() + d);
+    std::vector<float> in(2 * d), x(2 * dc), hid(dc), logits(V);
+    auto project = [&](const float * rows, int64_t n, float * out) {
+        if (!mtp) { std::memcpy(out, rows, (size_t) n * d * sizeof(float)); return; }
+        gemv_t(m, m->mtp_w, dc, d, rows, n, out);
+        for (int64_t i = 0; i < n; ++i)
+            for (int64_t j = 0; j < dc; ++j) out[i * dc + j] = out[i * dc + j] + fp(m->mtp_b)[j];
+    };
+    std::memcpy(in.data(), hidden, d * sizeof(float));
+    embd_row(m->codec_embd, d, cb0, in.data() + d);
+    project(in.data(), 2, x.data());
     for (int il = 0; il < c.cp_layers; ++il)
-        layer_forward(m, m->cp[il], c.cp_ffn, x.data(), 2, 0, m->cp_kv, il, m->cp_rope_cos.data(), m->cp_rope_sin.data());
-    orc_rmsnorm(x.data() + d, fp(m->cp_out_norm), d, c.rms_eps, hid.data());
-    gemv_t(m, m->cp_head[0], V, d, hid.data(), 1, logits.data());
+        layer_forward(m, m->cp[il], dc, c.cp_ffn, x.data(), 2, 0, m->cp_kv, il, m->cp_rope_cos.data(),
+                      m->cp_rope_sin.data());
+    orc_rmsnorm(x.data() + dc, fp(m->cp_out_norm), dc, c.rms_eps, hid.data());
+    gemv_t(m, m->cp_head[0], V, dc, hid.data(), 1, logits.data());
     if (logits_out) std::memcpy(logits_out, logits.data(), V * sizeof(float));
     codes_out[0] = orc_sample_cp(logits.data(), V, temperature, top_k, seed, frame, 1);
     for (int s = 1; s < ng; ++s) {
         if (codes_out[s - 1] < 0 || codes_out[s - 1] >= V) { m->err = "Embedding token ID out of range"; return -1; }
-        embd_row(m->cp_embd[s - 1], d, codes_out[s - 1], x.data());
+        embd_row(m->cp_embd[s - 1], d, codes_out[s - 1], in.data());
+        project(in.data(), 1, x.data());
         for (int il = 0; il < c.cp_layers; ++il)
-            layer_forward(m, m->cp[il], c.cp_ffn, x.data(), 1, s + 1, m->cp_kv, il, m->cp_rope_cos.data(), m->cp_rope_sin.data());
-        orc_rmsnorm(x.data(), fp(m->cp_out_norm), d, c.rms_eps, hid.data());
-        gemv_t(m, m->cp_head[s], V, d, hid.data(), 1, logits.data());
+            layer_forward(m, m->cp[il], dc, c.cp_ffn, x.data(), 1, s + 1, m->cp_kv, il, m->cp_rope_cos.data(),
+                          m->cp_rope_sin.data());
+        orc_rmsnorm(x.data(), fp(m->cp_out_norm), dc, c.rms_eps, hid.data());
+        gemv_t(m, m->cp_head[s], V, dc, hid.data(), 1, logits.data());
         if (logits_out) std::memcpy(logits_out + (size_t) s * V, logits.data(), V * sizeof(float));
         codes_out[s] = orc_sample_cp(logits.data(), V, temperature, top_k, seed, frame, (uint32_t) (s + 1));
     }

@@ -58,6 +58,8 @@ struct q3t_dev {
     std::vector<LayerDev> talker, cp;
     std::vector<Slot> cp_embd, cp_head;
     Slot codec_embd, codec_head, text_embd, fc1, fc1_b, fc2, fc2_b, out_norm, cp_out_norm;
+    Slot mtp_w, mtp_b;                 // code_pred.mtp_proj (cp_hidden != hidden_size, the 1.7B layout)
+    float * cpx = nullptr;             // the code predictor's projected input rows [2][cp_hidden]
 
     // workspace
     float * xa = nullptr, * xb = nullptr, * qkv = nullptr, * attn = nullptr, * ffn = nullptr;
@@ -192,7 +194,12 @@ bool expected_shape(const q3t_config & g, const std::string & n, int64_t & ne0, 
     if (n == "talker.text_proj.fc2.weight") { ne0 = g.text_embd_dim; ne1 = d; return true; }
     if (n == "talker.text_proj.fc2.bias") { ne0 = d; return true; }
     if (n == "talker.codec_embd.weight" || n == "talker.codec_head.weight") { ne0 = d; ne1 = g.codec_vocab; return true; }
-    if (n == "talker.output_norm.weight" || n == "code_pred.output_norm.weight") { ne0 = d; return true; }
+    if (n == "talker.output_norm.weight") { ne0 = d; return true; }
+    // the code predictor's own width (the 1.7B layout) and the projection to it
+    const int64_t dc = g.cp_hidden;
+    if (n == "code_pred.output_norm.weight") { ne0 = dc; return true; }
+    if (dc != d && n == "code_pred.mtp_proj.weight") { ne0 = d; ne1 = dc; return true; }
+    if (dc != d && n == "code_pred.mtp_proj.bias") { ne0 = dc; return true; }
     int idx = -1; char buf[64] = {0};
     const char * s = n.c_str();
     if (std::sscanf(s, "code_pred.codec_embd.%d.weight", &idx) == 1) {
@@ -201,22 +208,23 @@ bool expected_shape(const q3t_config & g, const std::string & n, int64_t & ne0, 
     }
     if (std::sscanf(s, "code_pred.lm_head.%d.weight", &idx) == 1) {
         if (idx < 0 || idx >= g.n_codebooks - 1) return false;
-        cb = idx; field = "cp_head"; ne0 = d; ne1 = g.cp_vocab; return true;
+        cb = idx; field = "cp_head"; ne0 = dc; ne1 = g.cp_vocab; return true;
     }
     int nl = 0, ffn = 0;
+    int64_t w = d;
     if (std::sscanf(s, "talker.blk.%d.%63s", &idx, buf) == 2) { nl = g.n_layers; ffn = g.ffn_size; }
-    else if (std::sscanf(s, "code_pred.blk.%d.%63s", &idx, buf) == 2) { nl = g.cp_layers; ffn = g.cp_ffn; is_cp = true; }
+    else if (std::sscanf(s, "code_pred.blk.%d.%63s", &idx, buf) == 2) { nl = g.cp_layers; ffn = g.cp_ffn; is_cp = true; w = dc; }
     else return false;
     if (idx < 0 || idx >= nl) return false;
     layer = idx;
     field = buf;
-    if (field == "attn_norm.weight" || field == "ffn_norm.weight") { ne0 = d; return true; }
+    if (field == "attn_norm.weight" || field == "ffn_norm.weight") { ne0 = w; return true; }
     if (field == "attn_q_norm.weight" || field == "attn_k_norm.weight") { ne0 = g.head_dim; return true; }
-    if (field == "attn_q.weight") { ne0 = d; ne1 = qd; return true; }
-    if (field == "attn_k.weight" || field == "attn_v.weight") { ne0 = d; ne1 = kd; return true; }
-    if (field == "attn_output.weight") { ne0 = qd; ne1 = d; return true; }
-    if (field == "ffn_gate.weight" || field == "ffn_up.weight") { ne0 = d; ne1 = ffn; return true; }
-    if (field == "ffn_down.weight") { ne0 = ffn; ne1 = d; return true; }
+    if (field == "attn_q.weight") { ne0 = w; ne1 = qd; return true; }
+    if (field == "attn_k.weight" || field == "attn_v.weight") { ne0 = w; ne1 = kd; return true; }
+    if (field == "attn_output.weight") { ne0 = qd; ne1 = w; return true; }
+    if (field == "ffn_gate.weight" || field == "ffn_up.weight") { ne0 = w; ne1 = ffn; return true; }
+    if (field == "ffn_down.weight") { ne0 = ffn; ne1 = w; return true; }
     return false;
 }
 
@@ -293,6 +301,9 @@ int resolve(q3t_dev * c) {
         return -1;
     if (c->codec_embd.type != Q3T_TYPE_F16 || c->codec_head.type != Q3T_TYPE_F16)
         return fail(c, "talker.codec_embd / codec_head must be F16");
+    if (g.cp_hidden != g.hidden_size &&
+        (need(c->mtp_w, "code_pred.mtp_proj.weight") || need(c->mtp_b, "code_pred.mtp_proj.bias")))
+        return -1;
     c->resolved = true;
     return 0;
 }
@@ -425,10 +436,10 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
 
 // One transformer block over nt tokens; input rows `xin` (stride d),
 // output rows left in c->xa.
-void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int ffn, uint16_t * kc, uint16_t * vc,
+void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, int ffn, uint16_t * kc, uint16_t * vc,
            int n_ctx, const float * rc, const float * rs, const int32_t * pos_ptr, int pos_const) {
     const q3t_config & g = c->cfg;
-    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     GemvSpec s{};
     s.w = weight_of(L.qkv); s.rows = qkvd; s.K = d; s.x = xin; s.x_stride = d; s.norm_w = L.attn_norm;
     s.y = c->qkv; s.y_stride = qkvd;
@@ -457,7 +468,7 @@ void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_pt
     const int d = g.hidden_size;
     const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
     for (int il = 0; il < g.n_layers; ++il)
-        layer(c, c->talker[il], il == 0 ? xin : c->xa, nt, g.ffn_size, c->kc + il * lstride, c->vc + il * lstride,
+        layer(c, c->talker[il], il == 0 ? xin : c->xa, nt, d, g.ffn_size, c->kc + il * lstride, c->vc + il * lstride,
               c->n_ctx, c->rope_cos, c->rope_sin, pos_ptr, pos_const);
     if (head) {
         GemvSpec h{};
@@ -489,14 +500,23 @@ SampleArgs sample_args(q3t_dev * c, int mode, int group) {
 // gathers the talker step embedding.
 void code_pred_seq(q3t_dev * c, bool frame_loop) {
     const q3t_config & g = c->cfg;
-    const int d = g.hidden_size;
+    const int d = g.cp_hidden;
+    const bool mtp = g.cp_hidden != g.hidden_size;
     const size_t lstride = (size_t) g.n_kv_head * 16 * g.head_dim;
     for (int step = 0; step < g.n_codebooks - 1; ++step) {
         const int nt = step == 0 ? 2 : 1;
         const int pos = step == 0 ? 0 : step + 1;
+        if (mtp) {
+            // talker-width input rows -> the code predictor's width
+            // (src/tts_transformer.cpp:1942-1947, :2096-2101)
+            GemvSpec m{};
+            m.w = weight_of(c->mtp_w); m.rows = d; m.K = g.hidden_size; m.x = c->stage; m.x_stride = g.hidden_size;
+            m.y = c->cpx; m.y_stride = d; m.bias = (const float *) c->mtp_b.data; m.epi = EPI_BIAS;
+            gemv(c, m, nt);
+        }
         for (int il = 0; il < g.cp_layers; ++il)
-            layer(c, c->cp[il], il == 0 ? c->stage : c->xa, nt, g.cp_ffn, c->cpk + il * lstride, c->cpv + il * lstride,
-                  16, c->cp_rope_cos, c->cp_rope_sin, nullptr, pos);
+            layer(c, c->cp[il], il == 0 ? (mtp ? c->cpx : c->stage) : c->xa, nt, d, g.cp_ffn, c->cpk + il * lstride,
+                  c->cpv + il * lstride, 16, c->cp_rope_cos, c->cp_rope_sin, nullptr, pos);
         GemvSpec h{};
         h.w = weight_of(c->cp_head[step]); h.rows = g.cp_vocab; h.K = d;
         h.x = c->xa + (size_t) (nt - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->cp_out_norm.data;
@@ -796,12 +816,13 @@ int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
     const q3t_config & g = c->cfg;
     auto bad = [&](const char * m) { c->err = m; *out = c; return -1; };
     if (g.head_dim != 128) return bad("head_dim must be 128");
-    if (g.cp_hidden != g.hidden_size) return bad("code predictor width must equal talker width (mtp_proj unsupported)");
-    if (g.hidden_size % 256 || g.ffn_size % 256 || g.cp_ffn % 256 || g.text_embd_dim % 256)
+    if (g.cp_hidden <= 0 || g.cp_hidden > g.hidden_size)
+        return bad("code predictor width must be positive and at most the talker width");
+    if (g.hidden_size % 256 || g.cp_hidden % 256 || g.ffn_size % 256 || g.cp_ffn % 256 || g.text_embd_dim % 256)
         return bad("hidden/ffn/text widths must be multiples of 256");
     auto ok_k = [](int k) { int b = k / 32; return b % 32 == 0 || (b <= 32 && (b & (b - 1)) == 0); };
-    if (!ok_k(g.hidden_size) || !ok_k(g.ffn_size) || !ok_k(g.cp_ffn) || !ok_k(g.text_embd_dim) ||
-        !ok_k(g.n_head * g.head_dim))
+    if (!ok_k(g.hidden_size) || !ok_k(g.cp_hidden) || !ok_k(g.ffn_size) || !ok_k(g.cp_ffn) ||
+        !ok_k(g.text_embd_dim) || !ok_k(g.n_head * g.head_dim))
         return bad("unsupported reduction width");
     if (g.n_head % g.n_kv_head) return bad("n_head must be a multiple of n_kv_head");
     if (g.codec_vocab > kMaxVocab || g.cp_vocab > kMaxVocab) return bad("vocabulary too large for the on-device sampler");
@@ -825,6 +846,7 @@ int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
     rc |= dev_alloc_t(c, &c->tp_a, (size_t) 4 * wide);
     rc |= dev_alloc_t(c, &c->tp_b, (size_t) 4 * wide);
     rc |= dev_alloc_t(c, &c->hidden, (size_t) 4 * d);
+    rc |= dev_alloc_t(c, &c->cpx, (size_t) 2 * g.cp_hidden);
     rc |= dev_alloc_t(c, &c->logits, (size_t) g.codec_vocab);
     rc |= dev_alloc_t(c, &c->cp_logits, (size_t) (g.n_codebooks - 1) * g.cp_vocab);
     rc |= dev_alloc_t(c, &c->st, 1);
@@ -921,6 +943,8 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
     else if (n == "talker.codec_head.weight") c->codec_head = s;
     else if (n == "talker.output_norm.weight") c->out_norm = s;
     else if (n == "code_pred.output_norm.weight") c->cp_out_norm = s;
+    else if (n == "code_pred.mtp_proj.weight") c->mtp_w = s;
+    else if (n == "code_pred.mtp_proj.bias") c->mtp_b = s;
     return 0;
 }
 

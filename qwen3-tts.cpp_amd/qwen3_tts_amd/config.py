@@ -77,3 +77,19 @@ def tiny(n_layers=2, cp_layers=2, hidden=256, ffn=512, n_head=4, n_kv_head=2, te
                   cp_layers=cp_layers, cp_hidden=hidden, cp_ffn=ffn, text_vocab=text_vocab,
                   text_embd_dim=text_embd, tts_bos_id=text_vocab - 3, tts_eos_id=text_vocab - 2,
                   tts_pad_id=text_vocab - 4)
+
+
+def tiny_mtp(n_layers=2, cp_layers=2, hidden=512, cp_hidden=256, ffn=512, cp_ffn=512, n_head=4, n_kv_head=2,
+             text_vocab=4096, text_embd=256):
+    """Small shapes of the 1.7B layout: the code predictor is narrower than the
+    talker and its inputs pass through code_pred.mtp_proj."""
+    return Config(hidden_size=hidden, n_layers=n_layers, n_head=n_head, n_kv_head=n_kv_head, ffn_size=ffn,
+                  cp_layers=cp_layers, cp_hidden=cp_hidden, cp_ffn=cp_ffn, text_vocab=text_vocab,
+                  text_embd_dim=text_embd, tts_bos_id=text_vocab - 3, tts_eos_id=text_vocab - 2,
+                  tts_pad_id=text_vocab - 4)
+
+
+def full_17b():
+    """The 1.7B layout: a 2048-wide talker (FFN 6144) over a 1024-wide code
+    predictor reached through code_pred.mtp_proj."""
+    return Config(hidden_size=2048, ffn_size=6144, cp_hidden=1024, cp_ffn=3072)

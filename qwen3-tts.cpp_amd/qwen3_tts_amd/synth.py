@@ -42,8 +42,12 @@ def dequantize_q8_0(blocks):
 
 
 def tensor_specs(cfg, wtype="q8_0"):
-    """[(name, type, (ne0, ne1))] for every tensor the frame loop reads."""
-    d, te = cfg.hidden_size, cfg.text_embd_dim
+    """[(name, type, (ne0, ne1))] for every tensor the frame loop reads.  The
+    code predictor's blocks, output norm and heads have its own width
+    cp_hidden; its embeddings have the talker width, and a model whose widths
+    differ (the 1.7B layout) carries code_pred.mtp_proj between the two
+    (src/tts_transformer.cpp:496-553)."""
+    d, te, dc = cfg.hidden_size, cfg.text_embd_dim, cfg.cp_hidden
     qd, kd = cfg.n_head * cfg.head_dim, cfg.n_kv_head * cfg.head_dim
     mat = Q8_0 if wtype == "q8_0" else F16
     specs = [
@@ -55,9 +59,11 @@ def tensor_specs(cfg, wtype="q8_0"):
         ("talker.codec_embd.weight", F16, (d, cfg.codec_vocab)),
         ("talker.codec_head.weight", F16, (d, cfg.codec_vocab)),
         ("talker.output_norm.weight", F32, (d, 1)),
-        ("code_pred.output_norm.weight", F32, (d, 1)),
+        ("code_pred.output_norm.weight", F32, (dc, 1)),
     ]
-    for prefix, nl, ffn in (("talker", cfg.n_layers, cfg.ffn_size), ("code_pred", cfg.cp_layers, cfg.cp_ffn)):
+    if dc != d:
+        specs += [("code_pred.mtp_proj.weight", mat, (d, dc)), ("code_pred.mtp_proj.bias", F32, (dc, 1))]
+    for prefix, nl, ffn, d in (("talker", cfg.n_layers, cfg.ffn_size, d), ("code_pred", cfg.cp_layers, cfg.cp_ffn, dc)):
         for i in range(nl):
             p = f"{prefix}.blk.{i}."
             specs += [
@@ -74,8 +80,8 @@ def tensor_specs(cfg, wtype="q8_0"):
                 (p + "ffn_down.weight", mat, (ffn, d)),
             ]
     for g in range(cfg.n_codebooks - 1):
-        specs.append((f"code_pred.codec_embd.{g}.weight", F16, (d, cfg.cp_vocab)))
-        specs.append((f"code_pred.lm_head.{g}.weight", F16, (d, cfg.cp_vocab)))
+        specs.append((f"code_pred.codec_embd.{g}.weight", F16, (cfg.hidden_size, cfg.cp_vocab)))
+        specs.append((f"code_pred.lm_head.{g}.weight", F16, (dc, cfg.cp_vocab)))
     return specs
 
 

@@ -384,3 +384,47 @@ def test_steps_and_code_pred_full_q8(step_path):
     """The same at the 0.6B shapes with Q8_0 layers, after a 300-row prefill
     (the talker steps take the split attention of the persistent kernel)."""
     _steps_and_code_pred(qcfg.full_06b(), "q8_0", 32, 300, step_path)
+
+
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_mtp_layout_matches_oracle(wtype):
+    """The 1.7B layout at small shapes: a code predictor narrower than the
+    talker, reached through code_pred.mtp_proj (src/tts_transformer.cpp:
+    1942-1947, :2096-2101).  Talker steps, greedy and sampled code-predictor
+    calls and whole greedy and sampled frame loops equal the oracle; the
+    frame loop runs the multi-kernel frame (the persistent kernel needs equal
+    widths)."""
+    cfg = qcfg.tiny_mtp()
+    say(f"[gpu] mtp layout {wtype}")
+    w, dev, o = make(cfg, wtype, seed=41, n_ctx=64)
+    try:
+        rng = np.random.default_rng(42)
+        d = cfg.hidden_size
+        embd = (rng.standard_normal((10, d)) * 0.05).astype(np.float32)
+        hid_g, log_g = dev.prefill(embd, 0)
+        hid_o, log_o = o.prefill(embd, 0)
+        assert np.array_equal(log_g, log_o)
+        for s in range(2):
+            e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+            lg, hg = dev.talker_step(e, 10 + s)
+            lo, ho = o.step(e, 10 + s)
+            assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+            cb0 = int(np.argmax(lg[:cfg.codec_vocab - 1024]))
+            cg, lcg = dev.code_pred(hg, cb0, frame=s)
+            co, lco = o.code_pred(ho, cb0, frame=s)
+            assert np.array_equal(cg, co) and np.array_equal(lcg, lco)
+            cg, _ = dev.code_pred(hg, cb0, temperature=0.9, top_k=50, seed=7, frame=s)
+            co, _ = o.code_pred(ho, cb0, temperature=0.9, top_k=50, seed=7, frame=s)
+            assert np.array_equal(cg, co)
+        text = rng.integers(0, cfg.text_vocab - 8, 24).astype(np.int32)
+        spk = rng.standard_normal(d).astype(np.float32)
+        co, _ = o.generate(text, spk, max_len=20, temperature=0.0, top_k=0)
+        cg = driver.generate(dev, cfg, text, spk, max_len=20, temperature=0.0, top_k=0, chunk=7)
+        assert co.shape == cg.shape and np.array_equal(cg, co)
+        co, _ = o.generate(text, None, max_len=16, temperature=0.9, top_k=50, seed=13)
+        cg = driver.generate(dev, cfg, text, None, max_len=16, temperature=0.9, top_k=50, seed=13, chunk=5)
+        assert np.array_equal(cg, co)
+        us, n, path = dev.frames_stats()
+        assert path == 0
+    finally:
+        dev.close()

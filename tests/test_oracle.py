@@ -404,3 +404,56 @@ def test_golden_codes_fixture(tiny):
     codes, first = o.generate(g["text"], g["speaker"], max_len=int(g["max_len"]), temperature=0.0)
     assert np.array_equal(codes, g["codes"])
     assert np.array_equal(first, g["first_logits"])
+
+
+class _Tensors:
+    def __init__(self, d):
+        self.tensors = d
+
+    def items(self):
+        return self.tensors.items()
+
+
+def test_mtp_projection_equals_projected_inputs():
+    """The 1.7B layout (code predictor narrower than the talker, inputs through
+    code_pred.mtp_proj, src/tts_transformer.cpp:1942-1947, :2096-2101), pinned
+    against a model of the code predictor's width without the projection whose
+    hidden row and embedding tables are the projected rows, formed here in
+    numpy: y = fp32(sum of fp16(x) * w, exact) + bias in fp32 (F16 weights).
+    A projection applied to the wrong rows, or skipped on the step inputs,
+    changes the codes."""
+    import dataclasses
+    cfg = qcfg.tiny_mtp()
+    w = Weights(cfg, "f16", seed=21)
+    o = orc.Oracle(cfg, w, threads=4)
+    d, dc = cfg.hidden_size, cfg.cp_hidden
+    W = w["code_pred.mtp_proj.weight"][2].astype(np.float64).reshape(dc, d)
+    b = w["code_pred.mtp_proj.bias"][2].astype(np.float32)
+
+    def proj(rows):
+        x = np.asarray(rows, np.float32).astype(np.float16).astype(np.float64)
+        return (x @ W.T).astype(np.float32) + b
+
+    cfg2 = dataclasses.replace(cfg, hidden_size=dc)
+    w2 = Weights(cfg2, "f16", seed=22)
+    t = dict(w2.items())
+    for name, v in w.items():
+        if name.startswith("code_pred.") and "codec_embd" not in name and "mtp_proj" not in name:
+            t[name] = v
+    codec = w["talker.codec_embd.weight"][2].astype(np.float32).reshape(cfg.codec_vocab, d)
+    t["talker.codec_embd.weight"] = (0, (dc, cfg.codec_vocab), np.ascontiguousarray(proj(codec)))
+    for g in range(cfg.n_codebooks - 1):
+        e = w[f"code_pred.codec_embd.{g}.weight"][2].astype(np.float32).reshape(cfg.cp_vocab, d)
+        t[f"code_pred.codec_embd.{g}.weight"] = (0, (dc, cfg.cp_vocab), np.ascontiguousarray(proj(e)))
+    o2 = orc.Oracle(cfg2, _Tensors(t), threads=4)
+    rng = np.random.default_rng(23)
+    for cb0 in (3, 1500):
+        hid = rng.standard_normal(d).astype(np.float32)
+        o.kv_reset(16)
+        o2.kv_reset(16)
+        c1, l1 = o.code_pred(hid, cb0)
+        c2, l2 = o2.code_pred(proj(hid[None])[0], cb0)
+        assert np.array_equal(c1, c2) and np.array_equal(l1, l2)
+        c1, _ = o.code_pred(hid, cb0, temperature=0.9, top_k=50, seed=4, frame=2)
+        c2, _ = o2.code_pred(proj(hid[None])[0], cb0, temperature=0.9, top_k=50, seed=4, frame=2)
+        assert np.array_equal(c1, c2)
