@@ -48,10 +48,13 @@ def icl_rows(o, cfg, text, ref_text, ref_codes, spk):
     return prefill, trailing, pad
 
 
+@pytest.mark.parametrize("layout", ["tiny", "tiny_mtp"])
 @pytest.mark.parametrize("wtype", ["q8_0", "f16"])
-def test_facade_matches_oracle(tmp_path, wtype):
+def test_facade_matches_oracle(tmp_path, wtype, layout):
+    """tiny_mtp: the 1.7B layout (code_pred.mtp_proj, a narrower code
+    predictor) read from the GGUF keys and tensors."""
     assert os.path.exists(BIN), "build() first"
-    cfg = qcfg.tiny()
+    cfg = getattr(qcfg, layout)()
     w = Weights(cfg, wtype, seed=31)
     model = tmp_path / "tiny.gguf"
     gguf.write(str(model), cfg, w)
@@ -63,7 +66,7 @@ def test_facade_matches_oracle(tmp_path, wtype):
     with open(tmp_path / "in.bin", "wb") as f:
         f.write(struct.pack("<i", len(text)) + text.tobytes() + spk.tobytes())
         f.write(struct.pack("<ii", max_len, ref_codes.shape[0]) + ref_codes.tobytes())
-    print(f"[gpu] facade {wtype}", file=sys.stderr, flush=True)
+    print(f"[gpu] facade {wtype} {layout}", file=sys.stderr, flush=True)
     r = subprocess.run([BIN, str(model), str(tmp_path / "in.bin"), str(tmp_path)], capture_output=True, text=True,
                        timeout=300)
     print(r.stdout, r.stderr, file=sys.stderr)
