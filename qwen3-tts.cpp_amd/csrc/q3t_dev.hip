@@ -400,8 +400,8 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     const q3t_config & g = c->cfg;
     const int G = g.n_head / g.n_kv_head;
     if (nt == 1 && s.rc == c->rope_cos && !s.probs && (G == 1 || G == 2 || G == 4) && c->gqa_lds_ok) {
-        // one talker token: a 16-wave workgroup per KV head reads each cached
-        // K/V row once for the group's query heads (ms::k_attn_gqa)
+        // one talker token: a 16-wave workgroup per query head streams its KV
+        // head's cache (ms::k_attn_gqa, one head per workgroup)
         ms::GqaArgs q{};
         q.qkv = s.qkv; q.qkv_stride = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
         q.q_norm = s.L->q_norm; q.k_norm = s.L->k_norm; q.eps = g.rms_eps;
@@ -412,11 +412,8 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
         q.done = &c->st->done; q.done_stream = 0;
         q.out = c->attn; q.out_stride = g.n_head * g.head_dim;
         q.scale = 1.0f / std::sqrt((float) g.head_dim);
-        const dim3 grid(g.n_kv_head, 1), block(ms::kAThreads);
-        const size_t lds = ms::attn_gqa_lds_bytes(G, s.n_ctx);
-        if (G == 1) hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, lds, c->stream, q);
-        else if (G == 2) hipLaunchKernelGGL(ms::k_attn_gqa<2>, grid, block, lds, c->stream, q);
-        else hipLaunchKernelGGL(ms::k_attn_gqa<4>, grid, block, lds, c->stream, q);
+        const dim3 grid(g.n_head, 1), block(ms::kAThreads);
+        hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, s.n_ctx), c->stream, q);
         return;
     }
     AttnArgs a{};
@@ -1046,11 +1043,10 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
         const int G = g.n_kv_head > 0 ? g.n_head / g.n_kv_head : 0;
         c->gqa_lds_ok = false;
         if (G == 1 || G == 2 || G == 4) {
-            const size_t al = ms::attn_gqa_lds_bytes(G, n_ctx);
+            const size_t al = ms::attn_gqa_lds_bytes(1, n_ctx);
             if (al <= (size_t) max_lds) {
-                const void * fn = G == 1 ? (const void *) ms::k_attn_gqa<1>
-                                : G == 2 ? (const void *) ms::k_attn_gqa<2> : (const void *) ms::k_attn_gqa<4>;
-                HIP_OK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
+                HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int) al));
                 c->gqa_lds_ok = true;
             }
         }
@@ -1663,11 +1659,11 @@ void attn_gqa(q3t_dev * c, const LayerDev & L, const StreamKV & kv) {
     a.out = c->batt; a.out_stride = qd;
     a.out_q = c->bq8; a.out_dx = c->bdx8;
     a.scale = 1.0f / std::sqrt((float) g.head_dim);
-    const dim3 grid(g.n_kv_head, c->nb), block(ms::kAThreads);
-    const size_t lds = ms::attn_gqa_lds_bytes(G, kv.n_ctx);
-    if (G == 1) hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, lds, c->stream, a);
-    else if (G == 2) hipLaunchKernelGGL(ms::k_attn_gqa<2>, grid, block, lds, c->stream, a);
-    else hipLaunchKernelGGL(ms::k_attn_gqa<4>, grid, block, lds, c->stream, a);
+    // one query head per workgroup: twice the workgroups of one per KV head,
+    // each streaming its KV head's cache (the two of a group share it in L2)
+    (void) G;
+    const dim3 grid(g.n_head, c->nb), block(ms::kAThreads);
+    hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, kv.n_ctx), c->stream, a);
 }
 
 // One decoder layer over n = nb * nt rows (stream-major); output rows in c->bxa.
@@ -1821,7 +1817,7 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
         return fail(c, "multi-stream decode: unsupported model widths");
     int max_lds = 0;
     HIP_OK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device));
-    const size_t al = ms::attn_gqa_lds_bytes(G, n_ctx);
+    const size_t al = ms::attn_gqa_lds_bytes(1, n_ctx);
     const int kproj = std::max(qd, g.ffn_size);
     size_t gl = 0;
     for (int kind = 0; kind < 3; ++kind) gl = std::max(gl, gemm_lds(kind, 4, gemm_k(kind, d, kproj)));
@@ -1829,8 +1825,6 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     if (al > (size_t) max_lds) return fail(c, "multi-stream decode: n_ctx too large for the attention kernel's LDS");
     HIP_OK(allow_gemm_lds(d, kproj));
     HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
-    HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
-    HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
     // the streams' talker caches share the context's RoPE tables and KV layout stride
     if (c->n_ctx != n_ctx && q3t_dev_kv_reserve(c, n_ctx)) return -1;
     HIP_OK(hipStreamSynchronize(c->stream));

@@ -441,9 +441,15 @@ __device__ __forceinline__ void wave_norm_rope(float & x0, float & x1, const flo
     x1 = p1 + q1;
 }
 
+// Workgroup x takes query heads G x .. G x + G - 1 of stream blockIdx.y; with
+// G below the group size two or more workgroups share a KV head, read its
+// cache each, and only the first appends the new K/V row (the others take
+// the new row from their own LDS).
 template <int G>
 __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
-    const int g = blockIdx.x, z = blockIdx.y;
+    const int hq0 = blockIdx.x * G, z = blockIdx.y;
+    const int gsz = a.n_head / a.n_kv_head, g = hq0 / gsz;
+    const bool append = hq0 % gsz == 0;
     if (a.done && a.done[(size_t) z * a.done_stream]) return;
     extern __shared__ __align__(16) char smem[];
     float * qf = (float *) smem;                  // [G][128] fp16-rounded rotated q
@@ -464,7 +470,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
     const float * rs = a.rope_sin + (size_t) pos * 64;
 
     if (wave < G) {
-        const int h = g * G + wave;
+        const int h = hq0 + wave;
         float x0 = row[h * kHD + lane], x1 = row[h * kHD + 64 + lane];
         wave_norm_rope(x0, x1, a.q_norm, a.eps, rc, rs);
         qf[wave * kHD + lane] = round_f16(x0);
@@ -475,14 +481,18 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
         const uint16_t k0 = f2h(x0), k1 = f2h(x1);
         knew[lane] = h2f(k0);
         knew[lane + 64] = h2f(k1);
-        kbase[(size_t) pos * kHD + lane] = k0;
-        kbase[(size_t) pos * kHD + 64 + lane] = k1;
+        if (append) {
+            kbase[(size_t) pos * kHD + lane] = k0;
+            kbase[(size_t) pos * kHD + 64 + lane] = k1;
+        }
     } else if (wave == G + 1) {
         const uint16_t v0 = f2h(row[qd + kd + g * kHD + lane]), v1 = f2h(row[qd + kd + g * kHD + 64 + lane]);
         vnew[lane] = h2f(v0);
         vnew[lane + 64] = h2f(v1);
-        vbase[(size_t) pos * kHD + lane] = v0;
-        vbase[(size_t) pos * kHD + 64 + lane] = v1;
+        if (append) {
+            vbase[(size_t) pos * kHD + lane] = v0;
+            vbase[(size_t) pos * kHD + 64 + lane] = v1;
+        }
     }
     __syncthreads();
 
@@ -642,7 +652,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
 #pragma unroll
         for (int w = 0; w < kAWaves; ++w) r += pv[(w * G + h) * kHD + d];
         const float o = (float) r;
-        const size_t e = (size_t) z * a.out_stride + (g * G + h) * kHD + d;
+        const size_t e = (size_t) z * a.out_stride + (hq0 + h) * kHD + d;
         a.out[e] = o;
         if (a.out_q) a.out_q[e] = quant_lane32(o, a.out_dx + e / kQK, (t & 31) == 0);
     }
