@@ -328,7 +328,7 @@ void launch_gemv_t(q3t_dev * c, const GemvArgs & a) {
     const int groups = a.rows / RPW;
     int grid = (groups + 3) / 4;
     grid = std::max(1, std::min(grid, 2048));
-    const size_t lds = 64 + act_bytes<WT>(NT, a.K);
+    const size_t lds = act_red_bytes(NT) + act_bytes<WT>(NT, a.K);
     hipLaunchKernelGGL((k_gemv<WT, NT, DUAL>), dim3(grid), dim3(kBlock), lds, c->stream, a);
 }
 
@@ -355,7 +355,14 @@ void launch_gemv_nt(q3t_dev * c, const GemvArgs & a, int nt, bool reg) {
     else if (reg && nt == 2) launch_gemv_rs<WT, 2, DUAL>(c, a);
     else if (nt == 1) launch_gemv_t<WT, 1, DUAL>(c, a);
     else if (nt == 2) launch_gemv_t<WT, 2, DUAL>(c, a);
-    else launch_gemv_t<WT, 4, DUAL>(c, a);
+    else if constexpr (WT == W_F16 && !DUAL) {
+        // the multi-stream heads: up to 16 streams' rows per launch
+        if (nt == 16) launch_gemv_t<WT, 16, DUAL>(c, a);
+        else if (nt == 8) launch_gemv_t<WT, 8, DUAL>(c, a);
+        else launch_gemv_t<WT, 4, DUAL>(c, a);
+    } else {
+        launch_gemv_t<WT, 4, DUAL>(c, a);
+    }
 }
 
 // K values the register path covers: K/32 a power of two up to 32, or 64, or 96.
@@ -1544,8 +1551,9 @@ namespace {
 
 // F16 / Q8 GEMV over n rows in launches of 4, 2 or 1 rows.
 static void gemv_rows(q3t_dev * c, const GemvSpec & s, int n) {
+    const bool wide = s.w.kind == W_F16 && s.epi != EPI_SWIGLU;   // 8 / 16 rows per launch (F16 heads)
     for (int r = 0; r < n;) {
-        const int nt = n - r >= 4 ? 4 : n - r >= 2 ? 2 : 1;
+        const int nt = wide && n - r >= 16 ? 16 : wide && n - r >= 8 ? 8 : n - r >= 4 ? 4 : n - r >= 2 ? 2 : 1;
         GemvSpec t = s;
         t.x = s.x + (size_t) r * s.x_stride;
         t.y = s.y + (size_t) r * s.y_stride;

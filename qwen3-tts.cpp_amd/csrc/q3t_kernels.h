@@ -76,19 +76,41 @@ __host__ __device__ constexpr size_t act_bytes(int nt, int k) {
          : WT == W_F16 ? (size_t) nt * k * 2 : (size_t) nt * k * 4;
 }
 
+// LDS ahead of the activation rows: the RMSNorm partials [NT][4 waves] fp64.
+__host__ __device__ constexpr size_t act_red_bytes(int nt) { return (size_t) (nt < 2 ? 2 : nt) * 4 * 8; }
+
 template <int WT, int NT>
 __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char * act) {
     const int K = a.K, t = threadIdx.x;
+    // RMSNorm scales of all NT rows with one pair of workgroup barriers; each
+    // row's sum is formed in the order of block_sum_d
+    float scales[NT];
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok) scales[tok] = 1.0f;
+    if (a.pro == PRO_NORM) {
+        double ss[NT];
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) {
+            const float * x = a.x + (size_t) tok * a.x_stride;
+            ss[tok] = 0.0;
+            for (int e = t; e < K; e += kBlock) { const float v = x[e]; ss[tok] += (double) (v * v); }
+            ss[tok] = wave_sum_d(ss[tok]);
+        }
+        __syncthreads();
+        if ((t & 63) == 0)
+#pragma unroll
+            for (int tok = 0; tok < NT; ++tok) red[tok * 4 + (t >> 6)] = ss[tok];
+        __syncthreads();
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) {
+            const double tot = (red[tok * 4 + 0] + red[tok * 4 + 1]) + (red[tok * 4 + 2] + red[tok * 4 + 3]);
+            const float mean = (float) (tot / (double) K);
+            scales[tok] = 1.0f / sqrtf(mean + a.eps);
+        }
+    }
     for (int tok = 0; tok < NT; ++tok) {
         const float * x = a.x + (size_t) tok * a.x_stride;
-        float scale = 1.0f;
-        if (a.pro == PRO_NORM) {
-            double ss = 0.0;
-            for (int e = t; e < K; e += kBlock) { const float v = x[e]; ss += (double) (v * v); }
-            const double tot = block_sum_d(ss, red);
-            const float mean = (float) (tot / (double) K);
-            scale = 1.0f / sqrtf(mean + a.eps);
-        }
+        const float scale = scales[tok];
         for (int e = t; e < K; e += kBlock) {
             float v = x[e];
             if (a.pro == PRO_NORM) {
@@ -226,7 +248,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv(GemvArgs a) {
     if (a.done && *a.done) return;
     extern __shared__ __align__(16) char smem[];
     double * red = (double *) smem;
-    char * act = smem + 64;
+    char * act = smem + act_red_bytes(NT);
     build_act<WT, NT>(a, red, act);
     gemv_rows<WT, NT, DUAL>(a, act);
 }
