@@ -612,6 +612,13 @@ __device__ __forceinline__ float h8(const int4 & v, int j) {
     const int w = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
     return h2f((uint16_t) ((j & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu)));
 }
+// The same element as a half value.
+__device__ __forceinline__ _Float16 h8h(const int4 & v, int j) {
+    const int w = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
+    const uint16_t b = (uint16_t) ((j & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu));
+    return __builtin_bit_cast(_Float16, b);
+}
+
 
 template <int NT, int K, bool DUAL, bool WIDE>
 __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
@@ -657,7 +664,8 @@ __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Ld
                 if (DUAL) __asm__ volatile("" : "+v"(uv.x), "+v"(uv.y), "+v"(uv.z), "+v"(uv.w));
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float wf = h8(wv, j), uf = DUAL ? h8(uv, j) : 0.0f;
+                    const float wf = WIDE ? h8(wv, j) : 0.0f, uf = WIDE && DUAL ? h8(uv, j) : 0.0f;
+                    const _Float16 wh = h8h(wv, j), uh = DUAL ? h8h(uv, j) : (_Float16) 0.0f;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         if (WIDE) {
@@ -675,9 +683,9 @@ __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Ld
                             }
                         } else {
                             // fp16 x fp16: exact in fp32
-                            const float xf = h8(xp[t], j);
-                            acc[gi][t] += (double) (wf * xf);
-                            if (DUAL) acc2[gi][t] += (double) (uf * xf);
+                            const _Float16 xh = h8h(xp[t], j);
+                            acc[gi][t] += (double) hmul_exact(wh, xh);
+                            if (DUAL) acc2[gi][t] += (double) hmul_exact(uh, xh);
                         }
                     }
                 }

@@ -156,14 +156,14 @@ __global__ __launch_bounds__(kBlock) void k_gemv_r(GemvArgs a) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const float xv8 = xv[8 * c + j];
-                        const float xf = round_f16(xv8);
+                        const _Float16 xh = __builtin_bit_cast(_Float16, f2h(xv8));
 #pragma unroll
                         for (int g = 0; g < G; ++g) {
                             const uint16_t * wh = (const uint16_t *) &w[g][s][c];
                             const uint16_t * uh = (const uint16_t *) &u[g][s][c];
                             if (WT == W_F16) {
-                                acc[g][tok] += (double) (h2f(wh[j]) * xf);
-                                if (DUAL) acc2[g][tok] += (double) (h2f(uh[j]) * xf);
+                                acc[g][tok] += (double) hmul_exact(__builtin_bit_cast(_Float16, wh[j]), xh);
+                                if (DUAL) acc2[g][tok] += (double) hmul_exact(__builtin_bit_cast(_Float16, uh[j]), xh);
                             } else {
                                 acc[g][tok] = fma((double) h2f(wh[j]), (double) xv8, acc[g][tok]);
                             }

@@ -216,9 +216,10 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs & a, const char * act) 
                             const uint16_t * xh = (const uint16_t *) &xv;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
-                                const float xf = h2f(xh[j]);
-                                acc[tok] += (double) (h2f(wh[j]) * xf);   // exact fp16*fp16 product
-                                if (DUAL) acc2[tok] += (double) (h2f(uh[j]) * xf);
+                                const _Float16 xj = __builtin_bit_cast(_Float16, xh[j]);
+                                // exact fp16*fp16 product
+                                acc[tok] += (double) hmul_exact(__builtin_bit_cast(_Float16, wh[j]), xj);
+                                if (DUAL) acc2[tok] += (double) hmul_exact(__builtin_bit_cast(_Float16, uh[j]), xj);
                             }
                         } else {
                             const float * xf = (const float *) act + (size_t) tok * K + b * kQK + c * 8;

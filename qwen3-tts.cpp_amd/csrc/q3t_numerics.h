@@ -15,6 +15,9 @@ constexpr int kBlock = 256;   // threads per workgroup for GEMV / attention
 constexpr int kQK = 32;       // Q8_0 block length
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+// Exact fp32 product of two fp16 values (at most 22 significant bits, no
+// overflow or underflow in fp32) as one mixed-precision fma with a zero addend.
+__device__ __forceinline__ float hmul_exact(_Float16 a, _Float16 b) { return __builtin_fmaf((float) a, (float) b, 0.0f); }
 // The empty asm makes the fp32 value opaque: without it the compiler folds
 // f2h(a * b) into v_fma_mixlo_f16 (one rounding of the exact product to
 // fp16), which differs from rounding to fp32 and then to fp16 whenever the
