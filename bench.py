@@ -305,7 +305,7 @@ def main():
     os.environ["Q3T_FRAME_KERNEL"] = "1" if args.path == "persistent" else "0"
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (batch-1 decode is a single "
-              "dependent chain; see DESIGN.md for how independent streams would shard).", file=sys.stderr)
+              "dependent chain; independent streams shard by data parallelism, one process per GPU).", file=sys.stderr)
         sys.exit(2)
 
     from qwen3_tts_amd import config, driver
