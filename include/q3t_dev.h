@@ -156,6 +156,32 @@ int  q3t_dev_text_proj(q3t_dev * dev, const int32_t * tokens, int32_t n, float *
 int  q3t_dev_embed_rows(q3t_dev * dev, int32_t table, int32_t index,
                         const int32_t * tokens, int32_t n, float * out);
 
+/* Prefill rows in one call: build_prefill_graph (src/tts_transformer.cpp:1030-1186).
+ * Every text id of the layout (tts bos/eos/pad, the 3 role ids, the first text id,
+ * the instruct ids, the trailing ids text[4 .. n-5)) is projected in one batched
+ * pass, and the codec overlays are summed on the device.  Outputs: prefill_out
+ * [n_prefill][hidden], trailing_out [n_trailing][hidden] (trailing text rows, then
+ * tts_eos), tts_pad_out [hidden].  With prefill_out == NULL only the two counts are
+ * written (n_prefill = n_instruct + 3 + codec rows, n_trailing = max(0, n - 9) + 1).
+ * language_id < 0 selects the no-think codec prefix; speaker_embd may be NULL. */
+int  q3t_dev_build_prefill(q3t_dev * dev, const int32_t * text_tokens, int32_t n_tokens,
+                           const float * speaker_embd, int32_t language_id,
+                           const int32_t * instruct_tokens, int32_t n_instruct,
+                           float * prefill_out, int32_t * n_prefill_out,
+                           float * trailing_out, int32_t * n_trailing_out, float * tts_pad_out);
+/* The voice-clone prefill: build_prefill_graph_icl (src/tts_transformer.cpp:1188-1472).
+ * The text stream ref_text[3:-5] ++ text[3:-5] ++ tts_eos is interleaved with the
+ * codec stream [codec_bos, reference frames] (each frame the sum of its 16 codebook
+ * embeddings, ref_codec_tokens [n_ref_frames][16]) up to the codec length; the rest
+ * of the text stream is the trailing text (n_trailing may be 0).  Same output and
+ * size-query convention as q3t_dev_build_prefill. */
+int  q3t_dev_build_prefill_icl(q3t_dev * dev, const int32_t * text_tokens, int32_t n_tokens,
+                               const int32_t * ref_text_tokens, int32_t n_ref_text,
+                               const int32_t * ref_codec_tokens, int32_t n_ref_frames,
+                               const float * speaker_embd,
+                               float * prefill_out, int32_t * n_prefill_out,
+                               float * trailing_out, int32_t * n_trailing_out, float * tts_pad_out);
+
 /* Device-resident frame loop (the body of generate(),
  * src/tts_transformer.cpp:3108-3309).  frames_begin takes the logits and
  * normed hidden left on the device by the last q3t_dev_prefill /

@@ -96,6 +96,12 @@ struct q3t_dev {
     bool stats_streams = false;    // frame statistics describe the multi-stream loop
     std::vector<int32_t> s_emitted;
     int32_t * ids = nullptr; int32_t ids_cap = 0;
+    // text projection and prefill row assembly: fc1 rows (quantised and
+    // fp32) and projected rows for bp_rows ids; assembled rows, their specs
+    // and the ICL reference codes
+    int32_t bp_rows = 0; int8_t * bp_q = nullptr; float * bp_dx = nullptr, * bp_h = nullptr, * bp_proj = nullptr;
+    int32_t bp_out_rows = 0; float * bp_out = nullptr; RowSpec * bp_spec = nullptr;
+    int32_t * bp_frames = nullptr; int32_t bp_frames_cap = 0; float * bp_spk = nullptr;
     FrameState * st = nullptr;
     SampleParams * params = nullptr;
     uint8_t * seen = nullptr;
@@ -1086,6 +1092,10 @@ int q3t_dev_kv_write(q3t_dev * c, int32_t layer, int32_t n_pos, const uint16_t *
     return 0;
 }
 
+}  // extern "C"
+
+namespace {
+
 // Which tiled path the talker prefill of n tokens takes: 1 = int8 MFMA GEMMs
 // (Q8_0 layers), 2 = exact F16 VALU GEMMs (F16 layers), 0 = the chunked GEMV
 // prefill.  Tiled needs GEMM-friendly widths and n >= 16
@@ -1237,6 +1247,144 @@ void prefill_mfma(q3t_dev * c, int n, int n_past) {
     gemv(c, h, 1);
 }
 
+// y [n][N] = x [n][K] . W^T + bias on the tiled GEMMs (Q8_0: quantised rows on
+// int8 MFMA; F16: the exact VALU GEMM, x rounded to fp16): the GEMV's
+// EPI_BIAS, with the bias as a residual of row stride 0.
+void pf_linear_bias(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, const Slot & bias, float * y) {
+    if (w.type == Q3T_TYPE_Q8_0) {
+        pf_quant(c, x, n, K, nullptr, K, c->bp_q, c->bp_dx);
+        pf_gemm(c, w, N, K, n, y, (const float *) bias.data, 0, c->bp_q, c->bp_dx);
+    } else {
+        pf_gemm_f16(c, w, N, K, n, x, K, false, y, (const float *) bias.data, 0);
+    }
+}
+
+bool text_proj_tiled(const q3t_dev * c, int n) {
+    const char * e = std::getenv("Q3T_PREFILL_MFMA");
+    if (e && e[0] == '0') return false;
+    if (!(e && e[0] == '1') && n < 16) return false;
+    const int te = c->cfg.text_embd_dim, d = c->cfg.hidden_size;
+    const auto ok = [](const Slot & s) { return s.type == Q3T_TYPE_Q8_0 || s.type == Q3T_TYPE_F16; };
+    return ok(c->fc1) && ok(c->fc2) && te % 128 == 0 && d % pf::kTile == 0;
+}
+
+// project_text_tokens (src/tts_transformer.cpp:963-1028) of n ids into the
+// device rows dst [n][d]: text_embd rows -> fc1 + bias -> SiLU -> fc2 + bias.
+// n >= 16 runs the tiled GEMMs, fewer rows the GEMV in chunks of up to 4;
+// rows are independent and both forms keep one numerics contract, so a row's
+// result does not depend on n.  ids are range-checked by the caller.
+int project_rows(q3t_dev * c, const int32_t * tokens, int32_t n, float * dst) {
+    const q3t_config & g = c->cfg;
+    if (!c->text_embd.data || !c->fc1.data || !c->fc1_b.data || !c->fc2.data || !c->fc2_b.data)
+        return fail(c, "text projection tensors missing");
+    if (c->text_embd.type != Q3T_TYPE_F16) return fail(c, "talker.text_embd must be F16");
+    if (n > c->ids_cap) {
+        dev_free(c, c->ids);
+        c->ids = nullptr;
+        if (dev_alloc_t(c, &c->ids, (size_t) n)) return -1;
+        c->ids_cap = n;
+    }
+    if (ensure_stage(c, n)) return -1;
+    const int te = g.text_embd_dim, d = g.hidden_size;
+    HIP_OK(hipMemcpyAsync(c->ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
+    hipLaunchKernelGGL(k_gather_rows, dim3((te + 255) / 256, n), dim3(256), 0, c->stream,
+                       (const uint16_t *) c->text_embd.data, (int64_t) te, c->ids, n, c->stage);
+    if (text_proj_tiled(c, n)) {
+        if (n > c->bp_rows) {
+            for (void * p : {(void *) c->bp_q, (void *) c->bp_dx, (void *) c->bp_h}) dev_free(c, p);
+            c->bp_q = nullptr; c->bp_dx = nullptr; c->bp_h = nullptr; c->bp_rows = 0;
+            if (dev_alloc_t(c, &c->bp_q, (size_t) n * te) || dev_alloc_t(c, &c->bp_dx, (size_t) n * (te / kQK)) ||
+                dev_alloc_t(c, &c->bp_h, (size_t) n * te))
+                return -1;
+            c->bp_rows = n;
+        }
+        pf_linear_bias(c, c->fc1, te, te, n, c->stage, c->fc1_b, c->bp_h);
+        const size_t cnt = (size_t) n * te;
+        hipLaunchKernelGGL(k_silu_rows, dim3((unsigned) std::min<size_t>((cnt + 255) / 256, 4096)), dim3(256), 0,
+                           c->stream, c->bp_h, cnt);
+        pf_linear_bias(c, c->fc2, d, te, n, c->bp_h, c->fc2_b, dst);
+    } else {
+        for (int t0 = 0; t0 < n;) {
+            const int left = n - t0;
+            const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
+            GemvSpec a{};
+            a.w = weight_of(c->fc1); a.rows = te; a.K = te; a.x = c->stage + (size_t) t0 * te; a.x_stride = te;
+            a.y = c->tp_a; a.y_stride = te; a.bias = (const float *) c->fc1_b.data; a.epi = EPI_BIAS_SILU;
+            a.no_done = true;
+            gemv(c, a, nt);
+            GemvSpec b{};
+            b.w = weight_of(c->fc2); b.rows = d; b.K = te; b.x = c->tp_a; b.x_stride = te;
+            b.y = dst + (size_t) t0 * d; b.y_stride = d; b.bias = (const float *) c->fc2_b.data; b.epi = EPI_BIAS;
+            b.no_done = true;
+            gemv(c, b, nt);
+            t0 += nt;
+        }
+    }
+    HIP_OK(hipGetLastError());
+    return 0;
+}
+
+// Room for m projected rows, r assembled rows and f reference frames.
+int ensure_build(q3t_dev * c, int m, int r, int f) {
+    const int d = c->cfg.hidden_size;
+    if (m + r > c->bp_out_rows) {
+        for (void * p : {(void *) c->bp_proj, (void *) c->bp_out, (void *) c->bp_spec}) dev_free(c, p);
+        c->bp_proj = nullptr; c->bp_out = nullptr; c->bp_spec = nullptr; c->bp_out_rows = 0;
+        const int cap = std::max(m + r, 64);
+        if (dev_alloc_t(c, &c->bp_proj, (size_t) cap * d) || dev_alloc_t(c, &c->bp_out, (size_t) cap * d) ||
+            dev_alloc_t(c, &c->bp_spec, (size_t) cap))
+            return -1;
+        c->bp_out_rows = cap;
+    }
+    if (!c->bp_spk && dev_alloc_t(c, &c->bp_spk, (size_t) d)) return -1;
+    if (f > c->bp_frames_cap) {
+        dev_free(c, c->bp_frames);
+        c->bp_frames = nullptr; c->bp_frames_cap = 0;
+        if (dev_alloc_t(c, &c->bp_frames, (size_t) f * 16)) return -1;
+        c->bp_frames_cap = f;
+    }
+    return 0;
+}
+
+// Projects ids, assembles specs.size() rows and copies them out: rows
+// [0, n_pre) to prefill_out, the next n_trail to trailing_out, the last to
+// pad_out.  frames: ICL reference codes (n_frames x 16) or null.
+int build_rows(q3t_dev * c, const std::vector<int32_t> & ids, const std::vector<RowSpec> & specs,
+               const float * speaker, const int32_t * frames, int32_t n_frames, int32_t n_pre, int32_t n_trail,
+               float * prefill_out, float * trailing_out, float * pad_out) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, m = (int) ids.size(), r = (int) specs.size();
+    if (!c->codec_embd.data || c->codec_embd.type != Q3T_TYPE_F16) return fail(c, "talker.codec_embd must be F16");
+    for (int i = 0; frames && i < g.n_codebooks - 1; ++i)
+        if (!c->cp_embd[i].data || c->cp_embd[i].type != Q3T_TYPE_F16 || c->cp_embd[i].ne0 != d)
+            return fail(c, "code_pred.codec_embd tables must be F16 rows of hidden_size");
+    if (ensure_build(c, m, r, n_frames)) return -1;
+    if (project_rows(c, ids.data(), m, c->bp_proj)) return -1;
+    HIP_OK(hipMemcpyAsync(c->bp_spec, specs.data(), (size_t) r * sizeof(RowSpec), hipMemcpyHostToDevice, c->stream));
+    if (speaker)
+        HIP_OK(hipMemcpyAsync(c->bp_spk, speaker, (size_t) d * 4, hipMemcpyHostToDevice, c->stream));
+    if (n_frames > 0)
+        HIP_OK(hipMemcpyAsync(c->bp_frames, frames, (size_t) n_frames * 16 * 4, hipMemcpyHostToDevice, c->stream));
+    RowTables T{};
+    T.proj = c->bp_proj; T.codec_embd = (const uint16_t *) c->codec_embd.data;
+    for (int i = 0; frames && i < g.n_codebooks - 1; ++i) T.cp_embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    T.speaker = c->bp_spk; T.frames = c->bp_frames; T.n_cb = g.n_codebooks; T.d = d;
+    hipLaunchKernelGGL(k_prefill_rows, dim3((d + 255) / 256, r), dim3(256), 0, c->stream, T,
+                       (const RowSpec *) c->bp_spec, c->bp_out);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpyAsync(prefill_out, c->bp_out, (size_t) n_pre * d * 4, hipMemcpyDeviceToHost, c->stream));
+    if (n_trail > 0)
+        HIP_OK(hipMemcpyAsync(trailing_out, c->bp_out + (size_t) n_pre * d, (size_t) n_trail * d * 4,
+                              hipMemcpyDeviceToHost, c->stream));
+    HIP_OK(hipMemcpyAsync(pad_out, c->bp_out + (size_t) (n_pre + n_trail) * d, (size_t) d * 4, hipMemcpyDeviceToHost,
+                          c->stream));
+    return sync(c);
+}
+
+}  // namespace
+
+extern "C" {
+
 int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, float * hidden_out, float * logits_out) {
     if (!c || !embd) return -1;
     if (n <= 0) return fail(c, "n_tokens must be > 0");
@@ -1349,40 +1497,119 @@ int q3t_dev_text_proj(q3t_dev * c, const int32_t * tokens, int32_t n, float * ou
     if (n <= 0) return 0;
     HIP_OK(hipSetDevice(c->device));
     const q3t_config & g = c->cfg;
-    if (!c->text_embd.data || !c->fc1.data || !c->fc1_b.data || !c->fc2.data || !c->fc2_b.data)
-        return fail(c, "text projection tensors missing");
-    if (c->text_embd.type != Q3T_TYPE_F16) return fail(c, "talker.text_embd must be F16");
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= g.text_vocab) return fail(c, "Embedding token ID out of range");
-    if (n > c->ids_cap) {
-        dev_free(c, c->ids);
-        c->ids = nullptr;
-        if (dev_alloc_t(c, &c->ids, (size_t) n)) return -1;
-        c->ids_cap = n;
-    }
-    if (ensure_stage(c, n)) return -1;
-    FrameState s{};
-    if (set_state(c, s)) return -1;
-    HIP_OK(hipMemcpyAsync(c->ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
-    const int te = g.text_embd_dim, d = g.hidden_size;
-    hipLaunchKernelGGL(k_gather_rows, dim3((te + 255) / 256, n), dim3(256), 0, c->stream,
-                       (const uint16_t *) c->text_embd.data, (int64_t) te, c->ids, n, c->stage);
-    std::vector<float> tmp;
-    for (int t0 = 0; t0 < n;) {
-        const int left = n - t0;
-        const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        GemvSpec a{};
-        a.w = weight_of(c->fc1); a.rows = te; a.K = te; a.x = c->stage + (size_t) t0 * te; a.x_stride = te;
-        a.y = c->tp_a; a.y_stride = te; a.bias = (const float *) c->fc1_b.data; a.epi = EPI_BIAS_SILU;
-        gemv(c, a, nt);
-        GemvSpec b{};
-        b.w = weight_of(c->fc2); b.rows = d; b.K = te; b.x = c->tp_a; b.x_stride = te;
-        b.y = c->tp_b; b.y_stride = d; b.bias = (const float *) c->fc2_b.data; b.epi = EPI_BIAS;
-        gemv(c, b, nt);
-        HIP_OK(hipMemcpyAsync(out + (size_t) t0 * d, c->tp_b, (size_t) nt * d * 4, hipMemcpyDeviceToHost, c->stream));
-        t0 += nt;
-    }
+    if (ensure_build(c, n, 0, 0)) return -1;
+    if (project_rows(c, tokens, n, c->bp_proj)) return -1;
+    HIP_OK(hipMemcpyAsync(out, c->bp_proj, (size_t) n * g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
     return sync(c);
+}
+
+int q3t_dev_build_prefill(q3t_dev * c, const int32_t * text_tokens, int32_t n_tokens, const float * speaker_embd,
+                          int32_t language_id, const int32_t * instruct_tokens, int32_t n_instruct,
+                          float * prefill_out, int32_t * n_prefill_out, float * trailing_out,
+                          int32_t * n_trailing_out, float * tts_pad_out) {
+    if (!c || !n_prefill_out || !n_trailing_out) return -1;
+    if (!text_tokens) return fail(c, "text_tokens is null");
+    if (n_tokens < 4) return fail(c, "Need at least 4 text tokens for prefill");
+    const q3t_config & g = c->cfg;
+    if (!instruct_tokens || n_instruct < 0) n_instruct = 0;
+    const int n_codec_tok = language_id < 0 ? 3 : 4;
+    const int in_len = n_codec_tok + (speaker_embd ? 1 : 0) + 2, ov_len = in_len - 1;
+    const int n_trail = std::max(0, n_tokens - 9);
+    const int n_pre = n_instruct + 3 + ov_len + 1;
+    *n_prefill_out = n_pre;
+    *n_trailing_out = n_trail + 1;
+    if (!prefill_out) return 0;
+    if (!trailing_out || !tts_pad_out) return fail(c, "output buffers are null");
+    HIP_OK(hipSetDevice(c->device));
+    // projected ids: bos, eos, pad, text[0..3], instruct, text[4 .. 4 + n_trail)
+    std::vector<int32_t> ids = {g.tts_bos_id, g.tts_eos_id, g.tts_pad_id, text_tokens[0], text_tokens[1],
+                                text_tokens[2], text_tokens[3]};
+    ids.insert(ids.end(), instruct_tokens, instruct_tokens + n_instruct);
+    ids.insert(ids.end(), text_tokens + 4, text_tokens + 4 + n_trail);
+    for (int32_t t : ids)
+        if (t < 0 || t >= g.text_vocab) return fail(c, "Embedding token ID out of range");
+    std::vector<RowSpec> cin;   // the codec input rows as sources
+    const int32_t think[4] = {language_id < 0 ? g.codec_nothink_id : g.codec_think_id, g.codec_think_bos_id,
+                              language_id, g.codec_think_eos_id};
+    for (int k = 0; k < 4; ++k) {
+        if (language_id < 0 && k == 2) continue;
+        cin.push_back({0, RS_CODEC, think[k], 0, 0});
+    }
+    if (speaker_embd) cin.push_back({0, RS_SPEAKER, 0, 0, 0});
+    cin.push_back({0, RS_CODEC, g.codec_pad_id, 0, 0});
+    cin.push_back({0, RS_CODEC, g.codec_bos_id, 0, 0});
+    for (const RowSpec & r : cin)
+        if (r.a_src == RS_CODEC && (r.a_idx < 0 || r.a_idx >= g.codec_vocab))
+            return fail(c, "Embedding token ID out of range");
+    const int P_BOS = 0, P_EOS = 1, P_PAD = 2, P_ROLE = 3, P_FIRST = 6, P_INSTR = 7, P_TRAIL = 7 + n_instruct;
+    std::vector<RowSpec> sp;
+    for (int i = 0; i < n_instruct; ++i) sp.push_back({RO_COPY, RS_PROJ, P_INSTR + i, 0, 0});
+    for (int i = 0; i < 3; ++i) sp.push_back({RO_COPY, RS_PROJ, P_ROLE + i, 0, 0});
+    for (int t = 0; t < ov_len; ++t)
+        sp.push_back({RO_ADD, RS_PROJ, t == ov_len - 1 ? P_BOS : P_PAD, cin[t].a_src, cin[t].a_idx});
+    sp.push_back({RO_ADD, RS_PROJ, P_FIRST, cin[in_len - 1].a_src, cin[in_len - 1].a_idx});
+    for (int j = 0; j < n_trail; ++j) sp.push_back({RO_COPY, RS_PROJ, P_TRAIL + j, 0, 0});
+    sp.push_back({RO_COPY, RS_PROJ, P_EOS, 0, 0});
+    sp.push_back({RO_COPY, RS_PROJ, P_PAD, 0, 0});
+    return build_rows(c, ids, sp, speaker_embd, nullptr, 0, n_pre, n_trail + 1, prefill_out, trailing_out,
+                      tts_pad_out);
+}
+
+int q3t_dev_build_prefill_icl(q3t_dev * c, const int32_t * text_tokens, int32_t n_tokens,
+                              const int32_t * ref_text_tokens, int32_t n_ref_text, const int32_t * ref_codec_tokens,
+                              int32_t n_ref_frames, const float * speaker_embd, float * prefill_out,
+                              int32_t * n_prefill_out, float * trailing_out, int32_t * n_trailing_out,
+                              float * tts_pad_out) {
+    if (!c || !n_prefill_out || !n_trailing_out) return -1;
+    if (!text_tokens || n_tokens < 4) return fail(c, "ICL: need at least 4 target text tokens");
+    if (!ref_codec_tokens || n_ref_frames < 1) return fail(c, "ICL: need at least 1 reference codec frame");
+    if (!ref_text_tokens || n_ref_text < 0) n_ref_text = 0;
+    const q3t_config & g = c->cfg;
+    // text stream: ref_text[3:-5] ++ target[3:-5] ++ tts_eos
+    std::vector<int32_t> stream;
+    for (int32_t i = 3; i < std::max(3, n_ref_text - 5) && i < n_ref_text; ++i) stream.push_back(ref_text_tokens[i]);
+    for (int32_t i = 3; i < std::max(3, n_tokens - 5) && i < n_tokens; ++i) stream.push_back(text_tokens[i]);
+    stream.push_back(g.tts_eos_id);
+    const int n_text = (int) stream.size(), n_codec = n_ref_frames + 1;
+    const int in_len = 3 + (speaker_embd ? 1 : 0) + 2, ov_len = in_len - 1;
+    const int n_pre = 3 + ov_len + n_codec, n_trail = std::max(0, n_text - n_codec);
+    *n_prefill_out = n_pre;
+    *n_trailing_out = n_trail;
+    if (!prefill_out) return 0;
+    if ((n_trail > 0 && !trailing_out) || !tts_pad_out) return fail(c, "output buffers are null");
+    HIP_OK(hipSetDevice(c->device));
+    std::vector<int32_t> ids = {g.tts_bos_id, g.tts_eos_id, g.tts_pad_id, text_tokens[0], text_tokens[1],
+                                text_tokens[2]};
+    ids.insert(ids.end(), stream.begin(), stream.end());
+    for (int32_t t : ids)
+        if (t < 0 || t >= g.text_vocab) return fail(c, "Embedding token ID out of range");
+    for (int32_t f = 0; f < n_ref_frames; ++f)
+        for (int cb = 0; cb < 16 && cb < g.n_codebooks; ++cb) {
+            const int32_t t = ref_codec_tokens[(size_t) f * 16 + cb];
+            if (t < 0 || t >= (cb == 0 ? g.codec_vocab : g.cp_vocab)) return fail(c, "Embedding token ID out of range");
+        }
+    std::vector<RowSpec> cin = {{0, RS_CODEC, g.codec_nothink_id, 0, 0}, {0, RS_CODEC, g.codec_think_bos_id, 0, 0},
+                                {0, RS_CODEC, g.codec_think_eos_id, 0, 0}};
+    if (speaker_embd) cin.push_back({0, RS_SPEAKER, 0, 0, 0});
+    cin.push_back({0, RS_CODEC, g.codec_pad_id, 0, 0});
+    cin.push_back({0, RS_CODEC, g.codec_bos_id, 0, 0});
+    for (const RowSpec & r : cin)
+        if (r.a_src == RS_CODEC && (r.a_idx < 0 || r.a_idx >= g.codec_vocab))
+            return fail(c, "Embedding token ID out of range");
+    const int P_BOS = 0, P_PAD = 2, P_ROLE = 3, P_STREAM = 6;
+    std::vector<RowSpec> sp;
+    for (int i = 0; i < 3; ++i) sp.push_back({RO_COPY, RS_PROJ, P_ROLE + i, 0, 0});
+    for (int t = 0; t < ov_len; ++t)
+        sp.push_back({RO_ADD, RS_PROJ, t == ov_len - 1 ? P_BOS : P_PAD, cin[t].a_src, cin[t].a_idx});
+    for (int i = 0; i < n_codec; ++i)
+        sp.push_back({RO_ZERO_ADD, RS_PROJ, i < n_text ? P_STREAM + i : P_PAD, i == 0 ? RS_CODEC : RS_FRAME,
+                      i == 0 ? g.codec_bos_id : i - 1});
+    for (int j = 0; j < n_trail; ++j) sp.push_back({RO_COPY, RS_PROJ, P_STREAM + n_codec + j, 0, 0});
+    sp.push_back({RO_COPY, RS_PROJ, P_PAD, 0, 0});
+    return build_rows(c, ids, sp, speaker_embd, ref_codec_tokens, n_ref_frames, n_pre, n_trail, prefill_out,
+                      trailing_out, tts_pad_out);
 }
 
 int q3t_dev_embed_rows(q3t_dev * c, int32_t table, int32_t index, const int32_t * tokens, int32_t n, float * out) {

@@ -779,6 +779,61 @@ __global__ void k_gather_rows(const uint16_t * table, int64_t dim, const int32_t
         out[(size_t) r * dim + e] = h2f(table[(size_t) ids[r] * dim + e]);
 }
 
+// x = silu(x) over count elements (fc1 of the text projection after its
+// bias add: silu_q3t(v + b), the GEMV's EPI_BIAS_SILU, in two steps).
+__global__ void k_silu_rows(float * x, size_t count) {
+    for (size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (size_t) gridDim.x * blockDim.x)
+        x[i] = silu_q3t(x[i]);
+}
+
+// ---------------------------------------------------- prefill row assembly
+// The rows of build_prefill_graph (src/tts_transformer.cpp:1030-1186) and
+// build_prefill_graph_icl (:1188-1472): every output row is one source row,
+// the sum of two (a + b), or the ICL interleave's (0 + a) + b, each an fp32
+// addition in the order the reference's host loops make it.  Sources:
+// projected text rows, talker.codec_embd rows (F16, exact in fp32), the
+// speaker row, or an ICL reference frame's summed embeddings
+// (codec_embd[c0], then + code_pred.codec_embd[cb-1][c_cb] for cb = 1..15 in
+// order, :1348-1367).
+enum RowSrc : int32_t { RS_PROJ = 0, RS_CODEC = 1, RS_SPEAKER = 2, RS_FRAME = 3 };
+enum RowOp : int32_t { RO_COPY = 0, RO_ADD = 1, RO_ZERO_ADD = 2 };
+struct RowSpec {
+    int32_t op, a_src, a_idx, b_src, b_idx;
+};
+struct RowTables {
+    const float * proj;              // projected text rows [m][d]
+    const uint16_t * codec_embd;     // [codec_vocab][d]
+    const uint16_t * cp_embd[15];    // [cp_vocab][d] each
+    const float * speaker;           // [d]
+    const int32_t * frames;          // reference codes [n_frames][16]
+    int32_t n_cb, d;
+};
+
+__device__ __forceinline__ float row_src(const RowTables & T, int src, int idx, int h) {
+    if (src == RS_PROJ) return T.proj[(size_t) idx * T.d + h];
+    if (src == RS_CODEC) return h2f(T.codec_embd[(size_t) idx * T.d + h]);
+    if (src == RS_SPEAKER) return T.speaker[h];
+    const int32_t * f = T.frames + (size_t) idx * 16;
+    float r = h2f(T.codec_embd[(size_t) f[0] * T.d + h]);
+    for (int cb = 1; cb < 16 && cb < T.n_cb; ++cb) r = r + h2f(T.cp_embd[cb - 1][(size_t) f[cb] * T.d + h]);
+    return r;
+}
+
+// Block (x, row): out[row] from specs[row].  Every index was range-checked on
+// the host.
+__global__ void k_prefill_rows(RowTables T, const RowSpec * specs, float * out) {
+    const RowSpec s = specs[blockIdx.y];
+    for (int h = (int) (blockIdx.x * blockDim.x + threadIdx.x); h < T.d; h += (int) (gridDim.x * blockDim.x)) {
+        const float a = row_src(T, s.a_src, s.a_idx, h);
+        float o = a;
+        if (s.op != RO_COPY) {
+            const float b = row_src(T, s.b_src, s.b_idx, h);
+            o = s.op == RO_ADD ? a + b : (0.0f + a) + b;
+        }
+        out[(size_t) blockIdx.y * T.d + h] = o;
+    }
+}
+
 }  // namespace q3t
 
 #include "q3t_gemv_reg.h"

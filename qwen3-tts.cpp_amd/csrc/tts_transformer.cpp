@@ -251,52 +251,20 @@ bool TTSTransformer::build_prefill_graph(const int32_t * text_tokens, int32_t n_
                                          int32_t language_id, std::vector<float> & prefill_embd,
                                          std::vector<float> & trailing_text_hidden, std::vector<float> & tts_pad_embed,
                                          const int32_t * instruct_tokens, int32_t n_instruct) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
     if (!text_tokens) { error_msg_ = "text_tokens is null"; return false; }
     if (n_tokens < 4) { error_msg_ = "Need at least 4 text tokens for prefill"; return false; }
-    const tts_transformer_config & cfg = config_;
-    const int32_t d = cfg.hidden_size;
-    int32_t special[3] = {cfg.tts_bos_token_id, cfg.tts_eos_token_id, cfg.tts_pad_token_id};
-    std::vector<float> sp, role, first, codec_rows, tail_rows;
-    if (!project_text_tokens(special, 3, sp) || !project_text_tokens(text_tokens, 3, role)) return false;
-    const float * bos_e = sp.data();
-    const float * eos_e = sp.data() + d;
-    tts_pad_embed.assign(sp.begin() + 2 * d, sp.begin() + 3 * d);
-    std::vector<int32_t> codec_tok;
-    if (language_id < 0) codec_tok = {cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id};
-    else codec_tok = {cfg.codec_think_id, cfg.codec_think_bos_id, language_id, cfg.codec_think_eos_id};
-    int32_t tail_tok[2] = {cfg.codec_pad_id, cfg.codec_bos_id};
-    if (!lookup_rows(0, 0, codec_tok.data(), (int32_t) codec_tok.size(), codec_rows) ||
-        !lookup_rows(0, 0, tail_tok, 2, tail_rows))
+    const int32_t d = config_.hidden_size;
+    int32_t n_pre = 0, n_trail = 0;
+    if (!dev_ok(q3t_dev_build_prefill(dev_, text_tokens, n_tokens, speaker_embd, language_id, instruct_tokens,
+                                      n_instruct, nullptr, &n_pre, nullptr, &n_trail, nullptr)))
         return false;
-    std::vector<float> cin = codec_rows;
-    if (speaker_embd) cin.insert(cin.end(), speaker_embd, speaker_embd + d);
-    cin.insert(cin.end(), tail_rows.begin(), tail_rows.end());
-    const int32_t in_len = (int32_t) (cin.size() / d);
-    const int32_t ov_len = in_len - 1;
-    if (!project_text_tokens(text_tokens + 3, 1, first)) return false;
-    std::vector<float> instr;
-    if (instruct_tokens && n_instruct > 0) {
-        if (!project_text_tokens(instruct_tokens, n_instruct, instr)) return false;
-    } else {
-        n_instruct = 0;
-    }
-    const int32_t plen = n_instruct + 3 + ov_len + 1;
-    prefill_embd.assign((size_t) plen * d, 0.0f);
-    std::copy(instr.begin(), instr.end(), prefill_embd.begin());
-    std::copy(role.begin(), role.end(), prefill_embd.begin() + (size_t) n_instruct * d);
-    for (int32_t t = 0; t < ov_len; ++t) {
-        const float * ov = (t == ov_len - 1) ? bos_e : tts_pad_embed.data();
-        float * dst = prefill_embd.data() + (size_t) (n_instruct + 3 + t) * d;
-        for (int32_t h = 0; h < d; ++h) dst[h] = ov[h] + cin[(size_t) t * d + h];
-    }
-    float * last = prefill_embd.data() + (size_t) (plen - 1) * d;
-    for (int32_t h = 0; h < d; ++h) last[h] = first[h] + cin[(size_t) (in_len - 1) * d + h];
-    const int32_t n_trail = std::max(0, n_tokens - 9);
-    std::vector<float> tr;
-    if (n_trail > 0 && !project_text_tokens(text_tokens + 4, n_trail, tr)) return false;
-    trailing_text_hidden = tr;
-    trailing_text_hidden.insert(trailing_text_hidden.end(), eos_e, eos_e + d);
-    return true;
+    prefill_embd.resize((size_t) n_pre * d);
+    trailing_text_hidden.resize((size_t) n_trail * d);
+    tts_pad_embed.resize(d);
+    return dev_ok(q3t_dev_build_prefill(dev_, text_tokens, n_tokens, speaker_embd, language_id, instruct_tokens,
+                                        n_instruct, prefill_embd.data(), &n_pre, trailing_text_hidden.data(), &n_trail,
+                                        tts_pad_embed.data()));
 }
 
 bool TTSTransformer::build_prefill_graph_icl(const int32_t * text_tokens, int32_t n_tokens,
@@ -305,69 +273,20 @@ bool TTSTransformer::build_prefill_graph_icl(const int32_t * text_tokens, int32_
                                              const float * speaker_embd, std::vector<float> & prefill_embd,
                                              std::vector<float> & trailing_text_hidden,
                                              std::vector<float> & tts_pad_embed) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
     if (!text_tokens || n_tokens < 4) { error_msg_ = "ICL: need at least 4 target text tokens"; return false; }
     if (!ref_codec_tokens || n_ref_frames < 1) { error_msg_ = "ICL: need at least 1 reference codec frame"; return false; }
-    const tts_transformer_config & cfg = config_;
-    const int32_t d = cfg.hidden_size;
-    int32_t special[3] = {cfg.tts_bos_token_id, cfg.tts_eos_token_id, cfg.tts_pad_token_id};
-    std::vector<float> sp, role, codec_rows, tail_rows;
-    if (!project_text_tokens(special, 3, sp) || !project_text_tokens(text_tokens, 3, role)) return false;
-    const float * bos_e = sp.data();
-    tts_pad_embed.assign(sp.begin() + 2 * d, sp.begin() + 3 * d);
-    // ICL prefix has no language token
-    int32_t codec_tok[3] = {cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id};
-    int32_t tail_tok[2] = {cfg.codec_pad_id, cfg.codec_bos_id};
-    if (!lookup_rows(0, 0, codec_tok, 3, codec_rows) || !lookup_rows(0, 0, tail_tok, 2, tail_rows)) return false;
-    std::vector<float> cin = codec_rows;
-    if (speaker_embd) cin.insert(cin.end(), speaker_embd, speaker_embd + d);
-    cin.insert(cin.end(), tail_rows.begin(), tail_rows.end());
-    const int32_t ov_len = (int32_t) (cin.size() / d) - 1;
-    prefill_embd.assign((size_t) (3 + ov_len) * d, 0.0f);
-    std::copy(role.begin(), role.end(), prefill_embd.begin());
-    for (int32_t t = 0; t < ov_len; ++t) {
-        const float * ov = (t == ov_len - 1) ? bos_e : tts_pad_embed.data();
-        float * dst = prefill_embd.data() + (size_t) (3 + t) * d;
-        for (int32_t h = 0; h < d; ++h) dst[h] = ov[h] + cin[(size_t) t * d + h];
-    }
-    // text stream: ref_text[3:-5] ++ target[3:-5] ++ tts_eos
-    std::vector<int32_t> text;
-    const int32_t r_end = std::max(3, n_ref_text - 5);
-    for (int32_t i = 3; i < r_end && i < n_ref_text; ++i) text.push_back(ref_text_tokens[i]);
-    const int32_t t_end = std::max(3, n_tokens - 5);
-    for (int32_t i = 3; i < t_end && i < n_tokens; ++i) text.push_back(text_tokens[i]);
-    text.push_back(cfg.tts_eos_token_id);
-    // codec stream: codec_bos, then each reference frame's summed embeddings
-    const int32_t n_codec = n_ref_frames + 1;
-    std::vector<float> codec((size_t) n_codec * d, 0.0f), row;
-    int32_t bos = cfg.codec_bos_id;
-    if (!lookup_rows(0, 0, &bos, 1, row)) return false;
-    std::copy(row.begin(), row.end(), codec.begin());
-    for (int32_t f = 0; f < n_ref_frames; ++f) {
-        float * dst = codec.data() + (size_t) (f + 1) * d;
-        int32_t c0 = ref_codec_tokens[(size_t) f * 16];
-        if (!lookup_rows(0, 0, &c0, 1, row)) return false;
-        std::copy(row.begin(), row.end(), dst);
-        for (int32_t cb = 1; cb < 16 && cb < cfg.n_codebooks; ++cb) {
-            int32_t tok = ref_codec_tokens[(size_t) f * 16 + cb];
-            if (!lookup_rows(1, cb - 1, &tok, 1, row)) return false;
-            for (int32_t h = 0; h < d; ++h) dst[h] += row[h];
-        }
-    }
-    const int32_t n_text = (int32_t) text.size();
-    std::vector<float> tp;
-    if (!project_text_tokens(text.data(), n_text, tp)) return false;
-    std::vector<float> icl((size_t) n_codec * d, 0.0f);
-    for (int32_t i = 0; i < n_codec; ++i) {
-        float * dst = icl.data() + (size_t) i * d;
-        const float * trow = i < n_text ? tp.data() + (size_t) i * d : tts_pad_embed.data();
-        for (int32_t h = 0; h < d; ++h) dst[h] += trow[h];
-        const float * crow = codec.data() + (size_t) i * d;
-        for (int32_t h = 0; h < d; ++h) dst[h] += crow[h];
-    }
-    prefill_embd.insert(prefill_embd.end(), icl.begin(), icl.end());
-    trailing_text_hidden.clear();
-    if (n_text > n_codec) trailing_text_hidden.assign(tp.begin() + (size_t) n_codec * d, tp.end());
-    return true;
+    const int32_t d = config_.hidden_size;
+    int32_t n_pre = 0, n_trail = 0;
+    if (!dev_ok(q3t_dev_build_prefill_icl(dev_, text_tokens, n_tokens, ref_text_tokens, n_ref_text, ref_codec_tokens,
+                                          n_ref_frames, speaker_embd, nullptr, &n_pre, nullptr, &n_trail, nullptr)))
+        return false;
+    prefill_embd.resize((size_t) n_pre * d);
+    trailing_text_hidden.resize((size_t) n_trail * d);
+    tts_pad_embed.resize(d);
+    return dev_ok(q3t_dev_build_prefill_icl(dev_, text_tokens, n_tokens, ref_text_tokens, n_ref_text,
+                                            ref_codec_tokens, n_ref_frames, speaker_embd, prefill_embd.data(), &n_pre,
+                                            trailing_text_hidden.data(), &n_trail, tts_pad_embed.data()));
 }
 
 bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::vector<float> & trailing,

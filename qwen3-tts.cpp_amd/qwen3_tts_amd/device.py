@@ -19,7 +19,8 @@ EXPORTS = [
     "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
-    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_frames_begin",
+    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_build_prefill",
+    "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
     "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
     "q3t_dev_streams_begin", "q3t_dev_streams_run", "q3t_dev_sync", "q3t_dev_time_kernel",
 ]
@@ -64,6 +65,9 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
         lib.q3t_dev_text_proj.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_embed_rows.argtypes = [vp, i32, i32, vp, i32, f32p]
+        pi32 = ctypes.POINTER(i32)
+        lib.q3t_dev_build_prefill.argtypes = [vp, vp, i32, f32p, i32, vp, i32, f32p, pi32, f32p, pi32, f32p]
+        lib.q3t_dev_build_prefill_icl.argtypes = [vp, vp, i32, vp, i32, vp, i32, f32p, f32p, pi32, f32p, pi32, f32p]
         lib.q3t_dev_frames_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
         lib.q3t_dev_frames_run.argtypes = [vp, i32, vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
         lib.q3t_dev_sync.argtypes = [vp]
@@ -183,6 +187,42 @@ class Device:
         out = np.empty((len(tokens), dim), np.float32)
         self._check(self.lib.q3t_dev_embed_rows(self.h, table, index, _p(tokens), len(tokens), _p(out)), "embed_rows")
         return out
+
+    def build_prefill(self, text, speaker=None, language_id=2050, instruct=None):
+        """q3t_dev_build_prefill: (prefill [n][d], trailing [m][d], tts_pad [d])."""
+        text = np.ascontiguousarray(text, dtype=np.int32)
+        spk = None if speaker is None else np.ascontiguousarray(speaker, dtype=np.float32).reshape(-1)
+        instr = None if instruct is None or len(instruct) == 0 else np.ascontiguousarray(instruct, dtype=np.int32)
+        ni = 0 if instr is None else len(instr)
+        npre, ntr = ctypes.c_int32(), ctypes.c_int32()
+        args = (_p(text), len(text), _p(spk), int(language_id), _p(instr), ni)
+        self._check(self.lib.q3t_dev_build_prefill(self.h, *args, None, ctypes.byref(npre), None, ctypes.byref(ntr),
+                                                   None), "build_prefill")
+        d = self.cfg.hidden_size
+        pre = np.empty((npre.value, d), np.float32)
+        trail = np.empty((ntr.value, d), np.float32)
+        pad = np.empty(d, np.float32)
+        self._check(self.lib.q3t_dev_build_prefill(self.h, *args, _p(pre), ctypes.byref(npre), _p(trail),
+                                                   ctypes.byref(ntr), _p(pad)), "build_prefill")
+        return pre, trail, pad
+
+    def build_prefill_icl(self, text, ref_text, ref_codes, speaker=None):
+        """q3t_dev_build_prefill_icl: (prefill, trailing, tts_pad); ref_codes [frames][16]."""
+        text = np.ascontiguousarray(text, dtype=np.int32)
+        ref_text = np.ascontiguousarray(ref_text, dtype=np.int32)
+        ref_codes = np.ascontiguousarray(ref_codes, dtype=np.int32)
+        spk = None if speaker is None else np.ascontiguousarray(speaker, dtype=np.float32).reshape(-1)
+        npre, ntr = ctypes.c_int32(), ctypes.c_int32()
+        args = (_p(text), len(text), _p(ref_text), len(ref_text), _p(ref_codes), ref_codes.shape[0], _p(spk))
+        self._check(self.lib.q3t_dev_build_prefill_icl(self.h, *args, None, ctypes.byref(npre), None,
+                                                       ctypes.byref(ntr), None), "build_prefill_icl")
+        d = self.cfg.hidden_size
+        pre = np.empty((npre.value, d), np.float32)
+        trail = np.empty((ntr.value, d), np.float32)
+        pad = np.empty(d, np.float32)
+        self._check(self.lib.q3t_dev_build_prefill_icl(self.h, *args, _p(pre), ctypes.byref(npre), _p(trail),
+                                                       ctypes.byref(ntr), _p(pad)), "build_prefill_icl")
+        return pre, trail, pad
 
     # -- frame loop
     def frames_begin(self, trailing, tts_pad, n_past, max_len, repetition_penalty=1.05, temperature=0.0, top_k=0,

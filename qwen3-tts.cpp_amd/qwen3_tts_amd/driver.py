@@ -17,38 +17,12 @@ class GenerateError(RuntimeError):
 
 
 def build_prefill(dev, cfg, text, speaker=None, language_id=2050, instruct=None):
-    """build_prefill_graph (src/tts_transformer.cpp:1030-1186) on the device
-    text projection and embedding gathers.  Returns (prefill [n][d],
-    trailing [m][d], tts_pad [d])."""
-    text = np.asarray(text, np.int32)
+    """build_prefill_graph (src/tts_transformer.cpp:1030-1186) in one device
+    call (q3t_dev_build_prefill).  Returns (prefill [n][d], trailing [m][d],
+    tts_pad [d])."""
     if len(text) < 4:
         raise GenerateError("Need at least 4 text tokens for prefill")
-    sp = dev.text_proj([cfg.tts_bos_id, cfg.tts_eos_id, cfg.tts_pad_id])
-    bos_e, eos_e, pad_e = sp[0], sp[1], sp[2]
-    role = dev.text_proj(text[:3])
-    if language_id < 0:
-        codec_tok = [cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id]
-    else:
-        codec_tok = [cfg.codec_think_id, cfg.codec_think_bos_id, language_id, cfg.codec_think_eos_id]
-    rows = [dev.embed_rows(0, 0, codec_tok)]
-    if speaker is not None:
-        rows.append(np.asarray(speaker, np.float32).reshape(1, -1))
-    rows.append(dev.embed_rows(0, 0, [cfg.codec_pad_id, cfg.codec_bos_id]))
-    cin = np.concatenate(rows, axis=0)
-    ov_len = cin.shape[0] - 1
-    overlay = np.stack([bos_e if t == ov_len - 1 else pad_e for t in range(ov_len)])
-    codec_plus = (overlay + cin[:ov_len]).astype(np.float32)
-    first = dev.text_proj(text[3:4])[0]
-    last = (first + cin[-1]).astype(np.float32)
-    parts = []
-    if instruct is not None and len(instruct) > 0:
-        parts.append(dev.text_proj(instruct))
-    parts += [role, codec_plus, last[None]]
-    prefill = np.concatenate(parts, axis=0).astype(np.float32)
-    n_trail = max(0, len(text) - 9)
-    trail = [dev.text_proj(text[4:4 + n_trail])] if n_trail > 0 else []
-    trailing = np.concatenate(trail + [eos_e[None]], axis=0).astype(np.float32)
-    return prefill, trailing, pad_e.astype(np.float32)
+    return dev.build_prefill(text, speaker, language_id, instruct)
 
 
 def _rep_loop(frames, state, n_cb):

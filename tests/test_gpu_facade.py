@@ -26,7 +26,8 @@ def icl_rows(o, cfg, text, ref_text, ref_codes, spk):
     bos, eos, pad = o.text_proj(np.array([cfg.tts_bos_id, cfg.tts_eos_id, cfg.tts_pad_id], np.int32))
     role = o.text_proj(text[:3])
     rows = [o.embed_row("codec", 0, t) for t in (cfg.codec_nothink_id, cfg.codec_think_bos_id, cfg.codec_think_eos_id)]
-    rows += [spk] + [o.embed_row("codec", 0, cfg.codec_pad_id), o.embed_row("codec", 0, cfg.codec_bos_id)]
+    rows += ([] if spk is None else [spk]) + [o.embed_row("codec", 0, cfg.codec_pad_id),
+                                             o.embed_row("codec", 0, cfg.codec_bos_id)]
     cin = np.stack(rows).astype(np.float32)
     ov = len(rows) - 1
     over = np.stack([bos if t == ov - 1 else pad for t in range(ov)]) + cin[:ov]
