@@ -504,13 +504,13 @@ __device__ __forceinline__ float key2f(uint32_t k) {
 // LDS scratch of the sampling core for NTH threads.
 template <int NTH>
 struct SampleScratch {
-    uint32_t hist[256];
-    double dsc[NTH];
+    uint32_t hist[4][256];                   // one radix histogram per pass
+    double dw[NTH / 64], dw2[NTH / 64];
     float fv[NTH / 64];
-    int32_t iv[NTH / 64];
-    uint32_t sel[2];
-    int32_t pick[2];
+    int32_t iv[NTH / 64], iv2[NTH / 64];
+    uint32_t uv[NTH / 64];
 };
+constexpr int kMaxSampleVocab = 3072;        // codec vocabulary; the host checks both vocabularies
 
 // Token from prepared logits l[0..V) in LDS (suppression / penalty already
 // applied; `eff` is the EOS bias for the talker, 0 otherwise), following
@@ -539,120 +539,167 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
         __syncthreads();
         return i0;
     }
-    for (int i = t; i < V; i += NTH) l[i] = l[i] / temperature;
-    __syncthreads();
-    if (eff != 0.0f && t == 0) l[eos_id] += eff;
-    __syncthreads();
-    if (top_k > 0 && top_k < V) {
-        // radix select of the top_k-th largest key, 8 bits per pass from the top
-        uint32_t prefix = 0, mask = 0;
-        int remaining = top_k;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = t; i < 256; i += NTH) S.hist[i] = 0;
-            __syncthreads();
-            for (int i = t; i < V; i += NTH) {
-                const uint32_t k = f2key(l[i]);
-                if ((k & mask) == prefix) atomicAdd(&S.hist[(k >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (t < 64) {
-                // The bin holding the remaining-th largest key: the highest b >= 1
-                // with count(bins >= b) >= remaining (else bin 0), and how many of
-                // its keys are still to go.  Wave 0 finds it with a suffix scan,
-                // lane l owning bins 4l .. 4l+3.
-                int h[4], own = 0;
+    // Sampled path.  Thread t keeps the contiguous chunk l[t*C .. t*C+C) in
+    // registers; cross-thread steps are wave reductions plus one barrier each.
+    constexpr int NW = NTH / 64, MAXC = (kMaxSampleVocab + NTH - 1) / NTH;
+    const int lane = t & 63, wave = t >> 6;
+    const int C = (V + NTH - 1) / NTH;
+    float x[MAXC];
+    float lmax = -INFINITY;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) { h[e] = (int) S.hist[4 * t + e]; own += h[e]; }
-                int incl = own;                        // keys in bins of lanes >= t
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const int o = __shfl_down(incl, off);
-                    if (t + off < 64) incl += o;
-                }
-                int above = incl - own, best = -1, best_above = 0;
-#pragma unroll
-                for (int e = 3; e >= 0; --e) {
-                    const int b = 4 * t + e;
-                    if (best < 0 && b >= 1 && above + h[e] >= remaining) { best = b; best_above = above; }
-                    above += h[e];
-                }
-                int bmax = best;
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) bmax = max(bmax, __shfl_xor(bmax, off));
-                if (bmax >= 0 && best == bmax) {
-                    S.sel[0] = (uint32_t) best;
-                    S.sel[1] = (uint32_t) (remaining - best_above);
-                }
-                if (bmax < 0 && t == 0) {
-                    S.sel[0] = 0u;
-                    S.sel[1] = (uint32_t) (remaining - (incl - h[0]));
-                }
-            }
-            __syncthreads();
-            prefix |= S.sel[0] << shift;
-            mask |= 255u << shift;
-            remaining = (int) S.sel[1];
-            __syncthreads();
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = t * C + c;
+        float v = -INFINITY;
+        if (c < C && i < V) {
+            v = l[i] / temperature;
+            if (eff != 0.0f && i == eos_id) v += eff;
         }
-        const float thr = key2f(prefix);
-        for (int i = t; i < V; i += NTH)
-            if (l[i] < thr) l[i] = -INFINITY;
-        __syncthreads();
+        x[c] = v;
+        lmax = fmaxf(lmax, v);
     }
-    float lm = -INFINITY;
-    for (int i = t; i < V; i += NTH) lm = fmaxf(lm, l[i]);
-    lm = wave_max_f(lm);
-    if ((t & 63) == 0) S.fv[t >> 6] = lm;
+    // the maximum survives the top-k filter, so it is taken here
+    lmax = wave_max_f(lmax);
+    if (lane == 0) S.fv[wave] = lmax;
+    const bool topk = top_k > 0 && top_k < V;
+    if (topk)
+        for (int i = t; i < 4 * 256; i += NTH) (&S.hist[0][0])[i] = 0u;
     __syncthreads();
     float mx = S.fv[0];
-    for (int w = 1; w < NTH / 64; ++w) mx = fmaxf(mx, S.fv[w]);
-    __syncthreads();
-    const int C = (V + NTH - 1) / NTH;          // contiguous chunk per thread
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, S.fv[w]);
+    if (topk) {
+        // radix select of the top_k-th largest key, 8 bits per pass from the
+        // top; a pass whose selected bin holds exactly the keys still to go
+        // ends the search with that bin's smallest key
+        uint32_t k[MAXC];
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) k[c] = f2key(x[c]);
+        uint32_t prefix = 0, mask = 0, thr_key = 0;
+        int remaining = top_k;
+        for (int pass = 0; pass < 4; ++pass) {
+            const int shift = 24 - 8 * pass;
+            uint32_t * hist = S.hist[pass];
+#pragma unroll
+            for (int c = 0; c < MAXC; ++c)
+                if (c < C && t * C + c < V && (k[c] & mask) == prefix) atomicAdd(&hist[(k[c] >> shift) & 255u], 1u);
+            __syncthreads();
+            // every wave finds the bin holding the remaining-th largest key: the
+            // highest b >= 1 with count(bins >= b) >= remaining (else bin 0);
+            // lane l owns bins 4l .. 4l+3
+            int h[4], own = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { h[e] = (int) hist[4 * lane + e]; own += h[e]; }
+            int incl = own;                        // keys in bins of lanes >= lane
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int o = __shfl_down(incl, off);
+                if (lane + off < 64) incl += o;
+            }
+            int above = incl - own, best = -1, best_above = 0, best_cnt = 0;
+#pragma unroll
+            for (int e = 3; e >= 0; --e) {
+                const int b = 4 * lane + e;
+                if (best < 0 && b >= 1 && above + h[e] >= remaining) { best = b; best_above = above; best_cnt = h[e]; }
+                above += h[e];
+            }
+            int bmax = best;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) bmax = max(bmax, __shfl_xor(bmax, off));
+            int bin, cnt;
+            if (bmax >= 0) {
+                const int owner = bmax >> 2;
+                bin = bmax;
+                remaining -= __shfl(best_above, owner);
+                cnt = __shfl(best_cnt, owner);
+            } else {
+                bin = 0;
+                remaining -= __shfl(incl, 0) - __shfl(h[0], 0);
+                cnt = __shfl(h[0], 0);
+            }
+            prefix |= (uint32_t) bin << shift;
+            mask |= 255u << shift;
+            if (pass == 3) { thr_key = prefix; break; }
+            if (cnt == remaining) {
+                uint32_t m = 0xffffffffu;
+#pragma unroll
+                for (int c = 0; c < MAXC; ++c)
+                    if (c < C && t * C + c < V && (k[c] & mask) == prefix) m = min(m, k[c]);
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) m = min(m, (uint32_t) __shfl_xor((int) m, off));
+                if (lane == 0) S.uv[wave] = m;
+                __syncthreads();
+                thr_key = S.uv[0];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) thr_key = min(thr_key, S.uv[w]);
+                break;
+            }
+        }
+        const float thr = key2f(thr_key);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c)
+            if (x[c] < thr) x[c] = -INFINITY;
+    }
+    // softmax: exp and the fp64 denominator
     double ls = 0.0;
-    for (int c = 0; c < C; ++c) {
-        const int i = t * C + c;
-        if (i < V) { const float e = expf_q3t(l[i] - mx); l[i] = e; ls += (double) e; }
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        x[c] = c < C ? expf_q3t(x[c] - mx) : 0.0f;
+        ls += (double) x[c];
     }
-    S.dsc[t] = ls;
+    ls = wave_sum_d(ls);
+    if (lane == 0) S.dw[wave] = ls;
     __syncthreads();
-    for (int off = NTH / 2; off > 0; off >>= 1) {
-        if (t < off) S.dsc[t] += S.dsc[t + off];
-        __syncthreads();
-    }
-    const double sum = S.dsc[0];
-    __syncthreads();
+    double sum = S.dw[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) sum += S.dw[w];
+    // fp32 probabilities and the inclusive prefix of the per-thread sums (the CDF)
     double lp = 0.0;
-    for (int c = 0; c < C; ++c) {
-        const int i = t * C + c;
-        if (i < V) { const float p = (float) ((double) l[i] / sum); l[i] = p; lp += (double) p; }
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        x[c] = (float) ((double) x[c] / sum);
+        lp += (double) x[c];
     }
-    // inclusive scan of per-thread sums (Hillis-Steele) for the CDF
-    S.dsc[t] = lp;
+    double incl = lp;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) S.dw2[wave] = incl;
     __syncthreads();
-    for (int off = 1; off < NTH; off <<= 1) {
-        const double v = t >= off ? S.dsc[t - off] : 0.0;
-        __syncthreads();
-        S.dsc[t] += v;
-        __syncthreads();
+    double base = 0.0, total = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        if (w < wave) base += S.dw2[w];
+        total += S.dw2[w];
     }
-    const double total = S.dsc[NTH - 1];
     const double u = philox_uniform(seed, frame, group);
     const double target = u * total;
-    if (t == 0) { S.pick[0] = 0x7fffffff; S.pick[1] = -1; }
-    __syncthreads();
-    double cum = t > 0 ? S.dsc[t - 1] : 0.0;
-    for (int c = 0; c < C; ++c) {
+    // the first index whose running sum passes the target, else the last
+    // index of positive probability
+    double cum = base + (incl - lp);
+    int first = 0x7fffffff, last = -1;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
         const int i = t * C + c;
-        if (i < V && l[i] > 0.0f) {
-            cum += (double) l[i];
-            atomicMax(&S.pick[1], i);
-            if (cum > target) { atomicMin(&S.pick[0], i); break; }
+        if (c < C && i < V && x[c] > 0.0f && first == 0x7fffffff) {
+            cum += (double) x[c];
+            last = i;
+            if (cum > target) first = i;
         }
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        first = min(first, __shfl_xor(first, off));
+        last = max(last, __shfl_xor(last, off));
+    }
+    if (lane == 0) { S.iv[wave] = first; S.iv2[wave] = last; }
     __syncthreads();
-    const int32_t tok = S.pick[0] != 0x7fffffff ? S.pick[0] : (S.pick[1] >= 0 ? S.pick[1] : 0);
+    int pick = S.iv[0], lastp = S.iv2[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) { pick = min(pick, S.iv[w]); lastp = max(lastp, S.iv2[w]); }
     __syncthreads();
-    return tok;
+    return pick != 0x7fffffff ? pick : (lastp >= 0 ? lastp : 0);
 }
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
