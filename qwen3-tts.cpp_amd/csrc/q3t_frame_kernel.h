@@ -267,29 +267,6 @@ __device__ __forceinline__ void load_lds(const float * x, RowsT<NT, K> & v) {
     }
 }
 
-// Plain row [n] of a tagged slot into LDS dst[i] (sampler logits).
-__device__ __forceinline__ void stage_plain(const uint64_t * slot, int n, uint32_t tag, float * dst, bool & dead,
-                                            int32_t * err) {
-    for (int i0 = 0; i0 < n; i0 += kB * kT) {
-        const uint64_t * ptr[kB];
-        int cnt = 0;
-#pragma unroll
-        for (int k = 0; k < kB; ++k) {
-            const int i = i0 + k * kT + (int) threadIdx.x;
-            ptr[k] = slot + (i < n ? i : 0);
-            if (i < n) cnt = k + 1;
-        }
-        float val[kB];
-        twait_batch<kB>(ptr, cnt, tag, val, dead, err);
-#pragma unroll
-        for (int k = 0; k < kB; ++k) {
-            const int i = i0 + k * kT + (int) threadIdx.x;
-            if (i < n) dst[i] = val[k];
-        }
-    }
-    __syncthreads();
-}
-
 // ------------------------------------------------------ cross-lane helpers
 
 // ------------------------------------------------------- input preparation
@@ -1475,9 +1452,23 @@ __device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds 
         }
         return reduce_candidates(v, i, L);
     }
-    stage_plain(logits, A.cp_vocab, tag, L.x, dead, A.err);
-    return sample_core<kT>(L.x, A.cp_vocab, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame,
-                           (uint32_t) group, L.S);
+    // sampled: this thread's contiguous chunk of the logits straight into
+    // registers (the valid loads of a thread form a prefix of the batch)
+    constexpr int MAXC = sample_chunk<kT>();
+    const int V = A.cp_vocab, C = (V + kT - 1) / kT, t = threadIdx.x;
+    const uint64_t * ptr[MAXC];
+    int cnt = 0;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = t * C + c;
+        const bool ok = c < C && i < V;
+        ptr[c] = logits + (ok ? i : 0);
+        if (ok) cnt = c + 1;
+    }
+    float x[MAXC];
+    twait_batch<MAXC>(ptr, cnt, tag, x, dead, A.err);
+    return sample_regs<kT>(x, V, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame, (uint32_t) group,
+                           L.S);
 }
 
 // ------------------------------------------------------------------ layers

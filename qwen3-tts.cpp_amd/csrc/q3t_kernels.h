@@ -512,46 +512,26 @@ struct SampleScratch {
 };
 constexpr int kMaxSampleVocab = 3072;        // codec vocabulary; the host checks both vocabularies
 
-// Token from prepared logits l[0..V) in LDS (suppression / penalty already
-// applied; `eff` is the EOS bias for the talker, 0 otherwise), following
-// sample_or_argmax (src/tts_transformer.cpp:2750-2788) and the talker sampler
-// (:3146-3183): greedy first-index argmax, or temperature, EOS bias, top-k
-// threshold (ties kept), softmax with fp64 denominator, draw against the
-// Philox uniform of (seed, frame, group).  Every thread returns the token.
-// l is overwritten.
 template <int NTH>
-__device__ int32_t sample_core(float * l, int V, float temperature, int top_k, int eos_id, float eff,
-                               uint64_t seed, uint32_t frame, uint32_t group, SampleScratch<NTH> & S) {
-    const int t = threadIdx.x;
-    if (temperature <= 0.0f) {
-        if (eff != 0.0f && t == 0) l[eos_id] += eff;
-        __syncthreads();
-        // empty = (-inf, INT_MAX); ascending scan with strict '>' keeps the first maximum
-        float bv = -INFINITY; int32_t bi = 0x7fffffff;
-        for (int i = t; i < V; i += NTH)
-            if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
-        wave_argmax(bv, bi);
-        if ((t & 63) == 0) { S.fv[t >> 6] = bv; S.iv[t >> 6] = bi; }
-        __syncthreads();
-        float b = S.fv[0]; int32_t i0 = S.iv[0];
-        for (int w = 1; w < NTH / 64; ++w)
-            if (S.fv[w] > b || (S.fv[w] == b && S.iv[w] < i0)) { b = S.fv[w]; i0 = S.iv[w]; }
-        __syncthreads();
-        return i0;
-    }
-    // Sampled path.  Thread t keeps the contiguous chunk l[t*C .. t*C+C) in
-    // registers; cross-thread steps are wave reductions plus one barrier each.
-    constexpr int NW = NTH / 64, MAXC = (kMaxSampleVocab + NTH - 1) / NTH;
-    const int lane = t & 63, wave = t >> 6;
+__host__ __device__ constexpr int sample_chunk() { return (kMaxSampleVocab + NTH - 1) / NTH; }
+
+// The sampled path of sample_core on logits held in registers: thread t owns
+// the contiguous chunk [t*C, t*C + C), C = ceil(V / NTH), in x[0 .. C)
+// (entries at or past V are ignored).  Cross-thread steps are wave
+// reductions plus one workgroup barrier each.  Every thread returns the token.
+template <int NTH>
+__device__ int32_t sample_regs(float (&x)[sample_chunk<NTH>()], int V, float temperature, int top_k, int eos_id,
+                               float eff, uint64_t seed, uint32_t frame, uint32_t group, SampleScratch<NTH> & S) {
+    constexpr int NW = NTH / 64, MAXC = sample_chunk<NTH>();
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int C = (V + NTH - 1) / NTH;
-    float x[MAXC];
     float lmax = -INFINITY;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = t * C + c;
         float v = -INFINITY;
         if (c < C && i < V) {
-            v = l[i] / temperature;
+            v = x[c] / temperature;
             if (eff != 0.0f && i == eos_id) v += eff;
         }
         x[c] = v;
@@ -700,6 +680,41 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
     for (int w = 1; w < NW; ++w) { pick = min(pick, S.iv[w]); lastp = max(lastp, S.iv2[w]); }
     __syncthreads();
     return pick != 0x7fffffff ? pick : (lastp >= 0 ? lastp : 0);
+}
+
+// Token from prepared logits l[0..V) in LDS (suppression / penalty already
+// applied; `eff` is the EOS bias for the talker, 0 otherwise), following
+// sample_or_argmax (src/tts_transformer.cpp:2750-2788) and the talker sampler
+// (:3146-3183): greedy first-index argmax, or temperature, EOS bias, top-k
+// threshold (ties kept), softmax with fp64 denominator, draw against the
+// Philox uniform of (seed, frame, group).  Every thread returns the token.
+// The greedy path adds the EOS bias into l.
+template <int NTH>
+__device__ int32_t sample_core(float * l, int V, float temperature, int top_k, int eos_id, float eff,
+                               uint64_t seed, uint32_t frame, uint32_t group, SampleScratch<NTH> & S) {
+    const int t = threadIdx.x;
+    if (temperature <= 0.0f) {
+        if (eff != 0.0f && t == 0) l[eos_id] += eff;
+        __syncthreads();
+        // empty = (-inf, INT_MAX); ascending scan with strict '>' keeps the first maximum
+        float bv = -INFINITY; int32_t bi = 0x7fffffff;
+        for (int i = t; i < V; i += NTH)
+            if (l[i] > bv || (l[i] == bv && i < bi)) { bv = l[i]; bi = i; }
+        wave_argmax(bv, bi);
+        if ((t & 63) == 0) { S.fv[t >> 6] = bv; S.iv[t >> 6] = bi; }
+        __syncthreads();
+        float b = S.fv[0]; int32_t i0 = S.iv[0];
+        for (int w = 1; w < NTH / 64; ++w)
+            if (S.fv[w] > b || (S.fv[w] == b && S.iv[w] < i0)) { b = S.fv[w]; i0 = S.iv[w]; }
+        __syncthreads();
+        return i0;
+    }
+    constexpr int MAXC = sample_chunk<NTH>();
+    const int C = (V + NTH - 1) / NTH;
+    float x[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) x[c] = c < C && t * C + c < V ? l[t * C + c] : -INFINITY;
+    return sample_regs<NTH>(x, V, temperature, top_k, eos_id, eff, seed, frame, group, S);
 }
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
