@@ -1406,7 +1406,9 @@ __device__ __attribute__((always_inline)) void att_combine(const Args & A, Lds &
 // ------------------------------------------------------------- samplers
 // codebook-0 token from the talker logits (plain memory, written by the
 // previous kernel): suppression window, repetition penalty, EOS bias ramp.
-__device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
+// Out of line, once per frame, so the sampler's registers stay out of the
+// frame program's allocation.
+__device__ __attribute__((noinline)) int32_t sample_cb0(const Args & A, Lds & L, int frame) {
     const SampleParams & P = *A.params;
     const int V = A.codec_vocab;
     if (P.temperature <= 0.0f && frame > 0) {
@@ -1431,6 +1433,32 @@ __device__ int32_t sample_cb0(const Args & A, Lds & L, int frame) {
     return sample_core<kT>(L.x, V, P.temperature, P.top_k, A.eos_id, eff, P.seed, (uint32_t) frame, 0u, L.S);
 }
 
+// The sampled draw of sample_cp, kept out of line: its register arrays
+// would otherwise raise the register pressure of the whole frame program
+// (the greedy decode's phases included).  `dead` is passed through a local of
+// the caller so the caller's own flag stays in a register.
+__device__ __attribute__((noinline)) int32_t sample_cp_draw(const Args & A, Lds & L, const uint64_t * logits,
+                                                             uint32_t tag, int frame, int group, bool & dead) {
+    const SampleParams & P = *A.params;
+    // sampled: this thread's contiguous chunk of the logits straight into
+    // registers (the valid loads of a thread form a prefix of the batch)
+    constexpr int MAXC = sample_chunk<kT>();
+    const int V = A.cp_vocab, C = (V + kT - 1) / kT, t = threadIdx.x;
+    const uint64_t * ptr[MAXC];
+    int cnt = 0;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = t * C + c;
+        const bool ok = c < C && i < V;
+        ptr[c] = logits + (ok ? i : 0);
+        if (ok) cnt = c + 1;
+    }
+    float x[MAXC];
+    twait_batch<MAXC>(ptr, cnt, tag, x, dead, A.err);
+    return sample_regs<kT>(x, V, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame, (uint32_t) group,
+                           L.S);
+}
+
 // code-predictor token of codebook `group` from tagged head logits
 __device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds & L, const uint64_t * logits, uint32_t tag, int frame, int group,
                              bool & dead) {
@@ -1452,23 +1480,10 @@ __device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds 
         }
         return reduce_candidates(v, i, L);
     }
-    // sampled: this thread's contiguous chunk of the logits straight into
-    // registers (the valid loads of a thread form a prefix of the batch)
-    constexpr int MAXC = sample_chunk<kT>();
-    const int V = A.cp_vocab, C = (V + kT - 1) / kT, t = threadIdx.x;
-    const uint64_t * ptr[MAXC];
-    int cnt = 0;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-        const int i = t * C + c;
-        const bool ok = c < C && i < V;
-        ptr[c] = logits + (ok ? i : 0);
-        if (ok) cnt = c + 1;
-    }
-    float x[MAXC];
-    twait_batch<MAXC>(ptr, cnt, tag, x, dead, A.err);
-    return sample_regs<kT>(x, V, P.temperature, P.top_k, A.eos_id, 0.0f, P.seed, (uint32_t) frame, (uint32_t) group,
-                           L.S);
+    bool d2 = dead;
+    const int code = sample_cp_draw(A, L, logits, tag, frame, group, d2);
+    dead = d2;
+    return code;
 }
 
 // ------------------------------------------------------------------ layers

@@ -717,20 +717,21 @@ __device__ int32_t sample_core(float * l, int V, float temperature, int top_k, i
     return sample_regs<NTH>(x, V, temperature, top_k, eos_id, eff, seed, frame, group, S);
 }
 
-__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
-    {
-        const int b = blockIdx.x;
-        a.st += b; a.params += b;
-        a.logits += (size_t) b * a.logits_stream;
-        a.seen += (size_t) b * a.seen_stream;
-        if (a.stage) a.stage += (size_t) b * a.stage_stream;
-        if (a.codes_out) a.codes_out += (size_t) b * a.codes_stream;
-        if (a.hidden) a.hidden += (size_t) b * a.hidden_stream;
-        if (a.trailing) a.trailing += (size_t) b * a.trailing_stream;
-        if (a.pad) a.pad += (size_t) b * a.pad_stream;
-        if (a.n_trailing_arr) a.n_trailing = a.n_trailing_arr[b];
-    }
-    FrameState * st = a.st;
+// The argument block is never modified: its table of code-predictor
+// embeddings is indexed by a runtime group, and a modified copy would be
+// moved to scratch memory for that.
+__global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleArgs a) {
+    const int b = blockIdx.x;
+    FrameState * st = a.st + b;
+    const SampleParams & P = a.params[b];
+    const float * logits = a.logits + (size_t) b * a.logits_stream;
+    uint8_t * seen = a.seen + (size_t) b * a.seen_stream;
+    float * stage = a.stage ? a.stage + (size_t) b * a.stage_stream : nullptr;
+    int32_t * codes_out = a.codes_out ? a.codes_out + (size_t) b * a.codes_stream : nullptr;
+    const float * hidden = a.hidden ? a.hidden + (size_t) b * a.hidden_stream : nullptr;
+    const float * trailing = a.trailing ? a.trailing + (size_t) b * a.trailing_stream : nullptr;
+    const float * pad = a.pad ? a.pad + (size_t) b * a.pad_stream : nullptr;
+    const int32_t n_trailing = a.n_trailing_arr ? a.n_trailing_arr[b] : a.n_trailing;
     __shared__ int32_t s_frame;
     if (threadIdx.x == 0) {
         int32_t f = st->frame;
@@ -746,13 +747,12 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     __shared__ float l[kMaxVocab];
     __shared__ SampleScratch<kSampleThreads> S;
     const int t = threadIdx.x, V = a.vocab;
-    const SampleParams & P = *a.params;
     const int frame = s_frame;
     for (int i = t; i < V; i += kSampleThreads) {
-        float v = a.logits[i];
+        float v = logits[i];
         if (a.mode == 0) {
             if (i >= V - 1024 && i != a.eos_id) v = -INFINITY;
-            if (P.rep_penalty != 1.0f && a.seen[i]) v = v > 0.0f ? v / P.rep_penalty : v * P.rep_penalty;
+            if (P.rep_penalty != 1.0f && seen[i]) v = v > 0.0f ? v / P.rep_penalty : v * P.rep_penalty;
         }
         l[i] = v;
     }
@@ -771,27 +771,28 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         if (a.mode == 0) {
             st->codes[0] = tok;
             if (tok == a.eos_id) { st->done = 1; st->eos = 1; }
-            else a.seen[tok] = 1;
+            else seen[tok] = 1;
         } else {
             st->codes[a.group] = tok;
-            if (a.codes_out && a.group == 15) {
-                for (int g = 0; g < 15; ++g) a.codes_out[(size_t) frame * 16 + g] = st->codes[g];
-                a.codes_out[(size_t) frame * 16 + 15] = tok;
+            if (codes_out && a.group == 15) {
+                for (int g = 0; g < 15; ++g) codes_out[(size_t) frame * 16 + g] = st->codes[g];
+                codes_out[(size_t) frame * 16 + 15] = tok;
                 st->n_emitted = frame + 1;
             }
         }
     }
-    if (!a.stage) return;
+    if (!stage) return;
     const size_t d = (size_t) a.d;
     if (a.mode == 0) {
         if (tok == a.eos_id) return;
         for (int e = t; e < a.d; e += kSampleThreads) {
-            a.stage[e] = a.hidden[e];
-            a.stage[d + e] = h2f(a.codec_embd[(size_t) tok * d + e]);
+            stage[e] = hidden[e];
+            stage[d + e] = h2f(a.codec_embd[(size_t) tok * d + e]);
         }
     } else if (a.group < 15) {
-        for (int e = t; e < a.d; e += kSampleThreads) a.stage[e] = h2f(a.cp_embd[a.group - 1][(size_t) tok * d + e]);
-    } else if (a.codes_out) {
+        const uint16_t * row = a.cp_embd[a.group - 1] + (size_t) tok * d;
+        for (int e = t; e < a.d; e += kSampleThreads) stage[e] = h2f(row[e]);
+    } else if (codes_out) {
         // step embedding (src/tts_transformer.cpp:3264-3295), summed in the reference order
         __shared__ int32_t sc[16];
         if (t < 15) sc[t] = st->codes[t];
@@ -800,8 +801,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             float s = h2f(a.codec_embd[(size_t) sc[0] * d + e]);
             for (int g = 1; g < 15; ++g) s = s + h2f(a.cp_embd[g - 1][(size_t) sc[g] * d + e]);
             s = s + h2f(a.cp_embd[14][(size_t) tok * d + e]);
-            const float tr = frame < a.n_trailing ? a.trailing[(size_t) frame * d + e] : a.pad[e];
-            a.stage[e] = s + tr;
+            const float tr = frame < n_trailing ? trailing[(size_t) frame * d + e] : pad[e];
+            stage[e] = s + tr;
         }
     }
 }
