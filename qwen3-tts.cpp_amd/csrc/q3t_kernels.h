@@ -82,20 +82,43 @@ __host__ __device__ constexpr size_t act_red_bytes(int nt) { return (size_t) (nt
 template <int WT, int NT>
 __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char * act) {
     const int K = a.K, t = threadIdx.x;
+    // Elements e = e0 + u*kBlock + t (u < U) of all NT rows are loaded together,
+    // so their loads are in flight at once; for K <= U*kBlock they are loaded
+    // once and kept in registers for both passes.
+    constexpr int U = 4;
+    const bool once = K <= U * kBlock;
+    float v[NT][U];
+    const auto load = [&](int e0) {
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) {
+            const float * x = a.x + (size_t) tok * a.x_stride;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int e = e0 + u * kBlock + t;
+                v[tok][u] = e < K ? x[e] : 0.0f;
+            }
+        }
+    };
+    if (once) load(0);
     // RMSNorm scales of all NT rows with one pair of workgroup barriers; each
-    // row's sum is formed in the order of block_sum_d
+    // thread sums its elements in ascending order, then the order of block_sum_d
     float scales[NT];
 #pragma unroll
     for (int tok = 0; tok < NT; ++tok) scales[tok] = 1.0f;
     if (a.pro == PRO_NORM) {
         double ss[NT];
 #pragma unroll
-        for (int tok = 0; tok < NT; ++tok) {
-            const float * x = a.x + (size_t) tok * a.x_stride;
-            ss[tok] = 0.0;
-            for (int e = t; e < K; e += kBlock) { const float v = x[e]; ss[tok] += (double) (v * v); }
-            ss[tok] = wave_sum_d(ss[tok]);
+        for (int tok = 0; tok < NT; ++tok) ss[tok] = 0.0;
+        for (int e0 = 0; e0 < K; e0 += U * kBlock) {
+            if (!once) load(e0);
+#pragma unroll
+            for (int tok = 0; tok < NT; ++tok)
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (e0 + u * kBlock + t < K) ss[tok] += (double) (v[tok][u] * v[tok][u]);
         }
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) ss[tok] = wave_sum_d(ss[tok]);
         __syncthreads();
         if ((t & 63) == 0)
 #pragma unroll
@@ -108,33 +131,38 @@ __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char
             scales[tok] = 1.0f / sqrtf(mean + a.eps);
         }
     }
-    for (int tok = 0; tok < NT; ++tok) {
-        const float * x = a.x + (size_t) tok * a.x_stride;
-        const float scale = scales[tok];
-        for (int e = t; e < K; e += kBlock) {
-            float v = x[e];
-            if (a.pro == PRO_NORM) {
-                v = v * scale;
-                v = v * a.norm_w[e];
-                if (a.hidden_out && blockIdx.x == 0) a.hidden_out[(size_t) tok * a.hidden_stride + e] = v;
-            }
-            if (WT == W_Q8) {
-                // the 32 consecutive lanes t..t+31 hold one Q8_0 block
-                float am = fabsf(v);
+    for (int e0 = 0; e0 < K; e0 += U * kBlock) {
+        if (!once) load(e0);
 #pragma unroll
-                for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-                const float d = am / 127.0f;
-                const float id = am != 0.0f ? 127.0f / am : 0.0f;
-                int8_t * q = (int8_t *) act;
-                q[(size_t) tok * K + e] = (int8_t) (int) rintf(v * id);
-                if ((t & 31) == 0) {
-                    float * sd = (float *) (act + (size_t) NT * K);
-                    sd[tok * (K / kQK) + e / kQK] = round_f16(d);
+        for (int tok = 0; tok < NT; ++tok) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int e = e0 + u * kBlock + t;
+                if (e >= K) continue;      // K % 32 == 0: a Q8_0 block's 32 lanes agree
+                float y = v[tok][u];
+                if (a.pro == PRO_NORM) {
+                    y = y * scales[tok];
+                    y = y * a.norm_w[e];
+                    if (a.hidden_out && blockIdx.x == 0) a.hidden_out[(size_t) tok * a.hidden_stride + e] = y;
                 }
-            } else if (WT == W_F16) {
-                ((uint16_t *) act)[(size_t) tok * K + e] = f2h(v);
-            } else {
-                ((float *) act)[(size_t) tok * K + e] = v;
+                if (WT == W_Q8) {
+                    // the 32 consecutive lanes t..t+31 hold one Q8_0 block
+                    float am = fabsf(y);
+#pragma unroll
+                    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+                    const float d = am / 127.0f;
+                    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+                    int8_t * q = (int8_t *) act;
+                    q[(size_t) tok * K + e] = (int8_t) (int) rintf(y * id);
+                    if ((t & 31) == 0) {
+                        float * sd = (float *) (act + (size_t) NT * K);
+                        sd[tok * (K / kQK) + e / kQK] = round_f16(d);
+                    }
+                } else if (WT == W_F16) {
+                    ((uint16_t *) act)[(size_t) tok * K + e] = f2h(y);
+                } else {
+                    ((float *) act)[(size_t) tok * K + e] = y;
+                }
             }
         }
     }
