@@ -394,6 +394,16 @@ void gemv(q3t_dev * c, const GemvSpec & s, int nt) {
     // take the LDS path, which reads plain fp32 rows only
     const bool reg = nt <= 2 && reg_path_ok(s.K);
     const bool dual = s.epi == EPI_SWIGLU;
+    // 8 or 16 rows of an F16 head (the multi-stream heads): 1024-thread kernel
+    if (s.w.kind == W_F16 && (nt == 8 || nt == 16) && s.epi == EPI_STORE && s.rows % 8 == 0 && s.K % kQK == 0 &&
+        (nt == 16 ? gemv_mt_lds_bytes<16>(s.K) : gemv_mt_lds_bytes<8>(s.K)) <= 65536) {
+        const dim3 grid(s.rows / 8);
+        if (nt == 16)
+            hipLaunchKernelGGL(k_gemv_mt<16>, grid, dim3(kMtThreads), gemv_mt_lds_bytes<16>(s.K), c->stream, a);
+        else
+            hipLaunchKernelGGL(k_gemv_mt<8>, grid, dim3(kMtThreads), gemv_mt_lds_bytes<8>(s.K), c->stream, a);
+        return;
+    }
     switch (s.w.kind) {
         case W_Q8: dual ? launch_gemv_nt<W_Q8, true>(c, a, nt, reg) : launch_gemv_nt<W_Q8, false>(c, a, nt, reg); break;
         case W_F16: dual ? launch_gemv_nt<W_F16, true>(c, a, nt, reg) : launch_gemv_nt<W_F16, false>(c, a, nt, reg); break;

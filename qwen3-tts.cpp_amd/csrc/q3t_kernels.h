@@ -79,14 +79,14 @@ __host__ __device__ constexpr size_t act_bytes(int nt, int k) {
 // LDS ahead of the activation rows: the RMSNorm partials [NT][4 waves] fp64.
 __host__ __device__ constexpr size_t act_red_bytes(int nt) { return (size_t) (nt < 2 ? 2 : nt) * 4 * 8; }
 
-template <int WT, int NT>
+template <int WT, int NT, int NTH = kBlock>
 __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char * act) {
     const int K = a.K, t = threadIdx.x;
-    // Elements e = e0 + u*kBlock + t (u < U) of all NT rows are loaded together,
-    // so their loads are in flight at once; for K <= U*kBlock they are loaded
+    // Elements e = e0 + u*NTH + t (u < U) of all NT rows are loaded together,
+    // so their loads are in flight at once; for K <= U*NTH they are loaded
     // once and kept in registers for both passes.
-    constexpr int U = 4;
-    const bool once = K <= U * kBlock;
+    constexpr int U = NTH >= 1024 ? 1 : 4, NW = NTH / 64;
+    const bool once = K <= U * NTH;
     float v[NT][U];
     const auto load = [&](int e0) {
 #pragma unroll
@@ -94,7 +94,7 @@ __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char
             const float * x = a.x + (size_t) tok * a.x_stride;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int e = e0 + u * kBlock + t;
+                const int e = e0 + u * NTH + t;
                 v[tok][u] = e < K ? x[e] : 0.0f;
             }
         }
@@ -105,44 +105,87 @@ __device__ __forceinline__ void build_act(const GemvArgs & a, double * red, char
     float scales[NT];
 #pragma unroll
     for (int tok = 0; tok < NT; ++tok) scales[tok] = 1.0f;
-    if (a.pro == PRO_NORM) {
+    if (NTH >= 1024 && NT * 64 <= NTH && a.pro == PRO_NORM) {
+        // a wave per row: wave w sums the squares of row w (lane l: elements
+        // l, l + 64, ... in ascending order, loaded 16 at a time), one wave
+        // reduction per wave instead of NT
+        const int w = t >> 6, l = t & 63;
+        if (w < NT) {
+            const float * xr = a.x + (size_t) w * a.x_stride;
+            double ss = 0.0;
+            for (int e0 = 0; e0 < K; e0 += 16 * 64) {
+                float q[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int e = e0 + 64 * i + l;
+                    q[i] = e < K ? xr[e] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (e0 + 64 * i + l < K) ss += (double) (q[i] * q[i]);
+            }
+            ss = wave_sum_d(ss);
+            // the scale once per row (fp64 division, square root and
+            // reciprocal are long instruction sequences), shared through LDS
+            const float mean = (float) (ss / (double) K);
+            if (l == 0) ((float *) red)[w] = 1.0f / sqrtf(mean + a.eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) scales[tok] = ((const float *) red)[tok];
+    } else if (a.pro == PRO_NORM) {
         double ss[NT];
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) ss[tok] = 0.0;
-        for (int e0 = 0; e0 < K; e0 += U * kBlock) {
+        for (int e0 = 0; e0 < K; e0 += U * NTH) {
             if (!once) load(e0);
 #pragma unroll
             for (int tok = 0; tok < NT; ++tok)
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (e0 + u * kBlock + t < K) ss[tok] += (double) (v[tok][u] * v[tok][u]);
+                    if (e0 + u * NTH + t < K) ss[tok] += (double) (v[tok][u] * v[tok][u]);
         }
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) ss[tok] = wave_sum_d(ss[tok]);
         __syncthreads();
         if ((t & 63) == 0)
 #pragma unroll
-            for (int tok = 0; tok < NT; ++tok) red[tok * 4 + (t >> 6)] = ss[tok];
+            for (int tok = 0; tok < NT; ++tok) red[tok * NW + (t >> 6)] = ss[tok];
         __syncthreads();
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) {
-            const double tot = (red[tok * 4 + 0] + red[tok * 4 + 1]) + (red[tok * 4 + 2] + red[tok * 4 + 3]);
+            const double * rw = red + tok * NW;
+            double tot;
+            if (NW == 4) {
+                tot = (rw[0] + rw[1]) + (rw[2] + rw[3]);
+            } else {
+                tot = rw[0];
+                for (int w = 1; w < NW; ++w) tot += rw[w];
+            }
             const float mean = (float) (tot / (double) K);
             scales[tok] = 1.0f / sqrtf(mean + a.eps);
         }
     }
-    for (int e0 = 0; e0 < K; e0 += U * kBlock) {
+    for (int e0 = 0; e0 < K; e0 += U * NTH) {
         if (!once) load(e0);
+        // the gains are read before any store: a store through hidden_out
+        // could alias them and would force a reload per row
+        float nw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * NTH + t;
+            nw[u] = a.pro == PRO_NORM && e < K ? a.norm_w[e] : 1.0f;
+        }
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int e = e0 + u * kBlock + t;
+                const int e = e0 + u * NTH + t;
                 if (e >= K) continue;      // K % 32 == 0: a Q8_0 block's 32 lanes agree
                 float y = v[tok][u];
                 if (a.pro == PRO_NORM) {
                     y = y * scales[tok];
-                    y = y * a.norm_w[e];
+                    y = y * nw[u];
                     if (a.hidden_out && blockIdx.x == 0) a.hidden_out[(size_t) tok * a.hidden_stride + e] = y;
                 }
                 if (WT == W_Q8) {
@@ -280,6 +323,63 @@ __global__ __launch_bounds__(kBlock) void k_gemv(GemvArgs a) {
     char * act = smem + act_red_bytes(NT);
     build_act<WT, NT>(a, red, act);
     gemv_rows<WT, NT, DUAL>(a, act);
+}
+
+// F16 GEMV of NT rows (the multi-stream heads: 8 or 16 streams) on 1024
+// threads, EPI_STORE.  Block b owns output rows [8b, 8b + 8): wave w takes row
+// pair w % 4 over K quarter w / 4; lane l row 2 (w % 4) + l / 32 and the
+// 8-element chunks (l % 32) + 32 i of its quarter.  Four waves per SIMD hide
+// the latency of the exact fp64 accumulation that k_gemv's one row pair per
+// wave leaves exposed.  A lane's partials are summed over its row's 32 lanes
+// (xor tree), then over the quarters in a fixed order.  Requires rows % 8 == 0
+// and K % 32 == 0 (the host checks).
+constexpr int kMtThreads = 1024;
+template <int NT>
+__host__ __device__ constexpr size_t gemv_mt_lds_bytes(int K) {
+    return (size_t) NT * 16 * 8 + (size_t) 4 * 8 * NT * 8 + (size_t) NT * K * 2;
+}
+template <int NT>
+__global__ __launch_bounds__(kMtThreads) void k_gemv_mt(GemvArgs a) {
+    if (a.done && *a.done) return;
+    extern __shared__ __align__(16) char smem[];
+    double * red = (double *) smem;                  // [NT][16] RMSNorm partials
+    double * part = red + NT * 16;                   // [4 quarters][8 rows][NT]
+    char * act = (char *) (part + 4 * 8 * NT);       // fp16 [NT][K]
+    build_act<W_F16, NT, kMtThreads>(a, red, act);
+    const int K = a.K, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int q = wave >> 2, rl = 2 * (wave & 3) + (lane >> 5), r = blockIdx.x * 8 + rl;
+    const int KQ = K / 4, nch = KQ / 8;              // elements / 8-element chunks per quarter
+    const uint16_t * wrow = (const uint16_t *) a.w + (size_t) r * K + q * KQ;
+    const uint16_t * xq = (const uint16_t *) act + q * KQ;
+    double acc[NT];
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok) acc[tok] = 0.0;
+    for (int c = lane & 31; c < nch; c += 32) {
+        const int4 wv = *(const int4 *) (wrow + c * 8);
+        const uint16_t * wh = (const uint16_t *) &wv;
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) {
+            const int4 xv = *(const int4 *) (xq + (size_t) tok * K + c * 8);
+            const uint16_t * xh = (const uint16_t *) &xv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[tok] += (double) hmul_exact(__builtin_bit_cast(_Float16, wh[j]), __builtin_bit_cast(_Float16, xh[j]));
+        }
+    }
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok)
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) acc[tok] += __shfl_xor(acc[tok], o);
+    if ((lane & 31) == 0)
+#pragma unroll
+        for (int tok = 0; tok < NT; ++tok) part[(q * 8 + rl) * NT + tok] = acc[tok];
+    __syncthreads();
+    if (t < 8 * NT) {
+        const int rr = t / NT, tok = t - rr * NT;
+        const double * p = part + rr * NT + tok;
+        const double v = (p[0] + p[8 * NT]) + (p[16 * NT] + p[24 * NT]);
+        a.y[(size_t) tok * a.y_stride + blockIdx.x * 8 + rr] = (float) v;
+    }
 }
 
 // ------------------------------------------------------------- attention

@@ -112,6 +112,22 @@ def test_streams_single_stream_and_rerun(tiny_q8):
     _run(cfg, dev, o, [dict(seed_prompt=11, n_text=22, max_len=13, temperature=0.8, top_k=20, seed=5)], chunk=13)
 
 
+@pytest.mark.parametrize("n_streams", [16, 12])
+def test_streams_many_heads_rows(tiny_q8, n_streams):
+    """16 streams put all rows of every head GEMV in one launch of the
+    1024-thread multi-row kernel; 12 take one launch of 8 rows and one of 4."""
+    cfg, w, dev, o = tiny_q8
+    specs = []
+    for i in range(n_streams):
+        sp = dict(seed_prompt=30 + i, n_text=6 + 3 * i, max_len=6 + (i % 5))
+        if i % 3 == 0:
+            sp.update(temperature=0.0, top_k=0)
+        else:
+            sp.update(temperature=0.8, top_k=20, seed=100 + i)
+        specs.append(sp)
+    _run(cfg, dev, o, specs, chunk=5)
+
+
 def test_streams_reject_f16_layers():
     cfg = qcfg.tiny()
     w = Weights(cfg, "f16", seed=17, norm_mode="one")
