@@ -77,7 +77,7 @@ def cpu_baseline(cfg, w, text, spk, threads, budget_s):
     t0 = time.perf_counter()
     o.generate(text, spk, max_len=n2, temperature=0.0, eos_bias=-1e4)
     per = max((time.perf_counter() - t0 - base) / (n2 - 1), 1e-6)
-    n3 = int(max(4, min(64, budget_s / per)))
+    n3 = int(max(4, min(320, budget_s / per)))
     t0 = time.perf_counter()
     o.generate(text, spk, max_len=n3, temperature=0.0, eos_bias=-1e4)
     dt = time.perf_counter() - t0 - base
