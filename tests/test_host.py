@@ -54,3 +54,57 @@ def test_tensor_specs_follow_converter_policy():
     assert abs(n_params - 905.7e6) / 905.7e6 < 0.01
     f16 = {n: t for n, t, _ in tensor_specs(cfg, "f16")}
     assert f16["talker.blk.0.ffn_gate.weight"] == F16
+
+
+class _Shape:
+    """Byte size of a tensor from its spec alone (no data generated)."""
+
+    def __init__(self, ttype, ne):
+        n = ne[0] * ne[1]
+        self.nbytes = n * 34 // 32 if ttype == Q8_0 else n * (2 if ttype == F16 else 4)
+
+
+def _frame_bytes():
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "bench.py")
+    spec = importlib.util.spec_from_file_location("q3t_bench", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.frame_bytes
+
+
+def test_frame_bytes_follow_the_unit_figures():
+    """The bench's algorithmic bytes against figures fixed independently of
+    its formula: Q8_0 talker layers 15,728,640 params each at 34/32 bytes
+    (467,927,040 B for 28), the F16 codec head and code-predictor heads
+    (2 bytes a weight), the code-predictor layers read by 15 passes, and
+    114,688 B of talker KV per position (28 layers x 8 heads x 128 x fp16 K+V)."""
+    cfg = config.full_06b()
+    w = {n: (t, ne, _Shape(t, ne)) for n, t, ne in tensor_specs(cfg, "q8_0")}
+    fb = _frame_bytes()
+    assert fb(cfg, w, 201) - fb(cfg, w, 200) == 114_688
+    layer_params = 1024 * 4096 + 2048 * 1024 + 2 * 1024 * 3072 + 3072 * 1024
+    assert layer_params == 15_728_640
+    q8 = layer_params * 34 // 32
+    norms_talker = 28 * (2 * 1024 + 2 * 128) * 4 + 1024 * 4
+    norms_cp = 5 * (2 * 1024 + 2 * 128) * 4 + 1024 * 4
+    weights = 28 * q8 + 3072 * 1024 * 2 + norms_talker + 15 * (5 * q8 + norms_cp) + 15 * 2048 * 1024 * 2
+    kv_row = 114_688 // 28
+    per_frame_kv = 114_688 * 101 + 5 * kv_row * sum(g + 2 for g in range(15)) + 17 * 1024 * 2
+    assert fb(cfg, w, 100) == weights + per_frame_kv
+    # the multi-stream form: weights once, KV per stream
+    assert fb(cfg, w, [100, 100]) == weights + 2 * per_frame_kv
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says why,
+    before touching any device."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
