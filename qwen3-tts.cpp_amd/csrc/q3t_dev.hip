@@ -127,6 +127,10 @@ struct q3t_dev {
     fk::LayerQ8 * fk_layers = nullptr;
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
     int32_t * fk_err = nullptr;
+    // pinned host staging of the single-step calls (talker step): state and
+    // input row in, logits, hidden row and error flag out, so every copy is a
+    // plain DMA and one synchronisation ends the call
+    char * pin = nullptr; size_t pin_bytes = 0;
     fk::Args * fk_args_dev = nullptr;
     bool fk_args_ok = false;           // fk_args_dev holds this context's current arguments
     bool fk_layers_stale = false;      // a layer tensor was uploaded after fk_layers was built
@@ -894,6 +898,7 @@ void q3t_dev_destroy(q3t_dev * c) {
     drop_stream_graph(c);
     for (hipEvent_t e : c->run_ev) if (e) (void) hipEventDestroy(e);
     for (void * p : c->allocs) (void) hipFree(p);
+    if (c->pin) (void) hipHostFree(c->pin);
     if (c->stream) (void) hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1445,17 +1450,38 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     if (check_ready(c)) return -1;
     if (n_past < 0 || n_past + 1 > c->n_ctx) return fail(c, "Context length exceeded");
     const q3t_config & g = c->cfg;
+    const size_t d4 = (size_t) g.hidden_size * 4, v4 = (size_t) g.codec_vocab * 4;
+    // staging layout: [FrameState | pad to 256][embd d][logits vocab][hidden d][err]
+    static_assert(sizeof(FrameState) <= 256, "FrameState outgrew its staging slot");
+    const size_t o_embd = 256, o_logits = o_embd + d4, o_hidden = o_logits + v4, o_err = o_hidden + d4;
+    const size_t need = o_err + 256;
+    if (c->pin_bytes < need) {
+        if (c->pin) (void) hipHostFree(c->pin);
+        c->pin = nullptr; c->pin_bytes = 0;
+        HIP_OK(hipHostMalloc((void **) &c->pin, need, hipHostMallocDefault));
+        c->pin_bytes = need;
+    }
     FrameState s{};
     s.talker_pos = n_past;
-    if (set_state(c, s)) return -1;
-    HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
+    std::memcpy(c->pin, &s, sizeof s);
+    std::memcpy(c->pin + o_embd, embd, d4);
+    HIP_OK(hipMemcpyAsync(c->st, c->pin, sizeof s, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->stage, c->pin + o_embd, d4, hipMemcpyHostToDevice, c->stream));
     bool ran = false;
     if (fk_step(c, 0, fk::MODE_TALKER_STEP, ran)) return -1;
     if (!ran) talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
-    if (logits_out) HIP_OK(hipMemcpyAsync(logits_out, c->logits, (size_t) g.codec_vocab * 4, hipMemcpyDeviceToHost, c->stream));
-    if (hidden_out) HIP_OK(hipMemcpyAsync(hidden_out, c->hidden, (size_t) g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
+    if (logits_out) HIP_OK(hipMemcpyAsync(c->pin + o_logits, c->logits, v4, hipMemcpyDeviceToHost, c->stream));
+    if (hidden_out) HIP_OK(hipMemcpyAsync(c->pin + o_hidden, c->hidden, d4, hipMemcpyDeviceToHost, c->stream));
+    if (ran) HIP_OK(hipMemcpyAsync(c->pin + o_err, c->fk_err, 4, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
-    return ran ? fk_check_err(c) : 0;
+    if (logits_out) std::memcpy(logits_out, c->pin + o_logits, v4);
+    if (hidden_out) std::memcpy(hidden_out, c->pin + o_hidden, d4);
+    if (ran) {
+        int32_t err = 0;
+        std::memcpy(&err, c->pin + o_err, 4);
+        if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+    }
+    return 0;
 }
 
 int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_sampling * sampling, uint32_t frame,
