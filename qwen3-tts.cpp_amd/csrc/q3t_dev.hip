@@ -1113,12 +1113,16 @@ namespace {
 
 // Which tiled path the talker prefill of n tokens takes: 1 = int8 MFMA GEMMs
 // (Q8_0 layers), 2 = exact F16 VALU GEMMs (F16 layers), 0 = the chunked GEMV
-// prefill.  Tiled needs GEMM-friendly widths and n >= 16
-// (Q3T_PREFILL_MFMA=0 disables it, =1 uses it for any n).
+// prefill.  Tiled needs GEMM-friendly widths and, measured on the 0.6B shapes,
+// pays from 9 rows for Q8_0 (10 rows: 5.2 ms against 5.8 ms in 4-row GEMV
+// chunks) and from 40 rows for F16 (its VALU tiles take ~22 ms for any n up to
+// 64, the GEMV ~2.3 ms per 4 rows).  Q3T_PREFILL_MFMA=0 disables it, =1 uses
+// it for any n.
 int tiled_prefill(q3t_dev * c, int n) {
     const char * e = std::getenv("Q3T_PREFILL_MFMA");
     if (e && e[0] == '0') return 0;
-    if (!(e && e[0] == '1') && n < 16) return 0;
+    const bool any = e && e[0] == '1';
+    if (!any && n < 9) return 0;
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
     if (g.head_dim != 128 || d % 128 || qd % 128 || g.ffn_size % 128 || qkvd % pf::kTile || d % pf::kTile ||
@@ -1126,6 +1130,7 @@ int tiled_prefill(q3t_dev * c, int n) {
         return 0;
     const int lt = c->talker[0].qkv.type;
     if (lt != Q3T_TYPE_Q8_0 && lt != Q3T_TYPE_F16) return 0;
+    if (!any && lt == Q3T_TYPE_F16 && n < 40) return 0;
     for (int i = 0; i < g.n_layers; ++i) {
         const LayerDev & L = c->talker[i];
         if (L.qkv.type != lt || L.wo.type != lt || L.wg.type != lt || L.wu.type != lt || L.wd.type != lt) return 0;
