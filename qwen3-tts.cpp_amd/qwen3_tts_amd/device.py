@@ -159,10 +159,12 @@ class Device:
         self._check(self.lib.q3t_dev_prefill(self.h, _p(embd), n, n_past, _p(hid), _p(logits)), "prefill")
         return hid, logits
 
-    def talker_step(self, embd, n_past):
+    def talker_step(self, embd, n_past, want_logits=True, want_hidden=True):
+        """(logits, hidden) of one talker step; an output not wanted is None
+        (the C call then receives NULL for it)."""
         embd = np.ascontiguousarray(embd, dtype=np.float32)
-        logits = np.empty(self.cfg.codec_vocab, np.float32)
-        hid = np.empty(self.cfg.hidden_size, np.float32)
+        logits = np.empty(self.cfg.codec_vocab, np.float32) if want_logits else None
+        hid = np.empty(self.cfg.hidden_size, np.float32) if want_hidden else None
         self._check(self.lib.q3t_dev_talker_step(self.h, _p(embd), n_past, _p(logits), _p(hid)), "talker_step")
         return logits, hid
 

@@ -371,6 +371,31 @@ def _steps_and_code_pred(cfg, wtype, seed, n_prefill, step_path):
         dev.close()
 
 
+def test_talker_step_optional_outputs(step_path):
+    """q3t_dev_talker_step with only the logits or only the hidden row asked
+    for (the other output NULL): the steps still advance the cache, and what
+    is returned equals the oracle's."""
+    cfg = qcfg.tiny()
+    w, dev, o = make(cfg, "q8_0", seed=41, n_ctx=40)
+    try:
+        rng = np.random.default_rng(141)
+        d = cfg.hidden_size
+        embd = (rng.standard_normal((8, d)) * 0.05).astype(np.float32)
+        dev.prefill(embd, 0)
+        o.prefill(embd, 0)
+        for s, (wl, wh) in enumerate([(True, False), (False, True), (False, False), (True, True)]):
+            e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+            lg, hg = dev.talker_step(e, 8 + s, want_logits=wl, want_hidden=wh)
+            lo, ho = o.step(e, 8 + s)
+            assert (lg is not None) == wl and (hg is not None) == wh
+            if wl:
+                assert np.array_equal(lg, lo)
+            if wh:
+                assert np.array_equal(hg, ho)
+    finally:
+        dev.close()
+
+
 def test_steps_and_code_pred_tiny(step_path):
     """Talker steps then greedy and sampled code-predictor calls, each checked
     against the oracle, at the small shapes for both weight types."""
