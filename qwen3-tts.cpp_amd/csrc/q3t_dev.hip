@@ -803,13 +803,6 @@ int fk_step(q3t_dev * c, int32_t frame, int32_t mode, bool & ran) {
     return 0;
 }
 
-// The frame kernel's error flag after a launch has completed.
-int fk_check_err(q3t_dev * c) {
-    int32_t err = 0;
-    HIP_OK(hipMemcpy(&err, c->fk_err, sizeof err, hipMemcpyDeviceToHost));
-    if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
-    return 0;
-}
 
 
 // The captured multi-kernel frame, built on first use.
@@ -1449,6 +1442,24 @@ int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, 
     return sync(c);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The pinned staging buffer of the single-step calls, grown to `need` bytes.
+int ensure_pin(q3t_dev * c, size_t need) {
+    if (c->pin_bytes >= need) return 0;
+    if (c->pin) (void) hipHostFree(c->pin);
+    c->pin = nullptr; c->pin_bytes = 0;
+    HIP_OK(hipHostMalloc((void **) &c->pin, need, hipHostMallocDefault));
+    c->pin_bytes = need;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
 int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float * logits_out, float * hidden_out) {
     if (!c || !embd) return fail(c, "step_embd is null");
     HIP_OK(hipSetDevice(c->device));
@@ -1459,13 +1470,7 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     // staging layout: [FrameState | pad to 256][embd d][logits vocab][hidden d][err]
     static_assert(sizeof(FrameState) <= 256, "FrameState outgrew its staging slot");
     const size_t o_embd = 256, o_logits = o_embd + d4, o_hidden = o_logits + v4, o_err = o_hidden + d4;
-    const size_t need = o_err + 256;
-    if (c->pin_bytes < need) {
-        if (c->pin) (void) hipHostFree(c->pin);
-        c->pin = nullptr; c->pin_bytes = 0;
-        HIP_OK(hipHostMalloc((void **) &c->pin, need, hipHostMallocDefault));
-        c->pin_bytes = need;
-    }
+    if (ensure_pin(c, o_err + 256)) return -1;
     FrameState s{};
     s.talker_pos = n_past;
     std::memcpy(c->pin, &s, sizeof s);
@@ -1497,17 +1502,25 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     if (!c->cpk) return fail(c, "KV cache not reserved");
     const q3t_config & g = c->cfg;
     if (cb0 < 0 || cb0 >= g.codec_vocab) return fail(c, "Embedding token ID out of range");
+    // pinned staging: [SampleParams][FrameState in][hidden d][FrameState out][logits 15 x vocab][err]
+    static_assert(sizeof(SampleParams) <= 256 && sizeof(FrameState) <= 256, "staging slots");
+    const size_t d4 = (size_t) g.hidden_size * 4, l4 = (size_t) (g.n_codebooks - 1) * g.cp_vocab * 4;
+    const size_t o_st = 256, o_hid = 512, o_out = o_hid + d4, o_log = o_out + 256, o_err = o_log + l4;
+    if (ensure_pin(c, o_err + 256)) return -1;
     SampleParams p{};
     p.temperature = sampling ? sampling->temperature : 0.0f;
     p.top_k = sampling ? sampling->top_k : 0;
     p.rep_penalty = 1.0f;
     p.seed = sampling ? sampling->seed : 0;
-    HIP_OK(hipMemcpyAsync(c->params, &p, sizeof p, hipMemcpyHostToDevice, c->stream));
     FrameState s{};
     s.codes[0] = cb0;
     s.frame = (int32_t) frame;
-    if (set_state(c, s)) return -1;
-    HIP_OK(hipMemcpyAsync(c->hidden, hidden, (size_t) g.hidden_size * 4, hipMemcpyHostToDevice, c->stream));
+    std::memcpy(c->pin, &p, sizeof p);
+    std::memcpy(c->pin + o_st, &s, sizeof s);
+    std::memcpy(c->pin + o_hid, hidden, d4);
+    HIP_OK(hipMemcpyAsync(c->params, c->pin, sizeof p, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->st, c->pin + o_st, sizeof s, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(hipMemcpyAsync(c->hidden, c->pin + o_hid, d4, hipMemcpyHostToDevice, c->stream));
     // the persistent kernel needs the talker KV reservation for its tables
     bool ran = false;
     if (c->kc && fk_step(c, (int32_t) frame, fk::MODE_CODE_PRED, ran)) return -1;
@@ -1522,13 +1535,18 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
                            (const uint16_t *) c->codec_embd.data, g.hidden_size, c->stage);
         code_pred_seq(c, false);
     }
-    FrameState r{};
-    HIP_OK(hipMemcpyAsync(&r, c->st, sizeof r, hipMemcpyDeviceToHost, c->stream));
-    if (logits_out)
-        HIP_OK(hipMemcpyAsync(logits_out, c->cp_logits, (size_t) (g.n_codebooks - 1) * g.cp_vocab * 4,
-                              hipMemcpyDeviceToHost, c->stream));
+    HIP_OK(hipMemcpyAsync(c->pin + o_out, c->st, sizeof(FrameState), hipMemcpyDeviceToHost, c->stream));
+    if (logits_out) HIP_OK(hipMemcpyAsync(c->pin + o_log, c->cp_logits, l4, hipMemcpyDeviceToHost, c->stream));
+    if (ran) HIP_OK(hipMemcpyAsync(c->pin + o_err, c->fk_err, 4, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
-    if (ran && fk_check_err(c)) return -1;
+    if (ran) {
+        int32_t err = 0;
+        std::memcpy(&err, c->pin + o_err, 4);
+        if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+    }
+    FrameState r{};
+    std::memcpy(&r, c->pin + o_out, sizeof r);
+    if (logits_out) std::memcpy(logits_out, c->pin + o_log, l4);
     for (int i = 0; i < g.n_codebooks - 1; ++i) codes_out[i] = r.codes[i + 1];
     return 0;
 }
