@@ -378,6 +378,46 @@ void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
     }
 }
 
+// The code predictor's 2-token prefill attends over its F32 Kcur/Vcur, not
+// over the F16 cache (src/tts_transformer.cpp:1999-2012: K, V are permutes of
+// Kcur/Vcur; an F32 src0 in ggml_mul_mat leaves q and P unrounded).  Every
+// product of two fp32 values is exact in fp64; the score's 128-term sum is
+// taken in one fixed order, four sequential 32-dim partials combined as
+// (s0 + s1) + (s2 + s3), the order the device kernels use, so the fp64
+// rounding of the sum is the same everywhere.  P.V adds the exact products in
+// position order.  Rows j of k and v are at k + j * kv_stride + kvh * hd.
+void orc_attention_f32(const float * q, const float * k, const float * v, int64_t kv_stride,
+                       int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_kv, float * out) {
+    const float scale = 1.0f / std::sqrt((float) hd);
+    const int64_t group = n_head / n_kv_head, qtr = hd / 4;
+    std::vector<float> s(n_kv);
+    for (int64_t h = 0; h < n_head; ++h) {
+        const int64_t kvh = h / group;
+        const float * qh = q + h * hd;
+        float mx = -INFINITY;
+        for (int64_t j = 0; j < n_kv; ++j) {
+            const float * kj = k + j * kv_stride + kvh * hd;
+            double part[4];
+            for (int c = 0; c < 4; ++c) {
+                double acc = 0.0;
+                for (int64_t d = c * qtr; d < (c + 1) * qtr; ++d) acc += (double) qh[d] * (double) kj[d];
+                part[c] = acc;
+            }
+            s[j] = (float) ((part[0] + part[1]) + (part[2] + part[3])) * scale;
+            mx = std::max(mx, s[j]);
+        }
+        double sum = 0.0;
+        for (int64_t j = 0; j < n_kv; ++j) { s[j] = orc_expf(s[j] - mx); sum += (double) s[j]; }
+        const float inv = (float) (1.0 / sum);
+        for (int64_t j = 0; j < n_kv; ++j) s[j] = s[j] * inv;
+        for (int64_t d = 0; d < hd; ++d) {
+            double acc = 0.0;
+            for (int64_t j = 0; j < n_kv; ++j) acc += (double) s[j] * (double) v[j * kv_stride + kvh * hd + d];
+            out[h * hd + d] = (float) acc;
+        }
+    }
+}
+
 int32_t orc_argmax(const float * x, int32_t n) {
     int32_t best = 0;
     float bv = x[0];
@@ -500,9 +540,12 @@ void gemv_t(orc_model * m, const Tensor & w, int64_t rows, int64_t k, const floa
     gemv_impl(&m->pool, w.type, w.data, rows, k, x, ntok, y, is_down ? 1 : 0);
 }
 
-// One transformer layer of width d over ntok consecutive positions starting at pos0.
+// One transformer layer of width d over ntok consecutive positions starting at
+// pos0.  f32_attn: the code predictor's prefill, whose attention reads the
+// F32 rows of this call instead of the F16 cache (orc_attention_f32); the
+// cache rows are written either way, for the steps that follow.
 void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float * x, int64_t ntok, int32_t pos0,
-                   KV & kv, int32_t il, const float * rc, const float * rs) {
+                   KV & kv, int32_t il, const float * rc, const float * rs, bool f32_attn = false) {
     const orc_config & c = m->cfg;
     const int64_t hd = c.head_dim, nh = c.n_head, nkv = c.n_kv_head;
     const int64_t qd = nh * hd, kd = nkv * hd, half = hd / 2;
@@ -530,10 +573,17 @@ void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float
             }
         }
     }
-    m->pool.run(ntok, [&](int64_t i0, int64_t i1) {
-        for (int64_t i = i0; i < i1; ++i)
-            orc_attention(q.data() + i * qd, kc, vc, nh, nkv, hd, kv.n_ctx, pos0 + i + 1, o.data() + i * qd, nullptr);
-    });
+    if (f32_attn) {
+        // causal over this call's rows only (the prefill starts at position 0)
+        for (int64_t i = 0; i < ntok; ++i)
+            orc_attention_f32(q.data() + i * qd, k.data(), v.data(), kd, nh, nkv, hd, i + 1, o.data() + i * qd);
+    } else {
+        m->pool.run(ntok, [&](int64_t i0, int64_t i1) {
+            for (int64_t i = i0; i < i1; ++i)
+                orc_attention(q.data() + i * qd, kc, vc, nh, nkv, hd, kv.n_ctx, pos0 + i + 1, o.data() + i * qd,
+                              nullptr);
+        });
+    }
     gemv_t(m, L.wo, d, qd, o.data(), ntok, t.data());
     for (int64_t i = 0; i < ntok * d; ++i) x[i] = t[i] + x[i];
     for (int64_t i = 0; i < ntok; ++i) orc_rmsnorm(x + i * d, fp(L.ffn_norm), d, c.rms_eps, h.data() + i * d);
@@ -649,6 +699,23 @@ int orc_kv_reset(orc_model * m, int32_t n_ctx) {
     return 0;
 }
 
+int orc_kv_write(orc_model * m, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v) {
+    const orc_config & c = m->cfg;
+    if (layer < 0 || layer >= c.n_layers || n_pos < 0 || n_pos > m->kv.n_ctx) {
+        m->err = "kv_write: layer or position range outside the cache";
+        return -1;
+    }
+    const int64_t hd = c.head_dim, nkv = c.n_kv_head;
+    uint16_t * kc = m->kv.k.data() + (size_t) layer * nkv * m->kv.n_ctx * hd;
+    uint16_t * vc = m->kv.v.data() + (size_t) layer * nkv * m->kv.n_ctx * hd;
+    for (int64_t p = 0; p < n_pos; ++p)
+        for (int64_t h = 0; h < nkv; ++h) {
+            std::memcpy(kc + (h * m->kv.n_ctx + p) * hd, k + (p * nkv + h) * hd, hd * sizeof(uint16_t));
+            std::memcpy(vc + (h * m->kv.n_ctx + p) * hd, v + (p * nkv + h) * hd, hd * sizeof(uint16_t));
+        }
+    return 0;
+}
+
 int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
                 float * hidden_out, float * logits_out) {
     return talker_forward(m, embd, n, n_past, hidden_out, logits_out) ? 0 : -1;
@@ -689,7 +756,7 @@ int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,
     project(in.data(), 2, x.data());
     for (int il = 0; il < c.cp_layers; ++il)
         layer_forward(m, m->cp[il], dc, c.cp_ffn, x.data(), 2, 0, m->cp_kv, il, m->cp_rope_cos.data(),
-                      m->cp_rope_sin.data());
+                      m->cp_rope_sin.data(), true);
     orc_rmsnorm(x.data() + dc, fp(m->cp_out_norm), dc, c.rms_eps, hid.data());
     gemv_t(m, m->cp_head[0], V, dc, hid.data(), 1, logits.data());
     if (logits_out) std::memcpy(logits_out, logits.data(), V * sizeof(float));
@@ -799,6 +866,8 @@ int orc_build_prefill(orc_model * m, const int32_t * text, int32_t n_text,
 
 int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const float * trail, int32_t trail_len,
                       const float * pad, const orc_gen_params * p, int32_t * codes_out, float * first_logits_out);
+int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trail, int32_t trail_len,
+               const float * pad_row, const orc_gen_params * p, int32_t * codes_out);
 
 int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
                  const float * speaker, const orc_gen_params * p,
@@ -823,19 +892,31 @@ int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const floa
                       const float * pad_row, const orc_gen_params * p, int32_t * codes_out, float * first_logits_out) {
     const orc_config & c = m->cfg;
     if (p->max_len <= 0) return 0;
-    const int64_t d = c.hidden_size;
-    const int32_t ncb = c.n_codebooks;
-    std::vector<float> pad(pad_row, pad_row + d);
     orc_kv_reset(m, plen + p->max_len + 8);
     std::vector<float> logits(c.codec_vocab);
     if (orc_prefill(m, pre, plen, 0, nullptr, logits.data())) return -1;
     if (first_logits_out) std::memcpy(first_logits_out, logits.data(), logits.size() * sizeof(float));
+    return orc_frames(m, logits.data(), plen, trail, trail_len, pad_row, p, codes_out);
+}
+
+// The frame loop of generate() (src/tts_transformer.cpp:3108-3309) from the
+// current talker cache: `first_logits` and the normed hidden row left by the
+// last prefill or step, the next talker position n_past.
+int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trail, int32_t trail_len,
+               const float * pad_row, const orc_gen_params * p, int32_t * codes_out) {
+    const orc_config & c = m->cfg;
+    if (p->max_len <= 0) return 0;
+    if (m->last_hidden.size() != (size_t) c.hidden_size) { m->err = "frames: no prefill or step has run"; return -1; }
+    if (n_past + p->max_len > m->kv.n_ctx) { m->err = "Context length exceeded"; return -1; }
+    const int64_t d = c.hidden_size;
+    const int32_t ncb = c.n_codebooks;
+    std::vector<float> pad(pad_row, pad_row + d);
+    std::vector<float> logits(first_logits, first_logits + c.codec_vocab);
     std::vector<uint8_t> seen(c.codec_vocab, 0);
     std::vector<int32_t> frame_codes(ncb), cps(ncb - 1);
     std::vector<std::vector<int32_t>> rep_frames;
     int32_t rep_run_len = 0, rep_run_start = 0;
     int32_t n_frames = 0;
-    int32_t n_past = plen;
     std::vector<float> step(d), row(d);
     for (int32_t frame = 0; frame < p->max_len; ++frame) {
         const int32_t tok = orc_sample_cb0(logits.data(), c.codec_vocab, c.codec_eos_id, seen.data(),

@@ -27,6 +27,11 @@
  *   - F16 weight x fp32 activation: the activation is rounded to fp16 (RNE);
  *   - F16 ffn_down is widened to fp32 (ggml_cast) so its activation is NOT
  *     rounded (src/tts_transformer.cpp:1746-1748);
+ *   - attention over the F16 KV cache rounds q and P to fp16 (F16 src0 in
+ *     ggml_mul_mat); the code predictor's 2-token prefill instead attends
+ *     over its F32 Kcur/Vcur (src/tts_transformer.cpp:1999-2012), so q, K, V
+ *     and P stay fp32 there (orc_attention_f32); it still writes the F16
+ *     cache rows the 14 steps read;
  *   - every dot product / sum of squares / softmax denominator accumulates its
  *     (exact) terms in fp64 and rounds to fp32 once.  ggml accumulates in
  *     fp32 SIMD lanes in an order that cannot be reproduced here; fp64
@@ -133,6 +138,13 @@ void orc_rope_table(float theta_base, int64_t head_dim, int64_t n_pos, float * c
 void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
                    int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
                    int64_t n_kv, float * out, float * probs_out);
+/* the code predictor's 2-token prefill attention (src/tts_transformer.cpp:
+ * 1999-2012): q, K and V are the F32 rows of the call, P stays F32; causal
+ * over the first n_kv rows.  k, v: row j of KV head h at
+ * k + j * kv_stride + h * hd.  The score's fp64 sum is taken as four
+ * sequential 32-dim partials combined (s0 + s1) + (s2 + s3). */
+void orc_attention_f32(const float * q, const float * k, const float * v, int64_t kv_stride,
+                       int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_kv, float * out);
 int32_t orc_argmax(const float * x, int32_t n);
 /* talker cb0 sampler (src/tts_transformer.cpp:3109-3184); modifies logits. */
 int32_t orc_sample_cb0(float * logits, int32_t vocab, int32_t eos_id,
@@ -155,6 +167,9 @@ int         orc_set_tensor(orc_model * m, const char * name, int32_t type,
 int         orc_check_complete(orc_model * m);
 const char * orc_last_error(const orc_model * m);
 int         orc_kv_reset(orc_model * m, int32_t n_ctx);
+/* fp16 K/V rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos) of
+ * talker layer `layer` (the layout q3t_dev_kv_write takes). */
+int         orc_kv_write(orc_model * m, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v);
 /* n-token prefill at positions [n_past, n_past+n).  hidden_out: [n][d]
  * (normed), logits_out: last row [codec_vocab] (may be NULL). */
 int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
@@ -188,6 +203,12 @@ int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
 int orc_generate_rows(orc_model * m, const float * prefill, int32_t plen, const float * trailing,
                       int32_t trail_len, const float * pad, const orc_gen_params * p,
                       int32_t * codes_out, float * first_logits_out);
+
+/* the frame loop alone, from the current talker cache: first_logits and the
+ * normed hidden row of the last orc_prefill / orc_step, next position n_past
+ * (what q3t_dev_frames_begin continues from).  Returns frames written. */
+int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trailing,
+               int32_t trail_len, const float * pad, const orc_gen_params * p, int32_t * codes_out);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,8 @@ def lib():
         L.orc_rope_neox.argtypes = [vp, i64, vp, vp]; L.orc_rope_neox.restype = None
         L.orc_rope_table.argtypes = [f32, i64, i64, vp, vp]; L.orc_rope_table.restype = None
         L.orc_attention.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]; L.orc_attention.restype = None
+        L.orc_attention_f32.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp]
+        L.orc_attention_f32.restype = None
         L.orc_argmax.argtypes = [vp, i32]; L.orc_argmax.restype = i32
         L.orc_sample_cb0.argtypes = [vp, i32, i32, vp, f32, f32, i32, f32, i32, i32, u64]
         L.orc_sample_cb0.restype = i32
@@ -74,6 +76,7 @@ def lib():
         L.orc_check_complete.argtypes = [vp]
         L.orc_last_error.argtypes = [vp]; L.orc_last_error.restype = ctypes.c_char_p
         L.orc_kv_reset.argtypes = [vp, i32]
+        L.orc_kv_write.argtypes = [vp, i32, i32, vp, vp]
         L.orc_prefill.argtypes = [vp, vp, i32, i32, vp, vp]
         L.orc_step.argtypes = [vp, vp, i32, vp, vp]
         L.orc_code_pred.argtypes = [vp, vp, i32, f32, i32, u64, u32, vp, vp]
@@ -82,6 +85,7 @@ def lib():
         L.orc_build_prefill.argtypes = [vp, vp, i32, vp, i32, vp, i32, vp, vp, vp, ctypes.POINTER(i32)]
         L.orc_generate.argtypes = [vp, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, i32, vp, vp]
         L.orc_generate_rows.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, vp]
+        L.orc_frames.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp]
         _lib = L
     return _lib
 
@@ -165,6 +169,27 @@ def attention(q, k, v, n_kv):
     return out, probs
 
 
+def attention_f32(q, k, v):
+    """The code predictor's prefill attention: q [n_head][hd], k and v
+    [n_kv][n_kv_head][hd], all f32; causal, query i sees rows 0..i when q has
+    one row per position ([n_kv][n_head][hd]), or all n_kv rows for one query."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    n_kv, nkv, hd = k.shape
+    nh = q.shape[-2]
+    out = np.empty(q.shape, np.float32)
+    if q.ndim == 2:
+        lib().orc_attention_f32(_p(q), _p(k), _p(v), nkv * hd, nh, nkv, hd, n_kv, _p(out))
+    else:
+        for i in range(q.shape[0]):
+            qi = np.ascontiguousarray(q[i])
+            oi = np.empty_like(qi)
+            lib().orc_attention_f32(_p(qi), _p(k), _p(v), nkv * hd, nh, nkv, hd, i + 1, _p(oi))
+            out[i] = oi
+    return out
+
+
 def argmax(x):
     x = np.ascontiguousarray(x, np.float32)
     return lib().orc_argmax(_p(x), x.size)
@@ -227,6 +252,12 @@ class Oracle:
 
     def kv_reset(self, n_ctx):
         self._chk(self.L.orc_kv_reset(self.h, n_ctx), "kv_reset")
+
+    def kv_write(self, layer, k, v):
+        """fp16 rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos)."""
+        k = np.ascontiguousarray(k, np.float16)
+        v = np.ascontiguousarray(v, np.float16)
+        self._chk(self.L.orc_kv_write(self.h, layer, k.shape[0], _p(k), _p(v)), "kv_write")
 
     def prefill(self, embd, n_past=0):
         embd = np.ascontiguousarray(embd, np.float32)
@@ -304,6 +335,21 @@ class Oracle:
         codes = np.empty((max(max_len, 1), self.cfg.n_codebooks), np.int32)
         n = self.L.orc_generate_rows(self.h, _p(prefill), prefill.shape[0], _p(trailing), trailing.shape[0], _p(pad),
                                      ctypes.byref(p), _p(codes), None)
+        if n < 0:
+            raise RuntimeError(self.error())
+        return codes[:n].copy()
+
+    def frames(self, first_logits, n_past, trailing, pad, max_len, repetition_penalty=1.05, temperature=0.0,
+               top_k=0, eos_bias=0.0, target_frames=0, seed=0):
+        """The frame loop from the current cache (the device's frames_begin +
+        frames_run after a prefill or step)."""
+        first_logits = np.ascontiguousarray(first_logits, np.float32)
+        trailing = np.ascontiguousarray(trailing, np.float32).reshape(-1, self.cfg.hidden_size)
+        pad = np.ascontiguousarray(pad, np.float32)
+        p = OrcGenParams(max_len, 0, repetition_penalty, temperature, top_k, eos_bias, target_frames, 0, seed)
+        codes = np.empty((max(max_len, 1), self.cfg.n_codebooks), np.int32)
+        n = self.L.orc_frames(self.h, _p(first_logits), n_past, _p(trailing), trailing.shape[0], _p(pad),
+                              ctypes.byref(p), _p(codes))
         if n < 0:
             raise RuntimeError(self.error())
         return codes[:n].copy()

@@ -421,6 +421,7 @@ struct AttnSpec {
     const float * rc; const float * rs;
     const int32_t * pos_ptr; int pos_const;
     float * probs = nullptr;
+    bool f32_prefill = false;   // the code predictor's 2-token prefill: F32 q, K, V, P
 };
 
 void attention(q3t_dev * c, const AttnSpec & s, int nt) {
@@ -455,13 +456,15 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     a.scale = 1.0f / std::sqrt((float) g.head_dim);
     a.nt = nt;
     a.probs_out = s.probs;
+    a.f32_new = s.f32_prefill ? 1 : 0;
     hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt), dim3(kBlock), attn_lds_bytes(s.n_ctx), c->stream, a);
 }
 
 // One transformer block over nt tokens; input rows `xin` (stride d),
 // output rows left in c->xa.
 void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, int ffn, uint16_t * kc, uint16_t * vc,
-           int n_ctx, const float * rc, const float * rs, const int32_t * pos_ptr, int pos_const) {
+           int n_ctx, const float * rc, const float * rs, const int32_t * pos_ptr, int pos_const,
+           bool f32_prefill = false) {
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     GemvSpec s{};
@@ -469,6 +472,7 @@ void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, in
     s.y = c->qkv; s.y_stride = qkvd;
     gemv(c, s, nt);
     AttnSpec as{c->qkv, &L, kc, vc, n_ctx, rc, rs, pos_ptr, pos_const};
+    as.f32_prefill = f32_prefill;
     attention(c, as, nt);
     GemvSpec o{};
     o.w = weight_of(L.wo); o.rows = d; o.K = qd; o.x = c->attn; o.x_stride = qd;
@@ -540,7 +544,7 @@ void code_pred_seq(q3t_dev * c, bool frame_loop) {
         }
         for (int il = 0; il < g.cp_layers; ++il)
             layer(c, c->cp[il], il == 0 ? (mtp ? c->cpx : c->stage) : c->xa, nt, d, g.cp_ffn, c->cpk + il * lstride,
-                  c->cpv + il * lstride, 16, c->cp_rope_cos, c->cp_rope_sin, nullptr, pos);
+                  c->cpv + il * lstride, 16, c->cp_rope_cos, c->cp_rope_sin, nullptr, pos, step == 0);
         GemvSpec h{};
         h.w = weight_of(c->cp_head[step]); h.rows = g.cp_vocab; h.K = d;
         h.x = c->xa + (size_t) (nt - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->cp_out_norm.data;
@@ -1855,6 +1859,7 @@ struct StreamKV {
     int n_ctx;
     const float * rc; const float * rs;
     const int32_t * pos_ptr; int pos_const;
+    bool f32_prefill;               // the code predictor's 2-token prefill: F32 q, K, V, P
 };
 
 // The three shapes of decode GEMM a layer needs (ms::k_gemm_sk):
@@ -1997,6 +2002,7 @@ static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool 
         a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
         a.scale = 1.0f / std::sqrt((float) g.head_dim);
         a.nt = nt;
+        a.f32_new = kv.f32_prefill ? 1 : 0;
         hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
     }
     ms::GemmArgs o{};
@@ -2054,7 +2060,7 @@ static void streams_frame_seq(q3t_dev * c) {
         const float * x = c->sstage;
         for (int il = 0; il < g.cp_layers; ++il) {
             StreamKV kv{c->scpk + il * cp_lstride, c->scpv + il * cp_lstride, cp_lstride * g.cp_layers, 16,
-                        c->cp_rope_cos, c->cp_rope_sin, nullptr, pos};
+                        c->cp_rope_cos, c->cp_rope_sin, nullptr, pos, step == 0};
             stream_layer(c, c->cp[il], x, il > 0, nt, kv);
             x = c->bxa;
         }
@@ -2071,7 +2077,7 @@ static void streams_frame_seq(q3t_dev * c) {
     const float * x = c->sstage;
     for (int il = 0; il < g.n_layers; ++il) {
         StreamKV kv{c->skc + il * lstride, c->svc + il * lstride, lstride * g.n_layers, c->sb_ctx, c->rope_cos,
-                    c->rope_sin, &c->sst[0].talker_pos, 0};
+                    c->rope_sin, &c->sst[0].talker_pos, 0, false};
         stream_layer(c, c->talker[il], x, il > 0, 1, kv);
         x = c->bxa;
     }

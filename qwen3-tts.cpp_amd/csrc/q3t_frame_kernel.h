@@ -837,6 +837,12 @@ __device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
 // and nt tokens at positions pos0.. (causal); the 16-position KV cache of
 // every code-predictor layer lives in this workgroup's LDS.
 //
+// nt == 2 is the prefill (positions 0 and 1), which attends over the F32
+// rows of this call (src/tts_transformer.cpp:1999-2012): q, K, V and P stay
+// fp32, every product is exact in fp64, and a score's sum is the four 32-dim
+// partials of its quad combined (s0 + s1) + (s2 + s3).  It still writes the
+// fp16 cache rows the 14 steps read, where q and P are rounded to fp16.
+//
 // Wave w owns row w of (q0, q1, k, v): lane l holds elements l and l + 64,
 // which are exactly the NEOX rotation pairs, so QK-norm and RoPE need only
 // wave reductions; the new K/V rows go straight into the LDS cache.  Then
@@ -849,7 +855,10 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
                                                             bool & dead) {
     const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kd = qd / 2;
-    float * qf = L.a;                      // [tok][head][128] rotated, fp16-rounded q
+    const bool f32 = nt == 2;              // the prefill: unrounded q, K, V, P
+    float * qf = L.a;                      // [tok][head][128] rotated q (fp16-rounded in a step)
+    float * kf = L.a + 4 * 128;            // prefill: [tok][128] rotated k, fp32
+    float * vf = L.a + 6 * 128;            // prefill: [tok][128] v, fp32
     {
         const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
@@ -887,15 +896,23 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
                 const float a0 = y0 * c, b0 = y1 * sn, a1 = y0 * sn, b1 = y1 * c;
                 const float o0 = a0 - b0, o1 = a1 + b1;
                 if (wave < 2) {
-                    qf[(tok * 2 + wave) * 128 + lane] = round_f16(o0);
-                    qf[(tok * 2 + wave) * 128 + lane + 64] = round_f16(o1);
+                    qf[(tok * 2 + wave) * 128 + lane] = f32 ? o0 : round_f16(o0);
+                    qf[(tok * 2 + wave) * 128 + lane + 64] = f32 ? o1 : round_f16(o1);
                 } else {
                     L.cpk[layer][pos * 128 + lane] = f2h(o0);
                     L.cpk[layer][pos * 128 + lane + 64] = f2h(o1);
+                    if (f32) {
+                        kf[tok * 128 + lane] = o0;
+                        kf[tok * 128 + lane + 64] = o1;
+                    }
                 }
             } else {
                 L.cpv[layer][pos * 128 + lane] = f2h(x0);
                 L.cpv[layer][pos * 128 + lane + 64] = f2h(x1);
+                if (f32) {
+                    vf[tok * 128 + lane] = x0;
+                    vf[tok * 128 + lane + 64] = x1;
+                }
             }
         }
     }
@@ -913,13 +930,25 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
         double acc = 0.0;
         if (jq < n_kv) {
             const float * q = qf + (tok * 2 + hq) * 128 + sq * 32;
+            if (f32) {
+                const float * k = kf + jq * 128 + sq * 32;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int4 k4 = *(const int4 *) &kc[jq * 128 + sq * 32 + c * 8];
-                const float4 qa = *(const float4 *) &q[c * 8], qb = *(const float4 *) &q[c * 8 + 4];
-                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                for (int c = 0; c < 8; ++c) {
+                    const float4 k4 = *(const float4 *) &k[c * 4], q4 = *(const float4 *) &q[c * 4];
+                    acc = fma((double) q4.x, (double) k4.x, acc);
+                    acc = fma((double) q4.y, (double) k4.y, acc);
+                    acc = fma((double) q4.z, (double) k4.z, acc);
+                    acc = fma((double) q4.w, (double) k4.w, acc);
+                }
+            } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc = fma((double) qv[e], (double) h8(k4, e), acc);
+                for (int c = 0; c < 4; ++c) {
+                    const int4 k4 = *(const int4 *) &kc[jq * 128 + sq * 32 + c * 8];
+                    const float4 qa = *(const float4 *) &q[c * 8], qb = *(const float4 *) &q[c * 8 + 4];
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = fma((double) qv[e], (double) h8(k4, e), acc);
+                }
             }
         }
         acc += dpp_d<0xB1>(acc);
@@ -929,10 +958,10 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
         const float ev = jq < n_kv ? expf_q3t(sv - mx) : 0.0f;
         const double sum = wave_sum_d(sq == 0 ? (double) ev : 0.0);
         const float inv = (float) (1.0 / sum);
-        const float pr = round_f16(ev * inv);
+        const float pr = f32 ? ev * inv : round_f16(ev * inv);
         float vv[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) vv[j] = h2f(vc[j * 128 + d]);
+        for (int j = 0; j < 16; ++j) vv[j] = f32 ? (j < 2 ? vf[j * 128 + d] : 0.0f) : h2f(vc[j * 128 + d]);
         double o = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {

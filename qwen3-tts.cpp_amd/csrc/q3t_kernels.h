@@ -402,6 +402,10 @@ struct AttnArgs {
     // optional Q8_0 copy of the output rows for the next projection:
     // out_q [NT][out_stride] int8, out_dx [NT][out_stride / 32] (same stream offsets)
     int8_t * out_q; float * out_dx;
+    // 1: the code predictor's prefill (pos0 = 0, nt = 2), which attends over
+    // the F32 rows of this launch (src/tts_transformer.cpp:1999-2012): q, K, V
+    // and P stay fp32; the fp16 cache rows are still written
+    int32_t f32_new;
 };
 
 constexpr int kHD = 128;
@@ -472,7 +476,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         const float v = t < kHD ? row[h * kHD + t] : 0.0f;
         const float o = head_norm_rope(v, a.q_norm, a.eps, a.rope_cos + (size_t) pos * 64,
                                        a.rope_sin + (size_t) pos * 64, tmp, red);
-        if (t < kHD) qf[t] = round_f16(o);
+        if (t < kHD) qf[t] = a.f32_new ? o : round_f16(o);
     }
     // k, v of this KV head for the chunk tokens 0..tok (positions >= pos0 are
     // never read from the cache inside this launch)
@@ -482,10 +486,11 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         const float o = head_norm_rope(kvv, a.k_norm, a.eps, a.rope_cos + (size_t) (pos0 + j) * 64,
                                        a.rope_sin + (size_t) (pos0 + j) * 64, tmp, red);
         if (t < kHD) {
+            const float vraw = row[qd + kd + g * kHD + t];
             const uint16_t kh = f2h(o);
-            const uint16_t vh = f2h(row[qd + kd + g * kHD + t]);
-            knew[j * kHD + t] = h2f(kh);
-            vnew[j * kHD + t] = h2f(vh);
+            const uint16_t vh = f2h(vraw);
+            knew[j * kHD + t] = a.f32_new ? o : h2f(kh);
+            vnew[j * kHD + t] = a.f32_new ? vraw : h2f(vh);
             if (j == tok && (h % group) == 0) {
                 a.kc[((size_t) g * a.n_ctx + pos) * kHD + t] = kh;
                 a.vc[((size_t) g * a.n_ctx + pos) * kHD + t] = vh;
@@ -499,7 +504,27 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     const int sub = lane & 7, pw = lane >> 3;
     const uint16_t * kbase = a.kc + (size_t) g * a.n_ctx * kHD;
     float lmax = -INFINITY;
-    for (int j0 = 0; j0 < n_kv; j0 += 32) {
+    if (a.f32_new) {
+        // every position is a new fp32 row (pos0 = 0, n_kv <= 16): 4 lanes of
+        // wave 0 per position, each a sequential 32-dim partial of exact fp64
+        // products, combined (s0 + s1) + (s2 + s3)
+        const int j = lane >> 2, s4 = lane & 3;
+        double acc = 0.0;
+        if (wave == 0 && j < n_kv) {
+            const float * kr = knew + j * kHD + s4 * 32;
+            const float * qq = qf + s4 * 32;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) acc = fma((double) qq[e], (double) kr[e], acc);
+        }
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        if (wave == 0 && j < n_kv) {
+            const float s = (float) acc * a.scale;
+            if (s4 == 0) sc[j] = s;
+            lmax = s;
+        }
+    }
+    for (int j0 = 0; !a.f32_new && j0 < n_kv; j0 += 32) {
         const int j = j0 + wave * 8 + pw;
         double acc = 0.0;
         if (j < n_kv) {
@@ -539,7 +564,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     for (int j = t; j < n_kv; j += kBlock) {
         const float p = sc[j] * inv;
         if (a.probs_out && tok == 0) a.probs_out[(size_t) h * n_kv + j] = p;
-        sc[j] = round_f16(p);
+        sc[j] = a.f32_new ? p : round_f16(p);
     }
     __syncthreads();
 
@@ -557,11 +582,12 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
                 const int4 vv = *(const int4 *) (vbase + (size_t) j * kHD + dsub * 8);
                 const uint16_t * vh = (const uint16_t *) &vv;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] += (double) (p * h2f(vh[e]));
+                for (int e = 0; e < 8; ++e) o[e] += (double) p * (double) h2f(vh[e]);
             } else {
+                // fp16 x fp16 or (prefill) fp32 x fp32: exact in fp64 either way
                 const float * vr = vnew + (j - pos0) * kHD + dsub * 8;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] += (double) (p * vr[e]);
+                for (int e = 0; e < 8; ++e) o[e] += (double) p * (double) vr[e];
             }
         }
     }
