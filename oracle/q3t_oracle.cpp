@@ -716,6 +716,23 @@ int orc_kv_write(orc_model * m, int32_t layer, int32_t n_pos, const uint16_t * k
     return 0;
 }
 
+int orc_kv_read(orc_model * m, int32_t layer, int32_t n_pos, uint16_t * k, uint16_t * v) {
+    const orc_config & c = m->cfg;
+    if (layer < 0 || layer >= c.n_layers || n_pos < 0 || n_pos > m->kv.n_ctx) {
+        m->err = "kv_read: layer or position range outside the cache";
+        return -1;
+    }
+    const int64_t hd = c.head_dim, nkv = c.n_kv_head;
+    const uint16_t * kc = m->kv.k.data() + (size_t) layer * nkv * m->kv.n_ctx * hd;
+    const uint16_t * vc = m->kv.v.data() + (size_t) layer * nkv * m->kv.n_ctx * hd;
+    for (int64_t p = 0; p < n_pos; ++p)
+        for (int64_t h = 0; h < nkv; ++h) {
+            std::memcpy(k + (p * nkv + h) * hd, kc + (h * m->kv.n_ctx + p) * hd, hd * sizeof(uint16_t));
+            std::memcpy(v + (p * nkv + h) * hd, vc + (h * m->kv.n_ctx + p) * hd, hd * sizeof(uint16_t));
+        }
+    return 0;
+}
+
 int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
                 float * hidden_out, float * logits_out) {
     return talker_forward(m, embd, n, n_past, hidden_out, logits_out) ? 0 : -1;

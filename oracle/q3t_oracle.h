@@ -170,6 +170,8 @@ int         orc_kv_reset(orc_model * m, int32_t n_ctx);
 /* fp16 K/V rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos) of
  * talker layer `layer` (the layout q3t_dev_kv_write takes). */
 int         orc_kv_write(orc_model * m, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v);
+/* the inverse: rows of positions [0, n_pos) of talker layer `layer`. */
+int         orc_kv_read(orc_model * m, int32_t layer, int32_t n_pos, uint16_t * k, uint16_t * v);
 /* n-token prefill at positions [n_past, n_past+n).  hidden_out: [n][d]
  * (normed), logits_out: last row [codec_vocab] (may be NULL). */
 int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,

@@ -77,6 +77,7 @@ def lib():
         L.orc_last_error.argtypes = [vp]; L.orc_last_error.restype = ctypes.c_char_p
         L.orc_kv_reset.argtypes = [vp, i32]
         L.orc_kv_write.argtypes = [vp, i32, i32, vp, vp]
+        L.orc_kv_read.argtypes = [vp, i32, i32, vp, vp]
         L.orc_prefill.argtypes = [vp, vp, i32, i32, vp, vp]
         L.orc_step.argtypes = [vp, vp, i32, vp, vp]
         L.orc_code_pred.argtypes = [vp, vp, i32, f32, i32, u64, u32, vp, vp]
@@ -258,6 +259,12 @@ class Oracle:
         k = np.ascontiguousarray(k, np.float16)
         v = np.ascontiguousarray(v, np.float16)
         self._chk(self.L.orc_kv_write(self.h, layer, k.shape[0], _p(k), _p(v)), "kv_write")
+
+    def kv_read(self, layer, n_pos):
+        shape = (n_pos, self.cfg.n_kv_head, self.cfg.head_dim)
+        k, v = np.empty(shape, np.float16), np.empty(shape, np.float16)
+        self._chk(self.L.orc_kv_read(self.h, layer, n_pos, _p(k), _p(v)), "kv_read")
+        return k, v
 
     def prefill(self, embd, n_past=0):
         embd = np.ascontiguousarray(embd, np.float32)

@@ -1,0 +1,212 @@
+"""HIP path vs the CPU oracle at the benchmark workloads' shapes and contexts
+(0.6B shapes; through the device C ABI):
+
+  configuration 1  F16 weights, 32-token prompt, 64 greedy frames
+  configuration 2  F16 talker step at KV 512 (n_kv = 513: the persistent
+                   kernel's attention chunk is 32 positions), cache pre-filled
+                   with bfloat16-valued N(0,1) K/V through q3t_dev_kv_write
+  configuration 3  Q8_0 weights, 64-token prompt, 256 greedy frames
+  configuration 4  F16 long context: a tiled prefill that attends over more
+                   than 1,024 positions (the split attention's four-phase
+                   form), then sampled frames (T 0.9, top-k 50, repetition
+                   penalty 1.05); and decode past 4,096 positions
+
+Long contexts are pre-filled with seeded K/V rows on both sides (the oracle's
+orc_kv_write takes the same [n_pos][n_kv_head][head_dim] rows), so the
+oracle runs only the rows and frames under test.  Every comparison is bit for
+bit (codes, logits, hidden rows); the F16 logits bound of 1e-2 is asserted
+too.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import q3t_oracle as orc
+from qwen3_tts_amd import config as qcfg
+from qwen3_tts_amd import driver
+from qwen3_tts_amd.device import Device
+from qwen3_tts_amd.synth import Weights
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+LOGIT_TOL = 1e-2
+THREADS = 16
+
+_weights = {}
+_oracle_runs = {}
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def weights(wtype, seed):
+    """One 0.6B model held at a time (1-2 GB of host memory)."""
+    key = (wtype, seed)
+    if key not in _weights:
+        _weights.clear()
+        say(f"[gpu] synthesising 0.6B {wtype} weights (seed {seed})")
+        _weights[key] = Weights(qcfg.full_06b(), wtype, seed=seed)
+    return _weights[key]
+
+
+def open_pair(wtype, seed, n_ctx):
+    cfg = qcfg.full_06b()
+    w = weights(wtype, seed)
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    dev.kv_reserve(n_ctx)
+    o = orc.Oracle(cfg, w, threads=THREADS)
+    o.kv_reset(n_ctx)
+    return cfg, w, dev, o
+
+
+def bf16_kv(rng, n_pos, cfg):
+    """N(0,1) K and V rows [n_pos][n_kv_head][head_dim], rounded to bfloat16
+    (nearest even) and held in the fp16 cache.  bfloat16's 8-bit significand
+    fits fp16's 11 bits, so every value of magnitude at least 2^-17 is stored
+    exactly."""
+    x = rng.standard_normal((2, n_pos, cfg.n_kv_head, cfg.head_dim), dtype=np.float32)
+    u = x.view(np.uint32)
+    u = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)).astype(np.uint32)
+    return u.view(np.float32).astype(np.float16)
+
+
+def prefill_kv(dev, o, cfg, rng, n_pos):
+    say(f"[gpu] writing {n_pos} K/V positions x {cfg.n_layers} layers")
+    for il in range(cfg.n_layers):
+        kv = bf16_kv(rng, n_pos, cfg)
+        dev.kv_write(il, kv[0], kv[1])
+        o.kv_write(il, kv[0], kv[1])
+
+
+@pytest.fixture(params=["persistent", "graph"])
+def path(request, monkeypatch):
+    """The persistent frame kernel (default) or the captured multi-kernel
+    sequences (Q3T_FRAME_KERNEL=0); chosen when a context first runs."""
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
+    return request.param
+
+
+def check_path(dev, want):
+    _, _, used = dev.frames_stats()
+    assert used == (1 if want == "persistent" else 0), (want, used)
+
+
+def test_config2_f16_talker_step_kv512(path):
+    cfg, w, dev, o = open_pair("f16", 51, 528)
+    try:
+        rng = np.random.default_rng(52)
+        prefill_kv(dev, o, cfg, rng, 512)
+        for s in range(3):
+            e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+            say(f"[gpu] config 2 ({path}): step at n_past {512 + s}")
+            lg, hg = dev.talker_step(e, 512 + s)
+            lo, ho = o.step(e, 512 + s)
+            assert np.abs(lg - lo).max() <= LOGIT_TOL
+            assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
+            assert np.array_equal(hg, ho)
+    finally:
+        dev.close()
+
+
+def _frames_both(dev, o, cfg, lo, n_past, n_frames, seed):
+    rng = np.random.default_rng(seed)
+    trail = (rng.standard_normal((5, cfg.hidden_size)) * 0.05).astype(np.float32)
+    pad = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+    kw = dict(repetition_penalty=1.05, temperature=0.9, top_k=50, eos_bias=-1e4, seed=seed)
+    dev.frames_begin(trail, pad, n_past, n_frames, **kw)
+    cg, _ = dev.frames_run(n_frames)
+    co = o.frames(lo, n_past, trail, pad, n_frames, **kw)
+    return cg, co
+
+
+def test_config4_long_context_sampled_f16(path, monkeypatch):
+    cfg, w, dev, o = open_pair("f16", 53, 4200)
+    monkeypatch.setenv("Q3T_PREFILL_MFMA", "1")
+    try:
+        rng = np.random.default_rng(54)
+        # a 64-row tiled prefill after 1,000 cached positions: its causal
+        # attention spans up to 1,064 positions
+        prefill_kv(dev, o, cfg, rng, 1000)
+        rows = (rng.standard_normal((64, cfg.hidden_size)) * 0.05).astype(np.float32)
+        say(f"[gpu] config 4 ({path}): tiled prefill of 64 rows at n_past 1000")
+        hg, lg = dev.prefill(rows, 1000)
+        ho, lo = o.prefill(rows, 1000)
+        assert np.abs(lg - lo).max() <= LOGIT_TOL
+        assert np.array_equal(hg, ho) and np.array_equal(lg, lo)
+        say(f"[gpu] config 4 ({path}): 8 sampled frames from position 1064")
+        cg, co = _frames_both(dev, o, cfg, lo, 1064, 8, seed=55)
+        check_path(dev, path)
+        assert cg.shape == (8, 16) and np.array_equal(cg, co)
+        # past 4,096 positions: one step, then 4 sampled frames
+        prefill_kv(dev, o, cfg, rng, 4100)
+        e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+        say(f"[gpu] config 4 ({path}): step at n_past 4100, 4 sampled frames")
+        lg, hg = dev.talker_step(e, 4100)
+        lo, ho = o.step(e, 4100)
+        assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+        cg, co = _frames_both(dev, o, cfg, lo, 4101, 4, seed=56)
+        check_path(dev, path)
+        assert cg.shape == (4, 16) and np.array_equal(cg, co)
+    finally:
+        dev.close()
+
+
+def _oracle_generate(key, wtype, seed, text, spk, max_len):
+    if key not in _oracle_runs:
+        cfg = qcfg.full_06b()
+        o = orc.Oracle(cfg, weights(wtype, seed), threads=THREADS)
+        say(f"[gpu] {key}: oracle generate {max_len}")
+        _oracle_runs[key] = o.generate(text, spk, max_len=max_len, temperature=0.0, top_k=0)
+        o.close()
+    return _oracle_runs[key]
+
+
+def test_config1_f16_frame_loop_64_greedy(path):
+    """F16 GEMVs with fp16-rounded inputs and the widened fp32-input
+    ffn_down; a 32-token prompt, 64 greedy frames."""
+    cfg = qcfg.full_06b()
+    text = np.random.default_rng(18).integers(0, 151936, 32).astype(np.int32)
+    spk = np.random.default_rng(19).standard_normal(1024).astype(np.float32)
+    co, first_o = _oracle_generate("config1", "f16", 4, text, spk, 64)
+    w = weights("f16", 4)
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w)
+        say(f"[gpu] config 1: device generate 64 ({path})")
+        cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, chunk=16)
+        check_path(dev, path)
+    finally:
+        dev.close()
+    assert cg.shape == co.shape and np.array_equal(cg, co)
+
+
+def test_config3_q8_frame_loop_256_greedy(path):
+    """Q8_0 layers, a 64-token prompt, 256 greedy frames; the prefill rows
+    built on the device equal the oracle's, and so do the first logits."""
+    cfg = qcfg.full_06b()
+    text = np.random.default_rng(8).integers(0, 151936, 64).astype(np.int32)
+    spk = np.random.default_rng(9).standard_normal(1024).astype(np.float32)
+    co, first_o = _oracle_generate("config3", "q8_0", 3, text, spk, 256)
+    w = weights("q8_0", 3)
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w)
+        o = orc.Oracle(cfg, w, threads=THREADS)
+        pre = driver.build_prefill(dev, cfg, text, spk)
+        opre, otr, opad = o.build_prefill(text, spk)
+        o.close()
+        assert np.array_equal(pre[0], opre) and np.array_equal(pre[1], otr) and np.array_equal(pre[2], opad)
+        dev.kv_reserve(pre[0].shape[0] + 256 + 8)
+        _, first_g = dev.prefill(pre[0], 0, want_hidden=False)
+        assert np.array_equal(first_g, first_o)
+        say(f"[gpu] config 3: device generate 256 ({path})")
+        cg = driver.generate(dev, cfg, text, spk, max_len=256, temperature=0.0, top_k=0, prefill_rows=pre)
+        check_path(dev, path)
+    finally:
+        dev.close()
+    say(f"[gpu] config 3: frames oracle={co.shape[0]} device={cg.shape[0]}")
+    assert cg.shape == co.shape and np.array_equal(cg, co)

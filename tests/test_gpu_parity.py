@@ -185,29 +185,6 @@ def test_callback_abort(tiny_model, frame_path):
     assert cg.shape[0] == 5
 
 
-@pytest.mark.slow
-def test_full_q8_frame_loop_64_greedy(frame_path):
-    cfg = qcfg.full_06b()
-    say("[gpu] full 0.6B Q8_0: synth + upload")
-    w, dev, o = make(cfg, "q8_0", seed=3, n_ctx=256)
-    text = np.random.default_rng(8).integers(0, 151936, 32).astype(np.int32)
-    spk = np.random.default_rng(9).standard_normal(1024).astype(np.float32)
-    say("[gpu] full: oracle generate 64")
-    co, first_o = o.generate(text, spk, max_len=64, temperature=0.0, top_k=0)
-    say("[gpu] full: device generate 64")
-    pre = driver.build_prefill(dev, cfg, text, spk)
-    opre, otr, opad = o.build_prefill(text, spk)
-    assert np.array_equal(pre[0], opre) and np.array_equal(pre[1], otr) and np.array_equal(pre[2], opad)
-    _, first_g = dev.prefill(pre[0], 0, want_hidden=False)
-    assert np.abs(first_g - first_o).max() <= LOGIT_TOL
-    say(f"[gpu] full: device generate 64 ({frame_path})")
-    cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, prefill_rows=pre)
-    check_path(dev, "q8_0", frame_path)
-    say(f"[gpu] full: frames oracle={co.shape[0]} device={cg.shape[0]}")
-    assert np.array_equal(cg, co)
-    dev.close()
-
-
 def test_fp16_tie_rounding_regression(frame_path):
     """Weights and prompt on which one attention probability of the talker
     (frame 13, layer 1) lands exactly on an fp16 tie after fp32 rounding; a
@@ -280,24 +257,6 @@ def test_full_q8_mfma_prefill_200_rows():
     assert np.array_equal(hid_g, hid_o)
     assert np.array_equal(log_g, log_o)
     assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
-
-
-@pytest.mark.slow
-def test_full_f16_frame_loop_24_greedy(frame_path):
-    """0.6B shapes with F16 weights: F16 GEMVs with fp16-rounded inputs and the
-    widened fp32-input ffn_down, 24 greedy frames equal to the oracle."""
-    cfg = qcfg.full_06b()
-    say("[gpu] full 0.6B F16: synth + upload")
-    w, dev, o = make(cfg, "f16", seed=4, n_ctx=256)
-    text = np.random.default_rng(18).integers(0, 151936, 24).astype(np.int32)
-    spk = np.random.default_rng(19).standard_normal(1024).astype(np.float32)
-    say("[gpu] full F16: oracle generate 24")
-    co, _ = o.generate(text, spk, max_len=24, temperature=0.0, top_k=0)
-    say(f"[gpu] full F16: device generate 24 ({frame_path})")
-    cg = driver.generate(dev, cfg, text, spk, max_len=24, temperature=0.0, top_k=0, chunk=8)
-    check_path(dev, "f16", frame_path)
-    dev.close()
-    assert np.array_equal(cg, co)
 
 
 @pytest.mark.slow

@@ -457,3 +457,49 @@ def test_mtp_projection_equals_projected_inputs():
         c1, _ = o.code_pred(hid, cb0, temperature=0.9, top_k=50, seed=4, frame=2)
         c2, _ = o2.code_pred(proj(hid[None])[0], cb0, temperature=0.9, top_k=50, seed=4, frame=2)
         assert np.array_equal(c1, c2)
+
+
+def test_frames_from_cache_equals_generate_rows(tiny):
+    """orc_frames continues from the cache a prefill left: prefill + frames
+    gives generate_rows' codes, greedy and sampled."""
+    cfg, w, o = tiny
+    rng = np.random.default_rng(61)
+    d = cfg.hidden_size
+    pre = (rng.standard_normal((9, d)) * 0.05).astype(np.float32)
+    trail = (rng.standard_normal((4, d)) * 0.05).astype(np.float32)
+    pad = (rng.standard_normal(d) * 0.05).astype(np.float32)
+    for kw in (dict(temperature=0.0), dict(temperature=0.9, top_k=50, seed=3)):
+        ref = o.generate_rows(pre, trail, pad, max_len=10, **kw)
+        o.kv_reset(9 + 10 + 8)
+        _, lg = o.prefill(pre, 0)
+        got = o.frames(lg, 9, trail, pad, 10, **kw)
+        assert got.shape[0] > 0 and np.array_equal(got, ref)
+
+
+def test_kv_write_layout_matches_prefill_rows(tiny):
+    """orc_kv_write takes rows [n_pos][n_kv_head][head_dim]: the rows a
+    prefill stored, read back and written into a cleared cache, make the next
+    step identical; the same rows with two KV heads swapped do not."""
+    cfg, w, o = tiny
+    rng = np.random.default_rng(62)
+    d = cfg.hidden_size
+    pre = (rng.standard_normal((9, d)) * 0.05).astype(np.float32)
+    e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+    o.kv_reset(32)
+    o.prefill(pre, 0)
+    rows = [o.kv_read(il, 9) for il in range(cfg.n_layers)]
+    lo, ho = o.step(e, 9)
+    o.kv_reset(32)
+    for il, (k, v) in enumerate(rows):
+        assert k.shape == (9, cfg.n_kv_head, cfg.head_dim)
+        o.kv_write(il, k, v)
+    # the step reads only the cache and its own input, not the prefill state
+    l2, h2 = o.step(e, 9)
+    assert np.array_equal(l2, lo) and np.array_equal(h2, ho)
+    o.kv_reset(32)
+    for il, (k, v) in enumerate(rows):
+        o.kv_write(il, k[:, ::-1].copy(), v)
+    l3, _ = o.step(e, 9)
+    assert not np.array_equal(l3, lo)
+    with pytest.raises(RuntimeError):
+        o.kv_write(cfg.n_layers, rows[0][0], rows[0][1])
