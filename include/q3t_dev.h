@@ -150,6 +150,14 @@ int  q3t_dev_code_pred(q3t_dev * dev, const float * hidden, int32_t cb0,
 /* text_proj: fc2(silu(fc1(text_embd[tok]) + b1)) + b2 -> out [n][hidden].
  * Replaces project_text_tokens (src/tts_transformer.cpp:963-1028). */
 int  q3t_dev_text_proj(q3t_dev * dev, const int32_t * tokens, int32_t n, float * out);
+/* q3t_dev_text_proj without any device allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, results and errors
+ * as q3t_dev_text_proj for n <= 64 ids; more ids are rejected with an error.
+ * Its work buffers (2 MiB) are a static device array that each GPU holds until
+ * the process ends and that every call on that GPU shares: calls that overlap
+ * on one GPU (from several contexts or threads) race. */
+int  q3t_dev_text_proj_noalloc(q3t_dev * dev, const int32_t * tokens, int32_t n, float * out);
 /* Embedding rows as fp32: table 0 = talker.codec_embd, 1 = code_pred.codec_embd[index],
  * 2 = talker.text_embd.  Replaces lookup_embedding_rows /
  * lookup_single_embedding_row (src/tts_transformer.cpp:839-961). */

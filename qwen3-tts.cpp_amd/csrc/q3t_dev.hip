@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -48,10 +49,23 @@ struct LayerDev {
 
 }  // namespace
 
+// Device scratch of q3t_dev_text_proj_noalloc, the entry point for callers
+// that cannot allocate device memory: the ids, the gathered text_embd rows,
+// the fc1 output, the Q8_0 copies of the GEMM inputs and the result rows of
+// up to kNoAllocMaxIds ids.  Each GPU the library runs on holds its own copy
+// until the process ends; calls that overlap on one GPU share it and race.
+// In host code `scratch` names a host-side stand-in, never a device address:
+// kernels get the address hipGetSymbolAddress returns for the current device
+// (scratch_setup, once per device; q3t_dev::scratch).
+constexpr size_t kScratchBytes = (size_t) 2 << 20;
+constexpr int kNoAllocMaxIds = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 struct q3t_dev {
     q3t_config cfg{};
     int device = 0;
     hipStream_t stream = nullptr;
+    unsigned char * scratch = nullptr;   // this device's copy of `scratch` (q3t_dev_text_proj_noalloc)
     std::string err;
     std::vector<void *> allocs;
     std::map<std::string, Slot> slots;
@@ -825,6 +839,27 @@ int ensure_frame_graph(q3t_dev * c) {
 // =================================================================== C ABI
 extern "C" {
 
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, unsigned char *> g_scratch_addr;   // device ordinal -> its copy of `scratch`
+}  // namespace
+
+// With c->device current: the device address of this GPU's `scratch`, looked
+// up once per device.
+static int scratch_setup(q3t_dev * c) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_addr.find(c->device);
+    if (it == g_scratch_addr.end()) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(c, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        it = g_scratch_addr.emplace(c->device, (unsigned char *) p).first;
+    }
+    c->scratch = it->second;
+    return 0;
+}
+
 int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
     if (!cfg || !out) return -1;
     *out = nullptr;
@@ -850,6 +885,7 @@ int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
     if (g.codec_vocab < 1024 || g.n_codebooks != 16) return bad("codec vocabulary must be >= 1024 with 16 codebooks");
     if (hipSetDevice(device) != hipSuccess) return bad("hipSetDevice failed");
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bad("hipStreamCreate failed");
+    if (scratch_setup(c)) { *out = c; return -1; }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->n_cu = prop.multiProcessorCount;
     c->talker.resize(g.n_layers);
@@ -1267,10 +1303,12 @@ void prefill_mfma(q3t_dev * c, int n, int n_past) {
 // y [n][N] = x [n][K] . W^T + bias on the tiled GEMMs (Q8_0: quantised rows on
 // int8 MFMA; F16: the exact VALU GEMM, x rounded to fp16): the GEMV's
 // EPI_BIAS, with the bias as a residual of row stride 0.
-void pf_linear_bias(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, const Slot & bias, float * y) {
+// q, dx: room for the n quantised rows of x (Q8_0 weights).
+void pf_linear_bias(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, const Slot & bias, float * y,
+                    int8_t * q, float * dx) {
     if (w.type == Q3T_TYPE_Q8_0) {
-        pf_quant(c, x, n, K, nullptr, K, c->bp_q, c->bp_dx);
-        pf_gemm(c, w, N, K, n, y, (const float *) bias.data, 0, c->bp_q, c->bp_dx);
+        pf_quant(c, x, n, K, nullptr, K, q, dx);
+        pf_gemm(c, w, N, K, n, y, (const float *) bias.data, 0, q, dx);
     } else {
         pf_gemm_f16(c, w, N, K, n, x, K, false, y, (const float *) bias.data, 0);
     }
@@ -1290,11 +1328,55 @@ bool text_proj_tiled(const q3t_dev * c, int n) {
 // n >= 16 runs the tiled GEMMs, fewer rows the GEMV in chunks of up to 4;
 // rows are independent and both forms keep one numerics contract, so a row's
 // result does not depend on n.  ids are range-checked by the caller.
-int project_rows(q3t_dev * c, const int32_t * tokens, int32_t n, float * dst) {
-    const q3t_config & g = c->cfg;
+// Work buffers of one text projection of n ids: the ids on the device,
+// the gathered text_embd rows [n][te], the fc1 output (tiled: [n][te]; GEMV:
+// [4][te]) and the Q8_0 copies of the tiled GEMMs' input rows ([n][te] int8,
+// [n][te/32] scales).
+struct ProjWork {
+    const int32_t * ids; float * rows; float * h; int8_t * q; float * dx;
+};
+
+int proj_tensors_ok(q3t_dev * c) {
     if (!c->text_embd.data || !c->fc1.data || !c->fc1_b.data || !c->fc2.data || !c->fc2_b.data)
         return fail(c, "text projection tensors missing");
     if (c->text_embd.type != Q3T_TYPE_F16) return fail(c, "talker.text_embd must be F16");
+    return 0;
+}
+
+// The kernels of project_text_tokens on n ids already on the device.
+void project_rows_core(q3t_dev * c, int32_t n, const ProjWork & w, float * dst) {
+    const q3t_config & g = c->cfg;
+    const int te = g.text_embd_dim, d = g.hidden_size;
+    hipLaunchKernelGGL(k_gather_rows, dim3((te + 255) / 256, n), dim3(256), 0, c->stream,
+                       (const uint16_t *) c->text_embd.data, (int64_t) te, w.ids, n, w.rows);
+    if (text_proj_tiled(c, n)) {
+        pf_linear_bias(c, c->fc1, te, te, n, w.rows, c->fc1_b, w.h, w.q, w.dx);
+        const size_t cnt = (size_t) n * te;
+        hipLaunchKernelGGL(k_silu_rows, dim3((unsigned) std::min<size_t>((cnt + 255) / 256, 4096)), dim3(256), 0,
+                           c->stream, w.h, cnt);
+        pf_linear_bias(c, c->fc2, d, te, n, w.h, c->fc2_b, dst, w.q, w.dx);
+    } else {
+        for (int t0 = 0; t0 < n;) {
+            const int left = n - t0;
+            const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
+            GemvSpec a{};
+            a.w = weight_of(c->fc1); a.rows = te; a.K = te; a.x = w.rows + (size_t) t0 * te; a.x_stride = te;
+            a.y = w.h; a.y_stride = te; a.bias = (const float *) c->fc1_b.data; a.epi = EPI_BIAS_SILU;
+            a.no_done = true;
+            gemv(c, a, nt);
+            GemvSpec b{};
+            b.w = weight_of(c->fc2); b.rows = d; b.K = te; b.x = w.h; b.x_stride = te;
+            b.y = dst + (size_t) t0 * d; b.y_stride = d; b.bias = (const float *) c->fc2_b.data; b.epi = EPI_BIAS;
+            b.no_done = true;
+            gemv(c, b, nt);
+            t0 += nt;
+        }
+    }
+}
+
+int project_rows(q3t_dev * c, const int32_t * tokens, int32_t n, float * dst) {
+    const q3t_config & g = c->cfg;
+    if (proj_tensors_ok(c)) return -1;
     if (n > c->ids_cap) {
         dev_free(c, c->ids);
         c->ids = nullptr;
@@ -1302,10 +1384,9 @@ int project_rows(q3t_dev * c, const int32_t * tokens, int32_t n, float * dst) {
         c->ids_cap = n;
     }
     if (ensure_stage(c, n)) return -1;
-    const int te = g.text_embd_dim, d = g.hidden_size;
+    const int te = g.text_embd_dim;
     HIP_OK(hipMemcpyAsync(c->ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
-    hipLaunchKernelGGL(k_gather_rows, dim3((te + 255) / 256, n), dim3(256), 0, c->stream,
-                       (const uint16_t *) c->text_embd.data, (int64_t) te, c->ids, n, c->stage);
+    ProjWork w{c->ids, c->stage, c->tp_a, nullptr, nullptr};
     if (text_proj_tiled(c, n)) {
         if (n > c->bp_rows) {
             for (void * p : {(void *) c->bp_q, (void *) c->bp_dx, (void *) c->bp_h}) dev_free(c, p);
@@ -1315,28 +1396,9 @@ int project_rows(q3t_dev * c, const int32_t * tokens, int32_t n, float * dst) {
                 return -1;
             c->bp_rows = n;
         }
-        pf_linear_bias(c, c->fc1, te, te, n, c->stage, c->fc1_b, c->bp_h);
-        const size_t cnt = (size_t) n * te;
-        hipLaunchKernelGGL(k_silu_rows, dim3((unsigned) std::min<size_t>((cnt + 255) / 256, 4096)), dim3(256), 0,
-                           c->stream, c->bp_h, cnt);
-        pf_linear_bias(c, c->fc2, d, te, n, c->bp_h, c->fc2_b, dst);
-    } else {
-        for (int t0 = 0; t0 < n;) {
-            const int left = n - t0;
-            const int nt = left >= 4 ? 4 : left >= 2 ? 2 : 1;
-            GemvSpec a{};
-            a.w = weight_of(c->fc1); a.rows = te; a.K = te; a.x = c->stage + (size_t) t0 * te; a.x_stride = te;
-            a.y = c->tp_a; a.y_stride = te; a.bias = (const float *) c->fc1_b.data; a.epi = EPI_BIAS_SILU;
-            a.no_done = true;
-            gemv(c, a, nt);
-            GemvSpec b{};
-            b.w = weight_of(c->fc2); b.rows = d; b.K = te; b.x = c->tp_a; b.x_stride = te;
-            b.y = dst + (size_t) t0 * d; b.y_stride = d; b.bias = (const float *) c->fc2_b.data; b.epi = EPI_BIAS;
-            b.no_done = true;
-            gemv(c, b, nt);
-            t0 += nt;
-        }
+        w.h = c->bp_h; w.q = c->bp_q; w.dx = c->bp_dx;
     }
+    project_rows_core(c, n, w, dst);
     HIP_OK(hipGetLastError());
     return 0;
 }
@@ -1565,6 +1627,37 @@ int q3t_dev_text_proj(q3t_dev * c, const int32_t * tokens, int32_t n, float * ou
     if (ensure_build(c, n, 0, 0)) return -1;
     if (project_rows(c, tokens, n, c->bp_proj)) return -1;
     HIP_OK(hipMemcpyAsync(out, c->bp_proj, (size_t) n * g.hidden_size * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+int q3t_dev_text_proj_noalloc(q3t_dev * c, const int32_t * tokens, int32_t n, float * out) {
+    if (!c || !tokens || !out) return -1;
+    if (n <= 0) return 0;
+    if (n > kNoAllocMaxIds) return fail(c, "text_proj_noalloc: at most 64 ids per call");
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= g.text_vocab) return fail(c, "Embedding token ID out of range");
+    if (proj_tensors_ok(c)) return -1;
+    if (!c->scratch) return fail(c, "text_proj_noalloc: device scratch not set up");
+    const int te = g.text_embd_dim, d = g.hidden_size;
+    // carve the scratch: every region 256-byte aligned
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        unsigned char * p = c->scratch + off;
+        off += (bytes + 255) & ~(size_t) 255;
+        return p;
+    };
+    const size_t rows = (size_t) std::max(n, 4);   // the GEMV form writes fc1 rows in chunks of 4
+    int32_t * ids = (int32_t *) take((size_t) n * 4);
+    ProjWork w{ids, (float *) take(rows * te * 4), (float *) take(rows * te * 4), (int8_t *) take((size_t) n * te),
+               (float *) take((size_t) n * (te / kQK) * 4)};
+    float * res = (float *) take((size_t) n * d * 4);
+    if (off > kScratchBytes) return fail(c, "text_proj_noalloc: widths too large for the device scratch");
+    HIP_OK(hipMemcpyAsync(ids, tokens, (size_t) n * 4, hipMemcpyHostToDevice, c->stream));
+    project_rows_core(c, n, w, res);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpyAsync(out, res, (size_t) n * d * 4, hipMemcpyDeviceToHost, c->stream));
     return sync(c);
 }
 

@@ -19,7 +19,8 @@ EXPORTS = [
     "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
-    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_embed_rows", "q3t_dev_build_prefill",
+    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
+    "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
     "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
     "q3t_dev_streams_begin", "q3t_dev_streams_run", "q3t_dev_sync", "q3t_dev_time_kernel",
@@ -64,6 +65,7 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_talker_step.argtypes = [vp, f32p, i32, f32p, f32p]
         lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
         lib.q3t_dev_text_proj.argtypes = [vp, vp, i32, f32p]
+        lib.q3t_dev_text_proj_noalloc.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_embed_rows.argtypes = [vp, i32, i32, vp, i32, f32p]
         pi32 = ctypes.POINTER(i32)
         lib.q3t_dev_build_prefill.argtypes = [vp, vp, i32, f32p, i32, vp, i32, f32p, pi32, f32p, pi32, f32p]
@@ -181,6 +183,15 @@ class Device:
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         out = np.empty((len(tokens), self.cfg.hidden_size), np.float32)
         self._check(self.lib.q3t_dev_text_proj(self.h, _p(tokens), len(tokens), _p(out)), "text_proj")
+        return out
+
+    def text_proj_noalloc(self, tokens):
+        """q3t_dev_text_proj_noalloc: the same projection with no device
+        allocation (at most 64 ids; work buffers in the library's static
+        device scratch)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(tokens), self.cfg.hidden_size), np.float32)
+        self._check(self.lib.q3t_dev_text_proj_noalloc(self.h, _p(tokens), len(tokens), _p(out)), "text_proj_noalloc")
         return out
 
     def embed_rows(self, table, index, tokens):
