@@ -386,7 +386,7 @@ def main():
     kernels = {}
     names = {0: "gemv_gate_up_swiglu", 1: "gemv_qkv_rmsnorm", 2: "gemv_down_resid", 3: "gemv_wo_resid",
              4: "attention_decode"}
-    if args.kernel_iters > 0 or path != 1:
+    if args.kernel_iters > 0 or path not in (1, 3):
         for k, nm in names.items():
             us, b = dev.time_kernel(k, max(args.kernel_iters, 20))
             kernels[nm] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1) if us > 0 else None}
@@ -396,7 +396,7 @@ def main():
     kernels["k_copy16 (64 MiB device copy)"] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1)}
     dev.close()
     traffic = None
-    if path == 1:
+    if path in (1, 3):
         # HBM-side bytes per k_frame dispatch from the FETCH_SIZE / WRITE_SIZE
         # counter runs (calibrated on a 64 MiB copy kernel), when committed
         tp = os.path.join(ROOT, "profiles", "k_frame_q8_0_06b_traffic.json")
@@ -441,7 +441,7 @@ def main():
         "dtype": "int8" if args.weights == "q8_0" else "f16",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
         "config": {"workload": f"full frame loop, {args.weights.upper()} 0.6B shapes, {args.prompt}-token prompt, "
-                               f"greedy, " + ("one persistent kernel per frame" if path == 1 else "hipGraph per frame"),
+                               f"greedy, " + ("one persistent kernel per frame" + (", XCD-parallel layers" if path == 3 else "") if path in (1, 3) else "hipGraph per frame"),
                    "global_batch": 1, "frames": args.steps,
                    "weights": args.weights, "prompt_tokens": args.prompt, "prefill_rows": plen},
         "prefill_build_ms": round(build_s * 1e3, 3),

@@ -205,8 +205,9 @@ int  q3t_dev_frames_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
  * q3t_dev_streams_begin: GPU time of the frame launches (HIP events around
  * each frames_run / streams_run's launches, in microseconds), the number of
  * frame launches, and which implementation ran them (1 = one persistent
- * cooperative kernel per frame, 0 = the captured multi-kernel graph, 2 = the
- * multi-stream graph, one launch advancing every stream by a frame).  Instrumentation with no counterpart in the
+ * cooperative kernel per frame, 3 = the same with its XCD-parallel layer
+ * program, 0 = the captured multi-kernel graph, 2 = the multi-stream graph,
+ * one launch advancing every stream by a frame).  Instrumentation with no counterpart in the
  * reference; the benchmark and the tests use it. */
 int  q3t_dev_frames_stats(q3t_dev * dev, double * gpu_us_out, int64_t * frames_out,
                           int32_t * path_out);

@@ -135,6 +135,7 @@ struct q3t_dev {
     // persistent frame kernel (q3t_frame_kernel.h)
     bool fk_ok = false;            // model / context qualify this context for it
     int fk_variant = 0;            // see fk_kernel()
+    int xcd_map = -1;              // workgroup b of the frame launch on XCD b % 8: -1 unknown, 0 no, 1 yes
     bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
     bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
     int fk_grid = 0;
@@ -628,10 +629,11 @@ __global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, i
 // small test shapes.
 const void * fk_kernel(int variant) {
     switch (variant) {
-        case 1: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8>;
-        case 2: return (const void *) fk::k_frame<256, 512, 512, W_Q8>;
-        case 3: return (const void *) fk::k_frame<1024, 2048, 3072, W_F16>;
-        default: return (const void *) fk::k_frame<256, 512, 512, W_F16>;
+        case 1: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8, false>;
+        case 2: return (const void *) fk::k_frame<256, 512, 512, W_Q8, false>;
+        case 3: return (const void *) fk::k_frame<1024, 2048, 3072, W_F16, false>;
+        case 5: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8, true>;
+        default: return (const void *) fk::k_frame<256, 512, 512, W_F16, false>;
     }
 }
 
@@ -641,6 +643,45 @@ int slots_for(int K) {
     if (b == 64) return 2;
     if (b == 96) return 3;
     return 0;
+}
+
+// The XCD of each workgroup of a 256-workgroup cooperative launch with the
+// frame kernel's LDS footprint (one workgroup per CU, as the frame kernel).
+__global__ __launch_bounds__(fk::kT) void k_xcc_map(int32_t * out) {
+    __shared__ fk::Lds L;
+    if (threadIdx.x == 0) {
+        L.codes[0] = (int32_t) fk::xcc_id();
+        out[blockIdx.x] = L.codes[0];
+    }
+}
+
+// Whether workgroup b of the frame kernel's launch runs on XCD b % 8 (the
+// XCD-parallel layer program relies on it); checked once per context.
+int xcd_map_ok(q3t_dev * c, int grid, bool & ok) {
+    if (c->xcd_map < 0) {
+        int32_t * d = nullptr;
+        if (dev_alloc_t(c, &d, (size_t) grid)) return -1;
+        void * args[] = {&d};
+        std::vector<int32_t> h(grid, -1);
+        if (hipLaunchCooperativeKernel((const void *) k_xcc_map, dim3(grid), dim3(fk::kT), args, 0, c->stream) ==
+            hipSuccess) {
+            HIP_OK(hipMemcpyAsync(h.data(), d, (size_t) grid * 4, hipMemcpyDeviceToHost, c->stream));
+            HIP_OK(hipStreamSynchronize(c->stream));
+        } else {
+            (void) hipGetLastError();   // refused: the row-parallel program runs instead
+        }
+        dev_free(c, d);
+        int good = 0;
+        for (int b = 0; b < grid; ++b) good += h[b] == b % fk::kXcd;
+        c->xcd_map = good == grid ? 1 : 0;
+    }
+    ok = c->xcd_map == 1;
+    return 0;
+}
+
+const char * fk_err_msg(int32_t e) {
+    return e == 2 ? "frame kernel: a workgroup ran on another XCD than the XCD-parallel layers assume (results invalid)"
+                  : "frame kernel: a phase wait timed out (results invalid)";
 }
 
 int fk_prepare(q3t_dev * c) {
@@ -686,7 +727,17 @@ int fk_prepare(q3t_dev * c) {
     if (chunk_len > fk::kMaxChunk || chunks > 128 || (size_t) grid * 512 > (size_t) fk::kPvSlots * fk::kSlot ||
         (g.n_head * 128 + grid - 1) / grid * 2 * chunks > 2 * fk::kMaxChunk)
         return 0;
-    const int phases = 15 * (2 + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
+    // the XCD-parallel layer program: Q8_0 0.6B shapes, one workgroup per CU
+    // on 256 CUs with workgroup b on XCD b % 8 (Q3T_FRAME_XCD=0 turns it off)
+    bool xcd = variant == 1 && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0;
+    if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
+    if (xcd && xcd_map_ok(c, grid, xcd)) return -1;
+    if (xcd) variant = 5;
+    // arena slots: row-parallel layer 5 (code predictor) or 7 + kPvSlots
+    // (talker); XCD-parallel layer 15 or 17 + kPvSlots (device-wide partial
+    // sums take 4 slots, XCD-local rows 2)
+    const int phases = xcd ? 15 * (2 + 15 * g.cp_layers) + 1 + (17 + fk::kPvSlots) * g.n_layers
+                           : 15 * (2 + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
     if (phases >= 4096) return 0;
     if (!c->fk_layers || c->fk_layers_stale) {
         std::vector<fk::LayerQ8> t(g.n_layers + g.cp_layers);
@@ -1555,7 +1606,7 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     if (ran) {
         int32_t err = 0;
         std::memcpy(&err, c->pin + o_err, 4);
-        if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+        if (err) return fail(c, fk_err_msg(err));
     }
     return 0;
 }
@@ -1592,7 +1643,9 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     if (c->kc && fk_step(c, (int32_t) frame, fk::MODE_CODE_PRED, ran)) return -1;
     if (ran) {
         if (logits_out) {
-            const int stride = 2 + 5 * g.cp_layers, n = g.n_codebooks - 1;
+            // arena slots of one code-predictor pass (the input row, the
+            // layers, the head): the head's logits sit in its last slot
+            const int stride = 2 + (c->fk_variant == 5 ? 15 : 5) * g.cp_layers, n = g.n_codebooks - 1;
             hipLaunchKernelGGL(k_untag_heads, dim3((n * g.cp_vocab + 255) / 256), dim3(256), 0, c->stream,
                                c->fk_arena, stride - 1, stride, n, g.cp_vocab, c->cp_logits);
         }
@@ -1608,7 +1661,7 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     if (ran) {
         int32_t err = 0;
         std::memcpy(&err, c->pin + o_err, 4);
-        if (err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+        if (err) return fail(c, fk_err_msg(err));
     }
     FrameState r{};
     std::memcpy(&r, c->pin + o_out, sizeof r);
@@ -1904,7 +1957,7 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     int32_t fk_err = 0;
     if (c->fk_ok) HIP_OK(hipMemcpyAsync(&fk_err, c->fk_err, sizeof fk_err, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
-    if (fk_err) return fail(c, "frame kernel: a phase wait timed out (results invalid)");
+    if (fk_err) return fail(c, fk_err_msg(fk_err));
     if (n_frames > 0) {
         float ms = 0.0f;
         HIP_OK(hipEventElapsedTime(&ms, c->run_ev[0], c->run_ev[1]));
@@ -2416,7 +2469,7 @@ int q3t_dev_frames_stats(q3t_dev * c, double * gpu_us_out, int64_t * frames_out,
     if (!c) return -1;
     if (gpu_us_out) *gpu_us_out = c->run_us;
     if (frames_out) *frames_out = c->run_frames;
-    if (path_out) *path_out = c->stats_streams ? 2 : c->fk_ok ? 1 : 0;
+    if (path_out) *path_out = c->stats_streams ? 2 : c->fk_ok ? (c->fk_variant == 5 ? 3 : 1) : 0;
     return 0;
 }
 

@@ -100,10 +100,12 @@ struct Geo {
 // Thread t's share of NT input rows of width K: groups g = t + c * kT of 4
 // consecutive elements (4g .. 4g+3); 8 consecutive threads cover one Q8_0
 // block.  Groups with g >= K/4 belong to whole idle waves (K/4 % 64 == 0).
-template <int NT, int K>
-using RowsT = float[NT][Geo<K>::CHG][4];
 template <int K>
-using NormT = float[Geo<K>::CHG][4];
+constexpr int kChg = (K / 4 + kT - 1) / kT;        // groups of 4 per thread for width K
+template <int NT, int K>
+using RowsT = float[NT][kChg<K>][4];
+template <int K>
+using NormT = float[kChg<K>][4];
 
 struct Lds {
     alignas(16) float x[3072];                  // gathered layer-0 rows [nt][D] / sampler logits
@@ -119,6 +121,8 @@ struct Lds {
     };
     alignas(16) uint16_t cpk[kCpLayers][16 * 128];   // code-predictor KV of this workgroup's KV head
     alignas(16) uint16_t cpv[kCpLayers][16 * 128];
+    alignas(16) float att[2][256];              // XCD-parallel layers: this XCD's head-pair attention rows
+    float rx[2][32];                            // XCD-parallel layers: this workgroup's slice of the residual stream
     double red[2 * kW];
     float fred[2 * kW];
     int32_t ired[kW];
@@ -194,17 +198,52 @@ __device__ __forceinline__ float twait(const uint64_t * p, uint32_t tag, bool & 
     return __uint_as_float((uint32_t) v);
 }
 
+// XCD-local tagged I/O.  Workgroup b runs on XCD b % 8 (the host checks
+// this before it selects a kernel that relies on it), and the eight XCDs
+// have separate L2 caches.  Data exchanged only among the workgroups of one
+// XCD goes through that XCD's L2: a plain 64-bit store (wavefront scope),
+// polled with a load that skips the CU's L1 (system scope: sc0 sc1), at
+// about 0.7 us per hand-off against 1.1-1.9 us for the device-scope form.
+// A region written this way is only ever written and read by one XCD within
+// a launch, and never shares a cache line with another XCD's region.
+__device__ __forceinline__ uint64_t lload(const uint64_t * p) {
+    return __hip_atomic_load((const Q3T_GAS uint64_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void lstore(uint64_t * p, uint32_t tag, float v) {
+    __hip_atomic_store((Q3T_GAS uint64_t *) p, ((uint64_t) tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+// XL: XCD-local (lload / lstore) or device-wide (tload / tstore).
+template <bool XL>
+__device__ __forceinline__ uint64_t xload(const uint64_t * p) { return XL ? lload(p) : tload(p); }
+template <bool XL>
+__device__ __forceinline__ void xstore(uint64_t * p, uint32_t tag, float v) {
+    if (XL) lstore(p, tag, v);
+    else tstore(p, tag, v);
+}
+template <bool XL>
+__device__ __forceinline__ float xwait(const uint64_t * p, uint32_t tag, bool & dead, int32_t * err) {
+    uint64_t v = xload<XL>(p);
+    unsigned n = 0;
+    while ((uint32_t) (v >> 32) != tag && !dead) {
+        if (++n > kSpin) { dead = true; atomicExch(err, 1); break; }
+        __builtin_amdgcn_s_sleep(1);
+        v = xload<XL>(p);
+    }
+    return __uint_as_float((uint32_t) v);
+}
+
 // Waits for up to kB tagged elements at once: all loads are issued before
 // any tag is checked, and a re-poll reloads only the elements still missing,
 // so a thread pays about one round trip per batch instead of one per element.
 constexpr int kB = 8;
-template <int N>
+template <int N, bool XL = false>
 __device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[N], int cnt, uint32_t tag, float (&out)[N],
                                             bool & dead, int32_t * err) {
     uint64_t v[N];
     unsigned n = 0;
 #pragma unroll
-    for (int k = 0; k < N; ++k) v[k] = k < cnt ? tload(ptr[k]) : ((uint64_t) tag << 32);
+    for (int k = 0; k < N; ++k) v[k] = k < cnt ? xload<XL>(ptr[k]) : ((uint64_t) tag << 32);
     while (!dead) {
         bool all = true;
 #pragma unroll
@@ -214,19 +253,19 @@ __device__ __forceinline__ void twait_batch(const uint64_t * const (&ptr)[N], in
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < N; ++k)
-            if ((uint32_t) (v[k] >> 32) != tag) v[k] = tload(ptr[k]);
+            if ((uint32_t) (v[k] >> 32) != tag) v[k] = xload<XL>(ptr[k]);
     }
 #pragma unroll
     for (int k = 0; k < N; ++k) out[k] = __uint_as_float((uint32_t) v[k]);
 }
 
-// Thread t's groups of rows [NT][K] of a tagged slot (row stride kHS), in
+// Thread t's groups of rows [NT][K] of a tagged slot (row stride ts), in
 // batches of up to 12 loads ordered group-major, so the valid loads of a
-// thread always form a prefix of each batch.
-template <int NT, int K>
+// thread always form a prefix of each batch.  XL: an XCD-local slot.
+template <int NT, int K, bool XL = false>
 __device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag, RowsT<NT, K> & v, bool & dead,
-                                            int32_t * err) {
-    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4, F = CHG * NT * 4;
+                                            int32_t * err, int ts = kHS) {
+    constexpr int CHG = kChg<K>, G4 = K / 4, F = CHG * NT * 4;
     constexpr int NB = F <= 12 ? F : (F % 12 == 0 ? 12 : 8);
     static_assert(F % NB == 0, "batch split");
 #pragma unroll
@@ -238,11 +277,11 @@ __device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag,
             const int f = f0 + k, c = f / (NT * 4), tok = (f / 4) % NT, e = f % 4;
             const int g = (int) threadIdx.x + kT * c;
             const bool ok = g < G4;
-            ptr[k] = slot + (size_t) tok * kHS + (ok ? 4 * g + e : 0);
+            ptr[k] = slot + (size_t) tok * ts + (ok ? 4 * g + e : 0);
             if (ok) cnt = k + 1;
         }
         float val[NB];
-        twait_batch<NB>(ptr, cnt, tag, val, dead, err);
+        twait_batch<NB, XL>(ptr, cnt, tag, val, dead, err);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             const int f = f0 + k, c = f / (NT * 4), tok = (f / 4) % NT, e = f % 4;
@@ -253,15 +292,15 @@ __device__ __forceinline__ void load_tagged(const uint64_t * slot, uint32_t tag,
 
 // The same groups from plain LDS rows x [NT][K].
 template <int NT, int K>
-__device__ __forceinline__ void load_lds(const float * x, RowsT<NT, K> & v) {
-    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4;
+__device__ __forceinline__ void load_lds(const float * x, RowsT<NT, K> & v, int ts = K) {
+    constexpr int CHG = kChg<K>, G4 = K / 4;
 #pragma unroll
     for (int c = 0; c < CHG; ++c) {
         const int g = (int) threadIdx.x + kT * c;
         if (g >= G4) break;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float4 q = *(const float4 *) (x + t * K + 4 * g);
+            const float4 q = *(const float4 *) (x + t * ts + 4 * g);
             v[t][c][0] = q.x; v[t][c][1] = q.y; v[t][c][2] = q.z; v[t][c][3] = q.w;
         }
     }
@@ -329,11 +368,12 @@ __device__ __forceinline__ void rms_rows(RowsT<NT, K> & v, const NormT<K> & nw, 
 // shared by 4 elements.
 template <int NT, int K>
 __device__ __forceinline__ void quant_rows(const RowsT<NT, K> & v, Lds & L) {
-    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4, BPR = K / kQK;
+    constexpr int CHG = kChg<K>, G4 = K / 4, BPR = K / kQK;
+    static_assert(K % kQK == 0, "whole Q8_0 blocks");
 #pragma unroll
     for (int c = 0; c < CHG; ++c) {
         const int g = (int) threadIdx.x + kT * c;
-        if (g >= G4) break;                 // whole waves (G4 % 64 == 0)
+        if (g >= G4) break;                 // whole 8-lane blocks (K % 32 == 0)
         const int b = g >> 3, eo = (g & 7) * 4;
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) {
@@ -849,22 +889,26 @@ __device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
 // waves w and w + 2 both handle query head 2g + (w & 1): each computes the
 // (at most 16) scores and the softmax, and forms 64 of the head's 128 output
 // dims, so all four waves work and no workgroup barrier is needed.
+// XL (XCD-parallel layers): every workgroup of XCD g runs KV head g, reading
+// its rows [q0 q1 k v] (512 per token) from the XCD's local QKV region and
+// leaving the attention rows in L.att instead of publishing them.
+template <bool XL>
 __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                             int nt, int pos0, int qd, const uint64_t * qkv,
                                                             uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
                                                             bool & dead) {
-    const int g = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = XL ? (int) (blockIdx.x & 7) : (int) blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kd = qd / 2;
     const bool f32 = nt == 2;              // the prefill: unrounded q, K, V, P
     float * qf = L.a;                      // [tok][head][128] rotated q (fp16-rounded in a step)
     float * kf = L.a + 4 * 128;            // prefill: [tok][128] rotated k, fp32
     float * vf = L.a + 6 * 128;            // prefill: [tok][128] v, fp32
     {
-        const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
+        const int col = XL ? wave * 128 : wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const uint64_t * ptr[kB];
 #pragma unroll
         for (int tok = 0; tok < 2; ++tok) {
-            const uint64_t * row = qkv + (size_t) (tok < nt ? tok : 0) * kHS + col;
+            const uint64_t * row = qkv + (size_t) (tok < nt ? tok : 0) * (XL ? 512 : kHS) + col;
             ptr[2 * tok] = row + lane;
             ptr[2 * tok + 1] = row + lane + 64;
         }
@@ -881,7 +925,7 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
             rsv[tok] = gld(A.cp_rope_sin + (size_t) pos * 64 + lane);
         }
         float val[kB];
-        twait_batch<kB>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
+        twait_batch<kB, XL>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
         for (int tok = 0; tok < nt; ++tok) {
             const int pos = pos0 + tok;
             const float x0 = val[2 * tok], x1 = val[2 * tok + 1];
@@ -969,7 +1013,8 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
             const double pj = (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), j * 4));
             o = fma(pj, (double) vv[j], o);
         }
-        tstore(out + (size_t) tok * kHS + (g * 2 + hq) * 128 + d, out_tag, (float) o);
+        if (XL) L.att[tok][hq * 128 + d] = (float) o;
+        else tstore(out + (size_t) tok * kHS + (g * 2 + hq) * 128 + d, out_tag, (float) o);
     }
     __syncthreads();
 }
@@ -1034,6 +1079,10 @@ __device__ __forceinline__ void att_prefetch(const Args & A, int layer, const At
 
 // score_out != nullptr (two-phase form): the chunk's scores themselves are
 // published at score_out[(2g + h) * kScoreRow + j] instead of its maxima.
+// XL (XCD-parallel layers): q, k, v come from this XCD's local QKV region
+// ([q0 q1 k v]), and the scores or maxima go to XCD-local regions per KV
+// head (maxima at g * 64 + 2c + h).
+template <bool XL>
 __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                           int pos0, int qd, const AttSplit & s, const KvPre & P,
                                                           const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out,
@@ -1046,13 +1095,13 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
     float * vnew = knew + 128;             // [128]
     const size_t base = ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
     {
-        const int col = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
+        const int col = XL ? wave * 128 : wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
         const float nw0 = gld(nwp + lane), nw1 = gld(nwp + lane + 64);
         const float rcv = gld(A.rope_cos + (size_t) pos0 * 64 + lane), rsv = gld(A.rope_sin + (size_t) pos0 * 64 + lane);
         const uint64_t * ptr[2] = {qkv + col + lane, qkv + col + lane + 64};
         float val[2];
-        twait_batch<2>(ptr, 2, qkv_tag, val, dead, A.err);
+        twait_batch<2, XL>(ptr, 2, qkv_tag, val, dead, A.err);
         const float x0 = val[0], x1 = val[1];
         const bool writer = s.c == 0;      // one workgroup per KV head appends the new rows
         if (wave < 3) {
@@ -1128,8 +1177,8 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
             const float s0 = (float) a0 * A.attn_scale, s1 = (float) a1 * A.attn_scale;
             if (sub == 0) {
                 if (score_out) {
-                    tstore(score_out + (size_t) (2 * g) * kScoreRow + j, out_tag, s0);
-                    tstore(score_out + (size_t) (2 * g + 1) * kScoreRow + j, out_tag, s1);
+                    xstore<XL>(score_out + (size_t) (2 * g) * kScoreRow + j, out_tag, s0);
+                    xstore<XL>(score_out + (size_t) (2 * g + 1) * kScoreRow + j, out_tag, s1);
                 } else {
                     L.sc[j - s.j0] = s0;
                     L.sc[kMaxChunk + j - s.j0] = s1;
@@ -1148,17 +1197,21 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
         float m = L.fred[t * kW];
 #pragma unroll
         for (int w = 1; w < kW; ++w) m = fmaxf(m, L.fred[t * kW + w]);
-        tstore(out + blockIdx.x * 2 + t, out_tag, m);
+        if (XL) lstore(out + g * 64 + s.c * 2 + t, out_tag, m);
+        else tstore(out + blockIdx.x * 2 + t, out_tag, m);
     }
 }
 
+template <bool XL>
 __device__ __attribute__((always_inline)) void att_sums(const Args & A, Lds & L, const AttSplit & s,
                                                         const uint64_t * in, uint32_t in_tag, uint64_t * out,
                                                         uint32_t out_tag, bool & dead) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, H = A.n_kv_head;
     float * gm = L.a + 4 * 128;            // [C][2] chunk maxima of this KV head
     if (s.c < s.C) {
-        for (int i = t; i < 2 * s.C; i += kT) gm[i] = twait(in + (s.g + (i >> 1) * H) * 2 + (i & 1), in_tag, dead, A.err);
+        for (int i = t; i < 2 * s.C; i += kT)
+            gm[i] = XL ? xwait<true>(in + s.g * 64 + i, in_tag, dead, A.err)
+                       : twait(in + (s.g + (i >> 1) * H) * 2 + (i & 1), in_tag, dead, A.err);
     }
     __syncthreads();
     if (s.c >= s.C) return;
@@ -1179,11 +1232,13 @@ __device__ __attribute__((always_inline)) void att_sums(const Args & A, Lds & L,
         double sm = L.red[t * kW];
 #pragma unroll
         for (int w = 1; w < kW; ++w) sm += L.red[t * kW + w];
-        tstore(out + blockIdx.x * 4 + 2 * t, out_tag, __int_as_float(__double2loint(sm)));
-        tstore(out + blockIdx.x * 4 + 2 * t + 1, out_tag, __int_as_float(__double2hiint(sm)));
+        uint64_t * dst = XL ? out + s.g * 128 + s.c * 4 + 2 * t : out + blockIdx.x * 4 + 2 * t;
+        xstore<XL>(dst, out_tag, __int_as_float(__double2loint(sm)));
+        xstore<XL>(dst + 1, out_tag, __int_as_float(__double2hiint(sm)));
     }
 }
 
+template <bool XL>
 __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, int layer, int pos0,
                                                       const AttSplit & s, const KvPre & P, const uint64_t * in,
                                                       uint32_t in_tag, uint64_t * out, uint32_t out_tag,
@@ -1192,7 +1247,8 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
     uint32_t * gs = (uint32_t *) (L.a + 4 * 128);   // [C][2 heads][2 halves] chunk sums
     if (s.c < s.C) {
         for (int i = t; i < 4 * s.C; i += kT)
-            gs[i] = __float_as_uint(twait(in + (s.g + (i >> 2) * H) * 4 + (i & 3), in_tag, dead, A.err));
+            gs[i] = __float_as_uint(XL ? xwait<true>(in + s.g * 128 + i, in_tag, dead, A.err)
+                                       : twait(in + (s.g + (i >> 2) * H) * 4 + (i & 3), in_tag, dead, A.err));
     }
     __syncthreads();
     if (s.c >= s.C) return;
@@ -1266,9 +1322,9 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
         double r = part[h * 128 + d];
 #pragma unroll
         for (int w = 1; w < kW; ++w) r += part[(w * 2 + h) * 128 + d];
-        uint64_t * dst = out + (size_t) blockIdx.x * 512 + h * 256 + d * 2;
-        tstore(dst, out_tag, __int_as_float(__double2loint(r)));
-        tstore(dst + 1, out_tag, __int_as_float(__double2hiint(r)));
+        uint64_t * dst = out + (size_t) (XL ? s.g * s.C + s.c : (int) blockIdx.x) * 512 + h * 256 + d * 2;
+        xstore<XL>(dst, out_tag, __int_as_float(__double2loint(r)));
+        xstore<XL>(dst + 1, out_tag, __int_as_float(__double2hiint(r)));
     }
 }
 
@@ -1304,6 +1360,9 @@ __device__ __forceinline__ void att2_prefetch(const Args & A, int layer, int pos
     }
 }
 
+// XL: the scores come from XCD-local regions, and the attention rows of the
+// head pair go to this XCD's local region (out [h * 128 + d]).
+template <bool XL>
 __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, int pos0, const KvCols & P,
                                                        const uint64_t * scores, uint32_t sc_tag, uint64_t * out,
                                                        uint32_t out_tag, bool & dead) {
@@ -1324,7 +1383,7 @@ __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, 
             if (i < 2 * n_kv) cnt = k + 1;
         }
         float val[kB];
-        twait_batch<kB>(ptr, cnt, sc_tag, val, dead, A.err);
+        twait_batch<kB, XL>(ptr, cnt, sc_tag, val, dead, A.err);
 #pragma unroll
         for (int k = 0; k < kB; ++k) {
             const int i = i0 + k * kT + t;
@@ -1397,36 +1456,43 @@ __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, 
         double r = part[h * 4 + d];
 #pragma unroll
         for (int w = 1; w < kW; ++w) r += part[(w * 2 + h) * 4 + d];
-        tstore(out + (g * 2 + h) * 128 + c * dpw + d, out_tag, (float) r);
+        if (XL) lstore(out + h * 128 + c * dpw + d, out_tag, (float) r);
+        else tstore(out + (g * 2 + h) * 128 + c * dpw + d, out_tag, (float) r);
     }
 }
 
 // Phase D: 8 attention outputs per workgroup (n_head * 128 over the grid),
 // each the chunk-ordered fp64 sum of its KV head's C partials.
+// XL: workgroup (g, c) combines outputs [8c, 8c + 8) of KV head g's pair
+// (256 rows) from the head's XCD-local partials and writes them to the XCD's
+// local region (out [o]).
+template <bool XL>
 __device__ __attribute__((always_inline)) void att_combine(const Args & A, Lds & L, const uint64_t * in,
                                                            uint32_t in_tag, uint64_t * out, uint32_t out_tag,
                                                            bool & dead) {
     const int t = threadIdx.x, H = A.n_kv_head, C = (int) gridDim.x / H;
-    const int n_out = A.n_head * 128;
-    const int opw = (n_out + (int) gridDim.x - 1) / (int) gridDim.x;   // outputs per workgroup
+    const int n_out = XL ? 256 : A.n_head * 128;
+    const int opw = XL ? 256 / C : (n_out + (int) gridDim.x - 1) / (int) gridDim.x;   // outputs per workgroup
+    const int gx = (int) blockIdx.x % H, cx = (int) blockIdx.x / H;
     uint32_t * w = (uint32_t *) L.sc;        // [opw][C][2]
     for (int i = t; i < opw * 2 * C; i += kT) {
         const int k = i / (2 * C), c = (i >> 1) % C, half = i & 1;
-        const int o = (int) blockIdx.x * opw + k;
+        const int o = (XL ? cx : (int) blockIdx.x) * opw + k;
         uint32_t v = 0;
         if (o < n_out) {
-            const int hq = o >> 7, d = o & 127, g = hq >> 1, hh = hq & 1;
-            v = __float_as_uint(twait(in + (size_t) (g + c * H) * 512 + hh * 256 + d * 2 + half, in_tag, dead, A.err));
+            const int hq = o >> 7, d = o & 127, g = XL ? gx : hq >> 1, hh = hq & 1;
+            const size_t src = (size_t) (XL ? g * C + c : g + c * H) * 512 + hh * 256 + d * 2 + half;
+            v = __float_as_uint(XL ? xwait<true>(in + src, in_tag, dead, A.err) : twait(in + src, in_tag, dead, A.err));
         }
         w[i] = v;
     }
     __syncthreads();
     if (t < opw) {
-        const int o = (int) blockIdx.x * opw + t;
+        const int o = (XL ? cx : (int) blockIdx.x) * opw + t;
         if (o < n_out) {
             double r = 0.0;
             for (int c = 0; c < C; ++c) r += __hiloint2double((int) w[(t * C + c) * 2 + 1], (int) w[(t * C + c) * 2]);
-            tstore(out + o, out_tag, (float) r);
+            xstore<XL>(out + o, out_tag, (float) r);
         }
     }
     __syncthreads();
@@ -1569,7 +1635,7 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (cp) {
         p_att = p++;
         if ((int) blockIdx.x < A.n_kv_head)
-            attention_cp(A, L, W, layer, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+            attention_cp<false>(A, L, W, layer, NT, pos0, QD, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
                          ar + (size_t) p_att * kSlot, tb | p_att, dead);
         __syncthreads();
     } else if (two_phase) {
@@ -1579,25 +1645,25 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         const int p_a = p;
         p += 2 + kPvSlots;
         p_att = p++;
-        att_scores(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+        att_scores<false>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
                    ar + (size_t) p_a * kSlot, tb | p_a, dead, ar + (size_t) p_a * kSlot);
         __syncthreads();
-        att2_pv(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot, tb | p_att, dead);
+        att2_pv<false>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot, tb | p_att, dead);
         __syncthreads();
     } else {
         const AttSplit sp = att_split(A, pos0 + 1);
         const int p_a = p++, p_b = p++, p_c = p;
         p += kPvSlots;
         p_att = p++;
-        att_scores(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+        att_scores<false>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
                    ar + (size_t) p_a * kSlot, tb | p_a, dead);
         __syncthreads();
-        att_sums(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
+        att_sums<false>(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
         __syncthreads();
-        att_pv(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot, tb | p_c,
+        att_pv<false>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot, tb | p_c,
                dead);
         __syncthreads();
-        att_combine(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot, tb | p_att, dead);
+        att_combine<false>(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot, tb | p_att, dead);
     }
     // Wo + residual (the block input)
     const int p_wo = p++;
@@ -1670,6 +1736,318 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     p_out = p_dn;
 }
 
+// ---------------------------------------------------- XCD-parallel layers
+// The 0.6B shapes (hidden 1024, 16 query / 8 KV heads, FFN 3072) on 256
+// workgroups, workgroup b on XCD x = b % 8 with rank j = b / 8 among the
+// XCD's 32.  XCD x owns KV head x (query heads 2x, 2x+1) and the FFN
+// columns [384x, 384x + 384); a layer is
+//   QKV      XCD x: its heads' 512 rows, 16 per workgroup        -> XCD-local
+//   attn     code predictor: every workgroup of XCD x, the cache in its
+//            LDS; talker: the split attention of KV head x, whose 32 chunk
+//            workgroups are XCD x's                            -> XCD-local
+//   Wo       rows [32j, 32j+32) over the head pair's 256 inputs: fp64
+//            partial sums                                      -> device-wide
+//   reduce   rank j of every XCD adds the 8 XCDs' partials of its 32 outputs
+//            in XCD order, rounds once, adds its residual slice -> XCD-local
+//   gate/up  columns [384x + 12j, +12) of both, SwiGLU          -> XCD-local
+//   down     rows [32j, 32j+32) over the XCD's 384 inputs      -> device-wide
+//   reduce   as above                                          -> XCD-local
+// Each workgroup computes as many GEMV rows per phase as in the row-parallel
+// program, but only the two reductions cross XCDs.  Sums stay exact fp64
+// sums of exact terms, rounded to fp32 once.
+constexpr int kXcd = 8;                // XCDs = KV heads
+constexpr int kXcdWg = 32;             // workgroups per XCD
+
+enum XKind : int { XK_QKV = 0, XK_GU = 1, XK_WO = 2, XK_DN = 3 };
+// K: the slice of a weight row one phase reads; KS: the full row; LPR lanes
+// per row (one 32-element block each, lanes past K/32 idle); NG row groups
+// per wave.
+template <int KIND> struct XGeo;
+template <> struct XGeo<XK_QKV> { static constexpr int K = 1024, KS = 1024, LPR = 32, NG = 2; static constexpr bool DUAL = false; };
+template <> struct XGeo<XK_GU> { static constexpr int K = 1024, KS = 1024, LPR = 32, NG = 2; static constexpr bool DUAL = true; };
+template <> struct XGeo<XK_WO> { static constexpr int K = 256, KS = 2048, LPR = 8, NG = 1; static constexpr bool DUAL = false; };
+template <> struct XGeo<XK_DN> { static constexpr int K = 384, KS = 3072, LPR = 16, NG = 2; static constexpr bool DUAL = false; };
+
+// This lane's row in group gi: weight row r, output index o, offset k0 of
+// the slice in the row.  False when the group is past the phase's rows
+// (the same for every lane of a wave).
+template <int KIND>
+__device__ __forceinline__ bool xrow(int gi, int & r, int & o, int & k0) {
+    constexpr int RPW = 64 / XGeo<KIND>::LPR;
+    const int x = (int) blockIdx.x & 7, j = (int) blockIdx.x >> 3, w = (int) threadIdx.x >> 6;
+    const int rsub = ((int) threadIdx.x & 63) / XGeo<KIND>::LPR;
+    if (KIND == XK_QKV) {
+        // local rows [q head 2x | q head 2x+1 | k | v] of KV head x
+        const int lr = j * 16 + (w * 2 + gi) * RPW + rsub;
+        r = lr < 256 ? 256 * x + lr : lr < 384 ? 2048 + 128 * x + (lr - 256) : 3072 + 128 * x + (lr - 384);
+        o = lr;
+        k0 = 0;
+        return true;
+    } else if (KIND == XK_GU) {
+        const int gg = w + gi * 4;          // 6 groups over 4 waves
+        const int col = j * 12 + gg * RPW + rsub;
+        r = 384 * x + col;
+        o = col;
+        k0 = 0;
+        return gg < 6;
+    } else if (KIND == XK_WO) {
+        r = o = j * 32 + w * RPW + rsub;
+        k0 = 256 * x;
+        return true;
+    } else {
+        r = o = j * 32 + (w * 2 + gi) * RPW + rsub;
+        k0 = 384 * x;
+        return true;
+    }
+}
+
+template <int KIND>
+struct XRegs {
+    int4 w[XGeo<KIND>::NG][2], u[XGeo<KIND>::DUAL ? XGeo<KIND>::NG : 1][2];
+    uint16_t dw[XGeo<KIND>::NG], du[XGeo<KIND>::DUAL ? XGeo<KIND>::NG : 1];
+    int o[XGeo<KIND>::NG];                 // output index of this lane's row, -1: none
+};
+
+// The Q8_0 blocks of this lane's rows, loaded before the phase input is awaited.
+template <int KIND, bool NTL>
+__device__ __forceinline__ void xq8_prefetch(XRegs<KIND> & R, const int8_t * W, const uint16_t * Wd, const int8_t * U,
+                                             const uint16_t * Ud) {
+    using G = XGeo<KIND>;
+    constexpr int BPR = G::K / kQK;
+    const int lir = (int) threadIdx.x & (G::LPR - 1);
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi) {
+        int r, o, k0;
+        const bool row = xrow<KIND>(gi, r, o, k0);
+        R.o[gi] = row ? o : -1;
+        R.w[gi][0] = R.w[gi][1] = make_int4(0, 0, 0, 0);
+        R.dw[gi] = 0;
+        if (G::DUAL) { R.u[G::DUAL ? gi : 0][0] = R.u[G::DUAL ? gi : 0][1] = make_int4(0, 0, 0, 0); R.du[G::DUAL ? gi : 0] = 0; }
+        if (!row || lir >= BPR) continue;
+        const int4 * wp = (const int4 *) (W + (size_t) r * G::KS + k0 + lir * kQK);
+        R.w[gi][0] = gld4n<NTL>(wp);
+        R.w[gi][1] = gld4n<NTL>(wp + 1);
+        R.dw[gi] = gldn<NTL>(Wd + (size_t) r * (G::KS / kQK) + k0 / kQK + lir);
+        if (G::DUAL) {
+            const int4 * up = (const int4 *) (U + (size_t) r * G::KS + k0 + lir * kQK);
+            R.u[G::DUAL ? gi : 0][0] = gld4n<NTL>(up);
+            R.u[G::DUAL ? gi : 0][1] = gld4n<NTL>(up + 1);
+            R.du[G::DUAL ? gi : 0] = gldn<NTL>(Ud + (size_t) r * (G::KS / kQK) + k0 / kQK + lir);
+        }
+    }
+}
+
+// The dot products over the quantised LDS input (NT rows of K/32 blocks) and
+// the phase's epilogue: QKV stores its rows and gate/up its SwiGLU outputs
+// XCD-locally at out[t * ts + o]; Wo and down publish fp64 partial sums
+// device-wide at out[((x * 2 + t) * 1024 + o) * 2 + half].
+template <int NT, int KIND>
+__device__ __forceinline__ void xq8_compute(const XRegs<KIND> & R, const Lds & L, uint64_t * out, int ts,
+                                            uint32_t out_tag) {
+    using G = XGeo<KIND>;
+    constexpr int BPR = G::K / kQK;
+    const int lir = (int) threadIdx.x & (G::LPR - 1), x = (int) blockIdx.x & 7;
+    const int b = lir < BPR ? lir : 0;
+    double acc[G::NG][NT], acc2[G::NG][NT];
+    float sw[G::NG], su[G::NG];
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi) {
+        // the empty asm keeps the scale conversion (and the wait for its load)
+        // out of the prefetch
+        uint32_t a = R.dw[gi], c = G::DUAL ? R.du[G::DUAL ? gi : 0] : 0u;
+        asm volatile("" : "+v"(a), "+v"(c));
+        sw[gi] = h2f((uint16_t) a);
+        su[gi] = h2f((uint16_t) c);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int4 x0 = *(const int4 *) &L.qlo[(t * BPR + b) * 16];
+        const int4 x1 = *(const int4 *) &L.qhi[(t * BPR + b) * 16];
+        const float dx = L.qdx[t * BPR + b];
+#pragma unroll
+        for (int gi = 0; gi < G::NG; ++gi) {
+            // fp16(d_w) * fp16(d_x) is exact in fp32, its product with the int32
+            // block sum exact in fp64; lanes past the slice add nothing
+            acc[gi][t] = lir < BPR ? (double) (sw[gi] * dx) * (double) dot32_i8(R.w[gi][0], R.w[gi][1], x0, x1) : 0.0;
+            acc2[gi][t] = G::DUAL && lir < BPR
+                              ? (double) (su[gi] * dx) *
+                                    (double) dot32_i8(R.u[G::DUAL ? gi : 0][0], R.u[G::DUAL ? gi : 0][1], x0, x1)
+                              : 0.0;
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi) {
+        if (R.o[gi] < 0) continue;          // wave-uniform
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const double a1 = group_sum_d(acc[gi][t], G::LPR);
+            const double a2 = G::DUAL ? group_sum_d(acc2[gi][t], G::LPR) : 0.0;
+            if (lir != 0) continue;
+            const int o = R.o[gi];
+            if (KIND == XK_QKV) {
+                lstore(out + t * ts + o, out_tag, (float) a1);
+            } else if (KIND == XK_GU) {
+                lstore(out + t * ts + o, out_tag, silu_q3t((float) a1) * (float) a2);
+            } else {
+                uint64_t * dst = out + ((size_t) (x * 2 + t) * 1024 + o) * 2;
+                tstore(dst, out_tag, __int_as_float(__double2loint(a1)));
+                tstore(dst + 1, out_tag, __int_as_float(__double2hiint(a1)));
+            }
+        }
+    }
+}
+
+// Rank j's 32 outputs of a device-wide partial slot: the 8 XCDs' fp64
+// partials added in XCD order and rounded once, plus the residual slice
+// L.rx, which takes the sum; the sums also go to the XCD-local row
+// outl[t * 1024 + 32j + i].  Thread t < 32 * NT handles output t & 31 of
+// token t >> 5, the same thread that keeps that element of L.rx.
+template <int NT>
+__device__ __forceinline__ void xreduce(const Args & A, Lds & L, const uint64_t * part, uint32_t ptag, uint64_t * outl,
+                                        uint32_t otag, bool & dead) {
+    const int t = (int) threadIdx.x, j = (int) blockIdx.x >> 3;
+    const int i = t >> 3, xs = t & 7, o = 32 * j + i;
+    const uint64_t * ptr[4];
+#pragma unroll
+    for (int tok = 0; tok < 2; ++tok) {
+        const uint64_t * src = part + ((size_t) (xs * 2 + (tok < NT ? tok : 0)) * 1024 + o) * 2;
+        ptr[2 * tok] = src;
+        ptr[2 * tok + 1] = src + 1;
+    }
+    float val[4];
+    twait_batch<4>(ptr, 2 * NT, ptag, val, dead, A.err);
+    double * rd = (double *) L.sc;          // [NT][32 outputs][8 XCDs]
+#pragma unroll
+    for (int tok = 0; tok < NT; ++tok)
+        rd[(tok * 32 + i) * kXcd + xs] = __hiloint2double(__float_as_int(val[2 * tok + 1]), __float_as_int(val[2 * tok]));
+    __syncthreads();
+    if (t < 32 * NT) {
+        const int tok = t >> 5, ii = t & 31;
+        double sm = 0.0;
+#pragma unroll
+        for (int k = 0; k < kXcd; ++k) sm += rd[(tok * 32 + ii) * kXcd + k];
+        const float v = (float) sm + L.rx[tok][ii];
+        L.rx[tok][ii] = v;
+        lstore(outl + tok * 1024 + 32 * j + ii, otag, v);
+    }
+    __syncthreads();
+}
+
+// One XCD-parallel layer for NT tokens (Q8_0 weights).  Input: the rows
+// gathered into LDS (layer 0) or this XCD's local copy of the previous
+// layer's output (slot p_in); output: slot p_out (XCD-local copies).  The
+// slot numbering keeps one slot per phase (partials: 4, local rows: 2).
+template <int NT, bool TK>
+__device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp,
+                                                       int pos0, uint32_t tb, int & p, int p_in, const float * x_lds,
+                                                       int & p_out, bool & dead) {
+    constexpr int D = 1024, QD = 2048;
+    uint64_t * ar = A.arena;
+    const int x = (int) blockIdx.x & 7, j = (int) blockIdx.x >> 3, t = (int) threadIdx.x;
+    KvPre kv;
+    KvCols kc2;
+    const bool two_phase = !cp && att_two_phase(A, pos0 + 1);
+    if (!cp) att_prefetch(A, layer, att_split(A, pos0 + 1), pos0, kv);
+    if (two_phase) att2_prefetch(A, layer, pos0, kc2);
+    // QKV rows of KV head x -> local [NT][512]
+    const int p_qkv = p++;
+    uint64_t * qkv_l = ar + (size_t) p_qkv * kSlot + x * 1024;
+    {
+        XRegs<XK_QKV> R;
+        xq8_prefetch<XK_QKV, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr);
+        NormT<D> nw;
+        norm_prefetch<D>(W.attn_norm, nw);
+        RowsT<NT, D> v;
+        if (x_lds) {
+            load_lds<NT, D>(x_lds, v);
+            if (t < 32 * NT) L.rx[t >> 5][t & 31] = x_lds[(t >> 5) * D + 32 * j + (t & 31)];
+        } else {
+            load_tagged<NT, D, true>(ar + (size_t) p_in * kSlot + x * 2048, tb | p_in, v, dead, A.err, D);
+        }
+        rms_rows<NT, D>(v, nw, A.eps, L);
+        quant_rows<NT, D>(v, L);
+        xq8_compute<NT, XK_QKV>(R, L, qkv_l, 512, tb | p_qkv);
+    }
+    __syncthreads();
+    // attention of KV head x
+    int p_att = 0;
+    if (cp) {
+        p_att = p++;
+        attention_cp<true>(A, L, W, layer, NT, pos0, QD, qkv_l, tb | p_qkv, nullptr, 0, dead);
+    } else if (two_phase) {
+        const AttSplit sp = att_split(A, pos0 + 1);
+        const int p_a = p;
+        p += 2 + kPvSlots;
+        p_att = p++;
+        att_scores<true>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead,
+                         ar + (size_t) p_a * kSlot);
+        __syncthreads();
+        att2_pv<true>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot + x * 1024,
+                      tb | p_att, dead);
+        __syncthreads();
+    } else {
+        const AttSplit sp = att_split(A, pos0 + 1);
+        const int p_a = p++, p_b = p++, p_c = p;
+        p += kPvSlots;
+        p_att = p++;
+        att_scores<true>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead);
+        __syncthreads();
+        att_sums<true>(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
+        __syncthreads();
+        att_pv<true>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot,
+                     tb | p_c, dead);
+        __syncthreads();
+        att_combine<true>(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot + x * 1024, tb | p_att,
+                          dead);
+    }
+    // Wo partial sums over the head pair's 256 inputs -> device-wide
+    const int p_wo = p;
+    p += 4;
+    {
+        XRegs<XK_WO> R;
+        xq8_prefetch<XK_WO, TK>(R, W.wo, W.wo_d, nullptr, nullptr);
+        RowsT<NT, 256> va;
+        if (cp) load_lds<NT, 256>(&L.att[0][0], va, 256);
+        else load_tagged<NT, 256, true>(ar + (size_t) p_att * kSlot + x * 1024, tb | p_att, va, dead, A.err, 256);
+        quant_rows<NT, 256>(va, L);
+        xq8_compute<NT, XK_WO>(R, L, ar + (size_t) p_wo * kSlot, 0, tb | p_wo);
+    }
+    __syncthreads();
+    const int p_x1 = p;
+    p += 2;
+    xreduce<NT>(A, L, ar + (size_t) p_wo * kSlot, tb | p_wo, ar + (size_t) p_x1 * kSlot + x * 2048, tb | p_x1, dead);
+    // gate/up + SwiGLU of FFN columns [384x + 12j, +12) -> local [NT][384]
+    const int p_gu = p++;
+    {
+        XRegs<XK_GU> R;
+        xq8_prefetch<XK_GU, TK>(R, W.wg, W.wg_d, W.wu, W.wu_d);
+        NormT<D> nw;
+        norm_prefetch<D>(W.ffn_norm, nw);
+        RowsT<NT, D> v;
+        load_tagged<NT, D, true>(ar + (size_t) p_x1 * kSlot + x * 2048, tb | p_x1, v, dead, A.err, D);
+        rms_rows<NT, D>(v, nw, A.eps, L);
+        quant_rows<NT, D>(v, L);
+        xq8_compute<NT, XK_GU>(R, L, ar + (size_t) p_gu * kSlot + x * 1024, 384, tb | p_gu);
+    }
+    __syncthreads();
+    // down partial sums over the XCD's 384 FFN inputs -> device-wide
+    const int p_dn = p;
+    p += 4;
+    {
+        XRegs<XK_DN> R;
+        xq8_prefetch<XK_DN, TK>(R, W.wd, W.wd_d, nullptr, nullptr);
+        RowsT<NT, 384> vh;
+        load_tagged<NT, 384, true>(ar + (size_t) p_gu * kSlot + x * 1024, tb | p_gu, vh, dead, A.err, 384);
+        quant_rows<NT, 384>(vh, L);
+        xq8_compute<NT, XK_DN>(R, L, ar + (size_t) p_dn * kSlot, 0, tb | p_dn);
+    }
+    __syncthreads();
+    const int p_x2 = p;
+    p += 2;
+    xreduce<NT>(A, L, ar + (size_t) p_dn * kSlot, tb | p_dn, ar + (size_t) p_x2 * kSlot + x * 2048, tb | p_x2, dead);
+    p_out = p_x2;
+}
+
 // Publish LDS rows [nt][d] as the tagged slot p (workgroup 0 only): the
 // block's residual input for layer 0.
 __device__ __forceinline__ void publish(const Args & A, const float * x, int nt, int d, int p, uint32_t tb) {
@@ -1685,13 +2063,26 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
 // (256 VGPRs + 256 AGPRs) is available to every wave.
 // `frame` indexes the sampler streams and the frame state; `epoch` (distinct
 // for every launch since the arena was last cleared) makes the phase tags.
-template <int D, int QD, int FF, int WT>
+// XT: the XCD-parallel layer program (layer_x; Q8_0 0.6B shapes, 256
+// workgroups); a workgroup that finds itself on another XCD than b % 8
+// raises error 2 and does nothing more (its peers' waits then time out).
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    return v;
+}
+
+template <int D, int QD, int FF, int WT, bool XT>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(const Args * __restrict__ Ap,
                                                                                          int32_t frame, int32_t epoch,
                                                                                          int32_t mode) {
     const Args & A = *Ap;
     __shared__ Lds L;
     bool dead = false;
+    if (XT && xcc_id() != (blockIdx.x & 7)) {
+        if (threadIdx.x == 0) atomicExch(A.err, 2);
+        return;
+    }
     FrameState * st = A.st;
     if (st->done) return;
     const uint32_t tb = (uint32_t) (epoch + 1) << 12;
@@ -1746,16 +2137,22 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         __syncthreads();
         const int nt = s == 0 ? 2 : 1;
         const int pos0 = tk ? pos : s == 0 ? 0 : s + 1;
-        publish(A, L.x, nt, D, p_x, tb);
+        if (!XT) publish(A, L.x, nt, D, p_x, tb);
         int p_in = p_x, p_out = p_x;
         const int nl = tk ? A.n_layers : A.cp_layers;
         const LayerQ8 * Ls = tk ? A.talker : A.cp;
         for (int l = 0; l < nl; ++l) {
             const float * x_lds = l == 0 ? L.x : nullptr;
             const LayerQ8 Wl = layer_desc(Ls + l);
-            if (nt == 2) layer_t<2, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
-            else layer_t<1, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            if constexpr (XT) {
+                if (nt == 2) layer_x<2, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else if (tk) layer_x<1, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else layer_x<1, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            } else {
+                if (nt == 2) layer_t<2, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else layer_t<1, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+            }
             p_in = p_out;
         }
         // head on the last token's normed row
@@ -1767,7 +2164,12 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             NormT<D> nw;
             norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
             RowsT<1, D> v;
-            load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
+            if constexpr (XT)
+                load_tagged<1, D, true>(A.arena + (size_t) p_out * kSlot + ((int) blockIdx.x & 7) * 2048 +
+                                            (size_t) (nt - 1) * D,
+                                        tb | p_out, v, dead, A.err, D);
+            else
+                load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
             head_input<D>(v, nw, A.eps, L, tk ? A.hidden : nullptr);
         }
         if (tk) {

@@ -82,17 +82,26 @@ def prefill_kv(dev, o, cfg, rng, n_pos):
         o.kv_write(il, kv[0], kv[1])
 
 
-@pytest.fixture(params=["persistent", "graph"])
+@pytest.fixture(params=["persistent", "persistent_rows", "graph"])
 def path(request, monkeypatch):
-    """The persistent frame kernel (default) or the captured multi-kernel
-    sequences (Q3T_FRAME_KERNEL=0); chosen when a context first runs."""
-    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
+    """The persistent frame kernel (default: with the XCD-parallel layer
+    program for Q8_0 0.6B models), the persistent kernel with its
+    row-parallel layer program (Q3T_FRAME_XCD=0), or the captured
+    multi-kernel sequences (Q3T_FRAME_KERNEL=0); chosen when a context first
+    runs."""
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "0" if request.param == "graph" else "1")
+    monkeypatch.setenv("Q3T_FRAME_XCD", "0" if request.param == "persistent_rows" else "1")
     return request.param
 
 
-def check_path(dev, want):
+def check_path(dev, want, wtype="f16"):
     _, _, used = dev.frames_stats()
-    assert used == (1 if want == "persistent" else 0), (want, used)
+    if want == "graph":
+        assert used == 0, (want, used)
+    elif want == "persistent_rows" or wtype == "f16":
+        assert used == 1, (want, wtype, used)
+    else:
+        assert used == 3, (want, wtype, used)
 
 
 def test_config2_f16_talker_step_kv512(path):
@@ -205,7 +214,7 @@ def test_config3_q8_frame_loop_256_greedy(path):
         assert np.array_equal(first_g, first_o)
         say(f"[gpu] config 3: device generate 256 ({path})")
         cg = driver.generate(dev, cfg, text, spk, max_len=256, temperature=0.0, top_k=0, prefill_rows=pre)
-        check_path(dev, path)
+        check_path(dev, path, "q8_0")
     finally:
         dev.close()
     say(f"[gpu] config 3: frames oracle={co.shape[0]} device={cg.shape[0]}")

@@ -46,8 +46,8 @@ def frame_path(request, monkeypatch):
 
 def check_path(dev, wtype, frame_path):
     us, n, path = dev.frames_stats()
-    want = 1 if frame_path == "persistent" else 0
-    assert path == want, (frame_path, wtype, path)
+    want = (1, 3) if frame_path == "persistent" else (0,)
+    assert path in want, (frame_path, wtype, path)
 
 
 @pytest.fixture(scope="module", params=["q8_0", "f16"])
@@ -278,28 +278,34 @@ def test_long_context_persistent_matches_graph(wtype, monkeypatch):
     out = {}
     try:
         dev.kv_reserve(2100 + 16)
-        for path in ("1", "0"):
-            monkeypatch.setenv("Q3T_FRAME_KERNEL", path)
-            say(f"[gpu] long context {wtype}: prefill 2100, 6 frames, Q3T_FRAME_KERNEL={path}")
+        # (Q3T_FRAME_KERNEL, Q3T_FRAME_XCD) -> the path frames_stats reports
+        variants = [("1", "1", 3 if wtype == "q8_0" else 1), ("1", "0", 1), ("0", "1", 0)]
+        for kern, xcd, want in variants:
+            monkeypatch.setenv("Q3T_FRAME_KERNEL", kern)
+            monkeypatch.setenv("Q3T_FRAME_XCD", xcd)
+            say(f"[gpu] long context {wtype}: prefill 2100, 6 frames, Q3T_FRAME_KERNEL={kern} Q3T_FRAME_XCD={xcd}")
             dev.prefill(rows, 0, want_hidden=False)
             dev.frames_begin(pad[None], pad, 2100, 6, repetition_penalty=1.05, temperature=0.0, top_k=0,
                              eos_bias=-1e4)
             codes, eos = dev.frames_run(6)
             us, n, used = dev.frames_stats()
-            assert used == int(path) and codes.shape[0] == 6
-            out[path] = codes
+            assert used == want and codes.shape[0] == 6, (kern, xcd, used)
+            out[want] = codes
     finally:
         dev.close()
-    assert np.array_equal(out["1"], out["0"])
+    for k in out:
+        assert np.array_equal(out[k], out[0]), k
 
 
-@pytest.fixture(params=["persistent", "graph"])
+@pytest.fixture(params=["persistent", "persistent_rows", "graph"])
 def step_path(request, monkeypatch):
     """Single talker steps and code-predictor calls on the persistent kernel's
-    step modes (the default) and on the multi-kernel sequences
-    (Q3T_FRAME_KERNEL=0).  The choice is made when a context first runs
-    one, so each test builds its own device."""
-    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1" if request.param == "persistent" else "0")
+    step modes (the default; XCD-parallel layers for Q8_0 0.6B models), on
+    its row-parallel layer program (Q3T_FRAME_XCD=0) and on the multi-kernel
+    sequences (Q3T_FRAME_KERNEL=0).  The choice is made when a context first
+    runs one, so each test builds its own device."""
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "0" if request.param == "graph" else "1")
+    monkeypatch.setenv("Q3T_FRAME_XCD", "0" if request.param == "persistent_rows" else "1")
     return request.param
 
 
