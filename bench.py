@@ -85,6 +85,46 @@ def cpu_baseline(cfg, w, text, spk, threads, budget_s):
     return (n3 - 1) / dt, n3
 
 
+# The CPU leg is the oracle: a scalar C++ restatement that accumulates every
+# dot product in fp64.  ggml's x86 Q8_0 / F16 kernels (AVX2 / AVX-512 int8
+# and fp32 SIMD) are not in this tree, so this figure very likely understates
+# the reference's own CPU speed.
+PORT_NOTE = ("CPU leg = the oracle (scalar C++ restatement, fp64 accumulation), not ggml's SIMD kernels: "
+             "likely slower than the reference's CPU path")
+
+
+def config1_leg(args, cfg, Device, driver, Weights):
+    """Configuration 1 (F16 0.6B, 32-token prompt, greedy, 64 frames): the
+    device frame loop timed with HIP events, and the oracle on 4 host threads
+    over a bounded sample of the same workload."""
+    w16 = Weights(cfg, "f16", seed=2024)
+    rng = np.random.default_rng(18)
+    text = rng.integers(0, cfg.text_vocab, 32).astype(np.int32)
+    spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+    dev = Device(cfg, 0)
+    dev.upload_weights(w16)
+    pre, trail, pad = driver.build_prefill(dev, cfg, text, spk)
+    plen = pre.shape[0]
+    dev.kv_reserve(plen + 64 + 8)
+    dev.prefill(pre, 0, want_hidden=False)
+    dev.frames_begin(trail, pad, plen, 64, repetition_penalty=1.05, temperature=0.0, top_k=0, eos_bias=-1e4)
+    dev.frames_run(8)
+    us0, n0, _ = dev.frames_stats()
+    codes, eos = dev.frames_run(56)
+    us1, n1, path = dev.frames_stats()
+    dev.close()
+    assert not eos and codes.shape[0] == 56
+    gpu_fps = (n1 - n0) / ((us1 - us0) * 1e-6)
+    out = {"workload": "configuration 1: F16 0.6B shapes, 32-token prompt, greedy, 64 frames",
+           "gpu_frames_per_s": round(gpu_fps, 2), "gpu_path": path,
+           "gpu_sample": "frames 8..63 (HIP events around the frame launches)", "cpu": None}
+    if not args.no_cpu_baseline:
+        fps, n = cpu_baseline(cfg, w16, text, spk, 4, args.cpu_budget / 2)
+        out["cpu"] = {"value": round(fps, 3), "unit": "frames/s", "cores": 4, "kind": "port",
+                      "sample": f"oracle generate() of {n} frames minus a 1-frame run, 4 threads; {PORT_NOTE}"}
+    return out
+
+
 def prefill_bench(args, cfg, w):
     """One talker prefill of args.prefill rows (seeded N(0, 0.05) rows), the
     long-prompt half of the long-context configuration.  Q8_0 models take the
@@ -316,6 +356,8 @@ def main():
     ap.add_argument("--cpu-threads-max", type=int, default=16,
                     help="thread cap of the all-cores CPU baseline (the host share of one GPU)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-config1", dest="config1", action="store_false",
+                    help="skip the configuration-1 leg (F16, 32-token prompt: device frames/s and the CPU oracle)")
     ap.add_argument("--kernel-iters", type=int, default=200,
                     help="launches per per-kernel timing of the multi-kernel path (0: skip)")
     ap.add_argument("--prefill", type=int, default=0,
@@ -418,7 +460,7 @@ def main():
         cpu_fps, n_frames = cpu_baseline(cfg, w, text, spk, nthreads, args.cpu_budget)
         cpu = {"value": round(cpu_fps, 3), "unit": "frames/s", "cores": nthreads, "kind": "port",
                "sample": f"oracle generate() of {n_frames} frames minus a 1-frame run, same weights/prompt, "
-                         f"{nthreads} threads; {host}"}
+                         f"{nthreads} threads; {host}. " + PORT_NOTE}
         # the same leg on all the host cores this process may use (capped at
         # the GPU's share of them), with half the time budget
         nall = min(len(os.sched_getaffinity(0)), args.cpu_threads_max)
@@ -426,6 +468,10 @@ def main():
             fps_all, n_all = cpu_baseline(cfg, w, text, spk, nall, args.cpu_budget / 2)
             cpu_all = {"value": round(fps_all, 3), "unit": "frames/s", "cores": nall, "kind": "port",
                        "sample": f"as cpu_baseline with {nall} threads, {n_all} frames; {host}"}
+
+    config1 = None
+    if args.config1:
+        config1 = config1_leg(args, cfg, Device, driver, Weights)
 
     out = {
         "metric": "codec frames/sec at batch 1 Q8_0 (RTF vs 12 Hz); achieved HBM GB/s per step",
@@ -456,6 +502,7 @@ def main():
         "kernels": kernels,
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,
+        "config1": config1,
     }
     print(json.dumps(out))
 

@@ -119,6 +119,20 @@ int  q3t_dev_dequantize(q3t_dev * dev, const char * name, float * out, size_t n_
 int  q3t_dev_kv_reserve(q3t_dev * dev, int32_t n_ctx);
 int  q3t_dev_kv_clear(q3t_dev * dev);
 int32_t q3t_dev_kv_capacity(const q3t_dev * dev);
+/* Attention-row capture, the device side of set_attn_dump / attn_rows
+ * (src/tts_transformer.h:224-227; rows captured in forward_step,
+ * src/tts_transformer.cpp:1719-1724 and :2485-2497).  layer in
+ * [0, n_layers) turns it on for that talker layer, -1 turns it off; either
+ * call clears the kept rows and ends an open frame loop (call it before
+ * q3t_dev_frames_begin).  While it is on, every talker step (talker_step and
+ * each frame of frames_run that is not EOS) keeps the layer's post-softmax
+ * fp32 row [n_head][n_kv], heads as blocks of n_kv, n_kv = step position + 1;
+ * those steps run on the multi-kernel path and synchronise once per frame. */
+int  q3t_dev_set_attn_capture(q3t_dev * dev, int32_t layer);
+int32_t q3t_dev_attn_row_count(const q3t_dev * dev);
+/* Copies kept row `index` (n_head * n_kv floats) to out when out is non-null
+ * (cap: its size in floats); *n_kv_out receives n_kv. */
+int  q3t_dev_attn_row(q3t_dev * dev, int32_t index, float * out, int64_t cap, int32_t * n_kv_out);
 /* Writes fp16 K/V rows [n_pos][n_kv_head][head_dim] for positions
  * [0, n_pos) of talker layer `layer` (used to pre-fill a cache). */
 int  q3t_dev_kv_write(q3t_dev * dev, int32_t layer, int32_t n_pos,

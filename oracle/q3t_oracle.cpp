@@ -516,6 +516,8 @@ struct orc_model {
     std::vector<float> cp_rope_cos, cp_rope_sin;  // code-predictor theta
     int32_t rope_rows = 0;
     std::vector<float> last_hidden;
+    int32_t attn_layer = -1;                      // orc_set_attn_capture
+    std::vector<std::vector<float>> attn_rows;    // [n_head][n_kv] per talker step
     std::string err;
 };
 
@@ -545,7 +547,8 @@ void gemv_t(orc_model * m, const Tensor & w, int64_t rows, int64_t k, const floa
 // F32 rows of this call instead of the F16 cache (orc_attention_f32); the
 // cache rows are written either way, for the steps that follow.
 void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float * x, int64_t ntok, int32_t pos0,
-                   KV & kv, int32_t il, const float * rc, const float * rs, bool f32_attn = false) {
+                   KV & kv, int32_t il, const float * rc, const float * rs, bool f32_attn = false,
+                   float * probs = nullptr) {
     const orc_config & c = m->cfg;
     const int64_t hd = c.head_dim, nh = c.n_head, nkv = c.n_kv_head;
     const int64_t qd = nh * hd, kd = nkv * hd, half = hd / 2;
@@ -581,7 +584,7 @@ void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float
         m->pool.run(ntok, [&](int64_t i0, int64_t i1) {
             for (int64_t i = i0; i < i1; ++i)
                 orc_attention(q.data() + i * qd, kc, vc, nh, nkv, hd, kv.n_ctx, pos0 + i + 1, o.data() + i * qd,
-                              nullptr);
+                              ntok == 1 ? probs : nullptr);
         });
     }
     gemv_t(m, L.wo, d, qd, o.data(), ntok, t.data());
@@ -642,17 +645,22 @@ void embd_row(const Tensor & t, int64_t dim, int32_t tok, float * out) {
     }
 }
 
+// step: forward_step, which keeps the attention row of the capture layer
+// (src/tts_transformer.cpp:1719-1724, :2485-2497); forward_prefill keeps none.
 bool talker_forward(orc_model * m, const float * embd, int32_t n, int32_t n_past,
-                    float * hidden_out, float * logits_out) {
+                    float * hidden_out, float * logits_out, bool step = false) {
     const orc_config & c = m->cfg;
     if (m->talker.empty() && !resolve(m)) return false;
     if (n_past + n > m->kv.n_ctx) return fail(m, "Context length exceeded");
     ensure_rope(m, m->kv.n_ctx);
     const int64_t d = c.hidden_size;
     std::vector<float> x(embd, embd + (size_t) n * d);
+    std::vector<float> probs;
+    if (step && m->attn_layer >= 0) probs.resize((size_t) c.n_head * (n_past + 1));
     for (int il = 0; il < c.n_layers; ++il)
         layer_forward(m, m->talker[il], d, c.ffn_size, x.data(), n, n_past, m->kv, il, m->rope_cos.data(),
-                      m->rope_sin.data());
+                      m->rope_sin.data(), false, il == m->attn_layer && !probs.empty() ? probs.data() : nullptr);
+    if (!probs.empty()) m->attn_rows.push_back(std::move(probs));
     std::vector<float> hid((size_t) n * d);
     for (int32_t i = 0; i < n; ++i) orc_rmsnorm(x.data() + i * d, fp(m->out_norm), d, c.rms_eps, hid.data() + i * d);
     if (hidden_out) std::memcpy(hidden_out, hid.data(), hid.size() * sizeof(float));
@@ -739,7 +747,23 @@ int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
 }
 
 int orc_step(orc_model * m, const float * embd, int32_t n_past, float * logits_out, float * hidden_out) {
-    return talker_forward(m, embd, 1, n_past, hidden_out, logits_out) ? 0 : -1;
+    return talker_forward(m, embd, 1, n_past, hidden_out, logits_out, true) ? 0 : -1;
+}
+
+int orc_set_attn_capture(orc_model * m, int32_t layer) {
+    if (layer < -1 || layer >= m->cfg.n_layers) { m->err = "attention capture layer out of range"; return -1; }
+    m->attn_layer = layer;
+    m->attn_rows.clear();
+    return 0;
+}
+
+int32_t orc_attn_row_count(const orc_model * m) { return (int32_t) m->attn_rows.size(); }
+
+int32_t orc_attn_row(const orc_model * m, int32_t index, float * out, int64_t cap) {
+    if (index < 0 || index >= (int32_t) m->attn_rows.size()) return -1;
+    const std::vector<float> & r = m->attn_rows[(size_t) index];
+    if (out && cap >= (int64_t) r.size()) std::memcpy(out, r.data(), r.size() * sizeof(float));
+    return (int32_t) (r.size() / (size_t) m->cfg.n_head);
 }
 
 int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,

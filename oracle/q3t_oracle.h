@@ -178,6 +178,15 @@ int orc_prefill(orc_model * m, const float * embd, int32_t n, int32_t n_past,
                 float * hidden_out, float * logits_out);
 int orc_step(orc_model * m, const float * embd, int32_t n_past,
              float * logits_out, float * hidden_out);
+/* Attention-row capture (set_attn_dump, src/tts_transformer.cpp:1719-1724,
+ * :2485-2497): with layer in [0, n_layers) every orc_step (also inside
+ * orc_frames) keeps that talker layer's post-softmax fp32 row [n_head][n_kv];
+ * -1 turns it off.  Either call clears the kept rows.  orc_attn_row copies
+ * row `index` when out holds cap >= n_head * n_kv floats and returns n_kv
+ * (-1: no such row). */
+int     orc_set_attn_capture(orc_model * m, int32_t layer);
+int32_t orc_attn_row_count(const orc_model * m);
+int32_t orc_attn_row(const orc_model * m, int32_t index, float * out, int64_t cap);
 /* 15 codes for codebooks 1..15.  logits_out (optional): [15][cp_vocab]
  * logits as produced by each head before sampling. */
 int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,

@@ -80,6 +80,9 @@ def lib():
         L.orc_kv_read.argtypes = [vp, i32, i32, vp, vp]
         L.orc_prefill.argtypes = [vp, vp, i32, i32, vp, vp]
         L.orc_step.argtypes = [vp, vp, i32, vp, vp]
+        L.orc_set_attn_capture.argtypes = [vp, i32]
+        L.orc_attn_row_count.argtypes = [vp]; L.orc_attn_row_count.restype = i32
+        L.orc_attn_row.argtypes = [vp, i32, vp, i64]; L.orc_attn_row.restype = i32
         L.orc_code_pred.argtypes = [vp, vp, i32, f32, i32, u64, u32, vp, vp]
         L.orc_text_proj.argtypes = [vp, vp, i32, vp]
         L.orc_embed_row.argtypes = [vp, ctypes.c_char_p, i32, i32, vp]
@@ -273,6 +276,18 @@ class Oracle:
         logits = np.empty(self.cfg.codec_vocab, np.float32)
         self._chk(self.L.orc_prefill(self.h, _p(embd), n, n_past, _p(hid), _p(logits)), "prefill")
         return hid, logits
+
+    def set_attn_capture(self, layer):
+        self._chk(self.L.orc_set_attn_capture(self.h, int(layer)), "set_attn_capture")
+
+    def attn_rows(self):
+        rows = []
+        for i in range(self.L.orc_attn_row_count(self.h)):
+            n_kv = self.L.orc_attn_row(self.h, i, None, 0)
+            out = np.empty((self.cfg.n_head, n_kv), np.float32)
+            self.L.orc_attn_row(self.h, i, _p(out), out.size)
+            rows.append(out)
+        return rows
 
     def step(self, embd, n_past):
         embd = np.ascontiguousarray(embd, np.float32)

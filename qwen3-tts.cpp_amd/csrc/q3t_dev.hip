@@ -122,7 +122,12 @@ struct q3t_dev {
     int32_t * codes_out = nullptr; int32_t codes_cap = 0;
     float * trailing = nullptr; int32_t trailing_cap = 0; int32_t n_trailing = 0;
     float * pad = nullptr;
-    float * probs = nullptr;
+    // attention-row capture (q3t_dev_set_attn_capture): post-softmax rows
+    // [n_head][n_kv] of talker layer attn_layer, one per talker step
+    float * probs = nullptr; int32_t probs_cap = 0;
+    int32_t attn_layer = -1;
+    int32_t attn_emitted = 0;          // frames of the current loop whose rows are kept
+    std::vector<std::vector<float>> attn_rows;
 
     // caches
     uint16_t * kc = nullptr, * vc = nullptr; int32_t n_ctx = 0;
@@ -479,7 +484,7 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
 // output rows left in c->xa.
 void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, int ffn, uint16_t * kc, uint16_t * vc,
            int n_ctx, const float * rc, const float * rs, const int32_t * pos_ptr, int pos_const,
-           bool f32_prefill = false) {
+           bool f32_prefill = false, float * probs = nullptr) {
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     GemvSpec s{};
@@ -488,6 +493,7 @@ void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, in
     gemv(c, s, nt);
     AttnSpec as{c->qkv, &L, kc, vc, n_ctx, rc, rs, pos_ptr, pos_const};
     as.f32_prefill = f32_prefill;
+    as.probs = probs;
     attention(c, as, nt);
     GemvSpec o{};
     o.w = weight_of(L.wo); o.rows = d; o.K = qd; o.x = c->attn; o.x_stride = qd;
@@ -505,14 +511,17 @@ void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, in
 
 // Talker forward of nt (<= 4) tokens whose input rows are `xin`.  The codec
 // head runs on the last row when `head` is set (normed hidden of that row ->
-// c->hidden, logits -> c->logits).
-void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_ptr, int pos_const, bool head) {
+// c->hidden, logits -> c->logits).  A single-token step (`step`) writes the
+// post-softmax rows of layer c->attn_layer to c->probs when capture is on.
+void talker_chunk(q3t_dev * c, const float * xin, int nt, const int32_t * pos_ptr, int pos_const, bool head,
+                  bool step = false) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size;
     const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
     for (int il = 0; il < g.n_layers; ++il)
         layer(c, c->talker[il], il == 0 ? xin : c->xa, nt, d, g.ffn_size, c->kc + il * lstride, c->vc + il * lstride,
-              c->n_ctx, c->rope_cos, c->rope_sin, pos_ptr, pos_const);
+              c->n_ctx, c->rope_cos, c->rope_sin, pos_ptr, pos_const, false,
+              step && nt == 1 && il == c->attn_layer ? c->probs : nullptr);
     if (head) {
         GemvSpec h{};
         h.w = weight_of(c->codec_head); h.rows = g.codec_vocab; h.K = d;
@@ -580,7 +589,7 @@ void frame_seq(q3t_dev * c) {
     sa.open_frame = 1;
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
     code_pred_seq(c, true);
-    talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
+    talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true, true);
 }
 
 int set_state(q3t_dev * c, const FrameState & s) {
@@ -686,7 +695,7 @@ const char * fk_err_msg(int32_t e) {
 
 int fk_prepare(q3t_dev * c) {
     c->fk_ok = false;
-    if (c->fk_refused) return 0;
+    if (c->fk_refused || c->attn_layer >= 0) return 0;   // attention capture runs the multi-kernel step
     if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
@@ -874,6 +883,15 @@ int fk_step(q3t_dev * c, int32_t frame, int32_t mode, bool & ran) {
 
 
 
+// Appends the captured attention row of the step at position n_kv - 1
+// ([n_head][n_kv] floats in c->probs) to c->attn_rows.
+int keep_attn_row(q3t_dev * c, int n_kv) {
+    std::vector<float> row((size_t) c->cfg.n_head * n_kv);
+    HIP_OK(hipMemcpy(row.data(), c->probs, row.size() * 4, hipMemcpyDeviceToHost));
+    c->attn_rows.push_back(std::move(row));
+    return 0;
+}
+
 // The captured multi-kernel frame, built on first use.
 int ensure_frame_graph(q3t_dev * c) {
     if (c->frame_exec) return 0;
@@ -963,7 +981,6 @@ int q3t_dev_create(const q3t_config * cfg, int32_t device, q3t_dev ** out) {
     rc |= dev_alloc_t(c, &c->pad, (size_t) d);
     rc |= dev_alloc_t(c, &c->trailing, (size_t) d);
     rc |= dev_alloc_t(c, &c->codes_out, (size_t) 16);
-    rc |= dev_alloc_t(c, &c->probs, (size_t) g.n_head * 16384);
     c->trailing_cap = 1; c->codes_cap = 1;
     rc |= ensure_stage(c, 16);
     if (rc) { *out = c; return -1; }
@@ -1105,19 +1122,38 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
     if (!c) return -1;
     const q3t_config & g = c->cfg;
     if (n_ctx <= 0) return fail(c, "n_ctx must be > 0");
-    if (n_ctx > 12288) return fail(c, "n_ctx above 12288 is not supported by the decode attention kernel");
     HIP_OK(hipSetDevice(c->device));
+    // The single-workgroup attention kernels (k_attention, pf::k_attn_rows)
+    // hold a head's n_ctx scores in LDS: 160 KiB per workgroup on gfx950
+    // bounds n_ctx at about 38,600 positions (the talker's position table
+    // ends at 32,768).
+    int max_lds = 0;
+    HIP_OK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device));
+    const size_t need_att = attn_lds_bytes(n_ctx), need_pf = pf::attn_rows_lds_bytes(n_ctx);
+    if (std::max(need_att, need_pf) > (size_t) max_lds) {
+        char msg[160];
+        snprintf(msg, sizeof msg, "n_ctx %d needs %zu bytes of LDS for the decode attention; the device has %d",
+                 (int) n_ctx, std::max(need_att, need_pf), max_lds);
+        return fail(c, msg);
+    }
+    HIP_OK(hipFuncSetAttribute((const void *) k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int) need_att));
+    HIP_OK(hipFuncSetAttribute((const void *) pf::k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int) need_pf));
     HIP_OK(hipStreamSynchronize(c->stream));
     drop_graph(c);
     drop_stream_graph(c);
     dev_free(c, c->kc); dev_free(c, c->vc); dev_free(c, c->cpk); dev_free(c, c->cpv);
     dev_free(c, c->rope_cos); dev_free(c, c->rope_sin); dev_free(c, c->cp_rope_cos); dev_free(c, c->cp_rope_sin);
+    dev_free(c, c->probs);
     c->kc = c->vc = c->cpk = c->cpv = nullptr;
+    c->probs = nullptr;
+    c->probs_cap = 0;
     const size_t kv = (size_t) g.n_layers * g.n_kv_head * n_ctx * g.head_dim;
     const size_t ckv = (size_t) g.cp_layers * g.n_kv_head * 16 * g.head_dim;
     if (dev_alloc_t(c, &c->kc, kv) || dev_alloc_t(c, &c->vc, kv) || dev_alloc_t(c, &c->cpk, ckv) ||
-        dev_alloc_t(c, &c->cpv, ckv))
+        dev_alloc_t(c, &c->cpv, ckv) || dev_alloc_t(c, &c->probs, (size_t) g.n_head * n_ctx))
         return -1;
+    c->probs_cap = n_ctx;
     HIP_OK(hipMemsetAsync(c->kc, 0, kv * 2, c->stream));
     HIP_OK(hipMemsetAsync(c->vc, 0, kv * 2, c->stream));
     HIP_OK(hipMemsetAsync(c->cpk, 0, ckv * 2, c->stream));
@@ -1169,6 +1205,37 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
 int q3t_dev_kv_clear(q3t_dev * c) { return c ? 0 : -1; }
 
 int32_t q3t_dev_kv_capacity(const q3t_dev * c) { return c ? c->n_ctx : 0; }
+
+int q3t_dev_set_attn_capture(q3t_dev * c, int32_t layer) {
+    if (!c) return -1;
+    if (layer < -1 || layer >= c->cfg.n_layers) return fail(c, "attention capture layer out of range");
+    HIP_OK(hipSetDevice(c->device));
+    HIP_OK(hipStreamSynchronize(c->stream));
+    if (layer != c->attn_layer) {
+        // the captured frame and the persistent kernel's arguments describe
+        // the other mode; both are rebuilt on next use
+        drop_graph(c);
+        c->fk_ok = false;
+        c->fk_args_ok = false;
+        c->frames_ready = false;
+    }
+    c->attn_layer = layer;
+    c->attn_rows.clear();
+    return 0;
+}
+
+int32_t q3t_dev_attn_row_count(const q3t_dev * c) { return c ? (int32_t) c->attn_rows.size() : 0; }
+
+int q3t_dev_attn_row(q3t_dev * c, int32_t index, float * out, int64_t cap, int32_t * n_kv_out) {
+    if (!c) return -1;
+    if (index < 0 || index >= (int32_t) c->attn_rows.size()) return fail(c, "attention row index out of range");
+    const std::vector<float> & r = c->attn_rows[(size_t) index];
+    if (n_kv_out) *n_kv_out = (int32_t) (r.size() / (size_t) c->cfg.n_head);
+    if (!out) return 0;
+    if (cap < (int64_t) r.size()) return fail(c, "attention row buffer too small");
+    std::memcpy(out, r.data(), r.size() * sizeof(float));
+    return 0;
+}
 
 int q3t_dev_kv_write(q3t_dev * c, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v) {
     if (!c || !k || !v) return -1;
@@ -1596,11 +1663,12 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
     HIP_OK(hipMemcpyAsync(c->stage, c->pin + o_embd, d4, hipMemcpyHostToDevice, c->stream));
     bool ran = false;
     if (fk_step(c, 0, fk::MODE_TALKER_STEP, ran)) return -1;
-    if (!ran) talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true);
+    if (!ran) talker_chunk(c, c->stage, 1, &c->st->talker_pos, 0, true, true);
     if (logits_out) HIP_OK(hipMemcpyAsync(c->pin + o_logits, c->logits, v4, hipMemcpyDeviceToHost, c->stream));
     if (hidden_out) HIP_OK(hipMemcpyAsync(c->pin + o_hidden, c->hidden, d4, hipMemcpyDeviceToHost, c->stream));
     if (ran) HIP_OK(hipMemcpyAsync(c->pin + o_err, c->fk_err, 4, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
+    if (!ran && c->attn_layer >= 0 && keep_attn_row(c, n_past + 1)) return -1;
     if (logits_out) std::memcpy(logits_out, c->pin + o_logits, v4);
     if (hidden_out) std::memcpy(hidden_out, c->pin + o_hidden, d4);
     if (ran) {
@@ -1910,6 +1978,7 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     if (sync(c)) return -1;
     if (!c->fk_ok && ensure_frame_graph(c)) return -1;
     c->host_emitted = 0;
+    c->attn_emitted = 0;
     c->frames_launched = 0;
     c->run_us = 0.0;
     c->run_frames = 0;
@@ -1949,6 +2018,18 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
         }
         if (no_graph) frame_seq(c);
         else HIP_OK(hipGraphLaunch(c->frame_exec, c->stream));
+        if (c->attn_layer >= 0) {
+            // attention capture: a frame that emitted codes (no EOS) ran its
+            // talker step, whose row covers positions 0..talker_pos; the
+            // reference takes no step after the last frame
+            // (src/tts_transformer.cpp:3259-3261), so that row is not kept
+            FrameState f{};
+            HIP_OK(hipMemcpyAsync(&f, c->st, sizeof f, hipMemcpyDeviceToHost, c->stream));
+            if (sync(c)) return -1;
+            const bool last = c->frames_launched + i + 1 >= c->frames_max;
+            if (f.n_emitted > c->attn_emitted && !last && keep_attn_row(c, f.talker_pos + 1)) return -1;
+            c->attn_emitted = f.n_emitted;
+        }
     }
     if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[1], c->stream));
     c->frames_launched += n_frames;

@@ -210,7 +210,15 @@ bool TTSTransformer::forward_step(const float * step_embd, int32_t n_past, std::
     if (n_past + 1 > kv_n_ctx_) { error_msg_ = "Context length exceeded"; return false; }
     output.resize(config_.codec_vocab_size);
     last_hidden_.resize(config_.hidden_size);
+    // forward_step keeps the dump layer's attention row (src/tts_transformer.cpp:2485-2497)
+    if (!dev_ok(q3t_dev_set_attn_capture(dev_, attn_dump_ ? attn_dump_layer_ : -1))) return false;
     if (!dev_ok(q3t_dev_talker_step(dev_, step_embd, n_past, output.data(), last_hidden_.data()))) return false;
+    if (attn_dump_) {
+        int32_t n_kv = 0;
+        std::vector<float> row((size_t) config_.n_attention_heads * (n_past + 1));
+        if (!dev_ok(q3t_dev_attn_row(dev_, 0, row.data(), (int64_t) row.size(), &n_kv))) return false;
+        attn_rows_.push_back(std::move(row));
+    }
     if (hidden_out) *hidden_out = last_hidden_;
     kv_n_used_ = n_past + 1;
     return true;
@@ -314,15 +322,22 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
     a.target_frames = target_frames;
     a.sampling = q3t_sampling{temperature, top_k, seed_};
     if (temperature > 0.0f) seed_ = splitmix64(seed_);   // next call draws a fresh stream
+    // attention capture for set_attn_dump (src/tts_transformer.cpp:1719-1724)
+    if (!dev_ok(q3t_dev_set_attn_capture(dev_, attn_dump_ ? attn_dump_layer_ : -1))) return false;
     if (!dev_ok(q3t_dev_frames_begin(dev_, &a))) return false;
-    int chunk = 8;
+    // Frames per q3t_dev_frames_run call.  With a callback every frame is
+    // handed over before the next one is computed, as the reference does
+    // (src/tts_transformer.cpp:3213): an abort wastes no frame and streaming
+    // consumers see one frame at a time.  Without one, 8-frame chunks save
+    // host synchronisations.  QWEN3_TTS_FRAME_CHUNK overrides both.
+    int chunk = on_frame ? 1 : 8;
     if (const char * e = std::getenv("QWEN3_TTS_FRAME_CHUNK")) chunk = std::max(1, std::atoi(e));
     output.clear();
     output.reserve((size_t) max_len * ncb);
     std::vector<int32_t> buf((size_t) chunk * ncb);
     std::vector<std::vector<int32_t>> rep_frames;
     int32_t rep_run_len = 0, rep_run_start = 0;
-    int32_t produced = 0;
+    int32_t produced = 0, stop_frame = -1;
     while (produced < max_len) {
         const int32_t n = std::min(chunk, max_len - produced);
         int32_t got = 0, eos = 0;
@@ -332,7 +347,7 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
             const int32_t * codes = buf.data() + (size_t) f * ncb;
             const int32_t frame = produced + f;
             output.insert(output.end(), codes, codes + ncb);
-            if (on_frame && !on_frame(codes, ncb, frame)) { stop = true; break; }
+            if (on_frame && !on_frame(codes, ncb, frame)) { stop = true; stop_frame = frame; break; }
             if (rep_loop_detect) rep_frames.emplace_back(codes, codes + ncb);
             const size_t nf = rep_frames.size();
             bool is_rep = false;
@@ -348,12 +363,28 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
                         (int) rep_run_len);
                 output.resize((size_t) rep_run_start * ncb);
                 stop = true;
+                stop_frame = frame;
             }
         }
         produced += got;
         if (stop || eos || got < n) break;
     }
     kv_n_used_ = plen + produced;
+    if (attn_dump_) {
+        // one row per talker step the reference takes: none for the frame
+        // at which the loop stops (callback, repetition loop) or for frames
+        // the device computed past it
+        int32_t n_rows = q3t_dev_attn_row_count(dev_);
+        if (stop_frame >= 0) n_rows = std::min(n_rows, stop_frame);
+        attn_rows_.clear();
+        for (int32_t i = 0; i < n_rows; ++i) {
+            int32_t n_kv = 0;
+            if (!dev_ok(q3t_dev_attn_row(dev_, i, nullptr, 0, &n_kv))) return false;
+            std::vector<float> row((size_t) n_kv * cfg.n_attention_heads);
+            if (!dev_ok(q3t_dev_attn_row(dev_, i, row.data(), (int64_t) row.size(), &n_kv))) return false;
+            attn_rows_.push_back(std::move(row));
+        }
+    }
     return true;
 }
 
@@ -409,11 +440,31 @@ bool TTSTransformer::forward_with_audio(const int32_t * tokens, int32_t n_tokens
     return forward_text(tokens, n_tokens, nullptr, n_past, output);
 }
 
-// Attention-row capture is not wired into the device frame loop; an
-// enabled dump writes no file and says so.
+// The ATTD file of the reference (src/tts_transformer.cpp:2978-3005): magic,
+// version 1, layer, n_head, n_rows, then per row n_kv and n_kv * n_head
+// floats (heads as blocks of n_kv).
 bool TTSTransformer::write_attn_dump() {
-    if (!attn_dump_ || attn_dump_path_.empty()) return true;
-    fprintf(stderr, "attn-dump: not captured by the device frame loop; %s not written\n", attn_dump_path_.c_str());
+    if (!attn_dump_ || attn_dump_path_.empty() || attn_rows_.empty()) return true;
+    FILE * f = fopen(attn_dump_path_.c_str(), "wb");
+    if (!f) {
+        fprintf(stderr, "attn-dump: cannot open %s for writing\n", attn_dump_path_.c_str());
+        return false;
+    }
+    const int32_t n_head = config_.n_attention_heads, n_rows = (int32_t) attn_rows_.size(), version = 1;
+    const uint32_t magic = 0x41545444u;
+    bool ok = fwrite(&magic, 4, 1, f) == 1 && fwrite(&version, 4, 1, f) == 1 &&
+              fwrite(&attn_dump_layer_, 4, 1, f) == 1 && fwrite(&n_head, 4, 1, f) == 1 && fwrite(&n_rows, 4, 1, f) == 1;
+    for (const std::vector<float> & row : attn_rows_) {
+        const int32_t n_kv = (int32_t) (row.size() / (size_t) n_head);
+        ok = ok && fwrite(&n_kv, 4, 1, f) == 1 && fwrite(row.data(), sizeof(float), row.size(), f) == row.size();
+    }
+    ok = fclose(f) == 0 && ok;
+    if (!ok) {
+        fprintf(stderr, "attn-dump: write to %s failed\n", attn_dump_path_.c_str());
+        return false;
+    }
+    fprintf(stderr, "attn-dump: wrote %d rows (layer %d, %d heads) to %s\n", n_rows, attn_dump_layer_, n_head,
+            attn_dump_path_.c_str());
     return true;
 }
 

@@ -18,7 +18,8 @@ LIB_PATH = os.path.join(PKG_DIR, "lib", "libq3t_hip.so")
 EXPORTS = [
     "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
-    "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_prefill", "q3t_dev_talker_step",
+    "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
+    "q3t_dev_attn_row", "q3t_dev_prefill", "q3t_dev_talker_step",
     "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
     "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
@@ -61,6 +62,9 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_kv_clear.argtypes = [vp]
         lib.q3t_dev_kv_capacity.argtypes = [vp]
         lib.q3t_dev_kv_write.argtypes = [vp, i32, i32, vp, vp]
+        lib.q3t_dev_set_attn_capture.argtypes = [vp, i32]
+        lib.q3t_dev_attn_row_count.argtypes = [vp]
+        lib.q3t_dev_attn_row.argtypes = [vp, i32, f32p, ctypes.c_int64, ctypes.POINTER(i32)]
         lib.q3t_dev_prefill.argtypes = [vp, f32p, i32, i32, f32p, f32p]
         lib.q3t_dev_talker_step.argtypes = [vp, f32p, i32, f32p, f32p]
         lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
@@ -160,6 +164,22 @@ class Device:
         logits = np.empty(self.cfg.codec_vocab, np.float32)
         self._check(self.lib.q3t_dev_prefill(self.h, _p(embd), n, n_past, _p(hid), _p(logits)), "prefill")
         return hid, logits
+
+    def set_attn_capture(self, layer):
+        """Keep the post-softmax attention row of talker `layer` for every
+        talker step from now on (-1: off); clears the kept rows."""
+        self._check(self.lib.q3t_dev_set_attn_capture(self.h, int(layer)), "set_attn_capture")
+
+    def attn_rows(self):
+        """The kept rows, each [n_head, n_kv] float32."""
+        rows = []
+        for i in range(self.lib.q3t_dev_attn_row_count(self.h)):
+            n_kv = ctypes.c_int32(0)
+            self._check(self.lib.q3t_dev_attn_row(self.h, i, None, 0, ctypes.byref(n_kv)), "attn_row")
+            out = np.empty((self.cfg.n_head, n_kv.value), np.float32)
+            self._check(self.lib.q3t_dev_attn_row(self.h, i, _p(out), out.size, ctypes.byref(n_kv)), "attn_row")
+            rows.append(out)
+        return rows
 
     def talker_step(self, embd, n_past, want_logits=True, want_hidden=True):
         """(logits, hidden) of one talker step; an output not wanted is None

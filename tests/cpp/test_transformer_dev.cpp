@@ -71,6 +71,18 @@ int main(int argc, char ** argv) {
     if (cut.size() != 3 * 16 || calls != 3) { std::printf("FAIL callback abort %zu %d\n", cut.size(), calls); ++fails; }
     else std::printf("PASS callback abort\n");
 
+    // attention dump of talker layer 1 over a greedy generate (ATTD file)
+    tr.set_attn_dump(out + "/attn.bin", 1);
+    std::vector<int32_t> dumped;
+    if (!tr.generate(text.data(), n_text, spk.data(), max_len, dumped, cfg.english_language_id, 1.05f, 0.0f, 0) ||
+        dumped != codes) {
+        std::printf("FAIL attn-dump generate: %s\n", tr.get_error().c_str());
+        ++fails;
+    } else {
+        std::printf("PASS attn-dump generate: %zu rows\n", tr.attn_rows().size());
+    }
+    tr.set_attn_dump("", 1);
+
     // code predictor on the last hidden state
     std::vector<int32_t> cp;
     std::vector<float> h;

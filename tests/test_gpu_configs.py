@@ -121,6 +121,32 @@ def test_config2_f16_talker_step_kv512(path):
         dev.close()
 
 
+def test_context_past_12288_f16(path):
+    """A 16,400-position cache (the decode attention's scores then need more
+    than 64 KiB of LDS): talker steps at position 16,390 on every path, and
+    with attention capture of the last layer (the multi-kernel step), against
+    the oracle bit for bit."""
+    cfg, w, dev, o = open_pair("f16", 57, 16400)
+    try:
+        rng = np.random.default_rng(58)
+        prefill_kv(dev, o, cfg, rng, 16390)
+        e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+        say(f"[gpu] step at n_past 16390 ({path})")
+        lg, hg = dev.talker_step(e, 16390)
+        lo, ho = o.step(e, 16390)
+        assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+        dev.set_attn_capture(cfg.n_layers - 1)
+        o.set_attn_capture(cfg.n_layers - 1)
+        say(f"[gpu] captured step at n_past 16391 ({path})")
+        lg, hg = dev.talker_step(e, 16391)
+        lo, ho = o.step(e, 16391)
+        assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+        (rg,), (ro,) = dev.attn_rows(), o.attn_rows()
+        assert rg.shape == (cfg.n_head, 16392) and np.array_equal(rg, ro)
+    finally:
+        dev.close()
+
+
 def _frames_both(dev, o, cfg, lo, n_past, n_frames, seed):
     rng = np.random.default_rng(seed)
     trail = (rng.standard_normal((5, cfg.hidden_size)) * 0.05).astype(np.float32)

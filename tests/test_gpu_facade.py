@@ -76,6 +76,23 @@ def test_facade_matches_oracle(tmp_path, wtype, layout):
     o = orc.Oracle(cfg, w, threads=8)
     co, _ = o.generate(text, spk, max_len=max_len, temperature=0.0)
     assert np.array_equal(codes, co)
+    # the ATTD file of set_attn_dump (src/tts_transformer.cpp:2978-3005):
+    # one row per talker step of the frame loop, layer 1
+    raw = (tmp_path / "attn.bin").read_bytes()
+    magic, version, layer, n_head, n_rows = struct.unpack_from("<Iiiii", raw, 0)
+    assert (magic, version, layer, n_head) == (0x41545444, 1, 1, cfg.n_head)
+    o.set_attn_capture(1)
+    o.generate(text, spk, max_len=max_len, temperature=0.0)
+    rows_o = o.attn_rows()
+    o.set_attn_capture(-1)
+    assert n_rows == len(rows_o) == min(co.shape[0], max_len - 1)
+    off = 20
+    for ro in rows_o:
+        (n_kv,) = struct.unpack_from("<i", raw, off)
+        row = np.frombuffer(raw, np.float32, n_head * n_kv, off + 4).reshape(n_head, n_kv)
+        off += 4 + 4 * n_head * n_kv
+        assert np.array_equal(row, ro)
+    assert off == len(raw)
     hid = np.fromfile(tmp_path / "hidden.bin", np.float32)
     cp = np.fromfile(tmp_path / "cp.bin", np.int32)
     cpo, _ = o.code_pred(hid, 5)

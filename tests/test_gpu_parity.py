@@ -185,6 +185,45 @@ def test_callback_abort(tiny_model, frame_path):
     assert cg.shape[0] == 5
 
 
+def test_attention_capture_matches_oracle(tiny_model, frame_path):
+    """q3t_dev_set_attn_capture: the post-softmax rows of one talker layer,
+    one per talker step (single steps and every frame of the loop but the
+    last), bit for bit the oracle's; capture runs the multi-kernel step."""
+    cfg, w, dev, o = tiny_model
+    rng = np.random.default_rng(12)
+    d = cfg.hidden_size
+    try:
+        dev.set_attn_capture(1)
+        o.set_attn_capture(1)
+        embd = (rng.standard_normal((6, d)) * 0.05).astype(np.float32)
+        dev.prefill(embd, 0)
+        o.prefill(embd, 0)
+        for s in range(3):
+            e = (rng.standard_normal(d) * 0.05).astype(np.float32)
+            lg, _ = dev.talker_step(e, 6 + s)
+            lo, _ = o.step(e, 6 + s)
+            assert np.array_equal(lg, lo)
+        rg, ro = dev.attn_rows(), o.attn_rows()
+        assert len(rg) == len(ro) == 3
+        for a, b in zip(rg, ro):
+            assert a.shape == b.shape and np.array_equal(a, b)
+        text = rng.integers(0, cfg.text_vocab - 8, 16).astype(np.int32)
+        dev.set_attn_capture(0)
+        o.set_attn_capture(0)
+        say(f"[gpu] attention capture over 12 greedy frames ({frame_path})")
+        co, _ = o.generate(text, None, max_len=12, temperature=0.0, top_k=0)
+        cg = driver.generate(dev, cfg, text, None, max_len=12, temperature=0.0, top_k=0, chunk=5)
+        assert np.array_equal(cg, co)
+        assert dev.frames_stats()[2] == 0
+        rg, ro = dev.attn_rows(), o.attn_rows()
+        assert len(ro) == min(co.shape[0], 11) and len(rg) == len(ro)
+        for a, b in zip(rg, ro):
+            assert a.shape == b.shape and np.array_equal(a, b)
+    finally:
+        dev.set_attn_capture(-1)
+        o.set_attn_capture(-1)
+
+
 def test_fp16_tie_rounding_regression(frame_path):
     """Weights and prompt on which one attention probability of the talker
     (frame 13, layer 1) lands exactly on an fp16 tie after fp32 rounding; a

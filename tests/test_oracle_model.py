@@ -67,6 +67,7 @@ class NpRef:
         self.cfg, self.w, self.mistakes = cfg, w, set(mistakes)
         self.cache = {}
         self.kv = {}
+        self.capture = None      # (talker layer prefix, list): post-softmax rows [n_head][n_kv] of single-row calls
 
     # -- tensors
     def mat(self, name):
@@ -146,6 +147,10 @@ class NpRef:
                 s = K[:, g] @ qh / np.sqrt(hd)
                 p = np.exp(s - s.max())
                 p /= p.sum()
+                if self.capture is not None and n == 1 and prefix == self.capture[0]:
+                    if hh == 0:
+                        self.capture[1].append(np.empty((nh, pos + 1)))
+                    self.capture[1][-1][hh] = f16r(p) if "attn_row_f16" in self.mistakes else p
                 if not f32:
                     p = f16r(p)
                 out[i, hh * hd:(hh + 1) * hd] = p @ V[:, g]
@@ -439,3 +444,39 @@ def test_full_width_layer_matches_numpy_forward():
     n_same = int(np.argmax(codes_o != codes_r)) if np.any(codes_o != codes_r) else len(codes_o)
     errs += [rel_err(lgs_o[s], lgs_r[s]) for s in range(max(n_same, 1))]
     assert_agrees(errs, "q8_0")
+
+
+def test_attention_rows_match_numpy_forward():
+    """orc_set_attn_capture keeps layer L's post-softmax row of every
+    orc_step (not of the prefill): [n_head][n_kv] with n_kv = position + 1,
+    each head's row summing to 1, equal to the float64 forward's softmax
+    before the fp16 rounding that feeds P.V.  Capturing the neighbouring layer
+    or the fp16-rounded P misses."""
+    cfg = qcfg.tiny(n_layers=2, cp_layers=1)
+    w = Weights(cfg, "f16", seed=37)
+    o = orc.Oracle(cfg, w, threads=4)
+    embd = (np.random.default_rng(43).standard_normal((9, cfg.hidden_size)) * 0.5).astype(np.float32)
+
+    def run(layer, mistakes=()):
+        ref = NpRef(cfg, w, mistakes)
+        ref.capture = (f"talker.blk.{layer}.", [])
+        _talker_run(ref, o, cfg, embd)
+        return ref.capture[1]
+
+    o.set_attn_capture(1)
+    rows_r = run(1)
+    rows_o = o.attn_rows()
+    assert len(rows_o) == len(rows_r) == 4            # the four steps after a 5-row prefill
+    for i, (ro, rr) in enumerate(zip(rows_o, rows_r)):
+        assert ro.shape == (cfg.n_head, 5 + i + 1) and rr.shape == ro.shape
+        assert np.allclose(ro.astype(np.float64).sum(axis=1), 1.0, atol=1e-6)
+    assert_agrees([rel_err(ro, rr) for ro, rr in zip(rows_o, rows_r)], "f16")
+    o.set_attn_capture(1)
+    _talker_run(NpRef(cfg, w), o, cfg, embd)
+    rows_o = o.attn_rows()
+    for mistake, layer in ((("attn_row_f16",), 1), ((), 0)):
+        rows_m = run(layer, mistake)
+        assert_misses([rel_err(ro, rm) for ro, rm in zip(rows_o, rows_m)])
+    o.set_attn_capture(-1)
+    _talker_run(NpRef(cfg, w), o, cfg, embd)
+    assert o.attn_rows() == []
