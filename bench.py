@@ -159,21 +159,30 @@ def prefill_bench(args, cfg, w):
 def step_bench(args, cfg, w):
     """One talker decode step (forward_step: 28 layers + output norm + codec
     head, batch 1) with the KV cache pre-filled at 512 positions with seeded
-    N(0, 1) fp16 K/V rows, the new token at position 512.  Each call is one
-    q3t_dev_talker_step (the persistent kernel's talker pass, logits and
-    hidden copied back to the host); reports the mean wall time per step and
-    the HIP event timings of the multi-kernel step's kernels for talker layer
-    0 at that context."""
+    N(0, 1) bfloat16-valued K/V rows, the new token at position 512.  Each
+    call is one q3t_dev_talker_step (logits and hidden copied back to the
+    host): the persistent kernel's talker pass for an fp16 cache, the
+    multi-kernel step for a bfloat16 cache (--kv bf16).  Reports the mean wall
+    time per step and the HIP event timings of the multi-kernel step's kernels
+    for talker layer 0 at that context."""
     from qwen3_tts_amd.device import Device
     rng = np.random.default_rng(31)
     n_kv = 512
     dev = Device(cfg, 0)
     dev.upload_weights(w)
+    if args.kv == "bf16":
+        dev.kv_set_type(30)
     dev.kv_reserve(n_kv + 8)
+
+    def bf16_bits(x):
+        u = x.view(np.uint32)
+        return ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
     for layer in range(cfg.n_layers):
-        k = rng.standard_normal((n_kv, cfg.n_kv_head, cfg.head_dim)).astype(np.float16)
-        v = rng.standard_normal((n_kv, cfg.n_kv_head, cfg.head_dim)).astype(np.float16)
-        dev.kv_write(layer, k, v)
+        kv = [bf16_bits(rng.standard_normal((n_kv, cfg.n_kv_head, cfg.head_dim), dtype=np.float32)) for _ in range(2)]
+        if args.kv == "f16":    # the same bfloat16 values, held exactly in fp16
+            kv = [(b.astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float16) for b in kv]
+        dev.kv_write(layer, kv[0], kv[1])
     x = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
     for _ in range(max(args.warmup, 1)):
         dev.talker_step(x, n_kv)
@@ -196,9 +205,11 @@ def step_bench(args, cfg, w):
         "metric": "talker decode step latency (KV 512)", "value": round(dt * 1e3, 4), "unit": "ms",
         "n_gpus": 1, "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(dt * 1e3, 4),
         "higher_is_better": False, "dtype": "int8" if args.weights == "q8_0" else "f16",
-        "data": "synthetic (seeded weights, N(0,1) fp16 KV)",
-        "config": {"workload": f"one talker decode step, {args.weights.upper()} 0.6B shapes, KV pre-filled to "
-                               f"{n_kv} positions, persistent-kernel step with host copy-back", "global_batch": 1},
+        "data": f"synthetic (seeded weights, N(0,1) bfloat16-valued K/V in a {args.kv} cache)",
+        "config": {"workload": f"one talker decode step, {args.weights.upper()} 0.6B shapes, {args.kv} KV pre-filled to "
+                               f"{n_kv} positions, " + ("persistent-kernel step" if args.kv == "f16" else
+                                                        "multi-kernel step") + " with host copy-back",
+                   "global_batch": 1, "kv_type": args.kv},
         "step_algorithmic_bytes": int(wbytes + kvbytes),
         "step_hbm_gbs": round((wbytes + kvbytes) / dt / 1e9, 1),
         "kernels": kernels}))
@@ -364,6 +375,7 @@ def main():
                     help="instead of the frame loop, time one talker prefill of this many rows (Q8_0: int8 MFMA path)")
     ap.add_argument("--talker-step", action="store_true",
                     help="instead of the frame loop, time one talker decode step at a 512-position KV cache")
+    ap.add_argument("--kv", default="f16", choices=["f16", "bf16"], help="--talker-step: talker KV cache type")
     ap.add_argument("--long", action="store_true",
                     help="instead of the short-prompt greedy loop, time long-context sampled decode after a long prefill")
     ap.add_argument("--long-prompt", type=int, default=2048, help="text ids of the --long prefill")

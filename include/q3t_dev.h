@@ -18,7 +18,8 @@
  * per-32-block Q8_0-quantised activation (int8 x int8 block dots); F16
  * weights take an fp16-rounded activation; F16 ffn_down takes the fp32
  * activation; every dot product accumulates exact terms in fp64 and rounds
- * once to fp32.  KV cache is fp16.
+ * once to fp32.  The talker KV cache is fp16 as in the reference (bfloat16
+ * on request, q3t_dev_kv_set_type).
  */
 #ifndef Q3T_DEV_H
 #define Q3T_DEV_H
@@ -33,6 +34,7 @@ extern "C" {
 #define Q3T_TYPE_F32  0   /* ggml GGML_TYPE_F32  */
 #define Q3T_TYPE_F16  1   /* ggml GGML_TYPE_F16  */
 #define Q3T_TYPE_Q8_0 8   /* ggml GGML_TYPE_Q8_0 */
+#define Q3T_TYPE_BF16 30  /* ggml GGML_TYPE_BF16 (talker KV cache only) */
 
 /* Hyperparameters.  Mirrors tts_transformer_config
  * (src/tts_transformer.h:59-103) field for field; values come from the
@@ -114,11 +116,24 @@ int  q3t_dev_download_tensor(q3t_dev * dev, const char * name, void * data, size
 /* Dequantises a Q8_0 tensor on the device to fp32 [ne1][ne0] (fp32(d)*q). */
 int  q3t_dev_dequantize(q3t_dev * dev, const char * name, float * out, size_t n_floats);
 
-/* Talker KV cache of n_ctx positions (fp16, per layer [n_kv_head][n_ctx][head_dim]).
- * Replaces init_kv_cache / clear_kv_cache (src/tts_transformer.cpp:731-783). */
+/* Talker KV cache of n_ctx positions (fp16 or bfloat16, per layer
+ * [n_kv_head][n_ctx][head_dim]).  Replaces init_kv_cache / clear_kv_cache
+ * (src/tts_transformer.cpp:731-783).  n_ctx is bounded by the decode
+ * attention's LDS (a head's n_ctx fp32 scores in one workgroup: about 38,600
+ * positions on gfx950, past the talker's 32,768-position table). */
 int  q3t_dev_kv_reserve(q3t_dev * dev, int32_t n_ctx);
 int  q3t_dev_kv_clear(q3t_dev * dev);
 int32_t q3t_dev_kv_capacity(const q3t_dev * dev);
+/* Talker KV element type: Q3T_TYPE_F16 (the reference's, init_kv_cache at
+ * src/tts_transformer.cpp:761-768; the default) or Q3T_TYPE_BF16, the cache
+ * type as a parameter for timing configuration 2.  With BF16, q and the
+ * softmax probabilities are rounded to bfloat16 where the F16 cache rounds
+ * them to fp16 (ggml_mul_mat's conversion of its F32 operand to the cache's
+ * dot type).  A reserved cache is re-reserved (cleared).  BF16 runs the
+ * multi-kernel path (single steps, prefill, frame loop); the persistent frame
+ * kernel and multi-stream decode take F16 only.  q3t_dev_kv_write rows are
+ * then bfloat16 bits. */
+int  q3t_dev_kv_set_type(q3t_dev * dev, int32_t type);
 /* Attention-row capture, the device side of set_attn_dump / attn_rows
  * (src/tts_transformer.h:224-227; rows captured in forward_step,
  * src/tts_transformer.cpp:1719-1724 and :2485-2497).  layer in

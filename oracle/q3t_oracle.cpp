@@ -256,6 +256,16 @@ uint16_t orc_f32_to_f16(float f) {
     return sign | (uint16_t) h;
 }
 
+// bfloat16 <-> fp32 as ggml converts them (GGML_FP32_TO_BF16: round to
+// nearest even on the upper 16 bits, NaN kept quiet; the reverse is a shift).
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t) h << 16); }
+
+uint16_t orc_f32_to_bf16(float f) {
+    const uint32_t x = f2u(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t) ((x >> 16) | 64u);
+    return (uint16_t) ((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+}
+
 float orc_expf(float x) {
     if (x != x) return x;
     if (x < -87.0f) return 0.0f;
@@ -346,19 +356,30 @@ void orc_rope_neox(float * x, int64_t head_dim, const float * c, const float * s
 void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
                    int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
                    int64_t n_kv, float * out, float * probs_out) {
+    orc_attention_typed(q, k, v, n_head, n_kv_head, hd, n_ctx, n_kv, out, probs_out, 0);
+}
+
+// bf16: a BF16 cache.  ggml_mul_mat converts its F32 operand to the cache
+// type's dot type, so q and P are rounded to bfloat16 instead of fp16; the
+// products of two bfloat16 values (16 significant bits) stay exact in fp64.
+void orc_attention_typed(const float * q, const uint16_t * k, const uint16_t * v,
+                         int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
+                         int64_t n_kv, float * out, float * probs_out, int32_t bf16) {
     const float scale = 1.0f / std::sqrt((float) hd);
     const int64_t group = n_head / n_kv_head;
     std::vector<float> qh(hd), s(n_kv);
     std::vector<uint16_t> p16(n_kv);
+    auto to_f = [bf16](uint16_t x) { return bf16 ? orc_bf16_to_f32(x) : h2f(x); };
+    auto to_h = [bf16](float x) { return bf16 ? orc_f32_to_bf16(x) : orc_f32_to_f16(x); };
     for (int64_t h = 0; h < n_head; ++h) {
         const int64_t kvh = h / group;
-        for (int64_t d = 0; d < hd; ++d) qh[d] = h2f(orc_f32_to_f16(q[h * hd + d]));
+        for (int64_t d = 0; d < hd; ++d) qh[d] = to_f(to_h(q[h * hd + d]));
         const uint16_t * kh = k + kvh * n_ctx * hd;
         const uint16_t * vh = v + kvh * n_ctx * hd;
         float mx = -INFINITY;
         for (int64_t j = 0; j < n_kv; ++j) {
             double acc = 0.0;
-            for (int64_t d = 0; d < hd; ++d) acc += (double) qh[d] * (double) h2f(kh[j * hd + d]);
+            for (int64_t d = 0; d < hd; ++d) acc += (double) qh[d] * (double) to_f(kh[j * hd + d]);
             s[j] = (float) acc * scale;
             mx = std::max(mx, s[j]);
         }
@@ -368,11 +389,11 @@ void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
         for (int64_t j = 0; j < n_kv; ++j) {
             const float p = s[j] * inv;
             if (probs_out) probs_out[h * n_kv + j] = p;
-            p16[j] = orc_f32_to_f16(p);
+            p16[j] = to_h(p);
         }
         for (int64_t d = 0; d < hd; ++d) {
             double acc = 0.0;
-            for (int64_t j = 0; j < n_kv; ++j) acc += (double) h2f(p16[j]) * (double) h2f(vh[j * hd + d]);
+            for (int64_t j = 0; j < n_kv; ++j) acc += (double) to_f(p16[j]) * (double) to_f(vh[j * hd + d]);
             out[h * hd + d] = (float) acc;
         }
     }
@@ -497,8 +518,9 @@ struct Layer {
 };
 
 struct KV {
-    std::vector<uint16_t> k, v;   // [layers][n_kv_head][n_ctx][hd]
+    std::vector<uint16_t> k, v;   // [layers][n_kv_head][n_ctx][hd], fp16 or (bf16) bfloat16 bits
     int32_t n_ctx = 0;
+    int32_t bf16 = 0;
 };
 
 }  // namespace
@@ -571,8 +593,9 @@ void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float
             orc_rmsnorm(kh, fp(L.k_norm), hd, c.rms_eps, kh);
             orc_rope_neox(kh, hd, rc + pos * half, rs + pos * half);
             for (int64_t e = 0; e < hd; ++e) {
-                kc[(hh * kv.n_ctx + pos) * hd + e] = orc_f32_to_f16(kh[e]);
-                vc[(hh * kv.n_ctx + pos) * hd + e] = orc_f32_to_f16(v[i * kd + hh * hd + e]);
+                const float ve = v[i * kd + hh * hd + e];
+                kc[(hh * kv.n_ctx + pos) * hd + e] = kv.bf16 ? orc_f32_to_bf16(kh[e]) : orc_f32_to_f16(kh[e]);
+                vc[(hh * kv.n_ctx + pos) * hd + e] = kv.bf16 ? orc_f32_to_bf16(ve) : orc_f32_to_f16(ve);
             }
         }
     }
@@ -583,8 +606,8 @@ void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float
     } else {
         m->pool.run(ntok, [&](int64_t i0, int64_t i1) {
             for (int64_t i = i0; i < i1; ++i)
-                orc_attention(q.data() + i * qd, kc, vc, nh, nkv, hd, kv.n_ctx, pos0 + i + 1, o.data() + i * qd,
-                              ntok == 1 ? probs : nullptr);
+                orc_attention_typed(q.data() + i * qd, kc, vc, nh, nkv, hd, kv.n_ctx, pos0 + i + 1,
+                                    o.data() + i * qd, ntok == 1 ? probs : nullptr, kv.bf16);
         });
     }
     gemv_t(m, L.wo, d, qd, o.data(), ntok, t.data());
@@ -704,6 +727,12 @@ int orc_kv_reset(orc_model * m, int32_t n_ctx) {
     m->cp_kv.k.assign((size_t) c.cp_layers * c.n_kv_head * 16 * c.head_dim, 0);
     m->cp_kv.v.assign(m->cp_kv.k.size(), 0);
     ensure_rope(m, std::max(n_ctx, 16));
+    return 0;
+}
+
+int orc_kv_set_type(orc_model * m, int32_t type) {
+    if (type != 1 && type != 30) { m->err = "talker KV type must be F16 (1) or BF16 (30)"; return -1; }
+    m->kv.bf16 = type == 30;
     return 0;
 }
 

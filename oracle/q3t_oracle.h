@@ -138,6 +138,14 @@ void orc_rope_table(float theta_base, int64_t head_dim, int64_t n_pos, float * c
 void orc_attention(const float * q, const uint16_t * k, const uint16_t * v,
                    int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
                    int64_t n_kv, float * out, float * probs_out);
+/* the same over a bfloat16 cache when bf16 != 0 (the configuration-2 timing
+ * variant; the reference's cache is F16): q and P are rounded to bfloat16,
+ * ggml_mul_mat's conversion of its F32 operand to a BF16 cache's dot type. */
+void orc_attention_typed(const float * q, const uint16_t * k, const uint16_t * v,
+                         int64_t n_head, int64_t n_kv_head, int64_t hd, int64_t n_ctx,
+                         int64_t n_kv, float * out, float * probs_out, int32_t bf16);
+float    orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
 /* the code predictor's 2-token prefill attention (src/tts_transformer.cpp:
  * 1999-2012): q, K and V are the F32 rows of the call, P stays F32; causal
  * over the first n_kv rows.  k, v: row j of KV head h at
@@ -169,6 +177,9 @@ const char * orc_last_error(const orc_model * m);
 int         orc_kv_reset(orc_model * m, int32_t n_ctx);
 /* fp16 K/V rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos) of
  * talker layer `layer` (the layout q3t_dev_kv_write takes). */
+/* talker cache element type: 1 (F16, the reference's) or 30 (BF16); kept
+ * across orc_kv_reset, set it before the cache is filled. */
+int         orc_kv_set_type(orc_model * m, int32_t type);
 int         orc_kv_write(orc_model * m, int32_t layer, int32_t n_pos, const uint16_t * k, const uint16_t * v);
 /* the inverse: rows of positions [0, n_pos) of talker layer `layer`. */
 int         orc_kv_read(orc_model * m, int32_t layer, int32_t n_pos, uint16_t * k, uint16_t * v);

@@ -77,6 +77,11 @@ def lib():
         L.orc_last_error.argtypes = [vp]; L.orc_last_error.restype = ctypes.c_char_p
         L.orc_kv_reset.argtypes = [vp, i32]
         L.orc_kv_write.argtypes = [vp, i32, i32, vp, vp]
+        L.orc_kv_set_type.argtypes = [vp, i32]
+        L.orc_attention_typed.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, i32]
+        L.orc_attention_typed.restype = None
+        L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]; L.orc_bf16_to_f32.restype = f32
+        L.orc_f32_to_bf16.argtypes = [f32]; L.orc_f32_to_bf16.restype = ctypes.c_uint16
         L.orc_kv_read.argtypes = [vp, i32, i32, vp, vp]
         L.orc_prefill.argtypes = [vp, vp, i32, i32, vp, vp]
         L.orc_step.argtypes = [vp, vp, i32, vp, vp]
@@ -173,6 +178,20 @@ def attention(q, k, v, n_kv):
     return out, probs
 
 
+def attention_bf16(q, k, v, n_kv):
+    """attention() over a bfloat16 cache: k, v uint16 bfloat16 bits
+    [n_kv_head][n_ctx][hd]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.uint16)
+    v = np.ascontiguousarray(v, np.uint16)
+    nh, hd = q.shape
+    nkv, nctx, _ = k.shape
+    out = np.empty((nh, hd), np.float32)
+    probs = np.empty((nh, n_kv), np.float32)
+    lib().orc_attention_typed(_p(q), _p(k), _p(v), nh, nkv, hd, nctx, n_kv, _p(out), _p(probs), 1)
+    return out, probs
+
+
 def attention_f32(q, k, v):
     """The code predictor's prefill attention: q [n_head][hd], k and v
     [n_kv][n_kv_head][hd], all f32; causal, query i sees rows 0..i when q has
@@ -257,10 +276,15 @@ class Oracle:
     def kv_reset(self, n_ctx):
         self._chk(self.L.orc_kv_reset(self.h, n_ctx), "kv_reset")
 
+    def kv_set_type(self, ttype):
+        """Talker cache element type: 1 (F16) or 30 (BF16)."""
+        self._chk(self.L.orc_kv_set_type(self.h, int(ttype)), "kv_set_type")
+
     def kv_write(self, layer, k, v):
-        """fp16 rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos)."""
-        k = np.ascontiguousarray(k, np.float16)
-        v = np.ascontiguousarray(v, np.float16)
+        """Rows [n_pos][n_kv_head][head_dim] into positions [0, n_pos): fp16
+        values, or uint16 element bits as stored (bfloat16 for a BF16 cache)."""
+        k = np.ascontiguousarray(k, np.uint16 if np.asarray(k).dtype == np.uint16 else np.float16)
+        v = np.ascontiguousarray(v, np.uint16 if np.asarray(v).dtype == np.uint16 else np.float16)
         self._chk(self.L.orc_kv_write(self.h, layer, k.shape[0], _p(k), _p(v)), "kv_write")
 
     def kv_read(self, layer, n_pos):

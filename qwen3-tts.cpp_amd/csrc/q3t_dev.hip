@@ -131,6 +131,7 @@ struct q3t_dev {
 
     // caches
     uint16_t * kc = nullptr, * vc = nullptr; int32_t n_ctx = 0;
+    bool kv_bf16 = false;          // talker cache elements are bfloat16 (q3t_dev_kv_set_type), else fp16
     uint16_t * cpk = nullptr, * cpv = nullptr;
     float * rope_cos = nullptr, * rope_sin = nullptr, * cp_rope_cos = nullptr, * cp_rope_sin = nullptr;
     int32_t rope_rows = 0;
@@ -447,6 +448,9 @@ struct AttnSpec {
 void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     const q3t_config & g = c->cfg;
     const int G = g.n_head / g.n_kv_head;
+    // the talker cache may be bfloat16; the code predictor's is always fp16
+    const size_t kv_elems = (size_t) g.n_layers * g.n_kv_head * c->n_ctx * g.head_dim;
+    const bool bf = c->kv_bf16 && s.kc >= c->kc && s.kc < c->kc + kv_elems;
     if (nt == 1 && s.rc == c->rope_cos && !s.probs && (G == 1 || G == 2 || G == 4) && c->gqa_lds_ok) {
         // one talker token: a 16-wave workgroup per query head streams its KV
         // head's cache (ms::k_attn_gqa, one head per workgroup)
@@ -461,7 +465,8 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
         q.out = c->attn; q.out_stride = g.n_head * g.head_dim;
         q.scale = 1.0f / std::sqrt((float) g.head_dim);
         const dim3 grid(g.n_head, 1), block(ms::kAThreads);
-        hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, s.n_ctx), c->stream, q);
+        if (bf) hipLaunchKernelGGL((ms::k_attn_gqa<1, true>), grid, block, ms::attn_gqa_lds_bytes(1, s.n_ctx), c->stream, q);
+        else hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, s.n_ctx), c->stream, q);
         return;
     }
     AttnArgs a{};
@@ -477,6 +482,7 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     a.nt = nt;
     a.probs_out = s.probs;
     a.f32_new = s.f32_prefill ? 1 : 0;
+    a.kv_bf16 = bf ? 1 : 0;
     hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt), dim3(kBlock), attn_lds_bytes(s.n_ctx), c->stream, a);
 }
 
@@ -695,7 +701,9 @@ const char * fk_err_msg(int32_t e) {
 
 int fk_prepare(q3t_dev * c) {
     c->fk_ok = false;
-    if (c->fk_refused || c->attn_layer >= 0) return 0;   // attention capture runs the multi-kernel step
+    // attention capture runs the multi-kernel step; the persistent kernel
+    // reads an fp16 talker cache only
+    if (c->fk_refused || c->attn_layer >= 0 || c->kv_bf16) return 0;
     if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
@@ -1195,6 +1203,8 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
             if (al <= (size_t) max_lds) {
                 HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int) al));
+                HIP_OK(hipFuncSetAttribute((const void *) ms::k_attn_gqa<1, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int) al));
                 c->gqa_lds_ok = true;
             }
         }
@@ -1205,6 +1215,19 @@ int q3t_dev_kv_reserve(q3t_dev * c, int32_t n_ctx) {
 int q3t_dev_kv_clear(q3t_dev * c) { return c ? 0 : -1; }
 
 int32_t q3t_dev_kv_capacity(const q3t_dev * c) { return c ? c->n_ctx : 0; }
+
+int q3t_dev_kv_set_type(q3t_dev * c, int32_t type) {
+    if (!c) return -1;
+    if (type != Q3T_TYPE_F16 && type != Q3T_TYPE_BF16) return fail(c, "talker KV type must be F16 or BF16");
+    const bool bf = type == Q3T_TYPE_BF16;
+    if (bf == c->kv_bf16) return 0;
+    c->kv_bf16 = bf;
+    c->fk_ok = false;
+    c->fk_args_ok = false;
+    c->frames_ready = false;
+    // a reserved cache is re-reserved (cleared) in the new type
+    return c->n_ctx > 0 ? q3t_dev_kv_reserve(c, c->n_ctx) : 0;
+}
 
 int q3t_dev_set_attn_capture(q3t_dev * c, int32_t layer) {
     if (!c) return -1;
@@ -1354,11 +1377,11 @@ void prefill_f16(q3t_dev * c, int n, int n_past) {
         pf_gemm_f16(c, L.qkv, qkvd, d, n, c->pf_f, d, false, c->pf_qkv, nullptr, 0);
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
-                           kc, vc, c->n_ctx, n_past);
+                           kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
         hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
                            c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
                            (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
-                           g.n_kv_head, n_past, scale, c->pf_att, qd);
+                           g.n_kv_head, n_past, scale, c->pf_att, qd, c->kv_bf16 ? 1 : 0);
         pf_gemm_f16(c, L.wo, d, qd, n, c->pf_att, qd, false, c->pf_xb, x, d);
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xb, L.ffn_norm,
                            g.rms_eps, d, c->pf_f);
@@ -1394,11 +1417,11 @@ void prefill_mfma(q3t_dev * c, int n, int n_past) {
         pf_gemm(c, L.qkv, qkvd, d, n, c->pf_qkv, nullptr);
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
-                           kc, vc, c->n_ctx, n_past);
+                           kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
         hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
                            c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
                            (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
-                           g.n_kv_head, n_past, scale, c->pf_att, qd);
+                           g.n_kv_head, n_past, scale, c->pf_att, qd, c->kv_bf16 ? 1 : 0);
         pf_quant(c, c->pf_att, n, qd, nullptr);
         pf_gemm(c, L.wo, d, qd, n, c->pf_xb, x);
         pf_quant(c, c->pf_xb, n, d, L.ffn_norm);
@@ -2326,6 +2349,7 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     const q3t_config & g = c->cfg;
     if (n_streams < 1 || n_streams > 32) return fail(c, "n_streams must be in [1, 32]");
     if (n_ctx < 1) return fail(c, "n_ctx must be > 0");
+    if (c->kv_bf16) return fail(c, "multi-stream decode keeps an F16 talker cache (q3t_dev_kv_set_type F16 first)");
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
         if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||

@@ -406,6 +406,9 @@ struct AttnArgs {
     // the F32 rows of this launch (src/tts_transformer.cpp:1999-2012): q, K, V
     // and P stay fp32; the fp16 cache rows are still written
     int32_t f32_new;
+    // 1: a bfloat16 cache (q and P are rounded to bfloat16, ggml_mul_mat's
+    // conversion of its F32 operand to a BF16 cache's dot type)
+    int32_t kv_bf16;
 };
 
 constexpr int kHD = 128;
@@ -476,7 +479,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         const float v = t < kHD ? row[h * kHD + t] : 0.0f;
         const float o = head_norm_rope(v, a.q_norm, a.eps, a.rope_cos + (size_t) pos * 64,
                                        a.rope_sin + (size_t) pos * 64, tmp, red);
-        if (t < kHD) qf[t] = a.f32_new ? o : round_f16(o);
+        if (t < kHD) qf[t] = a.f32_new ? o : round_kv(o, a.kv_bf16);
     }
     // k, v of this KV head for the chunk tokens 0..tok (positions >= pos0 are
     // never read from the cache inside this launch)
@@ -487,10 +490,10 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
                                        a.rope_sin + (size_t) (pos0 + j) * 64, tmp, red);
         if (t < kHD) {
             const float vraw = row[qd + kd + g * kHD + t];
-            const uint16_t kh = f2h(o);
-            const uint16_t vh = f2h(vraw);
-            knew[j * kHD + t] = a.f32_new ? o : h2f(kh);
-            vnew[j * kHD + t] = a.f32_new ? vraw : h2f(vh);
+            const uint16_t kh = f2kv(o, a.kv_bf16);
+            const uint16_t vh = f2kv(vraw, a.kv_bf16);
+            knew[j * kHD + t] = a.f32_new ? o : kv2f(kh, a.kv_bf16);
+            vnew[j * kHD + t] = a.f32_new ? vraw : kv2f(vh, a.kv_bf16);
             if (j == tok && (h % group) == 0) {
                 a.kc[((size_t) g * a.n_ctx + pos) * kHD + t] = kh;
                 a.vc[((size_t) g * a.n_ctx + pos) * kHD + t] = vh;
@@ -534,9 +537,9 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
                 const uint16_t * kh0 = (const uint16_t *) &k0;
                 const uint16_t * kh1 = (const uint16_t *) &k1;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + e] * h2f(kh0[e]));
+                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + e] * kv2f(kh0[e], a.kv_bf16));
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + 8 + e] * h2f(kh1[e]));
+                for (int e = 0; e < 8; ++e) acc += (double) (qf[sub * 16 + 8 + e] * kv2f(kh1[e], a.kv_bf16));
             } else {
                 const float * kr = knew + (j - pos0) * kHD + sub * 16;
 #pragma unroll
@@ -564,7 +567,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     for (int j = t; j < n_kv; j += kBlock) {
         const float p = sc[j] * inv;
         if (a.probs_out && tok == 0) a.probs_out[(size_t) h * n_kv + j] = p;
-        sc[j] = a.f32_new ? p : round_f16(p);
+        sc[j] = a.f32_new ? p : round_kv(p, a.kv_bf16);
     }
     __syncthreads();
 
@@ -582,7 +585,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
                 const int4 vv = *(const int4 *) (vbase + (size_t) j * kHD + dsub * 8);
                 const uint16_t * vh = (const uint16_t *) &vv;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] += (double) p * (double) h2f(vh[e]);
+                for (int e = 0; e < 8; ++e) o[e] += (double) p * (double) kv2f(vh[e], a.kv_bf16);
             } else {
                 // fp16 x fp16 or (prefill) fp32 x fp32: exact in fp64 either way
                 const float * vr = vnew + (j - pos0) * kHD + dsub * 8;

@@ -28,6 +28,19 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 }
 __device__ __forceinline__ float round_f16(float f) { return h2f(f2h(f)); }
 
+// bfloat16 (a BF16 talker cache): round to nearest even on the upper 16 bits,
+// NaN kept quiet, as ggml's GGML_FP32_TO_BF16; widening is exact.
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t) h << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t) ((x >> 16) | 64u);
+    return (uint16_t) ((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+}
+// Cache element <-> fp32 for an F16 (bf = false) or BF16 (bf = true) cache.
+__device__ __forceinline__ float kv2f(uint16_t h, bool bf) { return bf ? bf2f(h) : h2f(h); }
+__device__ __forceinline__ uint16_t f2kv(float f, bool bf) { return bf ? f2bf(f) : f2h(f); }
+__device__ __forceinline__ float round_kv(float f, bool bf) { return kv2f(f2kv(f, bf), bf); }
+
 // exp(x): Cody-Waite reduction x = k*ln2 + r (ln2 split hi/lo, fused
 // multiply-add), exp(r) by its degree-7 Taylor polynomial in Horner form,
 // scaled by 2^k built from the exponent field.  Results below 2^-126 are

@@ -233,14 +233,14 @@ __global__ __launch_bounds__(kBlock) void k_swiglu_rows(const float * __restrict
         f[i] = silu_q3t(g[i]) * u[i];
 }
 
-// K (QK-norm + NEOX RoPE, fp16) and V (fp16) rows of n tokens into the KV
-// cache at positions pos0 + tok.  Block (g, tok), 256 threads (threads < 128
-// own one element each).
+// K (QK-norm + NEOX RoPE) and V rows of n tokens into the KV cache at
+// positions pos0 + tok, fp16 or (bf) bfloat16.  Block (g, tok), 256 threads
+// (threads < 128 own one element each).
 __global__ __launch_bounds__(kBlock) void k_kv_rows(const float * __restrict__ qkv, int32_t qkv_stride, int32_t qd,
                                                     int32_t kd, const float * __restrict__ k_norm, float eps,
                                                     const float * __restrict__ rc, const float * __restrict__ rs,
                                                     uint16_t * __restrict__ kc, uint16_t * __restrict__ vc, int32_t n_ctx,
-                                                    int32_t pos0) {
+                                                    int32_t pos0, int32_t bf) {
     __shared__ double red[4];
     __shared__ float tmp[kHD];
     const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, pos = pos0 + tok;
@@ -248,20 +248,22 @@ __global__ __launch_bounds__(kBlock) void k_kv_rows(const float * __restrict__ q
     const float kv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
     const float o = head_norm_rope(kv, k_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
     if (t < kHD) {
-        kc[((size_t) g * n_ctx + pos) * kHD + t] = f2h(o);
-        vc[((size_t) g * n_ctx + pos) * kHD + t] = f2h(row[qd + kd + g * kHD + t]);
+        kc[((size_t) g * n_ctx + pos) * kHD + t] = f2kv(o, bf);
+        vc[((size_t) g * n_ctx + pos) * kHD + t] = f2kv(row[qd + kd + g * kHD + t], bf);
     }
 }
 
 // Causal attention of n tokens over the cache (all rows already written).
 // Block (h, tok): q-norm + RoPE, scores over positions [0, pos0+tok], fp64
-// softmax denominator, fp16 probabilities, fp64 P.V.  out [n][qd].
+// softmax denominator, fp16 (bf: bfloat16) probabilities, fp64 P.V.
+// out [n][qd].
 __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__ qkv, int32_t qkv_stride,
                                                       const float * __restrict__ q_norm, float eps,
                                                       const float * __restrict__ rc, const float * __restrict__ rs,
                                                       const uint16_t * __restrict__ kc, const uint16_t * __restrict__ vc,
                                                       int32_t n_ctx, int32_t n_head, int32_t n_kv_head, int32_t pos0,
-                                                      float scale, float * __restrict__ out, int32_t out_stride) {
+                                                      float scale, float * __restrict__ out, int32_t out_stride,
+                                                      int32_t bf) {
     extern __shared__ __align__(16) char smem[];
     double * red = (double *) smem;                   // 4 doubles
     float * fred = (float *) (smem + 32);             // 4 floats
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__
     {
         const float v = t < kHD ? qkv[(size_t) tok * qkv_stride + h * kHD + t] : 0.0f;
         const float o = head_norm_rope(v, q_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
-        if (t < kHD) qf[t] = round_f16(o);
+        if (t < kHD) qf[t] = round_kv(o, bf);
     }
     __syncthreads();
     const int lane = t & 63, wave = t >> 6, sub = lane & 15, pw = lane >> 4;
@@ -292,7 +294,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__
             const int4 k4 = *(const int4 *) (kb + (size_t) j * kHD + sub * 8);
             const uint16_t * kh = (const uint16_t *) &k4;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc = fma(qd8[e], (double) h2f(kh[e]), acc);   // exact products
+            for (int e = 0; e < 8; ++e) acc = fma(qd8[e], (double) kv2f(kh[e], bf), acc);   // exact products
         }
         acc = group_sum_d(acc, 16);
         if (j < n_kv) {
@@ -310,15 +312,15 @@ __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__
     }
     const double sum = block_sum_d(lsum, red);
     const float inv = (float) (1.0 / sum);
-    for (int j = t; j < n_kv; j += kBlock) sc[j] = round_f16(sc[j] * inv);
+    for (int j = t; j < n_kv; j += kBlock) sc[j] = round_kv(sc[j] * inv, bf);
     __syncthreads();
     // P.V: lane owns dims 2*lane, 2*lane+1; wave w takes positions w, w+4, ...
     double o0 = 0.0, o1 = 0.0;
     for (int j = wave; j < n_kv; j += 4) {
         const double p = (double) sc[j];
         const uint32_t w2 = *(const uint32_t *) (vb + (size_t) j * kHD + 2 * lane);
-        o0 = fma(p, (double) h2f((uint16_t) (w2 & 0xffffu)), o0);
-        o1 = fma(p, (double) h2f((uint16_t) (w2 >> 16)), o1);
+        o0 = fma(p, (double) kv2f((uint16_t) (w2 & 0xffffu), bf), o0);
+        o1 = fma(p, (double) kv2f((uint16_t) (w2 >> 16), bf), o1);
     }
     pv[wave * kHD + 2 * lane] = o0;
     pv[wave * kHD + 2 * lane + 1] = o1;

@@ -444,8 +444,9 @@ __device__ __forceinline__ void wave_norm_rope(float & x0, float & x1, const flo
 // Workgroup x takes query heads G x .. G x + G - 1 of stream blockIdx.y; with
 // G below the group size two or more workgroups share a KV head, read its
 // cache each, and only the first appends the new K/V row (the others take
-// the new row from their own LDS).
-template <int G>
+// the new row from their own LDS).  BF: a bfloat16 cache (q and P rounded to
+// bfloat16 as well).
+template <int G, bool BF = false>
 __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
     const int hq0 = blockIdx.x * G, z = blockIdx.y;
     const int gsz = a.n_head / a.n_kv_head, g = hq0 / gsz;
@@ -473,22 +474,22 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
         const int h = hq0 + wave;
         float x0 = row[h * kHD + lane], x1 = row[h * kHD + 64 + lane];
         wave_norm_rope(x0, x1, a.q_norm, a.eps, rc, rs);
-        qf[wave * kHD + lane] = round_f16(x0);
-        qf[wave * kHD + 64 + lane] = round_f16(x1);
+        qf[wave * kHD + lane] = round_kv(x0, BF);
+        qf[wave * kHD + 64 + lane] = round_kv(x1, BF);
     } else if (wave == G) {
         float x0 = row[qd + g * kHD + lane], x1 = row[qd + g * kHD + 64 + lane];
         wave_norm_rope(x0, x1, a.k_norm, a.eps, rc, rs);
-        const uint16_t k0 = f2h(x0), k1 = f2h(x1);
-        knew[lane] = h2f(k0);
-        knew[lane + 64] = h2f(k1);
+        const uint16_t k0 = f2kv(x0, BF), k1 = f2kv(x1, BF);
+        knew[lane] = kv2f(k0, BF);
+        knew[lane + 64] = kv2f(k1, BF);
         if (append) {
             kbase[(size_t) pos * kHD + lane] = k0;
             kbase[(size_t) pos * kHD + 64 + lane] = k1;
         }
     } else if (wave == G + 1) {
-        const uint16_t v0 = f2h(row[qd + kd + g * kHD + lane]), v1 = f2h(row[qd + kd + g * kHD + 64 + lane]);
-        vnew[lane] = h2f(v0);
-        vnew[lane + 64] = h2f(v1);
+        const uint16_t v0 = f2kv(row[qd + kd + g * kHD + lane], BF), v1 = f2kv(row[qd + kd + g * kHD + 64 + lane], BF);
+        vnew[lane] = kv2f(v0, BF);
+        vnew[lane + 64] = kv2f(v1, BF);
         if (append) {
             vbase[(size_t) pos * kHD + lane] = v0;
             vbase[(size_t) pos * kHD + 64 + lane] = v1;
@@ -531,7 +532,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
             if (j < pos) {
                 const uint16_t * kh = (const uint16_t *) &kv[u];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) kf[e] = (double) h2f(kh[e]);
+                for (int e = 0; e < 8; ++e) kf[e] = (double) kv2f(kh[e], BF);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) kf[e] = j == pos ? (double) knew[dsub * 8 + e] : 0.0;
@@ -585,7 +586,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
     }
 #pragma unroll
     for (int h = 0; h < G; ++h)
-        for (int j = t; j < n_kv; j += kAThreads) sc[h * a.n_ctx + j] = round_f16(sc[h * a.n_ctx + j] * inv[h]);
+        for (int j = t; j < n_kv; j += kAThreads) sc[h * a.n_ctx + j] = round_kv(sc[h * a.n_ctx + j] * inv[h], BF);
     __syncthreads();
 
     // P.V: same position mapping; each V row read once for the group's heads
@@ -616,7 +617,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_gqa(GqaArgs a) {
             if (j < pos) {
                 const uint16_t * vh = (const uint16_t *) &vv[u];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = (double) h2f(vh[e]);
+                for (int e = 0; e < 8; ++e) vf[e] = (double) kv2f(vh[e], BF);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) vf[e] = (double) vnew[dsub * 8 + e];

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(PKG_DIR, "lib", "libq3t_hip.so")
 EXPORTS = [
     "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
-    "q3t_dev_kv_capacity", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
+    "q3t_dev_kv_capacity", "q3t_dev_kv_set_type", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
     "q3t_dev_attn_row", "q3t_dev_prefill", "q3t_dev_talker_step",
     "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
     "q3t_dev_build_prefill",
@@ -62,6 +62,7 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_kv_clear.argtypes = [vp]
         lib.q3t_dev_kv_capacity.argtypes = [vp]
         lib.q3t_dev_kv_write.argtypes = [vp, i32, i32, vp, vp]
+        lib.q3t_dev_kv_set_type.argtypes = [vp, i32]
         lib.q3t_dev_set_attn_capture.argtypes = [vp, i32]
         lib.q3t_dev_attn_row_count.argtypes = [vp]
         lib.q3t_dev_attn_row.argtypes = [vp, i32, f32p, ctypes.c_int64, ctypes.POINTER(i32)]
@@ -151,9 +152,14 @@ class Device:
     def kv_reserve(self, n_ctx):
         self._check(self.lib.q3t_dev_kv_reserve(self.h, n_ctx), "kv_reserve")
 
+    def kv_set_type(self, ttype):
+        """Talker cache element type for the next kv_reserve: 1 (F16) or 30 (BF16)."""
+        self._check(self.lib.q3t_dev_kv_set_type(self.h, int(ttype)), "kv_set_type")
+
     def kv_write(self, layer, k, v):
-        k = np.ascontiguousarray(k, dtype=np.float16)
-        v = np.ascontiguousarray(v, dtype=np.float16)
+        """fp16 values, or uint16 element bits as stored (bfloat16 for a BF16 cache)."""
+        k = np.ascontiguousarray(k, np.uint16 if np.asarray(k).dtype == np.uint16 else np.float16)
+        v = np.ascontiguousarray(v, np.uint16 if np.asarray(v).dtype == np.uint16 else np.float16)
         self._check(self.lib.q3t_dev_kv_write(self.h, layer, k.shape[0], _p(k), _p(v)), "kv_write")
 
     # -- forward passes

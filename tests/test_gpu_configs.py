@@ -147,6 +147,34 @@ def test_context_past_12288_f16(path):
         dev.close()
 
 
+def test_config2_bf16_kv_step():
+    """Configuration 2 with a bfloat16 talker cache (q3t_dev_kv_set_type):
+    N(0,1) bfloat16 K/V at 512 positions, then steps at 512.. on the
+    multi-kernel step, bit for bit the oracle's bfloat16 form."""
+    cfg, w, dev, o = open_pair("f16", 51, 528)
+    try:
+        dev.kv_set_type(30)
+        o.kv_set_type(30)
+        o.kv_reset(528)
+        rng = np.random.default_rng(59)
+        say("[gpu] writing 512 bfloat16 K/V positions x 28 layers")
+        for il in range(cfg.n_layers):
+            x = rng.standard_normal((2, 512, cfg.n_kv_head, cfg.head_dim), dtype=np.float32)
+            u = x.view(np.uint32)
+            bits = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+            dev.kv_write(il, bits[0], bits[1])
+            o.kv_write(il, bits[0], bits[1])
+        for s in range(3):
+            e = (rng.standard_normal(cfg.hidden_size) * 0.05).astype(np.float32)
+            say(f"[gpu] config 2 bf16 KV: step at n_past {512 + s}")
+            lg, hg = dev.talker_step(e, 512 + s)
+            lo, ho = o.step(e, 512 + s)
+            assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
+            assert np.array_equal(hg, ho)
+    finally:
+        dev.close()
+
+
 def _frames_both(dev, o, cfg, lo, n_past, n_frames, seed):
     rng = np.random.default_rng(seed)
     trail = (rng.standard_normal((5, cfg.hidden_size)) * 0.05).astype(np.float32)

@@ -224,6 +224,42 @@ def test_attention_capture_matches_oracle(tiny_model, frame_path):
         o.set_attn_capture(-1)
 
 
+def test_bf16_kv_prefill_steps_frames(prefill_path):
+    """A bfloat16 talker cache: prefill (GEMV or MFMA path), single steps and
+    a greedy frame loop (multi-kernel), each bit for bit the oracle's
+    bfloat16 form; the fp16 cache gives other logits on the same inputs."""
+    cfg = qcfg.tiny()
+    w, dev, o = make(cfg, "q8_0", seed=41)
+    try:
+        dev.kv_set_type(30)
+        o.kv_set_type(30)
+        o.kv_reset(256)
+        rng = np.random.default_rng(42)
+        d = cfg.hidden_size
+        embd = (rng.standard_normal((10, d)) * 0.5).astype(np.float32)
+        say(f"[gpu] bf16 KV: prefill 10 rows ({prefill_path})")
+        hid_g, log_g = dev.prefill(embd, 0)
+        hid_o, log_o = o.prefill(embd, 0)
+        assert np.array_equal(hid_g, hid_o) and np.array_equal(log_g, log_o)
+        for s in range(4):
+            e = (rng.standard_normal(d) * 0.5).astype(np.float32)
+            lg, hg = dev.talker_step(e, 10 + s)
+            lo, ho = o.step(e, 10 + s)
+            assert np.array_equal(lg, lo) and np.array_equal(hg, ho)
+        o16 = orc.Oracle(cfg, w, threads=8)
+        o16.kv_reset(256)
+        _, log16 = o16.prefill(embd, 0)
+        o16.close()
+        assert not np.array_equal(log16, log_o)
+        text = rng.integers(0, cfg.text_vocab - 8, 18).astype(np.int32)
+        co, _ = o.generate(text, None, max_len=16, temperature=0.0, top_k=0)
+        cg = driver.generate(dev, cfg, text, None, max_len=16, temperature=0.0, top_k=0, chunk=8)
+        assert dev.frames_stats()[2] == 0
+        assert np.array_equal(cg, co)
+    finally:
+        dev.close()
+
+
 def test_fp16_tie_rounding_regression(frame_path):
     """Weights and prompt on which one attention probability of the talker
     (frame 13, layer 1) lands exactly on an fp16 tie after fp32 rounding; a

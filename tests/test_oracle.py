@@ -250,6 +250,63 @@ def test_attention_matches_float64_softmax():
     assert np.allclose(out2[0], v[0, 7].astype(np.float32), atol=1e-2)
 
 
+def np_bf16_bits(x):
+    """fp32 -> bfloat16 bits, round to nearest even (numpy restatement)."""
+    u = np.asarray(x, np.float32).view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    return np.where(nan, ((u >> np.uint32(16)) | np.uint32(64)).astype(np.uint16), r)
+
+
+def bf16_to_f64(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float64)
+
+
+def test_bf16_conversions():
+    rng = np.random.default_rng(13)
+    x = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 10, rng.standard_normal(500).astype(np.float32)
+                        * 1e-39, np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, 1e-45], np.float32),
+                        # exact ties between two bfloat16 values: 1 + (2k+1) 2^-8
+                        (1.0 + (2 * np.arange(40) + 1) * 2.0 ** -8).astype(np.float32)])
+    L = orc.lib()
+    got = np.array([L.orc_f32_to_bf16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, np_bf16_bits(x))
+    # ties go to the even neighbour: 1 + 2^-8 -> 1.0, 1 + 3*2^-8 -> 1 + 2^-6
+    assert L.orc_f32_to_bf16(1.0 + 2.0 ** -8) == 0x3F80 and L.orc_f32_to_bf16(1.0 + 3 * 2.0 ** -8) == 0x3F82
+    assert (L.orc_f32_to_bf16(float("nan")) & 0x7FC0) == 0x7FC0
+    b = rng.integers(0, 65536, 2000).astype(np.uint16)
+    b = b[(b & 0x7F80) != 0x7F80]
+    assert np.array_equal(np.array([L.orc_bf16_to_f32(int(v)) for v in b], np.float32), bf16_to_f64(b).astype(np.float32))
+
+
+def test_attention_bf16_cache_matches_float64():
+    """Over a bfloat16 cache q and P are rounded to bfloat16 (not fp16): the
+    rows match a float64 evaluation with those rounding points; the fp16 form
+    misses."""
+    rng = np.random.default_rng(14)
+    nh, nkv, hd, nctx, n = 4, 2, 128, 40, 33
+    q = rng.standard_normal((nh, hd)).astype(np.float32)
+    k = np_bf16_bits(rng.standard_normal((nkv, nctx, hd)).astype(np.float32))
+    v = np_bf16_bits(rng.standard_normal((nkv, nctx, hd)).astype(np.float32))
+    out, p = orc.attention_bf16(q, k, v, n)
+    kf, vf = bf16_to_f64(k), bf16_to_f64(v)
+    for h in range(nh):
+        g = h // 2
+        qb = bf16_to_f64(np_bf16_bits(q[h]))
+        s = (kf[g, :n] @ qb).astype(np.float32) * np.float32(1.0 / np.sqrt(128.0))
+        pe = np.exp(s.astype(np.float64) - s.max())
+        pe /= pe.sum()
+        assert np.allclose(p[h], pe, rtol=1e-5, atol=1e-7)
+        o = bf16_to_f64(np_bf16_bits(p[h])) @ vf[g, :n]
+        assert np.allclose(out[h], o, rtol=1e-5, atol=1e-6)
+        o16 = p[h].astype(np.float16).astype(np.float64) @ vf[g, :n]
+        assert np.abs(out[h] - o16).max() > 1e-4
+    # the same values in an fp16 cache (bfloat16 values are exact in fp16 at
+    # these magnitudes) attend with fp16-rounded q and P: a different result
+    out16, _ = orc.attention(q, kf.astype(np.float16), vf.astype(np.float16), n)
+    assert np.abs(out16 - out).max() > 1e-4
+
+
 # ---------------------------------------------------------------- sampler
 def test_argmax_first_index_on_ties():
     x = np.array([0.1, 0.7, 0.2, 0.7, 0.7], np.float32)
