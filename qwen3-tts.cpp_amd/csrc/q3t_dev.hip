@@ -144,6 +144,7 @@ struct q3t_dev {
     int xcd_map = -1;              // workgroup b of the frame launch on XCD b % 8: -1 unknown, 0 no, 1 yes
     bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
     bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
+    bool fk_tab = false;           // the persistent kernel reads cp_tab
     int fk_grid = 0;
     fk::LayerQ8 * fk_layers = nullptr;
     uint64_t * fk_arena = nullptr; size_t fk_arena_bytes = 0;
@@ -157,6 +158,11 @@ struct q3t_dev {
     bool fk_layers_stale = false;      // a layer tensor was uploaded after fk_layers was built
     int32_t fk_epoch = 0;              // launches since the arena was cleared (the phase tags)
     float * fk_cand = nullptr;         // talker-head greedy candidates: 256 values then 256 indices
+    // code-predictor layer-0 QKV rows of every (codebook step, code): the
+    // input of steps 1..14 is an embedding row, so their first QKV GEMV is a
+    // table lookup ([15][cp_vocab][qkv width] fp32, XCD-parallel program only)
+    float * cp_tab = nullptr;
+    bool cp_tab_stale = true;
     hipEvent_t run_ev[2] = {nullptr, nullptr};
     uint8_t * copy_buf = nullptr;      // copy-kernel calibration buffers (time_kernel class 5)
     double run_us = 0.0;
@@ -699,6 +705,10 @@ const char * fk_err_msg(int32_t e) {
                   : "frame kernel: a phase wait timed out (results invalid)";
 }
 
+namespace {
+int build_cp_tab(q3t_dev * c);   // below, with the prefill helpers it uses
+}  // namespace
+
 int fk_prepare(q3t_dev * c) {
     c->fk_ok = false;
     // attention capture runs the multi-kernel step; the persistent kernel
@@ -750,6 +760,10 @@ int fk_prepare(q3t_dev * c) {
     if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
     if (xcd && xcd_map_ok(c, grid, xcd)) return -1;
     if (xcd) variant = 5;
+    bool tab = xcd;
+    if (const char * e = std::getenv("Q3T_CP_QKV_TABLE")) if (e[0] == '0') tab = false;
+    if (tab && (!c->cp_tab || c->cp_tab_stale) && build_cp_tab(c)) return -1;
+    c->fk_tab = tab;
     // arena slots: row-parallel layer 5 (code predictor) or 7 + kPvSlots
     // (talker); XCD-parallel layer 15 or 17 + kPvSlots (device-wide partial
     // sums take 4 slots, XCD-local rows 2)
@@ -781,6 +795,7 @@ int fk_prepare(q3t_dev * c) {
     c->fk_grid = grid;
     c->fk_variant = variant;
     c->fk_ok = true;
+    c->fk_args_ok = false;
     return 0;
 }
 
@@ -809,6 +824,7 @@ fk::Args fk_args(q3t_dev * c) {
     A.cand_val = c->fk_cand;
     A.cand_idx = (int32_t *) (c->fk_cand + 256);
     A.step_in = c->stage;
+    A.cp_qkv0 = c->fk_tab ? c->cp_tab : nullptr;
     return A;
 }
 
@@ -1031,6 +1047,7 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
     drop_graph(c);
     c->resolved = false;
     c->fk_layers_stale = true;
+    c->cp_tab_stale = true;
     const q3t_config & g = c->cfg;
     if (layer >= 0) {
         LayerDev & L = is_cp ? c->cp[layer] : c->talker[layer];
@@ -1344,6 +1361,36 @@ void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w, int x
               float * dx = nullptr) {
     hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, xs < 0 ? K : xs, K, w, c->cfg.rms_eps,
                        q ? q : c->pf_q, dx ? dx : c->pf_dx);
+}
+
+__global__ __launch_bounds__(256) void k_h2f(const uint16_t * __restrict__ in, size_t n, float * __restrict__ out) {
+    const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = h2f(in[i]);
+}
+
+// cp_tab[s][code] = the QKV output of code-predictor layer 0 on the row
+// codec_embd.s[code] (the input of codebook step s + 1): RMSNorm, Q8_0
+// activation quantisation and the int8 GEMM of the prefill path, whose rows
+// equal the frame kernel's GEMV bit for bit.  Rebuilt after any upload.
+int build_cp_tab(q3t_dev * c) {
+    const q3t_config & g = c->cfg;
+    const int d = g.cp_hidden, V = g.cp_vocab, ncb = g.n_codebooks - 1;
+    const int qkvd = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
+    const LayerDev & L = c->cp[0];
+    if (L.qkv.type != Q3T_TYPE_Q8_0 || d != g.hidden_size) return fail(c, "cp QKV table needs Q8_0 layers");
+    if (!c->cp_tab && dev_alloc_t(c, &c->cp_tab, (size_t) ncb * V * qkvd)) return -1;
+    if (ensure_pf(c, V)) return -1;
+    const size_t n = (size_t) V * d;
+    for (int sidx = 0; sidx < ncb; ++sidx) {
+        if (c->cp_embd[sidx].type != Q3T_TYPE_F16) return fail(c, "embedding tables must be F16");
+        hipLaunchKernelGGL(k_h2f, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, c->stream,
+                           (const uint16_t *) c->cp_embd[sidx].data, n, c->pf_xa);
+        pf_quant(c, c->pf_xa, V, d, L.attn_norm);
+        pf_gemm(c, L.qkv, qkvd, d, V, c->cp_tab + (size_t) sidx * V * qkvd, nullptr);
+    }
+    HIP_OK(hipStreamSynchronize(c->stream));
+    c->cp_tab_stale = false;
+    return 0;
 }
 
 // F16 weights x fp32 rows on the exact VALU GEMM: y = epi(W . rows of x),

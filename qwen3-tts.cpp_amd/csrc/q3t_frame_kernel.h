@@ -73,6 +73,9 @@ struct Args {
     int32_t * err;
     float * cand_val; int32_t * cand_idx;    // talker-head greedy candidates, one per workgroup
     const float * step_in;                   // MODE_TALKER_STEP: the step embedding [D]
+    // XCD-parallel program: code-predictor layer 0's QKV rows of every
+    // (codebook step s, code), [15][cp_vocab][4096] (null: computed)
+    const float * cp_qkv0;
 };
 
 // What one launch runs: a whole frame, or one of its two halves alone (the
@@ -892,11 +895,13 @@ __device__ __forceinline__ int32_t reduce_candidates(float v, int i, Lds & L) {
 // XL (XCD-parallel layers): every workgroup of XCD g runs KV head g, reading
 // its rows [q0 q1 k v] (512 per token) from the XCD's local QKV region and
 // leaving the attention rows in L.att instead of publishing them.
+// tab (one token): the QKV row comes from plain memory in the GEMV's layout
+// (the layer-0 table) instead of a tagged slot.
 template <bool XL>
 __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                             int nt, int pos0, int qd, const uint64_t * qkv,
                                                             uint32_t qkv_tag, uint64_t * out, uint32_t out_tag,
-                                                            bool & dead) {
+                                                            bool & dead, const float * tab = nullptr) {
     const int g = XL ? (int) (blockIdx.x & 7) : (int) blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kd = qd / 2;
     const bool f32 = nt == 2;              // the prefill: unrounded q, K, V, P
@@ -925,7 +930,13 @@ __device__ __attribute__((always_inline)) void attention_cp(const Args & A, Lds 
             rsv[tok] = gld(A.cp_rope_sin + (size_t) pos * 64 + lane);
         }
         float val[kB];
-        twait_batch<kB, XL>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
+        if (tab) {
+            const int tcol = wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
+            val[0] = gld(tab + tcol + lane);
+            val[1] = gld(tab + tcol + lane + 64);
+        } else {
+            twait_batch<kB, XL>(ptr, 2 * nt, qkv_tag, val, dead, A.err);
+        }
         for (int tok = 0; tok < nt; ++tok) {
             const int pos = pos0 + tok;
             const float x0 = val[2 * tok], x1 = val[2 * tok + 1];
@@ -1937,10 +1948,14 @@ __device__ __forceinline__ void xreduce(const Args & A, Lds & L, const uint64_t 
 // gathered into LDS (layer 0) or this XCD's local copy of the previous
 // layer's output (slot p_in); output: slot p_out (XCD-local copies).  The
 // slot numbering keeps one slot per phase (partials: 4, local rows: 2).
+// tab_row (code-predictor layer 0 of steps 1..14): the layer's QKV row from
+// the table, and rx_row the embedding row whose slice is the residual; the
+// QKV phase is skipped.
 template <int NT, bool TK>
 __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp,
                                                        int pos0, uint32_t tb, int & p, int p_in, const float * x_lds,
-                                                       int & p_out, bool & dead) {
+                                                       int & p_out, bool & dead, const float * tab_row = nullptr,
+                                                       const uint16_t * rx_row = nullptr) {
     constexpr int D = 1024, QD = 2048;
     uint64_t * ar = A.arena;
     const int x = (int) blockIdx.x & 7, j = (int) blockIdx.x >> 3, t = (int) threadIdx.x;
@@ -1952,7 +1967,9 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
     // QKV rows of KV head x -> local [NT][512]
     const int p_qkv = p++;
     uint64_t * qkv_l = ar + (size_t) p_qkv * kSlot + x * 1024;
-    {
+    if (tab_row) {
+        if (t < 32) L.rx[0][t] = h2f(gld(rx_row + 32 * j + t));
+    } else {
         XRegs<XK_QKV> R;
         xq8_prefetch<XK_QKV, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr);
         NormT<D> nw;
@@ -1973,7 +1990,7 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
     int p_att = 0;
     if (cp) {
         p_att = p++;
-        attention_cp<true>(A, L, W, layer, NT, pos0, QD, qkv_l, tb | p_qkv, nullptr, 0, dead);
+        attention_cp<true>(A, L, W, layer, NT, pos0, QD, qkv_l, tb | p_qkv, nullptr, 0, dead, tab_row);
     } else if (two_phase) {
         const AttSplit sp = att_split(A, pos0 + 1);
         const int p_a = p;
@@ -2121,7 +2138,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 L.x[D + i] = h2f(gld(A.codec_embd + (size_t) tok0 * D + i));
             }
         } else if (!tk) {
-            for (int i = t; i < D; i += kT) L.x[i] = h2f(gld(A.cp_embd[s - 1] + (size_t) code * D + i));
+            if (!(XT && A.cp_qkv0))
+                for (int i = t; i < D; i += kT) L.x[i] = h2f(gld(A.cp_embd[s - 1] + (size_t) code * D + i));
         } else if (mode == MODE_TALKER_STEP) {
             for (int i = t; i < D; i += kT) L.x[i] = gld(A.step_in + i);
         } else {
@@ -2145,9 +2163,13 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             const float * x_lds = l == 0 ? L.x : nullptr;
             const LayerQ8 Wl = layer_desc(Ls + l);
             if constexpr (XT) {
+                const bool tabl = A.cp_qkv0 && !tk && s > 0 && l == 0;
+                const float * tab_row =
+                    tabl ? A.cp_qkv0 + ((size_t) (s - 1) * A.cp_vocab + code) * (size_t) (QD + QD) : nullptr;
+                const uint16_t * rx_row = tabl ? A.cp_embd[s - 1] + (size_t) code * D : nullptr;
                 if (nt == 2) layer_x<2, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
                 else if (tk) layer_x<1, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
-                else layer_x<1, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else layer_x<1, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead, tab_row, rx_row);
             } else {
                 if (nt == 2) layer_t<2, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
                 else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
