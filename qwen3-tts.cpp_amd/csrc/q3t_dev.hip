@@ -84,6 +84,8 @@ struct q3t_dev {
     int32_t pf_rows = 0;
     int8_t * pf_q = nullptr; float * pf_dx = nullptr;
     float * pf_xa = nullptr, * pf_xb = nullptr, * pf_qkv = nullptr, * pf_att = nullptr;
+    // f64 MFMA prefill attention: scores and probabilities [n_head][n][ls]
+    float * pf_s = nullptr; uint16_t * pf_p = nullptr; size_t pf_sp_cap = 0;
     float * pf_g = nullptr, * pf_u = nullptr, * pf_f = nullptr;
     // multi-stream decode: nb independent streams sharing the weights
     int32_t nb = 0, sb_ctx = 0;
@@ -1406,10 +1408,46 @@ void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float *
                            xs, n, y, N, res, rs);
 }
 
+// Causal attention of the n prefill rows (QKV rows in c->pf_qkv, K/V already
+// in the layer's cache) into c->pf_att.  From 64 rows on: the f64 MFMA
+// kernels (scores, softmax, P.V; Q3T_PF_ATT_MFMA=0 keeps the row kernel);
+// below, or when the scores would not fit 4 GiB, one workgroup per row.
+int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uint16_t * vc, int n, int n_past) {
+    const q3t_config & g = c->cfg;
+    const int qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    const float scale = 1.0f / std::sqrt((float) g.head_dim);
+    const int bf = c->kv_bf16 ? 1 : 0;
+    static const bool off = [] { const char * e = std::getenv("Q3T_PF_ATT_MFMA"); return e && e[0] == '0'; }();
+    const int ls = (n_past + n + pf::kAT - 1) / pf::kAT * pf::kAT;
+    const size_t cells = (size_t) g.n_head * n * ls;
+    if (off || n < pf::kAT || cells * 6 > ((size_t) 4 << 30)) {
+        hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
+                           c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
+                           (const float *) c->rope_sin, kc, vc, c->n_ctx, g.n_head, g.n_kv_head, n_past, scale,
+                           c->pf_att, qd, bf);
+        return 0;
+    }
+    if (cells > c->pf_sp_cap) {
+        dev_free(c, c->pf_s); dev_free(c, c->pf_p);
+        c->pf_s = nullptr; c->pf_p = nullptr; c->pf_sp_cap = 0;
+        if (dev_alloc_t(c, &c->pf_s, cells) || dev_alloc_t(c, &c->pf_p, cells)) return -1;
+        c->pf_sp_cap = cells;
+    }
+    const dim3 tiles(g.n_head, (n + pf::kAT - 1) / pf::kAT);
+    hipLaunchKernelGGL(pf::k_att_scores, tiles, dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm,
+                       g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, kc, c->n_ctx, g.n_head,
+                       g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
+    hipLaunchKernelGGL(pf::k_att_softmax, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_s, n,
+                       n_past, ls, c->pf_p, bf);
+    hipLaunchKernelGGL(pf::k_att_pv, tiles, dim3(kBlock), 0, c->stream, (const uint16_t *) c->pf_p, ls, vc, c->n_ctx,
+                       g.n_head, g.n_kv_head, n, n_past, c->pf_att, qd, bf);
+    return 0;
+}
+
 // Talker prefill of n tokens (rows in c->stage) with F16 layers on the exact
 // VALU GEMMs; same layer program and buffers as prefill_mfma (c->pf_f holds
 // the RMSNorm'd rows until SwiGLU overwrites it).
-void prefill_f16(q3t_dev * c, int n, int n_past) {
+int prefill_f16(q3t_dev * c, int n, int n_past) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int ffn = g.ffn_size;
@@ -1425,10 +1463,7 @@ void prefill_f16(q3t_dev * c, int n, int n_past) {
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
-        hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
-                           c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
-                           (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
-                           g.n_kv_head, n_past, scale, c->pf_att, qd, c->kv_bf16 ? 1 : 0);
+        if (pf_attention(c, L, kc, vc, n, n_past)) return -1;
         pf_gemm_f16(c, L.wo, d, qd, n, c->pf_att, qd, false, c->pf_xb, x, d);
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xb, L.ffn_norm,
                            g.rms_eps, d, c->pf_f);
@@ -1445,11 +1480,12 @@ void prefill_f16(q3t_dev * c, int n, int n_past) {
     h.x = c->pf_xa + (size_t) (n - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
     h.hidden_out = c->hidden; h.hidden_stride = d; h.y = c->logits; h.y_stride = g.codec_vocab;
     gemv(c, h, 1);
+    return 0;
 }
 
 // Talker prefill of n tokens (rows in c->stage) on the MFMA path; the output
 // rows end in c->pf_xa, the last row's head output in c->hidden / c->logits.
-void prefill_mfma(q3t_dev * c, int n, int n_past) {
+int prefill_mfma(q3t_dev * c, int n, int n_past) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int ffn = g.ffn_size;
@@ -1465,10 +1501,7 @@ void prefill_mfma(q3t_dev * c, int n, int n_past) {
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
-        hipLaunchKernelGGL(pf::k_attn_rows, dim3(g.n_head, n), dim3(kBlock), pf::attn_rows_lds_bytes(n_past + n),
-                           c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos,
-                           (const float *) c->rope_sin, (const uint16_t *) kc, (const uint16_t *) vc, c->n_ctx, g.n_head,
-                           g.n_kv_head, n_past, scale, c->pf_att, qd, c->kv_bf16 ? 1 : 0);
+        if (pf_attention(c, L, kc, vc, n, n_past)) return -1;
         pf_quant(c, c->pf_att, n, qd, nullptr);
         pf_gemm(c, L.wo, d, qd, n, c->pf_xb, x);
         pf_quant(c, c->pf_xb, n, d, L.ffn_norm);
@@ -1486,6 +1519,7 @@ void prefill_mfma(q3t_dev * c, int n, int n_past) {
     h.x = c->pf_xa + (size_t) (n - 1) * d; h.x_stride = d; h.norm_w = (const float *) c->out_norm.data;
     h.hidden_out = c->hidden; h.hidden_stride = d; h.y = c->logits; h.y_stride = g.codec_vocab;
     gemv(c, h, 1);
+    return 0;
 }
 
 // y [n][N] = x [n][K] . W^T + bias on the tiled GEMMs (Q8_0: quantised rows on
@@ -1672,8 +1706,7 @@ int q3t_dev_prefill(q3t_dev * c, const float * embd, int32_t n, int32_t n_past, 
     HIP_OK(hipMemcpyAsync(c->stage, embd, (size_t) n * d * 4, hipMemcpyHostToDevice, c->stream));
     if (const int tp = tiled_prefill(c, n)) {
         if (ensure_pf(c, n)) return -1;
-        if (tp == 1) prefill_mfma(c, n, n_past);
-        else prefill_f16(c, n, n_past);
+        if (tp == 1 ? prefill_mfma(c, n, n_past) : prefill_f16(c, n, n_past)) return -1;
         if (hidden_out)
             hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xa,
                                (const float *) c->out_norm.data, g.rms_eps, d, c->hidden_all);

@@ -331,6 +331,218 @@ __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__
     }
 }
 
+// ------------------------------------------- causal attention on f64 MFMA
+// The prefill's causal attention as three kernels per layer, for n rows at
+// positions n_past.. (the K/V rows of all n tokens already in the cache):
+//   k_att_scores  S[h][r][j] = fp32(q_r . k_j) * scale for j <= n_past + r,
+//                 one workgroup per (head, 64-row tile) sweeping 64-position
+//                 K tiles on v_mfma_f64_16x16x4f64;
+//   k_att_softmax per row: maximum, exp, fp64 sum, P = fp16(e / sum) (the
+//                 probabilities the reference's KQV product rounds to);
+//   k_att_pv      O[r][h*128 + d] = fp32(sum_j P[r][j] V[j][d]) on the same
+//                 MFMA, P and V^T staged in LDS per 64-position tile.
+// q and k are fp16 values (or bfloat16 with a BF16 cache), so every product
+// is exact in fp64 and every sum is an fp64 sum of exact terms, rounded once:
+// the numbers of pf::k_attn_rows, whatever order the MFMA adds them in.
+// MFMA lane layout (16x16x4 f64): A[m = l%16][k = l/16], B[k = l/16][n =
+// l%16], D[m = 4r + l/16][n = l%16] in element r.  Step s of a contraction
+// gives lane group k = l/16 the index 32k + s (scores, 128 dims: each lane
+// reads 32 contiguous dims of its row) or 16k + s (P.V, 64 positions).
+typedef double v4d __attribute__((ext_vector_type(4)));
+constexpr int kAT = 64;          // rows and positions per attention tile
+constexpr int kKS = 136;         // LDS row stride (halves) of a staged K tile: conflict-free 16-byte reads
+constexpr int kVS = 72;          // LDS row stride (halves) of staged P and V^T tiles
+
+__device__ __forceinline__ double kvd(uint16_t h, bool bf) { return (double) kv2f(h, bf); }
+
+// grid (n_head, ceil(n / 64)); wave w owns rows 16w..16w+15 of the tile and
+// prepares their q (QK-norm, NEOX RoPE, rounding to the cache type) itself:
+// lane (i = l%16, k = l/16) holds dims 32k..32k+31 of row 16w + i, whose RoPE
+// partners (d +- 64) sit in lane l ^ 32.
+__global__ __launch_bounds__(kBlock) void k_att_scores(const float * __restrict__ qkv, int32_t qkv_stride,
+                                                       const float * __restrict__ q_norm, float eps,
+                                                       const float * __restrict__ rc, const float * __restrict__ rs,
+                                                       const uint16_t * __restrict__ kc, int32_t n_ctx, int32_t n_head,
+                                                       int32_t n_kv_head, int32_t n, int32_t n_past, float scale,
+                                                       float * __restrict__ S, int32_t ls, int32_t bf) {
+    __shared__ __align__(16) uint16_t kt[kAT * kKS];
+    const int h = blockIdx.x, tile = (int) gridDim.y - 1 - (int) blockIdx.y;   // longest tiles first
+    const int g = h / (n_head / n_kv_head), row0 = tile * kAT;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int my_row = row0 + 16 * w + i;
+    // q of row my_row, dims 32k .. 32k+31
+    double a[32];
+    {
+        float x[32];
+        const bool ok = my_row < n;
+        const float * src = qkv + (size_t) (ok ? my_row : 0) * qkv_stride + h * kHD + 32 * k;
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            x[e] = ok ? src[e] : 0.0f;
+            ss += (double) (x[e] * x[e]);
+        }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        const float mean = (float) (ss / (double) kHD);
+        const float sc = 1.0f / sqrtf(mean + eps);
+        const int pos = n_past + (ok ? my_row : 0);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float y = x[e] * sc;
+            x[e] = y * q_norm[32 * k + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float other = __shfl_xor(x[e], 32);   // dim d + 64 (k < 2) or d - 64 (k >= 2)
+            const int ci = (32 * k + e) & 63;
+            const float c = rc[(size_t) pos * 64 + ci], sn = rs[(size_t) pos * 64 + ci];
+            float o;
+            if (k < 2) { const float p0 = x[e] * c, q0 = other * sn; o = p0 - q0; }
+            else { const float p0 = other * sn, q0 = x[e] * c; o = p0 + q0; }
+            a[e] = ok ? (double) round_kv(o, bf) : 0.0;
+        }
+    }
+    const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
+    for (int j0 = 0; j0 <= lim_tile; j0 += kAT) {
+        __syncthreads();
+        // stage K rows j0..j0+63 of KV head g (16-byte chunks; rows past the tile's limit zero)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int pr = (t >> 4) + 16 * u, c = t & 15, j = j0 + pr;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (j <= lim_tile) v = *(const int4 *) (kc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
+            *(int4 *) (kt + pr * kKS + 8 * c) = v;
+        }
+        __syncthreads();
+        v4d acc[4];
+        int4 kb[4][4];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            acc[t4] = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kb[t4][c] = *(const int4 *) (kt + (16 * t4 + i) * kKS + 32 * k + 8 * c);
+        }
+#pragma unroll
+        for (int st = 0; st < 32; ++st) {
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) {
+                const int wv = st >> 1;
+                const int word = (wv & 3) == 0 ? kb[t4][wv >> 2].x : (wv & 3) == 1 ? kb[t4][wv >> 2].y
+                               : (wv & 3) == 2 ? kb[t4][wv >> 2].z : kb[t4][wv >> 2].w;
+                const uint16_t hv = (uint16_t) ((st & 1) ? ((uint32_t) word >> 16) : ((uint32_t) word & 0xffffu));
+                acc[t4] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[st], kvd(hv, bf), acc[t4], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + 16 * w + 4 * r + k, j = j0 + 16 * t4 + i;
+                if (row < n && j <= n_past + row) S[((size_t) h * n + row) * ls + j] = (float) acc[t4][r] * scale;
+            }
+    }
+}
+
+// grid (n, n_head): P[h][r][j] = fp16(exp(S - max) / sum) for j <= n_past + r
+// (bfloat16 with a BF16 cache), as pf::k_attn_rows rounds it.
+__global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict__ S, int32_t n, int32_t n_past,
+                                                        int32_t ls, uint16_t * __restrict__ P, int32_t bf) {
+    __shared__ double red[4];
+    __shared__ float fred[4];
+    const int row = blockIdx.x, h = blockIdx.y, t = threadIdx.x, cnt = n_past + row + 1;
+    const float * sr = S + ((size_t) h * n + row) * ls;
+    uint16_t * pr = P + ((size_t) h * n + row) * ls;
+    float m = -INFINITY;
+    for (int j = t; j < cnt; j += kBlock) m = fmaxf(m, sr[j]);
+    const float mx = block_max_f(m, fred);
+    double sum = 0.0;
+    for (int j = t; j < cnt; j += kBlock) sum += (double) expf_q3t(sr[j] - mx);
+    const double tot = block_sum_d(sum, red);
+    const float inv = (float) (1.0 / tot);
+    for (int j = t; j < cnt; j += kBlock) pr[j] = f2kv(expf_q3t(sr[j] - mx) * inv, bf);
+}
+
+// grid (n_head, ceil(n / 64)): wave w owns rows 16w..16w+15, all 128 dims as
+// eight 16 x 16 accumulators.  Probabilities past a row's last position are
+// taken as zero.
+__global__ __launch_bounds__(kBlock) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
+                                                   const uint16_t * __restrict__ vc, int32_t n_ctx, int32_t n_head,
+                                                   int32_t n_kv_head, int32_t n, int32_t n_past,
+                                                   float * __restrict__ out, int32_t out_stride, int32_t bf) {
+    __shared__ __align__(16) uint16_t pt[kAT * kVS];         // [row][position]
+    __shared__ __align__(16) uint16_t vt[kHD * kVS];         // [dim][position]
+    const int h = blockIdx.x, tile = (int) gridDim.y - 1 - (int) blockIdx.y;
+    const int g = h / (n_head / n_kv_head), row0 = tile * kAT;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int lim_tile = n_past + min(row0 + kAT, n) - 1;
+    v4d acc[8];
+#pragma unroll
+    for (int d8 = 0; d8 < 8; ++d8) acc[d8] = v4d{0.0, 0.0, 0.0, 0.0};
+    for (int j0 = 0; j0 <= lim_tile; j0 += kAT) {
+        __syncthreads();
+        // P tile: 64 rows x 64 positions (8-position chunks), masked to each row's limit
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int idx = t + kBlock * u, r = idx >> 3, c = idx & 7, row = row0 + r;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (row < n) {
+                const int lim = n_past + row, j = j0 + 8 * c;
+                if (j + 7 <= lim) v = *(const int4 *) (P + ((size_t) h * n + row) * ls + j);
+                else if (j <= lim) {
+                    uint16_t tmp[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) tmp[e] = j + e <= lim ? P[((size_t) h * n + row) * ls + j + e] : 0;
+                    v = *(const int4 *) tmp;
+                }
+            }
+            *(int4 *) (pt + r * kVS + 8 * c) = v;
+        }
+        // V^T tile: positions j0..j0+63 (past the limit: zero) of KV head g
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = t + kBlock * u, pr = idx >> 4, c = idx & 15, j = j0 + pr;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (j <= lim_tile) v = *(const int4 *) (vc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
+            const uint16_t * vh = (const uint16_t *) &v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[(8 * c + e) * kVS + pr] = vh[e];
+        }
+        __syncthreads();
+        int4 pa[2], vb[8][2];
+        pa[0] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k);
+        pa[1] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k + 8);
+#pragma unroll
+        for (int d8 = 0; d8 < 8; ++d8) {
+            vb[d8][0] = *(const int4 *) (vt + (16 * d8 + i) * kVS + 16 * k);
+            vb[d8][1] = *(const int4 *) (vt + (16 * d8 + i) * kVS + 16 * k + 8);
+        }
+        // eight independent accumulators per step keep the MFMA pipe busy
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+            const int e = st & 7, wv = e >> 1;
+            const int4 & pv4 = pa[st >> 3];
+            const int pw = wv == 0 ? pv4.x : wv == 1 ? pv4.y : wv == 2 ? pv4.z : pv4.w;
+            const uint16_t ph = (uint16_t) ((e & 1) ? ((uint32_t) pw >> 16) : ((uint32_t) pw & 0xffffu));
+            const double pd = kvd(ph, bf);
+#pragma unroll
+            for (int d8 = 0; d8 < 8; ++d8) {
+                const int4 & v4 = vb[d8][st >> 3];
+                const int vw = wv == 0 ? v4.x : wv == 1 ? v4.y : wv == 2 ? v4.z : v4.w;
+                const uint16_t vh = (uint16_t) ((e & 1) ? ((uint32_t) vw >> 16) : ((uint32_t) vw & 0xffffu));
+                acc[d8] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d8], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int d8 = 0; d8 < 8; ++d8)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 16 * w + 4 * r + k;
+            if (row < n) out[(size_t) row * out_stride + h * kHD + 16 * d8 + i] = (float) acc[d8][r];
+        }
+}
+
 __host__ __device__ constexpr size_t attn_rows_lds_bytes(int n_ctx) {
     return 64 + 2 * kHD * sizeof(float) + 4 * kHD * sizeof(double) + (size_t) n_ctx * sizeof(float);
 }

@@ -100,6 +100,38 @@ def test_prefill_and_steps_match_oracle(tiny_model, prefill_path):
         assert np.array_equal(hg, ho)
 
 
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+@pytest.mark.parametrize("att", ["mfma", "rows"])
+def test_tiled_prefill_attention_paths(wtype_tiny, kv, att, monkeypatch):
+    """A 100-row prefill after 37 cached positions on the tiled prefill
+    (MFMA attention over 64-row tiles, or Q3T_PF_ATT_MFMA=0 one workgroup per
+    row), then 35 rows more: hidden rows and logits bit for bit the oracle's."""
+    monkeypatch.setenv("Q3T_PREFILL_MFMA", "1")
+    monkeypatch.setenv("Q3T_PF_ATT_MFMA", "1" if att == "mfma" else "0")
+    cfg = qcfg.tiny()
+    w, dev, o = make(cfg, wtype_tiny, seed=43, n_ctx=256)
+    try:
+        if kv == "bf16":
+            dev.kv_set_type(30)
+            o.kv_set_type(30)
+            o.kv_reset(256)
+        rng = np.random.default_rng(44)
+        d = cfg.hidden_size
+        for n_past, n in ((0, 37), (37, 100), (137, 35)):
+            rows = (rng.standard_normal((n, d)) * 0.5).astype(np.float32)
+            say(f"[gpu] tiled prefill {n} rows at {n_past} ({wtype_tiny}, {kv} KV, {att})")
+            hg, lg = dev.prefill(rows, n_past)
+            ho, lo = o.prefill(rows, n_past)
+            assert np.array_equal(hg, ho) and np.array_equal(lg, lo), (n_past, n)
+    finally:
+        dev.close()
+
+
+@pytest.fixture(params=["q8_0", "f16"])
+def wtype_tiny(request):
+    return request.param
+
+
 def test_code_pred_greedy_matches_oracle(tiny_model):
     cfg, w, dev, o = tiny_model
     rng = np.random.default_rng(2)
