@@ -1427,19 +1427,24 @@ int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uin
                            c->pf_att, qd, bf);
         return 0;
     }
-    if (cells > c->pf_sp_cap) {
+    // the probabilities buffer also holds the q rows [n_head][n][128] first
+    const size_t need = std::max(cells, (size_t) g.n_head * n * g.head_dim);
+    if (need > c->pf_sp_cap) {
         dev_free(c, c->pf_s); dev_free(c, c->pf_p);
         c->pf_s = nullptr; c->pf_p = nullptr; c->pf_sp_cap = 0;
-        if (dev_alloc_t(c, &c->pf_s, cells) || dev_alloc_t(c, &c->pf_p, cells)) return -1;
-        c->pf_sp_cap = cells;
+        if (dev_alloc_t(c, &c->pf_s, need) || dev_alloc_t(c, &c->pf_p, need)) return -1;
+        c->pf_sp_cap = need;
     }
-    const dim3 tiles(g.n_head, (n + pf::kAT - 1) / pf::kAT);
-    hipLaunchKernelGGL(pf::k_att_scores, tiles, dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd, L.q_norm,
-                       g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, kc, c->n_ctx, g.n_head,
-                       g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
-    hipLaunchKernelGGL(pf::k_att_softmax, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_s, n,
-                       n_past, ls, c->pf_p, bf);
-    hipLaunchKernelGGL(pf::k_att_pv, tiles, dim3(kBlock), 0, c->stream, (const uint16_t *) c->pf_p, ls, vc, c->n_ctx,
+    const dim3 tiles(g.n_head, ((n + pf::kAT - 1) / pf::kAT + 1) / 2);   // tile pairs
+    // q rows into the probabilities buffer's head (they are consumed before it is written)
+    uint16_t * qh = c->pf_p;
+    hipLaunchKernelGGL(pf::k_att_q, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd,
+                       L.q_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, n, n_past, qh, bf);
+    hipLaunchKernelGGL(pf::k_att_scores, tiles, dim3(pf::kAttT), 0, c->stream, (const uint16_t *) qh, kc, c->n_ctx,
+                       g.n_head, g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
+    hipLaunchKernelGGL(pf::k_att_softmax, dim3((n + 3) / 4, g.n_head), dim3(kBlock), 0, c->stream,
+                       (const float *) c->pf_s, n, n_past, ls, c->pf_p, bf);
+    hipLaunchKernelGGL(pf::k_att_pv, tiles, dim3(pf::kAttT), 0, c->stream, (const uint16_t *) c->pf_p, ls, vc, c->n_ctx,
                        g.n_head, g.n_kv_head, n, n_past, c->pf_att, qd, bf);
     return 0;
 }

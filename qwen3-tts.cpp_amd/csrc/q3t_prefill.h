@@ -354,137 +354,177 @@ constexpr int kKS = 136;         // LDS row stride (halves) of a staged K tile: 
 constexpr int kVS = 72;          // LDS row stride (halves) of staged P and V^T tiles
 
 __device__ __forceinline__ double kvd(uint16_t h, bool bf) { return (double) kv2f(h, bf); }
+// Element e (0..7) of eight 16-bit values packed in an int4.
+__device__ __forceinline__ uint16_t h8bits(const int4 & v, int e) {
+    const int w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+    return (uint16_t) ((e & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu));
+}
 
-// grid (n_head, ceil(n / 64)); wave w owns rows 16w..16w+15 of the tile and
-// prepares their q (QK-norm, NEOX RoPE, rounding to the cache type) itself:
-// lane (i = l%16, k = l/16) holds dims 32k..32k+31 of row 16w + i, whose RoPE
-// partners (d +- 64) sit in lane l ^ 32.
-__global__ __launch_bounds__(kBlock) void k_att_scores(const float * __restrict__ qkv, int32_t qkv_stride,
-                                                       const float * __restrict__ q_norm, float eps,
-                                                       const float * __restrict__ rc, const float * __restrict__ rs,
+// grid (n, n_head): q of row r, head h (QK-norm, NEOX RoPE at position
+// n_past + r) rounded to the cache type, into Qh[h][r][128].
+__global__ __launch_bounds__(kBlock) void k_att_q(const float * __restrict__ qkv, int32_t qkv_stride,
+                                                  const float * __restrict__ q_norm, float eps,
+                                                  const float * __restrict__ rc, const float * __restrict__ rs,
+                                                  int32_t n, int32_t n_past, uint16_t * __restrict__ Qh, int32_t bf) {
+    __shared__ double red[4];
+    __shared__ float tmp[kHD];
+    const int row = blockIdx.x, h = blockIdx.y, t = threadIdx.x, pos = n_past + row;
+    const float v = t < kHD ? qkv[(size_t) row * qkv_stride + h * kHD + t] : 0.0f;
+    const float o = head_norm_rope(v, q_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
+    if (t < kHD) Qh[((size_t) h * n + row) * kHD + t] = f2kv(o, bf);
+}
+
+// grid (n_head, ceil(tiles / 2)): workgroup y takes 64-row tiles y and
+// tiles - 1 - y, so every workgroup sweeps about the same number of K tiles
+// (the causal sweep of tile y is y + 1 tiles long).  Wave w owns rows
+// 16w..16w+15 of a tile (q from k_att_q): lane (i = l%16, k = l/16) holds
+// dims 32k..32k+31 of row 16w + i.  K tiles are
+// 128 positions; eight waves, two per SIMD: wave group grp = t / 256 takes
+// positions 64 grp .. 64 grp + 63 of each tile (four 16-position
+// accumulators per wave).
+constexpr int kKT = 128;         // positions per staged K tile of the scores kernel
+constexpr int kAttT = 512;       // threads of the MFMA attention kernels
+__global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restrict__ Qh,
                                                        const uint16_t * __restrict__ kc, int32_t n_ctx, int32_t n_head,
                                                        int32_t n_kv_head, int32_t n, int32_t n_past, float scale,
                                                        float * __restrict__ S, int32_t ls, int32_t bf) {
-    __shared__ __align__(16) uint16_t kt[kAT * kKS];
-    const int h = blockIdx.x, tile = (int) gridDim.y - 1 - (int) blockIdx.y;   // longest tiles first
-    const int g = h / (n_head / n_kv_head), row0 = tile * kAT;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
-    const int my_row = row0 + 16 * w + i;
-    // q of row my_row, dims 32k .. 32k+31
-    double a[32];
-    {
-        float x[32];
-        const bool ok = my_row < n;
-        const float * src = qkv + (size_t) (ok ? my_row : 0) * qkv_stride + h * kHD + 32 * k;
-        double ss = 0.0;
+    __shared__ __align__(16) uint16_t kt[kKT * kKS];
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head);
+    const int t = threadIdx.x, grp = t >> 8, w = (t >> 6) & 3, l = t & 63, i = l & 15, k = l >> 4;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
+        if (pass == 1 && tile == (int) blockIdx.y) break;     // the middle tile of an odd count
+        const int row0 = tile * kAT, my_row = row0 + 16 * w + i;
+        // q of row my_row, dims 32k .. 32k+31 (fp16 / bfloat16 values, held as fp32)
+        float a[32];
+        {
+            const bool ok = my_row < n;
+            const int4 * src = (const int4 *) (Qh + ((size_t) h * n + (ok ? my_row : 0)) * kHD + 32 * k);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            x[e] = ok ? src[e] : 0.0f;
-            ss += (double) (x[e] * x[e]);
-        }
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        const float mean = (float) (ss / (double) kHD);
-        const float sc = 1.0f / sqrtf(mean + eps);
-        const int pos = n_past + (ok ? my_row : 0);
+            for (int c = 0; c < 4; ++c) {
+                const int4 v = ok ? src[c] : make_int4(0, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float y = x[e] * sc;
-            x[e] = y * q_norm[32 * k + e];
-        }
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float other = __shfl_xor(x[e], 32);   // dim d + 64 (k < 2) or d - 64 (k >= 2)
-            const int ci = (32 * k + e) & 63;
-            const float c = rc[(size_t) pos * 64 + ci], sn = rs[(size_t) pos * 64 + ci];
-            float o;
-            if (k < 2) { const float p0 = x[e] * c, q0 = other * sn; o = p0 - q0; }
-            else { const float p0 = other * sn, q0 = x[e] * c; o = p0 + q0; }
-            a[e] = ok ? (double) round_kv(o, bf) : 0.0;
-        }
-    }
-    const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
-    for (int j0 = 0; j0 <= lim_tile; j0 += kAT) {
-        __syncthreads();
-        // stage K rows j0..j0+63 of KV head g (16-byte chunks; rows past the tile's limit zero)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int pr = (t >> 4) + 16 * u, c = t & 15, j = j0 + pr;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (j <= lim_tile) v = *(const int4 *) (kc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
-            *(int4 *) (kt + pr * kKS + 8 * c) = v;
-        }
-        __syncthreads();
-        v4d acc[4];
-        int4 kb[4][4];
-#pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-            acc[t4] = v4d{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kb[t4][c] = *(const int4 *) (kt + (16 * t4 + i) * kKS + 32 * k + 8 * c);
-        }
-#pragma unroll
-        for (int st = 0; st < 32; ++st) {
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) {
-                const int wv = st >> 1;
-                const int word = (wv & 3) == 0 ? kb[t4][wv >> 2].x : (wv & 3) == 1 ? kb[t4][wv >> 2].y
-                               : (wv & 3) == 2 ? kb[t4][wv >> 2].z : kb[t4][wv >> 2].w;
-                const uint16_t hv = (uint16_t) ((st & 1) ? ((uint32_t) word >> 16) : ((uint32_t) word & 0xffffu));
-                acc[t4] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[st], kvd(hv, bf), acc[t4], 0, 0, 0);
+                for (int e = 0; e < 8; ++e) a[8 * c + e] = kv2f(h8bits(v, e), bf);
             }
         }
+        const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
+        for (int j0 = 0; j0 <= lim_tile; j0 += kKT) {
+            __syncthreads();
+            // stage K rows j0..j0+127 of KV head g (16-byte chunks; rows past the tile's limit zero)
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = row0 + 16 * w + 4 * r + k, j = j0 + 16 * t4 + i;
-                if (row < n && j <= n_past + row) S[((size_t) h * n + row) * ls + j] = (float) acc[t4][r] * scale;
+            for (int u = 0; u < 4; ++u) {
+                const int pr = (t >> 4) + 32 * u, c = t & 15, j = j0 + pr;
+                int4 v = make_int4(0, 0, 0, 0);
+                if (j <= lim_tile) v = *(const int4 *) (kc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
+                *(int4 *) (kt + pr * kKS + 8 * c) = v;
             }
+            __syncthreads();
+            v4d acc[4];
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) acc[t4] = v4d{0.0, 0.0, 0.0, 0.0};
+            // positions past the tile's limit are zero in kt and never stored
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {                      // dims 32k + 8c .. +7
+                int4 kb[4];
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) kb[t4] = *(const int4 *) (kt + (64 * grp + 16 * t4 + i) * kKS + 32 * k + 8 * c);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int wv = e >> 1;
+                    const double ad = (double) a[8 * c + e];
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4) {
+                        const int word = wv == 0 ? kb[t4].x : wv == 1 ? kb[t4].y : wv == 2 ? kb[t4].z : kb[t4].w;
+                        const uint16_t hv = (uint16_t) ((e & 1) ? ((uint32_t) word >> 16) : ((uint32_t) word & 0xffffu));
+                        acc[t4] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad, kvd(hv, bf), acc[t4], 0, 0, 0);
+                    }
+                }
+                // keep the next dims' loads and conversions after these MFMAs (register pressure)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + 16 * w + 4 * r + k, j = j0 + 64 * grp + 16 * t4 + i;
+                    if (row < n && j <= n_past + row)
+                        S[((size_t) h * n + row) * ls + j] = (float) acc[t4][r] * scale;
+                }
+        }
     }
 }
 
-// grid (n, n_head): P[h][r][j] = fp16(exp(S - max) / sum) for j <= n_past + r
-// (bfloat16 with a BF16 cache), as pf::k_attn_rows rounds it.
+// grid (ceil(n / 4), n_head), one wave per row: P[h][r][j] = fp16(exp(S -
+// max) / sum) for j <= n_past + r (bfloat16 with a BF16 cache), as
+// pf::k_attn_rows rounds it.  Rows of up to 2048 positions stay in registers
+// (one read of S); longer rows are read three times.
+constexpr int kSmReg = 32;       // positions per lane held in registers
 __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict__ S, int32_t n, int32_t n_past,
                                                         int32_t ls, uint16_t * __restrict__ P, int32_t bf) {
-    __shared__ double red[4];
-    __shared__ float fred[4];
-    const int row = blockIdx.x, h = blockIdx.y, t = threadIdx.x, cnt = n_past + row + 1;
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y;
+    if (row >= n) return;                   // whole wave
+    const int cnt = n_past + row + 1;
     const float * sr = S + ((size_t) h * n + row) * ls;
     uint16_t * pr = P + ((size_t) h * n + row) * ls;
+    if (cnt <= 64 * kSmReg) {
+        float v[kSmReg];
+        float m = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kSmReg; ++u) {
+            const int j = lane + 64 * u;
+            v[u] = j < cnt ? sr[j] : -INFINITY;
+            m = fmaxf(m, v[u]);
+        }
+        const float mx = wave_max_f(m);
+        double sum = 0.0;
+#pragma unroll
+        for (int u = 0; u < kSmReg; ++u) {
+            const int j = lane + 64 * u;
+            v[u] = j < cnt ? expf_q3t(v[u] - mx) : 0.0f;
+            sum += (double) v[u];
+        }
+        const float inv = (float) (1.0 / wave_sum_d(sum));
+#pragma unroll
+        for (int u = 0; u < kSmReg; ++u) {
+            const int j = lane + 64 * u;
+            if (j < cnt) pr[j] = f2kv(v[u] * inv, bf);
+        }
+        return;
+    }
     float m = -INFINITY;
-    for (int j = t; j < cnt; j += kBlock) m = fmaxf(m, sr[j]);
-    const float mx = block_max_f(m, fred);
+    for (int j = lane; j < cnt; j += 64) m = fmaxf(m, sr[j]);
+    const float mx = wave_max_f(m);
     double sum = 0.0;
-    for (int j = t; j < cnt; j += kBlock) sum += (double) expf_q3t(sr[j] - mx);
-    const double tot = block_sum_d(sum, red);
-    const float inv = (float) (1.0 / tot);
-    for (int j = t; j < cnt; j += kBlock) pr[j] = f2kv(expf_q3t(sr[j] - mx) * inv, bf);
+    for (int j = lane; j < cnt; j += 64) sum += (double) expf_q3t(sr[j] - mx);
+    const float inv = (float) (1.0 / wave_sum_d(sum));
+    for (int j = lane; j < cnt; j += 64) pr[j] = f2kv(expf_q3t(sr[j] - mx) * inv, bf);
 }
 
-// grid (n_head, ceil(n / 64)): wave w owns rows 16w..16w+15, all 128 dims as
-// eight 16 x 16 accumulators.  Probabilities past a row's last position are
-// taken as zero.
-__global__ __launch_bounds__(kBlock) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
+// grid (n_head, ceil(tiles / 2)), tiles paired as in k_att_scores; eight
+// waves: wave w of group grp owns rows 16w..16w+15 of a tile and dims
+// 64 grp .. 64 grp + 63 as four 16 x 16 accumulators.  Probabilities past a
+// row's last position are taken as zero.
+__global__ __launch_bounds__(kAttT) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
                                                    const uint16_t * __restrict__ vc, int32_t n_ctx, int32_t n_head,
                                                    int32_t n_kv_head, int32_t n, int32_t n_past,
                                                    float * __restrict__ out, int32_t out_stride, int32_t bf) {
     __shared__ __align__(16) uint16_t pt[kAT * kVS];         // [row][position]
     __shared__ __align__(16) uint16_t vt[kHD * kVS];         // [dim][position]
-    const int h = blockIdx.x, tile = (int) gridDim.y - 1 - (int) blockIdx.y;
-    const int g = h / (n_head / n_kv_head), row0 = tile * kAT;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head);
+    const int t = threadIdx.x, grp = t >> 8, w = (t >> 6) & 3, l = t & 63, i = l & 15, k = l >> 4;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
+    if (pass == 1 && tile == (int) blockIdx.y) break;         // the middle tile of an odd count
+    const int row0 = tile * kAT;
     const int lim_tile = n_past + min(row0 + kAT, n) - 1;
-    v4d acc[8];
+    v4d acc[4];
 #pragma unroll
-    for (int d8 = 0; d8 < 8; ++d8) acc[d8] = v4d{0.0, 0.0, 0.0, 0.0};
+    for (int d4 = 0; d4 < 4; ++d4) acc[d4] = v4d{0.0, 0.0, 0.0, 0.0};
     for (int j0 = 0; j0 <= lim_tile; j0 += kAT) {
         __syncthreads();
         // P tile: 64 rows x 64 positions (8-position chunks), masked to each row's limit
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int idx = t + kBlock * u, r = idx >> 3, c = idx & 7, row = row0 + r;
+        {
+            const int idx = t, r = idx >> 3, c = idx & 7, row = row0 + r;
             int4 v = make_int4(0, 0, 0, 0);
             if (row < n) {
                 const int lim = n_past + row, j = j0 + 8 * c;
@@ -500,8 +540,8 @@ __global__ __launch_bounds__(kBlock) void k_att_pv(const uint16_t * __restrict__
         }
         // V^T tile: positions j0..j0+63 (past the limit: zero) of KV head g
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int idx = t + kBlock * u, pr = idx >> 4, c = idx & 15, j = j0 + pr;
+        for (int u = 0; u < 2; ++u) {
+            const int idx = t + kAttT * u, pr = idx >> 4, c = idx & 15, j = j0 + pr;
             int4 v = make_int4(0, 0, 0, 0);
             if (j <= lim_tile) v = *(const int4 *) (vc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
             const uint16_t * vh = (const uint16_t *) &v;
@@ -509,15 +549,14 @@ __global__ __launch_bounds__(kBlock) void k_att_pv(const uint16_t * __restrict__
             for (int e = 0; e < 8; ++e) vt[(8 * c + e) * kVS + pr] = vh[e];
         }
         __syncthreads();
-        int4 pa[2], vb[8][2];
+        int4 pa[2], vb[4][2];
         pa[0] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k);
         pa[1] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k + 8);
 #pragma unroll
-        for (int d8 = 0; d8 < 8; ++d8) {
-            vb[d8][0] = *(const int4 *) (vt + (16 * d8 + i) * kVS + 16 * k);
-            vb[d8][1] = *(const int4 *) (vt + (16 * d8 + i) * kVS + 16 * k + 8);
+        for (int d4 = 0; d4 < 4; ++d4) {
+            vb[d4][0] = *(const int4 *) (vt + (64 * grp + 16 * d4 + i) * kVS + 16 * k);
+            vb[d4][1] = *(const int4 *) (vt + (64 * grp + 16 * d4 + i) * kVS + 16 * k + 8);
         }
-        // eight independent accumulators per step keep the MFMA pipe busy
 #pragma unroll
         for (int st = 0; st < 16; ++st) {
             const int e = st & 7, wv = e >> 1;
@@ -526,21 +565,22 @@ __global__ __launch_bounds__(kBlock) void k_att_pv(const uint16_t * __restrict__
             const uint16_t ph = (uint16_t) ((e & 1) ? ((uint32_t) pw >> 16) : ((uint32_t) pw & 0xffffu));
             const double pd = kvd(ph, bf);
 #pragma unroll
-            for (int d8 = 0; d8 < 8; ++d8) {
-                const int4 & v4 = vb[d8][st >> 3];
+            for (int d4 = 0; d4 < 4; ++d4) {
+                const int4 & v4 = vb[d4][st >> 3];
                 const int vw = wv == 0 ? v4.x : wv == 1 ? v4.y : wv == 2 ? v4.z : v4.w;
                 const uint16_t vh = (uint16_t) ((e & 1) ? ((uint32_t) vw >> 16) : ((uint32_t) vw & 0xffffu));
-                acc[d8] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d8], 0, 0, 0);
+                acc[d4] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d4], 0, 0, 0);
             }
         }
     }
 #pragma unroll
-    for (int d8 = 0; d8 < 8; ++d8)
+    for (int d4 = 0; d4 < 4; ++d4)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = row0 + 16 * w + 4 * r + k;
-            if (row < n) out[(size_t) row * out_stride + h * kHD + 16 * d8 + i] = (float) acc[d8][r];
+            if (row < n) out[(size_t) row * out_stride + h * kHD + 64 * grp + 16 * d4 + i] = (float) acc[d4][r];
         }
+  }
 }
 
 __host__ __device__ constexpr size_t attn_rows_lds_bytes(int n_ctx) {
