@@ -114,12 +114,14 @@ __global__ __launch_bounds__(kBlock) void k_gemm_q8(const int8_t * __restrict__ 
         for (int u = 0; u < kU; ++u)
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                a[u][i] = *(const long *) (wrow[i] + (b0 + u) * kQK);
-                bq[u][i] = qok[i] ? *(const long *) (qrow[i] + (b0 + u) * kQK) : 0L;
+                const bool in = b0 + u < BPR;   // K % (32 kU) may leave a short last step
+                a[u][i] = in ? *(const long *) (wrow[i] + (b0 + u) * kQK) : 0L;
+                bq[u][i] = in && qok[i] ? *(const long *) (qrow[i] + (b0 + u) * kQK) : 0L;
             }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int b = b0 + u;
+            if (b >= BPR) break;               // uniform
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 float dwv[4];
