@@ -27,13 +27,15 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 
 
-def frame_bytes(cfg, w, n_kv):
+def frame_bytes(cfg, w, n_kv, cp_table=False):
     """Algorithmic HBM bytes of one frame: every weight byte once per pass
     that reads it (talker once; code predictor 15 passes; heads once per
     pass), plus KV reads/writes.  Activations are excluded (<0.1%).  n_kv is
     the talker KV length, or a list of lengths (one per stream) for the
     multi-stream loop, which reads every weight once per frame for all
-    streams together."""
+    streams together.  cp_table: steps 1..14 take code-predictor layer 0's
+    QKV rows from the per-code table (one fp32 row each) instead of reading
+    that layer's QKV weights."""
     def nbytes(name):
         return w[name][2].nbytes
     talker = sum(nbytes(n) for n in w if n.startswith("talker.blk."))
@@ -41,6 +43,11 @@ def frame_bytes(cfg, w, n_kv):
     cp_layers = sum(nbytes(n) for n in w if n.startswith("code_pred.blk."))
     cp = 15 * (cp_layers + nbytes("code_pred.output_norm.weight")) + sum(
         nbytes(f"code_pred.lm_head.{g}.weight") for g in range(15))
+    if cp_table:
+        qkv0 = sum(nbytes(f"code_pred.blk.0.attn_{x}.weight") for x in "qkv") + nbytes("code_pred.blk.0.attn_norm.weight")
+        qkvd = (cfg.n_head + 2 * cfg.n_kv_head) * cfg.head_dim
+        cp -= 14 * qkv0
+        cp += 14 * qkvd * 4
     kv_row = cfg.n_kv_head * cfg.head_dim * 2 * 2          # K and V, fp16
     per_stream = 0
     for n in (n_kv if isinstance(n_kv, (list, tuple)) else [n_kv]):
@@ -434,7 +441,7 @@ def main():
     ms_per_step = elapsed * 1000.0 / args.steps
     fps = args.steps / elapsed
     n_kv_mid = plen + args.warmup + args.steps // 2
-    fbytes = frame_bytes(cfg, w.tensors, n_kv_mid)
+    fbytes = frame_bytes(cfg, w.tensors, n_kv_mid, cp_table=path == 3 and os.environ.get("Q3T_CP_QKV_TABLE") != "0")
 
     # per-kernel HIP-event timing on the context's stream (talker layer 0)
     kernels = {}

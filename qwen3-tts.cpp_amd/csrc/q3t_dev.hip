@@ -143,7 +143,7 @@ struct q3t_dev {
     // persistent frame kernel (q3t_frame_kernel.h)
     bool fk_ok = false;            // model / context qualify this context for it
     int fk_variant = 0;            // see fk_kernel()
-    int xcd_map = -1;              // workgroup b of the frame launch on XCD b % 8: -1 unknown, 0 no, 1 yes
+    int xcd_map = -1;              // frame-launch workgroups dealt round-robin over the XCDs: -1 unknown, 0 no, 1 yes
     bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
     bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
     bool fk_tab = false;           // the persistent kernel reads cp_tab
@@ -678,16 +678,19 @@ __global__ __launch_bounds__(fk::kT) void k_xcc_map(int32_t * out) {
     }
 }
 
-// Whether workgroup b of the frame kernel's launch runs on XCD b % 8 (the
-// XCD-parallel layer program relies on it); checked once per context.
+// Whether the workgroups of a frame-sized cooperative launch are dealt to the
+// XCDs round-robin, workgroup b on XCD (b + r) % 8 for one rotation r (the
+// XCD-parallel layer program relies on the classes b % 8 each sharing an
+// XCD; r itself varies between launches); checked once per context.
 int xcd_map_ok(q3t_dev * c, int grid, bool & ok) {
     if (c->xcd_map < 0) {
         int32_t * d = nullptr;
         if (dev_alloc_t(c, &d, (size_t) grid)) return -1;
         void * args[] = {&d};
         std::vector<int32_t> h(grid, -1);
-        if (hipLaunchCooperativeKernel((const void *) k_xcc_map, dim3(grid), dim3(fk::kT), args, 0, c->stream) ==
-            hipSuccess) {
+        const hipError_t e =
+            hipLaunchCooperativeKernel((const void *) k_xcc_map, dim3(grid), dim3(fk::kT), args, 0, c->stream);
+        if (e == hipSuccess) {
             HIP_OK(hipMemcpyAsync(h.data(), d, (size_t) grid * 4, hipMemcpyDeviceToHost, c->stream));
             HIP_OK(hipStreamSynchronize(c->stream));
         } else {
@@ -695,17 +698,19 @@ int xcd_map_ok(q3t_dev * c, int grid, bool & ok) {
         }
         dev_free(c, d);
         int good = 0;
-        for (int b = 0; b < grid; ++b) good += h[b] == b % fk::kXcd;
+        for (int b = 0; b < grid; ++b) good += h[b] == (h[0] + b) % fk::kXcd;
         c->xcd_map = good == grid ? 1 : 0;
+        if (!c->xcd_map)
+            std::fprintf(stderr, "q3t: XCD map check %s (%d of %d workgroups dealt round-robin; wg 0..7 on %d %d %d %d %d %d %d %d); "
+                                 "using the row-parallel frame program\n",
+                         e == hipSuccess ? "failed" : hipGetErrorString(e), good, grid, h[0], h[1], h[2], h[3], h[4], h[5],
+                         h[6], h[7]);
     }
     ok = c->xcd_map == 1;
     return 0;
 }
 
-const char * fk_err_msg(int32_t e) {
-    return e == 2 ? "frame kernel: a workgroup ran on another XCD than the XCD-parallel layers assume (results invalid)"
-                  : "frame kernel: a phase wait timed out (results invalid)";
-}
+const char * fk_err_msg(int32_t) { return "frame kernel: a phase wait timed out (results invalid)"; }
 
 namespace {
 int build_cp_tab(q3t_dev * c);   // below, with the prefill helpers it uses
@@ -757,7 +762,7 @@ int fk_prepare(q3t_dev * c) {
         (g.n_head * 128 + grid - 1) / grid * 2 * chunks > 2 * fk::kMaxChunk)
         return 0;
     // the XCD-parallel layer program: Q8_0 0.6B shapes, one workgroup per CU
-    // on 256 CUs with workgroup b on XCD b % 8 (Q3T_FRAME_XCD=0 turns it off)
+    // on 256 CUs, workgroups dealt round-robin over the 8 XCDs (Q3T_FRAME_XCD=0 turns it off)
     bool xcd = variant == 1 && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0;
     if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
     if (xcd && xcd_map_ok(c, grid, xcd)) return -1;

@@ -201,14 +201,20 @@ __device__ __forceinline__ float twait(const uint64_t * p, uint32_t tag, bool & 
     return __uint_as_float((uint32_t) v);
 }
 
-// XCD-local tagged I/O.  Workgroup b runs on XCD b % 8 (the host checks
-// this before it selects a kernel that relies on it), and the eight XCDs
-// have separate L2 caches.  Data exchanged only among the workgroups of one
+// XCD-local tagged I/O.  The hardware deals the workgroups of a launch to
+// the eight XCDs round-robin: workgroup b runs on XCD (b + r) % 8 for a
+// rotation r that can differ between launches (the host checks the
+// round-robin form before it selects a kernel that relies on it), so the
+// workgroups with equal b % 8 always share an XCD, and the eight XCDs have
+// separate L2 caches.  Data exchanged only among the workgroups of one
 // XCD goes through that XCD's L2: a plain 64-bit store (wavefront scope),
 // polled with a load that skips the CU's L1 (system scope: sc0 sc1), at
 // about 0.7 us per hand-off against 1.1-1.9 us for the device-scope form.
-// A region written this way is only ever written and read by one XCD within
-// a launch, and never shares a cache line with another XCD's region.
+// A region written this way is only ever written and read by the workgroups
+// of one b % 8 class within a launch, and never shares a cache line with
+// another class's region.  Were the dealing not round-robin, a reader on
+// another XCD would not see the writer's L2 line and its wait would time out
+// (error 1): never a stale value, since every tag is unique.
 __device__ __forceinline__ uint64_t lload(const uint64_t * p) {
     return __hip_atomic_load((const Q3T_GAS uint64_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -1749,8 +1755,8 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
 
 // ---------------------------------------------------- XCD-parallel layers
 // The 0.6B shapes (hidden 1024, 16 query / 8 KV heads, FFN 3072) on 256
-// workgroups, workgroup b on XCD x = b % 8 with rank j = b / 8 among the
-// XCD's 32.  XCD x owns KV head x (query heads 2x, 2x+1) and the FFN
+// workgroups, workgroup b in XCD class x = b % 8 (one physical XCD, see the
+// XCD-local I/O above) with rank j = b / 8 among the class's 32.  XCD x owns KV head x (query heads 2x, 2x+1) and the FFN
 // columns [384x, 384x + 384); a layer is
 //   QKV      XCD x: its heads' 512 rows, 16 per workgroup        -> XCD-local
 //   attn     code predictor: every workgroup of XCD x, the cache in its
@@ -2081,8 +2087,7 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
 // `frame` indexes the sampler streams and the frame state; `epoch` (distinct
 // for every launch since the arena was last cleared) makes the phase tags.
 // XT: the XCD-parallel layer program (layer_x; Q8_0 0.6B shapes, 256
-// workgroups); a workgroup that finds itself on another XCD than b % 8
-// raises error 2 and does nothing more (its peers' waits then time out).
+// workgroups dealt round-robin over the XCDs).
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t v;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
@@ -2096,10 +2101,6 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const Args & A = *Ap;
     __shared__ Lds L;
     bool dead = false;
-    if (XT && xcc_id() != (blockIdx.x & 7)) {
-        if (threadIdx.x == 0) atomicExch(A.err, 2);
-        return;
-    }
     FrameState * st = A.st;
     if (st->done) return;
     const uint32_t tb = (uint32_t) (epoch + 1) << 12;
