@@ -232,6 +232,60 @@ int orc_generate_rows(orc_model * m, const float * prefill, int32_t plen, const 
 int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trailing,
                int32_t trail_len, const float * pad, const orc_gen_params * p, int32_t * codes_out);
 
+/* ---- audio-tokenizer decoder (vocoder), q3t_vocoder.cpp ----
+ * Restates src/audio_tokenizer_decoder.cpp (build_graph :636-843,
+ * decode_window :946).  Widths come from the config; tensors are named and
+ * laid out as the GGUF's tok_dec.* tensors (ggml ne order, ne0 contiguous).
+ * Numerics: fp16-rounded activations into every F16-weight product, exact
+ * products summed in fp64 and rounded once; F32 attention; the C library's
+ * expf/sinf/tanhf.  Parity with ggml is tolerance-level (its fp32 lane sums
+ * and SIMD exp are not restated). */
+typedef struct orc_voc_config {
+    int32_t n_codebooks;      /* 16 */
+    int32_t codebook_size;    /* 2048 */
+    int32_t codebook_dim;     /* 256 */
+    int32_t hidden;           /* 512: VQ output and pre-transformer width */
+    int32_t latent;           /* 1024: pre_conv / attention q,k,v / upsample width */
+    int32_t n_layers;         /* 8 */
+    int32_t n_heads;          /* 16 (head_dim = latent / n_heads) */
+    int32_t ffn;              /* 1024 */
+    int32_t cnx_ffn;          /* 4096: ConvNeXt pwconv1 width */
+    int32_t up_kernel;        /* 2: upsample conv_t kernel (stride 2) */
+    int32_t decoder_dim;      /* 1536 */
+    int32_t rates[4];         /* 8 5 4 3 */
+    int32_t dec_kernel[4];    /* conv_t kernels, 2 * rate */
+    float   rms_eps;          /* 1e-5 */
+    float   rope_theta;       /* 1e4 */
+} orc_voc_config;
+
+typedef struct orc_voc orc_voc;
+orc_voc *    orc_voc_create(const orc_voc_config * cfg);
+void         orc_voc_destroy(orc_voc * m);
+void         orc_voc_set_threads(orc_voc * m, int32_t n);
+const char * orc_voc_last_error(const orc_voc * m);
+/* Borrows `data`. */
+int          orc_voc_set_tensor(orc_voc * m, const char * name, int32_t type, const void * data, size_t nbytes);
+/* checks every tensor, then normalises the codebooks (load_model :318-340) */
+int          orc_voc_finalize(orc_voc * m);
+int64_t      orc_voc_samples_for_frames(const orc_voc * m, int32_t n_frames);
+/* decode_single: codes [n][n_codebooks] at positions pos0..; out holds
+ * orc_voc_samples_for_frames(n) floats; latent_out (optional) [n][hidden]. */
+int          orc_voc_decode_single(orc_voc * m, const int32_t * codes, int32_t n, int32_t pos0, float * out,
+                                   float * latent_out);
+int          orc_voc_decode_window(orc_voc * m, const int32_t * codes, int32_t n_frames, int32_t start,
+                                   int32_t end, int32_t context, float * out, int64_t cap, int64_t * n_out);
+/* one named stage (see orc_voc_set_record for the names) from in [T][C]
+ * (or, for "latent", from codes [T][n_codebooks]); out [T_out][C_out]. */
+int          orc_voc_run_stage(orc_voc * m, const char * name, const float * in, const int32_t * codes, int64_t T,
+                               int64_t C, int32_t pos0, float * out, int64_t cap, int64_t * T_out, int64_t * C_out);
+/* stage recording: with on != 0 every decode_single keeps each stage's fp32
+ * rows (latent, pre_conv, input_proj, pre_tfm.<l>, output_proj,
+ * upsample.<i>, dec.0, dec.<b>.conv_t, dec.<b>.res.<r>, dec.6). */
+void         orc_voc_set_record(orc_voc * m, int32_t on);
+int32_t      orc_voc_stage_count(const orc_voc * m);
+int          orc_voc_stage(const orc_voc * m, int32_t i, char * name, int32_t name_cap, float * out, int64_t cap,
+                           int64_t * T, int64_t * C);
+
 #ifdef __cplusplus
 }
 #endif

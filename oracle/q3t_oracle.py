@@ -95,6 +95,20 @@ def lib():
         L.orc_generate.argtypes = [vp, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, i32, vp, vp]
         L.orc_generate_rows.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, vp]
         L.orc_frames.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp]
+        L.orc_voc_create.argtypes = [vp]; L.orc_voc_create.restype = vp
+        L.orc_voc_destroy.argtypes = [vp]; L.orc_voc_destroy.restype = None
+        L.orc_voc_set_threads.argtypes = [vp, i32]; L.orc_voc_set_threads.restype = None
+        L.orc_voc_last_error.argtypes = [vp]; L.orc_voc_last_error.restype = ctypes.c_char_p
+        L.orc_voc_set_tensor.argtypes = [vp, ctypes.c_char_p, i32, vp, ctypes.c_size_t]
+        L.orc_voc_finalize.argtypes = [vp]
+        L.orc_voc_samples_for_frames.argtypes = [vp, i32]; L.orc_voc_samples_for_frames.restype = i64
+        L.orc_voc_decode_single.argtypes = [vp, vp, i32, i32, vp, vp]
+        L.orc_voc_decode_window.argtypes = [vp, vp, i32, i32, i32, i32, vp, i64, ctypes.POINTER(i64)]
+        L.orc_voc_set_record.argtypes = [vp, i32]; L.orc_voc_set_record.restype = None
+        L.orc_voc_run_stage.argtypes = [vp, ctypes.c_char_p, vp, vp, i64, i64, i32, vp, i64,
+                                        ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        L.orc_voc_stage_count.argtypes = [vp]; L.orc_voc_stage_count.restype = i32
+        L.orc_voc_stage.argtypes = [vp, i32, ctypes.c_char_p, i32, vp, i64, ctypes.POINTER(i64), ctypes.POINTER(i64)]
         _lib = L
     return _lib
 
@@ -399,3 +413,88 @@ class Oracle:
         if n < 0:
             raise RuntimeError(self.error())
         return codes[:n].copy()
+
+
+class VocOracle:
+    """CPU restatement of the audio-tokenizer decoder (q3t_vocoder.cpp);
+    borrows the arrays of `weights` (qwen3_tts_amd.vocoder.VocWeights)."""
+
+    def __init__(self, cfg, weights, threads=8):
+        self.L = lib()
+        self.cfg = cfg
+        self._cc = cfg.to_c()
+        self.h = self.L.orc_voc_create(ctypes.byref(self._cc))
+        self.weights = weights
+        for name, (ttype, ne, arr) in weights.items():
+            self.L.orc_voc_set_tensor(self.h, name.encode(), ttype, _p(arr), arr.nbytes)
+        if self.L.orc_voc_finalize(self.h) != 0:
+            raise RuntimeError(self.error())
+        self.L.orc_voc_set_threads(self.h, threads)
+
+    def error(self):
+        return self.L.orc_voc_last_error(self.h).decode()
+
+    def close(self):
+        if self.h:
+            self.L.orc_voc_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def samples_for_frames(self, n):
+        return int(self.L.orc_voc_samples_for_frames(self.h, n))
+
+    def decode_single(self, codes, pos0=0, want_latent=False):
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        n = codes.shape[0]
+        out = np.zeros(self.samples_for_frames(n), np.float32)
+        lat = np.zeros((n, self.cfg.hidden), np.float32) if want_latent else None
+        if self.L.orc_voc_decode_single(self.h, _p(codes), n, pos0, _p(out), _p(lat)) != 0:
+            raise RuntimeError(self.error())
+        return (out, lat) if want_latent else out
+
+    def stages(self, codes, pos0=0):
+        """{name: [T][C] fp32} of every stage of decode_single(codes, pos0)."""
+        self.L.orc_voc_set_record(self.h, 1)
+        try:
+            self.decode_single(codes, pos0)
+            out = {}
+            for i in range(self.L.orc_voc_stage_count(self.h)):
+                T, C = ctypes.c_int64(0), ctypes.c_int64(0)
+                name = ctypes.create_string_buffer(64)
+                self.L.orc_voc_stage(self.h, i, name, 64, None, 0, ctypes.byref(T), ctypes.byref(C))
+                a = np.zeros((T.value, C.value), np.float32)
+                self.L.orc_voc_stage(self.h, i, name, 64, _p(a), a.size, ctypes.byref(T), ctypes.byref(C))
+                out[name.value.decode()] = a
+            return out
+        finally:
+            self.L.orc_voc_set_record(self.h, 0)
+
+    def run_stage(self, name, x, pos0=0):
+        """one stage from fp32 rows x [T][C] (codes [T][16] for "latent")."""
+        T = x.shape[0]
+        if name == "latent":
+            codes = np.ascontiguousarray(x, dtype=np.int32)
+            xin, C = None, 16
+        else:
+            codes, xin = None, np.ascontiguousarray(x, dtype=np.float32)
+            C = xin.shape[1]
+        c = self.cfg
+        cap = max(T, self.samples_for_frames(1)) * 8 * max(c.latent, c.cnx_ffn, c.decoder_dim, 16) + 64
+        out = np.zeros(cap, np.float32)
+        To, Co = ctypes.c_int64(0), ctypes.c_int64(0)
+        if self.L.orc_voc_run_stage(self.h, name.encode(), _p(xin), _p(codes), T, C, pos0, _p(out), cap,
+                                    ctypes.byref(To), ctypes.byref(Co)) != 0:
+            raise RuntimeError(self.error())
+        return out[:To.value * Co.value].reshape(To.value, Co.value).copy()
+
+    def decode_window(self, codes, start, end, context):
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        cap = self.samples_for_frames(end - max(0, start - max(0, context)))
+        out = np.zeros(max(cap, 1), np.float32)
+        n = ctypes.c_int64(0)
+        if self.L.orc_voc_decode_window(self.h, _p(codes), codes.shape[0], start, end, context, _p(out), cap,
+                                        ctypes.byref(n)) != 0:
+            raise RuntimeError(self.error())
+        return out[:n.value].copy()
