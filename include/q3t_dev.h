@@ -229,6 +229,14 @@ int  q3t_dev_build_prefill_icl(q3t_dev * dev, const int32_t * text_tokens, int32
 int  q3t_dev_frames_begin(q3t_dev * dev, const q3t_frame_args * args);
 int  q3t_dev_frames_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
                         int32_t * n_emitted_out, int32_t * eos_out);
+/* Device address of the frame loop's code rows: frame f's n_codebooks codes
+ * at + f * n_codebooks, valid for the frames emitted since the last
+ * q3t_dev_frames_begin (complete once frames_run returns).  The streaming
+ * vocoder reads them in place (q3t_voc_decode_window with codes_on_device),
+ * where the reference hands codes_total from its FrameCallback
+ * (src/tts_transformer.cpp:3213, src/qwen3_tts.cpp:294) to decode_window.
+ * NULL before the first q3t_dev_frames_begin. */
+const int32_t * q3t_dev_frame_codes(const q3t_dev * dev);
 
 /* Frame-loop statistics since the last q3t_dev_frames_begin or
  * q3t_dev_streams_begin: GPU time of the frame launches (HIP events around

@@ -122,6 +122,7 @@ struct q3t_dev {
     SampleParams * params = nullptr;
     uint8_t * seen = nullptr;
     int32_t * codes_out = nullptr; int32_t codes_cap = 0;
+    bool codes_begun = false;          // codes_out holds a frame loop's rows (q3t_dev_frame_codes)
     float * trailing = nullptr; int32_t trailing_cap = 0; int32_t n_trailing = 0;
     float * pad = nullptr;
     // attention-row capture (q3t_dev_set_attn_capture): post-softmax rows
@@ -2097,8 +2098,13 @@ int q3t_dev_frames_begin(q3t_dev * c, const q3t_frame_args * a) {
     c->run_frames = 0;
     c->frames_max = a->max_len;
     c->frames_ready = true;
+    c->codes_begun = true;
     c->stats_streams = false;
     return 0;
+}
+
+const int32_t * q3t_dev_frame_codes(const q3t_dev * c) {
+    return c && c->codes_begun ? c->codes_out : nullptr;
 }
 
 int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32_t * n_emitted_out, int32_t * eos_out) {

@@ -1,0 +1,357 @@
+// q3t_voc_kernels.h -- gfx950 kernels of the audio-tokenizer decoder (the
+// vocoder after the frame loop, src/audio_tokenizer_decoder.cpp).
+//
+// Layout: activations are time-major rows [t][c] with the channel stride
+// padded to a multiple of 32 (pad channels hold zeros), so that every
+// convolution and linear layer is one GEMM over (tap, channel) on
+// v_mfma_f32_16x16x32_f16: the F16 weights times the fp16-rounded activation
+// (ggml's F16 im2col / vec_dot_type), accumulated in fp32 as ggml does.
+// Element-wise work (bias, layer scale, residual add, snake / GELU / SwiGLU
+// and the fp16 rounding of the next layer's input) runs in the GEMM's
+// epilogue, so each conv reads its input once and writes its output once.
+#pragma once
+
+#include "q3t_numerics.h"
+
+namespace q3t {
+namespace voc {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+enum : int32_t { ACT_NONE = 0, ACT_SNAKE = 1, ACT_GELU = 2, ACT_SWIGLU = 3 };
+
+// snake (src/audio_tokenizer_decoder.cpp:402-426): x + sin(x e^a)^2 e^-b,
+// with ea = e^alpha and eb = e^-beta per channel (computed on the host).
+__device__ __forceinline__ float snake(float x, float ea, float eb) {
+    const float s = sinf(x * ea);
+    const float sq = s * s;
+    return x + sq * eb;
+}
+
+// ggml_gelu's tanh form
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float c = 0.79788456080286535587989211986876f, a = 0.044715f;
+    return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + a * x * x)));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// One GEMM launch: Y[m * ostride + phase][n] = epi(sum_{tap, c} W[phase][n][tap][c]
+//                                                   * X[m + off0 + tap * dil][c])
+// X rows outside [0, rows_in) are zero (causal padding).  Epilogue, in the
+// graph's op order: v = acc; v += bias[n]; v *= scale[n]; v = res[row][n] + v;
+// yf[row][n] = v; yh[row][n] = fp16(act(v)).  ACT_SWIGLU pairs 16-channel
+// tiles (2q: gate, 2q+1: up, interleaved at upload) and writes
+// fp16(silu(gate) * up) at channel 16q + i.
+struct ConvArgs {
+    const uint16_t * x; int32_t xs, rows_in;
+    const uint16_t * w; int32_t Cp, KT, dil, off0;
+    int32_t M, N, Np, ostride;
+    const float * bias, * scale, * res; int32_t rs;
+    float * yf; int32_t yfs;
+    uint16_t * yh; int32_t yhs;
+    int32_t act;
+    const float * ea, * eb;
+};
+
+constexpr int kGemmT = 256;    // 4 waves: 2 along channels x 2 along time
+
+// fragments of K step s (tap s / CB, channels 32 (s % CB) ..) for k_conv_gemm
+template <int WM, int WN>
+__device__ __forceinline__ void gemm_load(const uint16_t * x, int xs, int rows_in, int Cp, int dil,
+                                          const uint16_t * const (&wrow)[WM], const int (&trow)[WN], int lk, int CB,
+                                          int s, v8h (&a)[WM], v8h (&b)[WN]) {
+    const int tap = s / CB, cc = (s - tap * CB) * 32;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) a[i] = *(const v8h *) (wrow[i] + (size_t) tap * Cp + cc);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const int src = trow[j] + tap * dil;
+        if (src >= 0 && src < rows_in)
+            b[j] = *(const v8h *) (x + (size_t) src * xs + cc + 8 * lk);
+        else
+            b[j] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+}
+
+// Wave (wc, wt) owns WM 16-channel tiles x WN 16-row tiles.  MFMA lane layout
+// (16x16x32): A[m = l%16][k = 8(l/16)..+7] (weights, m = channel), B[k][n =
+// l%16] (activations, n = time row), D[m = 4(l/16)+e][n = l%16]: a lane ends
+// with 4 consecutive channels of one time row.  The SwiGLU pairing needs the
+// wave's first channel tile even (WM even).
+template <int WM, int WN>
+__global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wc = wave & 1, wt = wave >> 1;
+    const int lm = lane & 15, lk = lane >> 4;
+    const int phase = blockIdx.z;
+    const int ch0 = blockIdx.x * (2 * WM * 16) + wc * WM * 16;
+    const int t0 = blockIdx.y * (2 * WN * 16) + wt * WN * 16;
+    const uint16_t * wbase = A.w + (size_t) phase * A.Np * A.KT * A.Cp;
+    const int CB = A.Cp >> 5, S = A.KT * CB;
+
+    const uint16_t * wrow[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) wrow[i] = wbase + (size_t) (ch0 + i * 16 + lm) * A.KT * A.Cp + 8 * lk;
+    int trow[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const int t = t0 + j * 16 + lm;
+        trow[j] = t < A.M ? t + A.off0 : -(1 << 30);
+    }
+
+    v4f acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    v8h a0[WM], b0[WN], a1[WM], b1[WN];
+    gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, 0, a0, b0);
+    for (int s = 0; s < S; s += 2) {
+        if (s + 1 < S) gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, s + 1, a1, b1);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+        if (s + 1 >= S) break;
+        if (s + 2 < S) gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, s + 2, a0, b0);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+    }
+
+    // epilogue through LDS: the wave's tile as [t][channel], then 64 lanes
+    // walk it channel-fastest (coalesced row stores)
+    constexpr int TC = WM * 16, TT = WN * 16, TS = TC + 4;
+    __shared__ float tile[4][TT * TS];
+    float * my = tile[wave];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) my[(j * 16 + lm) * TS + i * 16 + 4 * lk + e] = acc[i][j][e];
+    __syncthreads();
+    if (A.act == ACT_SWIGLU) {
+        // tiles 2q (gate) and 2q + 1 (up) of channel group q
+        for (int idx = lane; idx < TT * (TC / 2); idx += 64) {
+            const int tl = idx / (TC / 2), ol = idx - tl * (TC / 2);
+            const int t = t0 + tl;
+            const int pr = ol >> 4, w = ol & 15;
+            const int n = ((ch0 >> 1) + pr * 16) + w;
+            if (t >= A.M || n >= (A.N >> 1)) continue;
+            const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
+            A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
+        }
+        return;
+    }
+    for (int idx = lane; idx < TT * TC; idx += 64) {
+        const int tl = idx / TC, cl = idx - tl * TC;
+        const int t = t0 + tl, n = ch0 + cl;
+        if (t >= A.M || n >= A.N) continue;
+        const size_t row = (size_t) t * A.ostride + phase;
+        float v = my[tl * TS + cl];
+        if (A.bias) v = v + A.bias[n];
+        if (A.scale) v = v * A.scale[n];
+        if (A.res) v = A.res[row * A.rs + n] + v;
+        if (A.yf) A.yf[row * A.yfs + n] = v;
+        if (A.yh) {
+            float h = v;
+            if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
+            else if (A.act == ACT_GELU) h = gelu_tanh(v);
+            A.yh[row * A.yhs + n] = f2h(h);
+        }
+    }
+}
+
+// yh[t][c] = fp16(act(x[t][c])) for c < C (the input of a stage whose
+// producer is not a fused epilogue: the stage runner, or fp32 rows).
+__global__ void k_prep(const float * __restrict__ x, int32_t xs, int32_t T, int32_t C, int32_t act,
+                       const float * __restrict__ ea, const float * __restrict__ eb, uint16_t * __restrict__ yh,
+                       int32_t yhs) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t) T * C) return;
+    const int t = (int) (i / C), c = (int) (i - (int64_t) t * C);
+    float v = x[(size_t) t * xs + c];
+    if (act == ACT_SNAKE) v = snake(v, ea[c], eb[c]);
+    else if (act == ACT_GELU) v = gelu_tanh(v);
+    yh[(size_t) t * yhs + c] = f2h(v);
+}
+
+// VQ (src/audio_tokenizer_decoder.cpp:663-727): lat[f][d] = tab_0[code_0][d]
+// + ((tab_1[code_1][d] + tab_2[code_2][d]) + ...), tab_q = the codebook's
+// normalised rows through its output projection (built at finalize).  A code
+// outside [0, size) raises *bad and reads row 0.
+__global__ void k_vq_sum(const int32_t * __restrict__ codes, int32_t n_cb, int32_t n, const float * __restrict__ tab,
+                         int32_t size, int32_t hidden, float * __restrict__ latf, int32_t lfs,
+                         uint16_t * __restrict__ lath, int32_t lhs, int32_t * __restrict__ bad) {
+    const int f = blockIdx.x;
+    const int32_t * cf = codes + (size_t) f * n_cb;
+    for (int d = threadIdx.x; d < hidden; d += blockDim.x) {
+        float r = 0.0f, first = 0.0f;
+        for (int q = 0; q < n_cb; ++q) {
+            int code = cf[q];
+            if (code < 0 || code >= size) {
+                if (d == 0) atomicOr(bad, 1);
+                code = 0;
+            }
+            const float v = tab[((size_t) q * size + code) * hidden + d];
+            if (q == 0) first = v;
+            else if (q == 1) r = v;
+            else r = r + v;
+        }
+        const float y = first + r;
+        latf[(size_t) f * lfs + d] = y;
+        lath[(size_t) f * lhs + d] = f2h(y);
+    }
+}
+
+// RMSNorm rows (eps, weight) -> fp16: sum of fp32 squares in fp64,
+// y = (x * (1 / sqrtf(mean + eps))) * w.  One wave per row.
+__global__ void k_rms_h(const float * __restrict__ x, int32_t xs, int32_t T, int32_t C, const float * __restrict__ w,
+                        float eps, uint16_t * __restrict__ y, int32_t ys) {
+    const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float * r = x + (size_t) t * xs;
+    double s = 0.0;
+    for (int c = lane; c < C; c += 64) s += (double) (r[c] * r[c]);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float mean = (float) (s / (double) C);
+    const float sc = 1.0f / sqrtf(mean + eps);
+    for (int c = lane; c < C; c += 64) {
+        const float v = r[c] * sc;
+        y[(size_t) t * ys + c] = f2h(v * w[c]);
+    }
+}
+
+// NEOX RoPE in place on the q and k parts of qkv rows [t][3L] (q: [0, L),
+// k: [L, 2L)), positions pos0 + t, table rows [pos][hd/2].
+__global__ void k_rope_qk(float * __restrict__ qkv, int32_t qs, int32_t T, int32_t L, int32_t hd,
+                          const float * __restrict__ cs, const float * __restrict__ sn, int32_t pos0) {
+    const int half = hd >> 1;
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_row = 2 * (L / hd) * half;           // (q, k) x heads x pairs
+    if (i >= (int64_t) T * per_row) return;
+    const int t = (int) (i / per_row);
+    int r = (int) (i - (int64_t) t * per_row);
+    const int part = r / (per_row / 2);
+    r -= part * (per_row / 2);
+    const int h = r / half, p = r - h * half;
+    float * v = qkv + (size_t) t * qs + part * L + h * hd;
+    const float c = cs[(size_t) (pos0 + t) * half + p], s = sn[(size_t) (pos0 + t) * half + p];
+    const float x0 = v[p], x1 = v[p + half];
+    const float a = x0 * c, b = x1 * s, e = x0 * s, f = x1 * c;
+    v[p] = a - b;
+    v[p + half] = e + f;
+}
+
+// Causal F32 attention of one query row (blockIdx.x) and head (blockIdx.y),
+// one wave: scores q.k_j (fp64 sums of exact fp32 products, rounded once) *
+// scale, softmax with an fp64 denominator, P.V in fp64 -> fp16 row (the
+// input of attn_output).  hd <= 64.  Dynamic LDS: T floats.
+__global__ __launch_bounds__(64) void k_attn_causal(const float * __restrict__ qkv, int32_t qs, int32_t L, int32_t hd,
+                                                    float scale, uint16_t * __restrict__ out, int32_t os) {
+    extern __shared__ float p[];
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const float * q = qkv + (size_t) t * qs + h * hd;
+    float mx = -INFINITY;
+    for (int j = lane; j <= t; j += 64) {
+        const float * k = qkv + (size_t) j * qs + L + h * hd;
+        double s = 0.0;
+        for (int d = 0; d < hd; ++d) s = fma((double) q[d], (double) k[d], s);
+        const float v = (float) s * scale;
+        p[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    double sum = 0.0;
+    for (int j = lane; j <= t; j += 64) {
+        const float e = expf(p[j] - mx);
+        p[j] = e;
+        sum += (double) e;
+    }
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const float inv = (float) (1.0 / sum);
+    __syncthreads();
+    if (lane < hd) {
+        double o = 0.0;
+        for (int j = 0; j <= t; ++j) o = fma((double) (p[j] * inv), (double) qkv[(size_t) j * qs + 2 * L + h * hd + lane], o);
+        out[(size_t) t * os + h * hd + lane] = f2h((float) o);
+    }
+}
+
+// ConvNeXt front (src/audio_tokenizer_decoder.cpp:515-539): causal depthwise
+// k7 over fp16-rounded y, + bias, then LayerNorm over the C channels (eps
+// 1e-6, ggml_norm: fp64 mean, centred fp32 values, fp64 variance), * w + b,
+// rounded to fp16 for pwconv1.  One workgroup per row; LDS C floats.
+__global__ __launch_bounds__(256) void k_dwconv_ln(const float * __restrict__ y, int32_t ys, int32_t T, int32_t C,
+                                                   const uint16_t * __restrict__ w, const float * __restrict__ b,
+                                                   const float * __restrict__ nw, const float * __restrict__ nb,
+                                                   uint16_t * __restrict__ out, int32_t os) {
+    extern __shared__ float z[];
+    __shared__ double red[4];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double s = 0.0;
+    for (int c = tid; c < C; c += 256) {
+        double acc = 0.0;
+        for (int k = 0; k < 7; ++k) {
+            const int src = t + k - 6;
+            if (src < 0) continue;
+            acc += (double) round_f16(y[(size_t) src * ys + c]) * (double) h2f(w[c * 7 + k]);
+        }
+        const float v = (float) acc + b[c];
+        z[c] = v;
+        s += (double) v;
+    }
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    const float mean = (float) ((red[0] + red[1] + red[2] + red[3]) / (double) C);
+    __syncthreads();
+    double s2 = 0.0;
+    for (int c = tid; c < C; c += 256) {
+        const float v = z[c] - mean;
+        z[c] = v;
+        s2 += (double) (v * v);
+    }
+    for (int o = 32; o > 0; o >>= 1) s2 += __shfl_xor(s2, o);
+    if (lane == 0) red[wave] = s2;
+    __syncthreads();
+    const float var = (float) ((red[0] + red[1] + red[2] + red[3]) / (double) C);
+    const float sc = 1.0f / sqrtf(var + 1e-6f);
+    for (int c = tid; c < C; c += 256) {
+        float v = z[c] * sc;
+        v = v * nw[c];
+        out[(size_t) t * os + c] = f2h(v + nb[c]);
+    }
+}
+
+// Output conv (C -> 1, k7, causal) over the fp16 snake'd rows, + bias, tanh.
+// pre (optional) keeps the value before tanh; out gets samples t >= drop at
+// out[t - drop].  One thread per sample; C % 8 == 0.
+__global__ void k_out_conv(const uint16_t * __restrict__ x, int32_t xs, int32_t T, int32_t C,
+                           const uint16_t * __restrict__ w, float bias, float * __restrict__ pre,
+                           float * __restrict__ out, int64_t drop) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    double acc = 0.0;
+    for (int k = 0; k < 7; ++k) {
+        const int64_t src = t + k - 6;
+        if (src < 0) continue;
+        const uint16_t * r = x + src * xs;
+        for (int c = 0; c < C; c += 8) {
+            const v8h v = *(const v8h *) (r + c);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc = fma((double) (float) v[e], (double) h2f(w[(c + e) * 7 + k]), acc);
+        }
+    }
+    const float y = (float) acc + bias;
+    if (pre) pre[t] = y;
+    if (t >= drop) out[t - drop] = tanhf(y);
+}
+
+}  // namespace voc
+}  // namespace q3t

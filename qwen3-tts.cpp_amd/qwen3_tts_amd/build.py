@@ -16,12 +16,12 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
 
 
 def build_device_lib(verbose=False):
-    src = os.path.join(PKG_DIR, "csrc", "q3t_dev.hip")
+    srcs = [os.path.join(PKG_DIR, "csrc", f) for f in ("q3t_dev.hip", "q3t_voc.hip")]
     out_dir = os.path.join(PKG_DIR, "lib")
     os.makedirs(out_dir, exist_ok=True)
     out = os.path.join(out_dir, "libq3t_hip.so")
     tmp = out + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", *HIP_FLAGS, "-shared", "-o", tmp, src]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *HIP_FLAGS, "-shared", "-o", tmp, *srcs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + r.stderr[-4000:])

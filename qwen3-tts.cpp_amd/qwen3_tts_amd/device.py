@@ -23,7 +23,7 @@ EXPORTS = [
     "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
     "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
-    "q3t_dev_frames_run", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
+    "q3t_dev_frames_run", "q3t_dev_frame_codes", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
     "q3t_dev_streams_begin", "q3t_dev_streams_run", "q3t_dev_sync", "q3t_dev_time_kernel",
 ]
 
@@ -78,6 +78,8 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_frames_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
         lib.q3t_dev_frames_run.argtypes = [vp, i32, vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
         lib.q3t_dev_sync.argtypes = [vp]
+        lib.q3t_dev_frame_codes.argtypes = [vp]
+        lib.q3t_dev_frame_codes.restype = vp
         lib.q3t_dev_frames_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
                                              ctypes.POINTER(i32)]
         lib.q3t_dev_streams_reserve.argtypes = [vp, i32, i32]
@@ -280,6 +282,10 @@ class Device:
         self._check(self.lib.q3t_dev_frames_run(self.h, n_frames, _p(out), ctypes.byref(n), ctypes.byref(eos)),
                     "frames_run")
         return out[: n.value].copy(), bool(eos.value)
+
+    def frame_codes_ptr(self):
+        """device address of the frame loop's code rows (q3t_dev_frame_codes), or None"""
+        return self.lib.q3t_dev_frame_codes(self.h)
 
     def streams_reserve(self, n_streams, n_ctx):
         self._check(self.lib.q3t_dev_streams_reserve(self.h, n_streams, n_ctx), "streams_reserve")

@@ -93,6 +93,47 @@ def generate(dev, cfg, text, speaker=None, max_len=64, language_id=2050, repetit
     return np.stack(out).astype(np.int32)
 
 
+def stream_audio(dev, voc, cfg, text, speaker=None, max_len=64, chunk_frames=25, context_frames=48, on_audio=None,
+                 frame_chunk=1, **gen_kw):
+    """generate() with the streaming vocoder after it, as the reference's
+    StreamDecoderDriver (src/qwen3_tts.cpp:271-316, tail flush :615-633):
+    once chunk_frames new frames exist, decode_window decodes them with
+    context_frames of warm-up before them and hands the new samples to
+    on_audio(samples) (returning False stops generation).  The vocoder reads
+    the frame loop's device code rows in place (Device.frame_codes_ptr): no
+    host copy of codes feeds it.  Returns (codes, audio, n_windows)."""
+    state = {"emitted": 0, "windows": 0, "aborted": False}
+    audio = []
+
+    def deliver(samples):
+        if samples.size == 0:
+            return True
+        audio.append(samples)
+        state["windows"] += 1
+        if on_audio is not None and not state["aborted"]:
+            return bool(on_audio(samples))
+        return True
+
+    def on_frame(row, ncb, frame):
+        n = frame + 1
+        if state["aborted"] or n - state["emitted"] < chunk_frames:
+            return not state["aborted"]
+        s = voc.decode_window(None, state["emitted"], n, context_frames, n_frames=n, device_ptr=dev.frame_codes_ptr())
+        state["emitted"] = n
+        if not deliver(s):
+            state["aborted"] = True
+            return False
+        return True
+
+    codes = generate(dev, cfg, text, speaker, max_len=max_len, on_frame=on_frame, chunk=frame_chunk, **gen_kw)
+    total = codes.shape[0]
+    if total > state["emitted"] and not state["aborted"]:
+        deliver(voc.decode_window(None, state["emitted"], total, context_frames, n_frames=total,
+                                  device_ptr=dev.frame_codes_ptr()))
+    out = np.concatenate(audio) if audio else np.zeros(0, np.float32)
+    return codes, out, state["windows"]
+
+
 def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None):
     """Batched form of generate() over independent utterances.
 

@@ -210,3 +210,121 @@ class VocWeights:
 
     def nbytes(self):
         return sum(a.nbytes for _, _, a in self.tensors.values())
+
+
+# ---------------------------------------------------------------- device
+VOC_EXPORTS = [
+    "q3t_voc_create", "q3t_voc_destroy", "q3t_voc_last_error", "q3t_voc_set_tensor", "q3t_voc_finalize",
+    "q3t_voc_reserve", "q3t_voc_samples_for_frames", "q3t_voc_decode_window", "q3t_voc_decode",
+    "q3t_voc_run_stage",
+]
+
+_voc_lib = None
+
+
+def load_voc_library():
+    """the device library (lib/libq3t_hip.so) with the vocoder entry points typed"""
+    global _voc_lib
+    if _voc_lib is None:
+        from .device import load_library
+        lib = load_library()
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        lib.q3t_voc_create.argtypes = [ctypes.POINTER(CVocConfig), i32, ctypes.POINTER(ctypes.c_char_p)]
+        lib.q3t_voc_create.restype = vp
+        lib.q3t_voc_destroy.argtypes = [vp]
+        lib.q3t_voc_destroy.restype = None
+        lib.q3t_voc_last_error.argtypes = [vp]
+        lib.q3t_voc_last_error.restype = ctypes.c_char_p
+        lib.q3t_voc_set_tensor.argtypes = [vp, ctypes.c_char_p, i32, vp, ctypes.c_size_t]
+        lib.q3t_voc_finalize.argtypes = [vp]
+        lib.q3t_voc_reserve.argtypes = [vp, i32]
+        lib.q3t_voc_samples_for_frames.argtypes = [vp, i32]
+        lib.q3t_voc_samples_for_frames.restype = i64
+        lib.q3t_voc_decode_window.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp, i64, ctypes.POINTER(i64)]
+        lib.q3t_voc_decode.argtypes = [vp, vp, i32, i32, vp, i64, ctypes.POINTER(i64)]
+        lib.q3t_voc_run_stage.argtypes = [vp, ctypes.c_char_p, vp, vp, i64, i64, i32, vp, i64,
+                                          ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        _voc_lib = lib
+    return _voc_lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class VocError(RuntimeError):
+    pass
+
+
+class VocDevice:
+    """One HIP vocoder context (q3t_voc) on HIP device `device`."""
+
+    def __init__(self, cfg, weights, device=0):
+        self.lib = load_voc_library()
+        self.cfg = cfg
+        self._cc = cfg.to_c()
+        err = ctypes.c_char_p()
+        self.h = self.lib.q3t_voc_create(ctypes.byref(self._cc), device, ctypes.byref(err))
+        if not self.h:
+            raise VocError(err.value.decode() if err.value else "q3t_voc_create failed")
+        for name, (ttype, ne, arr) in weights.items():
+            self._check(self.lib.q3t_voc_set_tensor(self.h, name.encode(), ttype, _p(arr), arr.nbytes), name)
+        self._check(self.lib.q3t_voc_finalize(self.h), "finalize")
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise VocError(f"{what}: {self.lib.q3t_voc_last_error(self.h).decode()}")
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.q3t_voc_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def reserve(self, max_frames):
+        self._check(self.lib.q3t_voc_reserve(self.h, max_frames), "reserve")
+
+    def samples_for_frames(self, n):
+        return int(self.lib.q3t_voc_samples_for_frames(self.h, n))
+
+    def decode_window(self, codes, start, end, context, n_frames=None, device_ptr=None):
+        """codes: host [n_frames][16] int32, or device_ptr (int address of
+        device code rows, e.g. Device.frame_codes_ptr()) with n_frames."""
+        if device_ptr is None:
+            codes = np.ascontiguousarray(codes, dtype=np.int32)
+            ptr, on_dev, n_frames = _p(codes), 0, codes.shape[0]
+        else:
+            ptr, on_dev = ctypes.c_void_p(device_ptr), 1
+        cap = self.samples_for_frames(end - max(0, start - max(0, context)))
+        out = np.zeros(max(cap, 1), np.float32)
+        n = ctypes.c_int64(0)
+        self._check(self.lib.q3t_voc_decode_window(self.h, ptr, on_dev, n_frames, start, end, context, _p(out), cap,
+                                                   ctypes.byref(n)), "decode_window")
+        return out[:n.value].copy()
+
+    def decode(self, codes):
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        cap = self.samples_for_frames(codes.shape[0])
+        out = np.zeros(max(cap, 1), np.float32)
+        n = ctypes.c_int64(0)
+        self._check(self.lib.q3t_voc_decode(self.h, _p(codes), 0, codes.shape[0], _p(out), cap, ctypes.byref(n)),
+                    "decode")
+        return out[:n.value].copy()
+
+    def run_stage(self, name, x, pos0=0):
+        """one stage from fp32 rows x [T][C] (codes [T][16] for "latent")"""
+        T = x.shape[0]
+        if name == "latent":
+            codes, xin, C = np.ascontiguousarray(x, dtype=np.int32), None, 16
+        else:
+            codes, xin = None, np.ascontiguousarray(x, dtype=np.float32)
+            C = xin.shape[1]
+        c = self.cfg
+        cap = max(T, 2) * 8 * max(c.latent, c.cnx_ffn, c.decoder_dim, 16) + 64
+        out = np.zeros(cap, np.float32)
+        To, Co = ctypes.c_int64(0), ctypes.c_int64(0)
+        self._check(self.lib.q3t_voc_run_stage(self.h, name.encode(), _p(xin), _p(codes), T, C, pos0, _p(out), cap,
+                                               ctypes.byref(To), ctypes.byref(Co)), f"run_stage {name}")
+        return out[:To.value * Co.value].reshape(To.value, Co.value).copy()
