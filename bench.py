@@ -362,6 +362,77 @@ def streams_bench(args, cfg, w):
     print(json.dumps(out))
 
 
+def voc_flops(c, n):
+    """GEMM flops of one decode of an n-frame segment (the conv / linear
+    products and the pre-transformer attention; element-wise work excluded)"""
+    L, H, F = c.latent, c.hidden, c.ffn
+    f = 2.0 * n * 3 * H * L + 2.0 * n * L * H + 2.0 * n * H * L
+    f += c.n_layers * (2.0 * n * H * 3 * L + 2.0 * n * L * H + 2.0 * n * H * 2 * F + 2.0 * n * F * H
+                       + 2.0 * (n * (n + 1) / 2) * L * 2)
+    r = n
+    for _ in range(2):
+        f += 2.0 * r * L * L * 2
+        r = (r - 1) * 2 + c.up_kernel
+        f += 2.0 * r * L * c.cnx_ffn * 2
+    ch = c.decoder_dim
+    f += 2.0 * r * 7 * L * ch
+    for s in c.rates:
+        co = ch // 2
+        f += 2.0 * s * (r - 1) * 2 * ch * co
+        r = (r - 1) * s
+        f += 3 * (2.0 * r * 7 * co * co + 2.0 * r * co * co)
+        ch = co
+    return f + 2.0 * r * 7 * ch
+
+
+def vocoder_bench(args):
+    """The streaming vocoder's unit of work: one decode_window of the
+    reference's default stream shape (src/qwen3_tts.cpp:246-268: 48 frames of
+    warm-up context + 25 new frames = 2 s of 24 kHz audio), at the 12 Hz
+    tokenizer's decoder widths with seeded random weights.  Reports windows/s,
+    the real-time factor (audio seconds per wall second) and the GEMM
+    TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak."""
+    from qwen3_tts_amd import vocoder as V
+    c = V.full()
+    w = V.VocWeights(c, seed=5)
+    g = V.VocDevice(c, w)
+    ctx, chunk = args.voc_context, args.voc_chunk
+    n = ctx + chunk
+    codes = np.random.default_rng(9).integers(0, c.codebook_size, (n, c.n_codebooks)).astype(np.int32)
+    g.reserve(n)
+    for _ in range(max(args.warmup, 1)):
+        out = g.decode_window(codes, ctx, n, ctx)
+    steps = max(args.steps, 1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = g.decode_window(codes, ctx, n, ctx)
+    dt = (time.perf_counter() - t0) / steps
+    g.close()
+    audio_s = out.size / 24000.0
+    flops = voc_flops(c, n)
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the oracle on a bounded sample: a 2 + 2-frame window, scaled per new frame
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import q3t_oracle as orc
+        o = orc.VocOracle(c, w, threads=args.cpu_threads_max)
+        t0 = time.perf_counter()
+        small = o.decode_window(codes[:4], 2, 4, 2)
+        cdt = time.perf_counter() - t0
+        o.close()
+        cpu = {"value": round((small.size / 24000.0) / cdt, 4), "unit": "audio s per s", "cores": args.cpu_threads_max,
+               "kind": "port", "sample": "oracle decode_window of 2 context + 2 new frames at full widths"}
+    print(json.dumps({
+        "metric": "vocoder decode_window real-time factor (audio s per s)", "value": round(audio_s / dt, 1),
+        "unit": "audio s/s", "n_gpus": 1, "steps": steps, "warmup": max(args.warmup, 1),
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic", "config": {"workload": f"decode_window, {ctx} context + {chunk} new frames, 12 Hz "
+                                                    f"tokenizer decoder widths", "frames": n,
+                                        "samples_out": int(out.size)},
+        "gemm_tflops": round(flops / dt / 1e12, 2), "mfma_frac_whole_window": round(flops / dt / 2.5e15, 4),
+        "cpu_baseline": cpu}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +458,10 @@ def main():
                     help="instead of the short-prompt greedy loop, time long-context sampled decode after a long prefill")
     ap.add_argument("--long-prompt", type=int, default=2048, help="text ids of the --long prefill")
     ap.add_argument("--temperature", type=float, default=0.9, help="--long sampling temperature (0: greedy)")
+    ap.add_argument("--vocoder", action="store_true",
+                    help="time the streaming vocoder's decode_window (48 context + 25 new frames)")
+    ap.add_argument("--voc-context", type=int, default=48)
+    ap.add_argument("--voc-chunk", type=int, default=25)
     ap.add_argument("--streams", type=int, default=0,
                     help="instead of batch 1, time multi-stream batched decode of this many streams (Q8_0)")
     ap.add_argument("--path", default="persistent", choices=["persistent", "graph"],
@@ -402,6 +477,8 @@ def main():
     from qwen3_tts_amd.device import Device
     from qwen3_tts_amd.synth import Weights
 
+    if args.vocoder:
+        return vocoder_bench(args)
     cfg = config.full_06b()
     w = Weights(cfg, args.weights, seed=2024)
     if args.prefill > 0:

@@ -126,6 +126,7 @@ struct q3t_voc {
              * ffn = nullptr;
     int32_t * codes = nullptr;
     int32_t * bad = nullptr;
+    int n_cu = 256;
     size_t xf_n = 0, h_n = 0, mid_n = 0, wide_n = 0, audio_n = 0;
 };
 
@@ -275,14 +276,35 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
     a.act = act;
     a.ea = sn ? sn->ea : nullptr;
     a.eb = sn ? sn->eb : nullptr;
-    constexpr int WN = 4;
-    const dim3 grid((unsigned) (W.Np / (32 * W.WM)), (unsigned) ((M + 32 * WN - 1) / (32 * WN)), (unsigned) W.phases);
-    switch (W.WM) {
-    case 4: hipLaunchKernelGGL((k_conv_gemm<4, WN>), grid, dim3(kGemmT), 0, v->stream, a); break;
-    case 3: hipLaunchKernelGGL((k_conv_gemm<3, WN>), grid, dim3(kGemmT), 0, v->stream, a); break;
-    case 2: hipLaunchKernelGGL((k_conv_gemm<2, WN>), grid, dim3(kGemmT), 0, v->stream, a); break;
-    default: hipLaunchKernelGGL((k_conv_gemm<1, WN>), grid, dim3(kGemmT), 0, v->stream, a); break;
+    // tile: the largest (32 WM channels x 32 WN rows per workgroup) that
+    // still gives the launch a workgroup per CU; a smaller WM
+    // divides the weights' padded width (SwiGLU pairs need WM even)
+    int WM = W.WM, WN = 4;
+    auto wgs = [&](int wm, int wn) {
+        return (int64_t) (W.Np / (32 * wm)) * ((M + 32 * wn - 1) / (32 * wn)) * W.phases;
+    };
+    while (wgs(WM, WN) < v->n_cu) {
+        if (WN > 1) WN >>= 1;
+        else if (WM == 4) WM = 2;
+        else if ((WM == 2 || WM == 3) && act != ACT_SWIGLU) WM = 1;
+        else break;
     }
+    const dim3 grid((unsigned) (W.Np / (32 * WM)), (unsigned) ((M + 32 * WN - 1) / (32 * WN)), (unsigned) W.phases);
+#define Q3T_VOC_GEMM(wm, wn) hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a)
+#define Q3T_VOC_GEMM_WN(wm)                   \
+    switch (WN) {                             \
+    case 4: Q3T_VOC_GEMM(wm, 4); break;       \
+    case 2: Q3T_VOC_GEMM(wm, 2); break;       \
+    default: Q3T_VOC_GEMM(wm, 1); break;      \
+    }
+    switch (WM) {
+    case 4: Q3T_VOC_GEMM_WN(4); break;
+    case 3: Q3T_VOC_GEMM_WN(3); break;
+    case 2: Q3T_VOC_GEMM_WN(2); break;
+    default: Q3T_VOC_GEMM_WN(1); break;
+    }
+#undef Q3T_VOC_GEMM_WN
+#undef Q3T_VOC_GEMM
     HIP_OK(hipGetLastError());
     return 0;
 }
@@ -609,6 +631,9 @@ q3t_voc * q3t_voc_create(const q3t_voc_config * cfg, int32_t device, const char 
     q3t_voc * v = new q3t_voc();
     v->device = device;
     v->cfg = c;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        v->n_cu = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking) != hipSuccess) {
         delete v;
         return bad("hipStreamCreate failed");

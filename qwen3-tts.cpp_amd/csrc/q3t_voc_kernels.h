@@ -57,49 +57,83 @@ struct ConvArgs {
 
 constexpr int kGemmT = 256;    // 4 waves: 2 along channels x 2 along time
 
-// fragments of K step s (tap s / CB, channels 32 (s % CB) ..) for k_conv_gemm
+// The workgroup tile is 32 WM channels x 32 WN rows; wave (wc, wt) owns WM
+// 16-channel tiles x WN 16-row tiles.  Each K step (one tap, 32 channels)
+// stages the weight rows and the activation rows of the tile in LDS (16-byte
+// chunks, chunk index XOR (row & 3) against bank conflicts), double-buffered:
+// the global loads of step s + 1 are in flight while step s runs on the
+// matrix cores.  MFMA lane layout (16x16x32): A[m = l%16][k = 8(l/16)..+7]
+// (weights, m = channel), B[k][n = l%16] (activations, n = time row),
+// D[m = 4(l/16)+e][n = l%16].  The SwiGLU pairing needs WM even.
 template <int WM, int WN>
-__device__ __forceinline__ void gemm_load(const uint16_t * x, int xs, int rows_in, int Cp, int dil,
-                                          const uint16_t * const (&wrow)[WM], const int (&trow)[WN], int lk, int CB,
-                                          int s, v8h (&a)[WM], v8h (&b)[WN]) {
-    const int tap = s / CB, cc = (s - tap * CB) * 32;
-#pragma unroll
-    for (int i = 0; i < WM; ++i) a[i] = *(const v8h *) (wrow[i] + (size_t) tap * Cp + cc);
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-        const int src = trow[j] + tap * dil;
-        if (src >= 0 && src < rows_in)
-            b[j] = *(const v8h *) (x + (size_t) src * xs + cc + 8 * lk);
-        else
-            b[j] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
-    }
-}
+struct GemmTile {
+    static constexpr int BC = 32 * WM, BT = 32 * WN;
+    static constexpr int NA = (BC * 4 + kGemmT - 1) / kGemmT, NB = (BT * 4 + kGemmT - 1) / kGemmT;
+    static constexpr int STAGE = (BC + BT) * 32;                    // halfs per stage
+    static constexpr int TS = WM * 16 + 4;                          // epilogue row stride (floats)
+    static constexpr int LDS_STAGE = 2 * STAGE * 2, LDS_EPI = 4 * 16 * TS * 4;
+    static constexpr int LDS = LDS_STAGE > LDS_EPI ? LDS_STAGE : LDS_EPI;
+};
 
-// Wave (wc, wt) owns WM 16-channel tiles x WN 16-row tiles.  MFMA lane layout
-// (16x16x32): A[m = l%16][k = 8(l/16)..+7] (weights, m = channel), B[k][n =
-// l%16] (activations, n = time row), D[m = 4(l/16)+e][n = l%16]: a lane ends
-// with 4 consecutive channels of one time row.  The SwiGLU pairing needs the
-// wave's first channel tile even (WM even).
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chunk ^ (row & 3)) << 3); }
+
 template <int WM, int WN>
 __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    using G = GemmTile<WM, WN>;
+    __shared__ __align__(16) char smem[G::LDS];
+    uint16_t * lds = (uint16_t *) smem;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wc = wave & 1, wt = wave >> 1;
     const int lm = lane & 15, lk = lane >> 4;
     const int phase = blockIdx.z;
-    const int ch0 = blockIdx.x * (2 * WM * 16) + wc * WM * 16;
-    const int t0 = blockIdx.y * (2 * WN * 16) + wt * WN * 16;
+    const int cb0 = blockIdx.x * G::BC, tb0 = blockIdx.y * G::BT;
     const uint16_t * wbase = A.w + (size_t) phase * A.Np * A.KT * A.Cp;
     const int CB = A.Cp >> 5, S = A.KT * CB;
 
-    const uint16_t * wrow[WM];
+    // this thread's 16-byte chunks of the A (weights) and B (activations) tiles
+    const uint16_t * ga[G::NA];
+    int la[G::NA];
+    bool oa[G::NA];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) wrow[i] = wbase + (size_t) (ch0 + i * 16 + lm) * A.KT * A.Cp + 8 * lk;
-    int trow[WN];
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-        const int t = t0 + j * 16 + lm;
-        trow[j] = t < A.M ? t + A.off0 : -(1 << 30);
+    for (int r = 0; r < G::NA; ++r) {
+        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
+        oa[r] = c < G::BC * 4;
+        ga[r] = wbase + (size_t) (cb0 + (oa[r] ? row : 0)) * A.KT * A.Cp + col * 8;
+        la[r] = swz(row, col);
     }
+    int tb[G::NB], lb[G::NB], cbk[G::NB];
+    bool ob[G::NB];
+#pragma unroll
+    for (int r = 0; r < G::NB; ++r) {
+        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
+        ob[r] = c < G::BT * 4;
+        const int t = tb0 + row;
+        tb[r] = (ob[r] && t < A.M) ? t + A.off0 : -(1 << 30);
+        cbk[r] = col * 8;
+        lb[r] = G::BC * 32 + swz(row, col);
+    }
+    uint4 ra[G::NA], rb[G::NB];
+    auto fetch = [&](int s) {
+        const int tap = s / CB, cc = (s - tap * CB) * 32;
+#pragma unroll
+        for (int r = 0; r < G::NA; ++r)
+            ra[r] = oa[r] ? *(const uint4 *) (ga[r] + (size_t) tap * A.Cp + cc) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < G::NB; ++r) {
+            const int src = tb[r] + tap * A.dil;
+            rb[r] = (src >= 0 && src < A.rows_in) ? *(const uint4 *) (A.x + (size_t) src * A.xs + cc + cbk[r])
+                                                  : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto stash = [&](int buf) {
+        uint16_t * st = lds + buf * G::STAGE;
+#pragma unroll
+        for (int r = 0; r < G::NA; ++r)
+            if (oa[r]) *(uint4 *) (st + la[r]) = ra[r];
+#pragma unroll
+        for (int r = 0; r < G::NB; ++r)
+            if (ob[r]) *(uint4 *) (st + lb[r]) = rb[r];
+    };
 
     v4f acc[WM][WN];
 #pragma unroll
@@ -107,63 +141,71 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    v8h a0[WM], b0[WN], a1[WM], b1[WN];
-    gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, 0, a0, b0);
-    for (int s = 0; s < S; s += 2) {
-        if (s + 1 < S) gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, s + 1, a1, b1);
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int s = 0; s < S; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < S) fetch(s + 1);
+        const uint16_t * st = lds + buf * G::STAGE;
+        v8h af[WM], bf[WN];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) af[i] = *(const v8h *) (st + swz(wc * WM * 16 + i * 16 + lm, lk));
+#pragma unroll
+        for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (st + G::BC * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[i], b0[j], acc[i][j], 0, 0, 0);
-        if (s + 1 >= S) break;
-        if (s + 2 < S) gemm_load<WM, WN>(A.x, A.xs, A.rows_in, A.Cp, A.dil, wrow, trow, lk, CB, s + 2, a0, b0);
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        if (s + 1 < S) stash(buf ^ 1);
+        __syncthreads();
     }
 
-    // epilogue through LDS: the wave's tile as [t][channel], then 64 lanes
-    // walk it channel-fastest (coalesced row stores)
-    constexpr int TC = WM * 16, TT = WN * 16, TS = TC + 4;
-    __shared__ float tile[4][TT * TS];
-    float * my = tile[wave];
+    // epilogue one 16-row tile at a time through the wave's LDS slice
+    // ([row][channel]), then 64 lanes walk it channel-fastest (coalesced row
+    // stores).  LDS is in order within a wave, so no barrier is needed.
+    constexpr int TC = WM * 16, TS = G::TS;
+    float * my = (float *) smem + wave * 16 * TS;
+    const int ch0 = cb0 + wc * WM * 16, t0 = tb0 + wt * WN * 16;
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int j = 0; j < WN; ++j) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) my[(j * 16 + lm) * TS + i * 16 + 4 * lk + e] = acc[i][j][e];
-    __syncthreads();
-    if (A.act == ACT_SWIGLU) {
-        // tiles 2q (gate) and 2q + 1 (up) of channel group q
-        for (int idx = lane; idx < TT * (TC / 2); idx += 64) {
-            const int tl = idx / (TC / 2), ol = idx - tl * (TC / 2);
-            const int t = t0 + tl;
-            const int pr = ol >> 4, w = ol & 15;
-            const int n = ((ch0 >> 1) + pr * 16) + w;
-            if (t >= A.M || n >= (A.N >> 1)) continue;
-            const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
-            A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
+            for (int e = 0; e < 4; ++e) my[lm * TS + i * 16 + 4 * lk + e] = acc[i][j][e];
+        __builtin_amdgcn_wave_barrier();
+        const int tbase = t0 + j * 16;
+        if (A.act == ACT_SWIGLU) {
+            // tiles 2q (gate) and 2q + 1 (up) of channel group q
+            for (int idx = lane; idx < 16 * (TC / 2); idx += 64) {
+                const int tl = idx / (TC / 2), ol = idx - tl * (TC / 2);
+                const int t = tbase + tl;
+                const int pr = ol >> 4, w = ol & 15;
+                const int n = ((ch0 >> 1) + pr * 16) + w;
+                if (t >= A.M || n >= (A.N >> 1)) continue;
+                const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
+                A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
+            }
+        } else {
+            for (int idx = lane; idx < 16 * TC; idx += 64) {
+                const int tl = idx / TC, cl = idx - tl * TC;
+                const int t = tbase + tl, n = ch0 + cl;
+                if (t >= A.M || n >= A.N) continue;
+                const size_t row = (size_t) t * A.ostride + phase;
+                float v = my[tl * TS + cl];
+                if (A.bias) v = v + A.bias[n];
+                if (A.scale) v = v * A.scale[n];
+                if (A.res) v = A.res[row * A.rs + n] + v;
+                if (A.yf) A.yf[row * A.yfs + n] = v;
+                if (A.yh) {
+                    float h = v;
+                    if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
+                    else if (A.act == ACT_GELU) h = gelu_tanh(v);
+                    A.yh[row * A.yhs + n] = f2h(h);
+                }
+            }
         }
-        return;
-    }
-    for (int idx = lane; idx < TT * TC; idx += 64) {
-        const int tl = idx / TC, cl = idx - tl * TC;
-        const int t = t0 + tl, n = ch0 + cl;
-        if (t >= A.M || n >= A.N) continue;
-        const size_t row = (size_t) t * A.ostride + phase;
-        float v = my[tl * TS + cl];
-        if (A.bias) v = v + A.bias[n];
-        if (A.scale) v = v * A.scale[n];
-        if (A.res) v = A.res[row * A.rs + n] + v;
-        if (A.yf) A.yf[row * A.yfs + n] = v;
-        if (A.yh) {
-            float h = v;
-            if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
-            else if (A.act == ACT_GELU) h = gelu_tanh(v);
-            A.yh[row * A.yhs + n] = f2h(h);
-        }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 

@@ -94,6 +94,8 @@ TTSTransformer::TTSTransformer() = default;
 
 TTSTransformer::~TTSTransformer() { unload_model(); }
 
+const int32_t * TTSTransformer::device_frame_codes() const { return dev_ ? q3t_dev_frame_codes(dev_) : nullptr; }
+
 bool TTSTransformer::dev_ok(int rc) {
     if (rc == 0) return true;
     error_msg_ = dev_ ? q3t_dev_last_error(dev_) : "device not initialised";

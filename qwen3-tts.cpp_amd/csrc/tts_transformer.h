@@ -112,6 +112,14 @@ public:
     // keyed by this seed, so a fixed seed makes sampled decoding repeatable).
     void set_seed(uint64_t seed) { seed_ = seed; }
 
+    // Not in the reference: the device address of generate()'s code rows
+    // (frame f's n_codebooks codes at + f * n_codebooks), complete for every
+    // frame passed to the FrameCallback so far.  A streaming vocoder reads
+    // them in place (AudioTokenizerDecoder::decode_window_device) instead of
+    // the host codes_total the reference's driver hands to decode_window
+    // (src/qwen3_tts.cpp:294-306).  NULL before the first generate().
+    const int32_t * device_frame_codes() const;
+
 private:
     bool build_prefill_graph(const int32_t * text_tokens, int32_t n_tokens, const float * speaker_embd,
                              int32_t language_id, std::vector<float> & prefill_embd,

@@ -38,16 +38,19 @@ def build_facade(verbose=False):
     lib_dir = os.path.join(PKG_DIR, "lib")
     out = os.path.join(lib_dir, "libqwen3tts_amd.so")
     cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-o", out + ".tmp",
-           os.path.join(csrc, "tts_transformer.cpp"), os.path.join(csrc, "gguf_reader.cpp"),
+           os.path.join(csrc, "tts_transformer.cpp"), os.path.join(csrc, "audio_tokenizer_decoder.cpp"),
+           os.path.join(csrc, "gguf_reader.cpp"),
            "-L" + lib_dir, "-lq3t_hip", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("g++ (facade) failed:\n" + r.stderr[-4000:])
     os.replace(out + ".tmp", out)
     root = os.path.dirname(PKG_DIR)
-    test_src = os.path.join(root, "tests", "cpp", "test_transformer_dev.cpp")
-    test_bin = os.path.join(lib_dir, "test_transformer_dev")
-    if os.path.exists(test_src):
+    for name in ("test_transformer_dev", "test_vocoder_dev"):
+        test_src = os.path.join(root, "tests", "cpp", name + ".cpp")
+        test_bin = os.path.join(lib_dir, name)
+        if not os.path.exists(test_src):
+            continue
         cmd = ["g++", "-O2", "-std=c++17", "-I" + csrc, "-o", test_bin, test_src, "-L" + lib_dir,
                "-lqwen3tts_amd", "-lq3t_hip", "-Wl,-rpath," + lib_dir, "-Wl,-rpath,$ORIGIN"]
         r = subprocess.run(cmd, capture_output=True, text=True)

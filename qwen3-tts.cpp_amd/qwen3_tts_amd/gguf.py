@@ -40,9 +40,20 @@ def config_kv(cfg):
 
 def write(path, cfg, weights):
     u, f = config_kv(cfg)
+    _write(path, u, f, list(weights.items()))
+
+
+def write_vocoder(path, vcfg, weights):
+    """the tokenizer GGUF's decoder part: the three keys load_model reads
+    (src/audio_tokenizer_decoder.cpp:108-110) and the tok_dec.* tensors"""
+    u = {"qwen3-tts.tokenizer.sample_rate": 24000, "qwen3-tts.tokenizer.num_codebooks": vcfg.n_codebooks,
+         "qwen3-tts.tokenizer.codebook_size": vcfg.codebook_size}
+    _write(path, u, {}, list(weights.items()))
+
+
+def _write(path, u, f, tensors):
     kv = [("general.architecture", T_STR, "qwen3-tts"), ("general.alignment", T_U32, ALIGN)]
     kv += [(k, T_U32, v) for k, v in u.items()] + [(k, T_F32, v) for k, v in f.items()]
-    tensors = list(weights.items())
     head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv))
     for k, t, v in kv:
         head += _s(k) + struct.pack("<I", t)
@@ -50,7 +61,10 @@ def write(path, cfg, weights):
     off = 0
     offsets = []
     for name, (ttype, ne, arr) in tensors:
-        dims = [ne[0]] if ne[1] == 1 else [ne[0], ne[1]]
+        if len(ne) == 2:
+            dims = [ne[0]] if ne[1] == 1 else [ne[0], ne[1]]
+        else:
+            dims = list(ne)
         head += _s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
         head += struct.pack("<IQ", ttype, off)
         offsets.append(off)

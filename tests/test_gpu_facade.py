@@ -101,3 +101,48 @@ def test_facade_matches_oracle(tmp_path, wtype, layout):
     pre, trail, pad = icl_rows(o, cfg, text, text, ref_codes, spk)
     io = o.generate_rows(pre, trail, pad, max_len=max_len, temperature=0.0)
     assert np.array_equal(icl, io)
+
+
+def test_vocoder_facade_streams_from_device_codes(tmp_path):
+    """The drop-in AudioTokenizerDecoder loads a tokenizer GGUF (decoder
+    widths read from the tensor shapes) and streams generate()'s frames the
+    way src/qwen3_tts.cpp:271-316 does, from the frame loop's device code rows:
+    the windows equal the host-codes windows bit for bit, their audio equals
+    the oracle's windows within the vocoder tolerance, and the streamed length
+    equals the whole decode's."""
+    from qwen3_tts_amd import vocoder as V
+    vbin = os.path.join(PKG_DIR, "lib", "test_vocoder_dev")
+    assert os.path.exists(vbin), "build() first"
+    cfg = qcfg.tiny()
+    w = Weights(cfg, "q8_0", seed=33)
+    gguf.write(str(tmp_path / "tts.gguf"), cfg, w)
+    vc = V.VocConfig(codebook_dim=16, hidden=64, latent=128, n_layers=2, n_heads=2, ffn=128, cnx_ffn=256,
+                     decoder_dim=128)          # head_dim 64, as load_model assumes
+    vw = V.VocWeights(vc, seed=34)
+    gguf.write_vocoder(str(tmp_path / "voc.gguf"), vc, vw)
+    text = np.random.default_rng(35).integers(0, cfg.text_vocab - 8, 18).astype(np.int32)
+    chunk, context, max_len = 7, 5, 30
+    with open(tmp_path / "in.bin", "wb") as f:
+        f.write(struct.pack("<i", len(text)) + text.tobytes() + struct.pack("<iii", max_len, chunk, context))
+    print("[gpu] vocoder facade", file=sys.stderr, flush=True)
+    r = subprocess.run([vbin, str(tmp_path / "tts.gguf"), str(tmp_path / "voc.gguf"), str(tmp_path / "in.bin"),
+                        str(tmp_path)], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:], file=sys.stderr)
+    assert r.returncode == 0 and "ALL PASS" in r.stdout
+    codes = np.fromfile(tmp_path / "codes.bin", np.int32).reshape(-1, 16)
+    stream = np.fromfile(tmp_path / "stream.bin", np.float32)
+    bounds = np.fromfile(tmp_path / "bounds.bin", np.int32)
+    whole = np.fromfile(tmp_path / "whole.bin", np.float32)
+    n = codes.shape[0]
+    assert n > chunk and bounds[-1] == n
+    assert stream.size == whole.size == vc.samples_for_frames(n)
+    o = orc.VocOracle(vc, vw, threads=8)
+    at, start = 0, 0
+    for end in bounds:
+        ref = o.decode_window(codes, start, int(end), context)
+        got = stream[at:at + ref.size]
+        snr = 10 * np.log10((ref.astype(np.float64) ** 2).mean() / max(((got - ref) ** 2).mean(), 1e-30))
+        assert snr >= 30.0, (start, end, snr)
+        at += ref.size
+        start = int(end)
+    assert at == stream.size
