@@ -273,3 +273,42 @@ def test_config3_q8_frame_loop_256_greedy(path):
         dev.close()
     say(f"[gpu] config 3: frames oracle={co.shape[0]} device={cg.shape[0]}")
     assert cg.shape == co.shape and np.array_equal(cg, co)
+
+
+def test_icl_long_reference_q8(path):
+    """generate_icl's layout at the 0.6B shapes with a long reference clip:
+    200 reference codec frames and 30 reference text ids make a 210-row
+    prefill (the tiled int8 MFMA prefill), built on the device
+    (q3t_dev_build_prefill_icl) equal to the oracle's rows, then 24 greedy
+    frames with repetition-loop detection on (generate_icl's default)."""
+    from test_gpu_facade import icl_rows
+    cfg = qcfg.full_06b()
+    rng = np.random.default_rng(77)
+    text = rng.integers(0, 151936, 40).astype(np.int32)
+    ref_text = rng.integers(0, 151936, 30).astype(np.int32)
+    ref_codes = np.concatenate([rng.integers(0, 2048, (200, 1)), rng.integers(0, 2048, (200, 15))],
+                               axis=1).astype(np.int32)
+    spk = rng.standard_normal(1024).astype(np.float32)
+    key = "icl200"
+    w = weights("q8_0", 3)
+    if key not in _oracle_runs:
+        o = orc.Oracle(cfg, w, threads=THREADS)
+        rows = icl_rows(o, cfg, text, ref_text, ref_codes, spk)
+        say(f"[gpu] icl: oracle prefill {rows[0].shape[0]} rows + 24 frames")
+        codes = o.generate_rows(*rows, max_len=24, temperature=0.0, top_k=0, rep_loop_detect=True)
+        _oracle_runs[key] = (rows, codes)
+        o.close()
+    (pre_o, trail_o, pad_o), co = _oracle_runs[key]
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w)
+        pre, trail, pad = dev.build_prefill_icl(text, ref_text, ref_codes, spk)
+        assert pre.shape == pre_o.shape and pre.shape[0] >= 200
+        assert np.array_equal(pre, pre_o) and np.array_equal(trail, trail_o) and np.array_equal(pad, pad_o)
+        say(f"[gpu] icl: device prefill {pre.shape[0]} rows + 24 frames ({path})")
+        cg = driver.generate(dev, cfg, None, None, max_len=24, temperature=0.0, top_k=0, rep_loop_detect=True,
+                             prefill_rows=(pre, trail, pad))
+        check_path(dev, path, "q8_0")
+    finally:
+        dev.close()
+    assert cg.shape == co.shape and np.array_equal(cg, co)
