@@ -1358,11 +1358,32 @@ int ensure_pf(q3t_dev * c, int n) {
 
 void pf_gemm(q3t_dev * c, const Slot & w, int N, int K, int n, float * y, const float * res, int rs = -1,
              const int8_t * q = nullptr, const float * dx = nullptr) {
-    const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
-    hipLaunchKernelGGL(pf::k_gemm_q8, grid, dim3(kBlock), pf::gemm_lds_bytes(K), c->stream, (const int8_t *) w.data,
-                       (const uint16_t *) w.scales, N, K, q ? q : (const int8_t *) c->pf_q,
-                       dx ? dx : (const float *) c->pf_dx, n, y, N, res, rs < 0 ? N : rs,
-                       res ? (int) EPI_RESID : (int) EPI_STORE);
+    // tile: 64 weight rows x 32 JT tokens, JT = 2 unless that leaves the launch
+    // with fewer workgroups than CUs; two Q8_0 blocks per stage
+    int IR = 2, JT = 2, GB = 2;
+    while (JT > 1 && (int64_t) (N / (32 * IR)) * ((n + 32 * JT - 1) / (32 * JT)) < c->n_cu) JT >>= 1;
+    if (const char * e = std::getenv("Q3T_PF_TILE")) {      // "<IR>x<JT>x<GB>"
+        const int ir = e[0] - '0', jt = e[1] == 'x' ? e[2] - '0' : 0, gb = e[1] == 'x' && e[3] == 'x' ? e[4] - '0' : 2;
+        if ((ir == 2 || (ir == 4 && N % 128 == 0 && gb == 2)) && (jt == 1 || jt == 2 || jt == 4) &&
+            (gb == 2 || gb == 4) && (K / kQK) % gb == 0) { IR = ir; JT = jt; GB = gb; }
+    }
+    const dim3 grid(N / (32 * IR), (n + 32 * JT - 1) / (32 * JT));
+    const int8_t * qq = q ? q : (const int8_t *) c->pf_q;
+    const float * dd = dx ? dx : (const float *) c->pf_dx;
+    const int epi = res ? (int) EPI_RESID : (int) EPI_STORE;
+    const int r = rs < 0 ? N : rs;
+#define Q3T_PF_GEMM(ir, jt, gb)                                                                                  \
+    hipLaunchKernelGGL((pf::k_gemm_q8<ir, jt, gb>), grid, dim3(kBlock), 0, c->stream, (const int8_t *) w.data, \
+                       (const uint16_t *) w.scales, N, K, qq, dd, n, y, N, res, r, epi)
+#define Q3T_PF_GEMM_JT(ir, gb)                                                                                   \
+    if (JT == 4) Q3T_PF_GEMM(ir, 4, gb); else if (JT == 2) Q3T_PF_GEMM(ir, 2, gb); else Q3T_PF_GEMM(ir, 1, gb)
+    if (GB == 4) {
+        Q3T_PF_GEMM_JT(2, 4);
+    } else {
+        if (IR == 4) { Q3T_PF_GEMM_JT(4, 2); } else { Q3T_PF_GEMM_JT(2, 2); }
+    }
+#undef Q3T_PF_GEMM_JT
+#undef Q3T_PF_GEMM
 }
 
 void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w, int xs = -1, int8_t * q = nullptr,

@@ -63,98 +63,165 @@ __global__ __launch_bounds__(kBlock) void k_quant_rows(const float * __restrict_
     }
 }
 
-constexpr int kTile = 64;       // output rows and tokens per workgroup
-constexpr int kU = 4;           // Q8_0 blocks loaded ahead per step
-
 // Y[t][r] = epi(sum_b fp16(dw[r][b]) * dx[t][b] * sum_k W[r][32b+k] Q[t][32b+k])
-// for a 64-row x 64-token tile.  Wave (wr, wt) = (wave & 1, wave >> 1) owns
-// rows wr*32.. and tokens wt*32.. as 2 x 2 MFMA tiles of 16 x 16.  MFMA lane
-// layout (16x16x32 i8): A[m = l%16][k = 8(l/16)..+7], B[k = 8(l/16)..+7][n =
-// l%16], D[m = 4(l/16)+i][n = l%16].  epi: EPI_STORE or EPI_RESID (res [n][rs]).
-// Requires N % 64 == 0 and K % 128 == 0 (the host checks).
+// on a (32 IR rows) x (32 JT tokens) tile per workgroup: wave (wr, wt) =
+// (wave & 1, wave >> 1) owns IR x JT MFMA tiles of 16 x 16.  Each stage holds
+// kGB Q8_0 blocks of the tile's weight and activation rows in LDS (rows padded
+// by 8 bytes against bank conflicts) with their scales, double-buffered: the
+// next stage's global loads are in flight during this stage's MFMAs.  MFMA
+// lane layout (16x16x32 i8): A[m = l%16][k = 8(l/16)..+7], B[k][n = l%16],
+// D[m = 4(l/16)+i][n = l%16]; each block's exact int32 sums take the fp16 x
+// fp16 scale product (exact in fp32) in an fp64 fma, so the fp64 sum of exact
+// terms is rounded to fp32 once.  epi: EPI_STORE or EPI_RESID (res [n][rs],
+// rs = 0 broadcasts one row).  Requires N % (32 IR) == 0, K % (32 kGB) == 0.
+template <int IR, int JT, int GB>
+struct Q8Tile {
+    static constexpr int TN = 32 * IR, TM = 32 * JT;
+    static constexpr int ROWB = GB * kQK + 8;          // bytes per staged row (padded against bank conflicts)
+    static constexpr int A_BYTES = TN * ROWB, B_BYTES = TM * ROWB;
+    static constexpr int STAGE = A_BYTES + B_BYTES + (TN + TM) * GB * 4;
+    static constexpr int LDS = 2 * STAGE;
+};
+
+template <int IR, int JT, int kGB>
 __global__ __launch_bounds__(kBlock) void k_gemm_q8(const int8_t * __restrict__ W, const uint16_t * __restrict__ Wd,
                                                     int32_t N, int32_t K, const int8_t * __restrict__ Q,
                                                     const float * __restrict__ dx, int32_t n, float * __restrict__ Y,
                                                     int32_t ys, const float * __restrict__ res, int32_t rs, int32_t epi) {
-    extern __shared__ __align__(16) char smem[];
-    const int BPR = K / kQK;
-    float * sdw = (float *) smem;                  // [64 rows][BPR] weight scales
-    float * sdx = sdw + kTile * BPR;               // [64 tokens][BPR] activation scales
-    const int r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wr = wave & 1, wt = wave >> 1;
-    for (int i = t; i < kTile * BPR; i += kBlock) {
-        const int rr = i / BPR, b = i - rr * BPR;
-        sdw[i] = h2f(Wd[(size_t) (r0 + rr) * BPR + b]);
-        const int tok = t0 + rr;
-        sdx[i] = tok < n ? dx[(size_t) tok * BPR + b] : 0.0f;
-    }
-    __syncthreads();
+    using T = Q8Tile<IR, JT, kGB>;
+    constexpr int kRowB = T::ROWB;
+    __shared__ __align__(16) char smem[T::LDS];
+    const int BPR = K / kQK, S = BPR / kGB;
+    const int r0 = blockIdx.x * T::TN, t0 = blockIdx.y * T::TM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wr = wave & 1, wt = wave >> 1;
     const int lm = lane & 15, lk = lane >> 4;
-    const int8_t * wrow[2];
-    const int8_t * qrow[2];
-    bool qok[2];
+    // staging: 16-byte chunks, kGB * 2 per row (A then B rows), scale pairs
+    constexpr int CPR = kGB * kQK / 16;                  // chunks per row
+    constexpr int NA = (T::TN * CPR + kBlock - 1) / kBlock, NB = (T::TM * CPR + kBlock - 1) / kBlock;
+    int4 ra[NA], rb[NB];
+    float sw[kGB], sx[kGB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        wrow[i] = W + (size_t) (r0 + wr * 32 + i * 16 + lm) * K + 8 * lk;
-        const int tok = t0 + wt * 32 + i * 16 + lm;
-        qok[i] = tok < n;
-        qrow[i] = Q + (size_t) (qok[i] ? tok : 0) * K + 8 * lk;
-    }
-    double acc[2][2][4];
+    for (int g = 0; g < kGB; ++g) { sw[g] = 0.f; sx[g] = 0.f; }
+    auto fetch = [&](int st) {
+        const int kb = st * kGB;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NA; ++i) {
+            const int c = tid + i * kBlock, row = c / CPR, col = c - row * CPR;
+            ra[i] = c < T::TN * CPR ? *(const int4 *) (W + (size_t) (r0 + row) * K + kb * kQK + col * 16) : make_int4(0, 0, 0, 0);
+        }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int i = 0; i < NB; ++i) {
+            const int c = tid + i * kBlock, row = c / CPR, col = c - row * CPR;
+            const int tok = t0 + row;
+            rb[i] = (c < T::TM * CPR && tok < n) ? *(const int4 *) (Q + (size_t) tok * K + kb * kQK + col * 16)
+                                                 : make_int4(0, 0, 0, 0);
+        }
+        if (tid < T::TN) {
+            const uint16_t * p = Wd + (size_t) (r0 + tid) * BPR + kb;
+#pragma unroll
+            for (int g = 0; g < kGB; ++g) sw[g] = h2f(p[g]);
+        }
+        if (tid < T::TM) {
+            const int tok = t0 + tid;
+#pragma unroll
+            for (int g = 0; g < kGB; ++g) sx[g] = tok < n ? dx[(size_t) tok * BPR + kb + g] : 0.f;
+        }
+    };
+    auto stash = [&](int buf) {
+        char * st = smem + buf * T::STAGE;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int c = tid + i * kBlock, row = c / CPR, col = c - row * CPR;
+            if (c < T::TN * CPR) {
+                long * d = (long *) (st + row * kRowB + col * 16);   // 8-byte aligned rows
+                d[0] = ((const long *) &ra[i])[0];
+                d[1] = ((const long *) &ra[i])[1];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int c = tid + i * kBlock, row = c / CPR, col = c - row * CPR;
+            if (c < T::TM * CPR) {
+                long * d = (long *) (st + T::A_BYTES + row * kRowB + col * 16);
+                d[0] = ((const long *) &rb[i])[0];
+                d[1] = ((const long *) &rb[i])[1];
+            }
+        }
+        float * sdw = (float *) (st + T::A_BYTES + T::B_BYTES);   // [kGB][TN]
+        float * sdx = sdw + kGB * T::TN;                          // [kGB][TM]
+#pragma unroll
+        for (int g = 0; g < kGB; ++g) {
+            if (tid < T::TN) sdw[g * T::TN + tid] = sw[g];
+            if (tid < T::TM) sdx[g * T::TM + tid] = sx[g];
+        }
+    };
+
+    double acc[IR][JT][4];
+#pragma unroll
+    for (int i = 0; i < IR; ++i)
+#pragma unroll
+        for (int j = 0; j < JT; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0;
     const v4i zero = {0, 0, 0, 0};
-    for (int b0 = 0; b0 < BPR; b0 += kU) {
-        long a[kU][2], bq[kU][2];
+
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int st = 0; st < S; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < S) fetch(st + 1);
+        const char * sb = smem + buf * T::STAGE;
+        const float * sdw = (const float *) (sb + T::A_BYTES + T::B_BYTES);
+        const float * sdx = sdw + kGB * T::TN;
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
+        for (int kb = 0; kb < kGB; ++kb) {
+            long bq[JT];
+            float dxv[JT];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const bool in = b0 + u < BPR;   // K % (32 kU) may leave a short last step
-                a[u][i] = in ? *(const long *) (wrow[i] + (b0 + u) * kQK) : 0L;
-                bq[u][i] = in && qok[i] ? *(const long *) (qrow[i] + (b0 + u) * kQK) : 0L;
+            for (int j = 0; j < JT; ++j) {
+                const int tl = wt * JT * 16 + j * 16 + lm;
+                bq[j] = *(const long *) (sb + T::A_BYTES + tl * kRowB + kb * kQK + 8 * lk);
+                dxv[j] = sdx[kb * T::TM + tl];
             }
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int b = b0 + u;
-            if (b >= BPR) break;               // uniform
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < IR; ++i) {
+                const int rl = wr * IR * 16 + i * 16;
+                const long a = *(const long *) (sb + (rl + lm) * kRowB + kb * kQK + 8 * lk);
                 float dwv[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dwv[e] = sdw[(wr * 32 + i * 16 + 4 * lk + e) * BPR + b];
+                for (int e = 0; e < 4; ++e) dwv[e] = sdw[kb * T::TN + rl + 4 * lk + e];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u][i], bq[u][j], zero, 0, 0, 0);
-                    const float dxv = sdx[(wt * 32 + j * 16 + lm) * BPR + b];
+                for (int j = 0; j < JT; ++j) {
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[j], zero, 0, 0, 0);
                     // fp16 x fp16 scale product exact in fp32; times the int32 block sum exact in fp64
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fma((double) (dwv[e] * dxv), (double) d[e], acc[i][j][e]);
+                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fma((double) (dwv[e] * dxv[j]), (double) d[e], acc[i][j][e]);
                 }
             }
         }
+        if (st + 1 < S) stash(buf ^ 1);
+        __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < JT; ++j) {
+        const int tok = t0 + wt * JT * 16 + j * 16 + lm;
+        if (tok >= n) continue;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int tok = t0 + wt * 32 + j * 16 + lm;
-            if (tok >= n) continue;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + wr * 32 + i * 16 + 4 * lk + e;
-                float v = (float) acc[i][j][e];
-                if (epi == EPI_RESID) v = v + res[(size_t) tok * rs + r];
-                Y[(size_t) tok * ys + r] = v;
+        for (int i = 0; i < IR; ++i) {
+            const int r = r0 + wr * IR * 16 + i * 16 + 4 * lk;
+            float4 v = make_float4((float) acc[i][j][0], (float) acc[i][j][1], (float) acc[i][j][2], (float) acc[i][j][3]);
+            if (epi == EPI_RESID) {
+                const float * rr = res + (size_t) tok * rs + r;
+                v.x = v.x + rr[0]; v.y = v.y + rr[1]; v.z = v.z + rr[2]; v.w = v.w + rr[3];
             }
+            *(float4 *) (Y + (size_t) tok * ys + r) = v;
         }
+    }
 }
 
-__host__ __device__ constexpr size_t gemm_lds_bytes(int K) { return (size_t) 2 * kTile * (K / kQK) * sizeof(float); }
+
+constexpr int kTile = 64;         // output rows and tokens per workgroup of the F16 GEMM
 
 // F16 weights: Y[t][r] = epi(sum_k W[r][k] * x[t][k]) with x rounded to fp16
 // (WIDE = false, the F16-weight contract) or kept fp32 (WIDE = true, the
