@@ -43,6 +43,8 @@ def frame_bytes(cfg, w, n_kv, cp_table=False):
     cp_layers = sum(nbytes(n) for n in w if n.startswith("code_pred.blk."))
     cp = 15 * (cp_layers + nbytes("code_pred.output_norm.weight")) + sum(
         nbytes(f"code_pred.lm_head.{g}.weight") for g in range(15))
+    if "code_pred.mtp_proj.weight" in w:      # the 1.7B layout: each pass projects its input rows
+        cp += 15 * (nbytes("code_pred.mtp_proj.weight") + nbytes("code_pred.mtp_proj.bias"))
     if cp_table:
         qkv0 = sum(nbytes(f"code_pred.blk.0.attn_{x}.weight") for x in "qkv") + nbytes("code_pred.blk.0.attn_norm.weight")
         qkvd = (cfg.n_head + 2 * cfg.n_kv_head) * cfg.head_dim
@@ -458,6 +460,8 @@ def main():
                     help="instead of the short-prompt greedy loop, time long-context sampled decode after a long prefill")
     ap.add_argument("--long-prompt", type=int, default=2048, help="text ids of the --long prefill")
     ap.add_argument("--temperature", type=float, default=0.9, help="--long sampling temperature (0: greedy)")
+    ap.add_argument("--model", default="0.6b", choices=["0.6b", "1.7b"],
+                    help="frame-loop shapes: the 0.6B model (the headline) or the 1.7B layout (code_pred.mtp_proj)")
     ap.add_argument("--vocoder", action="store_true",
                     help="time the streaming vocoder's decode_window (48 context + 25 new frames)")
     ap.add_argument("--voc-context", type=int, default=48)
@@ -479,7 +483,7 @@ def main():
 
     if args.vocoder:
         return vocoder_bench(args)
-    cfg = config.full_06b()
+    cfg = config.full_17b() if args.model == "1.7b" else config.full_06b()
     w = Weights(cfg, args.weights, seed=2024)
     if args.prefill > 0:
         return prefill_bench(args, cfg, w)
@@ -538,7 +542,7 @@ def main():
         # HBM-side bytes per k_frame dispatch from the FETCH_SIZE / WRITE_SIZE
         # counter runs (calibrated on a 64 MiB copy kernel), when committed
         tp = os.path.join(ROOT, "profiles", "k_frame_q8_0_06b_traffic.json")
-        if args.weights == "q8_0" and os.path.exists(tp):
+        if args.weights == "q8_0" and args.model == "0.6b" and os.path.exists(tp):
             with open(tp) as f:
                 traffic = json.load(f)["traffic_bytes_per_dispatch"]
         # the whole frame is one kernel: its roofline is the frame's algorithmic bytes over its duration
@@ -566,7 +570,7 @@ def main():
                        "sample": f"as cpu_baseline with {nall} threads, {n_all} frames; {host}"}
 
     config1 = None
-    if args.config1:
+    if args.config1 and args.model == "0.6b":
         config1 = config1_leg(args, cfg, Device, driver, Weights)
 
     out = {
@@ -582,7 +586,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8" if args.weights == "q8_0" else "f16",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
-        "config": {"workload": f"full frame loop, {args.weights.upper()} 0.6B shapes, {args.prompt}-token prompt, "
+        "config": {"workload": f"full frame loop, {args.weights.upper()} {args.model.upper()} shapes, {args.prompt}-token prompt, "
                                f"greedy, " + ("one persistent kernel per frame" + (", XCD-parallel layers" if path == 3 else "") if path in (1, 3) else "hipGraph per frame"),
                    "global_batch": 1, "frames": args.steps,
                    "weights": args.weights, "prompt_tokens": args.prompt, "prefill_rows": plen},

@@ -647,26 +647,31 @@ __global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, i
 
 // Decides whether the persistent frame kernel can run this context and
 // prepares its tables.  Falls back to the multi-kernel graph otherwise.
-// The kernel is instantiated for fixed (hidden, query width, FFN width) and
-// layer weight type: variant 1 / 3 = (1024, 2048, 3072), the 0.6B talker and
-// code predictor, Q8_0 / F16 layers; variant 2 / 4 = (256, 512, 512), the
-// small test shapes.
+// The kernel is instantiated for fixed (talker width, code-predictor width,
+// query width, talker FFN, code-predictor FFN) and layer weight type:
+// variant 1 / 3 = (1024, 1024, 2048, 3072, 3072), the 0.6B talker and code
+// predictor, Q8_0 / F16 layers; variant 2 / 4 = (256, 256, 512, 512, 512), the
+// small test shapes; 5 = the 0.6B Q8_0 shapes on the XCD-parallel layer
+// program; 6 = the 1.7B layout (2048, 1024, 2048, 6144, 3072) with
+// code_pred.mtp_proj, Q8_0; 7 = its small test form (512, 256, 512, 512, 512).
 const void * fk_kernel(int variant) {
     switch (variant) {
-        case 1: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8, false>;
-        case 2: return (const void *) fk::k_frame<256, 512, 512, W_Q8, false>;
-        case 3: return (const void *) fk::k_frame<1024, 2048, 3072, W_F16, false>;
-        case 5: return (const void *) fk::k_frame<1024, 2048, 3072, W_Q8, true>;
-        default: return (const void *) fk::k_frame<256, 512, 512, W_F16, false>;
+        case 1: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_Q8, false>;
+        case 2: return (const void *) fk::k_frame<256, 256, 512, 512, 512, W_Q8, false>;
+        case 3: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_F16, false>;
+        case 5: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_Q8, true>;
+        case 6: return (const void *) fk::k_frame<2048, 1024, 2048, 6144, 3072, W_Q8, false>;
+        case 7: return (const void *) fk::k_frame<512, 256, 512, 512, 512, W_Q8, false>;
+        default: return (const void *) fk::k_frame<256, 256, 512, 512, 512, W_F16, false>;
     }
 }
 
+// Q8_0 block slots per lane of the frame kernel's GEMV geometry (Geo<K>):
+// up to 32 blocks, a power of two, in one slot; wider rows in slots of 32.
 int slots_for(int K) {
     const int b = K / kQK;
-    if (b <= 32 && (b & (b - 1)) == 0) return 1;
-    if (b == 64) return 2;
-    if (b == 96) return 3;
-    return 0;
+    if (b <= 32) return (b & (b - 1)) == 0 ? 1 : 0;
+    return b % 32 == 0 ? b / 32 : 0;
 }
 
 // The XCD of each workgroup of a 256-workgroup cooperative launch with the
@@ -725,14 +730,21 @@ int fk_prepare(q3t_dev * c) {
     if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int dc = g.cp_hidden;
     const int sq = slots_for(g.hidden_size), so = slots_for(qd), sd = slots_for(g.ffn_size);
+    const int sqc = slots_for(dc), sdc = slots_for(g.cp_ffn);
+    const bool mtp = dc != g.hidden_size;
     int variant = 0;
-    if (g.hidden_size == 1024 && qd == 2048 && g.ffn_size == 3072) variant = 1;
-    if (g.hidden_size == 256 && qd == 512 && g.ffn_size == 512) variant = 2;
-    if (!variant || g.ffn_size != g.cp_ffn || g.cp_hidden != g.hidden_size || g.n_head != 2 * g.n_kv_head ||
+    if (!mtp && g.hidden_size == 1024 && qd == 2048 && g.ffn_size == 3072 && g.cp_ffn == 3072) variant = 1;
+    if (!mtp && g.hidden_size == 256 && qd == 512 && g.ffn_size == 512 && g.cp_ffn == 512) variant = 2;
+    if (mtp && g.hidden_size == 2048 && dc == 1024 && qd == 2048 && g.ffn_size == 6144 && g.cp_ffn == 3072) variant = 6;
+    if (mtp && g.hidden_size == 512 && dc == 256 && qd == 512 && g.ffn_size == 512 && g.cp_ffn == 512) variant = 7;
+    if (!variant || g.n_head != 2 * g.n_kv_head ||
         g.head_dim != 128 || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
         g.cp_vocab > 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 || qkvd > fk::kHS)
         return 0;
+    // the 1.7B layout runs Q8_0 models only (an F16 one takes the multi-kernel frame)
+    if (mtp && (c->mtp_w.type != Q3T_TYPE_Q8_0 || !c->mtp_b.data)) return 0;
     // every layer matrix Q8_0, or every one F16
     const int lt = c->talker[0].qkv.type;
     if (lt != Q3T_TYPE_Q8_0 && lt != Q3T_TYPE_F16) return 0;
@@ -740,20 +752,36 @@ int fk_prepare(q3t_dev * c) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
         if (L.qkv.type != lt || L.wo.type != lt || L.wg.type != lt || L.wu.type != lt || L.wd.type != lt) return 0;
     }
-    if (lt == Q3T_TYPE_F16) variant += 2;
+    if (lt == Q3T_TYPE_F16) {
+        if (mtp) return 0;
+        variant += 2;
+    }
     // one workgroup per CU (the LDS footprint allows no more), all co-resident
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fk_kernel(variant), fk::kT, 0));
     const int grid = std::min(256, per_cu * c->n_cu);
     if (grid < 1) return 0;
     const int nw = grid * fk::kW;
-    auto fits = [&](int rows, int K, int slots) {
+    // row groups per wave: 2, or 3 for a gate/up whose rows need it on 1024
+    // waves (the kernel's Q8Regs<.., NGU>)
+    auto fits = [&](int rows, int K, int slots, int ng = 2) {
+        if (slots <= 0) return false;
         const int rpw = 64 / ((K / kQK) / slots);
-        return rows % rpw == 0 && rows / rpw <= 2 * nw;
+        return rows % rpw == 0 && rows / rpw <= ng * nw;
     };
-    if (!fits(qkvd, g.hidden_size, sq) || !fits(g.ffn_size, g.hidden_size, sq) || !fits(g.hidden_size, qd, so) ||
-        !fits(g.hidden_size, g.ffn_size, sd) || !fits(g.codec_vocab, g.hidden_size, 1) ||
-        !fits(g.cp_vocab, g.hidden_size, 1) || g.n_kv_head > grid)
+    auto ngu = [&](int ffn, int K, int slots) {
+        const int rpw = 64 / ((K / kQK) / slots);
+        return (ffn / rpw + 1023) / 1024 > 2 ? 3 : 2;
+    };
+    auto head_fits = [&](int rows, int K) {
+        const int lpr = std::min(K / kQK, 32);
+        return (K / kQK) % lpr == 0 && (K / kQK) / lpr <= 2 && rows % (64 / lpr) == 0 && rows / (64 / lpr) <= 2 * nw;
+    };
+    if (!fits(qkvd, g.hidden_size, sq) || !fits(g.ffn_size, g.hidden_size, sq, ngu(g.ffn_size, g.hidden_size, sq)) ||
+        !fits(g.hidden_size, qd, so) || !fits(g.hidden_size, g.ffn_size, sd) || !head_fits(g.codec_vocab, g.hidden_size) ||
+        !fits(qkvd, dc, sqc) || !fits(g.cp_ffn, dc, sqc, ngu(g.cp_ffn, dc, sqc)) || !fits(dc, qd, so) ||
+        !fits(dc, g.cp_ffn, sdc) || !head_fits(g.cp_vocab, dc) || (mtp && !fits(dc, g.hidden_size, sq)) ||
+        g.n_kv_head > grid)
         return 0;
     // talker attention: grid / n_kv_head position chunks per KV head, each
     // chunk's scores in LDS; phase C's partials fill kPvSlots slots
@@ -776,7 +804,7 @@ int fk_prepare(q3t_dev * c) {
     // (talker); XCD-parallel layer 15 or 17 + kPvSlots (device-wide partial
     // sums take 4 slots, XCD-local rows 2)
     const int phases = xcd ? 15 * (2 + 15 * g.cp_layers) + 1 + (17 + fk::kPvSlots) * g.n_layers
-                           : 15 * (2 + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
+                           : 15 * (2 + (mtp ? 1 : 0) + 5 * g.cp_layers) + 1 + (7 + fk::kPvSlots) * g.n_layers;
     if (phases >= 4096) return 0;
     if (!c->fk_layers || c->fk_layers_stale) {
         std::vector<fk::LayerQ8> t(g.n_layers + g.cp_layers);
@@ -833,6 +861,11 @@ fk::Args fk_args(q3t_dev * c) {
     A.cand_idx = (int32_t *) (c->fk_cand + 256);
     A.step_in = c->stage;
     A.cp_qkv0 = c->fk_tab ? c->cp_tab : nullptr;
+    if (g.cp_hidden != g.hidden_size) {
+        A.mtp_w = (const int8_t *) c->mtp_w.data;
+        A.mtp_d = c->mtp_w.scales;
+        A.mtp_b = (const float *) c->mtp_b.data;
+    }
     return A;
 }
 
@@ -1847,8 +1880,10 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
     if (ran) {
         if (logits_out) {
             // arena slots of one code-predictor pass (the input row, the
-            // layers, the head): the head's logits sit in its last slot
-            const int stride = 2 + (c->fk_variant == 5 ? 15 : 5) * g.cp_layers, n = g.n_codebooks - 1;
+            // mtp_proj output in the 1.7B layout, the layers, the head): the
+            // head's logits sit in its last slot
+            const int mtp = g.cp_hidden != g.hidden_size ? 1 : 0;
+            const int stride = 2 + mtp + (c->fk_variant == 5 ? 15 : 5) * g.cp_layers, n = g.n_codebooks - 1;
             hipLaunchKernelGGL(k_untag_heads, dim3((n * g.cp_vocab + 255) / 256), dim3(256), 0, c->stream,
                                c->fk_arena, stride - 1, stride, n, g.cp_vocab, c->cp_logits);
         }

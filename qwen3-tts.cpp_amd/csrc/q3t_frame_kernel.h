@@ -76,6 +76,8 @@ struct Args {
     // XCD-parallel program: code-predictor layer 0's QKV rows of every
     // (codebook step s, code), [15][cp_vocab][4096] (null: computed)
     const float * cp_qkv0;
+    // 1.7B layout: code_pred.mtp_proj (talker width -> code-predictor width) and its bias
+    const int8_t * mtp_w; const uint16_t * mtp_d; const float * mtp_b;
 };
 
 // What one launch runs: a whole frame, or one of its two halves alone (the
@@ -111,11 +113,11 @@ template <int K>
 using NormT = float[kChg<K>][4];
 
 struct Lds {
-    alignas(16) float x[3072];                  // gathered layer-0 rows [nt][D] / sampler logits
+    alignas(16) float x[4096];                  // gathered layer-0 rows [nt][D] / sampler logits
     alignas(16) int8_t qlo[2 * kMaxBlk * 16];   // Q8 input: bytes 0..15 of block b of token t at (t*BPR+b)*16
     alignas(16) int8_t qhi[2 * kMaxBlk * 16];   // bytes 16..31
     float qdx[2 * kMaxBlk];                     // fp16-rounded block scales
-    alignas(16) uint16_t hq[4][32 * 8];         // F16 head input: halves 8c..8c+7 of block b at hq[c][b*8]
+    alignas(16) uint16_t hq[4][64 * 8];         // F16 head input: halves 8c..8c+7 of block b at hq[c][b*8]
     float a[2 * 4 * 128];                       // attention: q (2 tok x 2 heads), new k, new v rows
     union {                                     // attention and F16 GEMV inputs are never live together
         alignas(16) float sc[2 * kMaxCtx];      // attention scores / probabilities, 2 heads; P.V partials
@@ -405,14 +407,15 @@ __device__ __forceinline__ void quant_rows(const RowsT<NT, K> & v, Lds & L) {
 
 // ------------------------------------------------------------------- GEMV
 // Row groups of a GEMV are dealt to the grid's waves: wave gw takes groups
-// gw and gw + nwaves (at most two per wave; the host checks).
-template <int K, bool DUAL>
+// gw, gw + nwaves, ... (at most NG per wave; the host checks).  NG = 3 only
+// for the 1.7B talker's 6144-row gate/up.
+template <int K, bool DUAL, int NG = 2>
 struct Q8Regs {
     static constexpr int S = Geo<K>::SLOTS;
-    int4 w[2][S][2], u[2][S][2];
-    uint16_t dw[2][S], du[2][S];   // fp16 block scales, converted at use so the prefetch never waits
-    uint64_t res[2][2];   // residual elements (tagged) read early by the storing lanes
-    int ng;               // groups this wave owns (0..2)
+    int4 w[NG][S][2], u[NG][S][2];
+    uint16_t dw[NG][S], du[NG][S];   // fp16 block scales, converted at use so the prefetch never waits
+    uint64_t res[NG][2];  // residual elements (tagged) read early by the storing lanes
+    int ng;               // groups this wave owns (0..NG)
 };
 
 // Row-group owner of wave gw when a phase's groups start at wave `rot`
@@ -423,8 +426,8 @@ __device__ __forceinline__ int rot_wave(int rot) {
     return gw >= nw ? gw - nw : gw;
 }
 
-template <int K, bool DUAL, bool NTL>
-__device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * W, const uint16_t * Wd,
+template <int K, bool DUAL, bool NTL, int NG = 2>
+__device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL, NG> & R, const int8_t * W, const uint16_t * Wd,
                                             const int8_t * U, const uint16_t * Ud, int rows, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
@@ -432,7 +435,7 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * 
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
     R.ng = 0;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         const int g = gw + gi * nw;
         if (g >= groups) break;
         R.ng = gi + 1;
@@ -454,14 +457,14 @@ __device__ __forceinline__ void q8_prefetch(Q8Regs<K, DUAL> & R, const int8_t * 
 
 // Issues the residual loads of the rows this lane will store (EPI_RESID),
 // before the phase input is awaited; q8_compute re-polls any not yet tagged.
-template <int NT, int K, bool DUAL>
-__device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL> & R, const uint64_t * res, int rot) {
+template <int NT, int K, bool DUAL, int NG = 2>
+__device__ __forceinline__ void res_prefetch(Q8Regs<K, DUAL, NG> & R, const uint64_t * res, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
     if (lir != 0) return;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         if (gi >= R.ng) break;
         const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
@@ -481,25 +484,26 @@ __device__ __forceinline__ bool wg_has_rows(int rows, int rot) {
 }
 
 // Q8_0 GEMV over the quantised LDS input, epilogue, tagged stores into
-// out [NT][kHS].  res: residual slot (tagged) for EPI_RESID.
-template <int NT, int K, bool DUAL>
-__device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
+// out [NT][kHS].  res: residual slot (tagged) for EPI_RESID; bias: fp32 per
+// row for EPI_BIAS.
+template <int NT, int K, bool DUAL, int NG = 2>
+__device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL, NG> & R, const Lds & L, int epi, const uint64_t * res,
                                            uint32_t res_tag, uint64_t * out, uint32_t out_tag, int rot, bool & dead,
-                                           int32_t * err) {
+                                           int32_t * err, const float * bias = nullptr) {
     using G = Geo<K>;
     if (R.ng == 0) return;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
-    double acc[2][NT], acc2[2][NT];
+    double acc[NG][NT], acc2[NG][NT];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
+    for (int gi = 0; gi < NG; ++gi)
 #pragma unroll
         for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
     // the scales enter here: the empty asm keeps their conversion (and the
     // wait for their loads) from being hoisted into the prefetch
-    float sw[2][G::SLOTS], su[2][G::SLOTS];
+    float sw[NG][G::SLOTS], su[NG][G::SLOTS];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
+    for (int gi = 0; gi < NG; ++gi)
 #pragma unroll
         for (int s = 0; s < G::SLOTS; ++s) {
             uint32_t a = R.dw[gi][s], c = DUAL ? R.du[gi][s] : 0u;
@@ -516,7 +520,7 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
             const int4 x1 = *(const int4 *) &L.qhi[(t * G::BPR + b) * 16];
             const float dx = L.qdx[t * G::BPR + b];
 #pragma unroll
-            for (int gi = 0; gi < 2; ++gi) {
+            for (int gi = 0; gi < NG; ++gi) {
                 if (gi >= R.ng) break;
                 // d_w * d_x (two fp16 values) is exact in fp32 and its product with
                 // the int32 block sum exact in fp64: fma rounds like mul + add
@@ -529,7 +533,7 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
         }
     }
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         if (gi >= R.ng) break;
         const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
@@ -545,6 +549,8 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL> & R, const Lds 
                                                           : twait(res + (size_t) t * kHS + r, res_tag, dead, err));
             } else if (epi == EPI_SWIGLU) {
                 o = silu_q3t(v) * (float) a2;
+            } else if (epi == EPI_BIAS) {
+                o = v + gld(bias + r);
             } else {
                 o = v;
             }
@@ -781,17 +787,26 @@ struct Cb0Xf {
 // transforms when xf != nullptr), tagged at cand_tagged[2b], [2b+1] or plain
 // in cand_val[b] / cand_idx[b] (neither when both are null).  All threads of
 // the workgroup must call it.
+// Head geometry: a row is split over LPR lanes holding HS blocks each
+// (HS = 2 for the 1.7B talker's 2048-wide rows).
+template <int K>
+struct HeadGeo {
+    static constexpr int BPR = K / kQK;
+    static constexpr int LPR = BPR > 32 ? 32 : BPR, HS = BPR / LPR, RPW = 64 / LPR;
+    static_assert((LPR & (LPR - 1)) == 0 && BPR % LPR == 0 && HS <= 2, "head width");
+};
+
 struct HeadRegs {
-    int4 w[2][4];
+    int4 w[2][2][4];      // [row group][block slot][16-byte chunk]
     int ng;
 };
 
 // The head rows' weights of this lane, loaded before the head input is awaited.
 template <int K, bool NTL>
 __device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, HeadRegs & H) {
-    constexpr int LPR = K / kQK, RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
-    const int groups = rows / RPW;
+    using G = HeadGeo<K>;
+    const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR, wave = threadIdx.x >> 6;
+    const int groups = rows / G::RPW;
     const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;
     H.ng = 0;
 #pragma unroll
@@ -799,9 +814,12 @@ __device__ __forceinline__ void f16_head_prefetch(const uint16_t * W, int rows, 
         const int g = gw + gi * nw;
         if (g >= groups) break;
         H.ng = gi + 1;
-        const int4 * wp = (const int4 *) (W + (size_t) (g * RPW + rsub) * K + lir * kQK);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) H.w[gi][c] = gld4n<NTL>(wp + c);
+        for (int hs = 0; hs < G::HS; ++hs) {
+            const int4 * wp = (const int4 *) (W + (size_t) (g * G::RPW + rsub) * K + (lir + hs * G::LPR) * kQK);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) H.w[gi][hs][c] = gld4n<NTL>(wp + c);
+        }
     }
 }
 
@@ -809,8 +827,8 @@ template <int K>
 __device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, uint64_t * out_tagged,
                                          uint32_t tag, float * out_plain, const Cb0Xf * xf, uint64_t * cand_tagged,
                                          float * cand_val, int32_t * cand_idx) {
-    static_assert(K / kQK <= 32 && ((K / kQK) & (K / kQK - 1)) == 0, "head width");
-    constexpr int LPR = K / kQK, RPW = 64 / LPR;
+    using G = HeadGeo<K>;
+    constexpr int LPR = G::LPR, RPW = G::RPW;
     const int lane = threadIdx.x & 63, lir = lane & (LPR - 1), rsub = lane / LPR, wave = threadIdx.x >> 6;
     const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;
     const int ng = H.ng;
@@ -820,17 +838,19 @@ __device__ __forceinline__ void f16_head(const HeadRegs & H, int rows, Lds & L, 
     if (ng > 0) {
         double acc[2] = {0.0, 0.0};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int4 x4 = *(const int4 *) &L.hq[c][lir * 8];
-            const uint16_t * xh = (const uint16_t *) &x4;
+        for (int hs = 0; hs < G::HS; ++hs)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const double xd = (double) h2f(xh[j]);
+            for (int c = 0; c < 4; ++c) {
+                const int4 x4 = *(const int4 *) &L.hq[c][(lir + hs * LPR) * 8];
+                const uint16_t * xh = (const uint16_t *) &x4;
 #pragma unroll
-                for (int gi = 0; gi < 2; ++gi)
-                    acc[gi] = fma((double) h8(H.w[gi][c], j), xd, acc[gi]);   // fp16 x fp16: exact product
+                for (int j = 0; j < 8; ++j) {
+                    const double xd = (double) h2f(xh[j]);
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        acc[gi] = fma((double) h8(H.w[gi][hs][c], j), xd, acc[gi]);   // fp16 x fp16: exact product
+                }
             }
-        }
 #pragma unroll
         for (int gi = 0; gi < 2; ++gi) {
             if (gi >= ng) break;
@@ -1705,12 +1725,14 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         }
     }
     __syncthreads();
-    // gate/up + SwiGLU (RMSNorm'd)
+    // gate/up + SwiGLU (RMSNorm'd); NGU row groups per wave (3 for the 1.7B
+    // talker's 6144 rows over 1024 waves)
+    constexpr int NGU = (FF / Geo<D>::RPW + 1023) / 1024 > 2 ? 3 : 2;
     const int p_gu = p++;
     if (wg_has_rows<D>(FF, 0)) {
-        Q8Regs<D, true> R;
+        Q8Regs<D, true, NGU> R;
         F16Regs<D, true> F;
-        if constexpr (WT == W_Q8) q8_prefetch<D, true, TK>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
+        if constexpr (WT == W_Q8) q8_prefetch<D, true, TK, NGU>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
         else f16_prefetch<D, true, TK>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
@@ -1719,7 +1741,8 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         rms_rows<NT, D>(v, nw, A.eps, L);
         if constexpr (WT == W_Q8) {
             quant_rows<NT, D>(v, L);
-            q8_compute<NT, D, true>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0, dead, A.err);
+            q8_compute<NT, D, true, NGU>(R, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0, dead,
+                                         A.err);
         } else {
             f16_rows<NT, D, false>(v, L);
             f16_compute<NT, D, true, false>(F, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0,
@@ -2080,6 +2103,41 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
             tstore(A.arena + (size_t) p * kSlot + (size_t) t * kHS + i, tb | p, x[t * d + i]);
 }
 
+// code_pred.mtp_proj: the NT gathered rows of width K in L.x, Q8_0-quantised,
+// through the projection (rows = the code predictor's width) plus its bias,
+// tagged into slot p.
+template <int NT, int K>
+__device__ __attribute__((always_inline)) void mtp_phase(const Args & A, Lds & L, int rows, int p, uint32_t tb,
+                                                         bool & dead) {
+    if (wg_has_rows<K>(rows, 0)) {
+        Q8Regs<K, false> R;
+        q8_prefetch<K, false, false>(R, A.mtp_w, A.mtp_d, nullptr, nullptr, rows, 0);
+        RowsT<NT, K> v;
+        load_lds<NT, K>(L.x, v);
+        quant_rows<NT, K>(v, L);
+        q8_compute<NT, K, false>(R, L, EPI_BIAS, nullptr, 0, A.arena + (size_t) p * kSlot, tb | p, 0, dead, A.err,
+                                 A.mtp_b);
+    }
+    __syncthreads();
+}
+
+// The head's input: the last token's row of the pass's output slot, normed
+// (width K), into L.hq (and, for the talker, the hidden row the next frame's
+// code predictor reads).
+template <int K, bool XT>
+__device__ __attribute__((always_inline)) void head_rows(const Args & A, Lds & L, const float * norm, int p_out,
+                                                         int nt, uint32_t tb, float * hidden, bool & dead) {
+    NormT<K> nw;
+    norm_prefetch<K>(norm, nw);
+    RowsT<1, K> v;
+    if constexpr (XT)
+        load_tagged<1, K, true>(A.arena + (size_t) p_out * kSlot + ((int) blockIdx.x & 7) * 2048 + (size_t) (nt - 1) * K,
+                                tb | p_out, v, dead, A.err, K);
+    else
+        load_tagged<1, K>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
+    head_input<K>(v, nw, A.eps, L, hidden);
+}
+
 // The argument block lives in device memory: dynamic indexing into a by-value
 // kernel argument (cp_embd[s], cp_head[s]) would copy it to private scratch.
 // One workgroup per CU, so one wave per SIMD: the full unified register file
@@ -2094,7 +2152,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
     return v;
 }
 
-template <int D, int QD, int FF, int WT, bool XT>
+template <int D, int DC, int QD, int FF, int FFC, int WT, bool XT>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(const Args * __restrict__ Ap,
                                                                                          int32_t frame, int32_t epoch,
                                                                                          int32_t mode) {
@@ -2156,12 +2214,24 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         __syncthreads();
         const int nt = s == 0 ? 2 : 1;
         const int pos0 = tk ? pos : s == 0 ? 0 : s + 1;
-        if (!XT) publish(A, L.x, nt, D, p_x, tb);
         int p_in = p_x, p_out = p_x;
+        const float * x0 = L.x;
+        if constexpr (DC != D) {
+            if (!tk) {
+                // the 1.7B layout: the code predictor's input rows pass through
+                // code_pred.mtp_proj (+ bias) into its own width
+                const int p_m = p++;
+                if (nt == 2) mtp_phase<2, D>(A, L, DC, p_m, tb, dead);
+                else mtp_phase<1, D>(A, L, DC, p_m, tb, dead);
+                p_in = p_out = p_m;
+                x0 = nullptr;
+            }
+        }
+        if (!XT && x0) publish(A, L.x, nt, tk ? D : DC, p_x, tb);
         const int nl = tk ? A.n_layers : A.cp_layers;
         const LayerQ8 * Ls = tk ? A.talker : A.cp;
         for (int l = 0; l < nl; ++l) {
-            const float * x_lds = l == 0 ? L.x : nullptr;
+            const float * x_lds = l == 0 ? x0 : nullptr;
             const LayerQ8 Wl = layer_desc(Ls + l);
             if constexpr (XT) {
                 const bool tabl = A.cp_qkv0 && !tk && s > 0 && l == 0;
@@ -2172,28 +2242,21 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 else if (tk) layer_x<1, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
                 else layer_x<1, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead, tab_row, rx_row);
             } else {
-                if (nt == 2) layer_t<2, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                if (nt == 2) layer_t<2, DC, QD, FFC, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
                 else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
-                else layer_t<1, D, QD, FF, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else layer_t<1, DC, QD, FFC, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
             }
             p_in = p_out;
         }
         // head on the last token's normed row
         const int p_head = tk ? 0 : p++;
         HeadRegs hr;
-        if (tk) f16_head_prefetch<D, true>(A.codec_head, A.codec_vocab, hr);
-        else f16_head_prefetch<D, false>(A.cp_head[s], A.cp_vocab, hr);
-        {
-            NormT<D> nw;
-            norm_prefetch<D>(tk ? A.out_norm : A.cp_out_norm, nw);
-            RowsT<1, D> v;
-            if constexpr (XT)
-                load_tagged<1, D, true>(A.arena + (size_t) p_out * kSlot + ((int) blockIdx.x & 7) * 2048 +
-                                            (size_t) (nt - 1) * D,
-                                        tb | p_out, v, dead, A.err, D);
-            else
-                load_tagged<1, D>(A.arena + (size_t) p_out * kSlot + (size_t) (nt - 1) * kHS, tb | p_out, v, dead, A.err);
-            head_input<D>(v, nw, A.eps, L, tk ? A.hidden : nullptr);
+        if (tk) {
+            f16_head_prefetch<D, true>(A.codec_head, A.codec_vocab, hr);
+            head_rows<D, XT>(A, L, A.out_norm, p_out, nt, tb, A.hidden, dead);
+        } else {
+            f16_head_prefetch<DC, false>(A.cp_head[s], A.cp_vocab, hr);
+            head_rows<DC, XT>(A, L, A.cp_out_norm, p_out, nt, tb, nullptr, dead);
         }
         if (tk) {
             const SampleParams & P = *A.params;
@@ -2208,7 +2271,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 f16_head<D>(hr, A.codec_vocab, L, nullptr, 0, A.logits, nullptr, nullptr, nullptr, nullptr);
         } else {
             uint64_t * hs = A.arena + (size_t) p_head * kSlot;
-            f16_head<D>(hr, A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
+            f16_head<DC>(hr, A.cp_vocab, L, hs, tb | p_head, nullptr, nullptr, hs + kHS, nullptr, nullptr);
             __syncthreads();
             code = sample_cp(A, L, A.arena + (size_t) p_head * kSlot, tb | p_head, frame, s + 1, dead);
             if (t == 0) L.codes[s + 1] = code;

@@ -312,3 +312,42 @@ def test_icl_long_reference_q8(path):
     finally:
         dev.close()
     assert cg.shape == co.shape and np.array_equal(cg, co)
+
+
+def weights17(wtype, seed):
+    key = ("17b", wtype, seed)
+    if key not in _weights:
+        _weights.clear()
+        say(f"[gpu] synthesising 1.7B {wtype} weights (seed {seed})")
+        _weights[key] = Weights(qcfg.full_17b(), wtype, seed=seed)
+    return _weights[key]
+
+
+def test_17b_q8_frame_loop_greedy(path):
+    """The 1.7B layout at its full shapes (talker 2048 wide with FFN 6144, code
+    predictor 1024 wide behind code_pred.mtp_proj), Q8_0: a 24-token prompt
+    and 16 greedy frames on the persistent kernel's 1.7B variant (three
+    gate/up row groups per wave, the projection as a GEMV phase per pass) and
+    on the multi-kernel frame, against the oracle."""
+    if path == "persistent_rows":
+        pytest.skip("the 1.7B layout has one persistent program (row-parallel)")
+    cfg = qcfg.full_17b()
+    text = np.random.default_rng(28).integers(0, 151936, 24).astype(np.int32)
+    spk = np.random.default_rng(29).standard_normal(cfg.hidden_size).astype(np.float32)
+    w = weights17("q8_0", 5)
+    if "17b" not in _oracle_runs:
+        o = orc.Oracle(cfg, w, threads=THREADS)
+        say("[gpu] 1.7B: oracle generate 16")
+        _oracle_runs["17b"] = o.generate(text, spk, max_len=16, temperature=0.0, top_k=0)
+        o.close()
+    co, first_o = _oracle_runs["17b"]
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w)
+        say(f"[gpu] 1.7B: device generate 16 ({path})")
+        cg = driver.generate(dev, cfg, text, spk, max_len=16, temperature=0.0, top_k=0, chunk=8)
+        _, _, used = dev.frames_stats()
+        assert used == (0 if path == "graph" else 1), used
+    finally:
+        dev.close()
+    assert cg.shape == co.shape and np.array_equal(cg, co)
