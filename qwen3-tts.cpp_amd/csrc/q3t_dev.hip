@@ -1455,17 +1455,23 @@ int build_cp_tab(q3t_dev * c) {
     return 0;
 }
 
-// F16 weights x fp32 rows on the exact VALU GEMM: y = epi(W . rows of x),
-// x rounded to fp16 unless wide (the widened ffn_down).
+// F16 weights x fp32 rows on the exact f64-MFMA GEMM: y = epi(W . rows of x),
+// x rounded to fp16 unless wide (the widened ffn_down).  K chunks of 64
+// where K allows (Q3T_PF_F16_KC=32 forces 32).
 void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, int xs, bool wide, float * y,
                  const float * res, int rs) {
+    static const int kc_env = [] { const char * e = std::getenv("Q3T_PF_F16_KC"); return e ? std::atoi(e) : 0; }();
+    const int kc = (kc_env == 32 || K % 64) ? 32 : 64;
     const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
-    if (wide)
-        hipLaunchKernelGGL(pf::k_gemm_f16<true>, grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, x, xs,
-                           n, y, N, res, rs);
-    else
-        hipLaunchKernelGGL(pf::k_gemm_f16<false>, grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, x,
-                           xs, n, y, N, res, rs);
+#define Q3T_PF_F16(wd, kcv)                                                                                       \
+    hipLaunchKernelGGL((pf::k_gemm_f16<wd, kcv>), grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, \
+                       x, xs, n, y, N, res, rs)
+    if (wide) {
+        if (kc == 64) Q3T_PF_F16(true, 64); else Q3T_PF_F16(true, 32);
+    } else {
+        if (kc == 64) Q3T_PF_F16(false, 64); else Q3T_PF_F16(false, 32);
+    }
+#undef Q3T_PF_F16
 }
 
 // Causal attention of the n prefill rows (QKV rows in c->pf_qkv, K/V already

@@ -1,4 +1,5 @@
-// q3t_prefill.h -- long-prompt talker prefill for Q8_0 models on int8 MFMA.
+// q3t_prefill.h -- long-prompt talker prefill on MFMA: int8 GEMMs for Q8_0
+// layers, f64 GEMMs for F16 layers, f64 causal attention.
 //
 // The n-token prefill (forward_prefill, src/tts_transformer.cpp:2217-2347 /
 // build_prefill_forward_graph :1474-1617) is a real contraction once n is in
@@ -19,6 +20,13 @@ namespace q3t {
 namespace pf {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+// Element e (0..7) of eight 16-bit values packed in an int4.
+__device__ __forceinline__ uint16_t h8bits(const int4 & v, int e) {
+    const int w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+    return (uint16_t) ((e & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu));
+}
 
 // One row per block: optional RMSNorm (y = (x * scale) * w, scale from the
 // fp64 sum of fp32 squares), then Q8_0 quantisation per 32-element block
@@ -225,74 +233,146 @@ constexpr int kTile = 64;         // output rows and tokens per workgroup of the
 
 // F16 weights: Y[t][r] = epi(sum_k W[r][k] * x[t][k]) with x rounded to fp16
 // (WIDE = false, the F16-weight contract) or kept fp32 (WIDE = true, the
-// widened ffn_down).  Both products are exact in fp64, so each is one fp64
-// fma and the sum is rounded to fp32 once, as in the GEMV path.  fp16 MFMA
-// would accumulate in fp32, so this runs on the VALU: a 64-row x 64-token
-// tile per workgroup, K in steps of 32 staged as fp32 in LDS, each thread a
-// 4 x 4 block of outputs (rows 4*(t%16).., tokens 4*(t/16)..).
-// Requires N % 64 == 0, K % 32 == 0 (the host checks).
-constexpr int kF16Kc = 32;
-template <bool WIDE>
+// widened ffn_down).  Both products are exact in fp64 (11 x 11 or 11 x 24
+// significant bits), so the GEMM runs on v_mfma_f64_16x16x4f64: exact
+// products summed in fp64 and rounded to fp32 once, the numbers of the GEMV
+// path.  (fp16 MFMA would accumulate in fp32.)
+//
+// A 64-row x 64-token tile per workgroup, K in chunks of KC (32 or 64)
+// staged in LDS as fp16 (weights, and activations when !WIDE) or fp32 (WIDE
+// activations), double-buffered: chunk c + 1 is loaded into registers while
+// chunk c's MFMAs run.  Four waves in a 2 x 2 arrangement, each 32 tokens x
+// 32 rows as 2 x 2 MFMA tiles with the tokens as the A operand (m) and the
+// weight rows as B (n), so lane l's element r is token 4r + l/16 of its tile
+// and row l%16: 16 consecutive lanes store 16 consecutive floats of one
+// output row.  Step s (0 .. KC/4 - 1) of a chunk gives lane group k = l/16
+// the index (KC/4) k + s, so each lane reads KC/4 contiguous elements of its
+// row with 16-byte loads.
+// Requires N % 64 == 0, K % KC == 0 (the host checks).
+template <bool WIDE, int KC>
+struct F16Tile {
+    static constexpr int HS = KC + 8;          // LDS row stride (halves) of fp16 rows: conflict-free 16-byte reads
+    static constexpr int FS = KC + 4;          // LDS row stride (floats) of fp32 rows
+    static constexpr int W_BYTES = kTile * HS * 2;
+    static constexpr int X_BYTES = WIDE ? kTile * FS * 4 : kTile * HS * 2;
+    static constexpr int STAGE = W_BYTES + X_BYTES;
+    static constexpr int E = KC / 4;           // elements per lane group and chunk (= MFMA steps)
+    static constexpr int SP = KC / 4;          // elements staged per thread (4 threads per row)
+};
+
+template <bool WIDE, int KC>
 __global__ __launch_bounds__(kBlock) void k_gemm_f16(const uint16_t * __restrict__ W, int32_t N, int32_t K,
                                                      const float * __restrict__ x, int32_t xs, int32_t n,
                                                      float * __restrict__ Y, int32_t ys, const float * __restrict__ res,
                                                      int32_t rs) {
-    __shared__ float sw[kF16Kc][kTile + 1];   // [k][row]
-    __shared__ float sx[kF16Kc][kTile + 1];   // [k][token]
+    using T = F16Tile<WIDE, KC>;
+    constexpr int E = T::E, NW = T::SP / 8, NX = T::SP / 4;
+    __shared__ __align__(16) char smem[2 * T::STAGE];
     const int t = threadIdx.x, r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
-    const int tr = (t & 15) * 4, tt = (t >> 4) * 4;
-    double acc[4][4];
+    const int lane = t & 63, wave = t >> 6, wr = wave & 1, wt = wave >> 1, li = lane & 15, lk = lane >> 4;
+    // staging: thread t loads SP consecutive k of weight row / token t / 4, part t % 4
+    const int sr = t >> 2, sp = (t & 3) * T::SP;
+    const bool sok = t0 + sr < n;                 // tokens past n load row n - 1 and stage zeros
+    const float * sx = x + (size_t) (sok ? t0 + sr : n - 1) * xs + sp;
+    const uint16_t * sw = W + (size_t) (r0 + sr) * K + sp;
+    v4i rw[NW];                                   // clang vectors: arrays of these stay in registers
+    float4 rx[NX];
+    auto fetch = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int u = 0; u < NW; ++u) rw[u] = *(const v4i *) (sw + k0 + 8 * u);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
-    // staging: thread t loads 8 consecutive k of row / token (t / 4), part t % 4
-    const int lr = t >> 2, lk = (t & 3) * 8;
-    for (int k0 = 0; k0 < K; k0 += kF16Kc) {
-        {
-            const int4 wv = *(const int4 *) (W + (size_t) (r0 + lr) * K + k0 + lk);
-            const uint16_t * wh = (const uint16_t *) &wv;
-            const int tok = t0 + lr;
-            float xv[8];
-            if (tok < n) {
-                const float4 a = *(const float4 *) (x + (size_t) tok * xs + k0 + lk);
-                const float4 b = *(const float4 *) (x + (size_t) tok * xs + k0 + lk + 4);
-                xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        for (int u = 0; u < NX; ++u) rx[u] = *(const float4 *) (sx + k0 + 4 * u);
+    };
+    auto stash = [&](int buf) {
+        char * st = smem + buf * T::STAGE;
+#pragma unroll
+        for (int u = 0; u < NW; ++u) *(v4i *) (st + (sr * T::HS + sp + 8 * u) * 2) = rw[u];
+        if (!sok) {                               // zeroed here, not at the load (which stays in flight)
+#pragma unroll
+            for (int u = 0; u < NX; ++u) rx[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (WIDE) {
+            float * xr = (float *) (st + T::W_BYTES) + sr * T::FS + sp;
+#pragma unroll
+            for (int u = 0; u < NX; ++u) *(float4 *) (xr + 4 * u) = rx[u];
+        } else {
+            auto pk = [](float a, float b) { return (int) ((uint32_t) f2h(a) | ((uint32_t) f2h(b) << 16)); };
+#pragma unroll
+            for (int u = 0; u < NX / 2; ++u) {
+                const float4 a = rx[2 * u], b = rx[2 * u + 1];
+                *(int4 *) (st + T::W_BYTES + (sr * T::HS + sp + 8 * u) * 2) =
+                    make_int4(pk(a.x, a.y), pk(a.z, a.w), pk(b.x, b.y), pk(b.z, b.w));
+            }
+        }
+    };
+    v4d acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+    const int C = K / KC;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int ch = 0; ch < C; ++ch) {
+        const int buf = ch & 1;
+        if (ch + 1 < C) fetch((ch + 1) * KC);
+        const char * sb = smem + buf * T::STAGE;
+        int4 bw[2][E / 8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int u = 0; u < E / 8; ++u)
+                bw[j][u] = *(const int4 *) (sb + ((wr * 32 + 16 * j + li) * T::HS + E * lk + 8 * u) * 2);
+        float ax[2][E];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int tr = wt * 32 + 16 * i + li;
+            if (WIDE) {
+                const float * xr = (const float *) (sb + T::W_BYTES) + tr * T::FS + E * lk;
+#pragma unroll
+                for (int u = 0; u < E / 4; ++u) {
+                    const float4 q = *(const float4 *) (xr + 4 * u);
+                    ax[i][4 * u] = q.x; ax[i][4 * u + 1] = q.y; ax[i][4 * u + 2] = q.z; ax[i][4 * u + 3] = q.w;
+                }
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+                for (int u = 0; u < E / 8; ++u) {
+                    const int4 hv = *(const int4 *) (sb + T::W_BYTES + (tr * T::HS + E * lk + 8 * u) * 2);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ax[i][8 * u + e] = h2f(h8bits(hv, e));
+                }
             }
-            __syncthreads();
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                sw[lk + e][lr] = h2f(wh[e]);
-                sx[lk + e][lr] = WIDE ? xv[e] : round_f16(xv[e]);
+        for (int s = 0; s < E; ++s) {
+            double bd[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bd[j] = (double) h2f(h8bits(bw[j][s >> 3], s & 7));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const double ad = (double) ax[i][s];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad, bd[j], acc[i][j], 0, 0, 0);
             }
-            __syncthreads();
         }
-#pragma unroll 8
-        for (int k = 0; k < kF16Kc; ++k) {
-            double wd[4], xd[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { wd[i] = (double) sw[k][tr + i]; xd[i] = (double) sx[k][tt + i]; }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fma(wd[i], xd[j], acc[i][j]);   // exact products
-        }
+        if (ch + 1 < C) stash(buf ^ 1);
+        __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int tok = t0 + tt + j;
-        if (tok >= n) continue;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r0 + tr + i;
-            float v = (float) acc[i][j];
-            if (res) v = v + res[(size_t) tok * rs + r];
-            Y[(size_t) tok * ys + r] = v;
+        for (int r = 0; r < 4; ++r) {
+            const int tok = t0 + wt * 32 + 16 * i + 4 * r + lk;
+            if (tok >= n) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int row = r0 + wr * 32 + 16 * j + li;
+                float v = (float) acc[i][j][r];
+                if (res) v = v + res[(size_t) tok * rs + row];
+                Y[(size_t) tok * ys + row] = v;
+            }
         }
-    }
 }
 
 // SwiGLU over rows: f = silu(g) * u.
@@ -417,17 +497,11 @@ __global__ __launch_bounds__(kBlock) void k_attn_rows(const float * __restrict__
 // l%16], D[m = 4r + l/16][n = l%16] in element r.  Step s of a contraction
 // gives lane group k = l/16 the index 32k + s (scores, 128 dims: each lane
 // reads 32 contiguous dims of its row) or 16k + s (P.V, 64 positions).
-typedef double v4d __attribute__((ext_vector_type(4)));
 constexpr int kAT = 64;          // rows and positions per attention tile
 constexpr int kKS = 136;         // LDS row stride (halves) of a staged K tile: conflict-free 16-byte reads
 constexpr int kVS = 72;          // LDS row stride (halves) of staged P and V^T tiles
 
 __device__ __forceinline__ double kvd(uint16_t h, bool bf) { return (double) kv2f(h, bf); }
-// Element e (0..7) of eight 16-bit values packed in an int4.
-__device__ __forceinline__ uint16_t h8bits(const int4 & v, int e) {
-    const int w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
-    return (uint16_t) ((e & 1) ? ((uint32_t) w >> 16) : ((uint32_t) w & 0xffffu));
-}
 
 // grid (n, n_head): q of row r, head h (QK-norm, NEOX RoPE at position
 // n_past + r) rounded to the cache type, into Qh[h][r][128].
