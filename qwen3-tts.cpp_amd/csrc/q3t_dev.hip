@@ -1501,7 +1501,7 @@ int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uin
         if (dev_alloc_t(c, &c->pf_s, need) || dev_alloc_t(c, &c->pf_p, need)) return -1;
         c->pf_sp_cap = need;
     }
-    const dim3 tiles(g.n_head, ((n + pf::kAT - 1) / pf::kAT + 1) / 2);   // tile pairs
+    const dim3 tiles(g.n_head, ((n + pf::kAT - 1) / pf::kAT + 1) / 2, 2);   // tile pairs x position / dim halves
     // q rows into the probabilities buffer's head (they are consumed before it is written)
     uint16_t * qh = c->pf_p;
     hipLaunchKernelGGL(pf::k_att_q, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd,

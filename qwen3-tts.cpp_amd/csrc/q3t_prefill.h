@@ -517,27 +517,33 @@ __global__ __launch_bounds__(kBlock) void k_att_q(const float * __restrict__ qkv
     if (t < kHD) Qh[((size_t) h * n + row) * kHD + t] = f2kv(o, bf);
 }
 
-// grid (n_head, ceil(tiles / 2)): workgroup y takes 64-row tiles y and
+// grid (n_head, ceil(tiles / 2), 2): workgroup y takes 64-row tiles y and
 // tiles - 1 - y, so every workgroup sweeps about the same number of K tiles
-// (the causal sweep of tile y is y + 1 tiles long).  Wave w owns rows
-// 16w..16w+15 of a tile (q from k_att_q): lane (i = l%16, k = l/16) holds
-// dims 32k..32k+31 of row 16w + i.  K tiles are
-// 128 positions; eight waves, two per SIMD: wave group grp = t / 256 takes
-// positions 64 grp .. 64 grp + 63 of each tile (four 16-position
-// accumulators per wave).
-constexpr int kKT = 128;         // positions per staged K tile of the scores kernel
-constexpr int kAttT = 512;       // threads of the MFMA attention kernels
+// (the causal sweep of tile y is y + 1 tiles long); grid z = grp takes the
+// 64-position K tiles at 128 s + 64 grp, so that two workgroups of four waves
+// share each CU and one's MFMAs run while the other waits at a barrier.
+// Wave w owns rows 16w..16w+15 of a tile (q from k_att_q): lane (i = l%16,
+// k = l/16) holds dims 32k..32k+31 of row 16w + i, and four 16-position
+// accumulators.  K tiles are double-buffered in LDS (tile s + 1 loaded into
+// registers while tile s's MFMAs run; rows past the tile's last position
+// staged as zero).
+constexpr int kAttT = 256;       // threads of the MFMA attention kernels
 __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restrict__ Qh,
                                                        const uint16_t * __restrict__ kc, int32_t n_ctx, int32_t n_head,
                                                        int32_t n_kv_head, int32_t n, int32_t n_past, float scale,
                                                        float * __restrict__ S, int32_t ls, int32_t bf) {
-    __shared__ __align__(16) uint16_t kt[kKT * kKS];
-    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head);
-    const int t = threadIdx.x, grp = t >> 8, w = (t >> 6) & 3, l = t & 63, i = l & 15, k = l >> 4;
+    __shared__ __align__(16) uint16_t kt[2][kAT * kKS];
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head), grp = blockIdx.z;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int krow = t >> 4, kch = t & 15;                  // staging: positions krow + 16u, 8-dim chunk
+    const uint16_t * kbase = kc + (size_t) g * n_ctx * kHD + 8 * kch;
     for (int pass = 0; pass < 2; ++pass) {
         const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
         if (pass == 1 && tile == (int) blockIdx.y) break;     // the middle tile of an odd count
         const int row0 = tile * kAT, my_row = row0 + 16 * w + i;
+        const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
+        if (lim_tile < 64 * grp) continue;                      // no K tile for this group
+        const int nst = (lim_tile - 64 * grp) / (2 * kAT) + 1;
         // q of row my_row, dims 32k .. 32k+31 (fp16 / bfloat16 values, held as fp32)
         float a[32];
         {
@@ -550,18 +556,27 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
                 for (int e = 0; e < 8; ++e) a[8 * c + e] = kv2f(h8bits(v, e), bf);
             }
         }
-        const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
-        for (int j0 = 0; j0 <= lim_tile; j0 += kKT) {
-            __syncthreads();
-            // stage K rows j0..j0+127 of KV head g (16-byte chunks; rows past the tile's limit zero)
+        int4 rk[4];
+        int kok[4];
+        auto fetch = [&](int j0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int pr = (t >> 4) + 32 * u, c = t & 15, j = j0 + pr;
-                int4 v = make_int4(0, 0, 0, 0);
-                if (j <= lim_tile) v = *(const int4 *) (kc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
-                *(int4 *) (kt + pr * kKS + 8 * c) = v;
+                const int j = j0 + krow + 16 * u;
+                kok[u] = j <= lim_tile;
+                rk[u] = *(const int4 *) (kbase + (size_t) min(j, lim_tile) * kHD);
             }
-            __syncthreads();
+        };
+        auto stash = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                *(int4 *) (&kt[buf][(krow + 16 * u) * kKS + 8 * kch]) = kok[u] ? rk[u] : make_int4(0, 0, 0, 0);
+        };
+        fetch(64 * grp);
+        stash(0);
+        __syncthreads();
+        for (int st = 0; st < nst; ++st) {
+            const int buf = st & 1, j0 = 2 * kAT * st + 64 * grp;
+            if (st + 1 < nst) fetch(j0 + 2 * kAT);
             v4d acc[4];
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) acc[t4] = v4d{0.0, 0.0, 0.0, 0.0};
@@ -570,17 +585,14 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
             for (int c = 0; c < 4; ++c) {                      // dims 32k + 8c .. +7
                 int4 kb[4];
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) kb[t4] = *(const int4 *) (kt + (64 * grp + 16 * t4 + i) * kKS + 32 * k + 8 * c);
+                for (int t4 = 0; t4 < 4; ++t4)
+                    kb[t4] = *(const int4 *) (&kt[buf][(16 * t4 + i) * kKS + 32 * k + 8 * c]);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const int wv = e >> 1;
                     const double ad = (double) a[8 * c + e];
 #pragma unroll
-                    for (int t4 = 0; t4 < 4; ++t4) {
-                        const int word = wv == 0 ? kb[t4].x : wv == 1 ? kb[t4].y : wv == 2 ? kb[t4].z : kb[t4].w;
-                        const uint16_t hv = (uint16_t) ((e & 1) ? ((uint32_t) word >> 16) : ((uint32_t) word & 0xffffu));
-                        acc[t4] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad, kvd(hv, bf), acc[t4], 0, 0, 0);
-                    }
+                    for (int t4 = 0; t4 < 4; ++t4)
+                        acc[t4] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad, kvd(h8bits(kb[t4], e), bf), acc[t4], 0, 0, 0);
                 }
                 // keep the next dims' loads and conversions after these MFMAs (register pressure)
                 __builtin_amdgcn_sched_barrier(0);
@@ -589,10 +601,12 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
             for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int row = row0 + 16 * w + 4 * r + k, j = j0 + 64 * grp + 16 * t4 + i;
+                    const int row = row0 + 16 * w + 4 * r + k, j = j0 + 16 * t4 + i;
                     if (row < n && j <= n_past + row)
                         S[((size_t) h * n + row) * ls + j] = (float) acc[t4][r] * scale;
                 }
+            if (st + 1 < nst) stash(buf ^ 1);
+            __syncthreads();
         }
     }
 }
@@ -643,86 +657,101 @@ __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict
     for (int j = lane; j < cnt; j += 64) pr[j] = f2kv(expf_q3t(sr[j] - mx) * inv, bf);
 }
 
-// grid (n_head, ceil(tiles / 2)), tiles paired as in k_att_scores; eight
-// waves: wave w of group grp owns rows 16w..16w+15 of a tile and dims
-// 64 grp .. 64 grp + 63 as four 16 x 16 accumulators.  Probabilities past a
-// row's last position are taken as zero.
+// grid (n_head, ceil(tiles / 2), 2), tiles paired as in k_att_scores; grid
+// z = grp takes dims 64 grp .. 64 grp + 63.  Four waves: wave w owns rows
+// 16w..16w+15 of a tile and dims 64 grp + 4 i + d4 (lane i = l%16, d4 =
+// 0..3) as four 16 x 16 accumulators, so each lane reads its four B operands
+// of a step with one 8-byte load and stores four consecutive floats.  P tiles
+// [row][position] and V tiles [position][dim] are double-buffered in LDS:
+// step s + 1's tiles are loaded into registers while step s's MFMAs run.
+// Probabilities past a row's last position, and V rows past the tile's last
+// position, are staged as zero.
+constexpr int kVN = 64 + 8;      // LDS row stride (halves) of a staged V half-tile: conflict-free 16-byte writes
 __global__ __launch_bounds__(kAttT) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
                                                    const uint16_t * __restrict__ vc, int32_t n_ctx, int32_t n_head,
                                                    int32_t n_kv_head, int32_t n, int32_t n_past,
                                                    float * __restrict__ out, int32_t out_stride, int32_t bf) {
-    __shared__ __align__(16) uint16_t pt[kAT * kVS];         // [row][position]
-    __shared__ __align__(16) uint16_t vt[kHD * kVS];         // [dim][position]
-    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head);
-    const int t = threadIdx.x, grp = t >> 8, w = (t >> 6) & 3, l = t & 63, i = l & 15, k = l >> 4;
+    __shared__ __align__(16) uint16_t pt[2][kAT * kVS];      // [row][position]
+    __shared__ __align__(16) uint16_t vt[2][kAT * kVN];      // [position][dim - 64 grp]
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head), grp = blockIdx.z;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int srow = t >> 3, sch = t & 7;                    // staging: rows / positions srow + 32u, 8-wide chunk
+    const uint16_t * vbase = vc + (size_t) g * n_ctx * kHD + 64 * grp + 8 * sch;
   for (int pass = 0; pass < 2; ++pass) {
     const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
     if (pass == 1 && tile == (int) blockIdx.y) break;         // the middle tile of an odd count
     const int row0 = tile * kAT;
     const int lim_tile = n_past + min(row0 + kAT, n) - 1;
+    const int nst = lim_tile / kAT + 1;
+    int plim[2];
+    const uint16_t * prp[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int prw = row0 + srow + 32 * u;
+        plim[u] = prw < n ? n_past + prw : -1;
+        prp[u] = P + ((size_t) h * n + (prw < n ? prw : 0)) * ls + 8 * sch;
+    }
+    int4 rp[2], rv[2];
+    int pvalid[2], vok[2];
+    // loads for step j0 / kAT into registers; the masks are applied at stash
+    // time so that the loads stay in flight across the MFMAs
+    auto fetch = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            pvalid[u] = min(max(plim[u] - (j0 + 8 * sch) + 1, 0), 8);   // valid positions of the chunk
+            rp[u] = *(const int4 *) (prp[u] + (pvalid[u] > 0 ? j0 : 0)); // j0 + 63 < ls: in the row
+            const int pos = j0 + srow + 32 * u;
+            vok[u] = pos <= lim_tile;
+            rv[u] = *(const int4 *) (vbase + (size_t) min(pos, lim_tile) * kHD);
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            int4 v = rp[u];
+            const int pv = pvalid[u];
+            if (pv < 8) {
+                const auto m = [pv](int e) { return (2 * e < pv ? 0xffff : 0) | (2 * e + 1 < pv ? (int) 0xffff0000u : 0); };
+                v.x &= m(0); v.y &= m(1); v.z &= m(2); v.w &= m(3);
+            }
+            *(int4 *) (&pt[buf][(srow + 32 * u) * kVS + 8 * sch]) = v;
+            *(int4 *) (&vt[buf][(srow + 32 * u) * kVN + 8 * sch]) = vok[u] ? rv[u] : make_int4(0, 0, 0, 0);
+        }
+    };
     v4d acc[4];
 #pragma unroll
     for (int d4 = 0; d4 < 4; ++d4) acc[d4] = v4d{0.0, 0.0, 0.0, 0.0};
-    for (int j0 = 0; j0 <= lim_tile; j0 += kAT) {
-        __syncthreads();
-        // P tile: 64 rows x 64 positions (8-position chunks), masked to each row's limit
-        {
-            const int idx = t, r = idx >> 3, c = idx & 7, row = row0 + r;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (row < n) {
-                const int lim = n_past + row, j = j0 + 8 * c;
-                if (j + 7 <= lim) v = *(const int4 *) (P + ((size_t) h * n + row) * ls + j);
-                else if (j <= lim) {
-                    uint16_t tmp[8];
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < nst) fetch((st + 1) * kAT);
+        int4 pa[2];
+        pa[0] = *(const int4 *) (&pt[buf][(16 * w + i) * kVS + 16 * k]);
+        pa[1] = *(const int4 *) (&pt[buf][(16 * w + i) * kVS + 16 * k + 8]);
+        const uint16_t * vr = &vt[buf][16 * k * kVN + 4 * i];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) tmp[e] = j + e <= lim ? P[((size_t) h * n + row) * ls + j + e] : 0;
-                    v = *(const int4 *) tmp;
-                }
-            }
-            *(int4 *) (pt + r * kVS + 8 * c) = v;
-        }
-        // V^T tile: positions j0..j0+63 (past the limit: zero) of KV head g
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int idx = t + kAttT * u, pr = idx >> 4, c = idx & 15, j = j0 + pr;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (j <= lim_tile) v = *(const int4 *) (vc + ((size_t) g * n_ctx + j) * kHD + 8 * c);
-            const uint16_t * vh = (const uint16_t *) &v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vt[(8 * c + e) * kVS + pr] = vh[e];
-        }
-        __syncthreads();
-        int4 pa[2], vb[4][2];
-        pa[0] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k);
-        pa[1] = *(const int4 *) (pt + (16 * w + i) * kVS + 16 * k + 8);
-#pragma unroll
-        for (int d4 = 0; d4 < 4; ++d4) {
-            vb[d4][0] = *(const int4 *) (vt + (64 * grp + 16 * d4 + i) * kVS + 16 * k);
-            vb[d4][1] = *(const int4 *) (vt + (64 * grp + 16 * d4 + i) * kVS + 16 * k + 8);
-        }
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-            const int e = st & 7, wv = e >> 1;
-            const int4 & pv4 = pa[st >> 3];
-            const int pw = wv == 0 ? pv4.x : wv == 1 ? pv4.y : wv == 2 ? pv4.z : pv4.w;
-            const uint16_t ph = (uint16_t) ((e & 1) ? ((uint32_t) pw >> 16) : ((uint32_t) pw & 0xffffu));
-            const double pd = kvd(ph, bf);
+        for (int s = 0; s < 16; ++s) {                       // position 16k + s of the tile
+            const double pd = kvd(h8bits(pa[s >> 3], s & 7), bf);
+            const uint2 vv = *(const uint2 *) (vr + s * kVN);
 #pragma unroll
             for (int d4 = 0; d4 < 4; ++d4) {
-                const int4 & v4 = vb[d4][st >> 3];
-                const int vw = wv == 0 ? v4.x : wv == 1 ? v4.y : wv == 2 ? v4.z : v4.w;
-                const uint16_t vh = (uint16_t) ((e & 1) ? ((uint32_t) vw >> 16) : ((uint32_t) vw & 0xffffu));
+                const uint32_t word = (d4 >> 1) ? vv.y : vv.x;
+                const uint16_t vh = (uint16_t) ((d4 & 1) ? (word >> 16) : (word & 0xffffu));
                 acc[d4] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d4], 0, 0, 0);
             }
         }
+        if (st + 1 < nst) stash(buf ^ 1);
+        __syncthreads();
     }
 #pragma unroll
-    for (int d4 = 0; d4 < 4; ++d4)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = row0 + 16 * w + 4 * r + k;
-            if (row < n) out[(size_t) row * out_stride + h * kHD + 64 * grp + 16 * d4 + i] = (float) acc[d4][r];
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * w + 4 * r + k;
+        if (row < n)
+            *(float4 *) (out + (size_t) row * out_stride + h * kHD + 64 * grp + 4 * i) =
+                make_float4((float) acc[0][r], (float) acc[1][r], (float) acc[2][r], (float) acc[3][r]);
+    }
   }
 }
 
