@@ -269,6 +269,14 @@ int  q3t_dev_frames_stats(q3t_dev * dev, double * gpu_us_out, int64_t * frames_o
  * that stopped (EOS or max_len) idle while the others run. */
 int  q3t_dev_streams_reserve(q3t_dev * dev, int32_t n_streams, int32_t n_ctx);
 int  q3t_dev_stream_prefill(q3t_dev * dev, int32_t stream, const float * embd, int32_t n);
+/* Stream b's counterparts of q3t_dev_kv_write and q3t_dev_prefill(n_past):
+ * rows [0, n_pos) of talker layer `layer` of the stream's cache, and the
+ * prefill of n rows at positions [n_past, n_past+n) over that cache (a stream
+ * resumed from a cached history).  stream_prefill is stream_prefill_at with
+ * n_past 0. */
+int  q3t_dev_stream_kv_write(q3t_dev * dev, int32_t stream, int32_t layer, int32_t n_pos,
+                             const uint16_t * k, const uint16_t * v);
+int  q3t_dev_stream_prefill_at(q3t_dev * dev, int32_t stream, const float * embd, int32_t n, int32_t n_past);
 int  q3t_dev_streams_begin(q3t_dev * dev, const q3t_frame_args * args);
 int  q3t_dev_streams_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
                          int32_t * n_emitted_out, int32_t * eos_out);

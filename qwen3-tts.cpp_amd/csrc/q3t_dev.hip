@@ -2590,27 +2590,53 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     return sync(c);
 }
 
-int q3t_dev_stream_prefill(q3t_dev * c, int32_t stream, const float * embd, int32_t n) {
-    if (!c || !embd) return -1;
+}  // extern "C"
+
+namespace {
+
+// Runs fn with the context's cache pointers set to stream b's cache slice.
+template <class F>
+int with_stream_cache(q3t_dev * c, int32_t stream, F fn) {
     if (stream < 0 || stream >= c->nb) return fail(c, "stream index out of range (q3t_dev_streams_reserve first)");
-    if (n < 1 || n > c->sb_ctx) return fail(c, "Context length exceeded");
     if (c->n_ctx != c->sb_ctx) return fail(c, "KV cache re-reserved since q3t_dev_streams_reserve; reserve the streams again");
-    HIP_OK(hipSetDevice(c->device));
     const q3t_config & g = c->cfg;
     const size_t kv = (size_t) g.n_layers * g.n_kv_head * c->sb_ctx * g.head_dim;
-    // run the single-stream prefill against this stream's cache
     uint16_t * kc0 = c->kc, * vc0 = c->vc;
     c->kc = c->skc + stream * kv;
     c->vc = c->svc + stream * kv;
-    const int rc = q3t_dev_prefill(c, embd, n, 0, nullptr, nullptr);
+    const int rc = fn();
     c->kc = kc0;
     c->vc = vc0;
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3t_dev_stream_kv_write(q3t_dev * c, int32_t stream, int32_t layer, int32_t n_pos, const uint16_t * k,
+                            const uint16_t * v) {
+    if (!c || !k || !v) return -1;
+    return with_stream_cache(c, stream, [&] { return q3t_dev_kv_write(c, layer, n_pos, k, v); });
+}
+
+int q3t_dev_stream_prefill_at(q3t_dev * c, int32_t stream, const float * embd, int32_t n, int32_t n_past) {
+    if (!c || !embd) return -1;
+    if (n < 1 || n_past < 0 || n_past + n > c->sb_ctx) return fail(c, "Context length exceeded");
+    HIP_OK(hipSetDevice(c->device));
+    const q3t_config & g = c->cfg;
+    // the single-stream prefill against this stream's cache
+    const int rc = with_stream_cache(c, stream, [&] { return q3t_dev_prefill(c, embd, n, n_past, nullptr, nullptr); });
     if (rc) return rc;
     HIP_OK(hipMemcpyAsync(c->slogits + (size_t) stream * g.codec_vocab, c->logits, (size_t) g.codec_vocab * 4,
                           hipMemcpyDeviceToDevice, c->stream));
     HIP_OK(hipMemcpyAsync(c->shidden + (size_t) stream * g.hidden_size, c->hidden, (size_t) g.hidden_size * 4,
                           hipMemcpyDeviceToDevice, c->stream));
     return sync(c);
+}
+
+int q3t_dev_stream_prefill(q3t_dev * c, int32_t stream, const float * embd, int32_t n) {
+    return q3t_dev_stream_prefill_at(c, stream, embd, n, 0);
 }
 
 int q3t_dev_streams_begin(q3t_dev * c, const q3t_frame_args * args) {

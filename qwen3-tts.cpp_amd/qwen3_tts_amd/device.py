@@ -24,6 +24,7 @@ EXPORTS = [
     "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
     "q3t_dev_frames_run", "q3t_dev_frame_codes", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
+    "q3t_dev_stream_prefill_at", "q3t_dev_stream_kv_write",
     "q3t_dev_streams_begin", "q3t_dev_streams_run", "q3t_dev_sync", "q3t_dev_time_kernel",
 ]
 
@@ -84,6 +85,8 @@ def load_library(path=LIB_PATH):
                                              ctypes.POINTER(i32)]
         lib.q3t_dev_streams_reserve.argtypes = [vp, i32, i32]
         lib.q3t_dev_stream_prefill.argtypes = [vp, i32, f32p, i32]
+        lib.q3t_dev_stream_prefill_at.argtypes = [vp, i32, f32p, i32, i32]
+        lib.q3t_dev_stream_kv_write.argtypes = [vp, i32, i32, i32, vp, vp]
         lib.q3t_dev_streams_begin.argtypes = [vp, ctypes.POINTER(CFrameArgs)]
         lib.q3t_dev_streams_run.argtypes = [vp, i32, vp, vp, vp]
         lib.q3t_dev_time_kernel.argtypes = [vp, i32, i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
@@ -291,9 +294,20 @@ class Device:
         self._check(self.lib.q3t_dev_streams_reserve(self.h, n_streams, n_ctx), "streams_reserve")
         self.n_streams = n_streams
 
-    def stream_prefill(self, stream, embd):
+    def stream_prefill(self, stream, embd, n_past=0):
         embd = np.ascontiguousarray(embd, dtype=np.float32)
-        self._check(self.lib.q3t_dev_stream_prefill(self.h, stream, _p(embd), embd.shape[0]), "stream_prefill")
+        if n_past:
+            self._check(self.lib.q3t_dev_stream_prefill_at(self.h, stream, _p(embd), embd.shape[0], n_past),
+                        "stream_prefill_at")
+        else:
+            self._check(self.lib.q3t_dev_stream_prefill(self.h, stream, _p(embd), embd.shape[0]), "stream_prefill")
+
+    def stream_kv_write(self, stream, layer, k, v):
+        """stream's counterpart of kv_write: fp16 rows [n_pos][n_kv_head][head_dim]."""
+        k = np.ascontiguousarray(k, np.uint16 if np.asarray(k).dtype == np.uint16 else np.float16)
+        v = np.ascontiguousarray(v, np.uint16 if np.asarray(v).dtype == np.uint16 else np.float16)
+        self._check(self.lib.q3t_dev_stream_kv_write(self.h, stream, layer, k.shape[0], _p(k), _p(v)),
+                    "stream_kv_write")
 
     def streams_begin(self, streams):
         """streams: one dict per stream with the keyword arguments of

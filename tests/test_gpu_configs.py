@@ -10,6 +10,8 @@
                    than 1,024 positions (the split attention's four-phase
                    form), then sampled frames (T 0.9, top-k 50, repetition
                    penalty 1.05); and decode past 4,096 positions
+  configuration 5  16 Q8_0 streams with talker KV lengths uniform in
+                   [128, 2048], greedy, batched decode
 
 Long contexts are pre-filled with seeded K/V rows on both sides (the oracle's
 orc_kv_write takes the same [n_pos][n_kv_head][head_dim] rows), so the
@@ -312,6 +314,55 @@ def test_icl_long_reference_q8(path):
     finally:
         dev.close()
     assert cg.shape == co.shape and np.array_equal(cg, co)
+
+
+def test_config5_16_streams_ragged_kv_q8():
+    """Configuration 5's shape: 16 streams of the Q8_0 0.6B model whose talker
+    KV lengths are drawn uniformly from [128, 2048]: each stream's history is
+    seeded K/V rows written to both sides (q3t_dev_stream_kv_write /
+    orc_kv_write), then its own prompt rows prefilled at that offset
+    (q3t_dev_stream_prefill_at), then 6 greedy frames of all streams together
+    (EOS biased off).  Each stream's codes equal the oracle's frame loop over
+    the same cache."""
+    cfg = qcfg.full_06b()
+    w = weights("q8_0", 3)
+    B, frames = 16, 6
+    rng = np.random.default_rng(91)
+    kv_len = rng.integers(128, 2049, B)
+    n_ctx = int(kv_len.max()) + frames + 8
+    dev = Device(cfg)
+    o = orc.Oracle(cfg, w, threads=THREADS)
+    try:
+        dev.upload_weights(w)
+        dev.streams_reserve(B, n_ctx)
+        args, want = [], []
+        for b in range(B):
+            text = rng.integers(0, cfg.text_vocab - 8, int(rng.integers(9, 40))).astype(np.int32)
+            spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
+            pre, trail, pad = driver.build_prefill(dev, cfg, text, spk)
+            hist = int(kv_len[b]) - pre.shape[0]
+            say(f"[gpu] config 5: stream {b}: {hist} cached positions + {pre.shape[0]} prompt rows")
+            o.kv_reset(n_ctx)
+            for il in range(cfg.n_layers):
+                kv = bf16_kv(rng, hist, cfg)
+                dev.stream_kv_write(b, il, kv[0], kv[1])
+                o.kv_write(il, kv[0], kv[1])
+            dev.stream_prefill(b, pre, n_past=hist)
+            _, lo = o.prefill(pre, hist)
+            want.append(o.frames(lo, int(kv_len[b]), trail, pad, frames, temperature=0.0, top_k=0, eos_bias=-1e4))
+            args.append(dict(trailing=trail, tts_pad=pad, n_past=int(kv_len[b]), max_len=frames, temperature=0.0,
+                             top_k=0, eos_bias=-1e4))
+        say(f"[gpu] config 5: {B} streams x {frames} frames")
+        dev.streams_begin(args)
+        got, eos = dev.streams_run(frames)
+        _, _, used = dev.frames_stats()
+        assert used == 2, used
+        for b in range(B):
+            assert got[b].shape == (frames, 16) and want[b].shape == (frames, 16), b
+            assert np.array_equal(got[b], want[b]), b
+    finally:
+        o.close()
+        dev.close()
 
 
 def weights17(wtype, seed):
