@@ -345,18 +345,22 @@ def streams_bench(args, cfg, w):
     # talker: 1 row per stream per frame; code predictor: 2 + 14 rows per stream per frame
     frame_ops = 2.0 * B * layer_macs * (cfg.n_layers + 16 * cfg.cp_layers)
     fbytes = frame_bytes(cfg, w.tensors, [p + args.warmup + args.steps // 2 for p in plens])
+    q8 = args.weights == "q8_0"
+    # dense peaks: int8 MFMA 5.0 POP/s (Q8_0 layers), f64 MFMA 78.6 TFLOP/s (F16 layers)
+    peak = 5.0e15 if q8 else 78.6e12
     out = {
-        "metric": "aggregate codec frames/sec, multi-stream batched decode Q8_0", "value": round(fps, 1),
+        "metric": f"aggregate codec frames/sec, multi-stream batched decode {args.weights.upper()}", "value": round(fps, 1),
         "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded weights, uniform prompt ids, N(0,0.05) history)",
+        "vs_baseline": None, "dtype": "int8" if q8 else "f64 (fp16 operands)",
+        "data": "synthetic (seeded weights, uniform prompt ids, N(0,0.05) history)",
         "config": {"workload": f"{B} streams, 128-token prompts, talker KV lengths uniform in [128, 2048], greedy, "
-                               f"Q8_0 0.6B shapes, one hipGraph per frame of all streams",
+                               f"{args.weights.upper()} 0.6B shapes, one hipGraph per frame of all streams",
                    "global_batch": B, "frames_per_stream": args.steps, "kv_lengths": [int(x) for x in plens]},
         "gpu_ms_per_frame": round(gpu_frame_s * 1e3, 4),
         "per_stream_fps": round(args.steps / elapsed, 2),
         "layer_gemm_tops": round(frame_ops / gpu_frame_s / 1e12, 2),
-        "mfma_util": round(frame_ops / gpu_frame_s / 5.0e15, 5),
+        "mfma_util": round(frame_ops / gpu_frame_s / peak, 5),
         "frame_algorithmic_bytes": int(fbytes),
         "frame_hbm_gbs": round(fbytes / gpu_frame_s / 1e9, 1),
         "frame_roofline_frac": round(fbytes / gpu_frame_s / 1e9 / HBM_PEAK_GBS, 4),

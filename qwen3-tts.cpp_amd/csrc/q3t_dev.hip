@@ -102,6 +102,8 @@ struct q3t_dev {
     float * sstage = nullptr;                         // [stream][2][d]
     float * bxa = nullptr, * bxb = nullptr, * bqkv = nullptr, * batt = nullptr;   // [2 * nb][...]
     int8_t * bq8 = nullptr; float * bdx8 = nullptr;   // Q8_0 rows [2 * nb][max(qd, ffn)] and scales
+    float * bff = nullptr;                             // F16 layers: SwiGLU rows [2 * nb][ffn]
+    bool s_f16 = false;                                // multi-stream layers are F16 (else Q8_0)
     float * srs = nullptr;                            // RMSNorm row scales [2 * nb]
     double * sss[2] = {nullptr, nullptr};             // per-tile sums of squares of Wo / down outputs [d/16][2 nb]
     // split-K partials and per-tile tickets, one set per GEMM call type
@@ -2332,6 +2334,61 @@ void gemm_rows(q3t_dev * c, int kind, int site, ms::GemmArgs a) {
                            gemm_lds(kind, nt, a.K), c->stream);
 }
 
+// F16 layers: the four decode GEMMs of a layer on ms::k_gemm_h, 16-row tiles,
+// K split up to 8 ways (kHKB chunks of 32 per wave at most).
+enum HKind { H_QKV = 0, H_WO = 1, H_GATE_UP = 2, H_DOWN = 3 };
+constexpr int kHKB[4] = {1, 2, 1, 3};
+
+template <int NT, int KIND>
+const void * hgemm_kernel() {
+    if (KIND == H_QKV) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_NORM, ms::OUT_F32, kHKB[H_QKV]>;
+    if (KIND == H_WO) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_ROUND, ms::OUT_RESID, kHKB[H_WO]>;
+    if (KIND == H_GATE_UP)
+        return (const void *) ms::k_gemm_h<NT, 1, true, ms::IN_NORM, ms::OUT_SWIGLU_F32, kHKB[H_GATE_UP]>;
+    return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_WIDE, ms::OUT_RESID, kHKB[H_DOWN]>;
+}
+
+template <int KIND>
+const void * hgemm_kernel_nt(int nt) {
+    switch (nt) {
+        case 1: return hgemm_kernel<1, KIND>();
+        case 2: return hgemm_kernel<2, KIND>();
+        case 3: return hgemm_kernel<3, KIND>();
+        default: return hgemm_kernel<4, KIND>();
+    }
+}
+
+const void * hgemm_fn(int kind, int nt) {
+    switch (kind) {
+        case H_QKV: return hgemm_kernel_nt<H_QKV>(nt);
+        case H_WO: return hgemm_kernel_nt<H_WO>(nt);
+        case H_GATE_UP: return hgemm_kernel_nt<H_GATE_UP>(nt);
+        default: return hgemm_kernel_nt<H_DOWN>(nt);
+    }
+}
+
+// K splits of an F16 contraction of nb 32-element chunks: the largest S <= 8
+// with nb % (4 S) == 0 and at most kHKB chunks per wave; 0 if none.
+int hgemm_splits(int kind, int nb) {
+    for (int S = 8; S >= 1; S >>= 1)
+        if (nb % (ms::kWaves * S) == 0 && nb / (ms::kWaves * S) <= kHKB[kind]) return S;
+    return 0;
+}
+
+size_t hgemm_part_words(int kind, int nt, int N, int K) {
+    const int nw = kind == H_GATE_UP ? 2 : 1;
+    return (size_t) (N / ms::kRows) * hgemm_splits(kind, K / kQK) * 2 * nw * nt * 4 * 64;
+}
+
+void hgemm_rows(q3t_dev * c, int kind, int site, ms::GemmArgs a) {
+    const int nt = (a.n + 15) / 16;
+    const int S = hgemm_splits(kind, a.K / kQK);
+    a.part = c->spart[site]; a.cnt = c->scnt[site]; a.err = c->serr;
+    void * args[] = {(void *) &a};
+    (void) hipLaunchKernel(hgemm_fn(kind, nt), dim3(a.N / ms::kRows, S), dim3(ms::kThreads), args,
+                           ms::gemm_h_lds_bytes(nt, 1, kind == H_GATE_UP), c->stream);
+}
+
 // Contraction length of each decode GEMM kind: the normed inputs are model
 // rows (d), the projections read attention or SwiGLU rows.
 int gemm_k(int kind, int d, int kproj) { return kind == G_PROJ ? kproj : d; }
@@ -2373,6 +2430,33 @@ void attn_gqa(q3t_dev * c, const LayerDev & L, const StreamKV & kv) {
     hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, kv.n_ctx), c->stream, a);
 }
 
+// The layer's attention over the QKV rows in c->bqkv: the talker's GQA kernel
+// for one token per stream; for the code predictor's 16-position cache the
+// per-head kernel over nt tokens.  Output rows (fp32) in c->batt, Q8_0 copies
+// in c->bq8 / c->bdx8.
+static void stream_attention(q3t_dev * c, const LayerDev & L, int nt, const StreamKV & kv) {
+    const q3t_config & g = c->cfg;
+    const int qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    if (kv.pos_ptr && nt == 1) {
+    attn_gqa(c, L, kv);
+    return;
+    }
+    AttnArgs a{};
+    a.qkv = c->bqkv; a.qkv_stride = qkvd; a.qkv_stream = nt * qkvd;
+    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
+    a.rope_cos = kv.rc; a.rope_sin = kv.rs;
+    a.kc = kv.kc; a.vc = kv.vc; a.n_ctx = kv.n_ctx; a.kv_stream = kv.stream;
+    a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
+    a.pos_ptr = kv.pos_ptr; a.pos_const = kv.pos_const; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.out = c->batt; a.out_stride = qd; a.out_stream = nt * qd;
+    a.out_q = c->bq8; a.out_dx = c->bdx8;
+    a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
+    a.scale = 1.0f / std::sqrt((float) g.head_dim);
+    a.nt = nt;
+    a.f32_new = kv.f32_prefill ? 1 : 0;
+    hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
+}
+
 // One decoder layer over n = nb * nt rows (stream-major); output rows in c->bxa.
 // The residual-producing GEMMs (Wo, down) also leave per-tile sums of squares
 // of their output rows, from which the next normed GEMM forms its RMSNorm
@@ -2395,24 +2479,7 @@ static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool 
     q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
     if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
     gemm_rows(c, G_QKV, S_QKV, q);
-    if (kv.pos_ptr && nt == 1) {
-        attn_gqa(c, L, kv);
-    } else {
-        AttnArgs a{};
-        a.qkv = c->bqkv; a.qkv_stride = qkvd; a.qkv_stream = nt * qkvd;
-        a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = g.rms_eps;
-        a.rope_cos = kv.rc; a.rope_sin = kv.rs;
-        a.kc = kv.kc; a.vc = kv.vc; a.n_ctx = kv.n_ctx; a.kv_stream = kv.stream;
-        a.n_head = g.n_head; a.n_kv_head = g.n_kv_head;
-        a.pos_ptr = kv.pos_ptr; a.pos_const = kv.pos_const; a.pos_stream = (int32_t) (sizeof(FrameState) / 4);
-        a.out = c->batt; a.out_stride = qd; a.out_stream = nt * qd;
-        a.out_q = c->bq8; a.out_dx = c->bdx8;
-        a.done = &c->sst[0].done; a.done_stream = (int32_t) (sizeof(FrameState) / 4);
-        a.scale = 1.0f / std::sqrt((float) g.head_dim);
-        a.nt = nt;
-        a.f32_new = kv.f32_prefill ? 1 : 0;
-        hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt, c->nb), dim3(kBlock), attn_lds_bytes(kv.n_ctx), c->stream, a);
-    }
+    stream_attention(c, L, nt, kv);
     ms::GemmArgs o{};
     o.W = (const int8_t *) L.wo.data; o.Wd = L.wo.scales; o.N = d; o.K = qd;
     o.q = c->bq8; o.qdx = c->bdx8; o.n = n; o.y = c->bxb; o.ys = d; o.res = x; o.rs = d;
@@ -2430,6 +2497,40 @@ static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool 
     dn.q = c->bq8; dn.qdx = c->bdx8; dn.n = n; dn.y = c->bxa; dn.ys = d; dn.res = c->bxb; dn.rs = d;
     if (fuse) dn.ss_out = c->sss[1];
     gemm_rows(c, G_PROJ, S_DOWN, dn);
+}
+
+// The same layer with F16 weights on the f64-MFMA decode GEMMs: inputs rounded
+// to fp16 as the batch-1 F16 GEMVs round them (the widened ffn_down takes the
+// fp32 SwiGLU rows in c->bff), row scales fused the same way.
+static void stream_layer_h(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv) {
+    const q3t_config & g = c->cfg;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
+    const int ffn = g.ffn_size, n = c->nb * nt, tiles = d / ms::kRows;
+    const bool fuse = tiles / 4 <= ms::kSsPer;
+    x_ss = x_ss && fuse;
+    if (!x_ss) row_scales(c, x, d, d, n);
+    ms::GemmArgs q{};
+    q.H = (const uint16_t *) L.qkv.data; q.N = qkvd; q.K = d;
+    q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
+    if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
+    hgemm_rows(c, H_QKV, S_QKV, q);
+    stream_attention(c, L, nt, kv);
+    ms::GemmArgs o{};
+    o.H = (const uint16_t *) L.wo.data; o.N = d; o.K = qd;
+    o.x = c->batt; o.xs = qd; o.n = n; o.y = c->bxb; o.ys = d; o.res = x; o.rs = d;
+    if (fuse) o.ss_out = c->sss[0];
+    hgemm_rows(c, H_WO, S_WO, o);
+    if (!fuse) row_scales(c, c->bxb, d, d, n);
+    ms::GemmArgs f{};
+    f.H = (const uint16_t *) L.wg.data; f.H2 = (const uint16_t *) L.wu.data; f.N = ffn; f.K = d;
+    f.x = c->bxb; f.xs = d; f.rscale = c->srs; f.norm_w = L.ffn_norm; f.n = n; f.y = c->bff; f.ys = ffn;
+    if (fuse) { f.ss_in = c->sss[0]; f.ss_tiles = tiles; f.eps = g.rms_eps; }
+    hgemm_rows(c, H_GATE_UP, S_GATE_UP, f);
+    ms::GemmArgs dn{};
+    dn.H = (const uint16_t *) L.wd.data; dn.N = d; dn.K = ffn;
+    dn.x = c->bff; dn.xs = ffn; dn.n = n; dn.y = c->bxa; dn.ys = d; dn.res = c->bxb; dn.rs = d;
+    if (fuse) dn.ss_out = c->sss[1];
+    hgemm_rows(c, H_DOWN, S_DOWN, dn);
 }
 
 static SampleArgs stream_sample_args(q3t_dev * c, int mode, int group) {
@@ -2469,7 +2570,7 @@ static void streams_frame_seq(q3t_dev * c) {
         for (int il = 0; il < g.cp_layers; ++il) {
             StreamKV kv{c->scpk + il * cp_lstride, c->scpv + il * cp_lstride, cp_lstride * g.cp_layers, 16,
                         c->cp_rope_cos, c->cp_rope_sin, nullptr, pos, step == 0};
-            stream_layer(c, c->cp[il], x, il > 0, nt, kv);
+            (c->s_f16 ? stream_layer_h : stream_layer)(c, c->cp[il], x, il > 0, nt, kv);
             x = c->bxa;
         }
         GemvSpec h{};
@@ -2486,7 +2587,7 @@ static void streams_frame_seq(q3t_dev * c) {
     for (int il = 0; il < g.n_layers; ++il) {
         StreamKV kv{c->skc + il * lstride, c->svc + il * lstride, lstride * g.n_layers, c->sb_ctx, c->rope_cos,
                     c->rope_sin, &c->sst[0].talker_pos, 0, false};
-        stream_layer(c, c->talker[il], x, il > 0, 1, kv);
+        (c->s_f16 ? stream_layer_h : stream_layer)(c, c->talker[il], x, il > 0, 1, kv);
         x = c->bxa;
     }
     GemvSpec h{};
@@ -2508,21 +2609,27 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     if (n_streams < 1 || n_streams > 32) return fail(c, "n_streams must be in [1, 32]");
     if (n_ctx < 1) return fail(c, "n_ctx must be > 0");
     if (c->kv_bf16) return fail(c, "multi-stream decode keeps an F16 talker cache (q3t_dev_kv_set_type F16 first)");
+    bool all_q8 = true, all_f16 = true;
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
-        if (L.qkv.type != Q3T_TYPE_Q8_0 || L.wo.type != Q3T_TYPE_Q8_0 || L.wg.type != Q3T_TYPE_Q8_0 ||
-            L.wu.type != Q3T_TYPE_Q8_0 || L.wd.type != Q3T_TYPE_Q8_0)
-            return fail(c, "multi-stream decode needs Q8_0 layer weights (int8 MFMA GEMMs)");
+        for (const Slot * w : {&L.qkv, &L.wo, &L.wg, &L.wu, &L.wd}) {
+            all_q8 = all_q8 && w->type == Q3T_TYPE_Q8_0;
+            all_f16 = all_f16 && w->type == Q3T_TYPE_F16;
+        }
     }
+    if (!all_q8 && !all_f16)
+        return fail(c, "multi-stream decode needs all layer weights Q8_0 (int8 MFMA GEMMs) or all F16 (f64 MFMA GEMMs)");
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
     const int G = g.n_kv_head > 0 ? g.n_head / g.n_kv_head : 0;
-    // decode GEMM: K a multiple of 8 waves x 32, at most 12 blocks per wave; N a multiple of 16
     // decode GEMMs: every contraction splits into 4-wave slices of at most KB
-    // blocks per wave; N a multiple of 16 (32 for gate/up)
-    if (g.head_dim != 128 || d % kQK || qd % kQK || g.ffn_size % kQK || !gemm_splits(G_QKV, d / kQK) ||
-        !gemm_splits(G_GATE_UP, d / kQK) || !gemm_splits(G_PROJ, qd / kQK) || !gemm_splits(G_PROJ, g.ffn_size / kQK) ||
-        qkvd % ms::kRows || d % ms::kRows || g.ffn_size % (2 * ms::kRows) || g.cp_ffn != g.ffn_size ||
-        g.cp_hidden != d || g.n_head % g.n_kv_head || !(G == 1 || G == 2 || G == 4))
+    // blocks (32-element chunks) per wave; N a multiple of 16 (Q8_0 gate/up: 32)
+    const bool splits_ok = all_q8 ? gemm_splits(G_QKV, d / kQK) && gemm_splits(G_GATE_UP, d / kQK) &&
+                                        gemm_splits(G_PROJ, qd / kQK) && gemm_splits(G_PROJ, g.ffn_size / kQK)
+                                  : hgemm_splits(H_QKV, d / kQK) && hgemm_splits(H_GATE_UP, d / kQK) &&
+                                        hgemm_splits(H_WO, qd / kQK) && hgemm_splits(H_DOWN, g.ffn_size / kQK);
+    if (g.head_dim != 128 || d % kQK || qd % kQK || g.ffn_size % kQK || !splits_ok || qkvd % ms::kRows ||
+        d % ms::kRows || g.ffn_size % (2 * ms::kRows) || g.cp_ffn != g.ffn_size || g.cp_hidden != d ||
+        g.n_head % g.n_kv_head || !(G == 1 || G == 2 || G == 4))
         return fail(c, "multi-stream decode: unsupported model widths");
     int max_lds = 0;
     HIP_OK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device));
@@ -2541,7 +2648,7 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     for (void * p : {(void *) c->skc, (void *) c->svc, (void *) c->scpk, (void *) c->scpv, (void *) c->sst,
                      (void *) c->sparams, (void *) c->sseen, (void *) c->sntrail, (void *) c->spad, (void *) c->shidden,
                      (void *) c->slogits, (void *) c->scplogits, (void *) c->sstage, (void *) c->bxa, (void *) c->bxb,
-                     (void *) c->bqkv, (void *) c->batt, (void *) c->bq8, (void *) c->bdx8, (void *) c->srs,
+                     (void *) c->bqkv, (void *) c->batt, (void *) c->bq8, (void *) c->bdx8, (void *) c->bff, (void *) c->srs,
                      (void *) c->serr, (void *) c->scodes, (void *) c->strail, (void *) c->sss[0], (void *) c->sss[1]})
         if (p) dev_free(c, p);
     for (int i = 0; i < 4; ++i) {
@@ -2560,16 +2667,19 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
         dev_alloc_t(c, &c->slogits, B * g.codec_vocab) || dev_alloc_t(c, &c->scplogits, B * g.cp_vocab) ||
         dev_alloc_t(c, &c->sstage, B * 2 * d) || dev_alloc_t(c, &c->bxa, rows * d) || dev_alloc_t(c, &c->bxb, rows * d) ||
         dev_alloc_t(c, &c->bqkv, rows * qkvd) || dev_alloc_t(c, &c->batt, rows * qd) ||
-        dev_alloc_t(c, &c->bq8, rows * std::max(qd, g.ffn_size)) ||
+        dev_alloc_t(c, &c->bq8, rows * std::max(qd, g.ffn_size)) || dev_alloc_t(c, &c->bff, rows * g.ffn_size) ||
         dev_alloc_t(c, &c->bdx8, rows * (std::max(qd, g.ffn_size) / kQK)) || dev_alloc_t(c, &c->srs, rows) ||
         dev_alloc_t(c, &c->sss[0], rows * (d / ms::kRows)) || dev_alloc_t(c, &c->sss[1], rows * (d / ms::kRows)))
         return -1;
     {
         // tickets and tags start at 0 (a tag is >= 1), zeroed here, outside any graph
         const int nt = (int) ((rows + 15) / 16);
-        const size_t words[4] = {gemm_part_words(G_QKV, nt, qkvd, d), gemm_part_words(G_PROJ, nt, d, qd),
-                                 gemm_part_words(G_GATE_UP, nt, g.ffn_size, d),
-                                 gemm_part_words(G_PROJ, nt, d, g.ffn_size)};
+        const size_t words[4] = {all_q8 ? gemm_part_words(G_QKV, nt, qkvd, d) : hgemm_part_words(H_QKV, nt, qkvd, d),
+                                 all_q8 ? gemm_part_words(G_PROJ, nt, d, qd) : hgemm_part_words(H_WO, nt, d, qd),
+                                 all_q8 ? gemm_part_words(G_GATE_UP, nt, g.ffn_size, d)
+                                        : hgemm_part_words(H_GATE_UP, nt, g.ffn_size, d),
+                                 all_q8 ? gemm_part_words(G_PROJ, nt, d, g.ffn_size)
+                                        : hgemm_part_words(H_DOWN, nt, d, g.ffn_size)};
         const size_t tiles = (size_t) std::max(qkvd, std::max(d, g.ffn_size)) / ms::kRows;
         for (int i = 0; i < 4; ++i) {
             const size_t nw = std::max(words[i], (size_t) 64);
@@ -2585,6 +2695,7 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     HIP_OK(hipMemsetAsync(c->scpk, 0, B * ckv * 2, c->stream));
     HIP_OK(hipMemsetAsync(c->scpv, 0, B * ckv * 2, c->stream));
     c->nb = n_streams;
+    c->s_f16 = all_f16;
     c->sb_ctx = n_ctx;
     c->s_emitted.assign(B, 0);
     return sync(c);

@@ -33,18 +33,20 @@ namespace q3t {
 namespace ms {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef double v4d __attribute__((ext_vector_type(4)));
 
 constexpr int kRows = 16;             // weight rows per MFMA tile (M)
 constexpr int kWaves = 4;             // waves per workgroup, each a part of the K slice
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxTok = 64;           // activation rows per launch (4 MFMA column tiles)
 
-enum GemmIn { IN_Q8 = 0, IN_NORM = 1 };
-enum GemmOut { OUT_F32 = 0, OUT_RESID = 1, OUT_SWIGLU_Q8 = 2 };
+enum GemmIn { IN_Q8 = 0, IN_NORM = 1, IN_ROUND = 2, IN_WIDE = 3 };
+enum GemmOut { OUT_F32 = 0, OUT_RESID = 1, OUT_SWIGLU_Q8 = 2, OUT_SWIGLU_F32 = 3 };
 
 struct GemmArgs {
     const int8_t * W; const uint16_t * Wd;     // [N][K] int8, [N][K/32] fp16 scales
     const int8_t * W2; const uint16_t * W2d;   // SwiGLU: the up matrix (W is gate)
+    const uint16_t * H; const uint16_t * H2;   // F16 weights [N][K] (k_gemm_h; H2: the up matrix)
     int32_t N, K;
     const int8_t * q; const float * qdx;       // IN_Q8: activation rows [n][K] int8, scales [n][K/32]
     const float * x; int32_t xs;               // IN_NORM: activation rows [n][xs] fp32
@@ -103,6 +105,75 @@ __device__ __forceinline__ long quant8(const float (&v)[8], float & dx) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) hi |= ((uint32_t) (int) rintf(v[4 + e] * id) & 0xffu) << (8 * e);
     return (long) (((uint64_t) hi << 32) | lo);
+}
+
+// Split-K exchange without fences (S > 1): every workgroup of a tile takes a
+// ticket; ticket / S + 1 tags this launch.  All but the last store their
+// partial as tagged 32-bit halves (relaxed agent-scope atomics) and return
+// false; the last adds the S partials in slice order (so the sum does not
+// depend on arrival order), polling each slot until its tags are current, and
+// returns true.  The writers hold their tickets already, so every wait ends;
+// a bounded poll count guards it anyway.  With S = 1 it returns true.
+template <int NV>
+__device__ __forceinline__ bool splitk_exchange(double (&acc)[NV], const GemmArgs & a, int tile, int s, int S,
+                                                int lane) {
+    if (S <= 1) return true;
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = (uint32_t) __builtin_amdgcn_readfirstlane((int) old);
+    const uint32_t tag = old / (uint32_t) S + 1u;
+    uint64_t * base = a.part + (size_t) tile * S * 2 * NV * 64;
+    if (old % (uint32_t) S != (uint32_t) (S - 1)) {
+        uint64_t * mine = base + (size_t) s * 2 * NV * 64;
+        const uint64_t th = (uint64_t) tag << 32;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            __hip_atomic_store(mine + (2 * v) * 64 + lane, th | (uint32_t) __double2loint(acc[v]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(mine + (2 * v + 1) * 64 + lane, th | (uint32_t) __double2hiint(acc[v]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return false;
+    }
+    bool dead = false;
+    constexpr int CH = NV < 8 ? NV : 8;          // values summed per pass over the slices
+#pragma unroll
+    for (int c0 = 0; c0 < NV; c0 += CH) {
+        double tot[CH];
+#pragma unroll
+        for (int v = 0; v < CH; ++v) tot[v] = 0.0;
+        for (int ss = 0; ss < S; ++ss) {
+            if (ss == s) {
+#pragma unroll
+                for (int v = 0; v < CH; ++v) tot[v] += acc[c0 + v];
+                continue;
+            }
+            const uint64_t * src = base + ((size_t) ss * 2 * NV + 2 * c0) * 64;
+            uint64_t w[2 * CH];
+#pragma unroll
+            for (int k = 0; k < 2 * CH; ++k)
+                w[k] = __hip_atomic_load(src + k * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            unsigned n = 0;
+            while (!dead) {
+                bool all = true;
+#pragma unroll
+                for (int k = 0; k < 2 * CH; ++k) all = all && (uint32_t) (w[k] >> 32) == tag;
+                if (__all(all)) break;
+                if (++n > kSkSpin) { dead = true; atomicExch(a.err, 1); break; }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int k = 0; k < 2 * CH; ++k)
+                    if ((uint32_t) (w[k] >> 32) != tag)
+                        w[k] = __hip_atomic_load(src + k * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int v = 0; v < CH; ++v)
+                tot[v] += __hiloint2double((int) (uint32_t) w[2 * v + 1], (int) (uint32_t) w[2 * v]);
+        }
+#pragma unroll
+        for (int v = 0; v < CH; ++v) acc[c0 + v] = tot[v];
+    }
+    return true;
 }
 
 // Y[t][r] = epi(sum_b fp16(dw[r][b]) * dx[t][b] * sum_k W[r][32b+k] q[t][32b+k]).
@@ -278,69 +349,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc[v] += spart[v * 64 + lane];
 
-    if (S > 1) {
-        // Split-K exchange without fences: every workgroup of the tile takes a
-        // ticket; ticket / S + 1 tags this launch.  All but the last store
-        // their partial as tagged 32-bit halves (relaxed agent-scope atomics);
-        // the last adds the S partials in slice order, polling each slot until
-        // its tags are current.  The writers hold their tickets already, so
-        // every wait ends; a bounded poll count guards it anyway.
-        uint32_t old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = (uint32_t) __builtin_amdgcn_readfirstlane((int) old);
-        const uint32_t tag = old / (uint32_t) S + 1u;
-        uint64_t * base = a.part + (size_t) tile * S * 2 * NV * 64;
-        if (old % (uint32_t) S != (uint32_t) (S - 1)) {
-            uint64_t * mine = base + (size_t) s * 2 * NV * 64;
-            const uint64_t th = (uint64_t) tag << 32;
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                __hip_atomic_store(mine + (2 * v) * 64 + lane, th | (uint32_t) __double2loint(acc[v]), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(mine + (2 * v + 1) * 64 + lane, th | (uint32_t) __double2hiint(acc[v]),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            return;
-        }
-        bool dead = false;
-        constexpr int CH = NV < 8 ? NV : 8;          // values summed per pass over the slices
-#pragma unroll
-        for (int c0 = 0; c0 < NV; c0 += CH) {
-            double tot[CH];
-#pragma unroll
-            for (int v = 0; v < CH; ++v) tot[v] = 0.0;
-            for (int ss = 0; ss < S; ++ss) {
-                if (ss == s) {
-#pragma unroll
-                    for (int v = 0; v < CH; ++v) tot[v] += acc[c0 + v];
-                    continue;
-                }
-                const uint64_t * src = base + ((size_t) ss * 2 * NV + 2 * c0) * 64;
-                uint64_t w[2 * CH];
-#pragma unroll
-                for (int k = 0; k < 2 * CH; ++k)
-                    w[k] = __hip_atomic_load(src + k * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                unsigned n = 0;
-                while (!dead) {
-                    bool all = true;
-#pragma unroll
-                    for (int k = 0; k < 2 * CH; ++k) all = all && (uint32_t) (w[k] >> 32) == tag;
-                    if (__all(all)) break;
-                    if (++n > kSkSpin) { dead = true; atomicExch(a.err, 1); break; }
-                    __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-                    for (int k = 0; k < 2 * CH; ++k)
-                        if ((uint32_t) (w[k] >> 32) != tag)
-                            w[k] = __hip_atomic_load(src + k * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-#pragma unroll
-                for (int v = 0; v < CH; ++v)
-                    tot[v] += __hiloint2double((int) (uint32_t) w[2 * v + 1], (int) (uint32_t) w[2 * v]);
-            }
-#pragma unroll
-            for (int v = 0; v < CH; ++v) acc[c0 + v] = tot[v];
-        }
-    }
+    if (!splitk_exchange<NV>(acc, a, tile, s, gridDim.y, lane)) return;
 
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -393,6 +402,207 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
             }
         }
     }
+}
+
+
+// F16 weights: Y[t][r] = epi(sum_k W[r][k] * x[t][k]) on v_mfma_f64_16x16x4f64,
+// the decode counterpart of the prefill's F16 GEMM.  The input rows are the
+// F16 contract's: IN_NORM RMSNorm'd (y = (x * scale) * w) and rounded to
+// fp16, IN_ROUND rounded to fp16, IN_WIDE fp32 as they are (the widened
+// ffn_down); fp16 x fp16 and fp16 x fp32 products are exact in fp64, so every
+// output is an fp64 sum of exact terms rounded to fp32 once, the numbers of
+// the batch-1 F16 GEMVs.
+//
+// Same workgroup shape and split-K exchange as k_gemm_sk: workgroup (tile, s)
+// owns MT 16-row tiles of W (and of H2), all n activation rows and K slice s,
+// wave w taking bpw 32-element chunks of it.  Lane layout (16x16x4 f64):
+// A[m = l%16][k = l/16] is activation row 16j + l%16, B[k = l/16][n = l%16]
+// weight row 16m + l%16, and step e (0..7) of a chunk gives lane group
+// k = l/16 the element 8k + e, so each lane loads 8 contiguous elements of
+// its weight row and of its activation row per chunk.  D element r of lane
+// l is activation row 16j + 4r + l/16, weight row 16m + l%16.  Epilogues:
+// OUT_F32, OUT_RESID (+ per-tile sums of squares of the output rows for the
+// next RMSNorm), OUT_SWIGLU_F32 (silu(gate) * up, fp32 rows).
+// Requires N % (16 MT) == 0, (K/32) % (4 S) == 0, K/32/S/4 <= KB, n <= 16 NT.
+template <int NT, int MT, bool DUAL, int IN, int OUT, int KB>
+__global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
+    constexpr int NW = DUAL ? 2 : 1;
+    constexpr int NA = NW * MT * NT;                  // 16 x 16 accumulators per lane
+    constexpr int NV = NA * 4;                        // fp64 partials per lane
+    extern __shared__ __align__(16) char smem[];
+    const int nb = a.K / kQK, S = gridDim.y, nbs = nb / S, bpw = nbs / kWaves;
+    double * spart = (double *) smem;                 // [2][NV][64]
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lm = lane & 15, lk = lane >> 4;
+    const int tile = blockIdx.x, s = blockIdx.y;
+    const int r0 = tile * (MT * kRows), b0 = s * nbs + wave * bpw;
+
+    // weights and activations of this wave's chunks, all in flight before any use
+    v4i wa[MT][KB], wb[DUAL ? MT : 1][KB];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const uint16_t * wr = a.H + (size_t) (r0 + 16 * m + lm) * a.K + 8 * lk;
+        const uint16_t * wr2 = DUAL ? a.H2 + (size_t) (r0 + 16 * m + lm) * a.K + 8 * lk : nullptr;
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+            if (i < bpw) {
+                wa[m][i] = *(const v4i *) (wr + (b0 + i) * kQK);
+                if (DUAL) wb[m][i] = *(const v4i *) (wr2 + (b0 + i) * kQK);
+            }
+    }
+    float4 xv[NT][KB][2];
+    float rsc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int tok = 16 * j + lm;
+        const bool ok = tok < a.n;
+        const float * xr = a.x + (size_t) (ok ? tok : 0) * a.xs + 8 * lk;
+        rsc[j] = 0.0f;
+        if (IN == IN_NORM) {
+            if (a.ss_in) {
+                // RMSNorm row scale from the producer's per-tile sums: lane
+                // group lk adds a quarter of the tiles in order, then a fixed
+                // pairwise tree ((q0 + q1) + (q2 + q3))
+                const int per = a.ss_tiles / 4;   // <= kSsPer (the host checks)
+                double sv[kSsPer];
+#pragma unroll
+                for (int i = 0; i < kSsPer; ++i)
+                    sv[i] = ok && i < per ? a.ss_in[(size_t) (lk * per + i) * a.n + tok] : 0.0;
+                double part = 0.0;
+#pragma unroll
+                for (int i = 0; i < kSsPer; ++i) part += sv[i];
+                part += __shfl_xor(part, 16);
+                part += __shfl_xor(part, 32);
+                const float mean = (float) (part / (double) a.K);
+                rsc[j] = ok ? 1.0f / sqrtf(mean + a.eps) : 0.0f;
+            } else {
+                rsc[j] = ok ? a.rscale[tok] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+            float4 u0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u1 = u0;
+            if (ok && i < bpw) {
+                u0 = *(const float4 *) (xr + (b0 + i) * kQK);
+                u1 = *(const float4 *) (xr + (b0 + i) * kQK + 4);
+            }
+            xv[j][i][0] = u0;
+            xv[j][i][1] = u1;
+        }
+    }
+
+    v4d acc[NA];
+#pragma unroll
+    for (int v = 0; v < NA; ++v) acc[v] = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+        if (i >= bpw) continue;
+        const int b = b0 + i;
+        // the chunk's activation values as the F16 contract rounds them
+        float av[NT][8];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const float4 u0 = xv[j][i][0], u1 = xv[j][i][1];
+            const float xs8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            if (IN == IN_NORM) {
+                const float * nw = a.norm_w + b * kQK + 8 * lk;
+                const float4 g0 = *(const float4 *) nw, g1 = *(const float4 *) (nw + 4);
+                const float gs8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) { const float sv = xs8[e] * rsc[j]; av[j][e] = round_f16(sv * gs8[e]); }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) av[j][e] = IN == IN_WIDE ? xs8[e] : round_f16(xs8[e]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            double bw[MT], bu[DUAL ? MT : 1];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const v4i & w4 = wa[m][i];
+                const uint32_t word = (uint32_t) w4[e >> 1];
+                bw[m] = (double) h2f((uint16_t) ((e & 1) ? (word >> 16) : (word & 0xffffu)));
+                if (DUAL) {
+                    const v4i & u4 = wb[m][i];
+                    const uint32_t uw = (uint32_t) u4[e >> 1];
+                    bu[DUAL ? m : 0] = (double) h2f((uint16_t) ((e & 1) ? (uw >> 16) : (uw & 0xffffu)));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const double ad = (double) av[j][e];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    acc[(0 * MT + m) * NT + j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad, bw[m], acc[(0 * MT + m) * NT + j], 0, 0, 0);
+                    if (DUAL)
+                        acc[(1 * MT + m) * NT + j] =
+                            __builtin_amdgcn_mfma_f64_16x16x4f64(ad, bu[DUAL ? m : 0], acc[(1 * MT + m) * NT + j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    double fl[NV];
+#pragma unroll
+    for (int v = 0; v < NA; ++v)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) fl[4 * v + r] = acc[v][r];
+
+    // fixed tree over the 4 waves: (0 + 2, 1 + 3), then (0 + 1)
+    if (wave >= 2) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) spart[((wave - 2) * NV + v) * 64 + lane] = fl[v];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) fl[v] += spart[(wave * NV + v) * 64 + lane];
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) spart[v * 64 + lane] = fl[v];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) fl[v] += spart[v * 64 + lane];
+    if (!splitk_exchange<NV>(fl, a, tile, s, S, lane)) return;
+
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * j + 4 * r + lk;
+            const bool ok = tok < a.n;
+            double sq = 0.0;   // this lane's square of row 16m + lm of token tok, summed over the tile's lanes below
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int row = r0 + 16 * m + lm;
+                const double g = fl[4 * ((0 * MT + m) * NT + j) + r];
+                float o;
+                if (OUT == OUT_SWIGLU_F32) {
+                    o = silu_q3t((float) g) * (float) fl[4 * (((NW - 1) * MT + m) * NT + j) + r];
+                } else {
+                    o = (float) g;
+                    if (OUT == OUT_RESID && ok) o = o + a.res[(size_t) tok * a.rs + row];
+                }
+                sq += (double) (o * o);
+                if (ok) a.y[(size_t) tok * a.ys + row] = o;
+            }
+            if (OUT == OUT_RESID && a.ss_out) {
+                // the tile's sum of squares of token tok: a fixed tree over its 16 lanes
+                sq += __shfl_xor(sq, 1);
+                sq += __shfl_xor(sq, 2);
+                sq += __shfl_xor(sq, 4);
+                sq += __shfl_xor(sq, 8);
+                if (ok && lm == 0) a.ss_out[(size_t) tile * a.n + tok] = sq;
+            }
+        }
+}
+
+__host__ __device__ constexpr size_t gemm_h_lds_bytes(int nt, int mt, bool dual) {
+    return (size_t) 2 * (dual ? 2 : 1) * mt * nt * 4 * 64 * 8;
 }
 
 // ------------------------------------------------------------- attention

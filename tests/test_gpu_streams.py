@@ -6,7 +6,9 @@ generate() produces for that utterance alone (src/tts_transformer.cpp:3007-3309
 is the per-utterance loop): the batched GEMMs, the per-stream attention and
 the per-stream samplers follow the same numerics contract as the batch-1 path.
 Streams differ in prompt length (ragged KV), max_len, sampling controls and
-seed, and stop at different frames.
+seed, and stop at different frames.  Q8_0 layers run the int8 MFMA decode
+GEMMs, F16 layers the f64 MFMA ones; both at the tiny shapes, and four
+streams at the full 0.6B shapes.
 """
 import sys
 
@@ -26,11 +28,13 @@ def say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-@pytest.fixture(scope="module")
-def tiny_q8():
+@pytest.fixture(scope="module", params=["q8_0", "f16"])
+def tiny_q8(request):
+    """The tiny model with Q8_0 layers (int8 MFMA decode GEMMs) or F16 layers
+    (f64 MFMA decode GEMMs)."""
     cfg = qcfg.tiny()
-    say("[gpu] streams: tiny q8_0 model")
-    w = Weights(cfg, "q8_0", seed=17, norm_mode="one")
+    say(f"[gpu] streams: tiny {request.param} model")
+    w = Weights(cfg, request.param, seed=17, norm_mode="one")
     dev = Device(cfg)
     dev.upload_weights(w)
     o = orc.Oracle(cfg, w, threads=8)
@@ -128,13 +132,18 @@ def test_streams_many_heads_rows(tiny_q8, n_streams):
     _run(cfg, dev, o, specs, chunk=5)
 
 
-def test_streams_reject_f16_layers():
+def test_streams_reject_mixed_layer_types():
+    """F16 layers take the f64 MFMA GEMMs and Q8_0 layers the int8 ones; a
+    model mixing the two in its layers is refused."""
     cfg = qcfg.tiny()
     w = Weights(cfg, "f16", seed=17, norm_mode="one")
+    wq = Weights(cfg, "q8_0", seed=17, norm_mode="one")
     dev = Device(cfg)
     dev.upload_weights(w)
+    name = next(n for n in wq.tensors if n.endswith("ffn_down.weight"))
+    dev.upload(name, *wq[name])
     try:
-        with pytest.raises(DeviceError, match="Q8_0"):
+        with pytest.raises(DeviceError, match="all layer weights"):
             dev.streams_reserve(2, 128)
     finally:
         dev.close()
@@ -155,6 +164,24 @@ def test_streams_argument_errors(tiny_q8):
     with pytest.raises(DeviceError, match="Context length"):
         dev.streams_begin([dict(trailing=tr, tts_pad=pad, n_past=10, max_len=60),
                            dict(trailing=tr, tts_pad=pad, n_past=10, max_len=4)])
+
+
+@pytest.mark.slow
+def test_streams_full_f16_4_streams():
+    """0.6B shapes, F16 layers on the f64 MFMA decode GEMMs: four streams
+    with ragged prompts, greedy, 16 frames."""
+    cfg = qcfg.full_06b()
+    say("[gpu] streams full 0.6B f16: synth + upload")
+    w = Weights(cfg, "f16", seed=5, norm_mode="one")
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    o = orc.Oracle(cfg, w, threads=8)
+    try:
+        specs = [dict(seed_prompt=40 + i, n_text=n, max_len=16, temperature=0.0, top_k=0)
+                 for i, n in enumerate([24, 9, 50, 13])]
+        _run(cfg, dev, o, specs, chunk=8)
+    finally:
+        dev.close()
 
 
 @pytest.mark.slow
