@@ -254,9 +254,10 @@ int  q3t_dev_frames_stats(q3t_dev * dev, double * gpu_us_out, int64_t * frames_o
  * The reference runs one utterance per TTSTransformer at batch 1; this is
  * the batched form of the same loop, each stream bit-identical to its own
  * q3t_dev_frames_* run (same weights, prompt rows, arguments and seed).
- * Every talker / code-predictor layer runs as one int8 MFMA GEMM over the
- * streams' rows, attention and the samplers as one block per stream.
- * Requires Q8_0 layer weights.
+ * Every talker / code-predictor layer runs as one MFMA GEMM over the
+ * streams' rows (int8 for Q8_0 layers, f64 for F16 layers), attention and
+ * the samplers as one block per stream.  Requires the layer weights to be all
+ * Q8_0 or all F16.
  *
  * streams_reserve allocates per-stream KV caches of n_ctx positions (and
  * re-reserves the context's own cache to n_ctx for the shared RoPE tables);
