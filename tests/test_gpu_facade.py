@@ -54,16 +54,30 @@ def icl_rows(o, cfg, text, ref_text, ref_codes, spk):
 def test_facade_matches_oracle(tmp_path, wtype, layout):
     """tiny_mtp: the 1.7B layout (code_pred.mtp_proj, a narrower code
     predictor) read from the GGUF keys and tensors."""
-    assert os.path.exists(BIN), "build() first"
     cfg = getattr(qcfg, layout)()
-    w = Weights(cfg, wtype, seed=31)
-    model = tmp_path / "tiny.gguf"
+    _facade_check(tmp_path, cfg, Weights(cfg, wtype, seed=31), wtype, layout, 20)
+
+
+@pytest.mark.slow
+def test_facade_full_06b_q8(tmp_path):
+    """The facade over a full-size Q8_0 0.6B GGUF file (about 1.3 GB: the
+    151,936-row text embedding, 28 + 5 layers, 16 heads) written with the
+    reference converter's names and key list: load_model, generate,
+    attention dump, predict_codes_autoregressive and generate_icl against the
+    oracle."""
+    cfg = qcfg.full_06b()
+    print("[gpu] facade full 0.6B q8_0: synth", file=sys.stderr, flush=True)
+    _facade_check(tmp_path, cfg, Weights(cfg, "q8_0", seed=31), "q8_0", "full_06b", 12)
+
+
+def _facade_check(tmp_path, cfg, w, wtype, layout, max_len):
+    assert os.path.exists(BIN), "build() first"
+    model = tmp_path / "model.gguf"
     gguf.write(str(model), cfg, w)
     rng = np.random.default_rng(32)
     text = rng.integers(0, cfg.text_vocab - 8, 26).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)
     ref_codes = np.concatenate([rng.integers(0, 2048, (6, 1)), rng.integers(0, 2048, (6, 15))], axis=1).astype(np.int32)
-    max_len = 20
     with open(tmp_path / "in.bin", "wb") as f:
         f.write(struct.pack("<i", len(text)) + text.tobytes() + spk.tobytes())
         f.write(struct.pack("<ii", max_len, ref_codes.shape[0]) + ref_codes.tobytes())
@@ -73,7 +87,7 @@ def test_facade_matches_oracle(tmp_path, wtype, layout):
     print(r.stdout, r.stderr, file=sys.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
     codes = np.fromfile(tmp_path / "codes.bin", np.int32).reshape(-1, 16)
-    o = orc.Oracle(cfg, w, threads=8)
+    o = orc.Oracle(cfg, w, threads=16)
     co, _ = o.generate(text, spk, max_len=max_len, temperature=0.0)
     assert np.array_equal(codes, co)
     # the ATTD file of set_attn_dump (src/tts_transformer.cpp:2978-3005):
