@@ -653,9 +653,11 @@ __global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, i
 // query width, talker FFN, code-predictor FFN) and layer weight type:
 // variant 1 / 3 = (1024, 1024, 2048, 3072, 3072), the 0.6B talker and code
 // predictor, Q8_0 / F16 layers; variant 2 / 4 = (256, 256, 512, 512, 512), the
-// small test shapes; 5 = the 0.6B Q8_0 shapes on the XCD-parallel layer
-// program; 6 = the 1.7B layout (2048, 1024, 2048, 6144, 3072) with
-// code_pred.mtp_proj, Q8_0; 7 = its small test form (512, 256, 512, 512, 512).
+// small test shapes; 5 / 8 = the 0.6B shapes on the XCD-parallel layer
+// program, Q8_0 / F16; 6 = the 1.7B layout (2048, 1024, 2048, 6144, 3072)
+// with code_pred.mtp_proj, Q8_0; 7 = its small test form (512, 256, 512, 512,
+// 512).
+bool fk_xcd(int variant) { return variant == 5 || variant == 8; }
 const void * fk_kernel(int variant) {
     switch (variant) {
         case 1: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_Q8, false>;
@@ -664,6 +666,7 @@ const void * fk_kernel(int variant) {
         case 5: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_Q8, true>;
         case 6: return (const void *) fk::k_frame<2048, 1024, 2048, 6144, 3072, W_Q8, false>;
         case 7: return (const void *) fk::k_frame<512, 256, 512, 512, 512, W_Q8, false>;
+        case 8: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_F16, true>;
         default: return (const void *) fk::k_frame<256, 256, 512, 512, 512, W_F16, false>;
     }
 }
@@ -792,13 +795,15 @@ int fk_prepare(q3t_dev * c) {
     if (chunk_len > fk::kMaxChunk || chunks > 128 || (size_t) grid * 512 > (size_t) fk::kPvSlots * fk::kSlot ||
         (g.n_head * 128 + grid - 1) / grid * 2 * chunks > 2 * fk::kMaxChunk)
         return 0;
-    // the XCD-parallel layer program: Q8_0 0.6B shapes, one workgroup per CU
-    // on 256 CUs, workgroups dealt round-robin over the 8 XCDs (Q3T_FRAME_XCD=0 turns it off)
-    bool xcd = variant == 1 && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0;
+    // the XCD-parallel layer program: 0.6B shapes (Q8_0 or F16), one
+    // workgroup per CU on 256 CUs, workgroups dealt round-robin over the 8
+    // XCDs (Q3T_FRAME_XCD=0 turns it off)
+    bool xcd = (variant == 1 || variant == 3) && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0;
     if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
     if (xcd && xcd_map_ok(c, grid, xcd)) return -1;
-    if (xcd) variant = 5;
-    bool tab = xcd;
+    if (xcd) variant = variant == 1 ? 5 : 8;
+    // the code predictor's layer-0 QKV table (Q8_0 layers)
+    bool tab = xcd && lt == Q3T_TYPE_Q8_0;
     if (const char * e = std::getenv("Q3T_CP_QKV_TABLE")) if (e[0] == '0') tab = false;
     if (tab && (!c->cp_tab || c->cp_tab_stale) && build_cp_tab(c)) return -1;
     c->fk_tab = tab;
@@ -1891,7 +1896,7 @@ int q3t_dev_code_pred(q3t_dev * c, const float * hidden, int32_t cb0, const q3t_
             // mtp_proj output in the 1.7B layout, the layers, the head): the
             // head's logits sit in its last slot
             const int mtp = g.cp_hidden != g.hidden_size ? 1 : 0;
-            const int stride = 2 + mtp + (c->fk_variant == 5 ? 15 : 5) * g.cp_layers, n = g.n_codebooks - 1;
+            const int stride = 2 + mtp + (fk_xcd(c->fk_variant) ? 15 : 5) * g.cp_layers, n = g.n_codebooks - 1;
             hipLaunchKernelGGL(k_untag_heads, dim3((n * g.cp_vocab + 255) / 256), dim3(256), 0, c->stream,
                                c->fk_arena, stride - 1, stride, n, g.cp_vocab, c->cp_logits);
         }
@@ -2869,7 +2874,7 @@ int q3t_dev_frames_stats(q3t_dev * c, double * gpu_us_out, int64_t * frames_out,
     if (!c) return -1;
     if (gpu_us_out) *gpu_us_out = c->run_us;
     if (frames_out) *frames_out = c->run_frames;
-    if (path_out) *path_out = c->stats_streams ? 2 : c->fk_ok ? (c->fk_variant == 5 ? 3 : 1) : 0;
+    if (path_out) *path_out = c->stats_streams ? 2 : c->fk_ok ? (fk_xcd(c->fk_variant) ? 3 : 1) : 0;
     return 0;
 }
 

@@ -620,7 +620,8 @@ __device__ __forceinline__ void res_prefetch16(F16Regs<K, DUAL> & R, const uint6
 // (WIDE = false) or kept fp32 (WIDE = true).
 template <int NT, int K, bool WIDE>
 __device__ __forceinline__ void f16_rows(const RowsT<NT, K> & v, Lds & L) {
-    constexpr int CHG = Geo<K>::CHG, G4 = Geo<K>::G4;
+    constexpr int CHG = kChg<K>, G4 = K / 4;
+    static_assert(K % kQK == 0, "whole 32-element blocks");
 #pragma unroll
     for (int c = 0; c < CHG; ++c) {
         const int g = (int) threadIdx.x + kT * c;
@@ -1937,6 +1938,131 @@ __device__ __forceinline__ void xq8_compute(const XRegs<KIND> & R, const Lds & L
     }
 }
 
+// F16 layers on the XCD-parallel program: a lane's 32-element block of each
+// of its rows as four 16-byte chunks (the same rows and lanes as XRegs).
+template <int KIND>
+struct XRegs16 {
+    int4 w[XGeo<KIND>::NG][4], u[XGeo<KIND>::DUAL ? XGeo<KIND>::NG : 1][4];
+    int o[XGeo<KIND>::NG];                 // output index of this lane's row, -1: none
+};
+
+template <int KIND, bool NTL>
+__device__ __forceinline__ void xf16_prefetch(XRegs16<KIND> & R, const uint16_t * W, const uint16_t * U) {
+    using G = XGeo<KIND>;
+    constexpr int BPR = G::K / kQK;
+    const int lir = (int) threadIdx.x & (G::LPR - 1);
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi) {
+        int r, o, k0;
+        const bool row = xrow<KIND>(gi, r, o, k0);
+        R.o[gi] = row ? o : -1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            R.w[gi][c] = make_int4(0, 0, 0, 0);
+            if (G::DUAL) R.u[G::DUAL ? gi : 0][c] = make_int4(0, 0, 0, 0);
+        }
+        if (!row || lir >= BPR) continue;
+        const int4 * wp = (const int4 *) (W + (size_t) r * G::KS + k0 + lir * kQK);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) R.w[gi][c] = gld4n<NTL>(wp + c);
+        if (G::DUAL) {
+            const int4 * up = (const int4 *) (U + (size_t) r * G::KS + k0 + lir * kQK);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) R.u[G::DUAL ? gi : 0][c] = gld4n<NTL>(up + c);
+        }
+    }
+}
+
+// xq8_compute for F16 weights: the input rows in L.hf (fp16, from f16_rows)
+// or, WIDE (the widened ffn_down), L.xw (fp32); each product exact in fp64
+// (fp16 x fp16 exact in fp32; fp16 x fp32 as the fp32 product plus its fma
+// residual), summed in fp64 as in f16_compute.  Same epilogues and outputs.
+template <int NT, int KIND, bool WIDE>
+__device__ __forceinline__ void xf16_compute(const XRegs16<KIND> & R, const Lds & L, uint64_t * out, int ts,
+                                             uint32_t out_tag) {
+    using G = XGeo<KIND>;
+    constexpr int BPR = G::K / kQK;
+    const int lir = (int) threadIdx.x & (G::LPR - 1), x = (int) blockIdx.x & 7;
+    const int b = lir < BPR ? lir : 0;
+    double acc[G::NG][NT], acc2[G::NG][NT];
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        int4 xp[NT];
+        float xa[WIDE ? NT : 1][8];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (WIDE) {
+                const float4 x0 = *(const float4 *) &L.xw[t][2 * c][b * 4];
+                const float4 x1 = *(const float4 *) &L.xw[t][2 * c + 1][b * 4];
+                float * xr = xa[WIDE ? t : 0];
+                xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w;
+                xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
+            } else {
+                xp[t] = *(const int4 *) &L.hf[t][c][b * 8];
+            }
+        }
+#pragma unroll
+        for (int gi = 0; gi < G::NG; ++gi) {
+            // the empty asm keeps the weights' conversions after the input barrier
+            int4 wv = R.w[gi][c], uv = R.u[G::DUAL ? gi : 0][c];
+            __asm__ volatile("" : "+v"(wv.x), "+v"(wv.y), "+v"(wv.z), "+v"(wv.w));
+            if (G::DUAL) __asm__ volatile("" : "+v"(uv.x), "+v"(uv.y), "+v"(uv.z), "+v"(uv.w));
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const float wf = WIDE ? h8(wv, jj) : 0.0f, uf = WIDE && G::DUAL ? h8(uv, jj) : 0.0f;
+                const _Float16 wh = h8h(wv, jj), uh = G::DUAL ? h8h(uv, jj) : (_Float16) 0.0f;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (WIDE) {
+                        const float xf = xa[WIDE ? t : 0][jj];
+                        const float pr = wf * xf, pe = fmaf(wf, xf, -pr);
+                        acc[gi][t] += (double) pr + (double) pe;
+                        if (G::DUAL) {
+                            const float qr = uf * xf, qe = fmaf(uf, xf, -qr);
+                            acc2[gi][t] += (double) qr + (double) qe;
+                        }
+                    } else {
+                        const _Float16 xh = h8h(xp[t], jj);
+                        acc[gi][t] += (double) hmul_exact(wh, xh);
+                        if (G::DUAL) acc2[gi][t] += (double) hmul_exact(uh, xh);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (lir >= BPR) {                       // lanes past the slice add nothing
+#pragma unroll
+        for (int gi = 0; gi < G::NG; ++gi)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G::NG; ++gi) {
+        if (R.o[gi] < 0) continue;          // wave-uniform
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const double a1 = group_sum_d(acc[gi][t], G::LPR);
+            const double a2 = G::DUAL ? group_sum_d(acc2[gi][t], G::LPR) : 0.0;
+            if (lir != 0) continue;
+            const int o = R.o[gi];
+            if (KIND == XK_QKV) {
+                lstore(out + t * ts + o, out_tag, (float) a1);
+            } else if (KIND == XK_GU) {
+                lstore(out + t * ts + o, out_tag, silu_q3t((float) a1) * (float) a2);
+            } else {
+                uint64_t * dst = out + ((size_t) (x * 2 + t) * 1024 + o) * 2;
+                tstore(dst, out_tag, __int_as_float(__double2loint(a1)));
+                tstore(dst + 1, out_tag, __int_as_float(__double2hiint(a1)));
+            }
+        }
+    }
+}
+
 // Rank j's 32 outputs of a device-wide partial slot: the 8 XCDs' fp64
 // partials added in XCD order and rounded once, plus the residual slice
 // L.rx, which takes the sum; the sums also go to the XCD-local row
@@ -1980,7 +2106,7 @@ __device__ __forceinline__ void xreduce(const Args & A, Lds & L, const uint64_t 
 // tab_row (code-predictor layer 0 of steps 1..14): the layer's QKV row from
 // the table, and rx_row the embedding row whose slice is the residual; the
 // QKV phase is skipped.
-template <int NT, bool TK>
+template <int NT, bool TK, int WT = W_Q8>
 __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, const LayerQ8 & W, int layer, bool cp,
                                                        int pos0, uint32_t tb, int & p, int p_in, const float * x_lds,
                                                        int & p_out, bool & dead, const float * tab_row = nullptr,
@@ -2000,7 +2126,9 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
         if (t < 32) L.rx[0][t] = h2f(gld(rx_row + 32 * j + t));
     } else {
         XRegs<XK_QKV> R;
-        xq8_prefetch<XK_QKV, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr);
+        XRegs16<XK_QKV> F;
+        if constexpr (WT == W_Q8) xq8_prefetch<XK_QKV, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr);
+        else xf16_prefetch<XK_QKV, TK>(F, (const uint16_t *) W.qkv, nullptr);
         NormT<D> nw;
         norm_prefetch<D>(W.attn_norm, nw);
         RowsT<NT, D> v;
@@ -2011,8 +2139,13 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
             load_tagged<NT, D, true>(ar + (size_t) p_in * kSlot + x * 2048, tb | p_in, v, dead, A.err, D);
         }
         rms_rows<NT, D>(v, nw, A.eps, L);
-        quant_rows<NT, D>(v, L);
-        xq8_compute<NT, XK_QKV>(R, L, qkv_l, 512, tb | p_qkv);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, D>(v, L);
+            xq8_compute<NT, XK_QKV>(R, L, qkv_l, 512, tb | p_qkv);
+        } else {
+            f16_rows<NT, D, false>(v, L);
+            xf16_compute<NT, XK_QKV, false>(F, L, qkv_l, 512, tb | p_qkv);
+        }
     }
     __syncthreads();
     // attention of KV head x
@@ -2051,12 +2184,19 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
     p += 4;
     {
         XRegs<XK_WO> R;
-        xq8_prefetch<XK_WO, TK>(R, W.wo, W.wo_d, nullptr, nullptr);
+        XRegs16<XK_WO> F;
+        if constexpr (WT == W_Q8) xq8_prefetch<XK_WO, TK>(R, W.wo, W.wo_d, nullptr, nullptr);
+        else xf16_prefetch<XK_WO, TK>(F, (const uint16_t *) W.wo, nullptr);
         RowsT<NT, 256> va;
         if (cp) load_lds<NT, 256>(&L.att[0][0], va, 256);
         else load_tagged<NT, 256, true>(ar + (size_t) p_att * kSlot + x * 1024, tb | p_att, va, dead, A.err, 256);
-        quant_rows<NT, 256>(va, L);
-        xq8_compute<NT, XK_WO>(R, L, ar + (size_t) p_wo * kSlot, 0, tb | p_wo);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, 256>(va, L);
+            xq8_compute<NT, XK_WO>(R, L, ar + (size_t) p_wo * kSlot, 0, tb | p_wo);
+        } else {
+            f16_rows<NT, 256, false>(va, L);
+            xf16_compute<NT, XK_WO, false>(F, L, ar + (size_t) p_wo * kSlot, 0, tb | p_wo);
+        }
     }
     __syncthreads();
     const int p_x1 = p;
@@ -2066,14 +2206,21 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
     const int p_gu = p++;
     {
         XRegs<XK_GU> R;
-        xq8_prefetch<XK_GU, TK>(R, W.wg, W.wg_d, W.wu, W.wu_d);
+        XRegs16<XK_GU> F;
+        if constexpr (WT == W_Q8) xq8_prefetch<XK_GU, TK>(R, W.wg, W.wg_d, W.wu, W.wu_d);
+        else xf16_prefetch<XK_GU, TK>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu);
         NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
         RowsT<NT, D> v;
         load_tagged<NT, D, true>(ar + (size_t) p_x1 * kSlot + x * 2048, tb | p_x1, v, dead, A.err, D);
         rms_rows<NT, D>(v, nw, A.eps, L);
-        quant_rows<NT, D>(v, L);
-        xq8_compute<NT, XK_GU>(R, L, ar + (size_t) p_gu * kSlot + x * 1024, 384, tb | p_gu);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, D>(v, L);
+            xq8_compute<NT, XK_GU>(R, L, ar + (size_t) p_gu * kSlot + x * 1024, 384, tb | p_gu);
+        } else {
+            f16_rows<NT, D, false>(v, L);
+            xf16_compute<NT, XK_GU, false>(F, L, ar + (size_t) p_gu * kSlot + x * 1024, 384, tb | p_gu);
+        }
     }
     __syncthreads();
     // down partial sums over the XCD's 384 FFN inputs -> device-wide
@@ -2081,11 +2228,19 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
     p += 4;
     {
         XRegs<XK_DN> R;
-        xq8_prefetch<XK_DN, TK>(R, W.wd, W.wd_d, nullptr, nullptr);
+        XRegs16<XK_DN> F;
+        if constexpr (WT == W_Q8) xq8_prefetch<XK_DN, TK>(R, W.wd, W.wd_d, nullptr, nullptr);
+        else xf16_prefetch<XK_DN, TK>(F, (const uint16_t *) W.wd, nullptr);
         RowsT<NT, 384> vh;
         load_tagged<NT, 384, true>(ar + (size_t) p_gu * kSlot + x * 1024, tb | p_gu, vh, dead, A.err, 384);
-        quant_rows<NT, 384>(vh, L);
-        xq8_compute<NT, XK_DN>(R, L, ar + (size_t) p_dn * kSlot, 0, tb | p_dn);
+        if constexpr (WT == W_Q8) {
+            quant_rows<NT, 384>(vh, L);
+            xq8_compute<NT, XK_DN>(R, L, ar + (size_t) p_dn * kSlot, 0, tb | p_dn);
+        } else {
+            // ffn_down widened to F32: the fp32 SwiGLU rows as they are
+            f16_rows<NT, 384, true>(vh, L);
+            xf16_compute<NT, XK_DN, true>(F, L, ar + (size_t) p_dn * kSlot, 0, tb | p_dn);
+        }
     }
     __syncthreads();
     const int p_x2 = p;
@@ -2238,9 +2393,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 const float * tab_row =
                     tabl ? A.cp_qkv0 + ((size_t) (s - 1) * A.cp_vocab + code) * (size_t) (QD + QD) : nullptr;
                 const uint16_t * rx_row = tabl ? A.cp_embd[s - 1] + (size_t) code * D : nullptr;
-                if (nt == 2) layer_x<2, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
-                else if (tk) layer_x<1, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
-                else layer_x<1, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead, tab_row, rx_row);
+                if (nt == 2) layer_x<2, false, WT>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else if (tk) layer_x<1, true, WT>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);
+                else layer_x<1, false, WT>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead, tab_row, rx_row);
             } else {
                 if (nt == 2) layer_t<2, DC, QD, FFC, WT, false>(A, L, Wl, l, true, pos0, tb, p, p_in, x_lds, p_out, dead);
                 else if (tk) layer_t<1, D, QD, FF, WT, true>(A, L, Wl, l, false, pos0, tb, p, p_in, x_lds, p_out, dead);

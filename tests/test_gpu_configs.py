@@ -87,7 +87,7 @@ def prefill_kv(dev, o, cfg, rng, n_pos):
 @pytest.fixture(params=["persistent", "persistent_rows", "graph"])
 def path(request, monkeypatch):
     """The persistent frame kernel (default: with the XCD-parallel layer
-    program for Q8_0 0.6B models), the persistent kernel with its
+    program for 0.6B models), the persistent kernel with its
     row-parallel layer program (Q3T_FRAME_XCD=0), or the captured
     multi-kernel sequences (Q3T_FRAME_KERNEL=0); chosen when a context first
     runs."""
@@ -97,10 +97,13 @@ def path(request, monkeypatch):
 
 
 def check_path(dev, want, wtype="f16"):
+    """graph: 0; persistent_rows: the row-parallel program (1); persistent:
+    the XCD-parallel program (3), which the 0.6B shapes take with Q8_0 and F16
+    layers alike."""
     _, _, used = dev.frames_stats()
     if want == "graph":
         assert used == 0, (want, used)
-    elif want == "persistent_rows" or wtype == "f16":
+    elif want == "persistent_rows":
         assert used == 1, (want, wtype, used)
     else:
         assert used == 3, (want, wtype, used)

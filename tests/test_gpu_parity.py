@@ -386,7 +386,7 @@ def test_long_context_persistent_matches_graph(wtype, monkeypatch):
     try:
         dev.kv_reserve(2100 + 16)
         # (Q3T_FRAME_KERNEL, Q3T_FRAME_XCD) -> the path frames_stats reports
-        variants = [("1", "1", 3 if wtype == "q8_0" else 1), ("1", "0", 1), ("0", "1", 0)]
+        variants = [("1", "1", 3), ("1", "0", 1), ("0", "1", 0)]
         for kern, xcd, want in variants:
             monkeypatch.setenv("Q3T_FRAME_KERNEL", kern)
             monkeypatch.setenv("Q3T_FRAME_XCD", xcd)
