@@ -200,6 +200,8 @@ def step_bench(args, cfg, w):
     for _ in range(steps):
         dev.talker_step(x, n_kv)
     dt = (time.perf_counter() - t0) / steps
+    step_path = {0: "multi-kernel step", 1: "persistent-kernel step (row-parallel program)",
+                 3: "persistent-kernel step (XCD-parallel program)"}.get(dev.frames_stats()[2], "?")
     kernels = {}
     names = {0: "gemv_gate_up_swiglu", 1: "gemv_qkv_rmsnorm", 2: "gemv_down_resid", 3: "gemv_wo_resid",
              4: "attention_decode"}
@@ -216,8 +218,7 @@ def step_bench(args, cfg, w):
         "higher_is_better": False, "dtype": "int8" if args.weights == "q8_0" else "f16",
         "data": f"synthetic (seeded weights, N(0,1) bfloat16-valued K/V in a {args.kv} cache)",
         "config": {"workload": f"one talker decode step, {args.weights.upper()} 0.6B shapes, {args.kv} KV pre-filled to "
-                               f"{n_kv} positions, " + ("persistent-kernel step" if args.kv == "f16" else
-                                                        "multi-kernel step") + " with host copy-back",
+                               f"{n_kv} positions, {step_path} with host copy-back",
                    "global_batch": 1, "kv_type": args.kv},
         "step_algorithmic_bytes": int(wbytes + kvbytes),
         "step_hbm_gbs": round((wbytes + kvbytes) / dt / 1e9, 1),

@@ -129,10 +129,10 @@ int32_t q3t_dev_kv_capacity(const q3t_dev * dev);
  * type as a parameter for timing configuration 2.  With BF16, q and the
  * softmax probabilities are rounded to bfloat16 where the F16 cache rounds
  * them to fp16 (ggml_mul_mat's conversion of its F32 operand to the cache's
- * dot type).  A reserved cache is re-reserved (cleared).  BF16 runs the
- * multi-kernel path (single steps, prefill, frame loop); the persistent frame
- * kernel and multi-stream decode take F16 only.  q3t_dev_kv_write rows are
- * then bfloat16 bits. */
+ * dot type).  A reserved cache is re-reserved (cleared).  Single steps,
+ * prefill and the frame loop (persistent kernel or multi-kernel) take either
+ * type; multi-stream decode takes F16 only.  q3t_dev_kv_write rows are then
+ * bfloat16 bits. */
 int  q3t_dev_kv_set_type(q3t_dev * dev, int32_t type);
 /* Attention-row capture, the device side of set_attn_dump / attn_rows
  * (src/tts_transformer.h:224-227; rows captured in forward_step,

@@ -729,9 +729,8 @@ int build_cp_tab(q3t_dev * c);   // below, with the prefill helpers it uses
 
 int fk_prepare(q3t_dev * c) {
     c->fk_ok = false;
-    // attention capture runs the multi-kernel step; the persistent kernel
-    // reads an fp16 talker cache only
-    if (c->fk_refused || c->attn_layer >= 0 || c->kv_bf16) return 0;
+    // attention capture runs the multi-kernel step
+    if (c->fk_refused || c->attn_layer >= 0) return 0;
     if (const char * e = std::getenv("Q3T_FRAME_KERNEL")) if (e[0] == '0') return 0;
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
@@ -848,7 +847,7 @@ fk::Args fk_args(q3t_dev * c) {
     A.talker = c->fk_layers; A.cp = c->fk_layers + g.n_layers;
     A.n_layers = g.n_layers; A.cp_layers = g.cp_layers; A.d = g.hidden_size; A.n_head = g.n_head;
     A.n_kv_head = g.n_kv_head; A.ffn = g.ffn_size; A.cp_ffn = g.cp_ffn; A.codec_vocab = g.codec_vocab;
-    A.cp_vocab = g.cp_vocab; A.eos_id = g.codec_eos_id; A.n_ctx = c->n_ctx;
+    A.cp_vocab = g.cp_vocab; A.eos_id = g.codec_eos_id; A.n_ctx = c->n_ctx; A.kv_bf16 = c->kv_bf16 ? 1 : 0;
     A.eps = g.rms_eps; A.attn_scale = 1.0f / std::sqrt((float) g.head_dim);
     A.codec_embd = (const uint16_t *) c->codec_embd.data;
     for (int i = 0; i < 15; ++i) {

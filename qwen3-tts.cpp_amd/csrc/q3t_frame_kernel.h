@@ -58,6 +58,7 @@ struct LayerQ8 {
 struct Args {
     const LayerQ8 * talker; const LayerQ8 * cp;
     int32_t n_layers, cp_layers, d, n_head, n_kv_head, ffn, cp_ffn, codec_vocab, cp_vocab, eos_id, n_ctx;
+    int32_t kv_bf16;                         // talker cache of bfloat16 values (else fp16)
     float eps, attn_scale;
     const uint16_t * codec_embd;
     const uint16_t * cp_embd[15];
@@ -1132,6 +1133,7 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
     float * knew = L.a + 2 * 128;          // [128]
     float * vnew = knew + 128;             // [128]
     const size_t base = ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
+    const bool bf = A.kv_bf16 != 0;       // bfloat16 cache: q, K, V (and P) rounded to bfloat16
     {
         const int col = XL ? wave * 128 : wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
@@ -1152,21 +1154,21 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
             const float a0 = y0 * rcv, b0 = y1 * rsv, a1 = y0 * rsv, b1 = y1 * rcv;
             const float o0 = a0 - b0, o1 = a1 + b1;
             if (wave < 2) {
-                qf[wave * 128 + lane] = round_f16(o0);
-                qf[wave * 128 + lane + 64] = round_f16(o1);
+                qf[wave * 128 + lane] = round_kv(o0, bf);
+                qf[wave * 128 + lane + 64] = round_kv(o1, bf);
             } else {
-                const uint16_t h0 = f2h(o0), h1 = f2h(o1);
-                knew[lane] = h2f(h0);
-                knew[lane + 64] = h2f(h1);
+                const uint16_t h0 = f2kv(o0, bf), h1 = f2kv(o1, bf);
+                knew[lane] = kv2f(h0, bf);
+                knew[lane + 64] = kv2f(h1, bf);
                 if (writer) {
                     gst(A.kc + base + (size_t) pos0 * 128 + lane, h0);
                     gst(A.kc + base + (size_t) pos0 * 128 + lane + 64, h1);
                 }
             }
         } else {
-            const uint16_t h0 = f2h(x0), h1 = f2h(x1);
-            vnew[lane] = h2f(h0);
-            vnew[lane + 64] = h2f(h1);
+            const uint16_t h0 = f2kv(x0, bf), h1 = f2kv(x1, bf);
+            vnew[lane] = kv2f(h0, bf);
+            vnew[lane + 64] = kv2f(h1, bf);
             if (writer) {
                 gst(A.vc + base + (size_t) pos0 * 128 + lane, h0);
                 gst(A.vc + base + (size_t) pos0 * 128 + lane + 64, h1);
@@ -1199,9 +1201,9 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
         } else {
             const uint16_t * kh = (const uint16_t *) &kk;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kv[e] = h2f(kh[e]);
+            for (int e = 0; e < 8; ++e) kv[e] = kv2f(kh[e], bf);
         }
-        // fp16 x fp16 products are exact in fp64: fma rounds like mul + add
+        // fp16 x fp16 (bfloat16 x bfloat16) products are exact in fp64: fma rounds like mul + add
         double a0 = 0.0, a1 = 0.0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -1298,8 +1300,8 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
     const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
     const int n = s.j1 - s.j0;
     for (int j = t; j < n; j += kT) {
-        L.sc[j] = round_f16(L.sc[j] * inv0);
-        L.sc[kMaxChunk + j] = round_f16(L.sc[kMaxChunk + j] * inv1);
+        L.sc[j] = round_kv(L.sc[j] * inv0, A.kv_bf16 != 0);
+        L.sc[kMaxChunk + j] = round_kv(L.sc[kMaxChunk + j] * inv1, A.kv_bf16 != 0);
     }
     __syncthreads();
     const int sub = lane & 15;
@@ -1327,7 +1329,7 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
             } else {
                 const uint16_t * vh = (const uint16_t *) &vv4;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vv[e] = h2f(vh[e]);
+                for (int e = 0; e < 8; ++e) vv[e] = kv2f(vh[e], A.kv_bf16 != 0);
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1465,12 +1467,12 @@ __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, 
     for (int u = 0; u < 4; ++u) {
         const int j = t + u * kT;
         if (j < n_kv) {
-            const double p0 = (double) round_f16(L.sc[j] * inv0), p1 = (double) round_f16(L.sc[kMaxChunk + j] * inv1);
+            const double p0 = (double) round_kv(L.sc[j] * inv0, A.kv_bf16 != 0), p1 = (double) round_kv(L.sc[kMaxChunk + j] * inv1, A.kv_bf16 != 0);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 if (d >= dpw) break;
                 // fp16 probability x fp16 value: exact in fp64
-                const double vd = (double) (j == pos0 ? vnew[c * dpw + d] : h2f(P.v[u][d]));
+                const double vd = (double) (j == pos0 ? vnew[c * dpw + d] : kv2f(P.v[u][d], A.kv_bf16 != 0));
                 o[0][d] = fma(p0, vd, o[0][d]);
                 o[1][d] = fma(p1, vd, o[1][d]);
             }

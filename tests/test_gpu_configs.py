@@ -122,6 +122,9 @@ def test_config2_f16_talker_step_kv512(path):
             assert np.abs(lg - lo).max() <= LOGIT_TOL
             assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
             assert np.array_equal(hg, ho)
+        cg, co = _frames_both(dev, o, cfg, lo, 515, 4, seed=60)
+        check_path(dev, path)
+        assert cg.shape == (4, 16) and np.array_equal(cg, co)
     finally:
         dev.close()
 
@@ -152,10 +155,11 @@ def test_context_past_12288_f16(path):
         dev.close()
 
 
-def test_config2_bf16_kv_step():
+def test_config2_bf16_kv_step(path):
     """Configuration 2 with a bfloat16 talker cache (q3t_dev_kv_set_type):
     N(0,1) bfloat16 K/V at 512 positions, then steps at 512.. on the
-    multi-kernel step, bit for bit the oracle's bfloat16 form."""
+    persistent kernel's step mode (either layer program) or the multi-kernel
+    step, bit for bit the oracle's bfloat16 form; then 4 sampled frames."""
     cfg, w, dev, o = open_pair("f16", 51, 528)
     try:
         dev.kv_set_type(30)
@@ -176,6 +180,9 @@ def test_config2_bf16_kv_step():
             lo, ho = o.step(e, 512 + s)
             assert np.array_equal(lg, lo), f"step {s}: max diff {np.abs(lg - lo).max()}"
             assert np.array_equal(hg, ho)
+        cg, co = _frames_both(dev, o, cfg, lo, 515, 4, seed=60)
+        check_path(dev, path)
+        assert cg.shape == (4, 16) and np.array_equal(cg, co)
     finally:
         dev.close()
 

@@ -256,10 +256,11 @@ def test_attention_capture_matches_oracle(tiny_model, frame_path):
         o.set_attn_capture(-1)
 
 
-def test_bf16_kv_prefill_steps_frames(prefill_path):
+def test_bf16_kv_prefill_steps_frames(prefill_path, frame_path):
     """A bfloat16 talker cache: prefill (GEMV or MFMA path), single steps and
-    a greedy frame loop (multi-kernel), each bit for bit the oracle's
-    bfloat16 form; the fp16 cache gives other logits on the same inputs."""
+    a greedy and a sampled frame loop (persistent kernel or multi-kernel),
+    each bit for bit the oracle's bfloat16 form; the fp16 cache gives other
+    logits on the same inputs."""
     cfg = qcfg.tiny()
     w, dev, o = make(cfg, "q8_0", seed=41)
     try:
@@ -286,7 +287,10 @@ def test_bf16_kv_prefill_steps_frames(prefill_path):
         text = rng.integers(0, cfg.text_vocab - 8, 18).astype(np.int32)
         co, _ = o.generate(text, None, max_len=16, temperature=0.0, top_k=0)
         cg = driver.generate(dev, cfg, text, None, max_len=16, temperature=0.0, top_k=0, chunk=8)
-        assert dev.frames_stats()[2] == 0
+        check_path(dev, "q8_0", frame_path)
+        assert np.array_equal(cg, co)
+        co, _ = o.generate(text, None, max_len=12, temperature=0.9, top_k=50, seed=3)
+        cg = driver.generate(dev, cfg, text, None, max_len=12, temperature=0.9, top_k=50, seed=3, chunk=5)
         assert np.array_equal(cg, co)
     finally:
         dev.close()
