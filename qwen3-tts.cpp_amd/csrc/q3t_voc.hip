@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -276,10 +277,17 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
     a.act = act;
     a.ea = sn ? sn->ea : nullptr;
     a.eb = sn ? sn->eb : nullptr;
-    // tile: the largest (32 WM channels x 32 WN rows per workgroup) that
-    // still gives the launch a workgroup per CU; a smaller WM
-    // divides the weights' padded width (SwiGLU pairs need WM even)
-    int WM = W.WM, WN = 4;
+    // tile: the largest (32 WM channels x 32 WN rows per workgroup, WN at
+    // most 2: measured faster than 4 over a streaming window, 3.13 against
+    // 3.51 ms) that still gives the launch a workgroup per CU; a smaller WM
+    // divides the weights' padded width (SwiGLU pairs need WM even).
+    // Q3T_VOC_WN=1/2/4 sets the largest WN.
+    static const int wn_max = [] {
+        const char * e = std::getenv("Q3T_VOC_WN");
+        const int v = e ? std::atoi(e) : 2;
+        return v == 1 || v == 4 ? v : 2;
+    }();
+    int WM = W.WM, WN = wn_max;
     auto wgs = [&](int wm, int wn) {
         return (int64_t) (W.Np / (32 * wm)) * ((M + 32 * wn - 1) / (32 * wn)) * W.phases;
     };
