@@ -298,6 +298,16 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
         else break;
     }
     const dim3 grid((unsigned) (W.Np / (32 * WM)), (unsigned) ((M + 32 * WN - 1) / (32 * WN)), (unsigned) W.phases);
+    // a launch that cannot fill the CUs (the 73-row pre-transformer GEMMs)
+    // stages 4 K chunks per step: a quarter of the serial load-and-barrier
+    // round trips of its K loop
+    const bool ks4 = wgs(WM, WN) < v->n_cu && WN == 1 && WM <= 2 && W.KT * (W.Cp / 32) >= 8;
+    if (ks4) {
+        if (WM == 2) hipLaunchKernelGGL((k_conv_gemm<2, 1, 4>), grid, dim3(kGemmT), 0, v->stream, a);
+        else hipLaunchKernelGGL((k_conv_gemm<1, 1, 4>), grid, dim3(kGemmT), 0, v->stream, a);
+        HIP_OK(hipGetLastError());
+        return 0;
+    }
 #define Q3T_VOC_GEMM(wm, wn) hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a)
 #define Q3T_VOC_GEMM_WN(wm)                   \
     switch (WN) {                             \

@@ -65,11 +65,15 @@ constexpr int kGemmT = 256;    // 4 waves: 2 along channels x 2 along time
 // matrix cores.  MFMA lane layout (16x16x32): A[m = l%16][k = 8(l/16)..+7]
 // (weights, m = channel), B[k][n = l%16] (activations, n = time row),
 // D[m = 4(l/16)+e][n = l%16].  The SwiGLU pairing needs WM even.
-template <int WM, int WN>
+// KS chunks (of 32 K elements) per step: KS = 4 for the small launches (the
+// 73-row pre-transformer GEMMs), whose K loop of 16-32 steps would otherwise
+// be a chain of load-and-barrier round trips.
+template <int WM, int WN, int KS = 1>
 struct GemmTile {
     static constexpr int BC = 32 * WM, BT = 32 * WN;
     static constexpr int NA = (BC * 4 + kGemmT - 1) / kGemmT, NB = (BT * 4 + kGemmT - 1) / kGemmT;
-    static constexpr int STAGE = (BC + BT) * 32;                    // halfs per stage
+    static constexpr int SUB = (BC + BT) * 32;                      // halfs per chunk
+    static constexpr int STAGE = KS * SUB;                          // halfs per stage
     static constexpr int TS = WM * 16 + 4;                          // epilogue row stride (floats)
     static constexpr int LDS_STAGE = 2 * STAGE * 2, LDS_EPI = 4 * 16 * TS * 4;
     static constexpr int LDS = LDS_STAGE > LDS_EPI ? LDS_STAGE : LDS_EPI;
@@ -77,9 +81,9 @@ struct GemmTile {
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chunk ^ (row & 3)) << 3); }
 
-template <int WM, int WN>
+template <int WM, int WN, int KS = 1>
 __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
-    using G = GemmTile<WM, WN>;
+    using G = GemmTile<WM, WN, KS>;
     __shared__ __align__(16) char smem[G::LDS];
     uint16_t * lds = (uint16_t *) smem;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     const int phase = blockIdx.z;
     const int cb0 = blockIdx.x * G::BC, tb0 = blockIdx.y * G::BT;
     const uint16_t * wbase = A.w + (size_t) phase * A.Np * A.KT * A.Cp;
-    const int CB = A.Cp >> 5, S = A.KT * CB;
+    const int CB = A.Cp >> 5, NCH = A.KT * CB, S = (NCH + KS - 1) / KS;
 
     // this thread's 16-byte chunks of the A (weights) and B (activations) tiles
     const uint16_t * ga[G::NA];
@@ -112,27 +116,35 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
         cbk[r] = col * 8;
         lb[r] = G::BC * 32 + swz(row, col);
     }
-    uint4 ra[G::NA], rb[G::NB];
+    uint4 ra[KS][G::NA], rb[KS][G::NB];
     auto fetch = [&](int s) {
-        const int tap = s / CB, cc = (s - tap * CB) * 32;
 #pragma unroll
-        for (int r = 0; r < G::NA; ++r)
-            ra[r] = oa[r] ? *(const uint4 *) (ga[r] + (size_t) tap * A.Cp + cc) : make_uint4(0, 0, 0, 0);
+        for (int q = 0; q < KS; ++q) {
+            const int ch = s * KS + q;               // chunks past the end load zeros
+            const int tap = ch / CB, cc = (ch - tap * CB) * 32;
 #pragma unroll
-        for (int r = 0; r < G::NB; ++r) {
-            const int src = tb[r] + tap * A.dil;
-            rb[r] = (src >= 0 && src < A.rows_in) ? *(const uint4 *) (A.x + (size_t) src * A.xs + cc + cbk[r])
-                                                  : make_uint4(0, 0, 0, 0);
+            for (int r = 0; r < G::NA; ++r)
+                ra[q][r] = oa[r] && ch < NCH ? *(const uint4 *) (ga[r] + (size_t) tap * A.Cp + cc) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < G::NB; ++r) {
+                const int src = tb[r] + tap * A.dil;
+                rb[q][r] = (ch < NCH && src >= 0 && src < A.rows_in)
+                               ? *(const uint4 *) (A.x + (size_t) src * A.xs + cc + cbk[r])
+                               : make_uint4(0, 0, 0, 0);
+            }
         }
     };
     auto stash = [&](int buf) {
-        uint16_t * st = lds + buf * G::STAGE;
 #pragma unroll
-        for (int r = 0; r < G::NA; ++r)
-            if (oa[r]) *(uint4 *) (st + la[r]) = ra[r];
+        for (int q = 0; q < KS; ++q) {
+            uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
 #pragma unroll
-        for (int r = 0; r < G::NB; ++r)
-            if (ob[r]) *(uint4 *) (st + lb[r]) = rb[r];
+            for (int r = 0; r < G::NA; ++r)
+                if (oa[r]) *(uint4 *) (st + la[r]) = ra[q][r];
+#pragma unroll
+            for (int r = 0; r < G::NB; ++r)
+                if (ob[r]) *(uint4 *) (st + lb[r]) = rb[q][r];
+        }
     };
 
     v4f acc[WM][WN];
@@ -147,16 +159,20 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     for (int s = 0; s < S; ++s) {
         const int buf = s & 1;
         if (s + 1 < S) fetch(s + 1);
-        const uint16_t * st = lds + buf * G::STAGE;
-        v8h af[WM], bf[WN];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) af[i] = *(const v8h *) (st + swz(wc * WM * 16 + i * 16 + lm, lk));
+        for (int q = 0; q < KS; ++q) {
+            const uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
+            v8h af[WM], bf[WN];
 #pragma unroll
-        for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (st + G::BC * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
+            for (int i = 0; i < WM; ++i) af[i] = *(const v8h *) (st + swz(wc * WM * 16 + i * 16 + lm, lk));
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
+            for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (st + G::BC * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
 #pragma unroll
-            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
         if (s + 1 < S) stash(buf ^ 1);
         __syncthreads();
     }

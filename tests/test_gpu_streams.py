@@ -159,6 +159,16 @@ def test_streams_argument_errors(tiny_q8):
         dev.stream_prefill(2, emb)
     with pytest.raises(DeviceError, match="Context length"):
         dev.stream_prefill(0, np.zeros((65, cfg.hidden_size), np.float32))
+    with pytest.raises(DeviceError, match="Context length"):
+        dev.stream_prefill(0, emb, n_past=61)
+    kv = np.zeros((8, cfg.n_kv_head, cfg.head_dim), np.float16)
+    with pytest.raises(DeviceError, match="out of range"):
+        dev.stream_kv_write(2, 0, kv, kv)
+    with pytest.raises(DeviceError, match="out of range"):
+        dev.stream_kv_write(0, cfg.n_layers, kv, kv)
+    with pytest.raises(DeviceError, match="out of range"):
+        big = np.zeros((65, cfg.n_kv_head, cfg.head_dim), np.float16)
+        dev.stream_kv_write(1, 0, big, big)
     pad = np.zeros(cfg.hidden_size, np.float32)
     tr = np.zeros((1, cfg.hidden_size), np.float32)
     with pytest.raises(DeviceError, match="Context length"):
