@@ -1121,7 +1121,7 @@ __device__ __forceinline__ void att_prefetch(const Args & A, int layer, const At
 // XL (XCD-parallel layers): q, k, v come from this XCD's local QKV region
 // ([q0 q1 k v]), and the scores or maxima go to XCD-local regions per KV
 // head (maxima at g * 64 + 2c + h).
-template <bool XL>
+template <bool XL, bool KB = false>
 __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & L, const LayerQ8 & W, int layer,
                                                           int pos0, int qd, const AttSplit & s, const KvPre & P,
                                                           const uint64_t * qkv, uint32_t qkv_tag, uint64_t * out,
@@ -1133,7 +1133,7 @@ __device__ __attribute__((always_inline)) void att_scores(const Args & A, Lds & 
     float * knew = L.a + 2 * 128;          // [128]
     float * vnew = knew + 128;             // [128]
     const size_t base = ((size_t) layer * A.n_kv_head + g) * A.n_ctx * 128;
-    const bool bf = A.kv_bf16 != 0;       // bfloat16 cache: q, K, V (and P) rounded to bfloat16
+    constexpr bool bf = KB;               // bfloat16 cache: q, K, V (and P) rounded to bfloat16
     {
         const int col = XL ? wave * 128 : wave < 2 ? (g * 2 + wave) * 128 : wave == 2 ? qd + g * 128 : qd + kd + g * 128;
         const float * nwp = wave < 2 ? W.q_norm : W.k_norm;
@@ -1278,7 +1278,7 @@ __device__ __attribute__((always_inline)) void att_sums(const Args & A, Lds & L,
     }
 }
 
-template <bool XL>
+template <bool XL, bool KB = false>
 __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, int layer, int pos0,
                                                       const AttSplit & s, const KvPre & P, const uint64_t * in,
                                                       uint32_t in_tag, uint64_t * out, uint32_t out_tag,
@@ -1300,8 +1300,8 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
     const float inv0 = (float) (1.0 / sum0), inv1 = (float) (1.0 / sum1);
     const int n = s.j1 - s.j0;
     for (int j = t; j < n; j += kT) {
-        L.sc[j] = round_kv(L.sc[j] * inv0, A.kv_bf16 != 0);
-        L.sc[kMaxChunk + j] = round_kv(L.sc[kMaxChunk + j] * inv1, A.kv_bf16 != 0);
+        L.sc[j] = round_kv(L.sc[j] * inv0, KB);
+        L.sc[kMaxChunk + j] = round_kv(L.sc[kMaxChunk + j] * inv1, KB);
     }
     __syncthreads();
     const int sub = lane & 15;
@@ -1329,7 +1329,7 @@ __device__ __attribute__((always_inline)) void att_pv(const Args & A, Lds & L, i
             } else {
                 const uint16_t * vh = (const uint16_t *) &vv4;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vv[e] = kv2f(vh[e], A.kv_bf16 != 0);
+                for (int e = 0; e < 8; ++e) vv[e] = kv2f(vh[e], KB);
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1402,7 +1402,7 @@ __device__ __forceinline__ void att2_prefetch(const Args & A, int layer, int pos
 
 // XL: the scores come from XCD-local regions, and the attention rows of the
 // head pair go to this XCD's local region (out [h * 128 + d]).
-template <bool XL>
+template <bool XL, bool KB = false>
 __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, int pos0, const KvCols & P,
                                                        const uint64_t * scores, uint32_t sc_tag, uint64_t * out,
                                                        uint32_t out_tag, bool & dead) {
@@ -1467,12 +1467,12 @@ __device__ __attribute__((always_inline)) void att2_pv(const Args & A, Lds & L, 
     for (int u = 0; u < 4; ++u) {
         const int j = t + u * kT;
         if (j < n_kv) {
-            const double p0 = (double) round_kv(L.sc[j] * inv0, A.kv_bf16 != 0), p1 = (double) round_kv(L.sc[kMaxChunk + j] * inv1, A.kv_bf16 != 0);
+            const double p0 = (double) round_kv(L.sc[j] * inv0, KB), p1 = (double) round_kv(L.sc[kMaxChunk + j] * inv1, KB);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 if (d >= dpw) break;
                 // fp16 probability x fp16 value: exact in fp64
-                const double vd = (double) (j == pos0 ? vnew[c * dpw + d] : kv2f(P.v[u][d], A.kv_bf16 != 0));
+                const double vd = (double) (j == pos0 ? vnew[c * dpw + d] : kv2f(P.v[u][d], KB));
                 o[0][d] = fma(p0, vd, o[0][d]);
                 o[1][d] = fma(p1, vd, o[1][d]);
             }
@@ -1621,6 +1621,19 @@ __device__ __attribute__((always_inline)) int32_t sample_cp(const Args & A, Lds 
     return code;
 }
 
+// The talker attention for the context's cache type, chosen once per call
+// (KB: bfloat16 cache) rather than per element.
+#define Q3T_KV_TYPED(...)                       \
+    do {                                        \
+        if (A.kv_bf16) {                        \
+            constexpr bool KB = true;           \
+            __VA_ARGS__;                        \
+        } else {                                \
+            constexpr bool KB = false;          \
+            __VA_ARGS__;                        \
+        }                                       \
+    } while (0)
+
 // ------------------------------------------------------------------ layers
 // One decoder layer (QKV -> attention -> Wo + residual -> gate/up SwiGLU ->
 // down + residual) for NT tokens.  The input rows come from tagged slot p_in,
@@ -1685,23 +1698,23 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         const int p_a = p;
         p += 2 + kPvSlots;
         p_att = p++;
-        att_scores<false>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
-                   ar + (size_t) p_a * kSlot, tb | p_a, dead, ar + (size_t) p_a * kSlot);
+        Q3T_KV_TYPED(att_scores<false, KB>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+                   ar + (size_t) p_a * kSlot, tb | p_a, dead, ar + (size_t) p_a * kSlot));
         __syncthreads();
-        att2_pv<false>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot, tb | p_att, dead);
+        Q3T_KV_TYPED(att2_pv<false, KB>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot, tb | p_att, dead));
         __syncthreads();
     } else {
         const AttSplit sp = att_split(A, pos0 + 1);
         const int p_a = p++, p_b = p++, p_c = p;
         p += kPvSlots;
         p_att = p++;
-        att_scores<false>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
-                   ar + (size_t) p_a * kSlot, tb | p_a, dead);
+        Q3T_KV_TYPED(att_scores<false, KB>(A, L, W, layer, pos0, QD, sp, kv, ar + (size_t) p_qkv * kSlot, tb | p_qkv,
+                   ar + (size_t) p_a * kSlot, tb | p_a, dead));
         __syncthreads();
         att_sums<false>(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
         __syncthreads();
-        att_pv<false>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot, tb | p_c,
-               dead);
+        Q3T_KV_TYPED(att_pv<false, KB>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot, tb | p_c,
+               dead));
         __syncthreads();
         att_combine<false>(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot, tb | p_att, dead);
     }
@@ -2160,23 +2173,23 @@ __device__ __attribute__((always_inline)) void layer_x(const Args & A, Lds & L, 
         const int p_a = p;
         p += 2 + kPvSlots;
         p_att = p++;
-        att_scores<true>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead,
-                         ar + (size_t) p_a * kSlot);
+        Q3T_KV_TYPED(att_scores<true, KB>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead,
+                         ar + (size_t) p_a * kSlot));
         __syncthreads();
-        att2_pv<true>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot + x * 1024,
-                      tb | p_att, dead);
+        Q3T_KV_TYPED(att2_pv<true, KB>(A, L, pos0, kc2, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_att * kSlot + x * 1024,
+                      tb | p_att, dead));
         __syncthreads();
     } else {
         const AttSplit sp = att_split(A, pos0 + 1);
         const int p_a = p++, p_b = p++, p_c = p;
         p += kPvSlots;
         p_att = p++;
-        att_scores<true>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead);
+        Q3T_KV_TYPED(att_scores<true, KB>(A, L, W, layer, pos0, QD, sp, kv, qkv_l, tb | p_qkv, ar + (size_t) p_a * kSlot, tb | p_a, dead));
         __syncthreads();
         att_sums<true>(A, L, sp, ar + (size_t) p_a * kSlot, tb | p_a, ar + (size_t) p_b * kSlot, tb | p_b, dead);
         __syncthreads();
-        att_pv<true>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot,
-                     tb | p_c, dead);
+        Q3T_KV_TYPED(att_pv<true, KB>(A, L, layer, pos0, sp, kv, ar + (size_t) p_b * kSlot, tb | p_b, ar + (size_t) p_c * kSlot,
+                     tb | p_c, dead));
         __syncthreads();
         att_combine<true>(A, L, ar + (size_t) p_c * kSlot, tb | p_c, ar + (size_t) p_att * kSlot + x * 1024, tb | p_att,
                           dead);
