@@ -801,8 +801,8 @@ int fk_prepare(q3t_dev * c) {
     if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
     if (xcd && xcd_map_ok(c, grid, xcd)) return -1;
     if (xcd) variant = variant == 1 ? 5 : 8;
-    // the code predictor's layer-0 QKV table (Q8_0 layers)
-    bool tab = xcd && lt == Q3T_TYPE_Q8_0;
+    // the code predictor's layer-0 QKV table
+    bool tab = xcd;
     if (const char * e = std::getenv("Q3T_CP_QKV_TABLE")) if (e[0] == '0') tab = false;
     if (tab && (!c->cp_tab || c->cp_tab_stale) && build_cp_tab(c)) return -1;
     c->fk_tab = tab;
@@ -1440,12 +1440,17 @@ __global__ __launch_bounds__(256) void k_h2f(const uint16_t * __restrict__ in, s
 // codec_embd.s[code] (the input of codebook step s + 1): RMSNorm, Q8_0
 // activation quantisation and the int8 GEMM of the prefill path, whose rows
 // equal the frame kernel's GEMV bit for bit.  Rebuilt after any upload.
+void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, int xs, bool wide, float * y,
+                 const float * res, int rs);
+
 int build_cp_tab(q3t_dev * c) {
     const q3t_config & g = c->cfg;
     const int d = g.cp_hidden, V = g.cp_vocab, ncb = g.n_codebooks - 1;
     const int qkvd = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
     const LayerDev & L = c->cp[0];
-    if (L.qkv.type != Q3T_TYPE_Q8_0 || d != g.hidden_size) return fail(c, "cp QKV table needs Q8_0 layers");
+    const bool q8 = L.qkv.type == Q3T_TYPE_Q8_0;
+    if ((!q8 && L.qkv.type != Q3T_TYPE_F16) || d != g.hidden_size)
+        return fail(c, "cp QKV table needs Q8_0 or F16 layers");
     if (!c->cp_tab && dev_alloc_t(c, &c->cp_tab, (size_t) ncb * V * qkvd)) return -1;
     if (ensure_pf(c, V)) return -1;
     const size_t n = (size_t) V * d;
@@ -1453,8 +1458,16 @@ int build_cp_tab(q3t_dev * c) {
         if (c->cp_embd[sidx].type != Q3T_TYPE_F16) return fail(c, "embedding tables must be F16");
         hipLaunchKernelGGL(k_h2f, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, c->stream,
                            (const uint16_t *) c->cp_embd[sidx].data, n, c->pf_xa);
-        pf_quant(c, c->pf_xa, V, d, L.attn_norm);
-        pf_gemm(c, L.qkv, qkvd, d, V, c->cp_tab + (size_t) sidx * V * qkvd, nullptr);
+        float * rows = c->cp_tab + (size_t) sidx * V * qkvd;
+        if (q8) {
+            pf_quant(c, c->pf_xa, V, d, L.attn_norm);
+            pf_gemm(c, L.qkv, qkvd, d, V, rows, nullptr);
+        } else {
+            // RMSNorm, then the exact F16 GEMM on fp16-rounded rows (the GEMV's numbers)
+            hipLaunchKernelGGL(k_rmsnorm_rows, dim3(V), dim3(kBlock), 0, c->stream, (const float *) c->pf_xa,
+                               L.attn_norm, g.rms_eps, d, c->pf_f);
+            pf_gemm_f16(c, L.qkv, qkvd, d, V, c->pf_f, d, false, rows, nullptr, 0);
+        }
     }
     HIP_OK(hipStreamSynchronize(c->stream));
     c->cp_tab_stale = false;
