@@ -168,6 +168,7 @@ struct q3t_dev {
     // table lookup ([15][cp_vocab][qkv width] fp32, XCD-parallel program only)
     float * cp_tab = nullptr;
     bool cp_tab_stale = true;
+    bool s_tab = false;                // multi-stream code-predictor layer 0 from cp_tab (steps 1..14)
     hipEvent_t run_ev[2] = {nullptr, nullptr};
     uint8_t * copy_buf = nullptr;      // copy-kernel calibration buffers (time_kernel class 5)
     double run_us = 0.0;
@@ -2447,6 +2448,28 @@ void attn_gqa(q3t_dev * c, const LayerDev & L, const StreamKV & kv) {
     hipLaunchKernelGGL(ms::k_attn_gqa<1>, grid, block, ms::attn_gqa_lds_bytes(1, kv.n_ctx), c->stream, a);
 }
 
+// Code-predictor layer 0 of step s (1..14) for every stream: the QKV row of
+// the stream's input code (sampled into its frame state by the previous
+// step) copied from the per-code table, in place of RMSNorm + the QKV GEMM
+// (the table rows equal the GEMM's bit for bit).
+__global__ __launch_bounds__(256) void k_cp_tab_rows(const float * __restrict__ tab, int32_t V, int32_t qkvd,
+                                                      int32_t step, const FrameState * __restrict__ st,
+                                                      float * __restrict__ out) {
+    const int b = blockIdx.x;
+    int code = st[b].codes[step];
+    code = code < 0 ? 0 : code >= V ? V - 1 : code;     // a finished stream's row is never used
+    const float4 * src = (const float4 *) (tab + ((size_t) (step - 1) * V + code) * qkvd);
+    float4 * dst = (float4 *) (out + (size_t) b * qkvd);
+    for (int i = threadIdx.x; i < qkvd / 4; i += 256) dst[i] = src[i];
+}
+
+static void cp_tab_rows(q3t_dev * c, int step) {
+    const q3t_config & g = c->cfg;
+    const int qkvd = (g.n_head + 2 * g.n_kv_head) * g.head_dim;
+    hipLaunchKernelGGL(k_cp_tab_rows, dim3(c->nb), dim3(256), 0, c->stream, (const float *) c->cp_tab, g.cp_vocab,
+                       qkvd, step, (const FrameState *) c->sst, c->bqkv);
+}
+
 // The layer's attention over the QKV rows in c->bqkv: the talker's GQA kernel
 // for one token per stream; for the code predictor's 16-position cache the
 // per-head kernel over nt tokens.  Output rows (fp32) in c->batt, Q8_0 copies
@@ -2484,18 +2507,23 @@ static void stream_attention(q3t_dev * c, const LayerDev & L, int nt, const Stre
 // per-head kernel over nt tokens).  Activations pass between them as fp32
 // residual rows (RMSNorm + quantisation inside the consuming GEMM) or as
 // Q8_0 rows quantised by the producer (attention output, SwiGLU output).
-static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv) {
+static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv,
+                        int tab_step = 0) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int ffn = g.ffn_size, n = c->nb * nt, tiles = d / ms::kRows;
     const bool fuse = tiles / 4 <= ms::kSsPer;   // row scales from the producer's per-tile sums
     x_ss = x_ss && fuse;
-    if (!x_ss) row_scales(c, x, d, d, n);
-    ms::GemmArgs q{};
-    q.W = (const int8_t *) L.qkv.data; q.Wd = L.qkv.scales; q.N = qkvd; q.K = d;
-    q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
-    if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
-    gemm_rows(c, G_QKV, S_QKV, q);
+    if (tab_step > 0) {
+        cp_tab_rows(c, tab_step);
+    } else {
+        if (!x_ss) row_scales(c, x, d, d, n);
+        ms::GemmArgs q{};
+        q.W = (const int8_t *) L.qkv.data; q.Wd = L.qkv.scales; q.N = qkvd; q.K = d;
+        q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
+        if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
+        gemm_rows(c, G_QKV, S_QKV, q);
+    }
     stream_attention(c, L, nt, kv);
     ms::GemmArgs o{};
     o.W = (const int8_t *) L.wo.data; o.Wd = L.wo.scales; o.N = d; o.K = qd;
@@ -2519,18 +2547,23 @@ static void stream_layer(q3t_dev * c, const LayerDev & L, const float * x, bool 
 // The same layer with F16 weights on the f64-MFMA decode GEMMs: inputs rounded
 // to fp16 as the batch-1 F16 GEMVs round them (the widened ffn_down takes the
 // fp32 SwiGLU rows in c->bff), row scales fused the same way.
-static void stream_layer_h(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv) {
+static void stream_layer_h(q3t_dev * c, const LayerDev & L, const float * x, bool x_ss, int nt, const StreamKV & kv,
+                        int tab_step = 0) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
     const int ffn = g.ffn_size, n = c->nb * nt, tiles = d / ms::kRows;
     const bool fuse = tiles / 4 <= ms::kSsPer;
     x_ss = x_ss && fuse;
-    if (!x_ss) row_scales(c, x, d, d, n);
-    ms::GemmArgs q{};
-    q.H = (const uint16_t *) L.qkv.data; q.N = qkvd; q.K = d;
-    q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
-    if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
-    hgemm_rows(c, H_QKV, S_QKV, q);
+    if (tab_step > 0) {
+        cp_tab_rows(c, tab_step);
+    } else {
+        if (!x_ss) row_scales(c, x, d, d, n);
+        ms::GemmArgs q{};
+        q.H = (const uint16_t *) L.qkv.data; q.N = qkvd; q.K = d;
+        q.x = x; q.xs = d; q.rscale = c->srs; q.norm_w = L.attn_norm; q.n = n; q.y = c->bqkv; q.ys = qkvd;
+        if (x_ss) { q.ss_in = c->sss[1]; q.ss_tiles = tiles; q.eps = g.rms_eps; }
+        hgemm_rows(c, H_QKV, S_QKV, q);
+    }
     stream_attention(c, L, nt, kv);
     ms::GemmArgs o{};
     o.H = (const uint16_t *) L.wo.data; o.N = d; o.K = qd;
@@ -2587,7 +2620,8 @@ static void streams_frame_seq(q3t_dev * c) {
         for (int il = 0; il < g.cp_layers; ++il) {
             StreamKV kv{c->scpk + il * cp_lstride, c->scpv + il * cp_lstride, cp_lstride * g.cp_layers, 16,
                         c->cp_rope_cos, c->cp_rope_sin, nullptr, pos, step == 0};
-            (c->s_f16 ? stream_layer_h : stream_layer)(c, c->cp[il], x, il > 0, nt, kv);
+            (c->s_f16 ? stream_layer_h : stream_layer)(c, c->cp[il], x, il > 0, nt, kv,
+                                                       c->s_tab && il == 0 && step > 0 ? step : 0);
             x = c->bxa;
         }
         GemvSpec h{};
@@ -2604,7 +2638,7 @@ static void streams_frame_seq(q3t_dev * c) {
     for (int il = 0; il < g.n_layers; ++il) {
         StreamKV kv{c->skc + il * lstride, c->svc + il * lstride, lstride * g.n_layers, c->sb_ctx, c->rope_cos,
                     c->rope_sin, &c->sst[0].talker_pos, 0, false};
-        (c->s_f16 ? stream_layer_h : stream_layer)(c, c->talker[il], x, il > 0, 1, kv);
+        (c->s_f16 ? stream_layer_h : stream_layer)(c, c->talker[il], x, il > 0, 1, kv, 0);
         x = c->bxa;
     }
     GemvSpec h{};
@@ -2713,6 +2747,10 @@ int q3t_dev_streams_reserve(q3t_dev * c, int32_t n_streams, int32_t n_ctx) {
     HIP_OK(hipMemsetAsync(c->scpv, 0, B * ckv * 2, c->stream));
     c->nb = n_streams;
     c->s_f16 = all_f16;
+    // code-predictor layer 0 of steps 1..14 from the per-code QKV table
+    // (built or refreshed at streams_begin; Q3T_CP_QKV_TABLE=0 turns it off)
+    c->s_tab = true;
+    if (const char * e = std::getenv("Q3T_CP_QKV_TABLE")) if (e[0] == '0') c->s_tab = false;
     c->sb_ctx = n_ctx;
     c->s_emitted.assign(B, 0);
     return sync(c);
@@ -2772,6 +2810,8 @@ int q3t_dev_streams_begin(q3t_dev * c, const q3t_frame_args * args) {
     if (c->nb < 1) return fail(c, "q3t_dev_streams_reserve first");
     if (c->n_ctx != c->sb_ctx) return fail(c, "KV cache re-reserved since q3t_dev_streams_reserve; reserve the streams again");
     HIP_OK(hipSetDevice(c->device));
+    // the table keeps its address when rebuilt, so a captured frame graph stays valid
+    if (c->s_tab && (!c->cp_tab || c->cp_tab_stale) && build_cp_tab(c)) return -1;
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, B = c->nb;
     int max_len = 0, max_trail = 1;
