@@ -1481,11 +1481,18 @@ int build_cp_tab(q3t_dev * c) {
 void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float * x, int xs, bool wide, float * y,
                  const float * res, int rs) {
     static const int kc_env = [] { const char * e = std::getenv("Q3T_PF_F16_KC"); return e ? std::atoi(e) : 0; }();
+    const char * te = std::getenv("Q3T_PF_F16_TAIL");   // read per call (tests switch it)
+    const bool tail_off = te && te[0] == '0';
     const int kc = (kc_env == 32 || K % 64) ? 32 : 64;
-    const dim3 grid(N / pf::kTile, (n + pf::kTile - 1) / pf::kTile);
+    // a remainder of at most 32 tokens goes to 16-row tail workgroups
+    // (Q3T_PF_F16_TAIL=0 keeps it in a partial 64-token tile)
+    const int rem = n % pf::kTile;
+    const bool tail = rem != 0 && rem <= 32 && !tail_off;
+    const int nfull = tail ? n / pf::kTile : (n + pf::kTile - 1) / pf::kTile;
+    const dim3 grid((unsigned) ((N / pf::kTile) * nfull + (tail ? N / 16 : 0)));
 #define Q3T_PF_F16(wd, kcv)                                                                                       \
     hipLaunchKernelGGL((pf::k_gemm_f16<wd, kcv>), grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, N, K, \
-                       x, xs, n, y, N, res, rs)
+                       x, xs, n, y, N, res, rs, nfull)
     if (wide) {
         if (kc == 64) Q3T_PF_F16(true, 64); else Q3T_PF_F16(true, 32);
     } else {
@@ -1521,7 +1528,13 @@ int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uin
         if (dev_alloc_t(c, &c->pf_s, need) || dev_alloc_t(c, &c->pf_p, need)) return -1;
         c->pf_sp_cap = need;
     }
-    const dim3 tiles(g.n_head, ((n + pf::kAT - 1) / pf::kAT + 1) / 2, 2);   // tile pairs x position / dim halves
+    const int nt = (n + pf::kAT - 1) / pf::kAT;
+    // grid: heads x tile pairs x position / dim halves; an odd count's middle
+    // tile dealt out over the pairs' workgroups by both kernels
+    // (Q3T_PF_ATT_SPREAD=0 gives it a workgroup of its own)
+    const char * se = std::getenv("Q3T_PF_ATT_SPREAD");  // read per call (tests switch it)
+    const bool no_spread = se && se[0] == '0';
+    const dim3 tiles(g.n_head, (nt % 2 && nt >= 3 && !no_spread) ? nt / 2 : (nt + 1) / 2, 2);
     // q rows into the probabilities buffer's head (they are consumed before it is written)
     uint16_t * qh = c->pf_p;
     hipLaunchKernelGGL(pf::k_att_q, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd,

@@ -260,15 +260,82 @@ struct F16Tile {
     static constexpr int SP = KC / 4;          // elements staged per thread (4 threads per row)
 };
 
+// Tail workgroup of the F16 GEMM: 16 weight rows from r0 x the at most 32
+// tokens t0 .. n - 1, in 16-token groups.  The four waves take interleaved
+// 32-wide K slices straight from global memory (no staging), each keeps fp64
+// partials, and the partials are added in wave order through LDS, so the
+// result does not depend on timing.  A 1-row remainder then costs 1/16 of a
+// 64 x 64 tile instead of a whole one.
+template <bool WIDE>
+__device__ __forceinline__ void gemm_f16_tail(const uint16_t * __restrict__ W, int K, const float * __restrict__ x,
+                                              int xs, int n, int t0, int r0, float * __restrict__ Y, int ys,
+                                              const float * __restrict__ res, int rs, char * smem) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, lk = lane >> 4;
+    const int ng = (n - t0 + 15) >> 4;            // token groups: 1 or 2
+    const int ta = t0 + li, tb = t0 + 16 + li;
+    const bool oka = ta < n, okb = tb < n;        // rows past n read row n - 1 and multiply zeros
+    const uint16_t * wp = W + (size_t) (r0 + li) * K + 8 * lk;
+    const float * xa = x + (size_t) (oka ? ta : n - 1) * xs + 8 * lk;
+    const float * xb = x + (size_t) (okb ? tb : n - 1) * xs + 8 * lk;
+    v4d acc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
+    auto arow = [&](const float * xp, bool ok, int k0, double (&ad)[8]) {
+        const float4 p = *(const float4 *) (xp + k0), q = *(const float4 *) (xp + k0 + 4);
+        const float v[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ad[e] = ok ? (double) (WIDE ? v[e] : round_f16(v[e])) : 0.0;
+    };
+#pragma unroll 2
+    for (int k0 = 32 * wave; k0 < K; k0 += 128) {
+        const int4 wv = *(const int4 *) (wp + k0);
+        double ad[8];
+        arow(xa, oka, k0, ad);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            acc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[s], (double) h2f(h8bits(wv, s)), acc[0], 0, 0, 0);
+        if (ng > 1) {
+            arow(xb, okb, k0, ad);
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                acc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[s], (double) h2f(h8bits(wv, s)), acc[1], 0, 0, 0);
+        }
+    }
+    double * red = (double *) smem;               // [wave][group][r][lane]
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave * 2 + g) * 4 + r) * 64 + lane] = acc[g][r];
+    __syncthreads();
+    for (int v = t; v < ng * 256; v += kBlock) {
+        const int g = v >> 8, r = (v >> 6) & 3, l = v & 63;
+        const int tok = t0 + 16 * g + 4 * r + (l >> 4), row = r0 + (l & 15);
+        if (tok >= n) continue;
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) sum += red[((w * 2 + g) * 4 + r) * 64 + l];
+        float o = (float) sum;
+        if (res) o = o + res[(size_t) tok * rs + row];
+        Y[(size_t) tok * ys + row] = o;
+    }
+}
+
+// One-dimensional grid: the first (N / 64) * nfull workgroups are 64 x 64
+// tiles (weight tile fastest), the rest 16-row tail workgroups over the
+// tokens from nfull * 64 on (at most 32 of them).
 template <bool WIDE, int KC>
 __global__ __launch_bounds__(kBlock) void k_gemm_f16(const uint16_t * __restrict__ W, int32_t N, int32_t K,
                                                      const float * __restrict__ x, int32_t xs, int32_t n,
                                                      float * __restrict__ Y, int32_t ys, const float * __restrict__ res,
-                                                     int32_t rs) {
+                                                     int32_t rs, int32_t nfull) {
     using T = F16Tile<WIDE, KC>;
     constexpr int E = T::E, NW = T::SP / 8, NX = T::SP / 4;
+    static_assert(2 * T::STAGE >= 4 * 2 * 4 * 64 * 8, "tail reduction fits the staging LDS");
     __shared__ __align__(16) char smem[2 * T::STAGE];
-    const int t = threadIdx.x, r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
+    const int nx = N / kTile, b = blockIdx.x;
+    if (b >= nx * nfull) {
+        gemm_f16_tail<WIDE>(W, K, x, xs, n, nfull * kTile, (b - nx * nfull) * 16, Y, ys, res, rs, smem);
+        return;
+    }
+    const int t = threadIdx.x, r0 = (b % nx) * kTile, t0 = (b / nx) * kTile;
     const int lane = t & 63, wave = t >> 6, wr = wave & 1, wt = wave >> 1, li = lane & 15, lk = lane >> 4;
     // staging: thread t loads SP consecutive k of weight row / token t / 4, part t % 4
     const int sr = t >> 2, sp = (t & 3) * T::SP;
@@ -517,11 +584,16 @@ __global__ __launch_bounds__(kBlock) void k_att_q(const float * __restrict__ qkv
     if (t < kHD) Qh[((size_t) h * n + row) * kHD + t] = f2kv(o, bf);
 }
 
-// grid (n_head, ceil(tiles / 2), 2): workgroup y takes 64-row tiles y and
-// tiles - 1 - y, so every workgroup sweeps about the same number of K tiles
-// (the causal sweep of tile y is y + 1 tiles long); grid z = grp takes the
-// 64-position K tiles at 128 s + 64 grp, so that two workgroups of four waves
-// share each CU and one's MFMAs run while the other waits at a barrier.
+// grid (n_head, Y, 2): workgroup y takes 64-row tiles y and tiles - 1 - y, so
+// every workgroup sweeps about the same number of K tiles (the causal sweep
+// of tile y is y + 1 tiles long); grid z = grp takes the 64-position K tiles
+// at 128 s + 64 grp, so that two workgroups of four waves share each CU and
+// one's MFMAs run while the other waits at a barrier.  An odd tile count
+// leaves a middle tile: with Y = (tiles + 1) / 2 its own workgroup sweeps
+// it; with Y = tiles / 2 (from 3 tiles on) its K steps are dealt out, step
+// st to workgroup st mod Y, since score blocks are independent outputs.  The
+// latter keeps 2 * n_head * tiles / 2 workgroups (two per CU at 2,049 rows,
+// where a workgroup of its own would leave 16 CUs a third one).
 // Wave w owns rows 16w..16w+15 of a tile (q from k_att_q): lane (i = l%16,
 // k = l/16) holds dims 32k..32k+31 of row 16w + i, and four 16-position
 // accumulators.  K tiles are double-buffered in LDS (tile s + 1 loaded into
@@ -537,13 +609,17 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
     const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
     const int krow = t >> 4, kch = t & 15;                  // staging: positions krow + 16u, 8-dim chunk
     const uint16_t * kbase = kc + (size_t) g * n_ctx * kHD + 8 * kch;
-    for (int pass = 0; pass < 2; ++pass) {
-        const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
-        if (pass == 1 && tile == (int) blockIdx.y) break;     // the middle tile of an odd count
+    const int y = blockIdx.y, Y = gridDim.y;
+    const bool spread = 2 * Y + 1 == tiles;                     // middle tile's K steps dealt out
+    for (int pass = 0; pass < (spread ? 3 : 2); ++pass) {
+        const int tile = pass == 0 ? y : pass == 1 ? tiles - 1 - y : Y;
+        if (pass == 1 && tile == y) break;                      // the middle tile of an odd count
         const int row0 = tile * kAT, my_row = row0 + 16 * w + i;
         const int lim_tile = n_past + min(row0 + kAT, n) - 1;   // last position any row of the tile sees
         if (lim_tile < 64 * grp) continue;                      // no K tile for this group
         const int nst = (lim_tile - 64 * grp) / (2 * kAT) + 1;
+        const int st0 = pass == 2 ? y : 0, sd = pass == 2 ? Y : 1;   // steps st0, st0 + sd, ...
+        if (st0 >= nst) continue;
         // q of row my_row, dims 32k .. 32k+31 (fp16 / bfloat16 values, held as fp32)
         float a[32];
         {
@@ -571,12 +647,13 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
             for (int u = 0; u < 4; ++u)
                 *(int4 *) (&kt[buf][(krow + 16 * u) * kKS + 8 * kch]) = kok[u] ? rk[u] : make_int4(0, 0, 0, 0);
         };
-        fetch(64 * grp);
+        fetch(2 * kAT * st0 + 64 * grp);
         stash(0);
         __syncthreads();
-        for (int st = 0; st < nst; ++st) {
-            const int buf = st & 1, j0 = 2 * kAT * st + 64 * grp;
-            if (st + 1 < nst) fetch(j0 + 2 * kAT);
+        for (int st = st0, it = 0; st < nst; st += sd, ++it) {
+            const int buf = it & 1, j0 = 2 * kAT * st + 64 * grp;
+            const bool more = st + sd < nst;
+            if (more) fetch(j0 + 2 * kAT * sd);
             v4d acc[4];
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) acc[t4] = v4d{0.0, 0.0, 0.0, 0.0};
@@ -605,17 +682,49 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
                     if (row < n && j <= n_past + row)
                         S[((size_t) h * n + row) * ls + j] = (float) acc[t4][r] * scale;
                 }
-            if (st + 1 < nst) stash(buf ^ 1);
+            if (more) stash(buf ^ 1);
             __syncthreads();
         }
     }
 }
 
+// One row held in registers, R positions per lane (cnt <= 64 R).  Each lane
+// adds its terms in position order and lanes past cnt add exact zeros, so the
+// sum is the one of the three-pass loop below, whatever R.
+template <int R>
+__device__ __forceinline__ void softmax_row_reg(const float * __restrict__ sr, uint16_t * __restrict__ pr, int cnt,
+                                                int lane, int bf) {
+    float v[R];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int j = lane + 64 * u;
+        v[u] = j < cnt ? sr[j] : -INFINITY;
+        m = fmaxf(m, v[u]);
+    }
+    const float mx = wave_max_f(m);
+    double sum = 0.0;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int j = lane + 64 * u;
+        v[u] = j < cnt ? expf_q3t(v[u] - mx) : 0.0f;
+        sum += (double) v[u];
+    }
+    const float inv = (float) (1.0 / wave_sum_d(sum));
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int j = lane + 64 * u;
+        if (j < cnt) pr[j] = f2kv(v[u] * inv, bf);
+    }
+}
+
 // grid (ceil(n / 4), n_head), one wave per row: P[h][r][j] = fp16(exp(S -
 // max) / sum) for j <= n_past + r (bfloat16 with a BF16 cache), as
-// pf::k_attn_rows rounds it.  Rows of up to 2048 positions stay in registers
-// (one read of S); longer rows are read three times.
-constexpr int kSmReg = 32;       // positions per lane held in registers
+// pf::k_attn_rows rounds it.  Rows of up to 2,560 positions stay in
+// registers (one read of S; 16, 32 or 40 per lane by length, so a 2,049-
+// position row is not the three-read straggler that ends the launch, and the
+// kernel keeps 64 VGPRs, eight waves per SIMD); longer rows are read three
+// times.
 __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict__ S, int32_t n, int32_t n_past,
                                                         int32_t ls, uint16_t * __restrict__ P, int32_t bf) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y;
@@ -623,31 +732,9 @@ __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict
     const int cnt = n_past + row + 1;
     const float * sr = S + ((size_t) h * n + row) * ls;
     uint16_t * pr = P + ((size_t) h * n + row) * ls;
-    if (cnt <= 64 * kSmReg) {
-        float v[kSmReg];
-        float m = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < kSmReg; ++u) {
-            const int j = lane + 64 * u;
-            v[u] = j < cnt ? sr[j] : -INFINITY;
-            m = fmaxf(m, v[u]);
-        }
-        const float mx = wave_max_f(m);
-        double sum = 0.0;
-#pragma unroll
-        for (int u = 0; u < kSmReg; ++u) {
-            const int j = lane + 64 * u;
-            v[u] = j < cnt ? expf_q3t(v[u] - mx) : 0.0f;
-            sum += (double) v[u];
-        }
-        const float inv = (float) (1.0 / wave_sum_d(sum));
-#pragma unroll
-        for (int u = 0; u < kSmReg; ++u) {
-            const int j = lane + 64 * u;
-            if (j < cnt) pr[j] = f2kv(v[u] * inv, bf);
-        }
-        return;
-    }
+    if (cnt <= 64 * 16) { softmax_row_reg<16>(sr, pr, cnt, lane, bf); return; }
+    if (cnt <= 64 * 32) { softmax_row_reg<32>(sr, pr, cnt, lane, bf); return; }
+    if (cnt <= 64 * 40) { softmax_row_reg<40>(sr, pr, cnt, lane, bf); return; }
     float m = -INFINITY;
     for (int j = lane; j < cnt; j += 64) m = fmaxf(m, sr[j]);
     const float mx = wave_max_f(m);
@@ -657,8 +744,13 @@ __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict
     for (int j = lane; j < cnt; j += 64) pr[j] = f2kv(expf_q3t(sr[j] - mx) * inv, bf);
 }
 
-// grid (n_head, ceil(tiles / 2), 2), tiles paired as in k_att_scores; grid
-// z = grp takes dims 64 grp .. 64 grp + 63.  Four waves: wave w owns rows
+// grid (n_head, Y, 2), tiles paired as in k_att_scores; grid z = grp takes
+// dims 64 grp .. 64 grp + 63.  An odd tile count's middle tile: with Y =
+// (tiles + 1) / 2 its own workgroup sweeps it; with Y = tiles / 2 (from 3
+// tiles on) its four 16-row groups are dealt out, group q to workgroup q mod
+// Y, which stages the tile as usual and sweeps it for those 16 rows only,
+// wave w taking dims 16 w .. 16 w + 15 (one accumulator; every output is the
+// same sum, in the same order, as in the undealt form).  Four waves: wave w owns rows
 // 16w..16w+15 of a tile and dims 64 grp + 4 i + d4 (lane i = l%16, d4 =
 // 0..3) as four 16 x 16 accumulators, so each lane reads its four B operands
 // of a step with one 8-byte load and stores four consecutive floats.  P tiles
@@ -667,7 +759,7 @@ __global__ __launch_bounds__(kBlock) void k_att_softmax(const float * __restrict
 // Probabilities past a row's last position, and V rows past the tile's last
 // position, are staged as zero.
 constexpr int kVN = 64 + 8;      // LDS row stride (halves) of a staged V half-tile: conflict-free 16-byte writes
-__global__ __launch_bounds__(kAttT) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
+__global__ __launch_bounds__(kAttT, 4) void k_att_pv(const uint16_t * __restrict__ P, int32_t ls,
                                                    const uint16_t * __restrict__ vc, int32_t n_ctx, int32_t n_head,
                                                    int32_t n_kv_head, int32_t n, int32_t n_past,
                                                    float * __restrict__ out, int32_t out_stride, int32_t bf) {
@@ -677,10 +769,14 @@ __global__ __launch_bounds__(kAttT) void k_att_pv(const uint16_t * __restrict__ 
     const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
     const int srow = t >> 3, sch = t & 7;                    // staging: rows / positions srow + 32u, 8-wide chunk
     const uint16_t * vbase = vc + (size_t) g * n_ctx * kHD + 64 * grp + 8 * sch;
-  for (int pass = 0; pass < 2; ++pass) {
-    const int tile = pass == 0 ? (int) blockIdx.y : tiles - 1 - (int) blockIdx.y;
-    if (pass == 1 && tile == (int) blockIdx.y) break;         // the middle tile of an odd count
-    const int row0 = tile * kAT;
+    const int y = blockIdx.y, Y = gridDim.y;
+    // passes: tiles y and tiles - 1 - y, then (spread) middle-tile row groups y, y + Y, ... < 4
+    const int nrg = (2 * Y + 1 == tiles && y < 4) ? (4 - y + Y - 1) / Y : 0;
+  for (int pass = 0; pass < 2 + nrg; ++pass) {
+    const int rg = pass < 2 ? -1 : y + (pass - 2) * Y;        // row group of the middle tile, or -1
+    const int tile = pass == 0 ? y : pass == 1 ? tiles - 1 - y : Y;
+    if (pass == 1 && tile == y) continue;                     // the middle tile of an odd count
+    const int row0 = tile * kAT, prow = rg < 0 ? 16 * w : 16 * rg;   // first A row of this wave in the tile
     const int lim_tile = n_past + min(row0 + kAT, n) - 1;
     const int nst = lim_tile / kAT + 1;
     int plim[2];
@@ -728,29 +824,45 @@ __global__ __launch_bounds__(kAttT) void k_att_pv(const uint16_t * __restrict__ 
         const int buf = st & 1;
         if (st + 1 < nst) fetch((st + 1) * kAT);
         int4 pa[2];
-        pa[0] = *(const int4 *) (&pt[buf][(16 * w + i) * kVS + 16 * k]);
-        pa[1] = *(const int4 *) (&pt[buf][(16 * w + i) * kVS + 16 * k + 8]);
-        const uint16_t * vr = &vt[buf][16 * k * kVN + 4 * i];
+        pa[0] = *(const int4 *) (&pt[buf][(prow + i) * kVS + 16 * k]);
+        pa[1] = *(const int4 *) (&pt[buf][(prow + i) * kVS + 16 * k + 8]);
+        if (rg < 0) {
+            const uint16_t * vr = &vt[buf][16 * k * kVN + 4 * i];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {                       // position 16k + s of the tile
-            const double pd = kvd(h8bits(pa[s >> 3], s & 7), bf);
-            const uint2 vv = *(const uint2 *) (vr + s * kVN);
+            for (int s = 0; s < 16; ++s) {                   // position 16k + s of the tile
+                const double pd = kvd(h8bits(pa[s >> 3], s & 7), bf);
+                const uint2 vv = *(const uint2 *) (vr + s * kVN);
 #pragma unroll
-            for (int d4 = 0; d4 < 4; ++d4) {
-                const uint32_t word = (d4 >> 1) ? vv.y : vv.x;
-                const uint16_t vh = (uint16_t) ((d4 & 1) ? (word >> 16) : (word & 0xffffu));
-                acc[d4] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d4], 0, 0, 0);
+                for (int d4 = 0; d4 < 4; ++d4) {
+                    const uint32_t word = (d4 >> 1) ? vv.y : vv.x;
+                    const uint16_t vh = (uint16_t) ((d4 & 1) ? (word >> 16) : (word & 0xffffu));
+                    acc[d4] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd, kvd(vh, bf), acc[d4], 0, 0, 0);
+                }
             }
+        } else {                                             // rows 16 rg + .., wave w: dims 16 w + i
+            const uint16_t * vr = &vt[buf][16 * k * kVN + 16 * w + i];
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+                acc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64(kvd(h8bits(pa[s >> 3], s & 7), bf), kvd(vr[s * kVN], bf),
+                                                              acc[0], 0, 0, 0);
         }
         if (st + 1 < nst) stash(buf ^ 1);
         __syncthreads();
     }
+    if (rg < 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * w + 4 * r + k;
-        if (row < n)
-            *(float4 *) (out + (size_t) row * out_stride + h * kHD + 64 * grp + 4 * i) =
-                make_float4((float) acc[0][r], (float) acc[1][r], (float) acc[2][r], (float) acc[3][r]);
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 16 * w + 4 * r + k;
+            if (row < n)
+                *(float4 *) (out + (size_t) row * out_stride + h * kHD + 64 * grp + 4 * i) =
+                    make_float4((float) acc[0][r], (float) acc[1][r], (float) acc[2][r], (float) acc[3][r]);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 16 * rg + 4 * r + k;
+            if (row < n) out[(size_t) row * out_stride + h * kHD + 64 * grp + 16 * w + i] = (float) acc[0][r];
+        }
     }
   }
 }

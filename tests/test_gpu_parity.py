@@ -105,19 +105,23 @@ def test_prefill_and_steps_match_oracle(tiny_model, prefill_path):
 def test_tiled_prefill_attention_paths(wtype_tiny, kv, att, monkeypatch):
     """A 100-row prefill after 37 cached positions on the tiled prefill
     (MFMA attention over 64-row tiles, or Q3T_PF_ATT_MFMA=0 one workgroup per
-    row), then 35 rows more: hidden rows and logits bit for bit the oracle's."""
+    row), then 35, 72, 12 and 150 rows more (72, 12 and 150 leave remainders of
+    8, 12 and 22 rows past the last full 64-row tile, which the F16 GEMM gives
+    to its tail workgroups; 150 rows are three tiles, whose middle tile the
+    scores kernel deals out over the pairs' workgroups): hidden rows and
+    logits bit for bit the oracle's."""
     monkeypatch.setenv("Q3T_PREFILL_MFMA", "1")
     monkeypatch.setenv("Q3T_PF_ATT_MFMA", "1" if att == "mfma" else "0")
     cfg = qcfg.tiny()
-    w, dev, o = make(cfg, wtype_tiny, seed=43, n_ctx=256)
+    w, dev, o = make(cfg, wtype_tiny, seed=43, n_ctx=512)
     try:
         if kv == "bf16":
             dev.kv_set_type(30)
             o.kv_set_type(30)
-            o.kv_reset(256)
+            o.kv_reset(512)
         rng = np.random.default_rng(44)
         d = cfg.hidden_size
-        for n_past, n in ((0, 37), (37, 100), (137, 35)):
+        for n_past, n in ((0, 37), (37, 100), (137, 35), (172, 72), (244, 12), (256, 150)):
             rows = (rng.standard_normal((n, d)) * 0.5).astype(np.float32)
             say(f"[gpu] tiled prefill {n} rows at {n_past} ({wtype_tiny}, {kv} KV, {att})")
             hg, lg = dev.prefill(rows, n_past)
@@ -406,6 +410,37 @@ def test_long_context_persistent_matches_graph(wtype, monkeypatch):
         dev.close()
     for k in out:
         assert np.array_equal(out[k], out[0]), k
+
+
+@pytest.mark.parametrize("wtype", ["f16", "q8_0"])
+def test_prefill_2049_rows_tail_forms(wtype, monkeypatch):
+    """A 2,049-row tiled prefill at the 0.6B shapes (the long-context
+    prompt: 33 row tiles, one row past the last full one).  The F16 GEMM's
+    16-row tail workgroups and the scores kernel's dealt-out middle tile
+    against the forms they replace (Q3T_PF_F16_TAIL=0, Q3T_PF_ATT_SPREAD=0:
+    a partial 64-row tile, a workgroup of its own), which the 200-row and
+    tiny tiled-prefill tests pin to the oracle: hidden rows and logits bit for
+    bit."""
+    cfg = qcfg.full_06b()
+    say(f"[gpu] 2049-row prefill {wtype}: synth + upload")
+    w = Weights(cfg, wtype, seed=8, norm_mode="one")
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    monkeypatch.setenv("Q3T_PREFILL_MFMA", "1")
+    rows = (np.random.default_rng(81).standard_normal((2049, cfg.hidden_size)) * 0.05).astype(np.float32)
+    out = []
+    try:
+        dev.kv_reserve(2049 + 16)
+        for knob in ("1", "0"):
+            monkeypatch.setenv("Q3T_PF_F16_TAIL", knob)
+            monkeypatch.setenv("Q3T_PF_ATT_SPREAD", knob)
+            say(f"[gpu] 2049-row prefill {wtype}: Q3T_PF_F16_TAIL=Q3T_PF_ATT_SPREAD={knob}")
+            out.append(dev.prefill(rows, 0))
+    finally:
+        dev.close()
+    (h1, l1), (h0, l0) = out
+    assert h1.shape == (2049, cfg.hidden_size) and np.isfinite(l1).all()
+    assert np.array_equal(h1, h0) and np.array_equal(l1, l0)
 
 
 @pytest.fixture(params=["persistent", "persistent_rows", "graph"])
