@@ -1537,8 +1537,9 @@ int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uin
     const dim3 tiles(g.n_head, (nt % 2 && nt >= 3 && !no_spread) ? nt / 2 : (nt + 1) / 2, 2);
     // q rows into the probabilities buffer's head (they are consumed before it is written)
     uint16_t * qh = c->pf_p;
-    hipLaunchKernelGGL(pf::k_att_q, dim3(n, g.n_head), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv, qkvd,
-                       L.q_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, n, n_past, qh, bf);
+    hipLaunchKernelGGL(pf::k_att_q, dim3(n, (g.n_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+                       qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, n, n_past,
+                       g.n_head, qh, bf);
     hipLaunchKernelGGL(pf::k_att_scores, tiles, dim3(pf::kAttT), 0, c->stream, (const uint16_t *) qh, kc, c->n_ctx,
                        g.n_head, g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
     hipLaunchKernelGGL(pf::k_att_softmax, dim3((n + 3) / 4, g.n_head), dim3(kBlock), 0, c->stream,
@@ -1564,7 +1565,7 @@ int prefill_f16(q3t_dev * c, int n, int n_past) {
         uint16_t * vc = c->vc + il * lstride;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, x, L.attn_norm, g.rms_eps, d, c->pf_f);
         pf_gemm_f16(c, L.qkv, qkvd, d, n, c->pf_f, d, false, c->pf_qkv, nullptr, 0);
-        hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+        hipLaunchKernelGGL(pf::k_kv_rows, dim3(n, (g.n_kv_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
         if (pf_attention(c, L, kc, vc, n, n_past)) return -1;
@@ -1602,7 +1603,7 @@ int prefill_mfma(q3t_dev * c, int n, int n_past) {
         uint16_t * vc = c->vc + il * lstride;
         pf_quant(c, x, n, d, L.attn_norm);
         pf_gemm(c, L.qkv, qkvd, d, n, c->pf_qkv, nullptr);
-        hipLaunchKernelGGL(pf::k_kv_rows, dim3(g.n_kv_head, n), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+        hipLaunchKernelGGL(pf::k_kv_rows, dim3(n, (g.n_kv_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
         if (pf_attention(c, L, kc, vc, n, n_past)) return -1;

@@ -435,6 +435,25 @@ __device__ __forceinline__ float head_norm_rope(float v, const float * w, float 
     return o;
 }
 
+// RMSNorm over one 128-element head held by a wave (lane holds elements
+// lane and lane + 64), then NEOX RoPE; returns the two rotated elements.
+// The arithmetic of head_norm_rope, with the sum of squares reduced over the
+// wave.
+__device__ __forceinline__ void wave_norm_rope(float & x0, float & x1, const float * w, float eps, const float * c,
+                                               const float * s) {
+    const int l = threadIdx.x & 63;
+    const double tot = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
+    const float mean = (float) (tot / (double) kHD);
+    const float sc = 1.0f / sqrtf(mean + eps);
+    float a0 = x0 * sc, a1 = x1 * sc;
+    a0 = a0 * w[l];
+    a1 = a1 * w[l + 64];
+    const float p0 = a0 * c[l], q0 = a1 * s[l];
+    const float p1 = a0 * s[l], q1 = a1 * c[l];
+    x0 = p0 - q0;
+    x1 = p1 + q1;
+}
+
 // Q8_0 quantisation of one value per lane, a block being 32 consecutive lanes
 // (d = amax/127 as fp16, q = rint(x * 127/amax)); the block's first lane
 // stores the scale.

@@ -450,23 +450,24 @@ __global__ __launch_bounds__(kBlock) void k_swiglu_rows(const float * __restrict
 }
 
 // K (QK-norm + NEOX RoPE) and V rows of n tokens into the KV cache at
-// positions pos0 + tok, fp16 or (bf) bfloat16.  Block (g, tok), 256 threads
-// (threads < 128 own one element each).
+// positions pos0 + tok, fp16 or (bf) bfloat16.  Grid (n, ceil(n_kv_head /
+// 4)), one wave per (token, KV head), each lane owning elements lane and
+// lane + 64.
 __global__ __launch_bounds__(kBlock) void k_kv_rows(const float * __restrict__ qkv, int32_t qkv_stride, int32_t qd,
                                                     int32_t kd, const float * __restrict__ k_norm, float eps,
                                                     const float * __restrict__ rc, const float * __restrict__ rs,
                                                     uint16_t * __restrict__ kc, uint16_t * __restrict__ vc, int32_t n_ctx,
                                                     int32_t pos0, int32_t bf) {
-    __shared__ double red[4];
-    __shared__ float tmp[kHD];
-    const int g = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, pos = pos0 + tok;
+    const int tok = blockIdx.x, g = blockIdx.y * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63, pos = pos0 + tok;
+    if (g * kHD >= kd) return;                    // whole wave; no workgroup barrier follows
     const float * row = qkv + (size_t) tok * qkv_stride;
-    const float kv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
-    const float o = head_norm_rope(kv, k_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
-    if (t < kHD) {
-        kc[((size_t) g * n_ctx + pos) * kHD + t] = f2kv(o, bf);
-        vc[((size_t) g * n_ctx + pos) * kHD + t] = f2kv(row[qd + kd + g * kHD + t], bf);
-    }
+    float x0 = row[qd + g * kHD + l], x1 = row[qd + g * kHD + 64 + l];
+    wave_norm_rope(x0, x1, k_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64);
+    const size_t o = ((size_t) g * n_ctx + pos) * kHD;
+    kc[o + l] = f2kv(x0, bf);
+    kc[o + 64 + l] = f2kv(x1, bf);
+    vc[o + l] = f2kv(row[qd + kd + g * kHD + l], bf);
+    vc[o + 64 + l] = f2kv(row[qd + kd + g * kHD + 64 + l], bf);
 }
 
 // Causal attention of n tokens over the cache (all rows already written).
@@ -570,18 +571,22 @@ constexpr int kVS = 72;          // LDS row stride (halves) of staged P and V^T 
 
 __device__ __forceinline__ double kvd(uint16_t h, bool bf) { return (double) kv2f(h, bf); }
 
-// grid (n, n_head): q of row r, head h (QK-norm, NEOX RoPE at position
-// n_past + r) rounded to the cache type, into Qh[h][r][128].
+// grid (n, ceil(n_head / 4)), one wave per (row, head): q of row r, head h
+// (QK-norm, NEOX RoPE at position n_past + r) rounded to the cache type, into
+// Qh[h][r][128].
 __global__ __launch_bounds__(kBlock) void k_att_q(const float * __restrict__ qkv, int32_t qkv_stride,
                                                   const float * __restrict__ q_norm, float eps,
                                                   const float * __restrict__ rc, const float * __restrict__ rs,
-                                                  int32_t n, int32_t n_past, uint16_t * __restrict__ Qh, int32_t bf) {
-    __shared__ double red[4];
-    __shared__ float tmp[kHD];
-    const int row = blockIdx.x, h = blockIdx.y, t = threadIdx.x, pos = n_past + row;
-    const float v = t < kHD ? qkv[(size_t) row * qkv_stride + h * kHD + t] : 0.0f;
-    const float o = head_norm_rope(v, q_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64, tmp, red);
-    if (t < kHD) Qh[((size_t) h * n + row) * kHD + t] = f2kv(o, bf);
+                                                  int32_t n, int32_t n_past, int32_t n_head, uint16_t * __restrict__ Qh,
+                                                  int32_t bf) {
+    const int row = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63, pos = n_past + row;
+    if (h >= n_head) return;                      // whole wave; no workgroup barrier follows
+    const float * src = qkv + (size_t) row * qkv_stride + h * kHD;
+    float x0 = src[l], x1 = src[64 + l];
+    wave_norm_rope(x0, x1, q_norm, eps, rc + (size_t) pos * 64, rs + (size_t) pos * 64);
+    uint16_t * dst = Qh + ((size_t) h * n + row) * kHD;
+    dst[l] = f2kv(x0, bf);
+    dst[64 + l] = f2kv(x1, bf);
 }
 
 // grid (n_head, Y, 2): workgroup y takes 64-row tiles y and tiles - 1 - y, so

@@ -634,23 +634,6 @@ __host__ __device__ constexpr size_t attn_gqa_lds_bytes(int g, int n_ctx) {
                                                                     : (size_t) kAWaves * g * kHD * 8);
 }
 
-// RMSNorm over one 128-element head held by a wave (lane holds elements
-// lane and lane + 64), then NEOX RoPE; returns the two rotated elements.
-__device__ __forceinline__ void wave_norm_rope(float & x0, float & x1, const float * w, float eps, const float * c,
-                                               const float * s) {
-    const int l = threadIdx.x & 63;
-    const double tot = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
-    const float mean = (float) (tot / (double) kHD);
-    const float sc = 1.0f / sqrtf(mean + eps);
-    float a0 = x0 * sc, a1 = x1 * sc;
-    a0 = a0 * w[l];
-    a1 = a1 * w[l + 64];
-    const float p0 = a0 * c[l], q0 = a1 * s[l];
-    const float p1 = a0 * s[l], q1 = a1 * c[l];
-    x0 = p0 - q0;
-    x1 = p1 + q1;
-}
-
 // Workgroup x takes query heads G x .. G x + G - 1 of stream blockIdx.y; with
 // G below the group size two or more workgroups share a KV head, read its
 // cache each, and only the first appends the new K/V row (the others take
