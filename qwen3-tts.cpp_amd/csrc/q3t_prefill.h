@@ -82,6 +82,9 @@ __global__ __launch_bounds__(kBlock) void k_quant_rows(const float * __restrict_
 // fp16 scale product (exact in fp32) in an fp64 fma, so the fp64 sum of exact
 // terms is rounded to fp32 once.  epi: EPI_STORE or EPI_RESID (res [n][rs],
 // rs = 0 broadcasts one row).  Requires N % (32 IR) == 0, K % (32 kGB) == 0.
+// A wave skips the MFMAs and epilogue of its 16-token groups that lie wholly
+// past n, so the partial last token tile (2,049 rows: one row) costs about
+// half a tile, not a whole one.
 template <int IR, int JT, int GB>
 struct Q8Tile {
     static constexpr int TN = 32 * IR, TM = 32 * JT;
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(kBlock) void k_gemm_q8(const int8_t * __restrict__ 
                 for (int e = 0; e < 4; ++e) dwv[e] = sdw[kb * T::TN + rl + 4 * lk + e];
 #pragma unroll
                 for (int j = 0; j < JT; ++j) {
+                    if (t0 + (wt * JT + j) * 16 >= n) continue;   // 16 tokens past n (wave-uniform): nothing to add
                     const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[j], zero, 0, 0, 0);
                     // fp16 x fp16 scale product exact in fp32; times the int32 block sum exact in fp64
 #pragma unroll
