@@ -1426,10 +1426,12 @@ void pf_gemm(q3t_dev * c, const Slot & w, int N, int K, int n, float * y, const 
 #undef Q3T_PF_GEMM
 }
 
+// Q8_0 rows of x (after an RMSNorm with weights w, or with u the SwiGLU
+// silu(x) * u) into q / dx (default: the prefill's pf_q / pf_dx).
 void pf_quant(q3t_dev * c, const float * x, int n, int K, const float * w, int xs = -1, int8_t * q = nullptr,
-              float * dx = nullptr) {
+              float * dx = nullptr, const float * u = nullptr) {
     hipLaunchKernelGGL(pf::k_quant_rows, dim3(n), dim3(kBlock), 0, c->stream, x, xs < 0 ? K : xs, K, w, c->cfg.rms_eps,
-                       q ? q : c->pf_q, dx ? dx : c->pf_dx);
+                       q ? q : c->pf_q, dx ? dx : c->pf_dx, u);
 }
 
 __global__ __launch_bounds__(256) void k_h2f(const uint16_t * __restrict__ in, size_t n, float * __restrict__ out) {
@@ -1612,10 +1614,7 @@ int prefill_mfma(q3t_dev * c, int n, int n_past) {
         pf_quant(c, c->pf_xb, n, d, L.ffn_norm);
         pf_gemm(c, L.wg, ffn, d, n, c->pf_g, nullptr);
         pf_gemm(c, L.wu, ffn, d, n, c->pf_u, nullptr);
-        const size_t cnt = (size_t) n * ffn;
-        hipLaunchKernelGGL(pf::k_swiglu_rows, dim3((unsigned) std::min<size_t>((cnt + kBlock - 1) / kBlock, 4096)),
-                           dim3(kBlock), 0, c->stream, (const float *) c->pf_g, (const float *) c->pf_u, c->pf_f, cnt);
-        pf_quant(c, c->pf_f, n, ffn, nullptr);
+        pf_quant(c, c->pf_g, n, ffn, nullptr, -1, nullptr, nullptr, c->pf_u);   // SwiGLU fused into the quantisation
         pf_gemm(c, L.wd, d, ffn, n, c->pf_xa, c->pf_xb);
         x = c->pf_xa;
     }

@@ -29,45 +29,53 @@ __device__ __forceinline__ uint16_t h8bits(const int4 & v, int e) {
 }
 
 // One row per block: optional RMSNorm (y = (x * scale) * w, scale from the
-// fp64 sum of fp32 squares), then Q8_0 quantisation per 32-element block
-// (d = amax/127 as fp16, q = rint(x * 127/amax)).  q: int8 [n][K]; dx: the
-// fp16-rounded scales as float [n][K/32].
+// fp64 sum of fp32 squares) or, with u, the SwiGLU y = silu(x) * u (x the
+// gate rows, u the up rows of the same stride; the numbers of k_swiglu_rows),
+// then Q8_0 quantisation per 32-element block (d = amax/127 as fp16, q =
+// rint(x * 127/amax)).  q: int8 [n][K]; dx: the fp16-rounded scales as float
+// [n][K/32].
 __global__ __launch_bounds__(kBlock) void k_quant_rows(const float * __restrict__ x, int32_t xs, int32_t K,
                                                        const float * __restrict__ w, float eps, int8_t * __restrict__ q,
-                                                       float * __restrict__ dx) {
+                                                       float * __restrict__ dx, const float * __restrict__ u) {
     __shared__ double red[4];
     const int row = blockIdx.x, t = threadIdx.x;
     const float * xr = x + (size_t) row * xs;
     float scale = 1.0f;
-    if (w) {
+    if (w && !u) {
         double ss = 0.0;
         for (int i = t; i < K; i += kBlock) ss += (double) (xr[i] * xr[i]);
         const double tot = block_sum_d(ss, red);
         const float mean = (float) (tot / (double) K);
         scale = 1.0f / sqrtf(mean + eps);
     }
+    // four elements per thread, a block being 8 consecutive lanes (K % 32 == 0
+    // keeps every 8-lane group wholly inside or outside the loop)
     const int nb = K / kQK;
-    for (int b = t; b < nb; b += kBlock) {
-        float v[kQK];
-        float am = 0.0f;
+    for (int g = t; g < K / 4; g += kBlock) {
+        const float4 xv = *(const float4 *) (xr + 4 * g);
+        float y[4] = {xv.x, xv.y, xv.z, xv.w};
+        if (u) {
+            const float4 uv = *(const float4 *) (u + (size_t) row * xs + 4 * g);
+            const float uk[4] = {uv.x, uv.y, uv.z, uv.w};
 #pragma unroll
-        for (int e = 0; e < kQK; ++e) {
-            float y = xr[b * kQK + e];
-            if (w) { const float s = y * scale; y = s * w[b * kQK + e]; }
-            v[e] = y;
-            am = fmaxf(am, fabsf(y));
+            for (int e = 0; e < 4; ++e) y[e] = silu_q3t(y[e]) * uk[e];
+        } else if (w) {
+            const float4 wv = *(const float4 *) (w + 4 * g);
+            const float wk[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { const float sv = y[e] * scale; y[e] = sv * wk[e]; }
         }
+        float am = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, __shfl_xor(am, 2));
+        am = fmaxf(am, __shfl_xor(am, 4));
         const float d = am / 127.0f;
         const float id = am != 0.0f ? 127.0f / am : 0.0f;
-        int8_t * qr = q + (size_t) row * K + b * kQK;
+        int p = 0;
 #pragma unroll
-        for (int c = 0; c < kQK / 4; ++c) {
-            int p = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p |= ((int) rintf(v[4 * c + e] * id) & 0xff) << (8 * e);
-            *(int *) (qr + 4 * c) = p;
-        }
-        dx[(size_t) row * nb + b] = round_f16(d);
+        for (int e = 0; e < 4; ++e) p |= ((int) rintf(y[e] * id) & 0xff) << (8 * e);
+        *(int *) (q + (size_t) row * K + 4 * g) = p;
+        if ((g & 7) == 0) dx[(size_t) row * nb + (g >> 3)] = round_f16(d);
     }
 }
 
