@@ -937,7 +937,7 @@ int orc_build_prefill(orc_model * m, const int32_t * text, int32_t n_text,
 int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const float * trail, int32_t trail_len,
                       const float * pad, const orc_gen_params * p, int32_t * codes_out, float * first_logits_out);
 int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trail, int32_t trail_len,
-               const float * pad_row, const orc_gen_params * p, int32_t * codes_out);
+               const float * pad_row, const orc_gen_params * p, int32_t * codes_out, float * frame_logits_out);
 
 int orc_generate(orc_model * m, const int32_t * text, int32_t n_text,
                  const float * speaker, const orc_gen_params * p,
@@ -966,14 +966,14 @@ int orc_generate_rows(orc_model * m, const float * pre, int32_t plen, const floa
     std::vector<float> logits(c.codec_vocab);
     if (orc_prefill(m, pre, plen, 0, nullptr, logits.data())) return -1;
     if (first_logits_out) std::memcpy(first_logits_out, logits.data(), logits.size() * sizeof(float));
-    return orc_frames(m, logits.data(), plen, trail, trail_len, pad_row, p, codes_out);
+    return orc_frames(m, logits.data(), plen, trail, trail_len, pad_row, p, codes_out, nullptr);
 }
 
 // The frame loop of generate() (src/tts_transformer.cpp:3108-3309) from the
 // current talker cache: `first_logits` and the normed hidden row left by the
 // last prefill or step, the next talker position n_past.
 int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trail, int32_t trail_len,
-               const float * pad_row, const orc_gen_params * p, int32_t * codes_out) {
+               const float * pad_row, const orc_gen_params * p, int32_t * codes_out, float * frame_logits_out) {
     const orc_config & c = m->cfg;
     if (p->max_len <= 0) return 0;
     if (m->last_hidden.size() != (size_t) c.hidden_size) { m->err = "frames: no prefill or step has run"; return -1; }
@@ -989,6 +989,8 @@ int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const 
     int32_t n_frames = 0;
     std::vector<float> step(d), row(d);
     for (int32_t frame = 0; frame < p->max_len; ++frame) {
+        if (frame_logits_out)
+            std::memcpy(frame_logits_out + (size_t) frame * c.codec_vocab, logits.data(), logits.size() * sizeof(float));
         const int32_t tok = orc_sample_cb0(logits.data(), c.codec_vocab, c.codec_eos_id, seen.data(),
                                            p->repetition_penalty, p->temperature, p->top_k, p->eos_bias,
                                            p->target_frames, frame, p->seed);

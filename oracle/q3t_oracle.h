@@ -49,10 +49,16 @@
  *     which cannot be reproduced on a GPU: distributional parity only with
  *     the reference, exact parity with the HIP path.
  *
- * Pinning status (tests/test_oracle.py): every function here is checked
- * against closed forms, fp64 brute force, the reference's fixture
- * reference/det_prefill_token_types.json, known-answer vectors (Philox) or
- * self-consistency (prefill == sequential steps).  What ggml's own CPU build
+ * Pinning status (tests/test_oracle.py, tests/test_oracle_model.py): every
+ * function here is checked against closed forms, fp64 brute force, the
+ * reference's fixture reference/det_prefill_token_types.json, known-answer
+ * vectors (Philox), self-consistency (prefill == sequential steps) or an
+ * independent float64 numpy forward written from the reference graphs; the
+ * frame loop (orc_frames / orc_generate_rows: the greedy codebook-0 rules,
+ * the code predictor fed the normed hidden row, the step-embedding order and
+ * trailing-row index, the EOS ramp) against a numpy loop written from
+ * src/tts_transformer.cpp:3108-3309, with planted loop mistakes that miss.
+ * What ggml's own CPU build
  * would decide differently is NOT pinned, because ggml is absent (empty
  * submodule) and the reference's det_*.bin fixtures are absent:
  *   orc_gemv            parity unpinned vs ggml's fp32 SIMD accumulation order
@@ -228,9 +234,12 @@ int orc_generate_rows(orc_model * m, const float * prefill, int32_t plen, const 
 
 /* the frame loop alone, from the current talker cache: first_logits and the
  * normed hidden row of the last orc_prefill / orc_step, next position n_past
- * (what q3t_dev_frames_begin continues from).  Returns frames written. */
+ * (what q3t_dev_frames_begin continues from).  Returns frames written.
+ * frame_logits_out (optional, [max_len][codec_vocab]): the talker logits each
+ * frame's codebook-0 sampler starts from, before suppression and penalty. */
 int orc_frames(orc_model * m, const float * first_logits, int32_t n_past, const float * trailing,
-               int32_t trail_len, const float * pad, const orc_gen_params * p, int32_t * codes_out);
+               int32_t trail_len, const float * pad, const orc_gen_params * p, int32_t * codes_out,
+               float * frame_logits_out);
 
 /* ---- audio-tokenizer decoder (vocoder), q3t_vocoder.cpp ----
  * Restates src/audio_tokenizer_decoder.cpp (build_graph :636-843,

@@ -94,7 +94,7 @@ def lib():
         L.orc_build_prefill.argtypes = [vp, vp, i32, vp, i32, vp, i32, vp, vp, vp, ctypes.POINTER(i32)]
         L.orc_generate.argtypes = [vp, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, i32, vp, vp]
         L.orc_generate_rows.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, vp]
-        L.orc_frames.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp]
+        L.orc_frames.argtypes = [vp, vp, i32, vp, i32, vp, ctypes.POINTER(OrcGenParams), vp, vp]
         L.orc_voc_create.argtypes = [vp]; L.orc_voc_create.restype = vp
         L.orc_voc_destroy.argtypes = [vp]; L.orc_voc_destroy.restype = None
         L.orc_voc_set_threads.argtypes = [vp, i32]; L.orc_voc_set_threads.restype = None
@@ -400,19 +400,25 @@ class Oracle:
         return codes[:n].copy()
 
     def frames(self, first_logits, n_past, trailing, pad, max_len, repetition_penalty=1.05, temperature=0.0,
-               top_k=0, eos_bias=0.0, target_frames=0, seed=0):
+               top_k=0, eos_bias=0.0, target_frames=0, seed=0, want_logits=False):
         """The frame loop from the current cache (the device's frames_begin +
-        frames_run after a prefill or step)."""
+        frames_run after a prefill or step).  want_logits: also return the
+        talker logits each frame's codebook-0 sampler started from
+        ([frames sampled][codec_vocab], the frame that drew EOS included)."""
         first_logits = np.ascontiguousarray(first_logits, np.float32)
         trailing = np.ascontiguousarray(trailing, np.float32).reshape(-1, self.cfg.hidden_size)
         pad = np.ascontiguousarray(pad, np.float32)
         p = OrcGenParams(max_len, 0, repetition_penalty, temperature, top_k, eos_bias, target_frames, 0, seed)
         codes = np.empty((max(max_len, 1), self.cfg.n_codebooks), np.int32)
+        lg = np.full((max(max_len, 1), self.cfg.codec_vocab), np.nan, np.float32) if want_logits else None
         n = self.L.orc_frames(self.h, _p(first_logits), n_past, _p(trailing), trailing.shape[0], _p(pad),
-                              ctypes.byref(p), _p(codes))
+                              ctypes.byref(p), _p(codes), _p(lg))
         if n < 0:
             raise RuntimeError(self.error())
-        return codes[:n].copy()
+        if not want_logits:
+            return codes[:n].copy()
+        n_lg = int(np.sum(~np.isnan(lg[:, 0])))
+        return codes[:n].copy(), lg[:n_lg].copy()
 
 
 class VocOracle:

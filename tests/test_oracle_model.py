@@ -1,12 +1,14 @@
 """Pins the oracle's model-level composition (orc_step, orc_prefill,
-orc_code_pred, orc_text_proj) against an independent float64 numpy forward
-written op by op from the reference graphs:
+orc_code_pred, orc_text_proj, and the frame loop orc_frames /
+orc_generate_rows) against an independent float64 numpy forward written op by
+op from the reference graphs:
 
   build_step_graph               src/tts_transformer.cpp:1652-1751
   build_prefill_forward_graph    src/tts_transformer.cpp:1474-1617
   build_code_pred_prefill_graph  src/tts_transformer.cpp:1929-2044
   build_code_pred_step_graph     src/tts_transformer.cpp:2055-2215
   project_text_tokens            src/tts_transformer.cpp:963-1028
+  generate() frame loop          src/tts_transformer.cpp:3108-3309
 
 The numpy forward keeps ggml's type rules only where they round: an F16 src0
 in ggml_mul_mat rounds its src1 to fp16, a Q8_0 src0 quantises it per
@@ -171,13 +173,82 @@ class NpRef:
         self.kv = {il: {} for il in range(self.cfg.n_layers)}
 
     def talker(self, embd, pos0):
-        """rows embd [n][d] at positions pos0..: (normed hidden [n][d], last-row logits)."""
+        """rows embd [n][d] at positions pos0..: (normed hidden [n][d], last-row logits).
+        The last row before the output norm is kept in self.last_x."""
         c = self.cfg
         x = np.asarray(embd, np.float64).reshape(-1, c.hidden_size)
         for il in range(c.n_layers):
             x = self.layer(f"talker.blk.{il}.", x, pos0, self.kv[il], c.rope_theta, False)
+        self.last_x = x[-1].copy()
         hid = np.stack([self.rms(r, self.vec("talker.output_norm.weight")) for r in x])
         return hid, self.mm("talker.codec_head.weight", hid[-1])
+
+    # -- the generate() frame loop, greedy (src/tts_transformer.cpp:3108-3309)
+    def cb0_greedy(self, logits, seen, frame, rep, eos_bias, target_frames):
+        """Codebook-0 choice of one frame (:3109-3145, :3177-3184): the top
+        1024 codec ids are suppressed except EOS; every distinct earlier token
+        gets the HF penalty (positive logits divided, others multiplied); the
+        EOS bias grows by 0.1 per frame past target_frames, capped at 6; the
+        first maximum wins."""
+        c = self.cfg
+        l = np.asarray(logits, np.float64).copy()
+        ids = np.arange(c.codec_vocab)
+        l[(ids >= c.codec_vocab - 1024) & (ids != c.codec_eos_id)] = -np.inf
+        penalised = list(seen)
+        if "penalty_per_occurrence" in self.mistakes:
+            penalised = self.cb0_history
+        eff = eos_bias
+        if target_frames > 0 and frame > target_frames:
+            slope = 0.2 if "ramp_slope" in self.mistakes else 0.1
+            eff = min(eff + slope * (frame - target_frames), 6.0)
+        if "penalty_after_bias" in self.mistakes:
+            l[c.codec_eos_id] += eff
+        for t in penalised:
+            if "penalty_sign" in self.mistakes:
+                l[t] = l[t] * rep if l[t] > 0 else l[t] / rep
+            else:
+                l[t] = l[t] / rep if l[t] > 0 else l[t] * rep
+        if "penalty_after_bias" not in self.mistakes:
+            l[c.codec_eos_id] += eff
+        return int(np.argmax(l))
+
+    def generate(self, prefill, trailing, pad, max_len, rep=1.05, eos_bias=0.0, target_frames=0):
+        """Greedy frames from prefill rows [n][d], trailing rows [t][d] and
+        the tts_pad row: (codes [frames][16], the talker logits each frame's
+        sampler started from).  Per frame: codebook 0 from the talker logits;
+        the code predictor on the talker's normed hidden row; the next step
+        embedding codec_embd[c0] + sum_g code_pred.codec_embd[g-1][c_g] +
+        (trailing[frame] if frame < len(trailing) else pad); one talker step."""
+        c = self.cfg
+        self.kv_reset()
+        hid, lg = self.talker(prefill, 0)
+        n_past = len(prefill)
+        codec = self.mat("talker.codec_embd.weight")[1]
+        cpe = [self.mat(f"code_pred.codec_embd.{g}.weight")[1] for g in range(c.n_codebooks - 1)]
+        seen, self.cb0_history = set(), []
+        codes, logs = [], []
+        for frame in range(max_len):
+            logs.append(lg)
+            tok = self.cb0_greedy(lg, seen, frame, rep, eos_bias, target_frames)
+            if tok == c.codec_eos_id:
+                break
+            seen.add(tok)
+            self.cb0_history.append(tok)
+            cp_in = self.last_x if "cp_unnormed" in self.mistakes else hid[-1]
+            rest, _ = self.code_pred(cp_in, tok)
+            fc = [tok] + [int(v) for v in rest]
+            codes.append(fc)
+            if frame + 1 >= max_len:
+                break
+            e = codec[fc[0]].copy()
+            for g in range(1, c.n_codebooks):
+                table = min(g, c.n_codebooks - 2) if "cp_embd_g" in self.mistakes else g - 1
+                e = e + cpe[table][fc[g]]
+            ti = frame + 1 if "trailing_next" in self.mistakes else frame
+            e = e + (trailing[ti] if ti < len(trailing) else pad)
+            hid, lg = self.talker(e[None], n_past)
+            n_past += 1
+        return np.array(codes, np.int32).reshape(-1, c.n_codebooks), np.stack(logs)
 
     # -- code predictor, greedy
     def code_pred(self, hidden, cb0):
@@ -480,3 +551,98 @@ def test_attention_rows_match_numpy_forward():
     o.set_attn_capture(-1)
     _talker_run(NpRef(cfg, w), o, cfg, embd)
     assert o.attn_rows() == []
+
+
+# ---------------------------------------------------------------- frame loop
+def _loop_weights(cfg, wt, seed):
+    """Synthetic weights whose talker output-norm gains spread over
+    [0.25, 1.75], so the talker's normed hidden row differs from the
+    un-normed one in direction, not only in scale (gains near 1 would leave
+    the code predictor's own RMSNorm nearly blind to the difference)."""
+    t = dict(Weights(cfg, wt, seed=seed).items())
+    rng = np.random.default_rng(seed + 1000)
+    g = rng.uniform(0.25, 1.75, cfg.hidden_size).astype(np.float32)
+    t["talker.output_norm.weight"] = (F32, (cfg.hidden_size, 1), g)
+    return _Tensors(t)
+
+
+def _loop_inputs(cfg, seed, n_pre=10, n_trail=4):
+    rng = np.random.default_rng(seed)
+    d = cfg.hidden_size
+    pre = (rng.standard_normal((n_pre, d)) * 0.5).astype(np.float32)
+    trail = (rng.standard_normal((n_trail, d)) * 0.5).astype(np.float32)
+    pad = (rng.standard_normal(d) * 0.5).astype(np.float32)
+    return pre, trail, pad
+
+
+def _oracle_loop(o, pre, trail, pad, max_len, rep, eos_bias, target_frames):
+    o.kv_reset(len(pre) + max_len + 8)
+    _, lg = o.prefill(pre, 0)
+    return o.frames(lg, len(pre), trail, pad, max_len, repetition_penalty=rep, eos_bias=eos_bias,
+                    target_frames=target_frames, want_logits=True)
+
+
+# (seed, planted sampler mistakes that change this run's codes)
+LOOP_RUNS = {"f16": ((31, ("penalty_per_occurrence", "penalty_sign")), (33, ("penalty_per_occurrence", "penalty_sign"))),
+             "q8_0": ((35, ("penalty_per_occurrence", "penalty_sign")), (36, ("penalty_per_occurrence",)))}
+
+
+@pytest.mark.parametrize("wt", ["f16", "q8_0"])
+def test_frame_loop_matches_numpy_generate(wt):
+    """orc_frames after orc_prefill (orc_generate_rows' composition) against
+    NpRef.generate, the float64 frame loop written from
+    src/tts_transformer.cpp:3108-3309: 12 greedy frames of the one-layer tiny
+    model from 10 prefill rows, 4 trailing rows (so frames 4.. add tts_pad),
+    repetition penalty 1.05 and an EOS bias of -2.  The codes agree exactly
+    and every frame's talker logits within the forward tolerance.  Planted
+    mistakes in the loop glue each miss: the trailing row of frame + 1, the
+    code-predictor embedding table g instead of g - 1, the talker's un-normed
+    hidden row into the code predictor (each moves the later frames' logits
+    far past the tolerance), the penalty once per earlier occurrence instead
+    of once per distinct token, and the inverted penalty sign rule (each
+    changes a code).  Applying the penalty after the EOS bias instead of
+    before cannot change a result, since the loop stops when EOS is drawn and
+    EOS never enters the penalised set; the test shows that too."""
+    cfg = small_cfg()
+    for seed, sampler_misses in LOOP_RUNS[wt]:
+        w = _loop_weights(cfg, wt, seed)
+        o = orc.Oracle(cfg, w, threads=4)
+        pre, trail, pad = _loop_inputs(cfg, seed)
+        kw = dict(rep=1.05, eos_bias=-2.0, target_frames=0)
+        co, lgo = _oracle_loop(o, pre, trail, pad, 12, **kw)
+        cr, lgr = NpRef(cfg, w).generate(pre, trail, pad, 12, **kw)
+        assert co.shape == (12, cfg.n_codebooks) and np.array_equal(co, cr), (seed, co, cr)
+        assert lgo.shape == lgr.shape == (12, cfg.codec_vocab)
+        assert_agrees([rel_err(lgo[f], lgr[f]) for f in range(12)], wt)
+        # a frame's logits are the talker's on the previous frame's step
+        # embedding; the code predictor's rows come out of the codes
+        for mistake in ("trailing_next", "cp_embd_g", "cp_unnormed"):
+            cm, lgm = NpRef(cfg, w, {mistake}).generate(pre, trail, pad, 12, **kw)
+            assert_misses([rel_err(lgo[f], lgm[f]) for f in range(1, min(len(lgm), 12))])
+        for mistake in sampler_misses:
+            cm, _ = NpRef(cfg, w, {mistake}).generate(pre, trail, pad, 12, **kw)
+            assert not np.array_equal(cm, co), (seed, mistake)
+        cm, _ = NpRef(cfg, w, {"penalty_after_bias"}).generate(pre, trail, pad, 12, **kw)
+        assert np.array_equal(cm, co)
+
+
+@pytest.mark.parametrize("wt", ["f16", "q8_0"])
+def test_frame_loop_eos_ramp_matches_numpy_generate(wt):
+    """The EOS ramp ends the loop (src/tts_transformer.cpp:3134-3145,
+    3186-3188): with target_frames 2 and no base bias, EOS gains 0.1 per
+    frame past frame 2 until it is the greedy choice.  The oracle and NpRef
+    stop at the same frame with the same codes and logits; a ramp of 0.2 per
+    frame stops earlier."""
+    cfg = small_cfg()
+    w = _loop_weights(cfg, wt, 31)
+    o = orc.Oracle(cfg, w, threads=4)
+    pre, trail, pad = _loop_inputs(cfg, 31)
+    kw = dict(rep=1.05, eos_bias=0.0, target_frames=2)
+    co, lgo = _oracle_loop(o, pre, trail, pad, 24, **kw)
+    cr, lgr = NpRef(cfg, w).generate(pre, trail, pad, 24, **kw)
+    assert 4 <= len(co) < 23, len(co)                 # stopped by EOS, not by max_len
+    assert np.array_equal(co, cr)
+    assert len(lgo) == len(lgr) == len(co) + 1        # the frame that drew EOS is logged too
+    assert_agrees([rel_err(a, b) for a, b in zip(lgo, lgr)], wt)
+    cm, _ = NpRef(cfg, w, {"ramp_slope"}).generate(pre, trail, pad, 24, **kw)
+    assert len(cm) < len(co)
