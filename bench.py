@@ -78,6 +78,8 @@ def cpu_baseline(cfg, w, text, spk, threads, budget_s):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import q3t_oracle as orc
     o = orc.Oracle(cfg, w, threads=threads)
+    global ORACLE_ISA
+    ORACLE_ISA = os.path.basename(orc.LIB_PATH)
     t0 = time.perf_counter()
     o.generate(text, spk, max_len=1, temperature=0.0, eos_bias=-1e4)
     t1 = time.perf_counter()
@@ -145,24 +147,45 @@ def prefill_bench(args, cfg, w):
     dev.upload_weights(w)
     dev.kv_reserve(n + 8)
     rows = (np.random.default_rng(21).standard_normal((n, cfg.hidden_size)) * 0.05).astype(np.float32)
-    for _ in range(max(args.warmup, 1)):
-        dev.prefill(rows, 0, want_hidden=False)
     steps = max(args.steps, 1)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        dev.prefill(rows, 0, want_hidden=False)
-    dt = (time.perf_counter() - t0) / steps
+
+    def timed():
+        for _ in range(max(args.warmup, 1)):
+            dev.prefill(rows, 0, want_hidden=False)
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dev.prefill(rows, 0, want_hidden=False)
+        return (time.perf_counter() - t0) / steps
+
+    dt = timed()
+    exact_ms = None
+    if args.weights == "f16":
+        # the exact f64-MFMA form of the F16 GEMMs beside the default fp16-MFMA one
+        prev = os.environ.get("Q3T_PF_EXACT")
+        os.environ["Q3T_PF_EXACT"] = "1"
+        try:
+            exact_ms = round(timed() * 1e3, 3)
+        finally:
+            if prev is None:
+                del os.environ["Q3T_PF_EXACT"]
+            else:
+                os.environ["Q3T_PF_EXACT"] = prev
     dev.close()
     d, qd = cfg.hidden_size, cfg.n_head * cfg.head_dim
     qkvd = qd + 2 * cfg.n_kv_head * cfg.head_dim
     gemm_ops = 2.0 * n * cfg.n_layers * (qkvd * d + d * qd + 2 * cfg.ffn_size * d + d * cfg.ffn_size)
+    fast = args.weights == "f16" and os.environ.get("Q3T_PF_EXACT", "0") != "1"
     print(json.dumps({
         "metric": "talker prefill rows/s (long prompt)", "value": round(n / dt, 1), "unit": "rows/s", "n_gpus": 1,
         "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True,
         "dtype": "int8" if args.weights == "q8_0" else "f16", "data": "synthetic",
-        "config": {"workload": f"talker prefill, {n} rows, {args.weights.upper()} 0.6B shapes", "rows": n},
+        "config": {"workload": f"talker prefill, {n} rows, {args.weights.upper()} 0.6B shapes", "rows": n,
+                   "gemm": "int8 MFMA, fp64 block epilogue" if args.weights == "q8_0" else
+                   ("fp16 MFMA, fp32 accumulation" if fast else "exact f64 MFMA")},
         "gemm_tops": round(gemm_ops / dt / 1e12, 2),
-        "mfma_util": round(gemm_ops / dt / 5.0e15, 4) if args.weights == "q8_0" else None}))
+        "mfma_util": round(gemm_ops / dt / (5.0e15 if args.weights == "q8_0" else 2.5e15), 4),
+        "exact_f64_form_ms": exact_ms}))
 
 
 def step_bench(args, cfg, w):
@@ -441,7 +464,16 @@ def vocoder_bench(args):
         "cpu_baseline": cpu}))
 
 
+ORACLE_ISA = "liboracle.so"
+
+
 def main():
+    # the CPU-baseline leg loads the oracle build for the widest ISA level this
+    # host supports (x86-64-v4 with AVX-512, else x86-64-v3)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from q3t_oracle import host_isa
+    if host_isa() == "v4" and os.path.exists(os.path.join(ROOT, "oracle", "liboracle_v4.so")):
+        os.environ.setdefault("Q3T_ORACLE_ISA", "v4")
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
@@ -566,7 +598,8 @@ def main():
         cpu_fps, n_frames = cpu_baseline(cfg, w, text, spk, nthreads, args.cpu_budget)
         cpu = {"value": round(cpu_fps, 3), "unit": "frames/s", "cores": nthreads, "kind": "port",
                "sample": f"oracle generate() of {n_frames} frames minus a 1-frame run, same weights/prompt, "
-                         f"{nthreads} threads; {host}. " + PORT_NOTE}
+                         f"{nthreads} threads; {host}; {ORACLE_ISA} (-march=x86-64-"
+                         f"{'v4' if 'v4' in ORACLE_ISA else 'v3'}, the host's widest level). " + PORT_NOTE}
         # the same leg on all the host cores this process may use (capped at
         # the GPU's share of them), with half the time budget
         nall = min(len(os.sched_getaffinity(0)), args.cpu_threads_max)

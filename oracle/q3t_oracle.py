@@ -10,7 +10,24 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+
+def host_isa():
+    """"v4" when the host CPU has the AVX-512 subsets of x86-64-v4, else "v3"."""
+    need = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return "v4" if need <= set(line.split(":", 1)[1].split()) else "v3"
+    except OSError:
+        pass
+    return "v3"
+
+
+# Q3T_ORACLE_ISA=v4 (the CPU-baseline leg, on a host with AVX-512) loads the
+# x86-64-v4 build; results are the same, only the speed differs.
+LIB_PATH = os.path.join(HERE, "liboracle_v4.so" if os.environ.get("Q3T_ORACLE_ISA") == "v4" else "liboracle.so")
 
 F32, F16, Q8_0 = 0, 1, 8
 

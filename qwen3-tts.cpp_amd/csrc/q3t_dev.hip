@@ -87,6 +87,8 @@ struct q3t_dev {
     // f64 MFMA prefill attention: scores and probabilities [n_head][n][ls]
     float * pf_s = nullptr; uint16_t * pf_p = nullptr; size_t pf_sp_cap = 0;
     float * pf_g = nullptr, * pf_u = nullptr, * pf_f = nullptr;
+    uint16_t * pf_h = nullptr, * pf_l = nullptr;  // fp16 GEMM inputs of the fast F16 prefill (rows x kmax / ffn)
+    float * pf_sc = nullptr;                      // per-row power-of-two scales of the widened ffn_down input
     // multi-stream decode: nb independent streams sharing the weights
     int32_t nb = 0, sb_ctx = 0;
     uint16_t * skc = nullptr, * svc = nullptr;        // [stream][layer][kv_head][sb_ctx][128]
@@ -147,6 +149,8 @@ struct q3t_dev {
     bool fk_ok = false;            // model / context qualify this context for it
     int fk_variant = 0;            // see fk_kernel()
     int xcd_map = -1;              // frame-launch workgroups dealt round-robin over the XCDs: -1 unknown, 0 no, 1 yes
+    bool fk_no_xcd = false;        // a re-probe found the dealing changed: the row-parallel program from then on
+    unsigned char * fk_snap = nullptr;   // the frame loop's carried state before a frames_run on the XCD program
     bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
     bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
     bool fk_tab = false;           // the persistent kernel reads cp_tab
@@ -694,7 +698,19 @@ __global__ __launch_bounds__(fk::kT) void k_xcc_map(int32_t * out) {
 // XCDs round-robin, workgroup b on XCD (b + r) % 8 for one rotation r (the
 // XCD-parallel layer program relies on the classes b % 8 each sharing an
 // XCD; r itself varies between launches); checked once per context.
-int xcd_map_ok(q3t_dev * c, int grid, bool & ok) {
+// Q3T_TEST_XCD_REPROBE_FAIL=1 (read per call) makes a re-probe after a
+// frames_run on the XCD-parallel program report a changed dealing, so tests
+// can exercise the switch to the row-parallel program from the host.
+bool test_reprobe_fail() {
+    const char * e = std::getenv("Q3T_TEST_XCD_REPROBE_FAIL");
+    return e && e[0] == '1';
+}
+
+int xcd_map_ok(q3t_dev * c, int grid, bool & ok, bool forced_fail = false) {
+    if (forced_fail) {
+        c->xcd_map = 0;
+        std::fprintf(stderr, "q3t: XCD map re-check forced to fail; using the row-parallel frame program\n");
+    }
     if (c->xcd_map < 0) {
         int32_t * d = nullptr;
         if (dev_alloc_t(c, &d, (size_t) grid)) return -1;
@@ -798,7 +814,8 @@ int fk_prepare(q3t_dev * c) {
     // the XCD-parallel layer program: 0.6B shapes (Q8_0 or F16), one
     // workgroup per CU on 256 CUs, workgroups dealt round-robin over the 8
     // XCDs (Q3T_FRAME_XCD=0 turns it off)
-    bool xcd = (variant == 1 || variant == 3) && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0;
+    bool xcd = (variant == 1 || variant == 3) && grid == 256 && g.n_kv_head == fk::kXcd && g.n_layers + g.cp_layers > 0 &&
+               !c->fk_no_xcd;
     if (const char * e = std::getenv("Q3T_FRAME_XCD")) if (e[0] == '0') xcd = false;
     if (xcd && xcd_map_ok(c, grid, xcd)) return -1;
     if (xcd) variant = variant == 1 ? 5 : 8;
@@ -902,6 +919,40 @@ hipError_t fk_launch(q3t_dev * c, int32_t frame, int32_t mode) {
         hipLaunchCooperativeKernel(fk_kernel(c->fk_variant), dim3(c->fk_grid), dim3(fk::kT), args, 0, c->stream);
     if (e == hipSuccess) ++c->fk_epoch;
     return e;
+}
+
+// The state one frame carries to the next on the persistent kernel: the frame
+// state, the repetition set, the talker's logits and normed hidden row, and
+// the talker head's greedy candidates.  frames_run keeps a copy while the
+// XCD-parallel program runs, so a batch whose waits timed out can be run again
+// from where it began.
+struct SnapPart { void * p; size_t bytes; };
+static int fk_snap_parts(q3t_dev * c, SnapPart (&parts)[5]) {
+    const q3t_config & g = c->cfg;
+    parts[0] = {c->st, sizeof(FrameState)};
+    parts[1] = {c->seen, (size_t) g.codec_vocab};
+    parts[2] = {c->logits, (size_t) g.codec_vocab * 4};
+    parts[3] = {c->hidden, (size_t) g.hidden_size * 4};
+    parts[4] = {c->fk_cand, (size_t) 2 * 256 * 4};
+    return 5;
+}
+
+static int fk_snapshot(q3t_dev * c, bool restore) {
+    SnapPart parts[5];
+    const int np = fk_snap_parts(c, parts);
+    if (!c->fk_snap) {
+        size_t total = 0;
+        for (int i = 0; i < np; ++i) total += (parts[i].bytes + 255) / 256 * 256;
+        if (dev_alloc(c, (void **) &c->fk_snap, total)) return -1;
+    }
+    size_t off = 0;
+    for (int i = 0; i < np; ++i) {
+        void * dst = restore ? parts[i].p : (void *) (c->fk_snap + off);
+        const void * src = restore ? (const void *) (c->fk_snap + off) : parts[i].p;
+        HIP_OK(hipMemcpyAsync(dst, src, parts[i].bytes, hipMemcpyDeviceToDevice, c->stream));
+        off += (parts[i].bytes + 255) / 256 * 256;
+    }
+    return 0;
 }
 
 // Whether a single-step call (talker step or code predictor) can run on the
@@ -1383,14 +1434,17 @@ int ensure_pf(q3t_dev * c, int n) {
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
     const int kmax = std::max(std::max(d, qd), g.ffn_size);
     for (void * p : {(void *) c->pf_q, (void *) c->pf_dx, (void *) c->pf_xa, (void *) c->pf_xb, (void *) c->pf_qkv,
-                     (void *) c->pf_att, (void *) c->pf_g, (void *) c->pf_u, (void *) c->pf_f})
+                     (void *) c->pf_att, (void *) c->pf_g, (void *) c->pf_u, (void *) c->pf_f, (void *) c->pf_h,
+                     (void *) c->pf_l, (void *) c->pf_sc})
         if (p) dev_free(c, p);
     c->pf_rows = 0;
     const size_t r = (size_t) n;
     if (dev_alloc_t(c, &c->pf_q, r * kmax) || dev_alloc_t(c, &c->pf_dx, r * (kmax / kQK)) ||
         dev_alloc_t(c, &c->pf_xa, r * d) || dev_alloc_t(c, &c->pf_xb, r * d) || dev_alloc_t(c, &c->pf_qkv, r * qkvd) ||
         dev_alloc_t(c, &c->pf_att, r * qd) || dev_alloc_t(c, &c->pf_g, r * g.ffn_size) ||
-        dev_alloc_t(c, &c->pf_u, r * g.ffn_size) || dev_alloc_t(c, &c->pf_f, r * g.ffn_size))
+        dev_alloc_t(c, &c->pf_u, r * g.ffn_size) || dev_alloc_t(c, &c->pf_f, r * g.ffn_size) ||
+        dev_alloc_t(c, &c->pf_h, r * kmax) || dev_alloc_t(c, &c->pf_l, r * g.ffn_size) ||
+        dev_alloc_t(c, &c->pf_sc, r))
         return -1;
     c->pf_rows = n;
     return 0;
@@ -1503,11 +1557,54 @@ void pf_gemm_f16(q3t_dev * c, const Slot & w, int N, int K, int n, const float *
 #undef Q3T_PF_F16
 }
 
+// F16 weights x fp16 rows on the fast fp16-MFMA GEMM (fp32 accumulation):
+// y = (W . xh[t] (+ W . xl[t])) * xsc[t] (+ res).  128 x 128 tiles with one
+// stage in flight when that gives at least one workgroup per CU, else
+// 128 x 64 tiles with two stages in flight (and always for the two-plane
+// input); measured best on the 0.6B shapes at 2,048 rows: QKV 30 us, Wo 27 us,
+// gate / up 29 us, the two-plane down 47 us.
+void pf_gemm_h16(q3t_dev * c, const Slot & w, int N, int K, int n, const uint16_t * xh, const uint16_t * xl, int xs,
+                 const float * xsc, float * y, const float * res, int rs) {
+    constexpr int BR = 32 * 4;
+    const bool big = !xl && (int64_t) (N / BR) * ((n + 127) / 128) >= c->n_cu;
+    const int TT = big ? 4 : 2;
+    const dim3 grid(N / BR, (n + 32 * TT - 1) / (32 * TT));
+#define Q3T_PF_H16(tt, lo, pd)                                                                                    \
+    hipLaunchKernelGGL((pf::k_gemm_h16<4, tt, lo, pd>), grid, dim3(kBlock), 0, c->stream, (const uint16_t *) w.data, \
+                       K, xh, xl, xs, xsc, n, y, N, res, rs)
+    if (xl) Q3T_PF_H16(2, true, 2);
+    else if (big) Q3T_PF_H16(4, false, 1);
+    else Q3T_PF_H16(2, false, 2);
+#undef Q3T_PF_H16
+}
+
+// The tiled prefill's fast forms for F16 layers (fp16 MFMA, fp32
+// accumulation: the F16 GEMMs and the causal attention's scores and P.V) are
+// the default; Q3T_PF_EXACT=1 (read per call) keeps the exact f64-MFMA forms,
+// whose rows equal the GEMV path's bit for bit.  Q8_0 layers keep the exact
+// attention: their GEMM inputs are quantised per 32-block, so a difference at
+// fp32 rounding level in an attention row can move a quantised value by a
+// whole step, and 28 layers of such steps leave the logits ~3e-2 apart
+// (measured on 200 rows), where the exact forms match the oracle bit for bit.
+bool pf_exact() {
+    const char * e = std::getenv("Q3T_PF_EXACT");
+    return e && e[0] == '1';
+}
+
+bool pf_f16_fast(const q3t_config & g) {
+    if (pf_exact()) return false;
+    const int d = g.hidden_size, qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
+    return d % 128 == 0 && qkvd % 128 == 0 && g.ffn_size % 128 == 0 && qd % pf::kHK == 0 && d % pf::kHK == 0 &&
+           g.ffn_size <= 16 * kBlock;
+}
+
 // Causal attention of the n prefill rows (QKV rows in c->pf_qkv, K/V already
-// in the layer's cache) into c->pf_att.  From 64 rows on: the f64 MFMA
-// kernels (scores, softmax, P.V; Q3T_PF_ATT_MFMA=0 keeps the row kernel);
-// below, or when the scores would not fit 4 GiB, one workgroup per row.
-int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uint16_t * vc, int n, int n_past) {
+// in the layer's cache) into c->pf_att.  From 64 rows on: the MFMA kernels
+// (scores, softmax, P.V; Q3T_PF_ATT_MFMA=0 keeps the row kernel), exact on f64
+// MFMA or, fast, on fp16 (bfloat16) MFMA with fp32 accumulation; below, or
+// when the scores would not fit 4 GiB, one workgroup per row.
+int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uint16_t * vc, int n, int n_past,
+                 bool fast) {
     const q3t_config & g = c->cfg;
     const int qd = g.n_head * g.head_dim, qkvd = qd + 2 * g.n_kv_head * g.head_dim;
     const float scale = 1.0f / std::sqrt((float) g.head_dim);
@@ -1542,18 +1639,22 @@ int pf_attention(q3t_dev * c, const LayerDev & L, const uint16_t * kc, const uin
     hipLaunchKernelGGL(pf::k_att_q, dim3(n, (g.n_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                        qkvd, L.q_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin, n, n_past,
                        g.n_head, qh, bf);
-    hipLaunchKernelGGL(pf::k_att_scores, tiles, dim3(pf::kAttT), 0, c->stream, (const uint16_t *) qh, kc, c->n_ctx,
-                       g.n_head, g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
+    hipLaunchKernelGGL(fast ? pf::k_att_scores_fast : pf::k_att_scores, tiles, dim3(pf::kAttT), 0, c->stream,
+                       (const uint16_t *) qh, kc, c->n_ctx, g.n_head, g.n_kv_head, n, n_past, scale, c->pf_s, ls, bf);
     hipLaunchKernelGGL(pf::k_att_softmax, dim3((n + 3) / 4, g.n_head), dim3(kBlock), 0, c->stream,
                        (const float *) c->pf_s, n, n_past, ls, c->pf_p, bf);
-    hipLaunchKernelGGL(pf::k_att_pv, tiles, dim3(pf::kAttT), 0, c->stream, (const uint16_t *) c->pf_p, ls, vc, c->n_ctx,
-                       g.n_head, g.n_kv_head, n, n_past, c->pf_att, qd, bf);
+    hipLaunchKernelGGL(fast ? pf::k_att_pv_fast : pf::k_att_pv, tiles, dim3(pf::kAttT), 0, c->stream,
+                       (const uint16_t *) c->pf_p, ls, vc, c->n_ctx, g.n_head, g.n_kv_head, n, n_past, c->pf_att, qd, bf);
     return 0;
 }
 
-// Talker prefill of n tokens (rows in c->stage) with F16 layers on the exact
-// VALU GEMMs; same layer program and buffers as prefill_mfma (c->pf_f holds
-// the RMSNorm'd rows until SwiGLU overwrites it).
+// Talker prefill of n tokens (rows in c->stage) with F16 layers: by default on
+// the fast fp16-MFMA GEMMs (fp32 accumulation, the inputs written as fp16
+// rows by the RMSNorm, a rounding pass over the attention rows, and the
+// SwiGLU's two-plane form for the widened ffn_down); with Q3T_PF_EXACT=1
+// on the exact f64-MFMA GEMMs, whose rows equal the GEMV path's.  Same layer
+// program and buffers as prefill_mfma (c->pf_f holds the RMSNorm'd rows of
+// the exact form until SwiGLU overwrites it).
 int prefill_f16(q3t_dev * c, int n, int n_past) {
     const q3t_config & g = c->cfg;
     const int d = g.hidden_size, qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim, qkvd = qd + 2 * kd;
@@ -1561,7 +1662,32 @@ int prefill_f16(q3t_dev * c, int n, int n_past) {
     const size_t lstride = (size_t) g.n_kv_head * c->n_ctx * g.head_dim;
     const float scale = 1.0f / std::sqrt((float) g.head_dim);
     const float * x = c->stage;
-    for (int il = 0; il < g.n_layers; ++il) {
+    const bool fast = pf_f16_fast(g);
+    for (int il = 0; il < g.n_layers && fast; ++il) {
+        const LayerDev & L = c->talker[il];
+        uint16_t * kc = c->kc + il * lstride;
+        uint16_t * vc = c->vc + il * lstride;
+        hipLaunchKernelGGL(pf::k_rmsnorm_rows_h16, dim3(n), dim3(kBlock), 0, c->stream, x, L.attn_norm, g.rms_eps, d,
+                           c->pf_h);
+        pf_gemm_h16(c, L.qkv, qkvd, d, n, c->pf_h, nullptr, d, nullptr, c->pf_qkv, nullptr, 0);
+        hipLaunchKernelGGL(pf::k_kv_rows, dim3(n, (g.n_kv_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
+                           qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
+                           kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
+        if (pf_attention(c, L, kc, vc, n, n_past, true)) return -1;
+        const size_t na = (size_t) n * qd;
+        hipLaunchKernelGGL(pf::k_rows_h16, dim3((unsigned) std::min<size_t>((na + kBlock - 1) / kBlock, 4096)),
+                           dim3(kBlock), 0, c->stream, (const float *) c->pf_att, qd, qd, n, c->pf_h);
+        pf_gemm_h16(c, L.wo, d, qd, n, c->pf_h, nullptr, qd, nullptr, c->pf_xb, x, d);
+        hipLaunchKernelGGL(pf::k_rmsnorm_rows_h16, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xb,
+                           L.ffn_norm, g.rms_eps, d, c->pf_h);
+        pf_gemm_h16(c, L.wg, ffn, d, n, c->pf_h, nullptr, d, nullptr, c->pf_g, nullptr, 0);
+        pf_gemm_h16(c, L.wu, ffn, d, n, c->pf_h, nullptr, d, nullptr, c->pf_u, nullptr, 0);
+        hipLaunchKernelGGL(pf::k_swiglu_h16, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_g,
+                           (const float *) c->pf_u, ffn, c->pf_h, c->pf_l, c->pf_sc);
+        pf_gemm_h16(c, L.wd, d, ffn, n, c->pf_h, c->pf_l, ffn, c->pf_sc, c->pf_xa, c->pf_xb, d);
+        x = c->pf_xa;
+    }
+    for (int il = 0; il < g.n_layers && !fast; ++il) {
         const LayerDev & L = c->talker[il];
         uint16_t * kc = c->kc + il * lstride;
         uint16_t * vc = c->vc + il * lstride;
@@ -1570,7 +1696,7 @@ int prefill_f16(q3t_dev * c, int n, int n_past) {
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(n, (g.n_kv_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
-        if (pf_attention(c, L, kc, vc, n, n_past)) return -1;
+        if (pf_attention(c, L, kc, vc, n, n_past, false)) return -1;
         pf_gemm_f16(c, L.wo, d, qd, n, c->pf_att, qd, false, c->pf_xb, x, d);
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(kBlock), 0, c->stream, (const float *) c->pf_xb, L.ffn_norm,
                            g.rms_eps, d, c->pf_f);
@@ -1608,7 +1734,7 @@ int prefill_mfma(q3t_dev * c, int n, int n_past) {
         hipLaunchKernelGGL(pf::k_kv_rows, dim3(n, (g.n_kv_head + 3) / 4), dim3(kBlock), 0, c->stream, (const float *) c->pf_qkv,
                            qkvd, qd, kd, L.k_norm, g.rms_eps, (const float *) c->rope_cos, (const float *) c->rope_sin,
                            kc, vc, c->n_ctx, n_past, c->kv_bf16 ? 1 : 0);
-        if (pf_attention(c, L, kc, vc, n, n_past)) return -1;
+        if (pf_attention(c, L, kc, vc, n, n_past, false)) return -1;
         pf_quant(c, c->pf_att, n, qd, nullptr);
         pf_gemm(c, L.wo, d, qd, n, c->pf_xb, x);
         pf_quant(c, c->pf_xb, n, d, L.ffn_norm);
@@ -2214,6 +2340,11 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
         HIP_OK(hipEventCreate(&c->run_ev[0]));
         HIP_OK(hipEventCreate(&c->run_ev[1]));
     }
+    // on the XCD-parallel program, keep the carried state: a wait timeout
+    // there is re-checked below and the batch run again on the row-parallel
+    // program if the workgroup dealing has changed
+    const bool xcd_run = c->fk_ok && fk_xcd(c->fk_variant) && n_frames > 0;
+    if (xcd_run && fk_snapshot(c, false)) return -1;
     if (n_frames > 0) HIP_OK(hipEventRecord(c->run_ev[0], c->stream));
     for (int i = 0; i < n_frames; ++i) {
         if (c->fk_ok) {
@@ -2252,6 +2383,34 @@ int q3t_dev_frames_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int32
     int32_t fk_err = 0;
     if (c->fk_ok) HIP_OK(hipMemcpyAsync(&fk_err, c->fk_err, sizeof fk_err, hipMemcpyDeviceToHost, c->stream));
     if (sync(c)) return -1;
+    const bool forced = xcd_run && c->fk_ok && fk_xcd(c->fk_variant) && test_reprobe_fail();
+    if ((fk_err || forced) && xcd_run && c->fk_ok && fk_xcd(c->fk_variant)) {
+        // A wait of the XCD-parallel program timed out.  Its hand-offs inside
+        // an XCD rely on the workgroups of each class b % 8 sharing one XCD;
+        // check the dealing again, and if it changed, rerun this batch from
+        // the kept state on the row-parallel program (fresh launches), which
+        // gives the same codes.
+        c->xcd_map = -1;
+        bool ok = false;
+        if (xcd_map_ok(c, c->fk_grid, ok, forced)) return -1;
+        if (!ok) {
+            if (fk_snapshot(c, true)) return -1;
+            c->frames_launched -= n_frames;
+            c->fk_no_xcd = true;
+            c->fk_ok = false;
+            if (fk_prepare(c)) return -1;
+            if (c->fk_ok) {
+                HIP_OK(hipMemsetAsync(c->fk_arena, 0, c->fk_arena_bytes, c->stream));
+                HIP_OK(hipMemsetAsync(c->fk_err, 0, sizeof(int32_t), c->stream));
+                c->fk_epoch = 0;
+                if (fk_upload_args(c)) return -1;
+            } else if (ensure_frame_graph(c)) {
+                return -1;
+            }
+            if (sync(c)) return -1;
+            return q3t_dev_frames_run(c, n_frames, codes_out, n_emitted_out, eos_out);
+        }
+    }
     if (fk_err) return fail(c, fk_err_msg(fk_err));
     if (n_frames > 0) {
         float ms = 0.0f;

@@ -14,6 +14,8 @@
 // path, so the result equals the chunked GEMV prefill bit for bit.
 #pragma once
 
+#include <type_traits>
+
 #include "q3t_kernels.h"
 
 namespace q3t {
@@ -454,6 +456,248 @@ __global__ __launch_bounds__(kBlock) void k_gemm_f16(const uint16_t * __restrict
         }
 }
 
+// ------------------------------------------------- F16 GEMM on fp16 MFMA
+// The fast form of the F16 prefill GEMM: the reference's F16 mul_mat rounds
+// its F32 activation to fp16 and accumulates fp16 x fp16 products in fp32
+// (src/tts_transformer.cpp:1474-1617 via ggml), so v_mfma_f32_16x16x32_f16
+// with fp32 accumulation is the same class of arithmetic (the exact
+// f64-MFMA form above stays selectable; the two differ at fp32 rounding
+// level).  Y[t][r] = (sum_k X[t][k] W[r][k]) * xsc[t] (+ res[t][r]).
+//   - X arrives as fp16 rows (xh [n][xs]); the widened ffn_down (F32 weights
+//     and activation in the reference) adds a low plane xl with
+//     xh + xl = x * 2^-e to about 22 bits, the row scaled by a power of two
+//     (xsc[t] = 2^e) so that neither plane overflows fp16; each weight
+//     fragment then meets both planes, two MFMAs per step;
+//   - the workgroup tile is 32 WM weight rows x 32 TT tokens, four waves in
+//     a 2 x 2 arrangement, each 16 WM rows x 16 TT tokens as WM x TT MFMA
+//     tiles with the weights as A (m = row) and the tokens as B (n = token),
+//     so lane l's accumulator holds rows 4 (l/16) .. +3 of token l % 16:
+//     one float4 store;
+//   - K in stages of 64 staged in LDS as 16-byte chunks, chunk c of row r at
+//     position c ^ (r & 7) (8 consecutive rows of one chunk hit distinct
+//     banks), double-buffered: stage s + 1's global loads are in flight
+//     during stage s's MFMAs;
+//   - tokens past n stage zeros and store nothing.
+// Requires N % (32 WM) == 0 and K % 64 == 0 (the host checks).
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+constexpr int kHK = 64;            // K per stage (8 chunks of 8 halves)
+
+__device__ __forceinline__ int hswz(int r, int c) { return r * kHK + ((c ^ (r & 7)) << 3); }
+
+// WM: 16-row MFMA tiles per wave along the weight rows (workgroup rows 32 WM);
+// TT: 16-token tiles per wave (workgroup tokens 32 TT); LO: the low plane;
+// PD: stages in flight (1: the next stage's loads overlap this stage's
+// MFMAs; 2: two register sets, loads issued two stages ahead).
+template <int WM, int TT, bool LO, int PD>
+struct H16Tile {
+    static constexpr int BR = 32 * WM, BT = 32 * TT;         // workgroup tile
+    static constexpr int WSUB = BR * kHK, XSUB = BT * kHK;   // halves per stage and plane
+    static constexpr int STAGE = WSUB + (LO ? 2 : 1) * XSUB;
+    static constexpr int NW = BR * 8 / kBlock;               // W chunks per thread per stage
+    static constexpr int NX = BT * 8 / kBlock;               // X chunks per thread per stage and plane
+};
+
+template <int WM, int TT, bool LO, int PD>
+__global__ __launch_bounds__(kBlock) void k_gemm_h16(const uint16_t * __restrict__ W, int32_t K,
+                                                     const uint16_t * __restrict__ xh, const uint16_t * __restrict__ xl,
+                                                     int32_t xs, const float * __restrict__ xsc, int32_t n,
+                                                     float * __restrict__ Y, int32_t ys, const float * __restrict__ res,
+                                                     int32_t rs) {
+    using T = H16Tile<WM, TT, LO, PD>;
+    __shared__ __align__(16) uint16_t lds[2 * T::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 1, wt = wave >> 1, lm = lane & 15, lk = lane >> 4;
+    const int r0 = blockIdx.x * T::BR, t0 = blockIdx.y * T::BT;
+    const uint16_t * gw[T::NW];
+    int lw[T::NW];
+#pragma unroll
+    for (int u = 0; u < T::NW; ++u) {
+        const int c = tid + u * kBlock, row = c >> 3, ch = c & 7;
+        gw[u] = W + (size_t) (r0 + row) * K + ch * 8;
+        lw[u] = hswz(row, ch);
+    }
+    size_t gx[T::NX];                              // element offsets of this thread's X chunks
+    int lx[T::NX];
+    bool ox[T::NX];
+#pragma unroll
+    for (int u = 0; u < T::NX; ++u) {
+        // tokens past n load row n - 1 (no branch around the load) and stage zeros
+        const int c = tid + u * kBlock, row = c >> 3, ch = c & 7;
+        ox[u] = t0 + row < n;
+        gx[u] = (size_t) (ox[u] ? t0 + row : n - 1) * xs + ch * 8;
+        lx[u] = T::WSUB + hswz(row, ch);
+    }
+    // register sets of the stages in flight, indexed by compile-time
+    // constants only (a runtime index would put them in scratch memory)
+    v4i rw[PD][T::NW], rx[PD][T::NX], rl[PD][LO ? T::NX : 1];
+    auto fetch = [&](auto set_c, int k0) {
+        constexpr int set = decltype(set_c)::value;
+#pragma unroll
+        for (int u = 0; u < T::NW; ++u) rw[set][u] = *(const v4i *) (gw[u] + k0);
+#pragma unroll
+        for (int u = 0; u < T::NX; ++u) {
+            rx[set][u] = *(const v4i *) (xh + gx[u] + k0);
+            if (LO) rl[set][LO ? u : 0] = *(const v4i *) (xl + gx[u] + k0);
+        }
+    };
+    auto stash = [&](auto set_c, int buf) {
+        constexpr int set = decltype(set_c)::value;
+        uint16_t * st = lds + buf * T::STAGE;
+#pragma unroll
+        for (int u = 0; u < T::NW; ++u) *(v4i *) (st + lw[u]) = rw[set][u];
+#pragma unroll
+        for (int u = 0; u < T::NX; ++u) {
+            v4i a = rx[set][u];
+            if (!ox[u]) a = (v4i){0, 0, 0, 0};
+            *(v4i *) (st + lx[u]) = a;
+            if (LO) {
+                v4i b = rl[set][LO ? u : 0];
+                if (!ox[u]) b = (v4i){0, 0, 0, 0};
+                *(v4i *) (st + T::XSUB + lx[u]) = b;
+            }
+        }
+    };
+    f4v acc[WM][TT];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < TT; ++j) acc[i][j] = (f4v){0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&](int buf) {
+        const uint16_t * st = lds + buf * T::STAGE;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            h8v af[WM], bf[TT], bl[LO ? TT : 1];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) af[i] = *(const h8v *) (st + hswz(wr * 16 * WM + 16 * i + lm, 4 * q + lk));
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const int off = T::WSUB + hswz(wt * 16 * TT + 16 * j + lm, 4 * q + lk);
+                bf[j] = *(const h8v *) (st + off);
+                if (LO) bl[LO ? j : 0] = *(const h8v *) (st + T::XSUB + off);
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < TT; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    if (LO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bl[LO ? j : 0], acc[i][j], 0, 0, 0);
+                }
+        }
+        // keep the next stage's LDS stores (and so the wait for its global
+        // loads) after this stage's MFMAs: without the barriers the compiler
+        // hoists them right behind the loads, which exposes the load latency
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, PD == 2 ? 1 : 0>;
+    const int S = K / kHK;
+    // stage s computes from LDS buffer s & 1.  PD 1: stage s + 1 is loaded into
+    // the one register set during stage s and stashed after its MFMAs.  PD 2:
+    // stage s + 2 is loaded into set s & 1 during stage s, while stage s + 1
+    // (set (s + 1) & 1, loaded during stage s - 1) is stashed after the MFMAs.
+    auto step = [&](int s, auto cur, auto nxt) {
+        if (PD == 1 && s + 1 < S) fetch(C0{}, (s + 1) * kHK);
+        if (PD == 2 && s + 2 < S) fetch(cur, (s + 2) * kHK);
+        mfmas(s & 1);
+        if (s + 1 < S) {
+            if (PD == 1) stash(C0{}, (s + 1) & 1);
+            else stash(nxt, (s + 1) & 1);
+        }
+        __syncthreads();
+    };
+    fetch(C0{}, 0);
+    stash(C0{}, 0);
+    if (PD == 2 && S > 1) fetch(C1{}, kHK);
+    __syncthreads();
+    for (int s = 0; s < S; s += 2) {
+        step(s, C0{}, C1{});
+        if (s + 1 < S) step(s + 1, C1{}, C0{});
+    }
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int tok = t0 + wt * 16 * TT + 16 * j + lm;
+        if (tok >= n) continue;
+        const float sc = xsc ? xsc[tok] : 1.0f;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int row = r0 + wr * 16 * WM + 16 * i + 4 * lk;
+            float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+            if (xsc) { v.x *= sc; v.y *= sc; v.z *= sc; v.w *= sc; }
+            if (res) {
+                const float4 q = *(const float4 *) (res + (size_t) tok * rs + row);
+                v.x = v.x + q.x; v.y = v.y + q.y; v.z = v.z + q.z; v.w = v.w + q.w;
+            }
+            *(float4 *) (Y + (size_t) tok * ys + row) = v;
+        }
+    }
+}
+
+// fp16 rows for the fast GEMM: yh[t][e] = fp16(x[t][e]) (the rounding the
+// reference's F16 mul_mat applies to its F32 activation).
+__global__ __launch_bounds__(kBlock) void k_rows_h16(const float * __restrict__ x, int32_t xs, int32_t K, int32_t n,
+                                                     uint16_t * __restrict__ yh) {
+    const size_t cnt = (size_t) n * K;
+    for (size_t i = (size_t) blockIdx.x * kBlock + threadIdx.x; i < cnt; i += (size_t) gridDim.x * kBlock) {
+        const size_t t = i / K, e = i - t * K;
+        yh[i] = f2h(x[t * xs + e]);
+    }
+}
+
+// RMSNorm rows (k_rmsnorm_rows' numbers) written as fp16: the input of an F16
+// GEMM, which rounds it to fp16 anyway.
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_rows_h16(const float * __restrict__ x, const float * __restrict__ w,
+                                                             float eps, int32_t d, uint16_t * __restrict__ yh) {
+    __shared__ double red[4];
+    const float * xr = x + (size_t) blockIdx.x * d;
+    double ss = 0.0;
+    for (int e = threadIdx.x; e < d; e += kBlock) { const float v = xr[e]; ss += (double) (v * v); }
+    const double tot = block_sum_d(ss, red);
+    const float mean = (float) (tot / (double) d);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int e = threadIdx.x; e < d; e += kBlock) { const float v = xr[e] * scale; yh[(size_t) blockIdx.x * d + e] = f2h(v * w[e]); }
+}
+
+// SwiGLU rows f = silu(g) * u (k_swiglu_rows' numbers) as the two fp16 planes
+// of the widened ffn_down's fast GEMM: with 2^e the power of two that puts
+// the row's largest |f| in [2^13, 2^14), hi = fp16(f * 2^-e) and lo =
+// fp16(f * 2^-e - hi) (the difference is exact in fp32), so hi + lo carries
+// f * 2^-e to about 22 bits and neither plane can overflow; xsc[row] = 2^e
+// undoes the scaling in the GEMM's epilogue.  One workgroup per row, ffn <=
+// 16 * kBlock.
+__global__ __launch_bounds__(kBlock) void k_swiglu_h16(const float * __restrict__ g, const float * __restrict__ u,
+                                                       int32_t ffn, uint16_t * __restrict__ xh,
+                                                       uint16_t * __restrict__ xl, float * __restrict__ xsc) {
+    __shared__ float red[kBlock / 64];
+    constexpr int M = 16;
+    const size_t base = (size_t) blockIdx.x * ffn;
+    float f[M];
+    float am = 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int e = threadIdx.x + m * kBlock;
+        f[m] = e < ffn ? silu_q3t(g[base + e]) * u[base + e] : 0.0f;
+        am = fmaxf(am, fabsf(f[m]));
+    }
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int ex = (am > 0.0f && am <= 3.0e38f) ? ilogbf(am) - 13 : 0;
+    const float down = ldexpf(1.0f, -ex);
+    if (threadIdx.x == 0) xsc[blockIdx.x] = ldexpf(1.0f, ex);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int e = threadIdx.x + m * kBlock;
+        if (e >= ffn) break;
+        const float v = f[m] * down;
+        const uint16_t h = f2h(v);
+        xh[base + e] = h;
+        xl[base + e] = f2h(v - h2f(h));
+    }
+}
+
 // SwiGLU over rows: f = silu(g) * u.
 __global__ __launch_bounds__(kBlock) void k_swiglu_rows(const float * __restrict__ g, const float * __restrict__ u,
                                                         float * __restrict__ f, size_t count) {
@@ -617,6 +861,31 @@ __global__ __launch_bounds__(kBlock) void k_att_q(const float * __restrict__ qkv
 // registers while tile s's MFMAs run; rows past the tile's last position
 // staged as zero).
 constexpr int kAttT = 256;       // threads of the MFMA attention kernels
+
+// One 16x16x32 MFMA with fp32 accumulation on fp16 (or, bf, bfloat16)
+// operands held as 16-bit patterns: the fast forms of the attention kernels.
+template <bool BF>
+__device__ __forceinline__ f4v mfma_h32(const int4 & a, const int4 & b, f4v c) {
+    const v4i av = (v4i){a.x, a.y, a.z, a.w}, bv = (v4i){b.x, b.y, b.z, b.w};
+    if constexpr (BF) {
+        typedef __bf16 b8v __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8v, av), __builtin_bit_cast(b8v, bv), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, av), __builtin_bit_cast(h8v, bv), c, 0, 0, 0);
+    }
+}
+
+// FAST: the scores of a step on 16x16x32 fp16 (bfloat16) MFMAs with fp32
+// accumulation (the reference's F16 K.Q product class) instead of the exact
+// f64 MFMA sums: lane (i, k) supplies dims 32c + 8k .. +7 of q row 16w + i as
+// A and of position 16 t4 + i as B for MFMA c of 4, and its accumulator
+// element r is row 16w + 4k + r, position 16 t4 + i.
+__global__ __launch_bounds__(kAttT) void k_att_scores_fast(const uint16_t * __restrict__ Qh,
+                                                            const uint16_t * __restrict__ kc, int32_t n_ctx,
+                                                            int32_t n_head, int32_t n_kv_head, int32_t n,
+                                                            int32_t n_past, float scale, float * __restrict__ S,
+                                                            int32_t ls, int32_t bf);
+
 __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restrict__ Qh,
                                                        const uint16_t * __restrict__ kc, int32_t n_ctx, int32_t n_head,
                                                        int32_t n_kv_head, int32_t n, int32_t n_past, float scale,
@@ -703,6 +972,90 @@ __global__ __launch_bounds__(kAttT) void k_att_scores(const uint16_t * __restric
             __syncthreads();
         }
     }
+}
+
+// The fast form of k_att_scores (see its declaration); same grid, tile
+// pairing, K staging and masking.
+template <bool BF>
+__device__ __forceinline__ void att_scores_fast_body(const uint16_t * __restrict__ Qh, const uint16_t * __restrict__ kc,
+                                                     int32_t n_ctx, int32_t n_head, int32_t n_kv_head, int32_t n,
+                                                     int32_t n_past, float scale, float * __restrict__ S, int32_t ls,
+                                                     uint16_t (*kt)[kAT * kKS]) {
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head), grp = blockIdx.z;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int krow = t >> 4, kch = t & 15;
+    const uint16_t * kbase = kc + (size_t) g * n_ctx * kHD + 8 * kch;
+    const int y = blockIdx.y, Y = gridDim.y;
+    const bool spread = 2 * Y + 1 == tiles;
+    for (int pass = 0; pass < (spread ? 3 : 2); ++pass) {
+        const int tile = pass == 0 ? y : pass == 1 ? tiles - 1 - y : Y;
+        if (pass == 1 && tile == y) break;
+        const int row0 = tile * kAT, my_row = row0 + 16 * w + i;
+        const int lim_tile = n_past + min(row0 + kAT, n) - 1;
+        if (lim_tile < 64 * grp) continue;
+        const int nst = (lim_tile - 64 * grp) / (2 * kAT) + 1;
+        const int st0 = pass == 2 ? y : 0, sd = pass == 2 ? Y : 1;
+        if (st0 >= nst) continue;
+        int4 qa[4];                                             // dims 32c + 8k .. +7 of row my_row
+        {
+            const bool ok = my_row < n;
+            const int4 * src = (const int4 *) (Qh + ((size_t) h * n + (ok ? my_row : 0)) * kHD + 8 * k);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qa[c] = ok ? src[4 * c] : make_int4(0, 0, 0, 0);
+        }
+        int4 rk[4];
+        int kok[4];
+        auto fetch = [&](int j0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + krow + 16 * u;
+                kok[u] = j <= lim_tile;
+                rk[u] = *(const int4 *) (kbase + (size_t) min(j, lim_tile) * kHD);
+            }
+        };
+        auto stash = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                *(int4 *) (&kt[buf][(krow + 16 * u) * kKS + 8 * kch]) = kok[u] ? rk[u] : make_int4(0, 0, 0, 0);
+        };
+        fetch(2 * kAT * st0 + 64 * grp);
+        stash(0);
+        __syncthreads();
+        for (int st = st0, it = 0; st < nst; st += sd, ++it) {
+            const int buf = it & 1, j0 = 2 * kAT * st + 64 * grp;
+            const bool more = st + sd < nst;
+            if (more) fetch(j0 + 2 * kAT * sd);
+            f4v acc[4];
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) acc[t4] = (f4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4)
+                    acc[t4] = mfma_h32<BF>(qa[c], *(const int4 *) (&kt[buf][(16 * t4 + i) * kKS + 32 * c + 8 * k]),
+                                           acc[t4]);
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + 16 * w + 4 * k + r, j = j0 + 16 * t4 + i;
+                    if (row < n && j <= n_past + row) S[((size_t) h * n + row) * ls + j] = acc[t4][r] * scale;
+                }
+            __asm__ volatile("" ::: "memory");
+            if (more) stash(buf ^ 1);
+            __syncthreads();
+        }
+    }
+}
+
+__global__ __launch_bounds__(kAttT) void k_att_scores_fast(const uint16_t * __restrict__ Qh,
+                                                            const uint16_t * __restrict__ kc, int32_t n_ctx,
+                                                            int32_t n_head, int32_t n_kv_head, int32_t n,
+                                                            int32_t n_past, float scale, float * __restrict__ S,
+                                                            int32_t ls, int32_t bf) {
+    __shared__ __align__(16) uint16_t kt[2][kAT * kKS];
+    if (bf) att_scores_fast_body<true>(Qh, kc, n_ctx, n_head, n_kv_head, n, n_past, scale, S, ls, kt);
+    else att_scores_fast_body<false>(Qh, kc, n_ctx, n_head, n_kv_head, n, n_past, scale, S, ls, kt);
 }
 
 // One row held in registers, R positions per lane (cnt <= 64 R).  Each lane
@@ -882,6 +1235,121 @@ __global__ __launch_bounds__(kAttT, 4) void k_att_pv(const uint16_t * __restrict
         }
     }
   }
+}
+
+// The fast form of k_att_pv: P.V on 16x16x32 fp16 (bfloat16) MFMAs with
+// fp32 accumulation.  Same grid, tile pairing, P staging and masks; the V
+// tile is staged transposed ([dim][position], 8 two-byte stores per 8-dim
+// chunk) so that lane (i, k) reads positions 32q + 8k .. +7 of dim 16 b + i as
+// one 16-byte B operand, against P row 16w + i (A).  Accumulator b holds dims
+// 64 grp + 16 b + i of rows 16w + 4k + r (the middle-tile row groups: wave w's
+// dims 16 w + i of rows 16 rg + 4k + r).
+constexpr int kVT = 64 + 8;      // LDS row stride (halves) of the transposed V tile
+template <bool BF>
+__device__ __forceinline__ void att_pv_fast_body(const uint16_t * __restrict__ P, int32_t ls,
+                                                 const uint16_t * __restrict__ vc, int32_t n_ctx, int32_t n_head,
+                                                 int32_t n_kv_head, int32_t n, int32_t n_past, float * __restrict__ out,
+                                                 int32_t out_stride, uint16_t (*pt)[kAT * kVS],
+                                                 uint16_t (*vt)[kAT * kVT]) {
+    const int h = blockIdx.x, tiles = (n + kAT - 1) / kAT, g = h / (n_head / n_kv_head), grp = blockIdx.z;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, i = l & 15, k = l >> 4;
+    const int srow = t >> 3, sch = t & 7;
+    const uint16_t * vbase = vc + (size_t) g * n_ctx * kHD + 64 * grp + 8 * sch;
+    const int y = blockIdx.y, Y = gridDim.y;
+    const int nrg = (2 * Y + 1 == tiles && y < 4) ? (4 - y + Y - 1) / Y : 0;
+  for (int pass = 0; pass < 2 + nrg; ++pass) {
+    const int rg = pass < 2 ? -1 : y + (pass - 2) * Y;
+    const int tile = pass == 0 ? y : pass == 1 ? tiles - 1 - y : Y;
+    if (pass == 1 && tile == y) continue;
+    const int row0 = tile * kAT, prow = rg < 0 ? 16 * w : 16 * rg;
+    const int lim_tile = n_past + min(row0 + kAT, n) - 1;
+    const int nst = lim_tile / kAT + 1;
+    int plim[2];
+    const uint16_t * prp[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int prw = row0 + srow + 32 * u;
+        plim[u] = prw < n ? n_past + prw : -1;
+        prp[u] = P + ((size_t) h * n + (prw < n ? prw : 0)) * ls + 8 * sch;
+    }
+    int4 rp[2], rv[2];
+    int pvalid[2], vok[2];
+    auto fetch = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            pvalid[u] = min(max(plim[u] - (j0 + 8 * sch) + 1, 0), 8);
+            rp[u] = *(const int4 *) (prp[u] + (pvalid[u] > 0 ? j0 : 0));
+            const int pos = j0 + srow + 32 * u;
+            vok[u] = pos <= lim_tile;
+            rv[u] = *(const int4 *) (vbase + (size_t) min(pos, lim_tile) * kHD);
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            int4 v = rp[u];
+            const int pv = pvalid[u];
+            if (pv < 8) {
+                const auto m = [pv](int e) { return (2 * e < pv ? 0xffff : 0) | (2 * e + 1 < pv ? (int) 0xffff0000u : 0); };
+                v.x &= m(0); v.y &= m(1); v.z &= m(2); v.w &= m(3);
+            }
+            *(int4 *) (&pt[buf][(srow + 32 * u) * kVS + 8 * sch]) = v;
+            const int4 vv = vok[u] ? rv[u] : make_int4(0, 0, 0, 0);
+            const int pos = srow + 32 * u;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[buf][(8 * sch + e) * kVT + pos] = h8bits(vv, e);
+        }
+    };
+    f4v acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[b] = (f4v){0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < nst) fetch((st + 1) * kAT);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int4 pa = *(const int4 *) (&pt[buf][(prow + i) * kVS + 32 * q + 8 * k]);
+            if (rg < 0) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[b] = mfma_h32<BF>(pa, *(const int4 *) (&vt[buf][(16 * b + i) * kVT + 32 * q + 8 * k]), acc[b]);
+            } else {
+                acc[0] = mfma_h32<BF>(pa, *(const int4 *) (&vt[buf][(16 * w + i) * kVT + 32 * q + 8 * k]), acc[0]);
+            }
+        }
+        __asm__ volatile("" ::: "memory");
+        if (st + 1 < nst) stash(buf ^ 1);
+        __syncthreads();
+    }
+    if (rg < 0) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + 16 * w + 4 * k + r;
+                if (row < n) out[(size_t) row * out_stride + h * kHD + 64 * grp + 16 * b + i] = acc[b][r];
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 16 * rg + 4 * k + r;
+            if (row < n) out[(size_t) row * out_stride + h * kHD + 64 * grp + 16 * w + i] = acc[0][r];
+        }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAttT, 4) void k_att_pv_fast(const uint16_t * __restrict__ P, int32_t ls,
+                                                        const uint16_t * __restrict__ vc, int32_t n_ctx,
+                                                        int32_t n_head, int32_t n_kv_head, int32_t n, int32_t n_past,
+                                                        float * __restrict__ out, int32_t out_stride, int32_t bf) {
+    __shared__ __align__(16) uint16_t pt[2][kAT * kVS];
+    __shared__ __align__(16) uint16_t vt[2][kAT * kVT];
+    if (bf) att_pv_fast_body<true>(P, ls, vc, n_ctx, n_head, n_kv_head, n, n_past, out, out_stride, pt, vt);
+    else att_pv_fast_body<false>(P, ls, vc, n_ctx, n_head, n_kv_head, n, n_past, out, out_stride, pt, vt);
 }
 
 __host__ __device__ constexpr size_t attn_rows_lds_bytes(int n_ctx) {

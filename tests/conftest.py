@@ -8,6 +8,11 @@ sys.path.insert(0, os.path.join(ROOT, "qwen3-tts.cpp_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, ROOT)
 
+# The parity tests compare the device with the oracle bit for bit, so they
+# run F16 prefills on the exact f64-MFMA GEMMs; the tests of the default fast
+# form (fp16 MFMA, fp32 accumulation; a tolerance) switch it back on.
+os.environ.setdefault("Q3T_PF_EXACT", "1")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X); runs the device C ABI")

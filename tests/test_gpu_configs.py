@@ -230,6 +230,176 @@ def test_config4_long_context_sampled_f16(path, monkeypatch):
         dev.close()
 
 
+def _golden_config4():
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import make_config4_golden as g4
+    return g4, np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_f16_2049.npz"))
+
+
+def test_config4_full_prefill_2049_sampled_f16(path):
+    """Configuration 4 at its full size against the oracle's recorded results
+    (tests/golden/config4_f16_2049.npz, made by make_config4_golden.py; the
+    oracle needs minutes for this prefill): one N(0,1) speaker row plus the
+    device text projection of 2,048 ids uniform in [0, 151936), a 2,049-row
+    F16 prefill from position 0 on the tiled MFMA path (causal attention over
+    up to 2,049 positions, softmax rows of 2,049-2,560 held in registers, the
+    ragged last row tile), then 16 sampled frames (T 0.9, top-k 50,
+    repetition penalty 1.05).  Projected rows, every hidden row (per-row
+    digests) and the last logits are bit-exact; the codes are identical."""
+    g4, gold = _golden_config4()
+    cfg = qcfg.full_06b()
+    ids, spk, trail_ids = g4.inputs(cfg)
+    assert np.array_equal(ids, gold["ids"])
+    w = weights("f16", g4.WEIGHT_SEED)
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w)
+        n = g4.N_IDS + 1
+        dev.kv_reserve(n + g4.N_FRAMES + 8)
+        say(f"[gpu] config 4 full ({path}): text_proj of {g4.N_IDS} ids")
+        tp = dev.text_proj(ids)
+        trail = dev.text_proj(trail_ids)
+        pad = dev.text_proj(np.array([cfg.tts_pad_id], np.int32))[0]
+        assert np.array_equal(g4.digest(tp), gold["text_proj_digest"])
+        assert np.array_equal(g4.digest(trail), gold["trail_digest"])
+        assert np.array_equal(g4.digest(pad), gold["pad_digest"])
+        rows = np.concatenate([spk[None], tp])
+        say(f"[gpu] config 4 full ({path}): prefill of {n} rows")
+        hid, lg = dev.prefill(rows, 0)
+        dg = g4.row_digests(hid)
+        bad = np.flatnonzero(np.any(dg != gold["hidden_digests"], axis=1))
+        assert bad.size == 0, f"hidden rows differ from the oracle's, first at row {bad[0]} ({bad.size} rows)"
+        assert np.abs(lg - gold["logits"]).max() <= LOGIT_TOL
+        assert np.array_equal(lg, gold["logits"])
+        say(f"[gpu] config 4 full ({path}): {g4.N_FRAMES} sampled frames from position {n}")
+        dev.frames_begin(trail, pad, n, g4.N_FRAMES, seed=g4.SAMPLE_SEED, **g4.SAMPLING)
+        cg, _ = dev.frames_run(g4.N_FRAMES)
+        check_path(dev, path)
+        assert cg.shape == gold["codes"].shape and np.array_equal(cg, gold["codes"])
+    finally:
+        dev.close()
+
+
+# The fast F16 prefill (fp16 MFMA, fp32 accumulation, the default for F16
+# layers) is checked against the exact oracle by tolerance: the last logits
+# within 1e-2 max-abs (the F16 bound of the path's contract) and every hidden
+# row within FAST_ROW_TOL of its largest element.
+FAST_ROW_TOL = 5e-3
+
+
+def _rows_rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.abs(a - b).max(axis=1) / np.maximum(np.abs(b).max(axis=1), 1e-30)
+
+
+@pytest.mark.parametrize("wtype", ["f16", "q8_0"])
+def test_fast_prefill_200_rows_within_tolerance(monkeypatch, wtype):
+    """200 prompt rows through the default tiled prefill against the oracle's
+    exact prefill at the 0.6B shapes.  F16 layers (the weights of
+    configuration 4) take the fast fp16-MFMA GEMMs and attention: the last
+    logits within 1e-2 max-abs and each hidden row within FAST_ROW_TOL, and the
+    exact form on the same rows is bit-exact (the control).  Q8_0 layers keep
+    the exact forms by default, so their rows equal the oracle's bit for bit
+    with or without Q3T_PF_EXACT."""
+    g4, _ = _golden_config4()
+    cfg = qcfg.full_06b()
+    w = weights(wtype, g4.WEIGHT_SEED if wtype == "f16" else 3)
+    dev = Device(cfg)
+    o = orc.Oracle(cfg, w, threads=THREADS)
+    try:
+        dev.upload_weights(w)
+        dev.kv_reserve(256)
+        o.kv_reset(256)
+        rows = (np.random.default_rng(71).standard_normal((200, cfg.hidden_size)) * 0.05).astype(np.float32)
+        say(f"[gpu] fast prefill ({wtype}): oracle 200 rows")
+        ho, lo = o.prefill(rows, 0)
+        monkeypatch.setenv("Q3T_PF_EXACT", "0")
+        say(f"[gpu] fast prefill ({wtype}): device 200 rows (fp16 MFMA)")
+        hf, lf = dev.prefill(rows, 0)
+        rel = _rows_rel(hf, ho)
+        say(f"[gpu] fast prefill ({wtype}): logits max-abs {np.abs(lf - lo).max():.3e}, hidden rows rel max "
+            f"{rel.max():.3e} median {np.median(rel):.3e}")
+        if wtype == "q8_0":
+            assert np.array_equal(hf, ho) and np.array_equal(lf, lo)
+            return
+        assert np.abs(lf - lo).max() <= LOGIT_TOL
+        assert rel.max() <= FAST_ROW_TOL
+        assert not np.array_equal(hf, ho)          # the fast form really ran
+        monkeypatch.setenv("Q3T_PF_EXACT", "1")
+        he, le = dev.prefill(rows, 0)
+        assert np.array_equal(he, ho) and np.array_equal(le, lo)
+    finally:
+        o.close()
+        dev.close()
+
+
+def test_fast_f16_config4_full_prefill_2049(monkeypatch):
+    """Configuration 4 at full size with the fast F16 prefill: the 2,049-row
+    prefill's last logits within 1e-2 of the oracle's recorded ones; then the
+    16 sampled frames.  Sampling reads the logits through a softmax and a
+    uniform draw, so a fast-form logit that moves by ~1e-4 can change a draw;
+    the first frame whose codes differ from the exact run's is reported, not
+    asserted."""
+    g4, gold = _golden_config4()
+    cfg = qcfg.full_06b()
+    ids, spk, trail_ids = g4.inputs(cfg)
+    w = weights("f16", g4.WEIGHT_SEED)
+    dev = Device(cfg)
+    monkeypatch.setenv("Q3T_PF_EXACT", "0")
+    try:
+        dev.upload_weights(w)
+        n = g4.N_IDS + 1
+        dev.kv_reserve(n + g4.N_FRAMES + 8)
+        tp = dev.text_proj(ids)
+        trail = dev.text_proj(trail_ids)
+        pad = dev.text_proj(np.array([cfg.tts_pad_id], np.int32))[0]
+        rows = np.concatenate([spk[None], tp])
+        say(f"[gpu] fast F16 config 4: prefill of {n} rows")
+        _, lg = dev.prefill(rows, 0)
+        err = np.abs(lg - gold["logits"]).max()
+        say(f"[gpu] fast F16 config 4: last logits max-abs vs oracle {err:.3e}")
+        assert err <= LOGIT_TOL
+        dev.frames_begin(trail, pad, n, g4.N_FRAMES, seed=g4.SAMPLE_SEED, **g4.SAMPLING)
+        cg, _ = dev.frames_run(g4.N_FRAMES)
+        diff = [f for f in range(min(len(cg), len(gold["codes"]))) if not np.array_equal(cg[f], gold["codes"][f])]
+        say(f"[gpu] fast F16 config 4: first frame differing from the exact run: "
+            f"{diff[0] if diff else 'none'} of {len(cg)}")
+    finally:
+        dev.close()
+
+
+def test_fast_f16_config1_tiled_prefill_64_greedy(monkeypatch):
+    """Configuration 1 (F16, 32-token prompt, 64 greedy frames) with its
+    10-row prompt forced through the tiled prefill in the fast form (its
+    default is the exact GEMV prefill): the first logits within 1e-2 of the
+    oracle's.  The decode that follows is exact, but it runs on K/V rows that
+    differ from the oracle's at fp32 rounding level, so a later greedy
+    near-tie can resolve differently; the first frame whose codes differ is
+    reported, not asserted."""
+    cfg = qcfg.full_06b()
+    text = np.random.default_rng(18).integers(0, 151936, 32).astype(np.int32)
+    spk = np.random.default_rng(19).standard_normal(1024).astype(np.float32)
+    co, first_o = _oracle_generate("config1", "f16", 4, text, spk, 64)
+    w = weights("f16", 4)
+    dev = Device(cfg)
+    monkeypatch.setenv("Q3T_PF_EXACT", "0")
+    monkeypatch.setenv("Q3T_PREFILL_MFMA", "1")
+    try:
+        dev.upload_weights(w)
+        pre = driver.build_prefill(dev, cfg, text, spk)
+        dev.kv_reserve(pre[0].shape[0] + 64 + 8)
+        _, first_g = dev.prefill(pre[0], 0, want_hidden=False)
+        say(f"[gpu] fast F16 config 1: first logits max-abs vs oracle {np.abs(first_g - first_o).max():.3e}")
+        assert np.abs(first_g - first_o).max() <= LOGIT_TOL
+        assert not np.array_equal(first_g, first_o)
+        cg = driver.generate(dev, cfg, text, spk, max_len=64, temperature=0.0, top_k=0, prefill_rows=pre)
+    finally:
+        dev.close()
+    diff = [f for f in range(min(len(cg), len(co))) if not np.array_equal(cg[f], co[f])]
+    say(f"[gpu] fast F16 config 1: first frame differing from the oracle: {diff[0] if diff else 'none'} of {len(co)}")
+    assert cg.shape == co.shape
+
+
 def _oracle_generate(key, wtype, seed, text, spk, max_len):
     if key not in _oracle_runs:
         cfg = qcfg.full_06b()
@@ -287,6 +457,51 @@ def test_config3_q8_frame_loop_256_greedy(path):
     assert cg.shape == co.shape and np.array_equal(cg, co)
 
 
+def test_xcd_reprobe_switches_to_row_program(monkeypatch):
+    """A frames_run on the XCD-parallel program whose waits time out
+    re-checks the workgroup dealing; if it changed, the batch runs again from
+    the state it began with on the row-parallel program.  The re-check's
+    result is forced from the host (Q3T_TEST_XCD_REPROBE_FAIL=1: the batch is
+    treated as timed out and the dealing as changed; no wait is made to time
+    out).  The second of three 8-frame batches takes the switch; the first
+    ran on the XCD-parallel program, the last stays on the row-parallel one,
+    and the 24 greedy frames equal the oracle's (configuration 3's model and
+    prompt), so the restored state (frame state, repetition set, logits,
+    hidden row, head candidates) is the one the batch began with."""
+    cfg = qcfg.full_06b()
+    text = np.random.default_rng(8).integers(0, 151936, 64).astype(np.int32)
+    spk = np.random.default_rng(9).standard_normal(1024).astype(np.float32)
+    co, _ = _oracle_generate("config3_24", "q8_0", 3, text, spk, 24)
+    w = weights("q8_0", 3)
+    dev = Device(cfg)
+    monkeypatch.setenv("Q3T_FRAME_KERNEL", "1")
+    monkeypatch.setenv("Q3T_FRAME_XCD", "1")
+    monkeypatch.delenv("Q3T_TEST_XCD_REPROBE_FAIL", raising=False)
+    try:
+        dev.upload_weights(w)
+        pre, trail, pad = driver.build_prefill(dev, cfg, text, spk)
+        dev.kv_reserve(pre.shape[0] + 24 + 8)
+        dev.prefill(pre, 0, want_hidden=False)
+        dev.frames_begin(trail, pad, pre.shape[0], 24, temperature=0.0, top_k=0)
+        got = []
+        c, _ = dev.frames_run(8)
+        got.append(c)
+        assert dev.frames_stats()[2] == 3
+        monkeypatch.setenv("Q3T_TEST_XCD_REPROBE_FAIL", "1")
+        say("[gpu] XCD re-probe forced to fail: batch 2 reruns on the row-parallel program")
+        c, _ = dev.frames_run(8)
+        got.append(c)
+        assert dev.frames_stats()[2] == 1
+        monkeypatch.delenv("Q3T_TEST_XCD_REPROBE_FAIL")
+        c, _ = dev.frames_run(8)
+        got.append(c)
+        assert dev.frames_stats()[2] == 1
+    finally:
+        dev.close()
+    cg = np.concatenate(got)
+    assert cg.shape == co.shape and np.array_equal(cg, co)
+
+
 def test_icl_long_reference_q8(path):
     """generate_icl's layout at the 0.6B shapes with a long reference clip:
     200 reference codec frames and 30 reference text ids make a 210-row
@@ -331,12 +546,12 @@ def test_config5_16_streams_ragged_kv_q8():
     KV lengths are drawn uniformly from [128, 2048]: each stream's history is
     seeded K/V rows written to both sides (q3t_dev_stream_kv_write /
     orc_kv_write), then its own prompt rows prefilled at that offset
-    (q3t_dev_stream_prefill_at), then 6 greedy frames of all streams together
+    (q3t_dev_stream_prefill_at), then 32 greedy frames of all streams together
     (EOS biased off).  Each stream's codes equal the oracle's frame loop over
     the same cache."""
     cfg = qcfg.full_06b()
     w = weights("q8_0", 3)
-    B, frames = 16, 6
+    B, frames = 16, 32
     rng = np.random.default_rng(91)
     kv_len = rng.integers(128, 2049, B)
     n_ctx = int(kv_len.max()) + frames + 8
