@@ -2081,8 +2081,11 @@ __device__ __forceinline__ void xf16_compute(const XRegs16<KIND> & R, const Lds 
 // Rank j's 32 outputs of a device-wide partial slot: the 8 XCDs' fp64
 // partials added in XCD order and rounded once, plus the residual slice
 // L.rx, which takes the sum; the sums also go to the XCD-local row
-// outl[t * 1024 + 32j + i].  Thread t < 32 * NT handles output t & 31 of
-// token t >> 5, the same thread that keeps that element of L.rx.
+// outl[t * 1024 + 32j + i].  Thread t = 8i + xs waits for output i's partial
+// from XCD xs; the 8 lanes of output i then form ((p0 + p1) + ...) + p7 as a
+// sequential scan over DPP shifts (step k: lane k adds lane k - 1's running
+// sum to its own partial), so lane 8i + 7 holds the sum, with no LDS round
+// trip or workgroup barrier.  That lane keeps L.rx[tok][i].
 template <int NT>
 __device__ __forceinline__ void xreduce(const Args & A, Lds & L, const uint64_t * part, uint32_t ptag, uint64_t * outl,
                                         uint32_t otag, bool & dead) {
@@ -2097,21 +2100,21 @@ __device__ __forceinline__ void xreduce(const Args & A, Lds & L, const uint64_t 
     }
     float val[4];
     twait_batch<4>(ptr, 2 * NT, ptag, val, dead, A.err);
-    double * rd = (double *) L.sc;          // [NT][32 outputs][8 XCDs]
 #pragma unroll
-    for (int tok = 0; tok < NT; ++tok)
-        rd[(tok * 32 + i) * kXcd + xs] = __hiloint2double(__float_as_int(val[2 * tok + 1]), __float_as_int(val[2 * tok]));
-    __syncthreads();
-    if (t < 32 * NT) {
-        const int tok = t >> 5, ii = t & 31;
-        double sm = 0.0;
+    for (int tok = 0; tok < NT; ++tok) {
+        const double pv = __hiloint2double(__float_as_int(val[2 * tok + 1]), __float_as_int(val[2 * tok]));
+        double sm = pv;
 #pragma unroll
-        for (int k = 0; k < kXcd; ++k) sm += rd[(tok * 32 + ii) * kXcd + k];
-        const float v = (float) sm + L.rx[tok][ii];
-        L.rx[tok][ii] = v;
-        lstore(outl + tok * 1024 + 32 * j + ii, otag, v);
+        for (int k = 1; k < kXcd; ++k) {
+            const double prev = dpp_d<0x111>(sm);          // row_shr:1, lane k - 1's running sum
+            if (xs == k) sm = prev + pv;
+        }
+        if (xs == kXcd - 1) {
+            const float v = (float) sm + L.rx[tok][i];
+            L.rx[tok][i] = v;
+            lstore(outl + tok * 1024 + 32 * j + i, otag, v);
+        }
     }
-    __syncthreads();
 }
 
 // One XCD-parallel layer for NT tokens (Q8_0 weights).  Input: the rows
