@@ -111,6 +111,22 @@ const char * q3t_dev_last_error(const q3t_dev * dev);
  * (int8 quants and fp16 scales split) without changing any value. */
 int  q3t_dev_upload_tensor(q3t_dev * dev, const char * name, int32_t ggml_type,
                            const int64_t ne[4], const void * data, size_t nbytes);
+/* The same upload in row ranges, for loaders that read a GGUF file in
+ * bounded pieces instead of holding whole tensors in host memory (the
+ * reference's load_tensor_data reads each tensor whole,
+ * src/tts_transformer.cpp:670-729): rows [row0, row0 + n_rows) of the ne[1]
+ * rows, `data` holding those rows in ggml layout (Q8_0: whole 34-byte
+ * blocks), nbytes their size.  A tensor's first range (row0 == 0) allocates
+ * it; the ranges must cover every row once (checked before the first compute
+ * call: "tensor ... incomplete").  Synchronous: `data` may be reused on
+ * return.  Q8_0 blocks are repacked on the device. */
+int  q3t_dev_upload_tensor_rows(q3t_dev * dev, const char * name, int32_t ggml_type, const int64_t ne[4],
+                                int64_t row0, int64_t n_rows, const void * data, size_t nbytes);
+/* The context's pinned host staging buffer for q3t_dev_upload_tensor_rows
+ * (at least min_bytes, 64 MiB by default; owned by the context, valid until
+ * the next call or q3t_dev_destroy); *cap_out receives its size.  Filling it
+ * from the file makes each range one DMA.  NULL on failure. */
+void * q3t_dev_staging(q3t_dev * dev, size_t min_bytes, size_t * cap_out);
 /* Copies a tensor back in ggml layout (used to check the upload). */
 int  q3t_dev_download_tensor(q3t_dev * dev, const char * name, void * data, size_t nbytes);
 /* Dequantises a Q8_0 tensor on the device to fp32 [ne1][ne0] (fp32(d)*q). */

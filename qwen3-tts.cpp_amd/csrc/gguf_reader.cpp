@@ -32,6 +32,16 @@ size_t gguf_tensor_nbytes(int32_t type, const int64_t ne[4]) {
     return 0;
 }
 
+std::string gguf_type_name(int32_t type) {
+    // ggml_type ids of the public GGUF specification
+    static const char * const names[] = {"F32", "F16", "Q4_0", "Q4_1", "type 4", "type 5", "Q5_0", "Q5_1", "Q8_0",
+                                         "Q8_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_K", "IQ2_XXS", "IQ2_XS",
+                                         "IQ3_XXS", "IQ1_S", "IQ4_NL", "IQ3_S", "IQ2_S", "IQ4_XS", "I8", "I16", "I32",
+                                         "I64", "F64", "IQ1_M", "BF16"};
+    if (type >= 0 && type < (int32_t) (sizeof(names) / sizeof(names[0]))) return names[type];
+    return "type " + std::to_string(type);
+}
+
 void GGUFReader::close() {
     if (f_) { std::fclose(f_); f_ = nullptr; }
     u32_.clear(); f32_.clear(); tensors_.clear();
@@ -132,6 +142,23 @@ bool GGUFReader::read_tensor(const GGUFTensorInfo & t, std::vector<uint8_t> & ds
         return false;
     }
     if (std::fread(dst.data(), 1, t.nbytes, f_) != t.nbytes) {
+        err_ = "Failed to read tensor data: " + t.name;
+        return false;
+    }
+    return true;
+}
+
+bool GGUFReader::read_tensor_rows(const GGUFTensorInfo & t, int64_t row0, int64_t n_rows, void * dst) {
+    if (!f_) { err_ = "GGUF file not open"; return false; }
+    if (t.nbytes == 0) { err_ = "unsupported tensor type for " + t.name; return false; }
+    const int64_t rows = t.n_dims >= 2 ? t.ne[1] * t.ne[2] * t.ne[3] : 1;
+    if (row0 < 0 || n_rows < 0 || row0 + n_rows > rows) { err_ = "row range out of bounds for " + t.name; return false; }
+    const size_t row_bytes = t.nbytes / (size_t) rows, n = row_bytes * (size_t) n_rows;
+    if (std::fseek(f_, (long) (data_offset_ + t.offset + row_bytes * (size_t) row0), SEEK_SET) != 0) {
+        err_ = "Failed to seek to tensor data: " + t.name;
+        return false;
+    }
+    if (std::fread(dst, 1, n, f_) != n) {
         err_ = "Failed to read tensor data: " + t.name;
         return false;
     }

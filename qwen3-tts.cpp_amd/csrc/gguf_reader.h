@@ -37,6 +37,9 @@ public:
     const std::vector<GGUFTensorInfo> & tensors() const { return tensors_; }
     // reads a tensor's bytes into dst (resized)
     bool read_tensor(const GGUFTensorInfo & t, std::vector<uint8_t> & dst);
+    // reads rows [row0, row0 + n_rows) of a tensor (rows along ne[1], each
+    // nbytes / ne[1] bytes) into dst, which holds at least that many bytes
+    bool read_tensor_rows(const GGUFTensorInfo & t, int64_t row0, int64_t n_rows, void * dst);
 
 private:
     FILE * f_ = nullptr;
@@ -50,5 +53,7 @@ private:
 // ggml tensor byte size for the types the frame loop uses (F32, F16, Q8_0);
 // 0 for anything else.
 size_t gguf_tensor_nbytes(int32_t type, const int64_t ne[4]);
+// ggml's name of a tensor type id ("F16", "Q4_K", ...; "type <id>" if unknown)
+std::string gguf_type_name(int32_t type);
 
 }  // namespace qwen3_tts

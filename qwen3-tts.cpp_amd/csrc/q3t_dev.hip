@@ -150,6 +150,12 @@ struct q3t_dev {
     int fk_variant = 0;            // see fk_kernel()
     int xcd_map = -1;              // frame-launch workgroups dealt round-robin over the XCDs: -1 unknown, 0 no, 1 yes
     bool fk_no_xcd = false;        // a re-probe found the dealing changed: the row-parallel program from then on
+    // streamed tensor upload (q3t_dev_upload_tensor_rows): the pinned host
+    // staging buffer callers fill from the file, the device buffer raw Q8_0
+    // blocks land in before the repack, and rows received per tensor
+    void * up_host = nullptr; size_t up_host_cap = 0;
+    void * up_raw = nullptr; size_t up_raw_cap = 0;
+    std::map<std::string, int64_t> up_rows;
     unsigned char * fk_snap = nullptr;   // the frame loop's carried state before a frames_run on the XCD program
     bool gqa_lds_ok = false;       // ms::k_attn_gqa may take the LDS this context's n_ctx needs
     bool fk_refused = false;       // a cooperative launch was refused: this context stays on the graph
@@ -283,22 +289,49 @@ size_t type_bytes(int type, int64_t ne0, int64_t ne1) {
 }
 
 // Repack ggml Q8_0 blocks (fp16 d + 32 int8) into split arrays and copy.
-int upload_rows(q3t_dev * c, Slot & s, int64_t row0, int type, int64_t ne0, int64_t ne1, const void * data) {
+// GGUF Q8_0 blocks (fp16 scale + 32 int8, 34 bytes) split into the int8
+// quants [row][K] and the fp16 scales [row][K/32]: one thread per block, no
+// value changes.
+__global__ void k_repack_q8(const uint8_t * __restrict__ raw, int64_t n_blocks, int8_t * __restrict__ q,
+                            uint16_t * __restrict__ d) {
+    const int64_t b = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blocks) return;
+    const uint8_t * src = raw + b * 34;
+    d[b] = (uint16_t) (src[0] | ((uint16_t) src[1] << 8));
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        w[i] = (uint32_t) src[2 + 4 * i] | ((uint32_t) src[3 + 4 * i] << 8) | ((uint32_t) src[4 + 4 * i] << 16) |
+               ((uint32_t) src[5 + 4 * i] << 24);
+    int4 * dst = (int4 *) (q + b * 32);
+    dst[0] = make_int4((int) w[0], (int) w[1], (int) w[2], (int) w[3]);
+    dst[1] = make_int4((int) w[4], (int) w[5], (int) w[6], (int) w[7]);
+}
+
+// Rows [row0, row0 + n) of a slot whose rows are ne0 wide, from host memory
+// in ggml layout (Q8_0: raw 34-byte blocks, repacked on the device through
+// c->up_raw).  Synchronous: the caller may reuse `data` on return.
+int upload_rows(q3t_dev * c, Slot & s, int64_t row0, int type, int64_t ne0, int64_t n, const void * data) {
+    if (n <= 0) return 0;
     if (type == Q3T_TYPE_Q8_0) {
-        const int64_t nb = ne0 / 32;
-        std::vector<int8_t> q((size_t) (ne0 * ne1));
-        std::vector<uint16_t> d((size_t) (nb * ne1));
-        const uint8_t * src = (const uint8_t *) data;
-        for (int64_t b = 0; b < nb * ne1; ++b) {
-            std::memcpy(&d[b], src + b * 34, 2);
-            std::memcpy(&q[b * 32], src + b * 34 + 2, 32);
+        const int64_t nb = ne0 / 32, blocks = nb * n;
+        const size_t raw = (size_t) blocks * 34;
+        if (raw > c->up_raw_cap) {
+            dev_free(c, c->up_raw);
+            c->up_raw = nullptr;
+            c->up_raw_cap = 0;
+            if (dev_alloc(c, &c->up_raw, raw)) return -1;
+            c->up_raw_cap = raw;
         }
-        HIP_OK(hipMemcpy((int8_t *) s.data + row0 * ne0, q.data(), q.size(), hipMemcpyHostToDevice));
-        HIP_OK(hipMemcpy(s.scales + row0 * nb, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpyAsync(c->up_raw, data, raw, hipMemcpyHostToDevice, c->stream));
+        hipLaunchKernelGGL(k_repack_q8, dim3((unsigned) ((blocks + 255) / 256)), dim3(256), 0, c->stream,
+                           (const uint8_t *) c->up_raw, blocks, (int8_t *) s.data + row0 * ne0, s.scales + row0 * nb);
     } else {
         const size_t eb = type == Q3T_TYPE_F16 ? 2 : 4;
-        HIP_OK(hipMemcpy((char *) s.data + row0 * ne0 * eb, data, (size_t) (ne0 * ne1) * eb, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpyAsync((char *) s.data + row0 * ne0 * eb, data, (size_t) (ne0 * n) * eb, hipMemcpyHostToDevice,
+                              c->stream));
     }
+    HIP_OK(hipStreamSynchronize(c->stream));
     return 0;
 }
 
@@ -325,6 +358,13 @@ Weight weight_of(const Slot & s, bool widen_f16 = false) {
 int resolve(q3t_dev * c) {
     if (c->resolved) return 0;
     const q3t_config & g = c->cfg;
+    // every tensor sent in row ranges must have all its rows
+    for (const auto & kv : c->up_rows) {
+        int64_t e0, e1; int layer, cb; std::string field; bool is_cp;
+        if (expected_shape(g, kv.first, e0, e1, layer, cb, field, is_cp) && kv.second != e1)
+            return fail(c, "tensor " + kv.first + " incomplete: " + std::to_string(kv.second) + " of " +
+                               std::to_string(e1) + " rows uploaded");
+    }
     auto need = [&](const Slot & s, const char * what) -> int {
         if (!s.data) return fail(c, std::string("missing tensor: ") + what);
         return 0;
@@ -1123,23 +1163,26 @@ void q3t_dev_destroy(q3t_dev * c) {
     for (hipEvent_t e : c->run_ev) if (e) (void) hipEventDestroy(e);
     for (void * p : c->allocs) (void) hipFree(p);
     if (c->pin) (void) hipHostFree(c->pin);
+    if (c->up_host) (void) hipHostFree(c->up_host);
     if (c->stream) (void) hipStreamDestroy(c->stream);
     delete c;
 }
 
 const char * q3t_dev_last_error(const q3t_dev * c) { return c ? c->err.c_str() : "null context"; }
 
-int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const int64_t ne[4], const void * data,
-                          size_t nbytes) {
-    if (!c || !name || !ne || !data) return -1;
+int q3t_dev_upload_tensor_rows(q3t_dev * c, const char * name, int32_t type, const int64_t ne[4], int64_t row0,
+                               int64_t n_rows, const void * data, size_t nbytes) {
+    if (!c || !name || !ne || (!data && n_rows > 0)) return -1;
     int64_t e0, e1; int layer, cb; std::string field; bool is_cp;
     if (!expected_shape(c->cfg, name, e0, e1, layer, cb, field, is_cp)) return 0;   // not on this path
     if (type != Q3T_TYPE_F32 && type != Q3T_TYPE_F16 && type != Q3T_TYPE_Q8_0)
-        return fail(c, std::string("unsupported tensor type for ") + name);
+        return fail(c, std::string("unsupported tensor type ") + std::to_string(type) + " for " + name +
+                           " (this build loads F32, F16 and Q8_0 tensors)");
     if (ne[0] != e0 || ne[1] != e1 || ne[2] != 1 || ne[3] != 1)
         return fail(c, std::string("shape mismatch for ") + name);
     if (type == Q3T_TYPE_Q8_0 && e0 % 32) return fail(c, std::string("Q8_0 row not a multiple of 32: ") + name);
-    if (nbytes != type_bytes(type, e0, e1)) return fail(c, std::string("byte size mismatch for ") + name);
+    if (row0 < 0 || n_rows < 0 || row0 + n_rows > e1) return fail(c, std::string("row range out of bounds for ") + name);
+    if (nbytes != type_bytes(type, e0, n_rows)) return fail(c, std::string("byte size mismatch for ") + name);
     const bool is_matrix = e1 > 1;
     if (!is_matrix && type != Q3T_TYPE_F32) return fail(c, std::string("1-D tensors must be F32: ") + name);
     HIP_OK(hipSetDevice(c->device));
@@ -1148,6 +1191,13 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
     c->fk_layers_stale = true;
     c->cp_tab_stale = true;
     const q3t_config & g = c->cfg;
+    // a tensor's slot is made by its first range (row0 == 0); later ranges fill it
+    auto seen = c->up_rows.find(name);
+    const bool first = row0 == 0 && (seen == c->up_rows.end() || seen->second >= e1);
+    if (!first && (seen == c->up_rows.end() || c->slots.find(name) == c->slots.end()))
+        return fail(c, std::string("rows of ") + name + " before its first range");
+    if (first) c->up_rows[name] = 0;
+    c->up_rows[name] += n_rows;
     if (layer >= 0) {
         LayerDev & L = is_cp ? c->cp[layer] : c->talker[layer];
         if (field == "attn_q.weight" || field == "attn_k.weight" || field == "attn_v.weight") {
@@ -1155,19 +1205,28 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
             if (!L.qkv.data) { if (alloc_slot(c, L.qkv, type, e0, qd + 2 * kd)) return -1; }
             else if (L.qkv.type != type) return fail(c, std::string("attn_q/k/v must share one type: ") + name);
             const int part = field == "attn_q.weight" ? 1 : field == "attn_k.weight" ? 2 : 4;
-            const int64_t row0 = part == 1 ? 0 : part == 2 ? qd : qd + kd;
-            if (upload_rows(c, L.qkv, row0, type, e0, e1, data)) return -1;
-            L.qkv_parts |= part;
+            const int64_t prow = part == 1 ? 0 : part == 2 ? qd : qd + kd;
+            if (upload_rows(c, L.qkv, prow + row0, type, e0, n_rows, data)) return -1;
+            if (c->up_rows[name] == e1) L.qkv_parts |= part;
             Slot v = L.qkv; v.ne1 = e1;
-            v.data = type == Q3T_TYPE_Q8_0 ? (void *) ((int8_t *) L.qkv.data + row0 * e0)
-                                           : (void *) ((char *) L.qkv.data + row0 * e0 * (type == Q3T_TYPE_F16 ? 2 : 4));
-            if (v.scales) v.scales = L.qkv.scales + row0 * (e0 / 32);
+            v.data = type == Q3T_TYPE_Q8_0 ? (void *) ((int8_t *) L.qkv.data + prow * e0)
+                                           : (void *) ((char *) L.qkv.data + prow * e0 * (type == Q3T_TYPE_F16 ? 2 : 4));
+            if (v.scales) v.scales = L.qkv.scales + prow * (e0 / 32);
             c->slots[name] = v;
             return 0;
         }
-        Slot s;
-        if (alloc_slot(c, s, type, e0, e1) || upload_rows(c, s, 0, type, e0, e1, data)) return -1;
+    }
+    Slot s;
+    if (first) {
+        if (alloc_slot(c, s, type, e0, e1)) return -1;
         c->slots[name] = s;
+    } else {
+        s = c->slots[name];
+        if (s.type != type) return fail(c, std::string("tensor type changed between ranges: ") + name);
+    }
+    if (upload_rows(c, s, row0, type, e0, n_rows, data)) return -1;
+    if (layer >= 0) {
+        LayerDev & L = is_cp ? c->cp[layer] : c->talker[layer];
         if (field == "attn_output.weight") L.wo = s;
         else if (field == "ffn_gate.weight") L.wg = s;
         else if (field == "ffn_up.weight") L.wu = s;
@@ -1178,9 +1237,6 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
         else if (field == "attn_k_norm.weight") L.k_norm = (const float *) s.data;
         return 0;
     }
-    Slot s;
-    if (alloc_slot(c, s, type, e0, e1) || upload_rows(c, s, 0, type, e0, e1, data)) return -1;
-    c->slots[name] = s;
     const std::string n = name;
     if (field == "cp_embd") c->cp_embd[cb] = s;
     else if (field == "cp_head") c->cp_head[cb] = s;
@@ -1196,6 +1252,32 @@ int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const in
     else if (n == "code_pred.mtp_proj.weight") c->mtp_w = s;
     else if (n == "code_pred.mtp_proj.bias") c->mtp_b = s;
     return 0;
+}
+
+int q3t_dev_upload_tensor(q3t_dev * c, const char * name, int32_t type, const int64_t ne[4], const void * data,
+                          size_t nbytes) {
+    if (!c || !name || !ne || !data) return -1;
+    return q3t_dev_upload_tensor_rows(c, name, type, ne, 0, ne[1], data, nbytes);
+}
+
+void * q3t_dev_staging(q3t_dev * c, size_t min_bytes, size_t * cap_out) {
+    if (!c) return nullptr;
+    if (hipSetDevice(c->device) != hipSuccess) { fail(c, "hipSetDevice failed"); return nullptr; }
+    constexpr size_t kDefault = (size_t) 64 << 20;
+    const size_t want = std::max(min_bytes, kDefault);
+    if (want > c->up_host_cap) {
+        if (c->up_host) (void) hipHostFree(c->up_host);
+        c->up_host = nullptr;
+        c->up_host_cap = 0;
+        if (hipHostMalloc(&c->up_host, want, hipHostMallocDefault) != hipSuccess) {
+            c->up_host = nullptr;
+            fail(c, "pinned staging allocation failed");
+            return nullptr;
+        }
+        c->up_host_cap = want;
+    }
+    if (cap_out) *cap_out = c->up_host_cap;
+    return c->up_host;
 }
 
 int q3t_dev_download_tensor(q3t_dev * c, const char * name, void * data, size_t nbytes) {

@@ -81,6 +81,20 @@ void parse_config(const GGUFReader & g, tts_transformer_config & cfg) {
                                    "qwen3-tts.language_id"}, 2050);
 }
 
+// The first talker / code-predictor tensor of a type this build cannot load
+// (it would otherwise surface later as a missing tensor): false with `err`.
+bool check_tensor_types(const GGUFReader & g, std::string & err) {
+    for (const GGUFTensorInfo & t : g.tensors()) {
+        const bool ours = t.name.rfind("talker.", 0) == 0 || t.name.rfind("code_pred.", 0) == 0;
+        if (ours && t.nbytes == 0) {
+            err = "unsupported tensor type " + gguf_type_name(t.type) + " for " + t.name +
+                  " (this build loads F32, F16 and Q8_0 tensors: convert with --type f16 or q8_0)";
+            return false;
+        }
+    }
+    return true;
+}
+
 uint64_t splitmix64(uint64_t x) {
     x += 0x9E3779B97F4A7C15ull;
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -112,11 +126,19 @@ void TTSTransformer::unload_model() {
 
 void TTSTransformer::set_n_threads(int32_t) {}
 
+bool load_gguf_config(const std::string & path, tts_transformer_config & out, std::string & err) {
+    GGUFReader g;
+    if (!g.open(path)) { err = g.error(); return false; }
+    parse_config(g, out);
+    return check_tensor_types(g, err);
+}
+
 bool TTSTransformer::load_model(const std::string & model_path) {
     unload_model();
     GGUFReader g;
     if (!g.open(model_path)) { error_msg_ = g.error(); return false; }
     parse_config(g, config_);
+    if (!check_tensor_types(g, error_msg_)) return false;
     const q3t_config dc = to_dev_config(config_);
     int device = 0;
     if (const char * e = std::getenv("QWEN3_TTS_DEVICE")) device = std::atoi(e);
@@ -126,14 +148,26 @@ bool TTSTransformer::load_model(const std::string & model_path) {
         if (dev_) { q3t_dev_destroy(dev_); dev_ = nullptr; }
         return false;
     }
-    std::vector<uint8_t> buf;
+    // Tensors go to HBM in row ranges through the context's pinned staging
+    // buffer (64 MiB): host memory stays bounded whatever the tensor size (the
+    // text embedding alone is 622 MB at F16), and each range is one DMA.
     for (const GGUFTensorInfo & t : g.tensors()) {
         if (t.name.find("spk_enc.") != std::string::npos || t.name.find("tok_") != std::string::npos) continue;
-        if (t.nbytes == 0) continue;
-        if (!g.read_tensor(t, buf)) { error_msg_ = g.error(); unload_model(); return false; }
-        if (!dev_ok(q3t_dev_upload_tensor(dev_, t.name.c_str(), t.type, t.ne, buf.data(), buf.size()))) {
-            unload_model();
-            return false;
+        if (t.nbytes == 0) continue;      // not ours (checked above)
+        const int64_t rows = t.n_dims >= 2 ? t.ne[1] * t.ne[2] * t.ne[3] : 1;
+        const size_t row_bytes = t.nbytes / (size_t) rows;
+        size_t cap = 0;
+        uint8_t * stage = (uint8_t *) q3t_dev_staging(dev_, row_bytes, &cap);
+        if (!stage) { dev_ok(-1); unload_model(); return false; }
+        const int64_t per = (int64_t) std::max<size_t>(1, cap / row_bytes);
+        for (int64_t r0 = 0; r0 < rows; r0 += per) {
+            const int64_t n = std::min(per, rows - r0);
+            if (!g.read_tensor_rows(t, r0, n, stage)) { error_msg_ = g.error(); unload_model(); return false; }
+            if (!dev_ok(q3t_dev_upload_tensor_rows(dev_, t.name.c_str(), t.type, t.ne, r0, n, stage,
+                                                   row_bytes * (size_t) n))) {
+                unload_model();
+                return false;
+            }
         }
     }
     fprintf(stderr, "  TTSTransformer backend: HIP (MI355X frame loop)\n");

@@ -153,4 +153,11 @@ private:
     std::vector<std::vector<float>> attn_rows_;
 };
 
+// A GGUF file's hyperparameters as load_model parses them (primary keys, then
+// the converter's aliases, then the defaults; src/tts_transformer.cpp:228-377),
+// and a check that every talker / code-predictor tensor has a type this build
+// loads (F32, F16, Q8_0).  No device is touched.  False with `err` set when
+// the file cannot be read or a tensor type is unsupported.
+bool load_gguf_config(const std::string & path, tts_transformer_config & out, std::string & err);
+
 }  // namespace qwen3_tts

@@ -46,7 +46,7 @@ def build_facade(verbose=False):
         raise RuntimeError("g++ (facade) failed:\n" + r.stderr[-4000:])
     os.replace(out + ".tmp", out)
     root = os.path.dirname(PKG_DIR)
-    for name in ("test_transformer_dev", "test_vocoder_dev"):
+    for name in ("test_transformer_dev", "test_vocoder_dev", "test_gguf_config"):
         test_src = os.path.join(root, "tests", "cpp", name + ".cpp")
         test_bin = os.path.join(lib_dir, name)
         if not os.path.exists(test_src):

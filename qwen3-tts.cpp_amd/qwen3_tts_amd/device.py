@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(PKG_DIR, "lib", "libq3t_hip.so")
 
 EXPORTS = [
     "q3t_dev_create", "q3t_dev_destroy", "q3t_dev_last_error", "q3t_dev_upload_tensor",
+    "q3t_dev_upload_tensor_rows", "q3t_dev_staging",
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_set_type", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
     "q3t_dev_attn_row", "q3t_dev_prefill", "q3t_dev_talker_step",
@@ -57,6 +58,10 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_last_error.argtypes = [vp]
         lib.q3t_dev_last_error.restype = ctypes.c_char_p
         lib.q3t_dev_upload_tensor.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(ctypes.c_int64), vp, ctypes.c_size_t]
+        lib.q3t_dev_upload_tensor_rows.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(ctypes.c_int64),
+                                                   ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_size_t]
+        lib.q3t_dev_staging.argtypes = [vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+        lib.q3t_dev_staging.restype = vp
         lib.q3t_dev_download_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
         lib.q3t_dev_dequantize.argtypes = [vp, ctypes.c_char_p, f32p, ctypes.c_size_t]
         lib.q3t_dev_kv_reserve.argtypes = [vp, i32]
@@ -139,9 +144,27 @@ class Device:
         ne4 = (ctypes.c_int64 * 4)(ne[0], ne[1], 1, 1)
         self._check(self.lib.q3t_dev_upload_tensor(self.h, name.encode(), ttype, ne4, _p(arr), arr.nbytes), f"upload {name}")
 
-    def upload_weights(self, weights):
+    def upload_rows(self, name, ttype, ne, row0, arr):
+        """rows [row0, row0 + n) of a tensor (arr: those rows, ggml layout)"""
+        arr = np.ascontiguousarray(arr)
+        ne4 = (ctypes.c_int64 * 4)(ne[0], ne[1], 1, 1)
+        row_bytes = ne[0] * 2 if ttype == 1 else ne[0] * 4 if ttype == 0 else ne[0] // 32 * 34
+        n = arr.nbytes // row_bytes
+        self._check(self.lib.q3t_dev_upload_tensor_rows(self.h, name.encode(), ttype, ne4, row0, n, _p(arr),
+                                                         arr.nbytes), f"upload rows of {name}")
+
+    def upload_weights(self, weights, chunk_rows=0):
+        """chunk_rows > 0: every tensor in ranges of that many rows, the last
+        range first (q3t_dev_upload_tensor_rows)"""
         for name, (ttype, ne, arr) in weights.items():
-            self.upload(name, ttype, ne, arr)
+            if chunk_rows <= 0 or ne[1] <= 1:
+                self.upload(name, ttype, ne, arr)
+                continue
+            flat = np.ascontiguousarray(arr).view(np.uint8).reshape(ne[1], -1)
+            starts = list(range(0, ne[1], chunk_rows))
+            # the first range allocates the tensor; the others in reverse order
+            for r0 in [0] + starts[1:][::-1]:
+                self.upload_rows(name, ttype, ne, r0, flat[r0:r0 + chunk_rows])
 
     def download(self, name, nbytes):
         out = np.empty(nbytes, dtype=np.uint8)

@@ -61,19 +61,28 @@ def test_facade_matches_oracle(tmp_path, wtype, layout):
 @pytest.mark.slow
 def test_facade_full_06b_q8(tmp_path):
     """The facade over a full-size Q8_0 0.6B GGUF file (about 1.3 GB: the
-    151,936-row text embedding, 28 + 5 layers, 16 heads) written with the
-    reference converter's names and key list: load_model, generate,
+    151,936-row text embedding, 28 + 5 layers, 16 heads) written in the
+    reference converter's metadata form (its key aliases, general.* strings,
+    the mrope_section array and tokenizer arrays): load_model, generate,
     attention dump, predict_codes_autoregressive and generate_icl against the
     oracle."""
     cfg = qcfg.full_06b()
     print("[gpu] facade full 0.6B q8_0: synth", file=sys.stderr, flush=True)
-    _facade_check(tmp_path, cfg, Weights(cfg, "q8_0", seed=31), "q8_0", "full_06b", 12)
+    _facade_check(tmp_path, cfg, Weights(cfg, "q8_0", seed=31), "q8_0", "full_06b", 12, converter=True)
 
 
-def _facade_check(tmp_path, cfg, w, wtype, layout, max_len):
+def _facade_check(tmp_path, cfg, w, wtype, layout, max_len, converter=False):
+    """converter: the file carries the reference converter's metadata form
+    (gguf.write_converter: alias keys, general.* strings, the mrope_section
+    array, tokenizer arrays).  load_model streams every tensor to HBM in row
+    ranges through the pinned staging buffer (the 622 MB text embedding in
+    64 MiB pieces)."""
     assert os.path.exists(BIN), "build() first"
     model = tmp_path / "model.gguf"
-    gguf.write(str(model), cfg, w)
+    if converter:
+        gguf.write_converter(str(model), cfg, w, wtype)
+    else:
+        gguf.write(str(model), cfg, w)
     rng = np.random.default_rng(32)
     text = rng.integers(0, cfg.text_vocab - 8, 26).astype(np.int32)
     spk = rng.standard_normal(cfg.hidden_size).astype(np.float32)

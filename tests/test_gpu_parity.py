@@ -72,6 +72,56 @@ def test_upload_roundtrip_and_dequant(tiny_model):
             assert np.array_equal(deq.view(np.uint32), orc.dequantize(arr, ne[0] * ne[1]).view(np.uint32))
 
 
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_ranged_upload_equals_whole_upload(wtype):
+    """q3t_dev_upload_tensor_rows: every tensor sent in ranges of 7 rows,
+    the first range first and the others in reverse order (Q8_0 blocks
+    repacked on the device), downloads equal the whole-tensor upload's bytes,
+    Q8_0 dequantises bit-exactly, and a prefill plus a code-predictor pass
+    equal the oracle's.  A tensor missing a range is reported by name."""
+    cfg = qcfg.tiny()
+    w = Weights(cfg, wtype, seed=19)
+    dev = Device(cfg)
+    try:
+        dev.upload_weights(w, chunk_rows=7)
+        for name in ["talker.blk.0.attn_q.weight", "talker.blk.0.attn_v.weight", "talker.blk.1.ffn_down.weight",
+                     "talker.codec_head.weight", "talker.text_embd.weight", "code_pred.lm_head.3.weight",
+                     "talker.output_norm.weight"]:
+            ttype, ne, arr = w[name]
+            assert np.array_equal(dev.download(name, arr.nbytes), arr.view(np.uint8).ravel()), name
+            if ttype == 8:
+                deq = dev.dequantize(name, ne[0] * ne[1])
+                assert np.array_equal(deq.view(np.uint32), dequantize_q8_0(arr).view(np.uint32)), name
+        o = orc.Oracle(cfg, w, threads=4)
+        dev.kv_reserve(32)
+        o.kv_reset(32)
+        embd = (np.random.default_rng(20).standard_normal((6, cfg.hidden_size)) * 0.05).astype(np.float32)
+        hg, lg = dev.prefill(embd, 0)
+        ho, lo = o.prefill(embd, 0)
+        assert np.array_equal(hg, ho) and np.array_equal(lg, lo)
+        cg, _ = dev.code_pred(ho[-1], 11)
+        co, _ = o.code_pred(ho[-1], 11)
+        assert np.array_equal(cg, co)
+        o.close()
+    finally:
+        dev.close()
+    # one range short: the first compute call names the tensor
+    dev = Device(cfg)
+    try:
+        items = list(w.items())
+        for name, (ttype, ne, arr) in items:
+            if name == "talker.blk.1.ffn_up.weight":
+                flat = np.ascontiguousarray(arr).view(np.uint8).reshape(ne[1], -1)
+                dev.upload_rows(name, ttype, ne, 0, flat[: ne[1] - 5])
+            else:
+                dev.upload(name, ttype, ne, arr)
+        dev.kv_reserve(16)
+        with pytest.raises(Exception, match="talker.blk.1.ffn_up.weight incomplete"):
+            dev.prefill(embd[:2], 0)
+    finally:
+        dev.close()
+
+
 @pytest.fixture(params=["gemv", "mfma"])
 def prefill_path(request, monkeypatch):
     """Runs a prefill test on the chunked GEMV prefill and on the int8 MFMA
