@@ -181,6 +181,17 @@ int  q3t_dev_prefill(q3t_dev * dev, const float * embd, int32_t n, int32_t n_pas
  * multi-kernel step; same results). */
 int  q3t_dev_talker_step(q3t_dev * dev, const float * embd, int32_t n_past,
                          float * logits_out, float * hidden_out);
+/* Single-pass code predictor: replaces TTSTransformer::predict_codes
+ * (src/tts_transformer.cpp:2531-2581, graph build_code_pred_graph :1771-1899).
+ * One row: hidden [hidden_size] plus, when prev_codes is not NULL, the 15
+ * code_pred.codec_embd[g][prev_codes[g]] rows (added in order, fp32); the
+ * MTP projection when the layout has one; the code-predictor layers on one
+ * position with no cache (each head's attention output is its V row); the 15
+ * heads on the last layer's row with no output norm.  logits_out:
+ * [15][cp_vocab].  Needs no KV reservation and leaves the frame loop's state
+ * alone.  A code outside [0, cp_vocab) fails ("Embedding token ID out of
+ * range"). */
+int  q3t_dev_predict_codes(q3t_dev * dev, const float * hidden, const int32_t * prev_codes, float * logits_out);
 /* Code predictor: 2-token prefill [hidden, codec_embd[cb0]] then 14 steps;
  * codes_out[15] = codebooks 1..15.  logits_out (NULL ok): [15][cp_vocab],
  * each head's logits before sampling.  `frame` keys the sampler's RNG.

@@ -621,6 +621,31 @@ void layer_forward(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float
     for (int64_t i = 0; i < ntok * d; ++i) x[i] = t[i] + x[i];
 }
 
+// One block of the single-pass code predictor: one row, one position, no
+// cache (src/tts_transformer.cpp:1823-1890).  Its attention is softmax over a
+// single score, which is exactly 1, times that row's fp32 V: query head h
+// gets V of KV head h / group (ggml_mul_mat broadcasts the KV heads over the
+// query heads, :1855-1864).  Q, K, their norms and the score do not reach the
+// output, so they are not computed.
+void layer_single(orc_model * m, const Layer & L, int64_t d, int64_t ffn, float * x) {
+    const orc_config & c = m->cfg;
+    const int64_t hd = c.head_dim, nh = c.n_head, nkv = c.n_kv_head;
+    const int64_t qd = nh * hd, kd = nkv * hd, group = nh / nkv;
+    std::vector<float> h(d), v(kd), o(qd), t(d), g(ffn), u(ffn);
+    orc_rmsnorm(x, fp(L.attn_norm), d, c.rms_eps, h.data());
+    gemv_t(m, L.wv, kd, d, h.data(), 1, v.data());
+    for (int64_t hh = 0; hh < nh; ++hh)
+        for (int64_t e = 0; e < hd; ++e) o[hh * hd + e] = v[(hh / group) * hd + e];
+    gemv_t(m, L.wo, d, qd, o.data(), 1, t.data());
+    for (int64_t i = 0; i < d; ++i) x[i] = t[i] + x[i];
+    orc_rmsnorm(x, fp(L.ffn_norm), d, c.rms_eps, h.data());
+    gemv_t(m, L.wg, ffn, d, h.data(), 1, g.data());
+    gemv_t(m, L.wu, ffn, d, h.data(), 1, u.data());
+    for (int64_t i = 0; i < ffn; ++i) g[i] = silu(g[i]) * u[i];
+    gemv_t(m, L.wd, d, ffn, g.data(), 1, t.data(), true);
+    for (int64_t i = 0; i < d; ++i) x[i] = t[i] + x[i];
+}
+
 bool resolve(orc_model * m) {
     const orc_config & c = m->cfg;
     auto get = [&](const std::string & n, Tensor & dst) -> bool {
@@ -843,6 +868,32 @@ int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,
         if (logits_out) std::memcpy(logits_out + (size_t) s * V, logits.data(), V * sizeof(float));
         codes_out[s] = orc_sample_cp(logits.data(), V, temperature, top_k, seed, frame, (uint32_t) (s + 1));
     }
+    return 0;
+}
+
+int orc_predict_codes(orc_model * m, const float * hidden, const int32_t * prev_codes, float * logits_out) {
+    const orc_config & c = m->cfg;
+    if (m->talker.empty() && !resolve(m)) return -1;
+    const int64_t d = c.hidden_size, dc = c.cp_hidden;
+    const int ng = c.n_codebooks - 1;
+    // hidden + code_pred.codec_embd[g][prev_codes[g]], added in codebook
+    // order in fp32 (:1801-1808)
+    std::vector<float> in(hidden, hidden + d), e(d), x(dc);
+    for (int g = 0; prev_codes && g < ng; ++g) {
+        if (prev_codes[g] < 0 || prev_codes[g] >= c.cp_vocab) { m->err = "Embedding token ID out of range"; return -1; }
+        embd_row(m->cp_embd[g], d, prev_codes[g], e.data());
+        for (int64_t i = 0; i < d; ++i) in[i] = in[i] + e[i];
+    }
+    // the MTP projection (:1811-1816); identity in the 0.6B layout
+    if (dc != d) {
+        gemv_t(m, m->mtp_w, dc, d, in.data(), 1, x.data());
+        for (int64_t j = 0; j < dc; ++j) x[j] = x[j] + fp(m->mtp_b)[j];
+    } else {
+        x = in;
+    }
+    for (int il = 0; il < c.cp_layers; ++il) layer_single(m, m->cp[il], dc, c.cp_ffn, x.data());
+    // the heads read the last layer's row as it is: no output norm (:1881-1888)
+    for (int g = 0; g < ng; ++g) gemv_t(m, m->cp_head[g], c.cp_vocab, dc, x.data(), 1, logits_out + (size_t) g * c.cp_vocab);
     return 0;
 }
 

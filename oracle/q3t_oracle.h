@@ -209,6 +209,12 @@ int32_t orc_attn_row(const orc_model * m, int32_t index, float * out, int64_t ca
 int orc_code_pred(orc_model * m, const float * hidden, int32_t cb0,
                   float temperature, int32_t top_k, uint64_t seed, uint32_t frame,
                   int32_t * codes_out, float * logits_out);
+/* Single-pass code predictor (src/tts_transformer.cpp:2531-2581 over
+ * build_code_pred_graph :1771-1899): logits_out [15][cp_vocab] of the 15
+ * heads on one row hidden (+ the 15 code-predictor embeddings of prev_codes
+ * when not NULL) after the MTP projection (if any) and the layers at one
+ * position with no cache and no output norm. */
+int orc_predict_codes(orc_model * m, const float * hidden, const int32_t * prev_codes, float * logits_out);
 int orc_text_proj(orc_model * m, const int32_t * tokens, int32_t n, float * out);
 int orc_embed_row(orc_model * m, const char * table, int32_t index, int32_t token, float * out);
 /* build_prefill_graph: prefill_out [(n_instruct+10 or 9)][d],

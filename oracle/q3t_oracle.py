@@ -106,6 +106,7 @@ def lib():
         L.orc_attn_row_count.argtypes = [vp]; L.orc_attn_row_count.restype = i32
         L.orc_attn_row.argtypes = [vp, i32, vp, i64]; L.orc_attn_row.restype = i32
         L.orc_code_pred.argtypes = [vp, vp, i32, f32, i32, u64, u32, vp, vp]
+        L.orc_predict_codes.argtypes = [vp, vp, vp, vp]
         L.orc_text_proj.argtypes = [vp, vp, i32, vp]
         L.orc_embed_row.argtypes = [vp, ctypes.c_char_p, i32, i32, vp]
         L.orc_build_prefill.argtypes = [vp, vp, i32, vp, i32, vp, i32, vp, vp, vp, ctypes.POINTER(i32)]
@@ -358,6 +359,15 @@ class Oracle:
         self._chk(self.L.orc_code_pred(self.h, _p(hidden), int(cb0), temperature, top_k, seed, frame, _p(codes), _p(logits)),
                   "code_pred")
         return codes, logits
+
+    def predict_codes(self, hidden, prev_codes=None):
+        """single-pass code predictor: logits [15][cp_vocab]"""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        prev = None if prev_codes is None else np.ascontiguousarray(prev_codes, np.int32)
+        logits = np.empty((self.cfg.n_codebooks - 1, self.cfg.cp_vocab), np.float32)
+        self._chk(self.L.orc_predict_codes(self.h, _p(hidden), None if prev is None else _p(prev), _p(logits)),
+                  "predict_codes")
+        return logits
 
     def text_proj(self, tokens):
         tokens = np.ascontiguousarray(tokens, np.int32)

@@ -542,6 +542,25 @@ void attention(q3t_dev * c, const AttnSpec & s, int nt) {
     hipLaunchKernelGGL(k_attention, dim3(g.n_head, nt), dim3(kBlock), attn_lds_bytes(s.n_ctx), c->stream, a);
 }
 
+// A block's second half over nt rows whose attention output is in c->attn:
+// Wo plus the residual `xin` into c->xb, then the FFN with its residual into
+// c->xa.  no_done: the kernels ignore the frame state's done flag.
+void layer_tail(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, int ffn, bool no_done) {
+    const int qd = c->cfg.n_head * c->cfg.head_dim;
+    GemvSpec o{};
+    o.w = weight_of(L.wo); o.rows = d; o.K = qd; o.x = c->attn; o.x_stride = qd;
+    o.y = c->xb; o.y_stride = d; o.resid = xin; o.resid_stride = d; o.epi = EPI_RESID; o.no_done = no_done;
+    gemv(c, o, nt);
+    GemvSpec f{};
+    f.w = weight_of(L.wg); f.w2 = weight_of(L.wu); f.rows = ffn; f.K = d; f.x = c->xb; f.x_stride = d;
+    f.norm_w = L.ffn_norm; f.y = c->ffn; f.y_stride = ffn; f.epi = EPI_SWIGLU; f.no_done = no_done;
+    gemv(c, f, nt);
+    GemvSpec dn{};
+    dn.w = weight_of(L.wd, true); dn.rows = d; dn.K = ffn; dn.x = c->ffn; dn.x_stride = ffn;
+    dn.y = c->xa; dn.y_stride = d; dn.resid = c->xb; dn.resid_stride = d; dn.epi = EPI_RESID; dn.no_done = no_done;
+    gemv(c, dn, nt);
+}
+
 // One transformer block over nt tokens; input rows `xin` (stride d),
 // output rows left in c->xa.
 void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, int ffn, uint16_t * kc, uint16_t * vc,
@@ -557,18 +576,36 @@ void layer(q3t_dev * c, const LayerDev & L, const float * xin, int nt, int d, in
     as.f32_prefill = f32_prefill;
     as.probs = probs;
     attention(c, as, nt);
-    GemvSpec o{};
-    o.w = weight_of(L.wo); o.rows = d; o.K = qd; o.x = c->attn; o.x_stride = qd;
-    o.y = c->xb; o.y_stride = d; o.resid = xin; o.resid_stride = d; o.epi = EPI_RESID;
-    gemv(c, o, nt);
-    GemvSpec f{};
-    f.w = weight_of(L.wg); f.w2 = weight_of(L.wu); f.rows = ffn; f.K = d; f.x = c->xb; f.x_stride = d;
-    f.norm_w = L.ffn_norm; f.y = c->ffn; f.y_stride = ffn; f.epi = EPI_SWIGLU;
-    gemv(c, f, nt);
-    GemvSpec dn{};
-    dn.w = weight_of(L.wd, true); dn.rows = d; dn.K = ffn; dn.x = c->ffn; dn.x_stride = ffn;
-    dn.y = c->xa; dn.y_stride = d; dn.resid = c->xb; dn.resid_stride = d; dn.epi = EPI_RESID;
-    gemv(c, dn, nt);
+    layer_tail(c, L, xin, nt, d, ffn, false);
+}
+
+// Rows [row0, ..) of a [rows][K] matrix as a weight of their own.
+Weight weight_rows(const Slot & s, int64_t row0, int64_t K) {
+    Weight w = weight_of(s);
+    if (s.type == Q3T_TYPE_Q8_0) {
+        w.w = (const int8_t *) s.data + row0 * K;
+        w.d = s.scales + row0 * (K / 32);
+    } else {
+        w.w = (const uint16_t *) s.data + row0 * K;
+    }
+    return w;
+}
+
+// One transformer block of the single-pass code predictor on one row at one
+// position with no cache (build_code_pred_graph, src/tts_transformer.cpp:
+// 1823-1890): the attention over the row itself returns its V row, so only
+// the V rows of the fused QKV matrix are multiplied; Q, K, their norms and
+// the score leave no trace in the output.  No kernel reads the frame state.
+void layer_single(q3t_dev * c, const LayerDev & L, const float * xin, int d, int ffn) {
+    const q3t_config & g = c->cfg;
+    const int qd = g.n_head * g.head_dim, kd = g.n_kv_head * g.head_dim;
+    GemvSpec s{};
+    s.w = weight_rows(L.qkv, qd + kd, d); s.rows = kd; s.K = d; s.x = xin; s.x_stride = d;
+    s.norm_w = L.attn_norm; s.y = c->qkv; s.y_stride = kd; s.no_done = true;
+    gemv(c, s, 1);
+    hipLaunchKernelGGL(k_v_to_heads, dim3((qd + 255) / 256), dim3(256), 0, c->stream, c->qkv, g.head_dim,
+                       g.n_head / g.n_kv_head, g.n_head, c->attn);
+    layer_tail(c, L, xin, 1, d, ffn, true);
 }
 
 // Talker forward of nt (<= 4) tokens whose input rows are `xin`.  The codec
@@ -639,6 +676,33 @@ void code_pred_seq(q3t_dev * c, bool frame_loop) {
         SampleArgs sa = sample_args(c, 1, step + 1);
         if (frame_loop) sa.codes_out = c->codes_out;
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), 0, c->stream, sa);
+    }
+}
+
+// The single-pass code predictor (build_code_pred_graph, src/tts_transformer.
+// cpp:1771-1899) on the row in c->stage: its input sum, the MTP projection
+// when the layout has one, the layers on one position with no cache, and the
+// 15 heads on the last layer's row with no output norm, into c->cp_logits.
+// Touches neither the frame state nor c->hidden / c->logits.
+void code_pred_single(q3t_dev * c, SingleInArgs in) {
+    const q3t_config & g = c->cfg;
+    const int d = g.cp_hidden;
+    const bool mtp = g.cp_hidden != g.hidden_size;
+    in.hidden = c->stage; in.out = c->stage; in.d = g.hidden_size;
+    hipLaunchKernelGGL(k_cp_single_input, dim3((g.hidden_size + 255) / 256), dim3(256), 0, c->stream, in);
+    if (mtp) {
+        GemvSpec m{};
+        m.w = weight_of(c->mtp_w); m.rows = d; m.K = g.hidden_size; m.x = c->stage; m.x_stride = g.hidden_size;
+        m.y = c->cpx; m.y_stride = d; m.bias = (const float *) c->mtp_b.data; m.epi = EPI_BIAS; m.no_done = true;
+        gemv(c, m, 1);
+    }
+    for (int il = 0; il < g.cp_layers; ++il)
+        layer_single(c, c->cp[il], il == 0 ? (mtp ? c->cpx : c->stage) : c->xa, d, g.cp_ffn);
+    for (int h = 0; h < g.n_codebooks - 1; ++h) {
+        GemvSpec o{};
+        o.w = weight_of(c->cp_head[h]); o.rows = g.cp_vocab; o.K = d; o.x = c->xa; o.x_stride = d;
+        o.y = c->cp_logits + (size_t) h * g.cp_vocab; o.y_stride = g.cp_vocab; o.no_done = true;
+        gemv(c, o, 1);
     }
 }
 
@@ -2091,6 +2155,30 @@ int q3t_dev_talker_step(q3t_dev * c, const float * embd, int32_t n_past, float *
         std::memcpy(&err, c->pin + o_err, 4);
         if (err) return fail(c, fk_err_msg(err));
     }
+    return 0;
+}
+
+int q3t_dev_predict_codes(q3t_dev * c, const float * hidden, const int32_t * prev_codes, float * logits_out) {
+    if (!c || !hidden || !logits_out) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (resolve(c)) return -1;
+    const q3t_config & g = c->cfg;
+    const int ng = g.n_codebooks - 1;
+    SingleInArgs in{};
+    in.n = prev_codes ? ng : 0;
+    for (int i = 0; i < in.n; ++i) {
+        if (prev_codes[i] < 0 || prev_codes[i] >= g.cp_vocab) return fail(c, "Embedding token ID out of range");
+        in.codes[i] = prev_codes[i];
+        in.embd[i] = (const uint16_t *) c->cp_embd[i].data;
+    }
+    const size_t d4 = (size_t) g.hidden_size * 4, l4 = (size_t) ng * g.cp_vocab * 4;
+    if (ensure_pin(c, d4 + l4)) return -1;
+    std::memcpy(c->pin, hidden, d4);
+    HIP_OK(hipMemcpyAsync(c->stage, c->pin, d4, hipMemcpyHostToDevice, c->stream));
+    code_pred_single(c, in);
+    HIP_OK(hipMemcpyAsync(c->pin + d4, c->cp_logits, l4, hipMemcpyDeviceToHost, c->stream));
+    if (sync(c)) return -1;
+    std::memcpy(logits_out, c->pin + d4, l4);
     return 0;
 }
 

@@ -992,6 +992,35 @@ __global__ void k_cp_input(const FrameState * st, const float * hidden, const ui
     stage[d + e] = h2f(codec_embd[(size_t) st->codes[0] * d + e]);
 }
 
+// The single-pass code predictor's input row (src/tts_transformer.cpp:1801-1808):
+// hidden + code_pred.codec_embd[g][codes[g]] for g = 0 .. n-1, added in that
+// order in fp32.  Codes are checked on the host.
+struct SingleInArgs {
+    const float * hidden;
+    float * out;
+    int32_t d, n;
+    int32_t codes[15];
+    const uint16_t * embd[15];
+};
+
+__global__ void k_cp_single_input(SingleInArgs a) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= a.d) return;
+    float v = a.hidden[e];
+    for (int g = 0; g < a.n; ++g) v = v + h2f(a.embd[g][(size_t) a.codes[g] * a.d + e]);
+    a.out[e] = v;
+}
+
+// Attention of one position over itself (src/tts_transformer.cpp:1855-1864):
+// the softmax of a single score is exactly 1, so query head h's output is the
+// fp32 V row of its KV head h / group.
+__global__ void k_v_to_heads(const float * v, int32_t head_dim, int32_t group, int32_t n_head, float * out) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_head * head_dim) return;
+    const int h = e / head_dim, i = e - h * head_dim;
+    out[e] = v[(size_t) (h / group) * head_dim + i];
+}
+
 // normed rows for the prefill's all-token hidden output
 __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float * x, const float * w, float eps, int32_t d,
                                                         float * y) {

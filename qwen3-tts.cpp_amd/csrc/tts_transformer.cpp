@@ -10,6 +10,7 @@
 #include "gguf_reader.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -273,13 +274,14 @@ bool TTSTransformer::get_hidden_states(std::vector<float> & hidden) const {
     return true;
 }
 
-// The reference's legacy single-pass predictor (build_code_pred_graph,
-// src/tts_transformer.cpp:1771-1899) is not used by generate(); the device
-// path does not implement it.
-bool TTSTransformer::predict_codes(const float *, const int32_t *, std::vector<float> &) {
-    error_msg_ = "predict_codes (legacy single-pass code predictor) is not available on the device path; "
-                 "use predict_codes_autoregressive";
-    return false;
+// The single-pass predictor (src/tts_transformer.cpp:2531-2581): output is
+// [15][code_pred_vocab_size] logits; prev_codes, when not null, holds the 15
+// previous codes whose code-predictor embeddings join the input row.
+bool TTSTransformer::predict_codes(const float * hidden, const int32_t * prev_codes, std::vector<float> & output) {
+    if (!dev_) { error_msg_ = "Model not loaded"; return false; }
+    if (!hidden) { error_msg_ = "hidden is null"; return false; }
+    output.resize((size_t) (config_.n_codebooks - 1) * config_.code_pred_vocab_size);
+    return dev_ok(q3t_dev_predict_codes(dev_, hidden, prev_codes, output.data()));
 }
 
 bool TTSTransformer::predict_codes_autoregressive(const float * hidden, int32_t codebook_0_token,
@@ -333,10 +335,56 @@ bool TTSTransformer::build_prefill_graph_icl(const int32_t * text_tokens, int32_
                                             trailing_text_hidden.data(), &n_trail, tts_pad_embed.data()));
 }
 
+// The QWEN3_TTS_TIMING report (src/tts_transformer.h:20-46, printed at
+// src/tts_transformer.cpp:3311-3352): compiled in with -DQWEN3_TTS_TIMING as
+// in the reference, or switched on at run time with QWEN3_TTS_TIMING=1.  The
+// device runs the codebook-0 sampler, the code predictor, the step embedding
+// and the talker step of a frame in one launch, so the frame loop is one
+// figure (wall time, and the GPU time of the frame launches from HIP events)
+// where the reference splits talker and code-predictor graphs.
+struct TTSTransformer::gen_timing {
+    double build_ms = 0, prefill_ms = 0, frames_ms = 0, frames_gpu_ms = 0, callback_ms = 0, total_ms = 0;
+    int32_t prefill_rows = 0, frames = 0, path = -1;
+    int64_t launches = 0;
+};
+
+namespace {
+
+using timing_clock = std::chrono::steady_clock;
+
+double ms_since(timing_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(timing_clock::now() - t0).count();
+}
+
+bool timing_enabled() {
+#ifdef QWEN3_TTS_TIMING
+    return true;
+#else
+    static const bool on = [] {
+        const char * e = std::getenv("QWEN3_TTS_TIMING");
+        return e && *e && std::strcmp(e, "0") != 0;
+    }();
+    return on;
+#endif
+}
+
+const char * frame_path_name(int32_t path) {
+    switch (path) {
+        case 1: return "persistent frame kernel, row-parallel layers";
+        case 3: return "persistent frame kernel, XCD-parallel layers";
+        case 0: return "captured multi-kernel graph";
+        case 2: return "multi-stream graph";
+        default: return "none";
+    }
+}
+
+}  // namespace
+
 bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::vector<float> & trailing,
                                 const std::vector<float> & pad, int32_t max_len, float repetition_penalty,
                                 float temperature, int32_t top_k, float eos_bias, int32_t target_frames,
-                                bool rep_loop_detect, const FrameCallback & on_frame, std::vector<int32_t> & output) {
+                                bool rep_loop_detect, const FrameCallback & on_frame, std::vector<int32_t> & output,
+                                gen_timing * tm) {
     const tts_transformer_config & cfg = config_;
     const int32_t d = cfg.hidden_size, ncb = cfg.n_codebooks;
     const int32_t plen = (int32_t) (prefill.size() / d);
@@ -346,7 +394,9 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
     }
     clear_kv_cache();
     std::vector<float> hidden;
+    auto t0 = timing_clock::now();
     if (!forward_prefill(prefill.data(), plen, 0, hidden, nullptr)) return false;
+    if (tm) { tm->prefill_ms = ms_since(t0); tm->prefill_rows = plen; }
     q3t_frame_args a{};
     a.trailing = trailing.empty() ? nullptr : trailing.data();
     a.n_trailing = (int32_t) (trailing.size() / d);
@@ -374,6 +424,7 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
     std::vector<std::vector<int32_t>> rep_frames;
     int32_t rep_run_len = 0, rep_run_start = 0;
     int32_t produced = 0, stop_frame = -1;
+    t0 = timing_clock::now();
     while (produced < max_len) {
         const int32_t n = std::min(chunk, max_len - produced);
         int32_t got = 0, eos = 0;
@@ -383,7 +434,12 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
             const int32_t * codes = buf.data() + (size_t) f * ncb;
             const int32_t frame = produced + f;
             output.insert(output.end(), codes, codes + ncb);
-            if (on_frame && !on_frame(codes, ncb, frame)) { stop = true; stop_frame = frame; break; }
+            if (on_frame) {
+                const auto tc = timing_clock::now();
+                const bool go_on = on_frame(codes, ncb, frame);
+                if (tm) tm->callback_ms += ms_since(tc);
+                if (!go_on) { stop = true; stop_frame = frame; break; }
+            }
             if (rep_loop_detect) rep_frames.emplace_back(codes, codes + ncb);
             const size_t nf = rep_frames.size();
             bool is_rep = false;
@@ -404,6 +460,12 @@ bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::v
         }
         produced += got;
         if (stop || eos || got < n) break;
+    }
+    if (tm) {
+        tm->frames_ms = ms_since(t0) - tm->callback_ms;
+        tm->frames = (int32_t) (output.size() / ncb);
+        double gpu_us = 0.0;
+        if (q3t_dev_frames_stats(dev_, &gpu_us, &tm->launches, &tm->path) == 0) tm->frames_gpu_ms = gpu_us / 1000.0;
     }
     kv_n_used_ = plen + produced;
     if (attn_dump_) {
@@ -434,14 +496,18 @@ bool TTSTransformer::generate(const int32_t * text_tokens, int32_t n_tokens, con
     if (!text_tokens) { error_msg_ = "text_tokens is null"; return false; }
     if (n_tokens < 4) { error_msg_ = "Need at least 4 text tokens for generation"; return false; }
     if (max_len <= 0) { output.clear(); return true; }
+    gen_timing timing, * tm = timing_enabled() ? &timing : nullptr;
+    const auto t_start = timing_clock::now();
     std::vector<float> prefill, trailing, pad;
     if (!build_prefill_graph(text_tokens, n_tokens, speaker_embd, language_id, prefill, trailing, pad,
                              instruct_tokens, n_instruct))
         return false;
+    if (tm) tm->build_ms = ms_since(t_start);
     if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
-                    rep_loop_detect, on_frame, output))
+                    rep_loop_detect, on_frame, output, tm))
         return false;
     write_attn_dump();
+    if (tm) { tm->total_ms = ms_since(t_start); print_timing(*tm); }
     return true;
 }
 
@@ -456,15 +522,42 @@ bool TTSTransformer::generate_icl(const int32_t * text_tokens, int32_t n_tokens,
     if (!text_tokens || n_tokens < 4) { error_msg_ = "ICL: need at least 4 target text tokens"; return false; }
     if (!ref_codec_tokens || n_ref_frames < 1) { error_msg_ = "ICL: need at least 1 reference codec frame"; return false; }
     if (max_len <= 0) { output.clear(); return true; }
+    gen_timing timing, * tm = timing_enabled() ? &timing : nullptr;
+    const auto t_start = timing_clock::now();
     std::vector<float> prefill, trailing, pad;
     if (!build_prefill_graph_icl(text_tokens, n_tokens, ref_text_tokens, n_ref_text, ref_codec_tokens, n_ref_frames,
                                  speaker_embd, prefill, trailing, pad))
         return false;
+    if (tm) tm->build_ms = ms_since(t_start);
     if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
-                    rep_loop_detect, on_frame, output))
+                    rep_loop_detect, on_frame, output, tm))
         return false;
     write_attn_dump();
+    if (tm) { tm->total_ms = ms_since(t_start); print_timing(*tm); }
     return true;
+}
+
+void TTSTransformer::print_timing(const gen_timing & t) {
+    const int nf = t.frames;
+    const double per = nf > 0 ? 1.0 / nf : 0.0;
+    fprintf(stderr, "\n=== Detailed Generation Timing (%d frames) ===\n", nf);
+    fprintf(stderr, "\n  Prefill:\n");
+    fprintf(stderr, "    Build rows:       %8.1f ms   (text projection and prompt layout on the device)\n", t.build_ms);
+    fprintf(stderr, "    Forward total:    %8.1f ms   (%d rows)\n", t.prefill_ms, t.prefill_rows);
+    fprintf(stderr, "\n  Frame loop (codebook-0 sampler, code predictor, step embedding, talker step; total / per-frame):\n");
+    fprintf(stderr, "    Implementation:   %s, %lld launches\n", frame_path_name(t.path), (long long) t.launches);
+    fprintf(stderr, "    Total:            %8.1f ms   (%.3f ms/frame)\n", t.frames_ms, t.frames_ms * per);
+    fprintf(stderr, "      GPU:            %8.1f ms   (%.3f ms/frame)\n", t.frames_gpu_ms, t.frames_gpu_ms * per);
+    fprintf(stderr, "      Host and sync:  %8.1f ms   (%.3f ms/frame)\n", t.frames_ms - t.frames_gpu_ms,
+            (t.frames_ms - t.frames_gpu_ms) * per);
+    fprintf(stderr, "    Callbacks:        %8.1f ms\n", t.callback_ms);
+    const double accounted = t.build_ms + t.prefill_ms + t.frames_ms + t.callback_ms;
+    fprintf(stderr, "\n  Other/overhead:     %8.1f ms\n", t.total_ms - accounted);
+    fprintf(stderr, "  -----------------------------------------\n");
+    fprintf(stderr, "  Total generate:     %8.1f ms\n", t.total_ms);
+    if (nf > 0)
+        fprintf(stderr, "  Throughput:         %8.3f ms/frame (%.1f frames/s)\n", t.total_ms / nf,
+                1000.0 * nf / t.total_ms);
 }
 
 bool TTSTransformer::forward(const int32_t * tokens, int32_t n_tokens, int32_t n_past, std::vector<float> & output) {

@@ -131,12 +131,15 @@ private:
                                  std::vector<float> & trailing_text_hidden, std::vector<float> & tts_pad_embed);
     bool project_text_tokens(const int32_t * text_tokens, int32_t n_tokens, std::vector<float> & output);
     bool lookup_rows(int32_t table, int32_t index, const int32_t * ids, int32_t n, std::vector<float> & out);
+    // figures of the QWEN3_TTS_TIMING report
+    struct gen_timing;
     bool run_frames(const std::vector<float> & prefill, const std::vector<float> & trailing,
                     const std::vector<float> & pad, int32_t max_len, float repetition_penalty, float temperature,
                     int32_t top_k, float eos_bias, int32_t target_frames, bool rep_loop_detect,
-                    const FrameCallback & on_frame, std::vector<int32_t> & output);
+                    const FrameCallback & on_frame, std::vector<int32_t> & output, gen_timing * tm);
     bool dev_ok(int rc);
     bool write_attn_dump();
+    static void print_timing(const gen_timing & t);
 
     q3t_dev * dev_ = nullptr;
     tts_transformer_config config_;

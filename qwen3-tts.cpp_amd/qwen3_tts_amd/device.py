@@ -21,7 +21,7 @@ EXPORTS = [
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_set_type", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
     "q3t_dev_attn_row", "q3t_dev_prefill", "q3t_dev_talker_step",
-    "q3t_dev_code_pred", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
+    "q3t_dev_code_pred", "q3t_dev_predict_codes", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
     "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
     "q3t_dev_frames_run", "q3t_dev_frame_codes", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
@@ -75,6 +75,7 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_prefill.argtypes = [vp, f32p, i32, i32, f32p, f32p]
         lib.q3t_dev_talker_step.argtypes = [vp, f32p, i32, f32p, f32p]
         lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
+        lib.q3t_dev_predict_codes.argtypes = [vp, f32p, vp, f32p]
         lib.q3t_dev_text_proj.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_text_proj_noalloc.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_embed_rows.argtypes = [vp, i32, i32, vp, i32, f32p]
@@ -232,6 +233,14 @@ class Device:
         self._check(self.lib.q3t_dev_code_pred(self.h, _p(hidden), int(cb0), ctypes.byref(s), frame, _p(codes), _p(logits)),
                     "code_pred")
         return codes, logits
+
+    def predict_codes(self, hidden, prev_codes=None):
+        """single-pass code predictor: logits [15][cp_vocab]"""
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+        prev = None if prev_codes is None else np.ascontiguousarray(prev_codes, dtype=np.int32)
+        logits = np.empty((self.cfg.n_codebooks - 1, self.cfg.cp_vocab), np.float32)
+        self._check(self.lib.q3t_dev_predict_codes(self.h, _p(hidden), _p(prev), _p(logits)), "predict_codes")
+        return logits
 
     def text_proj(self, tokens):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

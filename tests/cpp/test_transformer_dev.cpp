@@ -1,7 +1,8 @@
 // Drives the drop-in TTSTransformer (qwen3-tts.cpp_amd/csrc/tts_transformer.h)
 // the way the reference's tests/test_transformer.cpp drives its own: load a
 // GGUF, init the KV cache, forward_prefill, then generate() greedy; plus
-// generate_icl, predict_codes_autoregressive and the error paths.  Writes
+// generate_icl, predict_codes_autoregressive, predict_codes and the error
+// paths.  Writes
 // the results as raw binary files that the pytest wrapper compares with the
 // CPU oracle.
 //   usage: test_transformer_dev <model.gguf> <inputs.bin> <out_dir>
@@ -90,6 +91,27 @@ int main(int argc, char ** argv) {
     if (!tr.predict_codes_autoregressive(h.data(), 5, cp, 0.0f, 0)) { std::printf("FAIL code pred\n"); ++fails; }
     dump(out + "/hidden.bin", h.data(), h.size() * 4);
     dump(out + "/cp.bin", cp.data(), cp.size() * 4);
+
+    // the single-pass predictor on the same row, without and with the
+    // previous codes (those of the last generated frame)
+    std::vector<float> pl0, pl1;
+    const int32_t * prev = codes.size() >= 16 ? codes.data() + codes.size() - 15 : nullptr;
+    if (!tr.predict_codes(h.data(), nullptr, pl0) || !prev || !tr.predict_codes(h.data(), prev, pl1)) {
+        std::printf("FAIL predict_codes: %s\n", tr.get_error().c_str());
+        ++fails;
+    } else {
+        std::printf("PASS predict_codes: %zu logits\n", pl0.size());
+        dump(out + "/pc0.bin", pl0.data(), pl0.size() * 4);
+        dump(out + "/pc1.bin", pl1.data(), pl1.size() * 4);
+    }
+    {
+        int32_t bad[15];
+        for (int i = 0; i < 15; ++i) bad[i] = 1;
+        bad[7] = cfg.code_pred_vocab_size;
+        std::vector<float> pl;
+        if (tr.predict_codes(h.data(), bad, pl)) { std::printf("FAIL predict_codes accepted a bad code\n"); ++fails; }
+        else std::printf("PASS predict_codes bad code: %s\n", tr.get_error().c_str());
+    }
 
     // ICL
     if (n_ref > 0) {

@@ -1,6 +1,6 @@
 """The drop-in C++ TTSTransformer (qwen3-tts.cpp_amd/csrc/tts_transformer.h)
-loads a GGUF and runs generate / generate_icl / predict_codes_autoregressive
-on the GPU; its codes must equal the CPU oracle's.  Mirrors the reference's
+loads a GGUF and runs generate / generate_icl / predict_codes_autoregressive /
+predict_codes on the GPU; its codes must equal the CPU oracle's.  Mirrors the reference's
 tests/test_transformer.cpp (load, KV init, generate, frame comparison)."""
 import os
 import struct
@@ -92,9 +92,13 @@ def _facade_check(tmp_path, cfg, w, wtype, layout, max_len, converter=False):
         f.write(struct.pack("<ii", max_len, ref_codes.shape[0]) + ref_codes.tobytes())
     print(f"[gpu] facade {wtype} {layout}", file=sys.stderr, flush=True)
     r = subprocess.run([BIN, str(model), str(tmp_path / "in.bin"), str(tmp_path)], capture_output=True, text=True,
-                       timeout=300)
+                       timeout=300, env=dict(os.environ, QWEN3_TTS_TIMING="1"))
     print(r.stdout, r.stderr, file=sys.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
+    # QWEN3_TTS_TIMING=1: the timing report after every generate / generate_icl
+    # (src/tts_transformer.cpp:3311-3352)
+    assert r.stderr.count("=== Detailed Generation Timing") >= 3, r.stderr
+    assert "frames/s" in r.stderr and "Frame loop" in r.stderr
     codes = np.fromfile(tmp_path / "codes.bin", np.int32).reshape(-1, 16)
     o = orc.Oracle(cfg, w, threads=16)
     co, _ = o.generate(text, spk, max_len=max_len, temperature=0.0)
@@ -120,6 +124,12 @@ def _facade_check(tmp_path, cfg, w, wtype, layout, max_len, converter=False):
     cp = np.fromfile(tmp_path / "cp.bin", np.int32)
     cpo, _ = o.code_pred(hid, 5)
     assert np.array_equal(cp, cpo)
+    # predict_codes, the single-pass predictor, without and with the last
+    # frame's codes 1..15
+    pc0 = np.fromfile(tmp_path / "pc0.bin", np.float32).reshape(15, cfg.cp_vocab)
+    pc1 = np.fromfile(tmp_path / "pc1.bin", np.float32).reshape(15, cfg.cp_vocab)
+    assert np.array_equal(pc0, o.predict_codes(hid))
+    assert np.array_equal(pc1, o.predict_codes(hid, codes[-1, 1:]))
     icl = np.fromfile(tmp_path / "icl.bin", np.int32).reshape(-1, 16)
     pre, trail, pad = icl_rows(o, cfg, text, text, ref_codes, spk)
     io = o.generate_rows(pre, trail, pad, max_len=max_len, temperature=0.0)

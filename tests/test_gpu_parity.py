@@ -13,7 +13,7 @@ import pytest
 import q3t_oracle as orc
 from qwen3_tts_amd import config as qcfg
 from qwen3_tts_amd import driver
-from qwen3_tts_amd.device import Device
+from qwen3_tts_amd.device import Device, DeviceError
 from qwen3_tts_amd.synth import Weights, dequantize_q8_0
 
 pytestmark = pytest.mark.gpu
@@ -206,6 +206,69 @@ def test_code_pred_sampled_matches_oracle(tiny_model):
         cg, _ = dev.code_pred(hid, 5, temperature=0.9, top_k=50, seed=seed, frame=3)
         co, _ = o.code_pred(hid, 5, temperature=0.9, top_k=50, seed=seed, frame=3)
         assert np.array_equal(cg, co)
+
+
+def test_predict_codes_matches_oracle(tiny_model):
+    """q3t_dev_predict_codes, the single-pass code predictor
+    (src/tts_transformer.cpp:2531-2581): the 15 heads' logits bit for bit the
+    oracle's, with and without the 15 previous codes (including the last id
+    of each table); a code outside its table is an error."""
+    cfg, w, dev, o = tiny_model
+    rng = np.random.default_rng(21)
+    for i in range(3):
+        hid = (rng.standard_normal(cfg.hidden_size) * 0.5).astype(np.float32)
+        prev = rng.integers(0, cfg.cp_vocab, cfg.n_codebooks - 1).astype(np.int32)
+        if i == 2:
+            prev[:] = cfg.cp_vocab - 1
+        for p in (None, prev):
+            lg = dev.predict_codes(hid, p)
+            lo = o.predict_codes(hid, p)
+            assert np.array_equal(lg, lo), (i, p is None, np.abs(lg - lo).max())
+    bad = np.zeros(cfg.n_codebooks - 1, np.int32)
+    bad[14] = -1
+    with pytest.raises(DeviceError, match="out of range"):
+        dev.predict_codes(hid, bad)
+
+
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_predict_codes_mtp_layout(wtype):
+    """The single-pass predictor in the 1.7B layout: the input row passes
+    through code_pred.mtp_proj into the narrower code predictor."""
+    cfg = qcfg.tiny_mtp()
+    w, dev, o = make(cfg, wtype, seed=23)
+    try:
+        rng = np.random.default_rng(24)
+        for i in range(2):
+            hid = (rng.standard_normal(cfg.hidden_size) * 0.5).astype(np.float32)
+            prev = rng.integers(0, cfg.cp_vocab, cfg.n_codebooks - 1).astype(np.int32)
+            for p in (None, prev):
+                assert np.array_equal(dev.predict_codes(hid, p), o.predict_codes(hid, p)), (i, p is None)
+    finally:
+        dev.close()
+
+
+def test_predict_codes_between_frame_runs(tiny_model, frame_path):
+    """predict_codes between frames_run calls leaves the frame loop alone:
+    the codes equal the oracle's uninterrupted run, and each interleaved call
+    equals the oracle's."""
+    cfg, w, dev, o = tiny_model
+    text = np.random.default_rng(25).integers(0, cfg.text_vocab - 8, 16).astype(np.int32)
+    hid = (np.random.default_rng(26).standard_normal(cfg.hidden_size) * 0.5).astype(np.float32)
+    co, _ = o.generate(text, None, max_len=20, temperature=0.0)
+    calls = []
+
+    def between(codes, n_cb, frame):
+        if frame % 5 == 4:
+            calls.append((codes[1:].copy(), dev.predict_codes(hid, codes[1:])))
+        return True
+
+    say(f"[gpu] predict_codes between frame runs ({frame_path})")
+    cg = driver.generate(dev, cfg, text, None, max_len=20, temperature=0.0, chunk=5, on_frame=between)
+    check_path(dev, w.wtype, frame_path)
+    assert np.array_equal(cg, co)
+    assert len(calls) == co.shape[0] // 5
+    for prev, lg in calls:
+        assert np.array_equal(lg, o.predict_codes(hid, prev))
 
 
 def test_text_proj_and_embeddings(tiny_model):

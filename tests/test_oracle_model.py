@@ -270,6 +270,42 @@ class NpRef:
                 else None
         return np.array(codes), np.stack(logits)
 
+    # -- the single-pass code predictor (build_code_pred_graph,
+    # src/tts_transformer.cpp:1771-1899), written out as the graph does it:
+    # Q and K with their norms, a softmax over the one score, P times V
+    def predict_codes(self, hidden, prev=None):
+        c = self.cfg
+        nh, nkv, hd = c.n_head, c.n_kv_head, c.head_dim
+        x = np.asarray(hidden, np.float64)
+        if prev is not None:
+            n = c.n_codebooks - 2 if "single_drop_last" in self.mistakes else c.n_codebooks - 1
+            for g in range(n):
+                x = x + self.mat(f"code_pred.codec_embd.{g}.weight")[1][prev[g]]
+        if c.cp_hidden != c.hidden_size:
+            x = self.mm("code_pred.mtp_proj.weight", x) + self.vec("code_pred.mtp_proj.bias")
+        for il in range(c.cp_layers):
+            p = f"code_pred.blk.{il}."
+            h = self.rms(x, self.vec(p + "attn_norm.weight"))
+            q = self.mm(p + "attn_q.weight", h).reshape(nh, hd)
+            k = self.mm(p + "attn_k.weight", h).reshape(nkv, hd)
+            v = self.mm(p + "attn_v.weight", h).reshape(nkv, hd)
+            q = np.stack([self.rms(r, self.vec(p + "attn_q_norm.weight")) for r in q])
+            k = np.stack([self.rms(r, self.vec(p + "attn_k_norm.weight")) for r in k])
+            out = np.empty(nh * hd)
+            for hh in range(nh):
+                g = hh % nkv if "single_gqa_mod" in self.mistakes else hh // (nh // nkv)
+                s = np.array([k[g] @ q[hh] / np.sqrt(hd)])
+                pr = np.exp(s - s.max())
+                pr /= pr.sum()
+                out[hh * hd:(hh + 1) * hd] = pr[0] * v[g]
+            a = self.mm(p + "attn_output.weight", out) + x
+            h = self.rms(a, self.vec(p + "ffn_norm.weight"))
+            f = self.silu(self.mm(p + "ffn_gate.weight", h)) * self.mm(p + "ffn_up.weight", h)
+            x = self.mm(p + "ffn_down.weight", f, widen=True) + a
+        if "single_out_norm" in self.mistakes:
+            x = self.rms(x, self.vec("code_pred.output_norm.weight"))
+        return np.stack([self.mm(f"code_pred.lm_head.{g}.weight", x) for g in range(c.n_codebooks - 1)])
+
     def text_proj(self, tokens):
         te = self.mat("talker.text_embd.weight")[1]
         b1, b2 = self.vec("talker.text_proj.fc1.bias"), self.vec("talker.text_proj.fc2.bias")
@@ -646,3 +682,41 @@ def test_frame_loop_eos_ramp_matches_numpy_generate(wt):
     assert_agrees([rel_err(a, b) for a, b in zip(lgo, lgr)], wt)
     cm, _ = NpRef(cfg, w, {"ramp_slope"}).generate(pre, trail, pad, 24, **kw)
     assert len(cm) < len(co)
+
+
+SINGLE_MISTAKES = ["single_out_norm", "single_gqa_mod", "single_drop_last"]
+
+
+@pytest.mark.parametrize("layout", ["tiny", "tiny_mtp"])
+@pytest.mark.parametrize("wt", ["f16", "q8_0"])
+def test_predict_codes_matches_numpy(wt, layout):
+    """orc_predict_codes (the single-pass code predictor) against the float64
+    graph restatement above, which computes Q, K, their norms and the softmax
+    over the one score that the oracle leaves out; with and without the 15
+    previous codes, in both layouts (tiny_mtp: the MTP projection).  Dropping
+    the last embedding, normalising before the heads or pairing query heads
+    with KV heads by h % n_kv instead of h / group all miss."""
+    cfg = getattr(qcfg, layout)(n_layers=1, cp_layers=1)
+    w = Weights(cfg, wt, seed=37)
+    o = orc.Oracle(cfg, w, threads=4)
+    rng = np.random.default_rng(38)
+    cases = []
+    for i in range(3):
+        hid = (rng.standard_normal(cfg.hidden_size) * 0.5).astype(np.float32)
+        prev = rng.integers(0, cfg.cp_vocab, cfg.n_codebooks - 1).astype(np.int32)
+        cases += [(hid, None), (hid, prev)]
+    got = [o.predict_codes(h, p) for h, p in cases]
+    ref = NpRef(cfg, w)
+    assert_agrees([rel_err(g[j], r[j]) for g, (h, p) in zip(got, cases)
+                   for r in [ref.predict_codes(h, p)] for j in range(cfg.n_codebooks - 1)], wt)
+    for m in SINGLE_MISTAKES:
+        bad = NpRef(cfg, w, mistakes=[m])
+        sel = [(g, h, p) for g, (h, p) in zip(got, cases) if p is not None or m != "single_drop_last"]
+        assert_misses([rel_err(g[j], r[j]) for g, h, p in sel for r in [bad.predict_codes(h, p)]
+                       for j in range(cfg.n_codebooks - 1)])
+    # a code outside the table is an error, not a read past it
+    bad_prev = np.zeros(cfg.n_codebooks - 1, np.int32)
+    bad_prev[4] = cfg.cp_vocab
+    with pytest.raises(RuntimeError):
+        o.predict_codes(cases[0][0], bad_prev)
+    o.close()
