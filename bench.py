@@ -371,13 +371,16 @@ def streams_bench(args, cfg, w):
     frame_ops = 2.0 * B * layer_macs * (cfg.n_layers + 16 * cfg.cp_layers)
     fbytes = frame_bytes(cfg, w.tensors, [p + args.warmup + args.steps // 2 for p in plens])
     q8 = args.weights == "q8_0"
-    # dense peaks: int8 MFMA 5.0 POP/s (Q8_0 layers), f64 MFMA 78.6 TFLOP/s (F16 layers)
-    peak = 5.0e15 if q8 else 78.6e12
+    # F16 layers: the fp16-MFMA GEMMs unless Q3T_MS_EXACT=1 selects the exact f64-MFMA ones
+    f16_exact = os.environ.get("Q3T_MS_EXACT", "") == "1"
+    # dense peaks: int8 MFMA 5.0 POP/s (Q8_0 layers), fp16 MFMA 2.5 PFLOP/s or f64 MFMA 78.6 TFLOP/s (F16 layers)
+    peak = 5.0e15 if q8 else (78.6e12 if f16_exact else 2.5e15)
     out = {
         "metric": f"aggregate codec frames/sec, multi-stream batched decode {args.weights.upper()}", "value": round(fps, 1),
         "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8" if q8 else "f64 (fp16 operands)",
+        "vs_baseline": None,
+        "dtype": "int8" if q8 else ("f64 (fp16 operands)" if f16_exact else "fp16 (fp32 accumulation)"),
         "data": "synthetic (seeded weights, uniform prompt ids, N(0,0.05) history)",
         "config": {"workload": f"{B} streams, 128-token prompts, talker KV lengths uniform in [128, 2048], greedy, "
                                f"{args.weights.upper()} 0.6B shapes, one hipGraph per frame of all streams",

@@ -309,6 +309,12 @@ int  q3t_dev_streams_begin(q3t_dev * dev, const q3t_frame_args * args);
 int  q3t_dev_streams_run(q3t_dev * dev, int32_t n_frames, int32_t * codes_out,
                          int32_t * n_emitted_out, int32_t * eos_out);
 
+/* Copies stream `stream`'s talker logits [codec_vocab] into out: the row the
+ * stream's next codebook-0 sampler reads (after a streams_run, the logits of
+ * its last talker step).  Instrumentation with no counterpart in the
+ * reference: tests compare the decode GEMM forms of F16 layers with it. */
+int  q3t_dev_stream_logits(q3t_dev * dev, int32_t stream, float * out);
+
 /* Blocks until all work queued by this context has finished. */
 int  q3t_dev_sync(q3t_dev * dev);
 /* Times `iters` launches of one kernel class of the frame loop with HIP

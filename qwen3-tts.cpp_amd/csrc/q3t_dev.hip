@@ -112,6 +112,7 @@ struct q3t_dev {
     // (QKV, Wo, gate/up, down): a set's tickets advance by S per launch
     uint64_t * spart[4] = {}; uint32_t * scnt[4] = {}; int32_t * serr = nullptr;
     hipGraphExec_t s_exec = nullptr; hipGraph_t s_graph = nullptr;
+    bool s_hm = false;            // F16 layers: the fp16-MFMA decode GEMMs (else the exact f64-MFMA ones)
     int32_t s_launched = 0, s_max = 0; bool s_ready = false;
     bool stats_streams = false;    // frame statistics describe the multi-stream loop
     std::vector<int32_t> s_emitted;
@@ -2699,32 +2700,46 @@ void gemm_rows(q3t_dev * c, int kind, int site, ms::GemmArgs a) {
 enum HKind { H_QKV = 0, H_WO = 1, H_GATE_UP = 2, H_DOWN = 3 };
 constexpr int kHKB[4] = {1, 2, 1, 3};
 
-template <int NT, int KIND>
+template <int NT, int KIND, bool HM>
 const void * hgemm_kernel() {
-    if (KIND == H_QKV) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_NORM, ms::OUT_F32, kHKB[H_QKV]>;
-    if (KIND == H_WO) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_ROUND, ms::OUT_RESID, kHKB[H_WO]>;
+    if (KIND == H_QKV) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_NORM, ms::OUT_F32, kHKB[H_QKV], HM>;
+    if (KIND == H_WO) return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_ROUND, ms::OUT_RESID, kHKB[H_WO], HM>;
     if (KIND == H_GATE_UP)
-        return (const void *) ms::k_gemm_h<NT, 1, true, ms::IN_NORM, ms::OUT_SWIGLU_F32, kHKB[H_GATE_UP]>;
-    return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_WIDE, ms::OUT_RESID, kHKB[H_DOWN]>;
+        return (const void *) ms::k_gemm_h<NT, 1, true, ms::IN_NORM, ms::OUT_SWIGLU_F32, kHKB[H_GATE_UP], HM>;
+    return (const void *) ms::k_gemm_h<NT, 1, false, ms::IN_WIDE, ms::OUT_RESID, kHKB[H_DOWN], HM>;
 }
 
-template <int KIND>
+template <int KIND, bool HM>
 const void * hgemm_kernel_nt(int nt) {
     switch (nt) {
-        case 1: return hgemm_kernel<1, KIND>();
-        case 2: return hgemm_kernel<2, KIND>();
-        case 3: return hgemm_kernel<3, KIND>();
-        default: return hgemm_kernel<4, KIND>();
+        case 1: return hgemm_kernel<1, KIND, HM>();
+        case 2: return hgemm_kernel<2, KIND, HM>();
+        case 3: return hgemm_kernel<3, KIND, HM>();
+        default: return hgemm_kernel<4, KIND, HM>();
     }
 }
 
-const void * hgemm_fn(int kind, int nt) {
+template <bool HM>
+const void * hgemm_fn_form(int kind, int nt) {
     switch (kind) {
-        case H_QKV: return hgemm_kernel_nt<H_QKV>(nt);
-        case H_WO: return hgemm_kernel_nt<H_WO>(nt);
-        case H_GATE_UP: return hgemm_kernel_nt<H_GATE_UP>(nt);
-        default: return hgemm_kernel_nt<H_DOWN>(nt);
+        case H_QKV: return hgemm_kernel_nt<H_QKV, HM>(nt);
+        case H_WO: return hgemm_kernel_nt<H_WO, HM>(nt);
+        case H_GATE_UP: return hgemm_kernel_nt<H_GATE_UP, HM>(nt);
+        default: return hgemm_kernel_nt<H_DOWN, HM>(nt);
     }
+}
+
+// hm: the fp16-MFMA form (fp32 accumulation), else the exact f64-MFMA form
+const void * hgemm_fn(int kind, int nt, bool hm) {
+    return hm ? hgemm_fn_form<true>(kind, nt) : hgemm_fn_form<false>(kind, nt);
+}
+
+// Q3T_MS_EXACT=1: the multi-stream decode of F16 layers on the exact f64-MFMA
+// GEMMs, whose codes equal each stream's batch-1 run; by default the
+// fp16-MFMA GEMMs with fp32 accumulation (read at q3t_dev_streams_begin).
+bool ms_exact() {
+    const char * e = std::getenv("Q3T_MS_EXACT");
+    return e && e[0] == '1';
 }
 
 // K splits of an F16 contraction of nb 32-element chunks: the largest S <= 8
@@ -2745,7 +2760,7 @@ void hgemm_rows(q3t_dev * c, int kind, int site, ms::GemmArgs a) {
     const int S = hgemm_splits(kind, a.K / kQK);
     a.part = c->spart[site]; a.cnt = c->scnt[site]; a.err = c->serr;
     void * args[] = {(void *) &a};
-    (void) hipLaunchKernel(hgemm_fn(kind, nt), dim3(a.N / ms::kRows, S), dim3(ms::kThreads), args,
+    (void) hipLaunchKernel(hgemm_fn(kind, nt, c->s_hm), dim3(a.N / ms::kRows, S), dim3(ms::kThreads), args,
                            ms::gemm_h_lds_bytes(nt, 1, kind == H_GATE_UP), c->stream);
 }
 
@@ -3200,6 +3215,10 @@ int q3t_dev_streams_begin(q3t_dev * c, const q3t_frame_args * args) {
     HIP_OK(hipMemcpyAsync(c->sntrail, ntr.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice, c->stream));
     HIP_OK(hipMemsetAsync(c->sseen, 0, (size_t) B * g.codec_vocab, c->stream));
     if (sync(c)) return -1;
+    // the F16 GEMM form is fixed in the captured graph: recapture on a change
+    const bool hm = !ms_exact();
+    if (c->s_exec && hm != c->s_hm) drop_stream_graph(c);
+    c->s_hm = hm;
     if (!c->s_exec) {
         HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         streams_frame_seq(c);
@@ -3262,6 +3281,15 @@ int q3t_dev_streams_run(q3t_dev * c, int32_t n_frames, int32_t * codes_out, int3
         c->s_emitted[b] = st[b].n_emitted;
     }
     return 0;
+}
+
+int q3t_dev_stream_logits(q3t_dev * c, int32_t stream, float * out) {
+    if (!c || !out) return -1;
+    HIP_OK(hipSetDevice(c->device));
+    if (!c->slogits || stream < 0 || stream >= c->nb) return fail(c, "stream_logits: no such stream");
+    const size_t n = (size_t) c->cfg.codec_vocab;
+    HIP_OK(hipMemcpyAsync(out, c->slogits + (size_t) stream * n, n * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
 }
 
 int q3t_dev_frames_stats(q3t_dev * c, double * gpu_us_out, int64_t * frames_out, int32_t * path_out) {

@@ -34,6 +34,8 @@ namespace ms {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef double v4d __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kRows = 16;             // weight rows per MFMA tile (M)
 constexpr int kWaves = 4;             // waves per workgroup, each a part of the K slice
@@ -424,7 +426,16 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
 // OUT_F32, OUT_RESID (+ per-tile sums of squares of the output rows for the
 // next RMSNorm), OUT_SWIGLU_F32 (silu(gate) * up, fp32 rows).
 // Requires N % (16 MT) == 0, (K/32) % (4 S) == 0, K/32/S/4 <= KB, n <= 16 NT.
-template <int NT, int MT, bool DUAL, int IN, int OUT, int KB>
+//
+// HM: the fast form on v_mfma_f32_16x16x32_f16, fp32 accumulation as ggml's
+// F16 mul_mat accumulates: one MFMA per 32-element chunk with the same lane
+// operands (A[m = l%16][k = 8(l/16)..+7] activation row 16j + l%16, B[k =
+// 8(l/16)..+7][n = l%16] weight row 16m + l%16); D element r of lane l is
+// activation row 16j + 4(l/16) + r.  The widened ffn_down input (fp32) goes
+// in as two fp16 planes, hi = fp16(x) and lo = fp16(x - hi), so the product
+// keeps about 22 bits of x.  The wave tree and split-K exchange add the fp32
+// chunk sums in fp64 as before.
+template <int NT, int MT, bool DUAL, int IN, int OUT, int KB, bool HM = false>
 __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
     constexpr int NW = DUAL ? 2 : 1;
     constexpr int NA = NW * MT * NT;                  // 16 x 16 accumulators per lane
@@ -491,9 +502,12 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
         }
     }
 
-    v4d acc[NA];
+    v4d acc[HM ? 1 : NA];
+    v4f accf[HM ? NA : 1];
 #pragma unroll
-    for (int v = 0; v < NA; ++v) acc[v] = v4d{0.0, 0.0, 0.0, 0.0};
+    for (int v = 0; v < (HM ? 1 : NA); ++v) acc[v] = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int v = 0; v < (HM ? NA : 1); ++v) accf[v] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
         if (i >= bpw) continue;
@@ -514,6 +528,30 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) av[j][e] = IN == IN_WIDE ? xs8[e] : round_f16(xs8[e]);
             }
+        }
+        if (HM) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                h8 ah, al;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    ah[e] = (_Float16) av[j][e];
+                    al[e] = IN == IN_WIDE ? (_Float16) (av[j][e] - (float) ah[e]) : (_Float16) 0.0f;
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const h8 w8 = __builtin_bit_cast(h8, wa[m][i]);
+                    v4f & c0 = accf[(0 * MT + m) * NT + j];
+                    c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, w8, c0, 0, 0, 0);
+                    if (IN == IN_WIDE) c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, w8, c0, 0, 0, 0);
+                    if (DUAL) {
+                        v4f & c1 = accf[(1 * MT + m) * NT + j];
+                        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, __builtin_bit_cast(h8, wb[DUAL ? m : 0][i]),
+                                                                    c1, 0, 0, 0);
+                    }
+                }
+            }
+            continue;
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -546,7 +584,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
 #pragma unroll
     for (int v = 0; v < NA; ++v)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) fl[4 * v + r] = acc[v][r];
+        for (int r = 0; r < 4; ++r) fl[4 * v + r] = HM ? (double) accf[HM ? v : 0][r] : acc[HM ? 0 : v][r];
 
     // fixed tree over the 4 waves: (0 + 2, 1 + 3), then (0 + 1)
     if (wave >= 2) {
@@ -573,7 +611,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
     for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int tok = 16 * j + 4 * r + lk;
+            const int tok = HM ? 16 * j + 4 * lk + r : 16 * j + 4 * r + lk;
             const bool ok = tok < a.n;
             double sq = 0.0;   // this lane's square of row 16m + lm of token tok, summed over the tile's lanes below
 #pragma unroll

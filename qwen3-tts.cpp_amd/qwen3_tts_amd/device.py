@@ -21,7 +21,7 @@ EXPORTS = [
     "q3t_dev_download_tensor", "q3t_dev_dequantize", "q3t_dev_kv_reserve", "q3t_dev_kv_clear",
     "q3t_dev_kv_capacity", "q3t_dev_kv_set_type", "q3t_dev_kv_write", "q3t_dev_set_attn_capture", "q3t_dev_attn_row_count",
     "q3t_dev_attn_row", "q3t_dev_prefill", "q3t_dev_talker_step",
-    "q3t_dev_code_pred", "q3t_dev_predict_codes", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
+    "q3t_dev_code_pred", "q3t_dev_predict_codes", "q3t_dev_stream_logits", "q3t_dev_text_proj", "q3t_dev_text_proj_noalloc", "q3t_dev_embed_rows",
     "q3t_dev_build_prefill",
     "q3t_dev_build_prefill_icl", "q3t_dev_frames_begin",
     "q3t_dev_frames_run", "q3t_dev_frame_codes", "q3t_dev_frames_stats", "q3t_dev_streams_reserve", "q3t_dev_stream_prefill",
@@ -76,6 +76,7 @@ def load_library(path=LIB_PATH):
         lib.q3t_dev_talker_step.argtypes = [vp, f32p, i32, f32p, f32p]
         lib.q3t_dev_code_pred.argtypes = [vp, f32p, i32, ctypes.POINTER(CSampling), u32, vp, f32p]
         lib.q3t_dev_predict_codes.argtypes = [vp, f32p, vp, f32p]
+        lib.q3t_dev_stream_logits.argtypes = [vp, i32, f32p]
         lib.q3t_dev_text_proj.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_text_proj_noalloc.argtypes = [vp, vp, i32, f32p]
         lib.q3t_dev_embed_rows.argtypes = [vp, i32, i32, vp, i32, f32p]
@@ -366,6 +367,12 @@ class Device:
         eos = np.zeros(B, np.int32)
         self._check(self.lib.q3t_dev_streams_run(self.h, n_frames, _p(out), _p(n), _p(eos)), "streams_run")
         return [out[b, : n[b]].copy() for b in range(B)], [bool(e) for e in eos]
+
+    def stream_logits(self, stream):
+        """stream's talker logits [codec_vocab]: the row its next codebook-0 sampler reads"""
+        out = np.empty(self.cfg.codec_vocab, np.float32)
+        self._check(self.lib.q3t_dev_stream_logits(self.h, int(stream), _p(out)), "stream_logits")
+        return out
 
     def frames_stats(self):
         """(GPU microseconds of frame launches, frame launches, path) since

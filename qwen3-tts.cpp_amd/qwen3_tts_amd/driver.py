@@ -134,7 +134,7 @@ def stream_audio(dev, voc, cfg, text, speaker=None, max_len=64, chunk_frames=25,
     return codes, out, state["windows"]
 
 
-def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None):
+def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None, logits=None):
     """Batched form of generate() over independent utterances.
 
     `streams` is a list of dicts, one per utterance, each with `prefill_rows`
@@ -143,6 +143,8 @@ def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None):
     eos_bias, target_frames, seed.  Every stream's codes equal what
     generate() returns for it alone; all streams advance together, one
     device graph launch per frame.  Returns a list of [n_frames][16] arrays.
+    `logits`, a list, receives after every streams_run call the streams'
+    talker logits [n_streams][codec_vocab].
     """
     if not streams:
         return []
@@ -164,6 +166,8 @@ def generate_streams(dev, cfg, streams, chunk=32, n_ctx=None):
     while produced < max_len and any(live):
         n = min(chunk, max_len - produced)
         codes, eos = dev.streams_run(n)
+        if logits is not None:
+            logits.append(np.stack([dev.stream_logits(b) for b in range(len(streams))]))
         for b in range(len(streams)):
             if codes[b].shape[0]:
                 out[b].append(codes[b])

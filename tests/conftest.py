@@ -12,6 +12,9 @@ sys.path.insert(0, ROOT)
 # run F16 prefills on the exact f64-MFMA GEMMs; the tests of the default fast
 # form (fp16 MFMA, fp32 accumulation; a tolerance) switch it back on.
 os.environ.setdefault("Q3T_PF_EXACT", "1")
+# Likewise the multi-stream decode of F16 layers runs on the exact f64-MFMA
+# GEMMs; the test of its default fp16-MFMA form switches that back.
+os.environ.setdefault("Q3T_MS_EXACT", "1")
 
 
 def pytest_configure(config):

@@ -195,6 +195,49 @@ def test_streams_full_f16_4_streams():
 
 
 @pytest.mark.slow
+def test_streams_full_f16_fast_gemm_tolerance(monkeypatch):
+    """F16 layers on the fp16-MFMA decode GEMMs (fp32 accumulation, as
+    ggml's F16 mul_mat; the default form, Q3T_MS_EXACT=1 selects the exact
+    f64-MFMA one) at the 0.6B shapes: four greedy streams, frame by frame.
+    While a stream's codes agree with the exact form's, its talker logits
+    after every frame stay within 1e-2 of the exact form's (largest
+    difference over the largest |logit|); the first frame whose codes differ
+    is reported, not asserted."""
+    cfg = qcfg.full_06b()
+    say("[gpu] streams full 0.6B f16 fast form: synth + upload")
+    w = Weights(cfg, "f16", seed=5, norm_mode="one")
+    dev = Device(cfg)
+    dev.upload_weights(w)
+    try:
+        streams = []
+        for i, n in enumerate([24, 9, 50, 13]):
+            text, spk = _prompt(cfg, 40 + i, n, True)
+            streams.append(dict(prefill_rows=driver.build_prefill(dev, cfg, text, spk), max_len=16, temperature=0.0,
+                                top_k=0))
+        runs = {}
+        for form in ("exact", "fast"):
+            monkeypatch.setenv("Q3T_MS_EXACT", "1" if form == "exact" else "0")
+            lg = []
+            codes = driver.generate_streams(dev, cfg, streams, chunk=1, logits=lg)
+            runs[form] = (codes, lg)
+        worst = 0.0
+        for b in range(len(streams)):
+            ce, cf = runs["exact"][0][b], runs["fast"][0][b]
+            n = min(len(ce), len(cf))
+            diverge = next((f for f in range(n) if not np.array_equal(ce[f], cf[f])), None)
+            last = n if diverge is None else diverge
+            for f in range(last):
+                le, lf = runs["exact"][1][f][b], runs["fast"][1][f][b]
+                rel = float(np.abs(le - lf).max() / np.abs(le).max())
+                worst = max(worst, rel)
+                assert rel <= 1e-2, (b, f, rel)
+            say(f"[gpu] stream {b}: {n} frames, first frame whose codes differ: {diverge}")
+        say(f"[gpu] fast form: largest logit difference {worst:.2e} of the largest |logit|")
+    finally:
+        dev.close()
+
+
+@pytest.mark.slow
 def test_streams_full_q8_4_streams():
     """0.6B shapes, Q8_0: four streams with ragged prompts, greedy, 24 frames."""
     cfg = qcfg.full_06b()
