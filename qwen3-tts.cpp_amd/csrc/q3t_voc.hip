@@ -308,7 +308,12 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
         HIP_OK(hipGetLastError());
         return 0;
     }
-#define Q3T_VOC_GEMM(wm, wn) hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a)
+    // a residual input takes the form that prefetches it in the epilogue
+#define Q3T_VOC_GEMM(wm, wn)                                                                    \
+    do {                                                                                        \
+        if (res) hipLaunchKernelGGL((k_conv_gemm<wm, wn, 1, true>), grid, dim3(kGemmT), 0, v->stream, a); \
+        else hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a);    \
+    } while (0)
 #define Q3T_VOC_GEMM_WN(wm)                   \
     switch (WN) {                             \
     case 4: Q3T_VOC_GEMM(wm, 4); break;       \

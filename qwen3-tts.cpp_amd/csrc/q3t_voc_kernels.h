@@ -81,7 +81,11 @@ struct GemmTile {
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chunk ^ (row & 3)) << 3); }
 
-template <int WM, int WN, int KS = 1>
+// RP (A.res set): the epilogue loads every residual value of the tile before
+// it uses any, so their reads overlap; the registers this takes lower the
+// occupancy, which the convolutions without a residual (whose K loops need
+// it) keep.
+template <int WM, int WN, int KS = 1, bool RP = false>
 __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     using G = GemmTile<WM, WN, KS>;
     __shared__ __align__(16) char smem[G::LDS];
@@ -181,8 +185,23 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     // ([row][channel]), then 64 lanes walk it channel-fastest (coalesced row
     // stores).  LDS is in order within a wave, so no barrier is needed.
     constexpr int TC = WM * 16, TS = G::TS;
+    constexpr int IT = 16 * TC / 64;                 // elements per lane of one 16-row tile
     float * my = (float *) smem + wave * 16 * TS;
     const int ch0 = cb0 + wc * WM * 16, t0 = tb0 + wt * WN * 16;
+    // RP: the residual values of every tile, loaded before any is used so
+    // their global reads overlap instead of forming one dependent chain
+    float rv[RP ? WN : 1][RP ? IT : 1];
+    if (RP) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int k = 0; k < IT; ++k) {
+                const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
+                const int t = t0 + j * 16 + tl, n = ch0 + cl;
+                rv[RP ? j : 0][RP ? k : 0] =
+                    t < A.M && n < A.N ? A.res[((size_t) t * A.ostride + phase) * A.rs + n] : 0.0f;
+            }
+    }
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
 #pragma unroll
@@ -201,6 +220,26 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
                 if (t >= A.M || n >= (A.N >> 1)) continue;
                 const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
                 A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
+            }
+        } else if (RP) {
+            // unrolled, reading the prefetched residuals
+#pragma unroll
+            for (int k = 0; k < IT; ++k) {
+                const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
+                const int t = tbase + tl, n = ch0 + cl;
+                if (t >= A.M || n >= A.N) continue;
+                const size_t row = (size_t) t * A.ostride + phase;
+                float v = my[tl * TS + cl];
+                if (A.bias) v = v + A.bias[n];
+                if (A.scale) v = v * A.scale[n];
+                v = rv[RP ? j : 0][RP ? k : 0] + v;
+                if (A.yf) A.yf[row * A.yfs + n] = v;
+                if (A.yh) {
+                    float h = v;
+                    if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
+                    else if (A.act == ACT_GELU) h = gelu_tanh(v);
+                    A.yh[row * A.yhs + n] = f2h(h);
+                }
             }
         } else {
             for (int idx = lane; idx < 16 * TC; idx += 64) {
