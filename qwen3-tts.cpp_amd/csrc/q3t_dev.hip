@@ -766,7 +766,7 @@ __global__ __launch_bounds__(256) void k_copy16(const int4 * __restrict__ src, i
 // small test shapes; 5 / 8 = the 0.6B shapes on the XCD-parallel layer
 // program, Q8_0 / F16; 6 = the 1.7B layout (2048, 1024, 2048, 6144, 3072)
 // with code_pred.mtp_proj, Q8_0; 7 = its small test form (512, 256, 512, 512,
-// 512).
+// 512); 9 / 10 = the same two with F16 layers.
 bool fk_xcd(int variant) { return variant == 5 || variant == 8; }
 const void * fk_kernel(int variant) {
     switch (variant) {
@@ -777,6 +777,8 @@ const void * fk_kernel(int variant) {
         case 6: return (const void *) fk::k_frame<2048, 1024, 2048, 6144, 3072, W_Q8, false>;
         case 7: return (const void *) fk::k_frame<512, 256, 512, 512, 512, W_Q8, false>;
         case 8: return (const void *) fk::k_frame<1024, 1024, 2048, 3072, 3072, W_F16, true>;
+        case 9: return (const void *) fk::k_frame<2048, 1024, 2048, 6144, 3072, W_F16, false>;
+        case 10: return (const void *) fk::k_frame<512, 256, 512, 512, 512, W_F16, false>;
         default: return (const void *) fk::k_frame<256, 256, 512, 512, 512, W_F16, false>;
     }
 }
@@ -869,43 +871,38 @@ int fk_prepare(q3t_dev * c) {
         g.head_dim != 128 || g.cp_layers > fk::kCpLayers || g.codec_vocab > 3072 ||
         g.cp_vocab > 3072 || g.codec_vocab < 1024 || g.n_codebooks != 16 || qkvd > fk::kHS)
         return 0;
-    // the 1.7B layout runs Q8_0 models only (an F16 one takes the multi-kernel frame)
-    if (mtp && (c->mtp_w.type != Q3T_TYPE_Q8_0 || !c->mtp_b.data)) return 0;
-    // every layer matrix Q8_0, or every one F16
+    // every layer matrix Q8_0, or every one F16 (and code_pred.mtp_proj of the
+    // same type in the 1.7B layout)
     const int lt = c->talker[0].qkv.type;
     if (lt != Q3T_TYPE_Q8_0 && lt != Q3T_TYPE_F16) return 0;
+    if (mtp && (c->mtp_w.type != lt || !c->mtp_b.data)) return 0;
     for (int i = 0; i < g.n_layers + g.cp_layers; ++i) {
         const LayerDev & L = i < g.n_layers ? c->talker[i] : c->cp[i - g.n_layers];
         if (L.qkv.type != lt || L.wo.type != lt || L.wg.type != lt || L.wu.type != lt || L.wd.type != lt) return 0;
     }
-    if (lt == Q3T_TYPE_F16) {
-        if (mtp) return 0;
-        variant += 2;
-    }
+    if (lt == Q3T_TYPE_F16) variant = mtp ? variant + 3 : variant + 2;
     // one workgroup per CU (the LDS footprint allows no more), all co-resident
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fk_kernel(variant), fk::kT, 0));
     const int grid = std::min(256, per_cu * c->n_cu);
     if (grid < 1) return 0;
     const int nw = grid * fk::kW;
-    // row groups per wave: 2, or 3 for a gate/up whose rows need it on 1024
-    // waves (the kernel's Q8Regs<.., NGU>)
-    auto fits = [&](int rows, int K, int slots, int ng = 2) {
+    // row groups per wave: what the phase needs on 1024 waves, as the kernel's
+    // register sets hold (fk::ngroups); a smaller grid must cover the rows with
+    // that many
+    auto fits = [&](int rows, int K, int slots) {
         if (slots <= 0) return false;
         const int rpw = 64 / ((K / kQK) / slots);
+        const int ng = std::max(1, (rows / rpw + 1023) / 1024);
         return rows % rpw == 0 && rows / rpw <= ng * nw;
-    };
-    auto ngu = [&](int ffn, int K, int slots) {
-        const int rpw = 64 / ((K / kQK) / slots);
-        return (ffn / rpw + 1023) / 1024 > 2 ? 3 : 2;
     };
     auto head_fits = [&](int rows, int K) {
         const int lpr = std::min(K / kQK, 32);
         return (K / kQK) % lpr == 0 && (K / kQK) / lpr <= 2 && rows % (64 / lpr) == 0 && rows / (64 / lpr) <= 2 * nw;
     };
-    if (!fits(qkvd, g.hidden_size, sq) || !fits(g.ffn_size, g.hidden_size, sq, ngu(g.ffn_size, g.hidden_size, sq)) ||
+    if (!fits(qkvd, g.hidden_size, sq) || !fits(g.ffn_size, g.hidden_size, sq) ||
         !fits(g.hidden_size, qd, so) || !fits(g.hidden_size, g.ffn_size, sd) || !head_fits(g.codec_vocab, g.hidden_size) ||
-        !fits(qkvd, dc, sqc) || !fits(g.cp_ffn, dc, sqc, ngu(g.cp_ffn, dc, sqc)) || !fits(dc, qd, so) ||
+        !fits(qkvd, dc, sqc) || !fits(g.cp_ffn, dc, sqc) || !fits(dc, qd, so) ||
         !fits(dc, g.cp_ffn, sdc) || !head_fits(g.cp_vocab, dc) || (mtp && !fits(dc, g.hidden_size, sq)) ||
         g.n_kv_head > grid)
         return 0;

@@ -103,6 +103,14 @@ struct Geo {
                   "unsupported GEMV width");
 };
 
+// Row groups per wave that a GEMV phase of `rows` rows of input width K needs
+// on the 1,024 waves of a 256-workgroup launch; its register sets hold that
+// many (the host admits a launch only when its waves cover the rows with it).
+template <int K>
+constexpr int ngroups(int rows) {
+    return (rows / Geo<K>::RPW + 1023) / 1024 < 1 ? 1 : (rows / Geo<K>::RPW + 1023) / 1024;
+}
+
 // Thread t's share of NT input rows of width K: groups g = t + c * kT of 4
 // consecutive elements (4g .. 4g+3); 8 consecutive threads cover one Q8_0
 // block.  Groups with g >= K/4 belong to whole idle waves (K/4 % 64 == 0).
@@ -565,24 +573,24 @@ __device__ __forceinline__ void q8_compute(const Q8Regs<K, DUAL, NG> & R, const 
 // (or kept fp32 for ffn_down, which the reference widens to F32) and every
 // product, exact in fp64, is accumulated in fp64.  Same row geometry as the
 // Q8_0 GEMV: a lane holds whole 32-element blocks, 64 bytes each.
-template <int K, bool DUAL>
+template <int K, bool DUAL, int NG = 2>
 struct F16Regs {
     static constexpr int S = Geo<K>::SLOTS;
-    int4 w[2][S][4], u[DUAL ? 2 : 1][DUAL ? S : 1][4];
-    uint64_t res[2][2];
+    int4 w[NG][S][4], u[DUAL ? NG : 1][DUAL ? S : 1][4];
+    uint64_t res[NG][2];
     int ng;
 };
 
-template <int K, bool DUAL, bool NTL>
-__device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_t * W, const uint16_t * U, int rows,
-                                             int rot) {
+template <int K, bool DUAL, bool NTL, int NG = 2>
+__device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL, NG> & R, const uint16_t * W, const uint16_t * U,
+                                             int rows, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int groups = rows / G::RPW;
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
     R.ng = 0;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         const int g = gw + gi * nw;
         if (g >= groups) break;
         R.ng = gi + 1;
@@ -602,14 +610,14 @@ __device__ __forceinline__ void f16_prefetch(F16Regs<K, DUAL> & R, const uint16_
     }
 }
 
-template <int NT, int K, bool DUAL>
-__device__ __forceinline__ void res_prefetch16(F16Regs<K, DUAL> & R, const uint64_t * res, int rot) {
+template <int NT, int K, bool DUAL, int NG = 2>
+__device__ __forceinline__ void res_prefetch16(F16Regs<K, DUAL, NG> & R, const uint64_t * res, int rot) {
     using G = Geo<K>;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
     if (lir != 0) return;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         if (gi >= R.ng) break;
         const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
@@ -619,10 +627,32 @@ __device__ __forceinline__ void res_prefetch16(F16Regs<K, DUAL> & R, const uint6
 
 // Thread-distributed rows into the F16 GEMV input layout: rounded to fp16
 // (WIDE = false) or kept fp32 (WIDE = true).
+// The F16 GEMV input rows in LDS, packed by their width K (so one token of
+// the 1.7B talker's 6144-wide ffn_down input fits where two 3072-wide rows
+// do): fp16 halves 8c..8c+7 of block b of token t at hf_at<K>(t, c, b), the
+// widened form's fp32 values 4c..4c+3 at xw_at<K>(t, c, b).
+template <int K>
+__device__ __forceinline__ uint16_t * hf_at(Lds & L, int t, int c, int b) {
+    return &L.hf[0][0][0] + ((t * 4 + c) * (K / kQK) + b) * 8;
+}
+template <int K>
+__device__ __forceinline__ const uint16_t * hf_at(const Lds & L, int t, int c, int b) {
+    return &L.hf[0][0][0] + ((t * 4 + c) * (K / kQK) + b) * 8;
+}
+template <int K>
+__device__ __forceinline__ float * xw_at(Lds & L, int t, int c, int b) {
+    return &L.xw[0][0][0] + ((t * 8 + c) * (K / kQK) + b) * 4;
+}
+template <int K>
+__device__ __forceinline__ const float * xw_at(const Lds & L, int t, int c, int b) {
+    return &L.xw[0][0][0] + ((t * 8 + c) * (K / kQK) + b) * 4;
+}
+
 template <int NT, int K, bool WIDE>
 __device__ __forceinline__ void f16_rows(const RowsT<NT, K> & v, Lds & L) {
     constexpr int CHG = kChg<K>, G4 = K / 4;
     static_assert(K % kQK == 0, "whole 32-element blocks");
+    static_assert(NT * K <= 2 * kMaxBlk * kQK, "F16 GEMV input rows exceed their LDS buffer");
 #pragma unroll
     for (int c = 0; c < CHG; ++c) {
         const int g = (int) threadIdx.x + kT * c;
@@ -631,10 +661,10 @@ __device__ __forceinline__ void f16_rows(const RowsT<NT, K> & v, Lds & L) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if (WIDE) {
-                *(float4 *) &L.xw[t][g & 7][b * 4] = make_float4(v[t][c][0], v[t][c][1], v[t][c][2], v[t][c][3]);
+                *(float4 *) xw_at<K>(L, t, g & 7, b) = make_float4(v[t][c][0], v[t][c][1], v[t][c][2], v[t][c][3]);
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) L.hf[t][(e32 + e) >> 3][b * 8 + ((e32 + e) & 7)] = f2h(v[t][c][e]);
+                for (int e = 0; e < 4; ++e) hf_at<K>(L, t, (e32 + e) >> 3, b)[(e32 + e) & 7] = f2h(v[t][c][e]);
             }
         }
     }
@@ -654,17 +684,17 @@ __device__ __forceinline__ _Float16 h8h(const int4 & v, int j) {
 }
 
 
-template <int NT, int K, bool DUAL, bool WIDE>
-__device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Lds & L, int epi, const uint64_t * res,
+template <int NT, int K, bool DUAL, bool WIDE, int NG = 2>
+__device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL, NG> & R, const Lds & L, int epi, const uint64_t * res,
                                             uint32_t res_tag, uint64_t * out, uint32_t out_tag, int rot, bool & dead,
-                                            int32_t * err) {
+                                            int32_t * err, const float * bias = nullptr) {
     using G = Geo<K>;
     if (R.ng == 0) return;
     const int lane = threadIdx.x & 63, lir = lane & (G::LPR - 1), rsub = lane / G::LPR;
     const int gw = rot_wave(rot), nw = gridDim.x * kW;
-    double acc[2][NT], acc2[2][NT];
+    double acc[NG][NT], acc2[NG][NT];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
+    for (int gi = 0; gi < NG; ++gi)
 #pragma unroll
         for (int t = 0; t < NT; ++t) { acc[gi][t] = 0.0; acc2[gi][t] = 0.0; }
 #pragma unroll
@@ -679,17 +709,17 @@ __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Ld
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 if (WIDE) {
-                    const float4 x0 = *(const float4 *) &L.xw[t][2 * c][b * 4];
-                    const float4 x1 = *(const float4 *) &L.xw[t][2 * c + 1][b * 4];
+                    const float4 x0 = *(const float4 *) xw_at<K>(L, t, 2 * c, b);
+                    const float4 x1 = *(const float4 *) xw_at<K>(L, t, 2 * c + 1, b);
                     float * xr = xa[WIDE ? t : 0];
                     xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w;
                     xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
                 } else {
-                    xp[t] = *(const int4 *) &L.hf[t][c][b * 8];
+                    xp[t] = *(const int4 *) hf_at<K>(L, t, c, b);
                 }
             }
 #pragma unroll
-            for (int gi = 0; gi < 2; ++gi) {
+            for (int gi = 0; gi < NG; ++gi) {
                 if (gi >= R.ng) break;
                 // The packed weights pass through an empty asm here, so their
                 // conversions are not hoisted ahead of the input barrier.
@@ -729,7 +759,7 @@ __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Ld
         }
     }
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
         if (gi >= R.ng) break;
         const int r = (gw + gi * nw) * G::RPW + rsub;
 #pragma unroll
@@ -745,6 +775,8 @@ __device__ __forceinline__ void f16_compute(const F16Regs<K, DUAL> & R, const Ld
                                                           : twait(res + (size_t) t * kHS + r, res_tag, dead, err));
             } else if (epi == EPI_SWIGLU) {
                 o = silu_q3t(v) * (float) a2;
+            } else if (epi == EPI_BIAS) {
+                o = v + gld(bias + r);
             } else {
                 o = v;
             }
@@ -1658,11 +1690,12 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     if (two_phase) att2_prefetch(A, layer, pos0, kc2);
     // QKV (RMSNorm'd input)
     const int p_qkv = p++;
+    constexpr int NGQ = ngroups<D>(QKVD);
     if (wg_has_rows<D>(QKVD, 0)) {
-        Q8Regs<D, false> R;
-        F16Regs<D, false> F;
-        if constexpr (WT == W_Q8) q8_prefetch<D, false, TK>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
-        else f16_prefetch<D, false, TK>(F, (const uint16_t *) W.qkv, nullptr, QKVD, 0);
+        Q8Regs<D, false, NGQ> R;
+        F16Regs<D, false, NGQ> F;
+        if constexpr (WT == W_Q8) q8_prefetch<D, false, TK, NGQ>(R, W.qkv, W.qkv_d, nullptr, nullptr, QKVD, 0);
+        else f16_prefetch<D, false, TK, NGQ>(F, (const uint16_t *) W.qkv, nullptr, QKVD, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.attn_norm, nw);
         RowsT<NT, D> v;
@@ -1674,10 +1707,11 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
         rms_rows<NT, D>(v, nw, A.eps, L);
         if constexpr (WT == W_Q8) {
             quant_rows<NT, D>(v, L);
-            q8_compute<NT, D, false>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead, A.err);
+            q8_compute<NT, D, false, NGQ>(R, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0, dead,
+                                          A.err);
         } else {
             f16_rows<NT, D, false>(v, L);
-            f16_compute<NT, D, false, false>(F, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0,
+            f16_compute<NT, D, false, false, NGQ>(F, L, EPI_STORE, nullptr, 0, ar + (size_t) p_qkv * kSlot, tb | p_qkv, 0,
                                              dead, A.err);
         }
     }
@@ -1720,36 +1754,37 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     }
     // Wo + residual (the block input)
     const int p_wo = p++;
+    constexpr int NGO = ngroups<QD>(D);
     if (wg_has_rows<QD>(D, rot)) {
         RowsT<NT, QD> v;
         if constexpr (WT == W_Q8) {
-            Q8Regs<QD, false> R;
-            q8_prefetch<QD, false, TK>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
-            res_prefetch<NT, QD, false>(R, ar + (size_t) p_in * kSlot, rot);
+            Q8Regs<QD, false, NGO> R;
+            q8_prefetch<QD, false, TK, NGO>(R, W.wo, W.wo_d, nullptr, nullptr, D, rot);
+            res_prefetch<NT, QD, false, NGO>(R, ar + (size_t) p_in * kSlot, rot);
             load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
             quant_rows<NT, QD>(v, L);
-            q8_compute<NT, QD, false>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
-                                      ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
+            q8_compute<NT, QD, false, NGO>(R, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
+                                           ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
         } else {
-            F16Regs<QD, false> F;
-            f16_prefetch<QD, false, TK>(F, (const uint16_t *) W.wo, nullptr, D, rot);
-            res_prefetch16<NT, QD, false>(F, ar + (size_t) p_in * kSlot, rot);
+            F16Regs<QD, false, NGO> F;
+            f16_prefetch<QD, false, TK, NGO>(F, (const uint16_t *) W.wo, nullptr, D, rot);
+            res_prefetch16<NT, QD, false, NGO>(F, ar + (size_t) p_in * kSlot, rot);
             load_tagged<NT, QD>(ar + (size_t) p_att * kSlot, tb | p_att, v, dead, A.err);
             f16_rows<NT, QD, false>(v, L);
-            f16_compute<NT, QD, false, false>(F, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
-                                              ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
+            f16_compute<NT, QD, false, false, NGO>(F, L, EPI_RESID, ar + (size_t) p_in * kSlot, tb | p_in,
+                                                   ar + (size_t) p_wo * kSlot, tb | p_wo, rot, dead, A.err);
         }
     }
     __syncthreads();
     // gate/up + SwiGLU (RMSNorm'd); NGU row groups per wave (3 for the 1.7B
     // talker's 6144 rows over 1024 waves)
-    constexpr int NGU = (FF / Geo<D>::RPW + 1023) / 1024 > 2 ? 3 : 2;
+    constexpr int NGU = ngroups<D>(FF);
     const int p_gu = p++;
     if (wg_has_rows<D>(FF, 0)) {
         Q8Regs<D, true, NGU> R;
-        F16Regs<D, true> F;
+        F16Regs<D, true, NGU> F;
         if constexpr (WT == W_Q8) q8_prefetch<D, true, TK, NGU>(R, W.wg, W.wg_d, W.wu, W.wu_d, FF, 0);
-        else f16_prefetch<D, true, TK>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
+        else f16_prefetch<D, true, TK, NGU>(F, (const uint16_t *) W.wg, (const uint16_t *) W.wu, FF, 0);
         NormT<D> nw;
         norm_prefetch<D>(W.ffn_norm, nw);
         RowsT<NT, D> v;
@@ -1761,8 +1796,8 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
                                          A.err);
         } else {
             f16_rows<NT, D, false>(v, L);
-            f16_compute<NT, D, true, false>(F, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0,
-                                            dead, A.err);
+            f16_compute<NT, D, true, false, NGU>(F, L, EPI_SWIGLU, nullptr, 0, ar + (size_t) p_gu * kSlot, tb | p_gu, 0,
+                                                 dead, A.err);
         }
     }
     __syncthreads();
@@ -1770,22 +1805,23 @@ __device__ __attribute__((always_inline)) void layer_t(const Args & A, Lds & L, 
     const int p_dn = p++;
     if (wg_has_rows<FF>(D, rot)) {
         RowsT<NT, FF> v;
+        constexpr int NGD = ngroups<FF>(D);
         if constexpr (WT == W_Q8) {
-            Q8Regs<FF, false> R;
-            q8_prefetch<FF, false, TK>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
-            res_prefetch<NT, FF, false>(R, ar + (size_t) p_wo * kSlot, rot);
+            Q8Regs<FF, false, NGD> R;
+            q8_prefetch<FF, false, TK, NGD>(R, W.wd, W.wd_d, nullptr, nullptr, D, rot);
+            res_prefetch<NT, FF, false, NGD>(R, ar + (size_t) p_wo * kSlot, rot);
             load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
             quant_rows<NT, FF>(v, L);
-            q8_compute<NT, FF, false>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
-                                      ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
+            q8_compute<NT, FF, false, NGD>(R, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
+                                           ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
         } else {
-            F16Regs<FF, false> F;
-            f16_prefetch<FF, false, TK>(F, (const uint16_t *) W.wd, nullptr, D, rot);
-            res_prefetch16<NT, FF, false>(F, ar + (size_t) p_wo * kSlot, rot);
+            F16Regs<FF, false, NGD> F;
+            f16_prefetch<FF, false, TK, NGD>(F, (const uint16_t *) W.wd, nullptr, D, rot);
+            res_prefetch16<NT, FF, false, NGD>(F, ar + (size_t) p_wo * kSlot, rot);
             load_tagged<NT, FF>(ar + (size_t) p_gu * kSlot, tb | p_gu, v, dead, A.err);
             f16_rows<NT, FF, true>(v, L);
-            f16_compute<NT, FF, false, true>(F, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
-                                             ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
+            f16_compute<NT, FF, false, true, NGD>(F, L, EPI_RESID, ar + (size_t) p_wo * kSlot, tb | p_wo,
+                                                  ar + (size_t) p_dn * kSlot, tb | p_dn, rot, dead, A.err);
         }
     }
     __syncthreads();
@@ -2011,13 +2047,13 @@ __device__ __forceinline__ void xf16_compute(const XRegs16<KIND> & R, const Lds 
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if (WIDE) {
-                const float4 x0 = *(const float4 *) &L.xw[t][2 * c][b * 4];
-                const float4 x1 = *(const float4 *) &L.xw[t][2 * c + 1][b * 4];
+                const float4 x0 = *(const float4 *) xw_at<G::K>(L, t, 2 * c, b);
+                const float4 x1 = *(const float4 *) xw_at<G::K>(L, t, 2 * c + 1, b);
                 float * xr = xa[WIDE ? t : 0];
                 xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w;
                 xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
             } else {
-                xp[t] = *(const int4 *) &L.hf[t][c][b * 8];
+                xp[t] = *(const int4 *) hf_at<G::K>(L, t, c, b);
             }
         }
 #pragma unroll
@@ -2276,20 +2312,29 @@ __device__ __forceinline__ void publish(const Args & A, const float * x, int nt,
             tstore(A.arena + (size_t) p * kSlot + (size_t) t * kHS + i, tb | p, x[t * d + i]);
 }
 
-// code_pred.mtp_proj: the NT gathered rows of width K in L.x, Q8_0-quantised,
-// through the projection (rows = the code predictor's width) plus its bias,
-// tagged into slot p.
-template <int NT, int K>
+// code_pred.mtp_proj: the NT gathered rows of width K in L.x (Q8_0-quantised,
+// or rounded to fp16 for an F16 projection) through the projection (rows =
+// the code predictor's width) plus its bias, tagged into slot p.
+template <int NT, int K, int WT>
 __device__ __attribute__((always_inline)) void mtp_phase(const Args & A, Lds & L, int rows, int p, uint32_t tb,
                                                          bool & dead) {
     if (wg_has_rows<K>(rows, 0)) {
-        Q8Regs<K, false> R;
-        q8_prefetch<K, false, false>(R, A.mtp_w, A.mtp_d, nullptr, nullptr, rows, 0);
         RowsT<NT, K> v;
-        load_lds<NT, K>(L.x, v);
-        quant_rows<NT, K>(v, L);
-        q8_compute<NT, K, false>(R, L, EPI_BIAS, nullptr, 0, A.arena + (size_t) p * kSlot, tb | p, 0, dead, A.err,
-                                 A.mtp_b);
+        if constexpr (WT == W_Q8) {
+            Q8Regs<K, false> R;
+            q8_prefetch<K, false, false>(R, A.mtp_w, A.mtp_d, nullptr, nullptr, rows, 0);
+            load_lds<NT, K>(L.x, v);
+            quant_rows<NT, K>(v, L);
+            q8_compute<NT, K, false>(R, L, EPI_BIAS, nullptr, 0, A.arena + (size_t) p * kSlot, tb | p, 0, dead, A.err,
+                                     A.mtp_b);
+        } else {
+            F16Regs<K, false> F;
+            f16_prefetch<K, false, false>(F, (const uint16_t *) A.mtp_w, nullptr, rows, 0);
+            load_lds<NT, K>(L.x, v);
+            f16_rows<NT, K, false>(v, L);
+            f16_compute<NT, K, false, false>(F, L, EPI_BIAS, nullptr, 0, A.arena + (size_t) p * kSlot, tb | p, 0, dead,
+                                             A.err, A.mtp_b);
+        }
     }
     __syncthreads();
 }
@@ -2394,8 +2439,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 // the 1.7B layout: the code predictor's input rows pass through
                 // code_pred.mtp_proj (+ bias) into its own width
                 const int p_m = p++;
-                if (nt == 2) mtp_phase<2, D>(A, L, DC, p_m, tb, dead);
-                else mtp_phase<1, D>(A, L, DC, p_m, tb, dead);
+                if (nt == 2) mtp_phase<2, D, WT>(A, L, DC, p_m, tb, dead);
+                else mtp_phase<1, D, WT>(A, L, DC, p_m, tb, dead);
                 p_in = p_out = p_m;
                 x0 = nullptr;
             }

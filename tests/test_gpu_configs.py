@@ -599,28 +599,30 @@ def weights17(wtype, seed):
     return _weights[key]
 
 
-def test_17b_q8_frame_loop_greedy(path):
+@pytest.mark.parametrize("wtype", ["q8_0", "f16"])
+def test_17b_frame_loop_greedy(wtype, path):
     """The 1.7B layout at its full shapes (talker 2048 wide with FFN 6144, code
-    predictor 1024 wide behind code_pred.mtp_proj), Q8_0: a 24-token prompt
-    and 16 greedy frames on the persistent kernel's 1.7B variant (three
-    gate/up row groups per wave, the projection as a GEMV phase per pass) and
-    on the multi-kernel frame, against the oracle."""
+    predictor 1024 wide behind code_pred.mtp_proj), Q8_0 and F16: a 24-token
+    prompt and 16 greedy frames on the persistent kernel's 1.7B variants
+    (three gate/up row groups per wave, the projection as a GEMV phase per
+    pass) and on the multi-kernel frame, against the oracle."""
     if path == "persistent_rows":
         pytest.skip("the 1.7B layout has one persistent program (row-parallel)")
     cfg = qcfg.full_17b()
     text = np.random.default_rng(28).integers(0, 151936, 24).astype(np.int32)
     spk = np.random.default_rng(29).standard_normal(cfg.hidden_size).astype(np.float32)
-    w = weights17("q8_0", 5)
-    if "17b" not in _oracle_runs:
+    w = weights17(wtype, 5)
+    key = "17b_" + wtype
+    if key not in _oracle_runs:
         o = orc.Oracle(cfg, w, threads=THREADS)
-        say("[gpu] 1.7B: oracle generate 16")
-        _oracle_runs["17b"] = o.generate(text, spk, max_len=16, temperature=0.0, top_k=0)
+        say(f"[gpu] 1.7B {wtype}: oracle generate 16")
+        _oracle_runs[key] = o.generate(text, spk, max_len=16, temperature=0.0, top_k=0)
         o.close()
-    co, first_o = _oracle_runs["17b"]
+    co, first_o = _oracle_runs[key]
     dev = Device(cfg)
     try:
         dev.upload_weights(w)
-        say(f"[gpu] 1.7B: device generate 16 ({path})")
+        say(f"[gpu] 1.7B {wtype}: device generate 16 ({path})")
         cg = driver.generate(dev, cfg, text, spk, max_len=16, temperature=0.0, top_k=0, chunk=8)
         _, _, used = dev.frames_stats()
         assert used == (0 if path == "graph" else 1), used

@@ -640,10 +640,10 @@ def test_mtp_layout_matches_oracle(wtype, frame_path):
     """The 1.7B layout at small shapes: a code predictor narrower than the
     talker, reached through code_pred.mtp_proj (src/tts_transformer.cpp:
     1942-1947, :2096-2101).  Talker steps, greedy and sampled code-predictor
-    calls and whole greedy and sampled frame loops equal the oracle; Q8_0
-    models run them on the persistent frame kernel (its 1.7B-layout variant,
-    with the projection as one more GEMV phase per code-predictor pass), F16
-    models on the multi-kernel frame."""
+    calls and whole greedy and sampled frame loops equal the oracle, on the
+    persistent frame kernel (its 1.7B-layout variants, Q8_0 and F16, with the
+    projection as one more GEMV phase per code-predictor pass) and on the
+    multi-kernel frame."""
     cfg = qcfg.tiny_mtp()
     say(f"[gpu] mtp layout {wtype} ({frame_path})")
     w, dev, o = make(cfg, wtype, seed=41, n_ctx=64)
@@ -675,6 +675,6 @@ def test_mtp_layout_matches_oracle(wtype, frame_path):
         cg = driver.generate(dev, cfg, text, None, max_len=16, temperature=0.9, top_k=50, seed=13, chunk=5)
         assert np.array_equal(cg, co)
         us, n, path = dev.frames_stats()
-        assert path == (1 if wtype == "q8_0" and frame_path == "persistent" else 0), path
+        assert path == (1 if frame_path == "persistent" else 0), path
     finally:
         dev.close()
