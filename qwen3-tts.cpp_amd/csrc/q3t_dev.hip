@@ -2635,9 +2635,13 @@ struct StreamKV {
 //   PROJ     pre-quantised rows in (attention / SwiGLU output), + residual
 //   GATE_UP  RMSNorm'd rows, gate and up matrices, SwiGLU, Q8_0 out
 enum GemmKind { G_QKV = 0, G_PROJ = 1, G_GATE_UP = 2 };
-constexpr int kGemmKB[3] = {2, 4, 2};       // max Q8_0 blocks per wave
+// preferred K splits and the Q8_0 blocks per wave they leave (QKV and gate/up:
+// 32 blocks / (4 waves x 2); Wo / down: 64 or 96 / (4 x 4)).  Measured with
+// 16 streams on one box: {2, 4, 2} 2,567 aggregate frames/s, {2, 2, 2} 2,500,
+// the former {4, 8, 4} 2,340, no split {1, 1, 1} 2,051.
+constexpr int kGemmKB[3] = {4, 6, 4};       // max Q8_0 blocks per wave
 constexpr int kGemmMT[3] = {1, 1, 2};       // 16-row tiles per workgroup
-constexpr int kGemmS[3] = {4, 8, 4};        // preferred K splits
+constexpr int kGemmS[3] = {2, 4, 2};        // preferred K splits
 
 template <int NT, int KIND>
 const void * gemm_kernel() {
