@@ -378,6 +378,21 @@ const char * frame_path_name(int32_t path) {
     }
 }
 
+// QWEN3_TTS_DUMP_CODES=<path> (src/tts_transformer.cpp:3356-3366, 3641-3651):
+// after each generate / generate_icl the codes go to <path> as int32 n
+// followed by the n int32 codes.  The reference compiles this in with
+// -DQWEN3_TTS_DUMP_CODES; here the variable alone turns it on.
+void dump_codes(const std::vector<int32_t> & output) {
+    const char * path = std::getenv("QWEN3_TTS_DUMP_CODES");
+    if (!path || !*path) return;
+    FILE * f = fopen(path, "wb");
+    if (!f) return;
+    const int32_t n = (int32_t) output.size();
+    fwrite(&n, sizeof n, 1, f);
+    fwrite(output.data(), sizeof(int32_t), output.size(), f);
+    fclose(f);
+}
+
 }  // namespace
 
 bool TTSTransformer::run_frames(const std::vector<float> & prefill, const std::vector<float> & trailing,
@@ -506,6 +521,7 @@ bool TTSTransformer::generate(const int32_t * text_tokens, int32_t n_tokens, con
     if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
                     rep_loop_detect, on_frame, output, tm))
         return false;
+    dump_codes(output);
     write_attn_dump();
     if (tm) { tm->total_ms = ms_since(t_start); print_timing(*tm); }
     return true;
@@ -532,6 +548,7 @@ bool TTSTransformer::generate_icl(const int32_t * text_tokens, int32_t n_tokens,
     if (!run_frames(prefill, trailing, pad, max_len, repetition_penalty, temperature, top_k, eos_bias, target_frames,
                     rep_loop_detect, on_frame, output, tm))
         return false;
+    dump_codes(output);
     write_attn_dump();
     if (tm) { tm->total_ms = ms_since(t_start); print_timing(*tm); }
     return true;

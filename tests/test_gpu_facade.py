@@ -92,7 +92,8 @@ def _facade_check(tmp_path, cfg, w, wtype, layout, max_len, converter=False):
         f.write(struct.pack("<ii", max_len, ref_codes.shape[0]) + ref_codes.tobytes())
     print(f"[gpu] facade {wtype} {layout}", file=sys.stderr, flush=True)
     r = subprocess.run([BIN, str(model), str(tmp_path / "in.bin"), str(tmp_path)], capture_output=True, text=True,
-                       timeout=300, env=dict(os.environ, QWEN3_TTS_TIMING="1"))
+                       timeout=300, env=dict(os.environ, QWEN3_TTS_TIMING="1",
+                                             QWEN3_TTS_DUMP_CODES=str(tmp_path / "dump.bin")))
     print(r.stdout, r.stderr, file=sys.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
     # QWEN3_TTS_TIMING=1: the timing report after every generate / generate_icl
@@ -131,6 +132,9 @@ def _facade_check(tmp_path, cfg, w, wtype, layout, max_len, converter=False):
     assert np.array_equal(pc0, o.predict_codes(hid))
     assert np.array_equal(pc1, o.predict_codes(hid, codes[-1, 1:]))
     icl = np.fromfile(tmp_path / "icl.bin", np.int32).reshape(-1, 16)
+    # QWEN3_TTS_DUMP_CODES: the last call's codes (generate_icl), int32 n then the codes
+    dump = np.fromfile(tmp_path / "dump.bin", np.int32)
+    assert dump[0] == icl.size and np.array_equal(dump[1:], icl.ravel())
     pre, trail, pad = icl_rows(o, cfg, text, text, ref_codes, spk)
     io = o.generate_rows(pre, trail, pad, max_len=max_len, temperature=0.0)
     assert np.array_equal(icl, io)
