@@ -308,11 +308,17 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
         HIP_OK(hipGetLastError());
         return 0;
     }
-    // a residual input takes the form that prefetches it in the epilogue
-#define Q3T_VOC_GEMM(wm, wn)                                                                    \
-    do {                                                                                        \
+    // a residual input takes the form that prefetches it in the epilogue; a
+    // contraction of 64 or more 32-element chunks (the k7 convolutions of the
+    // 768- and 384-channel decoder blocks: 168 and 84) stages two chunks per
+    // K step (2.92-2.97 -> 2.83 ms per 73-frame window; four per step and two
+    // from 32 chunks measured no better)
+    const bool deep = W.KT * (W.Cp / 32) >= 64;
+#define Q3T_VOC_GEMM(wm, wn)                                                                             \
+    do {                                                                                                 \
         if (res) hipLaunchKernelGGL((k_conv_gemm<wm, wn, 1, true>), grid, dim3(kGemmT), 0, v->stream, a); \
-        else hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a);    \
+        else if (deep) hipLaunchKernelGGL((k_conv_gemm<wm, wn, 2>), grid, dim3(kGemmT), 0, v->stream, a); \
+        else hipLaunchKernelGGL((k_conv_gemm<wm, wn>), grid, dim3(kGemmT), 0, v->stream, a);             \
     } while (0)
 #define Q3T_VOC_GEMM_WN(wm)                   \
     switch (WN) {                             \
