@@ -483,8 +483,21 @@ int st_pre_tfm(q3t_voc * v, int l, int64_t n, int32_t pos0) {
     hipLaunchKernelGGL(k_rope_qk, dim3((unsigned) ((nr + 255) / 256)), dim3(256), 0, v->stream, v->qkv, Q, (int32_t) n,
                        c.latent, hd, v->rope_cos, v->rope_sin, pos0);
     HIP_OK(hipGetLastError());
-    hipLaunchKernelGGL(k_attn_causal, dim3((unsigned) n, (unsigned) c.n_heads), dim3(64), (size_t) n * 4, v->stream,
-                       v->qkv, Q, c.latent, hd, 1.0f / std::sqrt((float) hd), v->att, L);
+    // windows whose K and V rows fit in LDS take the staged kernel (4 query
+    // rows per workgroup, head widths 32 and 64); longer decodes the
+    // one-wave-per-row kernel
+    const size_t lds = ((size_t) 2 * n * hd + (size_t) 4 * hd + (size_t) 4 * n) * 4;
+    const dim3 sg((unsigned) ((n + 3) / 4), (unsigned) c.n_heads);
+    const float asc = 1.0f / std::sqrt((float) hd);
+    if (lds <= 65536 && hd == 64)
+        hipLaunchKernelGGL(k_attn_causal_lds<64>, sg, dim3(256), lds, v->stream, v->qkv, Q, c.latent, (int32_t) n, asc,
+                           v->att, L);
+    else if (lds <= 65536 && hd == 32)
+        hipLaunchKernelGGL(k_attn_causal_lds<32>, sg, dim3(256), lds, v->stream, v->qkv, Q, c.latent, (int32_t) n, asc,
+                           v->att, L);
+    else
+        hipLaunchKernelGGL(k_attn_causal, dim3((unsigned) n, (unsigned) c.n_heads), dim3(64), (size_t) n * 4, v->stream,
+                           v->qkv, Q, c.latent, hd, 1.0f / std::sqrt((float) hd), v->att, L);
     HIP_OK(hipGetLastError());
     if (gemm(v, P.wo, v->att, L, (int32_t) n, 0, 1, (int32_t) n, 1, nullptr, P.attn_scale, v->xf, H, v->xf, H,
              nullptr, 0, ACT_NONE, nullptr))

@@ -380,6 +380,69 @@ __global__ __launch_bounds__(64) void k_attn_causal(const float * __restrict__ q
     }
 }
 
+// k_attn_causal for short windows: workgroup (x, h) takes query rows 4x ..
+// 4x + 3 of head h, one wave each, with their q rows and the head's K and V
+// rows 0 .. 4x + 3 staged in LDS once, and the head width a constant so the
+// dot products unroll (the one-wave kernel reads q, K and V from global
+// memory inside its dependent fp64 chains).  Every lane computes what it
+// computes there, in the same order: scores as sequential fp64 fmas over
+// the head dims, the max and fp64 sum over the same lane split and shuffle
+// tree, P.V as one dim per lane over the keys in order.  Dynamic LDS:
+// (2 T HD + 4 HD + 4 T) floats.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_causal_lds(const float * __restrict__ qkv, int32_t qs, int32_t L, int32_t T,
+                                                         float scale, uint16_t * __restrict__ out, int32_t os) {
+    extern __shared__ float sm[];
+    const int h = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * 4, t = t0 + wave;
+    const int nrow = min(t0 + 4, T);                  // keys 0 .. nrow - 1 cover every row of the workgroup
+    // K transposed ([d][key], stride T), so the lanes of a wave, one key
+    // each, read consecutive words; V as rows ([key][d]), read one dim per lane
+    float * ks = sm;                                  // [HD][T]
+    float * vs = sm + (size_t) T * HD;                // [nrow][HD]
+    float * qv = sm + (size_t) 2 * T * HD;            // [4][HD]
+    float * p = qv + 4 * HD + (size_t) wave * T;      // [T] per wave
+    for (int i = threadIdx.x; i < nrow * HD; i += 256) {
+        const int j = i / HD, d = i - j * HD;
+        ks[(size_t) d * T + j] = qkv[(size_t) j * qs + L + h * HD + d];
+        vs[i] = qkv[(size_t) j * qs + 2 * L + h * HD + d];
+    }
+    for (int i = threadIdx.x; i < 4 * HD; i += 256) {
+        const int r = t0 + i / HD;
+        qv[i] = r < T ? qkv[(size_t) r * qs + h * HD + i % HD] : 0.0f;
+    }
+    __syncthreads();
+    const bool act = t < T;                           // wave-uniform: the last workgroup's spare waves idle
+    float inv = 0.0f;
+    if (act) {
+        const float * q = qv + wave * HD;
+        float mx = -INFINITY;
+        for (int j = lane; j <= t; j += 64) {
+            double s = 0.0;
+#pragma unroll
+            for (int d = 0; d < HD; ++d) s = fma((double) q[d], (double) ks[(size_t) d * T + j], s);
+            const float v = (float) s * scale;
+            p[j] = v;
+            mx = fmaxf(mx, v);
+        }
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        double sum = 0.0;
+        for (int j = lane; j <= t; j += 64) {
+            const float e = expf(p[j] - mx);
+            p[j] = e;
+            sum += (double) e;
+        }
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        inv = (float) (1.0 / sum);
+    }
+    __syncthreads();
+    if (act && lane < HD) {
+        double o = 0.0;
+        for (int j = 0; j <= t; ++j) o = fma((double) (p[j] * inv), (double) vs[(size_t) j * HD + lane], o);
+        out[(size_t) t * os + h * HD + lane] = f2h((float) o);
+    }
+}
+
 // ConvNeXt front (src/audio_tokenizer_decoder.cpp:515-539): causal depthwise
 // k7 over fp16-rounded y, + bias, then LayerNorm over the C channels (eps
 // 1e-6, ggml_norm: fp64 mean, centred fp32 values, fp64 variance), * w + b,

@@ -94,6 +94,23 @@ def test_stages_match_oracle(tiny_voc, n, pos0):
     assert errs[worst][1] <= STAGE_TOL_RMS, (worst, errs[worst])
 
 
+@pytest.mark.parametrize("n", [73, 239, 240, 400])
+def test_pre_transformer_attention_forms(tiny_voc, n):
+    """A pre-transformer layer over n rows at position 19: up to 239 rows at
+    these widths (head width 32) the attention stages each head's q, K and V
+    rows in LDS (four query rows per workgroup), from 240 rows it takes the
+    one-wave-per-row kernel; both within the stage tolerances of the oracle."""
+    c, w, g, o = tiny_voc
+    width = o.stages(codes_for(2, 1), 0)["input_proj"].shape[1]
+    x = (np.random.default_rng(n).standard_normal((n, width)) * 0.5).astype(np.float32)
+    say(f"[gpu] pre_tfm.0 over {n} rows")
+    got = g.run_stage("pre_tfm.0", x, 19)
+    want = o.run_stage("pre_tfm.0", x, 19)
+    assert got.shape == want.shape
+    mx, rms = rel_err(got, want)
+    assert mx <= STAGE_TOL_MAX and rms <= STAGE_TOL_RMS, (mx, rms)
+
+
 def test_decode_window_matches_oracle(tiny_voc):
     c, w, g, o = tiny_voc
     codes = codes_for(12, 3)
