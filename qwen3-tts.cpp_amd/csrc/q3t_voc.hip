@@ -574,8 +574,13 @@ int st_res(q3t_voc * v, int b, int r, int64_t T, const Io & io, bool last) {
 
 int st_out(q3t_voc * v, int64_t T, const uint16_t * hin, float * pre, int64_t drop) {
     const int32_t C = rup(v->cfg.decoder_dim >> 4, 32);
-    hipLaunchKernelGGL(k_out_conv, dim3((unsigned) ((T + 255) / 256)), dim3(256), 0, v->stream, hin, C, (int32_t) T, C,
-                       v->out_w, v->out_b, pre, v->audio, drop);
+    // up to 96 channels: the rows staged in LDS per 256 samples
+    if (C <= kOutMaxC)
+        hipLaunchKernelGGL(k_out_conv_lds, dim3((unsigned) ((T + 255) / 256)), dim3(256), 0, v->stream, hin, C,
+                           (int32_t) T, C, v->out_w, v->out_b, pre, v->audio, drop);
+    else
+        hipLaunchKernelGGL(k_out_conv, dim3((unsigned) ((T + 255) / 256)), dim3(256), 0, v->stream, hin, C, (int32_t) T,
+                           C, v->out_w, v->out_b, pre, v->audio, drop);
     HIP_OK(hipGetLastError());
     return 0;
 }

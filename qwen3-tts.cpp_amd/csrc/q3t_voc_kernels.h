@@ -489,6 +489,48 @@ __global__ __launch_bounds__(256) void k_dwconv_ln(const float * __restrict__ y,
     }
 }
 
+// k_out_conv with the workgroup's rows staged in LDS: samples t0 .. t0 + 255
+// read rows t0 - 6 .. t0 + 255, loaded once and coalesced, stored channel-
+// major (xt[c][row]) so that the lanes, one sample each, read consecutive
+// halves; the weights as fp64.  Each thread sums taps then channels in the
+// order of k_out_conv.  C <= 96.  Static LDS: 96 x 262 halves + 7 x 96
+// doubles (55 KB).
+constexpr int kOutRows = 256 + 6, kOutMaxC = 96;
+__global__ __launch_bounds__(256) void k_out_conv_lds(const uint16_t * __restrict__ x, int32_t xs, int32_t T, int32_t C,
+                                                      const uint16_t * __restrict__ w, float bias,
+                                                      float * __restrict__ pre, float * __restrict__ out, int64_t drop) {
+    __shared__ uint16_t xt[kOutMaxC][kOutRows];
+    __shared__ double wd[7][kOutMaxC];
+    const int64_t t0 = (int64_t) blockIdx.x * 256;
+    for (int i = threadIdx.x; i < C * 7; i += 256) {
+        const int c = i / 7, k = i - c * 7;
+        wd[k][c] = (double) h2f(w[c * 7 + k]);
+    }
+    // rows r = 0 .. 261 are samples t0 - 6 + r; eight channels per load
+    const int cg = C / 8;
+    for (int i = threadIdx.x; i < kOutRows * cg; i += 256) {
+        const int r = i / cg, c8 = (i - r * cg) * 8;
+        const int64_t src = t0 - 6 + r;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (src >= 0 && src < T) v = *(const uint4 *) (x + src * xs + c8);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xt[c8 + e][r] = (uint16_t) (wv[e >> 1] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+    const int64_t t = t0 + threadIdx.x;
+    if (t >= T) return;
+    double acc = 0.0;
+    for (int k = 0; k < 7; ++k) {
+        if (t + k - 6 < 0) continue;
+        const int r = (int) threadIdx.x + k;
+        for (int c = 0; c < C; ++c) acc = fma((double) h2f(xt[c][r]), wd[k][c], acc);
+    }
+    const float y = (float) acc + bias;
+    if (pre) pre[t] = y;
+    if (t >= drop) out[t - drop] = tanhf(y);
+}
+
 // Output conv (C -> 1, k7, causal) over the fp16 snake'd rows, + bias, tanh.
 // pre (optional) keeps the value before tanh; out gets samples t >= drop at
 // out[t - drop].  One thread per sample; C % 8 == 0.
