@@ -313,12 +313,16 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
     // 768- and 384-channel decoder blocks: 168 and 84) stages two chunks per
     // K step (2.92-2.97 -> 2.83 ms per 73-frame window; four per step and two
     // from 32 chunks measured no better)
-    const bool deep = W.KT * (W.Cp / 32) >= 64;
+    static const int deep_ks = [] {
+        const char * e = std::getenv("Q3T_VOC_DEEPKS");
+        return e ? std::atoi(e) : 2;
+    }();
+    const bool deep = W.KT * (W.Cp / 32) >= 64 && deep_ks == 2;
     // a deep contraction on the narrowest tile (the upsampler's 4096-deep
     // pwconv2 over 146 rows, narrowed to fill the CUs) stages four chunks per
     // step: its 128-chunk K loop is a chain of load round trips (2.72 -> 2.68
     // ms per window; eight per step no better)
-    if (deep && WM == 1 && WN == 1) {
+    if (W.KT * (W.Cp / 32) >= 64 && WM == 1 && WN == 1 && deep_ks != 1) {
         hipLaunchKernelGGL((k_conv_gemm<1, 1, 4>), grid, dim3(kGemmT), 0, v->stream, a);
         HIP_OK(hipGetLastError());
         return 0;

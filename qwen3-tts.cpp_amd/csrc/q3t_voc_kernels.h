@@ -58,16 +58,20 @@ struct ConvArgs {
 constexpr int kGemmT = 256;    // 4 waves: 2 along channels x 2 along time
 
 // The workgroup tile is 32 WM channels x 32 WN rows; wave (wc, wt) owns WM
-// 16-channel tiles x WN 16-row tiles.  Each K step (one tap, 32 channels)
-// stages the weight rows and the activation rows of the tile in LDS (16-byte
-// chunks, chunk index XOR (row & 3) against bank conflicts), double-buffered:
-// the global loads of step s + 1 are in flight while step s runs on the
-// matrix cores.  MFMA lane layout (16x16x32): A[m = l%16][k = 8(l/16)..+7]
-// (weights, m = channel), B[k][n = l%16] (activations, n = time row),
-// D[m = 4(l/16)+e][n = l%16].  The SwiGLU pairing needs WM even.
-// KS chunks (of 32 K elements) per step: KS = 4 for the small launches (the
-// 73-row pre-transformer GEMMs), whose K loop of 16-32 steps would otherwise
-// be a chain of load-and-barrier round trips.
+// 16-channel tiles x WN 16-row tiles.  Each K step (KS chunks of one tap x 32
+// channels) stages the weight rows and the activation rows of the tile in LDS,
+// double-buffered, from registers loaded two steps ahead: the loads of step
+// s + 2 are issued before step s runs on the matrix cores and stored to LDS
+// only after step s + 1 has run, so a load round trip overlaps two steps
+// (with the loads of step s + 1 stored right after step s, every step waited
+// for its own round trip).  The loads are buffer loads whose range check
+// returns zeros: causal padding rows, rows past the launch and chunks past
+// the contraction need no branches.  MFMA lane layout (16x16x32):
+// A[m = l%16][k = 8(l/16)..+7] (weights, m = channel), B[k][n = l%16]
+// (activations, n = time row), D[m = 4(l/16)+e][n = l%16].  The SwiGLU
+// pairing needs WM even.  KS = 4 for the small launches (the 73-row
+// pre-transformer GEMMs), whose K loop of 16-32 steps would otherwise be a
+// chain of load-and-barrier round trips.
 template <int WM, int WN, int KS = 1>
 struct GemmTile {
     static constexpr int BC = 32 * WM, BT = 32 * WN;
@@ -79,131 +83,60 @@ struct GemmTile {
     static constexpr int LDS = LDS_STAGE > LDS_EPI ? LDS_STAGE : LDS_EPI;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chunk ^ (row & 3)) << 3); }
+// LDS slot of 16-byte piece c of tile row r (rows of 4 pieces, 64 bytes):
+// piece c sits at c ^ ((r >> 1) & 3), so the pieces c of 8 consecutive rows
+// (a fragment read: 8 lanes, rows r0..r0+7) cover all 32 banks, and so do
+// 8 consecutive threads writing rows 2q and 2q + 1.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3); }
 
-// RP (A.res set): the epilogue loads every residual value of the tile before
-// it uses any, so their reads overlap; the registers this takes lower the
-// occupancy, which the convolutions without a residual (whose K loops need
-// it) keep.
-template <int WM, int WN, int KS = 1, bool RP = false>
-__global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
-    using G = GemmTile<WM, WN, KS>;
-    __shared__ __align__(16) char smem[G::LDS];
-    uint16_t * lds = (uint16_t *) smem;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wc = wave & 1, wt = wave >> 1;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource over `bytes` bytes at p: loads at offsets past `bytes`
+// (or at 0x80000000, the out-of-range marker used here) return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void * p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *) p, (short) 0, (int) bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int) off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+constexpr uint32_t kOut = 0x80000000u;
+
+// The epilogue of a wave's WM x WN tiles of 16 channels x 16 rows (channels
+// [ch0, ch0 + 16 WM), rows [t0, t0 + 16 WN)), one 16-row tile at a time
+// through the wave's LDS slice `my` (16 x (16 WM + 4) floats, [row][channel]),
+// then 64 lanes walk it channel-fastest (coalesced row stores).  LDS is in
+// order within a wave, so no barrier is needed.
+// RP (A.res set): every residual value of the tiles is loaded before any is
+// used, so their reads overlap instead of forming one dependent chain; the
+// registers this takes lower the occupancy, which the convolutions without a
+// residual (whose K loops need it) keep.
+template <int WM, int WN, bool RP>
+__device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&acc)[WM][WN], float * my, int ch0, int t0,
+                                              int phase, int lane) {
     const int lm = lane & 15, lk = lane >> 4;
-    const int phase = blockIdx.z;
-    const int cb0 = blockIdx.x * G::BC, tb0 = blockIdx.y * G::BT;
-    const uint16_t * wbase = A.w + (size_t) phase * A.Np * A.KT * A.Cp;
-    const int CB = A.Cp >> 5, NCH = A.KT * CB, S = (NCH + KS - 1) / KS;
-
-    // this thread's 16-byte chunks of the A (weights) and B (activations) tiles
-    const uint16_t * ga[G::NA];
-    int la[G::NA];
-    bool oa[G::NA];
-#pragma unroll
-    for (int r = 0; r < G::NA; ++r) {
-        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
-        oa[r] = c < G::BC * 4;
-        ga[r] = wbase + (size_t) (cb0 + (oa[r] ? row : 0)) * A.KT * A.Cp + col * 8;
-        la[r] = swz(row, col);
-    }
-    int tb[G::NB], lb[G::NB], cbk[G::NB];
-    bool ob[G::NB];
-#pragma unroll
-    for (int r = 0; r < G::NB; ++r) {
-        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
-        ob[r] = c < G::BT * 4;
-        const int t = tb0 + row;
-        tb[r] = (ob[r] && t < A.M) ? t + A.off0 : -(1 << 30);
-        cbk[r] = col * 8;
-        lb[r] = G::BC * 32 + swz(row, col);
-    }
-    uint4 ra[KS][G::NA], rb[KS][G::NB];
-    auto fetch = [&](int s) {
-#pragma unroll
-        for (int q = 0; q < KS; ++q) {
-            const int ch = s * KS + q;               // chunks past the end load zeros
-            const int tap = ch / CB, cc = (ch - tap * CB) * 32;
-#pragma unroll
-            for (int r = 0; r < G::NA; ++r)
-                ra[q][r] = oa[r] && ch < NCH ? *(const uint4 *) (ga[r] + (size_t) tap * A.Cp + cc) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < G::NB; ++r) {
-                const int src = tb[r] + tap * A.dil;
-                rb[q][r] = (ch < NCH && src >= 0 && src < A.rows_in)
-                               ? *(const uint4 *) (A.x + (size_t) src * A.xs + cc + cbk[r])
-                               : make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto stash = [&](int buf) {
-#pragma unroll
-        for (int q = 0; q < KS; ++q) {
-            uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
-#pragma unroll
-            for (int r = 0; r < G::NA; ++r)
-                if (oa[r]) *(uint4 *) (st + la[r]) = ra[q][r];
-#pragma unroll
-            for (int r = 0; r < G::NB; ++r)
-                if (ob[r]) *(uint4 *) (st + lb[r]) = rb[q][r];
-        }
-    };
-
-    v4f acc[WM][WN];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int s = 0; s < S; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < S) fetch(s + 1);
-#pragma unroll
-        for (int q = 0; q < KS; ++q) {
-            const uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
-            v8h af[WM], bf[WN];
-#pragma unroll
-            for (int i = 0; i < WM; ++i) af[i] = *(const v8h *) (st + swz(wc * WM * 16 + i * 16 + lm, lk));
-#pragma unroll
-            for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (st + G::BC * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (s + 1 < S) stash(buf ^ 1);
-        __syncthreads();
-    }
-
-    // epilogue one 16-row tile at a time through the wave's LDS slice
-    // ([row][channel]), then 64 lanes walk it channel-fastest (coalesced row
-    // stores).  LDS is in order within a wave, so no barrier is needed.
-    constexpr int TC = WM * 16, TS = G::TS;
+    constexpr int TC = WM * 16, TS = TC + 4;
     constexpr int IT = 16 * TC / 64;                 // elements per lane of one 16-row tile
-    float * my = (float *) smem + wave * 16 * TS;
-    const int ch0 = cb0 + wc * WM * 16, t0 = tb0 + wt * WN * 16;
-    // RP: the residual values of every tile, loaded before any is used so
-    // their global reads overlap instead of forming one dependent chain
-    float rv[RP ? WN : 1][RP ? IT : 1];
-    if (RP) {
+    // up to 48 residual values per lane are loaded for all tiles at once,
+    // more (the time-wide tiles) one 16-row tile at a time
+    constexpr bool ALL = WN * IT <= 48;
+    constexpr int RJ = RP && ALL ? WN : 1;
+    float rv[RJ][RP ? IT : 1];
+    auto load_res = [&](int j, int slot) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
+        for (int k = 0; k < IT; ++k) {
+            const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
+            const int t = t0 + j * 16 + tl, n = ch0 + cl;
+            rv[slot][RP ? k : 0] = t < A.M && n < A.N ? A.res[((size_t) t * A.ostride + phase) * A.rs + n] : 0.0f;
+        }
+    };
+    if (RP && ALL) {
 #pragma unroll
-            for (int k = 0; k < IT; ++k) {
-                const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
-                const int t = t0 + j * 16 + tl, n = ch0 + cl;
-                rv[RP ? j : 0][RP ? k : 0] =
-                    t < A.M && n < A.N ? A.res[((size_t) t * A.ostride + phase) * A.rs + n] : 0.0f;
-            }
+        for (int j = 0; j < WN; ++j) load_res(j, RJ > 1 ? j : 0);
     }
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
+        if (RP && !ALL) load_res(j, 0);
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -232,7 +165,7 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
                 float v = my[tl * TS + cl];
                 if (A.bias) v = v + A.bias[n];
                 if (A.scale) v = v * A.scale[n];
-                v = rv[RP ? j : 0][RP ? k : 0] + v;
+                v = rv[RJ > 1 ? j : 0][RP ? k : 0] + v;
                 if (A.yf) A.yf[row * A.yfs + n] = v;
                 if (A.yh) {
                     float h = v;
@@ -262,6 +195,126 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
         }
         __builtin_amdgcn_wave_barrier();
     }
+}
+
+template <int WM, int WN, int KS = 1, bool RP = false>
+__global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
+    using G = GemmTile<WM, WN, KS>;
+    __shared__ __align__(16) char smem[G::LDS];
+    uint16_t * lds = (uint16_t *) smem;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wc = wave & 1, wt = wave >> 1;
+    const int lm = lane & 15, lk = lane >> 4;
+    const int phase = blockIdx.z;
+    const int cb0 = blockIdx.x * G::BC, tb0 = blockIdx.y * G::BT;
+    const int CB = A.Cp >> 5, NCH = A.KT * CB, S = (NCH + KS - 1) / KS;
+    const uint32_t wrow = (uint32_t) A.KT * (uint32_t) A.Cp * 2u, xrow = (uint32_t) A.xs * 2u;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(A.w + (size_t) phase * A.Np * A.KT * A.Cp, (uint32_t) A.Np * wrow);
+    const __amdgpu_buffer_rsrc_t xr = rsrc(A.x, (uint32_t) A.rows_in * xrow);
+
+    // this thread's 16-byte pieces of the A (weights) and B (activations) tiles
+    uint32_t wo[G::NA];
+    int la[G::NA];
+    bool oa[G::NA];
+#pragma unroll
+    for (int r = 0; r < G::NA; ++r) {
+        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
+        oa[r] = c < G::BC * 4;
+        wo[r] = (uint32_t) (cb0 + (oa[r] ? row : 0)) * wrow + col * 16;
+        la[r] = swz(row, col);
+    }
+    int tb[G::NB], lb[G::NB];
+    uint32_t xo[G::NB];
+    bool ob[G::NB];
+#pragma unroll
+    for (int r = 0; r < G::NB; ++r) {
+        const int c = tid + r * kGemmT, row = c >> 2, col = c & 3;
+        ob[r] = c < G::BT * 4;
+        const int t = tb0 + row;
+        tb[r] = (ob[r] && t < A.M) ? t + A.off0 : -(1 << 30);
+        xo[r] = col * 16;
+        lb[r] = G::BC * 32 + swz(row, col);
+    }
+    struct Stage {
+        uint4 a[KS][G::NA], b[KS][G::NB];
+    };
+    auto fetch = [&](int s, Stage & R) {
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            const int ch = s * KS + q;
+            const int tap = ch / CB, cc = (ch - tap * CB) * 32;
+            const bool in = ch < NCH;
+            const uint32_t wk = in ? (uint32_t) (tap * A.Cp + cc) * 2u : kOut;
+#pragma unroll
+            for (int r = 0; r < G::NA; ++r) R.a[q][r] = bload(wr, wo[r] + wk);
+#pragma unroll
+            for (int r = 0; r < G::NB; ++r) {
+                const int src = tb[r] + tap * A.dil;
+                const bool ok = in && (unsigned) src < (unsigned) A.rows_in;
+                R.b[q][r] = bload(xr, ok ? (uint32_t) src * xrow + (uint32_t) cc * 2u + xo[r] : kOut);
+            }
+        }
+    };
+    auto stash = [&](int buf, const Stage & R) {
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
+#pragma unroll
+            for (int r = 0; r < G::NA; ++r)
+                if (oa[r]) *(uint4 *) (st + la[r]) = R.a[q][r];
+#pragma unroll
+            for (int r = 0; r < G::NB; ++r)
+                if (ob[r]) *(uint4 *) (st + lb[r]) = R.b[q][r];
+        }
+    };
+
+    v4f acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            const uint16_t * st = lds + buf * G::STAGE + q * G::SUB;
+            v8h af[WM], bf[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) af[i] = *(const v8h *) (st + swz(wc * WM * 16 + i * 16 + lm, lk));
+#pragma unroll
+            for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (st + G::BC * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // two register stages: Ra holds the even steps, Rb the odd ones.  The
+    // fetches and stores of steps past the end are not skipped (their loads
+    // are out of range and return zeros, into buffers no step reads): a
+    // branch around a load would cost the compiler's wait counts their
+    // precision, and a wait for the newest loads undoes the prefetch.
+    // An odd step count runs one more step of zeros (S2 even), so the loop
+    // body has no exit between its two halves.
+    Stage Ra, Rb;
+    const int S2 = S + (S & 1);
+    fetch(0, Ra);
+    fetch(1, Rb);
+    stash(0, Ra);
+    __syncthreads();
+    for (int s = 0; s < S2; s += 2) {
+        fetch(s + 2, Ra);
+        compute(0);
+        stash(1, Rb);
+        __syncthreads();
+        fetch(s + 3, Rb);
+        compute(1);
+        stash(0, Ra);
+        __syncthreads();
+    }
+    conv_epilogue<WM, WN, RP>(A, acc, (float *) smem + wave * 16 * G::TS, cb0 + wc * WM * 16, tb0 + wt * WN * 16,
+                              phase, lane);
 }
 
 // yh[t][c] = fp16(act(x[t][c])) for c < C (the input of a stage whose
