@@ -21,11 +21,34 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 enum : int32_t { ACT_NONE = 0, ACT_SNAKE = 1, ACT_GELU = 2, ACT_SWIGLU = 3 };
 
+// sin(y)^2 in fp32: Cody-Waite reduction r = y - k pi/2 (k = rint(y 2/pi),
+// pi/2 as a three-part sum applied with fused multiply-adds), the degree-9
+// Taylor polynomial of sin on |r| <= pi/4 (truncation below 3e-9 relative),
+// and sin^2(y) = sin^2(r) for even k, cos^2(r) = 1 - sin^2(r) for odd k.
+// Within 4 ulp of the true value (sinf squared: within 3), at about half of
+// sinf's instructions.  |y| beyond 2^13 takes sinf.
+__device__ __forceinline__ float sin_sq(float y) {
+    if (fabsf(y) > 8192.0f) {
+        const float s = sinf(y);
+        return s * s;
+    }
+    const float k = rintf(y * 0.636619746685028076171875f);
+    float r = fmaf(-k, 1.57079637050628662109375f, y);
+    r = fmaf(-k, -4.37113882867379300296306610107421875e-8f, r);
+    r = fmaf(-k, -1.715124510005881882e-15f, r);
+    const float r2 = r * r;
+    float p = fmaf(r2, 2.7557318844628753e-6f, -1.9841270113829523e-4f);
+    p = fmaf(r2, p, 8.333333767950535e-3f);
+    p = fmaf(r2, p, -0.1666666716337204f);
+    const float sn = fmaf(r * r2, p, r);
+    const float ss = sn * sn;
+    return ((int) k & 1) ? 1.0f - ss : ss;
+}
+
 // snake (src/audio_tokenizer_decoder.cpp:402-426): x + sin(x e^a)^2 e^-b,
 // with ea = e^alpha and eb = e^-beta per channel (computed on the host).
 __device__ __forceinline__ float snake(float x, float ea, float eb) {
-    const float s = sinf(x * ea);
-    const float sq = s * s;
+    const float sq = sin_sq(x * ea);
     return x + sq * eb;
 }
 
@@ -102,6 +125,8 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 }
 constexpr uint32_t kOut = 0x80000000u;
 
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+
 // The epilogue of a wave's WM x WN tiles of 16 channels x 16 rows (channels
 // [ch0, ch0 + 16 WM), rows [t0, t0 + 16 WN)), one 16-row tile at a time
 // through the wave's LDS slice `my` (16 x (16 WM + 4) floats, [row][channel]),
@@ -117,8 +142,22 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
     const int lm = lane & 15, lk = lane >> 4;
     constexpr int TC = WM * 16, TS = TC + 4;
     constexpr int IT = 16 * TC / 64;                 // elements per lane of one 16-row tile
+    // element k of a lane sits in channel (lane + 64 k) % TC, which repeats
+    // with period P in k: the per-channel parameters are loaded once
+    constexpr int P = TC / gcd_c(TC, 64);
+    static_assert(IT % P == 0, "whole periods");
+    float pb[P], ps[P], pa[P], pe[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int n = ch0 + (lane + 64 * p) % TC;
+        const bool ok = n < A.N;
+        pb[p] = A.bias && ok ? A.bias[n] : 0.0f;
+        ps[p] = A.scale && ok ? A.scale[n] : 0.0f;
+        pa[p] = A.act == ACT_SNAKE && ok ? A.ea[n] : 0.0f;
+        pe[p] = A.act == ACT_SNAKE && ok ? A.eb[n] : 0.0f;
+    }
     // up to 48 residual values per lane are loaded for all tiles at once,
-    // more (the time-wide tiles) one 16-row tile at a time
+    // more one 16-row tile at a time
     constexpr bool ALL = WN * IT <= 48;
     constexpr int RJ = RP && ALL ? WN : 1;
     float rv[RJ][RP ? IT : 1];
@@ -154,8 +193,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
                 const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
                 A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
             }
-        } else if (RP) {
-            // unrolled, reading the prefetched residuals
+        } else {
 #pragma unroll
             for (int k = 0; k < IT; ++k) {
                 const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
@@ -163,31 +201,14 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
                 if (t >= A.M || n >= A.N) continue;
                 const size_t row = (size_t) t * A.ostride + phase;
                 float v = my[tl * TS + cl];
-                if (A.bias) v = v + A.bias[n];
-                if (A.scale) v = v * A.scale[n];
-                v = rv[RJ > 1 ? j : 0][RP ? k : 0] + v;
+                if (A.bias) v = v + pb[k % P];
+                if (A.scale) v = v * ps[k % P];
+                if (RP) v = rv[RJ > 1 ? j : 0][RP ? k : 0] + v;
+                else if (A.res) v = A.res[row * A.rs + n] + v;
                 if (A.yf) A.yf[row * A.yfs + n] = v;
                 if (A.yh) {
                     float h = v;
-                    if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
-                    else if (A.act == ACT_GELU) h = gelu_tanh(v);
-                    A.yh[row * A.yhs + n] = f2h(h);
-                }
-            }
-        } else {
-            for (int idx = lane; idx < 16 * TC; idx += 64) {
-                const int tl = idx / TC, cl = idx - tl * TC;
-                const int t = tbase + tl, n = ch0 + cl;
-                if (t >= A.M || n >= A.N) continue;
-                const size_t row = (size_t) t * A.ostride + phase;
-                float v = my[tl * TS + cl];
-                if (A.bias) v = v + A.bias[n];
-                if (A.scale) v = v * A.scale[n];
-                if (A.res) v = A.res[row * A.rs + n] + v;
-                if (A.yf) A.yf[row * A.yfs + n] = v;
-                if (A.yh) {
-                    float h = v;
-                    if (A.act == ACT_SNAKE) h = snake(v, A.ea[n], A.eb[n]);
+                    if (A.act == ACT_SNAKE) h = snake(v, pa[k % P], pe[k % P]);
                     else if (A.act == ACT_GELU) h = gelu_tanh(v);
                     A.yh[row * A.yhs + n] = f2h(h);
                 }
