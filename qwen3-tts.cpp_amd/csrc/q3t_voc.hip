@@ -268,6 +268,12 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
          float * yf, int32_t yfs, uint16_t * yh, int32_t yhs, int32_t act, const Snake * sn) {
     if (M <= 0) return 0;
     if (xs % 8 || xs < W.Cp) return fail(v, "internal: GEMM input stride");
+    // the kernels address outputs and residuals with 32-bit element offsets
+    // and read inputs and weights through 32-bit buffer ranges
+    if ((int64_t) M * ostride * std::max({yfs, yhs, rs, W.N}) >= ((int64_t) 1 << 31) ||
+        (int64_t) rows_in * xs * 2 >= ((int64_t) 1 << 31) ||
+        (int64_t) W.Np * W.KT * W.Cp * 2 >= ((int64_t) 1 << 31))
+        return fail(v, "decode segment too long: a vocoder layer exceeds 2^31 elements");
     ConvArgs a{};
     a.x = x; a.xs = xs; a.rows_in = rows_in;
     a.w = W.w; a.Cp = W.Cp; a.KT = W.KT; a.dil = dil; a.off0 = off0;

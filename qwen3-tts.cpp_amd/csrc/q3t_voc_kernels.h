@@ -161,12 +161,15 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
     constexpr bool ALL = WN * IT <= 48;
     constexpr int RJ = RP && ALL ? WN : 1;
     float rv[RJ][RP ? IT : 1];
+    // element offsets in 32 bits (the host checks that they fit)
+    const uint32_t ost = (uint32_t) A.ostride, ph = (uint32_t) phase;
     auto load_res = [&](int j, int slot) {
 #pragma unroll
         for (int k = 0; k < IT; ++k) {
             const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
             const int t = t0 + j * 16 + tl, n = ch0 + cl;
-            rv[slot][RP ? k : 0] = t < A.M && n < A.N ? A.res[((size_t) t * A.ostride + phase) * A.rs + n] : 0.0f;
+            rv[slot][RP ? k : 0] =
+                t < A.M && n < A.N ? A.res[((uint32_t) t * ost + ph) * (uint32_t) A.rs + (uint32_t) n] : 0.0f;
         }
     };
     if (RP && ALL) {
@@ -191,7 +194,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
                 const int n = ((ch0 >> 1) + pr * 16) + w;
                 if (t >= A.M || n >= (A.N >> 1)) continue;
                 const float g = my[tl * TS + pr * 32 + w], u = my[tl * TS + pr * 32 + 16 + w];
-                A.yh[((size_t) t * A.ostride + phase) * A.yhs + n] = f2h(silu(g) * u);
+                A.yh[((uint32_t) t * ost + ph) * (uint32_t) A.yhs + (uint32_t) n] = f2h(silu(g) * u);
             }
         } else {
 #pragma unroll
@@ -199,18 +202,18 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
                 const int idx = lane + 64 * k, tl = idx / TC, cl = idx - tl * TC;
                 const int t = tbase + tl, n = ch0 + cl;
                 if (t >= A.M || n >= A.N) continue;
-                const size_t row = (size_t) t * A.ostride + phase;
+                const uint32_t row = (uint32_t) t * ost + ph;
                 float v = my[tl * TS + cl];
                 if (A.bias) v = v + pb[k % P];
                 if (A.scale) v = v * ps[k % P];
                 if (RP) v = rv[RJ > 1 ? j : 0][RP ? k : 0] + v;
-                else if (A.res) v = A.res[row * A.rs + n] + v;
-                if (A.yf) A.yf[row * A.yfs + n] = v;
+                else if (A.res) v = A.res[row * (uint32_t) A.rs + (uint32_t) n] + v;
+                if (A.yf) A.yf[row * (uint32_t) A.yfs + (uint32_t) n] = v;
                 if (A.yh) {
                     float h = v;
                     if (A.act == ACT_SNAKE) h = snake(v, pa[k % P], pe[k % P]);
                     else if (A.act == ACT_GELU) h = gelu_tanh(v);
-                    A.yh[row * A.yhs + n] = f2h(h);
+                    A.yh[row * (uint32_t) A.yhs + (uint32_t) n] = f2h(h);
                 }
             }
         }
