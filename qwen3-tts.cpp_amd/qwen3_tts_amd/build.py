@@ -2,7 +2,11 @@
 
 hipcc flags: -ffp-contract=off keeps every fp32 rounding where the kernels
 write it (no implicit fused multiply-add); the packed-fp32-ops target feature
-is disabled so the compiler emits no packed fp32 instructions.
+is disabled so the compiler emits no packed fp32 instructions.  The vocoder
+source is compiled with its matrix-core accumulators in ordinary vector
+registers (-amdgpu-mfma-vgpr-form): its GEMM's K loop, unrolled by two steps,
+otherwise copied every accumulator between the two register files each step
+(2.35 -> 2.27-2.30 ms per 73-frame window, the same results).
 """
 import os
 import subprocess
@@ -15,19 +19,31 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def build_device_lib(verbose=False):
-    srcs = [os.path.join(PKG_DIR, "csrc", f) for f in ("q3t_dev.hip", "q3t_voc.hip")]
-    out_dir = os.path.join(PKG_DIR, "lib")
-    os.makedirs(out_dir, exist_ok=True)
-    out = os.path.join(out_dir, "libq3t_hip.so")
-    tmp = out + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", *HIP_FLAGS, "-shared", "-o", tmp, *srcs]
+SRC_FLAGS = {"q3t_dev.hip": [], "q3t_voc.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
+def _run(cmd, verbose):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + r.stderr[-4000:])
-    os.replace(tmp, out)
     if verbose:
         print(" ".join(cmd))
+
+
+def build_device_lib(verbose=False):
+    out_dir = os.path.join(PKG_DIR, "lib")
+    obj_dir = os.path.join(out_dir, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = []
+    for src, extra in SRC_FLAGS.items():
+        obj = os.path.join(obj_dir, src.replace(".hip", ".o"))
+        _run([HIPCC, f"--offload-arch={ARCH}", *HIP_FLAGS, *extra, "-c", "-o", obj,
+              os.path.join(PKG_DIR, "csrc", src)], verbose)
+        objs.append(obj)
+    out = os.path.join(out_dir, "libq3t_hip.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs], verbose)
+    os.replace(tmp, out)
     return out
 
 
