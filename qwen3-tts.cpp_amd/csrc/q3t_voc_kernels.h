@@ -221,6 +221,75 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
     }
 }
 
+// The epilogue straight from the MFMA output layout, for launches whose
+// channel count is a multiple of 4 (all but SwiGLU): lane (lm, lk) of tile
+// (i, j) holds channels 16 i + 4 lk .. + 3 of row 16 j + lm, so each lane
+// loads its 4 residuals and stores its 4 fp32 results as one 16-byte access
+// and its 4 fp16 results as one 8-byte access, with the per-channel
+// parameters loaded once per tile column i.  No LDS round trip and no
+// per-element index arithmetic; the arithmetic per element is conv_epilogue's.
+template <int WM, int WN, bool RP>
+__device__ __forceinline__ void conv_epilogue_direct(const ConvArgs & A, const v4f (&acc)[WM][WN], int ch0, int t0,
+                                                     int phase, int lane) {
+    const int lm = lane & 15, lk = lane >> 4;
+    const uint32_t ost = (uint32_t) A.ostride, ph = (uint32_t) phase;
+    // RP: every residual quad of the wave's tiles is loaded before any is used
+    constexpr bool ALLR = RP && WM * WN <= 8;
+    float4 rq[ALLR ? WM : 1][ALLR ? WN : 1];
+    if (ALLR) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const int n0 = ch0 + i * 16 + 4 * lk, t = t0 + j * 16 + lm;
+                rq[ALLR ? i : 0][ALLR ? j : 0] =
+                    n0 < A.N && t < A.M
+                        ? *(const float4 *) (A.res + ((uint32_t) t * ost + ph) * (uint32_t) A.rs + (uint32_t) n0)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const int n0 = ch0 + i * 16 + 4 * lk;
+        if (n0 >= A.N) continue;
+        const float4 b4 = A.bias ? *(const float4 *) (A.bias + n0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 s4 = A.scale ? *(const float4 *) (A.scale + n0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool sn = A.act == ACT_SNAKE;
+        const float4 a4 = sn ? *(const float4 *) (A.ea + n0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 e4 = sn ? *(const float4 *) (A.eb + n0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float bb[4] = {b4.x, b4.y, b4.z, b4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+        const float aa[4] = {a4.x, a4.y, a4.z, a4.w}, ee[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int t = t0 + j * 16 + lm;
+            if (t >= A.M) continue;
+            const uint32_t row = (uint32_t) t * ost + ph;
+            float4 r4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (ALLR) r4 = rq[ALLR ? i : 0][ALLR ? j : 0];
+            else if (A.res) r4 = *(const float4 *) (A.res + row * (uint32_t) A.rs + (uint32_t) n0);
+            const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+            float v[4];
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x = acc[i][j][e];
+                if (A.bias) x = x + bb[e];
+                if (A.scale) x = x * ss[e];
+                if (A.res) x = rr[e] + x;
+                v[e] = x;
+                float y = x;
+                if (sn) y = snake(x, aa[e], ee[e]);
+                else if (A.act == ACT_GELU) y = gelu_tanh(x);
+                h[e] = f2h(y);
+            }
+            if (A.yf) *(float4 *) (A.yf + row * (uint32_t) A.yfs + (uint32_t) n0) = make_float4(v[0], v[1], v[2], v[3]);
+            if (A.yh)
+                *(uint2 *) (A.yh + row * (uint32_t) A.yhs + (uint32_t) n0) =
+                    make_uint2((uint32_t) h[0] | ((uint32_t) h[1] << 16), (uint32_t) h[2] | ((uint32_t) h[3] << 16));
+        }
+    }
+}
+
 template <int WM, int WN, int KS = 1, bool RP = false>
 __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     using G = GemmTile<WM, WN, KS>;
@@ -337,8 +406,11 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
         stash(0, Ra);
         __syncthreads();
     }
-    conv_epilogue<WM, WN, RP>(A, acc, (float *) smem + wave * 16 * G::TS, cb0 + wc * WM * 16, tb0 + wt * WN * 16,
-                              phase, lane);
+    if (A.act != ACT_SWIGLU && A.N % 4 == 0)
+        conv_epilogue_direct<WM, WN, RP>(A, acc, cb0 + wc * WM * 16, tb0 + wt * WN * 16, phase, lane);
+    else
+        conv_epilogue<WM, WN, RP>(A, acc, (float *) smem + wave * 16 * G::TS, cb0 + wc * WM * 16, tb0 + wt * WN * 16,
+                                  phase, lane);
 }
 
 // yh[t][c] = fp16(act(x[t][c])) for c < C (the input of a stage whose
