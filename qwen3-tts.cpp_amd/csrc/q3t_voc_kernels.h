@@ -436,18 +436,42 @@ __global__ void k_vq_sum(const int32_t * __restrict__ codes, int32_t n_cb, int32
                          uint16_t * __restrict__ lath, int32_t lhs, int32_t * __restrict__ bad) {
     const int f = blockIdx.x;
     const int32_t * cf = codes + (size_t) f * n_cb;
+    // up to 16 codebooks: every table load of an element is issued before the
+    // sum, which keeps its order
+    constexpr int QM = 16;
     for (int d = threadIdx.x; d < hidden; d += blockDim.x) {
         float r = 0.0f, first = 0.0f;
-        for (int q = 0; q < n_cb; ++q) {
-            int code = cf[q];
-            if (code < 0 || code >= size) {
-                if (d == 0) atomicOr(bad, 1);
-                code = 0;
+        if (n_cb <= QM) {
+            float tv[QM];
+#pragma unroll
+            for (int q = 0; q < QM; ++q) {
+                if (q >= n_cb) break;
+                int code = cf[q];
+                if (code < 0 || code >= size) {
+                    if (d == 0) atomicOr(bad, 1);
+                    code = 0;
+                }
+                tv[q] = tab[((size_t) q * size + code) * hidden + d];
             }
-            const float v = tab[((size_t) q * size + code) * hidden + d];
-            if (q == 0) first = v;
-            else if (q == 1) r = v;
-            else r = r + v;
+#pragma unroll
+            for (int q = 0; q < QM; ++q) {
+                if (q >= n_cb) break;
+                if (q == 0) first = tv[q];
+                else if (q == 1) r = tv[q];
+                else r = r + tv[q];
+            }
+        } else {
+            for (int q = 0; q < n_cb; ++q) {
+                int code = cf[q];
+                if (code < 0 || code >= size) {
+                    if (d == 0) atomicOr(bad, 1);
+                    code = 0;
+                }
+                const float v = tab[((size_t) q * size + code) * hidden + d];
+                if (q == 0) first = v;
+                else if (q == 1) r = v;
+                else r = r + v;
+            }
         }
         const float y = first + r;
         latf[(size_t) f * lfs + d] = y;
@@ -462,6 +486,32 @@ __global__ void k_rms_h(const float * __restrict__ x, int32_t xs, int32_t T, int
     const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= T) return;
     const float * r = x + (size_t) t * xs;
+    // up to 512 channels: all of a lane's loads are issued before its sum,
+    // which keeps its order (the terms past C add exact zeros)
+    constexpr int RV = 8;
+    if (C <= 64 * RV) {
+        float xv[RV], wv[RV];
+#pragma unroll
+        for (int k = 0; k < RV; ++k) {
+            const int c = lane + 64 * k;
+            xv[k] = c < C ? r[c] : 0.0f;
+            wv[k] = c < C ? w[c] : 0.0f;
+        }
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < RV; ++k) s += (double) (xv[k] * xv[k]);
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+        const float mean = (float) (s / (double) C);
+        const float sc = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int k = 0; k < RV; ++k) {
+            const int c = lane + 64 * k;
+            if (c >= C) break;
+            const float v = xv[k] * sc;
+            y[(size_t) t * ys + c] = f2h(v * wv[k]);
+        }
+        return;
+    }
     double s = 0.0;
     for (int c = lane; c < C; c += 64) s += (double) (r[c] * r[c]);
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
@@ -551,10 +601,26 @@ __global__ __launch_bounds__(256) void k_attn_causal_lds(const float * __restric
     float * vs = sm + (size_t) T * HD;                // [nrow][HD]
     float * qv = sm + (size_t) 2 * T * HD;            // [4][HD]
     float * p = qv + 4 * HD + (size_t) wave * T;      // [T] per wave
-    for (int i = threadIdx.x; i < nrow * HD; i += 256) {
-        const int j = i / HD, d = i - j * HD;
-        ks[(size_t) d * T + j] = qkv[(size_t) j * qs + L + h * HD + d];
-        vs[i] = qkv[(size_t) j * qs + 2 * L + h * HD + d];
+    // 8 elements of K and of V per thread in flight before they are stored
+    constexpr int U = 8;
+    for (int i0 = threadIdx.x; i0 < nrow * HD; i0 += 256 * U) {
+        float kv[U], vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + 256 * u, j = i / HD, d = i - j * HD;
+            if (i < nrow * HD) {
+                kv[u] = qkv[(size_t) j * qs + L + h * HD + d];
+                vv[u] = qkv[(size_t) j * qs + 2 * L + h * HD + d];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + 256 * u, j = i / HD, d = i - j * HD;
+            if (i < nrow * HD) {
+                ks[(size_t) d * T + j] = kv[u];
+                vs[i] = vv[u];
+            }
+        }
     }
     for (int i = threadIdx.x; i < 4 * HD; i += 256) {
         const int r = t0 + i / HD;
