@@ -331,13 +331,22 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     struct Stage {
         uint4 a[KS][G::NA], b[KS][G::NB];
     };
+    // fetches run in chunk order, so a cursor (tap, channel offset) replaces
+    // a division per chunk; chunk ch's weights start at byte 64 ch of a row
+    int f_ch = 0, f_tap = 0, f_cc = 0;
     auto fetch = [&](int s, Stage & R) {
+        (void) s;
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
-            const int ch = s * KS + q;
-            const int tap = ch / CB, cc = (ch - tap * CB) * 32;
-            const bool in = ch < NCH;
-            const uint32_t wk = in ? (uint32_t) (tap * A.Cp + cc) * 2u : kOut;
+            const int tap = f_tap, cc = f_cc;
+            const bool in = f_ch < NCH;
+            const uint32_t wk = in ? (uint32_t) f_ch * 64u : kOut;
+            f_ch += 1;
+            f_cc += 32;
+            if (f_cc == A.Cp) {
+                f_cc = 0;
+                f_tap += 1;
+            }
 #pragma unroll
             for (int r = 0; r < G::NA; ++r) R.a[q][r] = bload(wr, wo[r] + wk);
 #pragma unroll
