@@ -222,7 +222,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs & A, const v4f (&ac
 }
 
 // The epilogue straight from the MFMA output layout, for launches whose
-// channel count is a multiple of 4 (all but SwiGLU): lane (lm, lk) of tile
+// channel count and row strides are multiples of 4 (all but SwiGLU): lane (lm, lk) of tile
 // (i, j) holds channels 16 i + 4 lk .. + 3 of row 16 j + lm, so each lane
 // loads its 4 residuals and stores its 4 fp32 results as one 16-byte access
 // and its 4 fp16 results as one 8-byte access, with the per-channel
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
         stash(0, Ra);
         __syncthreads();
     }
-    if (A.act != ACT_SWIGLU && A.N % 4 == 0)
+    if (A.act != ACT_SWIGLU && ((A.N | A.rs | A.yfs | A.yhs) & 3) == 0)
         conv_epilogue_direct<WM, WN, RP>(A, acc, cb0 + wc * WM * 16, tb0 + wt * WN * 16, phase, lane);
     else
         conv_epilogue<WM, WN, RP>(A, acc, (float *) smem + wave * 16 * G::TS, cb0 + wc * WM * 16, tb0 + wt * WN * 16,
