@@ -578,10 +578,46 @@ int st_conv_t(q3t_voc * v, int b, int64_t T, const Io & io) {
                 v->xf, Co, io.hout, Co, io.nx.act, io.nx.sn);
 }
 
+// A residual unit of 96 or 192 channels over at least kFuseRows rows in one
+// launch (k_conv_gemm<WM, 2, 1, false, true>, one channel tile of 32 WM = C,
+// 64-row tiles): the decoder blocks at the 192- and 96-channel widths.
+// Q3T_VOC_FUSE=0 runs the two convolutions as separate launches.  Returns 1
+// when the unit does not qualify, else 0 or the launch's error.
+constexpr int64_t kFuseRows = 1024;
+
+int res_fused(q3t_voc * v, const ResUnit & U, int64_t T, int32_t d, const Io & io, bool last) {
+    static const bool off = [] {
+        const char * e = std::getenv("Q3T_VOC_FUSE");
+        return e && std::strcmp(e, "0") == 0;
+    }();
+    const int32_t C = U.conv1.N;
+    if (off || T < kFuseRows || (C != 96 && C != 192) || U.conv1.Cp != C || U.conv1.Np != C || U.conv1.KT != 7 ||
+        U.conv2.Cp != C || U.conv2.Np != C || U.conv2.N != C || U.conv2.KT != 1)
+        return 1;
+    if (T * C * 4 >= ((int64_t) 1 << 31)) return fail(v, "decode segment too long: a vocoder layer exceeds 2^31 elements");
+    ConvArgs a{};
+    a.x = io.hin; a.xs = C; a.rows_in = (int32_t) T;
+    a.w = U.conv1.w; a.Cp = C; a.KT = 7; a.dil = d; a.off0 = -6 * d;
+    a.M = (int32_t) T; a.N = C; a.Np = C; a.ostride = 1;
+    a.bias = U.b1; a.act = ACT_SNAKE; a.ea = U.act2.ea; a.eb = U.act2.eb;
+    a.w2 = U.conv2.w; a.bias2 = U.b2; a.act2 = io.nx.act;
+    a.ea2 = io.nx.sn ? io.nx.sn->ea : nullptr;
+    a.eb2 = io.nx.sn ? io.nx.sn->eb : nullptr;
+    a.res = v->xf; a.rs = C;
+    a.yf = (!last || io.want_f32) ? v->xf : nullptr; a.yfs = C;
+    a.yh = io.hout; a.yhs = C;
+    const dim3 grid(1, (unsigned) ((T + 63) / 64), 1);
+    if (C == 96) hipLaunchKernelGGL((k_conv_gemm<3, 2, 1, false, true>), grid, dim3(kGemmT), 0, v->stream, a);
+    else hipLaunchKernelGGL((k_conv_gemm<6, 2, 1, false, true>), grid, dim3(kGemmT), 0, v->stream, a);
+    HIP_OK(hipGetLastError());
+    return 0;
+}
+
 // residual unit r: x + conv2(snake2(conv1(snake1(x)))) with snake1(x) in hin
 int st_res(q3t_voc * v, int b, int r, int64_t T, const Io & io, bool last) {
     const ResUnit & U = v->dec[b].res[r];
     const int32_t C = U.conv1.N, Cp = rup(C, 32), d = r == 0 ? 1 : r == 1 ? 3 : 9;
+    if (const int rc = res_fused(v, U, T, d, io, last); rc <= 0) return rc;
     if (clear_pad(v, v->mid, T, C)) return -1;
     if (gemm(v, U.conv1, io.hin, Cp, (int32_t) T, -6 * d, d, (int32_t) T, 1, U.b1, nullptr, nullptr, 0, nullptr, 0,
              v->mid, Cp, ACT_SNAKE, &U.act2))

@@ -76,6 +76,14 @@ struct ConvArgs {
     uint16_t * yh; int32_t yhs;
     int32_t act;
     const float * ea, * eb;
+    // FU launches (a residual unit in one launch): this launch's GEMM is the
+    // unit's k7 conv, whose output (+ bias, snake ea/eb, fp16) stays in LDS
+    // as the input of the 1-tap conv w2 ([N][N] fp16), whose output takes
+    // bias2, the residual res and act2 (ea2, eb2) into yf / yh
+    const uint16_t * w2;
+    const float * bias2;
+    int32_t act2;
+    const float * ea2, * eb2;
 };
 
 constexpr int kGemmT = 256;    // 4 waves: 2 along channels x 2 along time
@@ -290,7 +298,14 @@ __device__ __forceinline__ void conv_epilogue_direct(const ConvArgs & A, const v
     }
 }
 
-template <int WM, int WN, int KS = 1, bool RP = false>
+// FU (a whole residual unit, x + conv1(snake2(conv7(snake1(x))))): the
+// workgroup's tile holds every channel of its rows (32 WM = N, one channel
+// tile), so after the k7 loop it rounds snake2(acc + bias) to fp16 into LDS
+// in the layout of a stage's activation rows, runs the 1-tap conv on it with
+// the weight fragments read straight from memory (N x N fp16, cache-resident),
+// and finishes with the direct epilogue: the intermediate tensor is neither
+// written nor read back, and the arithmetic is that of the two launches.
+template <int WM, int WN, int KS = 1, bool RP = false, bool FU = false>
 __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
     using G = GemmTile<WM, WN, KS>;
     __shared__ __align__(16) char smem[G::LDS];
@@ -414,6 +429,63 @@ __global__ __launch_bounds__(kGemmT) void k_conv_gemm(const ConvArgs A) {
         compute(1);
         stash(0, Ra);
         __syncthreads();
+    }
+    if constexpr (FU) {
+        static_assert(G::BC * G::BT <= G::LDS / 2, "the intermediate tile fits the stage buffers");
+        // the k7 outputs: lane (lm, lk) of tile (i, j) holds channels
+        // 16 (WM wc + i) + 4 lk .. + 3 of local row 16 (WN wt + j) + lm, half
+        // of a 16-byte piece of that row in chunk n0 / 32
+        uint16_t * mid = lds;                       // [N / 32][BT][32], swizzled rows
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int n0 = wc * WM * 16 + i * 16 + 4 * lk;
+            const float4 b4 = A.bias ? *(const float4 *) (A.bias + n0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 a4 = *(const float4 *) (A.ea + n0), e4 = *(const float4 *) (A.eb + n0);
+            const float bb[4] = {b4.x, b4.y, b4.z, b4.w}, aa[4] = {a4.x, a4.y, a4.z, a4.w};
+            const float ee[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const int rl = wt * WN * 16 + j * 16 + lm;
+                uint16_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = acc[i][j][e];
+                    if (A.bias) x = x + bb[e];
+                    h[e] = f2h(snake(x, aa[e], ee[e]));
+                }
+                *(uint2 *) (mid + (n0 >> 5) * G::BT * 32 + swz(rl, (n0 & 31) >> 3) + (n0 & 7)) =
+                    make_uint2((uint32_t) h[0] | ((uint32_t) h[1] << 16), (uint32_t) h[2] | ((uint32_t) h[3] << 16));
+            }
+        }
+        __syncthreads();
+        // the 1-tap conv over the tile, chunk by chunk in order
+        v4f acc2[WM][WN];
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc2[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < WM; ++q) {              // N / 32 = WM chunks
+            v8h af[WM], bf[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                af[i] = *(const v8h *) (A.w2 + (size_t) (wc * WM * 16 + i * 16 + lm) * (WM * 32) + q * 32 + 8 * lk);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) bf[j] = *(const v8h *) (mid + q * G::BT * 32 + swz(wt * WN * 16 + j * 16 + lm, lk));
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc2[i][j], 0, 0, 0);
+        }
+        ConvArgs B = A;
+        B.bias = A.bias2;
+        B.scale = nullptr;
+        B.act = A.act2;
+        B.ea = A.ea2;
+        B.eb = A.eb2;
+        conv_epilogue_direct<WM, WN, true>(B, acc2, wc * WM * 16, tb0 + wt * WN * 16, phase, lane);
+        return;
     }
     if (A.act != ACT_SWIGLU && ((A.N | A.rs | A.yfs | A.yhs) & 3) == 0)
         conv_epilogue_direct<WM, WN, RP>(A, acc, cb0 + wc * WM * 16, tb0 + wt * WN * 16, phase, lane);
