@@ -262,3 +262,34 @@ def test_full_size_stages_and_window():
     finally:
         g.close()
         o.close()
+
+
+FUSE_SCRIPT = r"""
+import sys, numpy as np
+from qwen3_tts_amd import vocoder as V
+c = V.full()
+g = V.VocDevice(c, V.VocWeights(c, seed=3))
+codes = np.random.default_rng(12).integers(0, c.codebook_size, (6, c.n_codebooks)).astype(np.int32)
+np.save(sys.argv[1], g.decode_window(codes, 3, 6, 3))
+g.close()
+"""
+
+
+def test_fused_residual_units_match_two_launches(tmp_path):
+    """The 96- and 192-channel residual units run as one launch (k7 conv,
+    snake and 1-tap conv with the intermediate tile in LDS); Q3T_VOC_FUSE=0
+    runs them as two.  A 6-frame window at the tokenizer's widths (decoder
+    blocks 3-4 over 3,840 and 11,520 rows) gives the same audio bit for bit."""
+    import os
+    import subprocess
+    from qwen3_tts_amd.device import PKG_DIR
+    out = {}
+    for name, env in (("two", {"Q3T_VOC_FUSE": "0"}), ("fused", {})):
+        say(f"[gpu] vocoder residual units: {name}")
+        path = tmp_path / f"{name}.npy"
+        r = subprocess.run([sys.executable, "-c", FUSE_SCRIPT, str(path)], capture_output=True, text=True, timeout=300,
+                           env=dict(os.environ, PYTHONPATH=PKG_DIR, **env))
+        assert r.returncode == 0, r.stderr[-2000:]
+        out[name] = np.load(path)
+    assert out["two"].size == 3 * 1920
+    assert np.array_equal(out["two"], out["fused"])
