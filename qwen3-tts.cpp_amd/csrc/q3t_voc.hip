@@ -307,7 +307,10 @@ int gemm(q3t_voc * v, const GemmW & W, const uint16_t * x, int32_t xs, int32_t r
     // a launch that cannot fill the CUs (the 73-row pre-transformer GEMMs)
     // stages 4 K chunks per step: a quarter of the serial load-and-barrier
     // round trips of its K loop
-    const bool ks4 = wgs(WM, WN) < v->n_cu && WN == 1 && WM <= 2 && W.KT * (W.Cp / 32) >= 8;
+    // (and any launch over at most 128 rows: the pre-transformer's Q/K/V
+    // GEMM fills the CUs with 288 workgroups but its 16-step K loop over 73
+    // rows is the same chain; 1.891-1.898 -> 1.871-1.877 ms per window)
+    const bool ks4 = (wgs(WM, WN) < v->n_cu || M <= 128) && WN == 1 && WM <= 2 && W.KT * (W.Cp / 32) >= 8;
     if (ks4) {
         if (WM == 2) hipLaunchKernelGGL((k_conv_gemm<2, 1, 4>), grid, dim3(kGemmT), 0, v->stream, a);
         else hipLaunchKernelGGL((k_conv_gemm<1, 1, 4>), grid, dim3(kGemmT), 0, v->stream, a);
