@@ -123,7 +123,10 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 32 + ((chu
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // A buffer resource over `bytes` bytes at p: loads at offsets past `bytes`
-// (or at 0x80000000, the out-of-range marker used here) return zeros.
+// (or at 0x80000000, the out-of-range marker used here) return zeros.  Stride
+// 0 (raw addressing: the range check applies to the byte offset); the last
+// word, 0x00020000, is the gfx9 format word for untyped 32-bit data.  The host
+// keeps every range below 2^31 bytes, so the marker is always out of range.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void * p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *) p, (short) 0, (int) bytes, 0x00020000);
 }
