@@ -692,7 +692,9 @@ int vq(q3t_voc * v, const int32_t * codes_dev, int64_t n, uint16_t * hout) {
     const q3t_voc_config & c = v->cfg;
     if (clear_pad(v, hout, n, c.hidden)) return -1;
     HIP_OK(hipMemsetAsync(v->bad, 0, 4, v->stream));
-    hipLaunchKernelGGL(k_vq_sum, dim3((unsigned) n), dim3(256), 0, v->stream, codes_dev, c.n_codebooks, (int32_t) n,
+    // a workgroup per 256 elements of a frame: one element per thread
+    hipLaunchKernelGGL(k_vq_sum, dim3((unsigned) n, (unsigned) ((c.hidden + 255) / 256)), dim3(256), 0, v->stream,
+                       codes_dev, c.n_codebooks, (int32_t) n,
                        v->vq_tab, c.codebook_size, c.hidden, v->xf, rup(c.hidden, 32), hout, rup(c.hidden, 32), v->bad);
     HIP_OK(hipGetLastError());
     return 0;

@@ -514,7 +514,8 @@ __global__ void k_prep(const float * __restrict__ x, int32_t xs, int32_t T, int3
 // VQ (src/audio_tokenizer_decoder.cpp:663-727): lat[f][d] = tab_0[code_0][d]
 // + ((tab_1[code_1][d] + tab_2[code_2][d]) + ...), tab_q = the codebook's
 // normalised rows through its output projection (built at finalize).  A code
-// outside [0, size) raises *bad and reads row 0.
+// outside [0, size) raises *bad and reads row 0.  Workgroup (f, y) takes
+// elements y * blockDim.x + i (stride blockDim.x * gridDim.y) of frame f.
 __global__ void k_vq_sum(const int32_t * __restrict__ codes, int32_t n_cb, int32_t n, const float * __restrict__ tab,
                          int32_t size, int32_t hidden, float * __restrict__ latf, int32_t lfs,
                          uint16_t * __restrict__ lath, int32_t lhs, int32_t * __restrict__ bad) {
@@ -523,7 +524,7 @@ __global__ void k_vq_sum(const int32_t * __restrict__ codes, int32_t n_cb, int32
     // up to 16 codebooks: every table load of an element is issued before the
     // sum, which keeps its order
     constexpr int QM = 16;
-    for (int d = threadIdx.x; d < hidden; d += blockDim.x) {
+    for (int d = blockIdx.y * blockDim.x + threadIdx.x; d < hidden; d += blockDim.x * gridDim.y) {
         float r = 0.0f, first = 0.0f;
         if (n_cb <= QM) {
             float tv[QM];
