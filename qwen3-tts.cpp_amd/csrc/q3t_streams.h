@@ -273,6 +273,23 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
             }
         }
     }
+    // OUT_RESID: wave 0 runs the epilogue if this workgroup arrives last; its
+    // residual values are loaded now, so the epilogue does not wait on them
+    // (no workgroup writes the tile's rows before the last arriver)
+    float rres[OUT == OUT_RESID ? NT : 1][OUT == OUT_RESID ? MT : 1][4];
+    if constexpr (OUT == OUT_RESID) {
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const int tok = 16 * j + lm;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        rres[j][m][e] = tok < a.n ? a.res[(size_t) tok * a.rs + r0 + 16 * m + 4 * lk + e] : 0.0f;
+            }
+        }
+    }
     // the slice's weight scales: rows r0.. of [N][nb] fp16, blocks bs..bs+nbs-1
     for (int i = t; i < MT * kRows * nbs; i += kThreads) {
         const int rr = i / nbs, bb = i - rr * nbs;
@@ -390,9 +407,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm_sk(GemmArgs a) {
                 float o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int r = r0 + 16 * m + 4 * lk + e;
                     const float v = (float) acc[(m * NT + j) * 4 + e];
-                    o[e] = OUT == OUT_RESID && ok ? v + a.res[(size_t) tok * a.rs + r] : v;
+                    float rv = 0.0f;
+                    if constexpr (OUT == OUT_RESID) rv = rres[j][m][e];
+                    o[e] = OUT == OUT_RESID && ok ? v + rv : v;
                     sq += (double) (o[e] * o[e]);
                 }
                 if (ok) *(float4 *) (a.y + (size_t) tok * a.ys + r0 + 16 * m + 4 * lk) = make_float4(o[0], o[1], o[2], o[3]);
@@ -499,6 +517,22 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
             }
             xv[j][i][0] = u0;
             xv[j][i][1] = u1;
+        }
+    }
+    // OUT_RESID: the epilogue's residual values, loaded now by wave 0 (as in
+    // k_gemm_sk), in the epilogue's (token, row) order
+    float rres[OUT == OUT_RESID ? NT : 1][4][OUT == OUT_RESID ? MT : 1];
+    if constexpr (OUT == OUT_RESID) {
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = HM ? 16 * j + 4 * lk + r : 16 * j + 4 * r + lk;
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+                        rres[j][r][m] = tok < a.n ? a.res[(size_t) tok * a.rs + r0 + 16 * m + lm] : 0.0f;
+                }
         }
     }
 
@@ -623,7 +657,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_h(GemmArgs a) {
                     o = silu_q3t((float) g) * (float) fl[4 * (((NW - 1) * MT + m) * NT + j) + r];
                 } else {
                     o = (float) g;
-                    if (OUT == OUT_RESID && ok) o = o + a.res[(size_t) tok * a.rs + row];
+                    if constexpr (OUT == OUT_RESID)
+                        if (ok) o = o + rres[j][r][m];
                 }
                 sq += (double) (o * o);
                 if (ok) a.y[(size_t) tok * a.ys + row] = o;
