@@ -435,6 +435,28 @@ __device__ __forceinline__ float head_norm_rope(float v, const float * w, float 
     return o;
 }
 
+// head_norm_rope with this thread's operands already loaded: wv = w[t], cv =
+// c[t & 63], sv = s[t & 63] (threads < 128); the same arithmetic.
+__device__ __forceinline__ float head_norm_rope_v(float v, float wv, float eps, float cv, float sv, float * tmp,
+                                                  double * red) {
+    const int t = threadIdx.x;
+    const double ss = t < kHD ? (double) (v * v) : 0.0;
+    const double tot = block_sum_d(ss, red);
+    const float mean = (float) (tot / (double) kHD);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    if (t < kHD) { v = v * scale; v = v * wv; tmp[t] = v; }
+    __syncthreads();
+    float o = 0.0f;
+    if (t < kHD) {
+        const int i = t & 63;
+        const float x0 = tmp[i], x1 = tmp[i + 64];
+        if (t < 64) { const float p = x0 * cv, q = x1 * sv; o = p - q; }
+        else        { const float p = x0 * sv, q = x1 * cv; o = p + q; }
+    }
+    __syncthreads();
+    return o;
+}
+
 // RMSNorm over one 128-element head held by a wave (lane holds elements
 // lane and lane + 64), then NEOX RoPE; returns the two rotated elements.
 // The arithmetic of head_norm_rope, with the sum of squares reduced over the
@@ -492,23 +514,54 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     const int pos0 = a.pos_ptr ? *a.pos_ptr : a.pos_const;
     const int pos = pos0 + tok, n_kv = pos + 1;
 
+    const int lane = t & 63, wave = t >> 6;
+    const int sub = lane & 7, pw = lane >> 3;          // scores: 8 lanes per position
+    const int dsub = lane & 15, pq = lane >> 4;        // P.V: 16 lanes per position
+    const uint16_t * kbase = a.kc + (size_t) g * a.n_ctx * kHD;
+    const uint16_t * vbase = a.vc + (size_t) g * a.n_ctx * kHD;
+    // every global operand of the q row, the first new K/V row and the first
+    // score and P.V steps is loaded here, once the position is known, so that
+    // they cost one memory round trip instead of one per step
+    const int i63 = t & 63;
+    const float * row0 = a.qkv;
+    const float * rowq = a.qkv + (size_t) tok * a.qkv_stride;
+    const float qraw = t < kHD ? rowq[h * kHD + t] : 0.0f;
+    const float wq = t < kHD ? a.q_norm[t] : 0.0f, wk = t < kHD ? a.k_norm[t] : 0.0f;
+    const float cq = t < kHD ? a.rope_cos[(size_t) pos * 64 + i63] : 0.0f;
+    const float sq = t < kHD ? a.rope_sin[(size_t) pos * 64 + i63] : 0.0f;
+    const float ck0 = t < kHD ? a.rope_cos[(size_t) pos0 * 64 + i63] : 0.0f;
+    const float sk0 = t < kHD ? a.rope_sin[(size_t) pos0 * 64 + i63] : 0.0f;
+    const float k0raw = t < kHD ? row0[qd + g * kHD + t] : 0.0f;
+    const float v0raw = t < kHD ? row0[qd + kd + g * kHD + t] : 0.0f;
+    int4 kpre0 = make_int4(0, 0, 0, 0), kpre1 = kpre0, vpre = kpre0;
+    if (!a.f32_new) {
+        const int jk = wave * 8 + pw, jv = wave * 4 + pq;
+        if (jk < n_kv && jk < pos0) {
+            const int4 * kp = (const int4 *) (kbase + (size_t) jk * kHD + sub * 16);
+            kpre0 = kp[0];
+            kpre1 = kp[1];
+        }
+        if (jv < n_kv && jv < pos0) vpre = *(const int4 *) (vbase + (size_t) jv * kHD + dsub * 8);
+    }
     // q of this head/token
     {
-        const float * row = a.qkv + (size_t) tok * a.qkv_stride;
-        const float v = t < kHD ? row[h * kHD + t] : 0.0f;
-        const float o = head_norm_rope(v, a.q_norm, a.eps, a.rope_cos + (size_t) pos * 64,
-                                       a.rope_sin + (size_t) pos * 64, tmp, red);
+        const float o = head_norm_rope_v(qraw, wq, a.eps, cq, sq, tmp, red);
         if (t < kHD) qf[t] = a.f32_new ? o : round_kv(o, a.kv_bf16);
     }
     // k, v of this KV head for the chunk tokens 0..tok (positions >= pos0 are
     // never read from the cache inside this launch)
     for (int j = 0; j <= tok; ++j) {
         const float * row = a.qkv + (size_t) j * a.qkv_stride;
-        const float kvv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
-        const float o = head_norm_rope(kvv, a.k_norm, a.eps, a.rope_cos + (size_t) (pos0 + j) * 64,
-                                       a.rope_sin + (size_t) (pos0 + j) * 64, tmp, red);
+        float o;
+        if (j == 0) {
+            o = head_norm_rope_v(k0raw, wk, a.eps, ck0, sk0, tmp, red);
+        } else {
+            const float kvv = t < kHD ? row[qd + g * kHD + t] : 0.0f;
+            o = head_norm_rope(kvv, a.k_norm, a.eps, a.rope_cos + (size_t) (pos0 + j) * 64,
+                               a.rope_sin + (size_t) (pos0 + j) * 64, tmp, red);
+        }
         if (t < kHD) {
-            const float vraw = row[qd + kd + g * kHD + t];
+            const float vraw = j == 0 ? v0raw : row[qd + kd + g * kHD + t];
             const uint16_t kh = f2kv(o, a.kv_bf16);
             const uint16_t vh = f2kv(vraw, a.kv_bf16);
             knew[j * kHD + t] = a.f32_new ? o : kv2f(kh, a.kv_bf16);
@@ -522,9 +575,6 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     __syncthreads();
 
     // scores: 8 lanes per position, 16 dims per lane
-    const int lane = t & 63, wave = t >> 6;
-    const int sub = lane & 7, pw = lane >> 3;
-    const uint16_t * kbase = a.kc + (size_t) g * a.n_ctx * kHD;
     float lmax = -INFINITY;
     if (a.f32_new) {
         // every position is a new fp32 row (pos0 = 0, n_kv <= 16): 4 lanes of
@@ -552,7 +602,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         if (j < n_kv) {
             if (j < pos0) {
                 const int4 * kp = (const int4 *) (kbase + (size_t) j * kHD + sub * 16);
-                const int4 k0 = kp[0], k1 = kp[1];
+                const int4 k0 = j0 == 0 ? kpre0 : kp[0], k1 = j0 == 0 ? kpre1 : kp[1];
                 const uint16_t * kh0 = (const uint16_t *) &k0;
                 const uint16_t * kh1 = (const uint16_t *) &k1;
 #pragma unroll
@@ -591,8 +641,6 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     __syncthreads();
 
     // P.V: 16 lanes per position, 8 dims per lane, 4 positions per wave step
-    const int dsub = lane & 15, pq = lane >> 4;
-    const uint16_t * vbase = a.vc + (size_t) g * a.n_ctx * kHD;
     double o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0;
@@ -601,7 +649,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         if (j < n_kv) {
             const float p = sc[j];
             if (j < pos0) {
-                const int4 vv = *(const int4 *) (vbase + (size_t) j * kHD + dsub * 8);
+                const int4 vv = j0 == 0 ? vpre : *(const int4 *) (vbase + (size_t) j * kHD + dsub * 8);
                 const uint16_t * vh = (const uint16_t *) &vv;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o[e] += (double) p * (double) kv2f(vh[e], a.kv_bf16);
